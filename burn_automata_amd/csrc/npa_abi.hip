@@ -1,0 +1,952 @@
+// npa_abi.cpp - the C ABI of libnpa_hip.so (declared in include/npa_abi.h).
+//
+// Validation mirrors the reference's error behaviour: HashGridConfig::validate
+// (crates/burn_automata_kernels/src/config.rs:65-84), check_shapes
+// (crates/burn_automata_kernels/src/reference/shape.rs:3-25), NpaModel::validate and the
+// grid/model dim check of step_cpu (crates/burn_automata/src/model.rs:756-783).
+#include <hip/hip_runtime.h>
+
+#include <float.h>
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "npa_internal.hpp"
+
+using npa::DevBuf;
+
+struct npa_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool host_io = false;
+    int cus = 256;
+    std::string last_error;
+    npa::Workspace ws;
+    npa::SplatWorkspace splat_ws;
+    npa::Profiler prof;
+    std::vector<DevBuf*> staging;
+    ~npa_context() {
+        ws.release();
+        splat_ws.release();
+        for (DevBuf* b : staging) {
+            b->release();
+            delete b;
+        }
+    }
+};
+
+struct npa_state {
+    npa_context* ctx = nullptr;
+    npa_model_cfg model{};
+    npa_grid_cfg grid{};
+    uint32_t B = 0, N = 0;
+    float dt = 1.0f, update_prob = 1.0f;
+    uint64_t seed = 0;
+    uint64_t step_index = 0;
+    DevBuf pos[2], states[2], density, w1, b1, w2, b2;
+    int cur = 0;
+    npa::Workspace ws;
+    npa::SplatWorkspace splat_ws;
+    npa::HashgridPlan plan;
+    int grid_blocks = 1;
+    ~npa_state() {
+        for (DevBuf* b : {&pos[0], &pos[1], &states[0], &states[1], &density, &w1, &b1, &w2, &b2}) b->release();
+        ws.release();
+        splat_ws.release();
+    }
+};
+
+namespace {
+
+npa_status fail(npa_context* ctx, npa_status st, const std::string& msg) {
+    if (ctx) ctx->last_error = msg;
+    return st;
+}
+
+npa_status hip_fail(npa_context* ctx, hipError_t e, const char* where) {
+    std::string msg = std::string(where) + ": " + hipGetErrorString(e);
+    return fail(ctx, e == hipErrorOutOfMemory ? NPA_ERR_OUT_OF_MEMORY : NPA_ERR_DEVICE, msg);
+}
+
+#define NPA_HIP(ctx, expr, where)                          \
+    do {                                                   \
+        hipError_t _e = (expr);                            \
+        if (_e != hipSuccess) return hip_fail(ctx, _e, where); \
+    } while (0)
+
+std::string fmt_f(float v) {
+    char buf[64];
+    snprintf(buf, sizeof buf, "%g", (double)v);
+    return buf;
+}
+
+// HashGridConfig::validate  config.rs:65-84
+npa_status validate_grid(npa_context* ctx, const npa_grid_cfg* cfg) {
+    if (!cfg) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null grid config");
+    if (!(cfg->dim == 2 || cfg->dim == 3))
+        return fail(ctx, NPA_ERR_INVALID_DIM, "expected spatial dim 2 or 3, got " + std::to_string(cfg->dim));
+    if (!std::isfinite(cfg->eps) || cfg->eps <= 0.0f)
+        return fail(ctx, NPA_ERR_INVALID_EPS, "eps must be finite and positive, got " + fmt_f(cfg->eps));
+    for (uint32_t a = 0; a < cfg->dim; ++a) {
+        const uint32_t s = cfg->grid_size[a];
+        if (s == 0) return fail(ctx, NPA_ERR_INVALID_GRID_SIZE, "grid sizes must be non-zero for active dimensions");
+        if (cfg->mode == NPA_MODE_PARTICLE && (s & (s - 1u)) != 0)
+            return fail(ctx, NPA_ERR_PARTICLE_MODE_POW2,
+                        "particle hashgrid mode requires power-of-two grid size at axis " + std::to_string(a) +
+                            ", got " + std::to_string(s));
+    }
+    if (cfg->boundary > 1 || cfg->mode > 1)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: unknown boundary or hashgrid mode");
+    return NPA_OK;
+}
+
+npa_status check_model(npa_context* ctx, const npa_model_cfg* m, const npa_grid_cfg* grid) {
+    if (!m) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null model config");
+    if (!(m->spatial_dims == 2 || m->spatial_dims == 3))
+        return fail(ctx, NPA_ERR_INVALID_MODEL,
+                    "invalid model: spatial_dims must be 2 or 3, got " + std::to_string(m->spatial_dims));
+    if (grid && grid->dim != m->spatial_dims)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT,
+                    "invalid argument: grid dim " + std::to_string(grid->dim) + " does not match model spatial dims " +
+                        std::to_string(m->spatial_dims));
+    if (m->state_dims == 0 || m->state_dims > 32)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT,
+                    "invalid argument: the device path supports 1..=32 state dims, got " + std::to_string(m->state_dims));
+    if (m->equivariance > 2) return fail(ctx, NPA_ERR_INVALID_MODEL, "invalid model: unknown equivariance mode");
+    if (m->spatial_dims == 3 && m->position_features && m->state_dims > 3 && m->state_dims < 8)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT,
+                    "invalid argument: position-conditioned 3D gates read state channel 7; need state_dims >= 8");
+    return NPA_OK;
+}
+
+uint32_t model_perception_dims(const npa_model_cfg& m) {  // config.rs:133-139
+    return m.state_dims * 2 + (m.state_grad ? m.state_dims * m.spatial_dims : 0) +
+           (m.density_grad ? m.spatial_dims : 0) + (m.position_features ? m.spatial_dims : 0);
+}
+
+npa_perception_opts opts_for_model(const npa_model_cfg& m) {  // model.rs:784-800
+    npa_perception_opts o{};
+    o.state_grad = m.state_grad;
+    o.density_grad = m.density_grad;
+    o.eps0 = m.eps0;
+    o.scale_equivariance = m.equivariance == NPA_EQUIV_PARTICLE_DENSITY_AND_SCALE;
+    o.particle_density_equivariance =
+        m.equivariance == NPA_EQUIV_PARTICLE_DENSITY || m.equivariance == NPA_EQUIV_PARTICLE_DENSITY_AND_SCALE;
+    o.log_norm_grad = m.log_norm_grad;
+    o.log_norm_density_grad = m.log_norm_density_grad;
+    o.hybrid_state_gradient = 1;
+    o.position_features = m.position_features;
+    return o;
+}
+
+npa::StepParams make_params(const npa_grid_cfg& cfg, const npa_perception_opts& o, uint32_t B, uint32_t N,
+                            uint32_t S) {
+    npa::StepParams p{};
+    p.g = npa::make_grid_params(cfg);
+    p.N = N;
+    p.B = B;
+    p.S = S;
+    p.state_grad = o.state_grad ? 1 : 0;
+    p.density_grad = o.density_grad ? 1 : 0;
+    p.log_norm_grad = o.log_norm_grad ? 1 : 0;
+    p.log_norm_dgrad = o.log_norm_density_grad ? 1 : 0;
+    p.hybrid = o.hybrid_state_gradient ? 1 : 0;
+    p.position_features = o.position_features ? 1 : 0;
+    p.F = S * 2 + (o.state_grad ? S * cfg.dim : 0) + (o.density_grad ? cfg.dim : 0) +
+          (o.position_features ? cfg.dim : 0);
+    // normalize_state_gradient / normalize_density_gradient  normalize.rs:5-58
+    const float eps0 = fmaxf(o.eps0, FLT_MIN);
+    p.state_scale = o.scale_equivariance ? cfg.eps / eps0 : 1.0f;
+    const float s1 = o.scale_equivariance ? npa::host_powi(cfg.eps / eps0, 1 + (int)cfg.dim) : 1.0f;
+    const float s2 = o.particle_density_equivariance ? 1.0f / (float)(N > 1 ? N : 1) : 1.0f;
+    p.dgrad_scale = s1 * s2;
+    p.update_prob = 1.0f;
+    p.dt = 1.0f;
+    return p;
+}
+
+void apply_model(npa::StepParams* p, const npa_model_cfg& m, float grid_eps) {
+    p->H = m.hidden_dims;
+    p->alpha = m.alpha;
+    // NpaConfig::motion_eps  config.rs:156-162
+    p->motion_eps = m.equivariance == NPA_EQUIV_PARTICLE_DENSITY_AND_SCALE ? grid_eps : m.eps0;
+    p->gates3d = (m.spatial_dims == 3 && m.position_features && m.state_dims > 3) ? 1 : 0;
+}
+
+uint32_t base_seed(uint64_t seed) { return (uint32_t)seed ^ (uint32_t)(seed >> 32); }  // params.rs:186-188
+
+int grid_blocks_for(const npa_context* ctx, const npa::HashgridPlan& plan) {
+    const uint64_t waves = plan.worklist_cap;
+    const uint64_t blocks = (waves + 3) / 4;
+    const uint64_t cap = (uint64_t)ctx->cus * 8;
+    return (int)std::max<uint64_t>(1, std::min(blocks, cap));
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Host I/O: stages host arrays through context-owned device buffers.
+struct HostIO {
+    npa_context* ctx;
+    bool active;
+    size_t slot = 0;
+    struct Out { void* host; void* dev; size_t bytes; };
+    std::vector<Out> outs;
+    hipError_t err = hipSuccess;
+    explicit HostIO(npa_context* c) : ctx(c), active(c->host_io) {}
+    void* buffer(size_t bytes) {
+        if (slot == ctx->staging.size()) ctx->staging.push_back(new DevBuf());
+        DevBuf* b = ctx->staging[slot++];
+        hipError_t e = b->reserve(bytes ? bytes : 16);
+        if (e != hipSuccess) {
+            err = e;
+            return nullptr;
+        }
+        return b->ptr;
+    }
+    template <class T>
+    const T* in(const T* p, size_t bytes) {
+        if (!active || !p) return p;
+        void* d = buffer(bytes);
+        if (!d) return nullptr;
+        if (bytes) {
+            hipError_t e = hipMemcpyAsync(d, p, bytes, hipMemcpyHostToDevice, ctx->stream);
+            if (e != hipSuccess) err = e;
+        }
+        return static_cast<const T*>(d);
+    }
+    template <class T>
+    T* out(T* p, size_t bytes) {
+        if (!active || !p) return p;
+        void* d = buffer(bytes);
+        if (!d) return nullptr;
+        outs.push_back({(void*)p, d, bytes});
+        return static_cast<T*>(d);
+    }
+    hipError_t finish() {
+        if (err != hipSuccess) return err;
+        if (!active) return hipSuccess;
+        for (const Out& o : outs) {
+            if (!o.bytes) continue;
+            hipError_t e = hipMemcpyAsync(o.host, o.dev, o.bytes, hipMemcpyDeviceToHost, ctx->stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipStreamSynchronize(ctx->stream);
+    }
+};
+
+npa_status check_flags(npa_context* ctx, npa::Workspace& ws) {
+    uint32_t flags = 0;
+    NPA_HIP(ctx, hipMemcpyAsync(&flags, ws.flags.ptr, 4, hipMemcpyDeviceToHost, ctx->stream), "flags readback");
+    NPA_HIP(ctx, hipStreamSynchronize(ctx->stream), "flags readback");
+    if (flags & 1u) {
+        uint32_t zero = 0;
+        NPA_HIP(ctx, hipMemcpy(ws.flags.ptr, &zero, 4, hipMemcpyHostToDevice), "flags reset");
+        return fail(ctx, NPA_ERR_COORD_OVERFLOW,
+                    "a particle-mode cell coordinate left the +-2^30 range the device path stores exactly");
+    }
+    return NPA_OK;
+}
+
+npa_status set_device(npa_context* ctx) {
+    NPA_HIP(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    return NPA_OK;
+}
+
+}  // namespace
+
+// ====================================================================== context
+extern "C" {
+
+const char* npa_version(void) { return "npa_hip 0.1.0 (gfx950)"; }
+
+npa_status npa_context_create(int device, void* stream, npa_context** out) {
+    if (!out) return NPA_ERR_INVALID_ARGUMENT;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return NPA_ERR_DEVICE;
+    if (device < 0 || device >= count) return NPA_ERR_INVALID_ARGUMENT;
+    npa_context* ctx = new npa_context();
+    ctx->device = device;
+    ctx->stream = (hipStream_t)stream;
+    if (hipSetDevice(device) != hipSuccess) {
+        delete ctx;
+        return NPA_ERR_DEVICE;
+    }
+    ctx->cus = npa::device_cu_count();
+    *out = ctx;
+    return NPA_OK;
+}
+
+void npa_context_destroy(npa_context* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    delete ctx;
+}
+
+npa_status npa_context_set_stream(npa_context* ctx, void* stream) {
+    if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
+    ctx->stream = (hipStream_t)stream;
+    return NPA_OK;
+}
+
+npa_status npa_context_set_host_io(npa_context* ctx, int host_io) {
+    if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
+    ctx->host_io = host_io != 0;
+    return NPA_OK;
+}
+
+npa_status npa_context_synchronize(npa_context* ctx) {
+    if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
+    NPA_HIP(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (ctx->ws.flags.ptr) return check_flags(ctx, ctx->ws);
+    return NPA_OK;
+}
+
+const char* npa_last_error(const npa_context* ctx) { return ctx ? ctx->last_error.c_str() : "null context"; }
+
+// ============================================================== operator surface
+npa_status npa_build_hashgrid(npa_context* ctx, const float* positions, uint32_t B, uint32_t N,
+                              const npa_grid_cfg* cfg, uint32_t* bin_offsets, size_t bin_offsets_len,
+                              uint32_t* permutation, uint32_t* inverse_permutation, size_t particles_len) {
+    if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
+    npa_status st = validate_grid(ctx, cfg);
+    if (st) return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint64_t total = (uint64_t)B * N;
+    uint64_t cells = 1;
+    for (uint32_t a = 0; a < cfg->dim; ++a) cells *= cfg->grid_size[a];
+    if (bin_offsets_len != (uint64_t)B * cells + 1)
+        return fail(ctx, NPA_ERR_OUTPUT_SHAPE,
+                    "output buffer length " + std::to_string(bin_offsets_len) + " does not match expected " +
+                        std::to_string((uint64_t)B * cells + 1));
+    if (particles_len != total)
+        return fail(ctx, NPA_ERR_OUTPUT_SHAPE,
+                    "output buffer length " + std::to_string(particles_len) + " does not match expected " +
+                        std::to_string(total));
+    if (!positions && total) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null positions");
+    npa::HashgridPlan plan;
+    std::string err;
+    if (!npa::make_plan(*cfg, B, N, &plan, &err)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
+    HostIO io(ctx);
+    const float4* pos = (const float4*)io.in(positions, total * 16);
+    uint32_t* bo = io.out(bin_offsets, bin_offsets_len * 4);
+    uint32_t* perm = io.out(permutation, total * 4);
+    uint32_t* inv = io.out(inverse_permutation, total * 4);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if (total && !aligned16(pos)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: positions must be 16-byte aligned");
+    NPA_HIP(ctx, ctx->ws.reserve(plan, total, B, 1, (int)cfg->dim), "workspace");
+    const npa::GridParams g = npa::make_grid_params(*cfg);
+    if (total) {
+        NPA_HIP(ctx, npa::launch_hashgrid(plan, g, pos, nullptr, 1, B, N, ctx->ws, false, ctx->stream, &ctx->prof),
+                "hashgrid");
+        NPA_HIP(ctx, hipMemcpyAsync(bo, ctx->ws.bin_offsets.ptr, bin_offsets_len * 4, hipMemcpyDeviceToDevice, ctx->stream),
+                "copy bin_offsets");
+        NPA_HIP(ctx, hipMemcpyAsync(perm, ctx->ws.perm.ptr, total * 4, hipMemcpyDeviceToDevice, ctx->stream), "copy perm");
+        NPA_HIP(ctx, hipMemcpyAsync(inv, ctx->ws.inv.ptr, total * 4, hipMemcpyDeviceToDevice, ctx->stream), "copy inv");
+    } else {
+        NPA_HIP(ctx, hipMemsetAsync(bo, 0, bin_offsets_len * 4, ctx->stream), "zero bin_offsets");
+    }
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
+npa_status npa_neighbor_lists(npa_context* ctx, const float* positions, uint32_t B, uint32_t N,
+                              const npa_grid_cfg* cfg, uint32_t* offsets, uint32_t* indices, size_t capacity,
+                              size_t* required) {
+    if (!ctx || !offsets || !required) return NPA_ERR_INVALID_ARGUMENT;
+    npa_status st = validate_grid(ctx, cfg);
+    if (st) return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint64_t total = (uint64_t)B * N;
+    npa::HashgridPlan plan;
+    std::string err;
+    if (!npa::make_plan(*cfg, B, N, &plan, &err)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
+    HostIO io(ctx);
+    const float4* pos = (const float4*)io.in(positions, total * 16);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    NPA_HIP(ctx, ctx->ws.reserve(plan, total, B, 1, (int)cfg->dim), "workspace");
+    npa_perception_opts o{};
+    npa::StepParams p = make_params(*cfg, o, B, N, 1);
+    const int blocks = grid_blocks_for(ctx, plan);
+    std::vector<uint32_t> counts(total + 1, 0);
+    DevBuf dcounts;
+    NPA_HIP(ctx, dcounts.reserve((total + 1) * 4), "counts");
+    if (total) {
+        NPA_HIP(ctx, npa::launch_hashgrid(plan, p.g, pos, nullptr, 1, B, N, ctx->ws, true, ctx->stream, nullptr),
+                "hashgrid");
+        NPA_HIP(ctx, npa::launch_neighbor_lists(p, ctx->ws, dcounts.as<uint32_t>(), nullptr, 0, blocks, ctx->stream),
+                "count");
+        NPA_HIP(ctx, hipMemcpyAsync(counts.data(), dcounts.ptr, total * 4, hipMemcpyDeviceToHost, ctx->stream),
+                "counts readback");
+        NPA_HIP(ctx, hipStreamSynchronize(ctx->stream), "sync");
+    }
+    std::vector<uint32_t> off(total + 1, 0);
+    for (uint64_t i = 0; i < total; ++i) off[i + 1] = off[i] + counts[i];
+    *required = off[total];
+    if (ctx->host_io) {
+        memcpy(offsets, off.data(), (total + 1) * 4);
+    } else {
+        NPA_HIP(ctx, hipMemcpy(offsets, off.data(), (total + 1) * 4, hipMemcpyHostToDevice), "offsets");
+    }
+    if (indices && capacity >= off[total] && total) {
+        NPA_HIP(ctx, hipMemcpy(dcounts.ptr, off.data(), total * 4, hipMemcpyHostToDevice), "offsets upload");
+        DevBuf didx;
+        uint32_t* dst = indices;
+        if (ctx->host_io) {
+            NPA_HIP(ctx, didx.reserve((size_t)off[total] * 4 + 4), "indices");
+            dst = didx.as<uint32_t>();
+        }
+        NPA_HIP(ctx, npa::launch_neighbor_lists(p, ctx->ws, dcounts.as<uint32_t>(), dst, 1, blocks, ctx->stream),
+                "fill");
+        if (ctx->host_io)
+            NPA_HIP(ctx, hipMemcpyAsync(indices, dst, (size_t)off[total] * 4, hipMemcpyDeviceToHost, ctx->stream),
+                    "indices readback");
+        NPA_HIP(ctx, hipStreamSynchronize(ctx->stream), "sync");
+        didx.release();
+    }
+    dcounts.release();
+    return NPA_OK;
+}
+
+npa_status npa_perceive(npa_context* ctx, const float* positions, const float* states, uint32_t B, uint32_t N,
+                        uint32_t S, const npa_grid_cfg* cfg, const npa_perception_opts* opts, float* features,
+                        size_t features_len, float* density, float* blurred_state, float* state_gradient,
+                        float* density_gradient, uint32_t* feature_dims) {
+    if (!ctx || !opts) return NPA_ERR_INVALID_ARGUMENT;
+    npa_status st = validate_grid(ctx, cfg);
+    if (st) return st;
+    if (S == 0 || S > 32)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: the device path supports 1..=32 state dims");
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint64_t total = (uint64_t)B * N;
+    const uint32_t d = cfg->dim;
+    const uint32_t F = S * 2 + (opts->state_grad ? S * d : 0) + (opts->density_grad ? d : 0) +
+                       (opts->position_features ? d : 0);
+    if (feature_dims) *feature_dims = F;
+    if (features_len != total * F)
+        return fail(ctx, NPA_ERR_OUTPUT_SHAPE,
+                    "output buffer length " + std::to_string(features_len) + " does not match expected " +
+                        std::to_string(total * F));
+    if (!features || !density || (total && (!positions || !states)))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null array");
+    npa::HashgridPlan plan;
+    std::string err;
+    if (!npa::make_plan(*cfg, B, N, &plan, &err)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
+    HostIO io(ctx);
+    const float4* pos = (const float4*)io.in(positions, total * 16);
+    const float* st_in = io.in(states, total * S * 4);
+    npa::StepIO sio;
+    sio.pos = pos;
+    sio.states = st_in;
+    sio.features = io.out(features, total * F * 4);
+    float* dens = io.out(density, total * 4);
+    sio.blurred = io.out(blurred_state, total * S * 4);
+    sio.state_gradient = opts->state_grad ? io.out(state_gradient, total * S * d * 4) : nullptr;
+    sio.density_gradient = opts->density_grad ? io.out(density_gradient, total * d * 4) : nullptr;
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if (total && !aligned16(pos)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: positions must be 16-byte aligned");
+    if (total && (S % 4 == 0) && !aligned16(st_in))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: states must be 16-byte aligned");
+    NPA_HIP(ctx, ctx->ws.reserve(plan, total, B, S, (int)d), "workspace");
+    npa::StepParams p = make_params(*cfg, *opts, B, N, S);
+    const int blocks = grid_blocks_for(ctx, plan);
+    if (total) {
+        NPA_HIP(ctx, npa::launch_hashgrid(plan, p.g, pos, st_in, S, B, N, ctx->ws, true, ctx->stream, &ctx->prof),
+                "hashgrid");
+        NPA_HIP(ctx, npa::launch_density(p, ctx->ws, dens, blocks, ctx->stream, &ctx->prof), "density");
+        NPA_HIP(ctx, npa::launch_update(p, ctx->ws, sio, 1, blocks, ctx->stream, &ctx->prof), "perceive");
+    }
+    NPA_HIP(ctx, io.finish(), "host io");
+    if (ctx->host_io) return check_flags(ctx, ctx->ws);
+    return NPA_OK;
+}
+
+npa_status npa_mlp_forward(npa_context* ctx, const float* features, uint32_t rows, const npa_model_cfg* model,
+                           const npa_weights* w, float eps, float* dx, float* ds) {
+    if (!ctx || !w) return NPA_ERR_INVALID_ARGUMENT;
+    npa_status st = check_model(ctx, model, nullptr);
+    if (st) return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint32_t F = model_perception_dims(*model), H = model->hidden_dims, S = model->state_dims;
+    const uint32_t O = model->spatial_dims + S;
+    HostIO io(ctx);
+    npa::StepIO sio;
+    const float* f = io.in(features, (uint64_t)rows * F * 4);
+    sio.w1 = io.in(w->w1, (uint64_t)H * F * 4);
+    sio.b1 = io.in(w->b1, (uint64_t)H * 4);
+    sio.w2 = io.in(w->w2, (uint64_t)O * H * 4);
+    sio.b2 = io.in(w->b2, (uint64_t)O * 4);
+    float* ddx = io.out(dx, (uint64_t)rows * 16);
+    float* dds = io.out(ds, (uint64_t)rows * S * 4);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    npa_grid_cfg gcfg{};
+    gcfg.dim = model->spatial_dims;
+    gcfg.eps = eps;
+    for (int a = 0; a < 3; ++a) gcfg.grid_size[a] = 1;
+    npa::StepParams p = make_params(gcfg, opts_for_model(*model), 1, rows ? rows : 1, S);
+    apply_model(&p, *model, eps);
+    p.F = F;
+    NPA_HIP(ctx, npa::launch_mlp_forward(p, f, rows, sio, ddx, dds, ctx->stream), "mlp");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
+npa_status npa_euler_step(npa_context* ctx, const float* positions, const float* states, const float* dx,
+                          const float* ds, uint32_t B, uint32_t N, uint32_t S, const npa_grid_cfg* cfg, float dt,
+                          const float* mask, float* out_positions, float* out_states) {
+    if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
+    npa_status st = validate_grid(ctx, cfg);
+    if (st) return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint64_t total = (uint64_t)B * N;
+    HostIO io(ctx);
+    const float4* pos = (const float4*)io.in(positions, total * 16);
+    const float* sin_ = io.in(states, total * S * 4);
+    const float4* ddx = (const float4*)io.in(dx, total * 16);
+    const float* dds = io.in(ds, total * S * 4);
+    const float* m = io.in(mask, total * 4);
+    float4* op = (float4*)io.out(out_positions, total * 16);
+    float* os = io.out(out_states, total * S * 4);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if (total && (!aligned16(pos) || !aligned16(ddx) || !aligned16(op)))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: position arrays must be 16-byte aligned");
+    npa_perception_opts o{};
+    npa::StepParams p = make_params(*cfg, o, B, N ? N : 1, S);
+    p.dt = dt;
+    NPA_HIP(ctx, npa::launch_euler(p, pos, sin_, ddx, dds, m, op, os, total, ctx->stream), "euler");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
+npa_status npa_step(npa_context* ctx, const float* positions, const float* states, uint32_t B, uint32_t N,
+                    const npa_grid_cfg* grid, const npa_model_cfg* model, const npa_weights* w, float dt,
+                    const float* mask, float* out_positions, float* out_states, float* out_density) {
+    if (!ctx || !w) return NPA_ERR_INVALID_ARGUMENT;
+    npa_status st = validate_grid(ctx, grid);
+    if (st) return st;
+    if ((st = check_model(ctx, model, grid))) return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint64_t total = (uint64_t)B * N;
+    const uint32_t S = model->state_dims, F = model_perception_dims(*model), H = model->hidden_dims;
+    const uint32_t O = model->spatial_dims + S;
+    npa::HashgridPlan plan;
+    std::string err;
+    if (!npa::make_plan(*grid, B, N, &plan, &err)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
+    HostIO io(ctx);
+    npa::StepIO sio;
+    sio.pos = (const float4*)io.in(positions, total * 16);
+    sio.states = io.in(states, total * S * 4);
+    sio.mask = io.in(mask, total * 4);
+    sio.w1 = io.in(w->w1, (uint64_t)H * F * 4);
+    sio.b1 = io.in(w->b1, (uint64_t)H * 4);
+    sio.w2 = io.in(w->w2, (uint64_t)O * H * 4);
+    sio.b2 = io.in(w->b2, (uint64_t)O * 4);
+    sio.out_pos = (float4*)io.out(out_positions, total * 16);
+    sio.out_states = io.out(out_states, total * S * 4);
+    float* dens = io.out(out_density, total * 4);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if (total && (!aligned16(sio.pos) || !aligned16(sio.out_pos)))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: positions must be 16-byte aligned");
+    if (total && (S % 4 == 0) && !aligned16(sio.states))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: states must be 16-byte aligned");
+    NPA_HIP(ctx, ctx->ws.reserve(plan, total, B, S, (int)grid->dim), "workspace");
+    npa::StepParams p = make_params(*grid, opts_for_model(*model), B, N, S);
+    apply_model(&p, *model, grid->eps);
+    p.dt = dt;
+    p.update_prob = 1.0f;
+    const int blocks = grid_blocks_for(ctx, plan);
+    if (total) {
+        NPA_HIP(ctx, npa::launch_hashgrid(plan, p.g, sio.pos, sio.states, S, B, N, ctx->ws, true, ctx->stream,
+                                          &ctx->prof),
+                "hashgrid");
+        NPA_HIP(ctx, npa::launch_density(p, ctx->ws, dens, blocks, ctx->stream, &ctx->prof), "density");
+        NPA_HIP(ctx, npa::launch_update(p, ctx->ws, sio, 0, blocks, ctx->stream, &ctx->prof), "update");
+    }
+    NPA_HIP(ctx, io.finish(), "host io");
+    if (ctx->host_io) return check_flags(ctx, ctx->ws);
+    return NPA_OK;
+}
+
+npa_status npa_update_mask(npa_context* ctx, uint32_t B, uint32_t N, float update_prob, uint32_t step_index,
+                           uint64_t seed, float* mask) {
+    if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    HostIO io(ctx);
+    float* m = io.out(mask, (uint64_t)B * N * 4);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    NPA_HIP(ctx, npa::launch_update_mask(B, N, update_prob, step_index, base_seed(seed), m, ctx->stream), "mask");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
+static npa_status check_decode(npa_context* ctx, uint32_t S, const npa_gaussian_decode_cfg* cfg) {
+    if (!cfg) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null decode config");
+    const uint32_t K = cfg->mode == NPA_DECODE_SH0_ORIENTED ? (cfg->sh_degree + 1) * (cfg->sh_degree + 1) : 1;
+    switch (cfg->mode) {  // validate_decode_layout gaussian.rs:102-125
+        case NPA_DECODE_PARTICLE_POINT:
+        case NPA_DECODE_SH0_FIXED_SCALE:
+            if (S < 3) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "state_dims must include an RGB tail for SH0 gaussian decoding");
+            break;
+        case NPA_DECODE_SH0_LEARNED_SCALE:
+            if (S < 5) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "state_dims must include scale, opacity, and RGB tail channels");
+            break;
+        case NPA_DECODE_SH0_ORIENTED:
+            if (cfg->sh_degree > 8 || S < K * 3 + 8)
+                return fail(ctx, NPA_ERR_INVALID_ARGUMENT,
+                            "state_dims must fit color/sh, rotation, and anisotropy/opacity tails");
+            break;
+        default:
+            return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: unknown decode mode");
+    }
+    return NPA_OK;
+}
+
+npa_status npa_decode_gaussians_3d(npa_context* ctx, const float* positions, const float* states, uint32_t count,
+                                   uint32_t S, const npa_gaussian_decode_cfg* cfg, float* pv, float* sh, float* rot,
+                                   float* so) {
+    if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
+    npa_status st = check_decode(ctx, S, cfg);
+    if (st) return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint32_t K = cfg->mode == NPA_DECODE_SH0_ORIENTED ? (cfg->sh_degree + 1) * (cfg->sh_degree + 1) : 1;
+    HostIO io(ctx);
+    const float4* pos = (const float4*)io.in(positions, (uint64_t)count * 16);
+    const float* s = io.in(states, (uint64_t)count * S * 4);
+    float* dpv = io.out(pv, (uint64_t)count * 16);
+    float* dsh = io.out(sh, (uint64_t)count * K * 12);
+    float* drot = io.out(rot, (uint64_t)count * 16);
+    float* dso = io.out(so, (uint64_t)count * 16);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if (count && (!aligned16(pos) || !aligned16(dpv) || !aligned16(drot) || !aligned16(dso)))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: 4-wide arrays must be 16-byte aligned");
+    NPA_HIP(ctx, npa::launch_decode_gaussians(pos, s, count, S, *cfg, dpv, dsh, drot, dso, ctx->stream), "decode");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
+static npa_status check_splat(npa_context* ctx, const npa_splat2d_cfg* cfg) {
+    if (!cfg) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null splat config");
+    if (cfg->image_size == 0 || cfg->image_size > 4096)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: splat image_size must be in 1..=4096");
+    float sigma = cfg->sigma;
+    if (cfg->normalize_color) sigma = sigma * (float)cfg->image_size * cfg->pixel_size / (cfg->hi - cfg->lo);
+    const float r = ceilf(5.0f * sigma);
+    if (!(r <= 1024.0f))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: splat radius ceil(5*sigma) must be <= 1024 pixels");
+    return NPA_OK;
+}
+
+npa_status npa_splat_2d(npa_context* ctx, const float* positions, const float* colors, uint32_t count,
+                        const npa_splat2d_cfg* cfg, float* image) {
+    if (!ctx || !image) return NPA_ERR_INVALID_ARGUMENT;
+    npa_status st = check_splat(ctx, cfg);
+    if (st) return st;
+    if (count && !colors) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null colors");
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    HostIO io(ctx);
+    const float4* pos = (const float4*)io.in(positions, (uint64_t)count * 16);
+    const float* col = io.in(colors, (uint64_t)count * 12);
+    float* img = io.out(image, (uint64_t)cfg->image_size * cfg->image_size * 16);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if ((count && !aligned16(pos)) || !aligned16(img))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: positions and image must be 16-byte aligned");
+    NPA_HIP(ctx, npa::launch_splat_2d(pos, col, nullptr, 3, count, *cfg, img, ctx->splat_ws, ctx->stream, &ctx->prof),
+            "splat");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
+// ==================================================================== executor
+npa_status npa_state_create(npa_context* ctx, const npa_model_cfg* model, const npa_weights* w,
+                            const npa_grid_cfg* grid, const float* positions, const float* states, uint32_t B,
+                            uint32_t N, float dt, float update_prob, uint64_t seed, npa_state** out) {
+    if (!ctx || !w || !out) return NPA_ERR_INVALID_ARGUMENT;
+    *out = nullptr;
+    npa_status st = validate_grid(ctx, grid);
+    if (st) return st;
+    if ((st = check_model(ctx, model, grid))) return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint64_t total = (uint64_t)B * N;
+    if (total == 0) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: empty particle system");
+    npa::HashgridPlan plan;
+    std::string err;
+    if (!npa::make_plan(*grid, B, N, &plan, &err)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
+    npa_state* s = new npa_state();
+    s->ctx = ctx;
+    s->model = *model;
+    s->grid = *grid;
+    s->B = B;
+    s->N = N;
+    s->dt = dt;
+    s->update_prob = update_prob;
+    s->seed = seed;
+    s->plan = plan;
+    s->grid_blocks = grid_blocks_for(ctx, plan);
+    const uint32_t S = model->state_dims, F = model_perception_dims(*model), H = model->hidden_dims;
+    const uint32_t O = model->spatial_dims + S;
+    const hipMemcpyKind kind = ctx->host_io ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
+    hipError_t e = hipSuccess;
+    for (int k = 0; k < 2 && e == hipSuccess; ++k) {
+        e = s->pos[k].reserve(total * 16);
+        if (e == hipSuccess) e = s->states[k].reserve(total * S * 4);
+    }
+    if (e == hipSuccess) e = s->density.reserve(total * 4);
+    if (e == hipSuccess) e = s->w1.reserve((uint64_t)H * F * 4 + 4);
+    if (e == hipSuccess) e = s->b1.reserve((uint64_t)H * 4 + 4);
+    if (e == hipSuccess) e = s->w2.reserve((uint64_t)O * H * 4 + 4);
+    if (e == hipSuccess) e = s->b2.reserve((uint64_t)O * 4 + 4);
+    if (e == hipSuccess) e = s->ws.reserve(plan, total, B, S, (int)grid->dim);
+    if (e == hipSuccess) e = hipMemcpyAsync(s->pos[0].ptr, positions, total * 16, kind, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(s->states[0].ptr, states, total * S * 4, kind, ctx->stream);
+    if (e == hipSuccess && (uint64_t)H * F) e = hipMemcpyAsync(s->w1.ptr, w->w1, (uint64_t)H * F * 4, kind, ctx->stream);
+    if (e == hipSuccess && H) e = hipMemcpyAsync(s->b1.ptr, w->b1, (uint64_t)H * 4, kind, ctx->stream);
+    if (e == hipSuccess && (uint64_t)O * H) e = hipMemcpyAsync(s->w2.ptr, w->w2, (uint64_t)O * H * 4, kind, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(s->b2.ptr, w->b2, (uint64_t)O * 4, kind, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(s->density.ptr, 0, total * 4, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        delete s;
+        return hip_fail(ctx, e, "state create");
+    }
+    *out = s;
+    return NPA_OK;
+}
+
+void npa_state_destroy(npa_state* s) {
+    if (!s) return;
+    (void)hipSetDevice(s->ctx->device);
+    (void)hipStreamSynchronize(s->ctx->stream);
+    delete s;
+}
+
+npa_status npa_state_step(npa_state* s, uint32_t steps) {
+    if (!s) return NPA_ERR_INVALID_ARGUMENT;
+    npa_context* ctx = s->ctx;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint32_t S = s->model.state_dims;
+    npa::StepParams p = make_params(s->grid, opts_for_model(s->model), s->B, s->N, S);
+    apply_model(&p, s->model, s->grid.eps);
+    p.dt = s->dt;
+    p.update_prob = s->update_prob;
+    p.base_seed = base_seed(s->seed);
+    npa::StepIO io;
+    io.w1 = s->w1.as<float>();
+    io.b1 = s->b1.as<float>();
+    io.w2 = s->w2.as<float>();
+    io.b2 = s->b2.as<float>();
+    for (uint32_t k = 0; k < steps; ++k) {
+        const int c = s->cur;
+        p.step_index = (uint32_t)s->step_index;
+        io.pos = s->pos[c].as<float4>();
+        io.states = s->states[c].as<float>();
+        io.out_pos = s->pos[1 - c].as<float4>();
+        io.out_states = s->states[1 - c].as<float>();
+        NPA_HIP(ctx, npa::launch_hashgrid(s->plan, p.g, io.pos, io.states, S, s->B, s->N, s->ws, true, ctx->stream,
+                                          &ctx->prof),
+                "hashgrid");
+        NPA_HIP(ctx, npa::launch_density(p, s->ws, s->density.as<float>(), s->grid_blocks, ctx->stream, &ctx->prof),
+                "density");
+        NPA_HIP(ctx, npa::launch_update(p, s->ws, io, 0, s->grid_blocks, ctx->stream, &ctx->prof), "update");
+        s->cur = 1 - c;
+        s->step_index += 1;
+    }
+    return NPA_OK;
+}
+
+npa_status npa_state_read(npa_state* s, float* positions, float* states, float* density) {
+    if (!s) return NPA_ERR_INVALID_ARGUMENT;
+    npa_context* ctx = s->ctx;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint64_t total = (uint64_t)s->B * s->N;
+    const hipMemcpyKind kind = ctx->host_io ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+    if (positions) NPA_HIP(ctx, hipMemcpyAsync(positions, s->pos[s->cur].ptr, total * 16, kind, ctx->stream), "read pos");
+    if (states)
+        NPA_HIP(ctx, hipMemcpyAsync(states, s->states[s->cur].ptr, total * s->model.state_dims * 4, kind, ctx->stream),
+                "read states");
+    if (density) NPA_HIP(ctx, hipMemcpyAsync(density, s->density.ptr, total * 4, kind, ctx->stream), "read density");
+    return check_flags(ctx, s->ws);
+}
+
+npa_status npa_state_update_model(npa_state* s, const npa_weights* w) {
+    if (!s || !w) return NPA_ERR_INVALID_ARGUMENT;
+    npa_context* ctx = s->ctx;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const npa_model_cfg& m = s->model;
+    const uint32_t F = model_perception_dims(m), H = m.hidden_dims, O = m.spatial_dims + m.state_dims;
+    const hipMemcpyKind kind = ctx->host_io ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
+    if ((uint64_t)H * F) NPA_HIP(ctx, hipMemcpyAsync(s->w1.ptr, w->w1, (uint64_t)H * F * 4, kind, ctx->stream), "w1");
+    if (H) NPA_HIP(ctx, hipMemcpyAsync(s->b1.ptr, w->b1, (uint64_t)H * 4, kind, ctx->stream), "b1");
+    if ((uint64_t)O * H) NPA_HIP(ctx, hipMemcpyAsync(s->w2.ptr, w->w2, (uint64_t)O * H * 4, kind, ctx->stream), "w2");
+    NPA_HIP(ctx, hipMemcpyAsync(s->b2.ptr, w->b2, (uint64_t)O * 4, kind, ctx->stream), "b2");
+    if (ctx->host_io) NPA_HIP(ctx, hipStreamSynchronize(ctx->stream), "sync");
+    return NPA_OK;
+}
+
+npa_status npa_state_step_index(const npa_state* s, uint64_t* step_index) {
+    if (!s || !step_index) return NPA_ERR_INVALID_ARGUMENT;
+    *step_index = s->step_index;
+    return NPA_OK;
+}
+
+npa_status npa_state_buffers(npa_state* s, float** positions, float** states) {
+    if (!s) return NPA_ERR_INVALID_ARGUMENT;
+    if (positions) *positions = s->pos[s->cur].as<float>();
+    if (states) *states = s->states[s->cur].as<float>();
+    return NPA_OK;
+}
+
+npa_status npa_state_splat_2d(npa_state* s, const npa_splat2d_cfg* cfg, float* image) {
+    if (!s || !image) return NPA_ERR_INVALID_ARGUMENT;
+    npa_context* ctx = s->ctx;
+    npa_status st = check_splat(ctx, cfg);
+    if (st) return st;
+    if (s->model.state_dims < 3)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: splat colours need state_dims >= 3");
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint64_t total = (uint64_t)s->B * s->N;
+    if (total >= (1ull << 32)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: too many particles");
+    HostIO io(ctx);
+    float* img = io.out(image, (uint64_t)cfg->image_size * cfg->image_size * 16);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if (!aligned16(img)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: image must be 16-byte aligned");
+    NPA_HIP(ctx, npa::launch_splat_2d(s->pos[s->cur].as<float4>(), nullptr, s->states[s->cur].as<float>(),
+                                      s->model.state_dims, (uint32_t)total, *cfg, img, s->splat_ws, ctx->stream,
+                                      &ctx->prof),
+            "splat");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
+npa_status npa_state_decode_gaussians_3d(npa_state* s, const npa_gaussian_decode_cfg* cfg, float* pv, float* sh,
+                                         float* rot, float* so) {
+    if (!s) return NPA_ERR_INVALID_ARGUMENT;
+    npa_context* ctx = s->ctx;
+    const uint32_t S = s->model.state_dims;
+    npa_status st = check_decode(ctx, S, cfg);
+    if (st) return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint64_t total = (uint64_t)s->B * s->N;
+    const uint32_t K = cfg->mode == NPA_DECODE_SH0_ORIENTED ? (cfg->sh_degree + 1) * (cfg->sh_degree + 1) : 1;
+    HostIO io(ctx);
+    float* dpv = io.out(pv, total * 16);
+    float* dsh = io.out(sh, total * K * 12);
+    float* drot = io.out(rot, total * 16);
+    float* dso = io.out(so, total * 16);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if (!aligned16(dpv) || !aligned16(drot) || !aligned16(dso))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: 4-wide arrays must be 16-byte aligned");
+    NPA_HIP(ctx, npa::launch_decode_gaussians(s->pos[s->cur].as<float4>(), s->states[s->cur].as<float>(),
+                                              (uint32_t)total, S, *cfg, dpv, dsh, drot, dso, ctx->stream),
+            "decode");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
+npa_status npa_state_pair_counts(npa_state* s, uint64_t* candidates, uint64_t* pairs) {
+    if (!s) return NPA_ERR_INVALID_ARGUMENT;
+    npa_context* ctx = s->ctx;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint32_t S = s->model.state_dims;
+    npa::StepParams p = make_params(s->grid, opts_for_model(s->model), s->B, s->N, S);
+    NPA_HIP(ctx, npa::launch_hashgrid(s->plan, p.g, s->pos[s->cur].as<float4>(), s->states[s->cur].as<float>(), S,
+                                      s->B, s->N, s->ws, true, ctx->stream, nullptr),
+            "hashgrid");
+    NPA_HIP(ctx, hipMemsetAsync(s->ws.counters.ptr, 0, 16, ctx->stream), "zero counters");
+    NPA_HIP(ctx, npa::launch_count_pairs(p, s->ws, s->grid_blocks, s->ws.counters.as<unsigned long long>(), ctx->stream),
+            "count");
+    unsigned long long h[2] = {0, 0};
+    NPA_HIP(ctx, hipMemcpyAsync(h, s->ws.counters.ptr, 16, hipMemcpyDeviceToHost, ctx->stream), "readback");
+    NPA_HIP(ctx, hipStreamSynchronize(ctx->stream), "sync");
+    if (candidates) *candidates = h[0];
+    if (pairs) *pairs = h[1];
+    return NPA_OK;
+}
+
+// ================================================================== profiling
+npa_status npa_profile_enable(npa_context* ctx, int enable) {
+    if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
+    ctx->prof.enabled = enable != 0;
+    return NPA_OK;
+}
+
+npa_status npa_profile_reset(npa_context* ctx) {
+    if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
+    NPA_HIP(ctx, ctx->prof.collect(), "profile collect");
+    ctx->prof.reset();
+    return NPA_OK;
+}
+
+npa_status npa_profile_read(npa_context* ctx, int kernel_id, double* total_ms, uint64_t* launches) {
+    if (!ctx || kernel_id < 0 || kernel_id >= NPA_KERNEL_COUNT) return NPA_ERR_INVALID_ARGUMENT;
+    NPA_HIP(ctx, ctx->prof.collect(), "profile collect");
+    if (total_ms) *total_ms = ctx->prof.total_ms[kernel_id];
+    if (launches) *launches = ctx->prof.launches[kernel_id];
+    return NPA_OK;
+}
+
+}  // extern "C"
+
+// ============================================================ profiler impl
+namespace npa {
+
+hipEvent_t Profiler::get() {
+    if (!pool.empty()) {
+        hipEvent_t e = pool.back();
+        pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+void Profiler::begin(int kernel, hipStream_t s, hipEvent_t* ev) {
+    (void)kernel;
+    *ev = get();
+    if (*ev) (void)hipEventRecord(*ev, s);
+}
+
+void Profiler::end(int kernel, hipStream_t s, hipEvent_t a) {
+    hipEvent_t b = get();
+    if (!b) return;
+    (void)hipEventRecord(b, s);
+    pending.push_back({a, b, kernel});
+}
+
+hipError_t Profiler::collect() {
+    for (const Pair& p : pending) {
+        hipError_t e = hipEventSynchronize(p.b);
+        if (e != hipSuccess) return e;
+        float ms = 0.0f;
+        e = hipEventElapsedTime(&ms, p.a, p.b);
+        if (e != hipSuccess) return e;
+        total_ms[p.kernel] += ms;
+        launches[p.kernel] += 1;
+        pool.push_back(p.a);
+        pool.push_back(p.b);
+    }
+    pending.clear();
+    return hipSuccess;
+}
+
+void Profiler::reset() {
+    for (int k = 0; k < NPA_KERNEL_COUNT; ++k) {
+        total_ms[k] = 0.0;
+        launches[k] = 0;
+    }
+}
+
+Profiler::~Profiler() {
+    for (const Pair& p : pending) {
+        (void)hipEventDestroy(p.a);
+        (void)hipEventDestroy(p.b);
+    }
+    for (hipEvent_t e : pool) (void)hipEventDestroy(e);
+}
+
+}  // namespace npa

@@ -1,0 +1,344 @@
+// npa_decode.hip - Gaussian decode and tile-binned 2D splat on gfx950.
+//
+// decode_gaussians_3d  crates/burn_automata_kernels/src/gaussian.rs:53-223: a per-particle map.
+//
+// splat_particles_2d   crates/burn_automata_kernels/src/splat.rs:30-93, as a deterministic
+// tile-binned rasteriser:
+//   k_splat_prep   per particle: pixel-space centre, the in-bounds window weight sum
+//                  (the normaliser), colour, and how many 16x16 screen tiles the
+//                  (2r+1)^2 window touches;
+//   k_scan_1block  exclusive prefix of the per-particle tile counts;
+//   k_splat_emit   one (tile, particle) item per touched tile, in particle order;
+//   stable key sort of the items by tile (the hashgrid's counting sort) -> per-tile
+//                  particle lists in ascending particle index;
+//   k_splat_tiles  one 256-thread block per tile, one pixel per thread: the tile's list
+//                  is staged through LDS 256 particles at a time and each pixel adds its
+//                  weights in list order - the order the reference's serial loop adds them.
+#include <hip/hip_runtime.h>
+
+#include "npa_internal.hpp"
+
+namespace npa {
+
+// --------------------------------------------------------------- decode
+__global__ __launch_bounds__(256) void k_decode(const float4* __restrict__ pos, const float* __restrict__ states,
+                                                uint32_t count, uint32_t S, npa_gaussian_decode_cfg cfg,
+                                                uint32_t K, float* __restrict__ pv, float* __restrict__ sh,
+                                                float* __restrict__ rot, float* __restrict__ so) {
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= count) return;
+    const float* s = states + (uint64_t)idx * S;
+    const float4 p = pos[idx];
+    const uint32_t color_start = cfg.mode == NPA_DECODE_SH0_ORIENTED ? S - K * 3 : S - 3;
+    for (uint32_t k = 0; k < K; ++k) {  // decode_sh gaussian.rs:134-158
+        const uint32_t base = color_start + k * 3;
+        for (int ch = 0; ch < 3; ++ch)
+            sh[((uint64_t)idx * K + k) * 3 + ch] = clampf_(s[base + ch] + 0.5f, 0.0f, 1.0f);
+    }
+    float q[4] = {1.0f, 0.0f, 0.0f, 0.0f};
+    if (cfg.mode == NPA_DECODE_SH0_ORIENTED) {  // normalize_quat gaussian.rs:214-223
+        const uint32_t rs = color_start - 4;
+        q[0] = s[rs];
+        q[1] = s[rs + 1];
+        q[2] = s[rs + 2];
+        q[3] = s[rs + 3];
+        const float norm = sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
+        if (norm <= 1e-8f) {
+            q[0] = 1.0f;
+            q[1] = q[2] = q[3] = 0.0f;
+        } else {
+            for (int k = 0; k < 4; ++k) q[k] /= norm;
+        }
+    }
+    float o[4];
+    switch (cfg.mode) {  // decode_scale_opacity gaussian.rs:160-208
+        case NPA_DECODE_PARTICLE_POINT: {
+            const float sc = fmaxf(cfg.min_scale, 1.0e-6f);
+            o[0] = o[1] = o[2] = sc;
+            o[3] = 1.0f;
+        } break;
+        case NPA_DECODE_SH0_FIXED_SCALE: {
+            const float sc = clampf_(cfg.sigma, cfg.min_scale, cfg.max_scale);
+            o[0] = o[1] = o[2] = sc;
+            o[3] = clampf_(cfg.opacity_scale, cfg.min_opacity, cfg.max_opacity);
+        } break;
+        case NPA_DECODE_SH0_LEARNED_SCALE: {
+            const float scale_logit = clampf_(s[S - 5], -8.0f, 8.0f);
+            const float opacity_logit = clampf_(s[S - 4], -12.0f, 12.0f);
+            const float sc = clampf_(cfg.sigma * expf(scale_logit), cfg.min_scale, cfg.max_scale);
+            const float sig = 1.0f / (1.0f + expf(-opacity_logit));
+            const float op = clampf_(sig, cfg.min_opacity, cfg.max_opacity) * cfg.opacity_scale;
+            o[0] = o[1] = o[2] = sc;
+            o[3] = clampf_(op, cfg.min_opacity, cfg.max_opacity);
+        } break;
+        default: {
+            const uint32_t anis = color_start - 8;
+            const float ma = fmaxf(cfg.max_anisotropy, 1e-6f);
+            const float ax = tanhf(s[anis] / ma) * cfg.max_anisotropy;
+            const float ay = tanhf(s[anis + 1] / ma) * cfg.max_anisotropy;
+            const float az = tanhf(s[anis + 2] / ma) * cfg.max_anisotropy;
+            const float ol = tanhf(s[anis + 3] / ma) * cfg.max_anisotropy;
+            o[0] = clampf_(cfg.sigma * expf(ax), cfg.min_scale, cfg.max_scale);
+            o[1] = clampf_(cfg.sigma * expf(ay), cfg.min_scale, cfg.max_scale);
+            o[2] = clampf_(cfg.sigma * expf(az), cfg.min_scale, cfg.max_scale);
+            o[3] = clampf_(cfg.opacity_scale * expf(ol), cfg.min_opacity, cfg.max_opacity);
+        } break;
+    }
+    reinterpret_cast<float4*>(pv)[idx] = make_float4(p.x, p.y, p.z, 1.0f);
+    reinterpret_cast<float4*>(rot)[idx] = make_float4(q[0], q[1], q[2], q[3]);
+    reinterpret_cast<float4*>(so)[idx] = make_float4(o[0], o[1], o[2], o[3]);
+}
+
+hipError_t launch_decode_gaussians(const float4* pos, const float* states, uint32_t count, uint32_t S,
+                                   const npa_gaussian_decode_cfg& cfg, float* pv, float* sh, float* rot,
+                                   float* so, hipStream_t stream) {
+    if (count == 0) return hipSuccess;
+    const uint32_t K = cfg.mode == NPA_DECODE_SH0_ORIENTED ? (cfg.sh_degree + 1) * (cfg.sh_degree + 1) : 1;
+    hipLaunchKernelGGL(k_decode, dim3((count + 255) / 256), dim3(256), 0, stream, pos, states, count, S, cfg, K,
+                       pv, sh, rot, so);
+    return hipGetLastError();
+}
+
+// ----------------------------------------------------------------- splat
+constexpr int kTile = 16;
+
+struct SplatParams {
+    int size;
+    int radius;
+    int tiles_x, tiles_y;
+    float sigma;      // pixel-space sigma after the normalize_color rescale
+    float two_sig2;   // 2 * sigma * sigma
+    float norm_scale;
+    float lo, hi;
+    int normalize, y_up;
+    int S;
+};
+
+struct SplatParticle {  // 32 bytes
+    float fx, fy;
+    int bx, by;
+    float denom;
+    float c[3];
+};
+
+__device__ __forceinline__ bool splat_tiles(const SplatParams& P, int64_t bx, int64_t by, int* tx0, int* tx1,
+                                            int* ty0, int* ty1) {
+    int64_t x0 = bx - P.radius, x1 = bx + P.radius, y0 = by - P.radius, y1 = by + P.radius;
+    if (x0 < 0) x0 = 0;
+    if (y0 < 0) y0 = 0;
+    if (x1 > P.size - 1) x1 = P.size - 1;
+    if (y1 > P.size - 1) y1 = P.size - 1;
+    if (x0 > x1 || y0 > y1) return false;
+    *tx0 = (int)(x0 / kTile);
+    *tx1 = (int)(x1 / kTile);
+    *ty0 = (int)(y0 / kTile);
+    *ty1 = (int)(y1 / kTile);
+    return true;
+}
+
+__global__ __launch_bounds__(256) void k_splat_prep(SplatParams P, const float4* __restrict__ pos,
+                                                    const float* __restrict__ colors,
+                                                    const float* __restrict__ states, uint32_t count,
+                                                    SplatParticle* __restrict__ out,
+                                                    uint32_t* __restrict__ ntiles) {
+    const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= count) return;
+    const float4 p = pos[n];
+    const float fsz = (float)P.size;
+    const float px = (p.x - P.lo) / (P.hi - P.lo) * (fsz - 1.0f);
+    float py = (p.y - P.lo) / (P.hi - P.lo) * (fsz - 1.0f);
+    if (P.y_up) py = (fsz - 1.0f) - py;
+    const int64_t bx = f32_to_isize(floorf(px)), by = f32_to_isize(floorf(py));
+    const float fx = px - (float)bx, fy = py - (float)by;
+    int tx0, tx1, ty0, ty1;
+    const bool any = splat_tiles(P, bx, by, &tx0, &tx1, &ty0, &ty1);
+    float weight_sum = 0.0f;
+    if (any) {
+        for (int oy = -P.radius; oy <= P.radius; ++oy)
+            for (int ox = -P.radius; ox <= P.radius; ++ox) {
+                const int64_t x = bx + ox, y = by + oy;
+                if (x < 0 || y < 0 || x >= P.size || y >= P.size) continue;
+                const float dx = (float)ox - fx, dy = (float)oy - fy;
+                weight_sum += expf(-(dx * dx + dy * dy) / P.two_sig2);
+            }
+    }
+    SplatParticle sp;
+    sp.fx = fx;
+    sp.fy = fy;
+    sp.bx = any ? (int)bx : 0;
+    sp.by = any ? (int)by : 0;
+    sp.denom = P.normalize ? fmaxf(weight_sum, 1e-8f) : 1.0f;
+    if (colors) {
+        sp.c[0] = colors[3 * (uint64_t)n];
+        sp.c[1] = colors[3 * (uint64_t)n + 1];
+        sp.c[2] = colors[3 * (uint64_t)n + 2];
+    } else {  // infer_2d.rs:20-31
+        const float* s = states + (uint64_t)n * P.S + (P.S - 3);
+        for (int k = 0; k < 3; ++k) sp.c[k] = clampf_(s[k] + 0.5f, 0.0f, 1.0f);
+    }
+    out[n] = sp;
+    ntiles[n] = any ? (uint32_t)((tx1 - tx0 + 1) * (ty1 - ty0 + 1)) : 0u;
+}
+
+__global__ __launch_bounds__(1024) void k_scan_1block(const uint32_t* __restrict__ in, uint32_t* __restrict__ out,
+                                                      uint32_t count, uint32_t* __restrict__ total_out) {
+    __shared__ uint32_t lds[32];
+    const uint32_t per = (count + blockDim.x - 1) / blockDim.x;
+    const uint32_t k0 = threadIdx.x * per;
+    uint32_t sum = 0;
+    for (uint32_t k = k0; k < k0 + per && k < count; ++k) sum += in[k];
+    const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    uint32_t x = sum;
+    for (int off = 1; off < 64; off <<= 1) {
+        uint32_t y = __shfl_up(x, off, 64);
+        if (lane >= (uint32_t)off) x += y;
+    }
+    if (lane == 63) lds[wid] = x;
+    __syncthreads();
+    if (wid == 0) {
+        uint32_t s = lane < nw ? lds[lane] : 0;
+        for (int off = 1; off < 64; off <<= 1) {
+            uint32_t y = __shfl_up(s, off, 64);
+            if (lane >= (uint32_t)off) s += y;
+        }
+        if (lane < nw) lds[lane] = s;
+    }
+    __syncthreads();
+    uint32_t run = (wid ? lds[wid - 1] : 0) + x - sum;
+    for (uint32_t k = k0; k < k0 + per && k < count; ++k) {
+        out[k] = run;
+        run += in[k];
+    }
+    if (threadIdx.x == 0) *total_out = lds[nw - 1];
+}
+
+__global__ __launch_bounds__(256) void k_splat_emit(SplatParams P, const SplatParticle* __restrict__ sp,
+                                                    const uint32_t* __restrict__ ntiles,
+                                                    const uint32_t* __restrict__ start, uint32_t count,
+                                                    uint32_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+    const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= count || ntiles[n] == 0) return;
+    int tx0, tx1, ty0, ty1;
+    splat_tiles(P, sp[n].bx, sp[n].by, &tx0, &tx1, &ty0, &ty1);
+    uint32_t k = start[n];
+    for (int ty = ty0; ty <= ty1; ++ty)
+        for (int tx = tx0; tx <= tx1; ++tx) {
+            keys[k] = (uint32_t)(ty * P.tiles_x + tx);
+            vals[k] = n;
+            ++k;
+        }
+}
+
+__global__ __launch_bounds__(256) void k_splat_tiles(SplatParams P, const SplatParticle* __restrict__ sp,
+                                                     const uint32_t* __restrict__ offsets,
+                                                     const uint32_t* __restrict__ sorted, float* __restrict__ image) {
+    __shared__ SplatParticle buf[256];
+    const uint32_t t = blockIdx.x;
+    const int tx = (int)(t % P.tiles_x), ty = (int)(t / P.tiles_x);
+    const int x = tx * kTile + (int)(threadIdx.x % kTile);
+    const int y = ty * kTile + (int)(threadIdx.x / kTile);
+    const uint32_t beg = offsets[t], end = offsets[t + 1];
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t base = beg; base < end; base += 256) {
+        const uint32_t k = base + threadIdx.x;
+        if (k < end) buf[threadIdx.x] = sp[sorted[k]];
+        __syncthreads();
+        const uint32_t m = end - base < 256 ? end - base : 256;
+        for (uint32_t q = 0; q < m; ++q) {
+            const SplatParticle& p = buf[q];
+            const int ox = x - p.bx, oy = y - p.by;
+            if (ox < -P.radius || ox > P.radius || oy < -P.radius || oy > P.radius) continue;
+            const float dx = (float)ox - p.fx, dy = (float)oy - p.fy;
+            float w = expf(-(dx * dx + dy * dy) / P.two_sig2);
+            w = w / p.denom * P.norm_scale;
+            acc[0] += p.c[0] * w;
+            acc[1] += p.c[1] * w;
+            acc[2] += p.c[2] * w;
+            acc[3] += w;
+        }
+        __syncthreads();
+    }
+    if (x < P.size && y < P.size)
+        reinterpret_cast<float4*>(image)[(uint64_t)y * P.size + x] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+}
+
+void SplatWorkspace::release() {
+    for (DevBuf* b : {&params, &item_start, &keys, &vals, &sorted, &ranks, &table, &totals, &offsets, &count, &flags})
+        b->release();
+}
+
+hipError_t launch_splat_2d(const float4* pos, const float* colors, const float* states, uint32_t S,
+                           uint32_t count, const npa_splat2d_cfg& cfg, float* image, SplatWorkspace& ws,
+                           hipStream_t stream, Profiler* prof) {
+    SplatParams P{};
+    P.size = (int)cfg.image_size;
+    const float fsz = (float)cfg.image_size;
+    float sigma = cfg.sigma;  // splat.rs:36-46
+    if (cfg.normalize_color) sigma = sigma * fsz * cfg.pixel_size / (cfg.hi - cfg.lo);
+    float rf = ceilf(5.0f * sigma);
+    if (!(rf >= 1.0f)) rf = rf != rf ? 1.0f : 1.0f;
+    if (rf > 4096.0f) rf = 4096.0f;  // windows wider than any supported image are clipped anyway
+    P.radius = (int)rf;
+    P.sigma = sigma;
+    P.two_sig2 = 2.0f * sigma * sigma;
+    P.norm_scale = 1.0f;
+    if (cfg.normalize_color) {
+        const float t = fsz * cfg.pixel_size / (cfg.hi - cfg.lo);
+        P.norm_scale = t * t;
+    }
+    P.lo = cfg.lo;
+    P.hi = cfg.hi;
+    P.normalize = cfg.normalize_color ? 1 : 0;
+    P.y_up = cfg.y_up ? 1 : 0;
+    P.S = (int)S;
+    P.tiles_x = (P.size + kTile - 1) / kTile;
+    P.tiles_y = P.tiles_x;
+    const uint32_t ntile_total = (uint32_t)(P.tiles_x * P.tiles_y);
+    const uint64_t per_axis = (uint64_t)((2 * P.radius + 1 + kTile - 1) / kTile + 1);
+    const uint64_t max_per = std::min<uint64_t>(per_axis * per_axis, ntile_total);
+    const uint64_t cap64 = (uint64_t)count * max_per;
+    if (cap64 >= (1ull << 31)) return hipErrorInvalidValue;
+    const uint32_t cap = (uint32_t)cap64;
+    HashgridPlan plan;
+    if (!make_key_sort_plan(cap, ntile_total, &plan)) return hipErrorInvalidValue;
+    hipError_t e;
+#define NPA_RES(buf, n) \
+    if ((e = (buf).reserve((size_t)(n))) != hipSuccess) return e;
+    NPA_RES(ws.params, (uint64_t)(count ? count : 1) * sizeof(SplatParticle));
+    NPA_RES(ws.item_start, (uint64_t)(count ? count : 1) * 8);
+    NPA_RES(ws.keys, (uint64_t)(cap ? cap : 1) * 4);
+    NPA_RES(ws.vals, (uint64_t)(cap ? cap : 1) * 4);
+    NPA_RES(ws.sorted, (uint64_t)(cap ? cap : 1) * 4);
+    NPA_RES(ws.ranks, (uint64_t)(cap ? cap : 1) * 4);
+    NPA_RES(ws.table, plan.table_entries * 4);
+    NPA_RES(ws.totals, (uint64_t)ntile_total * 4);
+    NPA_RES(ws.offsets, ((uint64_t)ntile_total + 1) * 4);
+    NPA_RES(ws.count, 64);
+    NPA_RES(ws.flags, 64);
+#undef NPA_RES
+    ProfScope ps(prof, NPA_KERNEL_SPLAT, stream);
+    uint32_t* ntiles = ws.item_start.as<uint32_t>() + (count ? count : 1);
+    uint32_t* start = ws.item_start.as<uint32_t>();
+    if (count) {
+        hipLaunchKernelGGL(k_splat_prep, dim3((count + 255) / 256), dim3(256), 0, stream, P, pos, colors, states,
+                           count, ws.params.as<SplatParticle>(), ntiles);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(k_scan_1block, dim3(1), dim3(1024), 0, stream, ntiles, start, count, ws.count.as<uint32_t>());
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (count) {
+        hipLaunchKernelGGL(k_splat_emit, dim3((count + 255) / 256), dim3(256), 0, stream, P,
+                           ws.params.as<SplatParticle>(), ntiles, start, count, ws.keys.as<uint32_t>(),
+                           ws.vals.as<uint32_t>());
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    e = launch_key_sort(plan, ws.keys.as<uint32_t>(), ws.vals.as<uint32_t>(), ws.count.as<uint32_t>(), cap,
+                        ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(), ws.totals.as<uint32_t>(),
+                        ws.offsets.as<uint32_t>(), ws.sorted.as<uint32_t>(), ws.flags.as<uint32_t>(), stream);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_splat_tiles, dim3(ntile_total), dim3(256), 0, stream, P, ws.params.as<SplatParticle>(),
+                       ws.offsets.as<uint32_t>(), ws.sorted.as<uint32_t>(), image);
+    return hipGetLastError();
+}
+
+}  // namespace npa

@@ -1,0 +1,236 @@
+// npa_device.hpp - device-side building blocks shared by the NPA kernels (gfx950, wave64).
+//
+// Numerics: every expression keeps the association order of the reference Rust
+// source it follows (cited per function) and the library is compiled with
+// -ffp-contract=off, so no a*b+c is fused. f32 division and sqrt are the
+// IEEE-correct sequences hipcc emits by default.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "npa_math.hpp"
+
+namespace npa {
+
+constexpr int kWave = 64;
+
+// Uniform parameters of a hashgrid (HashGridConfig plus derived constants).
+struct GridParams {
+    int dim;         // 2 or 3
+    int boundary;    // 0 periodic, 1 clamped
+    int mode;        // 0 grid, 1 particle
+    uint32_t size[3];
+    uint32_t cells;  // cells per system
+    float eps;
+    float eps2;      // eps * eps
+    float extent[3]; // size[a] as f32 * eps
+    float half[3];   // extent * 0.5
+    float k6;        // poly6 normalisation
+    float k5;        // spiky-gradient normalisation
+};
+
+// Rust `f as isize` of a floored f32: saturating, NaN -> 0.
+__device__ __forceinline__ int64_t f32_to_isize(float f) {
+    if (f != f) return 0;
+    if (f >= 9223372036854775808.0f) return INT64_MAX;
+    if (f <= -9223372036854775808.0f) return INT64_MIN;
+    return (int64_t)f;
+}
+
+__device__ __forceinline__ int64_t rem_euclid_i64(int64_t a, int64_t m) {
+    int64_t r = a % m;
+    return r < 0 ? r + m : r;
+}
+
+// mix_coord  crates/burn_automata_kernels/src/hashgrid.rs:155-163
+__device__ __forceinline__ uint32_t mix_coord(int64_t value, uint32_t salt) {
+    uint32_t x = ((uint32_t)(int32_t)value) ^ salt;
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+// particle_cell_hash  hashgrid.rs:147-153
+__device__ __forceinline__ uint32_t particle_hash(int64_t c0, int64_t c1, int64_t c2, const GridParams& g) {
+    uint32_t h = mix_coord(c0, 0x9e3779b9u) ^ mix_coord(c1, 0x85ebca6bu);
+    if (g.dim == 3) h ^= mix_coord(c2, 0xc2b2ae35u);
+    return h % g.cells;
+}
+
+// Largest |coordinate| the device path stores exactly in an i32 and can offset by +-1.
+constexpr int64_t kCoordLimit = (int64_t)1 << 30;
+
+// cell_coords_for_position  hashgrid.rs:98-121. Sets *overflow when a Particle-mode
+// coordinate leaves +-2^30 (the i32 records would no longer be exact).
+__device__ __forceinline__ void cell_coords(const float* p, const GridParams& g, int64_t c[3], bool* overflow) {
+    c[0] = c[1] = c[2] = 0;
+    for (int a = 0; a < g.dim; ++a) {
+        if (g.mode == 1) {
+            int64_t v = f32_to_isize(floorf(p[a] / g.eps));
+            if (v > kCoordLimit || v < -kCoordLimit) *overflow = true;
+            c[a] = v;
+            continue;
+        }
+        int64_t size = (int64_t)g.size[a];
+        int64_t cell = f32_to_isize(floorf((p[a] + g.half[a]) / g.eps));
+        if (g.boundary == 0) {
+            cell = rem_euclid_i64(cell, size);
+        } else {
+            if (cell < 0) cell = 0;
+            if (cell > size - 1) cell = size - 1;
+        }
+        c[a] = cell;
+    }
+}
+
+// cell_index_from_coords  hashgrid.rs:123-145 (false = None).
+__device__ __forceinline__ bool cell_index(int64_t c0, int64_t c1, int64_t c2, const GridParams& g, uint32_t* out) {
+    if (g.mode == 1) {
+        *out = particle_hash(c0, c1, c2, g);
+        return true;
+    }
+    int64_t cs[3] = {c0, c1, c2};
+    uint32_t stride = 1, hash = 0;
+    for (int a = 0; a < g.dim; ++a) {
+        int64_t size = (int64_t)g.size[a];
+        int64_t cell;
+        if (g.boundary == 0) {
+            cell = rem_euclid_i64(cs[a], size);
+        } else {
+            if (cs[a] < 0 || cs[a] >= size) return false;
+            cell = cs[a];
+        }
+        hash += (uint32_t)cell * stride;
+        stride *= (uint32_t)size;
+    }
+    *out = hash;
+    return true;
+}
+
+// cell_for_position  hashgrid.rs:71-96 (coords as computed above).
+__device__ __forceinline__ uint32_t cell_of_coords(const int64_t c[3], const GridParams& g) {
+    uint32_t out = 0;
+    cell_index(c[0], c[1], c[2], g, &out);  // in-range by construction for Grid mode
+    return out;
+}
+
+// neighbor_delta  hashgrid.rs:165-181, component a.
+__device__ __forceinline__ float delta_axis(float pi, float pj, int a, const GridParams& g) {
+    float v = pj - pi;
+    if (g.boundary == 0) {
+        if (v > g.half[a]) v -= g.extent[a];
+        else if (v < -g.half[a]) v += g.extent[a];
+    }
+    return v;
+}
+
+// smoothing_poly6_kernel  crates/burn_automata_kernels/src/reference/kernels.rs:51-58
+__device__ __forceinline__ float poly6(float r2, const GridParams& g) {
+    if (r2 >= g.eps2) return 0.0f;
+    float x = g.eps2 - r2;
+    return g.k6 * x * x * x;
+}
+
+// RecipFinite::recip_finite  kernels.rs:146-154
+__device__ __forceinline__ float recip_finite(float x) {
+    if (fabsf(x) <= 1e-20f || !isfinite(x)) return 0.0f;
+    return 1.0f / x;
+}
+
+// log_normalize_vector  crates/burn_automata_kernels/src/reference/normalize.rs:60-69
+template <int N>
+__device__ __forceinline__ void log_normalize(float* v) {
+    const float E = 1.0e-6f;
+    float s = v[0] * v[0];
+#pragma unroll
+    for (int k = 1; k < N; ++k) s += v[k] * v[k];
+    float norm = fmaxf(sqrtf(s + E * E), E);
+    float scale = npa_log1pf(norm) / norm;  // host-libm-identical log1pf (npa_math.hpp)
+#pragma unroll
+    for (int k = 0; k < N; ++k) v[k] *= scale;
+}
+
+// safe_inverse_symmetric  kernels.rs:3-49 (row-major D x D in, out)
+template <int D>
+__device__ __forceinline__ void safe_inverse(const float* m, float* out) {
+    const float TOL = 1e-3f;
+#pragma unroll
+    for (int k = 0; k < D * D; ++k) out[k] = 0.0f;
+    if constexpr (D == 2) {
+        float a = m[0], b = m[1], d = m[3];
+        float det = a * d - b * b;
+        if (fabsf(det) < TOL) {
+            out[0] = 1.0f;
+            out[3] = 1.0f;
+            return;
+        }
+        float inv = 1.0f / det;
+        out[0] = d * inv;
+        out[1] = -b * inv;
+        out[2] = -b * inv;
+        out[3] = a * inv;
+    } else {
+        float a = m[0], b = m[1], c = m[2], d = m[4], e = m[5], f = m[8];
+        float t1 = d * f - e * e;
+        float t2 = c * e - b * f;
+        float t3 = b * e - c * d;
+        float det = a * t1 + b * t2 + c * t3;
+        if (fabsf(det) < TOL) {
+            out[0] = 1.0f;
+            out[4] = 1.0f;
+            out[8] = 1.0f;
+            return;
+        }
+        float inv = 1.0f / det;
+        out[0] = t1 * inv;
+        out[1] = t2 * inv;
+        out[2] = t3 * inv;
+        out[3] = t2 * inv;
+        out[4] = (a * f - c * c) * inv;
+        out[5] = (b * c - a * e) * inv;
+        out[6] = t3 * inv;
+        out[7] = (b * c - a * e) * inv;
+        out[8] = (a * d - b * b) * inv;
+    }
+}
+
+// hash_u32 / random01  crates/burn_automata/src/gpu_step.wgsl:1019-1031
+__device__ __forceinline__ uint32_t hash_u32(uint32_t x) {
+    x = (x ^ 61u) ^ (x >> 16);
+    x = x + (x << 3);
+    x = x ^ (x >> 4);
+    x = x * 0x27d4eb2du;
+    x = x ^ (x >> 15);
+    return x;
+}
+
+__device__ __forceinline__ float random01(uint32_t particle, uint32_t step, uint32_t seed) {
+    uint32_t mixed = hash_u32(particle ^ hash_u32(step + 0x9e3779b9u) ^ seed);
+    return (float)(mixed >> 8) * (1.0f / 16777216.0f);
+}
+
+// update_mask  gpu_step.wgsl:1033-1056 with lane seed base ^ (lane * N).
+__device__ __forceinline__ float hash_mask(uint32_t local, uint32_t lane, uint32_t particle_count,
+                                           float p, uint32_t step, uint32_t base_seed) {
+    if (p >= 1.0f) return 1.0f;
+    if (p <= 0.0f) return 0.0f;
+    uint32_t seed = base_seed ^ (lane * particle_count);
+    return random01(local, step, seed) < p ? 1.0f : 0.0f;
+}
+
+__device__ __forceinline__ float clampf_(float v, float lo, float hi) {  // f32::clamp
+    if (v < lo) v = lo;
+    if (v > hi) v = hi;
+    return v;
+}
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+    uint32_t lane = __lane_id();
+    return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+}  // namespace npa

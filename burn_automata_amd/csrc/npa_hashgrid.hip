@@ -1,0 +1,552 @@
+// npa_hashgrid.hip - stable counting-sort hashgrid build on gfx950.
+//
+// Replaces build_hashgrid (crates/burn_automata_kernels/src/hashgrid.rs:16-69), bit-exact:
+// bin_offsets = exclusive prefix of per-bin counts, and inside each bin the particles
+// keep ascending original index (the reference's serial stable scatter).
+//
+// Four kernels per build:
+//   k_hash_rank    one block = one tile of `waves*R*64` consecutive particles of one
+//                  system. Each wave walks its contiguous slice in rounds of 64: the cell
+//                  key of each lane, its peers (lanes with the same key) from
+//                  ceil(log2 C) wavefront ballots, the rank among peers by popcount, and
+//                  a per-wave LDS counter per key (u16) carried across rounds. After a
+//                  barrier, ranks are offset by the earlier waves' counters and the tile's
+//                  per-key histogram row is written to table[tile][key].
+//   k_table_scan   per key, exclusive prefix over the system's tiles (column scan).
+//   k_offsets_scan per system, exclusive prefix over keys -> bin_offsets; also emits
+//                  the wave work list (one item per <=64 consecutive slots of a bin).
+//   k_scatter      dst = bin_offsets[key] + table[tile][key] + rank; writes the
+//                  permutation, its inverse and (for the rollout step) the sorted particle
+//                  records and state rows the neighbour passes read.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "npa_internal.hpp"
+
+namespace npa {
+
+// ------------------------------------------------------------------ DevBuf
+hipError_t DevBuf::reserve(size_t want) {
+    if (want <= bytes && ptr) return hipSuccess;
+    release();
+    size_t b = want ? want : 16;
+    hipError_t e = hipMalloc(&ptr, b);
+    if (e != hipSuccess) {
+        ptr = nullptr;
+        bytes = 0;
+        return e;
+    }
+    bytes = b;
+    return hipSuccess;
+}
+
+void DevBuf::release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+}
+
+hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t batch,
+                              uint32_t state_dims, int dim) {
+    hipError_t e;
+    const uint64_t t1 = total ? total : 1;
+    const uint64_t bins = (uint64_t)batch * plan.cells;
+#define NPA_RES(buf, n)                                 \
+    if ((e = (buf).reserve((size_t)(n))) != hipSuccess) \
+        return e;
+    NPA_RES(keys, t1 * 4);
+    NPA_RES(ranks, t1 * 4);
+    NPA_RES(table, (plan.table_entries ? plan.table_entries : 1) * 4);
+    NPA_RES(totals, (bins ? bins : 1) * 4);
+    NPA_RES(bin_offsets, (bins + 1) * 4);
+    NPA_RES(perm, t1 * 4);
+    NPA_RES(inv, t1 * 4);
+    NPA_RES(wl_count, 64);
+    NPA_RES(worklist, (plan.worklist_cap + 1) * 8);
+    NPA_RES(srec, t1 * 16);
+    NPA_RES(scoord, dim == 3 ? t1 * 16 : 16);
+    NPA_RES(sstate, t1 * (uint64_t)(state_dims ? state_dims : 1) * 4);
+    NPA_RES(svol, t1 * 4);
+    NPA_RES(counters, 64);
+#undef NPA_RES
+    if (!flags.ptr) {
+        if ((e = flags.reserve(64)) != hipSuccess) return e;
+        if ((e = hipMemset(flags.ptr, 0, 64)) != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+void Workspace::release() {
+    for (DevBuf* b : {&keys, &ranks, &table, &totals, &bin_offsets, &perm, &inv, &flags, &wl_count,
+                      &worklist, &srec, &scoord, &sstate, &svol, &counters})
+        b->release();
+}
+
+// ------------------------------------------------------------------- plan
+float host_powi(float x, int n) {  // f32::powi, see oracle powi_f32 for the derivation
+    bool recip = n < 0;
+    unsigned b = (unsigned)(recip ? -n : n);
+    float r = 1.0f;
+    for (;;) {
+        if (b & 1u) r *= x;
+        b >>= 1;
+        if (b == 0) break;
+        x *= x;
+    }
+    return recip ? 1.0f / r : r;
+}
+
+GridParams make_grid_params(const npa_grid_cfg& cfg) {
+    GridParams g{};
+    g.dim = (int)cfg.dim;
+    g.boundary = (int)cfg.boundary;
+    g.mode = (int)cfg.mode;
+    uint32_t cells = 1;
+    for (int a = 0; a < 3; ++a) g.size[a] = cfg.grid_size[a];
+    for (uint32_t a = 0; a < cfg.dim; ++a) cells *= cfg.grid_size[a];
+    g.cells = cells;
+    g.eps = cfg.eps;
+    g.eps2 = cfg.eps * cfg.eps;
+    for (int a = 0; a < 3; ++a) {
+        g.extent[a] = (float)cfg.grid_size[a] * cfg.eps;
+        g.half[a] = g.extent[a] * 0.5f;
+    }
+    const float PI_F = 3.14159265358979323846f;
+    // smoothing_poly6_normalization / gradient_spiky_normalization kernels.rs:126-140
+    if (cfg.dim == 2) {
+        g.k6 = 4.0f / (PI_F * host_powi(cfg.eps, 8));
+        g.k5 = 10.0f / (PI_F * host_powi(cfg.eps, 5));
+    } else {
+        g.k6 = 315.0f / (64.0f * PI_F * host_powi(cfg.eps, 9));
+        g.k5 = 15.0f / (PI_F * host_powi(cfg.eps, 6));
+    }
+    return g;
+}
+
+bool make_plan(const npa_grid_cfg& cfg, uint32_t batch, uint32_t n, HashgridPlan* plan,
+               std::string* err) {
+    uint64_t cells = 1;
+    for (uint32_t a = 0; a < cfg.dim; ++a) cells *= cfg.grid_size[a];
+    if (cells > 65536) {
+        *err = "device hashgrid supports at most 65536 cells per system, got " + std::to_string(cells);
+        return false;
+    }
+    const uint64_t total = (uint64_t)batch * n;
+    if (total >= (1ull << 31) || (uint64_t)batch * cells + 1 >= (1ull << 32)) {
+        *err = "batch_size * particle_count and batch_size * cell_count must stay below 2^31";
+        return false;
+    }
+    HashgridPlan p;
+    p.cells = (uint32_t)cells;
+    p.key_bits = cells <= 1 ? 0 : 32 - __builtin_clz((uint32_t)cells - 1);
+    p.waves = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(4, 32768 / cells));
+    p.lds_bytes = p.waves * p.cells * 2;
+    const uint64_t budget = std::max<uint64_t>(2 * (uint64_t)n, cells);
+    uint32_t rounds = 1;
+    while (rounds < 32) {
+        uint64_t tile = (uint64_t)p.waves * rounds * 64;
+        uint64_t tiles = (n + tile - 1) / tile;
+        if (tiles * cells <= budget) break;
+        rounds *= 2;
+    }
+    p.rounds = rounds;
+    p.tile = p.waves * rounds * 64;
+    p.tiles_per_sys = std::max<uint32_t>(1, (n + p.tile - 1) / p.tile);
+    p.table_entries = (uint64_t)batch * p.tiles_per_sys * cells;
+    if (p.table_entries >= (1ull << 32)) {
+        *err = "hashgrid tile table exceeds 2^32 entries";
+        return false;
+    }
+    p.worklist_cap = (total + 63) / 64 + std::min<uint64_t>(total, (uint64_t)batch * cells) + 1;
+    *plan = p;
+    return true;
+}
+
+// ---------------------------------------------------------------- kernels
+// keys_in == nullptr: keys are the cells of `pos` (hashgrid build); otherwise the keys
+// are read from keys_in and the item count from *d_count (a device-resident count
+// bounded by the tiles the grid covers).
+template <int R>
+__global__ __launch_bounds__(256) void k_hash_rank(const float4* __restrict__ pos,
+                                                   const uint32_t* __restrict__ keys_in,
+                                                   const uint32_t* __restrict__ d_count, uint32_t n,
+                                                   uint32_t tiles_per_sys, uint32_t waves,
+                                                   GridParams g, uint32_t key_bits,
+                                                   uint32_t* __restrict__ keys,
+                                                   uint32_t* __restrict__ ranks,
+                                                   uint32_t* __restrict__ table,
+                                                   uint32_t* __restrict__ flags,
+                                                   uint32_t* __restrict__ wl_count) {
+    extern __shared__ uint16_t cnt[];
+    const uint32_t C = g.cells;
+    const uint32_t tile = blockIdx.x;
+    const uint32_t b = tile / tiles_per_sys;
+    const uint32_t t = tile - b * tiles_per_sys;
+    const uint64_t sys_start = (uint64_t)b * n;
+    if (d_count) {
+        const uint32_t dc = *d_count;
+        n = dc < n ? dc : n;
+    }
+    const uint32_t nwords = waves * C;
+    for (uint32_t k = threadIdx.x; k < nwords; k += blockDim.x) cnt[k] = 0;
+    if (wl_count && tile == 0 && threadIdx.x == 0) *wl_count = 0;
+    __syncthreads();
+
+    const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    volatile uint16_t* mine = cnt + w * C;
+    const uint32_t wave_start = t * (waves * R * 64) + w * (R * 64);
+    const uint64_t lt = lanemask_lt();
+    uint32_t key_r[R], rank_r[R];
+    bool ovf = false;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t li = wave_start + r * 64 + lane;
+        const bool active = li < n;
+        uint32_t key = 0;
+        if (active) {
+            if (keys_in) {
+                key = keys_in[sys_start + li];
+            } else {
+                float4 p4 = pos[sys_start + li];
+                float p[4] = {p4.x, p4.y, p4.z, p4.w};
+                int64_t c[3];
+                cell_coords(p, g, c, &ovf);
+                key = cell_of_coords(c, g);
+            }
+        }
+        uint64_t peers = __ballot(active);
+        for (uint32_t bit = 0; bit < key_bits; ++bit) {
+            const uint32_t v = (key >> bit) & 1u;
+            const uint64_t m = __ballot(v);
+            peers &= v ? m : ~m;
+        }
+        uint32_t rank = 0;
+        if (active) {
+            const uint32_t below = (uint32_t)__popcll(peers & lt);
+            const uint32_t base = mine[key];
+            rank = base + below;
+            if ((peers >> lane) == 1ull) mine[key] = (uint16_t)(base + (uint32_t)__popcll(peers));
+        }
+        key_r[r] = key;
+        rank_r[r] = rank;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t li = wave_start + r * 64 + lane;
+        if (li < n) {
+            uint32_t prefix = 0;
+            for (uint32_t w2 = 0; w2 < w; ++w2) prefix += cnt[w2 * C + key_r[r]];
+            if (!keys_in) keys[sys_start + li] = key_r[r];
+            ranks[sys_start + li] = prefix + rank_r[r];
+        }
+    }
+    uint32_t* row = table + (uint64_t)tile * C;
+    for (uint32_t k = threadIdx.x; k < C; k += blockDim.x) {
+        uint32_t tot = 0;
+        for (uint32_t w2 = 0; w2 < waves; ++w2) tot += cnt[w2 * C + k];
+        row[k] = tot;
+    }
+    if (ovf) atomicOr(flags, 1u);
+}
+
+__global__ __launch_bounds__(256) void k_table_scan(uint32_t* __restrict__ table,
+                                                    uint32_t* __restrict__ totals, uint32_t C,
+                                                    uint32_t tiles_per_sys) {
+    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t b = blockIdx.y;
+    if (k >= C) return;
+    uint32_t* col = table + (uint64_t)b * tiles_per_sys * C + k;
+    uint32_t run = 0;
+    uint32_t t = 0;
+    for (; t + 4 <= tiles_per_sys; t += 4) {
+        uint32_t v0 = col[(uint64_t)(t + 0) * C], v1 = col[(uint64_t)(t + 1) * C];
+        uint32_t v2 = col[(uint64_t)(t + 2) * C], v3 = col[(uint64_t)(t + 3) * C];
+        col[(uint64_t)(t + 0) * C] = run;
+        run += v0;
+        col[(uint64_t)(t + 1) * C] = run;
+        run += v1;
+        col[(uint64_t)(t + 2) * C] = run;
+        run += v2;
+        col[(uint64_t)(t + 3) * C] = run;
+        run += v3;
+    }
+    for (; t < tiles_per_sys; ++t) {
+        uint32_t v = col[(uint64_t)t * C];
+        col[(uint64_t)t * C] = run;
+        run += v;
+    }
+    totals[(uint64_t)b * C + k] = run;
+}
+
+// Exclusive scan of one value per thread over a 1024-thread block.
+__device__ __forceinline__ uint32_t block_scan_1024(uint32_t v, uint32_t* lds, uint32_t* total) {
+    const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const uint32_t nw = blockDim.x >> 6;
+    uint32_t x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        uint32_t y = __shfl_up(x, off, 64);
+        if (lane >= (uint32_t)off) x += y;
+    }
+    if (lane == 63) lds[wid] = x;
+    __syncthreads();
+    if (wid == 0) {
+        uint32_t s = lane < nw ? lds[lane] : 0;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            uint32_t y = __shfl_up(s, off, 64);
+            if (lane >= (uint32_t)off) s += y;
+        }
+        if (lane < nw) lds[lane] = s;
+    }
+    __syncthreads();
+    const uint32_t wave_prefix = wid ? lds[wid - 1] : 0;
+    *total = lds[nw - 1];
+    __syncthreads();
+    return wave_prefix + x - v;
+}
+
+__global__ __launch_bounds__(1024) void k_offsets_scan(const uint32_t* __restrict__ totals,
+                                                       uint32_t* __restrict__ bin_offsets,
+                                                       uint32_t C, uint32_t n, uint32_t batch,
+                                                       uint2* __restrict__ worklist,
+                                                       uint32_t* __restrict__ wl_count,
+                                                       int emit_work) {
+    __shared__ uint32_t lds[32];
+    __shared__ uint32_t wl_base;
+    const uint32_t b = blockIdx.x;
+    const uint32_t per = (C + blockDim.x - 1) / blockDim.x;
+    const uint32_t k0 = threadIdx.x * per;
+    const uint32_t* tot = totals + (uint64_t)b * C;
+    uint32_t sum_c = 0, sum_i = 0;
+    for (uint32_t k = k0; k < k0 + per && k < C; ++k) {
+        uint32_t c = tot[k];
+        sum_c += c;
+        sum_i += (c + 63) / 64;
+    }
+    uint32_t all_c, all_i;
+    uint32_t pre_c = block_scan_1024(sum_c, lds, &all_c);
+    uint32_t pre_i = block_scan_1024(sum_i, lds, &all_i);
+    if (emit_work && threadIdx.x == 0) wl_base = atomicAdd(wl_count, all_i);
+    __syncthreads();
+    const uint32_t sys_base = b * n;
+    uint32_t run_c = pre_c, run_i = emit_work ? wl_base + pre_i : 0;
+    for (uint32_t k = k0; k < k0 + per && k < C; ++k) {
+        uint32_t c = tot[k];
+        bin_offsets[(uint64_t)b * C + k] = sys_base + run_c;
+        if (emit_work) {
+            for (uint32_t m = 0; m * 64 < c; ++m) {
+                uint32_t cnt = c - m * 64;
+                worklist[run_i++] = make_uint2(sys_base + run_c + m * 64, cnt < 64 ? cnt : 64);
+            }
+        }
+        run_c += c;
+    }
+    // last entry = total count (every system holds n entries when the counts are per system)
+    if (b == batch - 1 && threadIdx.x == 0) bin_offsets[(uint64_t)batch * C] = sys_base + all_c;
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void k_scatter(
+    const float4* __restrict__ pos, const float* __restrict__ states, uint32_t S, uint32_t n,
+    uint32_t total, uint32_t tile, uint32_t tiles_per_sys, GridParams g,
+    const uint32_t* __restrict__ keys, const uint32_t* __restrict__ ranks,
+    const uint32_t* __restrict__ table, const uint32_t* __restrict__ bin_offsets,
+    uint32_t* __restrict__ perm, uint32_t* __restrict__ inv, float4* __restrict__ srec,
+    int4* __restrict__ scoord, float* __restrict__ sstate, int payload) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const uint32_t C = g.cells;
+    const uint32_t b = i / n;
+    const uint32_t li = i - b * n;
+    const uint32_t t = li / tile;
+    const uint32_t key = keys[i];
+    const uint32_t dst_local = (bin_offsets[(uint64_t)b * C + key] - b * n) +
+                               table[((uint64_t)b * tiles_per_sys + t) * C + key] + ranks[i];
+    const uint32_t dst = b * n + dst_local;
+    perm[dst] = li;
+    inv[i] = dst_local;
+    if (!payload) return;
+    const float4 p4 = pos[i];
+    float p[4] = {p4.x, p4.y, p4.z, p4.w};
+    int64_t c[3];
+    bool ovf = false;
+    cell_coords(p, g, c, &ovf);
+    if (D == 2) {
+        srec[dst] = make_float4(p4.x, p4.y, __int_as_float((int)c[0]), __int_as_float((int)c[1]));
+    } else {
+        srec[dst] = p4;
+        scoord[dst] = make_int4((int)c[0], (int)c[1], (int)c[2], (int)i);
+    }
+    if (!states) return;  // neighbour-list export needs positions only
+    const float* src = states + (uint64_t)i * S;
+    float* out = sstate + (uint64_t)dst * S;
+    if ((S & 3u) == 0) {
+        const float4* s4 = reinterpret_cast<const float4*>(src);
+        float4* o4 = reinterpret_cast<float4*>(out);
+        for (uint32_t q = 0; q < S / 4; ++q) o4[q] = s4[q];
+    } else {
+        for (uint32_t q = 0; q < S; ++q) out[q] = src[q];
+    }
+}
+
+// ------------------------------------------------------------------ launch
+template <int R>
+static hipError_t launch_rank_r(uint32_t blocks, uint32_t waves, uint32_t lds_bytes,
+                                uint32_t tiles_per_sys, uint32_t key_bits, const GridParams& g,
+                                const float4* pos, const uint32_t* keys_in, const uint32_t* d_count,
+                                uint32_t n, uint32_t* keys, uint32_t* ranks, uint32_t* table,
+                                uint32_t* flags, uint32_t* wl_count, hipStream_t stream) {
+    static uint32_t attr_bytes = 32768;
+    if (lds_bytes > attr_bytes) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_hash_rank<R>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+        if (e != hipSuccess) return e;
+        attr_bytes = lds_bytes;
+    }
+    hipLaunchKernelGGL(k_hash_rank<R>, dim3(blocks), dim3(waves * 64), lds_bytes, stream, pos, keys_in,
+                       d_count, n, tiles_per_sys, waves, g, key_bits, keys, ranks, table, flags,
+                       wl_count);
+    return hipGetLastError();
+}
+
+static hipError_t launch_rank(uint32_t rounds, uint32_t blocks, uint32_t waves, uint32_t lds_bytes,
+                              uint32_t tiles_per_sys, uint32_t key_bits, const GridParams& g,
+                              const float4* pos, const uint32_t* keys_in, const uint32_t* d_count,
+                              uint32_t n, uint32_t* keys, uint32_t* ranks, uint32_t* table,
+                              uint32_t* flags, uint32_t* wl_count, hipStream_t stream) {
+#define NPA_RANK(RR)                                                                             \
+    return launch_rank_r<RR>(blocks, waves, lds_bytes, tiles_per_sys, key_bits, g, pos, keys_in, \
+                             d_count, n, keys, ranks, table, flags, wl_count, stream)
+    switch (rounds) {
+        case 1: NPA_RANK(1);
+        case 2: NPA_RANK(2);
+        case 4: NPA_RANK(4);
+        case 8: NPA_RANK(8);
+        case 16: NPA_RANK(16);
+        default: NPA_RANK(32);
+    }
+#undef NPA_RANK
+}
+
+hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const float4* pos,
+                           const float* states, uint32_t state_dims, uint32_t batch, uint32_t n,
+                           Workspace& ws, bool payload, hipStream_t stream, Profiler* prof) {
+    const uint64_t total = (uint64_t)batch * n;
+    hipError_t e = hipSuccess;
+    {
+        ProfScope ps(prof, NPA_KERNEL_HASH_RANK, stream);
+        e = launch_rank(plan.rounds, batch * plan.tiles_per_sys, plan.waves, plan.lds_bytes,
+                        plan.tiles_per_sys, plan.key_bits, g, pos, nullptr, nullptr, n,
+                        ws.keys.as<uint32_t>(), ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(),
+                        ws.flags.as<uint32_t>(), ws.wl_count.as<uint32_t>(), stream);
+    }
+    if (e != hipSuccess) return e;
+    {
+        ProfScope ps(prof, NPA_KERNEL_TABLE_SCAN, stream);
+        hipLaunchKernelGGL(k_table_scan, dim3((plan.cells + 255) / 256, batch), dim3(256), 0, stream,
+                           ws.table.as<uint32_t>(), ws.totals.as<uint32_t>(), plan.cells,
+                           plan.tiles_per_sys);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    {
+        ProfScope ps(prof, NPA_KERNEL_OFFSETS_SCAN, stream);
+        hipLaunchKernelGGL(k_offsets_scan, dim3(batch), dim3(1024), 0, stream,
+                           ws.totals.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), plan.cells, n,
+                           batch, ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(),
+                           payload ? 1 : 0);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    {
+        ProfScope ps(prof, NPA_KERNEL_SCATTER, stream);
+        const uint32_t blocks = (uint32_t)((total + 255) / 256);
+        if (g.dim == 2)
+            hipLaunchKernelGGL(k_scatter<2>, dim3(blocks), dim3(256), 0, stream, pos, states,
+                               state_dims, n, (uint32_t)total, plan.tile, plan.tiles_per_sys, g,
+                               ws.keys.as<uint32_t>(), ws.ranks.as<uint32_t>(),
+                               ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(),
+                               ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(),
+                               ws.scoord.as<int4>(), ws.sstate.as<float>(), payload ? 1 : 0);
+        else
+            hipLaunchKernelGGL(k_scatter<3>, dim3(blocks), dim3(256), 0, stream, pos, states,
+                               state_dims, n, (uint32_t)total, plan.tile, plan.tiles_per_sys, g,
+                               ws.keys.as<uint32_t>(), ws.ranks.as<uint32_t>(),
+                               ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(),
+                               ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(),
+                               ws.scoord.as<int4>(), ws.sstate.as<float>(), payload ? 1 : 0);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// ------------------------------------------------------ generic key sort
+__global__ __launch_bounds__(256) void k_scatter_vals(const uint32_t* __restrict__ keys,
+                                                      const uint32_t* __restrict__ vals,
+                                                      const uint32_t* __restrict__ d_count,
+                                                      uint32_t cap, uint32_t tile, uint32_t C,
+                                                      const uint32_t* __restrict__ ranks,
+                                                      const uint32_t* __restrict__ table,
+                                                      const uint32_t* __restrict__ offsets,
+                                                      uint32_t* __restrict__ out_vals) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t dc = *d_count;
+    const uint32_t count = dc < cap ? dc : cap;
+    if (i >= count) return;
+    const uint32_t key = keys[i];
+    const uint32_t dst = offsets[key] + table[(uint64_t)(i / tile) * C + key] + ranks[i];
+    out_vals[dst] = vals ? vals[i] : i;
+}
+
+bool make_key_sort_plan(uint32_t cap, uint32_t C, HashgridPlan* p) {
+    if (C == 0 || C > 65536) return false;
+    p->cells = C;
+    p->key_bits = C <= 1 ? 0 : 32 - __builtin_clz(C - 1);
+    p->waves = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(4, 32768 / C));
+    p->lds_bytes = p->waves * C * 2;
+    const uint64_t budget = std::max<uint64_t>(2 * (uint64_t)cap, C);
+    uint32_t rounds = 1;
+    while (rounds < 32) {
+        uint64_t tile = (uint64_t)p->waves * rounds * 64;
+        if (((cap + tile - 1) / tile) * (uint64_t)C <= budget) break;
+        rounds *= 2;
+    }
+    p->rounds = rounds;
+    p->tile = p->waves * rounds * 64;
+    p->tiles_per_sys = std::max<uint32_t>(1, (cap + p->tile - 1) / p->tile);
+    p->table_entries = (uint64_t)p->tiles_per_sys * C;
+    return true;
+}
+
+hipError_t launch_key_sort(const HashgridPlan& p, const uint32_t* keys, const uint32_t* vals,
+                           const uint32_t* d_count, uint32_t cap, uint32_t* ranks, uint32_t* table,
+                           uint32_t* totals, uint32_t* offsets, uint32_t* out_vals, uint32_t* flags,
+                           hipStream_t stream) {
+    GridParams g{};
+    g.cells = p.cells;
+    hipError_t e = launch_rank(p.rounds, p.tiles_per_sys, p.waves, p.lds_bytes, p.tiles_per_sys,
+                               p.key_bits, g, nullptr, keys, d_count, cap, nullptr, ranks, table,
+                               flags, nullptr, stream);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_table_scan, dim3((p.cells + 255) / 256, 1), dim3(256), 0, stream, table, totals,
+                       p.cells, p.tiles_per_sys);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_offsets_scan, dim3(1), dim3(1024), 0, stream, totals, offsets, p.cells, cap, 1u,
+                       (uint2*)nullptr, (uint32_t*)nullptr, 0);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (cap == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_scatter_vals, dim3((cap + 255) / 256), dim3(256), 0, stream, keys, vals, d_count,
+                       cap, p.tile, p.cells, ranks, table, offsets, out_vals);
+    return hipGetLastError();
+}
+
+int device_cu_count() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return 256;
+    return cus;
+}
+
+}  // namespace npa

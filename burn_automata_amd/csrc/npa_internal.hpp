@@ -1,0 +1,159 @@
+// npa_internal.hpp - host-side interfaces between the library's translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/npa_abi.h"
+#include "npa_device.hpp"
+
+namespace npa {
+
+// Grow-only device allocation.
+struct DevBuf {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    hipError_t reserve(size_t want);
+    void release();
+    template <class T>
+    T* as() const { return static_cast<T*>(ptr); }
+};
+
+// Per-context profiling: HIP events bracket launches of selected kernels.
+struct Profiler {
+    bool enabled = false;
+    struct Pair { hipEvent_t a, b; int kernel; };
+    std::vector<Pair> pending;
+    std::vector<hipEvent_t> pool;
+    double total_ms[NPA_KERNEL_COUNT] = {0};
+    uint64_t launches[NPA_KERNEL_COUNT] = {0};
+    hipEvent_t get();
+    void begin(int kernel, hipStream_t s, hipEvent_t* ev);
+    void end(int kernel, hipStream_t s, hipEvent_t ev);
+    hipError_t collect();  // synchronizes pending events into the totals
+    void reset();
+    ~Profiler();
+};
+
+struct ProfScope {
+    Profiler* p;
+    int kernel;
+    hipStream_t s;
+    hipEvent_t ev = nullptr;
+    ProfScope(Profiler* p_, int k, hipStream_t s_) : p(p_), kernel(k), s(s_) {
+        if (p && p->enabled) p->begin(kernel, s, &ev);
+    }
+    ~ProfScope() {
+        if (p && p->enabled && ev) p->end(kernel, s, ev);
+    }
+};
+
+// How the hashgrid build splits the particles of one system into tiles.
+struct HashgridPlan {
+    uint32_t cells = 0;          // C
+    uint32_t key_bits = 0;       // ceil(log2(C))
+    uint32_t waves = 0;          // waves per tile (block)
+    uint32_t rounds = 0;         // R: 64-particle rounds per wave
+    uint32_t tile = 0;           // particles per tile = waves * rounds * 64
+    uint32_t tiles_per_sys = 0;
+    uint32_t lds_bytes = 0;      // waves * C * 2
+    uint64_t table_entries = 0;  // B * tiles_per_sys * C
+    uint64_t worklist_cap = 0;   // upper bound of wave work items
+};
+
+// Device workspace of one hashgrid + perception pass.
+struct Workspace {
+    DevBuf keys, ranks, table, totals, bin_offsets, perm, inv, flags, wl_count, worklist;
+    DevBuf srec, scoord, sstate, svol, counters;
+    hipError_t reserve(const HashgridPlan& plan, uint64_t total, uint32_t batch, uint32_t state_dims,
+                       int dim);
+    void release();
+};
+
+bool make_plan(const npa_grid_cfg& cfg, uint32_t batch, uint32_t particle_count, HashgridPlan* plan,
+               std::string* err);
+GridParams make_grid_params(const npa_grid_cfg& cfg);
+float host_powi(float x, int n);
+
+// Builds the stable hashgrid; when `payload` is set also the sorted particle
+// records (positions + cell coords), sorted state rows, and the wave work list.
+hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const float4* pos,
+                           const float* states, uint32_t state_dims, uint32_t batch,
+                           uint32_t particle_count, Workspace& ws, bool payload,
+                           hipStream_t stream, Profiler* prof);
+
+// Stable counting sort of a device-resident number (<= cap) of items by key in [0, C):
+// out_vals[offsets[key] + rank] = vals[i] (or i when vals is null), offsets[C+1].
+bool make_key_sort_plan(uint32_t cap, uint32_t C, HashgridPlan* plan);
+hipError_t launch_key_sort(const HashgridPlan& plan, const uint32_t* keys, const uint32_t* vals,
+                           const uint32_t* d_count, uint32_t cap, uint32_t* ranks, uint32_t* table,
+                           uint32_t* totals, uint32_t* offsets, uint32_t* out_vals, uint32_t* flags,
+                           hipStream_t stream);
+
+// Fused per-step parameters for the perception / update kernels.
+struct StepParams {
+    GridParams g;
+    uint32_t N, B, S, H, F;
+    uint32_t state_grad, density_grad, log_norm_grad, log_norm_dgrad, hybrid, position_features;
+    float state_scale;  // normalize_state_gradient factor
+    float dgrad_scale;  // normalize_density_gradient factor
+    float alpha, motion_eps, dt;
+    uint32_t gates3d;
+    float update_prob;
+    uint32_t step_index;
+    uint32_t base_seed;
+};
+
+struct StepIO {
+    const float4* pos = nullptr;     // original order
+    const float* states = nullptr;   // original order
+    const float* mask = nullptr;     // optional, original order
+    const float* w1 = nullptr;
+    const float* b1 = nullptr;
+    const float* w2 = nullptr;
+    const float* b2 = nullptr;
+    float4* out_pos = nullptr;
+    float* out_states = nullptr;
+    float* out_density = nullptr;    // optional
+    // perceive-mode outputs
+    float* features = nullptr;
+    float* blurred = nullptr;
+    float* state_gradient = nullptr;
+    float* density_gradient = nullptr;
+};
+
+// density pass (always) then either the fused update (mode 0) or the perception write-out (mode 1).
+hipError_t launch_density(const StepParams& p, Workspace& ws, float* density_out, int grid_blocks,
+                          hipStream_t stream, Profiler* prof);
+hipError_t launch_update(const StepParams& p, Workspace& ws, const StepIO& io, int mode,
+                         int grid_blocks, hipStream_t stream, Profiler* prof);
+hipError_t launch_mlp_forward(const StepParams& p, const float* features, uint32_t rows,
+                              const StepIO& io, float* dx, float* ds, hipStream_t stream);
+hipError_t launch_euler(const StepParams& p, const float4* pos, const float* states,
+                        const float4* dx, const float* ds, const float* mask, float4* out_pos,
+                        float* out_states, uint64_t total, hipStream_t stream);
+hipError_t launch_update_mask(uint32_t batch, uint32_t n, float p, uint32_t step, uint32_t base_seed,
+                              float* mask, hipStream_t stream);
+hipError_t launch_count_pairs(const StepParams& p, Workspace& ws, int grid_blocks,
+                              unsigned long long* counters, hipStream_t stream);
+hipError_t launch_neighbor_lists(const StepParams& p, Workspace& ws, uint32_t* counts_or_offsets,
+                                 uint32_t* indices, int write, int grid_blocks, hipStream_t stream);
+
+// decode / splat
+hipError_t launch_decode_gaussians(const float4* pos, const float* states, uint32_t count,
+                                   uint32_t state_dims, const npa_gaussian_decode_cfg& cfg,
+                                   float* pv, float* sh, float* rot, float* so, hipStream_t stream);
+struct SplatWorkspace {
+    DevBuf params, item_start, keys, vals, sorted, ranks, table, totals, offsets, count, flags;
+    void release();
+};
+hipError_t launch_splat_2d(const float4* pos, const float* colors, const float* states,
+                           uint32_t state_dims, uint32_t count, const npa_splat2d_cfg& cfg,
+                           float* image, SplatWorkspace& ws, hipStream_t stream, Profiler* prof);
+
+int device_cu_count();
+
+}  // namespace npa

@@ -1,0 +1,124 @@
+"""Device-resident executor: the HIP counterpart of WgpuAutomataExecutor
+(crates/burn_automata/src/gpu/types.rs:418-457, crates/burn_automata/src/gpu/executor/*.rs).
+
+A state owns ping-pong particle buffers and every per-step workspace in HBM; a
+step is the hashgrid build, the density pass and the fused update, all queued on
+the context's stream with no host synchronisation.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+from ._lib import lib
+from .config import GaussianDecodeConfig, HashGridConfig, Splat2dConfig
+from .model import NpaModel, NpaWeights
+from .runtime import Context, default_context, device_f32, ptr
+
+
+class HipAutomataState:
+    def __init__(self, ctx: Context, handle, model: NpaModel, grid: HashGridConfig,
+                 batch_size: int, particle_count: int):
+        self.ctx = ctx
+        self.handle = handle
+        self.model = model
+        self.grid = grid
+        self.batch_size = batch_size
+        self.particle_count = particle_count
+
+    @property
+    def total(self) -> int:
+        return self.batch_size * self.particle_count
+
+    def step_index(self) -> int:
+        v = C.c_uint64()
+        self.ctx.check(lib().npa_state_step_index(self.handle, C.byref(v)))
+        return int(v.value)
+
+    def close(self):
+        if getattr(self, "handle", None) is not None and self.handle.value:
+            lib().npa_state_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class HipAutomataExecutor:
+    def __init__(self, device: int = 0, ctx: Context | None = None):
+        self.ctx = ctx or default_context(device)
+
+    def create_state(self, model: NpaModel, positions, states, batch_size: int,
+                     particle_count: int, grid: HashGridConfig, dt: float,
+                     update_prob: float = 1.0, seed: int = 0) -> HipAutomataState:
+        """create_state_with_update_prob (crates/burn_automata/src/gpu/executor/state.rs:82-111)."""
+        model.validate()
+        pos = device_f32(positions, device=self.ctx.device).reshape(-1, 4)
+        st = device_f32(states, device=self.ctx.device).reshape(-1)
+        w = model.weights.to_c()
+        h = C.c_void_p()
+        self.ctx.check(lib().npa_state_create(
+            self.ctx.handle, C.byref(model.config.to_c()), C.byref(w), C.byref(grid.to_c()),
+            ptr(pos), ptr(st), batch_size, particle_count, float(dt), float(update_prob),
+            int(seed) & 0xFFFFFFFFFFFFFFFF, C.byref(h)))
+        return HipAutomataState(self.ctx, h, model, grid, batch_size, particle_count)
+
+    def step_state(self, state: HipAutomataState):
+        self.ctx.check(lib().npa_state_step(state.handle, 1))
+
+    def step_state_many(self, state: HipAutomataState, steps: int):
+        self.ctx.check(lib().npa_state_step(state.handle, int(steps)))
+
+    def read_state(self, state: HipAutomataState):
+        """(positions [n,4], states [n,S], density [n]) as new device tensors."""
+        import torch
+
+        dev = f"cuda:{self.ctx.device}"
+        pos = torch.empty((state.total, 4), dtype=torch.float32, device=dev)
+        st = torch.empty((state.total, state.model.config.state_dims), dtype=torch.float32,
+                         device=dev)
+        dens = torch.empty(state.total, dtype=torch.float32, device=dev)
+        self.ctx.check(lib().npa_state_read(state.handle, ptr(pos), ptr(st), ptr(dens)))
+        return pos, st, dens
+
+    def update_state_model(self, state: HipAutomataState, weights):
+        w = weights if isinstance(weights, NpaWeights) else NpaWeights.from_arrays(weights,
+                                                                                   self.ctx.device)
+        w.validate(state.model.config)
+        wc = w.to_c()
+        self.ctx.check(lib().npa_state_update_model(state.handle, C.byref(wc)))
+        state.model = NpaModel(state.model.config, w)
+
+    def splat_2d(self, state: HipAutomataState, cfg: Splat2dConfig):
+        import torch
+
+        img = torch.empty((cfg.image_size * cfg.image_size, 4), dtype=torch.float32,
+                          device=f"cuda:{self.ctx.device}")
+        self.ctx.check(lib().npa_state_splat_2d(state.handle, C.byref(cfg.to_c()), ptr(img)))
+        return img
+
+    def decode_gaussians_3d(self, state: HipAutomataState, cfg: GaussianDecodeConfig):
+        import torch
+
+        n = state.total
+        K = cfg.sh_coeffs()
+        dev = f"cuda:{self.ctx.device}"
+        pv = torch.empty((n, 4), dtype=torch.float32, device=dev)
+        sh = torch.empty((n, K, 3), dtype=torch.float32, device=dev)
+        rot = torch.empty((n, 4), dtype=torch.float32, device=dev)
+        so = torch.empty((n, 4), dtype=torch.float32, device=dev)
+        self.ctx.check(lib().npa_state_decode_gaussians_3d(state.handle, C.byref(cfg.to_c()),
+                                                          ptr(pv), ptr(sh), ptr(rot), ptr(so)))
+        return {"position_visibility": pv, "spherical_harmonic": sh, "rotation": rot,
+                "scale_opacity": so}
+
+    def pair_counts(self, state: HipAutomataState):
+        """(candidates visited, pairs accepted) of the neighbour walk on the current particles."""
+        a, b = C.c_uint64(), C.c_uint64()
+        self.ctx.check(lib().npa_state_pair_counts(state.handle, C.byref(a), C.byref(b)))
+        return int(a.value), int(b.value)
+
+    def wait_idle(self):
+        self.ctx.synchronize()

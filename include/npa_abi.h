@@ -1,0 +1,288 @@
+/*
+ * npa_abi.h - C ABI of the MI355X-native fixed-NPA rollout library (libnpa_hip.so).
+ *
+ * Every entry point is `extern "C"`, takes plain pointers and sizes, and is
+ * stream-ordered on the stream owned by (or handed to) its npa_context.
+ * Array arguments are DEVICE pointers unless the context was switched to host
+ * I/O with npa_context_set_host_io(ctx, 1); then they are host pointers, the
+ * library stages them through device buffers it owns and the call returns
+ * only after the results are back in host memory.
+ *
+ * Layouts follow the reference (burn_automata_kernels, Rust):
+ *   positions  [B*N][4]   f32  (x, y, z, w)          `&[[f32; 4]]`
+ *   states     [B*N][S]   f32  row-major             `&[f32]`
+ *   features   [B*N][F]   f32  [state | blur | grad(S*d, channel-major) | dgrad(d)? | pos(d)?]
+ *   weights    w1[H][F], b1[H], w2[O][H], b2[O], O = d + S
+ * Index tables use u32 where the reference uses usize; sizes must keep
+ * B*N and B*C below 2^32 (checked, NPA_ERR_INVALID_ARGUMENT otherwise).
+ *
+ * Status codes map 1:1 onto `KernelError` variants
+ * (crates/burn_automata_kernels/src/config.rs:101-137); npa_last_error()
+ * returns the formatted message of the last failing call on a context.
+ */
+#ifndef NPA_ABI_H
+#define NPA_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+typedef enum npa_status {
+    NPA_OK = 0,
+    NPA_ERR_INVALID_DIM = 1,           /* KernelError::InvalidDim */
+    NPA_ERR_INVALID_EPS = 2,           /* KernelError::InvalidEps */
+    NPA_ERR_INVALID_GRID_SIZE = 3,     /* KernelError::InvalidGridSize */
+    NPA_ERR_PARTICLE_MODE_POW2 = 4,    /* KernelError::ParticleModeRequiresPowerOfTwo */
+    NPA_ERR_POSITION_SHAPE = 10,       /* KernelError::PositionShape */
+    NPA_ERR_STATE_SHAPE = 11,          /* KernelError::StateShape */
+    NPA_ERR_OUTPUT_SHAPE = 12,         /* KernelError::OutputShape */
+    NPA_ERR_INVALID_ARGUMENT = 13,     /* KernelError::InvalidArgument */
+    NPA_ERR_INVALID_MODEL = 20,        /* AutomataError::InvalidModel (crates/burn_automata/src/error.rs) */
+    NPA_ERR_DEVICE = 30,               /* HIP runtime failure */
+    NPA_ERR_OUT_OF_MEMORY = 31,
+    NPA_ERR_COORD_OVERFLOW = 32        /* a cell coordinate left the i32 range the device path supports */
+} npa_status;
+
+/* ---------------------------------------------------------------- config */
+/* Boundary / HashGridMode: crates/burn_automata_kernels/src/config.rs:4-18 */
+enum { NPA_BOUNDARY_PERIODIC = 0, NPA_BOUNDARY_CLAMPED = 1 };
+enum { NPA_MODE_GRID = 0, NPA_MODE_PARTICLE = 1 };
+
+/* HashGridConfig: crates/burn_automata_kernels/src/config.rs:20-29 */
+typedef struct npa_grid_cfg {
+    uint32_t dim;          /* 2 or 3 */
+    uint32_t boundary;     /* NPA_BOUNDARY_* */
+    uint32_t mode;         /* NPA_MODE_* */
+    uint32_t grid_size[3];
+    float eps;             /* cell size == kernel support radius */
+    uint32_t max_particles_per_block;  /* carried for fidelity; unused by the hot path */
+} npa_grid_cfg;
+
+/* PerceptionOptions: crates/burn_automata_kernels/src/reference/types.rs:4-15 (bools as u32) */
+typedef struct npa_perception_opts {
+    uint32_t state_grad;
+    uint32_t density_grad;
+    float eps0;
+    uint32_t scale_equivariance;
+    uint32_t particle_density_equivariance;
+    uint32_t log_norm_grad;
+    uint32_t log_norm_density_grad;
+    uint32_t hybrid_state_gradient;
+    uint32_t position_features;
+} npa_perception_opts;
+
+/* EquivarianceMode: crates/burn_automata/src/config.rs:22-28 */
+enum { NPA_EQUIV_NONE = 0, NPA_EQUIV_PARTICLE_DENSITY = 1, NPA_EQUIV_PARTICLE_DENSITY_AND_SCALE = 2 };
+
+/* NpaConfig (the fields the rollout step reads): crates/burn_automata/src/config.rs:30-53 */
+typedef struct npa_model_cfg {
+    uint32_t spatial_dims;
+    uint32_t state_dims;
+    uint32_t hidden_dims;
+    float eps0;
+    float alpha;
+    uint32_t density_grad;
+    uint32_t state_grad;
+    uint32_t log_norm_grad;
+    uint32_t log_norm_density_grad;
+    uint32_t equivariance;       /* NPA_EQUIV_* */
+    uint32_t position_features;
+} npa_model_cfg;
+
+/* NpaWeights: crates/burn_automata/src/model.rs:12-17 (row-major) */
+typedef struct npa_weights {
+    const float* w1;   /* [H][F] */
+    const float* b1;   /* [H]    */
+    const float* w2;   /* [O][H] */
+    const float* b2;   /* [O]    */
+} npa_weights;
+
+/* GaussianDecodeMode / GaussianDecodeConfig: crates/burn_automata_kernels/src/gaussian.rs:13-51 */
+enum {
+    NPA_DECODE_PARTICLE_POINT = 0,
+    NPA_DECODE_SH0_FIXED_SCALE = 1,
+    NPA_DECODE_SH0_LEARNED_SCALE = 2,
+    NPA_DECODE_SH0_ORIENTED = 3
+};
+typedef struct npa_gaussian_decode_cfg {
+    uint32_t mode;
+    float sigma;
+    float min_scale;
+    float max_scale;
+    float max_anisotropy;
+    float opacity_scale;
+    float min_opacity;
+    float max_opacity;
+    uint32_t sh_degree;
+} npa_gaussian_decode_cfg;
+
+/* Splat2dConfig: crates/burn_automata_kernels/src/splat.rs:6-14 */
+typedef struct npa_splat2d_cfg {
+    uint32_t image_size;
+    float sigma;
+    float lo;
+    float hi;
+    uint32_t normalize_color;
+    uint32_t y_up;
+    float pixel_size;
+} npa_splat2d_cfg;
+
+/* ------------------------------------------------------------- context */
+typedef struct npa_context npa_context;
+typedef struct npa_state npa_state;
+
+/* Creates a context bound to HIP device `device`. `stream` is a hipStream_t
+ * (may be NULL for the legacy default stream); the context never destroys it. */
+npa_status npa_context_create(int device, void* stream, npa_context** out);
+void npa_context_destroy(npa_context* ctx);
+npa_status npa_context_set_stream(npa_context* ctx, void* stream);
+/* 0: array arguments are device pointers (default). 1: host pointers, synchronous. */
+npa_status npa_context_set_host_io(npa_context* ctx, int host_io);
+/* Blocks until all work queued on the context's stream has finished. */
+npa_status npa_context_synchronize(npa_context* ctx);
+/* Message of the last failing call on this context ("" when none). */
+const char* npa_last_error(const npa_context* ctx);
+/* Library version string. */
+const char* npa_version(void);
+
+/* ------------------------------------------------ operator surface (L0) */
+/* Replaces build_hashgrid (crates/burn_automata_kernels/src/hashgrid.rs:16-69).
+ * bin_offsets[B*C+1], permutation[B*N] (binned -> local particle index),
+ * inverse_permutation[B*N] (global particle -> binned index - b*N).
+ * Bit-exact with the reference's stable counting sort. */
+npa_status npa_build_hashgrid(npa_context* ctx, const float* positions,
+                              uint32_t batch_size, uint32_t particle_count,
+                              const npa_grid_cfg* cfg,
+                              uint32_t* bin_offsets, size_t bin_offsets_len,
+                              uint32_t* permutation, uint32_t* inverse_permutation,
+                              size_t particles_len);
+
+/* Debug export of the ordered neighbour lists for_each_neighbor visits
+ * (crates/burn_automata_kernels/src/reference/neighbor.rs:3-44), CSR form:
+ * offsets[B*N+1], indices[capacity] (global particle indices, reference order).
+ * When capacity is too small, only offsets are written and *required receives
+ * the needed length. */
+npa_status npa_neighbor_lists(npa_context* ctx, const float* positions,
+                              uint32_t batch_size, uint32_t particle_count,
+                              const npa_grid_cfg* cfg, uint32_t* offsets,
+                              uint32_t* indices, size_t capacity, size_t* required);
+
+/* Replaces perceive_with_options (crates/burn_automata_kernels/src/reference/forward.rs:26-143).
+ * features[B*N][F]; density[B*N]; blurred_state[B*N][S];
+ * state_gradient[B*N][S*d] (may be NULL; ignored when !state_grad);
+ * density_gradient[B*N][d] (may be NULL; ignored when !density_grad).
+ * *feature_dims receives F. */
+npa_status npa_perceive(npa_context* ctx, const float* positions, const float* states,
+                        uint32_t batch_size, uint32_t particle_count, uint32_t state_dims,
+                        const npa_grid_cfg* cfg, const npa_perception_opts* opts,
+                        float* features, size_t features_len, float* density,
+                        float* blurred_state, float* state_gradient, float* density_gradient,
+                        uint32_t* feature_dims);
+
+/* Replaces NpaModel::forward_from_features_with_eps
+ * (crates/burn_automata/src/model.rs:867-940): update MLP, motion scaling.
+ * features[rows][F] -> dx[rows][4] (axes >= d written as 0), ds[rows][S]. */
+npa_status npa_mlp_forward(npa_context* ctx, const float* features, uint32_t rows,
+                           const npa_model_cfg* model, const npa_weights* weights,
+                           float eps, float* dx, float* ds);
+
+/* Replaces euler_step (crates/burn_automata_kernels/src/reference/step.rs:4-55).
+ * update_mask may be NULL (all ones). */
+npa_status npa_euler_step(npa_context* ctx, const float* positions, const float* states,
+                          const float* dx, const float* ds, uint32_t batch_size,
+                          uint32_t particle_count, uint32_t state_dims,
+                          const npa_grid_cfg* cfg, float dt, const float* update_mask,
+                          float* out_positions, float* out_states);
+
+/* Replaces NpaModel::step_cpu (crates/burn_automata/src/model.rs:768-858): one fused
+ * rollout step. update_mask may be NULL. density/dx/ds outputs are optional (NULL). */
+npa_status npa_step(npa_context* ctx, const float* positions, const float* states,
+                    uint32_t batch_size, uint32_t particle_count,
+                    const npa_grid_cfg* grid, const npa_model_cfg* model,
+                    const npa_weights* weights, float dt, const float* update_mask,
+                    float* out_positions, float* out_states, float* out_density);
+
+/* The device update mask of the reference GPU path (gpu_step.wgsl:1019-1056 with lane
+ * seeds from crates/burn_automata/src/gpu/executor/state.rs:1282-1315):
+ * mask[b*N+i] = random01(i, step_index, lane_seed(b)) < update_prob. */
+npa_status npa_update_mask(npa_context* ctx, uint32_t batch_size, uint32_t particle_count,
+                           float update_prob, uint32_t step_index, uint64_t seed,
+                           float* mask);
+
+/* Replaces decode_gaussians_3d (crates/burn_automata_kernels/src/gaussian.rs:53-100).
+ * Planar outputs: position_visibility[n][4], spherical_harmonic[n][K][3] with
+ * K = (sh_degree+1)^2 in oriented mode and 1 otherwise, rotation[n][4], scale_opacity[n][4]. */
+npa_status npa_decode_gaussians_3d(npa_context* ctx, const float* positions,
+                                   const float* states, uint32_t count, uint32_t state_dims,
+                                   const npa_gaussian_decode_cfg* cfg,
+                                   float* position_visibility, float* spherical_harmonic,
+                                   float* rotation, float* scale_opacity);
+
+/* Replaces splat_particles_2d (crates/burn_automata_kernels/src/splat.rs:30-93).
+ * colors[count][3]; image[size*size][4] is overwritten. Tile-binned and
+ * deterministic: each pixel sums particles in ascending index order. */
+npa_status npa_splat_2d(npa_context* ctx, const float* positions, const float* colors,
+                        uint32_t count, const npa_splat2d_cfg* cfg, float* image);
+
+/* ----------------------------------- device-resident executor (L2 twin) */
+/* Replaces WgpuAutomataExecutor::create_state_with_update_prob
+ * (crates/burn_automata/src/gpu/executor/state.rs:82-111). positions/states/weights
+ * follow the context's I/O mode. The state owns ping-pong particle buffers and all
+ * per-step workspaces; its first step has step index 0. */
+npa_status npa_state_create(npa_context* ctx, const npa_model_cfg* model,
+                            const npa_weights* weights, const npa_grid_cfg* grid,
+                            const float* positions, const float* states,
+                            uint32_t batch_size, uint32_t particle_count, float dt,
+                            float update_prob, uint64_t seed, npa_state** out);
+void npa_state_destroy(npa_state* state);
+/* step_state / step_state_many (crates/burn_automata/src/gpu/executor/steps.rs:6-69). */
+npa_status npa_state_step(npa_state* state, uint32_t steps);
+/* read_state (crates/burn_automata/src/gpu/executor/readback.rs:85): current particles
+ * and the density of the last step (density may be NULL). */
+npa_status npa_state_read(npa_state* state, float* positions, float* states, float* density);
+/* update_state_model (crates/burn_automata/src/gpu/executor/state.rs:626). */
+npa_status npa_state_update_model(npa_state* state, const npa_weights* weights);
+/* Current step index (number of steps taken). */
+npa_status npa_state_step_index(const npa_state* state, uint64_t* step_index);
+/* Device pointers of the current particle buffers (valid until the next step). */
+npa_status npa_state_buffers(npa_state* state, float** positions, float** states);
+/* Splat the current particles with colors clamp(state[S-3..S]+0.5, 0, 1)
+ * (crates/burn_automata/examples/infer_2d.rs:20-39). image per context I/O mode. */
+npa_status npa_state_splat_2d(npa_state* state, const npa_splat2d_cfg* cfg, float* image);
+/* decode_gaussians_3d of the current particles (the planar export the viewer reads,
+ * cf. write_gaussian_main gpu_step.wgsl:4929-5052). */
+npa_status npa_state_decode_gaussians_3d(npa_state* state, const npa_gaussian_decode_cfg* cfg,
+                                         float* position_visibility, float* spherical_harmonic,
+                                         float* rotation, float* scale_opacity);
+
+/* ---------------------------------------------------------- profiling */
+/* Kernel ids for npa_profile_read. */
+enum {
+    NPA_KERNEL_HASH_RANK = 0,
+    NPA_KERNEL_TABLE_SCAN = 1,
+    NPA_KERNEL_OFFSETS_SCAN = 2,
+    NPA_KERNEL_SCATTER = 3,
+    NPA_KERNEL_DENSITY = 4,
+    NPA_KERNEL_UPDATE = 5,
+    NPA_KERNEL_SPLAT = 6,
+    NPA_KERNEL_COUNT = 7
+};
+/* When enabled, the library brackets each launch of the listed kernels with HIP
+ * events on the context's stream. npa_profile_read synchronizes and returns the
+ * summed milliseconds and launch count since the last reset. */
+npa_status npa_profile_enable(npa_context* ctx, int enable);
+npa_status npa_profile_reset(npa_context* ctx);
+npa_status npa_profile_read(npa_context* ctx, int kernel_id, double* total_ms, uint64_t* launches);
+/* Work counters of the last step run through a state (exact, from the device):
+ * candidates tested and pairs accepted by the density pass. */
+npa_status npa_state_pair_counts(npa_state* state, uint64_t* candidates, uint64_t* pairs);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NPA_ABI_H */

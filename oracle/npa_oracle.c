@@ -1,0 +1,1142 @@
+/*
+ * npa_oracle.c - CPU restatement of burn_automata's fixed-NPA rollout path.
+ *
+ * TEST INFRASTRUCTURE ONLY (checker + "port" CPU baseline); see npa_oracle.h.
+ * Build: gcc -O3 -fopenmp -ffp-contract=off (no fast-math), see oracle/Makefile.
+ *
+ * Every function cites the reference file:line it restates. Float expressions
+ * keep the reference's left-to-right association; Rust never contracts a*b+c
+ * into an FMA, so neither does this file.
+ */
+#include "npa_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <omp.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define PI_F 3.14159265358979323846f /* std::f32::consts::PI */
+
+static double g_phase_perceive, g_phase_mlp, g_phase_integrate;
+
+void oracle_last_phase_seconds(double* perceive, double* mlp, double* integrate) {
+    if (perceive) *perceive = g_phase_perceive;
+    if (mlp) *mlp = g_phase_mlp;
+    if (integrate) *integrate = g_phase_integrate;
+}
+
+int oracle_max_threads(void) { return omp_get_max_threads(); }
+void oracle_set_threads(int threads) {
+    if (threads > 0) omp_set_num_threads(threads);
+}
+
+/* f32::powi with a non-negative exponent: LLVM expands llvm.powi with a constant
+ * exponent into the square-and-multiply tree below, and compiler-rt's __powisf2
+ * runs the same recurrence for a runtime exponent, so both give this value. */
+static float powi_f32(float x, int n) {
+    int recip = n < 0;
+    unsigned b = (unsigned)(recip ? -n : n);
+    float r = 1.0f;
+    for (;;) {
+        if (b & 1u) r *= x;
+        b >>= 1;
+        if (b == 0) break;
+        x *= x;
+    }
+    return recip ? 1.0f / r : r;
+}
+
+/* `f as isize` for a floored f32: saturating, NaN -> 0 (Rust float->int cast). */
+static int64_t f32_to_isize(float f) {
+    if (isnan(f)) return 0;
+    if (f >= 9223372036854775808.0f) return INT64_MAX;
+    if (f <= -9223372036854775808.0f) return INT64_MIN;
+    return (int64_t)f;
+}
+
+static int64_t rem_euclid_i64(int64_t a, int64_t m) {
+    int64_t r = a % m;
+    return r < 0 ? r + m : r;
+}
+
+static float rem_euclid_f32(float a, float m) {
+    float r = fmodf(a, m);
+    return r < 0.0f ? r + fabsf(m) : r;
+}
+
+static float clamp_f32(float v, float lo, float hi) { /* f32::clamp */
+    if (v < lo) v = lo;
+    if (v > hi) v = hi;
+    return v;
+}
+
+/* ---------------------------------------------------------------- config */
+
+/* HashGridConfig::validate  crates/burn_automata_kernels/src/config.rs:65-84 */
+int oracle_grid_validate(const npa_grid_cfg* cfg) {
+    if (!(cfg->dim == 2 || cfg->dim == 3)) return NPA_ERR_INVALID_DIM;
+    if (!isfinite(cfg->eps) || cfg->eps <= 0.0f) return NPA_ERR_INVALID_EPS;
+    for (uint32_t a = 0; a < cfg->dim; ++a) {
+        uint32_t s = cfg->grid_size[a];
+        if (s == 0) return NPA_ERR_INVALID_GRID_SIZE;
+        if (cfg->mode == NPA_MODE_PARTICLE && (s & (s - 1u)) != 0) return NPA_ERR_PARTICLE_MODE_POW2;
+    }
+    return NPA_OK;
+}
+
+/* HashGridConfig::cell_count  config.rs:86-88 */
+uint32_t oracle_cell_count(const npa_grid_cfg* cfg) {
+    uint32_t c = 1;
+    for (uint32_t a = 0; a < cfg->dim; ++a) c *= cfg->grid_size[a];
+    return c;
+}
+
+static int spatial_mem_dims(const npa_grid_cfg* cfg) { return cfg->dim == 3 ? 4 : 2; } /* config.rs:90-92 */
+
+/* ---------------------------------------------------------------- hashgrid */
+
+/* mix_coord  crates/burn_automata_kernels/src/hashgrid.rs:155-163 */
+static uint32_t mix_coord(int64_t value, uint32_t salt) {
+    uint32_t x = ((uint32_t)(int32_t)value) ^ salt;
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+/* particle_cell_hash  hashgrid.rs:147-153 */
+static uint32_t particle_cell_hash(const int64_t coords[3], const npa_grid_cfg* cfg) {
+    uint32_t h = mix_coord(coords[0], 0x9e3779b9u) ^ mix_coord(coords[1], 0x85ebca6bu);
+    if (cfg->dim == 3) h ^= mix_coord(coords[2], 0xc2b2ae35u);
+    return (uint32_t)((uint64_t)h % (uint64_t)oracle_cell_count(cfg));
+}
+
+/* cell_coords_for_position  hashgrid.rs:98-121 */
+void oracle_cell_coords(const float* p, const npa_grid_cfg* cfg, int64_t coords[3]) {
+    coords[0] = coords[1] = coords[2] = 0;
+    for (uint32_t a = 0; a < cfg->dim; ++a) {
+        if (cfg->mode == NPA_MODE_PARTICLE) {
+            coords[a] = f32_to_isize(floorf(p[a] / cfg->eps));
+            continue;
+        }
+        int64_t size = (int64_t)cfg->grid_size[a];
+        float extent = cfg->eps * (float)cfg->grid_size[a];
+        float half = extent * 0.5f;
+        int64_t cell = f32_to_isize(floorf((p[a] + half) / cfg->eps));
+        if (cfg->boundary == NPA_BOUNDARY_PERIODIC) {
+            cell = rem_euclid_i64(cell, size);
+        } else {
+            if (cell < 0) cell = 0;
+            if (cell > size - 1) cell = size - 1;
+        }
+        coords[a] = cell;
+    }
+}
+
+/* cell_index_from_coords  hashgrid.rs:123-145; returns 0 for None */
+static int cell_index_from_coords(const int64_t coords[3], const npa_grid_cfg* cfg, uint32_t* out) {
+    if (cfg->mode == NPA_MODE_PARTICLE) {
+        *out = particle_cell_hash(coords, cfg);
+        return 1;
+    }
+    uint64_t stride = 1, hash = 0;
+    for (uint32_t a = 0; a < cfg->dim; ++a) {
+        int64_t size = (int64_t)cfg->grid_size[a];
+        int64_t cell;
+        if (cfg->boundary == NPA_BOUNDARY_PERIODIC) {
+            cell = rem_euclid_i64(coords[a], size);
+        } else {
+            if (coords[a] < 0 || coords[a] >= size) return 0;
+            cell = coords[a];
+        }
+        hash += (uint64_t)cell * stride;
+        stride *= (uint64_t)size;
+    }
+    *out = (uint32_t)hash;
+    return 1;
+}
+
+/* cell_for_position  hashgrid.rs:71-96 */
+uint32_t oracle_cell_for_position(const float* p, const npa_grid_cfg* cfg) {
+    int64_t coords[3];
+    if (cfg->mode == NPA_MODE_PARTICLE) {
+        oracle_cell_coords(p, cfg, coords);
+        return particle_cell_hash(coords, cfg);
+    }
+    uint64_t stride = 1, hash = 0;
+    for (uint32_t a = 0; a < cfg->dim; ++a) {
+        int64_t size = (int64_t)cfg->grid_size[a];
+        float extent = cfg->eps * (float)cfg->grid_size[a];
+        float half = extent * 0.5f;
+        int64_t cell = f32_to_isize(floorf((p[a] + half) / cfg->eps));
+        if (cfg->boundary == NPA_BOUNDARY_PERIODIC) {
+            cell = rem_euclid_i64(cell, size);
+        } else {
+            if (cell < 0) cell = 0;
+            if (cell > size - 1) cell = size - 1;
+        }
+        hash += (uint64_t)cell * stride;
+        stride *= (uint64_t)size;
+    }
+    return (uint32_t)hash;
+}
+
+/* build_hashgrid  hashgrid.rs:16-69 (serial stable counting sort, as in the reference) */
+int oracle_build_hashgrid(const float* positions, uint32_t batch_size, uint32_t particle_count,
+                          const npa_grid_cfg* cfg, uint32_t* bin_offsets, uint32_t* permutation,
+                          uint32_t* inverse_permutation) {
+    int st = oracle_grid_validate(cfg);
+    if (st) return st;
+    const uint64_t cells = oracle_cell_count(cfg);
+    const uint64_t bins = (uint64_t)batch_size * cells;
+    uint32_t* counts = (uint32_t*)calloc(bins ? bins : 1, sizeof(uint32_t));
+    if (!counts) return NPA_ERR_OUT_OF_MEMORY;
+    for (uint64_t b = 0; b < batch_size; ++b)
+        for (uint64_t i = 0; i < particle_count; ++i) {
+            uint64_t idx = b * particle_count + i;
+            counts[b * cells + oracle_cell_for_position(positions + 4 * idx, cfg)] += 1;
+        }
+    bin_offsets[0] = 0;
+    for (uint64_t k = 0; k < bins; ++k) bin_offsets[k + 1] = bin_offsets[k] + counts[k];
+    /* write_heads = bin_offsets.clone() */
+    for (uint64_t k = 0; k < bins; ++k) counts[k] = bin_offsets[k];
+    for (uint64_t b = 0; b < batch_size; ++b)
+        for (uint64_t i = 0; i < particle_count; ++i) {
+            uint64_t idx = b * particle_count + i;
+            uint64_t bin = b * cells + oracle_cell_for_position(positions + 4 * idx, cfg);
+            uint32_t dst = counts[bin]++;
+            permutation[dst] = (uint32_t)i;
+            inverse_permutation[idx] = (uint32_t)(dst - b * particle_count);
+        }
+    free(counts);
+    return NPA_OK;
+}
+
+/* ------------------------------------------------------------ neighbours */
+
+typedef struct neighbor {
+    uint32_t j;
+    float delta[4];
+    float r2;
+} neighbor;
+
+typedef struct nbuf {
+    neighbor* v;
+    size_t len, cap;
+} nbuf;
+
+static void nbuf_push(nbuf* b, uint32_t j, const float d[4], float r2) {
+    if (b->len == b->cap) {
+        b->cap = b->cap ? 2 * b->cap : 256;
+        b->v = (neighbor*)realloc(b->v, b->cap * sizeof(neighbor));
+    }
+    neighbor* n = &b->v[b->len++];
+    n->j = j;
+    memcpy(n->delta, d, sizeof(n->delta));
+    n->r2 = r2;
+}
+
+/* neighbor_delta  hashgrid.rs:165-181 */
+static void neighbor_delta(const float* lhs, const float* rhs, const npa_grid_cfg* cfg, float d[4]) {
+    d[0] = d[1] = d[2] = d[3] = 0.0f;
+    for (uint32_t a = 0; a < cfg->dim; ++a) {
+        float v = rhs[a] - lhs[a];
+        if (cfg->boundary == NPA_BOUNDARY_PERIODIC) {
+            float extent = (float)cfg->grid_size[a] * cfg->eps;
+            float half = extent * 0.5f;
+            if (v > half) v -= extent;
+            else if (v < -half) v += extent;
+        }
+        d[a] = v;
+    }
+}
+
+typedef struct grid_view {
+    const uint32_t* bin_offsets;
+    const uint32_t* permutation;
+    uint32_t particle_count;
+    uint32_t cell_count;
+} grid_view;
+
+/* for_each_neighbor  crates/burn_automata_kernels/src/reference/neighbor.rs:3-44
+ * (collects the visited (j, delta, r2) triples in visit order) */
+static void collect_neighbors(uint64_t idx, const float* positions, const grid_view* g,
+                              const npa_grid_cfg* cfg, nbuf* out) {
+    out->len = 0;
+    const uint64_t batch = idx / g->particle_count;
+    const uint64_t base = batch * g->particle_count;
+    const float* pi = positions + 4 * idx;
+    int64_t center[3];
+    oracle_cell_coords(pi, cfg, center);
+    const int zmin = cfg->dim == 3 ? -1 : 0, zmax = cfg->dim == 3 ? 1 : 0;
+    const float eps2 = cfg->eps * cfg->eps;
+    for (int dz = zmin; dz <= zmax; ++dz)
+        for (int dy = -1; dy <= 1; ++dy)
+            for (int dx = -1; dx <= 1; ++dx) {
+                int64_t coords[3] = {center[0] + dx, center[1] + dy, center[2] + dz};
+                uint32_t cell;
+                if (!cell_index_from_coords(coords, cfg, &cell)) continue;
+                uint64_t bin = batch * g->cell_count + cell;
+                for (uint32_t s = g->bin_offsets[bin]; s < g->bin_offsets[bin + 1]; ++s) {
+                    uint64_t j = base + g->permutation[s];
+                    const float* pj = positions + 4 * j;
+                    if (cfg->mode == NPA_MODE_PARTICLE) {
+                        int64_t cj[3];
+                        oracle_cell_coords(pj, cfg, cj);
+                        if (cj[0] != coords[0] || cj[1] != coords[1] || cj[2] != coords[2]) continue;
+                    }
+                    float d[4];
+                    neighbor_delta(pi, pj, cfg, d);
+                    float r2 = d[0] * d[0];
+                    for (uint32_t a = 1; a < cfg->dim; ++a) r2 += d[a] * d[a];
+                    if (r2 < eps2) nbuf_push(out, (uint32_t)j, d, r2);
+                }
+            }
+}
+
+typedef struct hashgrid {
+    uint32_t* bin_offsets;
+    uint32_t* permutation;
+    uint32_t* inverse;
+    grid_view view;
+} hashgrid;
+
+static int hashgrid_build(const float* positions, uint32_t batch_size, uint32_t particle_count,
+                          const npa_grid_cfg* cfg, hashgrid* h) {
+    uint64_t total = (uint64_t)batch_size * particle_count;
+    uint64_t bins = (uint64_t)batch_size * oracle_cell_count(cfg);
+    h->bin_offsets = (uint32_t*)malloc((bins + 1) * sizeof(uint32_t));
+    h->permutation = (uint32_t*)malloc((total ? total : 1) * sizeof(uint32_t));
+    h->inverse = (uint32_t*)malloc((total ? total : 1) * sizeof(uint32_t));
+    if (!h->bin_offsets || !h->permutation || !h->inverse) return NPA_ERR_OUT_OF_MEMORY;
+    int st = oracle_build_hashgrid(positions, batch_size, particle_count, cfg, h->bin_offsets,
+                                   h->permutation, h->inverse);
+    h->view.bin_offsets = h->bin_offsets;
+    h->view.permutation = h->permutation;
+    h->view.particle_count = particle_count;
+    h->view.cell_count = oracle_cell_count(cfg);
+    return st;
+}
+
+static void hashgrid_free(hashgrid* h) {
+    free(h->bin_offsets);
+    free(h->permutation);
+    free(h->inverse);
+}
+
+size_t oracle_neighbor_lists(const float* positions, uint32_t batch_size, uint32_t particle_count,
+                             const npa_grid_cfg* cfg, uint32_t* offsets, uint32_t* indices) {
+    if (oracle_grid_validate(cfg)) return (size_t)-1;
+    hashgrid h;
+    if (hashgrid_build(positions, batch_size, particle_count, cfg, &h)) {
+        hashgrid_free(&h);
+        return (size_t)-1;
+    }
+    uint64_t total = (uint64_t)batch_size * particle_count;
+    nbuf buf = {0};
+    size_t len = 0;
+    offsets[0] = 0;
+    for (uint64_t i = 0; i < total; ++i) {
+        collect_neighbors(i, positions, &h.view, cfg, &buf);
+        if (indices)
+            for (size_t k = 0; k < buf.len; ++k) indices[len + k] = buf.v[k].j;
+        len += buf.len;
+        offsets[i + 1] = (uint32_t)len;
+    }
+    free(buf.v);
+    hashgrid_free(&h);
+    return len;
+}
+
+/* --------------------------------------------------------- SPH kernels */
+
+/* smoothing_poly6_normalization / gradient_spiky_normalization
+ * crates/burn_automata_kernels/src/reference/kernels.rs:126-140 */
+static float poly6_norm(const npa_grid_cfg* cfg) {
+    if (cfg->dim == 2) return 4.0f / (PI_F * powi_f32(cfg->eps, 8));
+    return 315.0f / (64.0f * PI_F * powi_f32(cfg->eps, 9));
+}
+static float spiky_norm(const npa_grid_cfg* cfg) {
+    if (cfg->dim == 2) return 10.0f / (PI_F * powi_f32(cfg->eps, 5));
+    return 15.0f / (PI_F * powi_f32(cfg->eps, 6));
+}
+
+/* smoothing_poly6_kernel  kernels.rs:51-58 */
+static float poly6(float r2, const npa_grid_cfg* cfg) {
+    float eps2 = cfg->eps * cfg->eps;
+    if (r2 >= eps2) return 0.0f;
+    float x = eps2 - r2;
+    return poly6_norm(cfg) * x * x * x;
+}
+
+/* spiky_gradient_kernel  kernels.rs:79-96 */
+static void spiky_grad(const float delta[4], float r2, const npa_grid_cfg* cfg, float coeff,
+                       float out[4]) {
+    out[0] = out[1] = out[2] = out[3] = 0.0f;
+    float eps2 = cfg->eps * cfg->eps;
+    if (r2 <= 0.0f || r2 >= eps2) return;
+    float r = sqrtf(r2);
+    float t = cfg->eps - r;
+    float mag = coeff * spiky_norm(cfg) * 3.0f * (t * t) / r;
+    for (uint32_t a = 0; a < cfg->dim; ++a) out[a] = mag * delta[a];
+}
+
+/* RecipFinite::recip_finite  kernels.rs:146-154 */
+static float recip_finite(float x) {
+    if (fabsf(x) <= 1e-20f || !isfinite(x)) return 0.0f;
+    return 1.0f / x;
+}
+
+/* safe_inverse_symmetric  kernels.rs:3-49 */
+static void safe_inverse_symmetric(const float* m, uint32_t dim, float out[9]) {
+    const float TOL = 1e-3f;
+    for (int k = 0; k < 9; ++k) out[k] = 0.0f;
+    if (dim == 2) {
+        float a = m[0], b = m[1], d = m[3];
+        float det = a * d - b * b;
+        if (fabsf(det) < TOL) {
+            out[0] = 1.0f;
+            out[3] = 1.0f;
+            return;
+        }
+        float inv = 1.0f / det;
+        out[0] = d * inv;
+        out[1] = -b * inv;
+        out[2] = -b * inv;
+        out[3] = a * inv;
+        return;
+    }
+    float a = m[0], b = m[1], c = m[2], d = m[4], e = m[5], f = m[8];
+    float t1 = d * f - e * e;
+    float t2 = c * e - b * f;
+    float t3 = b * e - c * d;
+    float det = a * t1 + b * t2 + c * t3;
+    if (fabsf(det) < TOL) {
+        out[0] = 1.0f;
+        out[4] = 1.0f;
+        out[8] = 1.0f;
+        return;
+    }
+    float inv = 1.0f / det;
+    out[0] = t1 * inv;
+    out[1] = t2 * inv;
+    out[2] = t3 * inv;
+    out[3] = t2 * inv;
+    out[4] = (a * f - c * c) * inv;
+    out[5] = (b * c - a * e) * inv;
+    out[6] = t3 * inv;
+    out[7] = (b * c - a * e) * inv;
+    out[8] = (a * d - b * b) * inv;
+}
+
+/* ------------------------------------------------------------- normalize */
+
+/* log_normalize_vector  crates/burn_automata_kernels/src/reference/normalize.rs:60-69 */
+static void log_normalize_vector(float* v, uint32_t n) {
+    const float E = 1.0e-6f;
+    float s = v[0] * v[0];
+    for (uint32_t k = 1; k < n; ++k) s += v[k] * v[k];
+    float norm = fmaxf(sqrtf(s + E * E), E);
+    float scale = log1pf(norm) / norm;
+    for (uint32_t k = 0; k < n; ++k) v[k] *= scale;
+}
+
+/* normalize_state_gradient  normalize.rs:5-30 */
+static void normalize_state_gradient(float* grad, uint64_t total, uint32_t S,
+                                     const npa_grid_cfg* cfg, const npa_perception_opts* o) {
+    float eps0 = fmaxf(o->eps0, FLT_MIN);
+    float scale = o->scale_equivariance ? cfg->eps / eps0 : 1.0f;
+    const uint32_t d = cfg->dim;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)total; ++i) {
+        float* pg = grad + (uint64_t)i * S * d;
+        for (uint32_t c = 0; c < S; ++c) {
+            for (uint32_t a = 0; a < d; ++a) pg[c * d + a] *= scale;
+            if (o->log_norm_grad) log_normalize_vector(pg + c * d, d);
+        }
+    }
+}
+
+/* normalize_density_gradient  normalize.rs:32-58 */
+static void normalize_density_gradient(float* grad, uint64_t total, uint32_t particle_count,
+                                       const npa_grid_cfg* cfg, const npa_perception_opts* o) {
+    float eps0 = fmaxf(o->eps0, FLT_MIN);
+    float s1 = o->scale_equivariance ? powi_f32(cfg->eps / eps0, 1 + (int)cfg->dim) : 1.0f;
+    float s2 = o->particle_density_equivariance
+                   ? 1.0f / (float)(particle_count > 1 ? particle_count : 1)
+                   : 1.0f;
+    float scale = s1 * s2;
+    const uint32_t d = cfg->dim;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)total; ++i) {
+        float* pg = grad + (uint64_t)i * d;
+        for (uint32_t a = 0; a < d; ++a) pg[a] *= scale;
+        if (o->log_norm_density_grad) log_normalize_vector(pg, d);
+    }
+}
+
+/* apply_moment_correction  normalize.rs:93-118 */
+static void apply_moment_correction(float* grad, const float* moment, uint64_t total, uint32_t S,
+                                    const npa_grid_cfg* cfg) {
+    const uint32_t d = cfg->dim;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)total; ++i) {
+        float* pg = grad + (uint64_t)i * S * d;
+        float inv[9];
+        safe_inverse_symmetric(moment + (uint64_t)i * d * d, d, inv);
+        for (uint32_t c = 0; c < S; ++c) {
+            float corrected[4];
+            for (uint32_t o = 0; o < d; ++o) corrected[o] = 0.0f;
+            for (uint32_t o = 0; o < d; ++o)
+                for (uint32_t k = 0; k < d; ++k) corrected[o] += pg[c * d + k] * inv[k * d + o];
+            for (uint32_t o = 0; o < d; ++o) pg[c * d + o] = corrected[o];
+        }
+    }
+}
+
+/* ------------------------------------------------------------ perception */
+
+uint32_t oracle_feature_dims(uint32_t S, uint32_t dim, const npa_perception_opts* o) {
+    /* forward.rs:100-103 */
+    return S * 2 + (o->state_grad ? S * dim : 0) + (o->density_grad ? dim : 0) +
+           (o->position_features ? dim : 0);
+}
+
+/* density  forward.rs:145-160 */
+static void pass_density(const float* positions, const grid_view* g, const npa_grid_cfg* cfg,
+                         uint64_t total, float* rho_out) {
+#pragma omp parallel
+    {
+        nbuf buf = {0};
+#pragma omp for schedule(dynamic, 64)
+        for (int64_t i = 0; i < (int64_t)total; ++i) {
+            collect_neighbors((uint64_t)i, positions, g, cfg, &buf);
+            float rho = 0.0f;
+            for (size_t k = 0; k < buf.len; ++k) rho += poly6(buf.v[k].r2, cfg);
+            rho_out[i] = rho;
+        }
+        free(buf.v);
+    }
+}
+
+/* second_pass_particle  forward.rs:248-295 (density_grad && state_grad branch) */
+static void pass_second(const float* positions, const float* states, const float* density,
+                        uint32_t S, const grid_view* g, const npa_grid_cfg* cfg, uint64_t total,
+                        float* blur, float* sgrad, float* dgrad, float* moment) {
+    const uint32_t d = cfg->dim;
+#pragma omp parallel
+    {
+        nbuf buf = {0};
+#pragma omp for schedule(dynamic, 64)
+        for (int64_t ii = 0; ii < (int64_t)total; ++ii) {
+            uint64_t idx = (uint64_t)ii;
+            collect_neighbors(idx, positions, g, cfg, &buf);
+            float* blur_row = blur + idx * S;
+            float* grad_row = sgrad + idx * S * d;
+            float* dg_row = dgrad + idx * d;
+            float* m_row = moment ? moment + idx * d * d : NULL;
+            const float* si = states + idx * S;
+            for (size_t k = 0; k < buf.len; ++k) {
+                const neighbor* n = &buf.v[k];
+                float volume_j = recip_finite(density[n->j]);
+                float smooth = poly6(n->r2, cfg);
+                const float* sj = states + (uint64_t)n->j * S;
+                for (uint32_t c = 0; c < S; ++c) blur_row[c] += sj[c] * smooth * volume_j;
+                if (idx == n->j) continue;
+                float dgk[4], vg[4];
+                spiky_grad(n->delta, n->r2, cfg, 1.0f, dgk);
+                for (uint32_t a = 0; a < d; ++a) dg_row[a] += dgk[a];
+                spiky_grad(n->delta, n->r2, cfg, volume_j, vg);
+                for (uint32_t c = 0; c < S; ++c) {
+                    float diff = sj[c] - si[c];
+                    for (uint32_t a = 0; a < d; ++a) grad_row[c * d + a] += diff * vg[a];
+                }
+                if (m_row)
+                    for (uint32_t r = 0; r < d; ++r)
+                        for (uint32_t c = 0; c < d; ++c) m_row[r * d + c] += n->delta[r] * vg[c];
+            }
+        }
+        free(buf.v);
+    }
+}
+
+/* blur_state  forward.rs:162-184 */
+static void pass_blur(const float* positions, const float* states, const float* density,
+                      uint32_t S, const grid_view* g, const npa_grid_cfg* cfg, uint64_t total,
+                      float* out) {
+#pragma omp parallel
+    {
+        nbuf buf = {0};
+#pragma omp for schedule(dynamic, 64)
+        for (int64_t i = 0; i < (int64_t)total; ++i) {
+            collect_neighbors((uint64_t)i, positions, g, cfg, &buf);
+            float* dst = out + (uint64_t)i * S;
+            for (size_t k = 0; k < buf.len; ++k) {
+                const neighbor* n = &buf.v[k];
+                float volume_j = recip_finite(density[n->j]);
+                float w = poly6(n->r2, cfg) * volume_j;
+                const float* sj = states + (uint64_t)n->j * S;
+                for (uint32_t c = 0; c < S; ++c) dst[c] += sj[c] * w;
+            }
+        }
+        free(buf.v);
+    }
+}
+
+/* moment_matrix  forward.rs:357-382 */
+static void pass_moment(const float* positions, const float* density, const grid_view* g,
+                        const npa_grid_cfg* cfg, uint64_t total, float* out) {
+    const uint32_t d = cfg->dim;
+#pragma omp parallel
+    {
+        nbuf buf = {0};
+#pragma omp for schedule(dynamic, 64)
+        for (int64_t i = 0; i < (int64_t)total; ++i) {
+            collect_neighbors((uint64_t)i, positions, g, cfg, &buf);
+            float* dst = out + (uint64_t)i * d * d;
+            for (size_t k = 0; k < buf.len; ++k) {
+                const neighbor* n = &buf.v[k];
+                if ((uint64_t)i == n->j) continue;
+                float volume_j = recip_finite(density[n->j]);
+                float grad[4];
+                spiky_grad(n->delta, n->r2, cfg, volume_j, grad);
+                for (uint32_t r = 0; r < d; ++r)
+                    for (uint32_t c = 0; c < d; ++c) dst[r * d + c] += n->delta[r] * grad[c];
+            }
+        }
+        free(buf.v);
+    }
+}
+
+/* compute_state_gradient  forward.rs:297-333 */
+static void pass_state_gradient(const float* positions, const float* states,
+                                const float* density, uint32_t S, const grid_view* g,
+                                const npa_grid_cfg* cfg, uint64_t total, int hybrid, float* out) {
+    const uint32_t d = cfg->dim;
+#pragma omp parallel
+    {
+        nbuf buf = {0};
+#pragma omp for schedule(dynamic, 64)
+        for (int64_t i = 0; i < (int64_t)total; ++i) {
+            collect_neighbors((uint64_t)i, positions, g, cfg, &buf);
+            float* dst = out + (uint64_t)i * S * d;
+            const float* si = states + (uint64_t)i * S;
+            for (size_t k = 0; k < buf.len; ++k) {
+                const neighbor* n = &buf.v[k];
+                if ((uint64_t)i == n->j) continue;
+                float volume_j = recip_finite(density[n->j]);
+                float grad[4];
+                spiky_grad(n->delta, n->r2, cfg, volume_j, grad);
+                const float* sj = states + (uint64_t)n->j * S;
+                for (uint32_t c = 0; c < S; ++c) {
+                    float diff = sj[c] - si[c];
+                    for (uint32_t a = 0; a < d; ++a) dst[c * d + a] += diff * grad[a];
+                }
+            }
+        }
+        free(buf.v);
+    }
+    if (hybrid) {
+        float* moment = (float*)calloc(total * d * d + 1, sizeof(float));
+        pass_moment(positions, density, g, cfg, total, moment);
+        apply_moment_correction(out, moment, total, S, cfg);
+        free(moment);
+    }
+}
+
+/* compute_density_gradient  forward.rs:335-355 */
+static void pass_density_gradient(const float* positions, const grid_view* g,
+                                  const npa_grid_cfg* cfg, uint64_t total, float* out) {
+    const uint32_t d = cfg->dim;
+#pragma omp parallel
+    {
+        nbuf buf = {0};
+#pragma omp for schedule(dynamic, 64)
+        for (int64_t i = 0; i < (int64_t)total; ++i) {
+            collect_neighbors((uint64_t)i, positions, g, cfg, &buf);
+            float* dst = out + (uint64_t)i * d;
+            for (size_t k = 0; k < buf.len; ++k) {
+                const neighbor* n = &buf.v[k];
+                if ((uint64_t)i == n->j) continue;
+                float grad[4];
+                spiky_grad(n->delta, n->r2, cfg, 1.0f, grad);
+                for (uint32_t a = 0; a < d; ++a) dst[a] += grad[a];
+            }
+        }
+        free(buf.v);
+    }
+}
+
+/* perceive_with_options  crates/burn_automata_kernels/src/reference/forward.rs:26-143 */
+int oracle_perceive(const float* positions, const float* states, uint32_t batch_size,
+                    uint32_t particle_count, uint32_t S, const npa_grid_cfg* cfg,
+                    const npa_perception_opts* o, float* features, float* density,
+                    float* blurred_out, float* sgrad_out, float* dgrad_out) {
+    int st = oracle_grid_validate(cfg);
+    if (st) return st;
+    const uint64_t total = (uint64_t)batch_size * particle_count;
+    const uint32_t d = cfg->dim;
+    hashgrid h;
+    st = hashgrid_build(positions, batch_size, particle_count, cfg, &h);
+    if (st) {
+        hashgrid_free(&h);
+        return st;
+    }
+    pass_density(positions, &h.view, cfg, total, density);
+
+    float* blur = (float*)calloc(total * S + 1, sizeof(float));
+    float* sgrad = (float*)calloc(o->state_grad ? total * S * d + 1 : 1, sizeof(float));
+    float* dgrad = (float*)calloc(o->density_grad ? total * d + 1 : 1, sizeof(float));
+    if (o->state_grad && o->density_grad) {
+        float* moment = o->hybrid_state_gradient ? (float*)calloc(total * d * d + 1, sizeof(float)) : NULL;
+        pass_second(positions, states, density, S, &h.view, cfg, total, blur, sgrad, dgrad, moment);
+        if (moment) apply_moment_correction(sgrad, moment, total, S, cfg);
+        normalize_state_gradient(sgrad, total, S, cfg, o);
+        normalize_density_gradient(dgrad, total, particle_count, cfg, o);
+        free(moment);
+    } else {
+        pass_blur(positions, states, density, S, &h.view, cfg, total, blur);
+        if (o->state_grad) {
+            pass_state_gradient(positions, states, density, S, &h.view, cfg, total,
+                                (int)o->hybrid_state_gradient, sgrad);
+            normalize_state_gradient(sgrad, total, S, cfg, o);
+        }
+        if (o->density_grad) {
+            pass_density_gradient(positions, &h.view, cfg, total, dgrad);
+            normalize_density_gradient(dgrad, total, particle_count, cfg, o);
+        }
+    }
+
+    const uint32_t F = oracle_feature_dims(S, d, o);
+    if (features) {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < (int64_t)total; ++i) {
+            float* f = features + (uint64_t)i * F;
+            uint32_t cur = 0;
+            memcpy(f + cur, states + (uint64_t)i * S, S * sizeof(float));
+            cur += S;
+            memcpy(f + cur, blur + (uint64_t)i * S, S * sizeof(float));
+            cur += S;
+            if (o->state_grad) {
+                memcpy(f + cur, sgrad + (uint64_t)i * S * d, S * d * sizeof(float));
+                cur += S * d;
+            }
+            if (o->density_grad) {
+                memcpy(f + cur, dgrad + (uint64_t)i * d, d * sizeof(float));
+                cur += d;
+            }
+            if (o->position_features) memcpy(f + cur, positions + 4 * (uint64_t)i, d * sizeof(float));
+        }
+    }
+    if (blurred_out) memcpy(blurred_out, blur, total * S * sizeof(float));
+    if (sgrad_out && o->state_grad) memcpy(sgrad_out, sgrad, total * S * d * sizeof(float));
+    if (dgrad_out && o->density_grad) memcpy(dgrad_out, dgrad, total * d * sizeof(float));
+    free(blur);
+    free(sgrad);
+    free(dgrad);
+    hashgrid_free(&h);
+    return NPA_OK;
+}
+
+/* ------------------------------------------------------------------ model */
+
+/* NpaConfig::scale_equivariant / particle_density_equivariant  config.rs:145-154 and the
+ * PerceptionOptions that step_cpu builds  crates/burn_automata/src/model.rs:784-800 */
+void oracle_perception_opts_for_model(const npa_model_cfg* m, npa_perception_opts* o) {
+    o->state_grad = m->state_grad;
+    o->density_grad = m->density_grad;
+    o->eps0 = m->eps0;
+    o->scale_equivariance = m->equivariance == NPA_EQUIV_PARTICLE_DENSITY_AND_SCALE;
+    o->particle_density_equivariance = m->equivariance == NPA_EQUIV_PARTICLE_DENSITY ||
+                                       m->equivariance == NPA_EQUIV_PARTICLE_DENSITY_AND_SCALE;
+    o->log_norm_grad = m->log_norm_grad;
+    o->log_norm_density_grad = m->log_norm_density_grad;
+    o->hybrid_state_gradient = 1;
+    o->position_features = m->position_features;
+}
+
+/* NpaConfig::perception_dims  crates/burn_automata/src/config.rs:133-139 (no auxiliary inputs) */
+uint32_t oracle_model_perception_dims(const npa_model_cfg* m) {
+    return m->state_dims * 2 + (m->state_grad ? m->state_dims * m->spatial_dims : 0) +
+           (m->density_grad ? m->spatial_dims : 0) + (m->position_features ? m->spatial_dims : 0);
+}
+
+/* forward_update_from_features  crates/burn_automata/src/model.rs:900-940 */
+int oracle_forward_update(const float* features, uint32_t rows, const npa_model_cfg* m,
+                          const npa_weights* w, float* update) {
+    const uint32_t F = oracle_model_perception_dims(m), H = m->hidden_dims;
+    const uint32_t O = m->spatial_dims + m->state_dims;
+#pragma omp parallel
+    {
+        float* hidden = (float*)malloc((H ? H : 1) * sizeof(float));
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < (int64_t)rows; ++r) {
+            const float* f = features + (uint64_t)r * F;
+            for (uint32_t h = 0; h < H; ++h) {
+                float sum = w->b1[h];
+                const float* wr = w->w1 + (uint64_t)h * F;
+                for (uint32_t i = 0; i < F; ++i) sum += wr[i] * f[i];
+                hidden[h] = fmaxf(sum, 0.0f);
+            }
+            float* u = update + (uint64_t)r * O;
+            for (uint32_t o = 0; o < O; ++o) {
+                float sum = w->b2[o];
+                const float* wr = w->w2 + (uint64_t)o * H;
+                for (uint32_t h = 0; h < H; ++h) sum += wr[h] * hidden[h];
+                u[o] = sum;
+            }
+        }
+        free(hidden);
+    }
+    return NPA_OK;
+}
+
+/* NpaConfig::motion_eps  config.rs:156-162 */
+static float motion_eps(const npa_model_cfg* m, float grid_eps) {
+    return m->equivariance == NPA_EQUIV_PARTICLE_DENSITY_AND_SCALE ? grid_eps : m->eps0;
+}
+
+/* forward_from_features_with_eps  model.rs:867-898 */
+int oracle_forward_from_features(const float* features, uint32_t rows, const npa_model_cfg* m,
+                                 const npa_weights* w, float eps, float* dx, float* ds) {
+    const uint32_t O = m->spatial_dims + m->state_dims, S = m->state_dims, d = m->spatial_dims;
+    float* update = (float*)malloc(((uint64_t)rows * O + 1) * sizeof(float));
+    if (!update) return NPA_ERR_OUT_OF_MEMORY;
+    oracle_forward_update(features, rows, m, w, update);
+    const float meps = motion_eps(m, eps);
+    for (uint64_t r = 0; r < rows; ++r) {
+        const float* u = update + r * O;
+        float norm = 0.0f;
+        for (uint32_t a = 0; a < d; ++a) norm += u[a] * u[a];
+        norm = sqrtf(norm);
+        float* px = dx + 4 * r;
+        px[0] = px[1] = px[2] = px[3] = 0.0f;
+        for (uint32_t a = 0; a < d; ++a) px[a] = m->alpha * u[a] * meps / (1.0f + norm);
+        memcpy(ds + r * S, u + d, S * sizeof(float));
+    }
+    free(update);
+    return NPA_OK;
+}
+
+/* euler_step  crates/burn_automata_kernels/src/reference/step.rs:4-55 */
+int oracle_euler_step(const float* positions, const float* states, const float* dx,
+                      const float* ds, uint32_t batch_size, uint32_t particle_count, uint32_t S,
+                      const npa_grid_cfg* cfg, float dt, const float* mask, float* out_pos,
+                      float* out_states) {
+    const uint64_t total = (uint64_t)batch_size * particle_count;
+    const int mem = spatial_mem_dims(cfg);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)total; ++i) {
+        float m = mask ? mask[i] : 1.0f;
+        float p[4];
+        memcpy(p, positions + 4 * (uint64_t)i, sizeof(p));
+        for (int a = 0; a < mem; ++a) p[a] += dt * dx[4 * (uint64_t)i + a] * m;
+        /* wrap_position  crates/burn_automata_kernels/src/hashgrid.rs:183-193 */
+        if (cfg->boundary == NPA_BOUNDARY_PERIODIC) {
+            for (uint32_t a = 0; a < cfg->dim; ++a) {
+                float extent = (float)cfg->grid_size[a] * cfg->eps;
+                float half = extent * 0.5f;
+                p[a] = rem_euclid_f32(p[a] + half, extent) - half;
+            }
+        }
+        memcpy(out_pos + 4 * (uint64_t)i, p, sizeof(p));
+        const float* s = states + (uint64_t)i * S;
+        const float* dsr = ds + (uint64_t)i * S;
+        float* os = out_states + (uint64_t)i * S;
+        for (uint32_t c = 0; c < S; ++c) {
+            float next = s[c] + dt * dsr[c] * m;
+            if (cfg->dim == 3 && S > 3 && (c == 3 || (S > 8 && c == 8)))
+                next = clamp_f32(next, -8.0f, 24.0f); /* GROWTH_3D_{MIN,MAX}_OPACITY_LOGIT types.rs:1-2 */
+            os[c] = next;
+        }
+    }
+    return NPA_OK;
+}
+
+/* position_conditioned_3d_maturity_gate / motion_gate  crates/burn_automata/src/rollout/mod.rs:67-91 */
+static float maturity_gate(float liveness) { return clamp_f32((4.0f - liveness) * 2.0f, 0.0f, 1.0f); }
+static float motion_gate(float liveness, float signed_distance, int anchored) {
+    if (anchored) return 0.0f;
+    float state_gate = maturity_gate(liveness);
+    float distance_gate = clamp_f32((fabsf(signed_distance) - 0.01f) / 0.02f, 0.0f, 1.0f);
+    return state_gate * distance_gate;
+}
+
+/* NpaModel::step_cpu  crates/burn_automata/src/model.rs:768-858 */
+int oracle_step(const float* positions, const float* states, uint32_t batch_size,
+                uint32_t particle_count, const npa_grid_cfg* grid, const npa_model_cfg* m,
+                const npa_weights* w, float dt, const float* mask, float* out_pos,
+                float* out_states, float* out_density, float* out_dx, float* out_ds) {
+    if (!(m->spatial_dims == 2 || m->spatial_dims == 3)) return NPA_ERR_INVALID_MODEL;
+    if (grid->dim != m->spatial_dims) return NPA_ERR_INVALID_ARGUMENT;
+    const uint64_t total = (uint64_t)batch_size * particle_count;
+    const uint32_t S = m->state_dims;
+    npa_perception_opts o;
+    oracle_perception_opts_for_model(m, &o);
+    const uint32_t F = oracle_model_perception_dims(m);
+    float* features = (float*)malloc((total * F + 1) * sizeof(float));
+    float* density = (float*)malloc((total + 1) * sizeof(float));
+    float* blur = (float*)malloc((total * S + 1) * sizeof(float));
+    float* dx = (float*)malloc((total * 4 + 1) * sizeof(float));
+    float* ds = (float*)malloc((total * S + 1) * sizeof(float));
+    if (!features || !density || !blur || !dx || !ds) return NPA_ERR_OUT_OF_MEMORY;
+
+    double t0 = omp_get_wtime();
+    int st = oracle_perceive(positions, states, batch_size, particle_count, S, grid, &o, features,
+                             density, blur, NULL, NULL);
+    double t1 = omp_get_wtime();
+    if (!st) st = oracle_forward_from_features(features, (uint32_t)total, m, w, grid->eps, dx, ds);
+    double t2 = omp_get_wtime();
+    if (!st && m->spatial_dims == 3 && m->position_features && S > 3) {
+        for (uint64_t r = 0; r < total; ++r) {
+            const float* s = states + r * S;
+            float liveness = s[3];                    /* GROWTH_3D_LIVENESS_CHANNEL */
+            float signed_distance = s[7];             /* UV_TORUS_SIGNED_DISTANCE_STATE_OFFSET */
+            float sg = maturity_gate(liveness);
+            float mg = motion_gate(liveness, signed_distance, positions[4 * r + 3] >= 0.5f);
+            for (uint32_t a = 0; a < m->spatial_dims; ++a) dx[4 * r + a] *= mg;
+            for (uint32_t c = 0; c < S; ++c) ds[r * S + c] *= sg;
+        }
+    }
+    if (!st) st = oracle_euler_step(positions, states, dx, ds, batch_size, particle_count, S, grid,
+                                    dt, mask, out_pos, out_states);
+    double t3 = omp_get_wtime();
+    g_phase_perceive = t1 - t0;
+    g_phase_mlp = t2 - t1;
+    g_phase_integrate = t3 - t2;
+    if (out_density) memcpy(out_density, density, total * sizeof(float));
+    if (out_dx) memcpy(out_dx, dx, total * 4 * sizeof(float));
+    if (out_ds) memcpy(out_ds, ds, total * S * sizeof(float));
+    free(features);
+    free(density);
+    free(blur);
+    free(dx);
+    free(ds);
+    return st;
+}
+
+/* ------------------------------------------------------------------- mask */
+
+/* hash_u32 / random01  crates/burn_automata/src/gpu_step.wgsl:1019-1031 */
+uint32_t oracle_hash_u32(uint32_t x) {
+    x = (x ^ 61u) ^ (x >> 16);
+    x = x + (x << 3);
+    x = x ^ (x >> 4);
+    x = x * 0x27d4eb2du;
+    x = x ^ (x >> 15);
+    return x;
+}
+
+float oracle_random01(uint32_t particle, uint32_t step, uint32_t seed) {
+    uint32_t mixed = oracle_hash_u32(particle ^ oracle_hash_u32(step + 0x9e3779b9u) ^ seed);
+    return (float)(mixed >> 8) * (1.0f / 16777216.0f);
+}
+
+/* gpu_random_seed  crates/burn_automata/src/gpu/helpers/params.rs:186-188 */
+uint32_t oracle_gpu_random_seed(uint64_t seed) { return (uint32_t)seed ^ (uint32_t)(seed >> 32); }
+
+/* update_mask  gpu_step.wgsl:1033-1056, lane seeds gpu_lane_seeds
+ * crates/burn_automata/src/gpu/executor/state.rs:1282-1315 (shared seed, no per-lane seeds) */
+void oracle_update_mask(uint32_t batch_size, uint32_t particle_count, float p, uint32_t step,
+                        uint64_t seed, float* mask) {
+    const uint32_t base = oracle_gpu_random_seed(seed);
+    for (uint64_t b = 0; b < batch_size; ++b) {
+        uint32_t lane_seed = base ^ (uint32_t)(b * particle_count);
+        for (uint64_t i = 0; i < particle_count; ++i) {
+            float v;
+            if (p >= 1.0f) v = 1.0f;
+            else if (p <= 0.0f) v = 0.0f;
+            else v = oracle_random01((uint32_t)i, step, lane_seed) < p ? 1.0f : 0.0f;
+            mask[b * particle_count + i] = v;
+        }
+    }
+}
+
+/* run_rollout_from_particles_with_mask_schedule  crates/burn_automata/src/rollout/mod.rs:240-297,
+ * with the device mask schedule in place of the host StdRng stream. */
+int oracle_rollout(float* positions, float* states, uint32_t batch_size, uint32_t particle_count,
+                   const npa_grid_cfg* grid, const npa_model_cfg* m, const npa_weights* w,
+                   float dt, float update_prob, uint64_t seed, uint32_t start_step,
+                   uint32_t steps) {
+    const uint64_t total = (uint64_t)batch_size * particle_count;
+    const uint32_t S = m->state_dims;
+    float* mask = (float*)malloc((total + 1) * sizeof(float));
+    float* np = (float*)malloc((total * 4 + 1) * sizeof(float));
+    float* ns = (float*)malloc((total * S + 1) * sizeof(float));
+    if (!mask || !np || !ns) return NPA_ERR_OUT_OF_MEMORY;
+    double acc[3] = {0, 0, 0};
+    int st = NPA_OK;
+    for (uint32_t k = 0; k < steps && !st; ++k) {
+        oracle_update_mask(batch_size, particle_count, update_prob, start_step + k, seed, mask);
+        st = oracle_step(positions, states, batch_size, particle_count, grid, m, w, dt, mask, np, ns,
+                         NULL, NULL, NULL);
+        memcpy(positions, np, total * 4 * sizeof(float));
+        memcpy(states, ns, total * S * sizeof(float));
+        acc[0] += g_phase_perceive;
+        acc[1] += g_phase_mlp;
+        acc[2] += g_phase_integrate;
+    }
+    g_phase_perceive = acc[0];
+    g_phase_mlp = acc[1];
+    g_phase_integrate = acc[2];
+    free(mask);
+    free(np);
+    free(ns);
+    return st;
+}
+
+/* ------------------------------------------------------------------ decode */
+
+/* decode_sh_coeffs  crates/burn_automata_kernels/src/gaussian.rs:127-132 */
+uint32_t oracle_decode_sh_coeffs(const npa_gaussian_decode_cfg* cfg) {
+    if (cfg->mode == NPA_DECODE_SH0_ORIENTED) return (cfg->sh_degree + 1) * (cfg->sh_degree + 1);
+    return 1;
+}
+
+static float sigmoid_f32(float v) { return 1.0f / (1.0f + expf(-v)); } /* gaussian.rs:210-212 */
+
+/* decode_gaussians_3d  gaussian.rs:53-100 (+ validate_decode_layout 102-125,
+ * decode_sh 134-158, decode_scale_opacity 160-208, normalize_quat 214-223).
+ * Returns NPA_ERR_INVALID_ARGUMENT where the reference panics. */
+int oracle_decode_gaussians_3d(const float* positions, const float* states, uint32_t count,
+                               uint32_t S, const npa_gaussian_decode_cfg* cfg, float* pos_vis,
+                               float* sh, float* rotation, float* scale_opacity) {
+    const uint32_t K = oracle_decode_sh_coeffs(cfg);
+    switch (cfg->mode) {
+        case NPA_DECODE_PARTICLE_POINT:
+        case NPA_DECODE_SH0_FIXED_SCALE:
+            if (S < 3) return NPA_ERR_INVALID_ARGUMENT;
+            break;
+        case NPA_DECODE_SH0_LEARNED_SCALE:
+            if (S < 5) return NPA_ERR_INVALID_ARGUMENT;
+            break;
+        case NPA_DECODE_SH0_ORIENTED:
+            if (S < K * 3 + 8) return NPA_ERR_INVALID_ARGUMENT;
+            break;
+        default:
+            return NPA_ERR_INVALID_ARGUMENT;
+    }
+    for (uint64_t idx = 0; idx < count; ++idx) {
+        const float* s = states + idx * S;
+        const float* p = positions + 4 * idx;
+        uint32_t color_start = cfg->mode == NPA_DECODE_SH0_ORIENTED ? S - K * 3 : S - 3;
+        for (uint32_t k = 0; k < K; ++k) {
+            uint32_t base = color_start + k * 3;
+            for (int ch = 0; ch < 3; ++ch)
+                sh[(idx * K + k) * 3 + ch] = clamp_f32(s[base + ch] + 0.5f, 0.0f, 1.0f);
+        }
+        float* rot = rotation + 4 * idx;
+        if (cfg->mode == NPA_DECODE_SH0_ORIENTED) {
+            uint32_t rs = color_start - 4;
+            float q[4] = {s[rs], s[rs + 1], s[rs + 2], s[rs + 3]};
+            float norm = sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
+            if (norm <= 1e-8f) {
+                q[0] = 1.0f;
+                q[1] = q[2] = q[3] = 0.0f;
+            } else {
+                for (int k = 0; k < 4; ++k) q[k] /= norm;
+            }
+            memcpy(rot, q, sizeof(q));
+        } else {
+            rot[0] = 1.0f;
+            rot[1] = rot[2] = rot[3] = 0.0f;
+        }
+        float* so = scale_opacity + 4 * idx;
+        switch (cfg->mode) {
+            case NPA_DECODE_PARTICLE_POINT: {
+                float sc = fmaxf(cfg->min_scale, 1.0e-6f);
+                so[0] = so[1] = so[2] = sc;
+                so[3] = 1.0f;
+            } break;
+            case NPA_DECODE_SH0_FIXED_SCALE: {
+                float sc = clamp_f32(cfg->sigma, cfg->min_scale, cfg->max_scale);
+                so[0] = so[1] = so[2] = sc;
+                so[3] = clamp_f32(cfg->opacity_scale, cfg->min_opacity, cfg->max_opacity);
+            } break;
+            case NPA_DECODE_SH0_LEARNED_SCALE: {
+                float scale_logit = clamp_f32(s[S - 5], -8.0f, 8.0f);
+                float opacity_logit = clamp_f32(s[S - 4], -12.0f, 12.0f);
+                float sc = clamp_f32(cfg->sigma * expf(scale_logit), cfg->min_scale, cfg->max_scale);
+                float op = clamp_f32(sigmoid_f32(opacity_logit), cfg->min_opacity, cfg->max_opacity) *
+                           cfg->opacity_scale;
+                so[0] = so[1] = so[2] = sc;
+                so[3] = clamp_f32(op, cfg->min_opacity, cfg->max_opacity);
+            } break;
+            default: { /* oriented */
+                uint32_t anis = color_start - 4 - 4;
+                float ma = fmaxf(cfg->max_anisotropy, 1e-6f);
+                float ax = tanhf(s[anis] / ma) * cfg->max_anisotropy;
+                float ay = tanhf(s[anis + 1] / ma) * cfg->max_anisotropy;
+                float az = tanhf(s[anis + 2] / ma) * cfg->max_anisotropy;
+                float ol = tanhf(s[anis + 3] / ma) * cfg->max_anisotropy;
+                so[0] = clamp_f32(cfg->sigma * expf(ax), cfg->min_scale, cfg->max_scale);
+                so[1] = clamp_f32(cfg->sigma * expf(ay), cfg->min_scale, cfg->max_scale);
+                so[2] = clamp_f32(cfg->sigma * expf(az), cfg->min_scale, cfg->max_scale);
+                so[3] = clamp_f32(cfg->opacity_scale * expf(ol), cfg->min_opacity, cfg->max_opacity);
+            } break;
+        }
+        float* pv = pos_vis + 4 * idx;
+        pv[0] = p[0];
+        pv[1] = p[1];
+        pv[2] = p[2];
+        pv[3] = 1.0f;
+    }
+    return NPA_OK;
+}
+
+/* splat_particles_2d  crates/burn_automata_kernels/src/splat.rs:30-93 */
+int oracle_splat_particles_2d(const float* positions, const float* colors, uint32_t count,
+                              const npa_splat2d_cfg* cfg, float* image) {
+    const int64_t size = cfg->image_size;
+    memset(image, 0, (size_t)(size * size * 4) * sizeof(float));
+    float sigma = cfg->sigma;
+    if (cfg->normalize_color) sigma = sigma * (float)size * cfg->pixel_size / (cfg->hi - cfg->lo);
+    float rf = fmaxf(ceilf(5.0f * sigma), 1.0f);
+    int64_t radius = f32_to_isize(rf);
+    float norm_scale = 1.0f;
+    if (cfg->normalize_color) {
+        float t = (float)size * cfg->pixel_size / (cfg->hi - cfg->lo);
+        norm_scale = t * t;
+    }
+    const int64_t side = 2 * radius + 1;
+    float* wbuf = (float*)malloc((size_t)(side * side) * sizeof(float));
+    int64_t* xbuf = (int64_t*)malloc((size_t)(side * side) * sizeof(int64_t));
+    if (!wbuf || !xbuf) return NPA_ERR_OUT_OF_MEMORY;
+    for (uint64_t n = 0; n < count; ++n) {
+        const float* pos = positions + 4 * n;
+        const float* color = colors + 3 * n;
+        float px = (pos[0] - cfg->lo) / (cfg->hi - cfg->lo) * ((float)size - 1.0f);
+        float py = (pos[1] - cfg->lo) / (cfg->hi - cfg->lo) * ((float)size - 1.0f);
+        if (cfg->y_up) py = ((float)size - 1.0f) - py;
+        int64_t bx = f32_to_isize(floorf(px)), by = f32_to_isize(floorf(py));
+        float fx = px - (float)bx, fy = py - (float)by;
+        size_t nw = 0;
+        float weight_sum = 0.0f;
+        for (int64_t oy = -radius; oy <= radius; ++oy)
+            for (int64_t ox = -radius; ox <= radius; ++ox) {
+                int64_t x = bx + ox, y = by + oy;
+                if (x < 0 || y < 0 || x >= size || y >= size) continue;
+                float dx = (float)ox - fx, dy = (float)oy - fy;
+                float w = expf(-(dx * dx + dy * dy) / (2.0f * sigma * sigma));
+                wbuf[nw] = w;
+                xbuf[nw] = y * size + x;
+                ++nw;
+                weight_sum += w;
+            }
+        float denom = cfg->normalize_color ? fmaxf(weight_sum, 1e-8f) : 1.0f;
+        for (size_t k = 0; k < nw; ++k) {
+            float w = wbuf[k] / denom * norm_scale;
+            float* px4 = image + 4 * xbuf[k];
+            px4[0] += color[0] * w;
+            px4[1] += color[1] * w;
+            px4[2] += color[2] * w;
+            px4[3] += w;
+        }
+    }
+    free(wbuf);
+    free(xbuf);
+    return NPA_OK;
+}

@@ -1,0 +1,350 @@
+"""numpy/ctypes front end of the CPU oracle (oracle/libnpa_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg use it as the checker / port baseline. The product package
+``burn_automata_amd`` never imports this module.
+
+Function names follow the reference's Rust API (crates/burn_automata_kernels,
+crates/burn_automata/src/model.rs); every call returns freshly allocated numpy
+arrays like the reference returns owned Vecs.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from dataclasses import dataclass
+
+import numpy as np
+
+from burn_automata_amd import _abi
+from burn_automata_amd.config import (GaussianDecodeConfig, HashGridConfig, NpaConfig,
+                                      PerceptionOptions, Splat2dConfig)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libnpa_oracle.so")
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compiles the oracle with its Makefile (gcc -O3 -fopenmp -ffp-contract=off)."""
+    args = ["make", "-C", _HERE] + (["-B"] if force else [])
+    subprocess.run(args, check=True, stdout=subprocess.DEVNULL)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = C.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+P = C.c_void_p
+u32 = C.c_uint32
+f32 = C.c_float
+
+
+def _declare(L):
+    L.oracle_grid_validate.argtypes = [C.POINTER(_abi.NpaGridCfg)]
+    L.oracle_cell_count.argtypes = [C.POINTER(_abi.NpaGridCfg)]
+    L.oracle_cell_count.restype = u32
+    L.oracle_cell_for_position.argtypes = [P, C.POINTER(_abi.NpaGridCfg)]
+    L.oracle_cell_for_position.restype = u32
+    L.oracle_cell_coords.argtypes = [P, C.POINTER(_abi.NpaGridCfg), P]
+    L.oracle_build_hashgrid.argtypes = [P, u32, u32, C.POINTER(_abi.NpaGridCfg), P, P, P]
+    L.oracle_neighbor_lists.argtypes = [P, u32, u32, C.POINTER(_abi.NpaGridCfg), P, P]
+    L.oracle_neighbor_lists.restype = C.c_size_t
+    L.oracle_perceive.argtypes = [P, P, u32, u32, u32, C.POINTER(_abi.NpaGridCfg),
+                                  C.POINTER(_abi.NpaPerceptionOpts), P, P, P, P, P]
+    L.oracle_forward_update.argtypes = [P, u32, C.POINTER(_abi.NpaModelCfg),
+                                        C.POINTER(_abi.NpaWeightsC), P]
+    L.oracle_forward_from_features.argtypes = [P, u32, C.POINTER(_abi.NpaModelCfg),
+                                               C.POINTER(_abi.NpaWeightsC), f32, P, P]
+    L.oracle_euler_step.argtypes = [P, P, P, P, u32, u32, u32, C.POINTER(_abi.NpaGridCfg), f32,
+                                    P, P, P]
+    L.oracle_step.argtypes = [P, P, u32, u32, C.POINTER(_abi.NpaGridCfg),
+                              C.POINTER(_abi.NpaModelCfg), C.POINTER(_abi.NpaWeightsC), f32, P,
+                              P, P, P, P, P]
+    L.oracle_hash_u32.argtypes = [u32]
+    L.oracle_hash_u32.restype = u32
+    L.oracle_random01.argtypes = [u32, u32, u32]
+    L.oracle_random01.restype = f32
+    L.oracle_gpu_random_seed.argtypes = [C.c_uint64]
+    L.oracle_gpu_random_seed.restype = u32
+    L.oracle_update_mask.argtypes = [u32, u32, f32, u32, C.c_uint64, P]
+    L.oracle_rollout.argtypes = [P, P, u32, u32, C.POINTER(_abi.NpaGridCfg),
+                                 C.POINTER(_abi.NpaModelCfg), C.POINTER(_abi.NpaWeightsC), f32,
+                                 f32, C.c_uint64, u32, u32]
+    L.oracle_decode_gaussians_3d.argtypes = [P, P, u32, u32,
+                                             C.POINTER(_abi.NpaGaussianDecodeCfg), P, P, P, P]
+    L.oracle_splat_particles_2d.argtypes = [P, P, u32, C.POINTER(_abi.NpaSplat2dCfg), P]
+    L.oracle_last_phase_seconds.argtypes = [C.POINTER(C.c_double)] * 3
+    L.oracle_max_threads.restype = C.c_int
+    L.oracle_set_threads.argtypes = [C.c_int]
+
+
+def _ptr(a):
+    return a.ctypes.data_as(C.c_void_p) if a is not None else None
+
+
+def _f32(a, shape=None):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    if shape is not None:
+        a = a.reshape(shape)
+    return a
+
+
+def _check(code):
+    if code:
+        raise _abi.error_for(code, f"oracle status {code}")
+
+
+def set_threads(n: int):
+    lib().oracle_set_threads(int(n))
+
+
+def max_threads() -> int:
+    return int(lib().oracle_max_threads())
+
+
+def phase_seconds():
+    a, b, c = C.c_double(), C.c_double(), C.c_double()
+    lib().oracle_last_phase_seconds(C.byref(a), C.byref(b), C.byref(c))
+    return {"perceive": a.value, "mlp": b.value, "integrate": c.value}
+
+
+@dataclass
+class HashGridSnapshot:
+    """HashGridSnapshot (crates/burn_automata_kernels/src/hashgrid.rs:3-14)."""
+
+    batch_size: int
+    particle_count: int
+    cell_count: int
+    bin_offsets: np.ndarray
+    permutation: np.ndarray
+    inverse_permutation: np.ndarray
+
+
+def cell_for_position(pos4, cfg: HashGridConfig) -> int:
+    p = _f32(pos4, (4,))
+    return int(lib().oracle_cell_for_position(_ptr(p), C.byref(cfg.to_c())))
+
+
+def cell_coords(pos4, cfg: HashGridConfig):
+    p = _f32(pos4, (4,))
+    out = np.zeros(3, np.int64)
+    lib().oracle_cell_coords(_ptr(p), C.byref(cfg.to_c()), _ptr(out))
+    return tuple(int(v) for v in out)
+
+
+def build_hashgrid(positions, batch_size: int, particle_count: int,
+                   cfg: HashGridConfig) -> HashGridSnapshot:
+    pos = _f32(positions, (-1, 4))
+    if pos.shape[0] != batch_size * particle_count:
+        raise _abi.PositionShape(f"positions {pos.shape[0]} != {batch_size * particle_count}")
+    cells = cfg.cell_count()
+    bo = np.zeros(batch_size * cells + 1, np.uint32)
+    perm = np.zeros(pos.shape[0], np.uint32)
+    inv = np.zeros(pos.shape[0], np.uint32)
+    _check(lib().oracle_build_hashgrid(_ptr(pos), batch_size, particle_count,
+                                       C.byref(cfg.to_c()), _ptr(bo), _ptr(perm), _ptr(inv)))
+    return HashGridSnapshot(batch_size, particle_count, cells, bo, perm, inv)
+
+
+def neighbor_lists(positions, batch_size: int, particle_count: int, cfg: HashGridConfig):
+    pos = _f32(positions, (-1, 4))
+    off = np.zeros(pos.shape[0] + 1, np.uint32)
+    c = cfg.to_c()
+    n = lib().oracle_neighbor_lists(_ptr(pos), batch_size, particle_count, C.byref(c), _ptr(off),
+                                    None)
+    if n == C.c_size_t(-1).value:
+        raise _abi.InvalidArgument("neighbor_lists config error")
+    idx = np.zeros(max(n, 1), np.uint32)
+    lib().oracle_neighbor_lists(_ptr(pos), batch_size, particle_count, C.byref(c), _ptr(off),
+                                _ptr(idx))
+    return off, idx[:n]
+
+
+@dataclass
+class PerceptionOutput:
+    """PerceptionOutput (crates/burn_automata_kernels/src/reference/types.rs:33-41)."""
+
+    features: np.ndarray
+    density: np.ndarray
+    blurred_state: np.ndarray
+    state_gradient: np.ndarray
+    density_gradient: np.ndarray
+    feature_dims: int
+
+
+def perceive_with_options(positions, states, batch_size, particle_count, state_dims,
+                          cfg: HashGridConfig, options: PerceptionOptions) -> PerceptionOutput:
+    pos = _f32(positions, (-1, 4))
+    st = _f32(states).reshape(-1)
+    total = batch_size * particle_count
+    if pos.shape[0] != total:
+        raise _abi.PositionShape(f"positions {pos.shape[0]} != {total}")
+    if st.size != total * state_dims:
+        raise _abi.StateShape(f"states {st.size} != {total * state_dims}")
+    d = cfg.dim
+    F = options.feature_dims(state_dims, d)
+    feats = np.zeros((total, F), np.float32)
+    dens = np.zeros(total, np.float32)
+    blur = np.zeros((total, state_dims), np.float32)
+    sg = np.zeros((total, state_dims * d) if options.state_grad else (0,), np.float32)
+    dg = np.zeros((total, d) if options.density_grad else (0,), np.float32)
+    _check(lib().oracle_perceive(_ptr(pos), _ptr(st), batch_size, particle_count, state_dims,
+                                 C.byref(cfg.to_c()), C.byref(options.to_c()), _ptr(feats),
+                                 _ptr(dens), _ptr(blur), _ptr(sg) if sg.size else None,
+                                 _ptr(dg) if dg.size else None))
+    return PerceptionOutput(feats, dens, blur, sg, dg, F)
+
+
+def perceive(positions, states, batch_size, particle_count, state_dims, cfg: HashGridConfig,
+             state_grad: bool, density_grad: bool) -> PerceptionOutput:
+    """perceive (forward.rs:3-23): PerceptionOptions::new(state_grad, density_grad, cfg.eps)."""
+    return perceive_with_options(positions, states, batch_size, particle_count, state_dims, cfg,
+                                 PerceptionOptions.new(state_grad, density_grad, cfg.eps))
+
+
+def _weights_c(weights):
+    arrs = {k: _f32(weights[k]).reshape(-1) for k in ("w1", "b1", "w2", "b2")}
+    c = _abi.NpaWeightsC(_ptr(arrs["w1"]), _ptr(arrs["b1"]), _ptr(arrs["w2"]), _ptr(arrs["b2"]))
+    return c, arrs
+
+
+def forward_update_from_features(model: NpaConfig, weights, features) -> np.ndarray:
+    f = _f32(features).reshape(-1, model.perception_dims())
+    out = np.zeros((f.shape[0], model.update_dims()), np.float32)
+    wc, keep = _weights_c(weights)
+    _check(lib().oracle_forward_update(_ptr(f), f.shape[0], C.byref(model.to_c()), C.byref(wc),
+                                       _ptr(out)))
+    return out
+
+
+def forward_from_features_with_eps(model: NpaConfig, weights, features, eps: float):
+    f = _f32(features).reshape(-1, model.perception_dims())
+    dx = np.zeros((f.shape[0], 4), np.float32)
+    ds = np.zeros((f.shape[0], model.state_dims), np.float32)
+    wc, keep = _weights_c(weights)
+    _check(lib().oracle_forward_from_features(_ptr(f), f.shape[0], C.byref(model.to_c()),
+                                              C.byref(wc), eps, _ptr(dx), _ptr(ds)))
+    return dx, ds
+
+
+def euler_step(positions, states, dx, ds, batch_size, particle_count, state_dims,
+               cfg: HashGridConfig, dt: float, update_mask=None):
+    pos = _f32(positions, (-1, 4))
+    st = _f32(states).reshape(-1)
+    dxa = _f32(dx, (-1, 4))
+    dsa = _f32(ds).reshape(-1)
+    if dxa.shape[0] != pos.shape[0]:
+        raise _abi.OutputShape(f"dx {dxa.shape[0]} != {pos.shape[0]}")
+    if dsa.size != st.size:
+        raise _abi.OutputShape(f"ds {dsa.size} != {st.size}")
+    m = None if update_mask is None else _f32(update_mask).reshape(-1)
+    op = np.zeros_like(pos)
+    os_ = np.zeros_like(st)
+    _check(lib().oracle_euler_step(_ptr(pos), _ptr(st), _ptr(dxa), _ptr(dsa), batch_size,
+                                   particle_count, state_dims, C.byref(cfg.to_c()), dt, _ptr(m),
+                                   _ptr(op), _ptr(os_)))
+    return op, os_.reshape(-1, state_dims)
+
+
+@dataclass
+class StepOutput:
+    """StepOutput (crates/burn_automata/src/model.rs:737-744) without the perception tensors."""
+
+    next_positions: np.ndarray
+    next_states: np.ndarray
+    density: np.ndarray
+    dx: np.ndarray
+    ds: np.ndarray
+
+
+def step(model: NpaConfig, weights, positions, states, batch_size, particle_count,
+         grid: HashGridConfig, dt: float, update_mask=None) -> StepOutput:
+    """NpaModel::step_cpu (crates/burn_automata/src/model.rs:768-858)."""
+    pos = _f32(positions, (-1, 4))
+    st = _f32(states).reshape(-1)
+    total = batch_size * particle_count
+    S = model.state_dims
+    m = None if update_mask is None else _f32(update_mask).reshape(-1)
+    op = np.zeros((total, 4), np.float32)
+    os_ = np.zeros(total * S, np.float32)
+    dens = np.zeros(total, np.float32)
+    dx = np.zeros((total, 4), np.float32)
+    ds = np.zeros(total * S, np.float32)
+    wc, keep = _weights_c(weights)
+    _check(lib().oracle_step(_ptr(pos), _ptr(st), batch_size, particle_count,
+                             C.byref(grid.to_c()), C.byref(model.to_c()), C.byref(wc), dt, _ptr(m),
+                             _ptr(op), _ptr(os_), _ptr(dens), _ptr(dx), _ptr(ds)))
+    return StepOutput(op, os_.reshape(total, S), dens, dx, ds.reshape(total, S))
+
+
+def hash_u32(v: int) -> int:
+    return int(lib().oracle_hash_u32(v & 0xFFFFFFFF))
+
+
+def random01(particle: int, step: int, seed: int) -> float:
+    return float(lib().oracle_random01(particle & 0xFFFFFFFF, step & 0xFFFFFFFF,
+                                       seed & 0xFFFFFFFF))
+
+
+def update_mask(batch_size, particle_count, update_prob, step_index, seed) -> np.ndarray:
+    out = np.zeros(batch_size * particle_count, np.float32)
+    lib().oracle_update_mask(batch_size, particle_count, update_prob, step_index,
+                             seed & 0xFFFFFFFFFFFFFFFF, _ptr(out))
+    return out
+
+
+def rollout(model: NpaConfig, weights, positions, states, batch_size, particle_count,
+            grid: HashGridConfig, steps: int, dt: float = 1.0, update_prob: float = 0.5,
+            seed: int = 42, start_step: int = 0):
+    pos = _f32(positions, (-1, 4)).copy()
+    st = _f32(states).reshape(-1).copy()
+    wc, keep = _weights_c(weights)
+    _check(lib().oracle_rollout(_ptr(pos), _ptr(st), batch_size, particle_count,
+                                C.byref(grid.to_c()), C.byref(model.to_c()), C.byref(wc), dt,
+                                update_prob, seed & 0xFFFFFFFFFFFFFFFF, start_step, steps))
+    return pos, st.reshape(-1, model.state_dims)
+
+
+def decode_gaussians_3d(positions, states, state_dims, cfg: GaussianDecodeConfig):
+    pos = _f32(positions, (-1, 4))
+    st = _f32(states).reshape(-1)
+    n = pos.shape[0]
+    if st.size != n * state_dims:
+        raise AssertionError("positions.len() * state_dims != states.len()")
+    K = cfg.sh_coeffs()
+    pv = np.zeros((n, 4), np.float32)
+    sh = np.zeros((n, K, 3), np.float32)
+    rot = np.zeros((n, 4), np.float32)
+    so = np.zeros((n, 4), np.float32)
+    _check(lib().oracle_decode_gaussians_3d(_ptr(pos), _ptr(st), n, state_dims,
+                                            C.byref(cfg.to_c()), _ptr(pv), _ptr(sh), _ptr(rot),
+                                            _ptr(so)))
+    return {"position_visibility": pv, "spherical_harmonic": sh, "rotation": rot,
+            "scale_opacity": so}
+
+
+def splat_particles_2d(positions, colors, cfg: Splat2dConfig) -> np.ndarray:
+    pos = _f32(positions, (-1, 4))
+    col = _f32(colors, (-1, 3))
+    if col.shape[0] != pos.shape[0]:
+        raise AssertionError("positions.len() != colors.len()")
+    img = np.zeros((cfg.image_size * cfg.image_size, 4), np.float32)
+    _check(lib().oracle_splat_particles_2d(_ptr(pos), _ptr(col), pos.shape[0],
+                                           C.byref(cfg.to_c()), _ptr(img)))
+    return img
+
+
+def tail_colors(states, state_dims: int) -> np.ndarray:
+    """clamp(state[S-3..S] + 0.5, 0, 1) (crates/burn_automata/examples/infer_2d.rs:20-31)."""
+    s = np.asarray(states, np.float32).reshape(-1, state_dims)
+    base = max(state_dims - 3, 0)
+    return np.clip(s[:, base:base + 3] + np.float32(0.5), 0.0, 1.0).astype(np.float32)
