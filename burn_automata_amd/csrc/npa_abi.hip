@@ -868,9 +868,10 @@ npa_status npa_state_pair_counts(npa_state* s, uint64_t* candidates, uint64_t* p
 }
 
 // ================================================================== profiling
-npa_status npa_profile_enable(npa_context* ctx, int enable) {
+npa_status npa_profile_enable(npa_context* ctx, int kernel_mask) {
     if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
-    ctx->prof.enabled = enable != 0;
+    ctx->prof.enabled = kernel_mask != 0;
+    ctx->prof.mask = (uint32_t)kernel_mask;
     return NPA_OK;
 }
 

@@ -25,6 +25,7 @@ struct DevBuf {
 // Per-context profiling: HIP events bracket launches of selected kernels.
 struct Profiler {
     bool enabled = false;
+    uint32_t mask = 0;  // bit k selects kernel id k
     struct Pair { hipEvent_t a, b; int kernel; };
     std::vector<Pair> pending;
     std::vector<hipEvent_t> pool;
@@ -44,7 +45,7 @@ struct ProfScope {
     hipStream_t s;
     hipEvent_t ev = nullptr;
     ProfScope(Profiler* p_, int k, hipStream_t s_) : p(p_), kernel(k), s(s_) {
-        if (p && p->enabled) p->begin(kernel, s, &ev);
+        if (p && p->enabled && ((p->mask >> kernel) & 1u)) p->begin(kernel, s, &ev);
     }
     ~ProfScope() {
         if (p && p->enabled && ev) p->end(kernel, s, ev);

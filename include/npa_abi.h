@@ -271,10 +271,11 @@ enum {
     NPA_KERNEL_SPLAT = 6,
     NPA_KERNEL_COUNT = 7
 };
-/* When enabled, the library brackets each launch of the listed kernels with HIP
- * events on the context's stream. npa_profile_read synchronizes and returns the
- * summed milliseconds and launch count since the last reset. */
-npa_status npa_profile_enable(npa_context* ctx, int enable);
+/* kernel_mask selects kernels by bit (1 << NPA_KERNEL_*; 0 = off, -1 = all). The
+ * library then brackets each launch of a selected kernel with HIP events on the
+ * context's stream. npa_profile_read synchronizes and returns the summed
+ * milliseconds and launch count since the last reset. */
+npa_status npa_profile_enable(npa_context* ctx, int kernel_mask);
 npa_status npa_profile_reset(npa_context* ctx);
 npa_status npa_profile_read(npa_context* ctx, int kernel_id, double* total_ms, uint64_t* launches);
 /* Work counters of the last step run through a state (exact, from the device):
