@@ -29,33 +29,35 @@ if ROOT not in sys.path:
 
 PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
-UPDATE_KERNEL = 5  # NPA_KERNEL_UPDATE
+KERNEL_IDS = {"density": 4, "perceive": 5, "mlp": 7}  # NPA_KERNEL_* in include/npa_abi.h
 
 
-def update_flops(model, candidates: int, pairs: int, particles: int) -> float:
-    """Algorithmic fp32 operations of one k_update launch: each IEEE add/sub/mul/div/sqrt the
-    reference performs on the density-grad-off path (d = spatial dims, S = state dims):
-      per candidate slot : delta 2 sub, r^2 2 mul + 1 add                                =  5
-      per accepted pair  : poly6 4, weight 1, blur 2S, sqrt+t+t^2+magnitude 7, vg d,
-                           gradient S(1 + 2d), moment 2d^2                      (S=16,d=2: 134)
-      per particle       : moment inverse 15, correction 2Sd^2, scaling Sd, log-norm S(3d+23)
-                           (log1p ~20), MLP 2(FH + HO), motion 3d + 2, Euler 3d + 3S
+def kernel_work(model, candidates: float, pairs: float, particles: int):
+    """Algorithmic fp32 operations and HBM bytes of one launch of each per-step kernel, counting
+    each IEEE add/sub/mul/div/sqrt the reference performs (density-grad-off path; d = spatial
+    dims, S = state dims, F/H/O = MLP widths):
+      density  : per candidate slot 5 (delta 2, r^2 3); per accepted pair 5 (poly6 4, sum 1);
+                 per particle 1 (volume)
+      perceive : per candidate slot 5; per accepted pair 4 + 1 + 2S + 7 + d + S(1 + 2d) + 2d^2
+                 (poly6, weight, blur, sqrt/t/t^2/magnitude, volume gradient, state gradient,
+                 moment; 134 for S=16, d=2); per particle 15 + 2Sd^2 + Sd + S(3d + 23)
+                 (inverse, correction, scaling, log-norm with log1p ~20)
+      mlp      : per particle 2(FH + HO) + (3d + 2) + 3d + 3S (MLP, motion, Euler)
+    Bytes count each particle's own rows once (neighbour rows are re-reads served by caches):
+      density 16 + 4 + 4; perceive 16 + 4S + 4 + 4 + 4F; mlp 4F + 4 + 16 + 4S + 16 + 4S.
     """
     S, d, H = model.state_dims, model.spatial_dims, model.hidden_dims
-    F = model.perception_dims()
-    O = model.update_dims()
+    F, O = model.perception_dims(), model.update_dims()
+    n = float(particles)
     per_pair = 4 + 1 + 2 * S + 7 + d + S * (1 + 2 * d) + 2 * d * d
-    per_particle = (15 + 2 * S * d * d + S * d + S * (3 * d + 23) + 2 * (F * H + H * O)
-                    + (3 * d + 2) + 3 * d + 3 * S)
-    return 5.0 * candidates + per_pair * float(pairs) + per_particle * float(particles)
-
-
-def update_bytes(model, particles: int) -> float:
-    """Algorithmic HBM bytes of one k_update launch: read the sorted record (16 B), state row
-    (4S B) and volume (4 B) of every target once, its original position (16 B) and the
-    permutation entry (4 B); write the new position (16 B) and state row (4S B)."""
-    S = model.state_dims
-    return particles * (16 + 4 * S + 4 + 16 + 4 + 16 + 4 * S)
+    return {
+        "density": (5.0 * candidates + 5.0 * pairs + n, n * 24),
+        "perceive": (5.0 * candidates + per_pair * pairs
+                     + n * (15 + 2 * S * d * d + S * d + S * (3 * d + 23)),
+                     n * (16 + 4 * S + 8 + 4 * F)),
+        "mlp": (n * (2 * (F * H + H * O) + (3 * d + 2) + 3 * d + 3 * S),
+                n * (4 * F + 4 + 32 + 8 * S)),
+    }
 
 
 def cpu_baseline(w, budget_s: float):
@@ -97,7 +99,9 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true",
-                    help="skip the HIP-event bracketing of the update kernel")
+                    help="skip the HIP-event bracketing of the per-step kernels")
+    ap.add_argument("--skip-replay", action="store_true",
+                    help="skip the untimed replay that counts candidates and pairs (profiling runs)")
     args = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -148,33 +152,39 @@ def main(argv=None) -> int:
     import ctypes as C
     if profile:
         ctx.check(L.npa_profile_reset(ctx.handle))
-        ctx.check(L.npa_profile_enable(ctx.handle, 1 << UPDATE_KERNEL))
+        mask = 0
+        for kid in KERNEL_IDS.values():
+            mask |= 1 << kid
+        ctx.check(L.npa_profile_enable(ctx.handle, mask))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     run(state, args.steps)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     elapsed = t1 - t0
-    upd_ms = None
+    kernel_ms = {}
     if profile:
-        tot = C.c_double()
-        cnt = C.c_uint64()
-        ctx.check(L.npa_profile_read(ctx.handle, UPDATE_KERNEL, C.byref(tot), C.byref(cnt)))
+        for name, kid in KERNEL_IDS.items():
+            tot = C.c_double()
+            cnt = C.c_uint64()
+            ctx.check(L.npa_profile_read(ctx.handle, kid, C.byref(tot), C.byref(cnt)))
+            if cnt.value:
+                kernel_ms[name] = tot.value / cnt.value
         ctx.check(L.npa_profile_enable(ctx.handle, 0))
-        upd_ms = tot.value / max(cnt.value, 1)
     _, final_states, _ = ex.read_state(state)
     finite = bool(torch.isfinite(final_states).all().item())
     state.close()
 
     # exact work counts of the timed trajectory (untimed replay of the same steps)
     cand_total = pairs_total = 0
-    rs = ex.create_state(model, pos, st, B, N, w["grid"], w["dt"], w["update_prob"], w["seed"])
-    for _ in range(args.steps):
-        c, p = ex.pair_counts(rs)
-        cand_total += c
-        pairs_total += p
-        ex.step_state(rs)
-    rs.close()
+    if not args.skip_replay:
+        rs = ex.create_state(model, pos, st, B, N, w["grid"], w["dt"], w["update_prob"], w["seed"])
+        for _ in range(args.steps):
+            c, p = ex.pair_counts(rs)
+            cand_total += c
+            pairs_total += p
+            ex.step_state(rs)
+        rs.close()
     mean_cand = cand_total / max(args.steps, 1)
     mean_pairs = pairs_total / max(args.steps, 1)
 
@@ -210,23 +220,28 @@ def main(argv=None) -> int:
             "final_state_finite": finite,
         },
     }
-    if upd_ms is not None:
-        flops = update_flops(w["model"], mean_cand, mean_pairs, total)
-        achieved = flops / (upd_ms * 1e-3) / 1e12
-        byts = update_bytes(w["model"], total)
-        gbs = byts / (upd_ms * 1e-3) / 1e9
+    if kernel_ms and not args.skip_replay:
+        work = kernel_work(w["model"], mean_cand, mean_pairs, total)
+        per_kernel = {}
+        for name, ms in kernel_ms.items():
+            fl, by = work[name]
+            per_kernel[name] = {"mean_launch_ms": ms, "tflops": fl / (ms * 1e-3) / 1e12,
+                                "gbs": by / (ms * 1e-3) / 1e9, "flops_per_launch": fl,
+                                "bytes_per_launch": by}
+        dom = max(kernel_ms, key=kernel_ms.get)
+        k = per_kernel[dom]
         line["roofline"] = {
-            "bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-            "frac": achieved / PEAK_FP32_TFLOPS, "traffic": None,
-            "kernel": "k_update (fused second neighbour pass + features + MLP + masked Euler)",
+            "bound": "mfma", "achieved": k["tflops"], "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+            "frac": k["tflops"] / PEAK_FP32_TFLOPS, "traffic": None, "kernel": dom,
             "engine": "fp32 VALU, unfused mul/add in the reference's order (bit-exact path); the "
                       "MI355X fp32 vector and fp32 matrix peaks are both 157.3 TFLOP/s",
-            "mean_launch_ms": upd_ms, "flops_per_launch": flops,
+            "mean_launch_ms": k["mean_launch_ms"], "flops_per_launch": k["flops_per_launch"],
         }
         line["roofline_hbm"] = {
-            "bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": gbs / PEAK_HBM_GBS, "bytes_per_launch": byts,
+            "bound": "hbm", "achieved": k["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": k["gbs"] / PEAK_HBM_GBS, "kernel": dom, "bytes_per_launch": k["bytes_per_launch"],
         }
+        line["kernels"] = per_kernel
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(line), flush=True)

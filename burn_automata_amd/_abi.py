@@ -26,7 +26,8 @@ NPA_ERR_OUT_OF_MEMORY = 31
 NPA_ERR_COORD_OVERFLOW = 32
 
 # kernel ids for npa_profile_read
-KERNEL_NAMES = ("hash_rank", "table_scan", "offsets_scan", "scatter", "density", "update", "splat")
+KERNEL_NAMES = ("hash_rank", "table_scan", "offsets_scan", "scatter", "density", "perceive", "splat",
+                "mlp")
 
 
 class NpaGridCfg(C.Structure):

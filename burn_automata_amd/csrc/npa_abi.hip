@@ -158,6 +158,10 @@ npa::StepParams make_params(const npa_grid_cfg& cfg, const npa_perception_opts& 
     p.position_features = o.position_features ? 1 : 0;
     p.F = S * 2 + (o.state_grad ? S * cfg.dim : 0) + (o.density_grad ? cfg.dim : 0) +
           (o.position_features ? cfg.dim : 0);
+    p.SS = npa::state_stride_for(S);
+    p.FP = npa::padded_features(p.SS, cfg.dim,
+                                (o.density_grad ? cfg.dim : 0) + (o.position_features ? cfg.dim : 0));
+    p.T = B * N;
     // normalize_state_gradient / normalize_density_gradient  normalize.rs:5-58
     const float eps0 = fmaxf(o.eps0, FLT_MIN);
     p.state_scale = o.scale_equivariance ? cfg.eps / eps0 : 1.0f;
@@ -554,13 +558,18 @@ npa_status npa_step(npa_context* ctx, const float* positions, const float* state
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: positions must be 16-byte aligned");
     if (total && (S % 4 == 0) && !aligned16(sio.states))
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: states must be 16-byte aligned");
-    NPA_HIP(ctx, ctx->ws.reserve(plan, total, B, S, (int)grid->dim), "workspace");
     npa::StepParams p = make_params(*grid, opts_for_model(*model), B, N, S);
     apply_model(&p, *model, grid->eps);
     p.dt = dt;
     p.update_prob = 1.0f;
+    if (total && npa::state_stride_for(S) == S && !aligned16(sio.out_states))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: output states must be 16-byte aligned");
+    NPA_HIP(ctx, ctx->ws.reserve(plan, total, B, S, (int)grid->dim, p.FP), "workspace");
+    NPA_HIP(ctx, ctx->ws.wpad.reserve(npa::padded_weight_floats(p) * 4), "workspace");
     const int blocks = grid_blocks_for(ctx, plan);
     if (total) {
+        NPA_HIP(ctx, npa::launch_pad_weights(p, sio.w1, sio.b1, sio.w2, sio.b2, ctx->ws.wpad.as<float>(), ctx->stream),
+                "pad weights");
         NPA_HIP(ctx, npa::launch_hashgrid(plan, p.g, sio.pos, sio.states, S, B, N, ctx->ws, true, ctx->stream,
                                           &ctx->prof),
                 "hashgrid");
@@ -700,7 +709,13 @@ npa_status npa_state_create(npa_context* ctx, const npa_model_cfg* model, const 
     if (e == hipSuccess) e = s->b1.reserve((uint64_t)H * 4 + 4);
     if (e == hipSuccess) e = s->w2.reserve((uint64_t)O * H * 4 + 4);
     if (e == hipSuccess) e = s->b2.reserve((uint64_t)O * 4 + 4);
-    if (e == hipSuccess) e = s->ws.reserve(plan, total, B, S, (int)grid->dim);
+    const npa::StepParams sp = [&] {
+        npa::StepParams q = make_params(*grid, opts_for_model(*model), B, N, S);
+        apply_model(&q, *model, grid->eps);
+        return q;
+    }();
+    if (e == hipSuccess) e = s->ws.reserve(plan, total, B, S, (int)grid->dim, sp.FP);
+    if (e == hipSuccess) e = s->ws.wpad.reserve(npa::padded_weight_floats(sp) * 4);
     if (e == hipSuccess) e = hipMemcpyAsync(s->pos[0].ptr, positions, total * 16, kind, ctx->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(s->states[0].ptr, states, total * S * 4, kind, ctx->stream);
     if (e == hipSuccess && (uint64_t)H * F) e = hipMemcpyAsync(s->w1.ptr, w->w1, (uint64_t)H * F * 4, kind, ctx->stream);
@@ -708,6 +723,9 @@ npa_status npa_state_create(npa_context* ctx, const npa_model_cfg* model, const 
     if (e == hipSuccess && (uint64_t)O * H) e = hipMemcpyAsync(s->w2.ptr, w->w2, (uint64_t)O * H * 4, kind, ctx->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(s->b2.ptr, w->b2, (uint64_t)O * 4, kind, ctx->stream);
     if (e == hipSuccess) e = hipMemsetAsync(s->density.ptr, 0, total * 4, ctx->stream);
+    if (e == hipSuccess)
+        e = npa::launch_pad_weights(sp, s->w1.as<float>(), s->b1.as<float>(), s->w2.as<float>(), s->b2.as<float>(),
+                                    s->ws.wpad.as<float>(), ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
         delete s;
@@ -783,6 +801,11 @@ npa_status npa_state_update_model(npa_state* s, const npa_weights* w) {
     if (H) NPA_HIP(ctx, hipMemcpyAsync(s->b1.ptr, w->b1, (uint64_t)H * 4, kind, ctx->stream), "b1");
     if ((uint64_t)O * H) NPA_HIP(ctx, hipMemcpyAsync(s->w2.ptr, w->w2, (uint64_t)O * H * 4, kind, ctx->stream), "w2");
     NPA_HIP(ctx, hipMemcpyAsync(s->b2.ptr, w->b2, (uint64_t)O * 4, kind, ctx->stream), "b2");
+    npa::StepParams sp = make_params(s->grid, opts_for_model(m), s->B, s->N, m.state_dims);
+    apply_model(&sp, m, s->grid.eps);
+    NPA_HIP(ctx, npa::launch_pad_weights(sp, s->w1.as<float>(), s->b1.as<float>(), s->w2.as<float>(),
+                                         s->b2.as<float>(), s->ws.wpad.as<float>(), ctx->stream),
+            "pad weights");
     if (ctx->host_io) NPA_HIP(ctx, hipStreamSynchronize(ctx->stream), "sync");
     return NPA_OK;
 }

@@ -48,7 +48,7 @@ void DevBuf::release() {
 }
 
 hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t batch,
-                              uint32_t state_dims, int dim) {
+                              uint32_t state_dims, int dim, uint32_t feature_dims) {
     hipError_t e;
     const uint64_t t1 = total ? total : 1;
     const uint64_t bins = (uint64_t)batch * plan.cells;
@@ -66,9 +66,11 @@ hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t
     NPA_RES(worklist, (plan.worklist_cap + 1) * 8);
     NPA_RES(srec, t1 * 16);
     NPA_RES(scoord, dim == 3 ? t1 * 16 : 16);
-    NPA_RES(sstate, t1 * (uint64_t)(state_dims ? state_dims : 1) * 4);
+    NPA_RES(sstate, t1 * (uint64_t)state_stride_for(state_dims ? state_dims : 1) * 4);
     NPA_RES(svol, t1 * 4);
     NPA_RES(counters, 64);
+    NPA_RES(features, t1 * (uint64_t)(feature_dims ? feature_dims : 1) * 4);
+    NPA_RES(wpad, 4);
 #undef NPA_RES
     if (!flags.ptr) {
         if ((e = flags.reserve(64)) != hipSuccess) return e;
@@ -79,7 +81,7 @@ hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t
 
 void Workspace::release() {
     for (DevBuf* b : {&keys, &ranks, &table, &totals, &bin_offsets, &perm, &inv, &flags, &wl_count,
-                      &worklist, &srec, &scoord, &sstate, &svol, &counters})
+                      &worklist, &srec, &scoord, &sstate, &svol, &counters, &features})
         b->release();
 }
 
@@ -381,14 +383,18 @@ __global__ __launch_bounds__(256) void k_scatter(
         scoord[dst] = make_int4((int)c[0], (int)c[1], (int)c[2], (int)i);
     }
     if (!states) return;  // neighbour-list export needs positions only
+    const uint32_t SS = state_stride_for(S);
     const float* src = states + (uint64_t)i * S;
-    float* out = sstate + (uint64_t)dst * S;
-    if ((S & 3u) == 0) {
+    float4* o4 = reinterpret_cast<float4*>(sstate + (uint64_t)dst * SS);
+    if (S == SS) {  // rows are 16-byte aligned (checked on the host)
         const float4* s4 = reinterpret_cast<const float4*>(src);
-        float4* o4 = reinterpret_cast<float4*>(out);
-        for (uint32_t q = 0; q < S / 4; ++q) o4[q] = s4[q];
+        for (uint32_t q = 0; q < SS / 4; ++q) o4[q] = s4[q];
     } else {
-        for (uint32_t q = 0; q < S; ++q) out[q] = src[q];
+        for (uint32_t q = 0; q < SS / 4; ++q) {
+            const uint32_t c = 4 * q;
+            o4[q] = make_float4(c < S ? src[c] : 0.0f, c + 1 < S ? src[c + 1] : 0.0f,
+                                c + 2 < S ? src[c + 2] : 0.0f, c + 3 < S ? src[c + 3] : 0.0f);
+        }
     }
 }
 

@@ -68,9 +68,9 @@ struct HashgridPlan {
 // Device workspace of one hashgrid + perception pass.
 struct Workspace {
     DevBuf keys, ranks, table, totals, bin_offsets, perm, inv, flags, wl_count, worklist;
-    DevBuf srec, scoord, sstate, svol, counters;
+    DevBuf srec, scoord, sstate, svol, counters, features, wpad;
     hipError_t reserve(const HashgridPlan& plan, uint64_t total, uint32_t batch, uint32_t state_dims,
-                       int dim);
+                       int dim, uint32_t feature_dims = 0);
     void release();
 };
 
@@ -85,6 +85,7 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                            const float* states, uint32_t state_dims, uint32_t batch,
                            uint32_t particle_count, Workspace& ws, bool payload,
                            hipStream_t stream, Profiler* prof);
+// the sorted state rows are written with stride state_stride_for(state_dims), zero padded
 
 // Stable counting sort of a device-resident number (<= cap) of items by key in [0, C):
 // out_vals[offsets[key] + rank] = vals[i] (or i when vals is null), offsets[C+1].
@@ -94,10 +95,24 @@ hipError_t launch_key_sort(const HashgridPlan& plan, const uint32_t* keys, const
                            uint32_t* totals, uint32_t* offsets, uint32_t* out_vals, uint32_t* flags,
                            hipStream_t stream);
 
+// Row width of the sorted state copy: S rounded up to the kernels' template width, zero padded,
+// so the neighbour loops run over a compile-time channel count without bounds guards.
+__host__ __device__ inline uint32_t state_stride_for(uint32_t S) {
+    return S <= 4 ? 4 : S <= 8 ? 8 : S <= 16 ? 16 : S <= 24 ? 24 : 32;
+}
+// Padded feature row used between the perception and MLP kernels:
+// [state SS][blur SS][grad SS*d][density-grad d?, position d?, zero padded to a multiple of 4].
+__host__ __device__ inline uint32_t padded_features(uint32_t SS, uint32_t d, uint32_t rest) {
+    return 2 * SS + SS * d + (rest == 0 ? 0u : rest <= 4 ? 4u : 8u);
+}
+
 // Fused per-step parameters for the perception / update kernels.
 struct StepParams {
     GridParams g;
     uint32_t N, B, S, H, F;
+    uint32_t SS;    // sorted state row stride (state_stride_for(S))
+    uint32_t FP;    // padded feature row width (padded_features)
+    uint32_t T;     // total particles B*N (feature-major row count)
     uint32_t state_grad, density_grad, log_norm_grad, log_norm_dgrad, hybrid, position_features;
     float state_scale;  // normalize_state_gradient factor
     float dgrad_scale;  // normalize_density_gradient factor
@@ -126,11 +141,17 @@ struct StepIO {
     float* density_gradient = nullptr;
 };
 
-// density pass (always) then either the fused update (mode 0) or the perception write-out (mode 1).
+// Density pass; then the perception pass writing feature rows (mode 0: sorted order into the
+// workspace, followed by the MLP + Euler kernel; mode 1: the perceive outputs in original order).
 hipError_t launch_density(const StepParams& p, Workspace& ws, float* density_out, int grid_blocks,
                           hipStream_t stream, Profiler* prof);
 hipError_t launch_update(const StepParams& p, Workspace& ws, const StepIO& io, int mode,
                          int grid_blocks, hipStream_t stream, Profiler* prof);
+// Padded weights for the MLP kernel: w1p [H][FP] (features at their padded positions),
+// b1 [H], w2t [H][D+SS] (transposed), b2p [D+SS]; zeros everywhere else.
+size_t padded_weight_floats(const StepParams& p);
+hipError_t launch_pad_weights(const StepParams& p, const float* w1, const float* b1, const float* w2,
+                              const float* b2, float* wpad, hipStream_t stream);
 hipError_t launch_mlp_forward(const StepParams& p, const float* features, uint32_t rows,
                               const StepIO& io, float* dx, float* ds, hipStream_t stream);
 hipError_t launch_euler(const StepParams& p, const float4* pos, const float* states,

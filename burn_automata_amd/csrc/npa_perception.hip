@@ -1,21 +1,21 @@
-// npa_perception.hip - SPH neighbour passes and the fused rollout update on gfx950.
+// npa_perception.hip - SPH neighbour passes and the rollout update on gfx950.
 //
 // Work mapping: the hashgrid build emits one work item per <=64 consecutive sorted
-// slots of a bin, so each wavefront's lanes are targets of one bin and (outside hash
-// collisions) share the same 3x3(x3) neighbour cells: the neighbour loop runs in
-// lockstep and every candidate record / state row is a single broadcast load.
-// Each lane accumulates its own sums serially in the reference's neighbour order
-// (cells dz, dy, dx; slots ascending = particle index ascending), so the sums are
-// bit-identical to the CPU path.
+// slots of a bin, so each wavefront's lanes are targets of one bin and share (per group
+// of equal cell coordinates) the same 3x3(x3) neighbour cells. Each lane accumulates its
+// own sums serially in the reference's neighbour order (cells dz, dy, dx; slots ascending
+// = particle index ascending), so the sums are bit-identical to the CPU path.
 //
-//   k_density  rho_i = sum_j W_poly6(r_ij^2)        forward.rs:145-160
-//   k_update   second pass (blur, state gradient, density gradient, moment matrix)
-//              forward.rs:162-382 -> moment correction, scaling, log-norm
-//              normalize.rs:5-118 -> feature row (never stored) -> update MLP
-//              model.rs:900-940 -> motion scaling model.rs:867-898 -> 3D gates
-//              model.rs:806-837 -> masked Euler step.rs:4-55, written to the
-//              ping-pong output in original particle order.
+//   k_density    rho_i = sum_j W_poly6(r_ij^2)                          forward.rs:145-160
+//   k_perceive   second pass (blur, state gradient, density gradient, moment matrix)
+//                forward.rs:162-382 -> moment correction, scaling, log-norm
+//                normalize.rs:5-118 -> feature row                     forward.rs:100-133
+//   k_mlp_euler  update MLP model.rs:900-940 -> motion scaling model.rs:867-898 -> 3D gates
+//                model.rs:806-837 -> masked Euler step.rs:4-55, written to the ping-pong
+//                output in original particle order.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 
 #include "npa_internal.hpp"
 
@@ -93,218 +93,476 @@ __device__ __forceinline__ void walk_neighbors(const GridParams& g, uint32_t b, 
         const uint32_t s = item.x + lane;
 #define NPA_WAVE_LOOP_END }
 
+// ------------------------------------------------------------------------------------------
+// Wave-per-bin neighbour passes with LDS-staged candidates.
+//
+// A work item is <= 64 consecutive sorted slots of one bin; the lanes are its targets.
+// Lanes are processed in groups of equal cell coordinates (a hash bin can hold several
+// true cells), so inside a group the 3x3(x3) neighbour bins, each candidate's Particle-mode
+// coordinate test and the loop bounds are wave-uniform. Each neighbour bin is streamed through
+// LDS 64 candidates at a time with one coalesced load per lane; lanes then read candidates
+// as LDS broadcasts. Per lane, candidates are visited in cell order and ascending slot order,
+// which is the reference's for_each_neighbor order, so every per-target sum is unchanged.
+constexpr int kChunk = 64;
+
+__device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+
 template <int D>
-__global__ __launch_bounds__(256) void k_density(StepParams P, const float4* __restrict__ srec,
+struct NbrStage {
+    float4 rec[kChunk];
+    int4 crd[D == 3 ? kChunk : 1];
+};
+
+template <int D>
+__device__ __forceinline__ void stage_records(NbrStage<D>& st, const float4* __restrict__ srec,
+                                              const int4* __restrict__ scoord, uint32_t base, uint32_t m,
+                                              uint32_t lane) {
+    if (lane < m) {
+        st.rec[lane] = srec[base + lane];
+        if constexpr (D == 3) st.crd[lane] = scoord[base + lane];
+    }
+}
+
+template <int D>
+__device__ __forceinline__ bool staged_coords_match(const NbrStage<D>& st, uint32_t k, const float4& r,
+                                                    int64_t n0, int64_t n1, int64_t n2) {
+    if constexpr (D == 2) {
+        return (int64_t)__float_as_int(r.z) == n0 && (int64_t)__float_as_int(r.w) == n1;
+    } else {
+        const int4 q = st.crd[k];
+        return (int64_t)q.x == n0 && (int64_t)q.y == n1 && (int64_t)q.z == n2;
+    }
+}
+
+// Iterates the coordinate groups of the current item and, per group, the staged candidate
+// chunks of its neighbour bins. `on_chunk(base, m, n0, n1, n2, in_group)` runs after each
+// chunk is staged (LDS written and visible to the wave).
+template <int D, class OnChunk, class Stage>
+__device__ __forceinline__ void for_each_group_chunk(const GridParams& g, uint32_t b, bool active, const int* ci,
+                                                     const uint32_t* __restrict__ bo, uint32_t lane,
+                                                     Stage&& stage, OnChunk&& on_chunk) {
+    uint64_t pending = __ballot(active);
+    while (pending) {
+        const int leader = __ffsll((unsigned long long)pending) - 1;
+        const int l0 = readlane_i(ci[0], leader), l1 = readlane_i(ci[1], leader);
+        const int l2 = D == 3 ? readlane_i(ci[2], leader) : 0;
+        const bool same = active && ci[0] == l0 && ci[1] == l1 && (D == 2 || ci[2] == l2);
+        const uint64_t group = __ballot(same) & pending;
+        pending &= ~group;
+        const bool in_group = (group >> lane) & 1ull;
+        constexpr int ZLO = D == 3 ? -1 : 0, ZHI = D == 3 ? 1 : 0;
+        for (int dz = ZLO; dz <= ZHI; ++dz)
+            for (int dy = -1; dy <= 1; ++dy)
+                for (int dx = -1; dx <= 1; ++dx) {
+                    const int64_t n0 = (int64_t)l0 + dx, n1 = (int64_t)l1 + dy, n2 = (int64_t)l2 + dz;
+                    uint32_t cell;
+                    if (!cell_index(n0, n1, n2, g, &cell)) continue;
+                    const uint64_t bin = (uint64_t)b * g.cells + cell;
+                    const uint32_t beg = bo[bin], end = bo[bin + 1];
+                    for (uint32_t base = beg; base < end; base += kChunk) {
+                        const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
+                        __syncthreads();  // the previous chunk has been consumed by every lane
+                        stage(base, m);
+                        __syncthreads();
+                        on_chunk(base, m, n0, n1, n2, in_group);
+                    }
+                }
+    }
+}
+
+// density  forward.rs:145-160: rho_i = sum_j W_poly6(r_ij^2)
+template <int D>
+__global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __restrict__ srec,
+                                                const int4* __restrict__ scoord,
+                                                const uint32_t* __restrict__ bo,
+                                                const uint32_t* __restrict__ perm,
+                                                const uint2* __restrict__ wl,
+                                                const uint32_t* __restrict__ wl_count,
+                                                float* __restrict__ svol, float* __restrict__ density_out) {
+    __shared__ NbrStage<D> st;
+    const uint32_t lane = threadIdx.x;
+    const uint32_t items = *wl_count;
+    for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
+        const uint2 item = wl[it];
+        const bool active = lane < item.y;
+        const uint32_t s = item.x + (active ? lane : 0u);
+        const uint32_t b = item.x / P.N;
+        float pi[3];
+        int ci[3];
+        load_rec<D>(srec, scoord, s, pi, ci);
+        float rho = 0.0f;
+        for_each_group_chunk<D>(
+            P.g, b, active, ci, bo, lane,
+            [&](uint32_t base, uint32_t m) { stage_records<D>(st, srec, scoord, base, m, lane); },
+            [&](uint32_t, uint32_t m, int64_t n0, int64_t n1, int64_t n2, bool in_group) {
+                for (uint32_t k = 0; k < m; ++k) {
+                    const float4 r = st.rec[k];
+                    if (P.g.mode == 1 && !staged_coords_match<D>(st, k, r, n0, n1, n2)) continue;
+                    const float d0 = delta_axis(pi[0], r.x, 0, P.g);
+                    const float d1 = delta_axis(pi[1], r.y, 1, P.g);
+                    float r2 = d0 * d0;
+                    r2 += d1 * d1;
+                    if constexpr (D == 3) {
+                        const float d2 = delta_axis(pi[2], r.z, 2, P.g);
+                        r2 += d2 * d2;
+                    }
+                    if (in_group && r2 < P.g.eps2) rho += poly6(r2, P.g);
+                }
+            });
+        if (active) {
+            svol[s] = recip_finite(rho);
+            if (density_out) density_out[b * P.N + perm[s]] = rho;
+        }
+    }
+}
+
+template <int D, int SM>
+struct PerceiveStage {
+    NbrStage<D> nb;
+    float vol[kChunk];
+    float st[kChunk * (SM + 1)];  // odd row stride keeps per-lane row gathers on distinct banks
+};
+
+// Second neighbour pass + normalisation + feature row. SM is the sorted-state row width
+// (state channels zero padded to SM), so every channel loop is a compile-time loop.
+// MODE 0: padded feature rows, feature-major (features[k * T + s]) for the MLP kernel.
+// MODE 1: the perceive_with_options outputs in original particle order.
+template <int D, int SM, int MODE>
+__global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __restrict__ srec,
                                                  const int4* __restrict__ scoord,
+                                                 const float* __restrict__ sstate,
+                                                 const float* __restrict__ svol,
                                                  const uint32_t* __restrict__ bo,
                                                  const uint32_t* __restrict__ perm,
                                                  const uint2* __restrict__ wl,
                                                  const uint32_t* __restrict__ wl_count,
-                                                 float* __restrict__ svol, float* __restrict__ density_out) {
-    NPA_WAVE_LOOP_BEGIN(wl, wl_count)
-    const uint32_t b = s / P.N;
-    float pi[3];
-    int ci[3];
-    load_rec<D>(srec, scoord, s, pi, ci);
-    float rho = 0.0f;
-    walk_neighbors<D>(P.g, b, pi, ci, bo, srec, scoord,
-                      [&](uint32_t, const float*, float r2) { rho += poly6(r2, P.g); });
-    svol[s] = recip_finite(rho);
-    if (density_out) density_out[b * P.N + perm[s]] = rho;
-    NPA_WAVE_LOOP_END
-}
-
-// MODE 0: fused rollout step. MODE 1: perception outputs (features etc.).
-template <int D, int SM, int MODE>
-__global__ __launch_bounds__(256) void k_update(StepParams P, const float4* __restrict__ srec,
-                                                const int4* __restrict__ scoord,
-                                                const float* __restrict__ sstate,
-                                                const float* __restrict__ svol,
-                                                const uint32_t* __restrict__ bo,
-                                                const uint32_t* __restrict__ perm,
-                                                const uint2* __restrict__ wl,
-                                                const uint32_t* __restrict__ wl_count, StepIO io) {
-    const uint32_t S = P.S;
-    NPA_WAVE_LOOP_BEGIN(wl, wl_count)
-    const uint32_t b = s / P.N;
-    const uint32_t li = perm[s];
-    const uint32_t i = b * P.N + li;
-    float pi[3];
-    int ci[3];
-    load_rec<D>(srec, scoord, s, pi, ci);
-
-    float si[SM], blur[SM], grad[SM * D], dg[D], mom[D * D];
-#pragma unroll
-    for (int c = 0; c < SM; ++c) {
-        si[c] = (uint32_t)c < S ? sstate[(uint64_t)s * S + c] : 0.0f;
-        blur[c] = 0.0f;
-    }
-#pragma unroll
-    for (int k = 0; k < SM * D; ++k) grad[k] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < D; ++k) dg[k] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < D * D; ++k) mom[k] = 0.0f;
-
+                                                 float* __restrict__ sfeatures, StepIO io) {
+    __shared__ PerceiveStage<D, SM> st;
+    const uint32_t lane = threadIdx.x;
+    const uint32_t items = *wl_count;
     const bool branch_a = P.state_grad && P.density_grad;
     const bool want_sg = P.state_grad != 0, want_dg = P.density_grad != 0;
     const bool want_m = want_sg && P.hybrid;
-    walk_neighbors<D>(P.g, b, pi, ci, bo, srec, scoord, [&](uint32_t j, const float* d, float r2) {
-        const float vol = svol[j];
-        const float smooth = poly6(r2, P.g);
-        const float* sj = sstate + (uint64_t)j * S;
-        float sv[SM];
+    for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
+        const uint2 item = wl[it];
+        const bool active = lane < item.y;
+        const uint32_t s = item.x + (active ? lane : 0u);
+        const uint32_t b = item.x / P.N;
+        float pi[3];
+        int ci[3];
+        load_rec<D>(srec, scoord, s, pi, ci);
+        float si[SM], blur[SM], grad[SM * D], dg[D], mom[D * D];
+        {
+            const float4* own = reinterpret_cast<const float4*>(sstate + (uint64_t)s * SM);
 #pragma unroll
-        for (int c = 0; c < SM; ++c) sv[c] = (uint32_t)c < S ? sj[c] : 0.0f;
-        if (branch_a) {  // second_pass_particle forward.rs:263-270
-#pragma unroll
-            for (int c = 0; c < SM; ++c)
-                if ((uint32_t)c < S) blur[c] += sv[c] * smooth * vol;
-        } else {  // blur_state forward.rs:174-180
-            const float w = smooth * vol;
-#pragma unroll
-            for (int c = 0; c < SM; ++c)
-                if ((uint32_t)c < S) blur[c] += sv[c] * w;
+            for (int q = 0; q < SM / 4; ++q) {
+                const float4 v = own[q];
+                si[4 * q] = v.x;
+                si[4 * q + 1] = v.y;
+                si[4 * q + 2] = v.z;
+                si[4 * q + 3] = v.w;
+            }
         }
-        if (j == s) return;
-        if (r2 <= 0.0f) return;  // spiky_gradient_kernel returns zeros (kernels.rs:87-89)
-        const float r = sqrtf(r2);
-        const float t = P.g.eps - r;
-        if (want_dg) {  // spiky_gradient_kernel(coeff = 1)
-            const float mag = 1.0f * P.g.k5 * 3.0f * (t * t) / r;
 #pragma unroll
-            for (int a = 0; a < D; ++a) dg[a] += mag * d[a];
-        }
-        if (want_sg) {  // spiky_gradient_kernel(coeff = volume_j)
-            const float mag = vol * P.g.k5 * 3.0f * (t * t) / r;
-            float vg[D];
+        for (int c = 0; c < SM; ++c) blur[c] = 0.0f;
 #pragma unroll
-            for (int a = 0; a < D; ++a) vg[a] = mag * d[a];
+        for (int k = 0; k < SM * D; ++k) grad[k] = 0.0f;
 #pragma unroll
-            for (int c = 0; c < SM; ++c) {
-                if ((uint32_t)c < S) {
-                    const float diff = sv[c] - si[c];
+        for (int k = 0; k < D; ++k) dg[k] = 0.0f;
 #pragma unroll
-                    for (int a = 0; a < D; ++a) grad[c * D + a] += diff * vg[a];
+        for (int k = 0; k < D * D; ++k) mom[k] = 0.0f;
+
+        for_each_group_chunk<D>(
+            P.g, b, active, ci, bo, lane,
+            [&](uint32_t base, uint32_t m) {
+                stage_records<D>(st.nb, srec, scoord, base, m, lane);
+                if (lane < m) {
+                    st.vol[lane] = svol[base + lane];
+                    const float4* src = reinterpret_cast<const float4*>(sstate + (uint64_t)(base + lane) * SM);
+                    float* dst = st.st + lane * (SM + 1);
+#pragma unroll
+                    for (int q = 0; q < SM / 4; ++q) {
+                        const float4 v = src[q];
+                        dst[4 * q] = v.x;
+                        dst[4 * q + 1] = v.y;
+                        dst[4 * q + 2] = v.z;
+                        dst[4 * q + 3] = v.w;
+                    }
                 }
-            }
-            if (want_m) {
+            },
+            [&](uint32_t base, uint32_t m, int64_t n0, int64_t n1, int64_t n2, bool in_group) {
+                // accepted candidates of this lane, as a bit mask over the chunk
+                uint64_t acc = 0;
+                for (uint32_t k = 0; k < m; ++k) {
+                    const float4 r = st.nb.rec[k];
+                    if (P.g.mode == 1 && !staged_coords_match<D>(st.nb, k, r, n0, n1, n2)) continue;
+                    const float d0 = delta_axis(pi[0], r.x, 0, P.g);
+                    const float d1 = delta_axis(pi[1], r.y, 1, P.g);
+                    float r2 = d0 * d0;
+                    r2 += d1 * d1;
+                    if constexpr (D == 3) {
+                        const float d2 = delta_axis(pi[2], r.z, 2, P.g);
+                        r2 += d2 * d2;
+                    }
+                    if (in_group && r2 < P.g.eps2) acc |= 1ull << k;
+                }
+                while (acc) {
+                    const uint32_t k = (uint32_t)__builtin_ctzll(acc);
+                    acc &= acc - 1;
+                    const float4 r = st.nb.rec[k];
+                    float d[3];
+                    d[0] = delta_axis(pi[0], r.x, 0, P.g);
+                    d[1] = delta_axis(pi[1], r.y, 1, P.g);
+                    float r2 = d[0] * d[0];
+                    r2 += d[1] * d[1];
+                    if constexpr (D == 3) {
+                        d[2] = delta_axis(pi[2], r.z, 2, P.g);
+                        r2 += d[2] * d[2];
+                    } else {
+                        d[2] = 0.0f;
+                    }
+                    const float vol = st.vol[k];
+                    const float smooth = poly6(r2, P.g);
+                    const float* sj = st.st + k * (SM + 1);
+                    float sv[SM];
 #pragma unroll
-                for (int rr = 0; rr < D; ++rr)
+                    for (int c = 0; c < SM; ++c) sv[c] = sj[c];
+                    if (branch_a) {  // second_pass_particle forward.rs:263-270
 #pragma unroll
-                    for (int cc = 0; cc < D; ++cc) mom[rr * D + cc] += d[rr] * vg[cc];
-            }
-        }
-    });
+                        for (int c = 0; c < SM; ++c) blur[c] += sv[c] * smooth * vol;
+                    } else {  // blur_state forward.rs:174-180
+                        const float w = smooth * vol;
+#pragma unroll
+                        for (int c = 0; c < SM; ++c) blur[c] += sv[c] * w;
+                    }
+                    if (base + k == s) continue;
+                    if (r2 <= 0.0f) continue;  // spiky_gradient_kernel returns zeros (kernels.rs:87-89)
+                    const float rr = sqrtf(r2);
+                    const float t = P.g.eps - rr;
+                    if (want_dg) {  // spiky_gradient_kernel(coeff = 1)
+                        const float mag = 1.0f * P.g.k5 * 3.0f * (t * t) / rr;
+#pragma unroll
+                        for (int a = 0; a < D; ++a) dg[a] += mag * d[a];
+                    }
+                    if (want_sg) {  // spiky_gradient_kernel(coeff = volume_j)
+                        const float mag = vol * P.g.k5 * 3.0f * (t * t) / rr;
+                        float vg[D];
+#pragma unroll
+                        for (int a = 0; a < D; ++a) vg[a] = mag * d[a];
+#pragma unroll
+                        for (int c = 0; c < SM; ++c) {
+                            const float diff = sv[c] - si[c];
+#pragma unroll
+                            for (int a = 0; a < D; ++a) grad[c * D + a] += diff * vg[a];
+                        }
+                        if (want_m) {
+#pragma unroll
+                            for (int ra = 0; ra < D; ++ra)
+#pragma unroll
+                                for (int ca = 0; ca < D; ++ca) mom[ra * D + ca] += d[ra] * vg[ca];
+                        }
+                    }
+                }
+            });
+        if (!active) continue;
 
-    if (want_sg) {
-        if (want_m) {  // apply_moment_correction normalize.rs:93-118
-            float inv[D * D];
-            safe_inverse<D>(mom, inv);
-#pragma unroll
-            for (int c = 0; c < SM; ++c) {
-                float corrected[D];
-#pragma unroll
-                for (int o = 0; o < D; ++o) corrected[o] = 0.0f;
-#pragma unroll
-                for (int o = 0; o < D; ++o)
-#pragma unroll
-                    for (int k = 0; k < D; ++k) corrected[o] += grad[c * D + k] * inv[k * D + o];
-#pragma unroll
-                for (int o = 0; o < D; ++o) grad[c * D + o] = corrected[o];
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < SM; ++c) {  // normalize_state_gradient normalize.rs:5-30
-#pragma unroll
-            for (int a = 0; a < D; ++a) grad[c * D + a] *= P.state_scale;
-            if (P.log_norm_grad) log_normalize<D>(&grad[c * D]);
-        }
-    }
-    if (want_dg) {  // normalize_density_gradient normalize.rs:32-58
-#pragma unroll
-        for (int a = 0; a < D; ++a) dg[a] *= P.dgrad_scale;
-        if (P.log_norm_dgrad) log_normalize<D>(dg);
-    }
-    const float4 pos4 = io.pos[i];
-    const float porig[4] = {pos4.x, pos4.y, pos4.z, pos4.w};
-
-    if constexpr (MODE == 1) {
-        // feature assembly forward.rs:100-133
-        float* f = io.features + (uint64_t)i * P.F;
-        uint32_t off = 0;
-#pragma unroll
-        for (int c = 0; c < SM; ++c)
-            if ((uint32_t)c < S) f[off + c] = si[c];
-        off += S;
-#pragma unroll
-        for (int c = 0; c < SM; ++c)
-            if ((uint32_t)c < S) {
-                f[off + c] = blur[c];
-                if (io.blurred) io.blurred[(uint64_t)i * S + c] = blur[c];
-            }
-        off += S;
         if (want_sg) {
+            if (want_m) {  // apply_moment_correction normalize.rs:93-118
+                float inv[D * D];
+                safe_inverse<D>(mom, inv);
 #pragma unroll
-            for (int k = 0; k < SM * D; ++k)
-                if ((uint32_t)k < S * D) {
-                    f[off + k] = grad[k];
-                    if (io.state_gradient) io.state_gradient[(uint64_t)i * S * D + k] = grad[k];
+                for (int c = 0; c < SM; ++c) {
+                    float corrected[D];
+#pragma unroll
+                    for (int o = 0; o < D; ++o) corrected[o] = 0.0f;
+#pragma unroll
+                    for (int o = 0; o < D; ++o)
+#pragma unroll
+                        for (int k = 0; k < D; ++k) corrected[o] += grad[c * D + k] * inv[k * D + o];
+#pragma unroll
+                    for (int o = 0; o < D; ++o) grad[c * D + o] = corrected[o];
                 }
-            off += S * D;
-        }
-        if (want_dg) {
-#pragma unroll
-            for (int a = 0; a < D; ++a) {
-                f[off + a] = dg[a];
-                if (io.density_gradient) io.density_gradient[(uint64_t)i * D + a] = dg[a];
             }
-            off += D;
+#pragma unroll
+            for (int c = 0; c < SM; ++c) {  // normalize_state_gradient normalize.rs:5-30
+#pragma unroll
+                for (int a = 0; a < D; ++a) grad[c * D + a] *= P.state_scale;
+                if (P.log_norm_grad) log_normalize<D>(&grad[c * D]);
+            }
         }
+        if (want_dg) {  // normalize_density_gradient normalize.rs:32-58
+#pragma unroll
+            for (int a = 0; a < D; ++a) dg[a] *= P.dgrad_scale;
+            if (P.log_norm_dgrad) log_normalize<D>(dg);
+        }
+        // feature assembly forward.rs:100-133
+        const uint32_t i = b * P.N + perm[s];
+        float pp[3] = {0.0f, 0.0f, 0.0f};
         if (P.position_features) {
-#pragma unroll
-            for (int a = 0; a < D; ++a) f[off + a] = porig[a];
+            const float4 p4 = io.pos[i];
+            pp[0] = p4.x;
+            pp[1] = p4.y;
+            pp[2] = p4.z;
         }
-    } else {
-        // update MLP forward_update_from_features model.rs:900-940. Each output sum still
-        // starts from its bias and adds hidden units in ascending order; the hidden
-        // layer is consumed as it is produced instead of being stored.
-        constexpr int OM = D + SM;
-        const uint32_t O = D + S, F = P.F, H = P.H;
-        float u[OM];
+        if constexpr (MODE == 0) {
+            // padded layout [si SM][blur SM][grad SM*D][rest], feature-major; rest holds the
+            // density gradient and/or position (runtime count) followed by zeros.
+            const uint32_t T = P.T;
+            float* f = sfeatures + s;
 #pragma unroll
-        for (int o = 0; o < OM; ++o) u[o] = (uint32_t)o < O ? io.b2[o] : 0.0f;
-        for (uint32_t h = 0; h < H; ++h) {
-            const float* wr = io.w1 + (uint64_t)h * F;
-            float sum = io.b1[h];
+            for (int c = 0; c < SM; ++c) f[(uint64_t)c * T] = si[c];
+#pragma unroll
+            for (int c = 0; c < SM; ++c) f[(uint64_t)(SM + c) * T] = blur[c];
+#pragma unroll
+            for (int k = 0; k < SM * D; ++k) f[(uint64_t)(2 * SM + k) * T] = want_sg ? grad[k] : 0.0f;
+            float rest[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) rest[k] = 0.0f;
+            int nr = 0;
+            if (want_dg) {
+#pragma unroll
+                for (int a = 0; a < D; ++a) rest[a] = dg[a];
+                nr = D;
+            }
+            if (P.position_features) {
+#pragma unroll
+                for (int a = 0; a < D; ++a) {
+                    if (nr == D) rest[D + a] = pp[a];
+                    else rest[a] = pp[a];
+                }
+            }
+            constexpr uint32_t base_rest = 2 * SM + SM * D;
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                if (base_rest + r < P.FP) f[(uint64_t)(base_rest + r) * T] = rest[r];
+        } else {
+            const uint32_t S = P.S;
+            float* f = io.features + (uint64_t)i * P.F;
+            uint32_t off = 0;
 #pragma unroll
             for (int c = 0; c < SM; ++c)
-                if ((uint32_t)c < S) sum += wr[c] * si[c];
+                if ((uint32_t)c < S) f[off + c] = si[c];
+            off += S;
 #pragma unroll
             for (int c = 0; c < SM; ++c)
-                if ((uint32_t)c < S) sum += wr[S + c] * blur[c];
-            uint32_t off = 2 * S;
+                if ((uint32_t)c < S) {
+                    f[off + c] = blur[c];
+                    if (io.blurred) io.blurred[(uint64_t)i * S + c] = blur[c];
+                }
+            off += S;
             if (want_sg) {
 #pragma unroll
-                for (int k = 0; k < SM * D; ++k)
-                    if ((uint32_t)k < S * D) sum += wr[off + k] * grad[k];
+                for (int c = 0; c < SM; ++c)
+#pragma unroll
+                    for (int a = 0; a < D; ++a)
+                        if ((uint32_t)c < S) {
+                            f[off + c * D + a] = grad[c * D + a];
+                            if (io.state_gradient) io.state_gradient[((uint64_t)i * S + c) * D + a] = grad[c * D + a];
+                        }
                 off += S * D;
             }
             if (want_dg) {
 #pragma unroll
-                for (int a = 0; a < D; ++a) sum += wr[off + a] * dg[a];
+                for (int a = 0; a < D; ++a) {
+                    f[off + a] = dg[a];
+                    if (io.density_gradient) io.density_gradient[(uint64_t)i * D + a] = dg[a];
+                }
                 off += D;
             }
             if (P.position_features) {
 #pragma unroll
-                for (int a = 0; a < D; ++a) sum += wr[off + a] * porig[a];
+                for (int a = 0; a < D; ++a) f[off + a] = pp[a];
             }
-            const float hv = fmaxf(sum, 0.0f);
-#pragma unroll
-            for (int o = 0; o < OM; ++o)
-                if ((uint32_t)o < O) u[o] += io.w2[(uint64_t)o * H + h] * hv;
         }
-        // forward_from_features_with_eps model.rs:875-895
+    }
+}
+
+// Pads the model weights into the MLP kernel's layout (zeros at padded feature positions and
+// padded outputs): w1p [H][FP], b1 [H], w2t [H][D + SS], b2p [D + SS].
+__global__ __launch_bounds__(256) void k_pad_weights(StepParams P, int D, const float* __restrict__ w1,
+                                                     const float* __restrict__ b1, const float* __restrict__ w2,
+                                                     const float* __restrict__ b2, float* __restrict__ wpad) {
+    const uint32_t S = P.S, SS = P.SS, F = P.F, H = P.H, FP = P.FP;
+    const uint32_t O = D + S, OP = D + SS;
+    const uint64_t n1 = (uint64_t)H * FP, n2 = (uint64_t)H * OP;
+    const uint64_t total = n1 + H + n2 + OP;
+    for (uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; k < total; k += (uint64_t)gridDim.x * blockDim.x) {
+        float v = 0.0f;
+        if (k < n1) {
+            const uint32_t h = (uint32_t)(k / FP), q = (uint32_t)(k - (uint64_t)h * FP);
+            // padded position q -> real feature index
+            int64_t fi = -1;
+            if (q < SS) fi = q < S ? (int64_t)q : -1;
+            else if (q < 2 * SS) fi = q - SS < S ? (int64_t)(S + q - SS) : -1;
+            else if (q < 2 * SS + SS * D) {
+                const uint32_t g = q - 2 * SS;
+                fi = g < S * D ? (int64_t)(2 * S + g) : -1;
+            } else {
+                const uint32_t r = q - (2 * SS + SS * D);
+                fi = 2 * S + S * D + r < F ? (int64_t)(2 * S + S * D + r) : -1;
+            }
+            if (fi >= 0) v = w1[(uint64_t)h * F + fi];
+        } else if (k < n1 + H) {
+            v = b1[k - n1];
+        } else if (k < n1 + H + n2) {
+            const uint64_t t = k - n1 - H;
+            const uint32_t h = (uint32_t)(t / OP), o = (uint32_t)(t - (uint64_t)h * OP);
+            if (o < O) v = w2[(uint64_t)o * H + h];
+        } else {
+            const uint32_t o = (uint32_t)(k - n1 - H - n2);
+            if (o < O) v = b2[o];
+        }
+        wpad[k] = v;
+    }
+}
+
+// Update MLP + motion scaling + 3D gates + masked Euler, one lane per sorted slot.
+// forward_update_from_features model.rs:900-940 (each output sum starts from its bias and adds
+// hidden units in ascending order; hidden unit h is consumed as soon as it is produced),
+// forward_from_features_with_eps model.rs:867-898, gates model.rs:806-837, euler_step step.rs:4-55.
+// Reads the padded feature rows and padded weights, from LDS when they fit (WLDS).
+template <int D, int SM, int FM, bool WLDS>
+__global__ __launch_bounds__(256) void k_mlp_euler(StepParams P, const float* __restrict__ sfeatures,
+                                                   const float* __restrict__ sstate,
+                                                   const uint32_t* __restrict__ perm,
+                                                   const float* __restrict__ wpad, StepIO io) {
+    extern __shared__ float wsm[];
+    constexpr int OM = D + SM;
+    const uint32_t S = P.S, H = P.H, T = P.T;
+    const uint64_t nw = (uint64_t)H * FM + H + (uint64_t)H * OM + OM;
+    const float* W = wpad;
+    if constexpr (WLDS) {
+        const float4* src = reinterpret_cast<const float4*>(wpad);
+        float4* dst = reinterpret_cast<float4*>(wsm);
+        for (uint32_t k = threadIdx.x; k < nw / 4; k += blockDim.x) dst[k] = src[k];
+        for (uint32_t k = (uint32_t)(nw / 4) * 4 + threadIdx.x; k < nw; k += blockDim.x) wsm[k] = wpad[k];
+        __syncthreads();
+        W = wsm;
+    }
+    const float* w1 = W;
+    const float* b1 = w1 + (uint64_t)H * FM;
+    const float* w2t = b1 + H;
+    const float* b2 = w2t + (uint64_t)H * OM;
+    for (uint32_t s = blockIdx.x * blockDim.x + threadIdx.x; s < T; s += gridDim.x * blockDim.x) {
+        const uint32_t b = s / P.N;
+        const uint32_t li = perm[s];
+        const uint32_t i = b * P.N + li;
+        float f[FM];
+#pragma unroll
+        for (int k = 0; k < FM; ++k) f[k] = sfeatures[(uint64_t)k * T + s];
+        float u[OM];
+#pragma unroll
+        for (int o = 0; o < OM; ++o) u[o] = b2[o];
+        for (uint32_t h = 0; h < H; ++h) {
+            const float* wr = w1 + (uint64_t)h * FM;
+            float sum = b1[h];
+#pragma unroll
+            for (int k = 0; k < FM; ++k) sum += wr[k] * f[k];
+            const float hv = fmaxf(sum, 0.0f);
+            const float* wc = w2t + (uint64_t)h * OM;
+#pragma unroll
+            for (int o = 0; o < OM; ++o) u[o] += wc[o] * hv;
+        }
         float norm = 0.0f;
 #pragma unroll
         for (int a = 0; a < D; ++a) norm += u[a] * u[a];
@@ -312,8 +570,22 @@ __global__ __launch_bounds__(256) void k_update(StepParams P, const float4* __re
         float dx[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int a = 0; a < D; ++a) dx[a] = P.alpha * u[a] * P.motion_eps / (1.0f + norm);
+        const float4 pos4 = io.pos[i];
+        const float porig[4] = {pos4.x, pos4.y, pos4.z, pos4.w};
+        float si[SM];
+        {
+            const float4* own = reinterpret_cast<const float4*>(sstate + (uint64_t)s * SM);
+#pragma unroll
+            for (int q = 0; q < SM / 4; ++q) {
+                const float4 v = own[q];
+                si[4 * q] = v.x;
+                si[4 * q + 1] = v.y;
+                si[4 * q + 2] = v.z;
+                si[4 * q + 3] = v.w;
+            }
+        }
         float sg = 1.0f;
-        if (P.gates3d) {  // position-conditioned 3D gates model.rs:806-837, rollout/mod.rs:67-91
+        if (P.gates3d) {
             const float liveness = si[3 < SM ? 3 : 0];
             const float sd = si[7 < SM ? 7 : 0];
             sg = clampf_((4.0f - liveness) * 2.0f, 0.0f, 1.0f);
@@ -327,9 +599,7 @@ __global__ __launch_bounds__(256) void k_update(StepParams P, const float4* __re
 #pragma unroll
             for (int a = 0; a < D; ++a) dx[a] *= mg;
         }
-        const float m = io.mask ? io.mask[i]
-                                : hash_mask(li, b, P.N, P.update_prob, P.step_index, P.base_seed);
-        // euler_step step.rs:31-53
+        const float m = io.mask ? io.mask[i] : hash_mask(li, b, P.N, P.update_prob, P.step_index, P.base_seed);
         float pn[4] = {porig[0], porig[1], porig[2], porig[3]};
         constexpr int MEM = D == 3 ? 4 : 2;
 #pragma unroll
@@ -344,19 +614,27 @@ __global__ __launch_bounds__(256) void k_update(StepParams P, const float4* __re
             }
         }
         io.out_pos[i] = make_float4(pn[0], pn[1], pn[2], pn[3]);
-        float* os = io.out_states + (uint64_t)i * S;
+        float nxt[SM];
 #pragma unroll
         for (int c = 0; c < SM; ++c) {
-            if ((uint32_t)c < S) {
-                float dsc = u[D + c];
-                if (P.gates3d) dsc *= sg;
-                float next = si[c] + P.dt * dsc * m;
-                if (D == 3 && S > 3 && (c == 3 || (S > 8 && c == 8))) next = clampf_(next, -8.0f, 24.0f);
-                os[c] = next;
-            }
+            float dsc = u[D + c];
+            if (P.gates3d) dsc *= sg;
+            float next = si[c] + P.dt * dsc * m;
+            if (D == 3 && S > 3 && (c == 3 || (S > 8 && c == 8))) next = clampf_(next, -8.0f, 24.0f);
+            nxt[c] = next;
+        }
+        float* os = io.out_states + (uint64_t)i * S;
+        if (S == SM) {  // 16-byte aligned rows (checked on the host)
+            float4* o4 = reinterpret_cast<float4*>(os);
+#pragma unroll
+            for (int q = 0; q < SM / 4; ++q)
+                o4[q] = make_float4(nxt[4 * q], nxt[4 * q + 1], nxt[4 * q + 2], nxt[4 * q + 3]);
+        } else {
+#pragma unroll
+            for (int c = 0; c < SM; ++c)
+                if ((uint32_t)c < S) os[c] = nxt[c];
         }
     }
-    NPA_WAVE_LOOP_END
 }
 
 // forward_from_features_with_eps (model.rs:867-940) for explicit feature rows.
@@ -492,49 +770,105 @@ __global__ __launch_bounds__(256) void k_neighbor_lists(StepParams P, const floa
 hipError_t launch_density(const StepParams& p, Workspace& ws, float* density_out, int grid_blocks,
                           hipStream_t stream, Profiler* prof) {
     ProfScope ps(prof, NPA_KERNEL_DENSITY, stream);
+    const int blocks = grid_blocks * 4;  // one wave per block
     if (p.g.dim == 2)
-        hipLaunchKernelGGL(k_density<2>, dim3(grid_blocks), dim3(256), 0, stream, p, ws.srec.as<float4>(),
+        hipLaunchKernelGGL(k_density<2>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
                            ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
-                           ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.svol.as<float>(),
-                           density_out);
+                           ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.svol.as<float>(), density_out);
     else
-        hipLaunchKernelGGL(k_density<3>, dim3(grid_blocks), dim3(256), 0, stream, p, ws.srec.as<float4>(),
+        hipLaunchKernelGGL(k_density<3>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
                            ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
-                           ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.svol.as<float>(),
-                           density_out);
+                           ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.svol.as<float>(), density_out);
     return hipGetLastError();
 }
 
 template <int D, int SM, int MODE>
-static void launch_update_t(const StepParams& p, Workspace& ws, const StepIO& io, int grid_blocks,
-                            hipStream_t stream) {
-    hipLaunchKernelGGL((k_update<D, SM, MODE>), dim3(grid_blocks), dim3(256), 0, stream, p,
-                       ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(),
-                       ws.svol.as<float>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
-                       ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), io);
+static void launch_perceive_t(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
+                              hipStream_t stream) {
+    hipLaunchKernelGGL((k_perceive<D, SM, MODE>), dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
+                       ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.svol.as<float>(),
+                       ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), ws.worklist.as<uint2>(),
+                       ws.wl_count.as<uint32_t>(), ws.features.as<float>(), io);
 }
 
 template <int D, int MODE>
-static void launch_update_d(const StepParams& p, Workspace& ws, const StepIO& io, int grid_blocks,
-                            hipStream_t stream) {
-    if (p.S <= 4) launch_update_t<D, 4, MODE>(p, ws, io, grid_blocks, stream);
-    else if (p.S <= 8) launch_update_t<D, 8, MODE>(p, ws, io, grid_blocks, stream);
-    else if (p.S <= 16) launch_update_t<D, 16, MODE>(p, ws, io, grid_blocks, stream);
-    else if (p.S <= 24) launch_update_t<D, 24, MODE>(p, ws, io, grid_blocks, stream);
-    else launch_update_t<D, 32, MODE>(p, ws, io, grid_blocks, stream);
+static void launch_perceive_d(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
+                              hipStream_t stream) {
+    switch (p.SS) {
+        case 4: launch_perceive_t<D, 4, MODE>(p, ws, io, blocks, stream); break;
+        case 8: launch_perceive_t<D, 8, MODE>(p, ws, io, blocks, stream); break;
+        case 16: launch_perceive_t<D, 16, MODE>(p, ws, io, blocks, stream); break;
+        case 24: launch_perceive_t<D, 24, MODE>(p, ws, io, blocks, stream); break;
+        default: launch_perceive_t<D, 32, MODE>(p, ws, io, blocks, stream); break;
+    }
+}
+
+size_t padded_weight_floats(const StepParams& p) {
+    const uint32_t D = (uint32_t)p.g.dim;
+    return (size_t)p.H * p.FP + p.H + (size_t)p.H * (D + p.SS) + (D + p.SS);
+}
+
+hipError_t launch_pad_weights(const StepParams& p, const float* w1, const float* b1, const float* w2,
+                              const float* b2, float* wpad, hipStream_t stream) {
+    const size_t n = padded_weight_floats(p);
+    const uint32_t blocks = (uint32_t)std::min<size_t>((n + 255) / 256, 1024);
+    hipLaunchKernelGGL(k_pad_weights, dim3(blocks), dim3(256), 0, stream, p, p.g.dim, w1, b1, w2, b2, wpad);
+    return hipGetLastError();
+}
+
+template <int D, int SM, int FM>
+static hipError_t launch_mlp_t(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream) {
+    const size_t wbytes = padded_weight_floats(p) * 4;
+    const uint32_t blocks = std::max<uint32_t>(1, std::min<uint32_t>((p.T + 255) / 256, (uint32_t)device_cu_count() * 8));
+    if (wbytes <= 64 * 1024) {
+        hipLaunchKernelGGL((k_mlp_euler<D, SM, FM, true>), dim3(blocks), dim3(256), wbytes, stream, p,
+                           ws.features.as<float>(), ws.sstate.as<float>(), ws.perm.as<uint32_t>(),
+                           ws.wpad.as<float>(), io);
+    } else {
+        hipLaunchKernelGGL((k_mlp_euler<D, SM, FM, false>), dim3(blocks), dim3(256), 0, stream, p,
+                           ws.features.as<float>(), ws.sstate.as<float>(), ws.perm.as<uint32_t>(),
+                           ws.wpad.as<float>(), io);
+    }
+    return hipGetLastError();
+}
+
+template <int D, int SM>
+static hipError_t launch_mlp_sm(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream) {
+    constexpr int base = 2 * SM + SM * D;
+    if (p.FP == (uint32_t)base) return launch_mlp_t<D, SM, base>(p, ws, io, stream);
+    if (p.FP == (uint32_t)base + 4) return launch_mlp_t<D, SM, base + 4>(p, ws, io, stream);
+    return launch_mlp_t<D, SM, base + 8>(p, ws, io, stream);
+}
+
+template <int D>
+static hipError_t launch_mlp_d(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream) {
+    switch (p.SS) {
+        case 4: return launch_mlp_sm<D, 4>(p, ws, io, stream);
+        case 8: return launch_mlp_sm<D, 8>(p, ws, io, stream);
+        case 16: return launch_mlp_sm<D, 16>(p, ws, io, stream);
+        case 24: return launch_mlp_sm<D, 24>(p, ws, io, stream);
+        default: return launch_mlp_sm<D, 32>(p, ws, io, stream);
+    }
 }
 
 hipError_t launch_update(const StepParams& p, Workspace& ws, const StepIO& io, int mode, int grid_blocks,
                          hipStream_t stream, Profiler* prof) {
-    ProfScope ps(prof, NPA_KERNEL_UPDATE, stream);
-    if (p.g.dim == 2) {
-        if (mode == 0) launch_update_d<2, 0>(p, ws, io, grid_blocks, stream);
-        else launch_update_d<2, 1>(p, ws, io, grid_blocks, stream);
-    } else {
-        if (mode == 0) launch_update_d<3, 0>(p, ws, io, grid_blocks, stream);
-        else launch_update_d<3, 1>(p, ws, io, grid_blocks, stream);
+    const int blocks = grid_blocks * 4;  // one wave per block
+    {
+        ProfScope ps(prof, NPA_KERNEL_PERCEIVE, stream);
+        if (p.g.dim == 2) {
+            if (mode == 0) launch_perceive_d<2, 0>(p, ws, io, blocks, stream);
+            else launch_perceive_d<2, 1>(p, ws, io, blocks, stream);
+        } else {
+            if (mode == 0) launch_perceive_d<3, 0>(p, ws, io, blocks, stream);
+            else launch_perceive_d<3, 1>(p, ws, io, blocks, stream);
+        }
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess || mode != 0) return e;
     }
-    return hipGetLastError();
+    ProfScope ps(prof, NPA_KERNEL_MLP, stream);
+    if (p.g.dim == 2) return launch_mlp_d<2>(p, ws, io, stream);
+    return launch_mlp_d<3>(p, ws, io, stream);
 }
 
 hipError_t launch_mlp_forward(const StepParams& p, const float* features, uint32_t rows, const StepIO& io,

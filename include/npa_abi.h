@@ -267,9 +267,10 @@ enum {
     NPA_KERNEL_OFFSETS_SCAN = 2,
     NPA_KERNEL_SCATTER = 3,
     NPA_KERNEL_DENSITY = 4,
-    NPA_KERNEL_UPDATE = 5,
-    NPA_KERNEL_SPLAT = 6,
-    NPA_KERNEL_COUNT = 7
+    NPA_KERNEL_PERCEIVE = 5,   /* second neighbour pass + normalisation + feature rows */
+    NPA_KERNEL_SPLAT = 6,      /* the whole 2D splat pipeline */
+    NPA_KERNEL_MLP = 7,        /* update MLP + masked Euler */
+    NPA_KERNEL_COUNT = 8
 };
 /* kernel_mask selects kernels by bit (1 << NPA_KERNEL_*; 0 = off, -1 = all). The
  * library then brackets each launch of a selected kernel with HIP events on the
