@@ -440,7 +440,8 @@ npa_status npa_perceive(npa_context* ctx, const float* positions, const float* s
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null array");
     npa::HashgridPlan plan;
     std::string err;
-    if (!npa::make_plan(*cfg, B, N, &plan, &err)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
+    if (!npa::make_plan(*cfg, B, N, &plan, &err, npa::targets_per_item(npa::state_stride_for(S))))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
     HostIO io(ctx);
     const float4* pos = (const float4*)io.in(positions, total * 16);
     const float* st_in = io.in(states, total * S * 4);
@@ -540,7 +541,8 @@ npa_status npa_step(npa_context* ctx, const float* positions, const float* state
     const uint32_t O = model->spatial_dims + S;
     npa::HashgridPlan plan;
     std::string err;
-    if (!npa::make_plan(*grid, B, N, &plan, &err)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
+    if (!npa::make_plan(*grid, B, N, &plan, &err, npa::targets_per_item(npa::state_stride_for(model->state_dims))))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
     HostIO io(ctx);
     npa::StepIO sio;
     sio.pos = (const float4*)io.in(positions, total * 16);
@@ -684,7 +686,8 @@ npa_status npa_state_create(npa_context* ctx, const npa_model_cfg* model, const 
     if (total == 0) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: empty particle system");
     npa::HashgridPlan plan;
     std::string err;
-    if (!npa::make_plan(*grid, B, N, &plan, &err)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
+    if (!npa::make_plan(*grid, B, N, &plan, &err, npa::targets_per_item(npa::state_stride_for(model->state_dims))))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
     npa_state* s = new npa_state();
     s->ctx = ctx;
     s->model = *model;

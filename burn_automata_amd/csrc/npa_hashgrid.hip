@@ -127,7 +127,7 @@ GridParams make_grid_params(const npa_grid_cfg& cfg) {
 }
 
 bool make_plan(const npa_grid_cfg& cfg, uint32_t batch, uint32_t n, HashgridPlan* plan,
-               std::string* err) {
+               std::string* err, uint32_t tpi) {
     uint64_t cells = 1;
     for (uint32_t a = 0; a < cfg.dim; ++a) cells *= cfg.grid_size[a];
     if (cells > 65536) {
@@ -160,7 +160,8 @@ bool make_plan(const npa_grid_cfg& cfg, uint32_t batch, uint32_t n, HashgridPlan
         *err = "hashgrid tile table exceeds 2^32 entries";
         return false;
     }
-    p.worklist_cap = (total + 63) / 64 + std::min<uint64_t>(total, (uint64_t)batch * cells) + 1;
+    p.tpi = tpi;
+    p.worklist_cap = (total + tpi - 1) / tpi + std::min<uint64_t>(total, (uint64_t)batch * cells) + 1;
     *plan = p;
     return true;
 }
@@ -315,7 +316,7 @@ __global__ __launch_bounds__(1024) void k_offsets_scan(const uint32_t* __restric
                                                        uint32_t C, uint32_t n, uint32_t batch,
                                                        uint2* __restrict__ worklist,
                                                        uint32_t* __restrict__ wl_count,
-                                                       int emit_work) {
+                                                       int emit_work, uint32_t tpi) {
     __shared__ uint32_t lds[32];
     __shared__ uint32_t wl_base;
     const uint32_t b = blockIdx.x;
@@ -326,7 +327,7 @@ __global__ __launch_bounds__(1024) void k_offsets_scan(const uint32_t* __restric
     for (uint32_t k = k0; k < k0 + per && k < C; ++k) {
         uint32_t c = tot[k];
         sum_c += c;
-        sum_i += (c + 63) / 64;
+        sum_i += (c + tpi - 1) / tpi;
     }
     uint32_t all_c, all_i;
     uint32_t pre_c = block_scan_1024(sum_c, lds, &all_c);
@@ -339,9 +340,9 @@ __global__ __launch_bounds__(1024) void k_offsets_scan(const uint32_t* __restric
         uint32_t c = tot[k];
         bin_offsets[(uint64_t)b * C + k] = sys_base + run_c;
         if (emit_work) {
-            for (uint32_t m = 0; m * 64 < c; ++m) {
-                uint32_t cnt = c - m * 64;
-                worklist[run_i++] = make_uint2(sys_base + run_c + m * 64, cnt < 64 ? cnt : 64);
+            for (uint32_t m = 0; m * tpi < c; ++m) {
+                uint32_t cnt = c - m * tpi;
+                worklist[run_i++] = make_uint2(sys_base + run_c + m * tpi, cnt < tpi ? cnt : tpi);
             }
         }
         run_c += c;
@@ -462,7 +463,7 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
         hipLaunchKernelGGL(k_offsets_scan, dim3(batch), dim3(1024), 0, stream,
                            ws.totals.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), plan.cells, n,
                            batch, ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(),
-                           payload ? 1 : 0);
+                           payload ? 1 : 0, plan.tpi);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     {
@@ -539,7 +540,7 @@ hipError_t launch_key_sort(const HashgridPlan& p, const uint32_t* keys, const ui
                        p.cells, p.tiles_per_sys);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_offsets_scan, dim3(1), dim3(1024), 0, stream, totals, offsets, p.cells, cap, 1u,
-                       (uint2*)nullptr, (uint32_t*)nullptr, 0);
+                       (uint2*)nullptr, (uint32_t*)nullptr, 0, 64u);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (cap == 0) return hipSuccess;
     hipLaunchKernelGGL(k_scatter_vals, dim3((cap + 255) / 256), dim3(256), 0, stream, keys, vals, d_count,

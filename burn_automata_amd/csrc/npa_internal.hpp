@@ -63,6 +63,7 @@ struct HashgridPlan {
     uint32_t lds_bytes = 0;      // waves * C * 2
     uint64_t table_entries = 0;  // B * tiles_per_sys * C
     uint64_t worklist_cap = 0;   // upper bound of wave work items
+    uint32_t tpi = 64;           // targets (slots) per work item
 };
 
 // Device workspace of one hashgrid + perception pass.
@@ -74,8 +75,9 @@ struct Workspace {
     void release();
 };
 
+// tpi: targets per wave work item emitted for the neighbour passes (64 / lanes per target).
 bool make_plan(const npa_grid_cfg& cfg, uint32_t batch, uint32_t particle_count, HashgridPlan* plan,
-               std::string* err);
+               std::string* err, uint32_t tpi = 64);
 GridParams make_grid_params(const npa_grid_cfg& cfg);
 float host_powi(float x, int n);
 
@@ -100,6 +102,10 @@ hipError_t launch_key_sort(const HashgridPlan& plan, const uint32_t* keys, const
 __host__ __device__ inline uint32_t state_stride_for(uint32_t S) {
     return S <= 4 ? 4 : S <= 8 ? 8 : S <= 16 ? 16 : S <= 24 ? 24 : 32;
 }
+// Lanes per target in the neighbour passes (each lane owns SS / L state channels) and the
+// targets per wave work item, 64 / L.
+__host__ __device__ inline uint32_t lanes_per_target(uint32_t SS) { return SS >= 16 ? 4u : SS / 4; }
+__host__ __device__ inline uint32_t targets_per_item(uint32_t SS) { return 64u / lanes_per_target(SS); }
 // Padded feature row used between the perception and MLP kernels:
 // [state SS][blur SS][grad SS*d][density-grad d?, position d?, zero padded to a multiple of 4].
 __host__ __device__ inline uint32_t padded_features(uint32_t SS, uint32_t d, uint32_t rest) {

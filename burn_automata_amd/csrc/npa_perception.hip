@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "npa_internal.hpp"
 
@@ -170,8 +171,61 @@ __device__ __forceinline__ void for_each_group_chunk(const GridParams& g, uint32
     }
 }
 
-// density  forward.rs:145-160: rho_i = sum_j W_poly6(r_ij^2)
-template <int D>
+// Lanes per target for a sorted-state row width SM (each lane owns SM / L state channels).
+template <int SM>
+struct LanesPerTarget {
+    static constexpr int L = SM >= 16 ? 4 : SM / 4;
+    static constexpr int CPL = SM / L;
+};
+
+// Value of lane (group base + j) for groups of L consecutive lanes (L = 1, 2 or 4), via DPP.
+template <int L, int J>
+__device__ __forceinline__ float group_bcast(float v) {
+    if constexpr (L == 1) {
+        return v;
+    } else if constexpr (L == 2) {
+        constexpr int c = J == 0 ? (0 | (0 << 2) | (2 << 4) | (2 << 6)) : (1 | (1 << 2) | (3 << 4) | (3 << 6));
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), c, 0xf, 0xf, false));
+    } else {
+        constexpr int c = J | (J << 2) | (J << 4) | (J << 6);
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), c, 0xf, 0xf, false));
+    }
+}
+
+// OR of a 64-bit value over each group of L consecutive lanes (L = 1, 2 or 4), via DPP.
+template <int L>
+__device__ __forceinline__ uint64_t group_or(uint64_t m) {
+    if constexpr (L == 1) return m;
+    uint32_t lo = (uint32_t)m, hi = (uint32_t)(m >> 32);
+    constexpr int swap1 = 1 | (0 << 2) | (3 << 4) | (2 << 6);  // quad_perm [1,0,3,2]
+    lo |= (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, swap1, 0xf, 0xf, false);
+    hi |= (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, swap1, 0xf, 0xf, false);
+    if constexpr (L == 4) {
+        constexpr int swap2 = 2 | (3 << 2) | (0 << 4) | (1 << 6);  // quad_perm [2,3,0,1]
+        lo |= (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, swap2, 0xf, 0xf, false);
+        hi |= (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, swap2, 0xf, 0xf, false);
+    }
+    return ((uint64_t)hi << 32) | lo;
+}
+
+template <int L>
+__device__ __forceinline__ float ordered_group_sum(float acc, float v) {
+    // acc + v(lane 0) + v(lane 1) + ... in lane order: candidate order within the round
+    acc += group_bcast<L, 0>(v);
+    if constexpr (L >= 2) acc += group_bcast<L, 1>(v);
+    if constexpr (L >= 4) {
+        acc += group_bcast<L, 2>(v);
+        acc += group_bcast<L, 3>(v);
+    }
+    return acc;
+}
+
+// density  forward.rs:145-160: rho_i = sum_j W_poly6(r_ij^2).
+// L lanes per target split each staged chunk round-robin; every lane rebuilds the target's
+// running sum in candidate order from the L per-lane terms of each round. A rejected candidate
+// contributes +0.0, which leaves the sum unchanged (it starts at +0.0, adds only non-negative
+// terms and therefore never holds -0.0).
+template <int D, int L>
 __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __restrict__ srec,
                                                 const int4* __restrict__ scoord,
                                                 const uint32_t* __restrict__ bo,
@@ -181,11 +235,12 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
                                                 float* __restrict__ svol, float* __restrict__ density_out) {
     __shared__ NbrStage<D> st;
     const uint32_t lane = threadIdx.x;
+    const uint32_t t = lane / L, q = lane % L;
     const uint32_t items = *wl_count;
     for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
         const uint2 item = wl[it];
-        const bool active = lane < item.y;
-        const uint32_t s = item.x + (active ? lane : 0u);
+        const bool active = t < item.y;
+        const uint32_t s = item.x + (active ? t : 0u);
         const uint32_t b = item.x / P.N;
         float pi[3];
         int ci[3];
@@ -195,21 +250,27 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
             P.g, b, active, ci, bo, lane,
             [&](uint32_t base, uint32_t m) { stage_records<D>(st, srec, scoord, base, m, lane); },
             [&](uint32_t, uint32_t m, int64_t n0, int64_t n1, int64_t n2, bool in_group) {
-                for (uint32_t k = 0; k < m; ++k) {
-                    const float4 r = st.rec[k];
-                    if (P.g.mode == 1 && !staged_coords_match<D>(st, k, r, n0, n1, n2)) continue;
-                    const float d0 = delta_axis(pi[0], r.x, 0, P.g);
-                    const float d1 = delta_axis(pi[1], r.y, 1, P.g);
-                    float r2 = d0 * d0;
-                    r2 += d1 * d1;
-                    if constexpr (D == 3) {
-                        const float d2 = delta_axis(pi[2], r.z, 2, P.g);
-                        r2 += d2 * d2;
+                for (uint32_t k0 = 0; k0 < m; k0 += L) {
+                    const uint32_t k = k0 + q;
+                    float v = 0.0f;
+                    if (k < m) {
+                        const float4 r = st.rec[k];
+                        bool ok = in_group;
+                        if (P.g.mode == 1) ok = ok && staged_coords_match<D>(st, k, r, n0, n1, n2);
+                        const float d0 = delta_axis(pi[0], r.x, 0, P.g);
+                        const float d1 = delta_axis(pi[1], r.y, 1, P.g);
+                        float r2 = d0 * d0;
+                        r2 += d1 * d1;
+                        if constexpr (D == 3) {
+                            const float d2 = delta_axis(pi[2], r.z, 2, P.g);
+                            r2 += d2 * d2;
+                        }
+                        if (ok && r2 < P.g.eps2) v = poly6(r2, P.g);
                     }
-                    if (in_group && r2 < P.g.eps2) rho += poly6(r2, P.g);
+                    rho = ordered_group_sum<L>(rho, v);
                 }
             });
-        if (active) {
+        if (active && q == 0) {
             svol[s] = recip_finite(rho);
             if (density_out) density_out[b * P.N + perm[s]] = rho;
         }
@@ -220,11 +281,13 @@ template <int D, int SM>
 struct PerceiveStage {
     NbrStage<D> nb;
     float vol[kChunk];
-    float st[kChunk * (SM + 1)];  // odd row stride keeps per-lane row gathers on distinct banks
+    float st[kChunk * (SM + 4)];  // 16-byte aligned rows
 };
 
-// Second neighbour pass + normalisation + feature row. SM is the sorted-state row width
-// (state channels zero padded to SM), so every channel loop is a compile-time loop.
+// Second neighbour pass + normalisation + feature row, L lanes per target, each lane owning
+// CPL = SM / L state channels. The L lanes test a chunk's candidates round-robin and OR their
+// accept masks; then every lane walks the target's accepted candidates in ascending order
+// (the reference's order), recomputing the pair scalars and updating its own channels' sums.
 // MODE 0: padded feature rows, feature-major (features[k * T + s]) for the MLP kernel.
 // MODE 1: the perceive_with_options outputs in original particle order.
 template <int D, int SM, int MODE>
@@ -237,36 +300,33 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                                                  const uint2* __restrict__ wl,
                                                  const uint32_t* __restrict__ wl_count,
                                                  float* __restrict__ sfeatures, StepIO io) {
+    constexpr int L = LanesPerTarget<SM>::L;
+    constexpr int CPL = LanesPerTarget<SM>::CPL;
+    constexpr int RS = SM + 4;
     __shared__ PerceiveStage<D, SM> st;
     const uint32_t lane = threadIdx.x;
+    const uint32_t t = lane / L, q = lane % L;
+    const uint32_t c0 = q * CPL;  // first channel of this lane
     const uint32_t items = *wl_count;
     const bool branch_a = P.state_grad && P.density_grad;
     const bool want_sg = P.state_grad != 0, want_dg = P.density_grad != 0;
     const bool want_m = want_sg && P.hybrid;
     for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
         const uint2 item = wl[it];
-        const bool active = lane < item.y;
-        const uint32_t s = item.x + (active ? lane : 0u);
+        const bool active = t < item.y;
+        const uint32_t s = item.x + (active ? t : 0u);
         const uint32_t b = item.x / P.N;
         float pi[3];
         int ci[3];
         load_rec<D>(srec, scoord, s, pi, ci);
-        float si[SM], blur[SM], grad[SM * D], dg[D], mom[D * D];
-        {
-            const float4* own = reinterpret_cast<const float4*>(sstate + (uint64_t)s * SM);
+        float si[CPL], blur[CPL], grad[CPL * D], dg[D], mom[D * D];
 #pragma unroll
-            for (int q = 0; q < SM / 4; ++q) {
-                const float4 v = own[q];
-                si[4 * q] = v.x;
-                si[4 * q + 1] = v.y;
-                si[4 * q + 2] = v.z;
-                si[4 * q + 3] = v.w;
-            }
+        for (int c = 0; c < CPL; ++c) {
+            si[c] = sstate[(uint64_t)s * SM + c0 + c];
+            blur[c] = 0.0f;
         }
 #pragma unroll
-        for (int c = 0; c < SM; ++c) blur[c] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < SM * D; ++k) grad[k] = 0.0f;
+        for (int k = 0; k < CPL * D; ++k) grad[k] = 0.0f;
 #pragma unroll
         for (int k = 0; k < D; ++k) dg[k] = 0.0f;
 #pragma unroll
@@ -279,21 +339,16 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                 if (lane < m) {
                     st.vol[lane] = svol[base + lane];
                     const float4* src = reinterpret_cast<const float4*>(sstate + (uint64_t)(base + lane) * SM);
-                    float* dst = st.st + lane * (SM + 1);
+                    float4* dst = reinterpret_cast<float4*>(st.st + lane * RS);
 #pragma unroll
-                    for (int q = 0; q < SM / 4; ++q) {
-                        const float4 v = src[q];
-                        dst[4 * q] = v.x;
-                        dst[4 * q + 1] = v.y;
-                        dst[4 * q + 2] = v.z;
-                        dst[4 * q + 3] = v.w;
-                    }
+                    for (int k = 0; k < SM / 4; ++k) dst[k] = src[k];
                 }
             },
             [&](uint32_t base, uint32_t m, int64_t n0, int64_t n1, int64_t n2, bool in_group) {
-                // accepted candidates of this lane, as a bit mask over the chunk
                 uint64_t acc = 0;
-                for (uint32_t k = 0; k < m; ++k) {
+                for (uint32_t k0 = 0; k0 < m; k0 += L) {
+                    const uint32_t k = k0 + q;
+                    if (k >= m) continue;
                     const float4 r = st.nb.rec[k];
                     if (P.g.mode == 1 && !staged_coords_match<D>(st.nb, k, r, n0, n1, n2)) continue;
                     const float d0 = delta_axis(pi[0], r.x, 0, P.g);
@@ -306,61 +361,111 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                     }
                     if (in_group && r2 < P.g.eps2) acc |= 1ull << k;
                 }
+                acc = group_or<L>(acc);
+                // Rounds of L accepted candidates: lane q computes the pair scalars of the
+                // round's q-th candidate, then every lane applies the round's candidates in
+                // ascending order to its own channels (scalars broadcast within the lane group).
+                // A missing candidate (short last round), the self pair and coincident
+                // particles contribute zeros, which leave every sum unchanged: each sum starts
+                // at +0.0 and so never holds -0.0.
                 while (acc) {
-                    const uint32_t k = (uint32_t)__builtin_ctzll(acc);
-                    acc &= acc - 1;
-                    const float4 r = st.nb.rec[k];
-                    float d[3];
-                    d[0] = delta_axis(pi[0], r.x, 0, P.g);
-                    d[1] = delta_axis(pi[1], r.y, 1, P.g);
-                    float r2 = d[0] * d[0];
-                    r2 += d[1] * d[1];
-                    if constexpr (D == 3) {
-                        d[2] = delta_axis(pi[2], r.z, 2, P.g);
-                        r2 += d[2] * d[2];
-                    } else {
-                        d[2] = 0.0f;
+                    const uint64_t round0 = acc;
+                    uint64_t mine = acc;
+#pragma unroll
+                    for (int j = 0; j < L - 1; ++j)
+                        if (j < (int)q) mine &= mine - 1;
+#pragma unroll
+                    for (int j = 0; j < L; ++j) acc &= acc - 1;
+                    const bool has = mine != 0;
+                    // a lane without a candidate points at the round's first (accepted) one, so
+                    // its zero-weight terms read a neighbour's row, never an unrelated one
+                    const uint32_t k = (uint32_t)__builtin_ctzll(has ? mine : round0);
+                    float smooth = 0.0f, vol = 0.0f, d[3] = {0.0f, 0.0f, 0.0f};
+                    float vg[D], dgv[D];
+#pragma unroll
+                    for (int a = 0; a < D; ++a) {
+                        vg[a] = 0.0f;
+                        dgv[a] = 0.0f;
                     }
-                    const float vol = st.vol[k];
-                    const float smooth = poly6(r2, P.g);
-                    const float* sj = st.st + k * (SM + 1);
-                    float sv[SM];
-#pragma unroll
-                    for (int c = 0; c < SM; ++c) sv[c] = sj[c];
-                    if (branch_a) {  // second_pass_particle forward.rs:263-270
-#pragma unroll
-                        for (int c = 0; c < SM; ++c) blur[c] += sv[c] * smooth * vol;
-                    } else {  // blur_state forward.rs:174-180
-                        const float w = smooth * vol;
-#pragma unroll
-                        for (int c = 0; c < SM; ++c) blur[c] += sv[c] * w;
-                    }
-                    if (base + k == s) continue;
-                    if (r2 <= 0.0f) continue;  // spiky_gradient_kernel returns zeros (kernels.rs:87-89)
-                    const float rr = sqrtf(r2);
-                    const float t = P.g.eps - rr;
-                    if (want_dg) {  // spiky_gradient_kernel(coeff = 1)
-                        const float mag = 1.0f * P.g.k5 * 3.0f * (t * t) / rr;
-#pragma unroll
-                        for (int a = 0; a < D; ++a) dg[a] += mag * d[a];
-                    }
-                    if (want_sg) {  // spiky_gradient_kernel(coeff = volume_j)
-                        const float mag = vol * P.g.k5 * 3.0f * (t * t) / rr;
-                        float vg[D];
-#pragma unroll
-                        for (int a = 0; a < D; ++a) vg[a] = mag * d[a];
-#pragma unroll
-                        for (int c = 0; c < SM; ++c) {
-                            const float diff = sv[c] - si[c];
-#pragma unroll
-                            for (int a = 0; a < D; ++a) grad[c * D + a] += diff * vg[a];
+                    if (has) {
+                        const float4 r = st.nb.rec[k];
+                        d[0] = delta_axis(pi[0], r.x, 0, P.g);
+                        d[1] = delta_axis(pi[1], r.y, 1, P.g);
+                        float r2 = d[0] * d[0];
+                        r2 += d[1] * d[1];
+                        if constexpr (D == 3) {
+                            d[2] = delta_axis(pi[2], r.z, 2, P.g);
+                            r2 += d[2] * d[2];
                         }
-                        if (want_m) {
+                        vol = st.vol[k];
+                        smooth = poly6(r2, P.g);
+                        if (base + k != s && r2 > 0.0f) {  // spiky_gradient_kernel kernels.rs:79-96
+                            const float rr = sqrtf(r2);
+                            const float tt = P.g.eps - rr;
+                            if (want_dg) {
+                                const float mag = 1.0f * P.g.k5 * 3.0f * (tt * tt) / rr;
 #pragma unroll
-                            for (int ra = 0; ra < D; ++ra)
+                                for (int a = 0; a < D; ++a) dgv[a] = mag * d[a];
+                            }
+                            if (want_sg) {
+                                const float mag = vol * P.g.k5 * 3.0f * (tt * tt) / rr;
 #pragma unroll
-                                for (int ca = 0; ca < D; ++ca) mom[ra * D + ca] += d[ra] * vg[ca];
+                                for (int a = 0; a < D; ++a) vg[a] = mag * d[a];
+                            }
                         }
+                    }
+                    const float w = smooth * vol;  // blur_state weight (density-grad-off branch)
+                    // the round's candidates in ascending order
+                    auto apply = [&](float c_smooth, float c_vol, float c_w, const float* c_d, const float* c_vg,
+                                     const float* c_dg, uint32_t c_k) {
+                        const float* sj = st.st + c_k * RS + c0;
+                        float sv[CPL];
+#pragma unroll
+                        for (int c = 0; c < CPL; ++c) sv[c] = sj[c];
+                        if (branch_a) {  // second_pass_particle forward.rs:263-270
+#pragma unroll
+                            for (int c = 0; c < CPL; ++c) blur[c] += sv[c] * c_smooth * c_vol;
+                        } else {  // blur_state forward.rs:174-180
+#pragma unroll
+                            for (int c = 0; c < CPL; ++c) blur[c] += sv[c] * c_w;
+                        }
+                        if (want_dg) {
+#pragma unroll
+                            for (int a = 0; a < D; ++a) dg[a] += c_dg[a];
+                        }
+                        if (want_sg) {
+#pragma unroll
+                            for (int c = 0; c < CPL; ++c) {
+                                const float diff = sv[c] - si[c];
+#pragma unroll
+                                for (int a = 0; a < D; ++a) grad[c * D + a] += diff * c_vg[a];
+                            }
+                            if (want_m) {
+#pragma unroll
+                                for (int ra = 0; ra < D; ++ra)
+#pragma unroll
+                                    for (int ca = 0; ca < D; ++ca) mom[ra * D + ca] += c_d[ra] * c_vg[ca];
+                            }
+                        }
+                    };
+                    auto round_step = [&](auto J) {
+                        constexpr int j = decltype(J)::value;
+                        float b_d[D], b_vg[D], b_dg[D];
+#pragma unroll
+                        for (int a = 0; a < D; ++a) {
+                            b_d[a] = group_bcast<L, j>(d[a]);
+                            b_vg[a] = group_bcast<L, j>(vg[a]);
+                            b_dg[a] = group_bcast<L, j>(dgv[a]);
+                        }
+                        const uint32_t b_k = (uint32_t)__float_as_int(group_bcast<L, j>(__int_as_float((int)k)));
+                        apply(group_bcast<L, j>(smooth), group_bcast<L, j>(vol), group_bcast<L, j>(w), b_d, b_vg,
+                              b_dg, b_k);
+                    };
+                    round_step(std::integral_constant<int, 0>{});
+                    if constexpr (L >= 2) round_step(std::integral_constant<int, 1>{});
+                    if constexpr (L >= 4) {
+                        round_step(std::integral_constant<int, 2>{});
+                        round_step(std::integral_constant<int, 3>{});
                     }
                 }
             });
@@ -371,7 +476,7 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                 float inv[D * D];
                 safe_inverse<D>(mom, inv);
 #pragma unroll
-                for (int c = 0; c < SM; ++c) {
+                for (int c = 0; c < CPL; ++c) {
                     float corrected[D];
 #pragma unroll
                     for (int o = 0; o < D; ++o) corrected[o] = 0.0f;
@@ -384,7 +489,7 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                 }
             }
 #pragma unroll
-            for (int c = 0; c < SM; ++c) {  // normalize_state_gradient normalize.rs:5-30
+            for (int c = 0; c < CPL; ++c) {  // normalize_state_gradient normalize.rs:5-30
 #pragma unroll
                 for (int a = 0; a < D; ++a) grad[c * D + a] *= P.state_scale;
                 if (P.log_norm_grad) log_normalize<D>(&grad[c * D]);
@@ -410,87 +515,88 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
             const uint32_t T = P.T;
             float* f = sfeatures + s;
 #pragma unroll
-            for (int c = 0; c < SM; ++c) f[(uint64_t)c * T] = si[c];
+            for (int c = 0; c < CPL; ++c) f[(uint64_t)(c0 + c) * T] = si[c];
 #pragma unroll
-            for (int c = 0; c < SM; ++c) f[(uint64_t)(SM + c) * T] = blur[c];
+            for (int c = 0; c < CPL; ++c) f[(uint64_t)(SM + c0 + c) * T] = blur[c];
 #pragma unroll
-            for (int k = 0; k < SM * D; ++k) f[(uint64_t)(2 * SM + k) * T] = want_sg ? grad[k] : 0.0f;
-            float rest[8];
+            for (int k = 0; k < CPL * D; ++k) f[(uint64_t)(2 * SM + c0 * D + k) * T] = want_sg ? grad[k] : 0.0f;
+            if (q == 0) {
+                float rest[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) rest[k] = 0.0f;
-            int nr = 0;
-            if (want_dg) {
+                for (int k = 0; k < 8; ++k) rest[k] = 0.0f;
+                int nr = 0;
+                if (want_dg) {
 #pragma unroll
-                for (int a = 0; a < D; ++a) rest[a] = dg[a];
-                nr = D;
-            }
-            if (P.position_features) {
-#pragma unroll
-                for (int a = 0; a < D; ++a) {
-                    if (nr == D) rest[D + a] = pp[a];
-                    else rest[a] = pp[a];
+                    for (int a = 0; a < D; ++a) rest[a] = dg[a];
+                    nr = D;
                 }
-            }
-            constexpr uint32_t base_rest = 2 * SM + SM * D;
+                if (P.position_features) {
 #pragma unroll
-            for (int r = 0; r < 8; ++r)
-                if (base_rest + r < P.FP) f[(uint64_t)(base_rest + r) * T] = rest[r];
+                    for (int a = 0; a < D; ++a) {
+                        if (nr == D) rest[D + a] = pp[a];
+                        else rest[a] = pp[a];
+                    }
+                }
+                constexpr uint32_t base_rest = 2 * SM + SM * D;
+#pragma unroll
+                for (int r = 0; r < 8; ++r)
+                    if (base_rest + r < P.FP) f[(uint64_t)(base_rest + r) * T] = rest[r];
+            }
         } else {
             const uint32_t S = P.S;
             float* f = io.features + (uint64_t)i * P.F;
-            uint32_t off = 0;
 #pragma unroll
-            for (int c = 0; c < SM; ++c)
-                if ((uint32_t)c < S) f[off + c] = si[c];
-            off += S;
+            for (int c = 0; c < CPL; ++c)
+                if (c0 + c < S) {
+                    f[c0 + c] = si[c];
+                    f[S + c0 + c] = blur[c];
+                    if (io.blurred) io.blurred[(uint64_t)i * S + c0 + c] = blur[c];
+                    if (want_sg) {
 #pragma unroll
-            for (int c = 0; c < SM; ++c)
-                if ((uint32_t)c < S) {
-                    f[off + c] = blur[c];
-                    if (io.blurred) io.blurred[(uint64_t)i * S + c] = blur[c];
-                }
-            off += S;
-            if (want_sg) {
-#pragma unroll
-                for (int c = 0; c < SM; ++c)
-#pragma unroll
-                    for (int a = 0; a < D; ++a)
-                        if ((uint32_t)c < S) {
-                            f[off + c * D + a] = grad[c * D + a];
-                            if (io.state_gradient) io.state_gradient[((uint64_t)i * S + c) * D + a] = grad[c * D + a];
+                        for (int a = 0; a < D; ++a) {
+                            f[2 * S + (c0 + c) * D + a] = grad[c * D + a];
+                            if (io.state_gradient)
+                                io.state_gradient[((uint64_t)i * S + c0 + c) * D + a] = grad[c * D + a];
                         }
-                off += S * D;
-            }
-            if (want_dg) {
-#pragma unroll
-                for (int a = 0; a < D; ++a) {
-                    f[off + a] = dg[a];
-                    if (io.density_gradient) io.density_gradient[(uint64_t)i * D + a] = dg[a];
+                    }
                 }
-                off += D;
-            }
-            if (P.position_features) {
+            if (q == 0) {
+                uint32_t off = 2 * S + (want_sg ? S * D : 0);
+                if (want_dg) {
 #pragma unroll
-                for (int a = 0; a < D; ++a) f[off + a] = pp[a];
+                    for (int a = 0; a < D; ++a) {
+                        f[off + a] = dg[a];
+                        if (io.density_gradient) io.density_gradient[(uint64_t)i * D + a] = dg[a];
+                    }
+                    off += D;
+                }
+                if (P.position_features) {
+#pragma unroll
+                    for (int a = 0; a < D; ++a) f[off + a] = pp[a];
+                }
             }
         }
     }
 }
 
-// Pads the model weights into the MLP kernel's layout (zeros at padded feature positions and
-// padded outputs): w1p [H][FP], b1 [H], w2t [H][D + SS], b2p [D + SS].
+// Pads the model weights into the MLP kernel's layout, zeros everywhere else:
+//   w1t [FP][HP]  w1 transposed, features at their padded positions, HP = H rounded up to 128
+//   b1p [HP]
+//   w2t [H][OP]   w2 transposed, OP = D + SS rounded up to a multiple of 4
+//   b2p [OP]
 __global__ __launch_bounds__(256) void k_pad_weights(StepParams P, int D, const float* __restrict__ w1,
                                                      const float* __restrict__ b1, const float* __restrict__ w2,
                                                      const float* __restrict__ b2, float* __restrict__ wpad) {
     const uint32_t S = P.S, SS = P.SS, F = P.F, H = P.H, FP = P.FP;
-    const uint32_t O = D + S, OP = D + SS;
-    const uint64_t n1 = (uint64_t)H * FP, n2 = (uint64_t)H * OP;
-    const uint64_t total = n1 + H + n2 + OP;
+    const uint32_t HP = (H + 127) / 128 * 128;
+    const uint32_t O = D + S, OP = (D + SS + 3) / 4 * 4;
+    const uint64_t n1 = (uint64_t)FP * HP, n2 = (uint64_t)H * OP;
+    const uint64_t total = n1 + HP + n2 + OP;
     for (uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; k < total; k += (uint64_t)gridDim.x * blockDim.x) {
         float v = 0.0f;
         if (k < n1) {
-            const uint32_t h = (uint32_t)(k / FP), q = (uint32_t)(k - (uint64_t)h * FP);
-            // padded position q -> real feature index
+            const uint32_t q = (uint32_t)(k / HP), h = (uint32_t)(k - (uint64_t)q * HP);
+            // padded feature position q -> real feature index
             int64_t fi = -1;
             if (q < SS) fi = q < S ? (int64_t)q : -1;
             else if (q < 2 * SS) fi = q - SS < S ? (int64_t)(S + q - SS) : -1;
@@ -501,139 +607,169 @@ __global__ __launch_bounds__(256) void k_pad_weights(StepParams P, int D, const 
                 const uint32_t r = q - (2 * SS + SS * D);
                 fi = 2 * S + S * D + r < F ? (int64_t)(2 * S + S * D + r) : -1;
             }
-            if (fi >= 0) v = w1[(uint64_t)h * F + fi];
-        } else if (k < n1 + H) {
-            v = b1[k - n1];
-        } else if (k < n1 + H + n2) {
-            const uint64_t t = k - n1 - H;
+            if (fi >= 0 && h < H) v = w1[(uint64_t)h * F + fi];
+        } else if (k < n1 + HP) {
+            const uint32_t h = (uint32_t)(k - n1);
+            if (h < H) v = b1[h];
+        } else if (k < n1 + HP + n2) {
+            const uint64_t t = k - n1 - HP;
             const uint32_t h = (uint32_t)(t / OP), o = (uint32_t)(t - (uint64_t)h * OP);
             if (o < O) v = w2[(uint64_t)o * H + h];
         } else {
-            const uint32_t o = (uint32_t)(k - n1 - H - n2);
+            const uint32_t o = (uint32_t)(k - n1 - HP - n2);
             if (o < O) v = b2[o];
         }
         wpad[k] = v;
     }
 }
 
-// Update MLP + motion scaling + 3D gates + masked Euler, one lane per sorted slot.
-// forward_update_from_features model.rs:900-940 (each output sum starts from its bias and adds
-// hidden units in ascending order; hidden unit h is consumed as soon as it is produced),
-// forward_from_features_with_eps model.rs:867-898, gates model.rs:806-837, euler_step step.rs:4-55.
-// Reads the padded feature rows and padded weights, from LDS when they fit (WLDS).
-template <int D, int SM, int FM, bool WLDS>
+// Update MLP + motion scaling + 3D gates + masked Euler for 64 sorted slots per 4-wave block.
+// forward_update_from_features model.rs:900-940, forward_from_features_with_eps model.rs:867-898,
+// gates model.rs:806-837, euler_step step.rs:4-55.
+//   phase 1: lane = row; wave w computes hidden units [32w + 128p, 32w + 128p + 32) with the
+//            weights of feature k as wave-uniform scalar loads; each hidden sum starts from its
+//            bias and adds features k = 0..FM-1 in order (padded positions carry zero weights).
+//   phase 2: lane = row; wave w owns outputs [OPW*w, OPW*w + OPW); each output sum starts from its
+//            bias and adds hidden units h = 0..H-1 in order, reading them from LDS.
+//   phase 3: wave 0 applies motion scaling, gates, mask and the Euler step for its 64 rows.
+template <int D, int SM, int FM>
 __global__ __launch_bounds__(256) void k_mlp_euler(StepParams P, const float* __restrict__ sfeatures,
                                                    const float* __restrict__ sstate,
                                                    const uint32_t* __restrict__ perm,
                                                    const float* __restrict__ wpad, StepIO io) {
-    extern __shared__ float wsm[];
-    constexpr int OM = D + SM;
-    const uint32_t S = P.S, H = P.H, T = P.T;
-    const uint64_t nw = (uint64_t)H * FM + H + (uint64_t)H * OM + OM;
-    const float* W = wpad;
-    if constexpr (WLDS) {
-        const float4* src = reinterpret_cast<const float4*>(wpad);
-        float4* dst = reinterpret_cast<float4*>(wsm);
-        for (uint32_t k = threadIdx.x; k < nw / 4; k += blockDim.x) dst[k] = src[k];
-        for (uint32_t k = (uint32_t)(nw / 4) * 4 + threadIdx.x; k < nw; k += blockDim.x) wsm[k] = wpad[k];
-        __syncthreads();
-        W = wsm;
+    constexpr int OP = (D + SM + 3) / 4 * 4;
+    constexpr int OPW = OP / 4;
+    extern __shared__ float lds[];
+    const uint32_t H = P.H, T = P.T;
+    const uint32_t HP = (H + 127) / 128 * 128;
+    float* hid = lds;                       // [HP][64]
+    float* ul = lds + (size_t)HP * 64;      // [64][OP + 1]
+    const float* w1t = wpad;
+    const float* b1p = w1t + (uint64_t)FM * HP;
+    const float* w2t = b1p + HP;
+    const float* b2p = w2t + (uint64_t)H * OP;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t row0 = blockIdx.x * 64;
+    const uint32_t s = row0 + lane;
+    const bool valid = s < T;
+
+    float f[FM];
+#pragma unroll
+    for (int k = 0; k < FM; ++k) f[k] = valid ? sfeatures[(uint64_t)k * T + s] : 0.0f;
+
+    // phase 1: hidden units
+    for (uint32_t hb = wave * 32; hb < HP; hb += 128) {
+        float acc[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) acc[j] = b1p[hb + j];
+#pragma unroll
+        for (int k = 0; k < FM; ++k) {
+            const float* wk = w1t + (uint64_t)k * HP + hb;
+            const float fk = f[k];
+#pragma unroll
+            for (int j = 0; j < 32; ++j) acc[j] += wk[j] * fk;
+        }
+#pragma unroll
+        for (int j = 0; j < 32; ++j) hid[(hb + j) * 64 + lane] = fmaxf(acc[j], 0.0f);
     }
-    const float* w1 = W;
-    const float* b1 = w1 + (uint64_t)H * FM;
-    const float* w2t = b1 + H;
-    const float* b2 = w2t + (uint64_t)H * OM;
-    for (uint32_t s = blockIdx.x * blockDim.x + threadIdx.x; s < T; s += gridDim.x * blockDim.x) {
-        const uint32_t b = s / P.N;
-        const uint32_t li = perm[s];
-        const uint32_t i = b * P.N + li;
-        float f[FM];
+    __syncthreads();
+
+    // phase 2: outputs
+    {
+        const uint32_t ob = wave * OPW;
+        float u[OPW];
 #pragma unroll
-        for (int k = 0; k < FM; ++k) f[k] = sfeatures[(uint64_t)k * T + s];
-        float u[OM];
-#pragma unroll
-        for (int o = 0; o < OM; ++o) u[o] = b2[o];
+        for (int o = 0; o < OPW; ++o) u[o] = b2p[ob + o];
         for (uint32_t h = 0; h < H; ++h) {
-            const float* wr = w1 + (uint64_t)h * FM;
-            float sum = b1[h];
+            const float hv = hid[h * 64 + lane];
+            const float* wr = w2t + (uint64_t)h * OP + ob;
 #pragma unroll
-            for (int k = 0; k < FM; ++k) sum += wr[k] * f[k];
-            const float hv = fmaxf(sum, 0.0f);
-            const float* wc = w2t + (uint64_t)h * OM;
-#pragma unroll
-            for (int o = 0; o < OM; ++o) u[o] += wc[o] * hv;
+            for (int o = 0; o < OPW; ++o) u[o] += wr[o] * hv;
         }
-        float norm = 0.0f;
 #pragma unroll
-        for (int a = 0; a < D; ++a) norm += u[a] * u[a];
-        norm = sqrtf(norm);
-        float dx[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int o = 0; o < OPW; ++o) ul[lane * (OP + 1) + ob + o] = u[o];
+    }
+    __syncthreads();
+    if (wave != 0 || !valid) return;
+
+    // phase 3: motion scaling, gates, mask, Euler
+    const uint32_t S = P.S;
+    float u[D + SM];
 #pragma unroll
-        for (int a = 0; a < D; ++a) dx[a] = P.alpha * u[a] * P.motion_eps / (1.0f + norm);
-        const float4 pos4 = io.pos[i];
-        const float porig[4] = {pos4.x, pos4.y, pos4.z, pos4.w};
-        float si[SM];
-        {
-            const float4* own = reinterpret_cast<const float4*>(sstate + (uint64_t)s * SM);
+    for (int o = 0; o < D + SM; ++o) u[o] = ul[lane * (OP + 1) + o];
+    const uint32_t b = s / P.N;
+    const uint32_t li = perm[s];
+    const uint32_t i = b * P.N + li;
+    float norm = 0.0f;
 #pragma unroll
-            for (int q = 0; q < SM / 4; ++q) {
-                const float4 v = own[q];
-                si[4 * q] = v.x;
-                si[4 * q + 1] = v.y;
-                si[4 * q + 2] = v.z;
-                si[4 * q + 3] = v.w;
-            }
+    for (int a = 0; a < D; ++a) norm += u[a] * u[a];
+    norm = sqrtf(norm);
+    float dx[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int a = 0; a < D; ++a) dx[a] = P.alpha * u[a] * P.motion_eps / (1.0f + norm);
+    const float4 pos4 = io.pos[i];
+    const float porig[4] = {pos4.x, pos4.y, pos4.z, pos4.w};
+    float si[SM];
+    {
+        const float4* own = reinterpret_cast<const float4*>(sstate + (uint64_t)s * SM);
+#pragma unroll
+        for (int q = 0; q < SM / 4; ++q) {
+            const float4 v = own[q];
+            si[4 * q] = v.x;
+            si[4 * q + 1] = v.y;
+            si[4 * q + 2] = v.z;
+            si[4 * q + 3] = v.w;
         }
-        float sg = 1.0f;
-        if (P.gates3d) {
-            const float liveness = si[3 < SM ? 3 : 0];
-            const float sd = si[7 < SM ? 7 : 0];
-            sg = clampf_((4.0f - liveness) * 2.0f, 0.0f, 1.0f);
-            float mg;
-            if (porig[3] >= 0.5f) {
-                mg = 0.0f;
-            } else {
-                const float dgate = clampf_((fabsf(sd) - 0.01f) / 0.02f, 0.0f, 1.0f);
-                mg = sg * dgate;
-            }
-#pragma unroll
-            for (int a = 0; a < D; ++a) dx[a] *= mg;
-        }
-        const float m = io.mask ? io.mask[i] : hash_mask(li, b, P.N, P.update_prob, P.step_index, P.base_seed);
-        float pn[4] = {porig[0], porig[1], porig[2], porig[3]};
-        constexpr int MEM = D == 3 ? 4 : 2;
-#pragma unroll
-        for (int a = 0; a < MEM; ++a) pn[a] += P.dt * dx[a] * m;
-        if (P.g.boundary == 0) {  // wrap_position hashgrid.rs:183-193
-#pragma unroll
-            for (int a = 0; a < D; ++a) {
-                const float v = pn[a] + P.g.half[a];
-                float r = fmodf(v, P.g.extent[a]);
-                if (r < 0.0f) r = r + fabsf(P.g.extent[a]);
-                pn[a] = r - P.g.half[a];
-            }
-        }
-        io.out_pos[i] = make_float4(pn[0], pn[1], pn[2], pn[3]);
-        float nxt[SM];
-#pragma unroll
-        for (int c = 0; c < SM; ++c) {
-            float dsc = u[D + c];
-            if (P.gates3d) dsc *= sg;
-            float next = si[c] + P.dt * dsc * m;
-            if (D == 3 && S > 3 && (c == 3 || (S > 8 && c == 8))) next = clampf_(next, -8.0f, 24.0f);
-            nxt[c] = next;
-        }
-        float* os = io.out_states + (uint64_t)i * S;
-        if (S == SM) {  // 16-byte aligned rows (checked on the host)
-            float4* o4 = reinterpret_cast<float4*>(os);
-#pragma unroll
-            for (int q = 0; q < SM / 4; ++q)
-                o4[q] = make_float4(nxt[4 * q], nxt[4 * q + 1], nxt[4 * q + 2], nxt[4 * q + 3]);
+    }
+    float sg = 1.0f;
+    if (P.gates3d) {
+        const float liveness = si[3 < SM ? 3 : 0];
+        const float sd = si[7 < SM ? 7 : 0];
+        sg = clampf_((4.0f - liveness) * 2.0f, 0.0f, 1.0f);
+        float mg;
+        if (porig[3] >= 0.5f) {
+            mg = 0.0f;
         } else {
-#pragma unroll
-            for (int c = 0; c < SM; ++c)
-                if ((uint32_t)c < S) os[c] = nxt[c];
+            const float dgate = clampf_((fabsf(sd) - 0.01f) / 0.02f, 0.0f, 1.0f);
+            mg = sg * dgate;
         }
+#pragma unroll
+        for (int a = 0; a < D; ++a) dx[a] *= mg;
+    }
+    const float m = io.mask ? io.mask[i] : hash_mask(li, b, P.N, P.update_prob, P.step_index, P.base_seed);
+    float pn[4] = {porig[0], porig[1], porig[2], porig[3]};
+    constexpr int MEM = D == 3 ? 4 : 2;
+#pragma unroll
+    for (int a = 0; a < MEM; ++a) pn[a] += P.dt * dx[a] * m;
+    if (P.g.boundary == 0) {  // wrap_position hashgrid.rs:183-193
+#pragma unroll
+        for (int a = 0; a < D; ++a) {
+            const float v = pn[a] + P.g.half[a];
+            float r = fmodf(v, P.g.extent[a]);
+            if (r < 0.0f) r = r + fabsf(P.g.extent[a]);
+            pn[a] = r - P.g.half[a];
+        }
+    }
+    io.out_pos[i] = make_float4(pn[0], pn[1], pn[2], pn[3]);
+    float nxt[SM];
+#pragma unroll
+    for (int c = 0; c < SM; ++c) {
+        float dsc = u[D + c];
+        if (P.gates3d) dsc *= sg;
+        float next = si[c] + P.dt * dsc * m;
+        if (D == 3 && S > 3 && (c == 3 || (S > 8 && c == 8))) next = clampf_(next, -8.0f, 24.0f);
+        nxt[c] = next;
+    }
+    float* os = io.out_states + (uint64_t)i * S;
+    if (S == SM) {  // 16-byte aligned rows (checked on the host)
+        float4* o4 = reinterpret_cast<float4*>(os);
+#pragma unroll
+        for (int q = 0; q < SM / 4; ++q) o4[q] = make_float4(nxt[4 * q], nxt[4 * q + 1], nxt[4 * q + 2], nxt[4 * q + 3]);
+    } else {
+#pragma unroll
+        for (int c = 0; c < SM; ++c)
+            if ((uint32_t)c < S) os[c] = nxt[c];
     }
 }
 
@@ -767,18 +903,27 @@ __global__ __launch_bounds__(256) void k_neighbor_lists(StepParams P, const floa
 }
 
 // ------------------------------------------------------------------ launch
+template <int D, int L>
+static void launch_density_t(const StepParams& p, Workspace& ws, float* density_out, int blocks, hipStream_t stream) {
+    hipLaunchKernelGGL((k_density<D, L>), dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
+                       ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
+                       ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.svol.as<float>(), density_out);
+}
+
+template <int D>
+static void launch_density_d(const StepParams& p, Workspace& ws, float* density_out, int blocks, hipStream_t stream) {
+    const uint32_t L = lanes_per_target(p.SS);
+    if (L == 1) launch_density_t<D, 1>(p, ws, density_out, blocks, stream);
+    else if (L == 2) launch_density_t<D, 2>(p, ws, density_out, blocks, stream);
+    else launch_density_t<D, 4>(p, ws, density_out, blocks, stream);
+}
+
 hipError_t launch_density(const StepParams& p, Workspace& ws, float* density_out, int grid_blocks,
                           hipStream_t stream, Profiler* prof) {
     ProfScope ps(prof, NPA_KERNEL_DENSITY, stream);
     const int blocks = grid_blocks * 4;  // one wave per block
-    if (p.g.dim == 2)
-        hipLaunchKernelGGL(k_density<2>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
-                           ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
-                           ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.svol.as<float>(), density_out);
-    else
-        hipLaunchKernelGGL(k_density<3>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
-                           ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
-                           ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.svol.as<float>(), density_out);
+    if (p.g.dim == 2) launch_density_d<2>(p, ws, density_out, blocks, stream);
+    else launch_density_d<3>(p, ws, density_out, blocks, stream);
     return hipGetLastError();
 }
 
@@ -805,7 +950,9 @@ static void launch_perceive_d(const StepParams& p, Workspace& ws, const StepIO& 
 
 size_t padded_weight_floats(const StepParams& p) {
     const uint32_t D = (uint32_t)p.g.dim;
-    return (size_t)p.H * p.FP + p.H + (size_t)p.H * (D + p.SS) + (D + p.SS);
+    const size_t HP = (p.H + 127) / 128 * 128;
+    const size_t OP = (D + p.SS + 3) / 4 * 4;
+    return (size_t)p.FP * HP + HP + (size_t)p.H * OP + OP;
 }
 
 hipError_t launch_pad_weights(const StepParams& p, const float* w1, const float* b1, const float* w2,
@@ -818,17 +965,19 @@ hipError_t launch_pad_weights(const StepParams& p, const float* w1, const float*
 
 template <int D, int SM, int FM>
 static hipError_t launch_mlp_t(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream) {
-    const size_t wbytes = padded_weight_floats(p) * 4;
-    const uint32_t blocks = std::max<uint32_t>(1, std::min<uint32_t>((p.T + 255) / 256, (uint32_t)device_cu_count() * 8));
-    if (wbytes <= 64 * 1024) {
-        hipLaunchKernelGGL((k_mlp_euler<D, SM, FM, true>), dim3(blocks), dim3(256), wbytes, stream, p,
-                           ws.features.as<float>(), ws.sstate.as<float>(), ws.perm.as<uint32_t>(),
-                           ws.wpad.as<float>(), io);
-    } else {
-        hipLaunchKernelGGL((k_mlp_euler<D, SM, FM, false>), dim3(blocks), dim3(256), 0, stream, p,
-                           ws.features.as<float>(), ws.sstate.as<float>(), ws.perm.as<uint32_t>(),
-                           ws.wpad.as<float>(), io);
+    constexpr int OP = (D + SM + 3) / 4 * 4;
+    const size_t HP = (p.H + 127) / 128 * 128;
+    const size_t lds = (HP * 64 + 64 * (OP + 1)) * 4;
+    static size_t attr = 65536;
+    if (lds > attr) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_mlp_euler<D, SM, FM>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr = lds;
     }
+    const uint32_t blocks = (p.T + 63) / 64;
+    hipLaunchKernelGGL((k_mlp_euler<D, SM, FM>), dim3(blocks), dim3(256), lds, stream, p, ws.features.as<float>(),
+                       ws.sstate.as<float>(), ws.perm.as<uint32_t>(), ws.wpad.as<float>(), io);
     return hipGetLastError();
 }
 
