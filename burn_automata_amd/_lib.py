@@ -22,6 +22,7 @@ st = C.c_int
 
 def _decl(L):
     ptr = C.POINTER
+    L.npa_version.argtypes = []
     L.npa_version.restype = C.c_char_p
     L.npa_context_create.argtypes = [C.c_int, P, ptr(P)]
     L.npa_context_destroy.argtypes = [P]

@@ -7,7 +7,7 @@
 // same algorithm glibc's float log1pf is built on - FDLIBM's s_log1pf (Sun Microsystems; "permission
 // to use, copy, modify, and distribute this software is freely granted, provided that this notice is
 // preserved") - evaluated in float with the same operation order and no FMA contraction. The test
-// tests/test_log1p.py compiles this header on the host and compares it with the host libm's log1pf
+// tests/test_abi.py (via tests/native/check_log1p.cpp) compiles this header on the host and compares it with the host libm's log1pf
 // for every float bit pattern in [-1, +inf]; the recorded result is zero mismatches.
 //
 // Outline: for x outside (-0.2929, 0.41422) reduce 1+x = 2^k * u with u in [sqrt(2)/2, sqrt(2)),

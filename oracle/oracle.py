@@ -22,12 +22,17 @@ from burn_automata_amd.config import (GaussianDecodeConfig, HashGridConfig, NpaC
                                       PerceptionOptions, Splat2dConfig)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "libnpa_oracle.so")
+# NPA_ORACLE_LIB points the loader at another build of the oracle; tests/test_oracle_mutants.py
+# uses it to run the pinning tests against copies with planted mistakes.
+_OVERRIDE = os.environ.get("NPA_ORACLE_LIB")
+_LIB_PATH = _OVERRIDE or os.path.join(_HERE, "libnpa_oracle.so")
 _lib = None
 
 
 def build(force: bool = False) -> str:
     """Compiles the oracle with its Makefile (gcc -O3 -fopenmp -ffp-contract=off)."""
+    if _OVERRIDE:
+        return _LIB_PATH
     args = ["make", "-C", _HERE] + (["-B"] if force else [])
     subprocess.run(args, check=True, stdout=subprocess.DEVNULL)
     return _LIB_PATH
@@ -144,6 +149,7 @@ def cell_coords(pos4, cfg: HashGridConfig):
 def build_hashgrid(positions, batch_size: int, particle_count: int,
                    cfg: HashGridConfig) -> HashGridSnapshot:
     pos = _f32(positions, (-1, 4))
+    _check(lib().oracle_grid_validate(C.byref(cfg.to_c())))
     if pos.shape[0] != batch_size * particle_count:
         raise _abi.PositionShape(f"positions {pos.shape[0]} != {batch_size * particle_count}")
     cells = cfg.cell_count()

@@ -1,0 +1,799 @@
+"""CPU checks that pin the oracle (oracle/libnpa_oracle.so) to the reference's behaviour.
+
+The reference path is Rust and cannot be built here, so the oracle is a C restatement. These
+tests pin it with, in order of strength:
+  * the reference's own known-answer unit tests for this path (values transcribed into
+    tests/golden/reference_known_answers.json, each with its file:line);
+  * integer closed forms restated from the reference source in a second language (cell hash,
+    mask hash), brute force on small inputs (counting sort, neighbour sets and order, density,
+    blur), and float64 closed forms (poly6/spiky constants, log-normalisation, equivariance
+    scales, motion, splat of one particle);
+  * invariants the mathematics fixes: the moment-corrected SPH gradient of a linear field is the
+    field's slope for every particle with an invertible moment matrix, rigid scale equivariance
+    of a scale-equivariant model (crates/burn_automata/tests/core/equivariance.rs:4-67),
+    composition (step == perceive -> MLP -> Euler; rollout == repeated masked steps), additivity
+    of the splat.
+Each check is chosen so that a plausible slip (a dropped term, a swapped sign, a transposed
+operand, a wrong index or order) fails it.
+"""
+from __future__ import annotations
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from burn_automata_amd import synthetic as syn
+from burn_automata_amd.config import (Boundary, EquivarianceMode, GaussianDecodeConfig,
+                                      GaussianDecodeMode, HashGridConfig, HashGridMode, NpaConfig,
+                                      PerceptionOptions, Splat2dConfig)
+from oracle import oracle as O
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KNOWN = json.load(open(os.path.join(HERE, "golden", "reference_known_answers.json")))
+
+M32 = 0xFFFFFFFF
+f32 = np.float32
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _built():
+    O.build()
+    O.lib()
+
+
+# --------------------------------------------------------------------------------------------
+# independent restatements (integer closed forms; float32 evaluation order as in the reference)
+# --------------------------------------------------------------------------------------------
+
+def mix_coord(value: int, salt: int) -> int:
+    """hashgrid.rs:157-165: (value as i32 as u32) ^ salt, then xorshift-multiply."""
+    x = (value & M32) ^ salt
+    x ^= x >> 16
+    x = (x * 0x7FEB352D) & M32
+    x ^= x >> 15
+    x = (x * 0x846CA68B) & M32
+    x ^= x >> 16
+    return x
+
+
+def cell_coords_ref(p, cfg: HashGridConfig):
+    """cell_coords_for_position (hashgrid.rs:98-121) in float32."""
+    out = [0, 0, 0]
+    eps = f32(cfg.eps)
+    for a in range(cfg.dim):
+        x = f32(p[a])
+        if cfg.mode == HashGridMode.Particle:
+            out[a] = int(math.floor(float(x / eps)))
+            continue
+        size = int(cfg.grid_size[a])
+        extent = eps * f32(size)
+        half = extent * f32(0.5)
+        c = int(math.floor(float((x + half) / eps)))
+        c = c % size if cfg.boundary == Boundary.Periodic else min(max(c, 0), size - 1)
+        out[a] = c
+    return tuple(out)
+
+
+def cell_index_ref(coords, cfg: HashGridConfig):
+    """cell_index_from_coords / particle_cell_hash (hashgrid.rs:123-155)."""
+    if cfg.mode == HashGridMode.Particle:
+        h = mix_coord(coords[0], 0x9E3779B9) ^ mix_coord(coords[1], 0x85EBCA6B)
+        if cfg.dim == 3:
+            h ^= mix_coord(coords[2], 0xC2B2AE35)
+        return h % cfg.cell_count()
+    stride, h = 1, 0
+    for a in range(cfg.dim):
+        size = int(cfg.grid_size[a])
+        c = coords[a]
+        if cfg.boundary == Boundary.Periodic:
+            c %= size
+        elif c < 0 or c >= size:
+            return None
+        h += c * stride
+        stride *= size
+    return h
+
+
+def hash_u32_ref(v: int) -> int:
+    """hash_u32 of the reference's CPU replica of the device mask
+    (crates/burn_automata/tests/gpu_wgpu/common.rs:126-133)."""
+    x = v & M32
+    x = (x ^ 61) ^ (x >> 16)
+    x = (x + (x << 3)) & M32
+    x ^= x >> 4
+    x = (x * 0x27D4EB2D) & M32
+    return x ^ (x >> 15)
+
+
+def random01_ref(particle: int, step: int, seed: int) -> float:
+    """gpu_random01 (common.rs:121-124)."""
+    mixed = hash_u32_ref(particle ^ hash_u32_ref((step + 0x9E3779B9) & M32) ^ seed)
+    return float(f32(mixed >> 8) * f32(1.0 / 16777216.0))
+
+
+def pair_table(pos: np.ndarray, cfg: HashGridConfig):
+    """All-pairs delta / r^2 in float32 with the reference's operation order
+    (neighbor_delta hashgrid.rs:167-181; r2 = sum of squares from 0, neighbor.rs:35-37)."""
+    d = cfg.dim
+    P = pos[:, :d].astype(f32)
+    D = P[None, :, :] - P[:, None, :]  # D[i, j] = p_j - p_i
+    if cfg.boundary == Boundary.Periodic:
+        for a in range(d):
+            extent = f32(cfg.grid_size[a]) * f32(cfg.eps)
+            half = extent * f32(0.5)
+            col = D[:, :, a]
+            col = np.where(col > half, col - extent, np.where(col < -half, col + extent, col))
+            D[:, :, a] = col
+    r2 = np.zeros(D.shape[:2], f32)
+    for a in range(d):
+        r2 = r2 + D[:, :, a] * D[:, :, a]
+    return D, r2
+
+
+def eps2(cfg):
+    return f32(cfg.eps) * f32(cfg.eps)
+
+
+def k6(cfg):
+    """smoothing_poly6_normalization (kernels.rs:126-132), float64."""
+    e = float(cfg.eps)
+    return 4.0 / (math.pi * e ** 8) if cfg.dim == 2 else 315.0 / (64.0 * math.pi * e ** 9)
+
+
+def k5(cfg):
+    """gradient_spiky_normalization (kernels.rs:134-140), float64."""
+    e = float(cfg.eps)
+    return 10.0 / (math.pi * e ** 5) if cfg.dim == 2 else 15.0 / (math.pi * e ** 6)
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / max(float(np.max(np.abs(b))), 1e-30)) if b.size else 0.0
+
+
+def _grids():
+    g2 = HashGridConfig.growing_2d().replace(eps=0.05, grid_size=(64, 64, 1))
+    return {
+        "particle2d": g2,
+        "particle2d_small_table": g2.replace(grid_size=(4, 4, 1)),  # many hash collisions
+        "grid2d_clamped": HashGridConfig(2, Boundary.Clamped, HashGridMode.Grid, (24, 20, 1), 0.08),
+        "grid2d_periodic": HashGridConfig(2, Boundary.Periodic, HashGridMode.Grid, (16, 12, 1), 0.1),
+        "particle3d": HashGridConfig.growing_3dgs().replace(eps=0.2, grid_size=(8, 8, 8)),
+        "grid3d_periodic": HashGridConfig(3, Boundary.Periodic, HashGridMode.Grid, (8, 6, 5), 0.25),
+    }
+
+
+def _positions(name, cfg, n, seed=7):
+    rng = np.random.default_rng(seed)
+    d = cfg.dim
+    pos = np.zeros((n, 4), f32)
+    if cfg.mode == HashGridMode.Grid and cfg.boundary == Boundary.Periodic:
+        for a in range(d):
+            half = cfg.grid_size[a] * cfg.eps / 2
+            pos[:, a] = rng.uniform(-half, half, n)
+    else:
+        pos[:, :d] = rng.uniform(-0.6, 0.6, (n, d))
+        pos[: n // 10, :d] *= 2.5  # some outside a clamped grid / far from the origin
+    return pos
+
+
+# --------------------------------------------------------------------------------------------
+# hashgrid
+# --------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", list(_grids()))
+def test_cell_hash_matches_integer_restatement(name):
+    cfg = _grids()[name]
+    pos = _positions(name, cfg, 400)
+    extra = np.array([[-1e-9, 0.0, 0.0, 0.0], [0.0, -0.0, 0.0, 0.0],
+                      [cfg.eps, -cfg.eps, cfg.eps, 0.0], [123.4, -77.7, 5.5, 0.0]], f32)
+    for p in np.concatenate([pos, extra]):
+        coords = cell_coords_ref(p, cfg)
+        assert O.cell_coords(p, cfg)[: cfg.dim] == coords[: cfg.dim]
+        idx = cell_index_ref(coords, cfg)
+        assert O.cell_for_position(p, cfg) == idx
+
+
+def test_hashgrid_counts_particles_per_cell():
+    """hashgrid_counts_particles_per_cell (crates/burn_automata_kernels/src/lib.rs:73-84)."""
+    ka = KNOWN["hashgrid_counts_particles_per_cell"]
+    cfg = HashGridConfig.growing_2d().replace(grid_size=tuple(ka["grid_size"]))
+    g = O.build_hashgrid(np.array(ka["positions"], f32), 1, 2, cfg)
+    assert len(g.bin_offsets) == cfg.cell_count() + 1
+    assert len(g.permutation) == 2
+    assert np.any(np.diff(g.bin_offsets.astype(np.int64)) > 0)
+
+
+@pytest.mark.parametrize("name", list(_grids()))
+@pytest.mark.parametrize("batch", [1, 3])
+def test_hashgrid_is_a_stable_counting_sort(name, batch):
+    cfg = _grids()[name]
+    n = 300
+    pos = np.concatenate([_positions(name, cfg, n, seed=11 + b) for b in range(batch)])
+    g = O.build_hashgrid(pos, batch, n, cfg)
+    C = cfg.cell_count()
+    cells = np.array([cell_index_ref(cell_coords_ref(p, cfg), cfg) for p in pos], np.int64)
+    assert g.bin_offsets[0] == 0 and g.bin_offsets[-1] == batch * n
+    for b in range(batch):
+        cb = cells[b * n:(b + 1) * n]
+        counts = np.bincount(cb, minlength=C)
+        want_off = b * n + np.concatenate([[0], np.cumsum(counts)])
+        np.testing.assert_array_equal(g.bin_offsets[b * C:(b + 1) * C + 1], want_off)
+        order = np.argsort(cb, kind="stable")  # stable: original order within a bin
+        np.testing.assert_array_equal(g.permutation[b * n:(b + 1) * n], order)
+        inv = g.inverse_permutation[b * n:(b + 1) * n]
+        np.testing.assert_array_equal(inv[order], np.arange(n))
+
+
+def test_hashgrid_rejects_invalid_configs():
+    """validate (crates/burn_automata_kernels/src/config.rs:66-99) error variants."""
+    from burn_automata_amd import _abi
+    pos = np.zeros((2, 4), f32)
+    good = HashGridConfig.growing_2d()
+    cases = [
+        (good.replace(dim=4), _abi.InvalidDim),
+        (good.replace(eps=0.0), _abi.InvalidEps),
+        (good.replace(eps=float("nan")), _abi.InvalidEps),
+        (good.replace(grid_size=(0, 64, 1)), _abi.InvalidGridSize),
+        (good.replace(grid_size=(48, 64, 1)), _abi.ParticleModeRequiresPowerOfTwo),
+    ]
+    for cfg, err in cases:
+        with pytest.raises(err):
+            O.build_hashgrid(pos, 1, 2, cfg)
+    with pytest.raises(_abi.PositionShape):
+        O.build_hashgrid(pos, 1, 3, good)
+
+
+# --------------------------------------------------------------------------------------------
+# neighbour lists
+# --------------------------------------------------------------------------------------------
+
+def _offset_order(dim):
+    zs = (-1, 0, 1) if dim == 3 else (0,)
+    return [(dx, dy, dz) for dz in zs for dy in (-1, 0, 1) for dx in (-1, 0, 1)]
+
+
+@pytest.mark.parametrize("name", list(_grids()))
+def test_neighbor_lists_match_brute_force_sets_and_order(name):
+    cfg = _grids()[name]
+    n = 500 if cfg.dim == 2 else 300
+    batch = 2
+    pos = np.concatenate([_positions(name, cfg, n, seed=21 + b) for b in range(batch)])
+    off, idx = O.neighbor_lists(pos, batch, n, cfg)
+    g = O.build_hashgrid(pos, batch, n, cfg)
+    offsets = _offset_order(cfg.dim)
+    total_pairs = 0
+    for b in range(batch):
+        P = pos[b * n:(b + 1) * n]
+        _, r2 = pair_table(P, cfg)
+        coords = [cell_coords_ref(p, cfg) for p in P]
+        inv = g.inverse_permutation[b * n:(b + 1) * n]
+        for i in range(n):
+            js = np.nonzero(r2[i] < eps2(cfg))[0]
+            keys = []
+            for j in js:
+                rel_c = []
+                for a in range(3 if cfg.dim == 3 else 2):
+                    dc = coords[j][a] - coords[i][a]
+                    if cfg.mode == HashGridMode.Grid and cfg.boundary == Boundary.Periodic:
+                        size = cfg.grid_size[a]
+                        dc = (dc + 1) % size - 1
+                    rel_c.append(dc)
+                if cfg.dim == 2:
+                    rel_c.append(0)
+                keys.append((offsets.index(tuple(rel_c)), int(inv[j]), int(j)))
+            want = [b * n + k[2] for k in sorted(keys)]
+            got = idx[off[b * n + i]:off[b * n + i + 1]].tolist()
+            assert got == want, (name, b, i)
+            total_pairs += len(want)
+    assert total_pairs > 2 * batch * n  # the fixture has real neighbourhoods
+
+
+def test_pair_at_exactly_eps_is_not_a_neighbour():
+    """Acceptance is r^2 < eps^2, strict (neighbor.rs:35-37): a pair exactly eps apart in float32
+    (delta = eps, so r^2 == eps^2 bit for bit) is not a neighbour."""
+    for mode in (HashGridMode.Particle, HashGridMode.Grid):
+        cfg = HashGridConfig(2, Boundary.Clamped, mode, (16, 16, 1), 0.05)
+        pos = np.array([[0.0, 0.0, 0, 0], [0.05, 0.0, 0, 0], [0.0, -0.05, 0, 0]], f32)
+        _, r2 = pair_table(pos, cfg)
+        assert r2[0, 1] == eps2(cfg) and r2[0, 2] == eps2(cfg)
+        off, idx = O.neighbor_lists(pos, 1, 3, cfg)
+        assert idx.tolist() == [0, 1, 2]  # each particle sees only itself
+        out = O.perceive_with_options(pos, np.zeros((3, 1), f32), 1, 3, 1, cfg, _opts(eps0=0.05))
+        assert out.density == pytest.approx([k6(cfg) * 0.05 ** 6] * 3, rel=1e-6)
+
+
+def test_neighbor_search_counts_match_reference_fixture():
+    """Exact pair count of spatial_strategy_bvh_matches_hashgrid_neighbor_counts
+    (crates/burn_automata_kernels/src/lib.rs:530-564) by brute force: the hashgrid walk must
+    find every pair within eps and nothing else."""
+    ka = KNOWN["spatial_strategy_bvh_matches_hashgrid_neighbor_counts"]
+    cfg = HashGridConfig.growing_3dgs().replace(grid_size=tuple(ka["grid_size"]))
+    pos = np.array(ka["positions"], f32)
+    off, idx = O.neighbor_lists(pos, 1, len(pos), cfg)
+    _, r2 = pair_table(pos, cfg)
+    assert len(idx) == int(np.sum(r2 < eps2(cfg)))
+
+
+# --------------------------------------------------------------------------------------------
+# SPH perception
+# --------------------------------------------------------------------------------------------
+
+def test_perceive_matches_upstream_sph_kernel_constants():
+    """perceive_matches_upstream_sph_kernel_constants (lib.rs:100-120), plus the same numbers
+    derived by hand from K6 = 4/(pi eps^8), K5 = 10/(pi eps^5)."""
+    ka = KNOWN["perceive_matches_upstream_sph_kernel_constants"]
+    cfg = HashGridConfig.growing_2d().replace(grid_size=tuple(ka["grid_size"]), eps=ka["eps"])
+    pos = np.array(ka["positions"], f32)
+    st = np.array(ka["states"], f32)
+    out = O.perceive(pos, st, 1, 2, 2, cfg, True, True)
+    for key, index, want, tol in ka["expect"]:
+        got = getattr(out, key).reshape(-1)[index]
+        assert abs(float(got) - want) <= tol, (key, index, got, want)
+    # closed forms in float64
+    e, r = float(cfg.eps), 0.05
+    rho = k6(cfg) * (e ** 6 + (e * e - r * r) ** 3)
+    w0, w1 = k6(cfg) * e ** 6, k6(cfg) * (e * e - r * r) ** 3
+    grad_mag = k5(cfg) * 3.0 * (e - r) ** 2 / r
+    assert out.density == pytest.approx([rho, rho], rel=2e-6)
+    assert out.blurred_state.reshape(-1) == pytest.approx(
+        [w0 / rho, w1 / rho, w1 / rho, w0 / rho], rel=2e-6)
+    # two particles: rank-1 moment matrix -> identity correction; scale eps/eps0 = 1
+    vol = 1.0 / rho
+    sg = out.state_gradient.reshape(2, 2, 2)  # [particle][channel][axis]
+    assert sg[0, 0, 0] == pytest.approx((0.0 - 1.0) * vol * grad_mag * r, rel=2e-6)
+    assert sg[0, 1, 0] == pytest.approx((1.0 - 0.0) * vol * grad_mag * r, rel=2e-6)
+    assert sg[1, 0, 0] == pytest.approx((1.0 - 0.0) * vol * grad_mag * (-r), rel=2e-6)
+    dg = out.density_gradient.reshape(2, 2)
+    assert dg[0, 0] == pytest.approx(grad_mag * r / 2, rel=2e-6)  # x (eps/eps0)^3 / N
+    assert dg[1, 0] == pytest.approx(-grad_mag * r / 2, rel=2e-6)
+    assert np.all(sg[:, :, 1] == 0) and np.all(dg[:, 1] == 0)
+
+
+def test_perceive_returns_finite_reference_features():
+    """perceive_returns_finite_reference_features (lib.rs:87-97)."""
+    ka = KNOWN["perceive_returns_finite_reference_features"]
+    cfg = HashGridConfig.growing_2d()
+    out = O.perceive(np.array(ka["positions"], f32), np.array(ka["states"], f32), 1, 2, 2, cfg,
+                     True, True)
+    assert out.feature_dims == 2 * 2 + 2 * cfg.dim + cfg.dim
+    assert out.features.size == 2 * out.feature_dims
+    assert np.all(np.isfinite(out.features))
+    assert np.all(out.density > 0)
+
+
+def _opts(**kw):
+    o = PerceptionOptions.new(True, True, kw.pop("eps0", 0.05))
+    for k, v in kw.items():
+        setattr(o, k, v)
+    return o
+
+
+@pytest.mark.parametrize("name", ["particle2d", "grid2d_periodic", "particle3d"])
+def test_density_and_blur_match_brute_force(name):
+    cfg = _grids()[name]
+    n, S = (600, 3) if cfg.dim == 2 else (400, 3)
+    pos = _positions(name, cfg, n, seed=5)
+    rng = np.random.default_rng(3)
+    st = rng.normal(0, 1, (n, S)).astype(f32)
+    out = O.perceive_with_options(pos, st, 1, n, S, cfg, _opts(eps0=cfg.eps))
+    _, r2 = pair_table(pos, cfg)
+    inside = r2 < eps2(cfg)
+    W = np.where(inside, k6(cfg) * (float(cfg.eps) ** 2 - r2.astype(np.float64)) ** 3, 0.0)
+    rho = W.sum(axis=1)
+    assert rel(out.density, rho) < 2e-6
+    # blur uses the oracle's own float32 density for the volume (isolates the blur sum)
+    vol = 1.0 / out.density.astype(np.float64)
+    blur = W @ (st.astype(np.float64) * vol[:, None])
+    assert rel(out.blurred_state, blur) < 2e-5
+
+
+def _linear_field_case(dim, S=4, h=None, eps=0.06, seed=0):
+    rng = np.random.default_rng(seed)
+    h = h or eps / 3.2
+    ax = np.arange(-0.5, 0.5, h)
+    grids = np.meshgrid(*([ax] * dim), indexing="ij")
+    P = np.stack([g.reshape(-1) for g in grids], axis=1)
+    P += rng.uniform(-0.3 * h, 0.3 * h, P.shape)
+    n = P.shape[0]
+    pos = np.zeros((n, 4), f32)
+    pos[:, :dim] = P
+    A = rng.uniform(-2, 2, (S, dim))
+    b = rng.uniform(-1, 1, S)
+    st = (pos[:, :dim].astype(np.float64) @ A.T + b).astype(f32)
+    interior = np.all(np.abs(P) < 0.5 - 1.5 * eps, axis=1)
+    return pos, st, A, interior
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_moment_corrected_gradient_of_a_linear_field_is_its_slope(dim):
+    """M = sum_j d (x) gradW_j V_j and g = sum_j (s_j - s_i) gradW_j V_j = a^T M for s = a.x,
+    so the hybrid gradient g M^-1 (normalize.rs:93-118) returns a for every particle with an
+    invertible M; without the correction the jittered lattice is off by a few percent."""
+    eps = 0.06 if dim == 2 else 0.12
+    pos, st, A, interior = _linear_field_case(dim, eps=eps, h=eps / (3.2 if dim == 2 else 2.2))
+    n, S = st.shape
+    if dim == 2:
+        cfg = HashGridConfig.growing_2d().replace(eps=eps, grid_size=(64, 64, 1))
+    else:
+        cfg = HashGridConfig.growing_3dgs().replace(eps=eps, grid_size=(16, 16, 16))
+    out = O.perceive_with_options(pos, st, 1, n, S, cfg, _opts(eps0=eps, density_grad=False))
+    g = out.state_gradient.reshape(n, S, dim)[interior]
+    assert interior.sum() > 50
+    want = np.broadcast_to(A, g.shape)
+    assert rel(g, want) < 2e-3
+    raw = O.perceive_with_options(pos, st, 1, n, S, cfg,
+                                  _opts(eps0=eps, density_grad=False, hybrid_state_gradient=False))
+    assert rel(raw.state_gradient.reshape(n, S, dim)[interior], want) > 1e-2
+
+
+def _log_norm(v):
+    """log_normalize_vector (normalize.rs:60-69) in float64."""
+    nrm = np.maximum(np.sqrt(np.sum(v * v, axis=-1, keepdims=True) + 1e-12), 1e-6)
+    return v * np.log1p(nrm) / nrm
+
+
+def test_gradient_scaling_and_log_normalisation_closed_forms():
+    """normalize_state_gradient / normalize_density_gradient (normalize.rs:5-58): state gradient
+    x eps/eps0, density gradient x (eps/eps0)^(1+d) / N, each followed by the per-vector
+    log-normalisation v ln1p(n)/n."""
+    cfg = _grids()["particle2d"]
+    n, S, d = 700, 3, 2
+    pos = _positions("particle2d", cfg, n, seed=9)
+    st = np.random.default_rng(1).normal(0, 0.5, (n, S)).astype(f32)
+    eps0 = 0.035
+    base = O.perceive_with_options(pos, st, 1, n, S, cfg, _opts(
+        eps0=eps0, scale_equivariance=False, particle_density_equivariance=False))
+    scaled = O.perceive_with_options(pos, st, 1, n, S, cfg, _opts(eps0=eps0))
+    logn = O.perceive_with_options(pos, st, 1, n, S, cfg, _opts(
+        eps0=eps0, log_norm_grad=True, log_norm_density_grad=True))
+    s = cfg.eps / eps0
+    sg0 = base.state_gradient.astype(np.float64).reshape(n, S, d)
+    dg0 = base.density_gradient.astype(np.float64).reshape(n, d)
+    assert rel(scaled.state_gradient.reshape(n, S, d), sg0 * s) < 1e-6
+    assert rel(scaled.density_gradient.reshape(n, d), dg0 * s ** (1 + d) / n) < 1e-6
+    assert rel(logn.state_gradient.reshape(n, S, d), _log_norm(sg0 * s)) < 1e-5
+    assert rel(logn.density_gradient.reshape(n, d), _log_norm(dg0 * s ** (1 + d) / n)) < 1e-5
+    # density, blur untouched by the options
+    np.testing.assert_array_equal(base.density, logn.density)
+    np.testing.assert_array_equal(base.blurred_state, logn.blurred_state)
+
+
+def test_log_normalisation_of_small_vectors_uses_log1p():
+    """log_normalize_vector calls ln_1p (normalize.rs:65): for gradient norms of 1e-7..1e-4 the
+    scale ln1p(n)/n is 1 - n/2 + ..., which log(1 + n) in float32 cannot resolve."""
+    cfg = _grids()["particle2d"]
+    n, S, d = 500, 2, 2
+    pos = _positions("particle2d", cfg, n, seed=12)
+    st = (np.random.default_rng(5).normal(0, 1, (n, S)) * np.array([1e-8, 3e-7])).astype(f32)
+    base = O.perceive_with_options(pos, st, 1, n, S, cfg, _opts(eps0=0.05, density_grad=False))
+    logn = O.perceive_with_options(pos, st, 1, n, S, cfg, _opts(
+        eps0=0.05, density_grad=False, log_norm_grad=True))
+    g = base.state_gradient.astype(np.float64).reshape(n, S, d)
+    nrm = np.sqrt(np.sum(g * g, axis=-1))
+    assert np.median(nrm) < 1e-4 and np.median(nrm) > 1e-7
+    want = _log_norm(g)
+    got = logn.state_gradient.reshape(n, S, d).astype(np.float64)
+    nz = want != 0
+    assert np.max(np.abs(got[nz] - want[nz]) / np.abs(want[nz])) < 3e-6
+
+
+@pytest.mark.parametrize("dgrad,posf", [(False, False), (True, False), (True, True)])
+def test_feature_row_layout(dgrad, posf):
+    """Feature row = [state, blur, state gradient (channel-major), density gradient?, position?]
+    (forward.rs:100-133; width crates/burn_automata/src/config.rs:133-139)."""
+    cfg = _grids()["particle2d"]
+    n, S, d = 300, 4, 2
+    pos = _positions("particle2d", cfg, n, seed=2)
+    st = np.random.default_rng(4).normal(0, 1, (n, S)).astype(f32)
+    out = O.perceive_with_options(pos, st, 1, n, S, cfg,
+                                  _opts(eps0=0.05, density_grad=dgrad, position_features=posf))
+    F = 2 * S + S * d + d * dgrad + d * posf
+    assert out.feature_dims == F and out.features.shape == (n, F)
+    f = out.features
+    np.testing.assert_array_equal(f[:, :S], st)
+    np.testing.assert_array_equal(f[:, S:2 * S], out.blurred_state)
+    np.testing.assert_array_equal(f[:, 2 * S:2 * S + S * d], out.state_gradient.reshape(n, -1))
+    c = 2 * S + S * d
+    if dgrad:
+        np.testing.assert_array_equal(f[:, c:c + d], out.density_gradient.reshape(n, d))
+        c += d
+    if posf:
+        np.testing.assert_array_equal(f[:, c:c + d], pos[:, :d])
+
+
+# --------------------------------------------------------------------------------------------
+# update MLP, motion, Euler
+# --------------------------------------------------------------------------------------------
+
+def _int_model(S=4, H=16, d=2, dgrad=False):
+    m = NpaConfig.growing_2d().replace(state_dims=S, hidden_dims=H, density_grad=dgrad, eps0=0.05)
+    F, Oo = m.perception_dims(), m.update_dims()
+    rng = np.random.default_rng(8)
+    w = {"w1": rng.integers(-3, 4, (H, F)).astype(f32), "b1": rng.integers(-5, 6, H).astype(f32),
+         "w2": rng.integers(-3, 4, (Oo, H)).astype(f32), "b2": rng.integers(-5, 6, Oo).astype(f32)}
+    return m, w
+
+
+def test_mlp_with_integer_weights_is_exact():
+    """forward_update_from_features (crates/burn_automata/src/model.rs:900-940): h = ReLU(b1 +
+    W1 f), u = b2 + W2 h. With small integers every partial sum is exact in float32."""
+    m, w = _int_model()
+    F = m.perception_dims()
+    feats = np.random.default_rng(0).integers(-4, 5, (257, F)).astype(f32)
+    h = np.maximum(feats.astype(np.int64) @ w["w1"].astype(np.int64).T + w["b1"].astype(np.int64), 0)
+    u = h @ w["w2"].astype(np.int64).T + w["b2"].astype(np.int64)
+    assert np.any(feats.astype(np.int64) @ w["w1"].astype(np.int64).T + w["b1"] < 0)  # ReLU active
+    got = O.forward_update_from_features(m, w, feats)
+    np.testing.assert_array_equal(got, u.astype(f32))
+
+
+@pytest.mark.parametrize("equiv", [EquivarianceMode.ParticleDensityAndScale,
+                                   EquivarianceMode.NoEquivariance])
+def test_motion_is_alpha_u_eps_over_one_plus_norm(equiv):
+    """forward_from_features_with_eps (model.rs:867-898) with motion_eps (config.rs:156-162)."""
+    m, w = _int_model()
+    m = m.replace(equivariance=equiv, alpha=0.37)
+    F, d, S = m.perception_dims(), 2, m.state_dims
+    feats = np.random.default_rng(1).integers(-4, 5, (64, F)).astype(f32)
+    u = O.forward_update_from_features(m, w, feats).astype(np.float64)
+    eps = 0.081
+    dx, ds = O.forward_from_features_with_eps(m, w, feats, eps)
+    meps = eps if equiv == EquivarianceMode.ParticleDensityAndScale else m.eps0
+    nrm = np.sqrt(np.sum(u[:, :d] ** 2, axis=1, keepdims=True))
+    assert rel(dx[:, :d], 0.37 * u[:, :d] * meps / (1 + nrm)) < 1e-6
+    assert np.all(dx[:, d:] == 0)
+    np.testing.assert_array_equal(ds, u[:, d:].astype(f32))
+
+
+def test_euler_step_applies_masks_and_boundaries():
+    """euler_step_applies_masks_and_boundaries (lib.rs:359-383)."""
+    ka = KNOWN["euler_step_applies_masks_and_boundaries"]
+    cfg = HashGridConfig.growing_2d()
+    npos, nst = O.euler_step(np.array(ka["positions"], f32), np.array(ka["states"], f32),
+                             np.array(ka["dx"], f32), np.array(ka["ds"], f32), 1, 2, 1, cfg, 1.0,
+                             np.array(ka["mask"], f32))
+    assert npos[0, 0] == ka["expect_pos0_x"] and npos[1, 0] == ka["expect_pos1_x"]
+    assert nst.reshape(-1).tolist() == ka["expect_states"]
+
+
+def test_euler_step_clamps_3d_opacity_logit():
+    """euler_step_clamps_3d_opacity_logit (lib.rs:386-403)."""
+    ka = KNOWN["euler_step_clamps_3d_opacity_logit"]
+    cfg = HashGridConfig.growing_3dgs()
+    for case in ka["cases"]:
+        _, nst = O.euler_step(np.zeros((1, 4), f32), np.array(case["states"], f32),
+                              np.zeros((1, 4), f32), np.array(case["ds"], f32), 1, 1, 4, cfg, 1.0)
+        assert nst.reshape(-1)[3] == case["expect_channel3"]
+
+
+def test_euler_closed_forms():
+    """p + dt dx m over spatial_mem_dims axes (4 in 3D), periodic wrap, s + dt ds m
+    (step.rs:4-55; wrap_position hashgrid.rs:183-193)."""
+    rng = np.random.default_rng(3)
+    n, S = 50, 5
+    pos = rng.uniform(-0.9, 0.9, (n, 4)).astype(f32)
+    st = rng.normal(0, 1, (n, S)).astype(f32)
+    dx = rng.normal(0, 0.2, (n, 4)).astype(f32)
+    ds = rng.normal(0, 1, (n, S)).astype(f32)
+    mask = (rng.uniform(size=n) < 0.5).astype(f32)
+    dt = f32(0.7)
+    cfg2 = HashGridConfig.growing_2d()
+    p2, s2 = O.euler_step(pos, st, dx, ds, 1, n, S, cfg2, float(dt), mask)
+    m = mask[:, None]
+    np.testing.assert_array_equal(p2[:, :2], pos[:, :2] + dt * dx[:, :2] * m)
+    np.testing.assert_array_equal(p2[:, 2:], pos[:, 2:])
+    np.testing.assert_array_equal(s2, st + dt * ds * m)
+    cfg3 = HashGridConfig.growing_3dgs()
+    p3, _ = O.euler_step(pos, st, dx, ds, 1, n, S, cfg3, float(dt), mask)
+    np.testing.assert_array_equal(p3, pos + dt * dx * m)  # all four lanes in 3D
+    tex = HashGridConfig.texture_2d()  # periodic, extent 2.0
+    pw, _ = O.euler_step(np.array([[0.95, -0.95, 0, 0]], f32), np.zeros(1, f32),
+                         np.array([[0.1, -0.1, 0, 0]], f32), np.zeros(1, f32), 1, 1, 1, tex, 1.0)
+    assert pw[0, 0] == pytest.approx(-0.95, abs=1e-6) and pw[0, 1] == pytest.approx(0.95, abs=1e-6)
+
+
+# --------------------------------------------------------------------------------------------
+# step, rollout, mask
+# --------------------------------------------------------------------------------------------
+
+def _small_c1(n=512, seed=42, **model_kw):
+    w = syn.workload("c1", seed=seed, particles=n)
+    if model_kw:
+        w["model"] = w["model"].replace(**model_kw)
+        w["weights"] = syn.seeded_weights(w["model"], seed)
+    return w
+
+
+def test_step_is_perceive_then_mlp_then_euler():
+    """NpaModel::step_cpu (model.rs:768-858): perceive with the model's options and hybrid
+    gradient on, forward_from_features_with_eps(grid eps), euler_step with the mask."""
+    w = _small_c1(400, density_grad=True)
+    m, grid = w["model"], w["grid"]
+    n = w["n"]
+    mask = O.update_mask(1, n, 0.5, 3, 42)
+    out = O.step(m, w["weights"], w["positions"], w["states"], 1, n, grid, 1.0, mask)
+    per = O.perceive_with_options(w["positions"], w["states"], 1, n, m.state_dims, grid,
+                                  m.perception_options())
+    dx, ds = O.forward_from_features_with_eps(m, w["weights"], per.features, grid.eps)
+    npos, nst = O.euler_step(w["positions"], w["states"], dx, ds, 1, n, m.state_dims, grid, 1.0,
+                             mask)
+    np.testing.assert_array_equal(out.next_positions, npos)
+    np.testing.assert_array_equal(out.next_states, nst)
+    np.testing.assert_array_equal(out.density, per.density)
+
+
+def test_scale_equivariant_step_preserves_scaled_rollout():
+    """scale_equivariant_cpu_step_preserves_scaled_rollout
+    (crates/burn_automata/tests/core/equivariance.rs:4-67): 32 particles in a disk of radius
+    0.2, hidden 8, ParticleDensityAndScale, scale 1.7 -> |base - scaled/scale| < 2e-4."""
+    ka = KNOWN["scale_equivariant_cpu_step_preserves_scaled_rollout"]
+    m = NpaConfig.growing_2d().replace(hidden_dims=ka["hidden_dims"],
+                                       equivariance=EquivarianceMode.ParticleDensityAndScale)
+    grid = HashGridConfig.growing_2d()
+    weights = syn.seeded_weights(m, 17)
+    n = ka["particles"]
+    pos = syn.uniform_disk(n, seed=23, radius=ka["radius"])
+    st = syn.normal_states(n, m.state_dims, seed=23, std=0.1)
+    s = ka["scale"]
+    spos = pos.copy()
+    spos[:, :3] *= f32(s)
+    base = O.step(m, weights, pos, st, 1, n, grid, 1.0)
+    scaled = O.step(m, weights, spos, st, 1, n, grid.replace(eps=grid.eps * s), 1.0)
+    tol = ka["tolerance"]
+    assert np.max(np.abs(base.next_positions[:, :2] - scaled.next_positions[:, :2] / f32(s))) < tol
+    assert np.max(np.abs(base.next_states - scaled.next_states)) < tol
+    assert np.max(np.abs(base.next_positions[:, :2] - pos[:, :2])) > 1e-4  # it moved
+
+
+def test_rollout_is_repeated_masked_steps():
+    """run_rollout_from_particles (rollout/mod.rs:240-297) with the device mask schedule:
+    step k uses update_mask(step index k)."""
+    w = _small_c1(256)
+    m, grid, n = w["model"], w["grid"], w["n"]
+    pos, st = w["positions"].copy(), w["states"].copy()
+    for k in range(4):
+        mask = O.update_mask(1, n, 0.5, k, 42)
+        out = O.step(m, w["weights"], pos, st, 1, n, grid, 1.0, mask)
+        pos, st = out.next_positions, out.next_states
+    rpos, rst = O.rollout(m, w["weights"], w["positions"], w["states"], 1, n, grid, 4, 1.0, 0.5, 42)
+    np.testing.assert_array_equal(rpos, pos)
+    np.testing.assert_array_equal(rst, st)
+
+
+def test_mask_hash_matches_reference_cpu_replica():
+    rng = np.random.default_rng(0)
+    for v in list(rng.integers(0, 2 ** 32, 200)) + [0, 1, 61, M32]:
+        assert O.hash_u32(int(v)) == hash_u32_ref(int(v))
+    for p, s, seed in rng.integers(0, 2 ** 32, (100, 3)):
+        assert O.random01(int(p), int(s), int(seed)) == random01_ref(int(p), int(s), int(seed))
+
+
+def test_update_mask_lane_seeds_and_statistics():
+    """gpu_update_mask (common.rs:115-124) with lane seeds gpu_random_seed(seed) ^ lane*N
+    (crates/burn_automata/src/gpu/executor/state.rs:1282-1315)."""
+    B, N, seed = 3, 1000, (7 << 32) | 42
+    base = (seed & M32) ^ (seed >> 32)
+    for step, p in [(0, 0.5), (5, 0.25)]:
+        m = O.update_mask(B, N, p, step, seed)
+        want = [float(random01_ref(i, step, base ^ (b * N)) < p) for b in range(B) for i in range(N)]
+        np.testing.assert_array_equal(m, np.array(want, f32))
+        assert abs(m.mean() - p) < 5 * math.sqrt(p * (1 - p) / m.size)
+    assert np.all(O.update_mask(2, 64, 0.0, 1, 42) == 0)
+    assert np.all(O.update_mask(2, 64, 1.0, 1, 42) == 1)
+
+
+# --------------------------------------------------------------------------------------------
+# decode
+# --------------------------------------------------------------------------------------------
+
+def test_gaussian_decode_known_answers():
+    """splat_and_gaussian_decode_are_shape_stable (lib.rs:406-434) and
+    gaussian_decode_modes_cover_fixed_learned_and_oriented_scale (lib.rs:437-482)."""
+    ka = KNOWN["splat_and_gaussian_decode_are_shape_stable"]
+    S = ka["state_dims"]
+    st = np.zeros(S, f32)
+    st[S - 3:] = ka["tail"]
+    g = O.decode_gaussians_3d(np.zeros((1, 4), f32), st, S, GaussianDecodeConfig())
+    assert g["spherical_harmonic"].shape == (1, 1, 3)
+    np.testing.assert_array_equal(g["spherical_harmonic"][0, 0], np.array(ka["expect_sh"], f32))
+    assert g["scale_opacity"][0, 3] > 0
+
+    kb = KNOWN["gaussian_decode_modes_cover_fixed_learned_and_oriented_scale"]
+    pos = np.array([kb["position"]], f32)
+    learned = np.zeros(8, f32)
+    for i, v in kb["learned_states"].items():
+        learned[int(i)] = v
+    g = O.decode_gaussians_3d(pos, learned, 8, GaussianDecodeConfig(
+        mode=GaussianDecodeMode.GaussianSh0LearnedScale, sigma=0.01, opacity_scale=1.0))
+    assert g["spherical_harmonic"].shape == (1, 1, 3)
+    assert g["spherical_harmonic"][0, 0].tolist() == kb["expect_learned_sh"]
+    assert g["scale_opacity"][0, 0] > 0.01 and g["scale_opacity"][0, 3] > 0.5
+    assert g["rotation"][0].tolist() == [1.0, 0.0, 0.0, 0.0]
+    oriented = np.zeros(20, f32)
+    for i, v in kb["oriented_states"].items():
+        oriented[int(i)] = v
+    g = O.decode_gaussians_3d(pos, oriented, 20, GaussianDecodeConfig(
+        mode=GaussianDecodeMode.GaussianSh0Oriented, sh_degree=1))
+    assert g["spherical_harmonic"].shape == (1, 4, 3)
+    assert abs(g["rotation"][0, 0] - 1.0) <= 1e-6
+    assert np.isfinite(g["scale_opacity"][0, 0])
+
+
+def test_fixed_decode_closed_form():
+    """GaussianSh0FixedScale (gaussian.rs:53-223): colour clamp(tail + 0.5, 0, 1), scale
+    clamp(sigma, min, max) on three axes, opacity clamp(opacity_scale, min, max), identity
+    rotation, position passed through."""
+    rng = np.random.default_rng(2)
+    n, S = 40, 9
+    pos = rng.uniform(-1, 1, (n, 4)).astype(f32)
+    st = rng.normal(0, 0.6, (n, S)).astype(f32)
+    cfg = GaussianDecodeConfig(sigma=0.5)
+    g = O.decode_gaussians_3d(pos, st, S, cfg)
+    np.testing.assert_array_equal(g["spherical_harmonic"][:, 0, :],
+                                  np.clip(st[:, S - 3:] + f32(0.5), 0, 1))
+    np.testing.assert_array_equal(g["position_visibility"][:, :3], pos[:, :3])
+    assert np.all(g["scale_opacity"][:, :3] == f32(cfg.max_scale))
+    assert np.all(g["scale_opacity"][:, 3] == f32(cfg.opacity_scale))
+    assert np.all(g["rotation"] == np.array([1, 0, 0, 0], f32))
+
+
+# --------------------------------------------------------------------------------------------
+# splat
+# --------------------------------------------------------------------------------------------
+
+def test_splat_shape_known_answer():
+    """splat_and_gaussian_decode_are_shape_stable (lib.rs:406-418)."""
+    img = O.splat_particles_2d(np.zeros((1, 4), f32), np.array([[1, 0, 0]], f32),
+                               Splat2dConfig(image_size=8))
+    assert img.shape == (64, 4) and np.any(img[:, 3] > 0)
+
+
+@pytest.mark.parametrize("y_up", [True, False])
+def test_single_particle_splat_is_a_normalised_gaussian(y_up):
+    """splat_particles_2d (splat.rs:30-93): one particle -> exp(-r^2/2s^2) over the
+    (2 ceil(5s)+1)^2 footprint, normalised to norm_scale, colour times alpha."""
+    size, sigma_w = 64, 2.3  # sigma in pixels of a (hi - lo) / size grid
+    cfg = Splat2dConfig(image_size=size, sigma=sigma_w, y_up=y_up, pixel_size=2.0 / size)
+    p = np.array([[0.131, -0.377, 0, 0]], f32)
+    c = np.array([[0.2, 0.7, 1.0]], f32)
+    img = O.splat_particles_2d(p, c, cfg).reshape(size, size, 4).astype(np.float64)
+    sig = sigma_w * size * cfg.pixel_size / (cfg.hi - cfg.lo)
+    rad = max(math.ceil(5 * sig), 1)
+    px = (0.131 + 1) / 2 * (size - 1)
+    py = (-0.377 + 1) / 2 * (size - 1)
+    if y_up:
+        py = (size - 1) - py
+    bx, by = math.floor(px), math.floor(py)
+    want = np.zeros((size, size))
+    for oy in range(-rad, rad + 1):
+        for ox in range(-rad, rad + 1):
+            dx, dy = ox - (px - bx), oy - (py - by)
+            want[by + oy, bx + ox] = math.exp(-(dx * dx + dy * dy) / (2 * sig * sig))
+    norm = (size * cfg.pixel_size / (cfg.hi - cfg.lo)) ** 2
+    want = want / want.sum() * norm
+    assert rel(img[:, :, 3], want) < 2e-5
+    for ch in range(3):
+        assert rel(img[:, :, ch], want * float(c[0, ch])) < 2e-5
+    assert img[:, :, 3].sum() == pytest.approx(norm, rel=1e-5)
+
+
+def test_splat_is_additive_and_clips_at_the_border():
+    rng = np.random.default_rng(6)
+    n = 300
+    pos = np.zeros((n, 4), f32)
+    pos[:, :2] = rng.uniform(-1.05, 1.05, (n, 2))
+    col = rng.uniform(0, 1, (n, 3)).astype(f32)
+    cfg = Splat2dConfig(image_size=48, sigma=1.4, pixel_size=2.0 / 48)
+    a = O.splat_particles_2d(pos[:150], col[:150], cfg).astype(np.float64)
+    b = O.splat_particles_2d(pos[150:], col[150:], cfg).astype(np.float64)
+    ab = O.splat_particles_2d(pos, col, cfg)
+    assert rel(ab, a + b) < 1e-6
+    # a particle outside the image keeps only its in-bounds weights, still normalised to 1
+    one = O.splat_particles_2d(np.array([[0.99, 0.99, 0, 0]], f32), np.ones((1, 3), f32), cfg)
+    norm = (48 * cfg.pixel_size / 2.0) ** 2
+    assert one[:, 3].sum() == pytest.approx(norm, rel=1e-5)

@@ -1,0 +1,67 @@
+"""Mutation check of the oracle's pinning tests.
+
+Each mutant plants one plausible mistake in a copy of oracle/npa_oracle.c (a dropped term, a
+flipped sign, a wrong exponent, index or loop order, a broken hash constant, an unstable sort),
+builds it with the oracle's own flags and runs tests/test_oracle.py against it through
+NPA_ORACLE_LIB. Every mutant must make that suite fail: a mistake that no pinning test notices
+would leave the oracle - and so every GPU parity claim that rests on it - unchecked.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SRC = os.path.join(ROOT, "oracle", "npa_oracle.c")
+CFLAGS = ["-O2", "-std=c11", "-fPIC", "-fopenmp", "-ffp-contract=off", "-fno-fast-math", "-shared"]
+
+# name -> (text in npa_oracle.c, replacement); the text must occur in the source
+MUTANTS = {
+    "radius_not_strict": ("if (r2 < eps2) nbuf_push", "if (r2 <= eps2) nbuf_push"),
+    "cell_walk_dx_outer": (
+        "for (int dy = -1; dy <= 1; ++dy)\n            for (int dx = -1; dx <= 1; ++dx) {\n"
+        "                int64_t coords[3] = {center[0] + dx",
+        "for (int dx = -1; dx <= 1; ++dx)\n            for (int dy = -1; dy <= 1; ++dy) {\n"
+        "                int64_t coords[3] = {center[0] + dx"),
+    "delta_sign": ("float v = rhs[a] - lhs[a];", "float v = lhs[a] - rhs[a];"),
+    "unstable_bins": ("uint32_t dst = counts[bin]++;",
+                      "uint32_t dst = bin_offsets[bin + 1] - 1 - (counts[bin]++ - bin_offsets[bin]);"),
+    "mix_multiplier": ("x *= 0x7feb352du;", "x *= 0x7feb352fu;"),
+    "poly6_exponent": ("4.0f / (PI_F * powi_f32(cfg->eps, 8))", "4.0f / (PI_F * powi_f32(cfg->eps, 6))"),
+    "spiky_cubed": ("3.0f * (t * t) / r;", "3.0f * (t * t * t) / r;"),
+    "blur_volume_dropped": ("blur_row[c] += sj[c] * smooth * volume_j;", "blur_row[c] += sj[c] * smooth;"),
+    "gradient_diff_sign": ("float diff = sj[c] - si[c];\n                    for (uint32_t a = 0; a < d; ++a) grad_row",
+                           "float diff = si[c] - sj[c];\n                    for (uint32_t a = 0; a < d; ++a) grad_row"),
+    "moment_uncorrected": ("pg[c * d + k] * inv[k * d + o]", "pg[c * d + k] * (k == o ? 1.0f : 0.0f)"),
+    "density_grad_power": ("powi_f32(cfg->eps / eps0, 1 + (int)cfg->dim)", "powi_f32(cfg->eps / eps0, (int)cfg->dim)"),
+    "log1p_as_log": ("float scale = log1pf(norm) / norm;", "float scale = logf(1.0f + norm) / norm;"),
+    "mlp_bias_dropped": ("float sum = w->b1[h];", "float sum = 0.0f;"),
+    "relu_dropped": ("hidden[h] = fmaxf(sum, 0.0f);", "hidden[h] = sum;"),
+    "motion_norm_squared": ("meps / (1.0f + norm);", "meps / (1.0f + norm * norm);"),
+    "state_mask_ignored": ("float next = s[c] + dt * dsr[c] * m;", "float next = s[c] + dt * dsr[c];"),
+    "mem_dims_3d": ("return cfg->dim == 3 ? 4 : 2;", "return cfg->dim == 3 ? 3 : 2;"),
+    "clamp_channel": ("(c == 3 || (S > 8 && c == 8))", "(c == 4 || (S > 8 && c == 8))"),
+    "mask_hash_multiplier": ("x = x * 0x27d4eb2du;", "x = x * 0x27d4eb2fu;"),
+    "decode_colour_offset": ("clamp_f32(s[base + ch] + 0.5f, 0.0f, 1.0f);", "clamp_f32(s[base + ch] + 0.4f, 0.0f, 1.0f);"),
+    "splat_radius": ("ceilf(5.0f * sigma)", "ceilf(3.0f * sigma)"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(MUTANTS))
+def test_planted_mistake_is_caught(name, tmp_path):
+    old, new = MUTANTS[name]
+    src = open(SRC).read()
+    assert old in src, f"mutation site of {name} no longer in the oracle source"
+    mutant = tmp_path / "npa_oracle_mutant.c"
+    mutant.write_text(src.replace(old, new, 1))
+    lib = tmp_path / "libnpa_oracle_mutant.so"
+    subprocess.run(["gcc", *CFLAGS, "-I", os.path.join(ROOT, "oracle"), "-I",
+                    os.path.join(ROOT, "include"), "-o", str(lib), str(mutant), "-lm"], check=True)
+    env = dict(os.environ, NPA_ORACLE_LIB=str(lib), OMP_NUM_THREADS="2")
+    r = subprocess.run([sys.executable, "-m", "pytest", "-x", "-q", "-p", "no:cacheprovider",
+                        os.path.join(ROOT, "tests", "test_oracle.py")], cwd=ROOT, env=env,
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=600)
+    assert r.returncode == 1, f"mutant {name} survived the pinning tests:\n{r.stdout[-2000:]}"
