@@ -286,8 +286,10 @@ struct PerceiveStage {
 
 // Second neighbour pass + normalisation + feature row, L lanes per target, each lane owning
 // CPL = SM / L state channels. The L lanes test a chunk's candidates round-robin and OR their
-// accept masks; then every lane walks the target's accepted candidates in ascending order
-// (the reference's order), recomputing the pair scalars and updating its own channels' sums.
+// accept masks; then the target's accepted candidates are consumed in rounds of L: lane q
+// computes the pair scalars (poly6, volume, spiky gradients) of the round's q-th candidate and
+// every lane applies the round's candidates in ascending order (the reference's order) to its
+// own channels, with the scalars broadcast inside the lane group.
 // MODE 0: padded feature rows, feature-major (features[k * T + s]) for the MLP kernel.
 // MODE 1: the perceive_with_options outputs in original particle order.
 template <int D, int SM, int MODE>

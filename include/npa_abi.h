@@ -199,7 +199,7 @@ npa_status npa_euler_step(npa_context* ctx, const float* positions, const float*
                           float* out_positions, float* out_states);
 
 /* Replaces NpaModel::step_cpu (crates/burn_automata/src/model.rs:768-858): one fused
- * rollout step. update_mask may be NULL. density/dx/ds outputs are optional (NULL). */
+ * rollout step. update_mask may be NULL (all ones); out_density may be NULL. */
 npa_status npa_step(npa_context* ctx, const float* positions, const float* states,
                     uint32_t batch_size, uint32_t particle_count,
                     const npa_grid_cfg* grid, const npa_model_cfg* model,
