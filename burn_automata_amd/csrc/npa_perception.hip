@@ -277,19 +277,43 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
     }
 }
 
-template <int D, int SM>
-struct PerceiveStage {
-    NbrStage<D> nb;
-    float vol[kChunk];
-    float st[kChunk * (SM + 4)];  // 16-byte aligned rows
+// Per-wave accepted-neighbour lists of the second pass. Entry = (chunk id << 6) | k, the k-th
+// candidate of the chunk whose first sorted slot is chunk_base[chunk id]; entries of a target are
+// appended in visit order (cells dz, dy, dx; slots ascending), so walking a list front to back
+// is the reference's neighbour order. LDS: kListBytes per wave for any targets-per-item.
+constexpr int kListBytes = 8192;
+constexpr int kMaxChunks = 64;
+
+template <int TPI>
+struct PerceiveLists {
+    static constexpr int CAP = kListBytes / (2 * TPI);
+    uint16_t entry[CAP][TPI];
+    uint32_t chunk_base[kMaxChunks];
 };
 
+// Bits k of a 64-bit chunk mask with k % L == q.
+template <int L>
+__device__ __forceinline__ uint64_t residue_mask(uint32_t q) {
+    if constexpr (L == 1) return ~0ull;
+    else if constexpr (L == 2) return 0x5555555555555555ull << q;
+    else return 0x1111111111111111ull << q;
+}
+
 // Second neighbour pass + normalisation + feature row, L lanes per target, each lane owning
-// CPL = SM / L state channels. The L lanes test a chunk's candidates round-robin and OR their
-// accept masks; then the target's accepted candidates are consumed in rounds of L: lane q
-// computes the pair scalars (poly6, volume, spiky gradients) of the round's q-th candidate and
-// every lane applies the round's candidates in ascending order (the reference's order) to its
-// own channels, with the scalars broadcast inside the lane group.
+// CPL = SM / L state channels.
+// Phase A: for each neighbour bin of the target's cell (reference order), the L lanes of a
+//   target test the bin's candidates round-robin straight from the sorted records, OR their
+//   accept masks and append the accepted candidates to the target's list in LDS.
+// Phase B (when a list would overflow, and at the end): the lists are consumed in rounds of L
+//   entries: lane q computes the pair scalars (poly6, volume, spiky gradients) of the round's
+//   q-th entry, and every lane applies the round's entries in list order to its own channels,
+//   with the scalars and the candidate slot broadcast inside the lane group and the candidate's
+//   state channels read from the sorted state rows. Rounds span all of a target's neighbour
+//   bins, so the targets of a wave stay busy for about the same number of rounds.
+// Padding entries (a short last round, a target with fewer entries than the wave's longest
+// list) use the target itself with zero weights; the self pair's gradient terms and those of
+// coincident particles are zero as well. Zero terms leave every sum unchanged: each sum starts
+// at +0.0 and so never holds -0.0.
 // MODE 0: padded feature rows, feature-major (features[k * T + s]) for the MLP kernel.
 // MODE 1: the perceive_with_options outputs in original particle order.
 template <int D, int SM, int MODE>
@@ -304,8 +328,10 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                                                  float* __restrict__ sfeatures, StepIO io) {
     constexpr int L = LanesPerTarget<SM>::L;
     constexpr int CPL = LanesPerTarget<SM>::CPL;
-    constexpr int RS = SM + 4;
-    __shared__ PerceiveStage<D, SM> st;
+    constexpr int TPI = 64 / L;
+    using Lists = PerceiveLists<TPI>;
+    constexpr uint32_t CAP = Lists::CAP;
+    __shared__ Lists lists;
     const uint32_t lane = threadIdx.x;
     const uint32_t t = lane / L, q = lane % L;
     const uint32_t c0 = q * CPL;  // first channel of this lane
@@ -313,6 +339,7 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
     const bool branch_a = P.state_grad && P.density_grad;
     const bool want_sg = P.state_grad != 0, want_dg = P.density_grad != 0;
     const bool want_m = want_sg && P.hybrid;
+    const uint64_t my_residue = residue_mask<L>(q);
     for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
         const uint2 item = wl[it];
         const bool active = t < item.y;
@@ -334,143 +361,210 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
 #pragma unroll
         for (int k = 0; k < D * D; ++k) mom[k] = 0.0f;
 
-        for_each_group_chunk<D>(
-            P.g, b, active, ci, bo, lane,
-            [&](uint32_t base, uint32_t m) {
-                stage_records<D>(st.nb, srec, scoord, base, m, lane);
-                if (lane < m) {
-                    st.vol[lane] = svol[base + lane];
-                    const float4* src = reinterpret_cast<const float4*>(sstate + (uint64_t)(base + lane) * SM);
-                    float4* dst = reinterpret_cast<float4*>(st.st + lane * RS);
-#pragma unroll
-                    for (int k = 0; k < SM / 4; ++k) dst[k] = src[k];
+        uint32_t cnt = 0;      // entries in this target's list (same in the L lanes of a target)
+        uint32_t nchunks = 0;  // chunk ids in use (wave-uniform)
+
+        // Phase B over the current lists.
+        auto flush = [&]() {
+            __syncthreads();  // list writes of every lane are visible
+            for (uint32_t r = 0;; ++r) {
+                const uint32_t e0 = r * L;
+                if (!__ballot(active && e0 < cnt)) break;
+                const uint32_t e = e0 + q;
+                const bool has = active && e < cnt;
+                uint32_t slot = s;
+                if (has) {
+                    const uint32_t en = lists.entry[e][t];
+                    slot = lists.chunk_base[en >> 6] + (en & 63u);
                 }
-            },
-            [&](uint32_t base, uint32_t m, int64_t n0, int64_t n1, int64_t n2, bool in_group) {
-                uint64_t acc = 0;
-                for (uint32_t k0 = 0; k0 < m; k0 += L) {
-                    const uint32_t k = k0 + q;
-                    if (k >= m) continue;
-                    const float4 r = st.nb.rec[k];
-                    if (P.g.mode == 1 && !staged_coords_match<D>(st.nb, k, r, n0, n1, n2)) continue;
-                    const float d0 = delta_axis(pi[0], r.x, 0, P.g);
-                    const float d1 = delta_axis(pi[1], r.y, 1, P.g);
-                    float r2 = d0 * d0;
-                    r2 += d1 * d1;
+                // the round's slots and their state channels (loads issued before the scalars)
+                uint32_t rs[L];
+                float sv[L][CPL];
+                auto bslot = [&](auto J) {
+                    return (uint32_t)__float_as_int(group_bcast<L, decltype(J)::value>(__int_as_float((int)slot)));
+                };
+                rs[0] = bslot(std::integral_constant<int, 0>{});
+                if constexpr (L >= 2) rs[1] = bslot(std::integral_constant<int, 1>{});
+                if constexpr (L >= 4) {
+                    rs[2] = bslot(std::integral_constant<int, 2>{});
+                    rs[3] = bslot(std::integral_constant<int, 3>{});
+                }
+#pragma unroll
+                for (int j = 0; j < L; ++j) {
+                    const float* rowp = sstate + (uint64_t)rs[j] * SM + c0;
+                    if constexpr (CPL % 4 == 0) {  // 16-byte aligned channel slices
+                        const float4* row = reinterpret_cast<const float4*>(rowp);
+#pragma unroll
+                        for (int v = 0; v < CPL / 4; ++v) {
+                            const float4 x = row[v];
+                            sv[j][4 * v + 0] = x.x;
+                            sv[j][4 * v + 1] = x.y;
+                            sv[j][4 * v + 2] = x.z;
+                            sv[j][4 * v + 3] = x.w;
+                        }
+                    } else {  // CPL = 6 (SM = 24): 8-byte aligned slices
+                        static_assert(CPL % 2 == 0, "channel slices are whole float2s");
+                        const float2* row = reinterpret_cast<const float2*>(rowp);
+#pragma unroll
+                        for (int v = 0; v < CPL / 2; ++v) {
+                            const float2 x = row[v];
+                            sv[j][2 * v + 0] = x.x;
+                            sv[j][2 * v + 1] = x.y;
+                        }
+                    }
+                }
+                // pair scalars of this lane's entry
+                float smooth = 0.0f, vol = 0.0f, d[3] = {0.0f, 0.0f, 0.0f};
+                float vg[D], dgv[D];
+#pragma unroll
+                for (int a = 0; a < D; ++a) {
+                    vg[a] = 0.0f;
+                    dgv[a] = 0.0f;
+                }
+                if (has) {
+                    const float4 rj = srec[slot];
+                    const float vj = svol[slot];
+                    d[0] = delta_axis(pi[0], rj.x, 0, P.g);
+                    d[1] = delta_axis(pi[1], rj.y, 1, P.g);
+                    float r2 = d[0] * d[0];
+                    r2 += d[1] * d[1];
                     if constexpr (D == 3) {
-                        const float d2 = delta_axis(pi[2], r.z, 2, P.g);
-                        r2 += d2 * d2;
+                        d[2] = delta_axis(pi[2], rj.z, 2, P.g);
+                        r2 += d[2] * d[2];
                     }
-                    if (in_group && r2 < P.g.eps2) acc |= 1ull << k;
-                }
-                acc = group_or<L>(acc);
-                // Rounds of L accepted candidates: lane q computes the pair scalars of the
-                // round's q-th candidate, then every lane applies the round's candidates in
-                // ascending order to its own channels (scalars broadcast within the lane group).
-                // A missing candidate (short last round), the self pair and coincident
-                // particles contribute zeros, which leave every sum unchanged: each sum starts
-                // at +0.0 and so never holds -0.0.
-                while (acc) {
-                    const uint64_t round0 = acc;
-                    uint64_t mine = acc;
-#pragma unroll
-                    for (int j = 0; j < L - 1; ++j)
-                        if (j < (int)q) mine &= mine - 1;
-#pragma unroll
-                    for (int j = 0; j < L; ++j) acc &= acc - 1;
-                    const bool has = mine != 0;
-                    // a lane without a candidate points at the round's first (accepted) one, so
-                    // its zero-weight terms read a neighbour's row, never an unrelated one
-                    const uint32_t k = (uint32_t)__builtin_ctzll(has ? mine : round0);
-                    float smooth = 0.0f, vol = 0.0f, d[3] = {0.0f, 0.0f, 0.0f};
-                    float vg[D], dgv[D];
-#pragma unroll
-                    for (int a = 0; a < D; ++a) {
-                        vg[a] = 0.0f;
-                        dgv[a] = 0.0f;
-                    }
-                    if (has) {
-                        const float4 r = st.nb.rec[k];
-                        d[0] = delta_axis(pi[0], r.x, 0, P.g);
-                        d[1] = delta_axis(pi[1], r.y, 1, P.g);
-                        float r2 = d[0] * d[0];
-                        r2 += d[1] * d[1];
-                        if constexpr (D == 3) {
-                            d[2] = delta_axis(pi[2], r.z, 2, P.g);
-                            r2 += d[2] * d[2];
-                        }
-                        vol = st.vol[k];
-                        smooth = poly6(r2, P.g);
-                        if (base + k != s && r2 > 0.0f) {  // spiky_gradient_kernel kernels.rs:79-96
-                            const float rr = sqrtf(r2);
-                            const float tt = P.g.eps - rr;
-                            if (want_dg) {
-                                const float mag = 1.0f * P.g.k5 * 3.0f * (tt * tt) / rr;
-#pragma unroll
-                                for (int a = 0; a < D; ++a) dgv[a] = mag * d[a];
-                            }
-                            if (want_sg) {
-                                const float mag = vol * P.g.k5 * 3.0f * (tt * tt) / rr;
-#pragma unroll
-                                for (int a = 0; a < D; ++a) vg[a] = mag * d[a];
-                            }
-                        }
-                    }
-                    const float w = smooth * vol;  // blur_state weight (density-grad-off branch)
-                    // the round's candidates in ascending order
-                    auto apply = [&](float c_smooth, float c_vol, float c_w, const float* c_d, const float* c_vg,
-                                     const float* c_dg, uint32_t c_k) {
-                        const float* sj = st.st + c_k * RS + c0;
-                        float sv[CPL];
-#pragma unroll
-                        for (int c = 0; c < CPL; ++c) sv[c] = sj[c];
-                        if (branch_a) {  // second_pass_particle forward.rs:263-270
-#pragma unroll
-                            for (int c = 0; c < CPL; ++c) blur[c] += sv[c] * c_smooth * c_vol;
-                        } else {  // blur_state forward.rs:174-180
-#pragma unroll
-                            for (int c = 0; c < CPL; ++c) blur[c] += sv[c] * c_w;
-                        }
+                    vol = vj;
+                    smooth = poly6(r2, P.g);
+                    if (slot != s && r2 > 0.0f) {  // spiky_gradient_kernel kernels.rs:79-96
+                        const float rr = sqrtf(r2);
+                        const float tt = P.g.eps - rr;
                         if (want_dg) {
+                            const float mag = 1.0f * P.g.k5 * 3.0f * (tt * tt) / rr;
 #pragma unroll
-                            for (int a = 0; a < D; ++a) dg[a] += c_dg[a];
+                            for (int a = 0; a < D; ++a) dgv[a] = mag * d[a];
                         }
                         if (want_sg) {
+                            const float mag = vol * P.g.k5 * 3.0f * (tt * tt) / rr;
 #pragma unroll
-                            for (int c = 0; c < CPL; ++c) {
-                                const float diff = sv[c] - si[c];
-#pragma unroll
-                                for (int a = 0; a < D; ++a) grad[c * D + a] += diff * c_vg[a];
-                            }
-                            if (want_m) {
-#pragma unroll
-                                for (int ra = 0; ra < D; ++ra)
-#pragma unroll
-                                    for (int ca = 0; ca < D; ++ca) mom[ra * D + ca] += c_d[ra] * c_vg[ca];
-                            }
+                            for (int a = 0; a < D; ++a) vg[a] = mag * d[a];
                         }
-                    };
-                    auto round_step = [&](auto J) {
-                        constexpr int j = decltype(J)::value;
-                        float b_d[D], b_vg[D], b_dg[D];
-#pragma unroll
-                        for (int a = 0; a < D; ++a) {
-                            b_d[a] = group_bcast<L, j>(d[a]);
-                            b_vg[a] = group_bcast<L, j>(vg[a]);
-                            b_dg[a] = group_bcast<L, j>(dgv[a]);
-                        }
-                        const uint32_t b_k = (uint32_t)__float_as_int(group_bcast<L, j>(__int_as_float((int)k)));
-                        apply(group_bcast<L, j>(smooth), group_bcast<L, j>(vol), group_bcast<L, j>(w), b_d, b_vg,
-                              b_dg, b_k);
-                    };
-                    round_step(std::integral_constant<int, 0>{});
-                    if constexpr (L >= 2) round_step(std::integral_constant<int, 1>{});
-                    if constexpr (L >= 4) {
-                        round_step(std::integral_constant<int, 2>{});
-                        round_step(std::integral_constant<int, 3>{});
                     }
                 }
-            });
+                const float w = smooth * vol;  // blur_state weight (density-grad-off branch)
+                // the round's entries in list order
+                auto round_step = [&](auto J) {
+                    constexpr int j = decltype(J)::value;
+                    if (branch_a) {  // second_pass_particle forward.rs:263-270
+                        const float c_smooth = group_bcast<L, j>(smooth), c_vol = group_bcast<L, j>(vol);
+#pragma unroll
+                        for (int c = 0; c < CPL; ++c) blur[c] += sv[j][c] * c_smooth * c_vol;
+                    } else {  // blur_state forward.rs:174-180
+                        const float c_w = group_bcast<L, j>(w);
+#pragma unroll
+                        for (int c = 0; c < CPL; ++c) blur[c] += sv[j][c] * c_w;
+                    }
+                    if (want_dg) {
+#pragma unroll
+                        for (int a = 0; a < D; ++a) dg[a] += group_bcast<L, j>(dgv[a]);
+                    }
+                    if (want_sg) {
+                        float c_vg[D];
+#pragma unroll
+                        for (int a = 0; a < D; ++a) c_vg[a] = group_bcast<L, j>(vg[a]);
+#pragma unroll
+                        for (int c = 0; c < CPL; ++c) {
+                            const float diff = sv[j][c] - si[c];
+#pragma unroll
+                            for (int a = 0; a < D; ++a) grad[c * D + a] += diff * c_vg[a];
+                        }
+                        if (want_m) {
+                            // only the upper triangle: safe_inverse_symmetric reads no other entry
+#pragma unroll
+                            for (int ra = 0; ra < D; ++ra) {
+                                const float c_d = group_bcast<L, j>(d[ra]);
+#pragma unroll
+                                for (int ca = ra; ca < D; ++ca) mom[ra * D + ca] += c_d * c_vg[ca];
+                            }
+                        }
+                    }
+                };
+                round_step(std::integral_constant<int, 0>{});
+                if constexpr (L >= 2) round_step(std::integral_constant<int, 1>{});
+                if constexpr (L >= 4) {
+                    round_step(std::integral_constant<int, 2>{});
+                    round_step(std::integral_constant<int, 3>{});
+                }
+            }
+            __syncthreads();  // every lane has read the lists before they are refilled
+            cnt = 0;
+            nchunks = 0;
+        };
+
+        // Phase A: coordinate groups of the item, then the group's neighbour bins in order.
+        uint64_t pending = __ballot(active);
+        while (pending) {
+            const int leader = __ffsll((unsigned long long)pending) - 1;
+            const int l0 = readlane_i(ci[0], leader), l1 = readlane_i(ci[1], leader);
+            const int l2 = D == 3 ? readlane_i(ci[2], leader) : 0;
+            const bool same = active && ci[0] == l0 && ci[1] == l1 && (D == 2 || ci[2] == l2);
+            const uint64_t group = __ballot(same) & pending;
+            pending &= ~group;
+            const bool in_group = (group >> lane) & 1ull;
+            constexpr int ZLO = D == 3 ? -1 : 0, ZHI = D == 3 ? 1 : 0;
+            for (int dz = ZLO; dz <= ZHI; ++dz)
+                for (int dy = -1; dy <= 1; ++dy)
+                    for (int dx = -1; dx <= 1; ++dx) {
+                        const int64_t n0 = (int64_t)l0 + dx, n1 = (int64_t)l1 + dy, n2 = (int64_t)l2 + dz;
+                        uint32_t cell;
+                        if (!cell_index(n0, n1, n2, P.g, &cell)) continue;
+                        const uint64_t bin = (uint64_t)b * P.g.cells + cell;
+                        const uint32_t beg = bo[bin], end = bo[bin + 1];
+                        for (uint32_t base = beg; base < end; base += kChunk) {
+                            const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
+                            uint64_t acc = 0;
+#pragma unroll 4
+                            for (int i = 0; i < kChunk / L; ++i) {
+                                const uint32_t k = q + (uint32_t)(i * L);
+                                if (k < m) {
+                                    const float4 r = srec[base + k];
+                                    bool ok = in_group;
+                                    if (P.g.mode == 1) {
+                                        if constexpr (D == 2) {
+                                            ok = ok && (int64_t)__float_as_int(r.z) == n0 &&
+                                                 (int64_t)__float_as_int(r.w) == n1;
+                                        } else {
+                                            const int4 cj = scoord[base + k];
+                                            ok = ok && (int64_t)cj.x == n0 && (int64_t)cj.y == n1 &&
+                                                 (int64_t)cj.z == n2;
+                                        }
+                                    }
+                                    const float d0 = delta_axis(pi[0], r.x, 0, P.g);
+                                    const float d1 = delta_axis(pi[1], r.y, 1, P.g);
+                                    float r2 = d0 * d0;
+                                    r2 += d1 * d1;
+                                    if constexpr (D == 3) {
+                                        const float d2 = delta_axis(pi[2], r.z, 2, P.g);
+                                        r2 += d2 * d2;
+                                    }
+                                    if (ok && r2 < P.g.eps2) acc |= 1ull << k;
+                                }
+                            }
+                            acc = group_or<L>(acc);
+                            const uint32_t add = (uint32_t)__popcll(acc);
+                            if (__ballot(cnt + add > CAP) || nchunks == (uint32_t)kMaxChunks) flush();
+                            if (lane == 0) lists.chunk_base[nchunks] = base;
+                            uint64_t mine = acc & my_residue;
+                            while (mine) {
+                                const uint32_t k = (uint32_t)__builtin_ctzll(mine);
+                                mine &= mine - 1;
+                                const uint32_t pos = cnt + (uint32_t)__popcll(acc & ((1ull << k) - 1ull));
+                                lists.entry[pos][t] = (uint16_t)((nchunks << 6) | k);
+                            }
+                            cnt += add;
+                            ++nchunks;
+                        }
+                    }
+        }
+        flush();
         if (!active) continue;
 
         if (want_sg) {
