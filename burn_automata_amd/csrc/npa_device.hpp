@@ -119,20 +119,22 @@ __device__ __forceinline__ uint32_t cell_of_coords(const int64_t c[3], const Gri
 }
 
 // neighbor_delta  hashgrid.rs:165-181, component a.
+// Branch-free: both wrapped candidates are computed and one is selected (same values as the
+// reference's if / else-if, NaN included).
 __device__ __forceinline__ float delta_axis(float pi, float pj, int a, const GridParams& g) {
-    float v = pj - pi;
-    if (g.boundary == 0) {
-        if (v > g.half[a]) v -= g.extent[a];
-        else if (v < -g.half[a]) v += g.extent[a];
+    const float v = pj - pi;
+    if (g.boundary == 0) {  // wave-uniform
+        const float up = v - g.extent[a], dn = v + g.extent[a];
+        return v > g.half[a] ? up : (v < -g.half[a] ? dn : v);
     }
     return v;
 }
 
 // smoothing_poly6_kernel  crates/burn_automata_kernels/src/reference/kernels.rs:51-58
 __device__ __forceinline__ float poly6(float r2, const GridParams& g) {
-    if (r2 >= g.eps2) return 0.0f;
-    float x = g.eps2 - r2;
-    return g.k6 * x * x * x;
+    const float x = g.eps2 - r2;
+    const float w = g.k6 * x * x * x;
+    return r2 >= g.eps2 ? 0.0f : w;
 }
 
 // RecipFinite::recip_finite  kernels.rs:146-154

@@ -372,11 +372,12 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                 if (!__ballot(active && e0 < cnt)) break;
                 const uint32_t e = e0 + q;
                 const bool has = active && e < cnt;
-                uint32_t slot = s;
-                if (has) {
-                    const uint32_t en = lists.entry[e][t];
-                    slot = lists.chunk_base[en >> 6] + (en & 63u);
-                }
+                // entry read at a clamped index; the slot of a lane without an entry is its target
+                const uint32_t en = lists.entry[has ? e : 0u][t];
+                const uint32_t cand = lists.chunk_base[(en >> 6) & (uint32_t)(kMaxChunks - 1)] + (en & 63u);
+                const uint32_t slot = has ? cand : s;
+                const float4 rj = srec[slot];
+                const float vj = svol[slot];
                 // the round's slots and their state channels (loads issued before the scalars)
                 uint32_t rs[L];
                 float sv[L][CPL];
@@ -413,41 +414,38 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                         }
                     }
                 }
-                // pair scalars of this lane's entry
-                float smooth = 0.0f, vol = 0.0f, d[3] = {0.0f, 0.0f, 0.0f};
+                // pair scalars of this lane's entry, branch-free; a lane without an entry (or the
+                // self pair / a coincident particle for the gradients) selects zeros
+                float d[3];
+                d[0] = delta_axis(pi[0], rj.x, 0, P.g);
+                d[1] = delta_axis(pi[1], rj.y, 1, P.g);
+                d[2] = 0.0f;
+                float r2 = d[0] * d[0];
+                r2 += d[1] * d[1];
+                if constexpr (D == 3) {
+                    d[2] = delta_axis(pi[2], rj.z, 2, P.g);
+                    r2 += d[2] * d[2];
+                }
+                const float smooth = has ? poly6(r2, P.g) : 0.0f;
+                const float vol = has ? vj : 0.0f;
+                const bool gok = has && slot != s && r2 > 0.0f;  // spiky_gradient_kernel kernels.rs:79-96
+                const float rr = sqrtf(r2);
+                const float tt = P.g.eps - rr;
                 float vg[D], dgv[D];
 #pragma unroll
                 for (int a = 0; a < D; ++a) {
                     vg[a] = 0.0f;
                     dgv[a] = 0.0f;
                 }
-                if (has) {
-                    const float4 rj = srec[slot];
-                    const float vj = svol[slot];
-                    d[0] = delta_axis(pi[0], rj.x, 0, P.g);
-                    d[1] = delta_axis(pi[1], rj.y, 1, P.g);
-                    float r2 = d[0] * d[0];
-                    r2 += d[1] * d[1];
-                    if constexpr (D == 3) {
-                        d[2] = delta_axis(pi[2], rj.z, 2, P.g);
-                        r2 += d[2] * d[2];
-                    }
-                    vol = vj;
-                    smooth = poly6(r2, P.g);
-                    if (slot != s && r2 > 0.0f) {  // spiky_gradient_kernel kernels.rs:79-96
-                        const float rr = sqrtf(r2);
-                        const float tt = P.g.eps - rr;
-                        if (want_dg) {
-                            const float mag = 1.0f * P.g.k5 * 3.0f * (tt * tt) / rr;
+                if (want_dg) {
+                    const float mag = 1.0f * P.g.k5 * 3.0f * (tt * tt) / rr;
 #pragma unroll
-                            for (int a = 0; a < D; ++a) dgv[a] = mag * d[a];
-                        }
-                        if (want_sg) {
-                            const float mag = vol * P.g.k5 * 3.0f * (tt * tt) / rr;
+                    for (int a = 0; a < D; ++a) dgv[a] = gok ? mag * d[a] : 0.0f;
+                }
+                if (want_sg) {
+                    const float mag = vj * P.g.k5 * 3.0f * (tt * tt) / rr;
 #pragma unroll
-                            for (int a = 0; a < D; ++a) vg[a] = mag * d[a];
-                        }
-                    }
+                    for (int a = 0; a < D; ++a) vg[a] = gok ? mag * d[a] : 0.0f;
                 }
                 const float w = smooth * vol;  // blur_state weight (density-grad-off branch)
                 // the round's entries in list order
@@ -520,21 +518,32 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                         const uint32_t beg = bo[bin], end = bo[bin + 1];
                         for (uint32_t base = beg; base < end; base += kChunk) {
                             const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
+                            // batches of 4 candidates per lane: loads first (index clamped to
+                            // the chunk, so every load is in bounds), then branch-free tests
                             uint64_t acc = 0;
-#pragma unroll 4
-                            for (int i = 0; i < kChunk / L; ++i) {
-                                const uint32_t k = q + (uint32_t)(i * L);
-                                if (k < m) {
-                                    const float4 r = srec[base + k];
-                                    bool ok = in_group;
+                            for (int i0 = 0; i0 < kChunk / L; i0 += 4) {
+                                if ((uint32_t)(i0 * L) >= m) break;  // wave-uniform
+                                float4 rc[4];
+                                int4 cc[4];
+#pragma unroll
+                                for (int u = 0; u < 4; ++u) {
+                                    const uint32_t k = q + (uint32_t)((i0 + u) * L);
+                                    const uint32_t kc = k < m ? k : m - 1;
+                                    rc[u] = srec[base + kc];
+                                    if constexpr (D == 3) cc[u] = scoord[base + kc];
+                                }
+#pragma unroll
+                                for (int u = 0; u < 4; ++u) {
+                                    const uint32_t k = q + (uint32_t)((i0 + u) * L);
+                                    const float4 r = rc[u];
+                                    bool ok = in_group & (k < m);
                                     if (P.g.mode == 1) {
                                         if constexpr (D == 2) {
-                                            ok = ok && (int64_t)__float_as_int(r.z) == n0 &&
-                                                 (int64_t)__float_as_int(r.w) == n1;
+                                            ok = ok & ((int64_t)__float_as_int(r.z) == n0) &
+                                                 ((int64_t)__float_as_int(r.w) == n1);
                                         } else {
-                                            const int4 cj = scoord[base + k];
-                                            ok = ok && (int64_t)cj.x == n0 && (int64_t)cj.y == n1 &&
-                                                 (int64_t)cj.z == n2;
+                                            ok = ok & ((int64_t)cc[u].x == n0) & ((int64_t)cc[u].y == n1) &
+                                                 ((int64_t)cc[u].z == n2);
                                         }
                                     }
                                     const float d0 = delta_axis(pi[0], r.x, 0, P.g);
@@ -545,7 +554,7 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                                         const float d2 = delta_axis(pi[2], r.z, 2, P.g);
                                         r2 += d2 * d2;
                                     }
-                                    if (ok && r2 < P.g.eps2) acc |= 1ull << k;
+                                    acc |= (ok & (r2 < P.g.eps2)) ? (1ull << (k & 63u)) : 0ull;
                                 }
                             }
                             acc = group_or<L>(acc);
