@@ -29,7 +29,8 @@ if ROOT not in sys.path:
 
 PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
-KERNEL_IDS = {"density": 4, "perceive": 5, "mlp": 7}  # NPA_KERNEL_* in include/npa_abi.h
+KERNEL_IDS = {"hash_rank": 0, "table_scan": 1, "offsets_scan": 2, "scatter": 3, "density": 4,
+              "perceive": 5, "mlp": 7}  # NPA_KERNEL_* in include/npa_abi.h
 
 
 def kernel_work(model, candidates: float, pairs: float, particles: int):
@@ -252,15 +253,19 @@ def main(argv=None) -> int:
             "final_state_finite": finite,
         },
     }
+    if kernel_ms:
+        line["kernel_mean_launch_ms"] = kernel_ms
     if kernel_ms and not args.skip_replay:
         work = kernel_work(w["model"], mean_cand, mean_pairs, total)
         per_kernel = {}
         for name, ms in kernel_ms.items():
+            if name not in work:
+                continue
             fl, by = work[name]
             per_kernel[name] = {"mean_launch_ms": ms, "tflops": fl / (ms * 1e-3) / 1e12,
                                 "gbs": by / (ms * 1e-3) / 1e9, "flops_per_launch": fl,
                                 "bytes_per_launch": by}
-        dom = max(kernel_ms, key=kernel_ms.get)
+        dom = max(per_kernel, key=lambda k: per_kernel[k]["mean_launch_ms"])
         k = per_kernel[dom]
         line["roofline"] = {
             "bound": "mfma", "achieved": k["tflops"], "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",

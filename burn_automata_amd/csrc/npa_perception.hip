@@ -221,7 +221,9 @@ __device__ __forceinline__ float ordered_group_sum(float acc, float v) {
 }
 
 // density  forward.rs:145-160: rho_i = sum_j W_poly6(r_ij^2).
-// L lanes per target split each staged chunk round-robin; every lane rebuilds the target's
+// L lanes per target split each chunk of a neighbour bin round-robin (lane q takes candidates
+// k = q, q + L, ...), loading candidate records straight from the sorted copy in batches of four
+// (indices clamped to the chunk) and testing them branch-free. Every lane rebuilds the target's
 // running sum in candidate order from the L per-lane terms of each round. A rejected candidate
 // contributes +0.0, which leaves the sum unchanged (it starts at +0.0, adds only non-negative
 // terms and therefore never holds -0.0).
@@ -233,7 +235,6 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
                                                 const uint2* __restrict__ wl,
                                                 const uint32_t* __restrict__ wl_count,
                                                 float* __restrict__ svol, float* __restrict__ density_out) {
-    __shared__ NbrStage<D> st;
     const uint32_t lane = threadIdx.x;
     const uint32_t t = lane / L, q = lane % L;
     const uint32_t items = *wl_count;
@@ -246,30 +247,66 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
         int ci[3];
         load_rec<D>(srec, scoord, s, pi, ci);
         float rho = 0.0f;
-        for_each_group_chunk<D>(
-            P.g, b, active, ci, bo, lane,
-            [&](uint32_t base, uint32_t m) { stage_records<D>(st, srec, scoord, base, m, lane); },
-            [&](uint32_t, uint32_t m, int64_t n0, int64_t n1, int64_t n2, bool in_group) {
-                for (uint32_t k0 = 0; k0 < m; k0 += L) {
-                    const uint32_t k = k0 + q;
-                    float v = 0.0f;
-                    if (k < m) {
-                        const float4 r = st.rec[k];
-                        bool ok = in_group;
-                        if (P.g.mode == 1) ok = ok && staged_coords_match<D>(st, k, r, n0, n1, n2);
-                        const float d0 = delta_axis(pi[0], r.x, 0, P.g);
-                        const float d1 = delta_axis(pi[1], r.y, 1, P.g);
-                        float r2 = d0 * d0;
-                        r2 += d1 * d1;
-                        if constexpr (D == 3) {
-                            const float d2 = delta_axis(pi[2], r.z, 2, P.g);
-                            r2 += d2 * d2;
+        uint64_t pending = __ballot(active);
+        while (pending) {
+            const int leader = __ffsll((unsigned long long)pending) - 1;
+            const int l0 = readlane_i(ci[0], leader), l1 = readlane_i(ci[1], leader);
+            const int l2 = D == 3 ? readlane_i(ci[2], leader) : 0;
+            const bool same = active && ci[0] == l0 && ci[1] == l1 && (D == 2 || ci[2] == l2);
+            const uint64_t group = __ballot(same) & pending;
+            pending &= ~group;
+            const bool in_group = (group >> lane) & 1ull;
+            constexpr int ZLO = D == 3 ? -1 : 0, ZHI = D == 3 ? 1 : 0;
+            for (int dz = ZLO; dz <= ZHI; ++dz)
+                for (int dy = -1; dy <= 1; ++dy)
+                    for (int dx = -1; dx <= 1; ++dx) {
+                        const int64_t n0 = (int64_t)l0 + dx, n1 = (int64_t)l1 + dy, n2 = (int64_t)l2 + dz;
+                        uint32_t cell;
+                        if (!cell_index(n0, n1, n2, P.g, &cell)) continue;
+                        const uint64_t bin = (uint64_t)b * P.g.cells + cell;
+                        const uint32_t beg = bo[bin], end = bo[bin + 1];
+                        for (uint32_t base = beg; base < end; base += kChunk) {
+                            const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
+                            for (int i0 = 0; i0 < kChunk / L; i0 += 4) {
+                                if ((uint32_t)(i0 * L) >= m) break;  // wave-uniform
+                                float4 rc[4];
+                                int4 cc[4];
+#pragma unroll
+                                for (int u = 0; u < 4; ++u) {
+                                    const uint32_t k = q + (uint32_t)((i0 + u) * L);
+                                    const uint32_t kc = k < m ? k : m - 1;
+                                    rc[u] = srec[base + kc];
+                                    if constexpr (D == 3) cc[u] = scoord[base + kc];
+                                }
+#pragma unroll
+                                for (int u = 0; u < 4; ++u) {
+                                    const uint32_t k = q + (uint32_t)((i0 + u) * L);
+                                    const float4 r = rc[u];
+                                    bool ok = in_group & (k < m);
+                                    if (P.g.mode == 1) {
+                                        if constexpr (D == 2) {
+                                            ok = ok & ((int64_t)__float_as_int(r.z) == n0) &
+                                                 ((int64_t)__float_as_int(r.w) == n1);
+                                        } else {
+                                            ok = ok & ((int64_t)cc[u].x == n0) & ((int64_t)cc[u].y == n1) &
+                                                 ((int64_t)cc[u].z == n2);
+                                        }
+                                    }
+                                    const float d0 = delta_axis(pi[0], r.x, 0, P.g);
+                                    const float d1 = delta_axis(pi[1], r.y, 1, P.g);
+                                    float r2 = d0 * d0;
+                                    r2 += d1 * d1;
+                                    if constexpr (D == 3) {
+                                        const float d2 = delta_axis(pi[2], r.z, 2, P.g);
+                                        r2 += d2 * d2;
+                                    }
+                                    const float v = ok ? poly6(r2, P.g) : 0.0f;  // poly6 is 0 beyond eps
+                                    rho = ordered_group_sum<L>(rho, v);
+                                }
+                            }
                         }
-                        if (ok && r2 < P.g.eps2) v = poly6(r2, P.g);
                     }
-                    rho = ordered_group_sum<L>(rho, v);
-                }
-            });
+        }
         if (active && q == 0) {
             svol[s] = recip_finite(rho);
             if (density_out) density_out[b * P.N + perm[s]] = rho;
