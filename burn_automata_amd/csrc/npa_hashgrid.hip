@@ -71,6 +71,9 @@ hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t
     NPA_RES(counters, 64);
     NPA_RES(features, t1 * (uint64_t)(feature_dims ? feature_dims : 1) * 4);
     NPA_RES(wpad, 4);
+    NPA_RES(tmpidx, t1 * 4);
+    NPA_RES(dir_n, (bins ? bins : 1) * 4);
+    NPA_RES(dir_e, (bins ? bins : 1) * kDirGroups * 16);
 #undef NPA_RES
     if (!flags.ptr) {
         if ((e = flags.reserve(64)) != hipSuccess) return e;
@@ -81,7 +84,8 @@ hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t
 
 void Workspace::release() {
     for (DevBuf* b : {&keys, &ranks, &table, &totals, &bin_offsets, &perm, &inv, &flags, &wl_count,
-                      &worklist, &srec, &scoord, &sstate, &svol, &counters, &features})
+                      &worklist, &srec, &scoord, &sstate, &svol, &counters, &features, &wpad, &tmpidx,
+                      &dir_n, &dir_e})
         b->release();
 }
 
@@ -161,7 +165,9 @@ bool make_plan(const npa_grid_cfg& cfg, uint32_t batch, uint32_t n, HashgridPlan
         return false;
     }
     p.tpi = tpi;
-    p.worklist_cap = (total + tpi - 1) / tpi + std::min<uint64_t>(total, (uint64_t)batch * cells) + 1;
+    // items: <= tpi slots of one cell run (or of an unsplit bin), so at most total / tpi full
+    // items plus one partial item per run
+    p.worklist_cap = (total + tpi - 1) / tpi + std::min<uint64_t>(total, (uint64_t)batch * cells * kDirGroups) + 1;
     *plan = p;
     return true;
 }
@@ -351,17 +357,19 @@ __global__ __launch_bounds__(1024) void k_offsets_scan(const uint32_t* __restric
     if (b == batch - 1 && threadIdx.x == 0) bin_offsets[(uint64_t)batch * C] = sys_base + all_c;
 }
 
-template <int D>
-__global__ __launch_bounds__(256) void k_scatter(
-    const float4* __restrict__ pos, const float* __restrict__ states, uint32_t S, uint32_t n,
-    uint32_t total, uint32_t tile, uint32_t tiles_per_sys, GridParams g,
-    const uint32_t* __restrict__ keys, const uint32_t* __restrict__ ranks,
-    const uint32_t* __restrict__ table, const uint32_t* __restrict__ bin_offsets,
-    uint32_t* __restrict__ perm, uint32_t* __restrict__ inv, float4* __restrict__ srec,
-    int4* __restrict__ scoord, float* __restrict__ sstate, int payload) {
+// payload == 0: perm (slot -> particle of the system) and inv, the reference's snapshot.
+// payload == 1: out[slot] = global particle index in the reference order; k_split then orders
+// each bin by cell and writes the snapshot and the sorted payload.
+__global__ __launch_bounds__(256) void k_scatter(uint32_t n, uint32_t total, uint32_t tile,
+                                                 uint32_t tiles_per_sys, uint32_t C,
+                                                 const uint32_t* __restrict__ keys,
+                                                 const uint32_t* __restrict__ ranks,
+                                                 const uint32_t* __restrict__ table,
+                                                 const uint32_t* __restrict__ bin_offsets,
+                                                 uint32_t* __restrict__ out, uint32_t* __restrict__ inv,
+                                                 int payload) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
-    const uint32_t C = g.cells;
     const uint32_t b = i / n;
     const uint32_t li = i - b * n;
     const uint32_t t = li / tile;
@@ -369,19 +377,29 @@ __global__ __launch_bounds__(256) void k_scatter(
     const uint32_t dst_local = (bin_offsets[(uint64_t)b * C + key] - b * n) +
                                table[((uint64_t)b * tiles_per_sys + t) * C + key] + ranks[i];
     const uint32_t dst = b * n + dst_local;
-    perm[dst] = li;
+    if (payload) {
+        out[dst] = i;
+        return;
+    }
+    out[dst] = li;
     inv[i] = dst_local;
-    if (!payload) return;
-    const float4 p4 = pos[i];
-    float p[4] = {p4.x, p4.y, p4.z, p4.w};
-    int64_t c[3];
-    bool ovf = false;
-    cell_coords(p, g, c, &ovf);
+}
+
+// Writes particle i (global index) to sorted slot dst: snapshot entries, sorted record
+// {x, y, bits(cx), bits(cy)} (2D) or position + coordinates (3D), and the zero-padded state row.
+template <int D>
+__device__ __forceinline__ void write_sorted(uint32_t dst, uint32_t i, uint32_t b, uint32_t n,
+                                             const float4& p4, const int c[3], const float* __restrict__ states,
+                                             uint32_t S, uint32_t* __restrict__ perm, uint32_t* __restrict__ inv,
+                                             float4* __restrict__ srec, int4* __restrict__ scoord,
+                                             float* __restrict__ sstate) {
+    perm[dst] = i - b * n;
+    inv[i] = dst - b * n;
     if (D == 2) {
-        srec[dst] = make_float4(p4.x, p4.y, __int_as_float((int)c[0]), __int_as_float((int)c[1]));
+        srec[dst] = make_float4(p4.x, p4.y, __int_as_float(c[0]), __int_as_float(c[1]));
     } else {
         srec[dst] = p4;
-        scoord[dst] = make_int4((int)c[0], (int)c[1], (int)c[2], (int)i);
+        scoord[dst] = make_int4(c[0], c[1], c[2], (int)i);
     }
     if (!states) return;  // neighbour-list export needs positions only
     const uint32_t SS = state_stride_for(S);
@@ -392,11 +410,167 @@ __global__ __launch_bounds__(256) void k_scatter(
         for (uint32_t q = 0; q < SS / 4; ++q) o4[q] = s4[q];
     } else {
         for (uint32_t q = 0; q < SS / 4; ++q) {
-            const uint32_t c = 4 * q;
-            o4[q] = make_float4(c < S ? src[c] : 0.0f, c + 1 < S ? src[c + 1] : 0.0f,
-                                c + 2 < S ? src[c + 2] : 0.0f, c + 3 < S ? src[c + 3] : 0.0f);
+            const uint32_t cc = 4 * q;
+            o4[q] = make_float4(cc < S ? src[cc] : 0.0f, cc + 1 < S ? src[cc + 1] : 0.0f,
+                                cc + 2 < S ? src[cc + 2] : 0.0f, cc + 3 < S ? src[cc + 3] : 0.0f);
         }
     }
+}
+
+// Orders each bin by true cell, one wave per bin. Pass 1 finds the bin's distinct cells in order
+// of first appearance and their counts; pass 2 writes each particle to
+// run start of its cell + its rank among the earlier particles of that cell, which keeps
+// ascending particle index inside every run (the reference's neighbour order). A bin with more
+// than kDirGroups cells keeps the reference order (dir_n = kDirGroups + 1). Also emits the wave
+// work items: <= tpi consecutive slots of one run (or of an unsplit bin).
+template <int D>
+__global__ __launch_bounds__(256) void k_split(const float4* __restrict__ pos, const float* __restrict__ states,
+                                               uint32_t S, uint32_t n, uint32_t nbins, GridParams g,
+                                               const uint32_t* __restrict__ bo,
+                                               const uint32_t* __restrict__ order,
+                                               uint32_t* __restrict__ perm, uint32_t* __restrict__ inv,
+                                               float4* __restrict__ srec, int4* __restrict__ scoord,
+                                               float* __restrict__ sstate, uint32_t* __restrict__ dir_n,
+                                               int4* __restrict__ dir_e, uint2* __restrict__ worklist,
+                                               uint32_t* __restrict__ wl_count, uint32_t tpi) {
+    constexpr uint32_t K = kDirGroups;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t bin = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (bin >= nbins) return;  // whole wave
+    const uint32_t beg = bo[bin], end = bo[bin + 1];
+    if (beg == end) {
+        if (lane == 0) dir_n[bin] = 0;
+        return;
+    }
+    const uint32_t b = bin / g.cells;
+    const uint64_t lt = lanemask_lt();
+    int gx[K], gy[K], gz[K];
+    uint32_t gc[K];
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) {
+        gx[k] = gy[k] = gz[k] = 0;
+        gc[k] = 0;
+    }
+    uint32_t ng = 0;
+    bool over = false;
+    // the particle of slot c0 + lane, its record and cell coordinates
+    auto load = [&](uint32_t c0, bool& valid, uint32_t& i, float4& p4, int c[3]) {
+        const uint32_t slot = c0 + lane;
+        valid = slot < end;
+        i = order[valid ? slot : c0];
+        p4 = pos[i];
+        const float p[4] = {p4.x, p4.y, p4.z, p4.w};
+        int64_t c64[3];
+        bool ovf = false;
+        cell_coords(p, g, c64, &ovf);  // overflow was flagged by the hash pass
+        c[0] = (int)c64[0];
+        c[1] = (int)c64[1];
+        c[2] = (int)c64[2];
+    };
+    auto group_of = [&](const int c[3]) -> int {
+        int gid = -1;
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k)
+            if (k < ng && c[0] == gx[k] && c[1] == gy[k] && c[2] == gz[k]) gid = (int)k;
+        return gid;
+    };
+    for (uint32_t c0 = beg; c0 < end && !over; c0 += 64) {
+        bool valid;
+        uint32_t i;
+        float4 p4;
+        int c[3];
+        load(c0, valid, i, p4, c);
+        int gid = group_of(c);
+        uint64_t unknown = __ballot(valid && gid < 0);
+        while (unknown) {
+            if (ng == K) {
+                over = true;
+                break;
+            }
+            const int leader = __ffsll((unsigned long long)unknown) - 1;
+            const int nx = __builtin_amdgcn_readlane(c[0], leader);
+            const int ny = __builtin_amdgcn_readlane(c[1], leader);
+            const int nz = __builtin_amdgcn_readlane(c[2], leader);
+#pragma unroll
+            for (uint32_t k = 0; k < K; ++k)
+                if (k == ng) {
+                    gx[k] = nx;
+                    gy[k] = ny;
+                    gz[k] = nz;
+                }
+            if (valid && gid < 0 && c[0] == nx && c[1] == ny && c[2] == nz) gid = (int)ng;
+            ++ng;
+            unknown = __ballot(valid && gid < 0);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k) gc[k] += (uint32_t)__popcll(__ballot(valid && gid == (int)k));
+    }
+    uint32_t nitems = 0;
+    uint32_t start[K];
+    if (over) {
+        nitems = (end - beg + tpi - 1) / tpi;
+    } else {
+        uint32_t run = beg;
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k) {
+            start[k] = run;
+            run += gc[k];
+            nitems += (gc[k] + tpi - 1) / tpi;
+        }
+    }
+    uint32_t wbase = 0;
+    if (lane == 0) wbase = atomicAdd(wl_count, nitems);
+    wbase = (uint32_t)__builtin_amdgcn_readfirstlane((int)wbase);
+    if (over) {
+        for (uint32_t c0 = beg; c0 < end; c0 += 64) {
+            bool valid;
+            uint32_t i;
+            float4 p4;
+            int c[3];
+            load(c0, valid, i, p4, c);
+            if (valid) write_sorted<D>(c0 + lane, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
+        }
+        const uint32_t cnt = end - beg;
+        for (uint32_t m = lane; m < nitems; m += 64) {
+            const uint32_t left = cnt - m * tpi;
+            worklist[wbase + m] = make_uint2(beg + m * tpi, left < tpi ? left : tpi);
+        }
+        if (lane == 0) dir_n[bin] = K + 1;
+        return;
+    }
+    uint32_t seen[K];
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) seen[k] = 0;
+    for (uint32_t c0 = beg; c0 < end; c0 += 64) {
+        bool valid;
+        uint32_t i;
+        float4 p4;
+        int c[3];
+        load(c0, valid, i, p4, c);
+        const int gid = group_of(c);
+        uint32_t dst = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k) {
+            const uint64_t m = __ballot(valid && gid == (int)k);
+            if (gid == (int)k) dst = start[k] + seen[k] + (uint32_t)__popcll(m & lt);
+            seen[k] += (uint32_t)__popcll(m);
+        }
+        if (valid) write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
+    }
+    uint32_t off = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) {
+        if (k < ng) {
+            const uint32_t it = (gc[k] + tpi - 1) / tpi;
+            for (uint32_t m = lane; m < it; m += 64) {
+                const uint32_t left = gc[k] - m * tpi;
+                worklist[wbase + off + m] = make_uint2(start[k] + m * tpi, left < tpi ? left : tpi);
+            }
+            off += it;
+            if (lane == 0) dir_e[(uint64_t)bin * K + k] = make_int4(gx[k], gy[k], gz[k], (int)start[k]);
+        }
+    }
+    if (lane == 0) dir_n[bin] = ng;
 }
 
 // ------------------------------------------------------------------ launch
@@ -462,28 +636,37 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
         ProfScope ps(prof, NPA_KERNEL_OFFSETS_SCAN, stream);
         hipLaunchKernelGGL(k_offsets_scan, dim3(batch), dim3(1024), 0, stream,
                            ws.totals.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), plan.cells, n,
-                           batch, ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(),
-                           payload ? 1 : 0, plan.tpi);
+                           batch, ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), 0, plan.tpi);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     {
         ProfScope ps(prof, NPA_KERNEL_SCATTER, stream);
         const uint32_t blocks = (uint32_t)((total + 255) / 256);
-        if (g.dim == 2)
-            hipLaunchKernelGGL(k_scatter<2>, dim3(blocks), dim3(256), 0, stream, pos, states,
-                               state_dims, n, (uint32_t)total, plan.tile, plan.tiles_per_sys, g,
-                               ws.keys.as<uint32_t>(), ws.ranks.as<uint32_t>(),
-                               ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(),
-                               ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(),
-                               ws.scoord.as<int4>(), ws.sstate.as<float>(), payload ? 1 : 0);
-        else
-            hipLaunchKernelGGL(k_scatter<3>, dim3(blocks), dim3(256), 0, stream, pos, states,
-                               state_dims, n, (uint32_t)total, plan.tile, plan.tiles_per_sys, g,
-                               ws.keys.as<uint32_t>(), ws.ranks.as<uint32_t>(),
-                               ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(),
-                               ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(),
-                               ws.scoord.as<int4>(), ws.sstate.as<float>(), payload ? 1 : 0);
+        hipLaunchKernelGGL(k_scatter, dim3(blocks), dim3(256), 0, stream, n, (uint32_t)total, plan.tile,
+                           plan.tiles_per_sys, plan.cells, ws.keys.as<uint32_t>(), ws.ranks.as<uint32_t>(),
+                           ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(),
+                           payload ? ws.tmpidx.as<uint32_t>() : ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(),
+                           payload ? 1 : 0);
         if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (payload) {
+            const uint32_t nbins = batch * plan.cells;
+            const uint32_t sblocks = (nbins + 3) / 4;
+            if (g.dim == 2)
+                hipLaunchKernelGGL(k_split<2>, dim3(sblocks), dim3(256), 0, stream, pos, states, state_dims, n,
+                                   nbins, g, ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(),
+                                   ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(),
+                                   ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.dir_n.as<uint32_t>(),
+                                   ws.dir_e.as<int4>(), ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(),
+                                   plan.tpi);
+            else
+                hipLaunchKernelGGL(k_split<3>, dim3(sblocks), dim3(256), 0, stream, pos, states, state_dims, n,
+                                   nbins, g, ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(),
+                                   ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(),
+                                   ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.dir_n.as<uint32_t>(),
+                                   ws.dir_e.as<int4>(), ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(),
+                                   plan.tpi);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
     }
     return hipSuccess;
 }

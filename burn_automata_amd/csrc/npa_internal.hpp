@@ -67,9 +67,16 @@ struct HashgridPlan {
 };
 
 // Device workspace of one hashgrid + perception pass.
+// Bins are split by true cell for the neighbour passes: a bin holding up to kDirGroups distinct
+// cells gets one contiguous run of slots per cell (ascending particle index inside each run) and a
+// directory entry {cx, cy, cz, first slot} per run; dir_n[bin] = number of runs, or
+// kDirGroups + 1 when the bin holds more cells and keeps the reference order.
+constexpr uint32_t kDirGroups = 8;
+
 struct Workspace {
     DevBuf keys, ranks, table, totals, bin_offsets, perm, inv, flags, wl_count, worklist;
     DevBuf srec, scoord, sstate, svol, counters, features, wpad;
+    DevBuf tmpidx, dir_n, dir_e;
     hipError_t reserve(const HashgridPlan& plan, uint64_t total, uint32_t batch, uint32_t state_dims,
                        int dim, uint32_t feature_dims = 0);
     void release();
@@ -127,6 +134,9 @@ struct StepParams {
     float update_prob;
     uint32_t step_index;
     uint32_t base_seed;
+    // cell directory of the split bins (set by the neighbour-pass launchers)
+    const uint32_t* dir_n;
+    const int4* dir_e;
 };
 
 struct StepIO {

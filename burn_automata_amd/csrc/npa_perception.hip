@@ -108,6 +108,41 @@ constexpr int kChunk = 64;
 
 __device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
 
+// Candidate slots of neighbour cell (n0, n1, n2) of system b: in Particle mode the cell's own run
+// of its split bin (no coordinate test needed) or, for an unsplit bin, the whole bin with
+// `filter` set; in Grid mode the cell's bin. False when the cell holds no particle.
+__device__ __forceinline__ bool cell_range(const StepParams& P, const uint32_t* __restrict__ bo, uint32_t b,
+                                           int64_t n0, int64_t n1, int64_t n2, uint32_t& beg, uint32_t& end,
+                                           bool& filter) {
+    uint32_t cell;
+    if (!cell_index(n0, n1, n2, P.g, &cell)) return false;
+    const uint64_t bin = (uint64_t)b * P.g.cells + cell;
+    filter = false;
+    if (P.g.mode != 1) {
+        beg = bo[bin];
+        end = bo[bin + 1];
+        return beg < end;
+    }
+    const uint32_t nd = P.dir_n[bin];
+    if (nd == 0) return false;
+    if (nd > kDirGroups) {
+        beg = bo[bin];
+        end = bo[bin + 1];
+        filter = true;
+        return true;
+    }
+    const int4* e = P.dir_e + bin * kDirGroups;
+    for (uint32_t k = 0; k < nd; ++k) {
+        const int4 ek = e[k];
+        if ((int64_t)ek.x == n0 && (int64_t)ek.y == n1 && (int64_t)ek.z == n2) {
+            beg = (uint32_t)ek.w;
+            end = k + 1 < nd ? (uint32_t)e[k + 1].w : bo[bin + 1];
+            return true;
+        }
+    }
+    return false;
+}
+
 template <int D>
 struct NbrStage {
     float4 rec[kChunk];
@@ -261,10 +296,9 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
                 for (int dy = -1; dy <= 1; ++dy)
                     for (int dx = -1; dx <= 1; ++dx) {
                         const int64_t n0 = (int64_t)l0 + dx, n1 = (int64_t)l1 + dy, n2 = (int64_t)l2 + dz;
-                        uint32_t cell;
-                        if (!cell_index(n0, n1, n2, P.g, &cell)) continue;
-                        const uint64_t bin = (uint64_t)b * P.g.cells + cell;
-                        const uint32_t beg = bo[bin], end = bo[bin + 1];
+                        uint32_t beg, end;
+                        bool filter;
+                        if (!cell_range(P, bo, b, n0, n1, n2, beg, end, filter)) continue;
                         for (uint32_t base = beg; base < end; base += kChunk) {
                             const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
                             for (int i0 = 0; i0 < kChunk / L; i0 += 4) {
@@ -283,7 +317,7 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
                                     const uint32_t k = q + (uint32_t)((i0 + u) * L);
                                     const float4 r = rc[u];
                                     bool ok = in_group & (k < m);
-                                    if (P.g.mode == 1) {
+                                    if (filter) {
                                         if constexpr (D == 2) {
                                             ok = ok & ((int64_t)__float_as_int(r.z) == n0) &
                                                  ((int64_t)__float_as_int(r.w) == n1);
@@ -549,10 +583,9 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                 for (int dy = -1; dy <= 1; ++dy)
                     for (int dx = -1; dx <= 1; ++dx) {
                         const int64_t n0 = (int64_t)l0 + dx, n1 = (int64_t)l1 + dy, n2 = (int64_t)l2 + dz;
-                        uint32_t cell;
-                        if (!cell_index(n0, n1, n2, P.g, &cell)) continue;
-                        const uint64_t bin = (uint64_t)b * P.g.cells + cell;
-                        const uint32_t beg = bo[bin], end = bo[bin + 1];
+                        uint32_t beg, end;
+                        bool filter;
+                        if (!cell_range(P, bo, b, n0, n1, n2, beg, end, filter)) continue;
                         for (uint32_t base = beg; base < end; base += kChunk) {
                             const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
                             // batches of 4 candidates per lane: loads first (index clamped to
@@ -574,7 +607,7 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                                     const uint32_t k = q + (uint32_t)((i0 + u) * L);
                                     const float4 r = rc[u];
                                     bool ok = in_group & (k < m);
-                                    if (P.g.mode == 1) {
+                                    if (filter) {
                                         if constexpr (D == 2) {
                                             ok = ok & ((int64_t)__float_as_int(r.z) == n0) &
                                                  ((int64_t)__float_as_int(r.w) == n1);
@@ -1060,9 +1093,17 @@ static void launch_density_d(const StepParams& p, Workspace& ws, float* density_
     else launch_density_t<D, 4>(p, ws, density_out, blocks, stream);
 }
 
-hipError_t launch_density(const StepParams& p, Workspace& ws, float* density_out, int grid_blocks,
+static StepParams with_directory(const StepParams& p, const Workspace& ws) {
+    StepParams q = p;
+    q.dir_n = ws.dir_n.as<uint32_t>();
+    q.dir_e = ws.dir_e.as<int4>();
+    return q;
+}
+
+hipError_t launch_density(const StepParams& p_in, Workspace& ws, float* density_out, int grid_blocks,
                           hipStream_t stream, Profiler* prof) {
     ProfScope ps(prof, NPA_KERNEL_DENSITY, stream);
+    const StepParams p = with_directory(p_in, ws);
     const int blocks = grid_blocks * 4;  // one wave per block
     if (p.g.dim == 2) launch_density_d<2>(p, ws, density_out, blocks, stream);
     else launch_density_d<3>(p, ws, density_out, blocks, stream);
@@ -1142,8 +1183,9 @@ static hipError_t launch_mlp_d(const StepParams& p, Workspace& ws, const StepIO&
     }
 }
 
-hipError_t launch_update(const StepParams& p, Workspace& ws, const StepIO& io, int mode, int grid_blocks,
+hipError_t launch_update(const StepParams& p_in, Workspace& ws, const StepIO& io, int mode, int grid_blocks,
                          hipStream_t stream, Profiler* prof) {
+    const StepParams p = with_directory(p_in, ws);
     const int blocks = grid_blocks * 4;  // one wave per block
     {
         ProfScope ps(prof, NPA_KERNEL_PERCEIVE, stream);
