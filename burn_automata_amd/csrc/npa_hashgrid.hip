@@ -474,12 +474,18 @@ __global__ __launch_bounds__(256) void k_split(const float4* __restrict__ pos, c
             if (k < ng && c[0] == gx[k] && c[1] == gy[k] && c[2] == gz[k]) gid = (int)k;
         return gid;
     };
+    // the first chunk (the whole bin for most bins) is loaded once for both passes
+    bool valid0;
+    uint32_t i0;
+    float4 p0;
+    int cf[3];
+    load(beg, valid0, i0, p0, cf);
     for (uint32_t c0 = beg; c0 < end && !over; c0 += 64) {
-        bool valid;
-        uint32_t i;
-        float4 p4;
-        int c[3];
-        load(c0, valid, i, p4, c);
+        bool valid = valid0;
+        uint32_t i = i0;
+        float4 p4 = p0;
+        int c[3] = {cf[0], cf[1], cf[2]};
+        if (c0 != beg) load(c0, valid, i, p4, c);
         int gid = group_of(c);
         uint64_t unknown = __ballot(valid && gid < 0);
         while (unknown) {
@@ -518,18 +524,18 @@ __global__ __launch_bounds__(256) void k_split(const float4* __restrict__ pos, c
             nitems += (gc[k] + tpi - 1) / tpi;
         }
     }
-    uint32_t wbase = 0;
+    uint32_t wbase = 0;  // first work item of this bin (used after the writes below)
     if (lane == 0) wbase = atomicAdd(wl_count, nitems);
-    wbase = (uint32_t)__builtin_amdgcn_readfirstlane((int)wbase);
     if (over) {
         for (uint32_t c0 = beg; c0 < end; c0 += 64) {
-            bool valid;
-            uint32_t i;
-            float4 p4;
-            int c[3];
-            load(c0, valid, i, p4, c);
+            bool valid = valid0;
+            uint32_t i = i0;
+            float4 p4 = p0;
+            int c[3] = {cf[0], cf[1], cf[2]};
+            if (c0 != beg) load(c0, valid, i, p4, c);
             if (valid) write_sorted<D>(c0 + lane, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
         }
+        wbase = (uint32_t)__builtin_amdgcn_readfirstlane((int)wbase);
         const uint32_t cnt = end - beg;
         for (uint32_t m = lane; m < nitems; m += 64) {
             const uint32_t left = cnt - m * tpi;
@@ -542,11 +548,11 @@ __global__ __launch_bounds__(256) void k_split(const float4* __restrict__ pos, c
 #pragma unroll
     for (uint32_t k = 0; k < K; ++k) seen[k] = 0;
     for (uint32_t c0 = beg; c0 < end; c0 += 64) {
-        bool valid;
-        uint32_t i;
-        float4 p4;
-        int c[3];
-        load(c0, valid, i, p4, c);
+        bool valid = valid0;
+        uint32_t i = i0;
+        float4 p4 = p0;
+        int c[3] = {cf[0], cf[1], cf[2]};
+        if (c0 != beg) load(c0, valid, i, p4, c);
         const int gid = group_of(c);
         uint32_t dst = 0;
 #pragma unroll
@@ -557,6 +563,7 @@ __global__ __launch_bounds__(256) void k_split(const float4* __restrict__ pos, c
         }
         if (valid) write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
     }
+    wbase = (uint32_t)__builtin_amdgcn_readfirstlane((int)wbase);
     uint32_t off = 0;
 #pragma unroll
     for (uint32_t k = 0; k < K; ++k) {

@@ -387,7 +387,9 @@ __device__ __forceinline__ uint64_t residue_mask(uint32_t q) {
 // at +0.0 and so never holds -0.0.
 // MODE 0: padded feature rows, feature-major (features[k * T + s]) for the MLP kernel.
 // MODE 1: the perceive_with_options outputs in original particle order.
-template <int D, int SM, int MODE>
+// FL >= 0 fixes the option flags at compile time (bit 0 state gradient, bit 1 density gradient,
+// bit 2 moment correction); FL < 0 reads them from P.
+template <int D, int SM, int MODE, int FL>
 __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __restrict__ srec,
                                                  const int4* __restrict__ scoord,
                                                  const float* __restrict__ sstate,
@@ -407,9 +409,10 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
     const uint32_t t = lane / L, q = lane % L;
     const uint32_t c0 = q * CPL;  // first channel of this lane
     const uint32_t items = *wl_count;
-    const bool branch_a = P.state_grad && P.density_grad;
-    const bool want_sg = P.state_grad != 0, want_dg = P.density_grad != 0;
-    const bool want_m = want_sg && P.hybrid;
+    const bool want_sg = FL >= 0 ? (FL & 1) != 0 : P.state_grad != 0;
+    const bool want_dg = FL >= 0 ? (FL & 2) != 0 : P.density_grad != 0;
+    const bool want_m = FL >= 0 ? (FL & 5) == 5 : (want_sg && P.hybrid);
+    const bool branch_a = want_sg && want_dg;
     const uint64_t my_residue = residue_mask<L>(q);
     for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
         const uint2 item = wl[it];
@@ -1110,13 +1113,25 @@ hipError_t launch_density(const StepParams& p_in, Workspace& ws, float* density_
     return hipGetLastError();
 }
 
-template <int D, int SM, int MODE>
-static void launch_perceive_t(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
+template <int D, int SM, int MODE, int FL>
+static void launch_perceive_f(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
                               hipStream_t stream) {
-    hipLaunchKernelGGL((k_perceive<D, SM, MODE>), dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
+    hipLaunchKernelGGL((k_perceive<D, SM, MODE, FL>), dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
                        ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.svol.as<float>(),
                        ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), ws.worklist.as<uint2>(),
                        ws.wl_count.as<uint32_t>(), ws.features.as<float>(), io);
+}
+
+// The rollout step's usual option sets run a specialised kernel; anything else reads the flags.
+template <int D, int SM, int MODE>
+static void launch_perceive_t(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
+                              hipStream_t stream) {
+    if (MODE == 0 && p.state_grad && p.hybrid && !p.density_grad)
+        launch_perceive_f<D, SM, MODE, 5>(p, ws, io, blocks, stream);
+    else if (MODE == 0 && p.state_grad && p.hybrid && p.density_grad)
+        launch_perceive_f<D, SM, MODE, 7>(p, ws, io, blocks, stream);
+    else
+        launch_perceive_f<D, SM, MODE, -1>(p, ws, io, blocks, stream);
 }
 
 template <int D, int MODE>
