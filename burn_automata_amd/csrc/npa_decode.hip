@@ -185,8 +185,16 @@ __global__ __launch_bounds__(1024) void k_scan_1block(const uint32_t* __restrict
     __shared__ uint32_t lds[32];
     const uint32_t per = (count + blockDim.x - 1) / blockDim.x;
     const uint32_t k0 = threadIdx.x * per;
+    const uint32_t k1 = k0 + per < count ? k0 + per : count;
     uint32_t sum = 0;
-    for (uint32_t k = k0; k < k0 + per && k < count; ++k) sum += in[k];
+    // batches of 8 independent loads (one memory round trip per batch, not per element)
+    for (uint32_t k = k0; k < k1; k += 8) {
+        uint32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = k + u < k1 ? in[k + u] : 0u;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) sum += v[u];
+    }
     const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
     uint32_t x = sum;
     for (int off = 1; off < 64; off <<= 1) {
@@ -205,11 +213,85 @@ __global__ __launch_bounds__(1024) void k_scan_1block(const uint32_t* __restrict
     }
     __syncthreads();
     uint32_t run = (wid ? lds[wid - 1] : 0) + x - sum;
-    for (uint32_t k = k0; k < k0 + per && k < count; ++k) {
-        out[k] = run;
-        run += in[k];
+    for (uint32_t k = k0; k < k1; k += 8) {
+        uint32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = k + u < k1 ? in[k + u] : 0u;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (k + u < k1) out[k + u] = run;
+            run += v[u];
+        }
     }
     if (threadIdx.x == 0) *total_out = lds[nw - 1];
+}
+
+// Multi-block exclusive scan: blocks of 256 threads own 1024 consecutive values each, loaded
+// coalesced through LDS; each thread scans 4 consecutive values.
+constexpr uint32_t kScanBlock = 1024;
+
+__device__ __forceinline__ uint32_t block_exclusive_256(uint32_t v, uint32_t* lds8, uint32_t* total) {
+    const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    uint32_t x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(x, off, 64);
+        if (lane >= (uint32_t)off) x += y;
+    }
+    if (lane == 63) lds8[wid] = x;
+    __syncthreads();
+    uint32_t pre = 0, all = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < 4; ++w) {
+        const uint32_t t = lds8[w];
+        if (w < wid) pre += t;
+        all += t;
+    }
+    *total = all;
+    return pre + x - v;
+}
+
+__global__ __launch_bounds__(256) void k_scan_partials(const uint32_t* __restrict__ in, uint32_t count,
+                                                       uint32_t* __restrict__ sums) {
+    __shared__ uint32_t lds8[4];
+    const uint32_t base = blockIdx.x * kScanBlock;
+    uint32_t v = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) {
+        const uint32_t k = base + u * 256 + threadIdx.x;
+        v += k < count ? in[k] : 0u;
+    }
+    uint32_t total;
+    (void)block_exclusive_256(v, lds8, &total);
+    if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(256) void k_scan_apply(const uint32_t* __restrict__ in, uint32_t* __restrict__ out,
+                                                    uint32_t count, const uint32_t* __restrict__ offsets) {
+    __shared__ uint32_t vals[kScanBlock];
+    __shared__ uint32_t lds8[4];
+    const uint32_t base = blockIdx.x * kScanBlock;
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) {
+        const uint32_t k = base + u * 256 + threadIdx.x;
+        vals[u * 256 + threadIdx.x] = k < count ? in[k] : 0u;
+    }
+    __syncthreads();
+    const uint32_t a = vals[4 * threadIdx.x], b = vals[4 * threadIdx.x + 1];
+    const uint32_t c = vals[4 * threadIdx.x + 2], d = vals[4 * threadIdx.x + 3];
+    uint32_t total;
+    const uint32_t pre = offsets[blockIdx.x] + block_exclusive_256(a + b + c + d, lds8, &total);
+    __syncthreads();
+    vals[4 * threadIdx.x] = pre;
+    vals[4 * threadIdx.x + 1] = pre + a;
+    vals[4 * threadIdx.x + 2] = pre + a + b;
+    vals[4 * threadIdx.x + 3] = pre + a + b + c;
+    __syncthreads();
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) {
+        const uint32_t k = base + u * 256 + threadIdx.x;
+        if (k < count) out[k] = vals[u * 256 + threadIdx.x];
+    }
 }
 
 __global__ __launch_bounds__(256) void k_splat_emit(SplatParams P, const SplatParticle* __restrict__ sp,
@@ -263,7 +345,7 @@ __global__ __launch_bounds__(256) void k_splat_tiles(SplatParams P, const SplatP
 }
 
 void SplatWorkspace::release() {
-    for (DevBuf* b : {&params, &item_start, &keys, &vals, &sorted, &ranks, &table, &totals, &offsets, &count, &flags})
+    for (DevBuf* b : {&params, &item_start, &keys, &vals, &sorted, &ranks, &table, &totals, &offsets, &count, &flags, &scan})
         b->release();
 }
 
@@ -314,6 +396,7 @@ hipError_t launch_splat_2d(const float4* pos, const float* colors, const float* 
     NPA_RES(ws.totals, (uint64_t)ntile_total * 4);
     NPA_RES(ws.offsets, ((uint64_t)ntile_total + 1) * 4);
     NPA_RES(ws.count, 64);
+    NPA_RES(ws.scan, (2 * ((uint64_t)count / kScanBlock + 1) + 2) * 4);
     NPA_RES(ws.flags, 64);
 #undef NPA_RES
     ProfScope ps(prof, NPA_KERNEL_SPLAT, stream);
@@ -324,8 +407,21 @@ hipError_t launch_splat_2d(const float4* pos, const float* colors, const float* 
                            count, ws.params.as<SplatParticle>(), ntiles);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(k_scan_1block, dim3(1), dim3(1024), 0, stream, ntiles, start, count, ws.count.as<uint32_t>());
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    {  // start = exclusive prefix of ntiles, total item count into ws.count
+        const uint32_t nb = (count + kScanBlock - 1) / kScanBlock;
+        uint32_t* sums = ws.scan.as<uint32_t>();
+        if (nb) {
+            hipLaunchKernelGGL(k_scan_partials, dim3(nb), dim3(256), 0, stream, ntiles, count, sums);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL(k_scan_1block, dim3(1), dim3(1024), 0, stream, sums, sums + nb + 1, nb,
+                           ws.count.as<uint32_t>());
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (nb) {
+            hipLaunchKernelGGL(k_scan_apply, dim3(nb), dim3(256), 0, stream, ntiles, start, count, sums + nb + 1);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+    }
     if (count) {
         hipLaunchKernelGGL(k_splat_emit, dim3((count + 255) / 256), dim3(256), 0, stream, P,
                            ws.params.as<SplatParticle>(), ntiles, start, count, ws.keys.as<uint32_t>(),

@@ -329,11 +329,17 @@ __global__ __launch_bounds__(1024) void k_offsets_scan(const uint32_t* __restric
     const uint32_t per = (C + blockDim.x - 1) / blockDim.x;
     const uint32_t k0 = threadIdx.x * per;
     const uint32_t* tot = totals + (uint64_t)b * C;
+    const uint32_t k1 = k0 + per < C ? k0 + per : C;
     uint32_t sum_c = 0, sum_i = 0;
-    for (uint32_t k = k0; k < k0 + per && k < C; ++k) {
-        uint32_t c = tot[k];
-        sum_c += c;
-        sum_i += (c + tpi - 1) / tpi;
+    for (uint32_t k = k0; k < k1; k += 8) {  // batches of 8 independent loads
+        uint32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = k + u < k1 ? tot[k + u] : 0u;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            sum_c += v[u];
+            sum_i += (v[u] + tpi - 1) / tpi;
+        }
     }
     uint32_t all_c, all_i;
     uint32_t pre_c = block_scan_1024(sum_c, lds, &all_c);
@@ -342,16 +348,23 @@ __global__ __launch_bounds__(1024) void k_offsets_scan(const uint32_t* __restric
     __syncthreads();
     const uint32_t sys_base = b * n;
     uint32_t run_c = pre_c, run_i = emit_work ? wl_base + pre_i : 0;
-    for (uint32_t k = k0; k < k0 + per && k < C; ++k) {
-        uint32_t c = tot[k];
-        bin_offsets[(uint64_t)b * C + k] = sys_base + run_c;
-        if (emit_work) {
-            for (uint32_t m = 0; m * tpi < c; ++m) {
-                uint32_t cnt = c - m * tpi;
-                worklist[run_i++] = make_uint2(sys_base + run_c + m * tpi, cnt < tpi ? cnt : tpi);
+    for (uint32_t k = k0; k < k1; k += 8) {
+        uint32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = k + u < k1 ? tot[k + u] : 0u;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (k + u >= k1) break;
+            const uint32_t c = v[u];
+            bin_offsets[(uint64_t)b * C + k + u] = sys_base + run_c;
+            if (emit_work) {
+                for (uint32_t m = 0; m * tpi < c; ++m) {
+                    uint32_t cnt = c - m * tpi;
+                    worklist[run_i++] = make_uint2(sys_base + run_c + m * tpi, cnt < tpi ? cnt : tpi);
+                }
             }
+            run_c += c;
         }
-        run_c += c;
     }
     // last entry = total count (every system holds n entries when the counts are per system)
     if (b == batch - 1 && threadIdx.x == 0) bin_offsets[(uint64_t)batch * C] = sys_base + all_c;

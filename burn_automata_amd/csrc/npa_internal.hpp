@@ -185,7 +185,7 @@ hipError_t launch_decode_gaussians(const float4* pos, const float* states, uint3
                                    uint32_t state_dims, const npa_gaussian_decode_cfg& cfg,
                                    float* pv, float* sh, float* rot, float* so, hipStream_t stream);
 struct SplatWorkspace {
-    DevBuf params, item_start, keys, vals, sorted, ranks, table, totals, offsets, count, flags;
+    DevBuf params, item_start, keys, vals, sorted, ranks, table, totals, offsets, count, flags, scan;
     void release();
 };
 hipError_t launch_splat_2d(const float4* pos, const float* colors, const float* states,
