@@ -436,8 +436,10 @@ __device__ __forceinline__ void write_sorted(uint32_t dst, uint32_t i, uint32_t 
 // ascending particle index inside every run (the reference's neighbour order). A bin with more
 // than kDirGroups cells keeps the reference order (dir_n = kDirGroups + 1). Also emits the wave
 // work items: <= tpi consecutive slots of one run (or of an unsplit bin).
+constexpr uint32_t kSplitWaves = 16;  // bins (waves) per k_split block
+
 template <int D>
-__global__ __launch_bounds__(256) void k_split(const float4* __restrict__ pos, const float* __restrict__ states,
+__global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, const float* __restrict__ states,
                                                uint32_t S, uint32_t n, uint32_t nbins, GridParams g,
                                                const uint32_t* __restrict__ bo,
                                                const uint32_t* __restrict__ order,
@@ -447,15 +449,13 @@ __global__ __launch_bounds__(256) void k_split(const float4* __restrict__ pos, c
                                                int4* __restrict__ dir_e, uint2* __restrict__ worklist,
                                                uint32_t* __restrict__ wl_count, uint32_t tpi) {
     constexpr uint32_t K = kDirGroups;
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t bin = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (bin >= nbins) return;  // whole wave
-    const uint32_t beg = bo[bin], end = bo[bin + 1];
-    if (beg == end) {
-        if (lane == 0) dir_n[bin] = 0;
-        return;
-    }
-    const uint32_t b = bin / g.cells;
+    __shared__ uint32_t s_items[kSplitWaves];
+    __shared__ uint32_t s_base;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t bin = blockIdx.x * kSplitWaves + wave;
+    const bool has_bin = bin < nbins;
+    const uint32_t beg = has_bin ? bo[bin] : 0u, end = has_bin ? bo[bin + 1] : 0u;
+    const uint32_t b = has_bin ? bin / g.cells : 0u;
     const uint64_t lt = lanemask_lt();
     int gx[K], gy[K], gz[K];
     uint32_t gc[K];
@@ -488,11 +488,11 @@ __global__ __launch_bounds__(256) void k_split(const float4* __restrict__ pos, c
         return gid;
     };
     // the first chunk (the whole bin for most bins) is loaded once for both passes
-    bool valid0;
-    uint32_t i0;
-    float4 p0;
-    int cf[3];
-    load(beg, valid0, i0, p0, cf);
+    bool valid0 = false;
+    uint32_t i0 = 0;
+    float4 p0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int cf[3] = {0, 0, 0};
+    if (beg < end) load(beg, valid0, i0, p0, cf);
     for (uint32_t c0 = beg; c0 < end && !over; c0 += 64) {
         bool valid = valid0;
         uint32_t i = i0;
@@ -537,8 +537,22 @@ __global__ __launch_bounds__(256) void k_split(const float4* __restrict__ pos, c
             nitems += (gc[k] + tpi - 1) / tpi;
         }
     }
-    uint32_t wbase = 0;  // first work item of this bin (used after the writes below)
-    if (lane == 0) wbase = atomicAdd(wl_count, nitems);
+    // one work-list reservation per block: the waves' item counts are summed in LDS
+    if (lane == 0) s_items[wave] = nitems;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t tot = 0;
+        for (uint32_t w = 0; w < kSplitWaves; ++w) tot += s_items[w];
+        s_base = tot ? atomicAdd(wl_count, tot) : 0u;
+    }
+    __syncthreads();
+    uint32_t wbase = s_base;  // first work item of this bin
+    for (uint32_t w = 0; w < wave; ++w) wbase += s_items[w];
+    if (!has_bin) return;
+    if (beg == end) {
+        if (lane == 0) dir_n[bin] = 0;
+        return;
+    }
     if (over) {
         for (uint32_t c0 = beg; c0 < end; c0 += 64) {
             bool valid = valid0;
@@ -548,7 +562,6 @@ __global__ __launch_bounds__(256) void k_split(const float4* __restrict__ pos, c
             if (c0 != beg) load(c0, valid, i, p4, c);
             if (valid) write_sorted<D>(c0 + lane, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
         }
-        wbase = (uint32_t)__builtin_amdgcn_readfirstlane((int)wbase);
         const uint32_t cnt = end - beg;
         for (uint32_t m = lane; m < nitems; m += 64) {
             const uint32_t left = cnt - m * tpi;
@@ -576,7 +589,6 @@ __global__ __launch_bounds__(256) void k_split(const float4* __restrict__ pos, c
         }
         if (valid) write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
     }
-    wbase = (uint32_t)__builtin_amdgcn_readfirstlane((int)wbase);
     uint32_t off = 0;
 #pragma unroll
     for (uint32_t k = 0; k < K; ++k) {
@@ -670,16 +682,16 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
         if ((e = hipGetLastError()) != hipSuccess) return e;
         if (payload) {
             const uint32_t nbins = batch * plan.cells;
-            const uint32_t sblocks = (nbins + 3) / 4;
+            const uint32_t sblocks = (nbins + kSplitWaves - 1) / kSplitWaves;
             if (g.dim == 2)
-                hipLaunchKernelGGL(k_split<2>, dim3(sblocks), dim3(256), 0, stream, pos, states, state_dims, n,
+                hipLaunchKernelGGL(k_split<2>, dim3(sblocks), dim3(64 * kSplitWaves), 0, stream, pos, states, state_dims, n,
                                    nbins, g, ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(),
                                    ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(),
                                    ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.dir_n.as<uint32_t>(),
                                    ws.dir_e.as<int4>(), ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(),
                                    plan.tpi);
             else
-                hipLaunchKernelGGL(k_split<3>, dim3(sblocks), dim3(256), 0, stream, pos, states, state_dims, n,
+                hipLaunchKernelGGL(k_split<3>, dim3(sblocks), dim3(64 * kSplitWaves), 0, stream, pos, states, state_dims, n,
                                    nbins, g, ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(),
                                    ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(),
                                    ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.dir_n.as<uint32_t>(),
