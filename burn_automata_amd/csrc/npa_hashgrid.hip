@@ -148,7 +148,7 @@ bool make_plan(const npa_grid_cfg& cfg, uint32_t batch, uint32_t n, HashgridPlan
     p.key_bits = cells <= 1 ? 0 : 32 - __builtin_clz((uint32_t)cells - 1);
     p.waves = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(4, 32768 / cells));
     p.lds_bytes = p.waves * p.cells * 2;
-    const uint64_t budget = std::max<uint64_t>(2 * (uint64_t)n, cells);
+    const uint64_t budget = std::max<uint64_t>(4 * (uint64_t)n, cells);
     uint32_t rounds = 1;
     while (rounds < 32) {
         uint64_t tile = (uint64_t)p.waves * rounds * 64;
@@ -269,17 +269,15 @@ __global__ __launch_bounds__(256) void k_table_scan(uint32_t* __restrict__ table
     uint32_t* col = table + (uint64_t)b * tiles_per_sys * C + k;
     uint32_t run = 0;
     uint32_t t = 0;
-    for (; t + 4 <= tiles_per_sys; t += 4) {
-        uint32_t v0 = col[(uint64_t)(t + 0) * C], v1 = col[(uint64_t)(t + 1) * C];
-        uint32_t v2 = col[(uint64_t)(t + 2) * C], v3 = col[(uint64_t)(t + 3) * C];
-        col[(uint64_t)(t + 0) * C] = run;
-        run += v0;
-        col[(uint64_t)(t + 1) * C] = run;
-        run += v1;
-        col[(uint64_t)(t + 2) * C] = run;
-        run += v2;
-        col[(uint64_t)(t + 3) * C] = run;
-        run += v3;
+    for (; t + 8 <= tiles_per_sys; t += 8) {  // 8 independent loads per batch
+        uint32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = col[(uint64_t)(t + u) * C];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            col[(uint64_t)(t + u) * C] = run;
+            run += v[u];
+        }
     }
     for (; t < tiles_per_sys; ++t) {
         uint32_t v = col[(uint64_t)t * C];

@@ -301,19 +301,20 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
                         if (!cell_range(P, bo, b, n0, n1, n2, beg, end, filter)) continue;
                         for (uint32_t base = beg; base < end; base += kChunk) {
                             const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
-                            for (int i0 = 0; i0 < kChunk / L; i0 += 4) {
+                            constexpr int BT = kChunk / L < 4 ? kChunk / L : 4;  // loads per batch
+                            for (int i0 = 0; i0 < kChunk / L; i0 += BT) {
                                 if ((uint32_t)(i0 * L) >= m) break;  // wave-uniform
-                                float4 rc[4];
-                                int4 cc[4];
+                                float4 rc[BT];
+                                int4 cc[BT];
 #pragma unroll
-                                for (int u = 0; u < 4; ++u) {
+                                for (int u = 0; u < BT; ++u) {
                                     const uint32_t k = q + (uint32_t)((i0 + u) * L);
                                     const uint32_t kc = k < m ? k : m - 1;
                                     rc[u] = srec[base + kc];
                                     if constexpr (D == 3) cc[u] = scoord[base + kc];
                                 }
 #pragma unroll
-                                for (int u = 0; u < 4; ++u) {
+                                for (int u = 0; u < BT; ++u) {
                                     const uint32_t k = q + (uint32_t)((i0 + u) * L);
                                     const float4 r = rc[u];
                                     bool ok = in_group & (k < m);
