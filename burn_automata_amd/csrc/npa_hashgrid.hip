@@ -396,6 +396,25 @@ __global__ __launch_bounds__(256) void k_scatter(uint32_t n, uint32_t total, uin
     inv[i] = dst_local;
 }
 
+// Copies nq (1, 2, 4, 6 or 8) float4s with every load issued before the first store.
+template <int NQ>
+__device__ __forceinline__ void copy_row4_n(float4* __restrict__ dst, const float4* __restrict__ src) {
+    float4 v[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) v[q] = src[q];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) dst[q] = v[q];
+}
+__device__ __forceinline__ void copy_row4(float4* __restrict__ dst, const float4* __restrict__ src, uint32_t nq) {
+    switch (nq) {
+        case 1: copy_row4_n<1>(dst, src); break;
+        case 2: copy_row4_n<2>(dst, src); break;
+        case 4: copy_row4_n<4>(dst, src); break;
+        case 6: copy_row4_n<6>(dst, src); break;
+        default: copy_row4_n<8>(dst, src); break;
+    }
+}
+
 // Writes particle i (global index) to sorted slot dst: snapshot entries, sorted record
 // {x, y, bits(cx), bits(cy)} (2D) or position + coordinates (3D), and the zero-padded state row.
 template <int D>
@@ -417,8 +436,7 @@ __device__ __forceinline__ void write_sorted(uint32_t dst, uint32_t i, uint32_t 
     const float* src = states + (uint64_t)i * S;
     float4* o4 = reinterpret_cast<float4*>(sstate + (uint64_t)dst * SS);
     if (S == SS) {  // rows are 16-byte aligned (checked on the host)
-        const float4* s4 = reinterpret_cast<const float4*>(src);
-        for (uint32_t q = 0; q < SS / 4; ++q) o4[q] = s4[q];
+        copy_row4(o4, reinterpret_cast<const float4*>(src), SS / 4);
     } else {
         for (uint32_t q = 0; q < SS / 4; ++q) {
             const uint32_t cc = 4 * q;
