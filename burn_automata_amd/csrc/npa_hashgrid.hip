@@ -64,6 +64,9 @@ hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t
     NPA_RES(inv, t1 * 4);
     NPA_RES(wl_count, 64);
     NPA_RES(worklist, (plan.worklist_cap + 1) * 8);
+    // second-pass items: at most one partial item per (64-slot window, cell run) pair
+    NPA_RES(act_items, (t1 / (plan.tpi ? plan.tpi : 1) + t1 / 64 + plan.worklist_cap + 2) * 16);
+    NPA_RES(act_rows, t1 * 4);
     NPA_RES(srec, t1 * 16);
     NPA_RES(scoord, dim == 3 ? t1 * 16 : 16);
     NPA_RES(sstate, t1 * (uint64_t)state_stride_for(state_dims ? state_dims : 1) * 4);
@@ -85,7 +88,7 @@ hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t
 void Workspace::release() {
     for (DevBuf* b : {&keys, &ranks, &table, &totals, &bin_offsets, &perm, &inv, &flags, &wl_count,
                       &worklist, &srec, &scoord, &sstate, &svol, &counters, &features, &wpad, &tmpidx,
-                      &dir_n, &dir_e})
+                      &dir_n, &dir_e, &act_items, &act_rows})
         b->release();
 }
 
@@ -199,7 +202,7 @@ __global__ __launch_bounds__(256) void k_hash_rank(const float4* __restrict__ po
     }
     const uint32_t nwords = waves * C;
     for (uint32_t k = threadIdx.x; k < nwords; k += blockDim.x) cnt[k] = 0;
-    if (wl_count && tile == 0 && threadIdx.x == 0) *wl_count = 0;
+    if (wl_count && tile == 0 && threadIdx.x < 4) wl_count[threadIdx.x] = 0;  // work-list counters
     __syncthreads();
 
     const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63;

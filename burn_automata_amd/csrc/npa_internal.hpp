@@ -77,6 +77,11 @@ struct Workspace {
     DevBuf keys, ranks, table, totals, bin_offsets, perm, inv, flags, wl_count, worklist;
     DevBuf srec, scoord, sstate, svol, counters, features, wpad;
     DevBuf tmpidx, dir_n, dir_e;
+    // Targets of the second pass and the update: particles whose update mask is not 0 (the others
+    // are copied to the output unchanged, as the reference's GPU update_particle does). act_items:
+    // uint4 {window base slot, target bitmask lo, hi, first compact row}; act_rows: compact row ->
+    // slot. Counts (u32 words of wl_count): [0] density items, [2] second-pass items, [3] rows.
+    DevBuf act_items, act_rows;
     hipError_t reserve(const HashgridPlan& plan, uint64_t total, uint32_t batch, uint32_t state_dims,
                        int dim, uint32_t feature_dims = 0);
     void release();

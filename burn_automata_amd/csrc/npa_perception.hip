@@ -349,6 +349,158 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
     }
 }
 
+// Position of the t-th (0-based) set bit of m; m has more than t set bits.
+__device__ __forceinline__ uint32_t nth_set_bit(uint64_t m, uint32_t t) {
+    uint32_t pos = 0;
+#pragma unroll
+    for (int w = 32; w >= 1; w >>= 1) {
+        const uint64_t low = m & ((1ull << w) - 1ull);
+        const uint32_t c = (uint32_t)__popcll(low);
+        if (t >= c) {
+            t -= c;
+            m >>= w;
+            pos += (uint32_t)w;
+        } else {
+            m = low;
+        }
+    }
+    return pos;
+}
+
+// Copies a particle's position and state row unchanged (every load issued before the stores).
+template <int NQ>
+__device__ __forceinline__ void copy_state_row(float* __restrict__ dst, const float* __restrict__ src) {
+    float4 v[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) v[q] = reinterpret_cast<const float4*>(src)[q];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) reinterpret_cast<float4*>(dst)[q] = v[q];
+}
+__device__ __forceinline__ void copy_particle(uint64_t i, uint32_t S, const float4* __restrict__ pos,
+                                              const float* __restrict__ states, float4* __restrict__ out_pos,
+                                              float* __restrict__ out_states) {
+    out_pos[i] = pos[i];
+    const float* src = states + i * S;
+    float* dst = out_states + i * S;
+    if (S == state_stride_for(S)) {  // 16-byte aligned rows (checked on the host)
+        switch (S) {
+            case 4: copy_state_row<1>(dst, src); return;
+            case 8: copy_state_row<2>(dst, src); return;
+            case 16: copy_state_row<4>(dst, src); return;
+            case 24: copy_state_row<6>(dst, src); return;
+            default: copy_state_row<8>(dst, src); return;
+        }
+    }
+    for (uint32_t c = 0; c < S; ++c) dst[c] = src[c];
+}
+
+// Targets of the second pass and the update MLP, one wave per bin (16 bins per block). A particle
+// whose update mask is 0 is copied to the step's output unchanged and gets no perception or MLP
+// work - the reference's GPU update_particle (gpu_step.wgsl:3664-3682) does the same; the CPU path
+// adds dt * ds * 0, which leaves the same values. The other particles are packed per 64-slot
+// window of a cell run into items of <= tpi targets {window base, target bitmask, first compact
+// row} and get consecutive compact rows (act_rows[row] = slot) for the feature rows and the MLP.
+// mask_mode: 0 every particle is a target (no copies), 1 the device hash mask, 2 a mask array.
+constexpr uint32_t kActWaves = 16;
+
+__global__ __launch_bounds__(1024) void k_active(StepParams P, int mask_mode, uint32_t nbins, uint32_t tpi,
+                                                 const uint32_t* __restrict__ bo,
+                                                 const uint32_t* __restrict__ perm,
+                                                 const float* __restrict__ user_mask,
+                                                 const float4* __restrict__ pos, const float* __restrict__ states,
+                                                 float4* __restrict__ out_pos, float* __restrict__ out_states,
+                                                 uint4* __restrict__ items, uint32_t* __restrict__ rows,
+                                                 uint32_t* __restrict__ counts) {
+    constexpr uint32_t K = kDirGroups;
+    __shared__ uint32_t s_it[kActWaves], s_rw[kActWaves];
+    __shared__ uint32_t s_bit, s_brw;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t bin = blockIdx.x * kActWaves + wave;
+    const bool has_bin = bin < nbins;
+    const uint32_t beg = has_bin ? bo[bin] : 0u, end = has_bin ? bo[bin + 1] : 0u;
+    const uint32_t b = has_bin ? bin / P.g.cells : 0u;
+    const uint32_t nd = beg < end ? (P.g.mode == 1 ? P.dir_n[bin] : 1u) : 0u;
+    const uint32_t nr = nd == 0 ? 0u : (nd > K ? 1u : nd);  // runs (an unsplit bin is one run)
+    const uint64_t lt = lanemask_lt();
+    auto run = [&](uint32_t k, uint32_t& rs, uint32_t& re) {
+        if (P.g.mode != 1 || nd > K) {
+            rs = beg;
+            re = end;
+        } else {
+            const int4* e = P.dir_e + (uint64_t)bin * K;
+            rs = (uint32_t)e[k].w;
+            re = k + 1 < nd ? (uint32_t)e[k + 1].w : end;
+        }
+    };
+    auto target = [&](bool valid, uint32_t li) -> bool {
+        if (!valid) return false;
+        if (mask_mode == 0) return true;
+        const float m = mask_mode == 1 ? hash_mask(li, b, P.N, P.update_prob, P.step_index, P.base_seed)
+                                       : user_mask[(uint64_t)b * P.N + li];
+        return m != 0.0f;
+    };
+    uint32_t nit = 0, nrw = 0;
+    for (uint32_t k = 0; k < nr; ++k) {
+        uint32_t rs, re;
+        run(k, rs, re);
+        for (uint32_t w0 = rs; w0 < re; w0 += 64) {
+            const bool valid = w0 + lane < re;
+            const uint32_t li = perm[valid ? w0 + lane : rs];
+            const uint32_t na = (uint32_t)__popcll(__ballot(target(valid, li)));
+            nit += (na + tpi - 1) / tpi;
+            nrw += na;
+        }
+    }
+    if (lane == 0) {
+        s_it[wave] = nit;
+        s_rw[wave] = nrw;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t ti = 0, tr = 0;
+        for (uint32_t w = 0; w < kActWaves; ++w) {
+            ti += s_it[w];
+            tr += s_rw[w];
+        }
+        unsigned long long both = 0;
+        if (ti | tr)
+            both = atomicAdd(reinterpret_cast<unsigned long long*>(counts + 2),
+                             ((unsigned long long)tr << 32) | (unsigned long long)ti);
+        s_bit = (uint32_t)both;
+        s_brw = (uint32_t)(both >> 32);
+    }
+    __syncthreads();
+    uint32_t ib = s_bit, rb = s_brw;
+    for (uint32_t w = 0; w < wave; ++w) {
+        ib += s_it[w];
+        rb += s_rw[w];
+    }
+    for (uint32_t k = 0; k < nr; ++k) {
+        uint32_t rs, re;
+        run(k, rs, re);
+        for (uint32_t w0 = rs; w0 < re; w0 += 64) {
+            const uint32_t slot = w0 + lane;
+            const bool valid = slot < re;
+            const uint32_t li = perm[valid ? slot : rs];
+            const bool act = target(valid, li);
+            const uint64_t am = __ballot(act);
+            const uint32_t rank = (uint32_t)__popcll(am & lt);
+            if (act) rows[rb + rank] = slot;
+            else if (valid && mask_mode != 0)  // masked out: copied unchanged
+                copy_particle((uint64_t)b * P.N + li, P.S, pos, states, out_pos, out_states);
+            const uint32_t na = (uint32_t)__popcll(am);
+            const uint32_t ni = (na + tpi - 1) / tpi;
+            const uint32_t jr = rank / tpi;
+            for (uint32_t j = 0; j < ni; ++j) {
+                const uint64_t sub = __ballot(act && jr == j);
+                if (lane == 0) items[ib + j] = make_uint4(w0, (uint32_t)sub, (uint32_t)(sub >> 32), rb + j * tpi);
+            }
+            ib += ni;
+            rb += na;
+        }
+    }
+}
+
 // Per-wave accepted-neighbour lists of the second pass. Entry = (chunk id << 6) | k, the k-th
 // candidate of the chunk whose first sorted slot is chunk_base[chunk id]; entries of a target are
 // appended in visit order (cells dz, dy, dx; slots ascending), so walking a list front to back
@@ -397,7 +549,7 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                                                  const float* __restrict__ svol,
                                                  const uint32_t* __restrict__ bo,
                                                  const uint32_t* __restrict__ perm,
-                                                 const uint2* __restrict__ wl,
+                                                 const uint4* __restrict__ wl,
                                                  const uint32_t* __restrict__ wl_count,
                                                  float* __restrict__ sfeatures, StepIO io) {
     constexpr int L = LanesPerTarget<SM>::L;
@@ -416,9 +568,11 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
     const bool branch_a = want_sg && want_dg;
     const uint64_t my_residue = residue_mask<L>(q);
     for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
-        const uint2 item = wl[it];
-        const bool active = t < item.y;
-        const uint32_t s = item.x + (active ? t : 0u);
+        const uint4 item = wl[it];
+        const uint64_t tmask = ((uint64_t)item.z << 32) | item.y;
+        const bool active = t < (uint32_t)__popcll(tmask);
+        const uint32_t s = item.x + (active ? nth_set_bit(tmask, t) : 0u);
+        const uint32_t row = item.w + t;  // compact feature row
         const uint32_t b = item.x / P.N;
         float pi[3];
         int ci[3];
@@ -692,7 +846,7 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
             // padded layout [si SM][blur SM][grad SM*D][rest], feature-major; rest holds the
             // density gradient and/or position (runtime count) followed by zeros.
             const uint32_t T = P.T;
-            float* f = sfeatures + s;
+            float* f = sfeatures + row;
 #pragma unroll
             for (int c = 0; c < CPL; ++c) f[(uint64_t)(c0 + c) * T] = si[c];
 #pragma unroll
@@ -815,6 +969,8 @@ template <int D, int SM, int FM>
 __global__ __launch_bounds__(256) void k_mlp_euler(StepParams P, const float* __restrict__ sfeatures,
                                                    const float* __restrict__ sstate,
                                                    const uint32_t* __restrict__ perm,
+                                                   const uint32_t* __restrict__ act_rows,
+                                                   const uint32_t* __restrict__ row_count,
                                                    const float* __restrict__ wpad, StepIO io) {
     constexpr int OP = (D + SM + 3) / 4 * 4;
     constexpr int OPW = OP / 4;
@@ -830,12 +986,15 @@ __global__ __launch_bounds__(256) void k_mlp_euler(StepParams P, const float* __
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t row0 = blockIdx.x * 64;
-    const uint32_t s = row0 + lane;
-    const bool valid = s < T;
+    const uint32_t nrows = *row_count;
+    if (row0 >= nrows) return;  // whole block
+    const uint32_t row = row0 + lane;
+    const bool valid = row < nrows;
+    const uint32_t s = act_rows[valid ? row : row0];  // sorted slot of this row's particle
 
     float f[FM];
 #pragma unroll
-    for (int k = 0; k < FM; ++k) f[k] = valid ? sfeatures[(uint64_t)k * T + s] : 0.0f;
+    for (int k = 0; k < FM; ++k) f[k] = valid ? sfeatures[(uint64_t)k * T + row] : 0.0f;
 
     // phase 1: hidden units
     for (uint32_t hb = wave * 32; hb < HP; hb += 128) {
@@ -1119,8 +1278,8 @@ static void launch_perceive_f(const StepParams& p, Workspace& ws, const StepIO& 
                               hipStream_t stream) {
     hipLaunchKernelGGL((k_perceive<D, SM, MODE, FL>), dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
                        ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.svol.as<float>(),
-                       ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), ws.worklist.as<uint2>(),
-                       ws.wl_count.as<uint32_t>(), ws.features.as<float>(), io);
+                       ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), ws.act_items.as<uint4>(),
+                       ws.wl_count.as<uint32_t>() + 2, ws.features.as<float>(), io);
 }
 
 // The rollout step's usual option sets run a specialised kernel; anything else reads the flags.
@@ -1176,7 +1335,8 @@ static hipError_t launch_mlp_t(const StepParams& p, Workspace& ws, const StepIO&
     }
     const uint32_t blocks = (p.T + 63) / 64;
     hipLaunchKernelGGL((k_mlp_euler<D, SM, FM>), dim3(blocks), dim3(256), lds, stream, p, ws.features.as<float>(),
-                       ws.sstate.as<float>(), ws.perm.as<uint32_t>(), ws.wpad.as<float>(), io);
+                       ws.sstate.as<float>(), ws.perm.as<uint32_t>(), ws.act_rows.as<uint32_t>(),
+                       ws.wl_count.as<uint32_t>() + 3, ws.wpad.as<float>(), io);
     return hipGetLastError();
 }
 
@@ -1205,6 +1365,13 @@ hipError_t launch_update(const StepParams& p_in, Workspace& ws, const StepIO& io
     const int blocks = grid_blocks * 4;  // one wave per block
     {
         ProfScope ps(prof, NPA_KERNEL_PERCEIVE, stream);
+        const int mask_mode = mode != 0 ? 0 : io.mask ? 2 : (p.update_prob < 1.0f ? 1 : 0);
+        const uint32_t nbins = p.B * p.g.cells;
+        hipLaunchKernelGGL(k_active, dim3((nbins + kActWaves - 1) / kActWaves), dim3(64 * kActWaves), 0, stream, p,
+                           mask_mode, nbins, targets_per_item(p.SS), ws.bin_offsets.as<uint32_t>(),
+                           ws.perm.as<uint32_t>(), io.mask, io.pos, io.states, io.out_pos, io.out_states,
+                           ws.act_items.as<uint4>(), ws.act_rows.as<uint32_t>(), ws.wl_count.as<uint32_t>());
+        if (hipError_t e0 = hipGetLastError(); e0 != hipSuccess) return e0;
         if (p.g.dim == 2) {
             if (mode == 0) launch_perceive_d<2, 0>(p, ws, io, blocks, stream);
             else launch_perceive_d<2, 1>(p, ws, io, blocks, stream);
