@@ -27,7 +27,7 @@ NPA_ERR_COORD_OVERFLOW = 32
 
 # kernel ids for npa_profile_read
 KERNEL_NAMES = ("hash_rank", "table_scan", "offsets_scan", "scatter", "density", "perceive", "splat",
-                "mlp")
+                "mlp", "split", "active")
 
 
 class NpaGridCfg(C.Structure):

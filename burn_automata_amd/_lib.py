@@ -59,7 +59,7 @@ def _decl(L):
     L.npa_profile_enable.argtypes = [P, C.c_int]
     L.npa_profile_reset.argtypes = [P]
     L.npa_profile_read.argtypes = [P, C.c_int, ptr(C.c_double), ptr(u64)]
-    L.npa_state_pair_counts.argtypes = [P, ptr(u64), ptr(u64)]
+    L.npa_state_pair_counts.argtypes = [P, ptr(u64), ptr(u64), ptr(u64), ptr(u64), ptr(u64)]
     for name in ("npa_context_create", "npa_context_set_stream", "npa_context_set_host_io",
                  "npa_context_synchronize", "npa_build_hashgrid", "npa_neighbor_lists",
                  "npa_perceive", "npa_mlp_forward", "npa_euler_step", "npa_step",

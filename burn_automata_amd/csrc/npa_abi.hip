@@ -873,23 +873,30 @@ npa_status npa_state_decode_gaussians_3d(npa_state* s, const npa_gaussian_decode
     return NPA_OK;
 }
 
-npa_status npa_state_pair_counts(npa_state* s, uint64_t* candidates, uint64_t* pairs) {
+npa_status npa_state_pair_counts(npa_state* s, uint64_t* candidates, uint64_t* pairs, uint64_t* targets,
+                                 uint64_t* target_candidates, uint64_t* target_pairs) {
     if (!s) return NPA_ERR_INVALID_ARGUMENT;
     npa_context* ctx = s->ctx;
     if (set_device(ctx)) return NPA_ERR_DEVICE;
     const uint32_t S = s->model.state_dims;
     npa::StepParams p = make_params(s->grid, opts_for_model(s->model), s->B, s->N, S);
+    p.update_prob = s->update_prob;
+    p.base_seed = base_seed(s->seed);
+    p.step_index = (uint32_t)s->step_index;
     NPA_HIP(ctx, npa::launch_hashgrid(s->plan, p.g, s->pos[s->cur].as<float4>(), s->states[s->cur].as<float>(), S,
                                       s->B, s->N, s->ws, true, ctx->stream, nullptr),
             "hashgrid");
-    NPA_HIP(ctx, hipMemsetAsync(s->ws.counters.ptr, 0, 16, ctx->stream), "zero counters");
+    NPA_HIP(ctx, hipMemsetAsync(s->ws.counters.ptr, 0, 40, ctx->stream), "zero counters");
     NPA_HIP(ctx, npa::launch_count_pairs(p, s->ws, s->grid_blocks, s->ws.counters.as<unsigned long long>(), ctx->stream),
             "count");
-    unsigned long long h[2] = {0, 0};
-    NPA_HIP(ctx, hipMemcpyAsync(h, s->ws.counters.ptr, 16, hipMemcpyDeviceToHost, ctx->stream), "readback");
+    unsigned long long h[5] = {0, 0, 0, 0, 0};
+    NPA_HIP(ctx, hipMemcpyAsync(h, s->ws.counters.ptr, 40, hipMemcpyDeviceToHost, ctx->stream), "readback");
     NPA_HIP(ctx, hipStreamSynchronize(ctx->stream), "sync");
     if (candidates) *candidates = h[0];
     if (pairs) *pairs = h[1];
+    if (targets) *targets = h[2];
+    if (target_candidates) *target_candidates = h[3];
+    if (target_pairs) *target_pairs = h[4];
     return NPA_OK;
 }
 
@@ -930,6 +937,18 @@ hipEvent_t Profiler::get() {
     hipEvent_t e = nullptr;
     if (hipEventCreate(&e) != hipSuccess) return nullptr;
     return e;
+}
+
+bool Profiler::pick(int kernel, hipEvent_t* a, hipEvent_t* b) {
+    *a = get();
+    if (!*a) return false;
+    *b = get();
+    if (!*b) {
+        pool.push_back(*a);
+        return false;
+    }
+    pending.push_back({*a, *b, kernel});
+    return true;
 }
 
 void Profiler::begin(int kernel, hipStream_t s, hipEvent_t* ev) {

@@ -630,7 +630,7 @@ static hipError_t launch_rank_r(uint32_t blocks, uint32_t waves, uint32_t lds_by
                                 uint32_t tiles_per_sys, uint32_t key_bits, const GridParams& g,
                                 const float4* pos, const uint32_t* keys_in, const uint32_t* d_count,
                                 uint32_t n, uint32_t* keys, uint32_t* ranks, uint32_t* table,
-                                uint32_t* flags, uint32_t* wl_count, hipStream_t stream) {
+                                uint32_t* flags, uint32_t* wl_count, hipStream_t stream, Profiler* prof) {
     static uint32_t attr_bytes = 32768;
     if (lds_bytes > attr_bytes) {
         hipError_t e = hipFuncSetAttribute((const void*)k_hash_rank<R>,
@@ -638,20 +638,19 @@ static hipError_t launch_rank_r(uint32_t blocks, uint32_t waves, uint32_t lds_by
         if (e != hipSuccess) return e;
         attr_bytes = lds_bytes;
     }
-    hipLaunchKernelGGL(k_hash_rank<R>, dim3(blocks), dim3(waves * 64), lds_bytes, stream, pos, keys_in,
-                       d_count, n, tiles_per_sys, waves, g, key_bits, keys, ranks, table, flags,
-                       wl_count);
-    return hipGetLastError();
+    return launch_timed(prof, NPA_KERNEL_HASH_RANK, k_hash_rank<R>, dim3(blocks), dim3(waves * 64), lds_bytes, stream,
+                        pos, keys_in, d_count, n, tiles_per_sys, waves, g, key_bits, keys, ranks, table, flags,
+                        wl_count);
 }
 
 static hipError_t launch_rank(uint32_t rounds, uint32_t blocks, uint32_t waves, uint32_t lds_bytes,
                               uint32_t tiles_per_sys, uint32_t key_bits, const GridParams& g,
                               const float4* pos, const uint32_t* keys_in, const uint32_t* d_count,
                               uint32_t n, uint32_t* keys, uint32_t* ranks, uint32_t* table,
-                              uint32_t* flags, uint32_t* wl_count, hipStream_t stream) {
+                              uint32_t* flags, uint32_t* wl_count, hipStream_t stream, Profiler* prof) {
 #define NPA_RANK(RR)                                                                             \
     return launch_rank_r<RR>(blocks, waves, lds_bytes, tiles_per_sys, key_bits, g, pos, keys_in, \
-                             d_count, n, keys, ranks, table, flags, wl_count, stream)
+                             d_count, n, keys, ranks, table, flags, wl_count, stream, prof)
     switch (rounds) {
         case 1: NPA_RANK(1);
         case 2: NPA_RANK(2);
@@ -667,59 +666,33 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                            const float* states, uint32_t state_dims, uint32_t batch, uint32_t n,
                            Workspace& ws, bool payload, hipStream_t stream, Profiler* prof) {
     const uint64_t total = (uint64_t)batch * n;
-    hipError_t e = hipSuccess;
-    {
-        ProfScope ps(prof, NPA_KERNEL_HASH_RANK, stream);
-        e = launch_rank(plan.rounds, batch * plan.tiles_per_sys, plan.waves, plan.lds_bytes,
-                        plan.tiles_per_sys, plan.key_bits, g, pos, nullptr, nullptr, n,
-                        ws.keys.as<uint32_t>(), ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(),
-                        ws.flags.as<uint32_t>(), ws.wl_count.as<uint32_t>(), stream);
-    }
+    hipError_t e = launch_rank(plan.rounds, batch * plan.tiles_per_sys, plan.waves, plan.lds_bytes,
+                               plan.tiles_per_sys, plan.key_bits, g, pos, nullptr, nullptr, n, ws.keys.as<uint32_t>(),
+                               ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(), ws.flags.as<uint32_t>(),
+                               ws.wl_count.as<uint32_t>(), stream, prof);
     if (e != hipSuccess) return e;
-    {
-        ProfScope ps(prof, NPA_KERNEL_TABLE_SCAN, stream);
-        hipLaunchKernelGGL(k_table_scan, dim3((plan.cells + 255) / 256, batch), dim3(256), 0, stream,
-                           ws.table.as<uint32_t>(), ws.totals.as<uint32_t>(), plan.cells,
-                           plan.tiles_per_sys);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-    }
-    {
-        ProfScope ps(prof, NPA_KERNEL_OFFSETS_SCAN, stream);
-        hipLaunchKernelGGL(k_offsets_scan, dim3(batch), dim3(1024), 0, stream,
-                           ws.totals.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), plan.cells, n,
-                           batch, ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), 0, plan.tpi);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-    }
-    {
-        ProfScope ps(prof, NPA_KERNEL_SCATTER, stream);
-        const uint32_t blocks = (uint32_t)((total + 255) / 256);
-        hipLaunchKernelGGL(k_scatter, dim3(blocks), dim3(256), 0, stream, n, (uint32_t)total, plan.tile,
-                           plan.tiles_per_sys, plan.cells, ws.keys.as<uint32_t>(), ws.ranks.as<uint32_t>(),
-                           ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(),
-                           payload ? ws.tmpidx.as<uint32_t>() : ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(),
-                           payload ? 1 : 0);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        if (payload) {
-            const uint32_t nbins = batch * plan.cells;
-            const uint32_t sblocks = (nbins + kSplitWaves - 1) / kSplitWaves;
-            if (g.dim == 2)
-                hipLaunchKernelGGL(k_split<2>, dim3(sblocks), dim3(64 * kSplitWaves), 0, stream, pos, states, state_dims, n,
-                                   nbins, g, ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(),
-                                   ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(),
-                                   ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.dir_n.as<uint32_t>(),
-                                   ws.dir_e.as<int4>(), ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(),
-                                   plan.tpi);
-            else
-                hipLaunchKernelGGL(k_split<3>, dim3(sblocks), dim3(64 * kSplitWaves), 0, stream, pos, states, state_dims, n,
-                                   nbins, g, ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(),
-                                   ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(),
-                                   ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.dir_n.as<uint32_t>(),
-                                   ws.dir_e.as<int4>(), ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(),
-                                   plan.tpi);
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-        }
-    }
-    return hipSuccess;
+    e = launch_timed(prof, NPA_KERNEL_TABLE_SCAN, k_table_scan, dim3((plan.cells + 255) / 256, batch), dim3(256), 0,
+                     stream, ws.table.as<uint32_t>(), ws.totals.as<uint32_t>(), plan.cells, plan.tiles_per_sys);
+    if (e != hipSuccess) return e;
+    e = launch_timed(prof, NPA_KERNEL_OFFSETS_SCAN, k_offsets_scan, dim3(batch), dim3(1024), 0, stream,
+                     ws.totals.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), plan.cells, n, batch,
+                     ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), 0, plan.tpi);
+    if (e != hipSuccess) return e;
+    const uint32_t blocks = (uint32_t)((total + 255) / 256);
+    e = launch_timed(prof, NPA_KERNEL_SCATTER, k_scatter, dim3(blocks), dim3(256), 0, stream, n, (uint32_t)total,
+                     plan.tile, plan.tiles_per_sys, plan.cells, ws.keys.as<uint32_t>(), ws.ranks.as<uint32_t>(),
+                     ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(),
+                     payload ? ws.tmpidx.as<uint32_t>() : ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(),
+                     payload ? 1 : 0);
+    if (e != hipSuccess || !payload) return e;
+    const uint32_t nbins = batch * plan.cells;
+    const uint32_t sblocks = (nbins + kSplitWaves - 1) / kSplitWaves;
+    auto split = g.dim == 2 ? k_split<2> : k_split<3>;
+    return launch_timed(prof, NPA_KERNEL_SPLIT, split, dim3(sblocks), dim3(64 * kSplitWaves), 0, stream, pos, states,
+                        state_dims, n, nbins, g, ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(),
+                        ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(), ws.scoord.as<int4>(),
+                        ws.sstate.as<float>(), ws.dir_n.as<uint32_t>(), ws.dir_e.as<int4>(),
+                        ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), plan.tpi);
 }
 
 // ------------------------------------------------------ generic key sort
@@ -768,7 +741,7 @@ hipError_t launch_key_sort(const HashgridPlan& p, const uint32_t* keys, const ui
     g.cells = p.cells;
     hipError_t e = launch_rank(p.rounds, p.tiles_per_sys, p.waves, p.lds_bytes, p.tiles_per_sys,
                                p.key_bits, g, nullptr, keys, d_count, cap, nullptr, ranks, table,
-                               flags, nullptr, stream);
+                               flags, nullptr, stream, nullptr);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_table_scan, dim3((p.cells + 255) / 256, 1), dim3(256), 0, stream, table, totals,
                        p.cells, p.tiles_per_sys);

@@ -1,6 +1,7 @@
 // npa_internal.hpp - host-side interfaces between the library's translation units.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -32,6 +33,9 @@ struct Profiler {
     double total_ms[NPA_KERNEL_COUNT] = {0};
     uint64_t launches[NPA_KERNEL_COUNT] = {0};
     hipEvent_t get();
+    bool selects(int kernel) const { return enabled && ((mask >> kernel) & 1u); }
+    // Start/stop events for one launch of `kernel`, queued for collect(); false when unavailable.
+    bool pick(int kernel, hipEvent_t* a, hipEvent_t* b);
     void begin(int kernel, hipStream_t s, hipEvent_t* ev);
     void end(int kernel, hipStream_t s, hipEvent_t ev);
     hipError_t collect();  // synchronizes pending events into the totals
@@ -39,6 +43,21 @@ struct Profiler {
     ~Profiler();
 };
 
+// Launches `kernel`; when the profiler selects `kernel_id`, through hipExtLaunchKernelGGL with
+// start/stop events that the dispatch itself timestamps, so the recorded time is the kernel's
+// execution alone (no queue gaps or launch overhead).
+template <class F, class... Args>
+inline hipError_t launch_timed(Profiler* prof, int kernel_id, F kernel, dim3 grid, dim3 block, uint32_t shmem,
+                               hipStream_t stream, Args... args) {
+    hipEvent_t a = nullptr, b = nullptr;
+    if (prof && prof->selects(kernel_id) && prof->pick(kernel_id, &a, &b))
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, a, b, 0u, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, shmem, stream, args...);
+    return hipGetLastError();
+}
+
+// Brackets a multi-kernel sequence with events recorded on the stream.
 struct ProfScope {
     Profiler* p;
     int kernel;

@@ -1182,21 +1182,26 @@ __global__ __launch_bounds__(256) void k_update_mask(uint32_t batch, uint32_t n,
     mask[i] = hash_mask(li, b, n, p, step, base_seed);
 }
 
-// Candidates visited / pairs accepted by the neighbour walk (diagnostic, not on the step path).
+// Candidates visited / pairs accepted by the neighbour walk (diagnostic, not on the step path):
+// counters[0..1] over every particle (the density pass), counters[2..4] the targets of the step's
+// hash update mask (P.update_prob, P.step_index), i.e. the second pass and the update MLP:
+// [2] targets, [3] their candidates, [4] their pairs.
 template <int D>
 __global__ __launch_bounds__(256) void k_count_pairs(StepParams P, const float4* __restrict__ srec,
                                                      const int4* __restrict__ scoord,
                                                      const uint32_t* __restrict__ bo,
+                                                     const uint32_t* __restrict__ perm,
                                                      const uint2* __restrict__ wl,
                                                      const uint32_t* __restrict__ wl_count,
                                                      unsigned long long* __restrict__ counters) {
-    unsigned long long cand = 0, pairs = 0;
+    unsigned long long cand = 0, pairs = 0, targets = 0, tcand = 0, tpairs = 0;
     {
         NPA_WAVE_LOOP_BEGIN(wl, wl_count)
         const uint32_t b = s / P.N;
         float pi[3];
         int ci[3];
         load_rec<D>(srec, scoord, s, pi, ci);
+        unsigned long long c = 0, pr = 0;
         constexpr int ZLO = D == 3 ? -1 : 0, ZHI = D == 3 ? 1 : 0;
         for (int dz = ZLO; dz <= ZHI; ++dz)
             for (int dy = -1; dy <= 1; ++dy)
@@ -1205,13 +1210,23 @@ __global__ __launch_bounds__(256) void k_count_pairs(StepParams P, const float4*
                     if (!cell_index((int64_t)ci[0] + dx, (int64_t)ci[1] + dy, (int64_t)ci[2] + dz, P.g, &cell))
                         continue;
                     const uint64_t bin = (uint64_t)b * P.g.cells + cell;
-                    cand += bo[bin + 1] - bo[bin];
+                    c += bo[bin + 1] - bo[bin];
                 }
-        walk_neighbors<D>(P.g, b, pi, ci, bo, srec, scoord, [&](uint32_t, const float*, float) { pairs += 1; });
+        walk_neighbors<D>(P.g, b, pi, ci, bo, srec, scoord, [&](uint32_t, const float*, float) { pr += 1; });
+        cand += c;
+        pairs += pr;
+        if (hash_mask(perm[s], b, P.N, P.update_prob, P.step_index, P.base_seed) != 0.0f) {
+            targets += 1;
+            tcand += c;
+            tpairs += pr;
+        }
         NPA_WAVE_LOOP_END
     }
     atomicAdd(&counters[0], cand);
     atomicAdd(&counters[1], pairs);
+    atomicAdd(&counters[2], targets);
+    atomicAdd(&counters[3], tcand);
+    atomicAdd(&counters[4], tpairs);
 }
 
 // Neighbour lists in reference order; write=0 stores per-particle counts, write=1 fills
@@ -1242,18 +1257,20 @@ __global__ __launch_bounds__(256) void k_neighbor_lists(StepParams P, const floa
 
 // ------------------------------------------------------------------ launch
 template <int D, int L>
-static void launch_density_t(const StepParams& p, Workspace& ws, float* density_out, int blocks, hipStream_t stream) {
-    hipLaunchKernelGGL((k_density<D, L>), dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
+static void launch_density_t(const StepParams& p, Workspace& ws, float* density_out, int blocks, hipStream_t stream,
+                             Profiler* prof) {
+    launch_timed(prof, NPA_KERNEL_DENSITY, k_density<D, L>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
                        ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
                        ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.svol.as<float>(), density_out);
 }
 
 template <int D>
-static void launch_density_d(const StepParams& p, Workspace& ws, float* density_out, int blocks, hipStream_t stream) {
+static void launch_density_d(const StepParams& p, Workspace& ws, float* density_out, int blocks, hipStream_t stream,
+                             Profiler* prof) {
     const uint32_t L = lanes_per_target(p.SS);
-    if (L == 1) launch_density_t<D, 1>(p, ws, density_out, blocks, stream);
-    else if (L == 2) launch_density_t<D, 2>(p, ws, density_out, blocks, stream);
-    else launch_density_t<D, 4>(p, ws, density_out, blocks, stream);
+    if (L == 1) launch_density_t<D, 1>(p, ws, density_out, blocks, stream, prof);
+    else if (L == 2) launch_density_t<D, 2>(p, ws, density_out, blocks, stream, prof);
+    else launch_density_t<D, 4>(p, ws, density_out, blocks, stream, prof);
 }
 
 static StepParams with_directory(const StepParams& p, const Workspace& ws) {
@@ -1265,18 +1282,17 @@ static StepParams with_directory(const StepParams& p, const Workspace& ws) {
 
 hipError_t launch_density(const StepParams& p_in, Workspace& ws, float* density_out, int grid_blocks,
                           hipStream_t stream, Profiler* prof) {
-    ProfScope ps(prof, NPA_KERNEL_DENSITY, stream);
     const StepParams p = with_directory(p_in, ws);
     const int blocks = grid_blocks * 4;  // one wave per block
-    if (p.g.dim == 2) launch_density_d<2>(p, ws, density_out, blocks, stream);
-    else launch_density_d<3>(p, ws, density_out, blocks, stream);
+    if (p.g.dim == 2) launch_density_d<2>(p, ws, density_out, blocks, stream, prof);
+    else launch_density_d<3>(p, ws, density_out, blocks, stream, prof);
     return hipGetLastError();
 }
 
 template <int D, int SM, int MODE, int FL>
 static void launch_perceive_f(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
-                              hipStream_t stream) {
-    hipLaunchKernelGGL((k_perceive<D, SM, MODE, FL>), dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
+                              hipStream_t stream, Profiler* prof) {
+    launch_timed(prof, NPA_KERNEL_PERCEIVE, k_perceive<D, SM, MODE, FL>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
                        ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.svol.as<float>(),
                        ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), ws.act_items.as<uint4>(),
                        ws.wl_count.as<uint32_t>() + 2, ws.features.as<float>(), io);
@@ -1285,24 +1301,24 @@ static void launch_perceive_f(const StepParams& p, Workspace& ws, const StepIO& 
 // The rollout step's usual option sets run a specialised kernel; anything else reads the flags.
 template <int D, int SM, int MODE>
 static void launch_perceive_t(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
-                              hipStream_t stream) {
+                              hipStream_t stream, Profiler* prof) {
     if (MODE == 0 && p.state_grad && p.hybrid && !p.density_grad)
-        launch_perceive_f<D, SM, MODE, 5>(p, ws, io, blocks, stream);
+        launch_perceive_f<D, SM, MODE, 5>(p, ws, io, blocks, stream, prof);
     else if (MODE == 0 && p.state_grad && p.hybrid && p.density_grad)
-        launch_perceive_f<D, SM, MODE, 7>(p, ws, io, blocks, stream);
+        launch_perceive_f<D, SM, MODE, 7>(p, ws, io, blocks, stream, prof);
     else
-        launch_perceive_f<D, SM, MODE, -1>(p, ws, io, blocks, stream);
+        launch_perceive_f<D, SM, MODE, -1>(p, ws, io, blocks, stream, prof);
 }
 
 template <int D, int MODE>
 static void launch_perceive_d(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
-                              hipStream_t stream) {
+                              hipStream_t stream, Profiler* prof) {
     switch (p.SS) {
-        case 4: launch_perceive_t<D, 4, MODE>(p, ws, io, blocks, stream); break;
-        case 8: launch_perceive_t<D, 8, MODE>(p, ws, io, blocks, stream); break;
-        case 16: launch_perceive_t<D, 16, MODE>(p, ws, io, blocks, stream); break;
-        case 24: launch_perceive_t<D, 24, MODE>(p, ws, io, blocks, stream); break;
-        default: launch_perceive_t<D, 32, MODE>(p, ws, io, blocks, stream); break;
+        case 4: launch_perceive_t<D, 4, MODE>(p, ws, io, blocks, stream, prof); break;
+        case 8: launch_perceive_t<D, 8, MODE>(p, ws, io, blocks, stream, prof); break;
+        case 16: launch_perceive_t<D, 16, MODE>(p, ws, io, blocks, stream, prof); break;
+        case 24: launch_perceive_t<D, 24, MODE>(p, ws, io, blocks, stream, prof); break;
+        default: launch_perceive_t<D, 32, MODE>(p, ws, io, blocks, stream, prof); break;
     }
 }
 
@@ -1322,7 +1338,8 @@ hipError_t launch_pad_weights(const StepParams& p, const float* w1, const float*
 }
 
 template <int D, int SM, int FM>
-static hipError_t launch_mlp_t(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream) {
+static hipError_t launch_mlp_t(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream,
+                               Profiler* prof) {
     constexpr int OP = (D + SM + 3) / 4 * 4;
     const size_t HP = (p.H + 127) / 128 * 128;
     const size_t lds = (HP * 64 + 64 * (OP + 1)) * 4;
@@ -1334,28 +1351,29 @@ static hipError_t launch_mlp_t(const StepParams& p, Workspace& ws, const StepIO&
         attr = lds;
     }
     const uint32_t blocks = (p.T + 63) / 64;
-    hipLaunchKernelGGL((k_mlp_euler<D, SM, FM>), dim3(blocks), dim3(256), lds, stream, p, ws.features.as<float>(),
-                       ws.sstate.as<float>(), ws.perm.as<uint32_t>(), ws.act_rows.as<uint32_t>(),
-                       ws.wl_count.as<uint32_t>() + 3, ws.wpad.as<float>(), io);
-    return hipGetLastError();
+    return launch_timed(prof, NPA_KERNEL_MLP, k_mlp_euler<D, SM, FM>, dim3(blocks), dim3(256), (uint32_t)lds, stream,
+                        p, ws.features.as<float>(), ws.sstate.as<float>(), ws.perm.as<uint32_t>(),
+                        ws.act_rows.as<uint32_t>(), ws.wl_count.as<uint32_t>() + 3, ws.wpad.as<float>(), io);
 }
 
 template <int D, int SM>
-static hipError_t launch_mlp_sm(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream) {
+static hipError_t launch_mlp_sm(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream,
+                                Profiler* prof) {
     constexpr int base = 2 * SM + SM * D;
-    if (p.FP == (uint32_t)base) return launch_mlp_t<D, SM, base>(p, ws, io, stream);
-    if (p.FP == (uint32_t)base + 4) return launch_mlp_t<D, SM, base + 4>(p, ws, io, stream);
-    return launch_mlp_t<D, SM, base + 8>(p, ws, io, stream);
+    if (p.FP == (uint32_t)base) return launch_mlp_t<D, SM, base>(p, ws, io, stream, prof);
+    if (p.FP == (uint32_t)base + 4) return launch_mlp_t<D, SM, base + 4>(p, ws, io, stream, prof);
+    return launch_mlp_t<D, SM, base + 8>(p, ws, io, stream, prof);
 }
 
 template <int D>
-static hipError_t launch_mlp_d(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream) {
+static hipError_t launch_mlp_d(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream,
+                               Profiler* prof) {
     switch (p.SS) {
-        case 4: return launch_mlp_sm<D, 4>(p, ws, io, stream);
-        case 8: return launch_mlp_sm<D, 8>(p, ws, io, stream);
-        case 16: return launch_mlp_sm<D, 16>(p, ws, io, stream);
-        case 24: return launch_mlp_sm<D, 24>(p, ws, io, stream);
-        default: return launch_mlp_sm<D, 32>(p, ws, io, stream);
+        case 4: return launch_mlp_sm<D, 4>(p, ws, io, stream, prof);
+        case 8: return launch_mlp_sm<D, 8>(p, ws, io, stream, prof);
+        case 16: return launch_mlp_sm<D, 16>(p, ws, io, stream, prof);
+        case 24: return launch_mlp_sm<D, 24>(p, ws, io, stream, prof);
+        default: return launch_mlp_sm<D, 32>(p, ws, io, stream, prof);
     }
 }
 
@@ -1363,28 +1381,25 @@ hipError_t launch_update(const StepParams& p_in, Workspace& ws, const StepIO& io
                          hipStream_t stream, Profiler* prof) {
     const StepParams p = with_directory(p_in, ws);
     const int blocks = grid_blocks * 4;  // one wave per block
-    {
-        ProfScope ps(prof, NPA_KERNEL_PERCEIVE, stream);
-        const int mask_mode = mode != 0 ? 0 : io.mask ? 2 : (p.update_prob < 1.0f ? 1 : 0);
-        const uint32_t nbins = p.B * p.g.cells;
-        hipLaunchKernelGGL(k_active, dim3((nbins + kActWaves - 1) / kActWaves), dim3(64 * kActWaves), 0, stream, p,
-                           mask_mode, nbins, targets_per_item(p.SS), ws.bin_offsets.as<uint32_t>(),
-                           ws.perm.as<uint32_t>(), io.mask, io.pos, io.states, io.out_pos, io.out_states,
-                           ws.act_items.as<uint4>(), ws.act_rows.as<uint32_t>(), ws.wl_count.as<uint32_t>());
-        if (hipError_t e0 = hipGetLastError(); e0 != hipSuccess) return e0;
-        if (p.g.dim == 2) {
-            if (mode == 0) launch_perceive_d<2, 0>(p, ws, io, blocks, stream);
-            else launch_perceive_d<2, 1>(p, ws, io, blocks, stream);
-        } else {
-            if (mode == 0) launch_perceive_d<3, 0>(p, ws, io, blocks, stream);
-            else launch_perceive_d<3, 1>(p, ws, io, blocks, stream);
-        }
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess || mode != 0) return e;
+    const int mask_mode = mode != 0 ? 0 : io.mask ? 2 : (p.update_prob < 1.0f ? 1 : 0);
+    const uint32_t nbins = p.B * p.g.cells;
+    hipError_t e = launch_timed(prof, NPA_KERNEL_ACTIVE, k_active, dim3((nbins + kActWaves - 1) / kActWaves),
+                                dim3(64 * kActWaves), 0, stream, p, mask_mode, nbins, targets_per_item(p.SS),
+                                ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), io.mask, io.pos, io.states,
+                                io.out_pos, io.out_states, ws.act_items.as<uint4>(), ws.act_rows.as<uint32_t>(),
+                                ws.wl_count.as<uint32_t>());
+    if (e != hipSuccess) return e;
+    if (p.g.dim == 2) {
+        if (mode == 0) launch_perceive_d<2, 0>(p, ws, io, blocks, stream, prof);
+        else launch_perceive_d<2, 1>(p, ws, io, blocks, stream, prof);
+    } else {
+        if (mode == 0) launch_perceive_d<3, 0>(p, ws, io, blocks, stream, prof);
+        else launch_perceive_d<3, 1>(p, ws, io, blocks, stream, prof);
     }
-    ProfScope ps(prof, NPA_KERNEL_MLP, stream);
-    if (p.g.dim == 2) return launch_mlp_d<2>(p, ws, io, stream);
-    return launch_mlp_d<3>(p, ws, io, stream);
+    e = hipGetLastError();
+    if (e != hipSuccess || mode != 0) return e;
+    if (p.g.dim == 2) return launch_mlp_d<2>(p, ws, io, stream, prof);
+    return launch_mlp_d<3>(p, ws, io, stream, prof);
 }
 
 hipError_t launch_mlp_forward(const StepParams& p, const float* features, uint32_t rows, const StepIO& io,
@@ -1417,12 +1432,12 @@ hipError_t launch_count_pairs(const StepParams& p, Workspace& ws, int grid_block
                               hipStream_t stream) {
     if (p.g.dim == 2)
         hipLaunchKernelGGL(k_count_pairs<2>, dim3(grid_blocks), dim3(256), 0, stream, p, ws.srec.as<float4>(),
-                           ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.worklist.as<uint2>(),
-                           ws.wl_count.as<uint32_t>(), counters);
+                           ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
+                           ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), counters);
     else
         hipLaunchKernelGGL(k_count_pairs<3>, dim3(grid_blocks), dim3(256), 0, stream, p, ws.srec.as<float4>(),
-                           ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.worklist.as<uint2>(),
-                           ws.wl_count.as<uint32_t>(), counters);
+                           ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
+                           ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), counters);
     return hipGetLastError();
 }
 

@@ -116,9 +116,17 @@ class HipAutomataExecutor:
 
     def pair_counts(self, state: HipAutomataState):
         """(candidates visited, pairs accepted) of the neighbour walk on the current particles."""
-        a, b = C.c_uint64(), C.c_uint64()
-        self.ctx.check(lib().npa_state_pair_counts(state.handle, C.byref(a), C.byref(b)))
-        return int(a.value), int(b.value)
+        c = self.work_counts(state)
+        return c["candidates"], c["pairs"]
+
+    def work_counts(self, state: HipAutomataState):
+        """Exact work of the state's next step: candidates and pairs of the density pass over every
+        particle, and the update mask's targets with their candidates and pairs (the particles the
+        second pass and the update MLP process)."""
+        v = [C.c_uint64() for _ in range(5)]
+        self.ctx.check(lib().npa_state_pair_counts(state.handle, *[C.byref(x) for x in v]))
+        keys = ("candidates", "pairs", "targets", "target_candidates", "target_pairs")
+        return {k: int(x.value) for k, x in zip(keys, v)}
 
     def wait_idle(self):
         self.ctx.synchronize()

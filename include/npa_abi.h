@@ -270,7 +270,9 @@ enum {
     NPA_KERNEL_PERCEIVE = 5,   /* second neighbour pass + normalisation + feature rows */
     NPA_KERNEL_SPLAT = 6,      /* the whole 2D splat pipeline */
     NPA_KERNEL_MLP = 7,        /* update MLP + masked Euler */
-    NPA_KERNEL_COUNT = 8
+    NPA_KERNEL_SPLIT = 8,      /* per-bin split by true cell + sorted payload + work items */
+    NPA_KERNEL_ACTIVE = 9,     /* update-mask targets (masked-out particles copied unchanged) */
+    NPA_KERNEL_COUNT = 10
 };
 /* kernel_mask selects kernels by bit (1 << NPA_KERNEL_*; 0 = off, -1 = all). The
  * library then brackets each launch of a selected kernel with HIP events on the
@@ -279,9 +281,13 @@ enum {
 npa_status npa_profile_enable(npa_context* ctx, int kernel_mask);
 npa_status npa_profile_reset(npa_context* ctx);
 npa_status npa_profile_read(npa_context* ctx, int kernel_id, double* total_ms, uint64_t* launches);
-/* Work counters of the last step run through a state (exact, from the device):
- * candidates tested and pairs accepted by the density pass. */
-npa_status npa_state_pair_counts(npa_state* state, uint64_t* candidates, uint64_t* pairs);
+/* Work counters of the state's next step on its current particles (exact, from the device;
+ * diagnostic, no counterpart in the reference): candidates tested and pairs accepted by the
+ * density pass over every particle, and the targets of the step's update mask (the particles the
+ * second pass and the update MLP process) with their candidates and pairs. Any pointer may be
+ * NULL. */
+npa_status npa_state_pair_counts(npa_state* state, uint64_t* candidates, uint64_t* pairs, uint64_t* targets,
+                                 uint64_t* target_candidates, uint64_t* target_pairs);
 
 #ifdef __cplusplus
 }

@@ -247,6 +247,40 @@ def test_update_probability_zero_keeps_state(ctx):
     np.testing.assert_array_equal(to_np(gs), st)
 
 
+@pytest.mark.parametrize("name,prob", [("c1", 0.5), ("growing_3d", 0.3), ("batch4", 1.0)])
+def test_work_counters_match_oracle(ctx, name, prob):
+    """npa_state_pair_counts (the bench's work counts): candidates and pairs of the density pass
+    over every particle and of the update mask's targets, against the oracle's hashgrid bins,
+    neighbour lists and mask on the state's particles after one step."""
+    from tests.test_oracle import cell_coords_ref, cell_index_ref
+
+    m, g, pos, st, w, b, n = _model_case(name)
+    ex = HipAutomataExecutor(ctx=ctx)
+    state = ex.create_state(NpaModel(m, w), pos, st, b, n, g, 1.0, prob, 42)
+    ex.step_state(state)  # the counters describe step 1, a nonzero step index
+    got = ex.work_counts(state)
+    p1 = to_np(ex.read_state(state)[0])
+    cells = g.cell_count()
+    sizes = np.diff(O.build_hashgrid(p1, b, n, g).bin_offsets.astype(np.int64))
+    off, _ = O.neighbor_lists(p1, b, n, g)
+    pairs = np.diff(off.astype(np.int64))
+    zs = (-1, 0, 1) if g.dim == 3 else (0,)
+    cand = np.zeros(b * n, np.int64)
+    for i in range(b * n):
+        c = cell_coords_ref(p1[i], g)
+        for dz in zs:
+            for dy in (-1, 0, 1):
+                for dx in (-1, 0, 1):
+                    cell = cell_index_ref((c[0] + dx, c[1] + dy, c[2] + dz), g)
+                    if cell is not None:
+                        cand[i] += sizes[(i // n) * cells + cell]
+    mask = O.update_mask(b, n, prob, 1, 42) != 0
+    want = {"candidates": int(cand.sum()), "pairs": int(pairs.sum()), "targets": int(mask.sum()),
+            "target_candidates": int(cand[mask].sum()), "target_pairs": int(pairs[mask].sum())}
+    assert got == want
+    state.close()
+
+
 def test_update_model_changes_trajectory(ctx):
     m, g, pos, st, w, b, n = _model_case("c1")
     ex = HipAutomataExecutor(ctx=ctx)
