@@ -84,10 +84,17 @@ def test_bench_refuses_more_than_one_gpu(capsys):
 def test_bench_kernel_work_counts():
     bench = _load("bench")
     m = syn.workload("c1", particles=64)["model"]
-    work = bench.kernel_work(m, candidates=1000.0, pairs=300.0, particles=100)
+    counts = {"candidates": 1000.0, "pairs": 300.0, "targets": 40.0, "target_candidates": 400.0,
+              "target_pairs": 120.0}
+    work = bench.kernel_work(m, counts, particles=100)
     fl, by = work["mlp"]
-    assert fl == 100 * (2 * (64 * 128 + 128 * 18) + 8 + 6 + 48)
-    assert work["perceive"][0] > work["density"][0] > 0
+    # the MLP runs over the update mask's targets only
+    assert fl == 40 * (2 * (64 * 128 + 128 * 18) + 8 + 6 + 48)
+    assert by == 40 * (4 * 64 + 4 + 32 + 8 * 16)
+    assert work["density"] == (5 * 1000 + 5 * 300 + 100, 100 * 24)
+    per_pair = 4 + 1 + 2 * 16 + 7 + 2 + 16 * 5 + 8
+    assert work["perceive"][0] == 5 * 400 + per_pair * 120 + 40 * (15 + 128 + 32 + 16 * 29)
+    assert work["perceive"][1] == 40 * (16 + 64 + 8 + 256)
 
 
 def test_graft_entry_points_exist():
