@@ -230,6 +230,21 @@ __device__ __forceinline__ float clampf_(float v, float lo, float hi) {  // f32:
     return v;
 }
 
+// wrap_position  crates/burn_automata_kernels/src/hashgrid.rs:183-193, axis a of a periodic grid:
+// (v + half).rem_euclid(extent) - half.
+__device__ __forceinline__ float wrap_axis(float v, int a, const GridParams& g) {
+    const float x = v + g.half[a];
+    float r = fmodf(x, g.extent[a]);
+    if (r < 0.0f) r = r + fabsf(g.extent[a]);
+    return r - g.half[a];
+}
+
+// The opacity-logit channels euler_step clamps in 3D (step.rs:47-50, GROWTH_3D_*_OPACITY_LOGIT
+// types.rs:1-2).
+__device__ __forceinline__ bool clamped_channel(int dim, uint32_t S, uint32_t c) {
+    return dim == 3 && S > 3 && (c == 3 || (S > 8 && c == 8));
+}
+
 __device__ __forceinline__ uint64_t lanemask_lt() {
     uint32_t lane = __lane_id();
     return lane == 0 ? 0ull : (~0ull >> (64 - lane));

@@ -367,31 +367,51 @@ __device__ __forceinline__ uint32_t nth_set_bit(uint64_t m, uint32_t t) {
     return pos;
 }
 
-// Copies a particle's position and state row unchanged (every load issued before the stores).
+// Copies a state row (every load issued before the stores); in 3D the opacity-logit channels are
+// clamped on the way.
 template <int NQ>
-__device__ __forceinline__ void copy_state_row(float* __restrict__ dst, const float* __restrict__ src) {
+__device__ __forceinline__ void hold_state_row(float* __restrict__ dst, const float* __restrict__ src, int dim) {
     float4 v[NQ];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) v[q] = reinterpret_cast<const float4*>(src)[q];
+    if (dim == 3) {
+        v[0].w = clampf_(v[0].w, -8.0f, 24.0f);                               // channel 3
+        if constexpr (NQ > 2) v[2].x = clampf_(v[2].x, -8.0f, 24.0f);          // channel 8 (S > 8)
+    }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) reinterpret_cast<float4*>(dst)[q] = v[q];
 }
-__device__ __forceinline__ void copy_particle(uint64_t i, uint32_t S, const float4* __restrict__ pos,
-                                              const float* __restrict__ states, float4* __restrict__ out_pos,
-                                              float* __restrict__ out_states) {
-    out_pos[i] = pos[i];
+
+// A particle whose update mask is 0. The CPU euler_step (step.rs:4-55) adds dt * d * 0 to each
+// value, which is +-0 for a finite update and leaves every value but -0.0 unchanged, and then still
+// applies the periodic wrap and the 3D opacity-logit clamp; those two are applied here, so the
+// result equals the CPU path's without evaluating the update. (The reference's GPU update_particle,
+// gpu_step.wgsl:3664-3682, copies such a particle without the wrap and the clamp.)
+__device__ __forceinline__ void hold_particle(uint64_t i, uint32_t S, const GridParams& g,
+                                              const float4* __restrict__ pos, const float* __restrict__ states,
+                                              float4* __restrict__ out_pos, float* __restrict__ out_states) {
+    float4 p = pos[i];
+    if (g.boundary == 0) {
+        p.x = wrap_axis(p.x, 0, g);
+        p.y = wrap_axis(p.y, 1, g);
+        if (g.dim == 3) p.z = wrap_axis(p.z, 2, g);
+    }
+    out_pos[i] = p;
     const float* src = states + i * S;
     float* dst = out_states + i * S;
     if (S == state_stride_for(S)) {  // 16-byte aligned rows (checked on the host)
         switch (S) {
-            case 4: copy_state_row<1>(dst, src); return;
-            case 8: copy_state_row<2>(dst, src); return;
-            case 16: copy_state_row<4>(dst, src); return;
-            case 24: copy_state_row<6>(dst, src); return;
-            default: copy_state_row<8>(dst, src); return;
+            case 4: hold_state_row<1>(dst, src, g.dim); return;
+            case 8: hold_state_row<2>(dst, src, g.dim); return;
+            case 16: hold_state_row<4>(dst, src, g.dim); return;
+            case 24: hold_state_row<6>(dst, src, g.dim); return;
+            default: hold_state_row<8>(dst, src, g.dim); return;
         }
     }
-    for (uint32_t c = 0; c < S; ++c) dst[c] = src[c];
+    for (uint32_t c = 0; c < S; ++c) {
+        const float v = src[c];
+        dst[c] = clamped_channel(g.dim, S, c) ? clampf_(v, -8.0f, 24.0f) : v;
+    }
 }
 
 // Targets of the second pass and the update MLP, one wave per bin (16 bins per block). A particle
@@ -486,8 +506,8 @@ __global__ __launch_bounds__(1024) void k_active(StepParams P, int mask_mode, ui
             const uint64_t am = __ballot(act);
             const uint32_t rank = (uint32_t)__popcll(am & lt);
             if (act) rows[rb + rank] = slot;
-            else if (valid && mask_mode != 0)  // masked out: copied unchanged
-                copy_particle((uint64_t)b * P.N + li, P.S, pos, states, out_pos, out_states);
+            else if (valid && mask_mode != 0)  // masked out: no update
+                hold_particle((uint64_t)b * P.N + li, P.S, P.g, pos, states, out_pos, out_states);
             const uint32_t na = (uint32_t)__popcll(am);
             const uint32_t ni = (na + tpi - 1) / tpi;
             const uint32_t jr = rank / tpi;
@@ -1080,14 +1100,9 @@ __global__ __launch_bounds__(256) void k_mlp_euler(StepParams P, const float* __
     constexpr int MEM = D == 3 ? 4 : 2;
 #pragma unroll
     for (int a = 0; a < MEM; ++a) pn[a] += P.dt * dx[a] * m;
-    if (P.g.boundary == 0) {  // wrap_position hashgrid.rs:183-193
+    if (P.g.boundary == 0) {
 #pragma unroll
-        for (int a = 0; a < D; ++a) {
-            const float v = pn[a] + P.g.half[a];
-            float r = fmodf(v, P.g.extent[a]);
-            if (r < 0.0f) r = r + fabsf(P.g.extent[a]);
-            pn[a] = r - P.g.half[a];
-        }
+        for (int a = 0; a < D; ++a) pn[a] = wrap_axis(pn[a], a, P.g);
     }
     io.out_pos[i] = make_float4(pn[0], pn[1], pn[2], pn[3]);
     float nxt[SM];
@@ -1096,7 +1111,7 @@ __global__ __launch_bounds__(256) void k_mlp_euler(StepParams P, const float* __
         float dsc = u[D + c];
         if (P.gates3d) dsc *= sg;
         float next = si[c] + P.dt * dsc * m;
-        if (D == 3 && S > 3 && (c == 3 || (S > 8 && c == 8))) next = clampf_(next, -8.0f, 24.0f);
+        if (clamped_channel(D, S, (uint32_t)c)) next = clampf_(next, -8.0f, 24.0f);
         nxt[c] = next;
     }
     float* os = io.out_states + (uint64_t)i * S;
@@ -1158,17 +1173,12 @@ __global__ __launch_bounds__(256) void k_euler(GridParams g, const float4* __res
     const int mem = g.dim == 3 ? 4 : 2;
     for (int a = 0; a < mem; ++a) p[a] += dt * d[a] * m;
     if (g.boundary == 0) {
-        for (int a = 0; a < g.dim; ++a) {
-            const float v = p[a] + g.half[a];
-            float r = fmodf(v, g.extent[a]);
-            if (r < 0.0f) r = r + fabsf(g.extent[a]);
-            p[a] = r - g.half[a];
-        }
+        for (int a = 0; a < g.dim; ++a) p[a] = wrap_axis(p[a], a, g);
     }
     out_pos[i] = make_float4(p[0], p[1], p[2], p[3]);
     for (uint32_t c = 0; c < S; ++c) {
         float next = states[i * S + c] + dt * ds[i * S + c] * m;
-        if (g.dim == 3 && S > 3 && (c == 3 || (S > 8 && c == 8))) next = clampf_(next, -8.0f, 24.0f);
+        if (clamped_channel(g.dim, S, c)) next = clampf_(next, -8.0f, 24.0f);
         out_states[i * S + c] = next;
     }
 }

@@ -247,6 +247,40 @@ def test_update_probability_zero_keeps_state(ctx):
     np.testing.assert_array_equal(to_np(gs), st)
 
 
+@pytest.mark.parametrize("name", ["texture_periodic", "torus_gates_3d"])
+def test_masked_particles_follow_the_cpu_euler_step(ctx, name):
+    """Particles with update mask 0 skip the second pass and the MLP on the device; the CPU
+    euler_step (step.rs:4-55) still wraps their positions on a periodic grid and clamps their 3D
+    opacity logits. Both step paths must equal the oracle bit for bit, masked particles included."""
+    m, g, pos, st, w, b, n = _model_case(name)
+    if g.dim == 3:  # opacity logits outside [-8, 24] on masked and unmasked particles
+        st = st.copy()
+        st[::3, 3] = 30.0
+        st[1::5, 8] = -20.0
+    if name == "texture_periodic":  # particles beyond the periodic extent and at its edges
+        pos = pos.copy()
+        half = 0.5 * g.grid_size[0] * g.eps
+        pos[::11, 0] = np.float32(half * 1.37)
+        pos[::13, 1] = np.float32(-half)
+    mask = O.update_mask(b, n, 0.5, 3, 42)
+    assert 0 < mask.sum() < mask.size
+    want = O.step(m, w, pos, st, b, n, g, 1.0, mask)
+    got = NpaModel(m, w).step(pos, st, b, n, g, 1.0, update_mask=mask, ctx=ctx)
+    np.testing.assert_array_equal(to_np(got.next_positions), want.next_positions)
+    np.testing.assert_array_equal(to_np(got.next_states), want.next_states)
+    held = mask == 0  # the case exercises the transform: some held values are not their inputs
+    assert ((want.next_positions[held] != pos[held]).any()
+            or (want.next_states[held] != st[held]).any())
+    want_p, want_s = O.rollout(m, w, pos, st, b, n, g, 4, 1.0, 0.5, 42, 0)
+    ex = HipAutomataExecutor(ctx=ctx)
+    state = ex.create_state(NpaModel(m, w), pos, st, b, n, g, 1.0, 0.5, 42)
+    ex.step_state_many(state, 4)
+    gp, gs, _ = ex.read_state(state)
+    np.testing.assert_array_equal(to_np(gp), want_p)
+    np.testing.assert_array_equal(to_np(gs), want_s)
+    state.close()
+
+
 @pytest.mark.parametrize("name,prob", [("c1", 0.5), ("growing_3d", 0.3), ("batch4", 1.0)])
 def test_work_counters_match_oracle(ctx, name, prob):
     """npa_state_pair_counts (the bench's work counts): candidates and pairs of the density pass
