@@ -1,12 +1,12 @@
 // npa_perception.hip - SPH neighbour passes and the rollout update on gfx950.
 //
-// Work mapping: the hashgrid build emits one work item per <=64 consecutive sorted
-// slots of a bin, so each wavefront's lanes are targets of one bin and share (per group
-// of equal cell coordinates) the same 3x3(x3) neighbour cells. Each lane accumulates its
-// own sums serially in the reference's neighbour order (cells dz, dy, dx; slots ascending
-// = particle index ascending), so the sums are bit-identical to the CPU path.
+// Work mapping: the hashgrid build splits every bin into runs of one true cell and emits work
+// items of <= 64/L consecutive slots of a run; L lanes serve each target. Every per-target sum is
+// taken in the reference's neighbour order (cells dz, dy, dx; slots ascending = particle index
+// ascending), so the sums are bit-identical to the CPU path.
 //
 //   k_density    rho_i = sum_j W_poly6(r_ij^2)                          forward.rs:145-160
+//   k_active     update-mask targets; masked-out particles get the Euler step's wrap/clamp only
 //   k_perceive   second pass (blur, state gradient, density gradient, moment matrix)
 //                forward.rs:162-382 -> moment correction, scaling, log-norm
 //                normalize.rs:5-118 -> feature row                     forward.rs:100-133
@@ -95,15 +95,14 @@ __device__ __forceinline__ void walk_neighbors(const GridParams& g, uint32_t b, 
 #define NPA_WAVE_LOOP_END }
 
 // ------------------------------------------------------------------------------------------
-// Wave-per-bin neighbour passes with LDS-staged candidates.
+// Neighbour passes over the split bins.
 //
-// A work item is <= 64 consecutive sorted slots of one bin; the lanes are its targets.
-// Lanes are processed in groups of equal cell coordinates (a hash bin can hold several
-// true cells), so inside a group the 3x3(x3) neighbour bins, each candidate's Particle-mode
-// coordinate test and the loop bounds are wave-uniform. Each neighbour bin is streamed through
-// LDS 64 candidates at a time with one coalesced load per lane; lanes then read candidates
-// as LDS broadcasts. Per lane, candidates are visited in cell order and ascending slot order,
-// which is the reference's for_each_neighbor order, so every per-target sum is unchanged.
+// A work item holds targets of one cell run, so their 3x3(x3) neighbour cells, the cells' runs and
+// the loop bounds are wave-uniform (targets are still grouped by cell coordinates, which covers
+// Grid mode and unsplit bins). A neighbour cell's run is walked in chunks of kChunk slots. Per
+// target, candidates are visited in cell order (dz, dy, dx) and ascending slot order - ascending
+// particle index within the cell, the reference's for_each_neighbor order - so every per-target
+// sum is unchanged.
 constexpr int kChunk = 64;
 
 __device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
@@ -141,69 +140,6 @@ __device__ __forceinline__ bool cell_range(const StepParams& P, const uint32_t* 
         }
     }
     return false;
-}
-
-template <int D>
-struct NbrStage {
-    float4 rec[kChunk];
-    int4 crd[D == 3 ? kChunk : 1];
-};
-
-template <int D>
-__device__ __forceinline__ void stage_records(NbrStage<D>& st, const float4* __restrict__ srec,
-                                              const int4* __restrict__ scoord, uint32_t base, uint32_t m,
-                                              uint32_t lane) {
-    if (lane < m) {
-        st.rec[lane] = srec[base + lane];
-        if constexpr (D == 3) st.crd[lane] = scoord[base + lane];
-    }
-}
-
-template <int D>
-__device__ __forceinline__ bool staged_coords_match(const NbrStage<D>& st, uint32_t k, const float4& r,
-                                                    int64_t n0, int64_t n1, int64_t n2) {
-    if constexpr (D == 2) {
-        return (int64_t)__float_as_int(r.z) == n0 && (int64_t)__float_as_int(r.w) == n1;
-    } else {
-        const int4 q = st.crd[k];
-        return (int64_t)q.x == n0 && (int64_t)q.y == n1 && (int64_t)q.z == n2;
-    }
-}
-
-// Iterates the coordinate groups of the current item and, per group, the staged candidate
-// chunks of its neighbour bins. `on_chunk(base, m, n0, n1, n2, in_group)` runs after each
-// chunk is staged (LDS written and visible to the wave).
-template <int D, class OnChunk, class Stage>
-__device__ __forceinline__ void for_each_group_chunk(const GridParams& g, uint32_t b, bool active, const int* ci,
-                                                     const uint32_t* __restrict__ bo, uint32_t lane,
-                                                     Stage&& stage, OnChunk&& on_chunk) {
-    uint64_t pending = __ballot(active);
-    while (pending) {
-        const int leader = __ffsll((unsigned long long)pending) - 1;
-        const int l0 = readlane_i(ci[0], leader), l1 = readlane_i(ci[1], leader);
-        const int l2 = D == 3 ? readlane_i(ci[2], leader) : 0;
-        const bool same = active && ci[0] == l0 && ci[1] == l1 && (D == 2 || ci[2] == l2);
-        const uint64_t group = __ballot(same) & pending;
-        pending &= ~group;
-        const bool in_group = (group >> lane) & 1ull;
-        constexpr int ZLO = D == 3 ? -1 : 0, ZHI = D == 3 ? 1 : 0;
-        for (int dz = ZLO; dz <= ZHI; ++dz)
-            for (int dy = -1; dy <= 1; ++dy)
-                for (int dx = -1; dx <= 1; ++dx) {
-                    const int64_t n0 = (int64_t)l0 + dx, n1 = (int64_t)l1 + dy, n2 = (int64_t)l2 + dz;
-                    uint32_t cell;
-                    if (!cell_index(n0, n1, n2, g, &cell)) continue;
-                    const uint64_t bin = (uint64_t)b * g.cells + cell;
-                    const uint32_t beg = bo[bin], end = bo[bin + 1];
-                    for (uint32_t base = beg; base < end; base += kChunk) {
-                        const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
-                        __syncthreads();  // the previous chunk has been consumed by every lane
-                        stage(base, m);
-                        __syncthreads();
-                        on_chunk(base, m, n0, n1, n2, in_group);
-                    }
-                }
-    }
 }
 
 // Lanes per target for a sorted-state row width SM (each lane owns SM / L state channels).
