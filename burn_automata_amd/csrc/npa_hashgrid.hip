@@ -77,6 +77,8 @@ hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t
     NPA_RES(tmpidx, t1 * 4);
     NPA_RES(dir_n, (bins ? bins : 1) * 4);
     NPA_RES(dir_e, (bins ? bins : 1) * kDirGroups * 16);
+    NPA_RES(nb_chunks, t1 * max_chunks(dim) * 16);
+    NPA_RES(nb_count, t1 * 4);
 #undef NPA_RES
     if (!flags.ptr) {
         if ((e = flags.reserve(64)) != hipSuccess) return e;
@@ -88,7 +90,7 @@ hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t
 void Workspace::release() {
     for (DevBuf* b : {&keys, &ranks, &table, &totals, &bin_offsets, &perm, &inv, &flags, &wl_count,
                       &worklist, &srec, &scoord, &sstate, &svol, &counters, &features, &wpad, &tmpidx,
-                      &dir_n, &dir_e, &act_items, &act_rows})
+                      &dir_n, &dir_e, &act_items, &act_rows, &nb_chunks, &nb_count})
         b->release();
 }
 

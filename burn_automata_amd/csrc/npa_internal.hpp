@@ -101,10 +101,19 @@ struct Workspace {
     // uint4 {window base slot, target bitmask lo, hi, first compact row}; act_rows: compact row ->
     // slot. Counts (u32 words of wl_count): [0] density items, [2] second-pass items, [3] rows.
     DevBuf act_items, act_rows;
+    // Accepted neighbours recorded by the density pass, per target and neighbour chunk (<= 64
+    // consecutive slots of a cell run, in visit order): chunk-major uint4 {first slot, length,
+    // accept mask lo, hi} at [chunk * T + slot] for the first max_chunks(dim) chunks, and the
+    // target's chunk count (the second pass tests the candidates itself when it exceeds the cap).
+    DevBuf nb_chunks, nb_count;
     hipError_t reserve(const HashgridPlan& plan, uint64_t total, uint32_t batch, uint32_t state_dims,
                        int dim, uint32_t feature_dims = 0);
     void release();
 };
+
+// Chunk records kept per target by the density pass (a 2D target visits 9 cells, a 3D one 27; a
+// cell run of more than 64 particles spans several chunks).
+__host__ __device__ constexpr uint32_t max_chunks(int dim) { return dim == 3 ? 48u : 24u; }
 
 // tpi: targets per wave work item emitted for the neighbour passes (64 / lanes per target).
 bool make_plan(const npa_grid_cfg& cfg, uint32_t batch, uint32_t particle_count, HashgridPlan* plan,

@@ -198,6 +198,9 @@ __device__ __forceinline__ float ordered_group_sum(float acc, float v) {
 // running sum in candidate order from the L per-lane terms of each round. A rejected candidate
 // contributes +0.0, which leaves the sum unchanged (it starts at +0.0, adds only non-negative
 // terms and therefore never holds -0.0).
+// The accepted candidates are recorded for the second pass, which needs exactly the same set in
+// the same order: per target and chunk (in visit order) {first slot, length, 64-bit accept mask}
+// at nb_chunks[chunk * T + slot] for the first max_chunks(D) chunks, and the chunk count.
 template <int D, int L>
 __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __restrict__ srec,
                                                 const int4* __restrict__ scoord,
@@ -205,7 +208,9 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
                                                 const uint32_t* __restrict__ perm,
                                                 const uint2* __restrict__ wl,
                                                 const uint32_t* __restrict__ wl_count,
-                                                float* __restrict__ svol, float* __restrict__ density_out) {
+                                                float* __restrict__ svol, float* __restrict__ density_out,
+                                                uint4* __restrict__ nb_chunks, uint32_t* __restrict__ nb_count) {
+    constexpr uint32_t MAXC = max_chunks(D);
     const uint32_t lane = threadIdx.x;
     const uint32_t t = lane / L, q = lane % L;
     const uint32_t items = *wl_count;
@@ -218,6 +223,7 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
         int ci[3];
         load_rec<D>(srec, scoord, s, pi, ci);
         float rho = 0.0f;
+        uint32_t nch = 0;  // chunks visited by this lane's coordinate group
         uint64_t pending = __ballot(active);
         while (pending) {
             const int leader = __ffsll((unsigned long long)pending) - 1;
@@ -227,6 +233,7 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
             const uint64_t group = __ballot(same) & pending;
             pending &= ~group;
             const bool in_group = (group >> lane) & 1ull;
+            uint32_t gch = 0;  // chunk index within this group's visit order (wave-uniform)
             constexpr int ZLO = D == 3 ? -1 : 0, ZHI = D == 3 ? 1 : 0;
             for (int dz = ZLO; dz <= ZHI; ++dz)
                 for (int dy = -1; dy <= 1; ++dy)
@@ -235,8 +242,9 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
                         uint32_t beg, end;
                         bool filter;
                         if (!cell_range(P, bo, b, n0, n1, n2, beg, end, filter)) continue;
-                        for (uint32_t base = beg; base < end; base += kChunk) {
+                        for (uint32_t base = beg; base < end; base += kChunk, ++gch) {
                             const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
+                            uint64_t acc = 0;  // accepted candidates of this lane's residue class
                             constexpr int BT = kChunk / L < 4 ? kChunk / L : 4;  // loads per batch
                             for (int i0 = 0; i0 < kChunk / L; i0 += BT) {
                                 if ((uint32_t)(i0 * L) >= m) break;  // wave-uniform
@@ -271,15 +279,23 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
                                         const float d2 = delta_axis(pi[2], r.z, 2, P.g);
                                         r2 += d2 * d2;
                                     }
-                                    const float v = ok ? poly6(r2, P.g) : 0.0f;  // poly6 is 0 beyond eps
+                                    const bool acc_ok = ok & (r2 < P.g.eps2);
+                                    const float v = acc_ok ? poly6(r2, P.g) : 0.0f;
+                                    acc |= acc_ok ? (1ull << k) : 0ull;  // k < m <= 64 when acc_ok
                                     rho = ordered_group_sum<L>(rho, v);
                                 }
                             }
+                            acc = group_or<L>(acc);
+                            if (in_group && q == 0 && gch < MAXC)
+                                nb_chunks[(uint64_t)gch * P.T + s] =
+                                    make_uint4(base, m, (uint32_t)acc, (uint32_t)(acc >> 32));
                         }
                     }
+            if (in_group) nch = gch;
         }
         if (active && q == 0) {
             svol[s] = recip_finite(rho);
+            nb_count[s] = nch;
             if (density_out) density_out[b * P.N + perm[s]] = rho;
         }
     }
@@ -458,17 +474,17 @@ __global__ __launch_bounds__(1024) void k_active(StepParams P, int mask_mode, ui
 }
 
 // Per-wave accepted-neighbour lists of the second pass. Entry = (chunk id << 6) | k, the k-th
-// candidate of the chunk whose first sorted slot is chunk_base[chunk id]; entries of a target are
-// appended in visit order (cells dz, dy, dx; slots ascending), so walking a list front to back
-// is the reference's neighbour order. LDS: kListBytes per wave for any targets-per-item.
+// candidate of the target's chunk whose first sorted slot is cbase[chunk id][target]; entries of a
+// target are appended in visit order (cells dz, dy, dx; slots ascending), so walking a list front
+// to back is the reference's neighbour order. LDS: kListBytes of entries per wave for any
+// targets-per-item, plus the chunk-base table.
 constexpr int kListBytes = 8192;
-constexpr int kMaxChunks = 64;
 
-template <int TPI>
+template <int TPI, int MAXC>
 struct PerceiveLists {
     static constexpr int CAP = kListBytes / (2 * TPI);
     uint16_t entry[CAP][TPI];
-    uint32_t chunk_base[kMaxChunks];
+    uint32_t cbase[MAXC][TPI];
 };
 
 // Bits k of a 64-bit chunk mask with k % L == q.
@@ -481,9 +497,11 @@ __device__ __forceinline__ uint64_t residue_mask(uint32_t q) {
 
 // Second neighbour pass + normalisation + feature row, L lanes per target, each lane owning
 // CPL = SM / L state channels.
-// Phase A: for each neighbour bin of the target's cell (reference order), the L lanes of a
-//   target test the bin's candidates round-robin straight from the sorted records, OR their
-//   accept masks and append the accepted candidates to the target's list in LDS.
+// Phase A: the target's accepted candidates are appended to its list in LDS, chunk by chunk in
+//   visit order, from the accept masks the density pass recorded (the same test on the same
+//   candidates). A target with more chunks than were recorded makes the item test them here: for
+//   each neighbour cell of the target's cell (reference order), the L lanes of a target test the
+//   candidates round-robin straight from the sorted records and OR their accept masks.
 // Phase B (when a list would overflow, and at the end): the lists are consumed in rounds of L
 //   entries: lane q computes the pair scalars (poly6, volume, spiky gradients) of the round's
 //   q-th entry, and every lane applies the round's entries in list order to its own channels,
@@ -507,11 +525,14 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                                                  const uint32_t* __restrict__ perm,
                                                  const uint4* __restrict__ wl,
                                                  const uint32_t* __restrict__ wl_count,
+                                                 const uint4* __restrict__ nb_chunks,
+                                                 const uint32_t* __restrict__ nb_count,
                                                  float* __restrict__ sfeatures, StepIO io) {
     constexpr int L = LanesPerTarget<SM>::L;
     constexpr int CPL = LanesPerTarget<SM>::CPL;
     constexpr int TPI = 64 / L;
-    using Lists = PerceiveLists<TPI>;
+    constexpr uint32_t MAXC = max_chunks(D);
+    using Lists = PerceiveLists<TPI, (int)MAXC>;
     constexpr uint32_t CAP = Lists::CAP;
     __shared__ Lists lists;
     const uint32_t lane = threadIdx.x;
@@ -559,7 +580,8 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                 const bool has = active && e < cnt;
                 // entry read at a clamped index; the slot of a lane without an entry is its target
                 const uint32_t en = lists.entry[has ? e : 0u][t];
-                const uint32_t cand = lists.chunk_base[(en >> 6) & (uint32_t)(kMaxChunks - 1)] + (en & 63u);
+                const uint32_t chunk = (en >> 6) < MAXC ? (en >> 6) : MAXC - 1;  // in bounds for any entry
+                const uint32_t cand = lists.cbase[chunk][t] + (en & 63u);
                 const uint32_t slot = has ? cand : s;
                 const float4 rj = srec[slot];
                 const float vj = svol[slot];
@@ -682,8 +704,38 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
             nchunks = 0;
         };
 
-        // Phase A: coordinate groups of the item, then the group's neighbour bins in order.
-        uint64_t pending = __ballot(active);
+        // Phase A. The density pass recorded each target's accepted candidates per chunk, in visit
+        // order; the lists are built from those masks (RB chunk records loaded per batch).
+        const uint32_t nct = active ? nb_count[s] : 0u;
+        const bool recorded = !__ballot(nct > MAXC);
+        constexpr int RB = 2;  // chunk records loaded per batch
+        for (uint32_t cb = 0; recorded && __ballot(cb < nct); cb += RB) {
+            uint4 rc[RB];
+#pragma unroll
+            for (int u = 0; u < RB; ++u) {
+                const uint32_t c = cb + (uint32_t)u;
+                rc[u] = c < nct ? nb_chunks[(uint64_t)c * P.T + s] : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int u = 0; u < RB; ++u) {
+                const uint32_t c = cb + (uint32_t)u;
+                const uint64_t acc = ((uint64_t)rc[u].w << 32) | rc[u].z;  // 0 past the target's chunks
+                const uint32_t add = (uint32_t)__popcll(acc);
+                if (__ballot(cnt + add > CAP)) flush();
+                if (q == 0 && c < nct) lists.cbase[c][t] = rc[u].x;
+                uint64_t mine = acc & my_residue;
+                while (mine) {
+                    const uint32_t k = (uint32_t)__builtin_ctzll(mine);
+                    mine &= mine - 1;
+                    const uint32_t pos = cnt + (uint32_t)__popcll(acc & ((1ull << k) - 1ull));
+                    lists.entry[pos][t] = (uint16_t)((c << 6) | k);
+                }
+                cnt += add;
+            }
+        }
+        // Otherwise (a target with more chunks than were recorded): the coordinate groups of the
+        // item, then each group's neighbour cells in order, testing the candidates here.
+        uint64_t pending = recorded ? 0ull : __ballot(active);
         while (pending) {
             const int leader = __ffsll((unsigned long long)pending) - 1;
             const int l0 = readlane_i(ci[0], leader), l1 = readlane_i(ci[1], leader);
@@ -743,8 +795,8 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                             }
                             acc = group_or<L>(acc);
                             const uint32_t add = (uint32_t)__popcll(acc);
-                            if (__ballot(cnt + add > CAP) || nchunks == (uint32_t)kMaxChunks) flush();
-                            if (lane == 0) lists.chunk_base[nchunks] = base;
+                            if (__ballot(cnt + add > CAP) || nchunks == MAXC) flush();
+                            if (q == 0) lists.cbase[nchunks][t] = base;
                             uint64_t mine = acc & my_residue;
                             while (mine) {
                                 const uint32_t k = (uint32_t)__builtin_ctzll(mine);
@@ -1207,7 +1259,8 @@ static void launch_density_t(const StepParams& p, Workspace& ws, float* density_
                              Profiler* prof) {
     launch_timed(prof, NPA_KERNEL_DENSITY, k_density<D, L>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
                        ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
-                       ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.svol.as<float>(), density_out);
+                       ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.svol.as<float>(), density_out,
+                       ws.nb_chunks.as<uint4>(), ws.nb_count.as<uint32_t>());
 }
 
 template <int D>
@@ -1241,7 +1294,8 @@ static void launch_perceive_f(const StepParams& p, Workspace& ws, const StepIO& 
     launch_timed(prof, NPA_KERNEL_PERCEIVE, k_perceive<D, SM, MODE, FL>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
                        ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.svol.as<float>(),
                        ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), ws.act_items.as<uint4>(),
-                       ws.wl_count.as<uint32_t>() + 2, ws.features.as<float>(), io);
+                       ws.wl_count.as<uint32_t>() + 2, ws.nb_chunks.as<uint4>(), ws.nb_count.as<uint32_t>(),
+                       ws.features.as<float>(), io);
 }
 
 // The rollout step's usual option sets run a specialised kernel; anything else reads the flags.

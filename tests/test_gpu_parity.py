@@ -111,6 +111,38 @@ def _perceive_cases():
     }
 
 
+def _dense_cell_case(dim, n_dense, n_rest, seed):
+    """A cell far denser than its neighbours: targets around it visit more neighbour chunks
+    (runs of <= 64 slots) than the density pass records, so their items take the second pass's
+    own candidate tests, while the other items build their lists from the recorded masks."""
+    rng = np.random.default_rng(seed)
+    if dim == 2:
+        cfg = syn.config_c1()[1]
+        rest = syn.uniform_disk(n_rest, seed, radius=0.4)
+    else:
+        cfg = HashGridConfig.growing_3dgs()
+        rest = syn.uniform_ball(n_rest, seed, radius=0.5)
+    lo, hi = 0.2 * cfg.eps, 0.8 * cfg.eps  # strictly inside the cell [0, eps)^dim
+    dense = np.zeros((n_dense, 4), np.float32)
+    dense[:, :dim] = rng.uniform(lo, hi, size=(n_dense, dim)).astype(np.float32)
+    pos = np.concatenate([dense, rest]).astype(np.float32)
+    pos = pos[rng.permutation(len(pos))]  # dense particles spread over the index range
+    return pos, cfg
+
+
+@pytest.mark.parametrize("dim,n_dense,n_rest", [(2, 1800, 3000), (3, 3400, 3000)])
+def test_perceive_dense_cell_bit_exact(ctx, dim, n_dense, n_rest):
+    pos, cfg = _dense_cell_case(dim, n_dense, n_rest, 5 + dim)
+    n = len(pos)
+    S = 16 if dim == 2 else 24
+    st = syn.normal_states(n, S, 9)
+    opts = (syn.config_c1()[0] if dim == 2 else NpaConfig.growing_3dgs()).perception_options()
+    want = O.perceive_with_options(pos, st, 1, n, S, cfg, opts)
+    got = K.perceive_with_options(pos, st, 1, n, S, cfg, opts, ctx=ctx)
+    np.testing.assert_array_equal(to_np(got.density), want.density)
+    np.testing.assert_array_equal(to_np(got.features), want.features)
+
+
 @pytest.mark.parametrize("name", list(_perceive_cases().keys()))
 def test_perceive_parity(ctx, name):
     pos, st, b, n, S, cfg, opts = _perceive_cases()[name]
