@@ -66,30 +66,57 @@ def kernel_work(model, counts, particles: int):
 
 
 def cpu_baseline(w, budget_s: float):
+    """The CPU oracle on this host's cores over a bounded sample of the workload: whole steps from
+    the seeded inputs when a step fits the budget, otherwise (C3) one step evaluated at a uniform
+    random sample of particles - their density pass and their second pass + MLP + Euler, the
+    per-particle work of a full step - scaled to particle-steps/s."""
+    import numpy as np
     from oracle import oracle as O
 
     O.build()
     threads = O.max_threads()
-    n = w["n"] * w["batch"]
+    b, n = w["batch"], w["n"]
+    total = n * b
     pos, st = w["positions"], w["states"]
-    t0 = time.perf_counter()
-    steps = 0
-    while True:
-        mask = O.update_mask(w["batch"], w["n"], w["update_prob"], steps, w["seed"])
-        out = O.step(w["model"], w["weights"], pos, st, w["batch"], w["n"], w["grid"], w["dt"], mask)
-        pos, st = out.next_positions, out.next_states
-        steps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or steps >= 256:
-            break
+    if total <= 262144:
+        t0 = time.perf_counter()
+        steps = 0
+        while True:
+            mask = O.update_mask(b, n, w["update_prob"], steps, w["seed"])
+            out = O.step(w["model"], w["weights"], pos, st, b, n, w["grid"], w["dt"], mask)
+            pos, st = out.next_positions, out.next_states
+            steps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or steps >= 256:
+                break
+        return {
+            "value": total * steps / el, "unit": "particle-steps/sec", "cores": threads,
+            "kind": "port",
+            "sample": (f"first {steps} steps of the same workload from its seeded inputs "
+                       f"({total} particles, oracle/libnpa_oracle.so, OpenMP {threads} threads, "
+                       f"{el:.1f} s; decode excluded)"),
+        }
+    mask = O.update_mask(b, n, w["update_prob"], 0, w["seed"])
+    rng = np.random.default_rng(0)
+    dens = np.zeros(total, np.float32)  # second-pass volumes; the timed work is the same for any
+    k, done, el = 256, 0, 0.0
+    while el < budget_s and done < total:
+        k = min(k, total - done)
+        sel = np.sort(rng.choice(total, k, replace=False)).astype(np.uint32)
+        t0 = time.perf_counter()
+        d = O.density_rows(pos, b, n, w["grid"], sel)
+        dens[sel] = d
+        O.step_rows(w["model"], w["weights"], pos, st, b, n, w["grid"], w["dt"], mask, dens, sel)
+        el += time.perf_counter() - t0
+        done += k
+        k *= 2
     return {
-        "value": n * steps / el,
-        "unit": "particle-steps/sec",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"first {steps} steps of the same workload from its seeded inputs "
-                   f"({n} particles, oracle/libnpa_oracle.so, OpenMP {threads} threads, "
-                   f"{el:.1f} s; decode excluded)"),
+        "value": done / el, "unit": "particle-steps/sec", "cores": threads, "kind": "port",
+        "sample": (f"step 0 of the same workload evaluated at {done} uniformly sampled particles "
+                   f"of {total} (density pass, second pass, MLP and Euler of each; a full "
+                   f"oracle step would take {total / (done / el) / 60:.0f} min here), "
+                   f"oracle/libnpa_oracle.so, OpenMP {threads} threads, "
+                   f"{el:.1f} s"),
     }
 
 
@@ -150,6 +177,7 @@ def main(argv=None) -> int:
     if args.copy_calibration is not None:
         return copy_calibration(torch, args.copy_calibration)
 
+    from burn_automata_amd import kernels as K
     from burn_automata_amd import synthetic as syn
     from burn_automata_amd._lib import lib
     from burn_automata_amd.executor import HipAutomataExecutor
@@ -157,6 +185,7 @@ def main(argv=None) -> int:
 
     w = syn.workload(args.workload, particles=args.particles)
     decode_every = args.decode_every if args.decode_every is not None else w.get("decode_every", 0)
+    decode_steps = set() if args.decode_every is not None else set(w.get("decode_steps", ()))
     splat = w.get("splat")
     model = NpaModel(w["model"], w["weights"])
     ex = HipAutomataExecutor()
@@ -165,16 +194,30 @@ def main(argv=None) -> int:
     pos = torch.from_numpy(w["positions"]).cuda()
     st = torch.from_numpy(w["states"]).cuda()
 
+    def due(k):  # decode after step k (1-based count of steps taken)
+        return splat is not None and ((decode_every and k % decode_every == 0) or k in decode_steps)
+
+    def decode(state):
+        if "tiles_x" in w:  # C5: every system in its own window
+            ex.splat_2d_tiled(state, splat, w["tiles_x"])
+        elif w.get("decode") is not None:  # C4: Gaussian decode, then a splat of the centres
+            dec = ex.decode_gaussians_3d(state, w["decode"])
+            K.splat_particles_2d(dec["position_visibility"], dec["spherical_harmonic"][:, 0, :],
+                                 splat, ctx=ctx)
+        else:
+            ex.splat_2d(state, splat)
+
     def run(state, steps):
         done = 0
         while done < steps:
-            chunk = steps - done
-            if decode_every and splat is not None:
-                chunk = min(chunk, decode_every - (state.step_index() % decode_every))
+            k0 = state.step_index()
+            chunk = 1
+            while done + chunk < steps and not due(k0 + chunk):
+                chunk += 1
             ex.step_state_many(state, chunk)
             done += chunk
-            if decode_every and splat is not None and state.step_index() % decode_every == 0:
-                ex.splat_2d(state, splat)
+            if due(state.step_index()):
+                decode(state)
 
     # warmup on a throwaway state
     if args.warmup > 0:
@@ -261,14 +304,18 @@ def main(argv=None) -> int:
         "dtype": "f32",
         "data": "synthetic (seeded counter-based generator; random-init weights U(-0.1, 0.1))",
         "config": {
-            "workload": (f"{args.workload.upper()}: 2D fixed NPA rollout, {total} particles "
-                         f"(batch {B} x {N}), S={w['model'].state_dims}, "
+            "workload": (f"{args.workload.upper()}: {w['grid'].dim}D fixed NPA rollout, {total} "
+                         f"particles (batch {B} x {N}), S={w['model'].state_dims}, "
                          f"F={w['model'].perception_dims()}, H={w['model'].hidden_dims}, "
                          f"O={w['model'].update_dims()}, eps={w['grid'].eps}, Particle hashgrid "
-                         f"{w['grid'].grid_size[0]}x{w['grid'].grid_size[1]}, update mask "
+                         + "x".join(str(v) for v in w['grid'].grid_size[:w['grid'].dim])
+                         + ", update mask "
                          f"p={w['update_prob']}"
                          + (f", {splat.image_size}x{splat.image_size} RGBA splat every "
-                            f"{decode_every} steps" if decode_every and splat else "")),
+                            f"{decode_every} steps" if decode_every and splat else "")
+                         + (f", {w['tiles_x'] * splat.image_size}x{w['tiles_x'] * splat.image_size}"
+                            f" tiled splat after steps {sorted(decode_steps)}"
+                            if decode_steps and splat else "")),
             "particles": total,
             "steps_timed": args.steps,
             "decode_every": decode_every,

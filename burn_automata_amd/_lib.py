@@ -45,6 +45,7 @@ def _decl(L):
     L.npa_decode_gaussians_3d.argtypes = [P, P, P, u32, u32, ptr(_abi.NpaGaussianDecodeCfg), P, P,
                                           P, P]
     L.npa_splat_2d.argtypes = [P, P, P, u32, ptr(_abi.NpaSplat2dCfg), P]
+    L.npa_splat_2d_tiled.argtypes = [P, P, P, u32, u32, ptr(_abi.NpaSplat2dCfg), u32, P]
     L.npa_state_create.argtypes = [P, ptr(_abi.NpaModelCfg), ptr(_abi.NpaWeightsC),
                                    ptr(_abi.NpaGridCfg), P, P, u32, u32, f32, f32, u64, ptr(P)]
     L.npa_state_destroy.argtypes = [P]
@@ -55,6 +56,7 @@ def _decl(L):
     L.npa_state_step_index.argtypes = [P, ptr(u64)]
     L.npa_state_buffers.argtypes = [P, ptr(P), ptr(P)]
     L.npa_state_splat_2d.argtypes = [P, ptr(_abi.NpaSplat2dCfg), P]
+    L.npa_state_splat_2d_tiled.argtypes = [P, ptr(_abi.NpaSplat2dCfg), u32, P]
     L.npa_state_decode_gaussians_3d.argtypes = [P, ptr(_abi.NpaGaussianDecodeCfg), P, P, P, P]
     L.npa_profile_enable.argtypes = [P, C.c_int]
     L.npa_profile_reset.argtypes = [P]
@@ -67,7 +69,8 @@ def _decl(L):
                  "npa_state_step", "npa_state_read", "npa_state_update_model",
                  "npa_state_step_index", "npa_state_buffers", "npa_state_splat_2d",
                  "npa_state_decode_gaussians_3d", "npa_profile_enable", "npa_profile_reset",
-                 "npa_profile_read", "npa_state_pair_counts"):
+                 "npa_profile_read", "npa_state_pair_counts", "npa_splat_2d_tiled",
+                 "npa_state_splat_2d_tiled"):
         getattr(L, name).restype = st
 
 
@@ -79,7 +82,7 @@ EXPORTED = (
     "npa_state_destroy", "npa_state_step", "npa_state_read", "npa_state_update_model",
     "npa_state_step_index", "npa_state_buffers", "npa_state_splat_2d",
     "npa_state_decode_gaussians_3d", "npa_profile_enable", "npa_profile_reset", "npa_profile_read",
-    "npa_state_pair_counts")
+    "npa_state_pair_counts", "npa_splat_2d_tiled", "npa_state_splat_2d_tiled")
 
 
 def lib():

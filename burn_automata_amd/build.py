@@ -9,11 +9,14 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libnpa_hip.so")
 SOURCES = ["npa_hashgrid.hip", "npa_perception.hip", "npa_decode.hip", "npa_abi.hip"]
+# npa_perception.hip compiles as three objects (its NPA_PART selects which kernels each holds)
+PARTS = {"npa_perception.hip": ["-DNPA_PART=0", "-DNPA_PART=2", "-DNPA_PART=3"]}
 ARCH = os.environ.get("NPA_OFFLOAD_ARCH", "gfx950")
 
 
@@ -24,23 +27,45 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; the HIP library cannot be built")
 
 
+FLAGS = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Xclang", "-target-feature",
+         "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-variable", "-Wno-unused-function"]
+NOISE = "'-packed-fp32-ops' is not a recognized feature"
+
+
 def command(out: str = LIB) -> list:
-    return [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
-            "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-            "-Wall", "-Wno-unused-variable", "-Wno-unused-function",
-            "-o", out] + [os.path.join(CSRC, s) for s in SOURCES]
+    """One-shot compile-and-link command (the build runs the same flags per source in parallel)."""
+    return [hipcc(), f"--offload-arch={ARCH}", "-shared"] + FLAGS + ["-o", out] + \
+        [os.path.join(CSRC, s) for s in SOURCES]
+
+
+def _check(proc, what: str) -> str:
+    errs = "\n".join(l for l in proc.stderr.splitlines() if NOISE not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {what} ({proc.returncode}):\n{errs}")
+    return errs
 
 
 def build(verbose: bool = False) -> str:
+    """Compiles every source to an object in parallel, then links libnpa_hip.so."""
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    jobs = []
+    for src in SOURCES:
+        for k, part in enumerate(PARTS.get(src, [None])):
+            obj = os.path.join(objdir, src.replace(".hip", f"_{k}.o"))
+            cmd = [hipcc(), f"--offload-arch={ARCH}", "-c"] + FLAGS + ([part] if part else []) + \
+                ["-o", obj, os.path.join(CSRC, src)]
+            jobs.append((src, obj, cmd))
+    with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 1)) as pool:
+        procs = list(pool.map(lambda j: subprocess.run(j[2], capture_output=True, text=True), jobs))
+    log = [_check(proc, src) for (src, _, _), proc in zip(jobs, procs)]
+    objs = [obj for _, obj, _ in jobs]
     tmp = LIB + ".tmp"
-    cmd = command(tmp)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "'-packed-fp32-ops' is not a recognized feature"
-    errs = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
-    if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{errs}")
-    if verbose and errs.strip():
-        print(errs, file=sys.stderr)
+    link = subprocess.run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs,
+                          capture_output=True, text=True)
+    log.append(_check(link, "link"))
+    if verbose and any(l.strip() for l in log):
+        print("\n".join(log), file=sys.stderr)
     os.replace(tmp, LIB)
     return LIB
 

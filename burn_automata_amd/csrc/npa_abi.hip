@@ -666,7 +666,50 @@ npa_status npa_splat_2d(npa_context* ctx, const float* positions, const float* c
     if (io.err) return hip_fail(ctx, io.err, "staging");
     if ((count && !aligned16(pos)) || !aligned16(img))
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: positions and image must be 16-byte aligned");
-    NPA_HIP(ctx, npa::launch_splat_2d(pos, col, nullptr, 3, count, *cfg, img, ctx->splat_ws, ctx->stream, &ctx->prof),
+    NPA_HIP(ctx, npa::launch_splat_2d(pos, col, nullptr, 3, count, *cfg, img, ctx->splat_ws, ctx->stream, &ctx->prof,
+                                      count ? count : 1u, 1u, 1u),
+            "splat");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
+// Window grid of a tiled splat: rows of tiles_x windows, each image_size pixels square.
+static npa_status check_tiling(npa_context* ctx, const npa_splat2d_cfg* cfg, uint32_t B, uint32_t N, uint32_t tiles_x,
+                               uint64_t* pixels) {
+    if (B == 0 || N == 0) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: empty batch");
+    if (tiles_x == 0 || tiles_x > B)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: tiles_x must be in 1..=batch_size");
+    const uint64_t rows = (B + tiles_x - 1) / tiles_x;
+    const uint64_t side = cfg->image_size;
+    const uint64_t tiles_per_win = ((side + 15) / 16) * ((side + 15) / 16);
+    if (rows * tiles_x * tiles_per_win > 65536 || tiles_x * side > 16384 || rows * side > 16384)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT,
+                    "invalid argument: tiled image too large (at most 65536 16x16 tiles, 16384 pixels a side)");
+    if ((uint64_t)B * N >= (1ull << 31)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: too many particles");
+    *pixels = rows * side * tiles_x * side;
+    return NPA_OK;
+}
+
+npa_status npa_splat_2d_tiled(npa_context* ctx, const float* positions, const float* colors, uint32_t B, uint32_t N,
+                              const npa_splat2d_cfg* cfg, uint32_t tiles_x, float* image) {
+    if (!ctx || !image) return NPA_ERR_INVALID_ARGUMENT;
+    npa_status st = check_splat(ctx, cfg);
+    if (st) return st;
+    uint64_t pixels = 0;
+    if ((st = check_tiling(ctx, cfg, B, N, tiles_x, &pixels))) return st;
+    if (!colors || !positions) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null positions or colors");
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint32_t count = B * N;
+    HostIO io(ctx);
+    const float4* pos = (const float4*)io.in(positions, (uint64_t)count * 16);
+    const float* col = io.in(colors, (uint64_t)count * 12);
+    float* img = io.out(image, pixels * 16);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if (!aligned16(pos) || !aligned16(img))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: positions and image must be 16-byte aligned");
+    const uint32_t windows = (B + tiles_x - 1) / tiles_x * tiles_x;
+    NPA_HIP(ctx, npa::launch_splat_2d(pos, col, nullptr, 3, count, *cfg, img, ctx->splat_ws, ctx->stream, &ctx->prof, N,
+                                      windows, tiles_x),
             "splat");
     NPA_HIP(ctx, io.finish(), "host io");
     return NPA_OK;
@@ -842,7 +885,30 @@ npa_status npa_state_splat_2d(npa_state* s, const npa_splat2d_cfg* cfg, float* i
     if (!aligned16(img)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: image must be 16-byte aligned");
     NPA_HIP(ctx, npa::launch_splat_2d(s->pos[s->cur].as<float4>(), nullptr, s->states[s->cur].as<float>(),
                                       s->model.state_dims, (uint32_t)total, *cfg, img, s->splat_ws, ctx->stream,
-                                      &ctx->prof),
+                                      &ctx->prof, (uint32_t)total, 1u, 1u),
+            "splat");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
+npa_status npa_state_splat_2d_tiled(npa_state* s, const npa_splat2d_cfg* cfg, uint32_t tiles_x, float* image) {
+    if (!s || !image) return NPA_ERR_INVALID_ARGUMENT;
+    npa_context* ctx = s->ctx;
+    npa_status st = check_splat(ctx, cfg);
+    if (st) return st;
+    if (s->model.state_dims < 3)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: splat colours need state_dims >= 3");
+    uint64_t pixels = 0;
+    if ((st = check_tiling(ctx, cfg, s->B, s->N, tiles_x, &pixels))) return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    HostIO io(ctx);
+    float* img = io.out(image, pixels * 16);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if (!aligned16(img)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: image must be 16-byte aligned");
+    const uint32_t windows = (s->B + tiles_x - 1) / tiles_x * tiles_x;
+    NPA_HIP(ctx, npa::launch_splat_2d(s->pos[s->cur].as<float4>(), nullptr, s->states[s->cur].as<float>(),
+                                      s->model.state_dims, s->B * s->N, *cfg, img, s->splat_ws, ctx->stream,
+                                      &ctx->prof, s->N, windows, tiles_x),
             "splat");
     NPA_HIP(ctx, io.finish(), "host io");
     return NPA_OK;

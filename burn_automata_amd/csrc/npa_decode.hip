@@ -112,6 +112,11 @@ struct SplatParams {
     float lo, hi;
     int normalize, y_up;
     int S;
+    // Tiled layout: particle n belongs to window n / per_window; windows are laid out row-major,
+    // win_cols per row, each size x size pixels with tiles_x * tiles_y screen tiles; the image row
+    // stride is stride pixels. A single image is one window.
+    uint32_t per_window, win_cols, tiles_per_win;
+    int stride;
 };
 
 struct SplatParticle {  // 32 bytes
@@ -303,9 +308,10 @@ __global__ __launch_bounds__(256) void k_splat_emit(SplatParams P, const SplatPa
     int tx0, tx1, ty0, ty1;
     splat_tiles(P, sp[n].bx, sp[n].by, &tx0, &tx1, &ty0, &ty1);
     uint32_t k = start[n];
+    const uint32_t win_base = (n / P.per_window) * P.tiles_per_win;
     for (int ty = ty0; ty <= ty1; ++ty)
         for (int tx = tx0; tx <= tx1; ++tx) {
-            keys[k] = (uint32_t)(ty * P.tiles_x + tx);
+            keys[k] = win_base + (uint32_t)(ty * P.tiles_x + tx);
             vals[k] = n;
             ++k;
         }
@@ -316,7 +322,8 @@ __global__ __launch_bounds__(256) void k_splat_tiles(SplatParams P, const SplatP
                                                      const uint32_t* __restrict__ sorted, float* __restrict__ image) {
     __shared__ SplatParticle buf[256];
     const uint32_t t = blockIdx.x;
-    const int tx = (int)(t % P.tiles_x), ty = (int)(t / P.tiles_x);
+    const uint32_t win = t / P.tiles_per_win, lt = t - win * P.tiles_per_win;
+    const int tx = (int)(lt % P.tiles_x), ty = (int)(lt / P.tiles_x);
     const int x = tx * kTile + (int)(threadIdx.x % kTile);
     const int y = ty * kTile + (int)(threadIdx.x / kTile);
     const uint32_t beg = offsets[t], end = offsets[t + 1];
@@ -340,8 +347,11 @@ __global__ __launch_bounds__(256) void k_splat_tiles(SplatParams P, const SplatP
         }
         __syncthreads();
     }
-    if (x < P.size && y < P.size)
-        reinterpret_cast<float4*>(image)[(uint64_t)y * P.size + x] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    if (x < P.size && y < P.size) {
+        const uint64_t row = (uint64_t)(win / P.win_cols) * P.size + y;
+        const uint64_t col = (uint64_t)(win % P.win_cols) * P.size + x;
+        reinterpret_cast<float4*>(image)[row * P.stride + col] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    }
 }
 
 void SplatWorkspace::release() {
@@ -351,7 +361,8 @@ void SplatWorkspace::release() {
 
 hipError_t launch_splat_2d(const float4* pos, const float* colors, const float* states, uint32_t S,
                            uint32_t count, const npa_splat2d_cfg& cfg, float* image, SplatWorkspace& ws,
-                           hipStream_t stream, Profiler* prof) {
+                           hipStream_t stream, Profiler* prof, uint32_t per_window, uint32_t windows,
+                           uint32_t win_cols) {
     SplatParams P{};
     P.size = (int)cfg.image_size;
     const float fsz = (float)cfg.image_size;
@@ -375,9 +386,18 @@ hipError_t launch_splat_2d(const float4* pos, const float* colors, const float* 
     P.S = (int)S;
     P.tiles_x = (P.size + kTile - 1) / kTile;
     P.tiles_y = P.tiles_x;
-    const uint32_t ntile_total = (uint32_t)(P.tiles_x * P.tiles_y);
+    if (windows == 0 || win_cols == 0 || per_window == 0) return hipErrorInvalidValue;
+    if ((uint64_t)per_window * windows < count) return hipErrorInvalidValue;
+    P.per_window = per_window;
+    P.win_cols = win_cols;
+    P.tiles_per_win = (uint32_t)(P.tiles_x * P.tiles_y);
+    P.stride = (int)(win_cols * (uint32_t)P.size);
+    const uint64_t ntile64 = (uint64_t)P.tiles_per_win * windows;
+    if (ntile64 > 65536) return hipErrorInvalidValue;  // the key sort's bin limit
+    const uint32_t ntile_total = (uint32_t)ntile64;
+    const uint32_t ntile_win = P.tiles_per_win;
     const uint64_t per_axis = (uint64_t)((2 * P.radius + 1 + kTile - 1) / kTile + 1);
-    const uint64_t max_per = std::min<uint64_t>(per_axis * per_axis, ntile_total);
+    const uint64_t max_per = std::min<uint64_t>(per_axis * per_axis, ntile_win);
     const uint64_t cap64 = (uint64_t)count * max_per;
     if (cap64 >= (1ull << 31)) return hipErrorInvalidValue;
     const uint32_t cap = (uint32_t)cap64;

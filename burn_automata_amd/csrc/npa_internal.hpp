@@ -196,6 +196,12 @@ hipError_t launch_density(const StepParams& p, Workspace& ws, float* density_out
                           hipStream_t stream, Profiler* prof);
 hipError_t launch_update(const StepParams& p, Workspace& ws, const StepIO& io, int mode,
                          int grid_blocks, hipStream_t stream, Profiler* prof);
+// The second pass (and in mode 0 the MLP) of one dimension; launch_update runs them after the
+// update-mask kernel. `blocks` = one wave per block.
+hipError_t launch_second_pass_2d(const StepParams& p, Workspace& ws, const StepIO& io, int mode, int blocks,
+                                 hipStream_t stream, Profiler* prof);
+hipError_t launch_second_pass_3d(const StepParams& p, Workspace& ws, const StepIO& io, int mode, int blocks,
+                                 hipStream_t stream, Profiler* prof);
 // Padded weights for the MLP kernel: w1p [H][FP] (features at their padded positions),
 // b1 [H], w2t [H][D+SS] (transposed), b2p [D+SS]; zeros everywhere else.
 size_t padded_weight_floats(const StepParams& p);
@@ -221,9 +227,12 @@ struct SplatWorkspace {
     DevBuf params, item_start, keys, vals, sorted, ranks, table, totals, offsets, count, flags, scan;
     void release();
 };
+// Particle n is drawn into window n / per_window of a grid of `windows` windows, win_cols per
+// row, each cfg.image_size pixels square (one window: the plain splat).
 hipError_t launch_splat_2d(const float4* pos, const float* colors, const float* states,
                            uint32_t state_dims, uint32_t count, const npa_splat2d_cfg& cfg,
-                           float* image, SplatWorkspace& ws, hipStream_t stream, Profiler* prof);
+                           float* image, SplatWorkspace& ws, hipStream_t stream, Profiler* prof,
+                           uint32_t per_window, uint32_t windows, uint32_t win_cols);
 
 int device_cu_count();
 

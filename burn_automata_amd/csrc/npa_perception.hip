@@ -20,6 +20,16 @@
 
 #include "npa_internal.hpp"
 
+// The build compiles this file once per part so the kernel instantiations compile in parallel:
+// NPA_PART 0 holds the non-template kernels and the host launchers, 2 and 3 the second-pass and
+// MLP kernels of that dimension (undefined: everything, one object).
+#ifndef NPA_PART
+#define NPA_PART -1
+#endif
+#define NPA_PART_MAIN (NPA_PART < 0 || NPA_PART == 0)
+#define NPA_PART_DIM2 (NPA_PART < 0 || NPA_PART == 2)
+#define NPA_PART_DIM3 (NPA_PART < 0 || NPA_PART == 3)
+
 namespace npa {
 
 template <int D>
@@ -373,6 +383,7 @@ __device__ __forceinline__ void hold_particle(uint64_t i, uint32_t S, const Grid
 // window of a cell run into items of <= tpi targets {window base, target bitmask, first compact
 // row} and get consecutive compact rows (act_rows[row] = slot) for the feature rows and the MLP.
 // mask_mode: 0 every particle is a target (no copies), 1 the device hash mask, 2 a mask array.
+#if NPA_PART_MAIN
 constexpr uint32_t kActWaves = 16;
 
 __global__ __launch_bounds__(1024) void k_active(StepParams P, int mask_mode, uint32_t nbins, uint32_t tpi,
@@ -472,6 +483,8 @@ __global__ __launch_bounds__(1024) void k_active(StepParams P, int mask_mode, ui
         }
     }
 }
+
+#endif  // NPA_PART_MAIN
 
 // Per-wave accepted-neighbour lists of the second pass. Entry = (chunk id << 6) | k, the k-th
 // candidate of the target's chunk whose first sorted slot is cbase[chunk id][target]; entries of a
@@ -920,6 +933,7 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
     }
 }
 
+#if NPA_PART_MAIN
 // Pads the model weights into the MLP kernel's layout, zeros everywhere else:
 //   w1t [FP][HP]  w1 transposed, features at their padded positions, HP = H rounded up to 128
 //   b1p [HP]
@@ -963,6 +977,8 @@ __global__ __launch_bounds__(256) void k_pad_weights(StepParams P, int D, const 
         wpad[k] = v;
     }
 }
+
+#endif  // NPA_PART_MAIN
 
 // Update MLP + motion scaling + 3D gates + masked Euler for 64 sorted slots per 4-wave block.
 // forward_update_from_features model.rs:900-940, forward_from_features_with_eps model.rs:867-898,
@@ -1114,6 +1130,7 @@ __global__ __launch_bounds__(256) void k_mlp_euler(StepParams P, const float* __
     }
 }
 
+#if NPA_PART_MAIN
 // forward_from_features_with_eps (model.rs:867-940) for explicit feature rows.
 __global__ __launch_bounds__(256) void k_mlp_forward(StepParams P, const float* __restrict__ features,
                                                      uint32_t rows, const float* __restrict__ w1,
@@ -1179,6 +1196,8 @@ __global__ __launch_bounds__(256) void k_update_mask(uint32_t batch, uint32_t n,
     const uint32_t li = (uint32_t)(i - (uint64_t)b * n);
     mask[i] = hash_mask(li, b, n, p, step, base_seed);
 }
+
+#endif  // NPA_PART_MAIN
 
 // Candidates visited / pairs accepted by the neighbour walk (diagnostic, not on the step path):
 // counters[0..1] over every particle (the density pass), counters[2..4] the targets of the step's
@@ -1254,6 +1273,7 @@ __global__ __launch_bounds__(256) void k_neighbor_lists(StepParams P, const floa
 }
 
 // ------------------------------------------------------------------ launch
+#if NPA_PART_MAIN
 template <int D, int L>
 static void launch_density_t(const StepParams& p, Workspace& ws, float* density_out, int blocks, hipStream_t stream,
                              Profiler* prof) {
@@ -1287,6 +1307,8 @@ hipError_t launch_density(const StepParams& p_in, Workspace& ws, float* density_
     else launch_density_d<3>(p, ws, density_out, blocks, stream, prof);
     return hipGetLastError();
 }
+
+#endif  // NPA_PART_MAIN
 
 template <int D, int SM, int MODE, int FL>
 static void launch_perceive_f(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
@@ -1322,6 +1344,7 @@ static void launch_perceive_d(const StepParams& p, Workspace& ws, const StepIO& 
     }
 }
 
+#if NPA_PART_MAIN
 size_t padded_weight_floats(const StepParams& p) {
     const uint32_t D = (uint32_t)p.g.dim;
     const size_t HP = (p.H + 127) / 128 * 128;
@@ -1336,6 +1359,8 @@ hipError_t launch_pad_weights(const StepParams& p, const float* w1, const float*
     hipLaunchKernelGGL(k_pad_weights, dim3(blocks), dim3(256), 0, stream, p, p.g.dim, w1, b1, w2, b2, wpad);
     return hipGetLastError();
 }
+
+#endif  // NPA_PART_MAIN
 
 template <int D, int SM, int FM>
 static hipError_t launch_mlp_t(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream,
@@ -1377,6 +1402,31 @@ static hipError_t launch_mlp_d(const StepParams& p, Workspace& ws, const StepIO&
     }
 }
 
+// Second pass, then (mode 0) the update MLP, for one dimension.
+template <int D>
+static hipError_t launch_second_pass(const StepParams& p, Workspace& ws, const StepIO& io, int mode, int blocks,
+                                     hipStream_t stream, Profiler* prof) {
+    if (mode == 0) launch_perceive_d<D, 0>(p, ws, io, blocks, stream, prof);
+    else launch_perceive_d<D, 1>(p, ws, io, blocks, stream, prof);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || mode != 0) return e;
+    return launch_mlp_d<D>(p, ws, io, stream, prof);
+}
+
+#if NPA_PART_DIM2
+hipError_t launch_second_pass_2d(const StepParams& p, Workspace& ws, const StepIO& io, int mode, int blocks,
+                                 hipStream_t stream, Profiler* prof) {
+    return launch_second_pass<2>(p, ws, io, mode, blocks, stream, prof);
+}
+#endif
+#if NPA_PART_DIM3
+hipError_t launch_second_pass_3d(const StepParams& p, Workspace& ws, const StepIO& io, int mode, int blocks,
+                                 hipStream_t stream, Profiler* prof) {
+    return launch_second_pass<3>(p, ws, io, mode, blocks, stream, prof);
+}
+#endif
+
+#if NPA_PART_MAIN
 hipError_t launch_update(const StepParams& p_in, Workspace& ws, const StepIO& io, int mode, int grid_blocks,
                          hipStream_t stream, Profiler* prof) {
     const StepParams p = with_directory(p_in, ws);
@@ -1389,17 +1439,8 @@ hipError_t launch_update(const StepParams& p_in, Workspace& ws, const StepIO& io
                                 io.out_pos, io.out_states, ws.act_items.as<uint4>(), ws.act_rows.as<uint32_t>(),
                                 ws.wl_count.as<uint32_t>());
     if (e != hipSuccess) return e;
-    if (p.g.dim == 2) {
-        if (mode == 0) launch_perceive_d<2, 0>(p, ws, io, blocks, stream, prof);
-        else launch_perceive_d<2, 1>(p, ws, io, blocks, stream, prof);
-    } else {
-        if (mode == 0) launch_perceive_d<3, 0>(p, ws, io, blocks, stream, prof);
-        else launch_perceive_d<3, 1>(p, ws, io, blocks, stream, prof);
-    }
-    e = hipGetLastError();
-    if (e != hipSuccess || mode != 0) return e;
-    if (p.g.dim == 2) return launch_mlp_d<2>(p, ws, io, stream, prof);
-    return launch_mlp_d<3>(p, ws, io, stream, prof);
+    return p.g.dim == 2 ? launch_second_pass_2d(p, ws, io, mode, blocks, stream, prof)
+                        : launch_second_pass_3d(p, ws, io, mode, blocks, stream, prof);
 }
 
 hipError_t launch_mlp_forward(const StepParams& p, const float* features, uint32_t rows, const StepIO& io,
@@ -1455,5 +1496,7 @@ hipError_t launch_neighbor_lists(const StepParams& p, Workspace& ws, uint32_t* c
                            counts_or_offsets, indices, write);
     return hipGetLastError();
 }
+
+#endif  // NPA_PART_MAIN
 
 }  // namespace npa

@@ -99,6 +99,18 @@ class HipAutomataExecutor:
         self.ctx.check(lib().npa_state_splat_2d(state.handle, C.byref(cfg.to_c()), ptr(img)))
         return img
 
+    def splat_2d_tiled(self, state: HipAutomataState, cfg: Splat2dConfig, tiles_x: int):
+        """Every system in its own image_size-square window, tiles_x windows per row
+        (image [rows * size, tiles_x * size, 4])."""
+        import torch
+
+        rows = -(-state.batch_size // tiles_x)
+        img = torch.empty((rows * cfg.image_size, tiles_x * cfg.image_size, 4),
+                          dtype=torch.float32, device=f"cuda:{self.ctx.device}")
+        self.ctx.check(lib().npa_state_splat_2d_tiled(state.handle, C.byref(cfg.to_c()),
+                                                      int(tiles_x), ptr(img)))
+        return img
+
     def decode_gaussians_3d(self, state: HipAutomataState, cfg: GaussianDecodeConfig):
         import torch
 

@@ -220,3 +220,21 @@ def splat_particles_2d(positions, colors, cfg: Splat2dConfig, ctx=None):
     ctx.check(lib().npa_splat_2d(ctx.handle, ptr(pos), ptr(col), pos.shape[0],
                                  C.byref(cfg.to_c()), ptr(img)))
     return img
+
+
+def splat_particles_2d_tiled(positions, colors, batch_size: int, particle_count: int,
+                             cfg: Splat2dConfig, tiles_x: int, ctx=None):
+    """Each of batch_size systems drawn as splat_particles_2d draws it alone, in its own
+    image_size-square window (tiles_x windows per row): image [rows * size, tiles_x * size, 4]."""
+    ctx = ctx or default_context()
+    torch = _torch()
+    pos = device_f32(positions, device=ctx.device).reshape(-1, 4)
+    col = device_f32(colors, device=ctx.device).reshape(-1, 3)
+    if col.shape[0] != pos.shape[0] or pos.shape[0] != batch_size * particle_count:
+        raise AssertionError("positions.len() != colors.len() != batch_size * particle_count")
+    rows = -(-batch_size // max(tiles_x, 1))
+    img = torch.empty((rows * cfg.image_size, max(tiles_x, 1) * cfg.image_size, 4),
+                      dtype=torch.float32, device=f"cuda:{ctx.device}")
+    ctx.check(lib().npa_splat_2d_tiled(ctx.handle, ptr(pos), ptr(col), batch_size, particle_count,
+                                       C.byref(cfg.to_c()), int(tiles_x), ptr(img)))
+    return img

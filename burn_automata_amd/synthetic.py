@@ -21,7 +21,8 @@ import math
 
 import numpy as np
 
-from .config import (Boundary, HashGridConfig, HashGridMode, NpaConfig, Splat2dConfig)
+from .config import (Boundary, GaussianDecodeConfig, GaussianDecodeMode, HashGridConfig, HashGridMode,
+                     NpaConfig, Splat2dConfig)
 
 _M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
 
@@ -221,17 +222,25 @@ def workload(name: str, seed: int = 42, particles: int | None = None):
         model = NpaConfig.growing_3dgs().replace(state_dims=16, hidden_dims=128, eps0=0.04,
                                                  density_grad=False, alpha=0.5)
         grid = HashGridConfig(3, Boundary.Clamped, HashGridMode.Particle, (32, 32, 32), 0.04, 64)
+        # decode: oriented Gaussians (gaussian.rs:53-223), drawn as an isotropic 2D splat of their
+        # x/y centres and SH0 colours (the oriented 3D raster has no reference CPU path)
         return dict(model=model, grid=grid, batch=1, n=n, positions=closed_surface_3d(n, seed),
                     states=normal_states(n, model.state_dims, seed),
                     weights=seeded_weights(model, seed), steps=256, dt=1.0, update_prob=0.5,
-                    seed=seed, decode_every=32)
+                    seed=seed, decode_every=32,
+                    decode=GaussianDecodeConfig(mode=GaussianDecodeMode.GaussianSh0Oriented),
+                    splat=Splat2dConfig(image_size=512, sigma=0.004 * 511 / 2, lo=-1.0, hi=1.0,
+                                        normalize_color=True, y_up=True, pixel_size=2.0 / 512))
     if name == "c5":
         n = particles or 4096
         b = 64
         model, grid = config_c1(n, seed)
         pos = np.concatenate([uniform_disk(n, seed, offset=k * n) for k in range(b)], axis=0)
+        # decode at steps 64 and 256: each system in a 128x128 window of a 1024x1024 image
         return dict(model=model, grid=grid, batch=b, n=n, positions=pos,
                     states=normal_states(b * n, model.state_dims, seed),
                     weights=seeded_weights(model, seed, bf16=True), steps=256, dt=1.0,
-                    update_prob=0.5, seed=seed)
+                    update_prob=0.5, seed=seed, decode_steps=(64, 256), tiles_x=8,
+                    splat=Splat2dConfig(image_size=128, sigma=0.004 * 127 / 2, lo=-1.0, hi=1.0,
+                                        normalize_color=True, y_up=True, pixel_size=2.0 / 128))
     raise ValueError(f"unknown workload {name!r}")

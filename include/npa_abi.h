@@ -228,6 +228,16 @@ npa_status npa_decode_gaussians_3d(npa_context* ctx, const float* positions,
 npa_status npa_splat_2d(npa_context* ctx, const float* positions, const float* colors,
                         uint32_t count, const npa_splat2d_cfg* cfg, float* image);
 
+/* Batched systems drawn side by side (no counterpart in the reference, whose
+ * splat_particles_2d draws one system; used for batched rollouts): system b of
+ * batch_size systems of particle_count particles is drawn exactly as
+ * splat_particles_2d draws it alone into an image_size-square window, placed at
+ * window column b % tiles_x, row b / tiles_x. image[rows*size][tiles_x*size][4]
+ * with rows = ceil(batch_size / tiles_x); windows past the last system are zero. */
+npa_status npa_splat_2d_tiled(npa_context* ctx, const float* positions, const float* colors,
+                              uint32_t batch_size, uint32_t particle_count,
+                              const npa_splat2d_cfg* cfg, uint32_t tiles_x, float* image);
+
 /* ----------------------------------- device-resident executor (L2 twin) */
 /* Replaces WgpuAutomataExecutor::create_state_with_update_prob
  * (crates/burn_automata/src/gpu/executor/state.rs:82-111). positions/states/weights
@@ -253,6 +263,10 @@ npa_status npa_state_buffers(npa_state* state, float** positions, float** states
 /* Splat the current particles with colors clamp(state[S-3..S]+0.5, 0, 1)
  * (crates/burn_automata/examples/infer_2d.rs:20-39). image per context I/O mode. */
 npa_status npa_state_splat_2d(npa_state* state, const npa_splat2d_cfg* cfg, float* image);
+/* npa_splat_2d_tiled of the current particles, one window per system, colours as in
+ * npa_state_splat_2d. */
+npa_status npa_state_splat_2d_tiled(npa_state* state, const npa_splat2d_cfg* cfg, uint32_t tiles_x,
+                                    float* image);
 /* decode_gaussians_3d of the current particles (the planar export the viewer reads,
  * cf. write_gaussian_main gpu_step.wgsl:4929-5052). */
 npa_status npa_state_decode_gaussians_3d(npa_state* state, const npa_gaussian_decode_cfg* cfg,

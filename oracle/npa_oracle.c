@@ -506,17 +506,20 @@ uint32_t oracle_feature_dims(uint32_t S, uint32_t dim, const npa_perception_opts
 }
 
 /* density  forward.rs:145-160 */
+/* Every pass below runs over `rows` targets: particle sel[r] (or r when sel is NULL) writes
+ * output row r, so a pass can evaluate a sample of a system too large for a full pass. */
 static void pass_density(const float* positions, const grid_view* g, const npa_grid_cfg* cfg,
-                         uint64_t total, float* rho_out) {
+                         const uint32_t* sel, uint64_t rows, float* rho_out) {
 #pragma omp parallel
     {
         nbuf buf = {0};
 #pragma omp for schedule(dynamic, 64)
-        for (int64_t i = 0; i < (int64_t)total; ++i) {
-            collect_neighbors((uint64_t)i, positions, g, cfg, &buf);
+        for (int64_t r = 0; r < (int64_t)rows; ++r) {
+            const uint64_t i = sel ? sel[r] : (uint64_t)r;
+            collect_neighbors(i, positions, g, cfg, &buf);
             float rho = 0.0f;
             for (size_t k = 0; k < buf.len; ++k) rho += poly6(buf.v[k].r2, cfg);
-            rho_out[i] = rho;
+            rho_out[r] = rho;
         }
         free(buf.v);
     }
@@ -524,20 +527,20 @@ static void pass_density(const float* positions, const grid_view* g, const npa_g
 
 /* second_pass_particle  forward.rs:248-295 (density_grad && state_grad branch) */
 static void pass_second(const float* positions, const float* states, const float* density,
-                        uint32_t S, const grid_view* g, const npa_grid_cfg* cfg, uint64_t total,
-                        float* blur, float* sgrad, float* dgrad, float* moment) {
+                        uint32_t S, const grid_view* g, const npa_grid_cfg* cfg, const uint32_t* sel,
+                        uint64_t rows, float* blur, float* sgrad, float* dgrad, float* moment) {
     const uint32_t d = cfg->dim;
 #pragma omp parallel
     {
         nbuf buf = {0};
 #pragma omp for schedule(dynamic, 64)
-        for (int64_t ii = 0; ii < (int64_t)total; ++ii) {
-            uint64_t idx = (uint64_t)ii;
+        for (int64_t r = 0; r < (int64_t)rows; ++r) {
+            const uint64_t idx = sel ? sel[r] : (uint64_t)r;
             collect_neighbors(idx, positions, g, cfg, &buf);
-            float* blur_row = blur + idx * S;
-            float* grad_row = sgrad + idx * S * d;
-            float* dg_row = dgrad + idx * d;
-            float* m_row = moment ? moment + idx * d * d : NULL;
+            float* blur_row = blur + (uint64_t)r * S;
+            float* grad_row = sgrad + (uint64_t)r * S * d;
+            float* dg_row = dgrad + (uint64_t)r * d;
+            float* m_row = moment ? moment + (uint64_t)r * d * d : NULL;
             const float* si = states + idx * S;
             for (size_t k = 0; k < buf.len; ++k) {
                 const neighbor* n = &buf.v[k];
@@ -565,15 +568,16 @@ static void pass_second(const float* positions, const float* states, const float
 
 /* blur_state  forward.rs:162-184 */
 static void pass_blur(const float* positions, const float* states, const float* density,
-                      uint32_t S, const grid_view* g, const npa_grid_cfg* cfg, uint64_t total,
-                      float* out) {
+                      uint32_t S, const grid_view* g, const npa_grid_cfg* cfg, const uint32_t* sel,
+                      uint64_t rows, float* out) {
 #pragma omp parallel
     {
         nbuf buf = {0};
 #pragma omp for schedule(dynamic, 64)
-        for (int64_t i = 0; i < (int64_t)total; ++i) {
-            collect_neighbors((uint64_t)i, positions, g, cfg, &buf);
-            float* dst = out + (uint64_t)i * S;
+        for (int64_t r = 0; r < (int64_t)rows; ++r) {
+            const uint64_t i = sel ? sel[r] : (uint64_t)r;
+            collect_neighbors(i, positions, g, cfg, &buf);
+            float* dst = out + (uint64_t)r * S;
             for (size_t k = 0; k < buf.len; ++k) {
                 const neighbor* n = &buf.v[k];
                 float volume_j = recip_finite(density[n->j]);
@@ -588,18 +592,19 @@ static void pass_blur(const float* positions, const float* states, const float* 
 
 /* moment_matrix  forward.rs:357-382 */
 static void pass_moment(const float* positions, const float* density, const grid_view* g,
-                        const npa_grid_cfg* cfg, uint64_t total, float* out) {
+                        const npa_grid_cfg* cfg, const uint32_t* sel, uint64_t rows, float* out) {
     const uint32_t d = cfg->dim;
 #pragma omp parallel
     {
         nbuf buf = {0};
 #pragma omp for schedule(dynamic, 64)
-        for (int64_t i = 0; i < (int64_t)total; ++i) {
-            collect_neighbors((uint64_t)i, positions, g, cfg, &buf);
-            float* dst = out + (uint64_t)i * d * d;
+        for (int64_t r = 0; r < (int64_t)rows; ++r) {
+            const uint64_t i = sel ? sel[r] : (uint64_t)r;
+            collect_neighbors(i, positions, g, cfg, &buf);
+            float* dst = out + (uint64_t)r * d * d;
             for (size_t k = 0; k < buf.len; ++k) {
                 const neighbor* n = &buf.v[k];
-                if ((uint64_t)i == n->j) continue;
+                if (i == n->j) continue;
                 float volume_j = recip_finite(density[n->j]);
                 float grad[4];
                 spiky_grad(n->delta, n->r2, cfg, volume_j, grad);
@@ -614,19 +619,21 @@ static void pass_moment(const float* positions, const float* density, const grid
 /* compute_state_gradient  forward.rs:297-333 */
 static void pass_state_gradient(const float* positions, const float* states,
                                 const float* density, uint32_t S, const grid_view* g,
-                                const npa_grid_cfg* cfg, uint64_t total, int hybrid, float* out) {
+                                const npa_grid_cfg* cfg, const uint32_t* sel, uint64_t rows, int hybrid,
+                                float* out) {
     const uint32_t d = cfg->dim;
 #pragma omp parallel
     {
         nbuf buf = {0};
 #pragma omp for schedule(dynamic, 64)
-        for (int64_t i = 0; i < (int64_t)total; ++i) {
-            collect_neighbors((uint64_t)i, positions, g, cfg, &buf);
-            float* dst = out + (uint64_t)i * S * d;
-            const float* si = states + (uint64_t)i * S;
+        for (int64_t r = 0; r < (int64_t)rows; ++r) {
+            const uint64_t i = sel ? sel[r] : (uint64_t)r;
+            collect_neighbors(i, positions, g, cfg, &buf);
+            float* dst = out + (uint64_t)r * S * d;
+            const float* si = states + i * S;
             for (size_t k = 0; k < buf.len; ++k) {
                 const neighbor* n = &buf.v[k];
-                if ((uint64_t)i == n->j) continue;
+                if (i == n->j) continue;
                 float volume_j = recip_finite(density[n->j]);
                 float grad[4];
                 spiky_grad(n->delta, n->r2, cfg, volume_j, grad);
@@ -640,27 +647,28 @@ static void pass_state_gradient(const float* positions, const float* states,
         free(buf.v);
     }
     if (hybrid) {
-        float* moment = (float*)calloc(total * d * d + 1, sizeof(float));
-        pass_moment(positions, density, g, cfg, total, moment);
-        apply_moment_correction(out, moment, total, S, cfg);
+        float* moment = (float*)calloc(rows * d * d + 1, sizeof(float));
+        pass_moment(positions, density, g, cfg, sel, rows, moment);
+        apply_moment_correction(out, moment, rows, S, cfg);
         free(moment);
     }
 }
 
 /* compute_density_gradient  forward.rs:335-355 */
 static void pass_density_gradient(const float* positions, const grid_view* g,
-                                  const npa_grid_cfg* cfg, uint64_t total, float* out) {
+                                  const npa_grid_cfg* cfg, const uint32_t* sel, uint64_t rows, float* out) {
     const uint32_t d = cfg->dim;
 #pragma omp parallel
     {
         nbuf buf = {0};
 #pragma omp for schedule(dynamic, 64)
-        for (int64_t i = 0; i < (int64_t)total; ++i) {
-            collect_neighbors((uint64_t)i, positions, g, cfg, &buf);
-            float* dst = out + (uint64_t)i * d;
+        for (int64_t r = 0; r < (int64_t)rows; ++r) {
+            const uint64_t i = sel ? sel[r] : (uint64_t)r;
+            collect_neighbors(i, positions, g, cfg, &buf);
+            float* dst = out + (uint64_t)r * d;
             for (size_t k = 0; k < buf.len; ++k) {
                 const neighbor* n = &buf.v[k];
-                if ((uint64_t)i == n->j) continue;
+                if (i == n->j) continue;
                 float grad[4];
                 spiky_grad(n->delta, n->r2, cfg, 1.0f, grad);
                 for (uint32_t a = 0; a < d; ++a) dst[a] += grad[a];
@@ -668,6 +676,75 @@ static void pass_density_gradient(const float* positions, const grid_view* g,
         }
         free(buf.v);
     }
+}
+
+/* The second half of perceive_with_options (forward.rs:26-143) for targets sel[0..rows) (all
+ * particles when sel is NULL), given the density of every particle: second pass, moment
+ * correction, normalisation and feature rows, written to rows 0..rows of the outputs. */
+static int perceive_rows(const float* positions, const float* states, uint32_t particle_count,
+                         uint32_t S, const npa_grid_cfg* cfg, const npa_perception_opts* o,
+                         const grid_view* g, const float* density, const uint32_t* sel,
+                         uint64_t rows, float* features, float* blurred_out, float* sgrad_out,
+                         float* dgrad_out) {
+    const uint32_t d = cfg->dim;
+    float* blur = (float*)calloc(rows * S + 1, sizeof(float));
+    float* sgrad = (float*)calloc(o->state_grad ? rows * S * d + 1 : 1, sizeof(float));
+    float* dgrad = (float*)calloc(o->density_grad ? rows * d + 1 : 1, sizeof(float));
+    if (!blur || !sgrad || !dgrad) {
+        free(blur);
+        free(sgrad);
+        free(dgrad);
+        return NPA_ERR_OUT_OF_MEMORY;
+    }
+    if (o->state_grad && o->density_grad) {
+        float* moment = o->hybrid_state_gradient ? (float*)calloc(rows * d * d + 1, sizeof(float)) : NULL;
+        pass_second(positions, states, density, S, g, cfg, sel, rows, blur, sgrad, dgrad, moment);
+        if (moment) apply_moment_correction(sgrad, moment, rows, S, cfg);
+        normalize_state_gradient(sgrad, rows, S, cfg, o);
+        normalize_density_gradient(dgrad, rows, particle_count, cfg, o);
+        free(moment);
+    } else {
+        pass_blur(positions, states, density, S, g, cfg, sel, rows, blur);
+        if (o->state_grad) {
+            pass_state_gradient(positions, states, density, S, g, cfg, sel, rows,
+                                (int)o->hybrid_state_gradient, sgrad);
+            normalize_state_gradient(sgrad, rows, S, cfg, o);
+        }
+        if (o->density_grad) {
+            pass_density_gradient(positions, g, cfg, sel, rows, dgrad);
+            normalize_density_gradient(dgrad, rows, particle_count, cfg, o);
+        }
+    }
+
+    const uint32_t F = oracle_feature_dims(S, d, o);
+    if (features) {
+#pragma omp parallel for schedule(static)
+        for (int64_t r = 0; r < (int64_t)rows; ++r) {
+            const uint64_t i = sel ? sel[r] : (uint64_t)r;
+            float* f = features + (uint64_t)r * F;
+            uint32_t cur = 0;
+            memcpy(f + cur, states + i * S, S * sizeof(float));
+            cur += S;
+            memcpy(f + cur, blur + (uint64_t)r * S, S * sizeof(float));
+            cur += S;
+            if (o->state_grad) {
+                memcpy(f + cur, sgrad + (uint64_t)r * S * d, S * d * sizeof(float));
+                cur += S * d;
+            }
+            if (o->density_grad) {
+                memcpy(f + cur, dgrad + (uint64_t)r * d, d * sizeof(float));
+                cur += d;
+            }
+            if (o->position_features) memcpy(f + cur, positions + 4 * i, d * sizeof(float));
+        }
+    }
+    if (blurred_out) memcpy(blurred_out, blur, rows * S * sizeof(float));
+    if (sgrad_out && o->state_grad) memcpy(sgrad_out, sgrad, rows * S * d * sizeof(float));
+    if (dgrad_out && o->density_grad) memcpy(dgrad_out, dgrad, rows * d * sizeof(float));
+    free(blur);
+    free(sgrad);
+    free(dgrad);
+    return NPA_OK;
 }
 
 /* perceive_with_options  crates/burn_automata_kernels/src/reference/forward.rs:26-143 */
@@ -678,67 +755,29 @@ int oracle_perceive(const float* positions, const float* states, uint32_t batch_
     int st = oracle_grid_validate(cfg);
     if (st) return st;
     const uint64_t total = (uint64_t)batch_size * particle_count;
-    const uint32_t d = cfg->dim;
     hashgrid h;
     st = hashgrid_build(positions, batch_size, particle_count, cfg, &h);
     if (st) {
         hashgrid_free(&h);
         return st;
     }
-    pass_density(positions, &h.view, cfg, total, density);
-
-    float* blur = (float*)calloc(total * S + 1, sizeof(float));
-    float* sgrad = (float*)calloc(o->state_grad ? total * S * d + 1 : 1, sizeof(float));
-    float* dgrad = (float*)calloc(o->density_grad ? total * d + 1 : 1, sizeof(float));
-    if (o->state_grad && o->density_grad) {
-        float* moment = o->hybrid_state_gradient ? (float*)calloc(total * d * d + 1, sizeof(float)) : NULL;
-        pass_second(positions, states, density, S, &h.view, cfg, total, blur, sgrad, dgrad, moment);
-        if (moment) apply_moment_correction(sgrad, moment, total, S, cfg);
-        normalize_state_gradient(sgrad, total, S, cfg, o);
-        normalize_density_gradient(dgrad, total, particle_count, cfg, o);
-        free(moment);
-    } else {
-        pass_blur(positions, states, density, S, &h.view, cfg, total, blur);
-        if (o->state_grad) {
-            pass_state_gradient(positions, states, density, S, &h.view, cfg, total,
-                                (int)o->hybrid_state_gradient, sgrad);
-            normalize_state_gradient(sgrad, total, S, cfg, o);
-        }
-        if (o->density_grad) {
-            pass_density_gradient(positions, &h.view, cfg, total, dgrad);
-            normalize_density_gradient(dgrad, total, particle_count, cfg, o);
-        }
-    }
-
-    const uint32_t F = oracle_feature_dims(S, d, o);
-    if (features) {
-#pragma omp parallel for schedule(static)
-        for (int64_t i = 0; i < (int64_t)total; ++i) {
-            float* f = features + (uint64_t)i * F;
-            uint32_t cur = 0;
-            memcpy(f + cur, states + (uint64_t)i * S, S * sizeof(float));
-            cur += S;
-            memcpy(f + cur, blur + (uint64_t)i * S, S * sizeof(float));
-            cur += S;
-            if (o->state_grad) {
-                memcpy(f + cur, sgrad + (uint64_t)i * S * d, S * d * sizeof(float));
-                cur += S * d;
-            }
-            if (o->density_grad) {
-                memcpy(f + cur, dgrad + (uint64_t)i * d, d * sizeof(float));
-                cur += d;
-            }
-            if (o->position_features) memcpy(f + cur, positions + 4 * (uint64_t)i, d * sizeof(float));
-        }
-    }
-    if (blurred_out) memcpy(blurred_out, blur, total * S * sizeof(float));
-    if (sgrad_out && o->state_grad) memcpy(sgrad_out, sgrad, total * S * d * sizeof(float));
-    if (dgrad_out && o->density_grad) memcpy(dgrad_out, dgrad, total * d * sizeof(float));
-    free(blur);
-    free(sgrad);
-    free(dgrad);
+    pass_density(positions, &h.view, cfg, NULL, total, density);
+    st = perceive_rows(positions, states, particle_count, S, cfg, o, &h.view, density, NULL, total,
+                       features, blurred_out, sgrad_out, dgrad_out);
     hashgrid_free(&h);
-    return NPA_OK;
+    return st;
+}
+
+/* density (forward.rs:145-160) of the particles sel[0..rows) only, into rho_out[0..rows). */
+int oracle_density_rows(const float* positions, uint32_t batch_size, uint32_t particle_count,
+                        const npa_grid_cfg* cfg, const uint32_t* sel, uint64_t rows, float* rho_out) {
+    int st = oracle_grid_validate(cfg);
+    if (st) return st;
+    hashgrid h;
+    st = hashgrid_build(positions, batch_size, particle_count, cfg, &h);
+    if (!st) pass_density(positions, &h.view, cfg, sel, rows, rho_out);
+    hashgrid_free(&h);
+    return st;
 }
 
 /* ------------------------------------------------------------------ model */
@@ -865,6 +904,55 @@ static float motion_gate(float liveness, float signed_distance, int anchored) {
     return state_gate * distance_gate;
 }
 
+/* The update half of NpaModel::step_cpu (model.rs:800-858) for `rows` feature rows: the MLP and
+ * motion scaling, the 3D gates and the masked Euler step. Row r is particle sel[r] (r when sel is
+ * NULL) of `positions` / `states` / `mask`; outputs are written to rows 0..rows. */
+static int update_rows(const float* positions, const float* states, const float* mask,
+                       const uint32_t* sel, uint64_t rows, const npa_grid_cfg* grid,
+                       const npa_model_cfg* m, const npa_weights* w, float dt,
+                       const float* features, float* out_pos, float* out_states, float* out_dx,
+                       float* out_ds) {
+    const uint32_t S = m->state_dims;
+    float* dx = (float*)malloc((rows * 4 + 1) * sizeof(float));
+    float* ds = (float*)malloc((rows * S + 1) * sizeof(float));
+    float* gp = sel ? (float*)malloc((rows * 4 + 1) * sizeof(float)) : NULL;
+    float* gs = sel ? (float*)malloc((rows * S + 1) * sizeof(float)) : NULL;
+    float* gm = sel && mask ? (float*)malloc((rows + 1) * sizeof(float)) : NULL;
+    int st = (!dx || !ds || (sel && (!gp || !gs)) || (sel && mask && !gm)) ? NPA_ERR_OUT_OF_MEMORY : NPA_OK;
+    if (!st && sel) {
+        for (uint64_t r = 0; r < rows; ++r) {
+            memcpy(gp + 4 * r, positions + 4 * (uint64_t)sel[r], 4 * sizeof(float));
+            memcpy(gs + r * S, states + (uint64_t)sel[r] * S, S * sizeof(float));
+            if (gm) gm[r] = mask[sel[r]];
+        }
+        positions = gp;
+        states = gs;
+        mask = gm;
+    }
+    if (!st) st = oracle_forward_from_features(features, (uint32_t)rows, m, w, grid->eps, dx, ds);
+    if (!st && m->spatial_dims == 3 && m->position_features && S > 3) {
+        for (uint64_t r = 0; r < rows; ++r) {
+            const float* s = states + r * S;
+            float liveness = s[3];                    /* GROWTH_3D_LIVENESS_CHANNEL */
+            float signed_distance = s[7];             /* UV_TORUS_SIGNED_DISTANCE_STATE_OFFSET */
+            float sg = maturity_gate(liveness);
+            float mg = motion_gate(liveness, signed_distance, positions[4 * r + 3] >= 0.5f);
+            for (uint32_t a = 0; a < m->spatial_dims; ++a) dx[4 * r + a] *= mg;
+            for (uint32_t c = 0; c < S; ++c) ds[r * S + c] *= sg;
+        }
+    }
+    if (!st) st = oracle_euler_step(positions, states, dx, ds, 1, (uint32_t)rows, S, grid, dt, mask,
+                                    out_pos, out_states);
+    if (!st && out_dx) memcpy(out_dx, dx, rows * 4 * sizeof(float));
+    if (!st && out_ds) memcpy(out_ds, ds, rows * S * sizeof(float));
+    free(dx);
+    free(ds);
+    free(gp);
+    free(gs);
+    free(gm);
+    return st;
+}
+
 /* NpaModel::step_cpu  crates/burn_automata/src/model.rs:768-858 */
 int oracle_step(const float* positions, const float* states, uint32_t batch_size,
                 uint32_t particle_count, const npa_grid_cfg* grid, const npa_model_cfg* m,
@@ -880,41 +968,54 @@ int oracle_step(const float* positions, const float* states, uint32_t batch_size
     float* features = (float*)malloc((total * F + 1) * sizeof(float));
     float* density = (float*)malloc((total + 1) * sizeof(float));
     float* blur = (float*)malloc((total * S + 1) * sizeof(float));
-    float* dx = (float*)malloc((total * 4 + 1) * sizeof(float));
-    float* ds = (float*)malloc((total * S + 1) * sizeof(float));
-    if (!features || !density || !blur || !dx || !ds) return NPA_ERR_OUT_OF_MEMORY;
+    if (!features || !density || !blur) {
+        free(features);
+        free(density);
+        free(blur);
+        return NPA_ERR_OUT_OF_MEMORY;
+    }
 
     double t0 = omp_get_wtime();
     int st = oracle_perceive(positions, states, batch_size, particle_count, S, grid, &o, features,
                              density, blur, NULL, NULL);
     double t1 = omp_get_wtime();
-    if (!st) st = oracle_forward_from_features(features, (uint32_t)total, m, w, grid->eps, dx, ds);
+    if (!st) st = update_rows(positions, states, mask, NULL, total, grid, m, w, dt, features, out_pos,
+                              out_states, out_dx, out_ds);
     double t2 = omp_get_wtime();
-    if (!st && m->spatial_dims == 3 && m->position_features && S > 3) {
-        for (uint64_t r = 0; r < total; ++r) {
-            const float* s = states + r * S;
-            float liveness = s[3];                    /* GROWTH_3D_LIVENESS_CHANNEL */
-            float signed_distance = s[7];             /* UV_TORUS_SIGNED_DISTANCE_STATE_OFFSET */
-            float sg = maturity_gate(liveness);
-            float mg = motion_gate(liveness, signed_distance, positions[4 * r + 3] >= 0.5f);
-            for (uint32_t a = 0; a < m->spatial_dims; ++a) dx[4 * r + a] *= mg;
-            for (uint32_t c = 0; c < S; ++c) ds[r * S + c] *= sg;
-        }
-    }
-    if (!st) st = oracle_euler_step(positions, states, dx, ds, batch_size, particle_count, S, grid,
-                                    dt, mask, out_pos, out_states);
-    double t3 = omp_get_wtime();
     g_phase_perceive = t1 - t0;
-    g_phase_mlp = t2 - t1;
-    g_phase_integrate = t3 - t2;
+    g_phase_mlp = t2 - t1;  /* MLP, gates and Euler */
+    g_phase_integrate = 0.0;
     if (out_density) memcpy(out_density, density, total * sizeof(float));
-    if (out_dx) memcpy(out_dx, dx, total * 4 * sizeof(float));
-    if (out_ds) memcpy(out_ds, ds, total * S * sizeof(float));
     free(features);
     free(density);
     free(blur);
-    free(dx);
-    free(ds);
+    return st;
+}
+
+/* NpaModel::step_cpu for the particles sel[0..rows) only, given the density of every particle
+ * (the first pass's output): second pass, feature rows, update MLP, gates and Euler step of those
+ * particles, written to rows 0..rows of out_positions / out_states. */
+int oracle_step_rows(const float* positions, const float* states, uint32_t batch_size,
+                     uint32_t particle_count, const npa_grid_cfg* grid, const npa_model_cfg* m,
+                     const npa_weights* w, float dt, const float* mask, const float* density,
+                     const uint32_t* sel, uint64_t rows, float* out_pos, float* out_states) {
+    if (!(m->spatial_dims == 2 || m->spatial_dims == 3)) return NPA_ERR_INVALID_MODEL;
+    if (grid->dim != m->spatial_dims) return NPA_ERR_INVALID_ARGUMENT;
+    int st = oracle_grid_validate(grid);
+    if (st) return st;
+    npa_perception_opts o;
+    oracle_perception_opts_for_model(m, &o);
+    const uint32_t F = oracle_model_perception_dims(m);
+    float* features = (float*)malloc((rows * F + 1) * sizeof(float));
+    if (!features) return NPA_ERR_OUT_OF_MEMORY;
+    hashgrid h;
+    st = hashgrid_build(positions, batch_size, particle_count, grid, &h);
+    if (!st) st = perceive_rows(positions, states, particle_count, m->state_dims, grid, &o, &h.view,
+                                density, sel, rows, features, NULL, NULL, NULL);
+    if (!st) st = update_rows(positions, states, mask, sel, rows, grid, m, w, dt, features, out_pos,
+                              out_states, NULL, NULL);
+    hashgrid_free(&h);
+    free(features);
     return st;
 }
 

@@ -83,6 +83,18 @@ int oracle_step(const float* positions, const float* states, uint32_t batch_size
                 float* out_positions, float* out_states, float* out_density, float* out_dx,
                 float* out_ds);
 
+/* Sampled evaluation for systems too large for a full pass: the density of particles
+ * sel[0..rows) only, and one step_cpu of those particles given every particle's density
+ * (rows 0..rows of the outputs). */
+int oracle_density_rows(const float* positions, uint32_t batch_size, uint32_t particle_count,
+                        const npa_grid_cfg* cfg, const uint32_t* sel, uint64_t rows,
+                        float* density);
+int oracle_step_rows(const float* positions, const float* states, uint32_t batch_size,
+                     uint32_t particle_count, const npa_grid_cfg* grid, const npa_model_cfg* model,
+                     const npa_weights* weights, float dt, const float* update_mask,
+                     const float* density, const uint32_t* sel, uint64_t rows,
+                     float* out_positions, float* out_states);
+
 uint32_t oracle_hash_u32(uint32_t value);
 float oracle_random01(uint32_t particle, uint32_t step, uint32_t seed);
 uint32_t oracle_gpu_random_seed(uint64_t seed);
@@ -106,7 +118,7 @@ int oracle_splat_particles_2d(const float* positions, const float* colors, uint3
                               const npa_splat2d_cfg* cfg, float* image);
 
 /* Per-phase wall-clock seconds of the last oracle_step / oracle_rollout call
- * (hashgrid+perceive, MLP, integrate), following profile_rollout
+ * (hashgrid+perceive, MLP+gates+integrate, 0), following profile_rollout
  * (crates/burn_automata/src/cli/bench.rs:652-722). */
 void oracle_last_phase_seconds(double* perceive, double* mlp, double* integrate);
 int oracle_max_threads(void);

@@ -74,6 +74,10 @@ def _declare(L):
     L.oracle_step.argtypes = [P, P, u32, u32, C.POINTER(_abi.NpaGridCfg),
                               C.POINTER(_abi.NpaModelCfg), C.POINTER(_abi.NpaWeightsC), f32, P,
                               P, P, P, P, P]
+    L.oracle_density_rows.argtypes = [P, u32, u32, C.POINTER(_abi.NpaGridCfg), P, C.c_uint64, P]
+    L.oracle_step_rows.argtypes = [P, P, u32, u32, C.POINTER(_abi.NpaGridCfg),
+                                   C.POINTER(_abi.NpaModelCfg), C.POINTER(_abi.NpaWeightsC), f32,
+                                   P, P, P, C.c_uint64, P, P]
     L.oracle_hash_u32.argtypes = [u32]
     L.oracle_hash_u32.restype = u32
     L.oracle_random01.argtypes = [u32, u32, u32]
@@ -290,6 +294,37 @@ def step(model: NpaConfig, weights, positions, states, batch_size, particle_coun
                              C.byref(grid.to_c()), C.byref(model.to_c()), C.byref(wc), dt, _ptr(m),
                              _ptr(op), _ptr(os_), _ptr(dens), _ptr(dx), _ptr(ds)))
     return StepOutput(op, os_.reshape(total, S), dens, dx, ds.reshape(total, S))
+
+
+def density_rows(positions, batch_size, particle_count, grid: HashGridConfig, sel) -> np.ndarray:
+    """density (forward.rs:145-160) of the particles `sel` only (global indices)."""
+    pos = _f32(positions, (-1, 4))
+    idx = np.ascontiguousarray(sel, dtype=np.uint32)
+    out = np.zeros(max(idx.size, 1), np.float32)
+    _check(lib().oracle_density_rows(_ptr(pos), batch_size, particle_count, C.byref(grid.to_c()),
+                                     _ptr(idx), idx.size, _ptr(out)))
+    return out[:idx.size]
+
+
+def step_rows(model: NpaConfig, weights, positions, states, batch_size, particle_count,
+              grid: HashGridConfig, dt: float, update_mask, density, sel):
+    """NpaModel::step_cpu (model.rs:768-858) of the particles `sel` only, given every particle's
+    density: (next positions [k, 4], next states [k, S]) of those particles."""
+    pos = _f32(positions, (-1, 4))
+    st = _f32(states).reshape(-1)
+    S = model.state_dims
+    m = None if update_mask is None else _f32(update_mask).reshape(-1)
+    dens = _f32(density).reshape(-1)
+    if dens.size != pos.shape[0]:
+        raise _abi.InvalidArgument("density must hold every particle")
+    idx = np.ascontiguousarray(sel, dtype=np.uint32)
+    op = np.zeros((max(idx.size, 1), 4), np.float32)
+    os_ = np.zeros(max(idx.size, 1) * S, np.float32)
+    wc, keep = _weights_c(weights)
+    _check(lib().oracle_step_rows(_ptr(pos), _ptr(st), batch_size, particle_count,
+                                  C.byref(grid.to_c()), C.byref(model.to_c()), C.byref(wc), dt,
+                                  _ptr(m), _ptr(dens), _ptr(idx), idx.size, _ptr(op), _ptr(os_)))
+    return op[:idx.size], os_.reshape(-1, S)[:idx.size]
 
 
 def hash_u32(v: int) -> int:

@@ -797,3 +797,31 @@ def test_splat_is_additive_and_clips_at_the_border():
     one = O.splat_particles_2d(np.array([[0.99, 0.99, 0, 0]], f32), np.ones((1, 3), f32), cfg)
     norm = (48 * cfg.pixel_size / 2.0) ** 2
     assert one[:, 3].sum() == pytest.approx(norm, rel=1e-5)
+
+
+@pytest.mark.parametrize("name,particles", [("c1", 2048), ("c4", 4096), ("c3", 8192),
+                                            ("torus", 1024)])
+def test_sampled_rows_equal_the_full_pass(name, particles):
+    """density_rows / step_rows (the sampled evaluation used at C3's full size) give exactly the
+    rows of the full density pass and the full step, incl. 3D gates and masked-out particles."""
+    if name == "torus":
+        m, g = NpaConfig.torus_field_3dgs(), HashGridConfig.growing_3dgs()
+        pos = syn.uniform_ball(particles, 6, 0.5)
+        pos[::7, 3] = 1.0
+        st = syn.normal_states(particles, m.state_dims, 6, std=1.0)
+        st[:, 3] += 3.5
+        w = {"model": m, "grid": g, "batch": 1, "n": particles, "positions": pos, "states": st,
+             "weights": syn.seeded_weights(m, 6)}
+    else:
+        w = syn.workload(name, particles=particles)
+    b, n = w["batch"], w["n"]
+    mask = O.update_mask(b, n, 0.5, 3, 42)
+    full = O.step(w["model"], w["weights"], w["positions"], w["states"], b, n, w["grid"], 1.0,
+                  mask)
+    sel = np.random.default_rng(1).choice(b * n, 300, replace=False).astype(np.uint32)
+    np.testing.assert_array_equal(O.density_rows(w["positions"], b, n, w["grid"], sel),
+                                  full.density[sel])
+    p, s = O.step_rows(w["model"], w["weights"], w["positions"], w["states"], b, n, w["grid"],
+                       1.0, mask, full.density, sel)
+    np.testing.assert_array_equal(p, full.next_positions[sel])
+    np.testing.assert_array_equal(s, full.next_states[sel])
