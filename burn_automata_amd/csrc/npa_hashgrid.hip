@@ -65,7 +65,6 @@ hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t
     NPA_RES(wl_count, 64);
     NPA_RES(worklist, (plan.worklist_cap + 1) * 8);
     // second-pass items: at most one partial item per (64-slot window, cell run) pair
-    NPA_RES(act_items, (t1 / (plan.tpi ? plan.tpi : 1) + t1 / 64 + plan.worklist_cap + 2) * 16);
     NPA_RES(act_rows, t1 * 4);
     NPA_RES(srec, t1 * 16);
     NPA_RES(scoord, dim == 3 ? t1 * 16 : 16);
@@ -90,7 +89,7 @@ hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t
 void Workspace::release() {
     for (DevBuf* b : {&keys, &ranks, &table, &totals, &bin_offsets, &perm, &inv, &flags, &wl_count,
                       &worklist, &srec, &scoord, &sstate, &svol, &counters, &features, &wpad, &tmpidx,
-                      &dir_n, &dir_e, &act_items, &act_rows, &nb_chunks, &nb_count})
+                      &dir_n, &dir_e, &act_rows, &nb_chunks, &nb_count})
         b->release();
 }
 

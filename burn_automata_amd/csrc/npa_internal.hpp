@@ -97,10 +97,9 @@ struct Workspace {
     DevBuf srec, scoord, sstate, svol, counters, features, wpad;
     DevBuf tmpidx, dir_n, dir_e;
     // Targets of the second pass and the update: particles whose update mask is not 0 (the others
-    // are copied to the output unchanged, as the reference's GPU update_particle does). act_items:
-    // uint4 {window base slot, target bitmask lo, hi, first compact row}; act_rows: compact row ->
-    // slot. Counts (u32 words of wl_count): [0] density items, [2] second-pass items, [3] rows.
-    DevBuf act_items, act_rows;
+    // are written to the output by the update-mask kernel). act_rows: compact row -> slot.
+    // Counts (u32 words of wl_count): [0] density items, [3] compact rows.
+    DevBuf act_rows;
     // Accepted neighbours recorded by the density pass, per target and neighbour chunk (<= 64
     // consecutive slots of a cell run, in visit order): chunk-major uint4 {first slot, length,
     // accept mask lo, hi} at [chunk * T + slot] for the first max_chunks(dim) chunks, and the

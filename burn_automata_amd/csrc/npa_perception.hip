@@ -311,24 +311,6 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
     }
 }
 
-// Position of the t-th (0-based) set bit of m; m has more than t set bits.
-__device__ __forceinline__ uint32_t nth_set_bit(uint64_t m, uint32_t t) {
-    uint32_t pos = 0;
-#pragma unroll
-    for (int w = 32; w >= 1; w >>= 1) {
-        const uint64_t low = m & ((1ull << w) - 1ull);
-        const uint32_t c = (uint32_t)__popcll(low);
-        if (t >= c) {
-            t -= c;
-            m >>= w;
-            pos += (uint32_t)w;
-        } else {
-            m = low;
-        }
-    }
-    return pos;
-}
-
 // Copies a state row (every load issued before the stores); in 3D the opacity-logit channels are
 // clamped on the way.
 template <int NQ>
@@ -377,26 +359,24 @@ __device__ __forceinline__ void hold_particle(uint64_t i, uint32_t S, const Grid
 }
 
 // Targets of the second pass and the update MLP, one wave per bin (16 bins per block). A particle
-// whose update mask is 0 is copied to the step's output unchanged and gets no perception or MLP
-// work - the reference's GPU update_particle (gpu_step.wgsl:3664-3682) does the same; the CPU path
-// adds dt * ds * 0, which leaves the same values. The other particles are packed per 64-slot
-// window of a cell run into items of <= tpi targets {window base, target bitmask, first compact
-// row} and get consecutive compact rows (act_rows[row] = slot) for the feature rows and the MLP.
+// whose update mask is 0 gets no perception or MLP work: it is written to the step's output with
+// the two transforms the CPU euler_step still applies to it (see hold_particle). The others get
+// consecutive compact rows (act_rows[row] = slot) in bin, run and slot order; the second pass
+// serves them in groups of consecutive rows and the MLP reads its feature rows by row.
 // mask_mode: 0 every particle is a target (no copies), 1 the device hash mask, 2 a mask array.
 #if NPA_PART_MAIN
 constexpr uint32_t kActWaves = 16;
 
-__global__ __launch_bounds__(1024) void k_active(StepParams P, int mask_mode, uint32_t nbins, uint32_t tpi,
+__global__ __launch_bounds__(1024) void k_active(StepParams P, int mask_mode, uint32_t nbins,
                                                  const uint32_t* __restrict__ bo,
                                                  const uint32_t* __restrict__ perm,
                                                  const float* __restrict__ user_mask,
                                                  const float4* __restrict__ pos, const float* __restrict__ states,
                                                  float4* __restrict__ out_pos, float* __restrict__ out_states,
-                                                 uint4* __restrict__ items, uint32_t* __restrict__ rows,
-                                                 uint32_t* __restrict__ counts) {
+                                                 uint32_t* __restrict__ rows, uint32_t* __restrict__ counts) {
     constexpr uint32_t K = kDirGroups;
-    __shared__ uint32_t s_it[kActWaves], s_rw[kActWaves];
-    __shared__ uint32_t s_bit, s_brw;
+    __shared__ uint32_t s_rw[kActWaves];
+    __shared__ uint32_t s_brw;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t bin = blockIdx.x * kActWaves + wave;
     const bool has_bin = bin < nbins;
@@ -422,42 +402,26 @@ __global__ __launch_bounds__(1024) void k_active(StepParams P, int mask_mode, ui
                                        : user_mask[(uint64_t)b * P.N + li];
         return m != 0.0f;
     };
-    uint32_t nit = 0, nrw = 0;
+    uint32_t nrw = 0;
     for (uint32_t k = 0; k < nr; ++k) {
         uint32_t rs, re;
         run(k, rs, re);
         for (uint32_t w0 = rs; w0 < re; w0 += 64) {
             const bool valid = w0 + lane < re;
             const uint32_t li = perm[valid ? w0 + lane : rs];
-            const uint32_t na = (uint32_t)__popcll(__ballot(target(valid, li)));
-            nit += (na + tpi - 1) / tpi;
-            nrw += na;
+            nrw += (uint32_t)__popcll(__ballot(target(valid, li)));
         }
     }
-    if (lane == 0) {
-        s_it[wave] = nit;
-        s_rw[wave] = nrw;
-    }
+    if (lane == 0) s_rw[wave] = nrw;
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t ti = 0, tr = 0;
-        for (uint32_t w = 0; w < kActWaves; ++w) {
-            ti += s_it[w];
-            tr += s_rw[w];
-        }
-        unsigned long long both = 0;
-        if (ti | tr)
-            both = atomicAdd(reinterpret_cast<unsigned long long*>(counts + 2),
-                             ((unsigned long long)tr << 32) | (unsigned long long)ti);
-        s_bit = (uint32_t)both;
-        s_brw = (uint32_t)(both >> 32);
+        uint32_t tr = 0;
+        for (uint32_t w = 0; w < kActWaves; ++w) tr += s_rw[w];
+        s_brw = tr ? atomicAdd(counts + 3, tr) : 0u;
     }
     __syncthreads();
-    uint32_t ib = s_bit, rb = s_brw;
-    for (uint32_t w = 0; w < wave; ++w) {
-        ib += s_it[w];
-        rb += s_rw[w];
-    }
+    uint32_t rb = s_brw;
+    for (uint32_t w = 0; w < wave; ++w) rb += s_rw[w];
     for (uint32_t k = 0; k < nr; ++k) {
         uint32_t rs, re;
         run(k, rs, re);
@@ -471,33 +435,22 @@ __global__ __launch_bounds__(1024) void k_active(StepParams P, int mask_mode, ui
             if (act) rows[rb + rank] = slot;
             else if (valid && mask_mode != 0)  // masked out: no update
                 hold_particle((uint64_t)b * P.N + li, P.S, P.g, pos, states, out_pos, out_states);
-            const uint32_t na = (uint32_t)__popcll(am);
-            const uint32_t ni = (na + tpi - 1) / tpi;
-            const uint32_t jr = rank / tpi;
-            for (uint32_t j = 0; j < ni; ++j) {
-                const uint64_t sub = __ballot(act && jr == j);
-                if (lane == 0) items[ib + j] = make_uint4(w0, (uint32_t)sub, (uint32_t)(sub >> 32), rb + j * tpi);
-            }
-            ib += ni;
-            rb += na;
+            rb += (uint32_t)__popcll(am);
         }
     }
 }
 
 #endif  // NPA_PART_MAIN
 
-// Per-wave accepted-neighbour lists of the second pass. Entry = (chunk id << 6) | k, the k-th
-// candidate of the target's chunk whose first sorted slot is cbase[chunk id][target]; entries of a
-// target are appended in visit order (cells dz, dy, dx; slots ascending), so walking a list front
-// to back is the reference's neighbour order. LDS: kListBytes of entries per wave for any
-// targets-per-item, plus the chunk-base table.
-constexpr int kListBytes = 8192;
+// Per-wave accepted-neighbour lists of the second pass: the sorted slots of each target's accepted
+// candidates, appended in visit order (cells dz, dy, dx; slots ascending), so walking a list front
+// to back is the reference's neighbour order. kListBytes of LDS per wave for any targets-per-item.
+constexpr int kListBytes = 12288;
 
-template <int TPI, int MAXC>
+template <int TPI>
 struct PerceiveLists {
-    static constexpr int CAP = kListBytes / (2 * TPI);
-    uint16_t entry[CAP][TPI];
-    uint32_t cbase[MAXC][TPI];
+    static constexpr int CAP = kListBytes / (4 * TPI);
+    uint32_t slot[CAP][TPI];
 };
 
 // Bits k of a 64-bit chunk mask with k % L == q.
@@ -520,7 +473,8 @@ __device__ __forceinline__ uint64_t residue_mask(uint32_t q) {
 //   q-th entry, and every lane applies the round's entries in list order to its own channels,
 //   with the scalars and the candidate slot broadcast inside the lane group and the candidate's
 //   state channels read from the sorted state rows. Rounds span all of a target's neighbour
-//   bins, so the targets of a wave stay busy for about the same number of rounds.
+//   bins, so the targets of a wave stay busy for about the same number of rounds. The next
+//   round's loads are issued before the current round is computed (two register sets).
 // Padding entries (a short last round, a target with fewer entries than the wave's longest
 // list) use the target itself with zero weights; the self pair's gradient terms and those of
 // coincident particles are zero as well. Zero terms leave every sum unchanged: each sum starts
@@ -536,8 +490,8 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                                                  const float* __restrict__ svol,
                                                  const uint32_t* __restrict__ bo,
                                                  const uint32_t* __restrict__ perm,
-                                                 const uint4* __restrict__ wl,
-                                                 const uint32_t* __restrict__ wl_count,
+                                                 const uint32_t* __restrict__ act_rows,
+                                                 const uint32_t* __restrict__ row_count,
                                                  const uint4* __restrict__ nb_chunks,
                                                  const uint32_t* __restrict__ nb_count,
                                                  float* __restrict__ sfeatures, StepIO io) {
@@ -545,25 +499,24 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
     constexpr int CPL = LanesPerTarget<SM>::CPL;
     constexpr int TPI = 64 / L;
     constexpr uint32_t MAXC = max_chunks(D);
-    using Lists = PerceiveLists<TPI, (int)MAXC>;
+    using Lists = PerceiveLists<TPI>;
     constexpr uint32_t CAP = Lists::CAP;
     __shared__ Lists lists;
     const uint32_t lane = threadIdx.x;
     const uint32_t t = lane / L, q = lane % L;
     const uint32_t c0 = q * CPL;  // first channel of this lane
-    const uint32_t items = *wl_count;
+    const uint32_t nrows = *row_count;
+    const uint32_t items = (nrows + TPI - 1) / TPI;  // TPI consecutive compact rows per wave
     const bool want_sg = FL >= 0 ? (FL & 1) != 0 : P.state_grad != 0;
     const bool want_dg = FL >= 0 ? (FL & 2) != 0 : P.density_grad != 0;
     const bool want_m = FL >= 0 ? (FL & 5) == 5 : (want_sg && P.hybrid);
     const bool branch_a = want_sg && want_dg;
     const uint64_t my_residue = residue_mask<L>(q);
     for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
-        const uint4 item = wl[it];
-        const uint64_t tmask = ((uint64_t)item.z << 32) | item.y;
-        const bool active = t < (uint32_t)__popcll(tmask);
-        const uint32_t s = item.x + (active ? nth_set_bit(tmask, t) : 0u);
-        const uint32_t row = item.w + t;  // compact feature row
-        const uint32_t b = item.x / P.N;
+        const uint32_t row = it * TPI + t;  // compact feature row
+        const bool active = row < nrows;
+        const uint32_t s = act_rows[active ? row : it * TPI];
+        const uint32_t b = s / P.N;
         float pi[3];
         int ci[3];
         load_rec<D>(srec, scoord, s, pi, ci);
@@ -581,140 +534,162 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
         for (int k = 0; k < D * D; ++k) mom[k] = 0.0f;
 
         uint32_t cnt = 0;      // entries in this target's list (same in the L lanes of a target)
-        uint32_t nchunks = 0;  // chunk ids in use (wave-uniform)
 
-        // Phase B over the current lists.
-        auto flush = [&]() {
-            __syncthreads();  // list writes of every lane are visible
-            for (uint32_t r = 0;; ++r) {
-                const uint32_t e0 = r * L;
-                if (!__ballot(active && e0 < cnt)) break;
-                const uint32_t e = e0 + q;
-                const bool has = active && e < cnt;
-                // entry read at a clamped index; the slot of a lane without an entry is its target
-                const uint32_t en = lists.entry[has ? e : 0u][t];
-                const uint32_t chunk = (en >> 6) < MAXC ? (en >> 6) : MAXC - 1;  // in bounds for any entry
-                const uint32_t cand = lists.cbase[chunk][t] + (en & 63u);
-                const uint32_t slot = has ? cand : s;
-                const float4 rj = srec[slot];
-                const float vj = svol[slot];
-                // the round's slots and their state channels (loads issued before the scalars)
-                uint32_t rs[L];
-                float sv[L][CPL];
-                auto bslot = [&](auto J) {
-                    return (uint32_t)__float_as_int(group_bcast<L, decltype(J)::value>(__int_as_float((int)slot)));
-                };
-                rs[0] = bslot(std::integral_constant<int, 0>{});
-                if constexpr (L >= 2) rs[1] = bslot(std::integral_constant<int, 1>{});
-                if constexpr (L >= 4) {
-                    rs[2] = bslot(std::integral_constant<int, 2>{});
-                    rs[3] = bslot(std::integral_constant<int, 3>{});
-                }
+        // Phase B over the current lists. Round r: lane q takes entry r * L + q of its target's list.
+        // The loads of round r + 1 (the entry's record, volume and the round's state rows) are
+        // issued before round r is computed, so their latency overlaps the arithmetic.
+        struct Fetch {
+            uint32_t slot;
+            bool has;
+            float4 rj;
+            float vj;
+            float sv[L][CPL];
+        };
+        auto fetch = [&](uint32_t r, Fetch& F) {
+            const uint32_t e = r * L + q;
+            F.has = active && e < cnt;
+            const uint32_t en = lists.slot[e < CAP ? e : CAP - 1][t];  // in bounds for any e
+            F.slot = F.has ? en : s;  // a lane without an entry uses its target
+            F.rj = srec[F.slot];
+            F.vj = svol[F.slot];
+            uint32_t rs[L];
+            auto bslot = [&](auto J) {
+                return (uint32_t)__float_as_int(group_bcast<L, decltype(J)::value>(__int_as_float((int)F.slot)));
+            };
+            rs[0] = bslot(std::integral_constant<int, 0>{});
+            if constexpr (L >= 2) rs[1] = bslot(std::integral_constant<int, 1>{});
+            if constexpr (L >= 4) {
+                rs[2] = bslot(std::integral_constant<int, 2>{});
+                rs[3] = bslot(std::integral_constant<int, 3>{});
+            }
 #pragma unroll
-                for (int j = 0; j < L; ++j) {
-                    const float* rowp = sstate + (uint64_t)rs[j] * SM + c0;
-                    if constexpr (CPL % 4 == 0) {  // 16-byte aligned channel slices
-                        const float4* row = reinterpret_cast<const float4*>(rowp);
+            for (int j = 0; j < L; ++j) {
+                const float* rowp = sstate + (uint64_t)rs[j] * SM + c0;
+                if constexpr (CPL % 4 == 0) {  // 16-byte aligned channel slices
+                    const float4* row = reinterpret_cast<const float4*>(rowp);
 #pragma unroll
-                        for (int v = 0; v < CPL / 4; ++v) {
-                            const float4 x = row[v];
-                            sv[j][4 * v + 0] = x.x;
-                            sv[j][4 * v + 1] = x.y;
-                            sv[j][4 * v + 2] = x.z;
-                            sv[j][4 * v + 3] = x.w;
-                        }
-                    } else {  // CPL = 6 (SM = 24): 8-byte aligned slices
-                        static_assert(CPL % 2 == 0, "channel slices are whole float2s");
-                        const float2* row = reinterpret_cast<const float2*>(rowp);
+                    for (int v = 0; v < CPL / 4; ++v) {
+                        const float4 x = row[v];
+                        F.sv[j][4 * v + 0] = x.x;
+                        F.sv[j][4 * v + 1] = x.y;
+                        F.sv[j][4 * v + 2] = x.z;
+                        F.sv[j][4 * v + 3] = x.w;
+                    }
+                } else {  // CPL = 6 (SM = 24): 8-byte aligned slices
+                    static_assert(CPL % 2 == 0, "channel slices are whole float2s");
+                    const float2* row = reinterpret_cast<const float2*>(rowp);
 #pragma unroll
-                        for (int v = 0; v < CPL / 2; ++v) {
-                            const float2 x = row[v];
-                            sv[j][2 * v + 0] = x.x;
-                            sv[j][2 * v + 1] = x.y;
-                        }
+                    for (int v = 0; v < CPL / 2; ++v) {
+                        const float2 x = row[v];
+                        F.sv[j][2 * v + 0] = x.x;
+                        F.sv[j][2 * v + 1] = x.y;
                     }
                 }
-                // pair scalars of this lane's entry, branch-free; a lane without an entry (or the
-                // self pair / a coincident particle for the gradients) selects zeros
-                float d[3];
-                d[0] = delta_axis(pi[0], rj.x, 0, P.g);
-                d[1] = delta_axis(pi[1], rj.y, 1, P.g);
-                d[2] = 0.0f;
-                float r2 = d[0] * d[0];
-                r2 += d[1] * d[1];
-                if constexpr (D == 3) {
-                    d[2] = delta_axis(pi[2], rj.z, 2, P.g);
-                    r2 += d[2] * d[2];
-                }
-                const float smooth = has ? poly6(r2, P.g) : 0.0f;
-                const float vol = has ? vj : 0.0f;
-                const bool gok = has && slot != s && r2 > 0.0f;  // spiky_gradient_kernel kernels.rs:79-96
-                const float rr = sqrtf(r2);
-                const float tt = P.g.eps - rr;
-                float vg[D], dgv[D];
+            }
+        };
+        auto compute = [&](const Fetch& F) {
+            // pair scalars of this lane's entry, branch-free; a lane without an entry (or the
+            // self pair / a coincident particle for the gradients) selects zeros
+            const bool has = F.has;
+            const float4 rj = F.rj;
+            const float vj = F.vj;
+            float d[3];
+            d[0] = delta_axis(pi[0], rj.x, 0, P.g);
+            d[1] = delta_axis(pi[1], rj.y, 1, P.g);
+            d[2] = 0.0f;
+            float r2 = d[0] * d[0];
+            r2 += d[1] * d[1];
+            if constexpr (D == 3) {
+                d[2] = delta_axis(pi[2], rj.z, 2, P.g);
+                r2 += d[2] * d[2];
+            }
+            const float smooth = has ? poly6(r2, P.g) : 0.0f;
+            const float vol = has ? vj : 0.0f;
+            const bool gok = has && F.slot != s && r2 > 0.0f;  // spiky_gradient_kernel kernels.rs:79-96
+            const float rr = sqrtf(r2);
+            const float tt = P.g.eps - rr;
+            float vg[D], dgv[D];
 #pragma unroll
-                for (int a = 0; a < D; ++a) {
-                    vg[a] = 0.0f;
-                    dgv[a] = 0.0f;
+            for (int a = 0; a < D; ++a) {
+                vg[a] = 0.0f;
+                dgv[a] = 0.0f;
+            }
+            if (want_dg) {
+                const float mag = 1.0f * P.g.k5 * 3.0f * (tt * tt) / rr;
+#pragma unroll
+                for (int a = 0; a < D; ++a) dgv[a] = gok ? mag * d[a] : 0.0f;
+            }
+            if (want_sg) {
+                const float mag = vj * P.g.k5 * 3.0f * (tt * tt) / rr;
+#pragma unroll
+                for (int a = 0; a < D; ++a) vg[a] = gok ? mag * d[a] : 0.0f;
+            }
+            const float w = smooth * vol;  // blur_state weight (density-grad-off branch)
+            // the round's entries in list order
+            auto round_step = [&](auto J) {
+                constexpr int j = decltype(J)::value;
+                if (branch_a) {  // second_pass_particle forward.rs:263-270
+                    const float c_smooth = group_bcast<L, j>(smooth), c_vol = group_bcast<L, j>(vol);
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) blur[c] += F.sv[j][c] * c_smooth * c_vol;
+                } else {  // blur_state forward.rs:174-180
+                    const float c_w = group_bcast<L, j>(w);
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) blur[c] += F.sv[j][c] * c_w;
                 }
                 if (want_dg) {
-                    const float mag = 1.0f * P.g.k5 * 3.0f * (tt * tt) / rr;
 #pragma unroll
-                    for (int a = 0; a < D; ++a) dgv[a] = gok ? mag * d[a] : 0.0f;
+                    for (int a = 0; a < D; ++a) dg[a] += group_bcast<L, j>(dgv[a]);
                 }
                 if (want_sg) {
-                    const float mag = vj * P.g.k5 * 3.0f * (tt * tt) / rr;
+                    float c_vg[D];
 #pragma unroll
-                    for (int a = 0; a < D; ++a) vg[a] = gok ? mag * d[a] : 0.0f;
+                    for (int a = 0; a < D; ++a) c_vg[a] = group_bcast<L, j>(vg[a]);
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) {
+                        const float diff = F.sv[j][c] - si[c];
+#pragma unroll
+                        for (int a = 0; a < D; ++a) grad[c * D + a] += diff * c_vg[a];
+                    }
+                    if (want_m) {
+                        // only the upper triangle: safe_inverse_symmetric reads no other entry
+#pragma unroll
+                        for (int ra = 0; ra < D; ++ra) {
+                            const float c_d = group_bcast<L, j>(d[ra]);
+#pragma unroll
+                            for (int ca = ra; ca < D; ++ca) mom[ra * D + ca] += c_d * c_vg[ca];
+                        }
+                    }
                 }
-                const float w = smooth * vol;  // blur_state weight (density-grad-off branch)
-                // the round's entries in list order
-                auto round_step = [&](auto J) {
-                    constexpr int j = decltype(J)::value;
-                    if (branch_a) {  // second_pass_particle forward.rs:263-270
-                        const float c_smooth = group_bcast<L, j>(smooth), c_vol = group_bcast<L, j>(vol);
-#pragma unroll
-                        for (int c = 0; c < CPL; ++c) blur[c] += sv[j][c] * c_smooth * c_vol;
-                    } else {  // blur_state forward.rs:174-180
-                        const float c_w = group_bcast<L, j>(w);
-#pragma unroll
-                        for (int c = 0; c < CPL; ++c) blur[c] += sv[j][c] * c_w;
-                    }
-                    if (want_dg) {
-#pragma unroll
-                        for (int a = 0; a < D; ++a) dg[a] += group_bcast<L, j>(dgv[a]);
-                    }
-                    if (want_sg) {
-                        float c_vg[D];
-#pragma unroll
-                        for (int a = 0; a < D; ++a) c_vg[a] = group_bcast<L, j>(vg[a]);
-#pragma unroll
-                        for (int c = 0; c < CPL; ++c) {
-                            const float diff = sv[j][c] - si[c];
-#pragma unroll
-                            for (int a = 0; a < D; ++a) grad[c * D + a] += diff * c_vg[a];
-                        }
-                        if (want_m) {
-                            // only the upper triangle: safe_inverse_symmetric reads no other entry
-#pragma unroll
-                            for (int ra = 0; ra < D; ++ra) {
-                                const float c_d = group_bcast<L, j>(d[ra]);
-#pragma unroll
-                                for (int ca = ra; ca < D; ++ca) mom[ra * D + ca] += c_d * c_vg[ca];
-                            }
-                        }
-                    }
-                };
-                round_step(std::integral_constant<int, 0>{});
-                if constexpr (L >= 2) round_step(std::integral_constant<int, 1>{});
-                if constexpr (L >= 4) {
-                    round_step(std::integral_constant<int, 2>{});
-                    round_step(std::integral_constant<int, 3>{});
+            };
+            round_step(std::integral_constant<int, 0>{});
+            if constexpr (L >= 2) round_step(std::integral_constant<int, 1>{});
+            if constexpr (L >= 4) {
+                round_step(std::integral_constant<int, 2>{});
+                round_step(std::integral_constant<int, 3>{});
+            }
+        };
+        auto flush = [&]() {
+            __syncthreads();  // list writes of every lane are visible
+            if (__ballot(active && 0u < cnt)) {
+                // The next round is fetched unconditionally (past the end every lane loads its own
+                // target's rows, unused), so no branch merges the load queues and each round waits
+                // only for its own loads.
+                Fetch A, B;
+                fetch(0, A);
+                for (uint32_t r = 0;; r += 2) {
+                    const bool more1 = __ballot(active && (r + 1) * L < cnt) != 0;
+                    fetch(r + 1, B);
+                    compute(A);
+                    if (!more1) break;
+                    const bool more2 = __ballot(active && (r + 2) * L < cnt) != 0;
+                    fetch(r + 2, A);
+                    compute(B);
+                    if (!more2) break;
                 }
             }
             __syncthreads();  // every lane has read the lists before they are refilled
             cnt = 0;
-            nchunks = 0;
         };
 
         // Phase A. The density pass recorded each target's accepted candidates per chunk, in visit
@@ -735,13 +710,12 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                 const uint64_t acc = ((uint64_t)rc[u].w << 32) | rc[u].z;  // 0 past the target's chunks
                 const uint32_t add = (uint32_t)__popcll(acc);
                 if (__ballot(cnt + add > CAP)) flush();
-                if (q == 0 && c < nct) lists.cbase[c][t] = rc[u].x;
                 uint64_t mine = acc & my_residue;
                 while (mine) {
                     const uint32_t k = (uint32_t)__builtin_ctzll(mine);
                     mine &= mine - 1;
                     const uint32_t pos = cnt + (uint32_t)__popcll(acc & ((1ull << k) - 1ull));
-                    lists.entry[pos][t] = (uint16_t)((c << 6) | k);
+                    lists.slot[pos][t] = rc[u].x + k;
                 }
                 cnt += add;
             }
@@ -753,7 +727,8 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
             const int leader = __ffsll((unsigned long long)pending) - 1;
             const int l0 = readlane_i(ci[0], leader), l1 = readlane_i(ci[1], leader);
             const int l2 = D == 3 ? readlane_i(ci[2], leader) : 0;
-            const bool same = active && ci[0] == l0 && ci[1] == l1 && (D == 2 || ci[2] == l2);
+            const uint32_t lb = (uint32_t)readlane_i((int)b, leader);
+            const bool same = active && ci[0] == l0 && ci[1] == l1 && (D == 2 || ci[2] == l2) && b == lb;
             const uint64_t group = __ballot(same) & pending;
             pending &= ~group;
             const bool in_group = (group >> lane) & 1ull;
@@ -764,7 +739,7 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                         const int64_t n0 = (int64_t)l0 + dx, n1 = (int64_t)l1 + dy, n2 = (int64_t)l2 + dz;
                         uint32_t beg, end;
                         bool filter;
-                        if (!cell_range(P, bo, b, n0, n1, n2, beg, end, filter)) continue;
+                        if (!cell_range(P, bo, lb, n0, n1, n2, beg, end, filter)) continue;
                         for (uint32_t base = beg; base < end; base += kChunk) {
                             const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
                             // batches of 4 candidates per lane: loads first (index clamped to
@@ -808,17 +783,15 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                             }
                             acc = group_or<L>(acc);
                             const uint32_t add = (uint32_t)__popcll(acc);
-                            if (__ballot(cnt + add > CAP) || nchunks == MAXC) flush();
-                            if (q == 0) lists.cbase[nchunks][t] = base;
+                            if (__ballot(cnt + add > CAP)) flush();
                             uint64_t mine = acc & my_residue;
                             while (mine) {
                                 const uint32_t k = (uint32_t)__builtin_ctzll(mine);
                                 mine &= mine - 1;
                                 const uint32_t pos = cnt + (uint32_t)__popcll(acc & ((1ull << k) - 1ull));
-                                lists.entry[pos][t] = (uint16_t)((nchunks << 6) | k);
+                                lists.slot[pos][t] = base + k;
                             }
                             cnt += add;
-                            ++nchunks;
                         }
                     }
         }
@@ -1315,8 +1288,8 @@ static void launch_perceive_f(const StepParams& p, Workspace& ws, const StepIO& 
                               hipStream_t stream, Profiler* prof) {
     launch_timed(prof, NPA_KERNEL_PERCEIVE, k_perceive<D, SM, MODE, FL>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
                        ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.svol.as<float>(),
-                       ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), ws.act_items.as<uint4>(),
-                       ws.wl_count.as<uint32_t>() + 2, ws.nb_chunks.as<uint4>(), ws.nb_count.as<uint32_t>(),
+                       ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), ws.act_rows.as<uint32_t>(),
+                       ws.wl_count.as<uint32_t>() + 3, ws.nb_chunks.as<uint4>(), ws.nb_count.as<uint32_t>(),
                        ws.features.as<float>(), io);
 }
 
@@ -1434,10 +1407,9 @@ hipError_t launch_update(const StepParams& p_in, Workspace& ws, const StepIO& io
     const int mask_mode = mode != 0 ? 0 : io.mask ? 2 : (p.update_prob < 1.0f ? 1 : 0);
     const uint32_t nbins = p.B * p.g.cells;
     hipError_t e = launch_timed(prof, NPA_KERNEL_ACTIVE, k_active, dim3((nbins + kActWaves - 1) / kActWaves),
-                                dim3(64 * kActWaves), 0, stream, p, mask_mode, nbins, targets_per_item(p.SS),
+                                dim3(64 * kActWaves), 0, stream, p, mask_mode, nbins,
                                 ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), io.mask, io.pos, io.states,
-                                io.out_pos, io.out_states, ws.act_items.as<uint4>(), ws.act_rows.as<uint32_t>(),
-                                ws.wl_count.as<uint32_t>());
+                                io.out_pos, io.out_states, ws.act_rows.as<uint32_t>(), ws.wl_count.as<uint32_t>());
     if (e != hipSuccess) return e;
     return p.g.dim == 2 ? launch_second_pass_2d(p, ws, io, mode, blocks, stream, prof)
                         : launch_second_pass_3d(p, ws, io, mode, blocks, stream, prof);
