@@ -160,16 +160,19 @@ struct LanesPerTarget {
 };
 
 // Value of lane (group base + j) for groups of L consecutive lanes (L = 1, 2 or 4), via DPP.
+// quad_perm reads a valid lane for every lane, so bound_ctrl (zero for an invalid source lane)
+// never applies; with it set the compiler folds the permutation into the consuming VALU
+// instruction (v_mul_f32_dpp, v_add_f32_dpp) instead of issuing a separate move.
 template <int L, int J>
 __device__ __forceinline__ float group_bcast(float v) {
     if constexpr (L == 1) {
         return v;
     } else if constexpr (L == 2) {
         constexpr int c = J == 0 ? (0 | (0 << 2) | (2 << 4) | (2 << 6)) : (1 | (1 << 2) | (3 << 4) | (3 << 6));
-        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), c, 0xf, 0xf, false));
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), c, 0xf, 0xf, true));
     } else {
         constexpr int c = J | (J << 2) | (J << 4) | (J << 6);
-        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), c, 0xf, 0xf, false));
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), c, 0xf, 0xf, true));
     }
 }
 
@@ -179,12 +182,12 @@ __device__ __forceinline__ uint64_t group_or(uint64_t m) {
     if constexpr (L == 1) return m;
     uint32_t lo = (uint32_t)m, hi = (uint32_t)(m >> 32);
     constexpr int swap1 = 1 | (0 << 2) | (3 << 4) | (2 << 6);  // quad_perm [1,0,3,2]
-    lo |= (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, swap1, 0xf, 0xf, false);
-    hi |= (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, swap1, 0xf, 0xf, false);
+    lo |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, swap1, 0xf, 0xf, true);
+    hi |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, swap1, 0xf, 0xf, true);
     if constexpr (L == 4) {
         constexpr int swap2 = 2 | (3 << 2) | (0 << 4) | (1 << 6);  // quad_perm [2,3,0,1]
-        lo |= (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, swap2, 0xf, 0xf, false);
-        hi |= (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, swap2, 0xf, 0xf, false);
+        lo |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, swap2, 0xf, 0xf, true);
+        hi |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, swap2, 0xf, 0xf, true);
     }
     return ((uint64_t)hi << 32) | lo;
 }
@@ -625,6 +628,16 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                 for (int a = 0; a < D; ++a) vg[a] = gok ? mag * d[a] : 0.0f;
             }
             const float w = smooth * vol;  // blur_state weight (density-grad-off branch)
+            // moment terms delta[ra] * grad[ca] of this lane's entry, upper triangle (the only
+            // entries safe_inverse_symmetric reads); the lanes then add the round's terms in order
+            float mp[D * (D + 1) / 2];
+            if (want_m) {
+                int k = 0;
+#pragma unroll
+                for (int ra = 0; ra < D; ++ra)
+#pragma unroll
+                    for (int ca = ra; ca < D; ++ca) mp[k++] = d[ra] * vg[ca];
+            }
             // the round's entries in list order
             auto round_step = [&](auto J) {
                 constexpr int j = decltype(J)::value;
@@ -652,13 +665,11 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                         for (int a = 0; a < D; ++a) grad[c * D + a] += diff * c_vg[a];
                     }
                     if (want_m) {
-                        // only the upper triangle: safe_inverse_symmetric reads no other entry
+                        int k = 0;
 #pragma unroll
-                        for (int ra = 0; ra < D; ++ra) {
-                            const float c_d = group_bcast<L, j>(d[ra]);
+                        for (int ra = 0; ra < D; ++ra)
 #pragma unroll
-                            for (int ca = ra; ca < D; ++ca) mom[ra * D + ca] += c_d * c_vg[ca];
-                        }
+                            for (int ca = ra; ca < D; ++ca) mom[ra * D + ca] += group_bcast<L, j>(mp[k++]);
                     }
                 }
             };
