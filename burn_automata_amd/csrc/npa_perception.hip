@@ -140,16 +140,40 @@ __device__ __forceinline__ bool cell_range(const StepParams& P, const uint32_t* 
         filter = true;
         return true;
     }
+    // every directory entry of the bin is loaded at once (no load waits on another)
     const int4* e = P.dir_e + bin * kDirGroups;
-    for (uint32_t k = 0; k < nd; ++k) {
-        const int4 ek = e[k];
-        if ((int64_t)ek.x == n0 && (int64_t)ek.y == n1 && (int64_t)ek.z == n2) {
-            beg = (uint32_t)ek.w;
-            end = k + 1 < nd ? (uint32_t)e[k + 1].w : bo[bin + 1];
-            return true;
+    int4 ek[kDirGroups];
+#pragma unroll
+    for (uint32_t k = 0; k < kDirGroups; ++k) ek[k] = k < nd ? e[k] : make_int4(0, 0, 0, 0);
+    const uint32_t last = bo[bin + 1];
+    bool found = false;
+#pragma unroll
+    for (uint32_t k = 0; k < kDirGroups; ++k) {
+        const bool hit = !found && k < nd && (int64_t)ek[k].x == n0 && (int64_t)ek[k].y == n1 &&
+                         (int64_t)ek[k].z == n2;
+        if (hit) {
+            beg = (uint32_t)ek[k].w;
+            end = k + 1 < nd ? (uint32_t)ek[k + 1 < kDirGroups ? k + 1 : k].w : last;
+            found = true;
         }
     }
-    return false;
+    return found;
+}
+
+// The candidate runs of the 3^D neighbour cells of cell (c0, c1, c2) of system b, looked up in
+// parallel: lane k < 3^D takes neighbour k in the reference's visit order (k = (dz+1)*9 +
+// (dy+1)*3 + (dx+1): dz, then dy, then dx). found: the cell holds particles.
+template <int D>
+__device__ __forceinline__ void neighbor_runs(const StepParams& P, const uint32_t* __restrict__ bo, uint32_t b,
+                                              int c0, int c1, int c2, uint32_t lane, uint32_t& beg, uint32_t& end,
+                                              bool& filter, bool& found) {
+    constexpr uint32_t NC = D == 3 ? 27 : 9;
+    beg = end = 0;
+    filter = false;
+    found = false;
+    if (lane >= NC) return;
+    const int dx = (int)(lane % 3) - 1, dy = (int)((lane / 3) % 3) - 1, dz = D == 3 ? (int)(lane / 9) - 1 : 0;
+    found = cell_range(P, bo, b, (int64_t)c0 + dx, (int64_t)c1 + dy, (int64_t)c2 + dz, beg, end, filter);
 }
 
 // Lanes per target for a sorted-state row width SM (each lane owns SM / L state channels).
@@ -247,63 +271,65 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
             pending &= ~group;
             const bool in_group = (group >> lane) & 1ull;
             uint32_t gch = 0;  // chunk index within this group's visit order (wave-uniform)
-            constexpr int ZLO = D == 3 ? -1 : 0, ZHI = D == 3 ? 1 : 0;
-            for (int dz = ZLO; dz <= ZHI; ++dz)
-                for (int dy = -1; dy <= 1; ++dy)
-                    for (int dx = -1; dx <= 1; ++dx) {
-                        const int64_t n0 = (int64_t)l0 + dx, n1 = (int64_t)l1 + dy, n2 = (int64_t)l2 + dz;
-                        uint32_t beg, end;
-                        bool filter;
-                        if (!cell_range(P, bo, b, n0, n1, n2, beg, end, filter)) continue;
-                        for (uint32_t base = beg; base < end; base += kChunk, ++gch) {
-                            const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
-                            uint64_t acc = 0;  // accepted candidates of this lane's residue class
-                            constexpr int BT = kChunk / L < 4 ? kChunk / L : 4;  // loads per batch
-                            for (int i0 = 0; i0 < kChunk / L; i0 += BT) {
-                                if ((uint32_t)(i0 * L) >= m) break;  // wave-uniform
-                                float4 rc[BT];
-                                int4 cc[BT];
+            uint32_t nb_beg, nb_end;
+            bool nb_filter, nb_found;
+            neighbor_runs<D>(P, bo, b, l0, l1, l2, lane, nb_beg, nb_end, nb_filter, nb_found);
+            for (uint64_t cells = __ballot(nb_found); cells; cells &= cells - 1) {
+                const int nk = __ffsll((unsigned long long)cells) - 1;  // ascending = visit order
+                const int64_t n0 = (int64_t)l0 + nk % 3 - 1, n1 = (int64_t)l1 + (nk / 3) % 3 - 1;
+                const int64_t n2 = D == 3 ? (int64_t)l2 + nk / 9 - 1 : 0;
+                const uint32_t beg = (uint32_t)readlane_i((int)nb_beg, nk);
+                const uint32_t end = (uint32_t)readlane_i((int)nb_end, nk);
+                const bool filter = readlane_i((int)nb_filter, nk) != 0;
+                for (uint32_t base = beg; base < end; base += kChunk, ++gch) {
+                    const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
+                    uint64_t acc = 0;  // accepted candidates of this lane's residue class
+                    constexpr int BT = kChunk / L < 4 ? kChunk / L : 4;  // loads per batch
+                    for (int i0 = 0; i0 < kChunk / L; i0 += BT) {
+                        if ((uint32_t)(i0 * L) >= m) break;  // wave-uniform
+                        float4 rc[BT];
+                        int4 cc[BT];
 #pragma unroll
-                                for (int u = 0; u < BT; ++u) {
-                                    const uint32_t k = q + (uint32_t)((i0 + u) * L);
-                                    const uint32_t kc = k < m ? k : m - 1;
-                                    rc[u] = srec[base + kc];
-                                    if constexpr (D == 3) cc[u] = scoord[base + kc];
-                                }
+                        for (int u = 0; u < BT; ++u) {
+                            const uint32_t k = q + (uint32_t)((i0 + u) * L);
+                            const uint32_t kc = k < m ? k : m - 1;
+                            rc[u] = srec[base + kc];
+                            if constexpr (D == 3) cc[u] = scoord[base + kc];
+                        }
 #pragma unroll
-                                for (int u = 0; u < BT; ++u) {
-                                    const uint32_t k = q + (uint32_t)((i0 + u) * L);
-                                    const float4 r = rc[u];
-                                    bool ok = in_group & (k < m);
-                                    if (filter) {
-                                        if constexpr (D == 2) {
-                                            ok = ok & ((int64_t)__float_as_int(r.z) == n0) &
-                                                 ((int64_t)__float_as_int(r.w) == n1);
-                                        } else {
-                                            ok = ok & ((int64_t)cc[u].x == n0) & ((int64_t)cc[u].y == n1) &
-                                                 ((int64_t)cc[u].z == n2);
-                                        }
-                                    }
-                                    const float d0 = delta_axis(pi[0], r.x, 0, P.g);
-                                    const float d1 = delta_axis(pi[1], r.y, 1, P.g);
-                                    float r2 = d0 * d0;
-                                    r2 += d1 * d1;
-                                    if constexpr (D == 3) {
-                                        const float d2 = delta_axis(pi[2], r.z, 2, P.g);
-                                        r2 += d2 * d2;
-                                    }
-                                    const bool acc_ok = ok & (r2 < P.g.eps2);
-                                    const float v = acc_ok ? poly6(r2, P.g) : 0.0f;
-                                    acc |= acc_ok ? (1ull << k) : 0ull;  // k < m <= 64 when acc_ok
-                                    rho = ordered_group_sum<L>(rho, v);
+                        for (int u = 0; u < BT; ++u) {
+                            const uint32_t k = q + (uint32_t)((i0 + u) * L);
+                            const float4 r = rc[u];
+                            bool ok = in_group & (k < m);
+                            if (filter) {
+                                if constexpr (D == 2) {
+                                    ok = ok & ((int64_t)__float_as_int(r.z) == n0) &
+                                         ((int64_t)__float_as_int(r.w) == n1);
+                                } else {
+                                    ok = ok & ((int64_t)cc[u].x == n0) & ((int64_t)cc[u].y == n1) &
+                                         ((int64_t)cc[u].z == n2);
                                 }
                             }
-                            acc = group_or<L>(acc);
-                            if (in_group && q == 0 && gch < MAXC)
-                                nb_chunks[(uint64_t)gch * P.T + s] =
-                                    make_uint4(base, m, (uint32_t)acc, (uint32_t)(acc >> 32));
+                            const float d0 = delta_axis(pi[0], r.x, 0, P.g);
+                            const float d1 = delta_axis(pi[1], r.y, 1, P.g);
+                            float r2 = d0 * d0;
+                            r2 += d1 * d1;
+                            if constexpr (D == 3) {
+                                const float d2 = delta_axis(pi[2], r.z, 2, P.g);
+                                r2 += d2 * d2;
+                            }
+                            const bool acc_ok = ok & (r2 < P.g.eps2);
+                            const float v = acc_ok ? poly6(r2, P.g) : 0.0f;
+                            acc |= acc_ok ? (1ull << k) : 0ull;  // k < m <= 64 when acc_ok
+                            rho = ordered_group_sum<L>(rho, v);
                         }
                     }
+                    acc = group_or<L>(acc);
+                    if (in_group && q == 0 && gch < MAXC)
+                        nb_chunks[(uint64_t)gch * P.T + s] =
+                            make_uint4(base, m, (uint32_t)acc, (uint32_t)(acc >> 32));
+                }
+            }
             if (in_group) nch = gch;
         }
         if (active && q == 0) {
@@ -476,8 +502,8 @@ __device__ __forceinline__ uint64_t residue_mask(uint32_t q) {
 //   q-th entry, and every lane applies the round's entries in list order to its own channels,
 //   with the scalars and the candidate slot broadcast inside the lane group and the candidate's
 //   state channels read from the sorted state rows. Rounds span all of a target's neighbour
-//   bins, so the targets of a wave stay busy for about the same number of rounds. The next
-//   round's loads are issued before the current round is computed (two register sets).
+//   bins, so the targets of a wave stay busy for about the same number of rounds. Each round's
+//   loads are issued two rounds before it is computed (three register sets).
 // Padding entries (a short last round, a target with fewer entries than the wave's longest
 // list) use the target itself with zero weights; the self pair's gradient terms and those of
 // coincident particles are zero as well. Zero terms leave every sum unchanged: each sum starts
@@ -683,20 +709,25 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
         auto flush = [&]() {
             __syncthreads();  // list writes of every lane are visible
             if (__ballot(active && 0u < cnt)) {
-                // The next round is fetched unconditionally (past the end every lane loads its own
-                // target's rows, unused), so no branch merges the load queues and each round waits
-                // only for its own loads.
-                Fetch A, B;
+                // Rounds are fetched two ahead, unconditionally (past the end every lane loads its
+                // own target's rows, unused), so no branch merges the load queues and each round
+                // waits only for its own loads.
+                Fetch A, B, C;
                 fetch(0, A);
-                for (uint32_t r = 0;; r += 2) {
-                    const bool more1 = __ballot(active && (r + 1) * L < cnt) != 0;
-                    fetch(r + 1, B);
+                fetch(1, B);
+                for (uint32_t r = 0;; r += 3) {
+                    const bool m1 = __ballot(active && (r + 1) * L < cnt) != 0;
+                    fetch(r + 2, C);
                     compute(A);
-                    if (!more1) break;
-                    const bool more2 = __ballot(active && (r + 2) * L < cnt) != 0;
-                    fetch(r + 2, A);
+                    if (!m1) break;
+                    const bool m2 = __ballot(active && (r + 2) * L < cnt) != 0;
+                    fetch(r + 3, A);
                     compute(B);
-                    if (!more2) break;
+                    if (!m2) break;
+                    const bool m3 = __ballot(active && (r + 3) * L < cnt) != 0;
+                    fetch(r + 4, B);
+                    compute(C);
+                    if (!m3) break;
                 }
             }
             __syncthreads();  // every lane has read the lists before they are refilled
@@ -743,68 +774,70 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
             const uint64_t group = __ballot(same) & pending;
             pending &= ~group;
             const bool in_group = (group >> lane) & 1ull;
-            constexpr int ZLO = D == 3 ? -1 : 0, ZHI = D == 3 ? 1 : 0;
-            for (int dz = ZLO; dz <= ZHI; ++dz)
-                for (int dy = -1; dy <= 1; ++dy)
-                    for (int dx = -1; dx <= 1; ++dx) {
-                        const int64_t n0 = (int64_t)l0 + dx, n1 = (int64_t)l1 + dy, n2 = (int64_t)l2 + dz;
-                        uint32_t beg, end;
-                        bool filter;
-                        if (!cell_range(P, bo, lb, n0, n1, n2, beg, end, filter)) continue;
-                        for (uint32_t base = beg; base < end; base += kChunk) {
-                            const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
-                            // batches of 4 candidates per lane: loads first (index clamped to
-                            // the chunk, so every load is in bounds), then branch-free tests
-                            uint64_t acc = 0;
-                            for (int i0 = 0; i0 < kChunk / L; i0 += 4) {
-                                if ((uint32_t)(i0 * L) >= m) break;  // wave-uniform
-                                float4 rc[4];
-                                int4 cc[4];
+            uint32_t nb_beg, nb_end;
+            bool nb_filter, nb_found;
+            neighbor_runs<D>(P, bo, lb, l0, l1, l2, lane, nb_beg, nb_end, nb_filter, nb_found);
+            for (uint64_t cells = __ballot(nb_found); cells; cells &= cells - 1) {
+                const int nk = __ffsll((unsigned long long)cells) - 1;  // ascending = visit order
+                const int64_t n0 = (int64_t)l0 + nk % 3 - 1, n1 = (int64_t)l1 + (nk / 3) % 3 - 1;
+                const int64_t n2 = D == 3 ? (int64_t)l2 + nk / 9 - 1 : 0;
+                const uint32_t beg = (uint32_t)readlane_i((int)nb_beg, nk);
+                const uint32_t end = (uint32_t)readlane_i((int)nb_end, nk);
+                const bool filter = readlane_i((int)nb_filter, nk) != 0;
+                for (uint32_t base = beg; base < end; base += kChunk) {
+                    const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
+                    // batches of 4 candidates per lane: loads first (index clamped to
+                    // the chunk, so every load is in bounds), then branch-free tests
+                    uint64_t acc = 0;
+                    for (int i0 = 0; i0 < kChunk / L; i0 += 4) {
+                        if ((uint32_t)(i0 * L) >= m) break;  // wave-uniform
+                        float4 rc[4];
+                        int4 cc[4];
 #pragma unroll
-                                for (int u = 0; u < 4; ++u) {
-                                    const uint32_t k = q + (uint32_t)((i0 + u) * L);
-                                    const uint32_t kc = k < m ? k : m - 1;
-                                    rc[u] = srec[base + kc];
-                                    if constexpr (D == 3) cc[u] = scoord[base + kc];
-                                }
+                        for (int u = 0; u < 4; ++u) {
+                            const uint32_t k = q + (uint32_t)((i0 + u) * L);
+                            const uint32_t kc = k < m ? k : m - 1;
+                            rc[u] = srec[base + kc];
+                            if constexpr (D == 3) cc[u] = scoord[base + kc];
+                        }
 #pragma unroll
-                                for (int u = 0; u < 4; ++u) {
-                                    const uint32_t k = q + (uint32_t)((i0 + u) * L);
-                                    const float4 r = rc[u];
-                                    bool ok = in_group & (k < m);
-                                    if (filter) {
-                                        if constexpr (D == 2) {
-                                            ok = ok & ((int64_t)__float_as_int(r.z) == n0) &
-                                                 ((int64_t)__float_as_int(r.w) == n1);
-                                        } else {
-                                            ok = ok & ((int64_t)cc[u].x == n0) & ((int64_t)cc[u].y == n1) &
-                                                 ((int64_t)cc[u].z == n2);
-                                        }
-                                    }
-                                    const float d0 = delta_axis(pi[0], r.x, 0, P.g);
-                                    const float d1 = delta_axis(pi[1], r.y, 1, P.g);
-                                    float r2 = d0 * d0;
-                                    r2 += d1 * d1;
-                                    if constexpr (D == 3) {
-                                        const float d2 = delta_axis(pi[2], r.z, 2, P.g);
-                                        r2 += d2 * d2;
-                                    }
-                                    acc |= (ok & (r2 < P.g.eps2)) ? (1ull << (k & 63u)) : 0ull;
+                        for (int u = 0; u < 4; ++u) {
+                            const uint32_t k = q + (uint32_t)((i0 + u) * L);
+                            const float4 r = rc[u];
+                            bool ok = in_group & (k < m);
+                            if (filter) {
+                                if constexpr (D == 2) {
+                                    ok = ok & ((int64_t)__float_as_int(r.z) == n0) &
+                                         ((int64_t)__float_as_int(r.w) == n1);
+                                } else {
+                                    ok = ok & ((int64_t)cc[u].x == n0) & ((int64_t)cc[u].y == n1) &
+                                         ((int64_t)cc[u].z == n2);
                                 }
                             }
-                            acc = group_or<L>(acc);
-                            const uint32_t add = (uint32_t)__popcll(acc);
-                            if (__ballot(cnt + add > CAP)) flush();
-                            uint64_t mine = acc & my_residue;
-                            while (mine) {
-                                const uint32_t k = (uint32_t)__builtin_ctzll(mine);
-                                mine &= mine - 1;
-                                const uint32_t pos = cnt + (uint32_t)__popcll(acc & ((1ull << k) - 1ull));
-                                lists.slot[pos][t] = base + k;
+                            const float d0 = delta_axis(pi[0], r.x, 0, P.g);
+                            const float d1 = delta_axis(pi[1], r.y, 1, P.g);
+                            float r2 = d0 * d0;
+                            r2 += d1 * d1;
+                            if constexpr (D == 3) {
+                                const float d2 = delta_axis(pi[2], r.z, 2, P.g);
+                                r2 += d2 * d2;
                             }
-                            cnt += add;
+                            acc |= (ok & (r2 < P.g.eps2)) ? (1ull << (k & 63u)) : 0ull;
                         }
                     }
+                    acc = group_or<L>(acc);
+                    const uint32_t add = (uint32_t)__popcll(acc);
+                    if (__ballot(cnt + add > CAP)) flush();
+                    uint64_t mine = acc & my_residue;
+                    while (mine) {
+                        const uint32_t k = (uint32_t)__builtin_ctzll(mine);
+                        mine &= mine - 1;
+                        const uint32_t pos = cnt + (uint32_t)__popcll(acc & ((1ull << k) - 1ull));
+                        lists.slot[pos][t] = base + k;
+                    }
+                    cnt += add;
+                }
+            }
         }
         flush();
         if (!active) continue;
