@@ -30,7 +30,7 @@ if ROOT not in sys.path:
 PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 KERNEL_IDS = {"hash_rank": 0, "table_scan": 1, "offsets_scan": 2, "scatter": 3, "density": 4,
-              "perceive": 5, "mlp": 7, "split": 8, "active": 9}  # NPA_KERNEL_* in include/npa_abi.h
+              "perceive": 5, "mlp": 7, "split": 8}  # NPA_KERNEL_* in include/npa_abi.h
 
 
 def kernel_work(model, counts, particles: int):

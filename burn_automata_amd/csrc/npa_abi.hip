@@ -572,8 +572,9 @@ npa_status npa_step(npa_context* ctx, const float* positions, const float* state
     if (total) {
         NPA_HIP(ctx, npa::launch_pad_weights(p, sio.w1, sio.b1, sio.w2, sio.b2, ctx->ws.wpad.as<float>(), ctx->stream),
                 "pad weights");
+        const npa::SplitTargets targets = npa::step_targets(p, sio);
         NPA_HIP(ctx, npa::launch_hashgrid(plan, p.g, sio.pos, sio.states, S, B, N, ctx->ws, true, ctx->stream,
-                                          &ctx->prof),
+                                          &ctx->prof, &targets),
                 "hashgrid");
         NPA_HIP(ctx, npa::launch_density(p, ctx->ws, dens, blocks, ctx->stream, &ctx->prof), "density");
         NPA_HIP(ctx, npa::launch_update(p, ctx->ws, sio, 0, blocks, ctx->stream, &ctx->prof), "update");
@@ -810,8 +811,9 @@ npa_status npa_state_step(npa_state* s, uint32_t steps) {
         io.states = s->states[c].as<float>();
         io.out_pos = s->pos[1 - c].as<float4>();
         io.out_states = s->states[1 - c].as<float>();
+        const npa::SplitTargets targets = npa::step_targets(p, io);
         NPA_HIP(ctx, npa::launch_hashgrid(s->plan, p.g, io.pos, io.states, S, s->B, s->N, s->ws, true, ctx->stream,
-                                          &ctx->prof),
+                                          &ctx->prof, &targets),
                 "hashgrid");
         NPA_HIP(ctx, npa::launch_density(p, s->ws, s->density.as<float>(), s->grid_blocks, ctx->stream, &ctx->prof),
                 "density");

@@ -455,7 +455,10 @@ __device__ __forceinline__ void write_sorted(uint32_t dst, uint32_t i, uint32_t 
 // run start of its cell + its rank among the earlier particles of that cell, which keeps
 // ascending particle index inside every run (the reference's neighbour order). A bin with more
 // than kDirGroups cells keeps the reference order (dir_n = kDirGroups + 1). Also emits the wave
-// work items: <= tpi consecutive slots of one run (or of an unsplit bin).
+// work items of the density pass (<= tpi consecutive slots of one run, or of an unsplit bin) and
+// the second pass's targets: the particles of the step's update mask get consecutive compact rows
+// (act_rows[row] = slot, in slot order within the bin); the others are written to the step's
+// output here (hold_particle), as the CPU euler_step leaves them.
 constexpr uint32_t kSplitWaves = 16;  // bins (waves) per k_split block
 
 template <int D>
@@ -467,10 +470,11 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
                                                float4* __restrict__ srec, int4* __restrict__ scoord,
                                                float* __restrict__ sstate, uint32_t* __restrict__ dir_n,
                                                int4* __restrict__ dir_e, uint2* __restrict__ worklist,
-                                               uint32_t* __restrict__ wl_count, uint32_t tpi) {
+                                               uint32_t* __restrict__ wl_count, uint32_t tpi, SplitTargets T,
+                                               uint32_t* __restrict__ act_rows) {
     constexpr uint32_t K = kDirGroups;
-    __shared__ uint32_t s_items[kSplitWaves];
-    __shared__ uint32_t s_base;
+    __shared__ uint32_t s_items[kSplitWaves], s_rows[kSplitWaves];
+    __shared__ uint32_t s_base, s_rbase;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t bin = blockIdx.x * kSplitWaves + wave;
     const bool has_bin = bin < nbins;
@@ -484,8 +488,19 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
         gx[k] = gy[k] = gz[k] = 0;
         gc[k] = 0;
     }
+    uint32_t gt[K];  // targets per run
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) gt[k] = 0;
     uint32_t ng = 0;
     bool over = false;
+    // update-mask target (the second pass and the MLP serve it)
+    auto is_target = [&](bool valid, uint32_t i) -> bool {
+        if (!valid) return false;
+        if (T.mask_mode == 0) return true;
+        const uint32_t li = i - b * n;
+        const float m = T.mask_mode == 1 ? hash_mask(li, b, n, T.update_prob, T.step_index, T.base_seed) : T.mask[i];
+        return m != 0.0f;
+    };
     // the particle of slot c0 + lane, its record and cell coordinates
     auto load = [&](uint32_t c0, bool& valid, uint32_t& i, float4& p4, int c[3]) {
         const uint32_t slot = c0 + lane;
@@ -541,13 +556,22 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
             ++ng;
             unknown = __ballot(valid && gid < 0);
         }
+        const bool tgt = is_target(valid, i);
 #pragma unroll
-        for (uint32_t k = 0; k < K; ++k) gc[k] += (uint32_t)__popcll(__ballot(valid && gid == (int)k));
+        for (uint32_t k = 0; k < K; ++k) {
+            gc[k] += (uint32_t)__popcll(__ballot(valid && gid == (int)k));
+            gt[k] += (uint32_t)__popcll(__ballot(tgt && gid == (int)k));
+        }
     }
-    uint32_t nitems = 0;
+    uint32_t nitems = 0, nrows = 0;
     uint32_t start[K];
-    if (over) {
+    if (over) {  // one run in the reference order: count its targets
         nitems = (end - beg + tpi - 1) / tpi;
+        for (uint32_t c0 = beg; c0 < end; c0 += 64) {
+            const uint32_t slot = c0 + lane;
+            const bool valid = slot < end;
+            nrows += (uint32_t)__popcll(__ballot(is_target(valid, order[valid ? slot : c0])));
+        }
     } else {
         uint32_t run = beg;
 #pragma unroll
@@ -555,32 +579,54 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
             start[k] = run;
             run += gc[k];
             nitems += (gc[k] + tpi - 1) / tpi;
+            nrows += gt[k];
         }
     }
-    // one work-list reservation per block: the waves' item counts are summed in LDS
-    if (lane == 0) s_items[wave] = nitems;
+    // one work-list and one row reservation per block: the waves' counts are summed in LDS
+    if (lane == 0) {
+        s_items[wave] = nitems;
+        s_rows[wave] = nrows;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t tot = 0;
-        for (uint32_t w = 0; w < kSplitWaves; ++w) tot += s_items[w];
+        uint32_t tot = 0, rows = 0;
+        for (uint32_t w = 0; w < kSplitWaves; ++w) {
+            tot += s_items[w];
+            rows += s_rows[w];
+        }
         s_base = tot ? atomicAdd(wl_count, tot) : 0u;
+        s_rbase = rows ? atomicAdd(wl_count + 3, rows) : 0u;
     }
     __syncthreads();
     uint32_t wbase = s_base;  // first work item of this bin
-    for (uint32_t w = 0; w < wave; ++w) wbase += s_items[w];
+    uint32_t rbase = s_rbase;  // first compact row of this bin
+    for (uint32_t w = 0; w < wave; ++w) {
+        wbase += s_items[w];
+        rbase += s_rows[w];
+    }
     if (!has_bin) return;
+    auto place = [&](bool valid, bool tgt, uint32_t i, uint32_t dst, uint32_t row) {
+        if (!valid) return;
+        if (tgt) act_rows[row] = dst;
+        else if (T.mask_mode != 0) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
+    };
     if (beg == end) {
         if (lane == 0) dir_n[bin] = 0;
         return;
     }
     if (over) {
+        uint32_t seen_t = 0;
         for (uint32_t c0 = beg; c0 < end; c0 += 64) {
             bool valid = valid0;
             uint32_t i = i0;
             float4 p4 = p0;
             int c[3] = {cf[0], cf[1], cf[2]};
             if (c0 != beg) load(c0, valid, i, p4, c);
+            const bool tgt = is_target(valid, i);
+            const uint64_t mt = __ballot(tgt);
             if (valid) write_sorted<D>(c0 + lane, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
+            place(valid, tgt, i, c0 + lane, rbase + seen_t + (uint32_t)__popcll(mt & lt));
+            seen_t += (uint32_t)__popcll(mt);
         }
         const uint32_t cnt = end - beg;
         for (uint32_t m = lane; m < nitems; m += 64) {
@@ -590,9 +636,17 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
         if (lane == 0) dir_n[bin] = K + 1;
         return;
     }
-    uint32_t seen[K];
+    uint32_t seen[K], seen_t[K], rstart[K];
+    {
+        uint32_t r = rbase;
 #pragma unroll
-    for (uint32_t k = 0; k < K; ++k) seen[k] = 0;
+        for (uint32_t k = 0; k < K; ++k) {
+            seen[k] = 0;
+            seen_t[k] = 0;
+            rstart[k] = r;  // targets take rows in run order, slot order within a run
+            r += gt[k];
+        }
+    }
     for (uint32_t c0 = beg; c0 < end; c0 += 64) {
         bool valid = valid0;
         uint32_t i = i0;
@@ -600,14 +654,21 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
         int c[3] = {cf[0], cf[1], cf[2]};
         if (c0 != beg) load(c0, valid, i, p4, c);
         const int gid = group_of(c);
-        uint32_t dst = 0;
+        const bool tgt = is_target(valid, i);
+        uint32_t dst = 0, row = 0;
 #pragma unroll
         for (uint32_t k = 0; k < K; ++k) {
             const uint64_t m = __ballot(valid && gid == (int)k);
-            if (gid == (int)k) dst = start[k] + seen[k] + (uint32_t)__popcll(m & lt);
+            const uint64_t mt = __ballot(tgt && gid == (int)k);
+            if (gid == (int)k) {
+                dst = start[k] + seen[k] + (uint32_t)__popcll(m & lt);
+                row = rstart[k] + seen_t[k] + (uint32_t)__popcll(mt & lt);
+            }
             seen[k] += (uint32_t)__popcll(m);
+            seen_t[k] += (uint32_t)__popcll(mt);
         }
         if (valid) write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
+        place(valid, tgt, i, dst, row);
     }
     uint32_t off = 0;
 #pragma unroll
@@ -665,7 +726,8 @@ static hipError_t launch_rank(uint32_t rounds, uint32_t blocks, uint32_t waves, 
 
 hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const float4* pos,
                            const float* states, uint32_t state_dims, uint32_t batch, uint32_t n,
-                           Workspace& ws, bool payload, hipStream_t stream, Profiler* prof) {
+                           Workspace& ws, bool payload, hipStream_t stream, Profiler* prof,
+                           const SplitTargets* targets) {
     const uint64_t total = (uint64_t)batch * n;
     hipError_t e = launch_rank(plan.rounds, batch * plan.tiles_per_sys, plan.waves, plan.lds_bytes,
                                plan.tiles_per_sys, plan.key_bits, g, pos, nullptr, nullptr, n, ws.keys.as<uint32_t>(),
@@ -693,7 +755,8 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                         state_dims, n, nbins, g, ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(),
                         ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(), ws.scoord.as<int4>(),
                         ws.sstate.as<float>(), ws.dir_n.as<uint32_t>(), ws.dir_e.as<int4>(),
-                        ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), plan.tpi);
+                        ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), plan.tpi,
+                        targets ? *targets : SplitTargets{}, ws.act_rows.as<uint32_t>());
 }
 
 // ------------------------------------------------------ generic key sort

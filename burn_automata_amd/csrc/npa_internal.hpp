@@ -120,12 +120,28 @@ bool make_plan(const npa_grid_cfg& cfg, uint32_t batch, uint32_t particle_count,
 GridParams make_grid_params(const npa_grid_cfg& cfg);
 float host_powi(float x, int n);
 
-// Builds the stable hashgrid; when `payload` is set also the sorted particle
-// records (positions + cell coords), sorted state rows, and the wave work list.
+// The particles a step's second pass and update MLP process: those whose update mask is not 0.
+// The split kernel gives them consecutive compact rows (act_rows, count in wl_count[3]) and writes
+// every other particle to the step's output with the Euler step's wrap / clamp only
+// (hold_particle). mask_mode: 0 every particle (no copies), 1 the device hash mask, 2 a mask array.
+struct SplitTargets {
+    int mask_mode = 0;
+    const float* mask = nullptr;
+    float update_prob = 1.0f;
+    uint32_t step_index = 0, base_seed = 0;
+    const float4* pos = nullptr;
+    const float* states = nullptr;
+    float4* out_pos = nullptr;
+    float* out_states = nullptr;
+};
+
+// Builds the stable hashgrid; when `payload` is set also the sorted particle records (positions
+// + cell coords), sorted state rows, the density work list and the second pass's targets
+// (`targets`, or every particle when null).
 hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const float4* pos,
                            const float* states, uint32_t state_dims, uint32_t batch,
                            uint32_t particle_count, Workspace& ws, bool payload,
-                           hipStream_t stream, Profiler* prof);
+                           hipStream_t stream, Profiler* prof, const SplitTargets* targets = nullptr);
 // the sorted state rows are written with stride state_stride_for(state_dims), zero padded
 
 // Stable counting sort of a device-resident number (<= cap) of items by key in [0, C):
@@ -145,6 +161,53 @@ __host__ __device__ inline uint32_t state_stride_for(uint32_t S) {
 // targets per wave work item, 64 / L.
 __host__ __device__ inline uint32_t lanes_per_target(uint32_t SS) { return SS >= 16 ? 4u : SS / 4; }
 __host__ __device__ inline uint32_t targets_per_item(uint32_t SS) { return 64u / lanes_per_target(SS); }
+// Copies a state row (every load issued before the stores); in 3D the opacity-logit channels are
+// clamped on the way.
+template <int NQ>
+__device__ __forceinline__ void hold_state_row(float* __restrict__ dst, const float* __restrict__ src, int dim) {
+    float4 v[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) v[q] = reinterpret_cast<const float4*>(src)[q];
+    if (dim == 3) {
+        v[0].w = clampf_(v[0].w, -8.0f, 24.0f);                               // channel 3
+        if constexpr (NQ > 2) v[2].x = clampf_(v[2].x, -8.0f, 24.0f);          // channel 8 (S > 8)
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) reinterpret_cast<float4*>(dst)[q] = v[q];
+}
+
+// A particle whose update mask is 0. The CPU euler_step (step.rs:4-55) adds dt * d * 0 to each
+// value, which is +-0 for a finite update and leaves every value but -0.0 unchanged, and then still
+// applies the periodic wrap and the 3D opacity-logit clamp; those two are applied here, so the
+// result equals the CPU path's without evaluating the update. (The reference's GPU update_particle,
+// gpu_step.wgsl:3664-3682, copies such a particle without the wrap and the clamp.)
+__device__ __forceinline__ void hold_particle(uint64_t i, uint32_t S, const GridParams& g,
+                                              const float4* __restrict__ pos, const float* __restrict__ states,
+                                              float4* __restrict__ out_pos, float* __restrict__ out_states) {
+    float4 p = pos[i];
+    if (g.boundary == 0) {
+        p.x = wrap_axis(p.x, 0, g);
+        p.y = wrap_axis(p.y, 1, g);
+        if (g.dim == 3) p.z = wrap_axis(p.z, 2, g);
+    }
+    out_pos[i] = p;
+    const float* src = states + i * S;
+    float* dst = out_states + i * S;
+    if (S == state_stride_for(S)) {  // 16-byte aligned rows (checked on the host)
+        switch (S) {
+            case 4: hold_state_row<1>(dst, src, g.dim); return;
+            case 8: hold_state_row<2>(dst, src, g.dim); return;
+            case 16: hold_state_row<4>(dst, src, g.dim); return;
+            case 24: hold_state_row<6>(dst, src, g.dim); return;
+            default: hold_state_row<8>(dst, src, g.dim); return;
+        }
+    }
+    for (uint32_t c = 0; c < S; ++c) {
+        const float v = src[c];
+        dst[c] = clamped_channel(g.dim, S, c) ? clampf_(v, -8.0f, 24.0f) : v;
+    }
+}
+
 // Padded feature row used between the perception and MLP kernels:
 // [state SS][blur SS][grad SS*d][density-grad d?, position d?, zero padded to a multiple of 4].
 __host__ __device__ inline uint32_t padded_features(uint32_t SS, uint32_t d, uint32_t rest) {
@@ -189,8 +252,25 @@ struct StepIO {
     float* density_gradient = nullptr;
 };
 
+// The targets of a fused step: the caller's mask, else the device hash mask when update_prob < 1,
+// else every particle.
+inline SplitTargets step_targets(const StepParams& p, const StepIO& io) {
+    SplitTargets t;
+    t.mask_mode = io.mask ? 2 : (p.update_prob < 1.0f ? 1 : 0);
+    t.mask = io.mask;
+    t.update_prob = p.update_prob;
+    t.step_index = p.step_index;
+    t.base_seed = p.base_seed;
+    t.pos = io.pos;
+    t.states = io.states;
+    t.out_pos = io.out_pos;
+    t.out_states = io.out_states;
+    return t;
+}
+
 // Density pass; then the perception pass writing feature rows (mode 0: sorted order into the
-// workspace, followed by the MLP + Euler kernel; mode 1: the perceive outputs in original order).
+// workspace, followed by the MLP + Euler kernel; mode 1: the perceive outputs in original order),
+// over the targets the hashgrid build selected.
 hipError_t launch_density(const StepParams& p, Workspace& ws, float* density_out, int grid_blocks,
                           hipStream_t stream, Profiler* prof);
 hipError_t launch_update(const StepParams& p, Workspace& ws, const StepIO& io, int mode,

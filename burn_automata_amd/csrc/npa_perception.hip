@@ -340,137 +340,6 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
     }
 }
 
-// Copies a state row (every load issued before the stores); in 3D the opacity-logit channels are
-// clamped on the way.
-template <int NQ>
-__device__ __forceinline__ void hold_state_row(float* __restrict__ dst, const float* __restrict__ src, int dim) {
-    float4 v[NQ];
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) v[q] = reinterpret_cast<const float4*>(src)[q];
-    if (dim == 3) {
-        v[0].w = clampf_(v[0].w, -8.0f, 24.0f);                               // channel 3
-        if constexpr (NQ > 2) v[2].x = clampf_(v[2].x, -8.0f, 24.0f);          // channel 8 (S > 8)
-    }
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) reinterpret_cast<float4*>(dst)[q] = v[q];
-}
-
-// A particle whose update mask is 0. The CPU euler_step (step.rs:4-55) adds dt * d * 0 to each
-// value, which is +-0 for a finite update and leaves every value but -0.0 unchanged, and then still
-// applies the periodic wrap and the 3D opacity-logit clamp; those two are applied here, so the
-// result equals the CPU path's without evaluating the update. (The reference's GPU update_particle,
-// gpu_step.wgsl:3664-3682, copies such a particle without the wrap and the clamp.)
-__device__ __forceinline__ void hold_particle(uint64_t i, uint32_t S, const GridParams& g,
-                                              const float4* __restrict__ pos, const float* __restrict__ states,
-                                              float4* __restrict__ out_pos, float* __restrict__ out_states) {
-    float4 p = pos[i];
-    if (g.boundary == 0) {
-        p.x = wrap_axis(p.x, 0, g);
-        p.y = wrap_axis(p.y, 1, g);
-        if (g.dim == 3) p.z = wrap_axis(p.z, 2, g);
-    }
-    out_pos[i] = p;
-    const float* src = states + i * S;
-    float* dst = out_states + i * S;
-    if (S == state_stride_for(S)) {  // 16-byte aligned rows (checked on the host)
-        switch (S) {
-            case 4: hold_state_row<1>(dst, src, g.dim); return;
-            case 8: hold_state_row<2>(dst, src, g.dim); return;
-            case 16: hold_state_row<4>(dst, src, g.dim); return;
-            case 24: hold_state_row<6>(dst, src, g.dim); return;
-            default: hold_state_row<8>(dst, src, g.dim); return;
-        }
-    }
-    for (uint32_t c = 0; c < S; ++c) {
-        const float v = src[c];
-        dst[c] = clamped_channel(g.dim, S, c) ? clampf_(v, -8.0f, 24.0f) : v;
-    }
-}
-
-// Targets of the second pass and the update MLP, one wave per bin (16 bins per block). A particle
-// whose update mask is 0 gets no perception or MLP work: it is written to the step's output with
-// the two transforms the CPU euler_step still applies to it (see hold_particle). The others get
-// consecutive compact rows (act_rows[row] = slot) in bin, run and slot order; the second pass
-// serves them in groups of consecutive rows and the MLP reads its feature rows by row.
-// mask_mode: 0 every particle is a target (no copies), 1 the device hash mask, 2 a mask array.
-#if NPA_PART_MAIN
-constexpr uint32_t kActWaves = 16;
-
-__global__ __launch_bounds__(1024) void k_active(StepParams P, int mask_mode, uint32_t nbins,
-                                                 const uint32_t* __restrict__ bo,
-                                                 const uint32_t* __restrict__ perm,
-                                                 const float* __restrict__ user_mask,
-                                                 const float4* __restrict__ pos, const float* __restrict__ states,
-                                                 float4* __restrict__ out_pos, float* __restrict__ out_states,
-                                                 uint32_t* __restrict__ rows, uint32_t* __restrict__ counts) {
-    constexpr uint32_t K = kDirGroups;
-    __shared__ uint32_t s_rw[kActWaves];
-    __shared__ uint32_t s_brw;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t bin = blockIdx.x * kActWaves + wave;
-    const bool has_bin = bin < nbins;
-    const uint32_t beg = has_bin ? bo[bin] : 0u, end = has_bin ? bo[bin + 1] : 0u;
-    const uint32_t b = has_bin ? bin / P.g.cells : 0u;
-    const uint32_t nd = beg < end ? (P.g.mode == 1 ? P.dir_n[bin] : 1u) : 0u;
-    const uint32_t nr = nd == 0 ? 0u : (nd > K ? 1u : nd);  // runs (an unsplit bin is one run)
-    const uint64_t lt = lanemask_lt();
-    auto run = [&](uint32_t k, uint32_t& rs, uint32_t& re) {
-        if (P.g.mode != 1 || nd > K) {
-            rs = beg;
-            re = end;
-        } else {
-            const int4* e = P.dir_e + (uint64_t)bin * K;
-            rs = (uint32_t)e[k].w;
-            re = k + 1 < nd ? (uint32_t)e[k + 1].w : end;
-        }
-    };
-    auto target = [&](bool valid, uint32_t li) -> bool {
-        if (!valid) return false;
-        if (mask_mode == 0) return true;
-        const float m = mask_mode == 1 ? hash_mask(li, b, P.N, P.update_prob, P.step_index, P.base_seed)
-                                       : user_mask[(uint64_t)b * P.N + li];
-        return m != 0.0f;
-    };
-    uint32_t nrw = 0;
-    for (uint32_t k = 0; k < nr; ++k) {
-        uint32_t rs, re;
-        run(k, rs, re);
-        for (uint32_t w0 = rs; w0 < re; w0 += 64) {
-            const bool valid = w0 + lane < re;
-            const uint32_t li = perm[valid ? w0 + lane : rs];
-            nrw += (uint32_t)__popcll(__ballot(target(valid, li)));
-        }
-    }
-    if (lane == 0) s_rw[wave] = nrw;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t tr = 0;
-        for (uint32_t w = 0; w < kActWaves; ++w) tr += s_rw[w];
-        s_brw = tr ? atomicAdd(counts + 3, tr) : 0u;
-    }
-    __syncthreads();
-    uint32_t rb = s_brw;
-    for (uint32_t w = 0; w < wave; ++w) rb += s_rw[w];
-    for (uint32_t k = 0; k < nr; ++k) {
-        uint32_t rs, re;
-        run(k, rs, re);
-        for (uint32_t w0 = rs; w0 < re; w0 += 64) {
-            const uint32_t slot = w0 + lane;
-            const bool valid = slot < re;
-            const uint32_t li = perm[valid ? slot : rs];
-            const bool act = target(valid, li);
-            const uint64_t am = __ballot(act);
-            const uint32_t rank = (uint32_t)__popcll(am & lt);
-            if (act) rows[rb + rank] = slot;
-            else if (valid && mask_mode != 0)  // masked out: no update
-                hold_particle((uint64_t)b * P.N + li, P.S, P.g, pos, states, out_pos, out_states);
-            rb += (uint32_t)__popcll(am);
-        }
-    }
-}
-
-#endif  // NPA_PART_MAIN
-
 // Per-wave accepted-neighbour lists of the second pass: the sorted slots of each target's accepted
 // candidates, appended in visit order (cells dz, dy, dx; slots ascending), so walking a list front
 // to back is the reference's neighbour order. kListBytes of LDS per wave for any targets-per-item.
@@ -1448,13 +1317,6 @@ hipError_t launch_update(const StepParams& p_in, Workspace& ws, const StepIO& io
                          hipStream_t stream, Profiler* prof) {
     const StepParams p = with_directory(p_in, ws);
     const int blocks = grid_blocks * 4;  // one wave per block
-    const int mask_mode = mode != 0 ? 0 : io.mask ? 2 : (p.update_prob < 1.0f ? 1 : 0);
-    const uint32_t nbins = p.B * p.g.cells;
-    hipError_t e = launch_timed(prof, NPA_KERNEL_ACTIVE, k_active, dim3((nbins + kActWaves - 1) / kActWaves),
-                                dim3(64 * kActWaves), 0, stream, p, mask_mode, nbins,
-                                ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), io.mask, io.pos, io.states,
-                                io.out_pos, io.out_states, ws.act_rows.as<uint32_t>(), ws.wl_count.as<uint32_t>());
-    if (e != hipSuccess) return e;
     return p.g.dim == 2 ? launch_second_pass_2d(p, ws, io, mode, blocks, stream, prof)
                         : launch_second_pass_3d(p, ws, io, mode, blocks, stream, prof);
 }

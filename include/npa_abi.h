@@ -284,8 +284,8 @@ enum {
     NPA_KERNEL_PERCEIVE = 5,   /* second neighbour pass + normalisation + feature rows */
     NPA_KERNEL_SPLAT = 6,      /* the whole 2D splat pipeline */
     NPA_KERNEL_MLP = 7,        /* update MLP + masked Euler */
-    NPA_KERNEL_SPLIT = 8,      /* per-bin split by true cell + sorted payload + work items */
-    NPA_KERNEL_ACTIVE = 9,     /* update-mask targets (masked-out particles copied unchanged) */
+    NPA_KERNEL_SPLIT = 8,      /* per-bin split by true cell + sorted payload + work items + update-mask targets */
+    NPA_KERNEL_ACTIVE = 9,     /* reserved: the split kernel (8) now selects the update-mask targets */
     NPA_KERNEL_COUNT = 10
 };
 /* kernel_mask selects kernels by bit (1 << NPA_KERNEL_*; 0 = off, -1 = all). The
