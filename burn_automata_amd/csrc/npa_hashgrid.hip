@@ -69,7 +69,7 @@ hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t
     NPA_RES(srec, t1 * 16);
     NPA_RES(scoord, dim == 3 ? t1 * 16 : 16);
     NPA_RES(sstate, t1 * (uint64_t)state_stride_for(state_dims ? state_dims : 1) * 4);
-    NPA_RES(svol, t1 * 4);
+    NPA_RES(svol, t1 * 16);
     NPA_RES(counters, 64);
     NPA_RES(features, t1 * (uint64_t)(feature_dims ? feature_dims : 1) * 4);
     NPA_RES(wpad, 4);

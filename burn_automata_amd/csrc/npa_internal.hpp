@@ -94,7 +94,10 @@ constexpr uint32_t kDirGroups = 8;
 
 struct Workspace {
     DevBuf keys, ranks, table, totals, bin_offsets, perm, inv, flags, wl_count, worklist;
-    DevBuf srec, scoord, sstate, svol, counters, features, wpad;
+    DevBuf srec, scoord, sstate, counters, features, wpad;
+    // svol: per sorted slot float4 {x, y, z, 1/rho (recip_finite)}, written by the density pass:
+    // the second pass gathers a neighbour's position and volume with one load
+    DevBuf svol;
     DevBuf tmpidx, dir_n, dir_e;
     // Targets of the second pass and the update: particles whose update mask is not 0 (the others
     // are written to the output by the update-mask kernel). act_rows: compact row -> slot.

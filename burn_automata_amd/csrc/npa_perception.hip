@@ -245,7 +245,7 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
                                                 const uint32_t* __restrict__ perm,
                                                 const uint2* __restrict__ wl,
                                                 const uint32_t* __restrict__ wl_count,
-                                                float* __restrict__ svol, float* __restrict__ density_out,
+                                                float4* __restrict__ svol, float* __restrict__ density_out,
                                                 uint4* __restrict__ nb_chunks, uint32_t* __restrict__ nb_count) {
     constexpr uint32_t MAXC = max_chunks(D);
     const uint32_t lane = threadIdx.x;
@@ -333,7 +333,7 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
             if (in_group) nch = gch;
         }
         if (active && q == 0) {
-            svol[s] = recip_finite(rho);
+            svol[s] = make_float4(pi[0], pi[1], pi[2], recip_finite(rho));
             nb_count[s] = nch;
             if (density_out) density_out[b * P.N + perm[s]] = rho;
         }
@@ -385,7 +385,7 @@ template <int D, int SM, int MODE, int FL>
 __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __restrict__ srec,
                                                  const int4* __restrict__ scoord,
                                                  const float* __restrict__ sstate,
-                                                 const float* __restrict__ svol,
+                                                 const float4* __restrict__ svol,
                                                  const uint32_t* __restrict__ bo,
                                                  const uint32_t* __restrict__ perm,
                                                  const uint32_t* __restrict__ act_rows,
@@ -443,13 +443,20 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
             float vj;
             float sv[L][CPL];
         };
+        // list entry of round r (index clamped: in bounds for any r)
+        auto entry = [&](uint32_t r) {
+            const uint32_t e = r * L + q;
+            return lists.slot[e < CAP ? e : CAP - 1][t];
+        };
+        uint32_t next_en = 0;  // entry of the next round to fetch, read one fetch ahead
         auto fetch = [&](uint32_t r, Fetch& F) {
             const uint32_t e = r * L + q;
             F.has = active && e < cnt;
-            const uint32_t en = lists.slot[e < CAP ? e : CAP - 1][t];  // in bounds for any e
+            const uint32_t en = next_en;
+            next_en = entry(r + 1);  // LDS latency overlaps the next round
             F.slot = F.has ? en : s;  // a lane without an entry uses its target
-            F.rj = srec[F.slot];
-            F.vj = svol[F.slot];
+            F.rj = svol[F.slot];  // position and volume of the candidate
+            F.vj = F.rj.w;
             uint32_t rs[L];
             auto bslot = [&](auto J) {
                 return (uint32_t)__float_as_int(group_bcast<L, decltype(J)::value>(__int_as_float((int)F.slot)));
@@ -582,6 +589,7 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                 // own target's rows, unused), so no branch merges the load queues and each round
                 // waits only for its own loads.
                 Fetch A, B, C;
+                next_en = entry(0);
                 fetch(0, A);
                 fetch(1, B);
                 for (uint32_t r = 0;; r += 3) {
@@ -1165,7 +1173,7 @@ static void launch_density_t(const StepParams& p, Workspace& ws, float* density_
                              Profiler* prof) {
     launch_timed(prof, NPA_KERNEL_DENSITY, k_density<D, L>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
                        ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
-                       ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.svol.as<float>(), density_out,
+                       ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.svol.as<float4>(), density_out,
                        ws.nb_chunks.as<uint4>(), ws.nb_count.as<uint32_t>());
 }
 
@@ -1200,7 +1208,7 @@ template <int D, int SM, int MODE, int FL>
 static void launch_perceive_f(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
                               hipStream_t stream, Profiler* prof) {
     launch_timed(prof, NPA_KERNEL_PERCEIVE, k_perceive<D, SM, MODE, FL>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
-                       ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.svol.as<float>(),
+                       ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.svol.as<float4>(),
                        ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), ws.act_rows.as<uint32_t>(),
                        ws.wl_count.as<uint32_t>() + 3, ws.nb_chunks.as<uint4>(), ws.nb_count.as<uint32_t>(),
                        ws.features.as<float>(), io);
