@@ -155,6 +155,9 @@ def main(argv=None) -> int:
     ap.add_argument("--particles", type=int, default=None)
     ap.add_argument("--decode-every", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--mlp-engine", choices=("valu", "mfma"), default="valu",
+                    help="update MLP on the vector ALUs in the reference's order (bit-exact, default) "
+                         "or on the fp32 matrix cores (single-step tolerance)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true",
                     help="skip the HIP-event bracketing of the per-step kernels")
@@ -207,6 +210,14 @@ def main(argv=None) -> int:
         else:
             ex.splat_2d(state, splat)
 
+    from burn_automata_amd import _abi
+    engine = _abi.MLP_MFMA if args.mlp_engine == "mfma" else _abi.MLP_VALU
+
+    def new_state():
+        st_ = ex.create_state(model, pos, st, B, N, w["grid"], w["dt"], w["update_prob"], w["seed"])
+        st_.set_mlp_engine(engine)
+        return st_
+
     def run(state, steps):
         done = 0
         while done < steps:
@@ -221,7 +232,7 @@ def main(argv=None) -> int:
 
     # warmup on a throwaway state
     if args.warmup > 0:
-        ws = ex.create_state(model, pos, st, B, N, w["grid"], w["dt"], w["update_prob"], w["seed"])
+        ws = new_state()
         run(ws, args.warmup)
         torch.cuda.synchronize()
         ws.close()
@@ -248,7 +259,7 @@ def main(argv=None) -> int:
     kernel_ms = {}
     dominant = None
     if profile:
-        ps = ex.create_state(model, pos, st, B, N, w["grid"], w["dt"], w["update_prob"], w["seed"])
+        ps = new_state()
         ctx.check(L.npa_profile_reset(ctx.handle))
         mask = 0
         for kid in KERNEL_IDS.values():
@@ -260,7 +271,7 @@ def main(argv=None) -> int:
         priced = [k for k in ("density", "perceive", "mlp") if k in kernel_ms]
         dominant = max(priced, key=lambda k: kernel_ms[k]) if priced else None
 
-    state = ex.create_state(model, pos, st, B, N, w["grid"], w["dt"], w["update_prob"], w["seed"])
+    state = new_state()
     if dominant is not None:
         ctx.check(L.npa_profile_reset(ctx.handle))
         ctx.check(L.npa_profile_enable(ctx.handle, 1 << KERNEL_IDS[dominant]))
@@ -279,7 +290,7 @@ def main(argv=None) -> int:
     keys = ("candidates", "pairs", "targets", "target_candidates", "target_pairs")
     sums = dict.fromkeys(keys, 0)
     if not args.skip_replay:
-        rs = ex.create_state(model, pos, st, B, N, w["grid"], w["dt"], w["update_prob"], w["seed"])
+        rs = new_state()
         for _ in range(args.steps):
             c = ex.work_counts(rs)
             for k in keys:
@@ -317,6 +328,7 @@ def main(argv=None) -> int:
                             f" tiled splat after steps {sorted(decode_steps)}"
                             if decode_steps and splat else "")),
             "particles": total,
+            "mlp_engine": args.mlp_engine,
             "steps_timed": args.steps,
             "decode_every": decode_every,
             "mean_candidates_per_step": mean["candidates"],

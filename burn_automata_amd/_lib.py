@@ -46,6 +46,8 @@ def _decl(L):
                                           P, P]
     L.npa_splat_2d.argtypes = [P, P, P, u32, ptr(_abi.NpaSplat2dCfg), P]
     L.npa_splat_2d_tiled.argtypes = [P, P, P, u32, u32, ptr(_abi.NpaSplat2dCfg), u32, P]
+    L.npa_context_set_mlp_engine.argtypes = [P, C.c_int]
+    L.npa_state_set_mlp_engine.argtypes = [P, C.c_int]
     L.npa_state_create.argtypes = [P, ptr(_abi.NpaModelCfg), ptr(_abi.NpaWeightsC),
                                    ptr(_abi.NpaGridCfg), P, P, u32, u32, f32, f32, u64, ptr(P)]
     L.npa_state_destroy.argtypes = [P]
@@ -70,7 +72,8 @@ def _decl(L):
                  "npa_state_step_index", "npa_state_buffers", "npa_state_splat_2d",
                  "npa_state_decode_gaussians_3d", "npa_profile_enable", "npa_profile_reset",
                  "npa_profile_read", "npa_state_pair_counts", "npa_splat_2d_tiled",
-                 "npa_state_splat_2d_tiled"):
+                 "npa_state_splat_2d_tiled", "npa_context_set_mlp_engine",
+                 "npa_state_set_mlp_engine"):
         getattr(L, name).restype = st
 
 
@@ -82,7 +85,8 @@ EXPORTED = (
     "npa_state_destroy", "npa_state_step", "npa_state_read", "npa_state_update_model",
     "npa_state_step_index", "npa_state_buffers", "npa_state_splat_2d",
     "npa_state_decode_gaussians_3d", "npa_profile_enable", "npa_profile_reset", "npa_profile_read",
-    "npa_state_pair_counts", "npa_splat_2d_tiled", "npa_state_splat_2d_tiled")
+    "npa_state_pair_counts", "npa_splat_2d_tiled", "npa_state_splat_2d_tiled",
+    "npa_context_set_mlp_engine", "npa_state_set_mlp_engine")
 
 
 def lib():

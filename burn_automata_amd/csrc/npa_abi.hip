@@ -23,6 +23,7 @@ struct npa_context {
     int device = 0;
     hipStream_t stream = nullptr;
     bool host_io = false;
+    int mlp_engine = NPA_MLP_VALU;  // npa_step's update-MLP engine
     int cus = 256;
     std::string last_error;
     npa::Workspace ws;
@@ -47,6 +48,7 @@ struct npa_state {
     float dt = 1.0f, update_prob = 1.0f;
     uint64_t seed = 0;
     uint64_t step_index = 0;
+    int mlp_engine = NPA_MLP_VALU;
     DevBuf pos[2], states[2], density, w1, b1, w2, b2;
     int cur = 0;
     npa::Workspace ws;
@@ -301,6 +303,14 @@ npa_status npa_context_set_stream(npa_context* ctx, void* stream) {
 npa_status npa_context_set_host_io(npa_context* ctx, int host_io) {
     if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
     ctx->host_io = host_io != 0;
+    return NPA_OK;
+}
+
+npa_status npa_context_set_mlp_engine(npa_context* ctx, int engine) {
+    if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
+    if (engine != NPA_MLP_VALU && engine != NPA_MLP_MFMA)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: unknown MLP engine " + std::to_string(engine));
+    ctx->mlp_engine = engine;
     return NPA_OK;
 }
 
@@ -564,6 +574,7 @@ npa_status npa_step(npa_context* ctx, const float* positions, const float* state
     apply_model(&p, *model, grid->eps);
     p.dt = dt;
     p.update_prob = 1.0f;
+    p.mlp_engine = (uint32_t)ctx->mlp_engine;
     if (total && npa::state_stride_for(S) == S && !aligned16(sio.out_states))
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: output states must be 16-byte aligned");
     NPA_HIP(ctx, ctx->ws.reserve(plan, total, B, S, (int)grid->dim, p.FP), "workspace");
@@ -799,6 +810,7 @@ npa_status npa_state_step(npa_state* s, uint32_t steps) {
     p.dt = s->dt;
     p.update_prob = s->update_prob;
     p.base_seed = base_seed(s->seed);
+    p.mlp_engine = (uint32_t)s->mlp_engine;
     npa::StepIO io;
     io.w1 = s->w1.as<float>();
     io.b1 = s->b1.as<float>();
@@ -821,6 +833,14 @@ npa_status npa_state_step(npa_state* s, uint32_t steps) {
         s->cur = 1 - c;
         s->step_index += 1;
     }
+    return NPA_OK;
+}
+
+npa_status npa_state_set_mlp_engine(npa_state* s, int engine) {
+    if (!s) return NPA_ERR_INVALID_ARGUMENT;
+    if (engine != NPA_MLP_VALU && engine != NPA_MLP_MFMA)
+        return fail(s->ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: unknown MLP engine " + std::to_string(engine));
+    s->mlp_engine = engine;
     return NPA_OK;
 }
 

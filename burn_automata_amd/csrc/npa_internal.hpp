@@ -232,6 +232,7 @@ struct StepParams {
     float update_prob;
     uint32_t step_index;
     uint32_t base_seed;
+    uint32_t mlp_engine;  // NPA_MLP_VALU (bit-exact) or NPA_MLP_MFMA
     // cell directory of the split bins (set by the neighbour-pass launchers)
     const uint32_t* dir_n;
     const int4* dir_e;

@@ -883,7 +883,78 @@ __global__ __launch_bounds__(256) void k_pad_weights(StepParams P, int D, const 
 //   phase 2: lane = row; wave w owns outputs [OPW*w, OPW*w + OPW); each output sum starts from its
 //            bias and adds hidden units h = 0..H-1 in order, reading them from LDS.
 //   phase 3: wave 0 applies motion scaling, gates, mask and the Euler step for its 64 rows.
-template <int D, int SM, int FM>
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Phases 1 and 2 on the fp32 matrix cores (v_mfma_f32_16x16x4_f32: A 16x4, B 4x16, D 16x16;
+// lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16] and holds D[4 (l / 16) + r][l % 16]).
+// Wave w serves rows 16w..16w+15 of the block's 64. Each accumulator starts from its bias; the
+// matrix cores add the products in their own order, so the result differs from the reference's
+// sequential sum in the last bits.
+template <int FM, int OP>
+__device__ __forceinline__ void mlp_mfma(const StepParams& P, const float* __restrict__ sfeatures, uint32_t row0,
+                                         uint32_t nrows, uint32_t wave, uint32_t lane, const float* __restrict__ wpad,
+                                         float* hid, float* ul) {
+    const uint32_t H = P.H, T = P.T;
+    const uint32_t HP = (H + 127) / 128 * 128;
+    const float* w1t = wpad;
+    const float* b1p = w1t + (uint64_t)FM * HP;
+    const float* w2t = b1p + HP;
+    const float* b2p = w2t + (uint64_t)H * OP;
+    const uint32_t li = lane % 16, lk = lane / 16;
+    const uint32_t rl = 16 * wave + li;          // block-local row this lane feeds as A
+    const bool rvalid = row0 + rl < nrows;
+    // layer 1: hidden = relu(b1 + F W1^T), 16 rows x HP hidden per wave, 16 columns per tile
+    for (uint32_t hb = 0; hb < HP; hb += 128) {
+        v4f acc[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float bias = b1p[hb + 16 * t + li];
+            acc[t] = v4f{bias, bias, bias, bias};
+        }
+#pragma unroll 4
+        for (int k0 = 0; k0 < FM; k0 += 4) {
+            const uint32_t k = (uint32_t)k0 + lk;
+            const float a = rvalid ? sfeatures[(uint64_t)k * T + row0 + rl] : 0.0f;
+            const float* wk = w1t + (uint64_t)k * HP + hb + li;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, wk[16 * t], acc[t], 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                hid[(hb + 16 * t + li) * 64 + 16 * wave + 4 * lk + r] = fmaxf(acc[t][r], 0.0f);
+    }
+    __syncthreads();
+    // layer 2: u = b2 + hidden W2^T, 16 rows x OP outputs per wave
+    constexpr int OT = (OP + 15) / 16;
+    v4f acc2[OT];
+#pragma unroll
+    for (int t = 0; t < OT; ++t) {
+        const uint32_t col = 16 * t + li;
+        const float bias = col < (uint32_t)OP ? b2p[col] : 0.0f;
+        acc2[t] = v4f{bias, bias, bias, bias};
+    }
+    for (uint32_t k0 = 0; k0 < HP; k0 += 4) {
+        const uint32_t k = k0 + lk;
+        const float a = hid[k * 64 + rl];
+#pragma unroll
+        for (int t = 0; t < OT; ++t) {
+            const uint32_t col = 16 * t + li;
+            const float b = (k < H && col < (uint32_t)OP) ? w2t[(uint64_t)k * OP + col] : 0.0f;
+            acc2[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc2[t], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < OT; ++t) {
+        const uint32_t col = 16 * t + li;
+        if (col < (uint32_t)OP)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ul[(16 * wave + 4 * lk + r) * (OP + 1) + col] = acc2[t][r];
+    }
+}
+
+template <int D, int SM, int FM, int ENG>
 __global__ __launch_bounds__(256) void k_mlp_euler(StepParams P, const float* __restrict__ sfeatures,
                                                    const float* __restrict__ sstate,
                                                    const uint32_t* __restrict__ perm,
@@ -895,8 +966,11 @@ __global__ __launch_bounds__(256) void k_mlp_euler(StepParams P, const float* __
     extern __shared__ float lds[];
     const uint32_t H = P.H, T = P.T;
     const uint32_t HP = (H + 127) / 128 * 128;
-    float* hid = lds;                       // [HP][64]
-    float* ul = lds + (size_t)HP * 64;      // [64][OP + 1]
+    // LDS: hid [HP][64] (for HP = 128 the four waves' w1t slices [4][FM][32] share its region
+    // before it is written); ul [64][OP + 1]; the VALU path's w2t copy [H][OP]
+    float* hid = lds;
+    const bool stage_w1 = HP == 128;  // one pass covers every hidden unit
+    float* ul = lds + (stage_w1 && 4 * FM * 32 > HP * 64 ? (size_t)4 * FM * 32 : (size_t)HP * 64);
     const float* w1t = wpad;
     const float* b1p = w1t + (uint64_t)FM * HP;
     const float* w2t = b1p + HP;
@@ -910,25 +984,57 @@ __global__ __launch_bounds__(256) void k_mlp_euler(StepParams P, const float* __
     const bool valid = row < nrows;
     const uint32_t s = act_rows[valid ? row : row0];  // sorted slot of this row's particle
 
+    if constexpr (ENG == 1) {
+        mlp_mfma<FM, OP>(P, sfeatures, row0, nrows, wave, lane, wpad, hid, ul);
+    } else {
     float f[FM];
 #pragma unroll
     for (int k = 0; k < FM; ++k) f[k] = valid ? sfeatures[(uint64_t)k * T + row] : 0.0f;
 
-    // phase 1: hidden units
-    for (uint32_t hb = wave * 32; hb < HP; hb += 128) {
+    // phase 1: hidden units. With one pass (HP = 128) each wave stages its 32-unit slice of w1t in
+    // LDS (the region hid takes afterwards) and reads it back with broadcast loads, so no weight
+    // load waits on L2; wider layers read w1t from memory.
+    float* w2s = ul + 64 * (OP + 1);  // [H][OP]
+    if (stage_w1) {
+        float* w1s = lds + (size_t)wave * FM * 32;  // [FM][32] of this wave
+        const uint32_t hb = wave * 32;
+        for (uint32_t v = lane; v < (uint32_t)FM * 8; v += 64) {  // float4 v = (k, 4 units)
+            const uint32_t k = v / 8, j4 = v % 8;
+            reinterpret_cast<float4*>(w1s)[v] =
+                *reinterpret_cast<const float4*>(w1t + (uint64_t)k * HP + hb + 4 * j4);
+        }
+        __syncthreads();
         float acc[32];
 #pragma unroll
         for (int j = 0; j < 32; ++j) acc[j] = b1p[hb + j];
 #pragma unroll
         for (int k = 0; k < FM; ++k) {
-            const float* wk = w1t + (uint64_t)k * HP + hb;
+            const float* wk = w1s + k * 32;
             const float fk = f[k];
 #pragma unroll
             for (int j = 0; j < 32; ++j) acc[j] += wk[j] * fk;
         }
+        __syncthreads();  // every wave has read its slice before hid overwrites the region
 #pragma unroll
         for (int j = 0; j < 32; ++j) hid[(hb + j) * 64 + lane] = fmaxf(acc[j], 0.0f);
+    } else {
+        for (uint32_t hb = wave * 32; hb < HP; hb += 128) {
+            float acc[32];
+#pragma unroll
+            for (int j = 0; j < 32; ++j) acc[j] = b1p[hb + j];
+#pragma unroll
+            for (int k = 0; k < FM; ++k) {
+                const float* wk = w1t + (uint64_t)k * HP + hb;
+                const float fk = f[k];
+#pragma unroll
+                for (int j = 0; j < 32; ++j) acc[j] += wk[j] * fk;
+            }
+#pragma unroll
+            for (int j = 0; j < 32; ++j) hid[(hb + j) * 64 + lane] = fmaxf(acc[j], 0.0f);
+        }
     }
+    for (uint32_t v = threadIdx.x; v < H * OP / 4; v += blockDim.x)  // OP is a multiple of 4
+        reinterpret_cast<float4*>(w2s)[v] = reinterpret_cast<const float4*>(w2t)[v];
     __syncthreads();
 
     // phase 2: outputs
@@ -939,13 +1045,14 @@ __global__ __launch_bounds__(256) void k_mlp_euler(StepParams P, const float* __
         for (int o = 0; o < OPW; ++o) u[o] = b2p[ob + o];
         for (uint32_t h = 0; h < H; ++h) {
             const float hv = hid[h * 64 + lane];
-            const float* wr = w2t + (uint64_t)h * OP + ob;
+            const float* wr = w2s + h * OP + ob;
 #pragma unroll
             for (int o = 0; o < OPW; ++o) u[o] += wr[o] * hv;
         }
 #pragma unroll
         for (int o = 0; o < OPW; ++o) ul[lane * (OP + 1) + ob + o] = u[o];
     }
+    }  // ENG
     __syncthreads();
     if (wave != 0 || !valid) return;
 
@@ -1256,23 +1363,33 @@ hipError_t launch_pad_weights(const StepParams& p, const float* w1, const float*
 
 #endif  // NPA_PART_MAIN
 
-template <int D, int SM, int FM>
-static hipError_t launch_mlp_t(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream,
+template <int D, int SM, int FM, int ENG>
+static hipError_t launch_mlp_e(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream,
                                Profiler* prof) {
     constexpr int OP = (D + SM + 3) / 4 * 4;
     const size_t HP = (p.H + 127) / 128 * 128;
-    const size_t lds = (HP * 64 + 64 * (OP + 1)) * 4;
+    // hid [HP][64] (the VALU path first holds the four waves' w1t slices there), ul [64][OP+1],
+    // then the VALU path's w2t copy [H][OP]
+    const size_t hid_end = HP == 128 ? std::max<size_t>(HP * 64, 4 * (size_t)FM * 32) : HP * 64;
+    const size_t lds = (hid_end + 64 * (OP + 1) + (ENG == 0 ? (size_t)p.H * OP : 0)) * 4;
     static size_t attr = 65536;
     if (lds > attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_mlp_euler<D, SM, FM>,
+        hipError_t e = hipFuncSetAttribute((const void*)k_mlp_euler<D, SM, FM, ENG>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr = lds;
     }
     const uint32_t blocks = (p.T + 63) / 64;
-    return launch_timed(prof, NPA_KERNEL_MLP, k_mlp_euler<D, SM, FM>, dim3(blocks), dim3(256), (uint32_t)lds, stream,
-                        p, ws.features.as<float>(), ws.sstate.as<float>(), ws.perm.as<uint32_t>(),
+    return launch_timed(prof, NPA_KERNEL_MLP, k_mlp_euler<D, SM, FM, ENG>, dim3(blocks), dim3(256), (uint32_t)lds,
+                        stream, p, ws.features.as<float>(), ws.sstate.as<float>(), ws.perm.as<uint32_t>(),
                         ws.act_rows.as<uint32_t>(), ws.wl_count.as<uint32_t>() + 3, ws.wpad.as<float>(), io);
+}
+
+template <int D, int SM, int FM>
+static hipError_t launch_mlp_t(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream,
+                               Profiler* prof) {
+    if (p.mlp_engine == NPA_MLP_MFMA) return launch_mlp_e<D, SM, FM, 1>(p, ws, io, stream, prof);
+    return launch_mlp_e<D, SM, FM, 0>(p, ws, io, stream, prof);
 }
 
 template <int D, int SM>

@@ -29,6 +29,10 @@ class HipAutomataState:
     def total(self) -> int:
         return self.batch_size * self.particle_count
 
+    def set_mlp_engine(self, engine: int):
+        """The update-MLP engine of this state's steps (_abi.MLP_VALU or _abi.MLP_MFMA)."""
+        self.ctx.check(lib().npa_state_set_mlp_engine(self.handle, int(engine)))
+
     def step_index(self) -> int:
         v = C.c_uint64()
         self.ctx.check(lib().npa_state_step_index(self.handle, C.byref(v)))

@@ -39,6 +39,10 @@ class Context:
         self.check(lib().npa_context_set_host_io(self.handle, int(bool(value))))
         self._host_io = bool(value)
 
+    def set_mlp_engine(self, engine: int):
+        """npa_step's update-MLP engine: MLP_VALU (bit-exact, default) or MLP_MFMA."""
+        self.check(lib().npa_context_set_mlp_engine(self.handle, int(engine)))
+
     def set_stream(self, stream):
         self.check(lib().npa_context_set_stream(self.handle, C.c_void_p(stream)))
 

@@ -142,6 +142,15 @@ void npa_context_destroy(npa_context* ctx);
 npa_status npa_context_set_stream(npa_context* ctx, void* stream);
 /* 0: array arguments are device pointers (default). 1: host pointers, synchronous. */
 npa_status npa_context_set_host_io(npa_context* ctx, int host_io);
+/* Update-MLP engine of npa_step and of states (no counterpart in the reference, whose MLP is a
+ * serial f32 loop). NPA_MLP_VALU (default): every sum in the reference's order on the vector
+ * ALUs, bit-identical to the CPU path. NPA_MLP_MFMA: the two dense layers on the fp32 matrix
+ * cores (v_mfma_f32_16x16x4_f32), whose accumulation order differs from the reference's: a single
+ * step stays within 1e-6 of it, while a rollout drifts apart like under any reordering of the
+ * sums (the dynamics amplify last-bit differences). */
+enum { NPA_MLP_VALU = 0, NPA_MLP_MFMA = 1 };
+npa_status npa_context_set_mlp_engine(npa_context* ctx, int engine);
+
 /* Blocks until all work queued on the context's stream has finished. */
 npa_status npa_context_synchronize(npa_context* ctx);
 /* Message of the last failing call on this context ("" when none). */
@@ -256,6 +265,8 @@ npa_status npa_state_step(npa_state* state, uint32_t steps);
 npa_status npa_state_read(npa_state* state, float* positions, float* states, float* density);
 /* update_state_model (crates/burn_automata/src/gpu/executor/state.rs:626). */
 npa_status npa_state_update_model(npa_state* state, const npa_weights* weights);
+/* The state's update-MLP engine (NPA_MLP_*; see npa_context_set_mlp_engine). */
+npa_status npa_state_set_mlp_engine(npa_state* state, int engine);
 /* Current step index (number of steps taken). */
 npa_status npa_state_step_index(const npa_state* state, uint64_t* step_index);
 /* Device pointers of the current particle buffers (valid until the next step). */

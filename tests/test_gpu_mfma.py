@@ -1,0 +1,76 @@
+"""The update MLP on the fp32 matrix cores (NPA_MLP_MFMA) against the CPU oracle (runs on an MI355X).
+
+The matrix cores accumulate the products in their own order, so the step is compared within the
+single-step gate (1e-5, norm-relative) instead of bit for bit; everything before the MLP (the
+hashgrid, density and features) is unchanged, so the density stays bit-exact.
+"""
+import numpy as np
+import pytest
+
+from burn_automata_amd import _abi
+from burn_automata_amd import synthetic as syn
+from burn_automata_amd.config import HashGridConfig, NpaConfig
+from burn_automata_amd.executor import HipAutomataExecutor
+from burn_automata_amd.model import NpaModel
+from burn_automata_amd.runtime import Context
+from oracle import oracle as O
+from tests.helpers import rel_err, to_np
+
+pytestmark = pytest.mark.gpu
+
+STEP_TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def mctx():
+    c = Context(0)
+    c.set_mlp_engine(_abi.MLP_MFMA)
+    yield c
+    c.close()
+
+
+def _case(name):
+    if name in ("c1", "c2", "c5"):
+        w = syn.workload(name)
+        return w["model"], w["grid"], w["positions"], w["states"], w["weights"], w["batch"], w["n"]
+    if name == "growing_3d":
+        m, g, n = NpaConfig.growing_3dgs(), HashGridConfig.growing_3dgs(), 2048
+        return (m, g, syn.uniform_ball(n, 4, 0.5), syn.normal_states(n, m.state_dims, 4),
+                syn.seeded_weights(m, 4), 1, n)
+    if name == "c4":
+        w = syn.workload("c4", particles=4096)
+        return w["model"], w["grid"], w["positions"], w["states"], w["weights"], 1, w["n"]
+    raise KeyError(name)
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c5", "growing_3d", "c4"])
+def test_mfma_step_within_single_step_gate(mctx, name):
+    m, g, pos, st, w, b, n = _case(name)
+    mask = O.update_mask(b, n, 0.5, 0, 42)
+    want = O.step(m, w, pos, st, b, n, g, 1.0, mask)
+    got = NpaModel(m, w).step(pos, st, b, n, g, 1.0, update_mask=mask, ctx=mctx)
+    np.testing.assert_array_equal(to_np(got.density), want.density)
+    ep, es = rel_err(got.next_positions, want.next_positions), rel_err(got.next_states, want.next_states)
+    # the update itself (next - current) carries the MLP's rounding; compare it on its own scale too
+    du = rel_err(to_np(got.next_states) - st, want.next_states - st)
+    print(f"{name}: mfma step rel err pos={ep:.2e} state={es:.2e} update={du:.2e}")
+    assert ep <= STEP_TOL and es <= STEP_TOL and du <= STEP_TOL
+    off = mask == 0  # masked-out particles take no update on either engine
+    np.testing.assert_array_equal(to_np(got.next_states)[off], want.next_states[off])
+
+
+def test_mfma_state_engine_and_errors(ctx):
+    m, g, pos, st, w, b, n = _case("c1")
+    ex = HipAutomataExecutor(ctx=ctx)
+    s_valu = ex.create_state(NpaModel(m, w), pos, st, b, n, g, 1.0, 0.5, 42)
+    s_mfma = ex.create_state(NpaModel(m, w), pos, st, b, n, g, 1.0, 0.5, 42)
+    s_mfma.set_mlp_engine(_abi.MLP_MFMA)
+    ex.step_state(s_valu)
+    ex.step_state(s_mfma)
+    pv, sv, _ = ex.read_state(s_valu)
+    pm, sm, _ = ex.read_state(s_mfma)
+    assert rel_err(sm, sv) <= STEP_TOL and rel_err(pm, pv) <= STEP_TOL
+    with pytest.raises(_abi.InvalidArgument):
+        s_mfma.set_mlp_engine(7)
+    s_valu.close()
+    s_mfma.close()
