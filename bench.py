@@ -354,9 +354,12 @@ def main(argv=None) -> int:
         k = per_kernel[dominant]
         line["roofline"] = {
             "bound": "mfma", "achieved": k["tflops"], "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-            "frac": k["tflops"] / PEAK_FP32_TFLOPS, "traffic": recorded_traffic(dominant),
-            "traffic_source": "profiles/c2_hbm_traffic.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
-                              "copy-kernel scaled)", "kernel": dominant,
+            "frac": k["tflops"] / PEAK_FP32_TFLOPS,
+            # the committed counter summary covers the C2 workload only
+            "traffic": recorded_traffic(dominant) if args.workload == "c2" and args.particles is None else None,
+            "traffic_source": ("profiles/c2_hbm_traffic.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                               "copy-kernel scaled)" if args.workload == "c2" and args.particles is None
+                               else "not measured for this workload"), "kernel": dominant,
             "engine": "fp32 VALU, unfused mul/add in the reference's order (bit-exact path); the "
                       "MI355X fp32 vector and fp32 matrix peaks are both 157.3 TFLOP/s",
             "mean_launch_ms": k["mean_launch_ms"], "flops_per_launch": k["flops_per_launch"],
