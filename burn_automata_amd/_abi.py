@@ -21,6 +21,9 @@ NPA_ERR_STATE_SHAPE = 11
 NPA_ERR_OUTPUT_SHAPE = 12
 NPA_ERR_INVALID_ARGUMENT = 13
 NPA_ERR_INVALID_MODEL = 20
+NPA_ERR_IO = 21
+NPA_ERR_JSON = 22
+NPA_ERR_INVALID_FORMAT = 23
 NPA_ERR_DEVICE = 30
 NPA_ERR_OUT_OF_MEMORY = 31
 NPA_ERR_COORD_OVERFLOW = 32
@@ -116,6 +119,31 @@ class InvalidModel(KernelError):
     code = NPA_ERR_INVALID_MODEL
 
 
+class IoError(KernelError):
+    """AutomataError::Io."""
+
+    code = NPA_ERR_IO
+
+
+class JsonError(KernelError):
+    """AutomataError::Json (a manifest that is not the reference's JSON)."""
+
+    code = NPA_ERR_JSON
+
+
+class InvalidFormat(KernelError):
+    """AutomataError::InvalidFormat (a damaged .bpk container)."""
+
+    code = NPA_ERR_INVALID_FORMAT
+
+
+class NpaManifestInfo(C.Structure):
+    _fields_ = [("format_version", u32), ("model_kind", C.c_char_p), ("source", C.c_char_p),
+                ("auxiliary_input_dims", u32), ("decoder_dims", C.c_int64),
+                ("output_dims", C.c_int64), ("stopgrad_pos", u32), ("stopgrad_state", u32),
+                ("initialization_particles", u32)]
+
+
 class DeviceError(KernelError):
     code = NPA_ERR_DEVICE
 
@@ -130,8 +158,8 @@ class CoordOverflow(KernelError):
 
 _BY_CODE = {cls.code: cls for cls in (
     InvalidDim, InvalidEps, InvalidGridSize, ParticleModeRequiresPowerOfTwo, PositionShape,
-    StateShape, OutputShape, InvalidArgument, InvalidModel, DeviceError, OutOfMemory,
-    CoordOverflow)}
+    StateShape, OutputShape, InvalidArgument, InvalidModel, IoError, JsonError, InvalidFormat,
+    DeviceError, OutOfMemory, CoordOverflow)}
 
 
 def error_for(code: int, message: str = "") -> KernelError:

@@ -46,6 +46,15 @@ def _decl(L):
                                           P, P]
     L.npa_splat_2d.argtypes = [P, P, P, u32, ptr(_abi.NpaSplat2dCfg), P]
     L.npa_splat_2d_tiled.argtypes = [P, P, P, u32, u32, ptr(_abi.NpaSplat2dCfg), u32, P]
+    L.npa_manifest_load.argtypes = [P, sz, ptr(P), C.c_char_p, sz]
+    L.npa_manifest_load_file.argtypes = [C.c_char_p, ptr(P), C.c_char_p, sz]
+    L.npa_manifest_destroy.argtypes = [P]
+    L.npa_manifest_destroy.restype = None
+    L.npa_manifest_info.argtypes = [P, ptr(_abi.NpaManifestInfo)]
+    L.npa_manifest_model.argtypes = [P, ptr(_abi.NpaModelCfg), ptr(_abi.NpaGridCfg), ptr(_abi.NpaWeightsC)]
+    L.npa_manifest_initialization.argtypes = [P, ptr(P), ptr(P), ptr(u32)]
+    L.npa_bpk_encode.argtypes = [P, sz, P, sz, ptr(sz)]
+    L.npa_sha256.argtypes = [P, sz, P]
     L.npa_context_set_mlp_engine.argtypes = [P, C.c_int]
     L.npa_state_set_mlp_engine.argtypes = [P, C.c_int]
     L.npa_state_create.argtypes = [P, ptr(_abi.NpaModelCfg), ptr(_abi.NpaWeightsC),
@@ -73,7 +82,9 @@ def _decl(L):
                  "npa_state_decode_gaussians_3d", "npa_profile_enable", "npa_profile_reset",
                  "npa_profile_read", "npa_state_pair_counts", "npa_splat_2d_tiled",
                  "npa_state_splat_2d_tiled", "npa_context_set_mlp_engine",
-                 "npa_state_set_mlp_engine"):
+                 "npa_state_set_mlp_engine", "npa_manifest_load", "npa_manifest_load_file",
+                 "npa_manifest_info", "npa_manifest_model", "npa_manifest_initialization",
+                 "npa_bpk_encode", "npa_sha256"):
         getattr(L, name).restype = st
 
 
@@ -86,7 +97,9 @@ EXPORTED = (
     "npa_state_step_index", "npa_state_buffers", "npa_state_splat_2d",
     "npa_state_decode_gaussians_3d", "npa_profile_enable", "npa_profile_reset", "npa_profile_read",
     "npa_state_pair_counts", "npa_splat_2d_tiled", "npa_state_splat_2d_tiled",
-    "npa_context_set_mlp_engine", "npa_state_set_mlp_engine")
+    "npa_context_set_mlp_engine", "npa_state_set_mlp_engine", "npa_manifest_load",
+    "npa_manifest_load_file", "npa_manifest_destroy", "npa_manifest_info", "npa_manifest_model",
+    "npa_manifest_initialization", "npa_bpk_encode", "npa_sha256")
 
 
 def lib():

@@ -14,7 +14,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libnpa_hip.so")
-SOURCES = ["npa_hashgrid.hip", "npa_perception.hip", "npa_decode.hip", "npa_abi.hip"]
+SOURCES = ["npa_hashgrid.hip", "npa_perception.hip", "npa_decode.hip", "npa_abi.hip", "npa_bpk.cpp"]
 # npa_perception.hip compiles as three objects (its NPA_PART selects which kernels each holds)
 PARTS = {"npa_perception.hip": ["-DNPA_PART=0", "-DNPA_PART=2", "-DNPA_PART=3"]}
 ARCH = os.environ.get("NPA_OFFLOAD_ARCH", "gfx950")
@@ -52,7 +52,7 @@ def build(verbose: bool = False) -> str:
     jobs = []
     for src in SOURCES:
         for k, part in enumerate(PARTS.get(src, [None])):
-            obj = os.path.join(objdir, src.replace(".hip", f"_{k}.o"))
+            obj = os.path.join(objdir, os.path.splitext(src)[0] + f"_{k}.o")
             cmd = [hipcc(), f"--offload-arch={ARCH}", "-c"] + FLAGS + ([part] if part else []) + \
                 ["-o", obj, os.path.join(CSRC, src)]
             jobs.append((src, obj, cmd))

@@ -42,6 +42,9 @@ typedef enum npa_status {
     NPA_ERR_OUTPUT_SHAPE = 12,         /* KernelError::OutputShape */
     NPA_ERR_INVALID_ARGUMENT = 13,     /* KernelError::InvalidArgument */
     NPA_ERR_INVALID_MODEL = 20,        /* AutomataError::InvalidModel (crates/burn_automata/src/error.rs) */
+    NPA_ERR_IO = 21,                   /* AutomataError::Io */
+    NPA_ERR_JSON = 22,                 /* AutomataError::Json */
+    NPA_ERR_INVALID_FORMAT = 23,       /* AutomataError::InvalidFormat */
     NPA_ERR_DEVICE = 30,               /* HIP runtime failure */
     NPA_ERR_OUT_OF_MEMORY = 31,
     NPA_ERR_COORD_OVERFLOW = 32        /* a cell coordinate left the i32 range the device path supports */
@@ -283,6 +286,50 @@ npa_status npa_state_splat_2d_tiled(npa_state* state, const npa_splat2d_cfg* cfg
 npa_status npa_state_decode_gaussians_3d(npa_state* state, const npa_gaussian_decode_cfg* cfg,
                                          float* position_visibility, float* spherical_harmonic,
                                          float* rotation, float* scale_opacity);
+
+/* ------------------------------------------------------- model files */
+/* A BpkModelManifest (crates/burn_automata/src/import.rs:20-31) read from a .bpk container or
+ * its bare JSON payload: replaces load_manifest / load_manifest_bytes (import.rs:378-390) and
+ * decode_bpk_manifest (import.rs:460-498), with the same checks in the same order (header
+ * length, magic, container version, payload length, SHA-256, JSON, validate_manifest
+ * import.rs:500-506) and the same status per failure (NPA_ERR_INVALID_FORMAT, NPA_ERR_JSON,
+ * NPA_ERR_INVALID_MODEL, NPA_ERR_IO). Host memory; no device is touched. The message of a
+ * failure is written to err (err_len bytes, NUL-terminated) when err is not NULL. */
+typedef struct npa_manifest npa_manifest;
+npa_status npa_manifest_load(const uint8_t* bytes, size_t len, npa_manifest** out, char* err,
+                             size_t err_len);
+npa_status npa_manifest_load_file(const char* path, npa_manifest** out, char* err, size_t err_len);
+void npa_manifest_destroy(npa_manifest* manifest);
+/* Manifest header fields; strings stay valid until npa_manifest_destroy (source is NULL for
+ * None; decoder_dims / output_dims are -1 for None). */
+typedef struct npa_manifest_info_t {
+    uint32_t format_version;
+    const char* model_kind;
+    const char* source;
+    uint32_t auxiliary_input_dims;
+    int64_t decoder_dims;
+    int64_t output_dims;
+    uint32_t stopgrad_pos;
+    uint32_t stopgrad_state;
+    uint32_t initialization_particles;  /* 0 when the manifest has no initialization */
+} npa_manifest_info_t;
+npa_status npa_manifest_info(const npa_manifest* manifest, npa_manifest_info_t* info);
+/* BpkModelManifest::into_model (import.rs:94-99) as the ABI's config structs; weights point into
+ * the manifest (host memory, valid until npa_manifest_destroy). NPA_ERR_INVALID_MODEL for a model
+ * with auxiliary inputs, which the rollout path does not take. Any pointer may be NULL. */
+npa_status npa_manifest_model(const npa_manifest* manifest, npa_model_cfg* model, npa_grid_cfg* grid,
+                              npa_weights* weights);
+/* The manifest's particle initialization (import.rs:33-37): positions[n][4], states[n][S];
+ * NPA_ERR_INVALID_ARGUMENT when it has none. */
+npa_status npa_manifest_initialization(const npa_manifest* manifest, const float** positions,
+                                       const float** states, uint32_t* particle_count);
+/* encode_bpk_manifest (import.rs:444-458) for an already serialized JSON payload: writes the
+ * container (52-byte header + payload) to out; *required receives its length. out may be NULL to
+ * query the length; NPA_ERR_OUTPUT_SHAPE when out_len is too small. */
+npa_status npa_bpk_encode(const uint8_t* payload, size_t len, uint8_t* out, size_t out_len,
+                          size_t* required);
+/* SHA-256 (FIPS 180-4) of data, the container's checksum (sha2::Sha256 in the reference). */
+npa_status npa_sha256(const uint8_t* data, size_t len, uint8_t* digest /* 32 bytes */);
 
 /* ---------------------------------------------------------- profiling */
 /* Kernel ids for npa_profile_read. */

@@ -71,7 +71,7 @@ def test_ctypes_declarations_match_prototype_arity(lib):
 def test_status_codes_match_header():
     text = _header_text()
     codes = {m.group(1): int(m.group(2)) for m in re.finditer(r"\b(NPA_(?:OK|ERR_\w+))\s*=\s*(\d+)", text)}
-    assert len(codes) == 13
+    assert len(codes) == 16
     for name, value in codes.items():
         assert getattr(_abi, name) == value, name
         if name != "NPA_OK":
@@ -83,6 +83,7 @@ def test_struct_layouts_match_the_c_compiler(tmp_path):
         "npa_grid_cfg": _abi.NpaGridCfg, "npa_perception_opts": _abi.NpaPerceptionOpts,
         "npa_model_cfg": _abi.NpaModelCfg, "npa_weights": _abi.NpaWeightsC,
         "npa_gaussian_decode_cfg": _abi.NpaGaussianDecodeCfg, "npa_splat2d_cfg": _abi.NpaSplat2dCfg,
+        "npa_manifest_info_t": _abi.NpaManifestInfo,
     }
     lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "npa_abi.h"', "int main(void) {"]
     for cname, py in structs.items():

@@ -162,3 +162,27 @@ def test_tiled_splat_matches_separate_splats(ctx):
         alone = to_np(K.splat_particles_2d(pos[k * n:(k + 1) * n], colors[k * n:(k + 1) * n], cfg,
                                            ctx=ctx))
         np.testing.assert_array_equal(win, alone)
+
+
+def test_bpk_model_drives_the_rollout(ctx):
+    """A model read from a .bpk container (burn_automata_amd.bpk, import.rs:378-498) steps on the
+    device exactly as the oracle steps the weights it was written from."""
+    from burn_automata_amd import bpk
+    from tests.test_bpk import container, manifest_json
+
+    w = syn.workload("c1", particles=2048)
+    pos = w["positions"]
+    st = w["states"]
+    man = bpk.load_manifest_bytes(container(manifest_json(w["model"], w["grid"], w["weights"],
+                                                          initialization=(pos, st))))
+    model = man.into_model()
+    p0, s0 = man.initialization
+    ex = HipAutomataExecutor(ctx=ctx)
+    state = ex.create_state(model, p0, s0, 1, p0.shape[0], man.hashgrid, 1.0, 0.5, 42)
+    ex.step_state_many(state, 8)
+    gp, gs, _ = ex.read_state(state)
+    want_p, want_s = O.rollout(man.config, man.weights, p0, s0, 1, p0.shape[0], man.hashgrid, 8, 1.0,
+                               0.5, 42, 0)
+    np.testing.assert_array_equal(to_np(gp), want_p)
+    np.testing.assert_array_equal(to_np(gs), want_s)
+    state.close()
