@@ -34,7 +34,7 @@ MLP_MFMA = 1
 
 # kernel ids for npa_profile_read
 KERNEL_NAMES = ("hash_rank", "table_scan", "offsets_scan", "scatter", "density", "perceive", "splat",
-                "mlp", "split", "active")
+                "mlp", "split", "active", "render")
 
 
 class NpaGridCfg(C.Structure):
@@ -69,6 +69,13 @@ class NpaGaussianDecodeCfg(C.Structure):
 class NpaSplat2dCfg(C.Structure):
     _fields_ = [("image_size", u32), ("sigma", f32), ("lo", f32), ("hi", f32),
                 ("normalize_color", u32), ("y_up", u32), ("pixel_size", f32)]
+
+
+class NpaRenderCfg(C.Structure):
+    _fields_ = [("image_size", u32), ("sigma", f32), ("min_sigma", f32), ("max_sigma", f32),
+                ("gaussian_decode_mode", u32), ("world_scale", f32), ("target_samples", u32),
+                ("opacity_logit_bias", f32), ("density_weight", f32), ("color_weight", f32),
+                ("depth_weight", f32)]
 
 
 class KernelError(RuntimeError):

@@ -6,6 +6,7 @@
 * ``NpaConfig`` / ``EquivarianceMode``: crates/burn_automata/src/config.rs:22-199
 * ``GaussianDecodeConfig`` / ``GaussianDecodeMode``: crates/burn_automata_kernels/src/gaussian.rs:13-51
 * ``Splat2dConfig``: crates/burn_automata_kernels/src/splat.rs:6-28
+* ``RenderLossConfig`` / ``RenderViewPreset``: crates/burn_automata/src/render_loss.rs:25-63
 """
 from __future__ import annotations
 
@@ -253,6 +254,53 @@ class Splat2dConfig:
         c.normalize_color = int(bool(self.normalize_color))
         c.y_up = int(bool(self.y_up))
         c.pixel_size = float(self.pixel_size)
+        return c
+
+
+class RenderViewPreset(IntEnum):
+    """RenderViewPreset (crates/burn_automata/src/render_loss.rs:25-31)."""
+
+    Xy = 0
+    Xz = 1
+    Yz = 2
+    Iso = 3
+
+
+ALL_VIEWS = (RenderViewPreset.Xy, RenderViewPreset.Xz, RenderViewPreset.Yz, RenderViewPreset.Iso)
+
+
+@dataclass
+class RenderLossConfig:
+    """RenderLossConfig (crates/burn_automata/src/render_loss.rs:33-63), reference defaults."""
+
+    image_size: int = 64
+    sigma: float = 2.5
+    min_sigma: float = 0.75
+    max_sigma: float = 5.0
+    gaussian_decode_mode: GaussianDecodeMode = GaussianDecodeMode.GaussianSh0FixedScale
+    world_scale: float = 1.25
+    target_samples: int = 8192
+    opacity_logit_bias: float = 0.0
+    density_weight: float = 1.0
+    color_weight: float = 1.0
+    depth_weight: float = 1.0
+
+    def replace(self, **kw) -> "RenderLossConfig":
+        return dataclasses.replace(self, **kw)
+
+    def to_c(self) -> _abi.NpaRenderCfg:
+        c = _abi.NpaRenderCfg()
+        c.image_size = int(self.image_size)
+        c.sigma = float(self.sigma)
+        c.min_sigma = float(self.min_sigma)
+        c.max_sigma = float(self.max_sigma)
+        c.gaussian_decode_mode = int(self.gaussian_decode_mode)
+        c.world_scale = float(self.world_scale)
+        c.target_samples = int(self.target_samples)
+        c.opacity_logit_bias = float(self.opacity_logit_bias)
+        c.density_weight = float(self.density_weight)
+        c.color_weight = float(self.color_weight)
+        c.depth_weight = float(self.depth_weight)
         return c
 
 

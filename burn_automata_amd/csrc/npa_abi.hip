@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <string>
 #include <vector>
 
@@ -727,6 +728,104 @@ npa_status npa_splat_2d_tiled(npa_context* ctx, const float* positions, const fl
     return NPA_OK;
 }
 
+// validate_render_loss_config (render_loss/attributes.rs:114-174), then this library's limits.
+static npa_status check_render(npa_context* ctx, const npa_render_cfg* cfg, const uint32_t* views, uint32_t nviews) {
+    if (!cfg) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null render config");
+    auto bad = [&](const std::string& m) { return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + m); };
+    if (cfg->image_size == 0) return bad("render loss image_size must be non-zero");
+    if (cfg->target_samples == 0) return bad("render loss target_samples must be non-zero");
+    if (!std::isfinite(cfg->sigma) || cfg->sigma <= 0.0f)
+        return bad("render loss sigma must be finite and positive, got " + fmt_f(cfg->sigma));
+    if (!std::isfinite(cfg->min_sigma) || cfg->min_sigma <= 0.0f)
+        return bad("render loss min_sigma must be finite and positive, got " + fmt_f(cfg->min_sigma));
+    if (!std::isfinite(cfg->max_sigma) || cfg->max_sigma < cfg->min_sigma)
+        return bad("render loss max_sigma must be finite and >= min_sigma, got max=" + fmt_f(cfg->max_sigma) +
+                   " min=" + fmt_f(cfg->min_sigma));
+    if (!std::isfinite(cfg->world_scale) || cfg->world_scale <= 0.0f)
+        return bad("render loss world_scale must be finite and positive, got " + fmt_f(cfg->world_scale));
+    if (!std::isfinite(cfg->opacity_logit_bias))
+        return bad("render loss opacity_logit_bias must be finite, got " + fmt_f(cfg->opacity_logit_bias));
+    if (!std::isfinite(cfg->density_weight) || cfg->density_weight < 0.0f)
+        return bad("render loss density_weight must be finite and non-negative, got " + fmt_f(cfg->density_weight));
+    if (!std::isfinite(cfg->color_weight) || cfg->color_weight < 0.0f)
+        return bad("render loss color_weight must be finite and non-negative, got " + fmt_f(cfg->color_weight));
+    if (!std::isfinite(cfg->depth_weight) || cfg->depth_weight < 0.0f)
+        return bad("render loss depth_weight must be finite and non-negative, got " + fmt_f(cfg->depth_weight));
+    if (cfg->gaussian_decode_mode > NPA_DECODE_SH0_ORIENTED) return bad("unknown gaussian decode mode");
+    if (cfg->image_size > 4096) return bad("render image_size must be <= 4096");
+    if (!(ceilf(5.0f * cfg->max_sigma) <= 1024.0f)) return bad("render radius ceil(5*max_sigma) must be <= 1024 pixels");
+    if (nviews == 0 || nviews > npa::kMaxRenderViews || !views) return bad("render needs 1..=16 views");
+    for (uint32_t v = 0; v < nviews; ++v)
+        if (views[v] > NPA_VIEW_ISO) return bad("unknown render view " + std::to_string(views[v]));
+    const uint64_t t = (cfg->image_size + 15) / 16;
+    if (t * t * nviews > 65536) return bad("render images too large (at most 65536 16x16 tiles over all views)");
+    return NPA_OK;
+}
+
+npa_status npa_render_views(npa_context* ctx, const float* positions, const float* colors, const float* opacities,
+                            const float* sigmas, uint32_t count, const uint32_t* views, uint32_t nviews,
+                            const npa_render_cfg* cfg, float* images) {
+    if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
+    npa_status st = check_render(ctx, cfg, views, nviews);
+    if (st) return st;
+    if (!images) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null images");
+    if (count && (!positions || !colors || !opacities || !sigmas))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null particle arrays");
+    if ((uint64_t)count * nviews >= (1ull << 31))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: too many particles");
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint64_t px = (uint64_t)cfg->image_size * cfg->image_size * nviews;
+    HostIO io(ctx);
+    const float4* pos = (const float4*)io.in(positions, (uint64_t)count * 16);
+    const float* col = io.in(colors, (uint64_t)count * 12);
+    const float* op = io.in(opacities, (uint64_t)count * 4);
+    const float* sg = io.in(sigmas, (uint64_t)count * 4);
+    float* img = io.out(images, px * 20);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if (count && !aligned16(pos)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: positions must be 16-byte aligned");
+    NPA_HIP(ctx, npa::launch_render_views(pos, col, op, sg, count, views, nviews, *cfg, img, ctx->splat_ws, ctx->stream,
+                                          &ctx->prof),
+            "render");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
+static npa_status check_render_states(npa_context* ctx, uint32_t S, const npa_render_cfg* cfg) {
+    if (S < 3)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT,
+                    "invalid argument: render loss needs at least 3 state channels for color, got " + std::to_string(S));
+    if (cfg->gaussian_decode_mode == NPA_DECODE_SH0_LEARNED_SCALE && S < 5)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT,
+                    "invalid argument: learned-scale render decode needs at least 5 state channels, got " +
+                        std::to_string(S));
+    return NPA_OK;
+}
+
+npa_status npa_render_attributes(npa_context* ctx, const float* states, uint32_t count, uint32_t S,
+                                 const npa_render_cfg* cfg, float* colors, float* opacities, float* sigmas,
+                                 float* derivatives) {
+    if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
+    if (!cfg) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null render config");
+    npa_status st = check_render_states(ctx, S, cfg);
+    if (st) return st;
+    if (cfg->gaussian_decode_mode > NPA_DECODE_SH0_ORIENTED)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: unknown gaussian decode mode");
+    if (count && (!states || !colors || !opacities || !sigmas))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null attribute arrays");
+    if ((uint64_t)count * S >= (1ull << 40)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: too many particles");
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    HostIO io(ctx);
+    const float* s = io.in(states, (uint64_t)count * S * 4);
+    float* col = io.out(colors, (uint64_t)count * 12);
+    float* op = io.out(opacities, (uint64_t)count * 4);
+    float* sg = io.out(sigmas, (uint64_t)count * 4);
+    float* dv = derivatives ? io.out(derivatives, (uint64_t)count * 4) : nullptr;
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    NPA_HIP(ctx, npa::launch_render_attributes(s, count, S, *cfg, col, op, sg, dv, ctx->stream), "render attributes");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
 // ==================================================================== executor
 npa_status npa_state_create(npa_context* ctx, const npa_model_cfg* model, const npa_weights* w,
                             const npa_grid_cfg* grid, const float* positions, const float* states, uint32_t B,
@@ -932,6 +1031,38 @@ npa_status npa_state_splat_2d_tiled(npa_state* s, const npa_splat2d_cfg* cfg, ui
                                       s->model.state_dims, s->B * s->N, *cfg, img, s->splat_ws, ctx->stream,
                                       &ctx->prof, s->N, windows, tiles_x),
             "splat");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
+npa_status npa_state_render_views(npa_state* s, const uint32_t* views, uint32_t nviews, const npa_render_cfg* cfg,
+                                  float* images) {
+    if (!s) return NPA_ERR_INVALID_ARGUMENT;
+    npa_context* ctx = s->ctx;
+    npa_status st = check_render(ctx, cfg, views, nviews);
+    if (st) return st;
+    if (!images) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null images");
+    const uint32_t S = s->model.state_dims;
+    if ((st = check_render_states(ctx, S, cfg))) return st;
+    if (s->B != 1)  // validate_render_trace (attributes.rs:89-112)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT,
+                    "invalid argument: render loss expects batch_size=1, got " + std::to_string(s->B));
+    const uint32_t n = s->N;
+    if ((uint64_t)n * nviews >= (1ull << 31)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: too many particles");
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    NPA_HIP(ctx, s->splat_ws.attrs.reserve((uint64_t)(n ? n : 1) * 20), "render attributes");
+    float* col = s->splat_ws.attrs.as<float>();
+    float* op = col + 3 * (uint64_t)n;
+    float* sg = op + n;
+    HostIO io(ctx);
+    float* img = io.out(images, (uint64_t)cfg->image_size * cfg->image_size * nviews * 20);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    NPA_HIP(ctx, npa::launch_render_attributes(s->states[s->cur].as<float>(), n, S, *cfg, col, op, sg, nullptr,
+                                               ctx->stream),
+            "render attributes");
+    NPA_HIP(ctx, npa::launch_render_views(s->pos[s->cur].as<float4>(), col, op, sg, n, views, nviews, *cfg, img,
+                                          s->splat_ws, ctx->stream, &ctx->prof),
+            "render");
     NPA_HIP(ctx, io.finish(), "host io");
     return NPA_OK;
 }

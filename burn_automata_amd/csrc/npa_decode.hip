@@ -355,7 +355,8 @@ __global__ __launch_bounds__(256) void k_splat_tiles(SplatParams P, const SplatP
 }
 
 void SplatWorkspace::release() {
-    for (DevBuf* b : {&params, &item_start, &keys, &vals, &sorted, &ranks, &table, &totals, &offsets, &count, &flags, &scan})
+    for (DevBuf* b : {&params, &item_start, &keys, &vals, &sorted, &ranks, &table, &totals, &offsets, &count, &flags, &scan,
+                      &attrs})
         b->release();
 }
 
@@ -454,6 +455,329 @@ hipError_t launch_splat_2d(const float4* pos, const float* colors, const float* 
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_splat_tiles, dim3(ntile_total), dim3(256), 0, stream, P, ws.params.as<SplatParticle>(),
                        ws.offsets.as<uint32_t>(), ws.sorted.as<uint32_t>(), image);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------- projected 3D render
+// project_positions (render_loss/projection.rs:11-29) + splat_projected (render_loss/image.rs:18-79)
+// for up to kMaxRenderViews views in one pipeline: item i = v * count + n is particle n seen
+// through view v; its screen tiles get keys v * tiles_per_view + tile, so one stable key sort
+// bins every view, and one tile kernel draws them all. Within a tile the items keep ascending
+// n, so every pixel sums its particles in the reference's order.
+constexpr float kRenderEps = 1.0e-8f;
+
+struct RenderParams {
+    int size, tiles_x;
+    uint32_t tiles_per_view, count;
+    float ws, min_sigma, max_sigma, norm_scale;
+    float basis[kMaxRenderViews][9];  // right, up, forward of each view
+};
+
+struct RenderParticle {  // 48 bytes
+    float fx, fy;
+    int bx, by;
+    int radius;
+    float two_sig2;  // 2 * sigma^2
+    float denom;     // max(in-bounds weight sum, EPS)
+    float opacity;   // clamped to [0, 1]
+    float c[3];
+    float depth;
+};
+
+__device__ __forceinline__ bool render_tiles(const RenderParams& P, int64_t bx, int64_t by, int64_t r, int* tx0,
+                                             int* tx1, int* ty0, int* ty1) {
+    int64_t x0 = bx - r, x1 = bx + r, y0 = by - r, y1 = by + r;
+    if (x0 < 0) x0 = 0;
+    if (y0 < 0) y0 = 0;
+    if (x1 > P.size - 1) x1 = P.size - 1;
+    if (y1 > P.size - 1) y1 = P.size - 1;
+    if (x0 > x1 || y0 > y1) return false;
+    *tx0 = (int)(x0 / kTile);
+    *tx1 = (int)(x1 / kTile);
+    *ty0 = (int)(y0 / kTile);
+    *ty1 = (int)(y1 / kTile);
+    return true;
+}
+
+// grid (ceil(count / 256), nviews): blockIdx.y is the view, so its basis is a uniform load.
+__global__ __launch_bounds__(256) void k_render_prep(RenderParams P, const float4* __restrict__ pos,
+                                                     const float* __restrict__ colors,
+                                                     const float* __restrict__ opacities,
+                                                     const float* __restrict__ sigmas,
+                                                     RenderParticle* __restrict__ out,
+                                                     uint32_t* __restrict__ ntiles) {
+    const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= P.count) return;
+    const uint32_t v = blockIdx.y;
+    const float* B = P.basis[v];
+    const float4 p = pos[n];
+    // dot3 (math.rs:20-22) in the reference's order, then the depth of projection.rs:20-21
+    const float x = p.x * B[0] + p.y * B[1] + p.z * B[2];
+    const float y = p.x * B[3] + p.y * B[4] + p.z * B[5];
+    const float f = p.x * B[6] + p.y * B[7] + p.z * B[8];
+    const float depth = clampf_(0.5f + 0.5f * f / fmaxf(P.ws, kRenderEps), 0.0f, 1.0f);
+    const float sigma = fmaxf(clampf_(sigmas[n], P.min_sigma, P.max_sigma), kRenderEps);
+    const float sigma2 = sigma * sigma;
+    const float two_sig2 = 2.0f * sigma2;
+    const int64_t radius = f32_to_isize(fmaxf(ceilf(5.0f * sigma), 1.0f));
+    const float fsz1 = (float)P.size - 1.0f;
+    const float px = (x + P.ws) / (2.0f * P.ws) * fsz1;
+    const float py = (P.ws - y) / (2.0f * P.ws) * fsz1;
+    const int64_t bx = f32_to_isize(floorf(px)), by = f32_to_isize(floorf(py));
+    const float fx = px - (float)bx, fy = py - (float)by;
+    int tx0 = 0, tx1 = -1, ty0 = 0, ty1 = -1;
+    const bool any = render_tiles(P, bx, by, radius, &tx0, &tx1, &ty0, &ty1);
+    float weight_sum = 0.0f;
+    if (any) {  // the in-bounds part of the footprint, rows then columns as image.rs:49-63 visits it
+        const int64_t oy0 = by - radius < 0 ? -by : -radius;
+        const int64_t oy1 = by + radius > P.size - 1 ? P.size - 1 - by : radius;
+        const int64_t ox0 = bx - radius < 0 ? -bx : -radius;
+        const int64_t ox1 = bx + radius > P.size - 1 ? P.size - 1 - bx : radius;
+        for (int oy = (int)oy0; oy <= (int)oy1; ++oy) {
+            const float dy = (float)oy - fy;
+            for (int ox = (int)ox0; ox <= (int)ox1; ++ox) {
+                const float dx = (float)ox - fx;
+                weight_sum += expf(-(dx * dx + dy * dy) / two_sig2);
+            }
+        }
+    }
+    const uint64_t i = (uint64_t)v * P.count + n;
+    RenderParticle rp;
+    rp.fx = fx;
+    rp.fy = fy;
+    rp.bx = any ? (int)bx : 0;
+    rp.by = any ? (int)by : 0;
+    rp.radius = (int)radius;
+    rp.two_sig2 = two_sig2;
+    rp.denom = fmaxf(weight_sum, kRenderEps);
+    rp.opacity = clampf_(opacities[n], 0.0f, 1.0f);
+    rp.c[0] = colors[3 * (uint64_t)n];
+    rp.c[1] = colors[3 * (uint64_t)n + 1];
+    rp.c[2] = colors[3 * (uint64_t)n + 2];
+    rp.depth = depth;
+    out[i] = rp;
+    ntiles[i] = any ? (uint32_t)((tx1 - tx0 + 1) * (ty1 - ty0 + 1)) : 0u;
+}
+
+__global__ __launch_bounds__(256) void k_render_emit(RenderParams P, const RenderParticle* __restrict__ rp,
+                                                     const uint32_t* __restrict__ ntiles,
+                                                     const uint32_t* __restrict__ start, uint32_t items,
+                                                     uint32_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= items || ntiles[i] == 0) return;
+    const RenderParticle q = rp[i];
+    int tx0, tx1, ty0, ty1;
+    render_tiles(P, q.bx, q.by, q.radius, &tx0, &tx1, &ty0, &ty1);
+    uint32_t k = start[i];
+    const uint32_t base = (i / P.count) * P.tiles_per_view;
+    for (int ty = ty0; ty <= ty1; ++ty)
+        for (int tx = tx0; tx <= tx1; ++tx) {
+            keys[k] = base + (uint32_t)(ty * P.tiles_x + tx);
+            vals[k] = i;
+            ++k;
+        }
+}
+
+// One 16x16 screen tile of one view per block; thread = pixel. The tile's particles are staged
+// through LDS 256 at a time.
+__global__ __launch_bounds__(256) void k_render_tiles(RenderParams P, const RenderParticle* __restrict__ rp,
+                                                      const uint32_t* __restrict__ offsets,
+                                                      const uint32_t* __restrict__ sorted, float* __restrict__ images) {
+    __shared__ RenderParticle buf[256];
+    const uint32_t t = blockIdx.x;
+    const uint32_t v = t / P.tiles_per_view, lt = t - v * P.tiles_per_view;
+    const int tx = (int)(lt % (uint32_t)P.tiles_x), ty = (int)(lt / (uint32_t)P.tiles_x);
+    const int x = tx * kTile + (int)(threadIdx.x % kTile);
+    const int y = ty * kTile + (int)(threadIdx.x / kTile);
+    const uint32_t beg = offsets[t], end = offsets[t + 1];
+    float acc[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t base = beg; base < end; base += 256) {
+        const uint32_t k = base + threadIdx.x;
+        if (k < end) buf[threadIdx.x] = rp[sorted[k]];
+        __syncthreads();
+        const uint32_t m = end - base < 256 ? end - base : 256;
+        for (uint32_t q = 0; q < m; ++q) {
+            const RenderParticle& p = buf[q];
+            const int ox = x - p.bx, oy = y - p.by;
+            if (ox < -p.radius || ox > p.radius || oy < -p.radius || oy > p.radius) continue;
+            const float dx = (float)ox - p.fx, dy = (float)oy - p.fy;
+            float w = expf(-(dx * dx + dy * dy) / p.two_sig2);
+            w = w / p.denom * P.norm_scale * p.opacity;  // image.rs:69
+            acc[0] += p.c[0] * w;
+            acc[1] += p.c[1] * w;
+            acc[2] += p.c[2] * w;
+            acc[3] += w;
+            acc[4] += p.depth * w;
+        }
+        __syncthreads();
+    }
+    if (x < P.size && y < P.size) {
+        float* o = images + (((uint64_t)v * P.size + y) * P.size + x) * 5;
+#pragma unroll
+        for (int c = 0; c < 5; ++c) o[c] = acc[c];
+    }
+}
+
+// view_basis (render_loss/projection.rs:31-43) with normalize3 / cross3 (render_loss/math.rs:24-39).
+static void render_normalize3(const float v[3], float* out) {
+    const float norm = sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+    if (norm <= kRenderEps) {
+        out[0] = 0.0f;
+        out[1] = 0.0f;
+        out[2] = 1.0f;
+        return;
+    }
+    for (int k = 0; k < 3; ++k) out[k] = v[k] / norm;
+}
+
+static bool render_view_basis(uint32_t view, float* b /* right, up, forward */) {
+    static const int axes[3][3] = {{0, 1, 2}, {0, 2, 1}, {1, 2, 0}};  // Xy, Xz, Yz
+    if (view < 3) {
+        for (int k = 0; k < 9; ++k) b[k] = 0.0f;
+        for (int r = 0; r < 3; ++r) b[3 * r + axes[view][r]] = 1.0f;
+        return true;
+    }
+    if (view != NPA_VIEW_ISO) return false;
+    const float a[3] = {1.0f, -1.0f, 0.0f}, u[3] = {1.0f, 1.0f, 2.0f};
+    render_normalize3(a, b);
+    render_normalize3(u, b + 3);
+    const float* r = b;
+    const float* up = b + 3;
+    const float c[3] = {r[1] * up[2] - r[2] * up[1], r[2] * up[0] - r[0] * up[2], r[0] * up[1] - r[1] * up[0]};
+    render_normalize3(c, b + 6);
+    return true;
+}
+
+hipError_t launch_render_views(const float4* pos, const float* colors, const float* opacities, const float* sigmas,
+                               uint32_t count, const uint32_t* views, uint32_t nviews, const npa_render_cfg& cfg,
+                               float* images, SplatWorkspace& ws, hipStream_t stream, Profiler* prof) {
+    if (nviews == 0 || nviews > kMaxRenderViews || !views) return hipErrorInvalidValue;
+    RenderParams P{};
+    P.size = (int)cfg.image_size;
+    P.tiles_x = (P.size + kTile - 1) / kTile;
+    P.tiles_per_view = (uint32_t)(P.tiles_x * P.tiles_x);
+    P.count = count;
+    P.ws = cfg.world_scale;
+    P.min_sigma = cfg.min_sigma;
+    P.max_sigma = cfg.max_sigma;
+    P.norm_scale = 1.0f / (float)(count > 1 ? count : 1);  // image.rs:29
+    for (uint32_t v = 0; v < nviews; ++v)
+        if (!render_view_basis(views[v], P.basis[v])) return hipErrorInvalidValue;
+    const uint64_t ntile64 = (uint64_t)P.tiles_per_view * nviews;
+    if (ntile64 > 65536) return hipErrorInvalidValue;  // the key sort's bin limit
+    const uint32_t ntile_total = (uint32_t)ntile64;
+    const uint64_t items64 = (uint64_t)count * nviews;
+    if (items64 >= (1ull << 31)) return hipErrorInvalidValue;
+    const uint32_t items = (uint32_t)items64;
+    // the widest footprint: sigma <= max(max_sigma, EPS)
+    const float rmaxf = fmaxf(ceilf(5.0f * fmaxf(cfg.max_sigma, kRenderEps)), 1.0f);
+    if (!(rmaxf <= 1024.0f)) return hipErrorInvalidValue;
+    const uint64_t per_axis = (uint64_t)((2 * (int)rmaxf + 1 + kTile - 1) / kTile + 1);
+    const uint64_t max_per = std::min<uint64_t>(per_axis * per_axis, P.tiles_per_view);
+    const uint64_t cap64 = items64 * max_per;
+    if (cap64 >= (1ull << 31)) return hipErrorInvalidValue;
+    const uint32_t cap = (uint32_t)cap64;
+    HashgridPlan plan;
+    if (!make_key_sort_plan(cap, ntile_total, &plan)) return hipErrorInvalidValue;
+    hipError_t e;
+#define NPA_RES(buf, n) \
+    if ((e = (buf).reserve((size_t)(n))) != hipSuccess) return e;
+    NPA_RES(ws.params, (uint64_t)(items ? items : 1) * sizeof(RenderParticle));
+    NPA_RES(ws.item_start, (uint64_t)(items ? items : 1) * 8);
+    NPA_RES(ws.keys, (uint64_t)(cap ? cap : 1) * 4);
+    NPA_RES(ws.vals, (uint64_t)(cap ? cap : 1) * 4);
+    NPA_RES(ws.sorted, (uint64_t)(cap ? cap : 1) * 4);
+    NPA_RES(ws.ranks, (uint64_t)(cap ? cap : 1) * 4);
+    NPA_RES(ws.table, plan.table_entries * 4);
+    NPA_RES(ws.totals, (uint64_t)ntile_total * 4);
+    NPA_RES(ws.offsets, ((uint64_t)ntile_total + 1) * 4);
+    NPA_RES(ws.count, 64);
+    NPA_RES(ws.scan, (2 * ((uint64_t)items / kScanBlock + 1) + 2) * 4);
+    NPA_RES(ws.flags, 64);
+#undef NPA_RES
+    ProfScope ps(prof, NPA_KERNEL_RENDER, stream);
+    uint32_t* ntiles = ws.item_start.as<uint32_t>() + (items ? items : 1);
+    uint32_t* start = ws.item_start.as<uint32_t>();
+    RenderParticle* rp = ws.params.as<RenderParticle>();
+    if (count) {
+        hipLaunchKernelGGL(k_render_prep, dim3((count + 255) / 256, nviews), dim3(256), 0, stream, P, pos, colors,
+                           opacities, sigmas, rp, ntiles);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    {  // start = exclusive prefix of ntiles, total key count into ws.count
+        const uint32_t nb = (items + kScanBlock - 1) / kScanBlock;
+        uint32_t* sums = ws.scan.as<uint32_t>();
+        if (nb) {
+            hipLaunchKernelGGL(k_scan_partials, dim3(nb), dim3(256), 0, stream, ntiles, items, sums);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL(k_scan_1block, dim3(1), dim3(1024), 0, stream, sums, sums + nb + 1, nb,
+                           ws.count.as<uint32_t>());
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (nb) {
+            hipLaunchKernelGGL(k_scan_apply, dim3(nb), dim3(256), 0, stream, ntiles, start, items, sums + nb + 1);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+    }
+    if (items) {
+        hipLaunchKernelGGL(k_render_emit, dim3((items + 255) / 256), dim3(256), 0, stream, P, rp, ntiles, start, items,
+                           ws.keys.as<uint32_t>(), ws.vals.as<uint32_t>());
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    e = launch_key_sort(plan, ws.keys.as<uint32_t>(), ws.vals.as<uint32_t>(), ws.count.as<uint32_t>(), cap,
+                        ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(), ws.totals.as<uint32_t>(),
+                        ws.offsets.as<uint32_t>(), ws.sorted.as<uint32_t>(), ws.flags.as<uint32_t>(), stream);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_render_tiles, dim3(ntile_total), dim3(256), 0, stream, P, rp, ws.offsets.as<uint32_t>(),
+                       ws.sorted.as<uint32_t>(), images);
+    return hipGetLastError();
+}
+
+// state_tail_render_attributes (render_loss/attributes.rs:15-87): one thread per particle.
+__global__ __launch_bounds__(256) void k_render_attrs(const float* __restrict__ states, uint32_t count, uint32_t S,
+                                                      npa_render_cfg cfg, float* __restrict__ colors,
+                                                      float* __restrict__ opacities, float* __restrict__ sigmas,
+                                                      float* __restrict__ derivatives) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    const float* s = states + (uint64_t)i * S;
+    for (uint32_t k = 0; k < 3; ++k) colors[3 * (uint64_t)i + k] = clampf_(s[S - 3 + k] + 0.5f, 0.0f, 1.0f);
+    // growth_3d_material_opacity_channel (rollout/mod.rs:37-45)
+    const int ch = S > 8 ? 8 : (S > 3 ? 3 : -1);
+    float opacity = 0.95f;  // RENDER_MAX_OPACITY (render_loss.rs:23)
+    if (ch >= 0) {
+        const float z = s[ch] + cfg.opacity_logit_bias;
+        float sg;  // sigmoid (render_loss/math.rs:11-18)
+        if (z >= 0.0f) {
+            sg = 1.0f / (1.0f + expf(-z));
+        } else {
+            const float e = expf(z);
+            sg = e / (1.0f + e);
+        }
+        opacity = clampf_(sg, 0.001f, 0.95f);
+    }
+    opacities[i] = opacity;
+    float sigma, derivative = 0.0f;
+    switch (cfg.gaussian_decode_mode) {
+        case NPA_DECODE_PARTICLE_POINT: sigma = fmaxf(cfg.min_sigma, kRenderEps); break;
+        case NPA_DECODE_SH0_LEARNED_SCALE: {
+            const float logit = clampf_(s[S - 5], -8.0f, 8.0f);
+            const float raw = cfg.sigma * expf(logit);
+            sigma = clampf_(raw, cfg.min_sigma, cfg.max_sigma);
+            derivative = (raw > cfg.min_sigma && raw < cfg.max_sigma) ? raw : 0.0f;
+        } break;
+        default: sigma = clampf_(cfg.sigma, cfg.min_sigma, cfg.max_sigma); break;
+    }
+    sigmas[i] = sigma;
+    if (derivatives) derivatives[i] = derivative;
+}
+
+hipError_t launch_render_attributes(const float* states, uint32_t count, uint32_t S, const npa_render_cfg& cfg,
+                                    float* colors, float* opacities, float* sigmas, float* derivatives,
+                                    hipStream_t stream) {
+    if (count == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_render_attrs, dim3((count + 255) / 256), dim3(256), 0, stream, states, count, S, cfg, colors,
+                       opacities, sigmas, derivatives);
     return hipGetLastError();
 }
 

@@ -308,6 +308,7 @@ hipError_t launch_decode_gaussians(const float4* pos, const float* states, uint3
                                    float* pv, float* sh, float* rot, float* so, hipStream_t stream);
 struct SplatWorkspace {
     DevBuf params, item_start, keys, vals, sorted, ranks, table, totals, offsets, count, flags, scan;
+    DevBuf attrs;  // render attributes of a state's particles: colours [n][3], opacities [n], sigmas [n]
     void release();
 };
 // Particle n is drawn into window n / per_window of a grid of `windows` windows, win_cols per
@@ -316,6 +317,18 @@ hipError_t launch_splat_2d(const float4* pos, const float* colors, const float* 
                            uint32_t state_dims, uint32_t count, const npa_splat2d_cfg& cfg,
                            float* image, SplatWorkspace& ws, hipStream_t stream, Profiler* prof,
                            uint32_t per_window, uint32_t windows, uint32_t win_cols);
+
+// Projected 3D render (render_loss/projection.rs + image.rs): images[nviews][size][size][5].
+// views is a host array of nviews <= kMaxRenderViews NPA_VIEW_* values.
+constexpr uint32_t kMaxRenderViews = 16;
+hipError_t launch_render_views(const float4* pos, const float* colors, const float* opacities,
+                               const float* sigmas, uint32_t count, const uint32_t* views, uint32_t nviews,
+                               const npa_render_cfg& cfg, float* images, SplatWorkspace& ws,
+                               hipStream_t stream, Profiler* prof);
+// state_tail_render_attributes (render_loss/attributes.rs:15-87); derivatives may be null.
+hipError_t launch_render_attributes(const float* states, uint32_t count, uint32_t state_dims,
+                                    const npa_render_cfg& cfg, float* colors, float* opacities,
+                                    float* sigmas, float* derivatives, hipStream_t stream);
 
 int device_cu_count();
 

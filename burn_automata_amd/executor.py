@@ -9,8 +9,10 @@ from __future__ import annotations
 
 import ctypes as C
 
+import numpy as np
+
 from ._lib import lib
-from .config import GaussianDecodeConfig, HashGridConfig, Splat2dConfig
+from .config import ALL_VIEWS, GaussianDecodeConfig, HashGridConfig, RenderLossConfig, Splat2dConfig
 from .model import NpaModel, NpaWeights
 from .runtime import Context, default_context, device_f32, ptr
 
@@ -113,6 +115,18 @@ class HipAutomataExecutor:
                           dtype=torch.float32, device=f"cuda:{self.ctx.device}")
         self.ctx.check(lib().npa_state_splat_2d_tiled(state.handle, C.byref(cfg.to_c()),
                                                       int(tiles_x), ptr(img)))
+        return img
+
+    def render_views(self, state: HipAutomataState, cfg: RenderLossConfig, views=ALL_VIEWS):
+        """The particle images of mesh_multiview_render_loss_from_trace (render_loss.rs:107-141)
+        for the current particles of a batch-1 state: [len(views), size, size, 5]."""
+        import torch
+
+        varr = np.ascontiguousarray([int(v) for v in views], dtype=np.uint32)
+        img = torch.empty((len(varr), cfg.image_size, cfg.image_size, 5), dtype=torch.float32,
+                          device=f"cuda:{self.ctx.device}")
+        self.ctx.check(lib().npa_state_render_views(state.handle, varr.ctypes.data_as(C.c_void_p),
+                                                    len(varr), C.byref(cfg.to_c()), ptr(img)))
         return img
 
     def decode_gaussians_3d(self, state: HipAutomataState, cfg: GaussianDecodeConfig):

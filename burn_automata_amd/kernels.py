@@ -9,6 +9,9 @@ and returns freshly allocated device tensors, as the reference returns owned Vec
 * ``euler_step``              crates/burn_automata_kernels/src/reference/step.rs:4-55
 * ``decode_gaussians_3d``     crates/burn_automata_kernels/src/gaussian.rs:53-100
 * ``splat_particles_2d``      crates/burn_automata_kernels/src/splat.rs:30-93
+* ``render_views``            crates/burn_automata/src/render_loss/projection.rs:11-29 +
+                              render_loss/image.rs:18-79 (project_positions + splat_projected)
+* ``render_attributes``       crates/burn_automata/src/render_loss/attributes.rs:15-87
 
 Inputs may be CUDA tensors (used in place) or host arrays (uploaded first).
 """
@@ -21,7 +24,8 @@ import numpy as np
 
 from . import _abi
 from ._lib import lib
-from .config import (GaussianDecodeConfig, HashGridConfig, PerceptionOptions, Splat2dConfig)
+from .config import (ALL_VIEWS, GaussianDecodeConfig, HashGridConfig, PerceptionOptions,
+                     RenderLossConfig, Splat2dConfig)
 from .runtime import default_context, device_f32, ptr
 
 
@@ -238,3 +242,46 @@ def splat_particles_2d_tiled(positions, colors, batch_size: int, particle_count:
     ctx.check(lib().npa_splat_2d_tiled(ctx.handle, ptr(pos), ptr(col), batch_size, particle_count,
                                        C.byref(cfg.to_c()), int(tiles_x), ptr(img)))
     return img
+
+
+def _views_array(views):
+    v = np.ascontiguousarray([int(x) for x in views], dtype=np.uint32)
+    return v, v.ctypes.data_as(C.c_void_p)
+
+
+def render_views(positions, colors, opacities, sigmas, cfg: RenderLossConfig, views=ALL_VIEWS, ctx=None):
+    """project_positions + splat_projected (render_loss/projection.rs:11-29, image.rs:18-79) for
+    each view: images [len(views), size, size, 5] holding r, g, b, alpha, depth_sum per pixel."""
+    ctx = ctx or default_context()
+    torch = _torch()
+    pos = device_f32(positions, device=ctx.device).reshape(-1, 4)
+    n = pos.shape[0]
+    col = device_f32(colors, device=ctx.device).reshape(-1, 3)
+    op = device_f32(opacities, device=ctx.device).reshape(-1)
+    sg = device_f32(sigmas, device=ctx.device).reshape(-1)
+    if col.shape[0] != n or op.shape[0] != n or sg.shape[0] != n:
+        raise AssertionError("positions, colors, opacities and sigmas differ in length")
+    varr, vptr = _views_array(views)
+    img = torch.empty((len(varr), cfg.image_size, cfg.image_size, 5), dtype=torch.float32,
+                      device=f"cuda:{ctx.device}")
+    ctx.check(lib().npa_render_views(ctx.handle, ptr(pos), ptr(col), ptr(op), ptr(sg), n, vptr,
+                                     len(varr), C.byref(cfg.to_c()), ptr(img)))
+    return img
+
+
+def render_attributes(states, state_dims: int, cfg: RenderLossConfig, ctx=None):
+    """state_tail_render_attributes (render_loss/attributes.rs:15-87): (colors [n, 3],
+    opacities [n], sigmas [n], scale_logit_derivatives [n]) on the device."""
+    ctx = ctx or default_context()
+    torch = _torch()
+    st = device_f32(states, device=ctx.device).reshape(-1)
+    if state_dims == 0 or st.numel() % state_dims:
+        raise _abi.InvalidArgument(f"invalid argument: state len {st.numel()} is not divisible by "
+                                   f"state_dims {state_dims}")
+    n = st.numel() // state_dims
+    dev = f"cuda:{ctx.device}"
+    col = torch.empty((n, 3), dtype=torch.float32, device=dev)
+    op, sg, dv = (torch.empty(n, dtype=torch.float32, device=dev) for _ in range(3))
+    ctx.check(lib().npa_render_attributes(ctx.handle, ptr(st), n, state_dims, C.byref(cfg.to_c()),
+                                          ptr(col), ptr(op), ptr(sg), ptr(dv)))
+    return col, op, sg, dv

@@ -134,6 +134,27 @@ typedef struct npa_splat2d_cfg {
     float pixel_size;
 } npa_splat2d_cfg;
 
+/* RenderViewPreset: crates/burn_automata/src/render_loss.rs:25-31 */
+enum { NPA_VIEW_XY = 0, NPA_VIEW_XZ = 1, NPA_VIEW_YZ = 2, NPA_VIEW_ISO = 3 };
+
+/* RenderLossConfig: crates/burn_automata/src/render_loss.rs:33-63 (reference defaults in
+ * brackets). The raster reads image_size, the sigma fields, gaussian_decode_mode,
+ * world_scale and opacity_logit_bias; the remaining fields are validated as the reference
+ * validates them (render_loss/attributes.rs:114-174). */
+typedef struct npa_render_cfg {
+    uint32_t image_size;           /* [64] */
+    float sigma;                   /* [2.5] pixels */
+    float min_sigma;               /* [0.75] */
+    float max_sigma;               /* [5.0] */
+    uint32_t gaussian_decode_mode; /* NPA_DECODE_* [NPA_DECODE_SH0_FIXED_SCALE] */
+    float world_scale;             /* [1.25] */
+    uint32_t target_samples;       /* [8192] */
+    float opacity_logit_bias;      /* [0.0] */
+    float density_weight;          /* [1.0] */
+    float color_weight;            /* [1.0] */
+    float depth_weight;            /* [1.0] */
+} npa_render_cfg;
+
 /* ------------------------------------------------------------- context */
 typedef struct npa_context npa_context;
 typedef struct npa_state npa_state;
@@ -250,6 +271,27 @@ npa_status npa_splat_2d_tiled(npa_context* ctx, const float* positions, const fl
                               uint32_t batch_size, uint32_t particle_count,
                               const npa_splat2d_cfg* cfg, uint32_t tiles_x, float* image);
 
+/* Replaces project_positions (crates/burn_automata/src/render_loss/projection.rs:11-29)
+ * followed by splat_projected (render_loss/image.rs:18-79), once per view: image v is the
+ * isotropic projected splat of all count particles seen through views[v] (NPA_VIEW_*, a
+ * HOST array of nviews <= 16 entries). colors[count][3], opacities[count], sigmas[count]
+ * (pixels; clamped to [min_sigma, max_sigma] by the splat). images[nviews][size][size][5]
+ * holds RenderedPixel (image.rs:4-9): r, g, b, alpha, depth_sum; it is overwritten. Each
+ * pixel sums particles in ascending index order, as the reference does. */
+npa_status npa_render_views(npa_context* ctx, const float* positions, const float* colors,
+                            const float* opacities, const float* sigmas, uint32_t count,
+                            const uint32_t* views, uint32_t nviews, const npa_render_cfg* cfg,
+                            float* images);
+
+/* Replaces state_tail_render_attributes (render_loss/attributes.rs:15-87): per particle
+ * colors[count][3] = clamp(tail + 0.5, 0, 1), opacities[count] (sigmoid of the material
+ * opacity channel plus opacity_logit_bias, clamped to [0.001, 0.95]), sigmas[count] by the
+ * decode mode, and scale_logit_derivatives[count] (may be NULL). */
+npa_status npa_render_attributes(npa_context* ctx, const float* states, uint32_t count,
+                                 uint32_t state_dims, const npa_render_cfg* cfg, float* colors,
+                                 float* opacities, float* sigmas,
+                                 float* scale_logit_derivatives);
+
 /* ----------------------------------- device-resident executor (L2 twin) */
 /* Replaces WgpuAutomataExecutor::create_state_with_update_prob
  * (crates/burn_automata/src/gpu/executor/state.rs:82-111). positions/states/weights
@@ -281,6 +323,12 @@ npa_status npa_state_splat_2d(npa_state* state, const npa_splat2d_cfg* cfg, floa
  * npa_state_splat_2d. */
 npa_status npa_state_splat_2d_tiled(npa_state* state, const npa_splat2d_cfg* cfg, uint32_t tiles_x,
                                     float* image);
+/* The particle images of mesh_multiview_render_loss_from_trace
+ * (crates/burn_automata/src/render_loss.rs:107-141) for the current particles: the render
+ * attributes of the current states (npa_render_attributes), then npa_render_views. The
+ * reference renders batch-1 traces only (validate_render_trace, attributes.rs:89-112). */
+npa_status npa_state_render_views(npa_state* state, const uint32_t* views, uint32_t nviews,
+                                  const npa_render_cfg* cfg, float* images);
 /* decode_gaussians_3d of the current particles (the planar export the viewer reads,
  * cf. write_gaussian_main gpu_step.wgsl:4929-5052). */
 npa_status npa_state_decode_gaussians_3d(npa_state* state, const npa_gaussian_decode_cfg* cfg,
@@ -344,7 +392,8 @@ enum {
     NPA_KERNEL_MLP = 7,        /* update MLP + masked Euler */
     NPA_KERNEL_SPLIT = 8,      /* per-bin split by true cell + sorted payload + work items + update-mask targets */
     NPA_KERNEL_ACTIVE = 9,     /* reserved: the split kernel (8) now selects the update-mask targets */
-    NPA_KERNEL_COUNT = 10
+    NPA_KERNEL_RENDER = 10,    /* the whole projected 3D render pipeline (npa_render_views) */
+    NPA_KERNEL_COUNT = 11
 };
 /* kernel_mask selects kernels by bit (1 << NPA_KERNEL_*; 0 = off, -1 = all). The
  * library then brackets each launch of a selected kernel with HIP events on the

@@ -1241,3 +1241,160 @@ int oracle_splat_particles_2d(const float* positions, const float* colors, uint3
     free(xbuf);
     return NPA_OK;
 }
+
+/* ------------------------------------------------------------ 3D render raster
+ * crates/burn_automata/src/render_loss/{math,projection,attributes,image}.rs */
+#define RENDER_EPS 1.0e-8f
+
+static float render_dot3(const float* p4, const float* r3) { /* math.rs:20-22 */
+    return p4[0] * r3[0] + p4[1] * r3[1] + p4[2] * r3[2];
+}
+
+static void render_normalize3(const float v[3], float out[3]) { /* math.rs:32-39 */
+    float norm = sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+    if (norm <= RENDER_EPS) {
+        out[0] = 0.0f;
+        out[1] = 0.0f;
+        out[2] = 1.0f;
+        return;
+    }
+    out[0] = v[0] / norm;
+    out[1] = v[1] / norm;
+    out[2] = v[2] / norm;
+}
+
+static float render_sigmoid(float v) { /* math.rs:11-18 */
+    if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
+    float e = expf(v);
+    return e / (1.0f + e);
+}
+
+/* view_basis (projection.rs:31-43); cross3 as math.rs:24-30. */
+int oracle_view_basis(uint32_t view, float right[3], float up[3], float forward[3]) {
+    static const float I[3][3] = {{1.0f, 0.0f, 0.0f}, {0.0f, 1.0f, 0.0f}, {0.0f, 0.0f, 1.0f}};
+    const float* r;
+    const float* u;
+    const float* f;
+    switch (view) {
+        case NPA_VIEW_XY: r = I[0], u = I[1], f = I[2]; break;
+        case NPA_VIEW_XZ: r = I[0], u = I[2], f = I[1]; break;
+        case NPA_VIEW_YZ: r = I[1], u = I[2], f = I[0]; break;
+        case NPA_VIEW_ISO: {
+            const float a[3] = {1.0f, -1.0f, 0.0f}, b[3] = {1.0f, 1.0f, 2.0f};
+            render_normalize3(a, right);
+            render_normalize3(b, up);
+            const float c[3] = {right[1] * up[2] - right[2] * up[1], right[2] * up[0] - right[0] * up[2],
+                                right[0] * up[1] - right[1] * up[0]};
+            render_normalize3(c, forward);
+            return NPA_OK;
+        }
+        default: return NPA_ERR_INVALID_ARGUMENT;
+    }
+    memcpy(right, r, 12);
+    memcpy(up, u, 12);
+    memcpy(forward, f, 12);
+    return NPA_OK;
+}
+
+/* project_positions (projection.rs:11-29): out[count][3] = (x, y, depth). */
+int oracle_project_positions(uint32_t view, const float* positions, uint32_t count, float world_scale,
+                             float* out) {
+    float right[3], up[3], fwd[3];
+    int st = oracle_view_basis(view, right, up, fwd);
+    if (st) return st;
+    for (uint64_t n = 0; n < count; ++n) {
+        const float* p = positions + 4 * n;
+        float depth = clamp_f32(0.5f + 0.5f * render_dot3(p, fwd) / fmaxf(world_scale, RENDER_EPS), 0.0f, 1.0f);
+        out[3 * n] = render_dot3(p, right);
+        out[3 * n + 1] = render_dot3(p, up);
+        out[3 * n + 2] = depth;
+    }
+    return NPA_OK;
+}
+
+/* splat_projected (image.rs:18-79): image[size*size][5] = (r, g, b, alpha, depth_sum). */
+int oracle_splat_projected(const float* projected, const float* colors, const float* opacities,
+                           const float* sigmas, uint32_t count, const npa_render_cfg* cfg, float* image) {
+    const int64_t size = cfg->image_size;
+    memset(image, 0, (size_t)(size * size * 5) * sizeof(float));
+    const float norm_scale = 1.0f / (float)(count > 1 ? count : 1);
+    const float ws = cfg->world_scale;
+    /* the largest footprint any particle can have: sigma <= max(max_sigma, EPS) */
+    const int64_t rmax = f32_to_isize(fmaxf(ceilf(5.0f * fmaxf(cfg->max_sigma, RENDER_EPS)), 1.0f));
+    const int64_t side = 2 * rmax + 1;
+    float* wbuf = (float*)malloc((size_t)(side * side) * sizeof(float));
+    int64_t* xbuf = (int64_t*)malloc((size_t)(side * side) * sizeof(int64_t));
+    if (!wbuf || !xbuf) {
+        free(wbuf);
+        free(xbuf);
+        return NPA_ERR_OUT_OF_MEMORY;
+    }
+    for (uint64_t n = 0; n < count; ++n) {
+        const float* pp = projected + 3 * n;
+        const float* color = colors + 3 * n;
+        float sigma = fmaxf(clamp_f32(sigmas[n], cfg->min_sigma, cfg->max_sigma), RENDER_EPS);
+        float sigma2 = sigma * sigma;
+        int64_t radius = f32_to_isize(fmaxf(ceilf(5.0f * sigma), 1.0f));
+        float px = (pp[0] + ws) / (2.0f * ws) * ((float)size - 1.0f);
+        float py = (ws - pp[1]) / (2.0f * ws) * ((float)size - 1.0f);
+        int64_t bx = f32_to_isize(floorf(px)), by = f32_to_isize(floorf(py));
+        float fx = px - (float)bx, fy = py - (float)by;
+        size_t nw = 0;
+        float weight_sum = 0.0f;
+        for (int64_t oy = -radius; oy <= radius; ++oy)
+            for (int64_t ox = -radius; ox <= radius; ++ox) {
+                int64_t x = bx + ox, y = by + oy;
+                if (x < 0 || y < 0 || x >= size || y >= size) continue;
+                float dx = (float)ox - fx, dy = (float)oy - fy;
+                float w = expf(-(dx * dx + dy * dy) / (2.0f * sigma2));
+                wbuf[nw] = w;
+                xbuf[nw] = y * size + x;
+                ++nw;
+                weight_sum += w;
+            }
+        float denom = fmaxf(weight_sum, RENDER_EPS);
+        float opacity = clamp_f32(opacities[n], 0.0f, 1.0f);
+        for (size_t k = 0; k < nw; ++k) {
+            float w = wbuf[k] / denom * norm_scale * opacity;
+            float* px5 = image + 5 * xbuf[k];
+            px5[0] += color[0] * w;
+            px5[1] += color[1] * w;
+            px5[2] += color[2] * w;
+            px5[3] += w;
+            px5[4] += pp[2] * w;
+        }
+    }
+    free(wbuf);
+    free(xbuf);
+    return NPA_OK;
+}
+
+/* state_tail_render_attributes (attributes.rs:15-87) with growth_3d_material_opacity_channel
+ * (crates/burn_automata/src/rollout/mod.rs:37-45: channel 8 when S > 8, else 3 when S > 3). */
+int oracle_render_attributes(const float* states, uint32_t count, uint32_t state_dims, const npa_render_cfg* cfg,
+                             float* colors, float* opacities, float* sigmas, float* derivatives) {
+    if (state_dims < 3) return NPA_ERR_INVALID_ARGUMENT;
+    if (cfg->gaussian_decode_mode == NPA_DECODE_SH0_LEARNED_SCALE && state_dims < 5) return NPA_ERR_INVALID_ARGUMENT;
+    const uint32_t S = state_dims, tail = S - 3;
+    const int opacity_ch = S > 8 ? 8 : (S > 3 ? 3 : -1);
+    for (uint64_t i = 0; i < count; ++i) {
+        const float* s = states + i * S;
+        for (int k = 0; k < 3; ++k) colors[3 * i + k] = clamp_f32(s[tail + k] + 0.5f, 0.0f, 1.0f);
+        opacities[i] = opacity_ch >= 0 ? clamp_f32(render_sigmoid(s[opacity_ch] + cfg->opacity_logit_bias), 0.001f, 0.95f)
+                                       : 0.95f;
+        float sigma, derivative = 0.0f;
+        switch (cfg->gaussian_decode_mode) {
+            case NPA_DECODE_PARTICLE_POINT: sigma = fmaxf(cfg->min_sigma, RENDER_EPS); break;
+            case NPA_DECODE_SH0_LEARNED_SCALE: {
+                float logit = clamp_f32(s[S - 5], -8.0f, 8.0f);
+                float raw = cfg->sigma * expf(logit);
+                sigma = clamp_f32(raw, cfg->min_sigma, cfg->max_sigma);
+                derivative = (raw > cfg->min_sigma && raw < cfg->max_sigma) ? raw : 0.0f;
+            } break;
+            default: sigma = clamp_f32(cfg->sigma, cfg->min_sigma, cfg->max_sigma); break;
+        }
+        sigmas[i] = sigma;
+        if (derivatives) derivatives[i] = derivative;
+    }
+    return NPA_OK;
+}

@@ -25,6 +25,12 @@
  *   decode_gaussians_3d       - reference tests splat_and_gaussian_decode_are_shape_stable,
  *                               gaussian_decode_modes_cover_fixed_learned_and_oriented_scale
  *   splat_particles_2d        - closed-form single-particle Gaussian, additivity
+ *   view_basis / project_positions / splat_projected / render attributes
+ *                             - orthonormal right-handed bases, axis views by coordinate
+ *                               permutation, single-particle moments (total alpha = opacity,
+ *                               centroid = projected pixel, second moment = sigma^2,
+ *                               depth_sum / alpha = depth), sigmoid against scipy's expit,
+ *                               reference test constants (RENDER_MIN/MAX_OPACITY, defaults)
  */
 #ifndef NPA_ORACLE_H
 #define NPA_ORACLE_H
@@ -116,6 +122,17 @@ int oracle_decode_gaussians_3d(const float* positions, const float* states, uint
 
 int oracle_splat_particles_2d(const float* positions, const float* colors, uint32_t count,
                               const npa_splat2d_cfg* cfg, float* image);
+
+/* 3D render raster (crates/burn_automata/src/render_loss/): view_basis, project_positions
+ * (projected[count][3] = x, y, depth), splat_projected (image[size*size][5] = r, g, b, alpha,
+ * depth_sum) and state_tail_render_attributes (derivatives may be NULL). */
+int oracle_view_basis(uint32_t view, float right[3], float up[3], float forward[3]);
+int oracle_project_positions(uint32_t view, const float* positions, uint32_t count, float world_scale,
+                             float* projected);
+int oracle_splat_projected(const float* projected, const float* colors, const float* opacities,
+                           const float* sigmas, uint32_t count, const npa_render_cfg* cfg, float* image);
+int oracle_render_attributes(const float* states, uint32_t count, uint32_t state_dims, const npa_render_cfg* cfg,
+                             float* colors, float* opacities, float* sigmas, float* derivatives);
 
 /* Per-phase wall-clock seconds of the last oracle_step / oracle_rollout call
  * (hashgrid+perceive, MLP+gates+integrate, 0), following profile_rollout

@@ -19,7 +19,7 @@ import numpy as np
 
 from burn_automata_amd import _abi
 from burn_automata_amd.config import (GaussianDecodeConfig, HashGridConfig, NpaConfig,
-                                      PerceptionOptions, Splat2dConfig)
+                                      PerceptionOptions, RenderLossConfig, Splat2dConfig)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 # NPA_ORACLE_LIB points the loader at another build of the oracle; tests/test_oracle_mutants.py
@@ -91,6 +91,10 @@ def _declare(L):
     L.oracle_decode_gaussians_3d.argtypes = [P, P, u32, u32,
                                              C.POINTER(_abi.NpaGaussianDecodeCfg), P, P, P, P]
     L.oracle_splat_particles_2d.argtypes = [P, P, u32, C.POINTER(_abi.NpaSplat2dCfg), P]
+    L.oracle_view_basis.argtypes = [u32, P, P, P]
+    L.oracle_project_positions.argtypes = [u32, P, u32, f32, P]
+    L.oracle_splat_projected.argtypes = [P, P, P, P, u32, C.POINTER(_abi.NpaRenderCfg), P]
+    L.oracle_render_attributes.argtypes = [P, u32, u32, C.POINTER(_abi.NpaRenderCfg), P, P, P, P]
     L.oracle_last_phase_seconds.argtypes = [C.POINTER(C.c_double)] * 3
     L.oracle_max_threads.restype = C.c_int
     L.oracle_set_threads.argtypes = [C.c_int]
@@ -382,6 +386,50 @@ def splat_particles_2d(positions, colors, cfg: Splat2dConfig) -> np.ndarray:
     _check(lib().oracle_splat_particles_2d(_ptr(pos), _ptr(col), pos.shape[0],
                                            C.byref(cfg.to_c()), _ptr(img)))
     return img
+
+
+def view_basis(view):
+    """view_basis (crates/burn_automata/src/render_loss/projection.rs:31-43): (right, up, forward)."""
+    r, u, f = (np.zeros(3, np.float32) for _ in range(3))
+    _check(lib().oracle_view_basis(int(view), _ptr(r), _ptr(u), _ptr(f)))
+    return r, u, f
+
+
+def project_positions(view, positions, world_scale: float) -> np.ndarray:
+    """project_positions (projection.rs:11-29): [n, 3] = (x, y, depth)."""
+    pos = _f32(positions, (-1, 4))
+    out = np.zeros((pos.shape[0], 3), np.float32)
+    _check(lib().oracle_project_positions(int(view), _ptr(pos), pos.shape[0], world_scale, _ptr(out)))
+    return out
+
+
+def splat_projected(projected, colors, opacities, sigmas, cfg: RenderLossConfig) -> np.ndarray:
+    """splat_projected (crates/burn_automata/src/render_loss/image.rs:18-79): [size*size, 5]."""
+    pp = _f32(projected, (-1, 3))
+    n = pp.shape[0]
+    col, op, sg = _f32(colors, (n, 3)), _f32(opacities, (n,)), _f32(sigmas, (n,))
+    img = np.zeros((cfg.image_size * cfg.image_size, 5), np.float32)
+    _check(lib().oracle_splat_projected(_ptr(pp), _ptr(col), _ptr(op), _ptr(sg), n,
+                                        C.byref(cfg.to_c()), _ptr(img)))
+    return img
+
+
+def render_views(positions, colors, opacities, sigmas, views, cfg: RenderLossConfig) -> np.ndarray:
+    """project_positions + splat_projected per view (render_loss.rs:314-335): [views, size*size, 5]."""
+    return np.stack([splat_projected(project_positions(v, positions, cfg.world_scale), colors,
+                                     opacities, sigmas, cfg) for v in views])
+
+
+def render_attributes(states, state_dims: int, cfg: RenderLossConfig):
+    """state_tail_render_attributes (render_loss/attributes.rs:15-87):
+    (colors [n, 3], opacities [n], sigmas [n], scale_logit_derivatives [n])."""
+    st = _f32(states).reshape(-1)
+    n = st.size // state_dims
+    col = np.zeros((n, 3), np.float32)
+    op, sg, dv = (np.zeros(n, np.float32) for _ in range(3))
+    _check(lib().oracle_render_attributes(_ptr(st), n, state_dims, C.byref(cfg.to_c()), _ptr(col),
+                                          _ptr(op), _ptr(sg), _ptr(dv)))
+    return col, op, sg, dv
 
 
 def tail_colors(states, state_dims: int) -> np.ndarray:

@@ -742,6 +742,26 @@ def test_fixed_decode_closed_form():
     assert np.all(g["rotation"] == np.array([1, 0, 0, 0], f32))
 
 
+def test_learned_decode_closed_form():
+    """GaussianSh0LearnedScale (gaussian.rs:172-184): scale = clamp(sigma exp(clamp(s[S-5], +-8)),
+    min, max) on three axes; opacity = clamp(clamp(sigmoid(clamp(s[S-4], +-12)), min, max) *
+    opacity_scale, min, max)."""
+    from scipy.special import expit
+    rng = np.random.default_rng(4)
+    n, S = 300, 10
+    st = rng.normal(0, 3, (n, S)).astype(f32)
+    cfg = GaussianDecodeConfig(mode=GaussianDecodeMode.GaussianSh0LearnedScale, sigma=0.02,
+                               min_scale=0.005, max_scale=0.2, opacity_scale=0.8)
+    g = O.decode_gaussians_3d(np.zeros((n, 4), f32), st, S, cfg)
+    sc = np.clip(0.02 * np.exp(np.clip(st[:, S - 5].astype(np.float64), -8, 8)), 0.005, 0.2)
+    op = np.clip(np.clip(expit(np.clip(st[:, S - 4].astype(np.float64), -12, 12)), 0.001, 0.95) * 0.8,
+                 0.001, 0.95)
+    for k in range(3):
+        np.testing.assert_allclose(g["scale_opacity"][:, k], sc, rtol=2e-6)
+    np.testing.assert_allclose(g["scale_opacity"][:, 3], op, rtol=2e-6)
+    assert ((sc > 0.005) & (sc < 0.2)).sum() > n // 4
+
+
 # --------------------------------------------------------------------------------------------
 # splat
 # --------------------------------------------------------------------------------------------
@@ -825,3 +845,181 @@ def test_sampled_rows_equal_the_full_pass(name, particles):
                        1.0, mask, full.density, sel)
     np.testing.assert_array_equal(p, full.next_positions[sel])
     np.testing.assert_array_equal(s, full.next_states[sel])
+
+
+# ------------------------------------------------------------------ 3D render raster
+def _moments(img, size):
+    """Total alpha, alpha-weighted centroid (column, row) and per-axis variance of one image."""
+    a = img[:, 3].astype(np.float64).reshape(size, size)
+    ys, xs = np.mgrid[0:size, 0:size]
+    tot = a.sum()
+    cx, cy = (a * xs).sum() / tot, (a * ys).sum() / tot
+    vx, vy = (a * (xs - cx) ** 2).sum() / tot, (a * (ys - cy) ** 2).sum() / tot
+    return tot, cx, cy, vx, vy
+
+
+def test_view_bases_are_right_handed_orthonormal_frames():
+    """view_basis (render_loss/projection.rs:31-43): the axis views pick coordinate axes; the
+    iso view looks along (right x up) with right = (1,-1,0)/sqrt2 and up = (1,1,2)/sqrt6."""
+    from burn_automata_amd.config import RenderViewPreset as V
+    e = np.eye(3, dtype=f32)
+    for v, (r, u, fw) in {V.Xy: (0, 1, 2), V.Xz: (0, 2, 1), V.Yz: (1, 2, 0)}.items():
+        got = O.view_basis(v)
+        for g, k in zip(got, (r, u, fw)):
+            np.testing.assert_array_equal(g, e[k])
+    r, u, fw = (b.astype(np.float64) for b in O.view_basis(V.Iso))
+    np.testing.assert_allclose(r, np.array([1, -1, 0]) / math.sqrt(2), rtol=0, atol=1e-7)
+    np.testing.assert_allclose(u, np.array([1, 1, 2]) / math.sqrt(6), rtol=0, atol=1e-7)
+    np.testing.assert_allclose(fw, np.array([-1, -1, 1]) / math.sqrt(3), rtol=0, atol=1e-7)
+    m = np.stack([r, u, fw])
+    np.testing.assert_allclose(m @ m.T, np.eye(3), atol=1e-6)
+    assert np.linalg.det(m) == pytest.approx(1.0, abs=1e-6)
+
+
+def test_project_positions_is_a_rotation_with_clamped_depth():
+    """project_positions (projection.rs:11-29): (x, y) = coordinates along right and up; depth
+    = clamp(0.5 + 0.5 forward.p / world_scale, 0, 1); the position's w is ignored."""
+    from burn_automata_amd.config import ALL_VIEWS
+    rng = np.random.default_rng(11)
+    pos = rng.uniform(-2, 2, (500, 4)).astype(f32)
+    ws = 1.25
+    for v in ALL_VIEWS:
+        r, u, fw = (b.astype(np.float64) for b in O.view_basis(v))
+        pp = O.project_positions(v, pos, ws).astype(np.float64)
+        p3 = pos[:, :3].astype(np.float64)
+        np.testing.assert_allclose(pp[:, 0], p3 @ r, atol=2e-6)
+        np.testing.assert_allclose(pp[:, 1], p3 @ u, atol=2e-6)
+        np.testing.assert_allclose(pp[:, 2], np.clip(0.5 + 0.5 * (p3 @ fw) / ws, 0, 1), atol=2e-6)
+        # a rotation keeps lengths: x^2 + y^2 + (forward.p)^2 = |p|^2
+        np.testing.assert_allclose(pp[:, 0] ** 2 + pp[:, 1] ** 2 + (p3 @ fw) ** 2,
+                                   (p3 ** 2).sum(1), rtol=1e-5)
+    pos2 = pos.copy()
+    pos2[:, 3] = 123.0
+    np.testing.assert_array_equal(O.project_positions(3, pos2, ws), O.project_positions(3, pos, ws))
+
+
+@pytest.mark.parametrize("sigma", [0.9, 2.5, 4.2])
+def test_projected_splat_of_one_particle_has_the_gaussian_moments(sigma):
+    """splat_projected (render_loss/image.rs:18-79) of one particle well inside the image: total
+    alpha = opacity, colour and depth_sum = colour and depth times alpha, centroid = the projected
+    pixel ((x+ws)/2ws (size-1), (ws-y)/2ws (size-1)), per-axis variance sigma^2, support radius
+    ceil(5 sigma)."""
+    from burn_automata_amd.config import RenderLossConfig
+    size, ws = 64, 1.25
+    cfg = RenderLossConfig(image_size=size, world_scale=ws)
+    x, y, depth, op = 0.213, -0.161, 0.37, 0.64
+    col = np.array([[0.2, 0.7, 1.0]], f32)
+    img = O.splat_projected(np.array([[x, y, depth]], f32), col, np.array([op], f32),
+                            np.array([sigma], f32), cfg)
+    tot, cx, cy, vx, vy = _moments(img, size)
+    assert tot == pytest.approx(op, rel=1e-5)
+    np.testing.assert_allclose(img[:, :3].sum(0), col[0] * op, rtol=1e-5)
+    assert img[:, 4].sum() == pytest.approx(depth * op, rel=1e-5)
+    assert cx == pytest.approx((x + ws) / (2 * ws) * (size - 1), abs=1e-3)
+    assert cy == pytest.approx((ws - y) / (2 * ws) * (size - 1), abs=1e-3)
+    assert vx == pytest.approx(sigma ** 2, rel=2e-3) and vy == pytest.approx(sigma ** 2, rel=2e-3)
+    a = img[:, 3].reshape(size, size)
+    cols = np.nonzero(a.any(0))[0]
+    bx = math.floor((x + ws) / (2 * ws) * (size - 1))
+    rad = math.ceil(5 * sigma)
+    assert cols.min() == bx - rad and cols.max() == bx + rad
+
+
+def test_projected_splat_clamps_sigma_and_opacity_and_divides_by_count():
+    """sigma is clamped to [min_sigma, max_sigma], opacity to [0, 1]; every particle's weights
+    carry 1/count (image.rs:29, 39, 69-71); edge particles renormalise over in-bounds pixels."""
+    from burn_automata_amd.config import RenderLossConfig
+    size = 64
+    cfg = RenderLossConfig(image_size=size, min_sigma=1.5, max_sigma=3.0)
+    pp = np.array([[0.0, 0.0, 0.5]], f32)
+    col = np.ones((1, 3), f32)
+    for s, want in ((0.2, 1.5), (2.0, 2.0), (9.0, 3.0)):
+        _, _, _, vx, _ = _moments(O.splat_projected(pp, col, np.ones(1, f32), np.array([s], f32), cfg), size)
+        assert vx == pytest.approx(want ** 2, rel=2e-3), s
+    assert O.splat_projected(pp, col, np.array([1.7], f32), np.array([2.0], f32), cfg)[:, 3].sum() == \
+        pytest.approx(1.0, rel=1e-5)
+    assert not O.splat_projected(pp, col, np.array([-0.3], f32), np.array([2.0], f32), cfg).any()
+    # two copies of one particle draw the single particle's image (each at weight 1/2)
+    one = O.splat_projected(pp, col, np.ones(1, f32), np.array([2.0], f32), cfg)
+    two = O.splat_projected(np.repeat(pp, 2, 0), np.repeat(col, 2, 0), np.ones(2, f32),
+                            np.full(2, 2.0, f32), cfg)
+    assert rel(two, one) < 1e-6
+    # a particle at the image corner keeps its full alpha on the pixels that remain
+    corner = O.splat_projected(np.array([[1.25, 1.25, 0.5]], f32), col, np.ones(1, f32),
+                               np.array([2.5], f32), cfg)
+    assert corner[:, 3].sum() == pytest.approx(1.0, rel=1e-5)
+    assert corner[:, 3].reshape(size, size)[0, size - 1] == corner[:, 3].max()
+    far = O.splat_projected(np.array([[9.0, 0.0, 0.5]], f32), col, np.ones(1, f32), np.array([2.5], f32), cfg)
+    assert not far.any()
+
+
+def test_projected_splat_is_linear_in_the_particle_sets():
+    from burn_automata_amd.config import RenderLossConfig
+    rng = np.random.default_rng(12)
+    n = 400
+    pp = np.concatenate([rng.uniform(-1.4, 1.4, (n, 2)), rng.uniform(0, 1, (n, 1))], 1).astype(f32)
+    col, op = rng.uniform(0, 1, (n, 3)).astype(f32), rng.uniform(0, 1, n).astype(f32)
+    sg = rng.uniform(0.5, 6, n).astype(f32)
+    cfg = RenderLossConfig(image_size=48)
+    a = O.splat_projected(pp[:100], col[:100], op[:100], sg[:100], cfg).astype(np.float64)
+    b = O.splat_projected(pp[100:], col[100:], op[100:], sg[100:], cfg).astype(np.float64)
+    ab = O.splat_projected(pp, col, op, sg, cfg)
+    assert rel(ab, (100 * a + 300 * b) / 400) < 1e-5
+
+
+def test_render_attributes_follow_the_state_tail():
+    """state_tail_render_attributes (render_loss/attributes.rs:15-87): colour = clamp(tail+0.5),
+    opacity = clamp(sigmoid(state[8 if S > 8 else 3] + bias), 0.001, 0.95) (0.95 when S <= 3;
+    rollout/mod.rs:37-45), sigma by decode mode, learned logit from state[S-5] clamped to +-8."""
+    from scipy.special import expit
+    from burn_automata_amd.config import RenderLossConfig
+    rng = np.random.default_rng(13)
+    n = 300
+    for S, ch in ((16, 8), (9, 8), (8, 3), (5, 3), (4, 3), (3, None)):
+        st = rng.normal(0, 3, (n, S)).astype(f32)
+        cfg = RenderLossConfig(opacity_logit_bias=0.7)
+        col, op, sg, dv = O.render_attributes(st, S, cfg)
+        np.testing.assert_array_equal(col, np.clip(st[:, S - 3:] + f32(0.5), 0, 1))
+        if ch is None:
+            np.testing.assert_array_equal(op, np.full(n, 0.95, f32))
+        else:
+            want = np.clip(expit(st[:, ch].astype(np.float64) + np.float64(f32(0.7))), 0.001, 0.95)
+            np.testing.assert_allclose(op, want, rtol=2e-6)
+            other = st.copy()
+            other[:, [c for c in range(S) if c != ch]] = 0
+            np.testing.assert_array_equal(O.render_attributes(other, S, cfg)[1], op)
+        np.testing.assert_array_equal(sg, np.full(n, 2.5, f32))
+        assert not dv.any()
+    S = 16
+    st = rng.normal(0, 4, (n, S)).astype(f32)
+    cfg = RenderLossConfig(gaussian_decode_mode=GaussianDecodeMode.GaussianSh0LearnedScale, sigma=2.0,
+                           min_sigma=0.5, max_sigma=6.0)
+    _, _, sg, dv = O.render_attributes(st, S, cfg)
+    raw = 2.0 * np.exp(np.clip(st[:, S - 5].astype(np.float64), -8, 8))
+    np.testing.assert_allclose(sg, np.clip(raw, 0.5, 6.0), rtol=2e-6)
+    inside = (raw > 0.5) & (raw < 6.0)
+    np.testing.assert_allclose(dv[inside], raw[inside], rtol=2e-6)
+    assert not dv[~inside].any() and inside.any() and (~inside).any()
+    _, _, sg, _ = O.render_attributes(st, S, cfg.replace(gaussian_decode_mode=GaussianDecodeMode.ParticlePoint))
+    np.testing.assert_array_equal(sg, np.full(n, 0.5, f32))
+    _, _, sg, _ = O.render_attributes(st, S, cfg.replace(gaussian_decode_mode=GaussianDecodeMode.GaussianSh0Oriented,
+                                                          sigma=9.0))
+    np.testing.assert_array_equal(sg, np.full(n, 6.0, f32))
+    from burn_automata_amd import _abi
+    with pytest.raises(_abi.InvalidArgument):
+        O.render_attributes(np.zeros((4, 2), f32), 2, RenderLossConfig())
+    with pytest.raises(_abi.InvalidArgument):
+        O.render_attributes(np.zeros((4, 4), f32), 4, cfg)
+
+
+def test_render_defaults_match_the_reference():
+    """RenderLossConfig::default (render_loss.rs:48-63) and the opacity limits (render_loss.rs:21-23)."""
+    from burn_automata_amd.config import RenderLossConfig
+    c = RenderLossConfig()
+    assert (c.image_size, c.sigma, c.min_sigma, c.max_sigma, c.world_scale, c.target_samples) == \
+        (64, 2.5, 0.75, 5.0, 1.25, 8192)
+    assert c.gaussian_decode_mode == GaussianDecodeMode.GaussianSh0FixedScale
+    st = np.zeros((2, 16), f32)
+    st[0, 8], st[1, 8] = 40.0, -40.0
+    _, op, _, _ = O.render_attributes(st, 16, c)
+    np.testing.assert_array_equal(op, np.array([0.95, 0.001], f32))

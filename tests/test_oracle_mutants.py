@@ -47,6 +47,23 @@ MUTANTS = {
     "mask_hash_multiplier": ("x = x * 0x27d4eb2du;", "x = x * 0x27d4eb2fu;"),
     "decode_colour_offset": ("clamp_f32(s[base + ch] + 0.5f, 0.0f, 1.0f);", "clamp_f32(s[base + ch] + 0.4f, 0.0f, 1.0f);"),
     "splat_radius": ("ceilf(5.0f * sigma)", "ceilf(3.0f * sigma)"),
+    "iso_up": ("b[3] = {1.0f, 1.0f, 2.0f}", "b[3] = {1.0f, 1.0f, 1.0f}"),
+    "xz_swapped": ("case NPA_VIEW_XZ: r = I[0], u = I[2], f = I[1];", "case NPA_VIEW_XZ: r = I[0], u = I[1], f = I[2];"),
+    "depth_unhalved": ("0.5f + 0.5f * render_dot3(p, fwd)", "0.5f + render_dot3(p, fwd)"),
+    "render_y_not_flipped": ("float py = (ws - pp[1])", "float py = (ws + pp[1])"),
+    "render_sigma2": ("/ (2.0f * sigma2));", "/ sigma2);"),
+    "render_radius": ("fmaxf(ceilf(5.0f * sigma), 1.0f)", "fmaxf(ceilf(4.0f * sigma), 1.0f)"),
+    "render_count_norm": ("const float norm_scale = 1.0f / (float)(count > 1 ? count : 1);",
+                          "const float norm_scale = 1.0f;"),
+    "render_opacity_dropped": ("wbuf[k] / denom * norm_scale * opacity;", "wbuf[k] / denom * norm_scale;"),
+    "render_depth_channel": ("px5[4] += pp[2] * w;", "px5[4] += pp[1] * w;"),
+    "render_sigma_unclamped": ("fmaxf(clamp_f32(sigmas[n], cfg->min_sigma, cfg->max_sigma), RENDER_EPS)",
+                               "fmaxf(sigmas[n], RENDER_EPS)"),
+    "opacity_channel": ("S > 8 ? 8 : (S > 3 ? 3 : -1)", "S > 8 ? 7 : (S > 3 ? 3 : -1)"),
+    "sigmoid_sign": ("return 1.0f / (1.0f + expf(-v));", "return 1.0f / (1.0f + expf(v));"),
+    "render_learned_channel": ("float logit = clamp_f32(s[S - 5]", "float logit = clamp_f32(s[S - 4]"),
+    "decode_learned_channel": ("float scale_logit = clamp_f32(s[S - 5]", "float scale_logit = clamp_f32(s[S - 6]"),
+    "decode_opacity_channel": ("float opacity_logit = clamp_f32(s[S - 4]", "float opacity_logit = clamp_f32(s[S - 5]"),
 }
 
 
