@@ -14,6 +14,9 @@ Prints ONE JSON line with the driver's fields plus:
   roofline_hbm  - the same kernel against the HBM roofline, as BASELINE.json asks;
   cpu_baseline  - the CPU oracle (C restatement of the reference CPU path) timed on
                   a bounded sample of the same workload on this host's cores.
+
+--workload c3 / c4 / c5 time BASELINE's other rollout workloads the same way; --workload render
+times the projected 3D render of a device-resident C4 state (particle-views/s, see bench_render).
 """
 from __future__ import annotations
 
@@ -120,6 +123,122 @@ def cpu_baseline(w, budget_s: float):
     }
 
 
+RENDER_FLOPS_PER_PIXEL = 29  # per footprint pixel of one particle in one view; see render_work
+
+
+def render_work(positions, sigmas, views, cfg):
+    """Footprint pixels of the projected render (render_loss/image.rs:18-79): for each particle
+    and view, the in-bounds part of its (2 ceil(5 sigma) + 1)^2 window. Each footprint pixel costs
+    the splat 29 fp32 operations, an exp counted as one: 8 for the weight sum of the first pass
+    (dx, dy, dx^2 + dy^2, / 2 sigma^2, exp, sum) and 21 for the accumulation (the same 7, w / denom
+    * norm * opacity, 5 multiply-adds into r, g, b, alpha, depth)."""
+    import numpy as np
+
+    p = np.asarray(positions, np.float64)[:, :3]
+    s = np.clip(np.asarray(sigmas, np.float64), cfg.min_sigma, cfg.max_sigma)
+    r = np.maximum(np.ceil(5.0 * s), 1.0)
+    size, ws = cfg.image_size, cfg.world_scale
+    bases = {0: ((1, 0, 0), (0, 1, 0)), 1: ((1, 0, 0), (0, 0, 1)), 2: ((0, 1, 0), (0, 0, 1)),
+             3: (np.array([1, -1, 0]) / np.sqrt(2), np.array([1, 1, 2]) / np.sqrt(6))}
+    total = 0.0
+    for v in views:
+        right, up = (np.asarray(b, np.float64) for b in bases[int(v)])
+        px = (p @ right + ws) / (2 * ws) * (size - 1)
+        py = (ws - p @ up) / (2 * ws) * (size - 1)
+        bx, by = np.floor(px), np.floor(py)
+        wx = np.clip(np.minimum(bx + r, size - 1) - np.maximum(bx - r, 0) + 1, 0, None)
+        wy = np.clip(np.minimum(by + r, size - 1) - np.maximum(by - r, 0) + 1, 0, None)
+        total += float((wx * wy).sum())
+    return total
+
+
+def bench_render(args, torch) -> int:
+    """The projected 3D render of a device-resident state: the particle images of
+    mesh_multiview_render_loss_from_trace (render_loss.rs:107-141) - render attributes from the
+    states, then project_positions + splat_projected for the four views - on C4's 16,384 surface
+    particles (S = 16) at the reference's RenderLossConfig defaults (64x64, sigma 2.5 px)."""
+    import ctypes as C
+
+    from burn_automata_amd import synthetic as syn
+    from burn_automata_amd._lib import lib
+    from burn_automata_amd.config import ALL_VIEWS, RenderLossConfig
+    from burn_automata_amd.executor import HipAutomataExecutor
+    from burn_automata_amd.model import NpaModel
+
+    w = syn.workload("c4", particles=args.particles)
+    cfg = RenderLossConfig(image_size=args.image_size)
+    ex = HipAutomataExecutor()
+    ctx = ex.ctx
+    n = w["n"]
+    state = ex.create_state(NpaModel(w["model"], w["weights"]), torch.from_numpy(w["positions"]).cuda(),
+                            torch.from_numpy(w["states"]).cuda(), 1, n, w["grid"], w["dt"],
+                            w["update_prob"], w["seed"])
+    for _ in range(args.warmup):
+        ex.render_views(state, cfg)
+    torch.cuda.synchronize()
+    L = lib()
+    kid = 10  # NPA_KERNEL_RENDER: the render pipeline after the attributes kernel
+    ctx.check(L.npa_profile_reset(ctx.handle))
+    ctx.check(L.npa_profile_enable(ctx.handle, 1 << kid))
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        img = ex.render_views(state, cfg)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    tot, cnt = C.c_double(), C.c_uint64()
+    ctx.check(L.npa_profile_read(ctx.handle, kid, C.byref(tot), C.byref(cnt)))
+    ctx.check(L.npa_profile_enable(ctx.handle, 0))
+    pipe_ms = tot.value / max(cnt.value, 1)
+    finite = bool(torch.isfinite(img).all().item())
+    state.close()
+    views = len(ALL_VIEWS)
+    value = n * views * args.steps / elapsed
+    pixels = render_work(w["positions"], [cfg.sigma] * n, ALL_VIEWS, cfg)
+    flops = pixels * RENDER_FLOPS_PER_PIXEL
+    achieved = flops / (pipe_ms * 1e-3) / 1e12
+    line = {
+        "metric": "particle-views/sec, projected 3D render (render-loss particle images)",
+        "value": value, "unit": "particle-views/sec", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": 1000.0 * elapsed / args.steps, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (C4 seeded surface particles and states)",
+        "config": {"workload": (f"render: C4 state ({n} particles, S={w['model'].state_dims}), "
+                                f"{views} views (Xy, Xz, Yz, Iso), {cfg.image_size}x{cfg.image_size} "
+                                f"RGBA+depth, sigma {cfg.sigma} px, FixedScale, world_scale "
+                                f"{cfg.world_scale}"),
+                   "particles": n, "views": views, "image_size": cfg.image_size,
+                   "footprint_pixels": pixels, "images_finite": finite},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_FP32_TFLOPS, "traffic": None,
+                     "kernel": "render pipeline (prep + scans + key sort + tiles)",
+                     "engine": "fp32 VALU; exp counted as one operation",
+                     "mean_launch_ms": pipe_ms, "flops_per_launch": flops,
+                     "timing": "HIP events around the render pipeline of every timed call, on the "
+                               "library's stream"},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+
+        O.build()
+        st = w["states"]
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            col, op, sg, _ = O.render_attributes(st, w["model"].state_dims, cfg)
+            O.render_views(w["positions"], col, op, sg, ALL_VIEWS, cfg)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= min(args.cpu_seconds, 20.0) or reps >= 64:
+                break
+        line["cpu_baseline"] = {
+            "value": n * views * reps / el, "unit": "particle-views/sec", "cores": 1, "kind": "port",
+            "sample": (f"{reps} renders of the same state and views (oracle/libnpa_oracle.so "
+                       f"render_attributes + project_positions + splat_projected, one thread, "
+                       f"{el:.1f} s)")}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def copy_calibration(torch, mib: float) -> int:
     n = int(mib * (1 << 20)) // 4
     src = torch.rand(n, device="cuda")
@@ -153,6 +272,7 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--workload", default="c2")
     ap.add_argument("--particles", type=int, default=None)
+    ap.add_argument("--image-size", type=int, default=64, help="render workload only")
     ap.add_argument("--decode-every", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--mlp-engine", choices=("valu", "mfma"), default="valu",
@@ -179,6 +299,8 @@ def main(argv=None) -> int:
 
     if args.copy_calibration is not None:
         return copy_calibration(torch, args.copy_calibration)
+    if args.workload == "render":
+        return bench_render(args, torch)
 
     from burn_automata_amd import kernels as K
     from burn_automata_amd import synthetic as syn

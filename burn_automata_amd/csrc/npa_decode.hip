@@ -356,7 +356,7 @@ __global__ __launch_bounds__(256) void k_splat_tiles(SplatParams P, const SplatP
 
 void SplatWorkspace::release() {
     for (DevBuf* b : {&params, &item_start, &keys, &vals, &sorted, &ranks, &table, &totals, &offsets, &count, &flags, &scan,
-                      &attrs})
+                      &attrs, &partials, &chunks})
         b->release();
 }
 
@@ -473,16 +473,21 @@ struct RenderParams {
     float basis[kMaxRenderViews][9];  // right, up, forward of each view
 };
 
-struct RenderParticle {  // 48 bytes
-    float fx, fy;
-    int bx, by;
-    int radius;
-    float two_sig2;  // 2 * sigma^2
-    float denom;     // max(in-bounds weight sum, EPS)
-    float opacity;   // clamped to [0, 1]
-    float c[3];
+struct alignas(16) RenderParticle {  // 48 bytes
+    float px, py;     // projected pixel coordinates
+    int x0, y0;       // first column / row of the (2 radius + 1)^2 footprint (image.rs:41-53)
+    uint32_t span;    // 2 radius
+    float k2;         // log2(e) / (2 sigma^2)
+    float scale;      // norm_scale * clamp(opacity, 0, 1) / max(in-bounds weight sum, EPS)
     float depth;
+    float c[3];
+    float pad;
 };
+
+// The splat weight exp(-d2 / (2 sigma^2)) (image.rs:61) as 2^(-d2 * k2) on the hardware exp2;
+// it differs from the reference's expf of the IEEE quotient by a few ulps at most.
+constexpr float kLog2e = 1.44269504088896340736f;
+__device__ __forceinline__ float splat_weight(float d2, float k2) { return __builtin_amdgcn_exp2f(-(d2 * k2)); }
 
 __device__ __forceinline__ bool render_tiles(const RenderParams& P, int64_t bx, int64_t by, int64_t r, int* tx0,
                                              int* tx1, int* ty0, int* ty1) {
@@ -499,26 +504,34 @@ __device__ __forceinline__ bool render_tiles(const RenderParams& P, int64_t bx, 
     return true;
 }
 
-// grid (ceil(count / 256), nviews): blockIdx.y is the view, so its basis is a uniform load.
+// kPrepLanes lanes per particle-view; grid (ceil(count * kPrepLanes / 256), nviews): blockIdx.y is
+// the view, so its basis is a uniform load. The lanes split the in-bounds footprint by rows (lane
+// l sums rows l, l + kPrepLanes, ... left to right) and combine their sums in a fixed butterfly,
+// so the weight sum is deterministic; it differs from the reference's single running sum only
+// by rounding.
+constexpr uint32_t kPrepLanes = 16;
+
 __global__ __launch_bounds__(256) void k_render_prep(RenderParams P, const float4* __restrict__ pos,
                                                      const float* __restrict__ colors,
                                                      const float* __restrict__ opacities,
                                                      const float* __restrict__ sigmas,
                                                      RenderParticle* __restrict__ out,
                                                      uint32_t* __restrict__ ntiles) {
-    const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x;
-    if (n >= P.count) return;
+    const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t n = g / kPrepLanes, lane = g % kPrepLanes;
+    const bool live = n < P.count;  // the whole group agrees: count * kPrepLanes threads are live
+    const uint32_t nn = live ? n : 0;
     const uint32_t v = blockIdx.y;
     const float* B = P.basis[v];
-    const float4 p = pos[n];
+    const float4 p = pos[nn];
     // dot3 (math.rs:20-22) in the reference's order, then the depth of projection.rs:20-21
     const float x = p.x * B[0] + p.y * B[1] + p.z * B[2];
     const float y = p.x * B[3] + p.y * B[4] + p.z * B[5];
     const float f = p.x * B[6] + p.y * B[7] + p.z * B[8];
     const float depth = clampf_(0.5f + 0.5f * f / fmaxf(P.ws, kRenderEps), 0.0f, 1.0f);
-    const float sigma = fmaxf(clampf_(sigmas[n], P.min_sigma, P.max_sigma), kRenderEps);
+    const float sigma = fmaxf(clampf_(sigmas[nn], P.min_sigma, P.max_sigma), kRenderEps);
     const float sigma2 = sigma * sigma;
-    const float two_sig2 = 2.0f * sigma2;
+    const float k2 = kLog2e / (2.0f * sigma2);
     const int64_t radius = f32_to_isize(fmaxf(ceilf(5.0f * sigma), 1.0f));
     const float fsz1 = (float)P.size - 1.0f;
     const float px = (x + P.ws) / (2.0f * P.ws) * fsz1;
@@ -526,35 +539,38 @@ __global__ __launch_bounds__(256) void k_render_prep(RenderParams P, const float
     const int64_t bx = f32_to_isize(floorf(px)), by = f32_to_isize(floorf(py));
     const float fx = px - (float)bx, fy = py - (float)by;
     int tx0 = 0, tx1 = -1, ty0 = 0, ty1 = -1;
-    const bool any = render_tiles(P, bx, by, radius, &tx0, &tx1, &ty0, &ty1);
-    float weight_sum = 0.0f;
-    if (any) {  // the in-bounds part of the footprint, rows then columns as image.rs:49-63 visits it
-        const int64_t oy0 = by - radius < 0 ? -by : -radius;
-        const int64_t oy1 = by + radius > P.size - 1 ? P.size - 1 - by : radius;
-        const int64_t ox0 = bx - radius < 0 ? -bx : -radius;
-        const int64_t ox1 = bx + radius > P.size - 1 ? P.size - 1 - bx : radius;
-        for (int oy = (int)oy0; oy <= (int)oy1; ++oy) {
+    const bool any = live && render_tiles(P, bx, by, radius, &tx0, &tx1, &ty0, &ty1);
+    float part = 0.0f;
+    if (any) {  // the in-bounds part of the footprint (image.rs:49-63)
+        const int oy0 = (int)(by - radius < 0 ? -by : -radius);
+        const int oy1 = (int)(by + radius > P.size - 1 ? P.size - 1 - by : radius);
+        const int ox0 = (int)(bx - radius < 0 ? -bx : -radius);
+        const int ox1 = (int)(bx + radius > P.size - 1 ? P.size - 1 - bx : radius);
+        for (int oy = oy0 + (int)lane; oy <= oy1; oy += (int)kPrepLanes) {
             const float dy = (float)oy - fy;
-            for (int ox = (int)ox0; ox <= (int)ox1; ++ox) {
+            for (int ox = ox0; ox <= ox1; ++ox) {
                 const float dx = (float)ox - fx;
-                weight_sum += expf(-(dx * dx + dy * dy) / two_sig2);
+                part += splat_weight(dx * dx + dy * dy, k2);
             }
         }
     }
+#pragma unroll
+    for (uint32_t m = kPrepLanes / 2; m >= 1; m >>= 1) part += __shfl_xor(part, (int)m, (int)kPrepLanes);
+    if (!live || lane != 0) return;
     const uint64_t i = (uint64_t)v * P.count + n;
     RenderParticle rp;
-    rp.fx = fx;
-    rp.fy = fy;
-    rp.bx = any ? (int)bx : 0;
-    rp.by = any ? (int)by : 0;
-    rp.radius = (int)radius;
-    rp.two_sig2 = two_sig2;
-    rp.denom = fmaxf(weight_sum, kRenderEps);
-    rp.opacity = clampf_(opacities[n], 0.0f, 1.0f);
+    rp.px = px;
+    rp.py = py;
+    rp.x0 = any ? (int)(bx - radius) : 0;
+    rp.y0 = any ? (int)(by - radius) : 0;
+    rp.span = any ? (uint32_t)(2 * radius) : 0u;
+    rp.k2 = k2;
+    rp.scale = P.norm_scale * clampf_(opacities[n], 0.0f, 1.0f) / fmaxf(part, kRenderEps);  // image.rs:67-69
+    rp.depth = depth;
     rp.c[0] = colors[3 * (uint64_t)n];
     rp.c[1] = colors[3 * (uint64_t)n + 1];
     rp.c[2] = colors[3 * (uint64_t)n + 2];
-    rp.depth = depth;
+    rp.pad = 0.0f;
     out[i] = rp;
     ntiles[i] = any ? (uint32_t)((tx1 - tx0 + 1) * (ty1 - ty0 + 1)) : 0u;
 }
@@ -566,8 +582,9 @@ __global__ __launch_bounds__(256) void k_render_emit(RenderParams P, const Rende
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= items || ntiles[i] == 0) return;
     const RenderParticle q = rp[i];
+    const int64_t r = q.span / 2;
     int tx0, tx1, ty0, ty1;
-    render_tiles(P, q.bx, q.by, q.radius, &tx0, &tx1, &ty0, &ty1);
+    render_tiles(P, (int64_t)q.x0 + r, (int64_t)q.y0 + r, r, &tx0, &tx1, &ty0, &ty1);
     uint32_t k = start[i];
     const uint32_t base = (i / P.count) * P.tiles_per_view;
     for (int ty = ty0; ty <= ty1; ++ty)
@@ -578,43 +595,133 @@ __global__ __launch_bounds__(256) void k_render_emit(RenderParams P, const Rende
         }
 }
 
-// One 16x16 screen tile of one view per block; thread = pixel. The tile's particles are staged
-// through LDS 256 at a time.
-__global__ __launch_bounds__(256) void k_render_tiles(RenderParams P, const RenderParticle* __restrict__ rp,
-                                                      const uint32_t* __restrict__ offsets,
-                                                      const uint32_t* __restrict__ sorted, float* __restrict__ images) {
-    __shared__ RenderParticle buf[256];
-    const uint32_t t = blockIdx.x;
-    const uint32_t v = t / P.tiles_per_view, lt = t - v * P.tiles_per_view;
-    const int tx = (int)(lt % (uint32_t)P.tiles_x), ty = (int)(lt / (uint32_t)P.tiles_x);
-    const int x = tx * kTile + (int)(threadIdx.x % kTile);
-    const int y = ty * kTile + (int)(threadIdx.x / kTile);
-    const uint32_t beg = offsets[t], end = offsets[t + 1];
-    float acc[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t base = beg; base < end; base += 256) {
-        const uint32_t k = base + threadIdx.x;
-        if (k < end) buf[threadIdx.x] = rp[sorted[k]];
+// The sorted particle list of each screen tile is cut into chunks of kChunk particles; a block
+// draws one chunk of one tile (thread = pixel, the chunk staged in LDS), summing its particles in
+// ascending index order into a partial tile. k_render_reduce then adds each tile's partials in
+// chunk order. A tile of one chunk is thus exactly the reference's running sum; a longer list
+// differs from it only by the rounding of the chunk boundaries.
+constexpr uint32_t kChunk = 256;
+
+// One block: nch[t] = ceil(tile t's key count / kChunk), chunk_start = its exclusive prefix, and
+// the total into *total. ntiles <= 65536, so each thread owns at most 64 consecutive tiles.
+__global__ __launch_bounds__(1024) void k_render_chunk_scan(const uint32_t* __restrict__ offsets, uint32_t ntiles,
+                                                            uint32_t* __restrict__ nch,
+                                                            uint32_t* __restrict__ chunk_start,
+                                                            uint32_t* __restrict__ total) {
+    __shared__ uint32_t lds[16];
+    const uint32_t per = (ntiles + blockDim.x - 1) / blockDim.x;
+    const uint32_t t0 = threadIdx.x * per;
+    const uint32_t t1 = t0 + per < ntiles ? t0 + per : ntiles;
+    uint32_t sum = 0;
+    for (uint32_t t = t0; t < t1; ++t) {
+        const uint32_t c = (offsets[t + 1] - offsets[t] + kChunk - 1) / kChunk;
+        nch[t] = c;
+        sum += c;
+    }
+    const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    uint32_t x = sum;
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(x, off, 64);
+        if (lane >= (uint32_t)off) x += y;
+    }
+    if (lane == 63) lds[wid] = x;
+    __syncthreads();
+    uint32_t base = 0, all = 0;
+    for (uint32_t w = 0; w < nw; ++w) {
+        const uint32_t v = lds[w];
+        if (w < wid) base += v;
+        all += v;
+    }
+    uint32_t run = base + x - sum;
+    for (uint32_t t = t0; t < t1; ++t) {
+        chunk_start[t] = run;
+        run += nch[t];
+    }
+    if (threadIdx.x == 0) *total = all;
+}
+
+// Grid-stride over the chunks; thread = pixel, the chunk's particles staged in LDS. dx = x - px
+// is the reference's (x - base_x) - frac_x exactly: both are one rounding of the same real number.
+// partials[c][5][256] (channel-planar, so the stores coalesce).
+__global__ __launch_bounds__(256) void k_render_chunks(RenderParams P, const RenderParticle* __restrict__ rp,
+                                                       const uint32_t* __restrict__ offsets,
+                                                       const uint32_t* __restrict__ sorted,
+                                                       const uint32_t* __restrict__ chunk_start,
+                                                       const uint32_t* __restrict__ total_chunks, uint32_t ntiles,
+                                                       float* __restrict__ partials) {
+    __shared__ RenderParticle buf[kChunk];
+    const uint32_t total = *total_chunks;
+    for (uint32_t c = blockIdx.x; c < total; c += gridDim.x) {
+        // the tile: the last t with chunk_start[t] <= c (tiles without chunks share the next start)
+        uint32_t lo = 0, hi = ntiles - 1;
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi + 1) / 2;
+            if (chunk_start[mid] <= c) lo = mid;
+            else hi = mid - 1;
+        }
+        const uint32_t t = lo;
+        const uint32_t v = t / P.tiles_per_view, lt = t - v * P.tiles_per_view;
+        const int x = (int)(lt % (uint32_t)P.tiles_x) * kTile + (int)(threadIdx.x % kTile);
+        const int y = (int)(lt / (uint32_t)P.tiles_x) * kTile + (int)(threadIdx.x / kTile);
+        const float xf = (float)x, yf = (float)y;
+        const uint32_t beg = offsets[t] + (c - chunk_start[t]) * kChunk;
+        const uint32_t end = min(beg + kChunk, offsets[t + 1]);
+        if (beg + threadIdx.x < end) buf[threadIdx.x] = rp[sorted[beg + threadIdx.x]];
         __syncthreads();
-        const uint32_t m = end - base < 256 ? end - base : 256;
+        float acc[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        const uint32_t m = end - beg;
         for (uint32_t q = 0; q < m; ++q) {
             const RenderParticle& p = buf[q];
-            const int ox = x - p.bx, oy = y - p.by;
-            if (ox < -p.radius || ox > p.radius || oy < -p.radius || oy > p.radius) continue;
-            const float dx = (float)ox - p.fx, dy = (float)oy - p.fy;
-            float w = expf(-(dx * dx + dy * dy) / p.two_sig2);
-            w = w / p.denom * P.norm_scale * p.opacity;  // image.rs:69
+            if ((uint32_t)(x - p.x0) > p.span || (uint32_t)(y - p.y0) > p.span) continue;
+            const float dx = xf - p.px, dy = yf - p.py;
+            const float w = splat_weight(dx * dx + dy * dy, p.k2) * p.scale;  // image.rs:61, 69
             acc[0] += p.c[0] * w;
             acc[1] += p.c[1] * w;
             acc[2] += p.c[2] * w;
             acc[3] += w;
             acc[4] += p.depth * w;
         }
-        __syncthreads();
+        float* o = partials + (uint64_t)c * (5 * kChunk) + threadIdx.x;
+#pragma unroll
+        for (int ch = 0; ch < 5; ++ch) o[ch * kChunk] = acc[ch];
+        __syncthreads();  // buf is refilled by the next chunk
+    }
+}
+
+// One tile per block, thread = pixel: the tile's partials in chunk order (zero for an empty tile).
+__global__ __launch_bounds__(256) void k_render_reduce(RenderParams P, const uint32_t* __restrict__ chunk_start,
+                                                       const uint32_t* __restrict__ nch,
+                                                       const float* __restrict__ partials,
+                                                       float* __restrict__ images) {
+    const uint32_t t = blockIdx.x;
+    const uint32_t v = t / P.tiles_per_view, lt = t - v * P.tiles_per_view;
+    const int x = (int)(lt % (uint32_t)P.tiles_x) * kTile + (int)(threadIdx.x % kTile);
+    const int y = (int)(lt / (uint32_t)P.tiles_x) * kTile + (int)(threadIdx.x / kTile);
+    float acc[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t c0 = chunk_start[t], c1 = c0 + nch[t];
+    uint32_t c = c0;
+    for (; c + 4 <= c1; c += 4) {  // four chunks' loads in flight, then added in chunk order
+        float v[4][5];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float* q = partials + (uint64_t)(c + u) * (5 * kChunk) + threadIdx.x;
+#pragma unroll
+            for (int ch = 0; ch < 5; ++ch) v[u][ch] = q[ch * kChunk];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int ch = 0; ch < 5; ++ch) acc[ch] += v[u][ch];
+    }
+    for (; c < c1; ++c) {
+        const float* q = partials + (uint64_t)c * (5 * kChunk) + threadIdx.x;
+#pragma unroll
+        for (int ch = 0; ch < 5; ++ch) acc[ch] += q[ch * kChunk];
     }
     if (x < P.size && y < P.size) {
         float* o = images + (((uint64_t)v * P.size + y) * P.size + x) * 5;
 #pragma unroll
-        for (int c = 0; c < 5; ++c) o[c] = acc[c];
+        for (int ch = 0; ch < 5; ++ch) o[ch] = acc[ch];
     }
 }
 
@@ -667,7 +774,7 @@ hipError_t launch_render_views(const float4* pos, const float* colors, const flo
     if (ntile64 > 65536) return hipErrorInvalidValue;  // the key sort's bin limit
     const uint32_t ntile_total = (uint32_t)ntile64;
     const uint64_t items64 = (uint64_t)count * nviews;
-    if (items64 >= (1ull << 31)) return hipErrorInvalidValue;
+    if (items64 >= (1ull << 31) || (uint64_t)count * kPrepLanes >= (1ull << 32)) return hipErrorInvalidValue;
     const uint32_t items = (uint32_t)items64;
     // the widest footprint: sigma <= max(max_sigma, EPS)
     const float rmaxf = fmaxf(ceilf(5.0f * fmaxf(cfg.max_sigma, kRenderEps)), 1.0f);
@@ -694,13 +801,18 @@ hipError_t launch_render_views(const float4* pos, const float* colors, const flo
     NPA_RES(ws.count, 64);
     NPA_RES(ws.scan, (2 * ((uint64_t)items / kScanBlock + 1) + 2) * 4);
     NPA_RES(ws.flags, 64);
+    // chunks: at most one partial per kChunk keys plus one per tile
+    const uint64_t max_chunks = (uint64_t)cap / kChunk + ntile_total;
+    NPA_RES(ws.partials, max_chunks * 5 * kChunk * 4);
+    NPA_RES(ws.chunks, (2 * (uint64_t)ntile_total + 1) * 4);
 #undef NPA_RES
     ProfScope ps(prof, NPA_KERNEL_RENDER, stream);
     uint32_t* ntiles = ws.item_start.as<uint32_t>() + (items ? items : 1);
     uint32_t* start = ws.item_start.as<uint32_t>();
     RenderParticle* rp = ws.params.as<RenderParticle>();
     if (count) {
-        hipLaunchKernelGGL(k_render_prep, dim3((count + 255) / 256, nviews), dim3(256), 0, stream, P, pos, colors,
+        hipLaunchKernelGGL(k_render_prep, dim3((uint32_t)(((uint64_t)count * kPrepLanes + 255) / 256), nviews), dim3(256),
+                           0, stream, P, pos, colors,
                            opacities, sigmas, rp, ntiles);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
@@ -728,8 +840,20 @@ hipError_t launch_render_views(const float4* pos, const float* colors, const flo
                         ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(), ws.totals.as<uint32_t>(),
                         ws.offsets.as<uint32_t>(), ws.sorted.as<uint32_t>(), ws.flags.as<uint32_t>(), stream);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_render_tiles, dim3(ntile_total), dim3(256), 0, stream, P, rp, ws.offsets.as<uint32_t>(),
-                       ws.sorted.as<uint32_t>(), images);
+    {  // chunks per tile, their exclusive prefix and total, then the chunks and the reduction
+        uint32_t* nch = ws.chunks.as<uint32_t>();
+        uint32_t* cstart = nch + ntile_total;
+        uint32_t* ctotal = cstart + ntile_total;
+        hipLaunchKernelGGL(k_render_chunk_scan, dim3(1), dim3(1024), 0, stream, ws.offsets.as<uint32_t>(), ntile_total,
+                           nch, cstart, ctotal);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        const uint32_t grid = (uint32_t)std::min<uint64_t>(max_chunks, 4096);
+        hipLaunchKernelGGL(k_render_chunks, dim3(grid), dim3(256), 0, stream, P, rp, ws.offsets.as<uint32_t>(),
+                           ws.sorted.as<uint32_t>(), cstart, ctotal, ntile_total, ws.partials.as<float>());
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        hipLaunchKernelGGL(k_render_reduce, dim3(ntile_total), dim3(256), 0, stream, P, cstart, nch,
+                           ws.partials.as<float>(), images);
+    }
     return hipGetLastError();
 }
 

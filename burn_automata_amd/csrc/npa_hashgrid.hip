@@ -790,6 +790,10 @@ bool make_key_sort_plan(uint32_t cap, uint32_t C, HashgridPlan* p) {
         if (((cap + tile - 1) / tile) * (uint64_t)C <= budget) break;
         rounds *= 2;
     }
+    // The table scan walks tiles_per_sys entries of each bin serially: with few bins (screen
+    // tiles) prefer fewer, larger rank tiles.
+    while (rounds < 32 && (cap + (uint64_t)p->waves * rounds * 64 - 1) / ((uint64_t)p->waves * rounds * 64) > 256)
+        rounds *= 2;
     p->rounds = rounds;
     p->tile = p->waves * rounds * 64;
     p->tiles_per_sys = std::max<uint32_t>(1, (cap + p->tile - 1) / p->tile);

@@ -309,6 +309,7 @@ hipError_t launch_decode_gaussians(const float4* pos, const float* states, uint3
 struct SplatWorkspace {
     DevBuf params, item_start, keys, vals, sorted, ranks, table, totals, offsets, count, flags, scan;
     DevBuf attrs;  // render attributes of a state's particles: colours [n][3], opacities [n], sigmas [n]
+    DevBuf partials, chunks;  // render: per-chunk partial tiles; chunk counts, starts and total
     void release();
 };
 // Particle n is drawn into window n / per_window of a grid of `windows` windows, win_cols per

@@ -276,8 +276,11 @@ npa_status npa_splat_2d_tiled(npa_context* ctx, const float* positions, const fl
  * isotropic projected splat of all count particles seen through views[v] (NPA_VIEW_*, a
  * HOST array of nviews <= 16 entries). colors[count][3], opacities[count], sigmas[count]
  * (pixels; clamped to [min_sigma, max_sigma] by the splat). images[nviews][size][size][5]
- * holds RenderedPixel (image.rs:4-9): r, g, b, alpha, depth_sum; it is overwritten. Each
- * pixel sums particles in ascending index order, as the reference does. */
+ * holds RenderedPixel (image.rs:4-9): r, g, b, alpha, depth_sum; it is overwritten.
+ * Deterministic; equal to the reference up to rounding: the weight is evaluated as
+ * 2^(-d^2 log2(e) / 2 sigma^2) with one combined scale, the footprint weight sum is split over
+ * 16 lanes, and a pixel adds its particles in ascending index order within chunks of 256,
+ * the chunks in order. */
 npa_status npa_render_views(npa_context* ctx, const float* positions, const float* colors,
                             const float* opacities, const float* sigmas, uint32_t count,
                             const uint32_t* views, uint32_t nviews, const npa_render_cfg* cfg,
