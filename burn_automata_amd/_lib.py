@@ -46,6 +46,8 @@ def _decl(L):
                                           P, P]
     L.npa_splat_2d.argtypes = [P, P, P, u32, ptr(_abi.NpaSplat2dCfg), P]
     L.npa_splat_2d_tiled.argtypes = [P, P, P, u32, u32, ptr(_abi.NpaSplat2dCfg), u32, P]
+    L.npa_perceive_adjoint.argtypes = [P, P, P, u32, u32, u32, ptr(_abi.NpaGridCfg),
+                                       ptr(_abi.NpaPerceptionOpts), P, sz, P, P]
     L.npa_render_views.argtypes = [P, P, P, P, P, u32, P, u32, ptr(_abi.NpaRenderCfg), P]
     L.npa_render_attributes.argtypes = [P, P, u32, u32, ptr(_abi.NpaRenderCfg), P, P, P, P]
     L.npa_state_render_views.argtypes = [P, P, u32, ptr(_abi.NpaRenderCfg), P]
@@ -88,7 +90,7 @@ def _decl(L):
                  "npa_state_set_mlp_engine", "npa_manifest_load", "npa_manifest_load_file",
                  "npa_manifest_info", "npa_manifest_model", "npa_manifest_initialization",
                  "npa_bpk_encode", "npa_sha256", "npa_render_views", "npa_render_attributes",
-                 "npa_state_render_views"):
+                 "npa_state_render_views", "npa_perceive_adjoint"):
         getattr(L, name).restype = st
 
 
@@ -104,7 +106,7 @@ EXPORTED = (
     "npa_context_set_mlp_engine", "npa_state_set_mlp_engine", "npa_manifest_load",
     "npa_manifest_load_file", "npa_manifest_destroy", "npa_manifest_info", "npa_manifest_model",
     "npa_manifest_initialization", "npa_bpk_encode", "npa_sha256", "npa_render_views",
-    "npa_render_attributes", "npa_state_render_views")
+    "npa_render_attributes", "npa_state_render_views", "npa_perceive_adjoint")
 
 
 def lib():

@@ -29,11 +29,13 @@ struct npa_context {
     std::string last_error;
     npa::Workspace ws;
     npa::SplatWorkspace splat_ws;
+    npa::AdjointWorkspace adj_ws;
     npa::Profiler prof;
     std::vector<DevBuf*> staging;
     ~npa_context() {
         ws.release();
         splat_ws.release();
+        adj_ws.release();
         for (DevBuf* b : staging) {
             b->release();
             delete b;
@@ -478,6 +480,60 @@ npa_status npa_perceive(npa_context* ctx, const float* positions, const float* s
         NPA_HIP(ctx, npa::launch_update(p, ctx->ws, sio, 1, blocks, ctx->stream, &ctx->prof), "perceive");
     }
     NPA_HIP(ctx, io.finish(), "host io");
+    if (ctx->host_io) return check_flags(ctx, ctx->ws);
+    return NPA_OK;
+}
+
+npa_status npa_perceive_adjoint(npa_context* ctx, const float* positions, const float* states, uint32_t B,
+                                uint32_t N, uint32_t S, const npa_grid_cfg* cfg, const npa_perception_opts* opts,
+                                const float* feature_adjoint, size_t feature_adjoint_len, float* state_adjoint,
+                                float* position_adjoint) {
+    if (!ctx || !opts) return NPA_ERR_INVALID_ARGUMENT;
+    npa_status st = validate_grid(ctx, cfg);
+    if (st) return st;
+    if (S == 0 || S > 32)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: the device path supports 1..=32 state dims");
+    const uint64_t total = (uint64_t)B * N;
+    const uint32_t d = cfg->dim;
+    const uint32_t F = S * 2 + (opts->state_grad ? S * d : 0) + (opts->density_grad ? d : 0) +
+                       (opts->position_features ? d : 0);
+    if (feature_adjoint_len != total * F)  // adjoint.rs:48-54
+        return fail(ctx, NPA_ERR_OUTPUT_SHAPE,
+                    "output buffer length " + std::to_string(feature_adjoint_len) + " does not match expected " +
+                        std::to_string(total * F));
+    if (!state_adjoint || (total && (!positions || !states || !feature_adjoint)))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null array");
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    npa::HashgridPlan plan;
+    std::string err;
+    if (!npa::make_plan(*cfg, B, N, &plan, &err, npa::targets_per_item(npa::state_stride_for(S))))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
+    HostIO io(ctx);
+    const float4* pos = (const float4*)io.in(positions, total * 16);
+    const float* st_in = io.in(states, total * S * 4);
+    const float* fa = io.in(feature_adjoint, total * F * 4);
+    float* sa = io.out(state_adjoint, total * S * 4);
+    DevBuf pos_scratch;  // the position adjoint is computed even when the caller does not want it
+    float4* pa = (float4*)(position_adjoint ? io.out(position_adjoint, total * 16) : nullptr);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if (!pa) {
+        NPA_HIP(ctx, pos_scratch.reserve(total * 16 + 16), "workspace");
+        pa = pos_scratch.as<float4>();
+    }
+    if (total && (!aligned16(pos) || !aligned16(pa)))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: position arrays must be 16-byte aligned");
+    NPA_HIP(ctx, ctx->ws.reserve(plan, total, B, S, (int)d), "workspace");
+    npa::StepParams p = make_params(*cfg, *opts, B, N, S);
+    if (total) {
+        NPA_HIP(ctx, npa::launch_hashgrid(plan, p.g, pos, st_in, S, B, N, ctx->ws, true, ctx->stream, &ctx->prof),
+                "hashgrid");
+        NPA_HIP(ctx, npa::launch_perceive_adjoint(p, ctx->ws, ctx->adj_ws, fa, sa, pa, ctx->stream), "adjoint");
+    }
+    NPA_HIP(ctx, io.finish(), "host io");
+    if (!position_adjoint) {
+        NPA_HIP(ctx, hipStreamSynchronize(ctx->stream), "sync");
+        pos_scratch.release();
+    }
     if (ctx->host_io) return check_flags(ctx, ctx->ws);
     return NPA_OK;
 }

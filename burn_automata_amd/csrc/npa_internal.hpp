@@ -331,6 +331,16 @@ hipError_t launch_render_attributes(const float* states, uint32_t count, uint32_
                                     const npa_render_cfg& cfg, float* colors, float* opacities,
                                     float* sigmas, float* derivatives, hipStream_t stream);
 
+// Perception adjoint (reference/adjoint.rs): per-slot scratch of the four adjoint passes.
+struct AdjointWorkspace {
+    DevBuf sdens, sfb, rga, madj, rda, dadj, ppos;
+    void release();
+};
+// Needs the hashgrid built with its payload (sorted records and states) in ws; fadj [T][F],
+// state_adj [T][S] and pos_adj [T] in particle order.
+hipError_t launch_perceive_adjoint(const StepParams& p, Workspace& ws, AdjointWorkspace& aw, const float* fadj,
+                                   float* state_adj, float4* pos_adj, hipStream_t stream);
+
 int device_cu_count();
 
 }  // namespace npa

@@ -32,67 +32,6 @@
 
 namespace npa {
 
-template <int D>
-__device__ __forceinline__ void load_rec(const float4* __restrict__ srec, const int4* __restrict__ scoord,
-                                         uint32_t j, float* p, int* c) {
-    const float4 r = srec[j];
-    if constexpr (D == 2) {
-        p[0] = r.x;
-        p[1] = r.y;
-        p[2] = 0.0f;
-        c[0] = __float_as_int(r.z);
-        c[1] = __float_as_int(r.w);
-        c[2] = 0;
-    } else {
-        p[0] = r.x;
-        p[1] = r.y;
-        p[2] = r.z;
-        const int4 q = scoord[j];
-        c[0] = q.x;
-        c[1] = q.y;
-        c[2] = q.z;
-    }
-}
-
-// for_each_neighbor  crates/burn_automata_kernels/src/reference/neighbor.rs:3-44
-template <int D, class Body>
-__device__ __forceinline__ void walk_neighbors(const GridParams& g, uint32_t b, const float* pi, const int* ci,
-                                               const uint32_t* __restrict__ bo,
-                                               const float4* __restrict__ srec,
-                                               const int4* __restrict__ scoord, Body&& body) {
-    constexpr int ZLO = D == 3 ? -1 : 0, ZHI = D == 3 ? 1 : 0;
-    for (int dz = ZLO; dz <= ZHI; ++dz)
-        for (int dy = -1; dy <= 1; ++dy)
-            for (int dx = -1; dx <= 1; ++dx) {
-                const int64_t n0 = (int64_t)ci[0] + dx, n1 = (int64_t)ci[1] + dy, n2 = (int64_t)ci[2] + dz;
-                uint32_t cell;
-                if (!cell_index(n0, n1, n2, g, &cell)) continue;
-                const uint64_t bin = (uint64_t)b * g.cells + cell;
-                const uint32_t beg = bo[bin], end = bo[bin + 1];
-                for (uint32_t j = beg; j < end; ++j) {
-                    float pj[3];
-                    int cj[3];
-                    load_rec<D>(srec, scoord, j, pj, cj);
-                    if (g.mode == 1) {
-                        if ((int64_t)cj[0] != n0 || (int64_t)cj[1] != n1) continue;
-                        if (D == 3 && (int64_t)cj[2] != n2) continue;
-                    }
-                    float d[3];
-                    d[0] = delta_axis(pi[0], pj[0], 0, g);
-                    d[1] = delta_axis(pi[1], pj[1], 1, g);
-                    float r2 = d[0] * d[0];
-                    r2 += d[1] * d[1];
-                    if constexpr (D == 3) {
-                        d[2] = delta_axis(pi[2], pj[2], 2, g);
-                        r2 += d[2] * d[2];
-                    } else {
-                        d[2] = 0.0f;
-                    }
-                    if (r2 < g.eps2) body(j, d, r2);
-                }
-            }
-}
-
 #define NPA_WAVE_LOOP_BEGIN(wl, wl_count)                                       \
     const uint32_t lane = threadIdx.x & 63;                                     \
     const uint32_t wave0 = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); \

@@ -6,6 +6,8 @@ and returns freshly allocated device tensors, as the reference returns owned Vec
 * ``build_hashgrid``          crates/burn_automata_kernels/src/hashgrid.rs:16-69
 * ``perceive`` / ``perceive_with_options``
                               crates/burn_automata_kernels/src/reference/forward.rs:3-143
+* ``perceive_adjoint_with_options`` / ``perceive_state_adjoint_with_options``
+                              crates/burn_automata_kernels/src/reference/adjoint.rs:3-136
 * ``euler_step``              crates/burn_automata_kernels/src/reference/step.rs:4-55
 * ``decode_gaussians_3d``     crates/burn_automata_kernels/src/gaussian.rs:53-100
 * ``splat_particles_2d``      crates/burn_automata_kernels/src/splat.rs:30-93
@@ -144,6 +146,41 @@ def perceive_with_options(positions, states, batch_size: int, particle_count: in
                                  ptr(sg) if sg.numel() else None, ptr(dg) if dg.numel() else None,
                                  C.byref(fd)))
     return PerceptionOutput(feats, dens, blur, sg, dg, int(fd.value))
+
+
+@dataclass
+class PerceptionAdjointOutput:
+    """PerceptionAdjointOutput (reference/types.rs:43-47): state [T * S], position [T, 4]."""
+
+    state: object
+    position: object
+
+
+def perceive_adjoint_with_options(positions, states, batch_size: int, particle_count: int,
+                                  state_dims: int, cfg: HashGridConfig, options: PerceptionOptions,
+                                  feature_adjoint, ctx=None) -> PerceptionAdjointOutput:
+    """perceive_adjoint_with_options (reference/adjoint.rs:27-136) on the device."""
+    ctx = ctx or default_context()
+    torch = _torch()
+    total = batch_size * particle_count
+    pos = _positions(positions, total, ctx)
+    st = _states(states, total * state_dims, ctx)
+    fa = device_f32(feature_adjoint, device=ctx.device).reshape(-1)
+    dev = f"cuda:{ctx.device}"
+    sa = torch.empty(total * state_dims, dtype=torch.float32, device=dev)
+    pa = torch.empty((total, 4), dtype=torch.float32, device=dev)
+    ctx.check(lib().npa_perceive_adjoint(ctx.handle, ptr(pos), ptr(st), batch_size, particle_count,
+                                         state_dims, C.byref(cfg.to_c()), C.byref(options.to_c()),
+                                         ptr(fa), fa.numel(), ptr(sa), ptr(pa)))
+    return PerceptionAdjointOutput(sa, pa)
+
+
+def perceive_state_adjoint_with_options(positions, states, batch_size: int, particle_count: int,
+                                        state_dims: int, cfg: HashGridConfig,
+                                        options: PerceptionOptions, feature_adjoint, ctx=None):
+    """perceive_state_adjoint_with_options (reference/adjoint.rs:3-25)."""
+    return perceive_adjoint_with_options(positions, states, batch_size, particle_count, state_dims,
+                                         cfg, options, feature_adjoint, ctx).state
 
 
 def perceive(positions, states, batch_size, particle_count, state_dims, cfg: HashGridConfig,

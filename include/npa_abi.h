@@ -216,6 +216,20 @@ npa_status npa_perceive(npa_context* ctx, const float* positions, const float* s
                         float* blurred_state, float* state_gradient, float* density_gradient,
                         uint32_t* feature_dims);
 
+/* Replaces perceive_adjoint_with_options
+ * (crates/burn_automata_kernels/src/reference/adjoint.rs:27-136; perceive_state_adjoint_with_options
+ * adjoint.rs:3-25 is its state half): the reverse mode of npa_perceive for the same positions,
+ * states, grid and options. feature_adjoint[B*N][F] (feature_adjoint_len must equal B*N*F,
+ * NPA_ERR_OUTPUT_SHAPE otherwise); state_adjoint[B*N][S]; position_adjoint[B*N][4] (w = 0; may be
+ * NULL). Deterministic; equal to the reference up to the order of each particle's sums: the
+ * reference scatters every pair's terms from idx into idx and j, this entry point gathers them
+ * per particle over its own neighbour list (the relation is symmetric). */
+npa_status npa_perceive_adjoint(npa_context* ctx, const float* positions, const float* states,
+                                uint32_t batch_size, uint32_t particle_count, uint32_t state_dims,
+                                const npa_grid_cfg* cfg, const npa_perception_opts* opts,
+                                const float* feature_adjoint, size_t feature_adjoint_len,
+                                float* state_adjoint, float* position_adjoint);
+
 /* Replaces NpaModel::forward_from_features_with_eps
  * (crates/burn_automata/src/model.rs:867-940): update MLP, motion scaling.
  * features[rows][F] -> dx[rows][4] (axes >= d written as 0), ds[rows][S]. */

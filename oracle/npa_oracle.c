@@ -1398,3 +1398,288 @@ int oracle_render_attributes(const float* states, uint32_t count, uint32_t state
     }
     return NPA_OK;
 }
+
+/* ------------------------------------------------------------ perception adjoint
+ * crates/burn_automata_kernels/src/reference/adjoint.rs, serial like the reference: every
+ * accumulation into the adjoint arrays happens in the reference's order. */
+
+/* smoothing_poly6_delta_adjoint  kernels.rs:62-79 */
+static void poly6_delta_adjoint(const float delta[4], float r2, const npa_grid_cfg* cfg, float out_adj,
+                                float out[4]) {
+    out[0] = out[1] = out[2] = out[3] = 0.0f;
+    float eps2 = cfg->eps * cfg->eps;
+    if (r2 >= eps2) return;
+    float x = eps2 - r2;
+    float dk = -3.0f * poly6_norm(cfg) * x * x;
+    for (uint32_t a = 0; a < cfg->dim; ++a) out[a] = out_adj * dk * 2.0f * delta[a];
+}
+
+/* spiky_gradient_delta_adjoint  kernels.rs:100-126 */
+static void spiky_delta_adjoint(const float delta[4], float r2, const npa_grid_cfg* cfg, float coeff,
+                                const float* out_adj, float out[4]) {
+    out[0] = out[1] = out[2] = out[3] = 0.0f;
+    float eps2 = cfg->eps * cfg->eps;
+    if (r2 <= 0.0f || r2 >= eps2) return;
+    float r = sqrtf(r2);
+    float norm = coeff * spiky_norm(cfg) * 3.0f;
+    float t = cfg->eps - r;
+    float scale = norm * (t * t) / r;
+    float dscale_dr = norm * (1.0f - (cfg->eps * cfg->eps) / r2);
+    float dot = out_adj[0] * delta[0];
+    for (uint32_t a = 1; a < cfg->dim; ++a) dot += out_adj[a] * delta[a];
+    for (uint32_t a = 0; a < cfg->dim; ++a) out[a] = scale * out_adj[a] + dscale_dr * dot * delta[a] / r;
+}
+
+/* log_normalize_adjoint  normalize.rs:71-91 (adds into in_adj) */
+static void log_normalize_adjoint(const float* in, const float* out_adj, float* in_adj, uint32_t n) {
+    const float E = 1.0e-6f;
+    float s = in[0] * in[0];
+    for (uint32_t k = 1; k < n; ++k) s += in[k] * in[k];
+    float norm = fmaxf(sqrtf(s + E * E), E);
+    float scale = log1pf(norm) / norm;
+    float dscale = (norm / (1.0f + norm) - log1pf(norm)) / (norm * norm);
+    float dot = in[0] * out_adj[0];
+    for (uint32_t k = 1; k < n; ++k) dot += in[k] * out_adj[k];
+    float radial = dscale * dot / norm;
+    for (uint32_t k = 0; k < n; ++k) in_adj[k] += scale * out_adj[k] + radial * in[k];
+}
+
+/* accumulate_volume_density_adjoint  adjoint.rs:420-431 */
+static void volume_density_adjoint(const float* density, float* density_adj, uint64_t j, float v_adj) {
+    float rho = density[j];
+    if (fabsf(rho) <= 1.0e-20f || !isfinite(rho)) return;
+    density_adj[j] -= v_adj / (rho * rho);
+}
+
+/* add_delta_position_adjoint  adjoint.rs:433-445 */
+static void add_delta_position_adjoint(float* pos_adj, uint64_t lhs, uint64_t rhs, uint32_t dim,
+                                       const float d_adj[4]) {
+    for (uint32_t a = 0; a < dim; ++a) {
+        pos_adj[4 * rhs + a] += d_adj[a];
+        pos_adj[4 * lhs + a] -= d_adj[a];
+    }
+}
+
+/* inverse_matrix_adjoint  adjoint.rs:447-468 (subtracts into m_adj) */
+static void inverse_matrix_adjoint(const float inv[9], const float inv_adj[9], uint32_t d, float m_adj[9]) {
+    for (uint32_t row = 0; row < d; ++row)
+        for (uint32_t col = 0; col < d; ++col) {
+            float v = 0.0f;
+            for (uint32_t ir = 0; ir < d; ++ir)
+                for (uint32_t ic = 0; ic < d; ++ic) v += inv[ir * d + row] * inv_adj[ir * d + ic] * inv[col * d + ic];
+            m_adj[row * d + col] -= v;
+        }
+}
+
+/* density_gradient_scale  adjoint.rs:470-489 */
+static float density_gradient_scale(const npa_grid_cfg* cfg, const npa_perception_opts* o, uint32_t particle_count) {
+    float eps0 = fmaxf(o->eps0, FLT_MIN);
+    float s = o->scale_equivariance ? powi_f32(cfg->eps / eps0, 1 + (int)cfg->dim) : 1.0f;
+    return s * (o->particle_density_equivariance ? 1.0f / (float)(particle_count > 1 ? particle_count : 1) : 1.0f);
+}
+
+/* perceive_adjoint_with_options  adjoint.rs:27-136 with accumulate_blurred_state_adjoint (138-166),
+ * accumulate_state_gradient_adjoint (168-348), accumulate_density_gradient_position_adjoint
+ * (350-397) and accumulate_density_kernel_position_adjoint (399-418). feature_adjoint
+ * [total][F]; outputs state_adj [total][S], pos_adj [total][4] (overwritten). */
+int oracle_perceive_adjoint(const float* positions, const float* states, uint32_t batch_size,
+                            uint32_t particle_count, uint32_t S, const npa_grid_cfg* cfg,
+                            const npa_perception_opts* o, const float* fadj, float* state_adj,
+                            float* pos_adj) {
+    int st = oracle_grid_validate(cfg);
+    if (st) return st;
+    const uint64_t total = (uint64_t)batch_size * particle_count;
+    const uint32_t d = cfg->dim, F = oracle_feature_dims(S, d, o);
+    hashgrid h;
+    st = hashgrid_build(positions, batch_size, particle_count, cfg, &h);
+    float* density = (float*)calloc(total + 1, sizeof(float));
+    float* dens_adj = (float*)calloc(total + 1, sizeof(float));
+    float* raw = (float*)calloc((size_t)S * d + 1, sizeof(float));
+    float* rga = (float*)calloc((size_t)S * d + 1, sizeof(float));
+    if (st || !density || !dens_adj || !raw || !rga) {
+        hashgrid_free(&h);
+        free(density);
+        free(dens_adj);
+        free(raw);
+        free(rga);
+        return st ? st : NPA_ERR_OUT_OF_MEMORY;
+    }
+    pass_density(positions, &h.view, cfg, NULL, total, density);
+    memset(state_adj, 0, total * S * sizeof(float));
+    memset(pos_adj, 0, total * 4 * sizeof(float));
+    nbuf buf = {0};
+    for (uint64_t idx = 0; idx < total; ++idx) {
+        const float* fa = fadj + idx * F;
+        uint32_t cur = 0;
+        for (uint32_t c = 0; c < S; ++c) state_adj[idx * S + c] += fa[cur + c];
+        cur += S;
+        collect_neighbors(idx, positions, &h.view, cfg, &buf);
+        /* blurred state (adjoint.rs:138-166) */
+        const float* badj = fa + cur;
+        for (size_t k = 0; k < buf.len; ++k) {
+            const neighbor* n = &buf.v[k];
+            float vol = recip_finite(density[n->j]);
+            float kern = poly6(n->r2, cfg);
+            float w = kern * vol;
+            const float* sj = states + (uint64_t)n->j * S;
+            float wadj = 0.0f;
+            for (uint32_t c = 0; c < S; ++c) {
+                state_adj[(uint64_t)n->j * S + c] += badj[c] * w;
+                wadj += badj[c] * sj[c];
+            }
+            float da[4];
+            poly6_delta_adjoint(n->delta, n->r2, cfg, wadj * vol, da);
+            add_delta_position_adjoint(pos_adj, idx, n->j, d, da);
+            volume_density_adjoint(density, dens_adj, n->j, wadj * kern);
+        }
+        cur += S;
+        if (o->state_grad) { /* adjoint.rs:168-348 */
+            const float* gadj = fa + cur;
+            const float* si = states + idx * S;
+            memset(raw, 0, (size_t)S * d * sizeof(float));
+            float moment[9] = {0};
+            for (size_t k = 0; k < buf.len; ++k) {
+                const neighbor* n = &buf.v[k];
+                if (n->j == idx) continue;
+                float vol = recip_finite(density[n->j]);
+                float g[4];
+                spiky_grad(n->delta, n->r2, cfg, vol, g);
+                const float* sj = states + (uint64_t)n->j * S;
+                for (uint32_t c = 0; c < S; ++c) {
+                    float diff = sj[c] - si[c];
+                    for (uint32_t a = 0; a < d; ++a) raw[c * d + a] += diff * g[a];
+                }
+                if (o->hybrid_state_gradient)
+                    for (uint32_t r = 0; r < d; ++r)
+                        for (uint32_t cc = 0; cc < d; ++cc) moment[r * d + cc] += n->delta[r] * g[cc];
+            }
+            float inv[9];
+            if (o->hybrid_state_gradient) safe_inverse_symmetric(moment, d, inv);
+            float scale = o->scale_equivariance ? cfg->eps / fmaxf(o->eps0, FLT_MIN) : 1.0f;
+            float inv_adj[9] = {0};
+            for (uint32_t c = 0; c < S; ++c) {
+                float corr[4] = {0};
+                const uint32_t gb = c * d;
+                for (uint32_t a = 0; a < d; ++a) corr[a] = raw[gb + a];
+                if (o->hybrid_state_gradient) {
+                    float mc[4] = {0};
+                    for (uint32_t oa = 0; oa < d; ++oa)
+                        for (uint32_t ia = 0; ia < d; ++ia) mc[oa] += corr[ia] * inv[ia * d + oa];
+                    memcpy(corr, mc, sizeof(corr));
+                }
+                float nin[4] = {0};
+                for (uint32_t a = 0; a < d; ++a) nin[a] = corr[a] * scale;
+                float cadj[4] = {0};
+                if (o->log_norm_grad) log_normalize_adjoint(nin, gadj + gb, cadj, d);
+                else
+                    for (uint32_t a = 0; a < d; ++a) cadj[a] = gadj[gb + a];
+                for (uint32_t a = 0; a < d; ++a) cadj[a] *= scale;
+                float radj[4] = {0};
+                if (o->hybrid_state_gradient) {
+                    for (uint32_t ia = 0; ia < d; ++ia)
+                        for (uint32_t oa = 0; oa < d; ++oa) radj[ia] += cadj[oa] * inv[ia * d + oa];
+                } else {
+                    for (uint32_t a = 0; a < d; ++a) radj[a] = cadj[a];
+                }
+                for (uint32_t a = 0; a < d; ++a) rga[gb + a] = radj[a];
+                if (o->hybrid_state_gradient)
+                    for (uint32_t ia = 0; ia < d; ++ia)
+                        for (uint32_t oa = 0; oa < d; ++oa) inv_adj[ia * d + oa] += raw[gb + ia] * cadj[oa];
+            }
+            float madj[9] = {0};
+            if (o->hybrid_state_gradient) inverse_matrix_adjoint(inv, inv_adj, d, madj);
+            for (size_t k = 0; k < buf.len; ++k) {
+                const neighbor* n = &buf.v[k];
+                if (n->j == idx) continue;
+                float vol = recip_finite(density[n->j]);
+                float vg[4], ug[4];
+                spiky_grad(n->delta, n->r2, cfg, vol, vg);
+                spiky_grad(n->delta, n->r2, cfg, 1.0f, ug);
+                const float* sj = states + (uint64_t)n->j * S;
+                for (uint32_t c = 0; c < S; ++c) {
+                    const uint32_t gb = c * d;
+                    float diff = sj[c] - si[c];
+                    float sc = rga[gb] * vg[0];
+                    for (uint32_t a = 1; a < d; ++a) sc += rga[gb + a] * vg[a];
+                    state_adj[(uint64_t)n->j * S + c] += sc;
+                    state_adj[idx * S + c] -= sc;
+                    float gda[4] = {0};
+                    for (uint32_t a = 0; a < d; ++a) gda[a] = rga[gb + a] * diff;
+                    float da[4];
+                    spiky_delta_adjoint(n->delta, n->r2, cfg, vol, gda, da);
+                    add_delta_position_adjoint(pos_adj, idx, n->j, d, da);
+                    float va = gda[0] * ug[0];
+                    for (uint32_t a = 1; a < d; ++a) va += gda[a] * ug[a];
+                    volume_density_adjoint(density, dens_adj, n->j, va);
+                }
+                if (o->hybrid_state_gradient) {
+                    float dda[4] = {0}, gda[4] = {0};
+                    for (uint32_t r = 0; r < d; ++r)
+                        for (uint32_t cc = 0; cc < d; ++cc) {
+                            float a = madj[r * d + cc];
+                            dda[r] += a * vg[cc];
+                            gda[cc] += a * n->delta[r];
+                        }
+                    float gd[4];
+                    spiky_delta_adjoint(n->delta, n->r2, cfg, vol, gda, gd);
+                    for (uint32_t a = 0; a < d; ++a) dda[a] += gd[a];
+                    add_delta_position_adjoint(pos_adj, idx, n->j, d, dda);
+                    float va = gda[0] * ug[0];
+                    for (uint32_t a = 1; a < d; ++a) va += gda[a] * ug[a];
+                    volume_density_adjoint(density, dens_adj, n->j, va);
+                }
+            }
+            cur += S * d;
+        }
+        if (o->density_grad) { /* adjoint.rs:350-397 */
+            const float* dadj = fa + cur;
+            float rawd[4] = {0};
+            for (size_t k = 0; k < buf.len; ++k) {
+                const neighbor* n = &buf.v[k];
+                if (n->j == idx) continue;
+                float g[4];
+                spiky_grad(n->delta, n->r2, cfg, 1.0f, g);
+                for (uint32_t a = 0; a < d; ++a) rawd[a] += g[a];
+            }
+            float scale = density_gradient_scale(cfg, o, particle_count);
+            float nin[4] = {0};
+            for (uint32_t a = 0; a < d; ++a) nin[a] = rawd[a] * scale;
+            float radj[4] = {0};
+            if (o->log_norm_density_grad) {
+                log_normalize_adjoint(nin, dadj, radj, d);
+                for (uint32_t a = 0; a < d; ++a) radj[a] *= scale;
+            } else {
+                for (uint32_t a = 0; a < d; ++a) radj[a] = dadj[a] * scale;
+            }
+            for (size_t k = 0; k < buf.len; ++k) {
+                const neighbor* n = &buf.v[k];
+                if (n->j == idx) continue;
+                float da[4];
+                spiky_delta_adjoint(n->delta, n->r2, cfg, 1.0f, radj, da);
+                add_delta_position_adjoint(pos_adj, idx, n->j, d, da);
+            }
+            cur += d;
+        }
+        if (o->position_features)
+            for (uint32_t a = 0; a < d; ++a) pos_adj[4 * idx + a] += fa[cur + a];
+    }
+    /* accumulate_density_kernel_position_adjoint (adjoint.rs:399-418) */
+    for (uint64_t idx = 0; idx < total; ++idx) {
+        float adj = dens_adj[idx];
+        if (adj == 0.0f) continue;
+        collect_neighbors(idx, positions, &h.view, cfg, &buf);
+        for (size_t k = 0; k < buf.len; ++k) {
+            const neighbor* n = &buf.v[k];
+            float da[4];
+            poly6_delta_adjoint(n->delta, n->r2, cfg, adj, da);
+            add_delta_position_adjoint(pos_adj, idx, n->j, d, da);
+        }
+    }
+    free(buf.v);
+    hashgrid_free(&h);
+    free(density);
+    free(dens_adj);
+    free(raw);
+    free(rga);
+    return NPA_OK;
+}

@@ -31,6 +31,11 @@
  *                               centroid = projected pixel, second moment = sigma^2,
  *                               depth_sum / alpha = depth), sigmoid against scipy's expit,
  *                               reference test constants (RENDER_MIN/MAX_OPACITY, defaults)
+ *   perceive_adjoint          - the reference's finite-difference tests (lib.rs:123-356) with their
+ *                               fixtures and tolerances; central differences of the oracle's
+ *                               forward at every state and position coordinate of small systems;
+ *                               linearity in the feature adjoint; identity and position-feature
+ *                               rows
  */
 #ifndef NPA_ORACLE_H
 #define NPA_ORACLE_H
@@ -133,6 +138,13 @@ int oracle_splat_projected(const float* projected, const float* colors, const fl
                            const float* sigmas, uint32_t count, const npa_render_cfg* cfg, float* image);
 int oracle_render_attributes(const float* states, uint32_t count, uint32_t state_dims, const npa_render_cfg* cfg,
                              float* colors, float* opacities, float* sigmas, float* derivatives);
+
+/* perceive_adjoint_with_options (crates/burn_automata_kernels/src/reference/adjoint.rs:27-136):
+ * feature_adjoint [total][F] -> state_adjoint [total][S], position_adjoint [total][4]. */
+int oracle_perceive_adjoint(const float* positions, const float* states, uint32_t batch_size,
+                            uint32_t particle_count, uint32_t state_dims, const npa_grid_cfg* cfg,
+                            const npa_perception_opts* opts, const float* feature_adjoint,
+                            float* state_adjoint, float* position_adjoint);
 
 /* Per-phase wall-clock seconds of the last oracle_step / oracle_rollout call
  * (hashgrid+perceive, MLP+gates+integrate, 0), following profile_rollout

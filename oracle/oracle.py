@@ -91,6 +91,8 @@ def _declare(L):
     L.oracle_decode_gaussians_3d.argtypes = [P, P, u32, u32,
                                              C.POINTER(_abi.NpaGaussianDecodeCfg), P, P, P, P]
     L.oracle_splat_particles_2d.argtypes = [P, P, u32, C.POINTER(_abi.NpaSplat2dCfg), P]
+    L.oracle_perceive_adjoint.argtypes = [P, P, u32, u32, u32, C.POINTER(_abi.NpaGridCfg),
+                                          C.POINTER(_abi.NpaPerceptionOpts), P, P, P]
     L.oracle_view_basis.argtypes = [u32, P, P, P]
     L.oracle_project_positions.argtypes = [u32, P, u32, f32, P]
     L.oracle_splat_projected.argtypes = [P, P, P, P, u32, C.POINTER(_abi.NpaRenderCfg), P]
@@ -216,6 +218,45 @@ def perceive_with_options(positions, states, batch_size, particle_count, state_d
                                  _ptr(dens), _ptr(blur), _ptr(sg) if sg.size else None,
                                  _ptr(dg) if dg.size else None))
     return PerceptionOutput(feats, dens, blur, sg, dg, F)
+
+
+@dataclass
+class PerceptionAdjointOutput:
+    """PerceptionAdjointOutput (crates/burn_automata_kernels/src/reference/types.rs:43-47)."""
+
+    state: np.ndarray     # [total * S]
+    position: np.ndarray  # [total, 4]
+
+
+def perceive_adjoint_with_options(positions, states, batch_size, particle_count, state_dims,
+                                  cfg: HashGridConfig, options: PerceptionOptions,
+                                  feature_adjoint) -> PerceptionAdjointOutput:
+    """perceive_adjoint_with_options (reference/adjoint.rs:27-136)."""
+    pos = _f32(positions, (-1, 4))
+    st = _f32(states).reshape(-1)
+    total = batch_size * particle_count
+    if pos.shape[0] != total:
+        raise _abi.PositionShape(f"positions {pos.shape[0]} != {total}")
+    if st.size != total * state_dims:
+        raise _abi.StateShape(f"states {st.size} != {total * state_dims}")
+    F = options.feature_dims(state_dims, cfg.dim)
+    fa = _f32(feature_adjoint).reshape(-1)
+    if fa.size != total * F:
+        raise _abi.OutputShape(f"feature adjoint {fa.size} != {total * F}")
+    sa = np.zeros(total * state_dims, np.float32)
+    pa = np.zeros((total, 4), np.float32)
+    _check(lib().oracle_perceive_adjoint(_ptr(pos), _ptr(st), batch_size, particle_count, state_dims,
+                                         C.byref(cfg.to_c()), C.byref(options.to_c()), _ptr(fa),
+                                         _ptr(sa), _ptr(pa)))
+    return PerceptionAdjointOutput(sa, pa)
+
+
+def perceive_state_adjoint_with_options(positions, states, batch_size, particle_count, state_dims,
+                                        cfg: HashGridConfig, options: PerceptionOptions,
+                                        feature_adjoint) -> np.ndarray:
+    """perceive_state_adjoint_with_options (reference/adjoint.rs:3-25)."""
+    return perceive_adjoint_with_options(positions, states, batch_size, particle_count, state_dims,
+                                         cfg, options, feature_adjoint).state
 
 
 def perceive(positions, states, batch_size, particle_count, state_dims, cfg: HashGridConfig,

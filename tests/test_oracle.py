@@ -1023,3 +1023,139 @@ def test_render_defaults_match_the_reference():
     st[0, 8], st[1, 8] = 40.0, -40.0
     _, op, _, _ = O.render_attributes(st, 16, c)
     np.testing.assert_array_equal(op, np.array([0.95, 0.001], f32))
+
+
+# ------------------------------------------------------------------ perception adjoint
+def _adjoint_fixture(eps):
+    cfg = HashGridConfig(3, Boundary.Clamped, HashGridMode.Particle, (8, 8, 8), eps, 16)
+    states = np.array([0.10, -0.20, 0.05, 0.30, 0.15, -0.10, -0.25, 0.35, 0.20, 0.05, -0.30, 0.40], f32)
+    return cfg, states
+
+
+def _opts(cfg, hybrid, position_features):
+    return PerceptionOptions(state_grad=True, density_grad=True, eps0=cfg.eps, scale_equivariance=True,
+                             particle_density_equivariance=True, log_norm_grad=True,
+                             log_norm_density_grad=True, hybrid_state_gradient=hybrid,
+                             position_features=position_features)
+
+
+def _loss(pos, st, n, S, cfg, opts, fa):
+    """sum(features * feature_adjoint), the scalar the reference's finite differences use."""
+    f = O.perceive_with_options(pos, st, 1, n, S, cfg, opts).features.astype(np.float64)
+    return float((f.ravel() * fa.astype(np.float64)).sum())
+
+
+def test_adjoint_reference_state_finite_difference():
+    """perceive_state_adjoint_matches_finite_difference (lib.rs:123-198), its fixture and bound."""
+    cfg, st = _adjoint_fixture(0.35)
+    pos = np.array([[0, 0, 0, 0], [0.12, 0.04, -0.03, 0], [-0.08, 0.10, 0.02, 0], [0.04, -0.09, 0.11, 0]], f32)
+    opts = _opts(cfg, True, False)
+    F = opts.feature_dims(3, 3)
+    fa = (np.sin((np.arange(4 * F, dtype=f32) + f32(1)) * f32(0.017)) * f32(0.1)).astype(f32)
+    adj = O.perceive_state_adjoint_with_options(pos, st, 1, 4, 3, cfg, opts, fa)
+    e = 1e-3
+    p, m = st.copy(), st.copy()
+    p[4] += f32(e)
+    m[4] -= f32(e)
+    fd = (_loss(pos, p, 4, 3, cfg, opts, fa) - _loss(pos, m, 4, 3, cfg, opts, fa)) / (2 * e)
+    assert abs(adj[4] - fd) <= 2e-3, (adj[4], fd)
+
+
+@pytest.mark.parametrize("hybrid,particle,axis,tol,phase,amp,shift", [
+    (False, 1, 0, 7.5e-2, 0.013, 0.05, 3.0),   # lib.rs:201-277
+    (True, 2, 1, 2.5e-1, 0.011, 0.03, 5.0),    # lib.rs:280-356
+])
+def test_adjoint_reference_position_finite_difference(hybrid, particle, axis, tol, phase, amp, shift):
+    """perceive_position_adjoint_matches_finite_difference_{without,with}_hybrid_moment."""
+    cfg, st = _adjoint_fixture(0.40)
+    pos = np.array([[0, 0, 0, 0], [0.11, 0.03, -0.02, 0], [-0.07, 0.09, 0.04, 0], [0.05, -0.08, 0.10, 0]], f32)
+    opts = _opts(cfg, hybrid, True)
+    F = opts.feature_dims(3, 3)
+    k = np.arange(4 * F, dtype=f32) + f32(shift)
+    fa = ((np.sin(k * f32(phase)) if hybrid else np.cos(k * f32(phase))) * f32(amp)).astype(f32)
+    adj = O.perceive_adjoint_with_options(pos, st, 1, 4, 3, cfg, opts, fa)
+    e = 1e-4
+    p, m = pos.copy(), pos.copy()
+    p[particle, axis] += f32(e)
+    m[particle, axis] -= f32(e)
+    fd = (_loss(p, st, 4, 3, cfg, opts, fa) - _loss(m, st, 4, 3, cfg, opts, fa)) / (2 * e)
+    assert abs(adj.position[particle, axis] - fd) <= tol, (adj.position[particle, axis], fd)
+
+
+ADJOINT_CASES = {
+    # name: (dim, boundary, hybrid, state_grad, density_grad, log_norm, position_features)
+    "2d_growing": (2, Boundary.Clamped, False, True, False, True, False),
+    "2d_hybrid_dgrad": (2, Boundary.Clamped, True, True, True, True, True),
+    "2d_periodic_plain": (2, Boundary.Periodic, False, True, True, False, False),
+    "3d_hybrid": (3, Boundary.Clamped, True, True, True, True, True),
+    "3d_blur_only": (3, Boundary.Clamped, False, False, False, False, True),
+}
+
+
+def _adjoint_case(name, n=14, S=3, seed=0):
+    dim, bnd, hyb, sg, dg, ln, pf = ADJOINT_CASES[name]
+    eps = 0.5
+    gs = (4, 4, 4 if dim == 3 else 1)
+    cfg = HashGridConfig(dim, bnd, HashGridMode.Grid, gs, eps, 16)
+    rng = np.random.default_rng(seed)
+    pos = np.zeros((n, 4), f32)
+    lo = 0.55 if bnd == Boundary.Periodic else 0.05
+    pos[:, :dim] = rng.uniform(lo, lo + 0.45, (n, dim))  # dense: every moment matrix well conditioned
+    st = rng.normal(0, 0.5, n * S).astype(f32)
+    opts = PerceptionOptions(state_grad=sg, density_grad=dg, eps0=0.35, scale_equivariance=True,
+                             particle_density_equivariance=True, log_norm_grad=ln,
+                             log_norm_density_grad=ln, hybrid_state_gradient=hyb, position_features=pf)
+    F = opts.feature_dims(S, dim)
+    fa = rng.normal(0, 0.1, n * F).astype(f32)
+    return cfg, pos, st, opts, fa, n, S, dim
+
+
+@pytest.mark.parametrize("name", sorted(ADJOINT_CASES))
+def test_adjoint_is_the_gradient_of_the_forward(name):
+    """Every state and position coordinate against central differences of the oracle's forward
+    (states: step 3e-3; positions: 1e-3; f32 forward, float64 loss).
+    A dropped or mis-signed term of adjoint.rs shows up as an O(1) relative error."""
+    cfg, pos, st, opts, fa, n, S, dim = _adjoint_case(name)
+    adj = O.perceive_adjoint_with_options(pos, st, 1, n, S, cfg, opts, fa)
+    fd_s = np.zeros(n * S)
+    for k in range(n * S):
+        p, m = st.copy(), st.copy()
+        p[k] += f32(3e-3)
+        m[k] -= f32(3e-3)
+        fd_s[k] = (_loss(pos, p, n, S, cfg, opts, fa) - _loss(pos, m, n, S, cfg, opts, fa)) / (
+            float(p[k]) - float(m[k]))
+    fd_p = np.zeros((n, dim))
+    for i in range(n):
+        for a in range(dim):
+            p, m = pos.copy(), pos.copy()
+            p[i, a] += f32(1e-3)
+            m[i, a] -= f32(1e-3)
+            fd_p[i, a] = (_loss(p, st, n, S, cfg, opts, fa) - _loss(m, st, n, S, cfg, opts, fa)) / (
+                float(p[i, a]) - float(m[i, a]))
+    es = np.abs(adj.state - fd_s).max() / np.abs(fd_s).max()
+    ep = np.abs(adj.position[:, :dim] - fd_p).max() / np.abs(fd_p).max()
+    assert es < 1e-3 and ep < 1e-2, (es, ep)
+    assert not adj.position[:, dim:].any()
+
+
+def test_adjoint_is_linear_and_carries_identity_rows():
+    cfg, pos, st, opts, fa, n, S, dim = _adjoint_case("2d_hybrid_dgrad")
+    F = opts.feature_dims(S, dim)
+    rng = np.random.default_rng(9)
+    fb = rng.normal(0, 0.1, n * F).astype(f32)
+    a = O.perceive_adjoint_with_options(pos, st, 1, n, S, cfg, opts, fa)
+    b = O.perceive_adjoint_with_options(pos, st, 1, n, S, cfg, opts, fb)
+    ab = O.perceive_adjoint_with_options(pos, st, 1, n, S, cfg, opts, fa + fb)
+    assert rel(ab.state, a.state.astype(np.float64) + b.state) < 1e-5
+    assert rel(ab.position, a.position.astype(np.float64) + b.position) < 1e-5
+    # only the identity rows set: state adjoint == those rows; only the position rows: position
+    only = np.zeros((n, F), f32)
+    only[:, :S] = fa.reshape(n, F)[:, :S]
+    r = O.perceive_adjoint_with_options(pos, st, 1, n, S, cfg, opts, only)
+    np.testing.assert_array_equal(r.state, only[:, :S].ravel())
+    assert not r.position.any()
+    only = np.zeros((n, F), f32)
+    only[:, F - dim:] = fa.reshape(n, F)[:, F - dim:]
+    r = O.perceive_adjoint_with_options(pos, st, 1, n, S, cfg, opts, only)
+    np.testing.assert_array_equal(r.position[:, :dim], only[:, F - dim:])
+    assert not r.state.any()

@@ -61,6 +61,19 @@ MUTANTS = {
                                "fmaxf(sigmas[n], RENDER_EPS)"),
     "opacity_channel": ("S > 8 ? 8 : (S > 3 ? 3 : -1)", "S > 8 ? 7 : (S > 3 ? 3 : -1)"),
     "sigmoid_sign": ("return 1.0f / (1.0f + expf(-v));", "return 1.0f / (1.0f + expf(v));"),
+    "adj_poly6_factor": ("out[a] = out_adj * dk * 2.0f * delta[a];", "out[a] = out_adj * dk * delta[a];"),
+    "adj_spiky_radial": ("out[a] = scale * out_adj[a] + dscale_dr * dot * delta[a] / r;", "out[a] = scale * out_adj[a];"),
+    "adj_log_radial": ("in_adj[k] += scale * out_adj[k] + radial * in[k];", "in_adj[k] += scale * out_adj[k];"),
+    "adj_volume_sign": ("density_adj[j] -= v_adj / (rho * rho);", "density_adj[j] += v_adj / (rho * rho);"),
+    "adj_position_sign": ("pos_adj[4 * lhs + a] -= d_adj[a];", "pos_adj[4 * lhs + a] += d_adj[a];"),
+    "adj_inverse_transpose": ("v += inv[ir * d + row] * inv_adj[ir * d + ic] * inv[col * d + ic];",
+                              "v += inv[row * d + ir] * inv_adj[ir * d + ic] * inv[col * d + ic];"),
+    "adj_self_gradient": ("state_adj[idx * S + c] -= sc;", "(void)sc;"),
+    "adj_blur_weight": ("state_adj[(uint64_t)n->j * S + c] += badj[c] * w;", "state_adj[(uint64_t)n->j * S + c] += badj[c] * kern;"),
+    "adj_density_kernel_pass": ("poly6_delta_adjoint(n->delta, n->r2, cfg, adj, da);", "poly6_delta_adjoint(n->delta, n->r2, cfg, 0.0f, da);"),
+    "adj_hybrid_grad": ("gda[cc] += a * n->delta[r];", "gda[cc] += 0.0f * n->delta[r];"),
+    "adj_dgrad_scale": ("for (uint32_t a = 0; a < d; ++a) radj[a] *= scale;\n            } else {",
+                        "for (uint32_t a = 0; a < d; ++a) radj[a] *= 1.0f;\n            } else {"),
     "render_learned_channel": ("float logit = clamp_f32(s[S - 5]", "float logit = clamp_f32(s[S - 4]"),
     "decode_learned_channel": ("float scale_logit = clamp_f32(s[S - 5]", "float scale_logit = clamp_f32(s[S - 6]"),
     "decode_opacity_channel": ("float opacity_logit = clamp_f32(s[S - 4]", "float opacity_logit = clamp_f32(s[S - 5]"),
