@@ -1032,7 +1032,7 @@ def _adjoint_fixture(eps):
     return cfg, states
 
 
-def _opts(cfg, hybrid, position_features):
+def _adj_opts(cfg, hybrid, position_features):
     return PerceptionOptions(state_grad=True, density_grad=True, eps0=cfg.eps, scale_equivariance=True,
                              particle_density_equivariance=True, log_norm_grad=True,
                              log_norm_density_grad=True, hybrid_state_gradient=hybrid,
@@ -1049,7 +1049,7 @@ def test_adjoint_reference_state_finite_difference():
     """perceive_state_adjoint_matches_finite_difference (lib.rs:123-198), its fixture and bound."""
     cfg, st = _adjoint_fixture(0.35)
     pos = np.array([[0, 0, 0, 0], [0.12, 0.04, -0.03, 0], [-0.08, 0.10, 0.02, 0], [0.04, -0.09, 0.11, 0]], f32)
-    opts = _opts(cfg, True, False)
+    opts = _adj_opts(cfg, True, False)
     F = opts.feature_dims(3, 3)
     fa = (np.sin((np.arange(4 * F, dtype=f32) + f32(1)) * f32(0.017)) * f32(0.1)).astype(f32)
     adj = O.perceive_state_adjoint_with_options(pos, st, 1, 4, 3, cfg, opts, fa)
@@ -1069,7 +1069,7 @@ def test_adjoint_reference_position_finite_difference(hybrid, particle, axis, to
     """perceive_position_adjoint_matches_finite_difference_{without,with}_hybrid_moment."""
     cfg, st = _adjoint_fixture(0.40)
     pos = np.array([[0, 0, 0, 0], [0.11, 0.03, -0.02, 0], [-0.07, 0.09, 0.04, 0], [0.05, -0.08, 0.10, 0]], f32)
-    opts = _opts(cfg, hybrid, True)
+    opts = _adj_opts(cfg, hybrid, True)
     F = opts.feature_dims(3, 3)
     k = np.arange(4 * F, dtype=f32) + f32(shift)
     fa = ((np.sin(k * f32(phase)) if hybrid else np.cos(k * f32(phase))) * f32(amp)).astype(f32)

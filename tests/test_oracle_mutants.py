@@ -66,8 +66,8 @@ MUTANTS = {
     "adj_log_radial": ("in_adj[k] += scale * out_adj[k] + radial * in[k];", "in_adj[k] += scale * out_adj[k];"),
     "adj_volume_sign": ("density_adj[j] -= v_adj / (rho * rho);", "density_adj[j] += v_adj / (rho * rho);"),
     "adj_position_sign": ("pos_adj[4 * lhs + a] -= d_adj[a];", "pos_adj[4 * lhs + a] += d_adj[a];"),
-    "adj_inverse_transpose": ("v += inv[ir * d + row] * inv_adj[ir * d + ic] * inv[col * d + ic];",
-                              "v += inv[row * d + ir] * inv_adj[ir * d + ic] * inv[col * d + ic];"),
+    # (transposing either factor is no mistake: the inverse and the moment matrix are symmetric)
+    "adj_inverse_adjoint_sign": ("            m_adj[row * d + col] -= v;", "            m_adj[row * d + col] += v;"),
     "adj_self_gradient": ("state_adj[idx * S + c] -= sc;", "(void)sc;"),
     "adj_blur_weight": ("state_adj[(uint64_t)n->j * S + c] += badj[c] * w;", "state_adj[(uint64_t)n->j * S + c] += badj[c] * kern;"),
     "adj_density_kernel_pass": ("poly6_delta_adjoint(n->delta, n->r2, cfg, adj, da);", "poly6_delta_adjoint(n->delta, n->r2, cfg, 0.0f, da);"),
