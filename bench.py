@@ -16,7 +16,8 @@ Prints ONE JSON line with the driver's fields plus:
                   a bounded sample of the same workload on this host's cores.
 
 --workload c3 / c4 / c5 time BASELINE's other rollout workloads the same way; --workload render
-times the projected 3D render of a device-resident C4 state (particle-views/s, see bench_render).
+times the projected 3D render of a device-resident C4 state (particle-views/s, see bench_render);
+--workload adjoint times the perception adjoint on C2's particles (see bench_adjoint).
 """
 from __future__ import annotations
 
@@ -239,6 +240,101 @@ def bench_render(args, torch) -> int:
     return 0
 
 
+def adjoint_work(S: int, d: int, hybrid: bool, state_grad: bool, density_grad: bool, pairs: float,
+                 particles: float) -> float:
+    """fp32 operations of perceive_adjoint_with_options (adjoint.rs), each add/sub/mul/div/sqrt
+    counted once, per ordered accepted pair (self pairs included; they cost the same to visit):
+      density pass           10                 (delta, r^2, poly6, sum)
+      blurred state          14 + 4S + 5d       (poly6 and its delta adjoint, weight and
+                                                 state terms per channel, volume adjoint)
+      gradient, first walk   8 + d + S(1 + 2d) + [hybrid] 2d^2
+      gradient, second walk  15 + 2d + S(14 + 14d) + [hybrid] 4d^2 + 12d + 13
+      density gradient       2 x (10 + 9d)      (its forward sum and the delta adjoint)
+      density kernel         4 + 5d
+    plus per particle S(6d^2 + 5d + 32) + 120 (moment correction, log-norm adjoint with its
+    log1p, inverse and inverse adjoint)."""
+    per_pair = 10 + 14 + 4 * S + 5 * d + 4 + 5 * d
+    if state_grad:
+        per_pair += 8 + d + S * (1 + 2 * d) + (2 * d * d if hybrid else 0)
+        per_pair += 15 + 2 * d + S * (14 + 14 * d) + ((4 * d * d + 12 * d + 13) if hybrid else 0)
+    if density_grad:
+        per_pair += 2 * (10 + 9 * d)
+    per_particle = S * (6 * d * d + 5 * d + 32) + 120
+    return pairs * per_pair + particles * per_particle
+
+
+def bench_adjoint(args, torch) -> int:
+    """The perception adjoint (perceive_adjoint_with_options, adjoint.rs:27-136) of C2's 65,536
+    particles with the growing-2D model's perception options and a seeded synthetic feature
+    adjoint: one call = hashgrid build + the four adjoint passes."""
+    import numpy as np
+
+    from burn_automata_amd import kernels as K
+    from burn_automata_amd import synthetic as syn
+    from burn_automata_amd.runtime import default_context
+
+    w = syn.workload("c2", particles=args.particles)
+    m, g = w["model"], w["grid"]
+    opts = m.perception_options()
+    n, S, d = w["n"], m.state_dims, g.dim
+    F = opts.feature_dims(S, d)
+    rng = np.random.default_rng(11)
+    pos = torch.from_numpy(w["positions"]).cuda()
+    st = torch.from_numpy(w["states"]).cuda()
+    fa_np = rng.normal(0.0, 0.1, n * F).astype(np.float32)
+    fa = torch.from_numpy(fa_np).cuda()
+    ctx = default_context()
+    for _ in range(args.warmup):
+        K.perceive_adjoint_with_options(pos, st, 1, n, S, g, opts, fa, ctx=ctx)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = K.perceive_adjoint_with_options(pos, st, 1, n, S, g, opts, fa, ctx=ctx)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    finite = bool(torch.isfinite(out.state).all().item() and torch.isfinite(out.position).all().item())
+    off, _ = K.neighbor_lists(pos, 1, n, g, ctx=ctx)
+    pairs = float(off[-1].item())
+    ms = 1000.0 * elapsed / args.steps
+    flops = adjoint_work(S, d, opts.hybrid_state_gradient, opts.state_grad, opts.density_grad, pairs, n)
+    achieved = flops / (ms * 1e-3) / 1e12
+    line = {
+        "metric": "particle-adjoints/sec, perception adjoint (training backward of the perception)",
+        "value": n * args.steps / elapsed, "unit": "particle-adjoints/sec", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (C2 seeded particles and states; feature adjoint N(0, 0.1^2))",
+        "config": {"workload": (f"adjoint: C2 particles ({n}), S={S}, F={F}, growing-2D perception "
+                                f"options (state gradient, hybrid moment, log-norm), eps={g.eps}"),
+                   "particles": n, "pairs": pairs, "outputs_finite": finite},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_FP32_TFLOPS, "traffic": None,
+                     "kernel": "whole call (hashgrid build + k_adj_density, k_adj_prep, k_adj_gather, "
+                               "k_adj_density_kernel)",
+                     "engine": "fp32 VALU", "mean_launch_ms": ms, "flops_per_launch": flops,
+                     "timing": "wall clock over the timed calls (synchronised on both sides)"},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+
+        O.build()
+        pos_np, st_np = w["positions"], w["states"]
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            O.perceive_adjoint_with_options(pos_np, st_np, 1, n, S, g, opts, fa_np)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= min(args.cpu_seconds, 20.0) or reps >= 32:
+                break
+        line["cpu_baseline"] = {
+            "value": n * reps / el, "unit": "particle-adjoints/sec", "cores": 1, "kind": "port",
+            "sample": (f"{reps} calls of oracle perceive_adjoint_with_options on the same inputs "
+                       f"(serial like the reference's loop, one thread, {el:.1f} s)")}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def copy_calibration(torch, mib: float) -> int:
     n = int(mib * (1 << 20)) // 4
     src = torch.rand(n, device="cuda")
@@ -301,6 +397,8 @@ def main(argv=None) -> int:
         return copy_calibration(torch, args.copy_calibration)
     if args.workload == "render":
         return bench_render(args, torch)
+    if args.workload == "adjoint":
+        return bench_adjoint(args, torch)
 
     from burn_automata_amd import kernels as K
     from burn_automata_amd import synthetic as syn

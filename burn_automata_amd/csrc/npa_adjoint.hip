@@ -7,8 +7,10 @@
 // the same cell offsets negated, the same r^2 < eps^2 test on the negated delta), so a particle
 // k receives, walking its own neighbour list, every term the reference adds into k - both the
 // terms of the pairs where k is the neighbour j of idx = that neighbour, and the terms where k
-// is idx. No atomics; the result is deterministic and equals the reference's up to the order in
-// which each particle's sums are added.
+// is idx. No atomics; the result is deterministic and equals the reference's up to rounding:
+// each particle adds its terms in its own neighbour order, and the state-gradient terms of a pair
+// sum their channels' gradient adjoints before the (linear) spiky delta adjoint, which the
+// reference applies once per channel.
 //
 //   k_adj_density  rho_k over the walk, as the forward density pass          forward.rs:145-160
 //   k_adj_prep     per particle: the forward state-gradient sums and moment matrix, then the
@@ -48,25 +50,6 @@ __device__ __forceinline__ void poly6_delta_adjoint(const float* d, float r2, co
     const float dk = -3.0f * g.k6 * x * x;
 #pragma unroll
     for (int a = 0; a < D; ++a) out[a] = adj * dk * 2.0f * d[a];
-}
-
-// spiky_gradient_delta_adjoint  kernels.rs:100-126
-template <int D>
-__device__ __forceinline__ void spiky_delta_adjoint(const float* d, float r2, const GridParams& g, float coeff,
-                                                    const float* adj, float* out) {
-#pragma unroll
-    for (int a = 0; a < D; ++a) out[a] = 0.0f;
-    if (r2 <= 0.0f || r2 >= g.eps2) return;
-    const float r = sqrtf(r2);
-    const float norm = coeff * g.k5 * 3.0f;
-    const float t = g.eps - r;
-    const float scale = norm * (t * t) / r;
-    const float dscale_dr = norm * (1.0f - (g.eps * g.eps) / r2);
-    float dot = adj[0] * d[0];
-#pragma unroll
-    for (int a = 1; a < D; ++a) dot += adj[a] * d[a];
-#pragma unroll
-    for (int a = 0; a < D; ++a) out[a] = scale * adj[a] + dscale_dr * dot * d[a] / r;
 }
 
 // log_normalize_adjoint  normalize.rs:71-91 (adds into in_adj)
@@ -127,27 +110,75 @@ __global__ __launch_bounds__(256) void k_adj_density(StepParams P, AdjointArgs A
     A.sdens[s] = rho;
 }
 
+// A particle's channels are split over a group of L = SM / kCpl lanes (lane l owns channels
+// l * kCpl .. l * kCpl + kCpl - 1): pair-level quantities are computed by every lane of the group,
+// per-channel terms by the channel's lane, and sums across channels are combined in a fixed
+// butterfly within the group, so results stay deterministic.
+constexpr int kCpl = 4;
+
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int m = L / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, L);
+    return v;
+}
+
+// spiky_gradient_delta_adjoint (kernels.rs:100-126), split: its pair-level part for one
+// coefficient (spiky_pre) and the per-channel part - the same operations on the same values as
+// the reference's one call per channel.
+struct SpikyPre {
+    float r, scale, dscale;
+    bool live;
+};
+__device__ __forceinline__ SpikyPre spiky_pre(float r2, const GridParams& g, float coeff) {
+    SpikyPre q{0.0f, 0.0f, 0.0f, false};
+    if (r2 <= 0.0f || r2 >= g.eps2) return q;
+    q.live = true;
+    q.r = sqrtf(r2);
+    const float norm = coeff * g.k5 * 3.0f;
+    const float t = g.eps - q.r;
+    q.scale = norm * (t * t) / q.r;
+    q.dscale = norm * (1.0f - (g.eps * g.eps) / r2);
+    return q;
+}
+template <int D>
+__device__ __forceinline__ void spiky_delta_adjoint_pre(const float* d, const SpikyPre& q, const float* adj,
+                                                        float* out) {
+#pragma unroll
+    for (int a = 0; a < D; ++a) out[a] = 0.0f;
+    if (!q.live) return;
+    float dot = adj[0] * d[0];
+#pragma unroll
+    for (int a = 1; a < D; ++a) dot += adj[a] * d[a];
+#pragma unroll
+    for (int a = 0; a < D; ++a) out[a] = q.scale * adj[a] + q.dscale * dot * d[a] / q.r;
+}
+
 template <int D, int SM>
 __global__ __launch_bounds__(256) void k_adj_prep(StepParams P, AdjointArgs A) {
-    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= P.T) return;
+    constexpr int L = SM / kCpl;
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t s = t / L, lane = t % L;
+    if (s >= P.T) return;  // whole groups leave together
     const uint32_t b = s / P.N;
     const uint64_t pk = (uint64_t)b * P.N + A.perm[s];
     const uint32_t S = P.S;
+    const int c0 = (int)lane * kCpl;
     const float* fa = A.fadj + pk * P.F;
 #pragma unroll
-    for (int c = 0; c < SM; ++c)
-        if (c < (int)S) A.sfb[(uint64_t)s * P.SS + c] = fa[S + c];
+    for (int u = 0; u < kCpl; ++u)
+        if (c0 + u < (int)S) A.sfb[(uint64_t)s * P.SS + c0 + u] = fa[S + c0 + u];
     float pi[3];
     int ci[3];
     load_rec<D>(A.srec, A.scoord, s, pi, ci);
-    const float* si = A.sstate + (uint64_t)s * P.SS;
+    const bool rowlane = c0 < (int)P.SS;  // lanes past the padded row (S <= 4 or S > 16) own no channel
+    const float* si = A.sstate + (uint64_t)s * P.SS + c0;
     uint32_t cur = 2 * S;
     if (P.state_grad) {
-        float raw[SM * D];
+        float raw[kCpl * D];
         float moment[D * D];
 #pragma unroll
-        for (int k = 0; k < SM * D; ++k) raw[k] = 0.0f;
+        for (int k = 0; k < kCpl * D; ++k) raw[k] = 0.0f;
 #pragma unroll
         for (int k = 0; k < D * D; ++k) moment[k] = 0.0f;
         walk_neighbors<D>(P.g, b, pi, ci, A.bo, A.srec, A.scoord, [&](uint32_t j, const float* d, float r2) {
@@ -155,13 +186,14 @@ __global__ __launch_bounds__(256) void k_adj_prep(StepParams P, AdjointArgs A) {
             const float vol = recip_finite(A.sdens[j]);
             float g[D];
             spiky<D>(d, r2, P.g, vol, g);
-            const float* sj = A.sstate + (uint64_t)j * P.SS;
+            if (rowlane) {
+                const float* sj = A.sstate + (uint64_t)j * P.SS + c0;
 #pragma unroll
-            for (int c = 0; c < SM; ++c) {
-                if (c >= (int)S) continue;
-                const float diff = sj[c] - si[c];
+                for (int u = 0; u < kCpl; ++u) {
+                    const float diff = sj[u] - si[u];
 #pragma unroll
-                for (int a = 0; a < D; ++a) raw[c * D + a] += diff * g[a];
+                    for (int a = 0; a < D; ++a) raw[u * D + a] += diff * g[a];
+                }
             }
             if (P.hybrid) {
 #pragma unroll
@@ -179,11 +211,12 @@ __global__ __launch_bounds__(256) void k_adj_prep(StepParams P, AdjointArgs A) {
         const float* gadj = fa + cur;
         float* rg = A.rga + (uint64_t)s * P.SS * D;
 #pragma unroll
-        for (int c = 0; c < SM; ++c) {
+        for (int u = 0; u < kCpl; ++u) {
+            const int c = c0 + u;
             if (c >= (int)S) continue;
             float corr[D];
 #pragma unroll
-            for (int a = 0; a < D; ++a) corr[a] = raw[c * D + a];
+            for (int a = 0; a < D; ++a) corr[a] = raw[u * D + a];
             if (P.hybrid) {
                 float mc[D];
 #pragma unroll
@@ -219,7 +252,7 @@ __global__ __launch_bounds__(256) void k_adj_prep(StepParams P, AdjointArgs A) {
 #pragma unroll
                 for (int ia = 0; ia < D; ++ia)
 #pragma unroll
-                    for (int o = 0; o < D; ++o) inv_adj[ia * D + o] += raw[c * D + ia] * cadj[o];
+                    for (int o = 0; o < D; ++o) inv_adj[ia * D + o] += raw[u * D + ia] * cadj[o];
             } else {
 #pragma unroll
                 for (int a = 0; a < D; ++a) radj[a] = cadj[a];
@@ -227,23 +260,27 @@ __global__ __launch_bounds__(256) void k_adj_prep(StepParams P, AdjointArgs A) {
 #pragma unroll
             for (int a = 0; a < D; ++a) rg[c * D + a] = radj[a];
         }
-        if (P.hybrid) {  // inverse_matrix_adjoint  adjoint.rs:447-468
-            float* m = A.madj + (uint64_t)s * 9;
+        if (P.hybrid) {  // inverse_matrix_adjoint  adjoint.rs:447-468, inv_adj summed over the group
 #pragma unroll
-            for (int row = 0; row < D; ++row)
+            for (int k = 0; k < D * D; ++k) inv_adj[k] = group_sum<L>(inv_adj[k]);
+            if (lane == 0) {
+                float* m = A.madj + (uint64_t)s * 9;
 #pragma unroll
-                for (int col = 0; col < D; ++col) {
-                    float v = 0.0f;
+                for (int row = 0; row < D; ++row)
 #pragma unroll
-                    for (int ir = 0; ir < D; ++ir)
+                    for (int col = 0; col < D; ++col) {
+                        float v = 0.0f;
 #pragma unroll
-                        for (int ic = 0; ic < D; ++ic) v += inv[ir * D + row] * inv_adj[ir * D + ic] * inv[col * D + ic];
-                    m[row * D + col] = 0.0f - v;
-                }
+                        for (int ir = 0; ir < D; ++ir)
+#pragma unroll
+                            for (int ic = 0; ic < D; ++ic) v += inv[ir * D + row] * inv_adj[ir * D + ic] * inv[col * D + ic];
+                        m[row * D + col] = 0.0f - v;
+                    }
+            }
         }
         cur += S * D;
     }
-    if (P.density_grad) {  // adjoint.rs:350-397
+    if (P.density_grad && lane == 0) {  // adjoint.rs:350-397
         float rawd[D];
 #pragma unroll
         for (int a = 0; a < D; ++a) rawd[a] = 0.0f;
@@ -277,21 +314,29 @@ __global__ __launch_bounds__(256) void k_adj_prep(StepParams P, AdjointArgs A) {
 
 // The pair terms of both roles, gathered by the receiving particle k (slot s). For a neighbour j
 // with delta d = p_j - p_k, the pair seen from j is delta -d (exact: IEEE subtraction and the
-// periodic wrap are sign-symmetric) with the same r^2.
+// periodic wrap are sign-symmetric) with the same r^2. Pair-level terms are added by lane 0 of
+// the group, per-channel terms by the channel's lane; the position and density adjoints are
+// summed over the group at the end.
 template <int D, int SM>
 __global__ __launch_bounds__(256) void k_adj_gather(StepParams P, AdjointArgs A) {
-    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= P.T) return;
+    constexpr int L = SM / kCpl;
+    const uint32_t tid = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t s = tid / L, lane = tid % L;
+    if (s >= P.T) return;  // whole groups leave together
     const uint32_t b = s / P.N;
     const uint64_t pk = (uint64_t)b * P.N + A.perm[s];
     const uint32_t S = P.S;
+    const int c0 = (int)lane * kCpl;
+    const bool lead = lane == 0;
+    const bool rowlane = c0 < (int)P.SS;  // lanes past the padded row own no channel
     const float* fa = A.fadj + pk * P.F;
-    float acc[SM], sk[SM], fbk[SM];
+    float acc[kCpl], sk[kCpl], fbk[kCpl];
 #pragma unroll
-    for (int c = 0; c < SM; ++c) {
-        acc[c] = c < (int)S ? fa[c] : 0.0f;  // the identity rows (adjoint.rs:68-71)
-        sk[c] = A.sstate[(uint64_t)s * P.SS + c];
-        fbk[c] = c < (int)S ? A.sfb[(uint64_t)s * P.SS + c] : 0.0f;
+    for (int u = 0; u < kCpl; ++u) {
+        const int c = c0 + u;
+        acc[u] = c < (int)S ? fa[c] : 0.0f;  // the identity rows (adjoint.rs:68-71)
+        sk[u] = rowlane ? A.sstate[(uint64_t)s * P.SS + c] : 0.0f;
+        fbk[u] = c < (int)S ? A.sfb[(uint64_t)s * P.SS + c] : 0.0f;
     }
     const float rho_k = A.sdens[s];
     const float vol_k = recip_finite(rho_k);
@@ -317,72 +362,96 @@ __global__ __launch_bounds__(256) void k_adj_gather(StepParams P, AdjointArgs A)
         for (int a = 0; a < D; ++a) dn[a] = -d[a];
         const float rho_j = A.sdens[j];
         const float vol_j = recip_finite(rho_j);
-        const float* sj = A.sstate + (uint64_t)j * P.SS;
-        const float* fbj = A.sfb + (uint64_t)j * P.SS;
+        float sj[kCpl], fbj[kCpl];
+#pragma unroll
+        for (int u = 0; u < kCpl; ++u) {
+            sj[u] = rowlane ? A.sstate[(uint64_t)j * P.SS + c0 + u] : 0.0f;
+            fbj[u] = c0 + u < (int)S ? A.sfb[(uint64_t)j * P.SS + c0 + u] : 0.0f;
+        }
         // blurred state (adjoint.rs:138-166): k as the neighbour of idx = j ...
         const float kern = poly6(r2, P.g);
         const float w = kern * vol_k;
-        float wadj = 0.0f;
+        float wadj = 0.0f, wk = 0.0f;
 #pragma unroll
-        for (int c = 0; c < SM; ++c) {
-            if (c >= (int)S) continue;
-            acc[c] += fbj[c] * w;
-            wadj += fbj[c] * sk[c];
+        for (int u = 0; u < kCpl; ++u) {
+            if (c0 + u >= (int)S) continue;
+            acc[u] += fbj[u] * w;
+            wadj += fbj[u] * sk[u];
+            wk += fbk[u] * sj[u];
         }
+        wadj = group_sum<L>(wadj);
+        wk = group_sum<L>(wk);
         float t[D];
-        poly6_delta_adjoint<D>(dn, r2, P.g, wadj * vol_k, t);
+        if (lead) {
+            poly6_delta_adjoint<D>(dn, r2, P.g, wadj * vol_k, t);
 #pragma unroll
-        for (int a = 0; a < D; ++a) pa[a] += t[a];
-        volume_density_adjoint(rho_k, wadj * kern, &dadj);
-        if (self) return;  // the self pair's other terms are zero
-        // ... and k as idx with neighbour j
-        float wk = 0.0f;
-#pragma unroll
-        for (int c = 0; c < SM; ++c) {
-            if (c >= (int)S) continue;
-            wk += fbk[c] * sj[c];
+            for (int a = 0; a < D; ++a) pa[a] += t[a];
+            volume_density_adjoint(rho_k, wadj * kern, &dadj);
         }
-        poly6_delta_adjoint<D>(d, r2, P.g, wk * vol_j, t);
+        if (self) return;  // the self pair's other terms are zero
+        if (lead) {  // ... and k as idx with neighbour j
+            poly6_delta_adjoint<D>(d, r2, P.g, wk * vol_j, t);
 #pragma unroll
-        for (int a = 0; a < D; ++a) pa[a] -= t[a];
+            for (int a = 0; a < D; ++a) pa[a] -= t[a];
+        }
         if (P.state_grad) {  // adjoint.rs:276-347
             const float* rg_j = A.rga + (uint64_t)j * P.SS * D;
+            // spiky_gradient_kernel for the three coefficients, from one square root: seen from j
+            // with k's volume (vg) and with 1 (ug), seen from k with j's volume (vgk)
+            const SpikyPre qk = spiky_pre(r2, P.g, vol_k), qj = spiky_pre(r2, P.g, vol_j);
+            const SpikyPre q1 = spiky_pre(r2, P.g, 1.0f);
             float vg[D], ug[D], vgk[D];
-            spiky<D>(dn, r2, P.g, vol_k, vg);  // seen from j: volume of k
-            spiky<D>(dn, r2, P.g, 1.0f, ug);
-            spiky<D>(d, r2, P.g, vol_j, vgk);  // seen from k: volume of j
 #pragma unroll
-            for (int c = 0; c < SM; ++c) {
+            for (int a = 0; a < D; ++a) {
+                vg[a] = qk.scale * dn[a];
+                ug[a] = q1.scale * dn[a];
+                vgk[a] = qj.scale * d[a];
+            }
+            // The delta adjoint is linear in its input: each role sums its channels' gradient
+            // adjoints (gj: k as the neighbour of idx = j, gk: k as idx) and applies it once.
+            float gj[D], gk[D];
+#pragma unroll
+            for (int a = 0; a < D; ++a) {
+                gj[a] = 0.0f;
+                gk[a] = 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < kCpl; ++u) {
+                const int c = c0 + u;
                 if (c >= (int)S) continue;
-                // k as the neighbour of idx = j
                 float sc = rg_j[c * D] * vg[0];
 #pragma unroll
                 for (int a = 1; a < D; ++a) sc += rg_j[c * D + a] * vg[a];
-                acc[c] += sc;
-                const float diff = sk[c] - sj[c];
-                float gda[D];
+                acc[u] += sc;
+                const float diff = sk[u] - sj[u];
 #pragma unroll
-                for (int a = 0; a < D; ++a) gda[a] = rg_j[c * D + a] * diff;
-                spiky_delta_adjoint<D>(dn, r2, P.g, vol_k, gda, t);
-#pragma unroll
-                for (int a = 0; a < D; ++a) pa[a] += t[a];
-                float va = gda[0] * ug[0];
-#pragma unroll
-                for (int a = 1; a < D; ++a) va += gda[a] * ug[a];
-                volume_density_adjoint(rho_k, va, &dadj);
-                // k as idx with neighbour j
+                for (int a = 0; a < D; ++a) gj[a] += rg_j[c * D + a] * diff;
                 float sk2 = rg_k[c * D] * vgk[0];
 #pragma unroll
                 for (int a = 1; a < D; ++a) sk2 += rg_k[c * D + a] * vgk[a];
-                acc[c] -= sk2;
-                const float diffk = sj[c] - sk[c];
+                acc[u] -= sk2;
+                const float diffk = sj[u] - sk[u];
 #pragma unroll
-                for (int a = 0; a < D; ++a) gda[a] = rg_k[c * D + a] * diffk;
-                spiky_delta_adjoint<D>(d, r2, P.g, vol_j, gda, t);
+                for (int a = 0; a < D; ++a) gk[a] += rg_k[c * D + a] * diffk;
+            }
+#pragma unroll
+            for (int a = 0; a < D; ++a) {
+                gj[a] = group_sum<L>(gj[a]);
+                gk[a] = group_sum<L>(gk[a]);
+            }
+            if (lead) {
+                spiky_delta_adjoint_pre<D>(dn, qk, gj, t);
+#pragma unroll
+                for (int a = 0; a < D; ++a) pa[a] += t[a];
+                float va = gj[0] * ug[0];
+#pragma unroll
+                for (int a = 1; a < D; ++a) va += gj[a] * ug[a];
+                volume_density_adjoint(rho_k, va, &dadj);
+                spiky_delta_adjoint_pre<D>(d, qj, gk, t);
 #pragma unroll
                 for (int a = 0; a < D; ++a) pa[a] -= t[a];
             }
-            if (P.hybrid) {
+            if (P.hybrid && lead) {
                 const float* mj = A.madj + (uint64_t)j * 9;
                 // k as the neighbour of idx = j
                 float dda[D], gda[D];
@@ -399,7 +468,7 @@ __global__ __launch_bounds__(256) void k_adj_gather(StepParams P, AdjointArgs A)
                         dda[r] += m * vg[cc];
                         gda[cc] += m * dn[r];
                     }
-                spiky_delta_adjoint<D>(dn, r2, P.g, vol_k, gda, t);
+                spiky_delta_adjoint_pre<D>(dn, qk, gda, t);
 #pragma unroll
                 for (int a = 0; a < D; ++a) pa[a] += dda[a] + t[a];
                 float va = gda[0] * ug[0];
@@ -420,33 +489,39 @@ __global__ __launch_bounds__(256) void k_adj_gather(StepParams P, AdjointArgs A)
                         dda[r] += m * vgk[cc];
                         gda[cc] += m * d[r];
                     }
-                spiky_delta_adjoint<D>(d, r2, P.g, vol_j, gda, t);
+                spiky_delta_adjoint_pre<D>(d, qj, gda, t);
 #pragma unroll
                 for (int a = 0; a < D; ++a) pa[a] -= dda[a] + t[a];
             }
         }
-        if (P.density_grad) {  // adjoint.rs:390-396
+        if (P.density_grad && lead) {  // adjoint.rs:390-396
+            const SpikyPre q1 = spiky_pre(r2, P.g, 1.0f);
             float rj[D];
 #pragma unroll
             for (int a = 0; a < D; ++a) rj[a] = A.rda[(uint64_t)j * 4 + a];
-            spiky_delta_adjoint<D>(dn, r2, P.g, 1.0f, rj, t);
+            spiky_delta_adjoint_pre<D>(dn, q1, rj, t);
 #pragma unroll
             for (int a = 0; a < D; ++a) pa[a] += t[a];
-            spiky_delta_adjoint<D>(d, r2, P.g, 1.0f, rda_k, t);
+            spiky_delta_adjoint_pre<D>(d, q1, rda_k, t);
 #pragma unroll
             for (int a = 0; a < D; ++a) pa[a] -= t[a];
         }
     });
+#pragma unroll
+    for (int a = 0; a < D; ++a) pa[a] = group_sum<L>(pa[a]);
+    dadj = group_sum<L>(dadj);
     if (P.position_features) {  // adjoint.rs:118-122
         const uint32_t off = P.F - D;
 #pragma unroll
         for (int a = 0; a < D; ++a) pa[a] += fa[off + a];
     }
 #pragma unroll
-    for (int c = 0; c < SM; ++c)
-        if (c < (int)S) A.state_adj[pk * S + c] = acc[c];
-    A.ppos[s] = make_float4(pa[0], D > 1 ? pa[1] : 0.0f, D > 2 ? pa[D > 2 ? 2 : 0] : 0.0f, 0.0f);
-    A.dadj[s] = dadj;
+    for (int u = 0; u < kCpl; ++u)
+        if (c0 + u < (int)S) A.state_adj[pk * S + c0 + u] = acc[u];
+    if (lead) {
+        A.ppos[s] = make_float4(pa[0], D > 1 ? pa[1] : 0.0f, D > 2 ? pa[D > 2 ? 2 : 0] : 0.0f, 0.0f);
+        A.dadj[s] = dadj;
+    }
 }
 
 // accumulate_density_kernel_position_adjoint (adjoint.rs:399-418), gathered.
@@ -480,12 +555,13 @@ __global__ __launch_bounds__(256) void k_adj_density_kernel(StepParams P, Adjoin
 template <int D, int SM>
 static hipError_t launch_adjoint_t(const StepParams& p, const AdjointArgs& a, hipStream_t stream) {
     const dim3 grid((p.T + 255) / 256), block(256);
+    const dim3 grid_l((uint32_t)(((uint64_t)p.T * (SM / kCpl) + 255) / 256));
     hipLaunchKernelGGL(k_adj_density<D>, grid, block, 0, stream, p, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_adj_prep<D, SM>), grid, block, 0, stream, p, a);
+    hipLaunchKernelGGL((k_adj_prep<D, SM>), grid_l, block, 0, stream, p, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL((k_adj_gather<D, SM>), grid, block, 0, stream, p, a);
+    hipLaunchKernelGGL((k_adj_gather<D, SM>), grid_l, block, 0, stream, p, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_adj_density_kernel<D>, grid, block, 0, stream, p, a);
     return hipGetLastError();
@@ -495,6 +571,7 @@ hipError_t launch_perceive_adjoint(const StepParams& p, Workspace& ws, AdjointWo
                                    float* state_adj, float4* pos_adj, hipStream_t stream) {
     if (p.T == 0) return hipSuccess;
     const uint64_t T = p.T;
+    if (T * (32 / kCpl) >= (1ull << 32)) return hipErrorInvalidValue;  // thread ids of the lane groups
     hipError_t e;
     if ((e = aw.sdens.reserve(T * 4)) != hipSuccess) return e;
     if ((e = aw.sfb.reserve(T * p.SS * 4)) != hipSuccess) return e;
