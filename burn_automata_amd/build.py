@@ -29,7 +29,9 @@ def hipcc() -> str:
 
 
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Xclang", "-target-feature",
-         "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-variable", "-Wno-unused-function"]
+         "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-variable", "-Wno-unused-function",
+         # the neighbour filters combine bools with & on purpose (branch-free)
+         "-Wno-bitwise-instead-of-logical"]
 NOISE = "'-packed-fp32-ops' is not a recognized feature"
 
 

@@ -13,8 +13,7 @@
 //                  barrier, ranks are offset by the earlier waves' counters and the tile's
 //                  per-key histogram row is written to table[tile][key].
 //   k_table_scan   per key, exclusive prefix over the system's tiles (column scan).
-//   k_offsets_scan per system, exclusive prefix over keys -> bin_offsets; also emits
-//                  the wave work list (one item per <=64 consecutive slots of a bin).
+//   k_offsets_scan per system, exclusive prefix over keys -> bin_offsets.
 //   k_scatter      dst = bin_offsets[key] + table[tile][key] + rank; writes the
 //                  permutation, its inverse and (for the rollout step) the sorted particle
 //                  records and state rows the neighbour passes read.
@@ -152,7 +151,9 @@ bool make_plan(const npa_grid_cfg& cfg, uint32_t batch, uint32_t n, HashgridPlan
     p.key_bits = cells <= 1 ? 0 : 32 - __builtin_clz((uint32_t)cells - 1);
     p.waves = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(4, 32768 / cells));
     p.lds_bytes = p.waves * p.cells * 2;
-    const uint64_t budget = std::max<uint64_t>(4 * (uint64_t)n, cells);
+    // table entries allowed: 4 per particle, or 64 rows of cells when the cells outnumber the
+    // particles (sparse grids: more, smaller tiles keep the O(cells) work per tile parallel)
+    const uint64_t budget = std::max<uint64_t>(4 * (uint64_t)n, cells > n ? 64 * cells : cells);
     uint32_t rounds = 1;
     while (rounds < 32) {
         uint64_t tile = (uint64_t)p.waves * rounds * 64;
@@ -206,12 +207,18 @@ __global__ __launch_bounds__(256) void k_hash_rank(const float4* __restrict__ po
     if (wl_count && tile == 0 && threadIdx.x < 4) wl_count[threadIdx.x] = 0;  // work-list counters
     __syncthreads();
 
+    // The first `waves` waves rank (one LDS counter row each); every wave of the block clears the
+    // counters and writes the histogram row, which costs O(C) whatever the tile size.
     const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    volatile uint16_t* mine = cnt + w * C;
+    const bool ranker = w < waves;
+    volatile uint16_t* mine = cnt + (ranker ? w : 0) * C;
     const uint32_t wave_start = t * (waves * R * 64) + w * (R * 64);
     const uint64_t lt = lanemask_lt();
     uint32_t key_r[R], rank_r[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) key_r[r] = rank_r[r] = 0;
     bool ovf = false;
+    if (ranker) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t li = wave_start + r * 64 + lane;
@@ -244,11 +251,12 @@ __global__ __launch_bounds__(256) void k_hash_rank(const float4* __restrict__ po
         key_r[r] = key;
         rank_r[r] = rank;
     }
+    }
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t li = wave_start + r * 64 + lane;
-        if (li < n) {
+        if (ranker && li < n) {
             uint32_t prefix = 0;
             for (uint32_t w2 = 0; w2 < w; ++w2) prefix += cnt[w2 * C + key_r[r]];
             if (!keys_in) keys[sys_start + li] = key_r[r];
@@ -319,57 +327,60 @@ __device__ __forceinline__ uint32_t block_scan_1024(uint32_t v, uint32_t* lds, u
     return wave_prefix + x - v;
 }
 
+// One block per system: bin_offsets[b][k] = b * n + exclusive prefix of totals[b][k] over k.
+// Wave w owns a contiguous range of keys and walks it in segments of 64 (lane = key), so every
+// load and store is coalesced: a first walk sums the range, a block scan orders the waves, and a
+// second walk writes the prefixes with a running carry.
 __global__ __launch_bounds__(1024) void k_offsets_scan(const uint32_t* __restrict__ totals,
                                                        uint32_t* __restrict__ bin_offsets,
-                                                       uint32_t C, uint32_t n, uint32_t batch,
-                                                       uint2* __restrict__ worklist,
-                                                       uint32_t* __restrict__ wl_count,
-                                                       int emit_work, uint32_t tpi) {
-    __shared__ uint32_t lds[32];
-    __shared__ uint32_t wl_base;
+                                                       uint32_t C, uint32_t n, uint32_t batch) {
+    __shared__ uint32_t wsum[16];
     const uint32_t b = blockIdx.x;
-    const uint32_t per = (C + blockDim.x - 1) / blockDim.x;
-    const uint32_t k0 = threadIdx.x * per;
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint32_t* tot = totals + (uint64_t)b * C;
+    uint32_t* out = bin_offsets + (uint64_t)b * C;
+    const uint32_t per = ((C + nw - 1) / nw + 63) / 64 * 64;  // keys per wave, whole segments
+    const uint32_t k0 = w * per < C ? w * per : C;
     const uint32_t k1 = k0 + per < C ? k0 + per : C;
-    uint32_t sum_c = 0, sum_i = 0;
-    for (uint32_t k = k0; k < k1; k += 8) {  // batches of 8 independent loads
-        uint32_t v[8];
+    uint32_t acc = 0;
+    for (uint32_t k = k0 + lane; k < k1; k += 4 * 64) {  // four segments' loads in flight
+        uint32_t v[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = k + u < k1 ? tot[k + u] : 0u;
+        for (int u = 0; u < 4; ++u) v[u] = k + u * 64 < k1 ? tot[k + u * 64] : 0u;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            sum_c += v[u];
-            sum_i += (v[u] + tpi - 1) / tpi;
-        }
+        for (int u = 0; u < 4; ++u) acc += v[u];
     }
-    uint32_t all_c, all_i;
-    uint32_t pre_c = block_scan_1024(sum_c, lds, &all_c);
-    uint32_t pre_i = block_scan_1024(sum_i, lds, &all_i);
-    if (emit_work && threadIdx.x == 0) wl_base = atomicAdd(wl_count, all_i);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) wsum[w] = acc;
     __syncthreads();
-    const uint32_t sys_base = b * n;
-    uint32_t run_c = pre_c, run_i = emit_work ? wl_base + pre_i : 0;
-    for (uint32_t k = k0; k < k1; k += 8) {
-        uint32_t v[8];
+    uint32_t carry = b * n, all = 0;
+    for (uint32_t v = 0; v < nw; ++v) {
+        if (v < w) carry += wsum[v];
+        all += wsum[v];
+    }
+    for (uint32_t s0 = k0; s0 < k1; s0 += 4 * 64) {
+        uint32_t v[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = k + u < k1 ? tot[k + u] : 0u;
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t k = s0 + u * 64 + lane;
+            v[u] = k < k1 ? tot[k] : 0u;
+        }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            if (k + u >= k1) break;
-            const uint32_t c = v[u];
-            bin_offsets[(uint64_t)b * C + k + u] = sys_base + run_c;
-            if (emit_work) {
-                for (uint32_t m = 0; m * tpi < c; ++m) {
-                    uint32_t cnt = c - m * tpi;
-                    worklist[run_i++] = make_uint2(sys_base + run_c + m * tpi, cnt < tpi ? cnt : tpi);
-                }
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t k = s0 + u * 64 + lane;
+            uint32_t x = v[u];
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t y = __shfl_up(x, off, 64);
+                if (lane >= (uint32_t)off) x += y;
             }
-            run_c += c;
+            if (k < k1) out[k] = carry + x - v[u];
+            carry += __shfl(x, 63, 64);
         }
     }
     // last entry = total count (every system holds n entries when the counts are per system)
-    if (b == batch - 1 && threadIdx.x == 0) bin_offsets[(uint64_t)batch * C] = sys_base + all_c;
+    if (b == batch - 1 && threadIdx.x == 0) bin_offsets[(uint64_t)batch * C] = b * n + all;
 }
 
 // payload == 0: perm (slot -> particle of the system) and inv, the reference's snapshot.
@@ -700,7 +711,7 @@ static hipError_t launch_rank_r(uint32_t blocks, uint32_t waves, uint32_t lds_by
         if (e != hipSuccess) return e;
         attr_bytes = lds_bytes;
     }
-    return launch_timed(prof, NPA_KERNEL_HASH_RANK, k_hash_rank<R>, dim3(blocks), dim3(waves * 64), lds_bytes, stream,
+    return launch_timed(prof, NPA_KERNEL_HASH_RANK, k_hash_rank<R>, dim3(blocks), dim3(256), lds_bytes, stream,
                         pos, keys_in, d_count, n, tiles_per_sys, waves, g, key_bits, keys, ranks, table, flags,
                         wl_count);
 }
@@ -738,8 +749,7 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                      stream, ws.table.as<uint32_t>(), ws.totals.as<uint32_t>(), plan.cells, plan.tiles_per_sys);
     if (e != hipSuccess) return e;
     e = launch_timed(prof, NPA_KERNEL_OFFSETS_SCAN, k_offsets_scan, dim3(batch), dim3(1024), 0, stream,
-                     ws.totals.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), plan.cells, n, batch,
-                     ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), 0, plan.tpi);
+                     ws.totals.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), plan.cells, n, batch);
     if (e != hipSuccess) return e;
     const uint32_t blocks = (uint32_t)((total + 255) / 256);
     e = launch_timed(prof, NPA_KERNEL_SCATTER, k_scatter, dim3(blocks), dim3(256), 0, stream, n, (uint32_t)total,
@@ -814,8 +824,7 @@ hipError_t launch_key_sort(const HashgridPlan& p, const uint32_t* keys, const ui
     hipLaunchKernelGGL(k_table_scan, dim3((p.cells + 255) / 256, 1), dim3(256), 0, stream, table, totals,
                        p.cells, p.tiles_per_sys);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_offsets_scan, dim3(1), dim3(1024), 0, stream, totals, offsets, p.cells, cap, 1u,
-                       (uint2*)nullptr, (uint32_t*)nullptr, 0, 64u);
+    hipLaunchKernelGGL(k_offsets_scan, dim3(1), dim3(1024), 0, stream, totals, offsets, p.cells, cap, 1u);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (cap == 0) return hipSuccess;
     hipLaunchKernelGGL(k_scatter_vals, dim3((cap + 255) / 256), dim3(256), 0, stream, keys, vals, d_count,

@@ -1215,21 +1215,21 @@ __global__ __launch_bounds__(256) void k_neighbor_lists(StepParams P, const floa
 // ------------------------------------------------------------------ launch
 #if NPA_PART_MAIN
 template <int D, int L>
-static void launch_density_t(const StepParams& p, Workspace& ws, float* density_out, int blocks, hipStream_t stream,
-                             Profiler* prof) {
-    launch_timed(prof, NPA_KERNEL_DENSITY, k_density<D, L>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
+static hipError_t launch_density_t(const StepParams& p, Workspace& ws, float* density_out, int blocks,
+                                   hipStream_t stream, Profiler* prof) {
+    return launch_timed(prof, NPA_KERNEL_DENSITY, k_density<D, L>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
                        ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
                        ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.svol.as<float4>(), density_out,
                        ws.nb_chunks.as<uint4>(), ws.nb_count.as<uint32_t>());
 }
 
 template <int D>
-static void launch_density_d(const StepParams& p, Workspace& ws, float* density_out, int blocks, hipStream_t stream,
-                             Profiler* prof) {
+static hipError_t launch_density_d(const StepParams& p, Workspace& ws, float* density_out, int blocks,
+                                   hipStream_t stream, Profiler* prof) {
     const uint32_t L = lanes_per_target(p.SS);
-    if (L == 1) launch_density_t<D, 1>(p, ws, density_out, blocks, stream, prof);
-    else if (L == 2) launch_density_t<D, 2>(p, ws, density_out, blocks, stream, prof);
-    else launch_density_t<D, 4>(p, ws, density_out, blocks, stream, prof);
+    if (L == 1) return launch_density_t<D, 1>(p, ws, density_out, blocks, stream, prof);
+    if (L == 2) return launch_density_t<D, 2>(p, ws, density_out, blocks, stream, prof);
+    return launch_density_t<D, 4>(p, ws, density_out, blocks, stream, prof);
 }
 
 static StepParams with_directory(const StepParams& p, const Workspace& ws) {
@@ -1243,17 +1243,16 @@ hipError_t launch_density(const StepParams& p_in, Workspace& ws, float* density_
                           hipStream_t stream, Profiler* prof) {
     const StepParams p = with_directory(p_in, ws);
     const int blocks = grid_blocks * 4;  // one wave per block
-    if (p.g.dim == 2) launch_density_d<2>(p, ws, density_out, blocks, stream, prof);
-    else launch_density_d<3>(p, ws, density_out, blocks, stream, prof);
-    return hipGetLastError();
+    return p.g.dim == 2 ? launch_density_d<2>(p, ws, density_out, blocks, stream, prof)
+                        : launch_density_d<3>(p, ws, density_out, blocks, stream, prof);
 }
 
 #endif  // NPA_PART_MAIN
 
 template <int D, int SM, int MODE, int FL>
-static void launch_perceive_f(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
-                              hipStream_t stream, Profiler* prof) {
-    launch_timed(prof, NPA_KERNEL_PERCEIVE, k_perceive<D, SM, MODE, FL>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
+static hipError_t launch_perceive_f(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
+                                    hipStream_t stream, Profiler* prof) {
+    return launch_timed(prof, NPA_KERNEL_PERCEIVE, k_perceive<D, SM, MODE, FL>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
                        ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.svol.as<float4>(),
                        ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), ws.act_rows.as<uint32_t>(),
                        ws.wl_count.as<uint32_t>() + 3, ws.nb_chunks.as<uint4>(), ws.nb_count.as<uint32_t>(),
@@ -1262,25 +1261,24 @@ static void launch_perceive_f(const StepParams& p, Workspace& ws, const StepIO& 
 
 // The rollout step's usual option sets run a specialised kernel; anything else reads the flags.
 template <int D, int SM, int MODE>
-static void launch_perceive_t(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
-                              hipStream_t stream, Profiler* prof) {
+static hipError_t launch_perceive_t(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
+                                    hipStream_t stream, Profiler* prof) {
     if (MODE == 0 && p.state_grad && p.hybrid && !p.density_grad)
-        launch_perceive_f<D, SM, MODE, 5>(p, ws, io, blocks, stream, prof);
-    else if (MODE == 0 && p.state_grad && p.hybrid && p.density_grad)
-        launch_perceive_f<D, SM, MODE, 7>(p, ws, io, blocks, stream, prof);
-    else
-        launch_perceive_f<D, SM, MODE, -1>(p, ws, io, blocks, stream, prof);
+        return launch_perceive_f<D, SM, MODE, 5>(p, ws, io, blocks, stream, prof);
+    if (MODE == 0 && p.state_grad && p.hybrid && p.density_grad)
+        return launch_perceive_f<D, SM, MODE, 7>(p, ws, io, blocks, stream, prof);
+    return launch_perceive_f<D, SM, MODE, -1>(p, ws, io, blocks, stream, prof);
 }
 
 template <int D, int MODE>
-static void launch_perceive_d(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
-                              hipStream_t stream, Profiler* prof) {
+static hipError_t launch_perceive_d(const StepParams& p, Workspace& ws, const StepIO& io, int blocks,
+                                    hipStream_t stream, Profiler* prof) {
     switch (p.SS) {
-        case 4: launch_perceive_t<D, 4, MODE>(p, ws, io, blocks, stream, prof); break;
-        case 8: launch_perceive_t<D, 8, MODE>(p, ws, io, blocks, stream, prof); break;
-        case 16: launch_perceive_t<D, 16, MODE>(p, ws, io, blocks, stream, prof); break;
-        case 24: launch_perceive_t<D, 24, MODE>(p, ws, io, blocks, stream, prof); break;
-        default: launch_perceive_t<D, 32, MODE>(p, ws, io, blocks, stream, prof); break;
+        case 4: return launch_perceive_t<D, 4, MODE>(p, ws, io, blocks, stream, prof);
+        case 8: return launch_perceive_t<D, 8, MODE>(p, ws, io, blocks, stream, prof);
+        case 16: return launch_perceive_t<D, 16, MODE>(p, ws, io, blocks, stream, prof);
+        case 24: return launch_perceive_t<D, 24, MODE>(p, ws, io, blocks, stream, prof);
+        default: return launch_perceive_t<D, 32, MODE>(p, ws, io, blocks, stream, prof);
     }
 }
 
@@ -1356,9 +1354,8 @@ static hipError_t launch_mlp_d(const StepParams& p, Workspace& ws, const StepIO&
 template <int D>
 static hipError_t launch_second_pass(const StepParams& p, Workspace& ws, const StepIO& io, int mode, int blocks,
                                      hipStream_t stream, Profiler* prof) {
-    if (mode == 0) launch_perceive_d<D, 0>(p, ws, io, blocks, stream, prof);
-    else launch_perceive_d<D, 1>(p, ws, io, blocks, stream, prof);
-    hipError_t e = hipGetLastError();
+    const hipError_t e = mode == 0 ? launch_perceive_d<D, 0>(p, ws, io, blocks, stream, prof)
+                                   : launch_perceive_d<D, 1>(p, ws, io, blocks, stream, prof);
     if (e != hipSuccess || mode != 0) return e;
     return launch_mlp_d<D>(p, ws, io, stream, prof);
 }
