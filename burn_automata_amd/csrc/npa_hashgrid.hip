@@ -74,6 +74,7 @@ hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t
     NPA_RES(wpad, 4);
     NPA_RES(tmpidx, t1 * 4);
     NPA_RES(dir_n, (bins ? bins : 1) * 4);
+    NPA_RES(bin_list, (bins ? bins : 1) * 4);
     NPA_RES(dir_e, (bins ? bins : 1) * kDirGroups * 16);
     NPA_RES(nb_chunks, t1 * max_chunks(dim) * 16);
     NPA_RES(nb_count, t1 * 4);
@@ -88,7 +89,7 @@ hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t
 void Workspace::release() {
     for (DevBuf* b : {&keys, &ranks, &table, &totals, &bin_offsets, &perm, &inv, &flags, &wl_count,
                       &worklist, &srec, &scoord, &sstate, &svol, &counters, &features, &wpad, &tmpidx,
-                      &dir_n, &dir_e, &act_rows, &nb_chunks, &nb_count})
+                      &dir_n, &dir_e, &bin_list, &act_rows, &nb_chunks, &nb_count})
         b->release();
 }
 
@@ -482,12 +483,20 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
                                                float* __restrict__ sstate, uint32_t* __restrict__ dir_n,
                                                int4* __restrict__ dir_e, uint2* __restrict__ worklist,
                                                uint32_t* __restrict__ wl_count, uint32_t tpi, SplitTargets T,
-                                               uint32_t* __restrict__ act_rows) {
+                                               uint32_t* __restrict__ act_rows,
+                                               const uint32_t* __restrict__ bin_list,
+                                               const uint32_t* __restrict__ bin_count) {
     constexpr uint32_t K = kDirGroups;
     __shared__ uint32_t s_items[kSplitWaves], s_rows[kSplitWaves];
     __shared__ uint32_t s_base, s_rbase;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t bin = blockIdx.x * kSplitWaves + wave;
+    // every bin in order, or (bin_list) the listed bins - the ones the one-lane pass left
+    uint32_t bin = blockIdx.x * kSplitWaves + wave;
+    if (bin_list) {
+        const uint32_t listed = *bin_count;
+        if (blockIdx.x * kSplitWaves >= listed) return;  // the whole block has no bin
+        bin = bin < listed ? bin_list[bin] : nbins;
+    }
     const bool has_bin = bin < nbins;
     const uint32_t beg = has_bin ? bo[bin] : 0u, end = has_bin ? bo[bin + 1] : 0u;
     const uint32_t b = has_bin ? bin / g.cells : 0u;
@@ -697,6 +706,187 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
     if (lane == 0) dir_n[bin] = ng;
 }
 
+// The same split for sparse grids, one lane per bin: a bin of at most kThinMax particles is split
+// by a single lane walking its slots in order (runs in order of first appearance, slot order
+// within a run, the same work items, compact rows and directory entries as k_split); larger bins
+// are listed for k_split. Used when bins outnumber a quarter of the particles, where a wave per
+// bin would spend a whole wave's instructions on an empty or one-particle bin.
+constexpr uint32_t kThinMax = kDirGroups;
+
+// Exclusive prefix of v over a 256-thread block and the block's total (4 waves).
+__device__ __forceinline__ uint32_t block_prefix_256(uint32_t v, uint32_t* lds4, uint32_t* total) {
+    const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    uint32_t x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(x, off, 64);
+        if (lane >= (uint32_t)off) x += y;
+    }
+    if (lane == 63) lds4[wid] = x;
+    __syncthreads();
+    uint32_t pre = 0, all = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < 4; ++w) {
+        const uint32_t t = lds4[w];
+        if (w < wid) pre += t;
+        all += t;
+    }
+    *total = all;
+    return pre + x - v;
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void k_split_thin(const float4* __restrict__ pos, const float* __restrict__ states,
+                                                   uint32_t S, uint32_t n, uint32_t nbins, GridParams g,
+                                                   const uint32_t* __restrict__ bo,
+                                                   const uint32_t* __restrict__ order,
+                                                   uint32_t* __restrict__ perm, uint32_t* __restrict__ inv,
+                                                   float4* __restrict__ srec, int4* __restrict__ scoord,
+                                                   float* __restrict__ sstate, uint32_t* __restrict__ dir_n,
+                                                   int4* __restrict__ dir_e, uint2* __restrict__ worklist,
+                                                   uint32_t* __restrict__ wl_count, uint32_t tpi, SplitTargets T,
+                                                   uint32_t* __restrict__ act_rows, uint32_t* __restrict__ bin_list) {
+    constexpr uint32_t K = kDirGroups;
+    __shared__ uint32_t lds_i[4], lds_r[4], lds_f[4];
+    __shared__ uint32_t s_base[3];
+    const uint32_t bin = blockIdx.x * blockDim.x + threadIdx.x;
+    const bool has_bin = bin < nbins;
+    const uint32_t beg = has_bin ? bo[bin] : 0u, end = has_bin ? bo[bin + 1] : 0u;
+    const bool thin = has_bin && end - beg <= kThinMax;
+    const bool fat = has_bin && !thin;
+    const uint32_t b = has_bin ? bin / g.cells : 0u;
+    auto is_target = [&](uint32_t i) -> bool {
+        if (T.mask_mode == 0) return true;
+        const uint32_t li = i - b * n;
+        const float m = T.mask_mode == 1 ? hash_mask(li, b, n, T.update_prob, T.step_index, T.base_seed) : T.mask[i];
+        return m != 0.0f;
+    };
+    auto load = [&](uint32_t q, uint32_t& i, float4& p4, int c[3]) {
+        i = order[q];
+        p4 = pos[i];
+        const float p[4] = {p4.x, p4.y, p4.z, p4.w};
+        int64_t c64[3];
+        bool ovf = false;
+        cell_coords(p, g, c64, &ovf);  // overflow was flagged by the hash pass
+        c[0] = (int)c64[0];
+        c[1] = (int)c64[1];
+        c[2] = (int)c64[2];
+    };
+    int gx[K], gy[K], gz[K];
+    uint32_t gc[K], gt[K];
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) {
+        gx[k] = gy[k] = gz[k] = 0;
+        gc[k] = gt[k] = 0;
+    }
+    uint32_t ng = 0;
+    auto group_of = [&](const int c[3]) -> int {
+        int gid = -1;
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k)
+            if (k < ng && c[0] == gx[k] && c[1] == gy[k] && c[2] == gz[k]) gid = (int)k;
+        return gid;
+    };
+    uint32_t nitems = 0, nrows = 0;
+    if (thin) {  // pass 1: runs in order of first appearance, their particles and targets
+        for (uint32_t q = beg; q < end; ++q) {
+            uint32_t i;
+            float4 p4;
+            int c[3];
+            load(q, i, p4, c);
+            int gid = group_of(c);
+            if (gid < 0) {
+                gid = (int)ng;
+#pragma unroll
+                for (uint32_t k = 0; k < K; ++k)
+                    if (k == ng) {
+                        gx[k] = c[0];
+                        gy[k] = c[1];
+                        gz[k] = c[2];
+                    }
+                ++ng;
+            }
+            const uint32_t t = is_target(i) ? 1u : 0u;
+#pragma unroll
+            for (uint32_t k = 0; k < K; ++k)
+                if ((int)k == gid) {
+                    gc[k] += 1;
+                    gt[k] += t;
+                }
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k) {
+            nitems += (gc[k] + tpi - 1) / tpi;
+            nrows += gt[k];
+        }
+    }
+    // one reservation per block: work items, compact rows and listed bins
+    uint32_t ti, tr, tf;
+    const uint32_t pi_ = block_prefix_256(nitems, lds_i, &ti);
+    const uint32_t pr_ = block_prefix_256(nrows, lds_r, &tr);
+    const uint32_t pf_ = block_prefix_256(fat ? 1u : 0u, lds_f, &tf);
+    if (threadIdx.x == 0) {
+        s_base[0] = ti ? atomicAdd(wl_count, ti) : 0u;
+        s_base[1] = tr ? atomicAdd(wl_count + 3, tr) : 0u;
+        s_base[2] = tf ? atomicAdd(wl_count + 1, tf) : 0u;
+    }
+    __syncthreads();
+    if (fat) bin_list[s_base[2] + pf_] = bin;
+    if (!thin) return;
+    if (beg == end) {
+        dir_n[bin] = 0;
+        return;
+    }
+    // pass 2: slots in order; targets take rows in run order, slot order within a run
+    const uint32_t wbase = s_base[0] + pi_, rbase = s_base[1] + pr_;
+    uint32_t start[K], rstart[K], seen[K], seen_t[K];
+    {
+        uint32_t run = beg, r = rbase;
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k) {
+            start[k] = run;
+            rstart[k] = r;
+            run += gc[k];
+            r += gt[k];
+            seen[k] = seen_t[k] = 0;
+        }
+    }
+    for (uint32_t q = beg; q < end; ++q) {
+        uint32_t i;
+        float4 p4;
+        int c[3];
+        load(q, i, p4, c);
+        const int gid = group_of(c);
+        const bool tgt = is_target(i);
+        uint32_t dst = 0, row = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k)
+            if ((int)k == gid) {
+                dst = start[k] + seen[k];
+                row = rstart[k] + seen_t[k];
+                seen[k] += 1;
+                seen_t[k] += tgt ? 1u : 0u;
+            }
+        write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
+        if (tgt) act_rows[row] = dst;
+        else if (T.mask_mode != 0) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
+    }
+    uint32_t off = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) {
+        if (k < ng) {
+            const uint32_t it = (gc[k] + tpi - 1) / tpi;
+            for (uint32_t m = 0; m < it; ++m) {
+                const uint32_t left = gc[k] - m * tpi;
+                worklist[wbase + off + m] = make_uint2(start[k] + m * tpi, left < tpi ? left : tpi);
+            }
+            off += it;
+            dir_e[(uint64_t)bin * K + k] = make_int4(gx[k], gy[k], gz[k], (int)start[k]);
+        }
+    }
+    dir_n[bin] = ng;
+}
+
 // ------------------------------------------------------------------ launch
 template <int R>
 static hipError_t launch_rank_r(uint32_t blocks, uint32_t waves, uint32_t lds_bytes,
@@ -759,14 +949,36 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                      payload ? 1 : 0);
     if (e != hipSuccess || !payload) return e;
     const uint32_t nbins = batch * plan.cells;
-    const uint32_t sblocks = (nbins + kSplitWaves - 1) / kSplitWaves;
     auto split = g.dim == 2 ? k_split<2> : k_split<3>;
-    return launch_timed(prof, NPA_KERNEL_SPLIT, split, dim3(sblocks), dim3(64 * kSplitWaves), 0, stream, pos, states,
-                        state_dims, n, nbins, g, ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(),
-                        ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(), ws.scoord.as<int4>(),
-                        ws.sstate.as<float>(), ws.dir_n.as<uint32_t>(), ws.dir_e.as<int4>(),
-                        ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), plan.tpi,
-                        targets ? *targets : SplitTargets{}, ws.act_rows.as<uint32_t>());
+    const SplitTargets tg = targets ? *targets : SplitTargets{};
+    if ((uint64_t)nbins * 4 <= total) {  // dense bins: a wave per bin
+        const uint32_t sblocks = (nbins + kSplitWaves - 1) / kSplitWaves;
+        return launch_timed(prof, NPA_KERNEL_SPLIT, split, dim3(sblocks), dim3(64 * kSplitWaves), 0, stream, pos,
+                            states, state_dims, n, nbins, g, ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(),
+                            ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(),
+                            ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.dir_n.as<uint32_t>(),
+                            ws.dir_e.as<int4>(), ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), plan.tpi, tg,
+                            ws.act_rows.as<uint32_t>(), (const uint32_t*)nullptr, (const uint32_t*)nullptr);
+    }
+    // sparse bins: one lane per small bin, then a wave per listed (larger) bin; a listed bin holds
+    // more than kThinMax particles, so at most total / (kThinMax + 1) bins are listed
+    ProfScope ps(prof, NPA_KERNEL_SPLIT, stream);  // both kernels count as the step's one split
+    auto thin = g.dim == 2 ? k_split_thin<2> : k_split_thin<3>;
+    hipLaunchKernelGGL(thin, dim3((nbins + 255) / 256), dim3(256), 0, stream, pos, states, state_dims, n, nbins, g,
+                       ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(), ws.perm.as<uint32_t>(),
+                       ws.inv.as<uint32_t>(), ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(),
+                       ws.dir_n.as<uint32_t>(), ws.dir_e.as<int4>(), ws.worklist.as<uint2>(),
+                       ws.wl_count.as<uint32_t>(), plan.tpi, tg, ws.act_rows.as<uint32_t>(), ws.bin_list.as<uint32_t>());
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const uint64_t listed_max = total / (kThinMax + 1);
+    const uint32_t sblocks = (uint32_t)std::max<uint64_t>(1, (listed_max + kSplitWaves - 1) / kSplitWaves);
+    hipLaunchKernelGGL(split, dim3(sblocks), dim3(64 * kSplitWaves), 0, stream, pos, states, state_dims, n, nbins, g,
+                       ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(), ws.perm.as<uint32_t>(),
+                       ws.inv.as<uint32_t>(), ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(),
+                       ws.dir_n.as<uint32_t>(), ws.dir_e.as<int4>(), ws.worklist.as<uint2>(),
+                       ws.wl_count.as<uint32_t>(), plan.tpi, tg, ws.act_rows.as<uint32_t>(),
+                       (const uint32_t*)ws.bin_list.as<uint32_t>(), (const uint32_t*)(ws.wl_count.as<uint32_t>() + 1));
+    return hipGetLastError();
 }
 
 // ------------------------------------------------------ generic key sort

@@ -99,9 +99,11 @@ struct Workspace {
     // the second pass gathers a neighbour's position and volume with one load
     DevBuf svol;
     DevBuf tmpidx, dir_n, dir_e;
+    // sparse grids: the bins too large for the one-lane split (count in wl_count[1])
+    DevBuf bin_list;
     // Targets of the second pass and the update: particles whose update mask is not 0 (the others
     // are written to the output by the update-mask kernel). act_rows: compact row -> slot.
-    // Counts (u32 words of wl_count): [0] density items, [3] compact rows.
+    // Counts (u32 words of wl_count): [0] density items, [1] listed bins, [3] compact rows.
     DevBuf act_rows;
     // Accepted neighbours recorded by the density pass, per target and neighbour chunk (<= 64
     // consecutive slots of a cell run, in visit order): chunk-major uint4 {first slot, length,
