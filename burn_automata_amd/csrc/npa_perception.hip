@@ -279,6 +279,66 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
     }
 }
 
+// The density pass for sparse 2D grids (fewer than 4 particles per bin on average), one thread per
+// target: the thread walks its 3^D neighbour runs itself (cells dz, dy, dx; slots ascending) and
+// writes exactly what k_density writes - the same sum in the same order, the same chunk records -
+// without spending a wave on a run of one or two targets.
+template <int D>
+__global__ __launch_bounds__(256) void k_density_sparse(StepParams P, const float4* __restrict__ srec,
+                                                        const int4* __restrict__ scoord,
+                                                        const uint32_t* __restrict__ bo,
+                                                        const uint32_t* __restrict__ perm,
+                                                        float4* __restrict__ svol, float* __restrict__ density_out,
+                                                        uint4* __restrict__ nb_chunks, uint32_t* __restrict__ nb_count) {
+    constexpr uint32_t MAXC = max_chunks(D);
+    constexpr int ZLO = D == 3 ? -1 : 0, ZHI = D == 3 ? 1 : 0;
+    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= P.T) return;
+    const uint32_t b = s / P.N;
+    float pi[3];
+    int ci[3];
+    load_rec<D>(srec, scoord, s, pi, ci);
+    float rho = 0.0f;
+    uint32_t gch = 0;
+    for (int dz = ZLO; dz <= ZHI; ++dz)
+        for (int dy = -1; dy <= 1; ++dy)
+            for (int dx = -1; dx <= 1; ++dx) {
+                const int64_t n0 = (int64_t)ci[0] + dx, n1 = (int64_t)ci[1] + dy, n2 = (int64_t)ci[2] + dz;
+                uint32_t beg, end;
+                bool filter;
+                if (!cell_range(P, bo, b, n0, n1, n2, beg, end, filter)) continue;
+                for (uint32_t base = beg; base < end; base += kChunk, ++gch) {
+                    const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
+                    uint64_t acc = 0;
+                    for (uint32_t k = 0; k < m; ++k) {
+                        float pj[3];
+                        int cj[3];
+                        load_rec<D>(srec, scoord, base + k, pj, cj);
+                        if (filter && ((int64_t)cj[0] != n0 || (int64_t)cj[1] != n1 ||
+                                       (D == 3 && (int64_t)cj[2] != n2)))
+                            continue;
+                        const float d0 = delta_axis(pi[0], pj[0], 0, P.g);
+                        const float d1 = delta_axis(pi[1], pj[1], 1, P.g);
+                        float r2 = d0 * d0;
+                        r2 += d1 * d1;
+                        if constexpr (D == 3) {
+                            const float d2 = delta_axis(pi[2], pj[2], 2, P.g);
+                            r2 += d2 * d2;
+                        }
+                        if (r2 < P.g.eps2) {
+                            rho += poly6(r2, P.g);
+                            acc |= 1ull << k;
+                        }
+                    }
+                    if (gch < MAXC)
+                        nb_chunks[(uint64_t)gch * P.T + s] = make_uint4(base, m, (uint32_t)acc, (uint32_t)(acc >> 32));
+                }
+            }
+    svol[s] = make_float4(pi[0], pi[1], pi[2], recip_finite(rho));
+    nb_count[s] = gch;
+    if (density_out) density_out[b * P.N + perm[s]] = rho;
+}
+
 // Per-wave accepted-neighbour lists of the second pass: the sorted slots of each target's accepted
 // candidates, appended in visit order (cells dz, dy, dx; slots ascending), so walking a list front
 // to back is the reference's neighbour order. kListBytes of LDS per wave for any targets-per-item.
@@ -1242,6 +1302,15 @@ static StepParams with_directory(const StepParams& p, const Workspace& ws) {
 hipError_t launch_density(const StepParams& p_in, Workspace& ws, float* density_out, int grid_blocks,
                           hipStream_t stream, Profiler* prof) {
     const StepParams p = with_directory(p_in, ws);
+    // sparse 2D bins: a thread per target (in 3D a target walks 27 cells, and the occupied cells of
+    // a sparse grid - a surface, say - hold several particles: the wave pass stays faster there)
+    if (p.g.dim == 2 && (uint64_t)p.B * p.g.cells * 4 > p.T) {
+        auto k = p.g.dim == 2 ? k_density_sparse<2> : k_density_sparse<3>;
+        return launch_timed(prof, NPA_KERNEL_DENSITY, k, dim3((p.T + 255) / 256), dim3(256), 0, stream, p,
+                            ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(),
+                            ws.perm.as<uint32_t>(), ws.svol.as<float4>(), density_out, ws.nb_chunks.as<uint4>(),
+                            ws.nb_count.as<uint32_t>());
+    }
     const int blocks = grid_blocks * 4;  // one wave per block
     return p.g.dim == 2 ? launch_density_d<2>(p, ws, density_out, blocks, stream, prof)
                         : launch_density_d<3>(p, ws, density_out, blocks, stream, prof);
