@@ -713,8 +713,11 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
 // bin would spend a whole wave's instructions on an empty or one-particle bin.
 constexpr uint32_t kThinMax = kDirGroups;
 
-// Exclusive prefix of v over a 256-thread block and the block's total (4 waves).
-__device__ __forceinline__ uint32_t block_prefix_256(uint32_t v, uint32_t* lds4, uint32_t* total) {
+constexpr uint32_t kThinThreads = 256;  // bins per k_split_thin block (one reservation each)
+
+// Exclusive prefix of v over a kThinThreads block and the block's total.
+__device__ __forceinline__ uint32_t block_prefix_thin(uint32_t v, uint32_t* ldsw, uint32_t* total) {
+    constexpr uint32_t NW = kThinThreads / 64;
     const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     uint32_t x = v;
 #pragma unroll
@@ -722,12 +725,12 @@ __device__ __forceinline__ uint32_t block_prefix_256(uint32_t v, uint32_t* lds4,
         const uint32_t y = __shfl_up(x, off, 64);
         if (lane >= (uint32_t)off) x += y;
     }
-    if (lane == 63) lds4[wid] = x;
+    if (lane == 63) ldsw[wid] = x;
     __syncthreads();
     uint32_t pre = 0, all = 0;
 #pragma unroll
-    for (uint32_t w = 0; w < 4; ++w) {
-        const uint32_t t = lds4[w];
+    for (uint32_t w = 0; w < NW; ++w) {
+        const uint32_t t = ldsw[w];
         if (w < wid) pre += t;
         all += t;
     }
@@ -736,7 +739,7 @@ __device__ __forceinline__ uint32_t block_prefix_256(uint32_t v, uint32_t* lds4,
 }
 
 template <int D>
-__global__ __launch_bounds__(256) void k_split_thin(const float4* __restrict__ pos, const float* __restrict__ states,
+__global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __restrict__ pos, const float* __restrict__ states,
                                                    uint32_t S, uint32_t n, uint32_t nbins, GridParams g,
                                                    const uint32_t* __restrict__ bo,
                                                    const uint32_t* __restrict__ order,
@@ -747,7 +750,7 @@ __global__ __launch_bounds__(256) void k_split_thin(const float4* __restrict__ p
                                                    uint32_t* __restrict__ wl_count, uint32_t tpi, SplitTargets T,
                                                    uint32_t* __restrict__ act_rows, uint32_t* __restrict__ bin_list) {
     constexpr uint32_t K = kDirGroups;
-    __shared__ uint32_t lds_i[4], lds_r[4], lds_f[4];
+    __shared__ uint32_t lds_i[kThinThreads / 64], lds_r[kThinThreads / 64], lds_f[kThinThreads / 64];
     __shared__ uint32_t s_base[3];
     const uint32_t bin = blockIdx.x * blockDim.x + threadIdx.x;
     const bool has_bin = bin < nbins;
@@ -822,9 +825,9 @@ __global__ __launch_bounds__(256) void k_split_thin(const float4* __restrict__ p
     }
     // one reservation per block: work items, compact rows and listed bins
     uint32_t ti, tr, tf;
-    const uint32_t pi_ = block_prefix_256(nitems, lds_i, &ti);
-    const uint32_t pr_ = block_prefix_256(nrows, lds_r, &tr);
-    const uint32_t pf_ = block_prefix_256(fat ? 1u : 0u, lds_f, &tf);
+    const uint32_t pi_ = block_prefix_thin(nitems, lds_i, &ti);
+    const uint32_t pr_ = block_prefix_thin(nrows, lds_r, &tr);
+    const uint32_t pf_ = block_prefix_thin(fat ? 1u : 0u, lds_f, &tf);
     if (threadIdx.x == 0) {
         s_base[0] = ti ? atomicAdd(wl_count, ti) : 0u;
         s_base[1] = tr ? atomicAdd(wl_count + 3, tr) : 0u;
@@ -964,7 +967,7 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
     // more than kThinMax particles, so at most total / (kThinMax + 1) bins are listed
     ProfScope ps(prof, NPA_KERNEL_SPLIT, stream);  // both kernels count as the step's one split
     auto thin = g.dim == 2 ? k_split_thin<2> : k_split_thin<3>;
-    hipLaunchKernelGGL(thin, dim3((nbins + 255) / 256), dim3(256), 0, stream, pos, states, state_dims, n, nbins, g,
+    hipLaunchKernelGGL(thin, dim3((nbins + kThinThreads - 1) / kThinThreads), dim3(kThinThreads), 0, stream, pos, states, state_dims, n, nbins, g,
                        ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(), ws.perm.as<uint32_t>(),
                        ws.inv.as<uint32_t>(), ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(),
                        ws.dir_n.as<uint32_t>(), ws.dir_e.as<int4>(), ws.worklist.as<uint2>(),
