@@ -18,6 +18,7 @@ Prints ONE JSON line with the driver's fields plus:
 --workload c3 / c4 / c5 time BASELINE's other rollout workloads the same way; --workload render
 times the projected 3D render of a device-resident C4 state (particle-views/s, see bench_render);
 --workload adjoint times the perception adjoint on C2's particles (see bench_adjoint).
+--workload raster times the EWA raster of a C4 state's decoded Gaussians (see bench_raster).
 """
 from __future__ import annotations
 
@@ -167,7 +168,7 @@ def bench_render(args, torch) -> int:
     from burn_automata_amd.model import NpaModel
 
     w = syn.workload("c4", particles=args.particles)
-    cfg = RenderLossConfig(image_size=args.image_size)
+    cfg = RenderLossConfig(image_size=args.image_size or 64)
     ex = HipAutomataExecutor()
     ctx = ex.ctx
     n = w["n"]
@@ -261,6 +262,104 @@ def adjoint_work(S: int, d: int, hybrid: bool, state_grad: bool, density_grad: b
         per_pair += 2 * (10 + 9 * d)
     per_particle = S * (6 * d * d + 5 * d + 32) + 120
     return pairs * per_pair + particles * per_particle
+
+
+RASTER_FLOPS_PER_PAIR = 25
+
+
+def bench_raster(args, torch) -> int:
+    """The frame the viewer draws from a device-resident state: decode_gaussians_3d of C4's
+    16,384 surface particles (FixedScale, colours as RGB) and the EWA raster of the Gaussians
+    (npa_state_raster_gaussians_3d) at 1024x1024, the camera framing the surface. Each (pixel,
+    Gaussian) evaluation before the pixel's stop costs the compositing loop 25 fp32 operations, an
+    exp counted as one (offsets 2, power 8, exp, opacity and clamp 2, floor test, 1 - alpha, T
+    product, cut test, colour 9); the count comes from the oracle's raster of the same frame in the
+    cpu_baseline leg (null without it)."""
+    import ctypes as C
+
+    import numpy as np
+
+    from burn_automata_amd import synthetic as syn
+    from burn_automata_amd._lib import lib
+    from burn_automata_amd.config import GaussianDecodeConfig, RasterCamera, RasterColor
+    from burn_automata_amd.executor import HipAutomataExecutor
+    from burn_automata_amd.model import NpaModel
+
+    size = args.image_size or 1024
+    w = syn.workload("c4", particles=args.particles)
+    ex = HipAutomataExecutor()
+    ctx = ex.ctx
+    n = w["n"]
+    state = ex.create_state(NpaModel(w["model"], w["weights"]), torch.from_numpy(w["positions"]).cuda(),
+                            torch.from_numpy(w["states"]).cuda(), 1, n, w["grid"], w["dt"],
+                            w["update_prob"], w["seed"])
+    dcfg = GaussianDecodeConfig()
+    p = w["positions"][:, :3].astype(np.float64)
+    centre = p.mean(axis=0)
+    ext = float(np.abs(p - centre).max())
+    cam = RasterCamera.look_at(tuple(centre + np.array([0.6, 0.9, 2.4]) * ext), tuple(centre), width=size,
+                               height=size, color_mode=RasterColor.Rgb)
+    for _ in range(args.warmup):
+        ex.raster_gaussians_3d(state, dcfg, cam)
+    torch.cuda.synchronize()
+    L = lib()
+    kid = 11  # NPA_KERNEL_RASTER: the raster pipeline after the decode kernel
+    ctx.check(L.npa_profile_reset(ctx.handle))
+    ctx.check(L.npa_profile_enable(ctx.handle, 1 << kid))
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        img = ex.raster_gaussians_3d(state, dcfg, cam)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    tot, cnt = C.c_double(), C.c_uint64()
+    ctx.check(L.npa_profile_read(ctx.handle, kid, C.byref(tot), C.byref(cnt)))
+    ctx.check(L.npa_profile_enable(ctx.handle, 0))
+    pipe_ms = tot.value / max(cnt.value, 1)
+    coverage = float((img[..., 3] > 0.01).float().mean().item())
+    dec = {k: v.cpu().numpy() for k, v in ex.decode_gaussians_3d(state, dcfg).items()}
+    state.close()
+    line = {
+        "metric": "Gaussian-frames/sec, EWA oriented-Gaussian raster of a device-resident state",
+        "value": n * args.steps / elapsed, "unit": "Gaussian-frames/sec", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": 1000.0 * elapsed / args.steps, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (C4 seeded surface particles and states)",
+        "config": {"workload": (f"raster: C4 state ({n} particles, S={w['model'].state_dims}) decoded "
+                                f"(GaussianSh0FixedScale) and drawn at {size}x{size}, 16x16 tiles, "
+                                f"front-to-back, camera framing the surface"),
+                   "particles": n, "image_size": size, "coverage": coverage},
+        "roofline": {"bound": "mfma", "achieved": None, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                     "frac": None, "traffic": None,
+                     "kernel": "raster pipeline (prep + depth sort + scans + emit + tile sort + tiles)",
+                     "engine": "fp32 VALU; exp counted as one operation",
+                     "mean_launch_ms": pipe_ms,
+                     "timing": "HIP events around the raster pipeline of every timed call, on the "
+                               "library's stream"},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+
+        O.build()
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            _, pairs = O.raster_gaussians_3d(dec["position_visibility"], dec["spherical_harmonic"],
+                                             dec["rotation"], dec["scale_opacity"], cam, return_evaluated=True)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= min(args.cpu_seconds, 20.0) or reps >= 64:
+                break
+        threads = O.max_threads()
+        flops = pairs * RASTER_FLOPS_PER_PAIR
+        achieved = flops / (pipe_ms * 1e-3) / 1e12
+        line["roofline"].update({"achieved": achieved, "frac": achieved / PEAK_FP32_TFLOPS,
+                                 "flops_per_launch": flops, "evaluated_pairs": pairs})
+        line["cpu_baseline"] = {
+            "value": n * reps / el, "unit": "Gaussian-frames/sec", "cores": threads, "kind": "port",
+            "sample": (f"{reps} rasters of the same decoded frame (oracle/libnpa_oracle.so "
+                       f"oracle_raster_gaussians_3d, {threads} OpenMP threads over tiles, {el:.1f} s)")}
+    print(json.dumps(line), flush=True)
+    return 0
 
 
 def bench_adjoint(args, torch) -> int:
@@ -368,7 +467,8 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--workload", default="c2")
     ap.add_argument("--particles", type=int, default=None)
-    ap.add_argument("--image-size", type=int, default=64, help="render workload only")
+    ap.add_argument("--image-size", type=int, default=None,
+                    help="render (default 64) and raster (default 1024) workloads only")
     ap.add_argument("--decode-every", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--mlp-engine", choices=("valu", "mfma"), default="valu",
@@ -399,6 +499,8 @@ def main(argv=None) -> int:
         return bench_render(args, torch)
     if args.workload == "adjoint":
         return bench_adjoint(args, torch)
+    if args.workload == "raster":
+        return bench_raster(args, torch)
 
     from burn_automata_amd import kernels as K
     from burn_automata_amd import synthetic as syn

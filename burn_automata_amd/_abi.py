@@ -34,7 +34,7 @@ MLP_MFMA = 1
 
 # kernel ids for npa_profile_read
 KERNEL_NAMES = ("hash_rank", "table_scan", "offsets_scan", "scatter", "density", "perceive", "splat",
-                "mlp", "split", "active", "render")
+                "mlp", "split", "active", "render", "raster")
 
 
 class NpaGridCfg(C.Structure):
@@ -76,6 +76,12 @@ class NpaRenderCfg(C.Structure):
                 ("gaussian_decode_mode", u32), ("world_scale", f32), ("target_samples", u32),
                 ("opacity_logit_bias", f32), ("density_weight", f32), ("color_weight", f32),
                 ("depth_weight", f32)]
+
+
+class NpaRasterCamera(C.Structure):
+    _fields_ = [("view", f32 * 16), ("fx", f32), ("fy", f32), ("cx", f32), ("cy", f32),
+                ("width", u32), ("height", u32), ("near_plane", f32), ("far_plane", f32),
+                ("sh_degree", u32), ("color_mode", u32)]
 
 
 class KernelError(RuntimeError):

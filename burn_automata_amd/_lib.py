@@ -51,6 +51,9 @@ def _decl(L):
     L.npa_render_views.argtypes = [P, P, P, P, P, u32, P, u32, ptr(_abi.NpaRenderCfg), P]
     L.npa_render_attributes.argtypes = [P, P, u32, u32, ptr(_abi.NpaRenderCfg), P, P, P, P]
     L.npa_state_render_views.argtypes = [P, P, u32, ptr(_abi.NpaRenderCfg), P]
+    L.npa_raster_gaussians_3d.argtypes = [P, P, P, P, P, u32, ptr(_abi.NpaRasterCamera), P]
+    L.npa_state_raster_gaussians_3d.argtypes = [P, ptr(_abi.NpaGaussianDecodeCfg),
+                                                ptr(_abi.NpaRasterCamera), P]
     L.npa_manifest_load.argtypes = [P, sz, ptr(P), C.c_char_p, sz]
     L.npa_manifest_load_file.argtypes = [C.c_char_p, ptr(P), C.c_char_p, sz]
     L.npa_manifest_destroy.argtypes = [P]
@@ -90,7 +93,8 @@ def _decl(L):
                  "npa_state_set_mlp_engine", "npa_manifest_load", "npa_manifest_load_file",
                  "npa_manifest_info", "npa_manifest_model", "npa_manifest_initialization",
                  "npa_bpk_encode", "npa_sha256", "npa_render_views", "npa_render_attributes",
-                 "npa_state_render_views", "npa_perceive_adjoint"):
+                 "npa_state_render_views", "npa_perceive_adjoint", "npa_raster_gaussians_3d",
+                 "npa_state_raster_gaussians_3d"):
         getattr(L, name).restype = st
 
 
@@ -106,7 +110,8 @@ EXPORTED = (
     "npa_context_set_mlp_engine", "npa_state_set_mlp_engine", "npa_manifest_load",
     "npa_manifest_load_file", "npa_manifest_destroy", "npa_manifest_info", "npa_manifest_model",
     "npa_manifest_initialization", "npa_bpk_encode", "npa_sha256", "npa_render_views",
-    "npa_render_attributes", "npa_state_render_views", "npa_perceive_adjoint")
+    "npa_render_attributes", "npa_state_render_views", "npa_perceive_adjoint",
+    "npa_raster_gaussians_3d", "npa_state_raster_gaussians_3d")
 
 
 def lib():

@@ -11,6 +11,7 @@
 from __future__ import annotations
 
 import dataclasses
+import math
 from dataclasses import dataclass, field
 from enum import IntEnum
 
@@ -301,6 +302,71 @@ class RenderLossConfig:
         c.density_weight = float(self.density_weight)
         c.color_weight = float(self.color_weight)
         c.depth_weight = float(self.depth_weight)
+        return c
+
+
+class RasterColor(IntEnum):
+    """How the oriented Gaussian raster reads the coefficients (NPA_RASTER_COLOR_*)."""
+
+    SphericalHarmonics = 0  # real SH of degree sh_degree at the view direction, + 0.5, floored at 0
+    Rgb = 1                 # coefficient 0 is the colour (decode_gaussians_3d, gaussian.rs:133-157)
+
+
+@dataclass
+class RasterCamera:
+    """The camera of the oriented Gaussian raster (npa_raster_camera): a row-major world-to-camera
+    matrix (camera looks down -z, +y up), pinhole intrinsics in pixels (y down), clip planes."""
+
+    view: tuple
+    fx: float
+    fy: float
+    cx: float
+    cy: float
+    width: int
+    height: int
+    near_plane: float = 0.1
+    far_plane: float = 1000.0
+    sh_degree: int = 0
+    color_mode: RasterColor = RasterColor.SphericalHarmonics
+
+    @classmethod
+    def look_at(cls, eye, target=(0.0, 0.0, 0.0), up=(0.0, 1.0, 0.0), width: int = 128, height: int = 128,
+                fov_y: float = math.pi / 4, near_plane: float = 0.1, far_plane: float = 1000.0,
+                sh_degree: int = 0, color_mode: RasterColor = RasterColor.SphericalHarmonics) -> "RasterCamera":
+        """A camera at `eye` looking at `target` (bevy's Transform::looking_at with the default
+        PerspectiveProjection: vertical field of view pi/4, near 0.1, far 1000), as the reference's
+        headless raster test places it (crates/bevy_automata/tests/gaussian_gpu_link/headless.rs:23-27)."""
+        eye = [float(v) for v in eye]
+        back = [eye[k] - float(target[k]) for k in range(3)]
+        nb = math.sqrt(sum(v * v for v in back))
+        back = [v / nb for v in back]
+        right = [up[1] * back[2] - up[2] * back[1], up[2] * back[0] - up[0] * back[2],
+                 up[0] * back[1] - up[1] * back[0]]
+        nr = math.sqrt(sum(v * v for v in right))
+        right = [v / nr for v in right]
+        upv = [back[1] * right[2] - back[2] * right[1], back[2] * right[0] - back[0] * right[2],
+               back[0] * right[1] - back[1] * right[0]]
+        view = []
+        for row in (right, upv, back):
+            view += row + [-sum(row[k] * eye[k] for k in range(3))]
+        view += [0.0, 0.0, 0.0, 1.0]
+        f = (height / 2.0) / math.tan(fov_y / 2.0)
+        return cls(tuple(view), f, f, width / 2.0, height / 2.0, width, height, near_plane, far_plane,
+                   sh_degree, color_mode)
+
+    def replace(self, **kw) -> "RasterCamera":
+        return dataclasses.replace(self, **kw)
+
+    def to_c(self) -> _abi.NpaRasterCamera:
+        c = _abi.NpaRasterCamera()
+        if len(self.view) != 16:
+            raise _abi.InvalidArgument("invalid argument: the view matrix has 16 entries")
+        for k, v in enumerate(self.view):
+            c.view[k] = float(v)
+        c.fx, c.fy, c.cx, c.cy = float(self.fx), float(self.fy), float(self.cx), float(self.cy)
+        c.width, c.height = int(self.width), int(self.height)
+        c.near_plane, c.far_plane = float(self.near_plane), float(self.far_plane)
+        c.sh_degree, c.color_mode = int(self.sh_degree), int(self.color_mode)
         return c
 
 

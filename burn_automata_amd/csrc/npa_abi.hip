@@ -1148,6 +1148,96 @@ npa_status npa_state_decode_gaussians_3d(npa_state* s, const npa_gaussian_decode
     return NPA_OK;
 }
 
+static npa_status check_raster_camera(npa_context* ctx, const npa_raster_camera* cam) {
+    if (!cam) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null raster camera");
+    auto bad = [&](const std::string& m) { return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + m); };
+    if (cam->width == 0 || cam->height == 0) return bad("raster width and height must be non-zero");
+    if (cam->width > 16384 || cam->height > 16384) return bad("raster width and height must be <= 16384");
+    const uint64_t tiles = (uint64_t)((cam->width + 15) / 16) * ((cam->height + 15) / 16);
+    if (tiles > 65536) return bad("raster image too large (at most 65536 16x16 tiles)");
+    if (cam->sh_degree > 3) return bad("raster sh_degree must be <= 3, got " + std::to_string(cam->sh_degree));
+    if (cam->color_mode > NPA_RASTER_COLOR_RGB) return bad("unknown raster color mode");
+    for (int k = 0; k < 16; ++k)
+        if (!std::isfinite(cam->view[k])) return bad("raster view matrix must be finite");
+    if (!std::isfinite(cam->fx) || cam->fx <= 0.0f || !std::isfinite(cam->fy) || cam->fy <= 0.0f)
+        return bad("raster focal lengths must be finite and positive");
+    if (!std::isfinite(cam->cx) || !std::isfinite(cam->cy)) return bad("raster principal point must be finite");
+    if (!std::isfinite(cam->near_plane) || cam->near_plane <= 0.0f)
+        return bad("raster near_plane must be finite and positive, got " + fmt_f(cam->near_plane));
+    if (!(cam->far_plane > cam->near_plane))
+        return bad("raster far_plane must exceed near_plane, got " + fmt_f(cam->far_plane));
+    return NPA_OK;
+}
+
+npa_status npa_raster_gaussians_3d(npa_context* ctx, const float* position_visibility, const float* spherical_harmonic,
+                                   const float* rotation, const float* scale_opacity, uint32_t count,
+                                   const npa_raster_camera* camera, float* image) {
+    if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
+    npa_status st = check_raster_camera(ctx, camera);
+    if (st) return st;
+    if (!image) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null image");
+    if (count && (!position_visibility || !spherical_harmonic || !rotation || !scale_opacity))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null Gaussian arrays");
+    if (count >= (1u << 31)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: too many Gaussians");
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint64_t K = (uint64_t)(camera->sh_degree + 1) * (camera->sh_degree + 1);
+    HostIO io(ctx);
+    const float4* pv = (const float4*)io.in(position_visibility, (uint64_t)count * 16);
+    const float* sh = io.in(spherical_harmonic, (uint64_t)count * K * 12);
+    const float4* rot = (const float4*)io.in(rotation, (uint64_t)count * 16);
+    const float4* so = (const float4*)io.in(scale_opacity, (uint64_t)count * 16);
+    float* img = io.out(image, (uint64_t)camera->width * camera->height * 16);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if ((count && (!aligned16(pv) || !aligned16(rot) || !aligned16(so))) || !aligned16(img))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: 4-wide arrays and the image must be 16-byte aligned");
+    NPA_HIP(ctx, npa::launch_raster_gaussians(pv, sh, rot, so, count, *camera, img, ctx->splat_ws, ctx->stream,
+                                              &ctx->prof),
+            "raster");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
+npa_status npa_state_raster_gaussians_3d(npa_state* s, const npa_gaussian_decode_cfg* cfg,
+                                         const npa_raster_camera* camera, float* image) {
+    if (!s) return NPA_ERR_INVALID_ARGUMENT;
+    npa_context* ctx = s->ctx;
+    npa_status st = check_decode(ctx, s->model.state_dims, cfg);
+    if (st) return st;
+    st = check_raster_camera(ctx, camera);
+    if (st) return st;
+    if (!image) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null image");
+    npa_raster_camera cam = *camera;
+    cam.sh_degree = cfg->mode == NPA_DECODE_SH0_ORIENTED ? cfg->sh_degree : 0;
+    if (cam.sh_degree > 3)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT,
+                    "invalid argument: raster sh_degree must be <= 3, got " + std::to_string(cam.sh_degree));
+    const uint64_t total = (uint64_t)s->B * s->N;
+    if (total >= (1ull << 31)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: too many Gaussians");
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    const uint64_t K = (uint64_t)(cam.sh_degree + 1) * (cam.sh_degree + 1);
+    const uint64_t t1 = total ? total : 1;
+    const uint64_t sh_bytes = (t1 * K * 12 + 15) / 16 * 16;
+    NPA_HIP(ctx, ctx->splat_ws.decoded.reserve(t1 * 48 + sh_bytes), "alloc");
+    char* base = ctx->splat_ws.decoded.as<char>();
+    float* dpv = (float*)base;
+    float* drot = (float*)(base + t1 * 16);
+    float* dso = (float*)(base + t1 * 32);
+    float* dsh = (float*)(base + t1 * 48);
+    HostIO io(ctx);
+    float* img = io.out(image, (uint64_t)cam.width * cam.height * 16);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if (!aligned16(img)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: the image must be 16-byte aligned");
+    NPA_HIP(ctx, npa::launch_decode_gaussians(s->pos[s->cur].as<float4>(), s->states[s->cur].as<float>(),
+                                              (uint32_t)total, s->model.state_dims, *cfg, dpv, dsh, drot, dso,
+                                              ctx->stream),
+            "decode");
+    NPA_HIP(ctx, npa::launch_raster_gaussians((const float4*)dpv, dsh, (const float4*)drot, (const float4*)dso,
+                                              (uint32_t)total, cam, img, ctx->splat_ws, ctx->stream, &ctx->prof),
+            "raster");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
 npa_status npa_state_pair_counts(npa_state* s, uint64_t* candidates, uint64_t* pairs, uint64_t* targets,
                                  uint64_t* target_candidates, uint64_t* target_pairs) {
     if (!s) return NPA_ERR_INVALID_ARGUMENT;

@@ -356,7 +356,7 @@ __global__ __launch_bounds__(256) void k_splat_tiles(SplatParams P, const SplatP
 
 void SplatWorkspace::release() {
     for (DevBuf* b : {&params, &item_start, &keys, &vals, &sorted, &ranks, &table, &totals, &offsets, &count, &flags, &scan,
-                      &attrs, &partials, &chunks})
+                      &attrs, &partials, &chunks, &order, &decoded})
         b->release();
 }
 
@@ -902,6 +902,401 @@ hipError_t launch_render_attributes(const float* states, uint32_t count, uint32_
     if (count == 0) return hipSuccess;
     hipLaunchKernelGGL(k_render_attrs, dim3((count + 255) / 256), dim3(256), 0, stream, states, count, S, cfg, colors,
                        opacities, sigmas, derivatives);
+    return hipGetLastError();
+}
+
+
+// ------------------------------------------------------------------ oriented Gaussian raster
+// The EWA raster of the planar Gaussian export (the image the reference's viewer draws through
+// the un-vendored bevy_gaussian_splatting 8.0.1, crates/bevy_automata/src/viewer/cloud.rs:80-97),
+// restating the published 3D Gaussian splatting forward pass (Kerbl et al. 2023; EWA projection,
+// Zwicker et al. 2001):
+//   k_raster_prep      per Gaussian: camera-frame centre, cull, Sigma = R S S^T R^T, the EWA 2D
+//                      covariance + 0.3 px^2, its conic, 3-sigma radius, tile rectangle, colour
+//                      (spherical harmonics or RGB), the tile count and the depth key;
+//   depth order        three stable counting-sort passes (11 + 10 + 10 bits) of the positive
+//                      depth's float bits: depth ascending, ties by index;
+//   k_raster_emit      the (tile, Gaussian) items in depth order, after a prefix of the tile
+//                      counts (its total read back to size the item buffers);
+//   stable key sort    by tile -> per-tile lists in depth order;
+//   k_raster_tiles     one 256-thread block per 16x16 tile, one pixel per thread: the list is
+//                      staged through LDS 256 Gaussians at a time; each pixel composites front to
+//                      back and stops at the transmittance cut; the block leaves when every pixel
+//                      has stopped.
+struct RasterParams {
+    float view[12];
+    float fx, fy, cx, cy, limx, limy, near_plane, far_plane;
+    float campos[3];
+    uint32_t width, height, tiles_x, tiles_y, count, K, sh_degree, color_mode;
+};
+
+struct alignas(16) RasterSplat {  // 48 bytes
+    float mx, my, ca, cb;
+    float cc, opacity, r, g;
+    float b;
+    uint32_t rx;  // tile columns [rx & 0xffff, rx >> 16)
+    uint32_t ry;  // tile rows
+    uint32_t pad;
+};
+
+constexpr uint32_t kRasterMaxAxis = 16384;  // pixels per axis: tile indices fit 16 bits
+constexpr uint32_t kDepthCulled = 0x7f800000u;  // +inf: sorts after every live depth
+
+__device__ __forceinline__ float raster_clamp(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+__global__ __launch_bounds__(256) void k_raster_prep(RasterParams P, const float4* __restrict__ pv,
+                                                     const float* __restrict__ sh, const float4* __restrict__ rot,
+                                                     const float4* __restrict__ so, RasterSplat* __restrict__ out,
+                                                     uint32_t* __restrict__ ntiles, uint32_t* __restrict__ dkey,
+                                                     uint32_t* __restrict__ d_count) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i == 0) *d_count = P.count;
+    if (i >= P.count) return;
+    ntiles[i] = 0;
+    dkey[i] = kDepthCulled;
+    const float4 p = pv[i];
+    if (!(p.w > 0.0f)) return;
+    const float* V = P.view;
+    const float vx = V[0] * p.x + V[1] * p.y + V[2] * p.z + V[3];
+    const float vy = V[4] * p.x + V[5] * p.y + V[6] * p.z + V[7];
+    const float vz = V[8] * p.x + V[9] * p.y + V[10] * p.z + V[11];
+    const float tx = vx, ty = -vy, tz = -vz;  // x right, y down, z forward
+    if (!(tz > P.near_plane) || !(tz <= P.far_plane)) return;
+    const float4 q4 = rot[i];
+    float qw = q4.x, qx = q4.y, qy = q4.z, qz = q4.w;
+    const float qn = sqrtf(qw * qw + qx * qx + qy * qy + qz * qz);
+    if (qn > 0.0f && qn < INFINITY) {
+        qw = qw / qn; qx = qx / qn; qy = qy / qn; qz = qz / qn;
+    } else {
+        qw = 1.0f; qx = qy = qz = 0.0f;
+    }
+    const float R[3][3] = {
+        {1.0f - 2.0f * (qy * qy + qz * qz), 2.0f * (qx * qy - qw * qz), 2.0f * (qx * qz + qw * qy)},
+        {2.0f * (qx * qy + qw * qz), 1.0f - 2.0f * (qx * qx + qz * qz), 2.0f * (qy * qz - qw * qx)},
+        {2.0f * (qx * qz - qw * qy), 2.0f * (qy * qz + qw * qx), 1.0f - 2.0f * (qx * qx + qy * qy)}};
+    const float4 s4 = so[i];
+    const float sc[3] = {s4.x, s4.y, s4.z};
+    float M[3][3], S[3][3];
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+#pragma unroll
+        for (int c = 0; c < 3; ++c) M[r][c] = R[r][c] * sc[c];
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+#pragma unroll
+        for (int c = 0; c < 3; ++c) S[r][c] = M[r][0] * M[c][0] + M[r][1] * M[c][1] + M[r][2] * M[c][2];
+    const float W[3][3] = {{V[0], V[1], V[2]}, {-V[4], -V[5], -V[6]}, {-V[8], -V[9], -V[10]}};
+    const float jx = raster_clamp(tx / tz, -P.limx, P.limx) * tz;
+    const float jy = raster_clamp(ty / tz, -P.limy, P.limy) * tz;
+    const float J[2][3] = {{P.fx / tz, 0.0f, -(P.fx * jx) / (tz * tz)}, {0.0f, P.fy / tz, -(P.fy * jy) / (tz * tz)}};
+    float T[2][3], U[2][3];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 3; ++c) T[r][c] = J[r][0] * W[0][c] + J[r][1] * W[1][c] + J[r][2] * W[2][c];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 3; ++c) U[r][c] = T[r][0] * S[0][c] + T[r][1] * S[1][c] + T[r][2] * S[2][c];
+    const float a = (U[0][0] * T[0][0] + U[0][1] * T[0][1] + U[0][2] * T[0][2]) + 0.3f;
+    const float b = U[0][0] * T[1][0] + U[0][1] * T[1][1] + U[0][2] * T[1][2];
+    const float c = (U[1][0] * T[1][0] + U[1][1] * T[1][1] + U[1][2] * T[1][2]) + 0.3f;
+    const float det = a * c - b * b;
+    if (!(det > 0.0f) || !(det < INFINITY)) return;
+    const float mid = 0.5f * (a + c);
+    const float lam = mid + sqrtf(fmaxf(0.1f, mid * mid - det));
+    const float radius = ceilf(3.0f * sqrtf(lam));
+    const float mx = P.cx + P.fx * tx / tz;
+    const float my = P.cy + P.fy * ty / tz;
+    if (!(fabsf(mx) < 1e30f) || !(fabsf(my) < 1e30f) || !(radius < 1e30f)) return;
+    const uint32_t x0 = (uint32_t)raster_clamp(floorf((mx - radius) / 16.0f), 0.0f, (float)P.tiles_x);
+    const uint32_t x1 = (uint32_t)raster_clamp(floorf((mx + radius) / 16.0f) + 1.0f, 0.0f, (float)P.tiles_x);
+    const uint32_t y0 = (uint32_t)raster_clamp(floorf((my - radius) / 16.0f), 0.0f, (float)P.tiles_y);
+    const uint32_t y1 = (uint32_t)raster_clamp(floorf((my + radius) / 16.0f) + 1.0f, 0.0f, (float)P.tiles_y);
+    if (x0 >= x1 || y0 >= y1) return;
+    RasterSplat o;
+    o.mx = mx;
+    o.my = my;
+    o.ca = c / det;
+    o.cb = -b / det;
+    o.cc = a / det;
+    o.opacity = s4.w;
+    o.rx = x0 | (x1 << 16);
+    o.ry = y0 | (y1 << 16);
+    o.pad = 0;
+    const float* coef = sh + (uint64_t)i * P.K * 3;
+    if (P.color_mode == NPA_RASTER_COLOR_RGB) {
+        o.r = coef[0];
+        o.g = coef[1];
+        o.b = coef[2];
+    } else {
+        float d[3] = {p.x - P.campos[0], p.y - P.campos[1], p.z - P.campos[2]};
+        const float dn = sqrtf(d[0] * d[0] + d[1] * d[1] + d[2] * d[2]);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) d[k] = dn > 0.0f ? d[k] / dn : 0.0f;
+        // real spherical harmonics, bands 0..3, in the 3DGS sign convention (Condon-Shortley phase)
+        const float x = d[0], y = d[1], z = d[2];
+        float basis[16];
+        basis[0] = 0.28209479177387814f;
+        if (P.sh_degree > 0) {
+            basis[1] = -0.4886025119029199f * y;
+            basis[2] = 0.4886025119029199f * z;
+            basis[3] = -0.4886025119029199f * x;
+        }
+        if (P.sh_degree > 1) {
+            const float xx = x * x, yy = y * y, zz = z * z;
+            basis[4] = 1.0925484305920792f * (x * y);
+            basis[5] = -1.0925484305920792f * (y * z);
+            basis[6] = 0.31539156525252005f * (2.0f * zz - xx - yy);
+            basis[7] = -1.0925484305920792f * (x * z);
+            basis[8] = 0.5462742152960396f * (xx - yy);
+            if (P.sh_degree > 2) {
+                basis[9] = -0.5900435899266435f * y * (3.0f * xx - yy);
+                basis[10] = 2.890611442640554f * (x * y) * z;
+                basis[11] = -0.4570457994644658f * y * (4.0f * zz - xx - yy);
+                basis[12] = 0.3731763325901154f * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);
+                basis[13] = -0.4570457994644658f * x * (4.0f * zz - xx - yy);
+                basis[14] = 1.445305721320277f * z * (xx - yy);
+                basis[15] = -0.5900435899266435f * x * (xx - 3.0f * yy);
+            }
+        }
+        float rgb[3];
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) {
+            float acc = 0.0f;
+            for (uint32_t k = 0; k < P.K; ++k) acc += basis[k] * coef[k * 3 + ch];
+            acc += 0.5f;
+            rgb[ch] = acc > 0.0f ? acc : 0.0f;
+        }
+        o.r = rgb[0];
+        o.g = rgb[1];
+        o.b = rgb[2];
+    }
+    out[i] = o;
+    ntiles[i] = (x1 - x0) * (y1 - y0);
+    dkey[i] = __float_as_uint(tz);
+}
+
+// keys_out[j] = bits [shift, shift + log2(mask + 1)) of the depth key of Gaussian order[j] (j when
+// order is null)
+__global__ __launch_bounds__(256) void k_raster_digits(const uint32_t* __restrict__ dkey,
+                                                       const uint32_t* __restrict__ order, uint32_t count,
+                                                       uint32_t shift, uint32_t mask, uint32_t* __restrict__ keys) {
+    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= count) return;
+    keys[j] = (dkey[order ? order[j] : j] >> shift) & mask;
+}
+
+__global__ __launch_bounds__(256) void k_raster_gather_counts(const uint32_t* __restrict__ ntiles,
+                                                              const uint32_t* __restrict__ order, uint32_t count,
+                                                              uint32_t* __restrict__ out) {
+    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j < count) out[j] = ntiles[order[j]];
+}
+
+// The 64-bit sum of the tile counts (the 32-bit scan total can wrap).
+__global__ __launch_bounds__(1024) void k_raster_sum64(const uint32_t* __restrict__ in, uint32_t count,
+                                                       unsigned long long* __restrict__ total) {
+    __shared__ unsigned long long lds[16];
+    unsigned long long s = 0;
+    for (uint32_t k = threadIdx.x; k < count; k += blockDim.x) s += in[k];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long t = 0;
+        for (uint32_t w = 0; w < blockDim.x / 64; ++w) t += lds[w];
+        *total = t;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_raster_emit(RasterParams P, const RasterSplat* __restrict__ sp,
+                                                     const uint32_t* __restrict__ order,
+                                                     const uint32_t* __restrict__ start, uint32_t* __restrict__ keys,
+                                                     uint32_t* __restrict__ vals) {
+    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= P.count) return;
+    const uint32_t g = order[j];
+    const uint32_t n = start[j + 1] - start[j];
+    if (n == 0) return;
+    const uint32_t rx = sp[g].rx, ry = sp[g].ry;
+    const uint32_t x0 = rx & 0xffffu, x1 = rx >> 16, y0 = ry & 0xffffu, y1 = ry >> 16;
+    uint32_t k = start[j];
+    for (uint32_t y = y0; y < y1; ++y)
+        for (uint32_t x = x0; x < x1; ++x) {
+            keys[k] = y * P.tiles_x + x;
+            vals[k] = g;
+            ++k;
+        }
+}
+
+__global__ __launch_bounds__(256) void k_raster_tiles(RasterParams P, const RasterSplat* __restrict__ sp,
+                                                      const uint32_t* __restrict__ offsets,
+                                                      const uint32_t* __restrict__ sorted, float4* __restrict__ image) {
+    __shared__ float4 la[256], lb[256];
+    __shared__ float lc[256];
+    const uint32_t tile = blockIdx.x;
+    const uint32_t px = (tile % P.tiles_x) * 16 + (threadIdx.x & 15);
+    const uint32_t py = (tile / P.tiles_x) * 16 + (threadIdx.x >> 4);
+    const bool inside = px < P.width && py < P.height;
+    const float pxc = (float)px + 0.5f, pyc = (float)py + 0.5f;
+    const uint32_t begin = offsets[tile], end = offsets[tile + 1];
+    float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
+    int done = inside ? 0 : 1;
+    for (uint32_t base = begin; base < end; base += 256) {
+        if (__syncthreads_count(done) == (int)blockDim.x) break;
+        const uint32_t k = base + threadIdx.x;
+        if (k < end) {
+            const float4* s4 = reinterpret_cast<const float4*>(sp + sorted[k]);
+            la[threadIdx.x] = s4[0];
+            lb[threadIdx.x] = s4[1];
+            lc[threadIdx.x] = s4[2].x;
+        }
+        __syncthreads();
+        const uint32_t n = end - base < 256 ? end - base : 256;
+        for (uint32_t u = 0; u < n && !done; ++u) {
+            const float4 A = la[u], B = lb[u];  // (mx, my, ca, cb), (cc, opacity, r, g)
+            const float dx = A.x - pxc, dy = A.y - pyc;
+            const float power = -0.5f * (A.z * dx * dx + B.x * dy * dy) - A.w * dx * dy;
+            if (power > 0.0f) continue;
+            const float alpha = fminf(0.99f, B.y * expf(power));
+            if (alpha < 1.0f / 255.0f) continue;
+            const float next = T * (1.0f - alpha);
+            if (next < 0.0001f) {
+                done = 1;
+                break;
+            }
+            cr += B.z * alpha * T;
+            cg += B.w * alpha * T;
+            cb += lc[u] * alpha * T;
+            T = next;
+        }
+    }
+    if (inside) image[(uint64_t)py * P.width + px] = make_float4(cr, cg, cb, 1.0f - T);
+}
+
+hipError_t launch_raster_gaussians(const float4* pv, const float* sh, const float4* rot, const float4* so,
+                                   uint32_t count, const npa_raster_camera& cam, float* image, SplatWorkspace& ws,
+                                   hipStream_t stream, Profiler* prof) {
+    if (cam.width == 0 || cam.height == 0 || cam.width > kRasterMaxAxis || cam.height > kRasterMaxAxis ||
+        cam.sh_degree > 3 || count >= (1u << 31))
+        return hipErrorInvalidValue;
+    RasterParams P{};
+    for (int k = 0; k < 12; ++k) P.view[k] = cam.view[k];
+    P.fx = cam.fx;
+    P.fy = cam.fy;
+    P.cx = cam.cx;
+    P.cy = cam.cy;
+    P.limx = 1.3f * fmaxf(cam.cx, (float)cam.width - cam.cx) / cam.fx;
+    P.limy = 1.3f * fmaxf(cam.cy, (float)cam.height - cam.cy) / cam.fy;
+    P.near_plane = cam.near_plane;
+    P.far_plane = cam.far_plane;
+    for (int k = 0; k < 3; ++k)  // camera centre -R^T t
+        P.campos[k] = -(cam.view[k] * cam.view[3] + cam.view[4 + k] * cam.view[7] + cam.view[8 + k] * cam.view[11]);
+    P.width = cam.width;
+    P.height = cam.height;
+    P.tiles_x = (cam.width + 15) / 16;
+    P.tiles_y = (cam.height + 15) / 16;
+    P.count = count;
+    P.K = (cam.sh_degree + 1) * (cam.sh_degree + 1);
+    P.sh_degree = cam.sh_degree;
+    P.color_mode = cam.color_mode;
+    const uint32_t ntile_total = P.tiles_x * P.tiles_y;
+    if (ntile_total > 65536) return hipErrorInvalidValue;  // the key sort's bin limit
+    HashgridPlan lo, hi;
+    if (!make_key_sort_plan(count, 2048, &lo) || !make_key_sort_plan(count, 1024, &hi)) return hipErrorInvalidValue;
+    const uint64_t n1 = count ? count : 1;
+    hipError_t e;
+#define NPA_RES(buf, n) \
+    if ((e = (buf).reserve((size_t)(n))) != hipSuccess) return e;
+    NPA_RES(ws.params, n1 * sizeof(RasterSplat));
+    NPA_RES(ws.item_start, (4 * n1 + 1) * 4);  // ntiles, depth keys, ordered counts, starts (+1)
+    NPA_RES(ws.order, 2 * n1 * 4);
+    NPA_RES(ws.keys, n1 * 4);
+    NPA_RES(ws.ranks, n1 * 4);
+    NPA_RES(ws.table, std::max(lo.table_entries, hi.table_entries) * 4);
+    NPA_RES(ws.totals, std::max<uint64_t>(2048, ntile_total) * 4);
+    NPA_RES(ws.offsets, (std::max<uint64_t>(2048, ntile_total) + 1) * 4);
+    NPA_RES(ws.count, 64);
+    NPA_RES(ws.scan, (2 * (n1 / kScanBlock + 1) + 2) * 4);
+    NPA_RES(ws.flags, 64);
+    ProfScope ps(prof, NPA_KERNEL_RASTER, stream);
+    RasterSplat* sp = ws.params.as<RasterSplat>();
+    uint32_t* ntiles = ws.item_start.as<uint32_t>();
+    uint32_t* dkey = ntiles + n1;
+    uint32_t* ocounts = dkey + n1;
+    uint32_t* start = ocounts + n1;  // n1 + 1 entries
+    uint32_t* ord_a = ws.order.as<uint32_t>();
+    uint32_t* ord_b = ord_a + n1;
+    uint32_t* d_items = ws.count.as<uint32_t>();      // item count (the tile sort's key count)
+    uint32_t* d_count = d_items + 1;                   // Gaussian count (the depth sort's key count)
+    unsigned long long* d_total64 = reinterpret_cast<unsigned long long*>(d_items + 2);
+    hipLaunchKernelGGL(k_raster_prep, dim3((uint32_t)std::max<uint64_t>(1, (count + 255) / 256)), dim3(256), 0, stream,
+                       P, pv, sh, rot, so, sp, ntiles, dkey, d_count);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    // depth order: stable LSD passes over bits 0-10, 11-20, 21-30 (depth keys are non-negative floats)
+    const uint32_t shifts[3] = {0, 11, 21}, masks[3] = {0x7ffu, 0x3ffu, 0x3ffu};
+    const uint32_t* in_order = nullptr;
+    uint32_t* outs[3] = {ord_a, ord_b, ord_a};
+    for (int pass = 0; pass < 3 && count; ++pass) {
+        hipLaunchKernelGGL(k_raster_digits, dim3((count + 255) / 256), dim3(256), 0, stream, dkey, in_order, count,
+                           shifts[pass], masks[pass], ws.keys.as<uint32_t>());
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        e = launch_key_sort(pass == 0 ? lo : hi, ws.keys.as<uint32_t>(), in_order, d_count, count,
+                            ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(), ws.totals.as<uint32_t>(),
+                            ws.offsets.as<uint32_t>(), outs[pass], ws.flags.as<uint32_t>(), stream);
+        if (e != hipSuccess) return e;
+        in_order = outs[pass];
+    }
+    const uint32_t* order = ord_a;
+    if (count) {
+        hipLaunchKernelGGL(k_raster_gather_counts, dim3((count + 255) / 256), dim3(256), 0, stream, ntiles, order,
+                           count, ocounts);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    {  // start = exclusive prefix of the ordered counts; start[count] = total
+        const uint32_t nb = (count + kScanBlock - 1) / kScanBlock;
+        uint32_t* sums = ws.scan.as<uint32_t>();
+        if (nb) {
+            hipLaunchKernelGGL(k_scan_partials, dim3(nb), dim3(256), 0, stream, ocounts, count, sums);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL(k_scan_1block, dim3(1), dim3(1024), 0, stream, sums, sums + nb + 1, nb, start + count);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (nb) {
+            hipLaunchKernelGGL(k_scan_apply, dim3(nb), dim3(256), 0, stream, ocounts, start, count, sums + nb + 1);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL(k_raster_sum64, dim3(1), dim3(1024), 0, stream, ocounts, count, d_total64);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    unsigned long long total = 0;
+    if ((e = hipMemcpyAsync(&total, d_total64, 8, hipMemcpyDeviceToHost, stream)) != hipSuccess) return e;
+    if ((e = hipStreamSynchronize(stream)) != hipSuccess) return e;
+    if (total >= (1ull << 31)) return hipErrorInvalidValue;  // more (tile, Gaussian) items than the sort takes
+    const uint32_t items = (uint32_t)total;
+    HashgridPlan plan;
+    if (!make_key_sort_plan(items, ntile_total, &plan)) return hipErrorInvalidValue;
+    const uint64_t i1 = items ? items : 1;
+    NPA_RES(ws.keys, std::max(i1, n1) * 4);
+    NPA_RES(ws.vals, i1 * 4);
+    NPA_RES(ws.sorted, i1 * 4);
+    NPA_RES(ws.ranks, std::max(i1, n1) * 4);
+    NPA_RES(ws.table, plan.table_entries * 4);
+#undef NPA_RES
+    if (count) {
+        hipLaunchKernelGGL(k_raster_emit, dim3((count + 255) / 256), dim3(256), 0, stream, P, sp, order, start,
+                           ws.keys.as<uint32_t>(), ws.vals.as<uint32_t>());
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    // the scan wrote the item count to start[count]; the tile sort reads it from there
+    e = launch_key_sort(plan, ws.keys.as<uint32_t>(), ws.vals.as<uint32_t>(), start + count, items,
+                        ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(), ws.totals.as<uint32_t>(),
+                        ws.offsets.as<uint32_t>(), ws.sorted.as<uint32_t>(), ws.flags.as<uint32_t>(), stream);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_raster_tiles, dim3(ntile_total), dim3(256), 0, stream, P, sp, ws.offsets.as<uint32_t>(),
+                       ws.sorted.as<uint32_t>(), reinterpret_cast<float4*>(image));
     return hipGetLastError();
 }
 

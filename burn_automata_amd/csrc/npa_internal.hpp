@@ -312,6 +312,8 @@ struct SplatWorkspace {
     DevBuf params, item_start, keys, vals, sorted, ranks, table, totals, offsets, count, flags, scan;
     DevBuf attrs;  // render attributes of a state's particles: colours [n][3], opacities [n], sigmas [n]
     DevBuf partials, chunks;  // render: per-chunk partial tiles; chunk counts, starts and total
+    DevBuf order;    // oriented raster: depth-order ping-pong
+    DevBuf decoded;  // oriented raster of a state: its decoded Gaussians
     void release();
 };
 // Particle n is drawn into window n / per_window of a grid of `windows` windows, win_cols per
@@ -328,6 +330,12 @@ hipError_t launch_render_views(const float4* pos, const float* colors, const flo
                                const float* sigmas, uint32_t count, const uint32_t* views, uint32_t nviews,
                                const npa_render_cfg& cfg, float* images, SplatWorkspace& ws,
                                hipStream_t stream, Profiler* prof);
+// EWA raster of oriented Gaussians (npa_raster_gaussians_3d): image[height][width][4]. Reads the
+// (tile, Gaussian) item total back to the host (one stream synchronisation).
+hipError_t launch_raster_gaussians(const float4* position_visibility, const float* spherical_harmonic,
+                                   const float4* rotation, const float4* scale_opacity, uint32_t count,
+                                   const npa_raster_camera& cam, float* image, SplatWorkspace& ws,
+                                   hipStream_t stream, Profiler* prof);
 // state_tail_render_attributes (render_loss/attributes.rs:15-87); derivatives may be null.
 hipError_t launch_render_attributes(const float* states, uint32_t count, uint32_t state_dims,
                                     const npa_render_cfg& cfg, float* colors, float* opacities,

@@ -144,6 +144,18 @@ class HipAutomataExecutor:
         return {"position_visibility": pv, "spherical_harmonic": sh, "rotation": rot,
                 "scale_opacity": so}
 
+    def raster_gaussians_3d(self, state: HipAutomataState, cfg: GaussianDecodeConfig, camera):
+        """decode_gaussians_3d of the current particles, then the EWA raster of them
+        (npa_state_raster_gaussians_3d): [height, width, 4]. The raster evaluates
+        cfg.sh_degree (oriented mode) or 0; camera.color_mode says how it reads the coefficients."""
+        import torch
+
+        img = torch.empty((camera.height, camera.width, 4), dtype=torch.float32,
+                          device=f"cuda:{self.ctx.device}")
+        self.ctx.check(lib().npa_state_raster_gaussians_3d(state.handle, C.byref(cfg.to_c()),
+                                                           C.byref(camera.to_c()), ptr(img)))
+        return img
+
     def pair_counts(self, state: HipAutomataState):
         """(candidates visited, pairs accepted) of the neighbour walk on the current particles."""
         c = self.work_counts(state)

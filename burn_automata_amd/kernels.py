@@ -26,7 +26,7 @@ import numpy as np
 
 from . import _abi
 from ._lib import lib
-from .config import (ALL_VIEWS, GaussianDecodeConfig, HashGridConfig, PerceptionOptions,
+from .config import (ALL_VIEWS, GaussianDecodeConfig, RasterCamera, HashGridConfig, PerceptionOptions,
                      RenderLossConfig, Splat2dConfig)
 from .runtime import default_context, device_f32, ptr
 
@@ -322,3 +322,27 @@ def render_attributes(states, state_dims: int, cfg: RenderLossConfig, ctx=None):
     ctx.check(lib().npa_render_attributes(ctx.handle, ptr(st), n, state_dims, C.byref(cfg.to_c()),
                                           ptr(col), ptr(op), ptr(sg), ptr(dv)))
     return col, op, sg, dv
+
+
+def raster_gaussians_3d(position_visibility, spherical_harmonic, rotation, scale_opacity,
+                        camera: RasterCamera, ctx=None):
+    """The EWA raster of oriented Gaussians (npa_raster_gaussians_3d): the frame the viewer draws
+    from the planar export through bevy_gaussian_splatting (crates/bevy_automata/src/viewer/cloud.rs:80-97),
+    as the published 3D Gaussian splatting forward pass. spherical_harmonic holds
+    (camera.sh_degree + 1)^2 coefficients per Gaussian. Returns [height, width, 4]: premultiplied
+    r, g, b and 1 - transmittance."""
+    ctx = ctx or default_context()
+    torch = _torch()
+    pv = device_f32(position_visibility, device=ctx.device).reshape(-1, 4)
+    n = pv.shape[0]
+    K = (int(camera.sh_degree) + 1) ** 2
+    sh = device_f32(spherical_harmonic, device=ctx.device).reshape(-1)
+    rot = device_f32(rotation, device=ctx.device).reshape(-1, 4)
+    so = device_f32(scale_opacity, device=ctx.device).reshape(-1, 4)
+    if sh.numel() != n * K * 3 or rot.shape[0] != n or so.shape[0] != n:
+        raise AssertionError("position_visibility, spherical_harmonic (K coefficients of 3), rotation "
+                             "and scale_opacity differ in length")
+    img = torch.empty((camera.height, camera.width, 4), dtype=torch.float32, device=f"cuda:{ctx.device}")
+    ctx.check(lib().npa_raster_gaussians_3d(ctx.handle, ptr(pv), ptr(sh), ptr(rot), ptr(so), n,
+                                            C.byref(camera.to_c()), ptr(img)))
+    return img

@@ -352,6 +352,51 @@ npa_status npa_state_decode_gaussians_3d(npa_state* state, const npa_gaussian_de
                                          float* position_visibility, float* spherical_harmonic,
                                          float* rotation, float* scale_opacity);
 
+/* ------------------------------------------------------- oriented Gaussian raster */
+/* The EWA raster of the planar Gaussian export: the image the viewer draws from
+ * decode_gaussians_3d / write_gaussian_main output through bevy_gaussian_splatting 8.0.1
+ * (Cargo.toml:23; crates/bevy_automata/src/viewer/cloud.rs:80-97: 3D clouds, radix sort on
+ * 32 depth bits). That crate is not vendored and no reference test pins its pixels, so this
+ * restates the published 3D Gaussian splatting forward pass (Kerbl et al. 2023; the EWA
+ * projection of Zwicker et al. 2001):
+ *   camera frame: v = view * [p, 1] (camera looks down -z, +y up, as a bevy view matrix);
+ *     depth z = -v.z; Gaussians with visibility <= 0, z <= near_plane or z > far_plane are culled;
+ *   covariance: Sigma = R diag(s)^2 R^T from the unit quaternion (w, x, y, z) and scale s;
+ *     Sigma2d = J W Sigma W^T J^T + 0.3 I (W: the view rotation with y and z flipped, J: the
+ *     perspective Jacobian, its x/z and y/z clamped to 1.3x the image half-extent);
+ *   footprint: the conic Sigma2d^-1 and radius ceil(3 sqrt(lambda_max)); the 16x16 pixel tiles
+ *     within the radius of the centre (cx + fx x/z, cy + fy y'/z, y' = -v.y) list the Gaussian;
+ *   colour: NPA_RASTER_COLOR_SH evaluates the real spherical harmonics of degree sh_degree at
+ *     the direction from the camera centre (coefficients [n][(d+1)^2][3]) plus 0.5, floored at 0;
+ *     NPA_RASTER_COLOR_RGB takes coefficient 0 as the colour (decode_gaussians_3d stores
+ *     clamp(state + 0.5, 0, 1) there, gaussian.rs:133-157);
+ *   compositing: each pixel (centre at +0.5) walks its tile's Gaussians front to back (depth
+ *     ascending, ties by index): power = -(a dx^2 + c dy^2)/2 - b dx dy (skip when > 0),
+ *     alpha = min(0.99, opacity e^power) (skip below 1/255); it stops before the Gaussian that
+ *     would take transmittance T below 1e-4; rgb += colour alpha T, T *= 1 - alpha.
+ * image[height][width][4] = premultiplied r, g, b and 1 - T; it is overwritten. */
+enum { NPA_RASTER_COLOR_SH = 0, NPA_RASTER_COLOR_RGB = 1 };
+typedef struct npa_raster_camera {
+    float view[16];           /* row-major world -> camera */
+    float fx, fy;             /* focal lengths, pixels */
+    float cx, cy;             /* principal point, pixels from the top-left corner (y down) */
+    uint32_t width, height;   /* pixels; at most 65536 16x16 tiles */
+    float near_plane;         /* > 0 */
+    float far_plane;          /* > near_plane */
+    uint32_t sh_degree;       /* 0..3: (sh_degree+1)^2 coefficients per Gaussian */
+    uint32_t color_mode;      /* NPA_RASTER_COLOR_* */
+} npa_raster_camera;
+
+npa_status npa_raster_gaussians_3d(npa_context* ctx, const float* position_visibility,
+                                   const float* spherical_harmonic, const float* rotation,
+                                   const float* scale_opacity, uint32_t count,
+                                   const npa_raster_camera* camera, float* image);
+/* npa_state_decode_gaussians_3d of the current particles into library-held buffers, then
+ * npa_raster_gaussians_3d of them with camera->sh_degree = cfg->sh_degree (oriented mode) or 0:
+ * the frame the viewer draws from a device-resident state. */
+npa_status npa_state_raster_gaussians_3d(npa_state* state, const npa_gaussian_decode_cfg* cfg,
+                                         const npa_raster_camera* camera, float* image);
+
 /* ------------------------------------------------------- model files */
 /* A BpkModelManifest (crates/burn_automata/src/import.rs:20-31) read from a .bpk container or
  * its bare JSON payload: replaces load_manifest / load_manifest_bytes (import.rs:378-390) and
@@ -410,7 +455,8 @@ enum {
     NPA_KERNEL_SPLIT = 8,      /* per-bin split by true cell + sorted payload + work items + update-mask targets */
     NPA_KERNEL_ACTIVE = 9,     /* reserved: the split kernel (8) now selects the update-mask targets */
     NPA_KERNEL_RENDER = 10,    /* the whole projected 3D render pipeline (npa_render_views) */
-    NPA_KERNEL_COUNT = 11
+    NPA_KERNEL_RASTER = 11,    /* the whole oriented Gaussian raster (npa_raster_gaussians_3d) */
+    NPA_KERNEL_COUNT = 12
 };
 /* kernel_mask selects kernels by bit (1 << NPA_KERNEL_*; 0 = off, -1 = all). The
  * library then brackets each launch of a selected kernel with HIP events on the

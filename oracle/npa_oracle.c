@@ -1683,3 +1683,241 @@ int oracle_perceive_adjoint(const float* positions, const float* states, uint32_
     free(rga);
     return NPA_OK;
 }
+
+/* ------------------------------------------------------------------ oriented Gaussian raster
+ * The EWA raster of the planar Gaussian export, restated from the published 3D Gaussian
+ * splatting forward pass (Kerbl et al. 2023, with the EWA splat projection of Zwicker et al.
+ * 2001). The reference draws the export through bevy_gaussian_splatting 8.0.1 (Cargo.toml:23;
+ * crates/bevy_automata/src/viewer/cloud.rs:80-97), which is not vendored: no reference test pins
+ * these pixels (parity unpinned against the reference; pinned by closed forms in the tests).
+ * Straightforward loops: each tile filters the depth-sorted Gaussians whose tile rectangle holds
+ * it, and each of its pixels walks that list serially. */
+typedef struct raster_splat {
+    int live;
+    float depth;
+    float mx, my, ca, cb, cc, opacity, rgb[3];
+    int tx0, tx1, ty0, ty1;
+} raster_splat;
+
+/* Real spherical harmonics in the sign convention of the 3DGS code (Condon-Shortley phase),
+ * bands 0..3: 1/(2 sqrt(pi)), sqrt(3/(4 pi)), ... */
+static const float kShC0 = 0.28209479177387814f;
+static const float kShC1 = 0.4886025119029199f;
+static const float kShC2[5] = {1.0925484305920792f, -1.0925484305920792f, 0.31539156525252005f,
+                               -1.0925484305920792f, 0.5462742152960396f};
+static const float kShC3[7] = {-0.5900435899266435f, 2.890611442640554f, -0.4570457994644658f,
+                               0.3731763325901154f, -0.4570457994644658f, 1.445305721320277f,
+                               -0.5900435899266435f};
+
+static void raster_sh_color(const float* sh, uint32_t degree, const float dir[3], float out[3]) {
+    const float x = dir[0], y = dir[1], z = dir[2];
+    float basis[16];
+    basis[0] = kShC0;
+    if (degree > 0) {
+        basis[1] = -kShC1 * y;
+        basis[2] = kShC1 * z;
+        basis[3] = -kShC1 * x;
+    }
+    if (degree > 1) {
+        const float xx = x * x, yy = y * y, zz = z * z;
+        basis[4] = kShC2[0] * (x * y);
+        basis[5] = kShC2[1] * (y * z);
+        basis[6] = kShC2[2] * (2.0f * zz - xx - yy);
+        basis[7] = kShC2[3] * (x * z);
+        basis[8] = kShC2[4] * (xx - yy);
+        if (degree > 2) {
+            basis[9] = kShC3[0] * y * (3.0f * xx - yy);
+            basis[10] = kShC3[1] * (x * y) * z;
+            basis[11] = kShC3[2] * y * (4.0f * zz - xx - yy);
+            basis[12] = kShC3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);
+            basis[13] = kShC3[4] * x * (4.0f * zz - xx - yy);
+            basis[14] = kShC3[5] * z * (xx - yy);
+            basis[15] = kShC3[6] * x * (xx - 3.0f * yy);
+        }
+    }
+    const uint32_t K = (degree + 1) * (degree + 1);
+    for (int ch = 0; ch < 3; ++ch) {
+        float acc = 0.0f;
+        for (uint32_t k = 0; k < K; ++k) acc += basis[k] * sh[k * 3 + ch];
+        acc += 0.5f;
+        out[ch] = acc > 0.0f ? acc : 0.0f;
+    }
+}
+
+static float raster_clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+static void raster_prepare(const float* pv, const float* sh, const float* rot, const float* so,
+                           const npa_raster_camera* cam, const float campos[3], uint32_t tiles_x,
+                           uint32_t tiles_y, raster_splat* out) {
+    const float* V = cam->view;
+    out->live = 0;
+    if (!(pv[3] > 0.0f)) return;
+    const float vx = V[0] * pv[0] + V[1] * pv[1] + V[2] * pv[2] + V[3];
+    const float vy = V[4] * pv[0] + V[5] * pv[1] + V[6] * pv[2] + V[7];
+    const float vz = V[8] * pv[0] + V[9] * pv[1] + V[10] * pv[2] + V[11];
+    /* the 3DGS camera frame: x right, y down, z forward */
+    const float tx = vx, ty = -vy, tz = -vz;
+    if (!(tz > cam->near_plane) || !(tz <= cam->far_plane)) return;
+    float qw = rot[0], qx = rot[1], qy = rot[2], qz = rot[3];
+    const float qn = sqrtf(qw * qw + qx * qx + qy * qy + qz * qz);
+    if (qn > 0.0f && qn < INFINITY) {
+        qw /= qn; qx /= qn; qy /= qn; qz /= qn;
+    } else {
+        qw = 1.0f; qx = qy = qz = 0.0f;
+    }
+    const float R[3][3] = {
+        {1.0f - 2.0f * (qy * qy + qz * qz), 2.0f * (qx * qy - qw * qz), 2.0f * (qx * qz + qw * qy)},
+        {2.0f * (qx * qy + qw * qz), 1.0f - 2.0f * (qx * qx + qz * qz), 2.0f * (qy * qz - qw * qx)},
+        {2.0f * (qx * qz - qw * qy), 2.0f * (qy * qz + qw * qx), 1.0f - 2.0f * (qx * qx + qy * qy)}};
+    float M[3][3];
+    for (int r = 0; r < 3; ++r)
+        for (int c = 0; c < 3; ++c) M[r][c] = R[r][c] * so[c];
+    float S[3][3];
+    for (int r = 0; r < 3; ++r)
+        for (int c = 0; c < 3; ++c) S[r][c] = M[r][0] * M[c][0] + M[r][1] * M[c][1] + M[r][2] * M[c][2];
+    /* view rotation in the 3DGS frame */
+    const float W[3][3] = {{V[0], V[1], V[2]}, {-V[4], -V[5], -V[6]}, {-V[8], -V[9], -V[10]}};
+    const float limx = 1.3f * fmaxf(cam->cx, (float)cam->width - cam->cx) / cam->fx;
+    const float limy = 1.3f * fmaxf(cam->cy, (float)cam->height - cam->cy) / cam->fy;
+    const float jx = raster_clampf(tx / tz, -limx, limx) * tz;
+    const float jy = raster_clampf(ty / tz, -limy, limy) * tz;
+    const float J[2][3] = {{cam->fx / tz, 0.0f, -(cam->fx * jx) / (tz * tz)},
+                           {0.0f, cam->fy / tz, -(cam->fy * jy) / (tz * tz)}};
+    float T[2][3];
+    for (int r = 0; r < 2; ++r)
+        for (int c = 0; c < 3; ++c) T[r][c] = J[r][0] * W[0][c] + J[r][1] * W[1][c] + J[r][2] * W[2][c];
+    float U[2][3];
+    for (int r = 0; r < 2; ++r)
+        for (int c = 0; c < 3; ++c) U[r][c] = T[r][0] * S[0][c] + T[r][1] * S[1][c] + T[r][2] * S[2][c];
+    const float a = (U[0][0] * T[0][0] + U[0][1] * T[0][1] + U[0][2] * T[0][2]) + 0.3f;
+    const float b = U[0][0] * T[1][0] + U[0][1] * T[1][1] + U[0][2] * T[1][2];
+    const float c = (U[1][0] * T[1][0] + U[1][1] * T[1][1] + U[1][2] * T[1][2]) + 0.3f;
+    const float det = a * c - b * b;
+    if (!(det > 0.0f) || !(det < INFINITY)) return;
+    const float mid = 0.5f * (a + c);
+    const float lam = mid + sqrtf(fmaxf(0.1f, mid * mid - det));
+    const float radius = ceilf(3.0f * sqrtf(lam));
+    const float mx = cam->cx + cam->fx * tx / tz;
+    const float my = cam->cy + cam->fy * ty / tz;
+    if (!(fabsf(mx) < 1e30f) || !(fabsf(my) < 1e30f) || !(radius < 1e30f)) return;
+    const float fx0 = raster_clampf(floorf((mx - radius) / 16.0f), 0.0f, (float)tiles_x);
+    const float fx1 = raster_clampf(floorf((mx + radius) / 16.0f) + 1.0f, 0.0f, (float)tiles_x);
+    const float fy0 = raster_clampf(floorf((my - radius) / 16.0f), 0.0f, (float)tiles_y);
+    const float fy1 = raster_clampf(floorf((my + radius) / 16.0f) + 1.0f, 0.0f, (float)tiles_y);
+    out->tx0 = (int)fx0; out->tx1 = (int)fx1; out->ty0 = (int)fy0; out->ty1 = (int)fy1;
+    if (out->tx0 >= out->tx1 || out->ty0 >= out->ty1) return;
+    out->ca = c / det;
+    out->cb = -b / det;
+    out->cc = a / det;
+    out->mx = mx;
+    out->my = my;
+    out->depth = tz;
+    out->opacity = so[3];
+    if (cam->color_mode == NPA_RASTER_COLOR_RGB) {
+        for (int ch = 0; ch < 3; ++ch) out->rgb[ch] = sh[ch];
+    } else {
+        float d[3] = {pv[0] - campos[0], pv[1] - campos[1], pv[2] - campos[2]};
+        const float dn = sqrtf(d[0] * d[0] + d[1] * d[1] + d[2] * d[2]);
+        for (int k = 0; k < 3; ++k) d[k] = dn > 0.0f ? d[k] / dn : 0.0f;
+        raster_sh_color(sh, cam->sh_degree, d, out->rgb);
+    }
+    out->live = 1;
+}
+
+static const raster_splat* g_raster_sort_base;
+static int raster_depth_order(const void* pa, const void* pb) {
+    const uint32_t ia = *(const uint32_t*)pa, ib = *(const uint32_t*)pb;
+    const float da = g_raster_sort_base[ia].depth, db = g_raster_sort_base[ib].depth;
+    if (da < db) return -1;
+    if (da > db) return 1;
+    return ia < ib ? -1 : (ia > ib ? 1 : 0);
+}
+
+int oracle_raster_camera_center(const npa_raster_camera* cam, float out[3]) {
+    /* view = [R | t] -> centre = -R^T t */
+    const float* V = cam->view;
+    for (int k = 0; k < 3; ++k) out[k] = -(V[k] * V[3] + V[4 + k] * V[7] + V[8 + k] * V[11]);
+    return 0;
+}
+
+int oracle_raster_gaussians_3d(const float* position_visibility, const float* spherical_harmonic,
+                               const float* rotation, const float* scale_opacity, uint32_t count,
+                               const npa_raster_camera* cam, float* image, uint64_t* evaluated) {
+    if (!cam || cam->width == 0 || cam->height == 0 || cam->sh_degree > 3 ||
+        cam->color_mode > NPA_RASTER_COLOR_RGB || !(cam->near_plane > 0.0f) ||
+        !(cam->far_plane > cam->near_plane))
+        return NPA_ERR_INVALID_ARGUMENT;
+    const uint32_t K = (cam->sh_degree + 1) * (cam->sh_degree + 1);
+    const uint32_t tiles_x = (cam->width + 15) / 16, tiles_y = (cam->height + 15) / 16;
+    float campos[3];
+    oracle_raster_camera_center(cam, campos);
+    raster_splat* sp = (raster_splat*)calloc(count ? count : 1, sizeof(raster_splat));
+    uint32_t* order = (uint32_t*)malloc((count ? count : 1) * sizeof(uint32_t));
+    if (!sp || !order) {
+        free(sp);
+        free(order);
+        return NPA_ERR_OUT_OF_MEMORY;
+    }
+    uint32_t live = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        raster_prepare(position_visibility + 4ull * i, spherical_harmonic + (uint64_t)i * K * 3,
+                       rotation + 4ull * i, scale_opacity + 4ull * i, cam, campos, tiles_x, tiles_y, &sp[i]);
+        if (sp[i].live) order[live++] = i;
+    }
+    g_raster_sort_base = sp;
+    qsort(order, live, sizeof(uint32_t), raster_depth_order);
+    int oom = 0;
+    uint64_t pairs = 0;
+#pragma omp parallel reduction(+ : pairs)
+    {
+        uint32_t* list = (uint32_t*)malloc((live ? live : 1) * sizeof(uint32_t));
+        if (!list) {
+#pragma omp atomic write
+            oom = 1;
+        }
+#pragma omp for schedule(dynamic, 1)
+        for (uint32_t t = 0; t < tiles_x * tiles_y; ++t) {
+            if (!list) continue;
+            const int tx = (int)(t % tiles_x), ty = (int)(t / tiles_x);
+            /* the tile's Gaussians, front to back */
+            uint32_t n = 0;
+            for (uint32_t k = 0; k < live; ++k) {
+                const raster_splat* g = &sp[order[k]];
+                if (tx >= g->tx0 && tx < g->tx1 && ty >= g->ty0 && ty < g->ty1) list[n++] = order[k];
+            }
+            for (uint32_t py = (uint32_t)ty * 16; py < (uint32_t)ty * 16 + 16 && py < cam->height; ++py)
+                for (uint32_t px = (uint32_t)tx * 16; px < (uint32_t)tx * 16 + 16 && px < cam->width; ++px) {
+                    float T = 1.0f, rgb[3] = {0.0f, 0.0f, 0.0f};
+                    const float pxc = (float)px + 0.5f, pyc = (float)py + 0.5f;
+                    for (uint32_t k = 0; k < n; ++k) {
+                        const raster_splat* g = &sp[list[k]];
+                        ++pairs;
+                        const float dx = g->mx - pxc, dy = g->my - pyc;
+                        const float power = -0.5f * (g->ca * dx * dx + g->cc * dy * dy) - g->cb * dx * dy;
+                        if (power > 0.0f) continue;
+                        const float alpha = fminf(0.99f, g->opacity * expf(power));
+                        if (alpha < 1.0f / 255.0f) continue;
+                        const float next = T * (1.0f - alpha);
+                        if (next < 0.0001f) break;
+                        for (int ch = 0; ch < 3; ++ch) rgb[ch] += g->rgb[ch] * alpha * T;
+                        T = next;
+                    }
+                    float* o = image + 4 * ((uint64_t)py * cam->width + px);
+                    o[0] = rgb[0];
+                    o[1] = rgb[1];
+                    o[2] = rgb[2];
+                    o[3] = 1.0f - T;
+                }
+        }
+        free(list);
+    }
+    if (evaluated) *evaluated = pairs;
+    if (oom) {
+        free(sp);
+        free(order);
+        return NPA_ERR_OUT_OF_MEMORY;
+    }
+    free(sp);
+    free(order);
+    return NPA_OK;
+}

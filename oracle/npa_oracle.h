@@ -31,6 +31,12 @@
  *                               centroid = projected pixel, second moment = sigma^2,
  *                               depth_sum / alpha = depth), sigmoid against scipy's expit,
  *                               reference test constants (RENDER_MIN/MAX_OPACITY, defaults)
+ *   raster_gaussians_3d       - parity unpinned against the reference (its raster lives in the
+ *                               un-vendored bevy_gaussian_splatting); pinned by closed forms: a
+ *                               centred isotropic Gaussian's alpha profile, rotation invariance of
+ *                               isotropic Gaussians, axis swaps of anisotropic ones, the analytic
+ *                               conic of a rotated ellipse, two-layer compositing order, the
+ *                               transmittance cut, SH bases against scipy's spherical harmonics
  *   perceive_adjoint          - the reference's finite-difference tests (lib.rs:123-356) with their
  *                               fixtures and tolerances; central differences of the oracle's
  *                               forward at every state and position coordinate of small systems;
@@ -145,6 +151,14 @@ int oracle_perceive_adjoint(const float* positions, const float* states, uint32_
                             uint32_t particle_count, uint32_t state_dims, const npa_grid_cfg* cfg,
                             const npa_perception_opts* opts, const float* feature_adjoint,
                             float* state_adjoint, float* position_adjoint);
+
+/* EWA raster of oriented 3D Gaussians (npa_raster_gaussians_3d's definition; the reference's
+ * bevy_gaussian_splatting raster is not vendored): image[height][width][4]; *evaluated (may be
+ * NULL) receives the number of (pixel, Gaussian) evaluations before each pixel's stop. */
+int oracle_raster_camera_center(const npa_raster_camera* cam, float out[3]);
+int oracle_raster_gaussians_3d(const float* position_visibility, const float* spherical_harmonic,
+                               const float* rotation, const float* scale_opacity, uint32_t count,
+                               const npa_raster_camera* cam, float* image, uint64_t* evaluated);
 
 /* Per-phase wall-clock seconds of the last oracle_step / oracle_rollout call
  * (hashgrid+perceive, MLP+gates+integrate, 0), following profile_rollout

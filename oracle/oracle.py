@@ -97,6 +97,9 @@ def _declare(L):
     L.oracle_project_positions.argtypes = [u32, P, u32, f32, P]
     L.oracle_splat_projected.argtypes = [P, P, P, P, u32, C.POINTER(_abi.NpaRenderCfg), P]
     L.oracle_render_attributes.argtypes = [P, u32, u32, C.POINTER(_abi.NpaRenderCfg), P, P, P, P]
+    L.oracle_raster_gaussians_3d.argtypes = [P, P, P, P, u32, C.POINTER(_abi.NpaRasterCamera), P,
+                                             C.POINTER(C.c_uint64)]
+    L.oracle_raster_camera_center.argtypes = [C.POINTER(_abi.NpaRasterCamera), P]
     L.oracle_last_phase_seconds.argtypes = [C.POINTER(C.c_double)] * 3
     L.oracle_max_threads.restype = C.c_int
     L.oracle_set_threads.argtypes = [C.c_int]
@@ -478,3 +481,28 @@ def tail_colors(states, state_dims: int) -> np.ndarray:
     s = np.asarray(states, np.float32).reshape(-1, state_dims)
     base = max(state_dims - 3, 0)
     return np.clip(s[:, base:base + 3] + np.float32(0.5), 0.0, 1.0).astype(np.float32)
+
+
+def raster_gaussians_3d(position_visibility, spherical_harmonic, rotation, scale_opacity, camera,
+                        return_evaluated: bool = False):
+    """The EWA raster of oriented Gaussians (npa_raster_gaussians_3d's definition; the published 3D
+    Gaussian splatting forward pass): image [height, width, 4] of premultiplied r, g, b, 1 - T
+    (and the number of (pixel, Gaussian) evaluations when return_evaluated)."""
+    pv = _f32(position_visibility).reshape(-1, 4)
+    n = pv.shape[0]
+    sh = _f32(spherical_harmonic).reshape(-1)
+    rot = _f32(rotation).reshape(-1, 4)
+    so = _f32(scale_opacity).reshape(-1, 4)
+    K = (camera.sh_degree + 1) ** 2
+    assert sh.size == n * K * 3 and rot.shape[0] == n and so.shape[0] == n
+    img = np.zeros((camera.height, camera.width, 4), np.float32)
+    ev = C.c_uint64(0)
+    _check(lib().oracle_raster_gaussians_3d(_ptr(pv), _ptr(sh), _ptr(rot), _ptr(so), n,
+                                            C.byref(camera.to_c()), _ptr(img), C.byref(ev)))
+    return (img, int(ev.value)) if return_evaluated else img
+
+
+def raster_camera_center(camera) -> np.ndarray:
+    out = np.zeros(3, np.float32)
+    lib().oracle_raster_camera_center(C.byref(camera.to_c()), _ptr(out))
+    return out

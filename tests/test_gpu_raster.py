@@ -1,0 +1,146 @@
+"""The oriented Gaussian raster on the HIP path (npa_raster_gaussians_3d) against the CPU oracle.
+
+The reference draws the planar Gaussian export through bevy_gaussian_splatting 8.0.1 (Cargo.toml:23;
+crates/bevy_automata/src/viewer/cloud.rs:80-97), which is not vendored and whose pixels no
+reference test pins (its headless test only asks for lit pixels,
+crates/bevy_automata/tests/gaussian_gpu_link/headless.rs:4-58). Both sides restate the published 3D
+Gaussian splatting forward pass; the oracle's restatement is pinned by closed forms in
+tests/test_oracle.py. Bar: PSNR >= 90 dB against the oracle's image, at most 1 in 10^4 values off
+by more than 1e-4 (the device's expf may differ from the host's by an ulp, which can move a pixel
+across the 1/255 alpha floor or the 1e-4 transmittance cut).
+"""
+import math
+
+import numpy as np
+import pytest
+
+from burn_automata_amd import _abi
+from burn_automata_amd import kernels as K
+from burn_automata_amd import synthetic as syn
+from burn_automata_amd.config import GaussianDecodeConfig, GaussianDecodeMode, RasterCamera, RasterColor
+from burn_automata_amd.executor import HipAutomataExecutor
+from burn_automata_amd.model import NpaModel
+from oracle import oracle as O
+from tests.helpers import psnr, rel_err, to_np
+
+pytestmark = pytest.mark.gpu
+
+f32 = np.float32
+
+
+def _check(got, want, what):
+    g = to_np(got).astype(np.float64)
+    w = np.asarray(want, np.float64)
+    assert g.shape == w.shape, (g.shape, w.shape)
+    d = np.abs(g - w)
+    off = float((d > 1e-4).mean())
+    p = psnr(g, w) if w.any() else (math.inf if not g.any() else 0.0)
+    print(f"{what}: max diff {d.max():.3e}, rel err {rel_err(g, w):.2e}, values off by >1e-4 {off:.2e}, "
+          f"psnr {p:.1f} dB, lit {float((w[..., 3] > 0).mean()):.2f}")
+    assert p >= 90.0 and off <= 1e-4, what
+
+
+def _cloud(n, degree, rng, spread=1.0, hidden=0.0):
+    Kc = (degree + 1) ** 2
+    pv = np.ones((n, 4), f32)
+    pv[:, :3] = rng.uniform(-spread, spread, (n, 3))
+    if hidden:
+        pv[:, 3] = (rng.uniform(size=n) >= hidden).astype(f32)
+    sh = rng.normal(0.0, 0.4, (n, Kc, 3)).astype(f32)
+    rot = rng.normal(size=(n, 4)).astype(f32)
+    so = np.empty((n, 4), f32)
+    so[:, :3] = np.exp(rng.uniform(math.log(0.004), math.log(0.08), (n, 3)))
+    so[:, 3] = rng.uniform(0.05, 1.0, n)
+    return pv, sh, rot, so
+
+
+CASES = {
+    # name: (gaussians, width, height, sh degree, colour mode, eye, spread, hidden fraction)
+    "one": (1, 64, 48, 0, RasterColor.Rgb, (0.0, 0.0, 3.0), 0.05, 0.0),
+    "sh1_small": (500, 100, 75, 1, RasterColor.SphericalHarmonics, (0.5, 0.8, 3.0), 1.0, 0.1),
+    "sh3_ragged": (5000, 257, 131, 3, RasterColor.SphericalHarmonics, (2.0, -1.0, 2.5), 1.0, 0.0),
+    "rgb_1024": (40000, 1024, 1024, 0, RasterColor.Rgb, (0.0, 0.0, 3.5), 1.0, 0.05),
+    "inside_the_cloud": (3000, 512, 384, 2, RasterColor.SphericalHarmonics, (0.1, 0.2, 0.6), 1.0, 0.0),
+}
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_raster_matches_the_oracle(ctx, name):
+    """Random clouds: oriented anisotropic Gaussians, spherical harmonics of degree 0..3 or RGB,
+    hidden ones, ragged edge tiles, and a camera inside the cloud (Gaussians behind it, beside it
+    and covering most of the screen)."""
+    n, W, H, deg, mode, eye, spread, hidden = CASES[name]
+    rng = np.random.default_rng(len(name))
+    pv, sh, rot, so = _cloud(n, deg, rng, spread, hidden)
+    cam = RasterCamera.look_at(eye, width=W, height=H, sh_degree=deg, color_mode=mode)
+    want = O.raster_gaussians_3d(pv, sh, rot, so, cam)
+    got = K.raster_gaussians_3d(pv, sh, rot, so, cam, ctx=ctx)
+    _check(got, want, f"raster {name} n={n} {W}x{H} deg={deg}")
+    again = K.raster_gaussians_3d(pv, sh, rot, so, cam, ctx=ctx)
+    np.testing.assert_array_equal(to_np(again), to_np(got))  # deterministic
+
+
+def test_raster_equal_depth_ties(ctx):
+    """Overlapping Gaussians on one plane facing the camera share a depth: the lower index is in
+    front on both sides."""
+    rng = np.random.default_rng(7)
+    n = 400
+    pv, sh, rot, so = _cloud(n, 0, rng)
+    pv[:, 2] = 0.0
+    pv[:, :2] = rng.uniform(-0.2, 0.2, (n, 2))
+    so[:, 3] = 0.6
+    cam = RasterCamera.look_at((0.0, 0.0, 2.0), width=128, height=128, color_mode=RasterColor.Rgb)
+    want = O.raster_gaussians_3d(pv, sh, rot, so, cam)
+    got = K.raster_gaussians_3d(pv, sh, rot, so, cam, ctx=ctx)
+    _check(got, want, "equal depths")
+
+
+def test_raster_empty_and_culled(ctx):
+    cam = RasterCamera.look_at((0.0, 0.0, 3.0), width=40, height=24, far_plane=10.0)
+    z = np.zeros((0, 4), f32)
+    img = K.raster_gaussians_3d(z, np.zeros(0, f32), z, z, cam, ctx=ctx)
+    assert img.shape == (24, 40, 4) and not to_np(img).any()
+    pv = np.array([[0, 0, 0, 0.0], [0, 0, 4, 1.0], [0, 0, -8, 1.0]], f32)  # hidden, behind, beyond far
+    so = np.full((3, 4), 0.5, f32)
+    rot = np.tile(np.array([1, 0, 0, 0], f32), (3, 1))
+    img = K.raster_gaussians_3d(pv, np.ones((3, 3), f32), rot, so, cam, ctx=ctx)
+    assert not to_np(img).any()
+
+
+@pytest.mark.parametrize("mode", [GaussianDecodeMode.GaussianSh0FixedScale, GaussianDecodeMode.GaussianSh0Oriented])
+def test_state_raster_after_a_c4_rollout(ctx, mode):
+    """C4's 16,384 surface particles after 8 steps: the frame of the device-resident state (decode
+    then raster in one call) equals the oracle's raster of the device decode."""
+    w = syn.workload("c4")
+    ex = HipAutomataExecutor(ctx=ctx)
+    state = ex.create_state(NpaModel(w["model"], w["weights"]), w["positions"], w["states"], 1, w["n"],
+                            w["grid"], w["dt"], w["update_prob"], w["seed"])
+    ex.step_state_many(state, 8)
+    dcfg = GaussianDecodeConfig(mode=mode)
+    dec = {k: to_np(v) for k, v in ex.decode_gaussians_3d(state, dcfg).items()}
+    p = dec["position_visibility"][:, :3]
+    centre = p.mean(axis=0)
+    ext = float(np.abs(p - centre).max())
+    eye = tuple(centre + np.array([0.6, 0.9, 2.4]) * ext)
+    color = RasterColor.Rgb if mode == GaussianDecodeMode.GaussianSh0FixedScale else RasterColor.SphericalHarmonics
+    cam = RasterCamera.look_at(eye, tuple(centre), width=320, height=240, color_mode=color)
+    got = ex.raster_gaussians_3d(state, dcfg, cam)
+    want = O.raster_gaussians_3d(dec["position_visibility"], dec["spherical_harmonic"], dec["rotation"],
+                                 dec["scale_opacity"], cam)
+    _check(got, want, f"c4 state raster ({mode.name})")
+    assert float((want[..., 3] > 0.01).mean()) > 0.05  # the surface is in view
+    state.close()
+
+
+def test_raster_errors(ctx):
+    pv, sh, rot, so = _cloud(4, 0, np.random.default_rng(1))
+    cam = RasterCamera.look_at((0.0, 0.0, 3.0), width=32, height=32)
+    for bad, msg in ((cam.replace(width=0), "non-zero"), (cam.replace(sh_degree=4), "sh_degree"),
+                     (cam.replace(near_plane=0.0), "near_plane"), (cam.replace(far_plane=0.05), "far_plane"),
+                     (cam.replace(width=16384, height=16384), "65536"), (cam.replace(fx=-1.0), "focal"),
+                     (cam.replace(width=20000), "16384")):
+        shb = np.zeros(4 * (bad.sh_degree + 1) ** 2 * 3, f32)  # sized for the camera's degree
+        with pytest.raises(_abi.InvalidArgument, match=msg):
+            K.raster_gaussians_3d(pv, shb, rot, so, bad, ctx=ctx)
+    with pytest.raises(AssertionError, match="differ in length"):
+        K.raster_gaussians_3d(pv, sh[:3], rot, so, cam, ctx=ctx)

@@ -1159,3 +1159,197 @@ def test_adjoint_is_linear_and_carries_identity_rows():
     r = O.perceive_adjoint_with_options(pos, st, 1, n, S, cfg, opts, only)
     np.testing.assert_array_equal(r.position[:, :dim], only[:, F - dim:])
     assert not r.state.any()
+
+
+# ---------------------------------------------------------------- oriented Gaussian raster
+# The reference's viewer draws the planar export through the un-vendored bevy_gaussian_splatting
+# 8.0.1; no reference test pins its pixels. The oracle's restatement of the published 3D Gaussian
+# splatting forward pass is pinned here by closed forms computed independently in float64.
+from burn_automata_amd.config import RasterCamera, RasterColor  # noqa: E402
+
+
+def _raster_one(cam, pos, scale, quat=(1.0, 0.0, 0.0, 0.0), opacity=0.8, sh=(0.3, 0.1, -0.2)):
+    pv = np.array([[*pos, 1.0]], f32)
+    so = np.array([[*scale, opacity]], f32)
+    return O.raster_gaussians_3d(pv, np.array(sh, f32), np.array([quat], f32), so, cam)
+
+
+def _expected_alpha(cam, a, b, c, mx, my, opacity):
+    """alpha over the image of one Gaussian with 2D covariance [[a, b], [b, c]] (0.3 included)
+    centred at (mx, my): min(0.99, o e^power), zero below 1/255 or outside its 3-sigma tiles."""
+    det = a * c - b * b
+    ca, cb, cc = c / det, -b / det, a / det
+    ys, xs = np.mgrid[0:cam.height, 0:cam.width].astype(np.float64)
+    dx, dy = mx - (xs + 0.5), my - (ys + 0.5)
+    power = -0.5 * (ca * dx * dx + cc * dy * dy) - cb * dx * dy
+    alpha = np.minimum(0.99, opacity * np.exp(power))
+    alpha[(power > 0) | (alpha < 1 / 255)] = 0.0
+    mid = 0.5 * (a + c)
+    r = math.ceil(3 * math.sqrt(mid + math.sqrt(max(0.1, mid * mid - det))))
+    tx, ty = xs // 16, ys // 16
+    inside = ((tx >= max(0, math.floor((mx - r) / 16))) & (tx < math.floor((mx + r) / 16) + 1) &
+              (ty >= max(0, math.floor((my - r) / 16))) & (ty < math.floor((my + r) / 16) + 1))
+    return np.where(inside, alpha, 0.0)
+
+
+@pytest.mark.parametrize("opacity", [0.8, 1.0])
+def test_raster_centred_isotropic_closed_form(opacity):
+    """A sphere of radius s on the optical axis at distance z: Sigma2d = (f s / z)^2 I + 0.3 I, so
+    every pixel is colour * alpha(d^2) with the centre clamped at 0.99 when the opacity is 1."""
+    cam = RasterCamera.look_at((0, 0, 3), width=64, height=48, color_mode=RasterColor.Rgb)
+    s = 0.1 if opacity < 1 else 0.3  # wide enough that the centre pixels reach the 0.99 clamp
+    img = _raster_one(cam, (0, 0, 0), (s, s, s), opacity=opacity, sh=(0.9, 0.5, 0.25))
+    var = (cam.fx * s / 3.0) ** 2 + 0.3
+    alpha = _expected_alpha(cam, var, 0.0, var, cam.cx, cam.cy, opacity)
+    np.testing.assert_allclose(img[..., 3], alpha, atol=2e-6)
+    for ch, col in enumerate((0.9, 0.5, 0.25)):
+        np.testing.assert_allclose(img[..., ch], col * alpha, atol=2e-6)
+    if opacity == 1.0:
+        assert img[..., 3].max() == np.float32(0.99) and (img[..., 3] == np.float32(0.99)).sum() >= 4
+
+
+def test_raster_off_axis_centre_and_y_flip():
+    """The alpha centroid of a small Gaussian sits at (cx + f x / z, cy - f y / z): world +y is up,
+    image rows grow downwards."""
+    cam = RasterCamera.look_at((0, 0, 3), width=96, height=96, color_mode=RasterColor.Rgb)
+    img = _raster_one(cam, (0.3, 0.2, 0.0), (0.03, 0.03, 0.03))
+    a = img[..., 3].astype(np.float64)
+    ys, xs = np.mgrid[0:96, 0:96] + 0.5
+    cxm, cym = (a * xs).sum() / a.sum(), (a * ys).sum() / a.sum()
+    assert abs(cxm - (cam.cx + cam.fx * 0.3 / 3)) < 0.05
+    assert abs(cym - (cam.cy - cam.fy * 0.2 / 3)) < 0.05
+
+
+def _quat(axis, angle):
+    axis = np.asarray(axis, np.float64) / np.linalg.norm(axis)
+    return (math.cos(angle / 2), *(math.sin(angle / 2) * axis))
+
+
+def test_raster_isotropic_rotation_invariance():
+    cam = RasterCamera.look_at((0.4, 0.7, 2.5), width=80, height=64, color_mode=RasterColor.Rgb)
+    ref = _raster_one(cam, (0.1, -0.05, 0.2), (0.08, 0.08, 0.08))
+    rng = np.random.default_rng(3)
+    for _ in range(4):
+        q = rng.normal(size=4)
+        got = _raster_one(cam, (0.1, -0.05, 0.2), (0.08, 0.08, 0.08), quat=tuple(q))
+        np.testing.assert_allclose(got, ref, atol=2e-6)
+    assert ref[..., 3].max() > 0.5
+
+
+@pytest.mark.parametrize("theta", [0.0, 0.4, math.pi / 2, 2.2])
+def test_raster_rotated_ellipse_conic(theta):
+    """A flat ellipse (sx, sy, sz) on the optical axis turned by theta about the view axis: its 2D
+    covariance is (f/z)^2 Rot(-theta) diag(sx^2, sy^2) Rot(-theta)^T + 0.3 I (image y points down, so
+    the on-screen turn is -theta)."""
+    cam = RasterCamera.look_at((0, 0, 3), width=96, height=80, color_mode=RasterColor.Rgb)
+    sx, sy = 0.15, 0.04
+    img = _raster_one(cam, (0, 0, 0), (sx, sy, 0.01), quat=_quat((0, 0, 1), theta), opacity=0.7)
+    k = cam.fx / 3.0
+    c, s = math.cos(-theta), math.sin(-theta)
+    Rt = np.array([[c, -s], [s, c]])
+    cov = k * k * Rt @ np.diag([sx * sx, sy * sy]) @ Rt.T
+    alpha = _expected_alpha(cam, cov[0, 0] + 0.3, cov[0, 1], cov[1, 1] + 0.3, cam.cx, cam.cy, 0.7)
+    np.testing.assert_allclose(img[..., 3], alpha, atol=3e-6)
+
+
+def test_raster_axis_swap():
+    """Scales (a, b, c) turned 90 degrees about the view axis draw the image of scales (b, a, c)."""
+    cam = RasterCamera.look_at((0, 0, 3), width=64, height=64, color_mode=RasterColor.Rgb)
+    turned = _raster_one(cam, (0, 0, 0), (0.12, 0.05, 0.02), quat=_quat((0, 0, 1), math.pi / 2))
+    swapped = _raster_one(cam, (0, 0, 0), (0.05, 0.12, 0.02))
+    np.testing.assert_allclose(turned, swapped, atol=2e-6)
+
+
+def test_raster_front_to_back_compositing():
+    """Two layers: rgb = c1 a1 + c2 a2 (1 - a1), alpha = 1 - (1 - a1)(1 - a2), the nearer first
+    whatever the input order; at equal depth the lower index is in front."""
+    cam = RasterCamera.look_at((0, 0, 3), width=48, height=48, color_mode=RasterColor.Rgb)
+    near = ((0.0, 0.0, 0.5), (0.1, 0.1, 0.1), 0.6, (1.0, 0.0, 0.0))
+    far = ((0.05, 0.0, -0.5), (0.12, 0.12, 0.12), 0.5, (0.0, 1.0, 0.0))
+
+    def run(gs):
+        pv = np.array([[*g[0], 1.0] for g in gs], f32)
+        so = np.array([[*g[1], g[2]] for g in gs], f32)
+        sh = np.array([g[3] for g in gs], f32)
+        rot = np.tile(np.array([1, 0, 0, 0], f32), (len(gs), 1))
+        return O.raster_gaussians_3d(pv, sh, rot, so, cam).astype(np.float64)
+
+    a, b = run([near]), run([far])
+    both = run([far, near])
+    np.testing.assert_allclose(both, run([near, far]), atol=0)
+    a1, a2 = a[..., 3], b[..., 3]
+    np.testing.assert_allclose(both[..., 0], a[..., 0] + b[..., 0] * (1 - a1), atol=2e-6)
+    np.testing.assert_allclose(both[..., 1], a[..., 1] + b[..., 1] * (1 - a1), atol=2e-6)
+    np.testing.assert_allclose(both[..., 3], 1 - (1 - a1) * (1 - a2), atol=2e-6)
+    tie = [((0, 0, 0), (0.1, 0.1, 0.1), 0.6, (1.0, 0.0, 0.0)), ((0, 0, 0), (0.1, 0.1, 0.1), 0.6, (0.0, 0.0, 1.0))]
+    t = run(tie)
+    assert t[24, 24, 0] > t[24, 24, 2] > 0  # index 0 (red) in front
+
+
+def test_raster_transmittance_cut():
+    """Layers of alpha 0.95: T runs 0.05, 0.0025, 1.25e-4; the fourth would take it below 1e-4,
+    so the pixel stops after three."""
+    cam = RasterCamera.look_at((0, 0, 3), width=32, height=32, color_mode=RasterColor.Rgb)
+    n = 6
+    pv = np.array([[0, 0, 0.1 * k, 1.0] for k in range(n)], f32)
+    so = np.array([[0.5, 0.5, 0.5, 0.95]] * n, f32)  # wide: alpha ~ 0.95 across the centre pixels
+    sh = np.array([[1.0, 1.0, 1.0]] * n, f32)
+    rot = np.tile(np.array([1, 0, 0, 0], f32), (n, 1))
+    img = O.raster_gaussians_3d(pv, sh, rot, so, cam)
+    # each layer alone, nearest first (layer k sits at depth 3 - 0.1 k)
+    a = [np.float64(O.raster_gaussians_3d(pv[k:k + 1], sh[:1], rot[:1], so[:1], cam)[16, 16, 3])
+         for k in range(n - 1, -1, -1)]
+    assert all(0.9 < x <= 0.95 for x in a)
+    t3 = (1 - a[0]) * (1 - a[1]) * (1 - a[2])
+    assert t3 >= 1e-4 > t3 * (1 - a[3])  # three layers pass the cut, the fourth would not
+    assert abs(img[16, 16, 3] - (1 - t3)) < 1e-6
+    assert abs(img[16, 16, 0] - (1 - t3)) < 1e-6
+
+
+def _sh_basis_scipy(lmax, d):
+    """Real spherical harmonics with the Condon-Shortley phase, index l^2 + l + m:
+    m < 0: sqrt2 Im Y_l^|m|, m = 0: Y_l^0, m > 0: sqrt2 Re Y_l^m (scipy's complex Y_l^m)."""
+    from scipy.special import sph_harm_y
+
+    x, y, z = d
+    polar, azim = math.acos(max(-1.0, min(1.0, z))), math.atan2(y, x)
+    out = []
+    for l in range(lmax + 1):
+        for m in range(-l, l + 1):
+            Y = complex(sph_harm_y(l, abs(m), polar, azim))
+            out.append(math.sqrt(2) * Y.imag if m < 0 else (Y.real if m == 0 else math.sqrt(2) * Y.real))
+    return np.array(out)
+
+
+@pytest.mark.parametrize("degree", [0, 1, 2, 3])
+def test_raster_sh_basis_against_scipy(degree):
+    """Colour = max(0, sum_k basis_k(view direction) coef_k + 0.5), read back as rgb / alpha at the
+    Gaussian's centre pixel, for each basis function alone."""
+    K = (degree + 1) ** 2
+    eye = (0.6, -0.4, 2.2)
+    cam = RasterCamera.look_at(eye, width=32, height=32, sh_degree=degree)
+    rng = np.random.default_rng(degree)
+    p = rng.uniform(-0.05, 0.05, 3)
+    centre = np.array(eye)
+    d = (p.astype(f32).astype(np.float64) - centre)
+    d /= np.linalg.norm(d)
+    basis = _sh_basis_scipy(degree, d)
+    for k in range(K):
+        coef = np.zeros((K, 3), f32)
+        coef[k] = (0.8, -0.8, 0.3)
+        img = _raster_one(cam, tuple(p), (0.3, 0.3, 0.3), opacity=0.5, sh=coef.ravel())
+        px = img[16, 16].astype(np.float64)
+        want = np.maximum(basis[k] * np.array([0.8, -0.8, 0.3]) + 0.5, 0.0)
+        np.testing.assert_allclose(px[:3] / px[3], want, atol=2e-5, err_msg=f"coefficient {k}")
+
+
+def test_raster_culling():
+    """Hidden (visibility 0), behind the camera, beyond the far plane: nothing is drawn."""
+    cam = RasterCamera.look_at((0, 0, 3), width=32, height=32, far_plane=10.0, color_mode=RasterColor.Rgb)
+    for pos, vis in (((0, 0, 0), 0.0), ((0, 0, 4), 1.0), ((0, 0, -8), 1.0)):
+        pv = np.array([[*pos, vis]], f32)
+        img = O.raster_gaussians_3d(pv, np.ones(3, f32), np.array([[1, 0, 0, 0]], f32),
+                                    np.array([[0.2, 0.2, 0.2, 0.9]], f32), cam)
+        assert not img.any()
+    assert O.raster_gaussians_3d(np.zeros((0, 4), f32), np.zeros(0, f32), np.zeros((0, 4), f32),
+                                 np.zeros((0, 4), f32), cam).sum() == 0

@@ -77,6 +77,25 @@ MUTANTS = {
     "render_learned_channel": ("float logit = clamp_f32(s[S - 5]", "float logit = clamp_f32(s[S - 4]"),
     "decode_learned_channel": ("float scale_logit = clamp_f32(s[S - 5]", "float scale_logit = clamp_f32(s[S - 6]"),
     "decode_opacity_channel": ("float opacity_logit = clamp_f32(s[S - 4]", "float opacity_logit = clamp_f32(s[S - 5]"),
+    "raster_lowpass_dropped": ('U[0][2] * T[0][2]) + 0.3f;', 'U[0][2] * T[0][2]);'),
+    "raster_y_not_flipped": ('const float tx = vx, ty = -vy, tz = -vz;', 'const float tx = vx, ty = vy, tz = -vz;'),
+    "raster_conic_cross_sign": ('out->cb = -b / det;', 'out->cb = b / det;'),
+    "raster_power_cross_sign": ('g->cc * dy * dy) - g->cb * dx * dy;', 'g->cc * dy * dy) + g->cb * dx * dy;'),
+    "raster_alpha_clamp": ('fminf(0.99f, g->opacity * expf(power))', 'fminf(1.0f, g->opacity * expf(power))'),
+    "raster_alpha_floor": ('if (alpha < 1.0f / 255.0f) continue;', 'if (alpha < 1.0f / 64.0f) continue;'),
+    "raster_no_cut": ('if (next < 0.0001f) break;', 'if (next < 0.0f) break;'),
+    "raster_pixel_centre": ('const float pxc = (float)px + 0.5f,', 'const float pxc = (float)px,'),
+    "raster_back_to_front": ('if (da < db) return -1;\n    if (da > db) return 1;', 'if (da < db) return 1;\n    if (da > db) return -1;'),
+    "raster_tie_order": ('return ia < ib ? -1 : (ia > ib ? 1 : 0);', 'return ia > ib ? -1 : (ia < ib ? 1 : 0);'),
+    "raster_quat_transposed": ('2.0f * (qx * qy - qw * qz), 2.0f * (qx * qz + qw * qy)}', '2.0f * (qx * qy + qw * qz), 2.0f * (qx * qz - qw * qy)}'),
+    "raster_scale_row": ('M[r][c] = R[r][c] * so[c];', 'M[r][c] = R[r][c] * so[r];'),
+    "raster_radius": ('const float radius = ceilf(3.0f * sqrtf(lam));', 'const float radius = ceilf(2.0f * sqrtf(lam));'),
+    "raster_sh1_sign": ('basis[1] = -kShC1 * y;', 'basis[1] = kShC1 * y;'),
+    "raster_sh2_term": ('basis[6] = kShC2[2] * (2.0f * zz - xx - yy);', 'basis[6] = kShC2[2] * (2.0f * zz - xx + yy);'),
+    "raster_sh3_term": ('kShC3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);', 'kShC3[3] * z * (2.0f * zz - 3.0f * xx - 2.0f * yy);'),
+    "raster_sh_offset": ('        acc += 0.5f;\n        out[ch]', '        acc += 0.25f;\n        out[ch]'),
+    "raster_view_dir_sign": ('float d[3] = {pv[0] - campos[0], pv[1] - campos[1], pv[2] - campos[2]};', 'float d[3] = {campos[0] - pv[0], campos[1] - pv[1], campos[2] - pv[2]};'),
+    "raster_camera_centre": ('out[k] = -(V[k] * V[3] + V[4 + k] * V[7] + V[8 + k] * V[11]);', 'out[k] = -(V[4 * k] * V[3] + V[4 * k + 1] * V[7] + V[4 * k + 2] * V[11]);'),
 }
 
 
