@@ -931,8 +931,8 @@ struct RasterParams {
 };
 
 struct alignas(16) RasterSplat {  // 48 bytes
-    float mx, my, ca, cb;
-    float cc, opacity, r, g;
+    float mx, my, qa, qb;  // qa, qb, qc: the conic scaled by -log2(e)/2, -log2(e), -log2(e)/2
+    float qc, opacity, r, g;
     float b;
     uint32_t rx;  // tile columns [rx & 0xffff, rx >> 16)
     uint32_t ry;  // tile rows
@@ -1017,9 +1017,10 @@ __global__ __launch_bounds__(256) void k_raster_prep(RasterParams P, const float
     RasterSplat o;
     o.mx = mx;
     o.my = my;
-    o.ca = c / det;
-    o.cb = -b / det;
-    o.cc = a / det;
+    const float L = 1.4426950408889634f;
+    o.qa = (c / det) * (-0.5f * L);
+    o.qb = (-b / det) * -L;
+    o.qc = (a / det) * (-0.5f * L);
     o.opacity = s4.w;
     o.rx = x0 | (x1 << 16);
     o.ry = y0 | (y1 << 16);
@@ -1111,24 +1112,38 @@ __global__ __launch_bounds__(1024) void k_raster_sum64(const uint32_t* __restric
     }
 }
 
+// kEmitLanes lanes per Gaussian write its (tile, Gaussian) items interleaved, row-major over its
+// tile rectangle from start[j].
+constexpr uint32_t kEmitLanes = 8;
+
 __global__ __launch_bounds__(256) void k_raster_emit(RasterParams P, const RasterSplat* __restrict__ sp,
                                                      const uint32_t* __restrict__ order,
                                                      const uint32_t* __restrict__ start, uint32_t* __restrict__ keys,
                                                      uint32_t* __restrict__ vals) {
-    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t j = t / kEmitLanes;
+    const uint32_t sub = (uint32_t)(t % kEmitLanes);
     if (j >= P.count) return;
+    const uint32_t begin = start[j], end = start[j + 1];
+    if (begin + sub >= end) return;
     const uint32_t g = order[j];
-    const uint32_t n = start[j + 1] - start[j];
-    if (n == 0) return;
     const uint32_t rx = sp[g].rx, ry = sp[g].ry;
-    const uint32_t x0 = rx & 0xffffu, x1 = rx >> 16, y0 = ry & 0xffffu, y1 = ry >> 16;
-    uint32_t k = start[j];
-    for (uint32_t y = y0; y < y1; ++y)
-        for (uint32_t x = x0; x < x1; ++x) {
-            keys[k] = y * P.tiles_x + x;
-            vals[k] = g;
-            ++k;
+    const uint32_t x0 = rx & 0xffffu, x1 = rx >> 16, y0 = ry & 0xffffu;
+    const uint32_t w = x1 - x0;  // >= 1: the Gaussian has items
+    uint32_t x = x0 + sub, y = y0;
+    while (x >= x1) {
+        x -= w;
+        ++y;
+    }
+    for (uint32_t k = begin + sub; k < end; k += kEmitLanes) {
+        keys[k] = y * P.tiles_x + x;
+        vals[k] = g;
+        x += kEmitLanes;
+        while (x >= x1) {
+            x -= w;
+            ++y;
         }
+    }
 }
 
 __global__ __launch_bounds__(256) void k_raster_tiles(RasterParams P, const RasterSplat* __restrict__ sp,
@@ -1155,22 +1170,33 @@ __global__ __launch_bounds__(256) void k_raster_tiles(RasterParams P, const Rast
         }
         __syncthreads();
         const uint32_t n = end - base < 256 ? end - base : 256;
-        for (uint32_t u = 0; u < n && !done; ++u) {
-            const float4 A = la[u], B = lb[u];  // (mx, my, ca, cb), (cc, opacity, r, g)
-            const float dx = A.x - pxc, dy = A.y - pyc;
-            const float power = -0.5f * (A.z * dx * dx + B.x * dy * dy) - A.w * dx * dy;
-            if (power > 0.0f) continue;
-            const float alpha = fminf(0.99f, B.y * expf(power));
-            if (alpha < 1.0f / 255.0f) continue;
-            const float next = T * (1.0f - alpha);
-            if (next < 0.0001f) {
-                done = 1;
-                break;
+        // Branch-free: every lane evaluates every entry and the tests become selects (the same
+        // comparisons, so NaN behaves as in a branching loop); a stopped lane keeps its values.
+        // The wave leaves the batch once all of its lanes have stopped.
+        for (uint32_t u0 = 0; u0 < n; u0 += 4) {
+#pragma unroll
+            for (uint32_t du = 0; du < 4; ++du) {
+                const uint32_t u = u0 + du;
+                if (u >= n) break;  // wave-uniform
+                const float4 A = la[u], B = lb[u];  // (mx, my, qa, qb), (qc, opacity, r, g)
+                const float C = lc[u];
+                const float dx = A.x - pxc, dy = A.y - pyc;
+                // power * log2(e), with the oracle's fused operations
+                const float p2 = __builtin_fmaf(A.z * dx, dx, __builtin_fmaf(B.x * dy, dy, A.w * dx * dy));
+                // the hardware 2^x: below 2^-126 alpha is far under the 1/255 floor either way
+                const float alpha = fminf(0.99f, B.y * __builtin_amdgcn_exp2f(p2));
+                const float next = T * (1.0f - alpha);
+                const bool ok = !done && !(p2 > 0.0f) && !(alpha < 1.0f / 255.0f);
+                const bool stop = ok && next < 0.0001f;
+                const bool apply = ok && !stop;
+                const float wgt = alpha * T;
+                cr = apply ? __builtin_fmaf(B.z, wgt, cr) : cr;
+                cg = apply ? __builtin_fmaf(B.w, wgt, cg) : cg;
+                cb = apply ? __builtin_fmaf(C, wgt, cb) : cb;
+                T = apply ? next : T;
+                done = done || stop;
             }
-            cr += B.z * alpha * T;
-            cg += B.w * alpha * T;
-            cb += lc[u] * alpha * T;
-            T = next;
+            if (__all(done)) break;
         }
     }
     if (inside) image[(uint64_t)py * P.width + px] = make_float4(cr, cg, cb, 1.0f - T);
@@ -1286,8 +1312,8 @@ hipError_t launch_raster_gaussians(const float4* pv, const float* sh, const floa
     NPA_RES(ws.table, plan.table_entries * 4);
 #undef NPA_RES
     if (count) {
-        hipLaunchKernelGGL(k_raster_emit, dim3((count + 255) / 256), dim3(256), 0, stream, P, sp, order, start,
-                           ws.keys.as<uint32_t>(), ws.vals.as<uint32_t>());
+        hipLaunchKernelGGL(k_raster_emit, dim3((uint32_t)(((uint64_t)count * kEmitLanes + 255) / 256)), dim3(256), 0,
+                           stream, P, sp, order, start, ws.keys.as<uint32_t>(), ws.vals.as<uint32_t>());
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     // the scan wrote the item count to start[count]; the tile sort reads it from there

@@ -373,7 +373,9 @@ npa_status npa_state_decode_gaussians_3d(npa_state* state, const npa_gaussian_de
  *   compositing: each pixel (centre at +0.5) walks its tile's Gaussians front to back (depth
  *     ascending, ties by index): power = -(a dx^2 + c dy^2)/2 - b dx dy (skip when > 0),
  *     alpha = min(0.99, opacity e^power) (skip below 1/255); it stops before the Gaussian that
- *     would take transmittance T below 1e-4; rgb += colour alpha T, T *= 1 - alpha.
+ *     would take transmittance T below 1e-4; rgb += colour alpha T, T *= 1 - alpha. The power is
+ *     evaluated as qa dx^2 + qc dy^2 + qb dx dy with the conic pre-scaled by -log2(e)/2, -log2(e),
+ *     -log2(e)/2 in fused multiply-adds, and e^power as 2^(that).
  * image[height][width][4] = premultiplied r, g, b and 1 - T; it is overwritten. */
 enum { NPA_RASTER_COLOR_SH = 0, NPA_RASTER_COLOR_RGB = 1 };
 typedef struct npa_raster_camera {

@@ -1695,7 +1695,7 @@ int oracle_perceive_adjoint(const float* positions, const float* states, uint32_
 typedef struct raster_splat {
     int live;
     float depth;
-    float mx, my, ca, cb, cc, opacity, rgb[3];
+    float mx, my, qa, qb, qc, opacity, rgb[3];
     int tx0, tx1, ty0, ty1;
 } raster_splat;
 
@@ -1806,9 +1806,11 @@ static void raster_prepare(const float* pv, const float* sh, const float* rot, c
     const float fy1 = raster_clampf(floorf((my + radius) / 16.0f) + 1.0f, 0.0f, (float)tiles_y);
     out->tx0 = (int)fx0; out->tx1 = (int)fx1; out->ty0 = (int)fy0; out->ty1 = (int)fy1;
     if (out->tx0 >= out->tx1 || out->ty0 >= out->ty1) return;
-    out->ca = c / det;
-    out->cb = -b / det;
-    out->cc = a / det;
+    /* the conic scaled so that power * log2(e) = qa dx^2 + qc dy^2 + qb dx dy */
+    const float L = 1.4426950408889634f;
+    out->qa = (c / det) * (-0.5f * L);
+    out->qb = (-b / det) * -L;
+    out->qc = (a / det) * (-0.5f * L);
     out->mx = mx;
     out->my = my;
     out->depth = tz;
@@ -1893,13 +1895,14 @@ int oracle_raster_gaussians_3d(const float* position_visibility, const float* sp
                         const raster_splat* g = &sp[list[k]];
                         ++pairs;
                         const float dx = g->mx - pxc, dy = g->my - pyc;
-                        const float power = -0.5f * (g->ca * dx * dx + g->cc * dy * dy) - g->cb * dx * dy;
-                        if (power > 0.0f) continue;
-                        const float alpha = fminf(0.99f, g->opacity * expf(power));
+                        const float p2 = fmaf(g->qa * dx, dx, fmaf(g->qc * dy, dy, g->qb * dx * dy));
+                        if (p2 > 0.0f) continue;
+                        const float alpha = fminf(0.99f, g->opacity * exp2f(p2));
                         if (alpha < 1.0f / 255.0f) continue;
                         const float next = T * (1.0f - alpha);
                         if (next < 0.0001f) break;
-                        for (int ch = 0; ch < 3; ++ch) rgb[ch] += g->rgb[ch] * alpha * T;
+                        const float wgt = alpha * T;
+                        for (int ch = 0; ch < 3; ++ch) rgb[ch] = fmaf(g->rgb[ch], wgt, rgb[ch]);
                         T = next;
                     }
                     float* o = image + 4 * ((uint64_t)py * cam->width + px);

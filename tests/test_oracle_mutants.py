@@ -79,9 +79,10 @@ MUTANTS = {
     "decode_opacity_channel": ("float opacity_logit = clamp_f32(s[S - 4]", "float opacity_logit = clamp_f32(s[S - 5]"),
     "raster_lowpass_dropped": ('U[0][2] * T[0][2]) + 0.3f;', 'U[0][2] * T[0][2]);'),
     "raster_y_not_flipped": ('const float tx = vx, ty = -vy, tz = -vz;', 'const float tx = vx, ty = vy, tz = -vz;'),
-    "raster_conic_cross_sign": ('out->cb = -b / det;', 'out->cb = b / det;'),
-    "raster_power_cross_sign": ('g->cc * dy * dy) - g->cb * dx * dy;', 'g->cc * dy * dy) + g->cb * dx * dy;'),
-    "raster_alpha_clamp": ('fminf(0.99f, g->opacity * expf(power))', 'fminf(1.0f, g->opacity * expf(power))'),
+    "raster_conic_cross_sign": ('out->qb = (-b / det) * -L;', 'out->qb = (b / det) * -L;'),
+    "raster_power_cross_sign": ('fmaf(g->qc * dy, dy, g->qb * dx * dy)', 'fmaf(g->qc * dy, dy, -g->qb * dx * dy)'),
+    "raster_log2e_dropped": ('out->qa = (c / det) * (-0.5f * L);', 'out->qa = (c / det) * -0.5f;'),
+    "raster_alpha_clamp": ('fminf(0.99f, g->opacity * exp2f(p2))', 'fminf(1.0f, g->opacity * exp2f(p2))'),
     "raster_alpha_floor": ('if (alpha < 1.0f / 255.0f) continue;', 'if (alpha < 1.0f / 64.0f) continue;'),
     "raster_no_cut": ('if (next < 0.0001f) break;', 'if (next < 0.0f) break;'),
     "raster_pixel_centre": ('const float pxc = (float)px + 0.5f,', 'const float pxc = (float)px,'),
