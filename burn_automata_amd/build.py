@@ -14,7 +14,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libnpa_hip.so")
-SOURCES = ["npa_hashgrid.hip", "npa_perception.hip", "npa_adjoint.hip", "npa_decode.hip", "npa_abi.hip",
+SOURCES = ["npa_hashgrid.hip", "npa_perception.hip", "npa_adjoint.hip", "npa_decode.hip", "npa_sort.hip", "npa_abi.hip",
            "npa_bpk.cpp"]
 # npa_perception.hip compiles as three objects (its NPA_PART selects which kernels each holds)
 PARTS = {"npa_perception.hip": ["-DNPA_PART=0", "-DNPA_PART=2", "-DNPA_PART=3"]}

@@ -356,7 +356,7 @@ __global__ __launch_bounds__(256) void k_splat_tiles(SplatParams P, const SplatP
 
 void SplatWorkspace::release() {
     for (DevBuf* b : {&params, &item_start, &keys, &vals, &sorted, &ranks, &table, &totals, &offsets, &count, &flags, &scan,
-                      &attrs, &partials, &chunks, &order, &decoded})
+                      &attrs, &partials, &chunks, &order, &decoded, &sort_temp})
         b->release();
 }
 
@@ -914,11 +914,11 @@ hipError_t launch_render_attributes(const float* states, uint32_t count, uint32_
 //   k_raster_prep      per Gaussian: camera-frame centre, cull, Sigma = R S S^T R^T, the EWA 2D
 //                      covariance + 0.3 px^2, its conic, 3-sigma radius, tile rectangle, colour
 //                      (spherical harmonics or RGB), the tile count and the depth key;
-//   depth order        three stable counting-sort passes (11 + 10 + 10 bits) of the positive
-//                      depth's float bits: depth ascending, ties by index;
+//   depth order        a stable radix sort of the indices by the positive depth's float bits
+//                      (rocPRIM): depth ascending, ties by index;
 //   k_raster_emit      the (tile, Gaussian) items in depth order, after a prefix of the tile
 //                      counts (its total read back to size the item buffers);
-//   stable key sort    by tile -> per-tile lists in depth order;
+//   stable key sort    by tile (the hashgrid's counting sort) -> per-tile lists in depth order;
 //   k_raster_tiles     one 256-thread block per 16x16 tile, one pixel per thread: the list is
 //                      staged through LDS 256 Gaussians at a time; each pixel composites front to
 //                      back and stops at the transmittance cut; the block leaves when every pixel
@@ -947,10 +947,8 @@ __device__ __forceinline__ float raster_clamp(float v, float lo, float hi) { ret
 __global__ __launch_bounds__(256) void k_raster_prep(RasterParams P, const float4* __restrict__ pv,
                                                      const float* __restrict__ sh, const float4* __restrict__ rot,
                                                      const float4* __restrict__ so, RasterSplat* __restrict__ out,
-                                                     uint32_t* __restrict__ ntiles, uint32_t* __restrict__ dkey,
-                                                     uint32_t* __restrict__ d_count) {
+                                                     uint32_t* __restrict__ ntiles, uint32_t* __restrict__ dkey) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i == 0) *d_count = P.count;
     if (i >= P.count) return;
     ntiles[i] = 0;
     dkey[i] = kDepthCulled;
@@ -1076,16 +1074,6 @@ __global__ __launch_bounds__(256) void k_raster_prep(RasterParams P, const float
     out[i] = o;
     ntiles[i] = (x1 - x0) * (y1 - y0);
     dkey[i] = __float_as_uint(tz);
-}
-
-// keys_out[j] = bits [shift, shift + log2(mask + 1)) of the depth key of Gaussian order[j] (j when
-// order is null)
-__global__ __launch_bounds__(256) void k_raster_digits(const uint32_t* __restrict__ dkey,
-                                                       const uint32_t* __restrict__ order, uint32_t count,
-                                                       uint32_t shift, uint32_t mask, uint32_t* __restrict__ keys) {
-    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= count) return;
-    keys[j] = (dkey[order ? order[j] : j] >> shift) & mask;
 }
 
 __global__ __launch_bounds__(256) void k_raster_gather_counts(const uint32_t* __restrict__ ntiles,
@@ -1230,23 +1218,17 @@ hipError_t launch_raster_gaussians(const float4* pv, const float* sh, const floa
     P.color_mode = cam.color_mode;
     const uint32_t ntile_total = P.tiles_x * P.tiles_y;
     if (ntile_total > 65536) return hipErrorInvalidValue;  // the key sort's bin limit
-    HashgridPlan lo, hi;
-    if (!make_key_sort_plan(count, 2048, &lo) || !make_key_sort_plan(count, 1024, &hi)) return hipErrorInvalidValue;
     const uint64_t n1 = count ? count : 1;
     hipError_t e;
 #define NPA_RES(buf, n) \
     if ((e = (buf).reserve((size_t)(n))) != hipSuccess) return e;
     NPA_RES(ws.params, n1 * sizeof(RasterSplat));
     NPA_RES(ws.item_start, (4 * n1 + 1) * 4);  // ntiles, depth keys, ordered counts, starts (+1)
-    NPA_RES(ws.order, 2 * n1 * 4);
+    NPA_RES(ws.order, n1 * 4);
     NPA_RES(ws.keys, n1 * 4);
-    NPA_RES(ws.ranks, n1 * 4);
-    NPA_RES(ws.table, std::max(lo.table_entries, hi.table_entries) * 4);
-    NPA_RES(ws.totals, std::max<uint64_t>(2048, ntile_total) * 4);
-    NPA_RES(ws.offsets, (std::max<uint64_t>(2048, ntile_total) + 1) * 4);
+    NPA_RES(ws.offsets, ((uint64_t)ntile_total + 1) * 4);
     NPA_RES(ws.count, 64);
     NPA_RES(ws.scan, (2 * (n1 / kScanBlock + 1) + 2) * 4);
-    NPA_RES(ws.flags, 64);
     ProfScope ps(prof, NPA_KERNEL_RASTER, stream);
     RasterSplat* sp = ws.params.as<RasterSplat>();
     uint32_t* ntiles = ws.item_start.as<uint32_t>();
@@ -1254,27 +1236,15 @@ hipError_t launch_raster_gaussians(const float4* pv, const float* sh, const floa
     uint32_t* ocounts = dkey + n1;
     uint32_t* start = ocounts + n1;  // n1 + 1 entries
     uint32_t* ord_a = ws.order.as<uint32_t>();
-    uint32_t* ord_b = ord_a + n1;
-    uint32_t* d_items = ws.count.as<uint32_t>();      // item count (the tile sort's key count)
-    uint32_t* d_count = d_items + 1;                   // Gaussian count (the depth sort's key count)
-    unsigned long long* d_total64 = reinterpret_cast<unsigned long long*>(d_items + 2);
-    hipLaunchKernelGGL(k_raster_prep, dim3((uint32_t)std::max<uint64_t>(1, (count + 255) / 256)), dim3(256), 0, stream,
-                       P, pv, sh, rot, so, sp, ntiles, dkey, d_count);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    // depth order: stable LSD passes over bits 0-10, 11-20, 21-30 (depth keys are non-negative floats)
-    const uint32_t shifts[3] = {0, 11, 21}, masks[3] = {0x7ffu, 0x3ffu, 0x3ffu};
-    const uint32_t* in_order = nullptr;
-    uint32_t* outs[3] = {ord_a, ord_b, ord_a};
-    for (int pass = 0; pass < 3 && count; ++pass) {
-        hipLaunchKernelGGL(k_raster_digits, dim3((count + 255) / 256), dim3(256), 0, stream, dkey, in_order, count,
-                           shifts[pass], masks[pass], ws.keys.as<uint32_t>());
+    unsigned long long* d_total64 = reinterpret_cast<unsigned long long*>(ws.count.as<uint32_t>() + 2);
+    if (count) {
+        hipLaunchKernelGGL(k_raster_prep, dim3((count + 255) / 256), dim3(256), 0, stream, P, pv, sh, rot, so, sp,
+                           ntiles, dkey);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        e = launch_key_sort(pass == 0 ? lo : hi, ws.keys.as<uint32_t>(), in_order, d_count, count,
-                            ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(), ws.totals.as<uint32_t>(),
-                            ws.offsets.as<uint32_t>(), outs[pass], ws.flags.as<uint32_t>(), stream);
-        if (e != hipSuccess) return e;
-        in_order = outs[pass];
     }
+    // depth order: stable radix sort of the indices by the depth keys' bits 0-30 (non-negative floats)
+    if ((e = sort_index_by_key(dkey, ws.keys.as<uint32_t>(), ord_a, count, 31, ws.sort_temp, stream)) != hipSuccess)
+        return e;
     const uint32_t* order = ord_a;
     if (count) {
         hipLaunchKernelGGL(k_raster_gather_counts, dim3((count + 255) / 256), dim3(256), 0, stream, ntiles, order,
@@ -1308,15 +1278,17 @@ hipError_t launch_raster_gaussians(const float4* pv, const float* sh, const floa
     NPA_RES(ws.keys, std::max(i1, n1) * 4);
     NPA_RES(ws.vals, i1 * 4);
     NPA_RES(ws.sorted, i1 * 4);
-    NPA_RES(ws.ranks, std::max(i1, n1) * 4);
+    NPA_RES(ws.ranks, i1 * 4);
     NPA_RES(ws.table, plan.table_entries * 4);
+    NPA_RES(ws.totals, (uint64_t)ntile_total * 4);
+    NPA_RES(ws.flags, 64);
 #undef NPA_RES
     if (count) {
         hipLaunchKernelGGL(k_raster_emit, dim3((uint32_t)(((uint64_t)count * kEmitLanes + 255) / 256)), dim3(256), 0,
                            stream, P, sp, order, start, ws.keys.as<uint32_t>(), ws.vals.as<uint32_t>());
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    // the scan wrote the item count to start[count]; the tile sort reads it from there
+    // stable counting sort of the items by tile (the scan wrote the item count to start[count])
     e = launch_key_sort(plan, ws.keys.as<uint32_t>(), ws.vals.as<uint32_t>(), start + count, items,
                         ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(), ws.totals.as<uint32_t>(),
                         ws.offsets.as<uint32_t>(), ws.sorted.as<uint32_t>(), ws.flags.as<uint32_t>(), stream);

@@ -312,7 +312,8 @@ struct SplatWorkspace {
     DevBuf params, item_start, keys, vals, sorted, ranks, table, totals, offsets, count, flags, scan;
     DevBuf attrs;  // render attributes of a state's particles: colours [n][3], opacities [n], sigmas [n]
     DevBuf partials, chunks;  // render: per-chunk partial tiles; chunk counts, starts and total
-    DevBuf order;    // oriented raster: depth-order ping-pong
+    DevBuf order;      // oriented raster: depth order
+    DevBuf sort_temp;  // oriented raster: the radix sort's temporary storage
     DevBuf decoded;  // oriented raster of a state: its decoded Gaussians
     void release();
 };
@@ -330,6 +331,10 @@ hipError_t launch_render_views(const float4* pos, const float* colors, const flo
                                const float* sigmas, uint32_t count, const uint32_t* views, uint32_t nviews,
                                const npa_render_cfg& cfg, float* images, SplatWorkspace& ws,
                                hipStream_t stream, Profiler* prof);
+// Stable sort of the indices 0..n-1 by keys[i] (bits [0, end_bit)): order[k] is the index of
+// the k-th smallest key, equal keys in ascending index; keys_out receives the sorted keys.
+hipError_t sort_index_by_key(const uint32_t* keys, uint32_t* keys_out, uint32_t* order, uint32_t n,
+                             uint32_t end_bit, DevBuf& temp, hipStream_t stream);
 // EWA raster of oriented Gaussians (npa_raster_gaussians_3d): image[height][width][4]. Reads the
 // (tile, Gaussian) item total back to the host (one stream synchronisation).
 hipError_t launch_raster_gaussians(const float4* position_visibility, const float* spherical_harmonic,
