@@ -100,3 +100,29 @@ def test_bench_kernel_work_counts():
 def test_graft_entry_points_exist():
     g = _load("__graft_entry__")
     assert callable(g.build) and callable(g.smoke)
+
+
+def test_raster_camera_look_at():
+    """RasterCamera.look_at (bevy's Transform::looking_at + default PerspectiveProjection): the view
+    rotation is orthonormal and right-handed, the eye maps to the origin, the target lies on the -z
+    axis at its distance, world up projects to +y, and fy = (height / 2) / tan(fov_y / 2)."""
+    import math
+
+    import numpy as np
+
+    from burn_automata_amd.config import RasterCamera
+
+    eye, target = np.array([0.6, -0.4, 2.2]), np.array([0.1, 0.2, -0.3])
+    cam = RasterCamera.look_at(tuple(eye), tuple(target), width=320, height=240)
+    V = np.array(cam.view, np.float64).reshape(4, 4)
+    R = V[:3, :3]
+    np.testing.assert_allclose(R @ R.T, np.eye(3), atol=1e-12)
+    assert abs(np.linalg.det(R) - 1.0) < 1e-12
+    np.testing.assert_allclose(V @ np.append(eye, 1.0), [0, 0, 0, 1], atol=1e-12)
+    t = V @ np.append(target, 1.0)
+    np.testing.assert_allclose(t[:2], 0.0, atol=1e-12)
+    assert abs(t[2] + np.linalg.norm(target - eye)) < 1e-12
+    up = R @ np.array([0.0, 1.0, 0.0])
+    assert up[1] > 0 and abs(up[0]) < 1e-12  # world up stays in the camera's y-z plane, pointing up
+    assert abs(cam.fy - 120.0 / math.tan(math.pi / 8)) < 1e-9 and cam.fx == cam.fy
+    assert (cam.cx, cam.cy) == (160.0, 120.0)
