@@ -3,7 +3,7 @@
 A context in host-I/O mode stages host inputs to the device and copies the outputs back before the
 call returns; the results must equal the same call's on device pointers bit for bit (the same
 kernels run on the same values). Covered here through the raw C-ABI with numpy arrays: the
-Gaussian decode, the 2D splat, the projected render and the oriented raster.
+Gaussian decode, the 2D splat, the projected render, the oriented raster and the rollout step.
 """
 import ctypes as C
 
@@ -78,3 +78,30 @@ def test_splat_and_render_on_host_pointers(ctx, host_ctx):
     host_ctx.check(lib().npa_render_views(host_ctx.handle, _p(pos), _p(col), _p(op), _p(sg), n, _p(views),
                                           len(views), C.byref(rcfg.to_c()), _p(imgs)))
     np.testing.assert_array_equal(imgs, to_np(K.render_views(pos, col, op, sg, rcfg, ctx=ctx)))
+
+
+def test_step_on_host_pointers(ctx, host_ctx):
+    """npa_step (NpaModel::step_cpu, model.rs:768-858) with host positions, states, mask, weights and
+    outputs: equal to the device-pointer step bit for bit."""
+    from burn_automata_amd import _abi
+    from burn_automata_amd import synthetic as syn
+    from burn_automata_amd.model import NpaModel
+
+    w = syn.workload("c1", particles=2048)
+    model = NpaModel(w["model"], w["weights"])
+    n, S = w["n"], w["model"].state_dims
+    pos = np.ascontiguousarray(w["positions"], f32)
+    st = np.ascontiguousarray(w["states"], f32).reshape(-1)
+    mask = (np.random.default_rng(9).uniform(size=n) < 0.5).astype(f32)
+    dev = model.step(pos, st, 1, n, w["grid"], w["dt"], mask, ctx=ctx)
+    W = model.weights
+    w1, b1, w2, b2 = (np.ascontiguousarray(to_np(a), f32) for a in (W.w1, W.b1, W.w2, W.b2))
+    wc = _abi.NpaWeightsC(_p(w1), _p(b1), _p(w2), _p(b2))
+    op, os_, dens = np.zeros((n, 4), f32), np.zeros(n * S, f32), np.zeros(n, f32)
+    host_ctx.check(lib().npa_step(host_ctx.handle, _p(pos), _p(st), 1, n, C.byref(w["grid"].to_c()),
+                                  C.byref(model.config.to_c()), C.byref(wc), float(w["dt"]), _p(mask), _p(op),
+                                  _p(os_), _p(dens)))
+    np.testing.assert_array_equal(op, to_np(dev.next_positions))
+    np.testing.assert_array_equal(os_.reshape(n, S), to_np(dev.next_states))
+    np.testing.assert_array_equal(dens, to_np(dev.density))
+    assert not np.array_equal(os_, st)  # the step changed the states
