@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <initializer_list>
 #include <string>
 #include <vector>
 
@@ -197,6 +198,22 @@ int grid_blocks_for(const npa_context* ctx, const npa::HashgridPlan& plan) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// A null array that the call reads or writes is a caller error, refused before any HIP call
+// (a null pointer would otherwise reach a kernel).
+npa_status need(npa_context* ctx, std::initializer_list<const void*> arrays, const char* what) {
+    for (const void* a : arrays)
+        if (!a) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, std::string("invalid argument: null ") + what);
+    return NPA_OK;
+}
+
+// The weight arrays of a model with F features, H hidden units and O outputs (empty ones may be null).
+npa_status need_weights(npa_context* ctx, const npa_weights* w, uint64_t F, uint64_t H, uint64_t O) {
+    if (!w) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null weights");
+    if ((H * F && !w->w1) || (H && !w->b1) || (O * H && !w->w2) || (O && !w->b2))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null weight array");
+    return NPA_OK;
+}
+
 // Host I/O: stages host arrays through context-owned device buffers.
 struct HostIO {
     npa_context* ctx;
@@ -247,13 +264,19 @@ struct HostIO {
     }
 };
 
+// Reports (and clears) the coordinate overflows of every hashgrid build on `ws` since the last
+// report: device-pointer calls queue their builds without waiting, so their overflow surfaces at
+// the next call that synchronises (host-I/O calls, npa_neighbor_lists, npa_state_read,
+// npa_context_synchronize).
 npa_status check_flags(npa_context* ctx, npa::Workspace& ws) {
-    uint32_t flags = 0;
-    NPA_HIP(ctx, hipMemcpyAsync(&flags, ws.flags.ptr, 4, hipMemcpyDeviceToHost, ctx->stream), "flags readback");
+    if (!ws.flags.ptr) return NPA_OK;
+    uint32_t flags[2] = {0, 0};
+    NPA_HIP(ctx, hipMemcpyAsync(flags, ws.flags.ptr, 8, hipMemcpyDeviceToHost, ctx->stream), "flags readback");
     NPA_HIP(ctx, hipStreamSynchronize(ctx->stream), "flags readback");
-    if (flags & 1u) {
-        uint32_t zero = 0;
-        NPA_HIP(ctx, hipMemcpy(ws.flags.ptr, &zero, 4, hipMemcpyHostToDevice), "flags reset");
+    if ((flags[0] | flags[1]) & 1u) {
+        const uint32_t zero[2] = {0, 0};
+        NPA_HIP(ctx, hipMemcpyAsync(ws.flags.ptr, zero, 8, hipMemcpyHostToDevice, ctx->stream), "flags reset");
+        NPA_HIP(ctx, hipStreamSynchronize(ctx->stream), "flags reset");
         return fail(ctx, NPA_ERR_COORD_OVERFLOW,
                     "a particle-mode cell coordinate left the +-2^30 range the device path stores exactly");
     }
@@ -369,6 +392,7 @@ npa_status npa_build_hashgrid(npa_context* ctx, const float* positions, uint32_t
         NPA_HIP(ctx, hipMemsetAsync(bo, 0, bin_offsets_len * 4, ctx->stream), "zero bin_offsets");
     }
     NPA_HIP(ctx, io.finish(), "host io");
+    if (ctx->host_io) return check_flags(ctx, ctx->ws);
     return NPA_OK;
 }
 
@@ -378,8 +402,9 @@ npa_status npa_neighbor_lists(npa_context* ctx, const float* positions, uint32_t
     if (!ctx || !offsets || !required) return NPA_ERR_INVALID_ARGUMENT;
     npa_status st = validate_grid(ctx, cfg);
     if (st) return st;
-    if (set_device(ctx)) return NPA_ERR_DEVICE;
     const uint64_t total = (uint64_t)B * N;
+    if (total && (st = need(ctx, {positions}, "positions"))) return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
     npa::HashgridPlan plan;
     std::string err;
     if (!npa::make_plan(*cfg, B, N, &plan, &err)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
@@ -427,7 +452,7 @@ npa_status npa_neighbor_lists(npa_context* ctx, const float* positions, uint32_t
         didx.release();
     }
     dcounts.release();
-    return NPA_OK;
+    return check_flags(ctx, ctx->ws);
 }
 
 npa_status npa_perceive(npa_context* ctx, const float* positions, const float* states, uint32_t B, uint32_t N,
@@ -543,9 +568,11 @@ npa_status npa_mlp_forward(npa_context* ctx, const float* features, uint32_t row
     if (!ctx || !w) return NPA_ERR_INVALID_ARGUMENT;
     npa_status st = check_model(ctx, model, nullptr);
     if (st) return st;
-    if (set_device(ctx)) return NPA_ERR_DEVICE;
     const uint32_t F = model_perception_dims(*model), H = model->hidden_dims, S = model->state_dims;
     const uint32_t O = model->spatial_dims + S;
+    if (rows && (st = need(ctx, {features, dx, ds}, "features or outputs"))) return st;
+    if ((st = need_weights(ctx, w, F, H, O))) return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
     HostIO io(ctx);
     npa::StepIO sio;
     const float* f = io.in(features, (uint64_t)rows * F * 4);
@@ -574,8 +601,10 @@ npa_status npa_euler_step(npa_context* ctx, const float* positions, const float*
     if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
     npa_status st = validate_grid(ctx, cfg);
     if (st) return st;
-    if (set_device(ctx)) return NPA_ERR_DEVICE;
     const uint64_t total = (uint64_t)B * N;
+    if (total && (st = need(ctx, {positions, states, dx, ds, out_positions, out_states}, "input or output array")))
+        return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
     HostIO io(ctx);
     const float4* pos = (const float4*)io.in(positions, total * 16);
     const float* sin_ = io.in(states, total * S * 4);
@@ -602,10 +631,13 @@ npa_status npa_step(npa_context* ctx, const float* positions, const float* state
     npa_status st = validate_grid(ctx, grid);
     if (st) return st;
     if ((st = check_model(ctx, model, grid))) return st;
-    if (set_device(ctx)) return NPA_ERR_DEVICE;
     const uint64_t total = (uint64_t)B * N;
     const uint32_t S = model->state_dims, F = model_perception_dims(*model), H = model->hidden_dims;
     const uint32_t O = model->spatial_dims + S;
+    if (total && (st = need(ctx, {positions, states, out_positions, out_states}, "positions, states or outputs")))
+        return st;
+    if ((st = need_weights(ctx, w, F, H, O))) return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
     npa::HashgridPlan plan;
     std::string err;
     if (!npa::make_plan(*grid, B, N, &plan, &err, npa::targets_per_item(npa::state_stride_for(model->state_dims))))
@@ -655,6 +687,8 @@ npa_status npa_step(npa_context* ctx, const float* positions, const float* state
 npa_status npa_update_mask(npa_context* ctx, uint32_t B, uint32_t N, float update_prob, uint32_t step_index,
                            uint64_t seed, float* mask) {
     if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
+    npa_status st = NPA_OK;
+    if ((uint64_t)B * N && (st = need(ctx, {mask}, "mask"))) return st;
     if (set_device(ctx)) return NPA_ERR_DEVICE;
     HostIO io(ctx);
     float* m = io.out(mask, (uint64_t)B * N * 4);
@@ -692,6 +726,7 @@ npa_status npa_decode_gaussians_3d(npa_context* ctx, const float* positions, con
     if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
     npa_status st = check_decode(ctx, S, cfg);
     if (st) return st;
+    if (count && (st = need(ctx, {positions, states, pv, sh, rot, so}, "input or output array"))) return st;
     if (set_device(ctx)) return NPA_ERR_DEVICE;
     const uint32_t K = cfg->mode == NPA_DECODE_SH0_ORIENTED ? (cfg->sh_degree + 1) * (cfg->sh_degree + 1) : 1;
     HostIO io(ctx);
@@ -726,7 +761,7 @@ npa_status npa_splat_2d(npa_context* ctx, const float* positions, const float* c
     if (!ctx || !image) return NPA_ERR_INVALID_ARGUMENT;
     npa_status st = check_splat(ctx, cfg);
     if (st) return st;
-    if (count && !colors) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null colors");
+    if (count && (!colors || !positions)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null positions or colors");
     if (set_device(ctx)) return NPA_ERR_DEVICE;
     HostIO io(ctx);
     const float4* pos = (const float4*)io.in(positions, (uint64_t)count * 16);
@@ -891,9 +926,13 @@ npa_status npa_state_create(npa_context* ctx, const npa_model_cfg* model, const 
     npa_status st = validate_grid(ctx, grid);
     if (st) return st;
     if ((st = check_model(ctx, model, grid))) return st;
-    if (set_device(ctx)) return NPA_ERR_DEVICE;
     const uint64_t total = (uint64_t)B * N;
     if (total == 0) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: empty particle system");
+    if ((st = need(ctx, {positions, states}, "positions or states"))) return st;
+    if ((st = need_weights(ctx, w, model_perception_dims(*model), model->hidden_dims,
+                           model->spatial_dims + model->state_dims)))
+        return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
     npa::HashgridPlan plan;
     std::string err;
     if (!npa::make_plan(*grid, B, N, &plan, &err, npa::targets_per_item(npa::state_stride_for(model->state_dims))))
@@ -1016,9 +1055,11 @@ npa_status npa_state_read(npa_state* s, float* positions, float* states, float* 
 npa_status npa_state_update_model(npa_state* s, const npa_weights* w) {
     if (!s || !w) return NPA_ERR_INVALID_ARGUMENT;
     npa_context* ctx = s->ctx;
-    if (set_device(ctx)) return NPA_ERR_DEVICE;
     const npa_model_cfg& m = s->model;
     const uint32_t F = model_perception_dims(m), H = m.hidden_dims, O = m.spatial_dims + m.state_dims;
+    npa_status st = need_weights(ctx, w, F, H, O);
+    if (st) return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
     const hipMemcpyKind kind = ctx->host_io ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
     if ((uint64_t)H * F) NPA_HIP(ctx, hipMemcpyAsync(s->w1.ptr, w->w1, (uint64_t)H * F * 4, kind, ctx->stream), "w1");
     if (H) NPA_HIP(ctx, hipMemcpyAsync(s->b1.ptr, w->b1, (uint64_t)H * 4, kind, ctx->stream), "b1");
@@ -1130,6 +1171,7 @@ npa_status npa_state_decode_gaussians_3d(npa_state* s, const npa_gaussian_decode
     const uint32_t S = s->model.state_dims;
     npa_status st = check_decode(ctx, S, cfg);
     if (st) return st;
+    if ((st = need(ctx, {pv, sh, rot, so}, "output array"))) return st;
     if (set_device(ctx)) return NPA_ERR_DEVICE;
     const uint64_t total = (uint64_t)s->B * s->N;
     const uint32_t K = cfg->mode == NPA_DECODE_SH0_ORIENTED ? (cfg->sh_degree + 1) * (cfg->sh_degree + 1) : 1;
@@ -1262,7 +1304,7 @@ npa_status npa_state_pair_counts(npa_state* s, uint64_t* candidates, uint64_t* p
     if (targets) *targets = h[2];
     if (target_candidates) *target_candidates = h[3];
     if (target_pairs) *target_pairs = h[4];
-    return NPA_OK;
+    return check_flags(ctx, s->ws);
 }
 
 // ================================================================== profiling

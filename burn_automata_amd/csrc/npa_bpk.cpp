@@ -202,6 +202,14 @@ class Json {
         return v;
     }
 
+    // A usize field that this library's C ABI carries as u32 (dims, grid sizes): values above
+    // u32::MAX are refused here rather than truncated.
+    uint32_t u32_integer() {
+        const uint64_t v = unsigned_integer();
+        if (v > 0xFFFFFFFFull) fail("invalid value: integer out of range for u32");
+        return (uint32_t)v;
+    }
+
     // f32 field: the literal read as f64, then rounded to f32.
     float f32() {
         const Number n = number();
@@ -407,9 +415,9 @@ void read_config(Json& js, npa_manifest& m) {
                   "log_norm_grad", "log_norm_density_grad", "stopgrad_pos", "stopgrad_state"});
     js.object([&](const std::string& k) {
         req.mark(js, k);
-        if (k == "spatial_dims") m.spatial_dims = js.unsigned_integer();
-        else if (k == "state_dims") m.state_dims = js.unsigned_integer();
-        else if (k == "hidden_dims") m.hidden_dims = js.unsigned_integer();
+        if (k == "spatial_dims") m.spatial_dims = js.u32_integer();
+        else if (k == "state_dims") m.state_dims = js.u32_integer();
+        else if (k == "hidden_dims") m.hidden_dims = js.u32_integer();
         else if (k == "eps0") m.eps0 = js.f32();
         else if (k == "alpha") m.alpha = js.f32();
         else if (k == "density_grad") m.density_grad = js.boolean();
@@ -421,7 +429,7 @@ void read_config(Json& js, npa_manifest& m) {
         else if (k == "equivariance")  // EquivarianceMode config.rs:22-28
             m.equivariance = enum_variant(js, {"None", "ParticleDensity", "ParticleDensityAndScale"});
         else if (k == "position_features") m.position_features = js.boolean();
-        else if (k == "auxiliary_input_dims") m.auxiliary_input_dims = js.unsigned_integer();
+        else if (k == "auxiliary_input_dims") m.auxiliary_input_dims = js.u32_integer();
         else if (k == "decoder_dims") {
             m.has_decoder_dims = !js.null_literal();
             if (m.has_decoder_dims) m.decoder_dims = js.unsigned_integer();
@@ -437,7 +445,7 @@ void read_hashgrid(Json& js, npa_manifest& m) {
     Required req({"dim", "boundary", "mode", "grid_size", "eps", "max_particles_per_block"});
     js.object([&](const std::string& k) {
         req.mark(js, k);
-        if (k == "dim") m.grid_dim = js.unsigned_integer();
+        if (k == "dim") m.grid_dim = js.u32_integer();
         else if (k == "boundary") m.grid.boundary = enum_variant(js, {"Periodic", "Clamped"}) == 0 ? NPA_BOUNDARY_PERIODIC
                                                                                                : NPA_BOUNDARY_CLAMPED;
         else if (k == "mode") m.grid.mode = enum_variant(js, {"Grid", "Particle"}) == 0 ? NPA_MODE_GRID : NPA_MODE_PARTICLE;
@@ -445,11 +453,11 @@ void read_hashgrid(Json& js, npa_manifest& m) {
             js.expect('[');
             for (int a = 0; a < 3; ++a) {
                 if (a) js.expect(',');
-                m.grid_size[a] = js.unsigned_integer();
+                m.grid_size[a] = js.u32_integer();
             }
             if (!js.eat(']')) js.fail("invalid length, expected an array of length 3");
         } else if (k == "eps") m.grid.eps = js.f32();
-        else if (k == "max_particles_per_block") m.max_particles_per_block = js.unsigned_integer();
+        else if (k == "max_particles_per_block") m.max_particles_per_block = js.u32_integer();
         else js.skip();
     });
     req.check(js);

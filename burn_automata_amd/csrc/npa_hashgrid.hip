@@ -394,8 +394,17 @@ __global__ __launch_bounds__(256) void k_scatter(uint32_t n, uint32_t total, uin
                                                  const uint32_t* __restrict__ table,
                                                  const uint32_t* __restrict__ bin_offsets,
                                                  uint32_t* __restrict__ out, uint32_t* __restrict__ inv,
-                                                 int payload) {
+                                                 int payload, uint32_t* __restrict__ flags) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    // This build's coordinate-overflow flag (set by k_hash_rank, which has finished) moves into the
+    // sticky word the synchronising entry points report, so the next build starts clean.
+    if (i == 0) {
+        const uint32_t f = flags[0];
+        if (f) {
+            flags[1] |= f;
+            flags[0] = 0;
+        }
+    }
     if (i >= total) return;
     const uint32_t b = i / n;
     const uint32_t li = i - b * n;
@@ -949,7 +958,7 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                      plan.tile, plan.tiles_per_sys, plan.cells, ws.keys.as<uint32_t>(), ws.ranks.as<uint32_t>(),
                      ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(),
                      payload ? ws.tmpidx.as<uint32_t>() : ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(),
-                     payload ? 1 : 0);
+                     payload ? 1 : 0, ws.flags.as<uint32_t>());
     if (e != hipSuccess || !payload) return e;
     const uint32_t nbins = batch * plan.cells;
     auto split = g.dim == 2 ? k_split<2> : k_split<3>;

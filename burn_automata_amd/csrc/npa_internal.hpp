@@ -93,6 +93,8 @@ struct HashgridPlan {
 constexpr uint32_t kDirGroups = 8;
 
 struct Workspace {
+    // flags: u32 [0] the current build's coordinate overflow (set by k_hash_rank, moved by
+    // k_scatter), [1] overflows not yet reported (read and cleared by the synchronising calls)
     DevBuf keys, ranks, table, totals, bin_offsets, perm, inv, flags, wl_count, worklist;
     DevBuf srec, scoord, sstate, counters, features, wpad;
     // svol: per sorted slot float4 {x, y, z, 1/rho (recip_finite)}, written by the density pass:

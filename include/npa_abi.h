@@ -47,8 +47,17 @@ typedef enum npa_status {
     NPA_ERR_INVALID_FORMAT = 23,       /* AutomataError::InvalidFormat */
     NPA_ERR_DEVICE = 30,               /* HIP runtime failure */
     NPA_ERR_OUT_OF_MEMORY = 31,
-    NPA_ERR_COORD_OVERFLOW = 32        /* a cell coordinate left the i32 range the device path supports */
+    NPA_ERR_COORD_OVERFLOW = 32        /* a Particle-mode cell coordinate left +-2^30 (see below) */
 } npa_status;
+
+/* Errors and argument checks. A null array that a call reads or writes (when its length is not 0)
+ * returns NPA_ERR_INVALID_ARGUMENT before any device work is queued. NPA_ERR_COORD_OVERFLOW:
+ * a hashgrid build met a Particle-mode cell coordinate beyond +-2^30 (positions beyond about
+ * 2^30 * eps), where the device path's i32 cell records are no longer exact. Device-pointer calls
+ * queue their work without waiting, so the overflow of such a call is returned by the next call
+ * on the same context (or, for a state, by npa_state_read) that synchronises: every call in
+ * host-I/O mode, npa_neighbor_lists, npa_state_read, npa_state_pair_counts and
+ * npa_context_synchronize. Reporting it clears it. */
 
 /* ---------------------------------------------------------------- config */
 /* Boundary / HashGridMode: crates/burn_automata_kernels/src/config.rs:4-18 */

@@ -154,6 +154,14 @@ def test_serde_json_rules(c1):
         bpk.load_manifest_bytes(manifest_json(m, g, w).replace(b'"hidden_dims":128', b'"hidden_dims":128.0'))
     with pytest.raises(_abi.JsonError):
         bpk.load_manifest_bytes(manifest_json(m, g, w)[:-1])
+    # usize fields the C ABI carries as u32 are refused above u32::MAX instead of truncated
+    # (2^32 + 64 would otherwise read as 64 and pass validation)
+    big = manifest_json(m, g, w).replace(b'"grid_size":[64,64,1]', b'"grid_size":[4294967360,64,1]')
+    assert big != manifest_json(m, g, w)
+    with pytest.raises(_abi.JsonError, match="out of range for u32"):
+        bpk.load_manifest_bytes(big)
+    with pytest.raises(_abi.JsonError, match="out of range for u32"):
+        bpk.load_manifest_bytes(manifest_json(m, g, w).replace(b'"state_dims":16', b'"state_dims":4294967312'))
     # f32 fields: shortest f32 text and the f64 text of the same f32 read the same
     got = bpk.load_manifest_bytes(manifest_json(m, g, w).replace(b'"eps":0.05', b'"eps":0.05000000074505806'))
     assert got.hashgrid.eps == np.float32(0.05)

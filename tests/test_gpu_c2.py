@@ -1,0 +1,79 @@
+"""The benchmarked C2 path (65,536 particles, default VALU engine) against the CPU oracle.
+
+The bench times `syn.workload("c2")`: a 64x64 Particle hashgrid rebuilt every step, the growing-2D
+model (F=64, H=128, O=18), the device hash mask with p=0.5 and a 512x512 splat every 32 steps.
+These tests run that exact configuration through the C ABI and compare it with the oracle's
+restatement of NpaModel::step_cpu (crates/burn_automata/src/model.rs:768-858), the rollout loop
+(crates/burn_automata/src/rollout/mod.rs:240-297) and splat_particles_2d
+(crates/burn_automata_kernels/src/splat.rs:30-93).
+
+Gates: every value bit-equal to the oracle (the device sums in the reference's order), with
+BASELINE's tolerances checked as well: 1e-5 (one step), 1e-3 (64-step rollout), images within
+0.5 dB PSNR of the CPU image against a common reference image and >= 100 dB against each other.
+"""
+import numpy as np
+import pytest
+
+from burn_automata_amd import synthetic as syn
+from burn_automata_amd.executor import HipAutomataExecutor
+from burn_automata_amd.model import NpaModel
+from oracle import oracle as O
+from tests.helpers import psnr, rel_err, to_np
+
+pytestmark = pytest.mark.gpu
+
+STEP_TOL = 1e-5
+ROLLOUT_TOL = 1e-3
+PSNR_GAP_DB = 0.5
+
+
+def test_c2_full_step_bit_exact(ctx):
+    w = syn.workload("c2")
+    m, g, n = w["model"], w["grid"], w["n"]
+    assert n == 65536 and m.perception_dims() == 64 and m.update_dims() == 18
+    mask = O.update_mask(1, n, w["update_prob"], 0, w["seed"])
+    want = O.step(m, w["weights"], w["positions"], w["states"], 1, n, g, w["dt"], mask)
+    got = NpaModel(m, w["weights"]).step(w["positions"], w["states"], 1, n, g, w["dt"],
+                                         update_mask=mask, ctx=ctx)
+    for name, a, b in (("density", got.density, want.density),
+                       ("positions", got.next_positions, want.next_positions),
+                       ("states", got.next_states, want.next_states)):
+        e = rel_err(a, b)
+        print(f"c2 step {name}: rel err {e:.3e}")
+        assert e <= STEP_TOL, name
+        np.testing.assert_array_equal(to_np(a), b, err_msg=name)
+
+
+def test_c2_rollout_64_steps_and_splats(ctx):
+    """The bench's pipeline for its first 64 steps: the resident rollout with the device hash mask,
+    and the 512x512 splat of the tail colours after steps 32 and 64."""
+    w = syn.workload("c2")
+    m, g, n, cfg = w["model"], w["grid"], w["n"], w["splat"]
+    every = w["decode_every"]
+    assert every == 32 and cfg.image_size == 512
+    ex = HipAutomataExecutor(ctx=ctx)
+    state = ex.create_state(NpaModel(m, w["weights"]), w["positions"], w["states"], 1, n, g,
+                            w["dt"], w["update_prob"], w["seed"])
+    # common reference for the PSNR gap: the image of the initial particles
+    ref0 = O.splat_particles_2d(w["positions"], O.tail_colors(w["states"], m.state_dims), cfg)
+    p, s = w["positions"], w["states"]
+    for stop in (every, 2 * every):
+        p, s = O.rollout(m, w["weights"], p, s, 1, n, g, every, w["dt"], w["update_prob"],
+                         w["seed"], stop - every)
+        ex.step_state_many(state, every)
+        assert state.step_index() == stop
+        gp, gs, _ = ex.read_state(state)
+        ep, es = rel_err(gp, p), rel_err(gs, s)
+        print(f"c2 after {stop} steps: rel err pos={ep:.3e} state={es:.3e}")
+        assert ep <= ROLLOUT_TOL and es <= ROLLOUT_TOL
+        np.testing.assert_array_equal(to_np(gp), p)
+        np.testing.assert_array_equal(to_np(gs), s)
+        img = to_np(ex.splat_2d(state, cfg))
+        want_img = O.splat_particles_2d(p, O.tail_colors(s, m.state_dims), cfg)
+        same = psnr(img, want_img)
+        gap = abs(psnr(img, ref0) - psnr(want_img, ref0))
+        print(f"c2 splat after {stop} steps: psnr vs CPU image {same:.1f} dB, "
+              f"gap against the step-0 image {gap:.2e} dB")
+        assert same >= 100.0
+        assert gap <= PSNR_GAP_DB
+    state.close()

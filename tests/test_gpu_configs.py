@@ -98,6 +98,8 @@ def test_c4_surface_rollout_decode_and_splat(ctx):
     ep, es = rel_err(gp, want_p), rel_err(gs, want_s)
     print(f"c4: {steps}-step rollout rel err pos={ep:.3e} state={es:.3e}")
     assert ep <= ROLLOUT_TOL and es <= ROLLOUT_TOL
+    np.testing.assert_array_equal(to_np(gp), want_p)
+    np.testing.assert_array_equal(to_np(gs), want_s)
     dec = ex.decode_gaussians_3d(state, w["decode"])
     want_dec = O.decode_gaussians_3d(want_p, want_s, w["model"].state_dims, w["decode"])
     for k in want_dec:
@@ -128,6 +130,8 @@ def test_c5_batched_bf16_rollout_and_tiled_splat(ctx):
     ep, es = rel_err(gp, want_p), rel_err(gs, want_s)
     print(f"c5: {steps}-step rollout rel err pos={ep:.3e} state={es:.3e}")
     assert ep <= ROLLOUT_TOL and es <= ROLLOUT_TOL
+    np.testing.assert_array_equal(to_np(gp), want_p)
+    np.testing.assert_array_equal(to_np(gs), want_s)
     cfg, tx = w["splat"], w["tiles_x"]
     img = to_np(ex.splat_2d_tiled(state, cfg, tx))
     size = cfg.image_size

@@ -249,6 +249,9 @@ def test_executor_rollout_64_steps(ctx, name):
     ep, es = rel_err(gp, want_p), rel_err(gs, want_s)
     print(f"{name}: 64-step rollout rel err pos={ep:.3e} state={es:.3e}")
     assert ep <= ROLLOUT_TOL and es <= ROLLOUT_TOL
+    # the VALU engine sums in the reference's order: the rollout is the oracle's bit for bit
+    np.testing.assert_array_equal(to_np(gp), want_p)
+    np.testing.assert_array_equal(to_np(gs), want_s)
 
 
 def test_executor_single_steps_match_fused_step(ctx):
