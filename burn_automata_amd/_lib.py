@@ -41,6 +41,8 @@ def _decl(L):
     L.npa_euler_step.argtypes = [P, P, P, P, P, u32, u32, u32, ptr(_abi.NpaGridCfg), f32, P, P, P]
     L.npa_step.argtypes = [P, P, P, u32, u32, ptr(_abi.NpaGridCfg), ptr(_abi.NpaModelCfg),
                            ptr(_abi.NpaWeightsC), f32, P, P, P, P]
+    L.npa_step_noalloc.argtypes = [P, P, P, u32, u32, ptr(_abi.NpaGridCfg), ptr(_abi.NpaModelCfg),
+                                   ptr(_abi.NpaWeightsC), f32, P, P, P, P]
     L.npa_update_mask.argtypes = [P, u32, u32, f32, u32, u64, P]
     L.npa_decode_gaussians_3d.argtypes = [P, P, P, u32, u32, ptr(_abi.NpaGaussianDecodeCfg), P, P,
                                           P, P]
@@ -94,7 +96,7 @@ def _decl(L):
                  "npa_manifest_info", "npa_manifest_model", "npa_manifest_initialization",
                  "npa_bpk_encode", "npa_sha256", "npa_render_views", "npa_render_attributes",
                  "npa_state_render_views", "npa_perceive_adjoint", "npa_raster_gaussians_3d",
-                 "npa_state_raster_gaussians_3d"):
+                 "npa_state_raster_gaussians_3d", "npa_step_noalloc"):
         getattr(L, name).restype = st
 
 
@@ -111,7 +113,7 @@ EXPORTED = (
     "npa_manifest_load_file", "npa_manifest_destroy", "npa_manifest_info", "npa_manifest_model",
     "npa_manifest_initialization", "npa_bpk_encode", "npa_sha256", "npa_render_views",
     "npa_render_attributes", "npa_state_render_views", "npa_perceive_adjoint",
-    "npa_raster_gaussians_3d", "npa_state_raster_gaussians_3d")
+    "npa_raster_gaussians_3d", "npa_state_raster_gaussians_3d", "npa_step_noalloc")
 
 
 def lib():

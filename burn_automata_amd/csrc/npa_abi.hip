@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <cmath>
 #include <initializer_list>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -33,6 +34,11 @@ struct npa_context {
     npa::AdjointWorkspace adj_ws;
     npa::Profiler prof;
     std::vector<DevBuf*> staging;
+    // npa_step_noalloc: this device's copy of the scratch array (null when it is unavailable, with
+    // the reason in scratch_err) and a view of its flag words for npa_context_synchronize
+    void* scratch = nullptr;
+    hipError_t scratch_err = hipSuccess;
+    npa::Workspace scratch_flags;
     ~npa_context() {
         ws.release();
         splat_ws.release();
@@ -198,6 +204,45 @@ int grid_blocks_for(const npa_context* ctx, const npa::HashgridPlan& plan) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// ------------------------------------------------------------ no-allocation workspace
+// npa_step_noalloc's workspace: a file-scope device array, one copy per GPU (each at its own
+// address), held until the process ends. In host code `scratch` is only a stand-in for the symbol,
+// not a device address: it is never passed to a kernel or a copy. Set-up resolves each device's
+// address with hipGetSymbolAddress (with that device current) and everything uses that address.
+static __device__ __align__(256) unsigned char scratch[NPA_STEP_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+bool g_scratch_done[kMaxScratchDevices] = {};
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+hipError_t g_scratch_err[kMaxScratchDevices] = {};
+
+// Once per device (the current one): the device address of `scratch`, with its flag words cleared.
+hipError_t scratch_address(int device, void** out) {
+    *out = nullptr;
+    if (device < 0 || device >= kMaxScratchDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_done[device]) {
+        void* p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e == hipSuccess) {
+            static const uint32_t zero[npa::kCarveFlagBytes / 4] = {};
+            e = hipMemcpy(p, zero, sizeof zero, hipMemcpyHostToDevice);
+        }
+        g_scratch_done[device] = true;
+        g_scratch_err[device] = e;
+        g_scratch_ptr[device] = e == hipSuccess ? p : nullptr;
+    }
+    *out = g_scratch_ptr[device];
+    return g_scratch_err[device];
+}
+
+// Clears the first n (<= 64) words of a buffer (a kernel rather than a memset node, so that a
+// caller may capture it in a graph).
+__global__ void k_clear_words(uint32_t* __restrict__ words, uint32_t n) {
+    if (threadIdx.x < n) words[threadIdx.x] = 0u;
+}
+
 // A null array that the call reads or writes is a caller error, refused before any HIP call
 // (a null pointer would otherwise reach a kernel).
 npa_status need(npa_context* ctx, std::initializer_list<const void*> arrays, const char* what) {
@@ -309,6 +354,8 @@ npa_status npa_context_create(int device, void* stream, npa_context** out) {
         return NPA_ERR_DEVICE;
     }
     ctx->cus = npa::device_cu_count();
+    ctx->scratch_err = scratch_address(device, &ctx->scratch);
+    if (ctx->scratch) ctx->scratch_flags.flags.view(ctx->scratch, npa::kCarveFlagBytes);
     *out = ctx;
     return NPA_OK;
 }
@@ -343,8 +390,9 @@ npa_status npa_context_set_mlp_engine(npa_context* ctx, int engine) {
 npa_status npa_context_synchronize(npa_context* ctx) {
     if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
     NPA_HIP(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
-    if (ctx->ws.flags.ptr) return check_flags(ctx, ctx->ws);
-    return NPA_OK;
+    npa_status st = check_flags(ctx, ctx->ws);
+    if (st) return st;
+    return check_flags(ctx, ctx->scratch_flags);
 }
 
 const char* npa_last_error(const npa_context* ctx) { return ctx ? ctx->last_error.c_str() : "null context"; }
@@ -681,6 +729,75 @@ npa_status npa_step(npa_context* ctx, const float* positions, const float* state
     }
     NPA_HIP(ctx, io.finish(), "host io");
     if (ctx->host_io) return check_flags(ctx, ctx->ws);
+    return NPA_OK;
+}
+
+npa_status npa_step_noalloc(npa_context* ctx, const float* positions, const float* states, uint32_t B, uint32_t N,
+                            const npa_grid_cfg* grid, const npa_model_cfg* model, const npa_weights* w, float dt,
+                            const float* mask, float* out_positions, float* out_states, float* out_density) {
+    if (!ctx || !w) return NPA_ERR_INVALID_ARGUMENT;
+    npa_status st = validate_grid(ctx, grid);
+    if (st) return st;
+    if ((st = check_model(ctx, model, grid))) return st;
+    const uint64_t total = (uint64_t)B * N;
+    const uint32_t S = model->state_dims, F = model_perception_dims(*model), H = model->hidden_dims;
+    const uint32_t O = model->spatial_dims + S;
+    if (total && (st = need(ctx, {positions, states, out_positions, out_states}, "positions, states or outputs")))
+        return st;
+    if ((st = need_weights(ctx, w, F, H, O))) return st;
+    if (ctx->host_io)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT,
+                    "invalid argument: npa_step_noalloc takes device pointers (host-I/O mode stages through "
+                    "allocations)");
+    if (!ctx->scratch)
+        return fail(ctx, NPA_ERR_DEVICE,
+                    std::string("no-allocation workspace unavailable: ") + hipGetErrorString(ctx->scratch_err));
+    npa::HashgridPlan plan;
+    std::string err;
+    if (!npa::make_plan(*grid, B, N, &plan, &err, npa::targets_per_item(npa::state_stride_for(S))))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
+    npa::StepParams p = make_params(*grid, opts_for_model(*model), B, N, S);
+    apply_model(&p, *model, grid->eps);
+    p.dt = dt;
+    p.update_prob = 1.0f;
+    p.mlp_engine = (uint32_t)ctx->mlp_engine;
+    npa::Workspace ws;  // views into this device's scratch array
+    const uint64_t need_bytes = ws.carve(plan, total, B, S, (int)grid->dim, p.FP, npa::padded_weight_floats(p) * 4,
+                                         ctx->scratch, NPA_STEP_NOALLOC_SCRATCH_BYTES);
+    if (need_bytes > NPA_STEP_NOALLOC_SCRATCH_BYTES)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT,
+                    "invalid argument: this system needs " + std::to_string(need_bytes) +
+                        " bytes of workspace, above npa_step_noalloc's fixed " +
+                        std::to_string((uint64_t)NPA_STEP_NOALLOC_SCRATCH_BYTES));
+    if (total && (!aligned16(positions) || !aligned16(out_positions)))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: positions must be 16-byte aligned");
+    if (total && (S % 4 == 0) && !aligned16(states))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: states must be 16-byte aligned");
+    if (total && npa::state_stride_for(S) == S && !aligned16(out_states))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: output states must be 16-byte aligned");
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    if (!total) return NPA_OK;
+    npa::StepIO sio;
+    sio.pos = (const float4*)positions;
+    sio.states = states;
+    sio.mask = mask;
+    sio.w1 = w->w1;
+    sio.b1 = w->b1;
+    sio.w2 = w->w2;
+    sio.b2 = w->b2;
+    sio.out_pos = (float4*)out_positions;
+    sio.out_states = out_states;
+    const int blocks = grid_blocks_for(ctx, plan);
+    // the build's overflow word must start at zero; everything else is written before it is read
+    hipLaunchKernelGGL(k_clear_words, dim3(1), dim3(64), 0, ctx->stream, ws.flags.as<uint32_t>(), 1u);
+    NPA_HIP(ctx, hipGetLastError(), "clear flags");
+    NPA_HIP(ctx, npa::launch_pad_weights(p, sio.w1, sio.b1, sio.w2, sio.b2, ws.wpad.as<float>(), ctx->stream),
+            "pad weights");
+    const npa::SplitTargets targets = npa::step_targets(p, sio);
+    NPA_HIP(ctx, npa::launch_hashgrid(plan, p.g, sio.pos, sio.states, S, B, N, ws, true, ctx->stream, nullptr, &targets),
+            "hashgrid");
+    NPA_HIP(ctx, npa::launch_density(p, ws, out_density, blocks, ctx->stream, nullptr), "density");
+    NPA_HIP(ctx, npa::launch_update(p, ws, sio, 0, blocks, ctx->stream, nullptr), "update");
     return NPA_OK;
 }
 

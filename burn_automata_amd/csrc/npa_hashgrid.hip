@@ -41,49 +41,82 @@ hipError_t DevBuf::reserve(size_t want) {
 }
 
 void DevBuf::release() {
-    if (ptr) (void)hipFree(ptr);
+    if (ptr && owned) (void)hipFree(ptr);
     ptr = nullptr;
     bytes = 0;
+    owned = true;
+}
+
+void DevBuf::view(void* p, size_t b) {
+    release();
+    ptr = p;
+    bytes = b;
+    owned = false;
+}
+
+// Every buffer of a hashgrid + step pass with its size, in one list for both set-ups (allocation
+// and carving); the coordinate-overflow flags are handled by each set-up itself.
+template <class F>
+static void each_buffer(Workspace& w, const HashgridPlan& plan, uint64_t total, uint32_t batch, uint32_t state_dims,
+                        int dim, uint32_t feature_dims, uint64_t wpad_bytes, F&& f) {
+    const uint64_t t1 = total ? total : 1;
+    const uint64_t bins = (uint64_t)batch * plan.cells;
+    f(w.keys, t1 * 4);
+    f(w.ranks, t1 * 4);
+    f(w.table, (plan.table_entries ? plan.table_entries : 1) * 4);
+    f(w.totals, (bins ? bins : 1) * 4);
+    f(w.bin_offsets, (bins + 1) * 4);
+    f(w.perm, t1 * 4);
+    f(w.inv, t1 * 4);
+    f(w.wl_count, 64);
+    f(w.worklist, (plan.worklist_cap + 1) * 8);
+    // second-pass items: at most one partial item per (64-slot window, cell run) pair
+    f(w.act_rows, t1 * 4);
+    f(w.srec, t1 * 16);
+    f(w.scoord, dim == 3 ? t1 * 16 : 16);
+    f(w.sstate, t1 * (uint64_t)state_stride_for(state_dims ? state_dims : 1) * 4);
+    f(w.svol, t1 * 16);
+    f(w.counters, 64);
+    f(w.features, t1 * (uint64_t)(feature_dims ? feature_dims : 1) * 4);
+    f(w.wpad, wpad_bytes ? wpad_bytes : 4);
+    f(w.tmpidx, t1 * 4);
+    f(w.dir_n, (bins ? bins : 1) * 4);
+    f(w.bin_list, (bins ? bins : 1) * 4);
+    f(w.dir_e, (bins ? bins : 1) * kDirGroups * 16);
+    f(w.nb_chunks, t1 * max_chunks(dim) * 16);
+    f(w.nb_count, t1 * 4);
 }
 
 hipError_t Workspace::reserve(const HashgridPlan& plan, uint64_t total, uint32_t batch,
                               uint32_t state_dims, int dim, uint32_t feature_dims) {
-    hipError_t e;
-    const uint64_t t1 = total ? total : 1;
-    const uint64_t bins = (uint64_t)batch * plan.cells;
-#define NPA_RES(buf, n)                                 \
-    if ((e = (buf).reserve((size_t)(n))) != hipSuccess) \
-        return e;
-    NPA_RES(keys, t1 * 4);
-    NPA_RES(ranks, t1 * 4);
-    NPA_RES(table, (plan.table_entries ? plan.table_entries : 1) * 4);
-    NPA_RES(totals, (bins ? bins : 1) * 4);
-    NPA_RES(bin_offsets, (bins + 1) * 4);
-    NPA_RES(perm, t1 * 4);
-    NPA_RES(inv, t1 * 4);
-    NPA_RES(wl_count, 64);
-    NPA_RES(worklist, (plan.worklist_cap + 1) * 8);
-    // second-pass items: at most one partial item per (64-slot window, cell run) pair
-    NPA_RES(act_rows, t1 * 4);
-    NPA_RES(srec, t1 * 16);
-    NPA_RES(scoord, dim == 3 ? t1 * 16 : 16);
-    NPA_RES(sstate, t1 * (uint64_t)state_stride_for(state_dims ? state_dims : 1) * 4);
-    NPA_RES(svol, t1 * 16);
-    NPA_RES(counters, 64);
-    NPA_RES(features, t1 * (uint64_t)(feature_dims ? feature_dims : 1) * 4);
-    NPA_RES(wpad, 4);
-    NPA_RES(tmpidx, t1 * 4);
-    NPA_RES(dir_n, (bins ? bins : 1) * 4);
-    NPA_RES(bin_list, (bins ? bins : 1) * 4);
-    NPA_RES(dir_e, (bins ? bins : 1) * kDirGroups * 16);
-    NPA_RES(nb_chunks, t1 * max_chunks(dim) * 16);
-    NPA_RES(nb_count, t1 * 4);
-#undef NPA_RES
+    hipError_t e = hipSuccess;
+    each_buffer(*this, plan, total, batch, state_dims, dim, feature_dims, 4, [&](DevBuf& b, uint64_t n) {
+        if (e == hipSuccess) e = b.reserve((size_t)n);
+    });
+    if (e != hipSuccess) return e;
     if (!flags.ptr) {
         if ((e = flags.reserve(64)) != hipSuccess) return e;
         if ((e = hipMemset(flags.ptr, 0, 64)) != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+uint64_t Workspace::carve(const HashgridPlan& plan, uint64_t total, uint32_t batch, uint32_t state_dims, int dim,
+                          uint32_t feature_dims, uint64_t wpad_bytes, void* base, uint64_t capacity) {
+    constexpr uint64_t kAlign = 256;
+    uint64_t off = kCarveFlagBytes;  // the flags take the first 256 bytes
+    each_buffer(*this, plan, total, batch, state_dims, dim, feature_dims, wpad_bytes, [&](DevBuf&, uint64_t n) {
+        off += (n + kAlign - 1) / kAlign * kAlign;
+    });
+    if (off > capacity || !base) return off;
+    char* p = static_cast<char*>(base);
+    flags.view(p, kCarveFlagBytes);
+    off = kCarveFlagBytes;
+    each_buffer(*this, plan, total, batch, state_dims, dim, feature_dims, wpad_bytes, [&](DevBuf& b, uint64_t n) {
+        b.view(p + off, (size_t)n);
+        off += (n + kAlign - 1) / kAlign * kAlign;
+    });
+    return off;
 }
 
 void Workspace::release() {

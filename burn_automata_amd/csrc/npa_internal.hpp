@@ -13,12 +13,15 @@
 
 namespace npa {
 
-// Grow-only device allocation.
+// Grow-only device allocation, or a view into memory the library does not allocate (view(); never
+// freed).
 struct DevBuf {
     void* ptr = nullptr;
     size_t bytes = 0;
+    bool owned = true;
     hipError_t reserve(size_t want);
     void release();
+    void view(void* p, size_t b);
     template <class T>
     T* as() const { return static_cast<T*>(ptr); }
 };
@@ -114,8 +117,14 @@ struct Workspace {
     DevBuf nb_chunks, nb_count;
     hipError_t reserve(const HashgridPlan& plan, uint64_t total, uint32_t batch, uint32_t state_dims,
                        int dim, uint32_t feature_dims = 0);
+    // The same buffers (with wpad_bytes for the padded weights) as views into [base, base +
+    // capacity): the flags first (kCarveFlagBytes), then every buffer on a 256-byte boundary. Returns
+    // the bytes the layout needs; the views are set only when it fits (and base is not null).
+    uint64_t carve(const HashgridPlan& plan, uint64_t total, uint32_t batch, uint32_t state_dims, int dim,
+                   uint32_t feature_dims, uint64_t wpad_bytes, void* base, uint64_t capacity);
     void release();
 };
+constexpr uint64_t kCarveFlagBytes = 256;
 
 // Chunk records kept per target by the density pass (a 2D target visits 9 cells, a 3D one 27; a
 // cell run of more than 64 particles spans several chunks).

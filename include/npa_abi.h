@@ -262,6 +262,24 @@ npa_status npa_step(npa_context* ctx, const float* positions, const float* state
                     const npa_weights* weights, float dt, const float* update_mask,
                     float* out_positions, float* out_states, float* out_density);
 
+/* npa_step without any allocation. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory - code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc. Same arguments, checks and results as npa_step (bit for bit), device pointers
+ * only (NPA_ERR_INVALID_ARGUMENT in host-I/O mode); it calls no hipMalloc, hipFree, memset or
+ * allocating library routine. Its workspace is a fixed device array of
+ * NPA_STEP_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on until the process
+ * ends; a system whose workspace does not fit is refused with NPA_ERR_INVALID_ARGUMENT before any
+ * work is queued (the C2 system - 65,536 particles, S = 16, F = 64, a 64x64 grid - fits). Every
+ * call on one GPU shares that array and the next call overwrites it: calls that overlap on one GPU
+ * (on other streams, contexts or threads) race. The kernel profiler does not time it; its
+ * coordinate overflows are reported by npa_context_synchronize. */
+#define NPA_STEP_NOALLOC_SCRATCH_BYTES (64u << 20)
+npa_status npa_step_noalloc(npa_context* ctx, const float* positions, const float* states,
+                            uint32_t batch_size, uint32_t particle_count,
+                            const npa_grid_cfg* grid, const npa_model_cfg* model,
+                            const npa_weights* weights, float dt, const float* update_mask,
+                            float* out_positions, float* out_states, float* out_density);
+
 /* The device update mask of the reference GPU path (gpu_step.wgsl:1019-1056 with lane
  * seeds from crates/burn_automata/src/gpu/executor/state.rs:1282-1315):
  * mask[b*N+i] = random01(i, step_index, lane_seed(b)) < update_prob. */
