@@ -79,6 +79,8 @@ def _decl(L):
     L.npa_state_splat_2d.argtypes = [P, ptr(_abi.NpaSplat2dCfg), P]
     L.npa_state_splat_2d_tiled.argtypes = [P, ptr(_abi.NpaSplat2dCfg), u32, P]
     L.npa_state_decode_gaussians_3d.argtypes = [P, ptr(_abi.NpaGaussianDecodeCfg), P, P, P, P]
+    L.npa_state_write_gaussians.argtypes = [P, u32, P, P, P, P]
+    L.npa_state_step_into_gaussians.argtypes = [P, u32, u32, P, P, P, P]
     L.npa_profile_enable.argtypes = [P, C.c_int]
     L.npa_profile_reset.argtypes = [P]
     L.npa_profile_read.argtypes = [P, C.c_int, ptr(C.c_double), ptr(u64)]
@@ -96,7 +98,8 @@ def _decl(L):
                  "npa_manifest_info", "npa_manifest_model", "npa_manifest_initialization",
                  "npa_bpk_encode", "npa_sha256", "npa_render_views", "npa_render_attributes",
                  "npa_state_render_views", "npa_perceive_adjoint", "npa_raster_gaussians_3d",
-                 "npa_state_raster_gaussians_3d", "npa_step_noalloc"):
+                 "npa_state_raster_gaussians_3d", "npa_step_noalloc", "npa_state_write_gaussians",
+                 "npa_state_step_into_gaussians"):
         getattr(L, name).restype = st
 
 
@@ -113,7 +116,8 @@ EXPORTED = (
     "npa_manifest_load_file", "npa_manifest_destroy", "npa_manifest_info", "npa_manifest_model",
     "npa_manifest_initialization", "npa_bpk_encode", "npa_sha256", "npa_render_views",
     "npa_render_attributes", "npa_state_render_views", "npa_perceive_adjoint",
-    "npa_raster_gaussians_3d", "npa_state_raster_gaussians_3d", "npa_step_noalloc")
+    "npa_raster_gaussians_3d", "npa_state_raster_gaussians_3d", "npa_step_noalloc", "npa_state_write_gaussians",
+    "npa_state_step_into_gaussians")
 
 
 def lib():

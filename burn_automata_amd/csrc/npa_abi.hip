@@ -1356,24 +1356,75 @@ npa_status npa_raster_gaussians_3d(npa_context* ctx, const float* position_visib
     return NPA_OK;
 }
 
+// Gaussian buffers of a state's export: `count` entries of each array, at least B*N
+// (write_state_into_gaussian_bind_group_impl steps.rs:93-98).
+static npa_status check_export(npa_context* ctx, const npa_state* s, uint32_t count, std::initializer_list<const void*> arrays) {
+    const uint64_t total = (uint64_t)s->B * s->N;
+    if (count < total)
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT,
+                    "invalid argument: gaussian bind group count " + std::to_string(count) +
+                        " is smaller than automata particle count " + std::to_string(total));
+    return need(ctx, arrays, "Gaussian array");
+}
+
+// The export of the state's current buffers into device (or staged host) arrays.
+static npa_status write_export(npa_state* s, float* pv, float* sh, float* rot, float* so) {
+    npa_context* ctx = s->ctx;
+    const uint64_t total = (uint64_t)s->B * s->N;
+    HostIO io(ctx);
+    float* dpv = io.out(pv, total * 16);
+    float* dsh = io.out(sh, total * NPA_GAUSSIAN_SH_COEFF_COUNT * 4);
+    float* drot = io.out(rot, total * 16);
+    float* dso = io.out(so, total * 16);
+    if (io.err) return hip_fail(ctx, io.err, "staging");
+    if (!aligned16(dpv) || !aligned16(dsh) || !aligned16(drot) || !aligned16(dso))
+        return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: Gaussian arrays must be 16-byte aligned");
+    NPA_HIP(ctx, npa::launch_write_gaussians(s->pos[s->cur].as<float4>(), s->states[s->cur].as<float>(),
+                                             (uint32_t)total, s->N, s->model.state_dims, s->model.spatial_dims,
+                                             s->grid.eps, s->model.position_features != 0, dpv, dsh, drot, dso,
+                                             ctx->stream),
+            "gaussian export");
+    NPA_HIP(ctx, io.finish(), "host io");
+    return NPA_OK;
+}
+
+npa_status npa_state_write_gaussians(npa_state* s, uint32_t count, float* pv, float* sh, float* rot, float* so) {
+    if (!s) return NPA_ERR_INVALID_ARGUMENT;
+    npa_context* ctx = s->ctx;
+    npa_status st = check_export(ctx, s, count, {pv, sh, rot, so});
+    if (st) return st;
+    if (set_device(ctx)) return NPA_ERR_DEVICE;
+    return write_export(s, pv, sh, rot, so);
+}
+
+npa_status npa_state_step_into_gaussians(npa_state* s, uint32_t steps, uint32_t count, float* pv, float* sh,
+                                         float* rot, float* so) {
+    if (!s) return NPA_ERR_INVALID_ARGUMENT;
+    npa_context* ctx = s->ctx;
+    npa_status st = check_export(ctx, s, count, {pv, sh, rot, so});
+    if (st) return st;
+    if ((st = npa_state_step(s, steps ? steps : 1u))) return st;
+    return write_export(s, pv, sh, rot, so);
+}
+
 npa_status npa_state_raster_gaussians_3d(npa_state* s, const npa_gaussian_decode_cfg* cfg,
                                          const npa_raster_camera* camera, float* image) {
     if (!s) return NPA_ERR_INVALID_ARGUMENT;
     npa_context* ctx = s->ctx;
-    npa_status st = check_decode(ctx, s->model.state_dims, cfg);
-    if (st) return st;
+    npa_status st = NPA_OK;
+    if (cfg && (st = check_decode(ctx, s->model.state_dims, cfg))) return st;
     st = check_raster_camera(ctx, camera);
     if (st) return st;
     if (!image) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null image");
     npa_raster_camera cam = *camera;
-    cam.sh_degree = cfg->mode == NPA_DECODE_SH0_ORIENTED ? cfg->sh_degree : 0;
-    if (cam.sh_degree > 3)
-        return fail(ctx, NPA_ERR_INVALID_ARGUMENT,
-                    "invalid argument: raster sh_degree must be <= 3, got " + std::to_string(cam.sh_degree));
+    // the export carries SH coefficients (degree-3 layout, DC only); the decode carries colours
+    cam.sh_degree = cfg ? 0u : 3u;
+    cam.color_mode = cfg ? NPA_RASTER_COLOR_RGB : NPA_RASTER_COLOR_SH;
+    const uint32_t K = cfg ? (cfg->mode == NPA_DECODE_SH0_ORIENTED ? (cfg->sh_degree + 1) * (cfg->sh_degree + 1) : 1u)
+                           : NPA_GAUSSIAN_SH_COEFF_COUNT / 3;
     const uint64_t total = (uint64_t)s->B * s->N;
     if (total >= (1ull << 31)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: too many Gaussians");
     if (set_device(ctx)) return NPA_ERR_DEVICE;
-    const uint64_t K = (uint64_t)(cam.sh_degree + 1) * (cam.sh_degree + 1);
     const uint64_t t1 = total ? total : 1;
     const uint64_t sh_bytes = (t1 * K * 12 + 15) / 16 * 16;
     NPA_HIP(ctx, ctx->splat_ws.decoded.reserve(t1 * 48 + sh_bytes), "alloc");
@@ -1386,10 +1437,17 @@ npa_status npa_state_raster_gaussians_3d(npa_state* s, const npa_gaussian_decode
     float* img = io.out(image, (uint64_t)cam.width * cam.height * 16);
     if (io.err) return hip_fail(ctx, io.err, "staging");
     if (!aligned16(img)) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: the image must be 16-byte aligned");
-    NPA_HIP(ctx, npa::launch_decode_gaussians(s->pos[s->cur].as<float4>(), s->states[s->cur].as<float>(),
-                                              (uint32_t)total, s->model.state_dims, *cfg, dpv, dsh, drot, dso,
-                                              ctx->stream),
-            "decode");
+    if (cfg)
+        NPA_HIP(ctx, npa::launch_decode_gaussians(s->pos[s->cur].as<float4>(), s->states[s->cur].as<float>(),
+                                                  (uint32_t)total, s->model.state_dims, *cfg, dpv, dsh, drot, dso,
+                                                  ctx->stream),
+                "decode");
+    else
+        NPA_HIP(ctx, npa::launch_write_gaussians(s->pos[s->cur].as<float4>(), s->states[s->cur].as<float>(),
+                                                 (uint32_t)total, s->N, s->model.state_dims, s->model.spatial_dims,
+                                                 s->grid.eps, s->model.position_features != 0, dpv, dsh, drot, dso,
+                                                 ctx->stream),
+                "gaussian export");
     NPA_HIP(ctx, npa::launch_raster_gaussians((const float4*)dpv, dsh, (const float4*)drot, (const float4*)dso,
                                               (uint32_t)total, cam, img, ctx->splat_ws, ctx->stream, &ctx->prof),
             "raster");

@@ -99,6 +99,111 @@ hipError_t launch_decode_gaussians(const float4* pos, const float* states, uint3
     return hipGetLastError();
 }
 
+// ------------------------------------------------------------ viewer export
+// write_gaussian_from_output  crates/burn_automata/src/gpu_step.wgsl:4963-5052 (write_gaussian_main
+// 4929-4936): position (z = 0 in 2D) and visibility 1; 48 SH coefficients, zero but for the DC
+// triple (clamp(tail + 0.5) - 0.5) / SH_C0 of the last three state channels (4981-4990); identity
+// rotation and isotropic scale max(eps * 0.12, 8e-5), or for 3D position-feature models with
+// S >= 9 the rotation taking +z onto the normal in channels 4..6 and a flattened tangent-plane
+// scale (4992-5045); opacity 1 in 2D, clamp(sigmoid(channel 8, or 3 when S <= 8), 0.001, 0.95) in
+// 3D (5046-5051). normalize() is v / sqrt(sum v^2) and length() sqrt(x^2 + y^2 + z^2), in that
+// order (the oracle's restatement evaluates the same operations). The material branch belongs to
+// the adaptive rollouts and is not built.
+constexpr float kShC0 = 0.28209479177387814f;  // SH_C0 gpu_step.wgsl:7
+constexpr uint32_t kShCoeffs = NPA_GAUSSIAN_SH_COEFF_COUNT;
+
+struct ExportParams {
+    uint32_t total, N, S, dim;
+    float eps;
+    uint32_t normal_branch;
+};
+
+__device__ __forceinline__ float export_channel(const float* s, uint32_t S, uint32_t c) {  // output_state_channel
+    return c < S ? s[c] : (S > 0 ? s[0] : 0.0f);
+}
+
+// One thread per particle for the 4-float records; each wave then writes its 64 particles' SH
+// rows (12 float4 each) as consecutive float4s, lane l taking float4 j * 64 + l of the wave's
+// block and the DC triple from the particle's lane.
+__global__ __launch_bounds__(256) void k_write_gaussians(ExportParams P, const float4* __restrict__ pos,
+                                                         const float* __restrict__ states, float4* __restrict__ pv,
+                                                         float4* __restrict__ sh, float4* __restrict__ rot,
+                                                         float4* __restrict__ so) {
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    float dc[3] = {0.0f, 0.0f, 0.0f};
+    if (idx < P.total) {
+        const uint32_t S = P.S;
+        const float* s = states + (uint64_t)idx * S;
+        const float4 p = pos[idx];
+        pv[idx] = make_float4(p.x, p.y, P.dim == 3 ? p.z : 0.0f, 1.0f);
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) {  // output_tail_state_channel(idx, 2 - ch)
+            const uint32_t off = 2u - (uint32_t)ch;
+            const float tail = S > off ? export_channel(s, S, S - 1 - off) : export_channel(s, S, 0);
+            const float color = clampf_(tail + 0.5f, 0.0f, 1.0f);
+            dc[ch] = (color - 0.5f) / kShC0;
+        }
+        const float iso = fmaxf(P.eps * 0.12f, 0.00008f);
+        float sc[3] = {iso, iso, iso};
+        float q[4] = {1.0f, 0.0f, 0.0f, 0.0f};
+        if (P.normal_branch) {
+            const float n0 = export_channel(s, S, 4), n1 = export_channel(s, S, 5), n2 = export_channel(s, S, 6);
+            const float nn = sqrtf(n0 * n0 + n1 * n1 + n2 * n2);
+            float u0 = 0.0f, u1 = 0.0f, u2 = 1.0f;
+            if (nn > 1.0e-6f && nn < 1.0e20f) {
+                u0 = n0 / nn;
+                u1 = n1 / nn;
+                u2 = n2 / nn;
+            }
+            if (u2 <= -0.999999f) {
+                q[0] = 0.0f;
+                q[1] = 1.0f;
+                q[2] = 0.0f;
+                q[3] = 0.0f;
+            } else {
+                const float r[4] = {1.0f + u2, -u1, u0, 0.0f};
+                const float rl = sqrtf(r[0] * r[0] + r[1] * r[1] + r[2] * r[2] + r[3] * r[3]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) q[k] = r[k] / rl;
+            }
+            const float density_scale = clampf_(sqrtf(4096.0f / fmaxf((float)P.N, 1.0f)), 0.4f, 2.0f);
+            const float tangent =
+                fmaxf(clampf_(P.eps * 0.32f * density_scale, P.eps * 0.08f, P.eps * 0.64f), 0.00008f);
+            sc[0] = tangent;
+            sc[1] = tangent;
+            sc[2] = fmaxf(tangent * 0.18f, 0.00008f);
+        }
+        float opacity = 1.0f;
+        if (P.dim == 3) {
+            const float logit = export_channel(s, S, S > 8 ? 8u : 3u);
+            opacity = clampf_(1.0f / (1.0f + expf(-logit)), 0.001f, 0.95f);
+        }
+        rot[idx] = make_float4(q[0], q[1], q[2], q[3]);
+        so[idx] = make_float4(sc[0], sc[1], sc[2], opacity * 1.0f);
+    }
+    constexpr uint32_t kRow = kShCoeffs / 4;  // float4s per particle
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t first = idx - lane;  // the wave's first particle
+#pragma unroll
+    for (uint32_t j = 0; j < kRow; ++j) {
+        const uint32_t v = j * 64 + lane;
+        const uint32_t pl = v / kRow, comp = v - pl * kRow;
+        const float d0 = __shfl(dc[0], (int)pl, 64), d1 = __shfl(dc[1], (int)pl, 64), d2 = __shfl(dc[2], (int)pl, 64);
+        if (first + pl < P.total)
+            sh[(uint64_t)(first + pl) * kRow + comp] = comp == 0 ? make_float4(d0, d1, d2, 0.0f) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+}
+
+hipError_t launch_write_gaussians(const float4* pos, const float* states, uint32_t total, uint32_t particle_count,
+                                  uint32_t S, uint32_t dim, float eps, bool position_features, float* pv, float* sh,
+                                  float* rot, float* so, hipStream_t stream) {
+    if (total == 0) return hipSuccess;
+    ExportParams P{total, particle_count, S, dim, eps, (dim == 3 && position_features && S >= 9) ? 1u : 0u};
+    hipLaunchKernelGGL(k_write_gaussians, dim3((total + 255) / 256), dim3(256), 0, stream, P, pos, states,
+                       (float4*)pv, (float4*)sh, (float4*)rot, (float4*)so);
+    return hipGetLastError();
+}
+
 // ----------------------------------------------------------------- splat
 constexpr int kTile = 16;
 

@@ -319,6 +319,11 @@ hipError_t launch_neighbor_lists(const StepParams& p, Workspace& ws, uint32_t* c
 hipError_t launch_decode_gaussians(const float4* pos, const float* states, uint32_t count,
                                    uint32_t state_dims, const npa_gaussian_decode_cfg& cfg,
                                    float* pv, float* sh, float* rot, float* so, hipStream_t stream);
+// write_gaussian_from_output (gpu_step.wgsl:4963-5052) of `total` particles: pv, rot, so [total][4],
+// sh [total][NPA_GAUSSIAN_SH_COEFF_COUNT], all 16-byte aligned.
+hipError_t launch_write_gaussians(const float4* pos, const float* states, uint32_t total, uint32_t particle_count,
+                                  uint32_t S, uint32_t dim, float eps, bool position_features, float* pv, float* sh,
+                                  float* rot, float* so, hipStream_t stream);
 struct SplatWorkspace {
     DevBuf params, item_start, keys, vals, sorted, ranks, table, totals, offsets, count, flags, scan;
     DevBuf attrs;  // render attributes of a state's particles: colours [n][3], opacities [n], sigmas [n]

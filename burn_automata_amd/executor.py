@@ -17,6 +17,10 @@ from .model import NpaModel, NpaWeights
 from .runtime import Context, default_context, device_f32, ptr
 
 
+GAUSSIAN_SH_COEFF_COUNT = 48  # NPA_GAUSSIAN_SH_COEFF_COUNT (gpu_step.wgsl:6)
+_EXPORT_KEYS = ("position_visibility", "spherical_harmonic", "rotation", "scale_opacity")
+
+
 class HipAutomataState:
     def __init__(self, ctx: Context, handle, model: NpaModel, grid: HashGridConfig,
                  batch_size: int, particle_count: int):
@@ -144,16 +148,43 @@ class HipAutomataExecutor:
         return {"position_visibility": pv, "spherical_harmonic": sh, "rotation": rot,
                 "scale_opacity": so}
 
-    def raster_gaussians_3d(self, state: HipAutomataState, cfg: GaussianDecodeConfig, camera):
-        """decode_gaussians_3d of the current particles, then the EWA raster of them
-        (npa_state_raster_gaussians_3d): [height, width, 4]. The raster evaluates
-        cfg.sh_degree (oriented mode) or 0; camera.color_mode says how it reads the coefficients."""
+    def _gaussian_buffers(self, count: int):
+        import torch
+
+        dev = f"cuda:{self.ctx.device}"
+        return {"position_visibility": torch.empty((count, 4), dtype=torch.float32, device=dev),
+                "spherical_harmonic": torch.empty((count, GAUSSIAN_SH_COEFF_COUNT), dtype=torch.float32, device=dev),
+                "rotation": torch.empty((count, 4), dtype=torch.float32, device=dev),
+                "scale_opacity": torch.empty((count, 4), dtype=torch.float32, device=dev)}
+
+    def write_gaussians(self, state: HipAutomataState, buffers=None):
+        """write_state_into_gaussian_bind_group (crates/burn_automata/src/gpu/executor/steps.rs:71-108):
+        the viewer's planar Gaussian export of the current particles (write_gaussian_from_output,
+        gpu_step.wgsl:4963-5052) into `buffers` (new device tensors when None)."""
+        g = buffers or self._gaussian_buffers(state.total)
+        count = g["position_visibility"].shape[0]
+        self.ctx.check(lib().npa_state_write_gaussians(state.handle, count, *(ptr(g[k]) for k in _EXPORT_KEYS)))
+        return g
+
+    def step_state_into_gaussians(self, state: HipAutomataState, steps: int = 1, buffers=None):
+        """step_state_into_gaussians / step_state_many_into_gaussian_bind_group (steps.rs:111-257):
+        max(steps, 1) steps, then the export of the last step's particles. Returns the buffers."""
+        g = buffers or self._gaussian_buffers(state.total)
+        count = g["position_visibility"].shape[0]
+        self.ctx.check(lib().npa_state_step_into_gaussians(state.handle, int(steps), count,
+                                                           *(ptr(g[k]) for k in _EXPORT_KEYS)))
+        return g
+
+    def raster_gaussians_3d(self, state: HipAutomataState, cfg, camera):
+        """The EWA raster (npa_state_raster_gaussians_3d) of the current particles: [height, width, 4].
+        cfg None draws the viewer's export (48 SH coefficients at degree 3); a GaussianDecodeConfig
+        draws decode_gaussians_3d's colours as RGB. The call sets the camera's colour mode and degree."""
         import torch
 
         img = torch.empty((camera.height, camera.width, 4), dtype=torch.float32,
                           device=f"cuda:{self.ctx.device}")
-        self.ctx.check(lib().npa_state_raster_gaussians_3d(state.handle, C.byref(cfg.to_c()),
-                                                           C.byref(camera.to_c()), ptr(img)))
+        cfg_c = None if cfg is None else C.byref(cfg.to_c())
+        self.ctx.check(lib().npa_state_raster_gaussians_3d(state.handle, cfg_c, C.byref(camera.to_c()), ptr(img)))
         return img
 
     def pair_counts(self, state: HipAutomataState):

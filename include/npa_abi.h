@@ -373,9 +373,36 @@ npa_status npa_state_splat_2d_tiled(npa_state* state, const npa_splat2d_cfg* cfg
  * reference renders batch-1 traces only (validate_render_trace, attributes.rs:89-112). */
 npa_status npa_state_render_views(npa_state* state, const uint32_t* views, uint32_t nviews,
                                   const npa_render_cfg* cfg, float* images);
-/* decode_gaussians_3d of the current particles (the planar export the viewer reads,
- * cf. write_gaussian_main gpu_step.wgsl:4929-5052). */
+/* decode_gaussians_3d (gaussian.rs:53-100) of the current particles; the viewer's export is
+ * npa_state_write_gaussians. */
 npa_status npa_state_decode_gaussians_3d(npa_state* state, const npa_gaussian_decode_cfg* cfg,
+                                         float* position_visibility, float* spherical_harmonic,
+                                         float* rotation, float* scale_opacity);
+
+/* ------------------------------------------------------- viewer export */
+/* GAUSSIAN_SH_COEFF_COUNT (crates/burn_automata/src/gpu_step.wgsl:6): SH floats per Gaussian. */
+#define NPA_GAUSSIAN_SH_COEFF_COUNT 48
+/* Replaces write_state_into_gaussian_bind_group (crates/burn_automata/src/gpu/executor/steps.rs:71-108):
+ * the planar Gaussian export the viewer reads (WgpuGaussianBufferRefs, crates/burn_automata/src/gpu/types.rs:55-60),
+ * of the state's current particles, written by write_gaussian_from_output (gpu_step.wgsl:4963-5052):
+ *   position_visibility[i] = (x, y, z (0 in 2D), 1);
+ *   spherical_harmonic[i][48] = 0 except [0..3] = (clamp(tail + 0.5, 0, 1) - 0.5) / SH_C0, tail = the
+ *     last three state channels (SH_C0 = 0.28209479177387814);
+ *   rotation[i] = (1, 0, 0, 0) and scale_opacity[i].xyz = max(eps * 0.12, 8e-5); for 3D models with
+ *     position features and S >= 9, the unit quaternion (w, x, y, z) taking +z onto the normal in
+ *     channels 4..6 and a tangent-plane scale (t, t, max(0.18 t, 8e-5)),
+ *     t = max(clamp(0.32 eps clamp(sqrt(4096 / N), 0.4, 2), 0.08 eps, 0.64 eps), 8e-5);
+ *   scale_opacity[i].w = 1 in 2D, clamp(sigmoid(channel 8, or 3 when S <= 8), 0.001, 0.95) in 3D.
+ * count is the capacity of the four arrays in Gaussians ([count][4], [count][48]): it must be at
+ * least B*N (NPA_ERR_INVALID_ARGUMENT otherwise, as the reference); only the first B*N are written.
+ * The reference's material branch (adaptive rollouts) is not part of this path. Deterministic; bit
+ * for bit the oracle's restatement except the 3D opacity's exp (within 1e-6). */
+npa_status npa_state_write_gaussians(npa_state* state, uint32_t count, float* position_visibility,
+                                     float* spherical_harmonic, float* rotation, float* scale_opacity);
+/* Replaces step_state_into_gaussians / step_state_many_into_gaussian_bind_group
+ * (crates/burn_automata/src/gpu/executor/steps.rs:111-257): max(steps, 1) steps (as the reference,
+ * 0 runs one), then the export of npa_state_write_gaussians of the particles the last step wrote. */
+npa_status npa_state_step_into_gaussians(npa_state* state, uint32_t steps, uint32_t count,
                                          float* position_visibility, float* spherical_harmonic,
                                          float* rotation, float* scale_opacity);
 
@@ -420,9 +447,12 @@ npa_status npa_raster_gaussians_3d(npa_context* ctx, const float* position_visib
                                    const float* spherical_harmonic, const float* rotation,
                                    const float* scale_opacity, uint32_t count,
                                    const npa_raster_camera* camera, float* image);
-/* npa_state_decode_gaussians_3d of the current particles into library-held buffers, then
- * npa_raster_gaussians_3d of them with camera->sh_degree = cfg->sh_degree (oriented mode) or 0:
- * the frame the viewer draws from a device-resident state. */
+/* The frame of a device-resident state, drawn by npa_raster_gaussians_3d from library-held buffers.
+ * cfg NULL: the viewer's export (npa_state_write_gaussians) with its 48 SH coefficients, as
+ * NPA_RASTER_COLOR_SH at degree 3 - the frame the viewer draws. cfg set: decode_gaussians_3d of the
+ * current particles, whose coefficients are colours clamp(state + 0.5, 0, 1), read as
+ * NPA_RASTER_COLOR_RGB from coefficient 0. camera->sh_degree and camera->color_mode are set by the
+ * call in both cases. */
 npa_status npa_state_raster_gaussians_3d(npa_state* state, const npa_gaussian_decode_cfg* cfg,
                                          const npa_raster_camera* camera, float* image);
 

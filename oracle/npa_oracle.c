@@ -1188,6 +1188,96 @@ int oracle_decode_gaussians_3d(const float* positions, const float* states, uint
     return NPA_OK;
 }
 
+/* write_gaussian_from_output  crates/burn_automata/src/gpu_step.wgsl:4963-5052: the executor's
+ * planar export for the viewer (write_gaussian_main 4929-4936), per particle of a state's current
+ * buffers. SH colour write_gaussian_sh0_color 4981-4990 (48 coefficients, only the DC triple
+ * non-zero), geometry write_gaussian_geometry_from_output 4992-5052, channel helpers
+ * output_state_channel / output_tail_state_channel / output_material_opacity_logit 1565-1591,
+ * sigmoid 1561-1563. particle_count is the per-system N (params.rs:142). The material branch
+ * (material_gaussian_geometry) belongs to the adaptive rollouts and is not restated. normalize()
+ * is evaluated as v / sqrt(v.x^2 + v.y^2 + v.z^2 + v.w^2) and length() as sqrt(x^2 + y^2 + z^2),
+ * in that order. */
+#define ORACLE_SH_COEFFS 48u
+static const float ORACLE_SH_C0 = 0.28209479177387814f;
+
+static float export_channel(const float* s, uint32_t S, uint32_t c) { /* output_state_channel */
+    if (c < S) return s[c];
+    return S > 0 ? s[0] : 0.0f;
+}
+
+static float export_tail_channel(const float* s, uint32_t S, uint32_t off) { /* output_tail_state_channel */
+    return S > off ? export_channel(s, S, S - 1 - off) : export_channel(s, S, 0);
+}
+
+int oracle_write_gaussians(const float* positions, const float* states, uint64_t total, uint32_t particle_count,
+                           uint32_t S, uint32_t dim, float eps, int position_features, float* pos_vis, float* sh,
+                           float* rotation, float* scale_opacity) {
+    if (dim != 2 && dim != 3) return NPA_ERR_INVALID_DIM;
+    const int normal_branch = dim == 3 && position_features && S >= 9;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)total; ++i) {
+        const uint64_t idx = (uint64_t)i;
+        const float* p = positions + 4 * idx;
+        const float* s = states + idx * S;
+        float* pv = pos_vis + 4 * idx;
+        pv[0] = p[0];
+        pv[1] = p[1];
+        pv[2] = dim == 3 ? p[2] : 0.0f;
+        pv[3] = 1.0f;
+        const float tail[3] = {export_tail_channel(s, S, 2), export_tail_channel(s, S, 1),
+                               export_tail_channel(s, S, 0)};
+        float* c = sh + idx * ORACLE_SH_COEFFS;
+        for (uint32_t k = 0; k < ORACLE_SH_COEFFS; ++k) c[k] = 0.0f;
+        for (int ch = 0; ch < 3; ++ch) {
+            const float color = clamp_f32(tail[ch] + 0.5f, 0.0f, 1.0f);
+            c[ch] = (color - 0.5f) / ORACLE_SH_C0;
+        }
+        float scale[3], rot[4] = {1.0f, 0.0f, 0.0f, 0.0f};
+        const float iso = fmaxf(eps * 0.12f, 0.00008f);
+        scale[0] = scale[1] = scale[2] = iso;
+        if (normal_branch) {
+            const float n[3] = {export_channel(s, S, 4), export_channel(s, S, 5), export_channel(s, S, 6)};
+            const float nn = sqrtf(n[0] * n[0] + n[1] * n[1] + n[2] * n[2]);
+            float u[3] = {0.0f, 0.0f, 1.0f};
+            if (nn > 1.0e-6f && nn < 1.0e20f) {
+                u[0] = n[0] / nn;
+                u[1] = n[1] / nn;
+                u[2] = n[2] / nn;
+            }
+            if (u[2] <= -0.999999f) {
+                rot[0] = 0.0f;
+                rot[1] = 1.0f;
+                rot[2] = 0.0f;
+                rot[3] = 0.0f;
+            } else {
+                const float q[4] = {1.0f + u[2], -u[1], u[0], 0.0f};
+                const float ql = sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
+                for (int k = 0; k < 4; ++k) rot[k] = q[k] / ql;
+            }
+            const float density_scale =
+                clamp_f32(sqrtf(4096.0f / fmaxf((float)particle_count, 1.0f)), 0.4f, 2.0f);
+            const float tangent =
+                fmaxf(clamp_f32(eps * 0.32f * density_scale, eps * 0.08f, eps * 0.64f), 0.00008f);
+            scale[0] = tangent;
+            scale[1] = tangent;
+            scale[2] = fmaxf(tangent * 0.18f, 0.00008f);
+        }
+        float opacity = 1.0f;
+        if (dim == 3) {
+            const float logit = export_channel(s, S, S > 8 ? 8u : 3u);
+            opacity = clamp_f32(1.0f / (1.0f + expf(-logit)), 0.001f, 0.95f);
+        }
+        float* r = rotation + 4 * idx;
+        for (int k = 0; k < 4; ++k) r[k] = rot[k];
+        float* so = scale_opacity + 4 * idx;
+        so[0] = scale[0];
+        so[1] = scale[1];
+        so[2] = scale[2];
+        so[3] = opacity * 1.0f;
+    }
+    return NPA_OK;
+}
+
 /* splat_particles_2d  crates/burn_automata_kernels/src/splat.rs:30-93 */
 int oracle_splat_particles_2d(const float* positions, const float* colors, uint32_t count,
                               const npa_splat2d_cfg* cfg, float* image) {

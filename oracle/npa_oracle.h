@@ -25,6 +25,12 @@
  *   decode_gaussians_3d       - reference tests splat_and_gaussian_decode_are_shape_stable,
  *                               gaussian_decode_modes_cover_fixed_learned_and_oriented_scale
  *   splat_particles_2d        - closed-form single-particle Gaussian, additivity
+ *   write_gaussians           - the reference's export tests (tests/gpu_wgpu/gaussian.rs:243-310:
+ *                               position, visibility, identity rotation, positive scale, opacity
+ *                               range), SH DC decoding back to the clamped colour
+ *                               (SH_C0 * dc + 0.5), the normal branch's quaternion rotating +z onto
+ *                               the unit normal (and the antipodal case), tangent scale and
+ *                               opacity against float64 closed forms and scipy's expit
  *   view_basis / project_positions / splat_projected / render attributes
  *                             - orthonormal right-handed bases, axis views by coordinate
  *                               permutation, single-particle moments (total alpha = opacity,
@@ -131,6 +137,11 @@ int oracle_decode_gaussians_3d(const float* positions, const float* states, uint
                                float* position_visibility, float* spherical_harmonic,
                                float* rotation, float* scale_opacity);
 
+/* write_gaussian_from_output (gpu_step.wgsl:4963-5052): pos_vis [total][4], sh [total][48],
+ * rotation [total][4], scale_opacity [total][4]. */
+int oracle_write_gaussians(const float* positions, const float* states, uint64_t total, uint32_t particle_count,
+                           uint32_t S, uint32_t dim, float eps, int position_features, float* pos_vis, float* sh,
+                           float* rotation, float* scale_opacity);
 int oracle_splat_particles_2d(const float* positions, const float* colors, uint32_t count,
                               const npa_splat2d_cfg* cfg, float* image);
 

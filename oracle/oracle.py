@@ -91,6 +91,7 @@ def _declare(L):
     L.oracle_decode_gaussians_3d.argtypes = [P, P, u32, u32,
                                              C.POINTER(_abi.NpaGaussianDecodeCfg), P, P, P, P]
     L.oracle_splat_particles_2d.argtypes = [P, P, u32, C.POINTER(_abi.NpaSplat2dCfg), P]
+    L.oracle_write_gaussians.argtypes = [P, P, C.c_uint64, u32, u32, u32, f32, C.c_int, P, P, P, P]
     L.oracle_perceive_adjoint.argtypes = [P, P, u32, u32, u32, C.POINTER(_abi.NpaGridCfg),
                                           C.POINTER(_abi.NpaPerceptionOpts), P, P, P]
     L.oracle_view_basis.argtypes = [u32, P, P, P]
@@ -419,6 +420,30 @@ def decode_gaussians_3d(positions, states, state_dims, cfg: GaussianDecodeConfig
                                             _ptr(so)))
     return {"position_visibility": pv, "spherical_harmonic": sh, "rotation": rot,
             "scale_opacity": so}
+
+
+SH_COEFF_COUNT = 48  # GAUSSIAN_SH_COEFF_COUNT gpu_step.wgsl:6
+SH_C0 = np.float32(0.28209479177387814)  # gpu_step.wgsl:7
+
+
+def write_gaussians(positions, states, particle_count: int, model: NpaConfig, grid: HashGridConfig):
+    """write_gaussian_from_output (crates/burn_automata/src/gpu_step.wgsl:4963-5052): the planar
+    Gaussian export the executor writes for the viewer, for the particles of a state (any batch;
+    particle_count is the per-system N)."""
+    pos = _f32(positions, (-1, 4))
+    S = model.state_dims
+    st = _f32(states).reshape(-1)
+    n = pos.shape[0]
+    if st.size != n * S:
+        raise _abi.StateShape(f"state length {st.size} != {n * S}")
+    pv = np.zeros((n, 4), np.float32)
+    sh = np.zeros((n, SH_COEFF_COUNT), np.float32)
+    rot = np.zeros((n, 4), np.float32)
+    so = np.zeros((n, 4), np.float32)
+    _check(lib().oracle_write_gaussians(_ptr(pos), _ptr(st), n, particle_count, S, model.spatial_dims,
+                                        float(grid.eps), int(bool(model.position_features)), _ptr(pv),
+                                        _ptr(sh), _ptr(rot), _ptr(so)))
+    return {"position_visibility": pv, "spherical_harmonic": sh, "rotation": rot, "scale_opacity": so}
 
 
 def splat_particles_2d(positions, colors, cfg: Splat2dConfig) -> np.ndarray:

@@ -107,28 +107,69 @@ def test_raster_empty_and_culled(ctx):
     assert not to_np(img).any()
 
 
-@pytest.mark.parametrize("mode", [GaussianDecodeMode.GaussianSh0FixedScale, GaussianDecodeMode.GaussianSh0Oriented])
+@pytest.mark.parametrize("mode", [GaussianDecodeMode.GaussianSh0FixedScale, GaussianDecodeMode.GaussianSh0Oriented,
+                                  None])
 def test_state_raster_after_a_c4_rollout(ctx, mode):
-    """C4's 16,384 surface particles after 8 steps: the frame of the device-resident state (decode
-    then raster in one call) equals the oracle's raster of the device decode."""
+    """C4's 16,384 surface particles after 8 steps: the frame of the device-resident state (decode or
+    viewer export, then raster, in one call) equals the oracle's raster of the same Gaussians. A decode
+    config draws the decoded colours as RGB; no config draws the viewer's export (48 SH coefficients,
+    evaluated at degree 3)."""
     w = syn.workload("c4")
     ex = HipAutomataExecutor(ctx=ctx)
     state = ex.create_state(NpaModel(w["model"], w["weights"]), w["positions"], w["states"], 1, w["n"],
                             w["grid"], w["dt"], w["update_prob"], w["seed"])
     ex.step_state_many(state, 8)
-    dcfg = GaussianDecodeConfig(mode=mode)
-    dec = {k: to_np(v) for k, v in ex.decode_gaussians_3d(state, dcfg).items()}
+    if mode is None:
+        dcfg = None
+        gp, gs, _ = ex.read_state(state)
+        dec = O.write_gaussians(to_np(gp), to_np(gs), w["n"], w["model"], w["grid"])
+        dec["spherical_harmonic"] = dec["spherical_harmonic"].reshape(-1, 16, 3)
+        color, deg = RasterColor.SphericalHarmonics, 3
+    else:
+        dcfg = GaussianDecodeConfig(mode=mode)
+        dec = {k: to_np(v) for k, v in ex.decode_gaussians_3d(state, dcfg).items()}
+        color, deg = RasterColor.Rgb, 0
     p = dec["position_visibility"][:, :3]
     centre = p.mean(axis=0)
     ext = float(np.abs(p - centre).max())
     eye = tuple(centre + np.array([0.6, 0.9, 2.4]) * ext)
-    color = RasterColor.Rgb if mode == GaussianDecodeMode.GaussianSh0FixedScale else RasterColor.SphericalHarmonics
-    cam = RasterCamera.look_at(eye, tuple(centre), width=320, height=240, color_mode=color)
+    cam = RasterCamera.look_at(eye, tuple(centre), width=320, height=240)  # default colour mode
     got = ex.raster_gaussians_3d(state, dcfg, cam)
     want = O.raster_gaussians_3d(dec["position_visibility"], dec["spherical_harmonic"], dec["rotation"],
-                                 dec["scale_opacity"], cam)
-    _check(got, want, f"c4 state raster ({mode.name})")
+                                 dec["scale_opacity"], cam.replace(color_mode=color, sh_degree=deg))
+    _check(got, want, f"c4 state raster ({mode.name if mode else 'viewer export'})")
     assert float((want[..., 3] > 0.01).mean()) > 0.05  # the surface is in view
+    state.close()
+
+
+def test_state_raster_default_camera_keeps_the_decoded_colour(ctx):
+    """One opaque particle in front of a default camera (colour mode SH): the state raster draws its
+    decoded colour clamp(tail + 0.5), not 0.5 + SH_C0 * colour, both from the decode (RGB) and from
+    the viewer export (whose DC coefficient (c - 0.5) / SH_C0 evaluates back to c)."""
+    from burn_automata_amd.config import HashGridConfig, NpaConfig
+
+    m = NpaConfig.growing_3dgs().replace(state_dims=12, hidden_dims=8)
+    g = HashGridConfig.growing_3dgs()
+    rgb = np.array([0.35, -0.2, 0.1], f32)  # tail: colours 0.85, 0.3, 0.6
+    st = np.zeros((1, m.state_dims), f32)
+    st[0, -3:] = rgb
+    st[0, 8] = 8.0  # opacity logit: sigmoid(8) clamps to 0.95
+    pos = np.zeros((1, 4), f32)
+    weights = {k: np.zeros(v, f32) for k, v in (("w1", m.hidden_dims * m.perception_dims()),
+                                                ("b1", m.hidden_dims),
+                                                ("w2", m.update_dims() * m.hidden_dims),
+                                                ("b2", m.update_dims()))}
+    ex = HipAutomataExecutor(ctx=ctx)
+    state = ex.create_state(NpaModel(m, weights), pos, st, 1, 1, g, 1.0, 1.0, 0)
+    cam = RasterCamera.look_at((0.0, 0.0, 1.0), width=33, height=33)
+    assert cam.color_mode == RasterColor.SphericalHarmonics
+    want = np.clip(rgb + 0.5, 0, 1)
+    for dcfg in (GaussianDecodeConfig(mode=GaussianDecodeMode.GaussianSh0FixedScale, sigma=0.2, opacity_scale=0.95,
+                                      max_opacity=0.95), None):
+        img = to_np(ex.raster_gaussians_3d(state, dcfg, cam))
+        centre = img[16, 16]
+        assert centre[3] > 0.5
+        np.testing.assert_allclose(centre[:3] / centre[3], want, rtol=1e-5, atol=1e-6)
     state.close()
 
 

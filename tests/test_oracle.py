@@ -763,6 +763,105 @@ def test_learned_decode_closed_form():
 
 
 # --------------------------------------------------------------------------------------------
+# viewer export (write_gaussian_from_output, gpu_step.wgsl:4963-5052)
+# --------------------------------------------------------------------------------------------
+
+def _quat_rotate(q, v):
+    """Rotates v by the unit quaternion q = (w, x, y, z), in float64."""
+    w, x, y, z = (np.asarray(q, np.float64)[..., k] for k in range(4))
+    R = np.stack([np.stack([1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y)], -1),
+                  np.stack([2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x)], -1),
+                  np.stack([2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)], -1)], -2)
+    return np.einsum("...ij,...j->...i", R, np.asarray(v, np.float64))
+
+
+def test_export_buffer_contents_known_properties():
+    """wgpu_state_writes_gaussian_buffers_on_gpu (tests/gpu_wgpu/gaussian.rs:243-310) on a growing-3DGS
+    model: positions copied, visibility 1, identity rotation (no position features), finite positive
+    scale max(eps * 0.12, 8e-5), opacity clamp(sigmoid(channel 8), 0.001, 0.95); the 48 SH floats are
+    zero but for the DC triple, which decodes back (SH_C0 * dc + 0.5) to clamp(tail + 0.5, 0, 1) of
+    channels S-3, S-2, S-1 in that order."""
+    from scipy.special import expit
+    rng = np.random.default_rng(11)
+    m, g = NpaConfig.growing_3dgs(), HashGridConfig.growing_3dgs()
+    n, S = 64, m.state_dims
+    pos = rng.uniform(-1, 1, (n, 4)).astype(f32)
+    st = rng.normal(0, 1.5, (n, S)).astype(f32)
+    ex = O.write_gaussians(pos, st, n, m, g)
+    np.testing.assert_array_equal(ex["position_visibility"][:, :3], pos[:, :3])
+    assert np.all(ex["position_visibility"][:, 3] == 1.0)
+    assert np.all(ex["rotation"] == np.array([1, 0, 0, 0], f32))
+    assert np.all(ex["scale_opacity"][:, :3] == f32(max(f32(g.eps) * f32(0.12), f32(0.00008))))
+    np.testing.assert_allclose(ex["scale_opacity"][:, 3], np.clip(expit(st[:, 8].astype(np.float64)), 0.001, 0.95),
+                               rtol=1e-6)
+    sh = ex["spherical_harmonic"]
+    assert sh.shape == (n, 48) and not sh[:, 3:].any()
+    colour = np.clip(st[:, S - 3:].astype(np.float64) + 0.5, 0, 1)
+    np.testing.assert_allclose(sh[:, :3] * 0.28209479177387814 + 0.5, colour, atol=1e-6)
+    assert np.unique(np.round(colour, 3)).size > 20  # distinct tail channels: their order is pinned
+
+
+def test_export_2d_and_small_state_rules():
+    """2D: z written as 0, opacity 1, scale floor 8e-5 at tiny eps. Fewer than three state channels:
+    the missing tail channels read channel 0 (output_tail_state_channel gpu_step.wgsl:1577-1583). A 3D
+    state of at most 8 channels takes the opacity logit from channel 3 (1585-1591)."""
+    from scipy.special import expit
+    rng = np.random.default_rng(12)
+    n = 20
+    pos = rng.uniform(-1, 1, (n, 4)).astype(f32)
+    m2 = NpaConfig.growing_2d().replace(state_dims=5)
+    st = rng.normal(0, 1, (n, 5)).astype(f32)
+    for eps, want_scale in ((0.05, max(f32(0.05) * f32(0.12), f32(0.00008))), (1e-4, f32(0.00008))):
+        ex = O.write_gaussians(pos, st, n, m2, HashGridConfig.growing_2d().replace(eps=eps))
+        assert np.all(ex["position_visibility"][:, 2] == 0.0)
+        np.testing.assert_array_equal(ex["position_visibility"][:, :2], pos[:, :2])
+        assert np.all(ex["scale_opacity"][:, 3] == 1.0)
+        assert np.all(ex["scale_opacity"][:, :3] == f32(want_scale))
+    m1 = NpaConfig.growing_2d().replace(state_dims=1)
+    ex = O.write_gaussians(pos, st[:, :1], n, m1, HashGridConfig.growing_2d())
+    dc = ex["spherical_harmonic"][:, :3] * 0.28209479177387814 + 0.5
+    np.testing.assert_allclose(dc, np.repeat(np.clip(st[:, :1] + 0.5, 0, 1), 3, axis=1), atol=1e-6)
+    m3 = NpaConfig.growing_3dgs().replace(state_dims=8)
+    ex = O.write_gaussians(pos, st[:, :5].repeat(2, axis=1)[:, :8], n, m3, HashGridConfig.growing_3dgs())
+    logit = st[:, :5].repeat(2, axis=1)[:, 3].astype(np.float64)
+    np.testing.assert_allclose(ex["scale_opacity"][:, 3], np.clip(expit(logit), 0.001, 0.95), rtol=1e-6)
+
+
+def test_export_surface_normal_branch():
+    """3D models with position features and S >= 9 (gpu_step.wgsl:5000-5040): the quaternion takes +z
+    onto the unit normal of channels 4..6 (normal near -z: the half turn (0, 1, 0, 0); degenerate
+    normal: +z, identity); tangent t = max(clamp(0.32 eps clamp(sqrt(4096 / N), 0.4, 2), 0.08 eps,
+    0.64 eps), 8e-5) on x and y, max(0.18 t, 8e-5) on z. S = 8 keeps the isotropic branch."""
+    rng = np.random.default_rng(13)
+    m = NpaConfig.torus_field_3dgs().replace(state_dims=12)
+    g = HashGridConfig.growing_3dgs()
+    n = 200
+    pos = rng.uniform(-1, 1, (n, 4)).astype(f32)
+    st = rng.normal(0, 1, (n, 12)).astype(f32)
+    st[0, 4:7] = (0.0, 0.0, 0.0)          # degenerate: identity
+    st[1, 4:7] = (1e-4, -2e-4, -3.0)      # within 1e-6 of -z: half turn about x
+    st[2, 4:7] = (0.0, 0.0, 2.5)          # +z: identity
+    for N, scale in ((100, 2.0), (4096, 1.0), (16384, 0.5), (65536, 0.4)):
+        ex = O.write_gaussians(pos, st, N, m, g)
+        q = ex["rotation"].astype(np.float64)
+        np.testing.assert_allclose(np.linalg.norm(q, axis=1), 1.0, atol=1e-6)
+        nrm = st[3:, 4:7].astype(np.float64)
+        unit = nrm / np.linalg.norm(nrm, axis=1, keepdims=True)
+        np.testing.assert_allclose(_quat_rotate(q[3:], [0, 0, 1]), unit, atol=2e-6)
+        np.testing.assert_array_equal(ex["rotation"][0], np.array([1, 0, 0, 0], f32))
+        np.testing.assert_array_equal(ex["rotation"][1], np.array([0, 1, 0, 0], f32))
+        np.testing.assert_array_equal(ex["rotation"][2], np.array([1, 0, 0, 0], f32))
+        eps = float(np.float32(g.eps))
+        t = max(min(max(0.32 * eps * scale, 0.08 * eps), 0.64 * eps), 8e-5)
+        np.testing.assert_allclose(ex["scale_opacity"][:, 0], t, rtol=1e-6)
+        np.testing.assert_allclose(ex["scale_opacity"][:, 1], t, rtol=1e-6)
+        np.testing.assert_allclose(ex["scale_opacity"][:, 2], max(0.18 * t, 8e-5), rtol=1e-6)
+    ex8 = O.write_gaussians(pos, st[:, :8], 4096, m.replace(state_dims=8), g)
+    assert np.all(ex8["rotation"] == np.array([1, 0, 0, 0], f32))
+    assert np.all(ex8["scale_opacity"][:, :3] == f32(max(f32(g.eps) * f32(0.12), f32(0.00008))))
+
+
+# --------------------------------------------------------------------------------------------
 # splat
 # --------------------------------------------------------------------------------------------
 

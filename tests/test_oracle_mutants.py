@@ -96,6 +96,17 @@ MUTANTS = {
     "raster_sh3_term": ('kShC3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);', 'kShC3[3] * z * (2.0f * zz - 3.0f * xx - 2.0f * yy);'),
     "raster_sh_offset": ('        acc += 0.5f;\n        out[ch]', '        acc += 0.25f;\n        out[ch]'),
     "raster_view_dir_sign": ('float d[3] = {pv[0] - campos[0], pv[1] - campos[1], pv[2] - campos[2]};', 'float d[3] = {campos[0] - pv[0], campos[1] - pv[1], campos[2] - pv[2]};'),
+    "export_tail_order": ("export_tail_channel(s, S, 2), export_tail_channel(s, S, 1),\n                               export_tail_channel(s, S, 0)",
+                          "export_tail_channel(s, S, 0), export_tail_channel(s, S, 1),\n                               export_tail_channel(s, S, 2)"),
+    "export_sh_offset": ("c[ch] = (color - 0.5f) / ORACLE_SH_C0;", "c[ch] = color / ORACLE_SH_C0;"),
+    "export_iso_scale": ("fmaxf(eps * 0.12f, 0.00008f);", "fmaxf(eps * 0.1f, 0.00008f);"),
+    "export_quat_sign": ("const float q[4] = {1.0f + u[2], -u[1], u[0], 0.0f};",
+                         "const float q[4] = {1.0f + u[2], u[1], u[0], 0.0f};"),
+    "export_density_scale": ("sqrtf(4096.0f / fmaxf((float)particle_count, 1.0f))",
+                             "sqrtf(1024.0f / fmaxf((float)particle_count, 1.0f))"),
+    "export_tangent_z": ("scale[2] = fmaxf(tangent * 0.18f, 0.00008f);", "scale[2] = fmaxf(tangent * 0.5f, 0.00008f);"),
+    "export_opacity_channel": ("export_channel(s, S, S > 8 ? 8u : 3u);", "export_channel(s, S, S > 8 ? 7u : 3u);"),
+    "export_2d_z": ("pv[2] = dim == 3 ? p[2] : 0.0f;", "pv[2] = p[2];"),
     "raster_camera_centre": ('out[k] = -(V[k] * V[3] + V[4 + k] * V[7] + V[8 + k] * V[11]);', 'out[k] = -(V[4 * k] * V[3] + V[4 * k + 1] * V[7] + V[4 * k + 2] * V[11]);'),
 }
 
