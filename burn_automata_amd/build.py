@@ -14,10 +14,12 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libnpa_hip.so")
-SOURCES = ["npa_hashgrid.hip", "npa_perception.hip", "npa_adjoint.hip", "npa_decode.hip", "npa_sort.hip", "npa_abi.hip",
-           "npa_bpk.cpp"]
-# npa_perception.hip compiles as three objects (its NPA_PART selects which kernels each holds)
-PARTS = {"npa_perception.hip": ["-DNPA_PART=0", "-DNPA_PART=2", "-DNPA_PART=3"]}
+SOURCES = ["npa_hashgrid.hip", "npa_perception.hip", "npa_update.hip", "npa_adjoint.hip", "npa_decode.hip",
+           "npa_sort.hip", "npa_abi.hip", "npa_bpk.cpp"]
+# npa_perception.hip and npa_update.hip compile as three objects each (NPA_PART selects which
+# kernels each holds)
+PARTS = {"npa_perception.hip": ["-DNPA_PART=0", "-DNPA_PART=2", "-DNPA_PART=3"],
+         "npa_update.hip": ["-DNPA_PART=0", "-DNPA_PART=2", "-DNPA_PART=3"]}
 ARCH = os.environ.get("NPA_OFFLOAD_ARCH", "gfx950")
 
 

@@ -298,11 +298,24 @@ hipError_t launch_second_pass_2d(const StepParams& p, Workspace& ws, const StepI
                                  hipStream_t stream, Profiler* prof);
 hipError_t launch_second_pass_3d(const StepParams& p, Workspace& ws, const StepIO& io, int mode, int blocks,
                                  hipStream_t stream, Profiler* prof);
-// Padded weights for the MLP kernel: w1p [H][FP] (features at their padded positions),
-// b1 [H], w2t [H][D+SS] (transposed), b2p [D+SS]; zeros everywhere else.
+// Padded weights, two layouts one after the other in one buffer: the MLP kernel's w1t [FP][HP]
+// (features at their padded positions), b1p [HP], w2t [H][OP] (transposed), b2p [OP]; then, at
+// float offset valu_weight_floats(p), the fused update kernel's (fused_weight_floats(p)).
+// Zeros everywhere else.
 size_t padded_weight_floats(const StepParams& p);
+size_t valu_weight_floats(const StepParams& p);
+size_t fused_weight_floats(const StepParams& p);
 hipError_t launch_pad_weights(const StepParams& p, const float* w1, const float* b1, const float* w2,
                               const float* b2, float* wpad, hipStream_t stream);
+hipError_t launch_pad_weights_fused(const StepParams& p, const float* w1, const float* b1, const float* w2,
+                                    const float* b2, float* wf, hipStream_t stream);
+// The fused second pass + update MLP + Euler step (npa_update.hip) for 16-wide sorted rows,
+// H <= 128 and the VALU engine; wfused = the fused layout of the padded weights.
+bool fused_update_applies(const StepParams& p);
+hipError_t launch_update_fused_2d(const StepParams& p, Workspace& ws, const StepIO& io, const float* wfused,
+                                  hipStream_t stream, Profiler* prof);
+hipError_t launch_update_fused_3d(const StepParams& p, Workspace& ws, const StepIO& io, const float* wfused,
+                                  hipStream_t stream, Profiler* prof);
 hipError_t launch_mlp_forward(const StepParams& p, const float* features, uint32_t rows,
                               const StepIO& io, float* dx, float* ds, hipStream_t stream);
 hipError_t launch_euler(const StepParams& p, const float4* pos, const float* states,

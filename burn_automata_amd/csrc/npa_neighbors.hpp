@@ -1,0 +1,76 @@
+// npa_neighbors.hpp - neighbour-cell lookups shared by the neighbour passes (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "npa_internal.hpp"
+
+namespace npa {
+
+// A neighbour cell's run is walked in chunks of kNbChunk consecutive slots; the density pass
+// records one accept mask per chunk.
+constexpr int kNbChunk = 64;
+
+__device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+
+// Candidate slots of neighbour cell (n0, n1, n2) of system b: in Particle mode the cell's own run
+// of its split bin (no coordinate test needed) or, for an unsplit bin, the whole bin with
+// `filter` set; in Grid mode the cell's bin. False when the cell holds no particle.
+__device__ __forceinline__ bool cell_range(const StepParams& P, const uint32_t* __restrict__ bo, uint32_t b,
+                                           int64_t n0, int64_t n1, int64_t n2, uint32_t& beg, uint32_t& end,
+                                           bool& filter) {
+    uint32_t cell;
+    if (!cell_index(n0, n1, n2, P.g, &cell)) return false;
+    const uint64_t bin = (uint64_t)b * P.g.cells + cell;
+    filter = false;
+    if (P.g.mode != 1) {
+        beg = bo[bin];
+        end = bo[bin + 1];
+        return beg < end;
+    }
+    const uint32_t nd = P.dir_n[bin];
+    if (nd == 0) return false;
+    if (nd > kDirGroups) {
+        beg = bo[bin];
+        end = bo[bin + 1];
+        filter = true;
+        return true;
+    }
+    // every directory entry of the bin is loaded at once (no load waits on another)
+    const int4* e = P.dir_e + bin * kDirGroups;
+    int4 ek[kDirGroups];
+#pragma unroll
+    for (uint32_t k = 0; k < kDirGroups; ++k) ek[k] = k < nd ? e[k] : make_int4(0, 0, 0, 0);
+    const uint32_t last = bo[bin + 1];
+    bool found = false;
+#pragma unroll
+    for (uint32_t k = 0; k < kDirGroups; ++k) {
+        const bool hit = !found && k < nd && (int64_t)ek[k].x == n0 && (int64_t)ek[k].y == n1 &&
+                         (int64_t)ek[k].z == n2;
+        if (hit) {
+            beg = (uint32_t)ek[k].w;
+            end = k + 1 < nd ? (uint32_t)ek[k + 1 < kDirGroups ? k + 1 : k].w : last;
+            found = true;
+        }
+    }
+    return found;
+}
+
+// The candidate runs of the 3^D neighbour cells of cell (c0, c1, c2) of system b, looked up in
+// parallel: lane k < 3^D takes neighbour k in the reference's visit order (k = (dz+1)*9 +
+// (dy+1)*3 + (dx+1): dz, then dy, then dx). found: the cell holds particles.
+template <int D>
+__device__ __forceinline__ void neighbor_runs(const StepParams& P, const uint32_t* __restrict__ bo, uint32_t b,
+                                              int c0, int c1, int c2, uint32_t lane, uint32_t& beg, uint32_t& end,
+                                              bool& filter, bool& found) {
+    constexpr uint32_t NC = D == 3 ? 27 : 9;
+    beg = end = 0;
+    filter = false;
+    found = false;
+    if (lane >= NC) return;
+    const int dx = (int)(lane % 3) - 1, dy = (int)((lane / 3) % 3) - 1, dz = D == 3 ? (int)(lane / 9) - 1 : 0;
+    found = cell_range(P, bo, b, (int64_t)c0 + dx, (int64_t)c1 + dy, (int64_t)c2 + dz, beg, end, filter);
+}
+
+}  // namespace npa

@@ -19,6 +19,7 @@
 #include <type_traits>
 
 #include "npa_internal.hpp"
+#include "npa_neighbors.hpp"
 
 // The build compiles this file once per part so the kernel instantiations compile in parallel:
 // NPA_PART 0 holds the non-template kernels and the host launchers, 2 and 3 the second-pass and
@@ -52,68 +53,7 @@ namespace npa {
 // target, candidates are visited in cell order (dz, dy, dx) and ascending slot order - ascending
 // particle index within the cell, the reference's for_each_neighbor order - so every per-target
 // sum is unchanged.
-constexpr int kChunk = 64;
-
-__device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
-
-// Candidate slots of neighbour cell (n0, n1, n2) of system b: in Particle mode the cell's own run
-// of its split bin (no coordinate test needed) or, for an unsplit bin, the whole bin with
-// `filter` set; in Grid mode the cell's bin. False when the cell holds no particle.
-__device__ __forceinline__ bool cell_range(const StepParams& P, const uint32_t* __restrict__ bo, uint32_t b,
-                                           int64_t n0, int64_t n1, int64_t n2, uint32_t& beg, uint32_t& end,
-                                           bool& filter) {
-    uint32_t cell;
-    if (!cell_index(n0, n1, n2, P.g, &cell)) return false;
-    const uint64_t bin = (uint64_t)b * P.g.cells + cell;
-    filter = false;
-    if (P.g.mode != 1) {
-        beg = bo[bin];
-        end = bo[bin + 1];
-        return beg < end;
-    }
-    const uint32_t nd = P.dir_n[bin];
-    if (nd == 0) return false;
-    if (nd > kDirGroups) {
-        beg = bo[bin];
-        end = bo[bin + 1];
-        filter = true;
-        return true;
-    }
-    // every directory entry of the bin is loaded at once (no load waits on another)
-    const int4* e = P.dir_e + bin * kDirGroups;
-    int4 ek[kDirGroups];
-#pragma unroll
-    for (uint32_t k = 0; k < kDirGroups; ++k) ek[k] = k < nd ? e[k] : make_int4(0, 0, 0, 0);
-    const uint32_t last = bo[bin + 1];
-    bool found = false;
-#pragma unroll
-    for (uint32_t k = 0; k < kDirGroups; ++k) {
-        const bool hit = !found && k < nd && (int64_t)ek[k].x == n0 && (int64_t)ek[k].y == n1 &&
-                         (int64_t)ek[k].z == n2;
-        if (hit) {
-            beg = (uint32_t)ek[k].w;
-            end = k + 1 < nd ? (uint32_t)ek[k + 1 < kDirGroups ? k + 1 : k].w : last;
-            found = true;
-        }
-    }
-    return found;
-}
-
-// The candidate runs of the 3^D neighbour cells of cell (c0, c1, c2) of system b, looked up in
-// parallel: lane k < 3^D takes neighbour k in the reference's visit order (k = (dz+1)*9 +
-// (dy+1)*3 + (dx+1): dz, then dy, then dx). found: the cell holds particles.
-template <int D>
-__device__ __forceinline__ void neighbor_runs(const StepParams& P, const uint32_t* __restrict__ bo, uint32_t b,
-                                              int c0, int c1, int c2, uint32_t lane, uint32_t& beg, uint32_t& end,
-                                              bool& filter, bool& found) {
-    constexpr uint32_t NC = D == 3 ? 27 : 9;
-    beg = end = 0;
-    filter = false;
-    found = false;
-    if (lane >= NC) return;
-    const int dx = (int)(lane % 3) - 1, dy = (int)((lane / 3) % 3) - 1, dz = D == 3 ? (int)(lane / 9) - 1 : 0;
-    found = cell_range(P, bo, b, (int64_t)c0 + dx, (int64_t)c1 + dy, (int64_t)c2 + dz, beg, end, filter);
-}
+constexpr int kChunk = kNbChunk;
 
 // Lanes per target for a sorted-state row width SM (each lane owns SM / L state channels).
 template <int SM>
@@ -848,12 +788,13 @@ __global__ __launch_bounds__(256) void k_pad_weights(StepParams P, int D, const 
             int64_t fi = -1;
             if (q < SS) fi = q < S ? (int64_t)q : -1;
             else if (q < 2 * SS) fi = q - SS < S ? (int64_t)(S + q - SS) : -1;
-            else if (q < 2 * SS + SS * D) {
+            else if (q < 2 * SS + SS * D) {  // gradient features exist only with the state gradient
                 const uint32_t g = q - 2 * SS;
-                fi = g < S * D ? (int64_t)(2 * S + g) : -1;
+                fi = P.state_grad && g < S * D ? (int64_t)(2 * S + g) : -1;
             } else {
                 const uint32_t r = q - (2 * SS + SS * D);
-                fi = 2 * S + S * D + r < F ? (int64_t)(2 * S + S * D + r) : -1;
+                const uint32_t first = 2 * S + (P.state_grad ? S * D : 0);
+                fi = first + r < F ? (int64_t)(first + r) : -1;
             }
             if (fi >= 0 && h < H) v = w1[(uint64_t)h * F + fi];
         } else if (k < n1 + HP) {
@@ -1352,19 +1293,27 @@ static hipError_t launch_perceive_d(const StepParams& p, Workspace& ws, const St
 }
 
 #if NPA_PART_MAIN
-size_t padded_weight_floats(const StepParams& p) {
+size_t valu_weight_floats(const StepParams& p) {
     const uint32_t D = (uint32_t)p.g.dim;
     const size_t HP = (p.H + 127) / 128 * 128;
     const size_t OP = (D + p.SS + 3) / 4 * 4;
-    return (size_t)p.FP * HP + HP + (size_t)p.H * OP + OP;
+    return ((size_t)p.FP * HP + HP + (size_t)p.H * OP + OP + 3) / 4 * 4;  // the fused layout stays 16-byte aligned
+}
+
+size_t padded_weight_floats(const StepParams& p) { return valu_weight_floats(p) + fused_weight_floats(p); }
+
+bool fused_update_applies(const StepParams& p) {
+    return p.SS == 16 && p.H <= 128 && p.mlp_engine == NPA_MLP_VALU && (uint64_t)p.T * 64 < (1ull << 32);
 }
 
 hipError_t launch_pad_weights(const StepParams& p, const float* w1, const float* b1, const float* w2,
                               const float* b2, float* wpad, hipStream_t stream) {
-    const size_t n = padded_weight_floats(p);
+    const size_t n = valu_weight_floats(p);
     const uint32_t blocks = (uint32_t)std::min<size_t>((n + 255) / 256, 1024);
     hipLaunchKernelGGL(k_pad_weights, dim3(blocks), dim3(256), 0, stream, p, p.g.dim, w1, b1, w2, b2, wpad);
-    return hipGetLastError();
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_pad_weights_fused(p, w1, b1, w2, b2, wpad + n, stream);
 }
 
 #endif  // NPA_PART_MAIN
@@ -1419,10 +1368,16 @@ static hipError_t launch_mlp_d(const StepParams& p, Workspace& ws, const StepIO&
     }
 }
 
-// Second pass, then (mode 0) the update MLP, for one dimension.
+// Second pass, then (mode 0) the update MLP, for one dimension; the rollout step's usual shape
+// (16-wide rows, H <= 128, VALU engine) runs both in the fused kernel.
 template <int D>
 static hipError_t launch_second_pass(const StepParams& p, Workspace& ws, const StepIO& io, int mode, int blocks,
                                      hipStream_t stream, Profiler* prof) {
+    if (mode == 0 && fused_update_applies(p)) {
+        const float* wfused = ws.wpad.as<float>() + valu_weight_floats(p);
+        return D == 2 ? launch_update_fused_2d(p, ws, io, wfused, stream, prof)
+                      : launch_update_fused_3d(p, ws, io, wfused, stream, prof);
+    }
     const hipError_t e = mode == 0 ? launch_perceive_d<D, 0>(p, ws, io, blocks, stream, prof)
                                    : launch_perceive_d<D, 1>(p, ws, io, blocks, stream, prof);
     if (e != hipSuccess || mode != 0) return e;

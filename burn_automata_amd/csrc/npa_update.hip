@@ -1,0 +1,707 @@
+// npa_update.hip - the rollout step's second neighbour pass, update MLP and masked Euler step in
+// one kernel, for sorted state rows of 16 channels (9 to 16 state channels) and H <= 128.
+//
+//   second pass   forward.rs:162-382 (blur_state, compute_state_gradient, moment_matrix,
+//                 second_pass_particle), moment correction / scaling / log-norm normalize.rs:5-118,
+//                 feature row forward.rs:100-133
+//   update MLP    model.rs:900-940, motion scaling model.rs:867-898, 3D gates model.rs:806-837
+//   Euler step    step.rs:4-55, written to the ping-pong output in original particle order
+//
+// Mapping. Sixteen lanes serve one target, lane c owning state channel c; a wave serves the four
+// targets of one item (four consecutive compact rows); a block takes a contiguous range of items.
+// The 16 waves of a block share the padded MLP weights in LDS.
+//
+// Per target, the accepted neighbours are appended to an LDS list in visit order (cells dz, dy, dx,
+// slots ascending: the reference's for_each_neighbor order) from the density pass's per-chunk
+// accept masks, or, for a target with more chunks than were recorded, by testing the candidates
+// here. The list is consumed in rounds of 16 entries: lane c computes the pair scalars of entry c
+// (poly6, volume, spiky gradient, moment terms) once and stages them in LDS; every lane then adds
+// the round's 16 entries in list order to its own channel, reading the entry's scalars back with
+// one broadcast load and the neighbour's channel from the sorted state rows. The per-target sums
+// that are not per channel (moment matrix, density gradient) are summed by lane k for component k
+// from a component-major copy of the round's terms. Padding entries (a short last round) use the
+// target itself with zero weights. Every sum therefore adds the reference's terms in the reference's
+// order, with the same roundings, and +0.0 terms that change nothing (each sum starts at +0.0).
+//
+// After the walk the feature row (state, blur, gradient, density gradient, position) is staged in
+// LDS; lane j of a target computes hidden units j, j + 16, ..., j + 112 (bias first, then features
+// in index order), the hidden activations go back to LDS, and lane c sums output D + c (its state
+// channel's update) and, for c < D, motion output c, hidden units in index order. Lane 0 writes the
+// position, every lane its state channel.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "npa_internal.hpp"
+#include "npa_neighbors.hpp"
+
+#ifndef NPA_PART
+#define NPA_PART -1
+#endif
+#define NPA_PART_MAIN (NPA_PART < 0 || NPA_PART == 0)
+#define NPA_PART_DIM2 (NPA_PART < 0 || NPA_PART == 2)
+#define NPA_PART_DIM3 (NPA_PART < 0 || NPA_PART == 3)
+
+namespace npa {
+
+constexpr int kFuseWaves = 16;          // waves per block (one block per CU)
+constexpr uint32_t kFuseHidden = 128;   // hidden units held per target (H <= 128, zero padded)
+constexpr uint32_t kFuseLdsBytes = 163840;
+
+// Per-variant shapes. FL: option flags fixed at compile time (bit 0 state gradient, bit 1 density
+// gradient, bit 2 moment correction; 5 = the rollout's usual set) or -1 (read from the params).
+template <int D, int FL>
+struct FuseShape {
+    static constexpr int NMOM = D * (D + 1) / 2;            // moment matrix, upper triangle
+    static constexpr int SREC = FL == 5 ? 4 : 8;           // floats staged per entry
+    static constexpr int NX = FL == 5 ? NMOM : NMOM + D;   // per-target sums over entries
+    static constexpr int CAP = D == 2 ? (FL == 5 ? 256 : 160) : (FL == 5 ? 128 : 64);  // list entries
+    static constexpr int OPAD = (D + 16 + 3) / 4 * 4;      // padded update outputs
+    // Per wave, one block per target group g: lists [CAP] u32, entry records [16][SREC], the sums'
+    // terms [NX][XSTR]. Every per-group block (and each term row) is padded by 4 floats so that the
+    // four groups' broadcast reads of the same offset fall in different LDS banks. After the walk
+    // the same region holds the feature rows [4][FP + 4] and hidden activations [4][132].
+    static constexpr int LSTR = CAP + 4;
+    static constexpr int SSTR = 16 * SREC + 4;
+    static constexpr int XSTR = 20;
+    static constexpr int XGSTR = NX * XSTR + 4;
+    static constexpr int HSTR = 128 + 4;
+    static constexpr int WAVE_FLOATS = 4 * LSTR + 4 * SSTR + 4 * XGSTR;
+    static_assert(4 * (88 + 4 + HSTR) <= WAVE_FLOATS, "feature and hidden rows fit the wave's region");
+};
+
+// Floats of the fused MLP's padded weights: w1q [FP/4][128][4], b1 [128], w2q [32][OPAD][4], b2 [OPAD].
+__host__ __device__ inline size_t fused_weight_floats(uint32_t FP, int dim) {
+    const size_t opad = (size_t)(dim + 16 + 3) / 4 * 4;
+    return (size_t)FP * kFuseHidden + kFuseHidden + kFuseHidden * opad + opad;
+}
+
+// Padded feature position q (16-wide rows) -> the model's feature index, or -1 for padding:
+// [state 16][blur 16][gradient 16 x D][density gradient D?, position D?, zeros].
+__device__ __forceinline__ int fused_feature_index(uint32_t q, const StepParams& P, int D) {
+    const uint32_t S = P.S;
+    if (q < 16) return q < S ? (int)q : -1;
+    if (q < 32) return q - 16 < S ? (int)(S + q - 16) : -1;
+    if (q < 32 + 16 * (uint32_t)D) {
+        const uint32_t c = (q - 32) / D, a = (q - 32) % D;
+        return P.state_grad && c < S ? (int)(2 * S + c * D + a) : -1;
+    }
+    const uint32_t r = q - (32 + 16 * D);
+    const uint32_t nrest = (P.density_grad ? D : 0) + (P.position_features ? D : 0);
+    return r < nrest ? (int)(2 * S + (P.state_grad ? S * D : 0) + r) : -1;
+}
+
+#if NPA_PART_MAIN
+__global__ __launch_bounds__(256) void k_pad_weights_fused(StepParams P, int D, const float* __restrict__ w1,
+                                                           const float* __restrict__ b1,
+                                                           const float* __restrict__ w2,
+                                                           const float* __restrict__ b2, float* __restrict__ wf) {
+    const uint32_t H = P.H, F = P.F, FP = P.FP, O = D + P.S;
+    const uint32_t HP = kFuseHidden, OPAD = (D + 16 + 3) / 4 * 4;
+    const uint64_t n1 = (uint64_t)FP * HP, n2 = (uint64_t)HP * OPAD;
+    const uint64_t total = n1 + HP + n2 + OPAD;
+    for (uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; k < total; k += (uint64_t)gridDim.x * blockDim.x) {
+        float v = 0.0f;
+        if (k < n1) {  // ((kb * HP + h) * 4 + i): feature 4 kb + i of hidden unit h
+            const uint32_t i = (uint32_t)(k & 3), h = (uint32_t)((k >> 2) % HP), kb = (uint32_t)((k >> 2) / HP);
+            const int fi = fused_feature_index(4 * kb + i, P, D);
+            if (fi >= 0 && (uint32_t)fi < F && h < H) v = w1[(uint64_t)h * F + fi];
+        } else if (k < n1 + HP) {
+            const uint32_t h = (uint32_t)(k - n1);
+            if (h < H) v = b1[h];
+        } else if (k < n1 + HP + n2) {  // ((hb * OPAD + o) * 4 + i): hidden unit 4 hb + i of output o
+            const uint64_t t = k - n1 - HP;
+            const uint32_t i = (uint32_t)(t & 3), o = (uint32_t)((t >> 2) % OPAD), hb = (uint32_t)((t >> 2) / OPAD);
+            const uint32_t h = 4 * hb + i;
+            if (o < O && h < H) v = w2[(uint64_t)o * H + h];
+        } else {
+            const uint32_t o = (uint32_t)(k - n1 - HP - n2);
+            if (o < O) v = b2[o];
+        }
+        wf[k] = v;
+    }
+}
+
+hipError_t launch_pad_weights_fused(const StepParams& p, const float* w1, const float* b1, const float* w2,
+                                    const float* b2, float* wf, hipStream_t stream) {
+    const size_t n = fused_weight_floats(p.FP, p.g.dim);
+    const uint32_t blocks = (uint32_t)std::min<size_t>((n + 255) / 256, 1024);
+    hipLaunchKernelGGL(k_pad_weights_fused, dim3(blocks), dim3(256), 0, stream, p, p.g.dim, w1, b1, w2, b2, wf);
+    return hipGetLastError();
+}
+
+size_t fused_weight_floats(const StepParams& p) { return fused_weight_floats(p.FP, p.g.dim); }
+#endif  // NPA_PART_MAIN
+
+// Makes the wave's LDS writes visible to its other lanes before they read (a wave's LDS operations
+// are performed in order; the barrier keeps the compiler from moving them across).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Value of `v` in lane (lane & ~15) + k: the same target's lane k.
+__device__ __forceinline__ float group_lane(float v, uint32_t lane, uint32_t k) {
+    return __shfl(v, (int)((lane & 48u) | k));
+}
+
+// Row-wise (16-lane) scans: row_shr:n reads lane i - n of the same row, 0 for the first n lanes.
+template <int N>
+__device__ __forceinline__ uint32_t row_shr(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x110 + N, 0xf, 0xf, false);
+}
+__device__ __forceinline__ uint32_t row_incl_sum(uint32_t v) {
+    v += row_shr<1>(v);
+    v += row_shr<2>(v);
+    v += row_shr<4>(v);
+    v += row_shr<8>(v);
+    return v;
+}
+__device__ __forceinline__ uint32_t row_incl_max(uint32_t v) {
+    v = max(v, row_shr<1>(v));
+    v = max(v, row_shr<2>(v));
+    v = max(v, row_shr<4>(v));
+    v = max(v, row_shr<8>(v));
+    return v;
+}
+// The row's last lane's value in every lane of the row (DPP row_newbcast:15).
+__device__ __forceinline__ uint32_t row_last(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x150 + 15, 0xf, 0xf, false);
+}
+
+template <int D, int FL>
+__global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float4* __restrict__ srec,
+                                                       const int4* __restrict__ scoord,
+                                                       const float* __restrict__ sstate,
+                                                       const float4* __restrict__ svol,
+                                                       const uint32_t* __restrict__ bo,
+                                                       const uint32_t* __restrict__ perm,
+                                                       const uint32_t* __restrict__ act_rows,
+                                                       const uint32_t* __restrict__ row_count,
+                                                       const uint4* __restrict__ nb_chunks,
+                                                       const uint32_t* __restrict__ nb_count,
+                                                       const float* __restrict__ wfused, StepIO io) {
+    using Sh = FuseShape<D, FL>;
+    constexpr uint32_t CAP = Sh::CAP, SREC = Sh::SREC, NX = Sh::NX, NMOM = Sh::NMOM, OPAD = Sh::OPAD;
+    constexpr uint32_t HP = kFuseHidden;
+    constexpr uint32_t MAXC = max_chunks(D);
+    extern __shared__ float lds[];
+    const uint32_t FP = P.FP;
+    const uint32_t wfloats = (uint32_t)fused_weight_floats(FP, D);
+
+    // the block's copy of the padded weights
+    for (uint32_t v = threadIdx.x; v < wfloats / 4; v += blockDim.x)
+        reinterpret_cast<float4*>(lds)[v] = reinterpret_cast<const float4*>(wfused)[v];
+    __syncthreads();
+    const float* w1q = lds;
+    const float* b1 = w1q + (size_t)FP * HP;
+    const float* w2q = b1 + HP;
+    const float* b2 = w2q + (size_t)HP * OPAD;
+
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t g = lane >> 4, c = lane & 15;
+    float* wl = lds + wfloats + (size_t)wave * Sh::WAVE_FLOATS;
+    uint32_t* mylist = reinterpret_cast<uint32_t*>(wl) + g * Sh::LSTR;
+    float* stage = wl + 4 * Sh::LSTR + g * Sh::SSTR;       // this group's entry records
+    float* ext = wl + 4 * Sh::LSTR + 4 * Sh::SSTR + g * Sh::XGSTR;  // this group's sums' terms
+    float* fg = wl + g * (FP + 4);                          // feature row (after the walk)
+    float* hg = wl + 4 * (FP + 4) + g * Sh::HSTR;           // hidden activations
+
+    const bool want_sg = FL >= 0 ? (FL & 1) != 0 : P.state_grad != 0;
+    const bool want_dg = FL >= 0 ? (FL & 2) != 0 : P.density_grad != 0;
+    const bool want_m = FL >= 0 ? (FL & 5) == 5 : (want_sg && P.hybrid);
+    const bool branch_a = want_sg && want_dg;
+    const uint32_t nrows = *row_count;
+    const uint32_t nitems = (nrows + 3) / 4;
+    const uint32_t xcomp = c < NX ? c : 0u;  // the per-target sum this lane keeps
+
+    // Items of four consecutive compact rows: block k takes a contiguous range, its waves
+    // interleaved (neighbouring rows share cells, so the CU's L1 serves their neighbours).
+    const uint32_t per_block = (nitems + gridDim.x - 1) / gridDim.x;
+    const uint32_t item_end = min(nitems, (blockIdx.x + 1) * per_block);
+    auto slot_of = [&](uint32_t it) {
+        const uint32_t r = it * 4 + g;
+        return act_rows[r < nrows ? r : it * 4];
+    };
+    uint32_t item = blockIdx.x * per_block + wave;
+    uint32_t s_next = item < item_end ? slot_of(item) : 0u;  // the next item's slot, loaded one item ahead
+    for (; item < item_end; item += kFuseWaves) {
+        const uint32_t row = item * 4 + g;
+        const bool active = row < nrows;
+        const uint32_t s = s_next;
+        // everything that depends only on the slot is issued together
+        float pi[3];
+        int ci[3];
+        load_rec<D>(srec, scoord, s, pi, ci);
+        const float si = sstate[(uint64_t)s * 16 + c];
+        const uint32_t nct = active ? nb_count[s] : 0u;
+        const uint4 rb0 = nb_chunks[(uint64_t)c * P.T + s];  // the first 16 chunk records (16 <= max_chunks)
+        const uint32_t li = perm[s];
+        if (item + kFuseWaves < item_end) s_next = slot_of(item + kFuseWaves);
+        const uint32_t b = s / P.N;
+        const uint32_t i = b * P.N + li;
+        const float4 pos4 = io.pos[i];
+        float blur = 0.0f, gr[3] = {0.0f, 0.0f, 0.0f}, xacc = 0.0f;
+        uint32_t cnt = 0;  // entries in this target's list
+
+        // ---- Phase B: the lists in rounds of 16 entries. sv[e] holds the neighbour channel of entry
+        // e of the current round; right after it is used, the same entry of the next round is loaded
+        // into it, so every load has about one round to arrive.
+        auto load_sv = [&](uint32_t slot) {
+            return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(sstate) + ((slot << 6) | (c << 2)));
+        };
+        auto process = [&]() {
+            if (!__ballot(cnt > 0u)) return;
+            const uint32_t padded = cnt == 0 ? 16u : (cnt + 15u) & ~15u;
+            if (cnt + c < padded) mylist[cnt + c] = s;  // whole rounds; padding entries are the target
+            const uint32_t nrg = padded / 16;           // a target with fewer rounds re-reads its last
+            uint32_t nr = (uint32_t)__builtin_amdgcn_readlane((int)nrg, 0);
+            nr = max(nr, (uint32_t)__builtin_amdgcn_readlane((int)nrg, 16));
+            nr = max(nr, (uint32_t)__builtin_amdgcn_readlane((int)nrg, 32));
+            nr = max(nr, (uint32_t)__builtin_amdgcn_readlane((int)nrg, 48));
+            wave_sync();
+            float sv[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 v = reinterpret_cast<const uint4*>(mylist)[q];
+                sv[4 * q] = load_sv(v.x);
+                sv[4 * q + 1] = load_sv(v.y);
+                sv[4 * q + 2] = load_sv(v.z);
+                sv[4 * q + 3] = load_sv(v.w);
+            }
+            uint32_t en = mylist[c];
+            float4 rj = svol[en];
+            for (uint32_t r = 0; r < nr; ++r) {
+                const uint32_t rn = r + 1 < nrg ? r + 1 : nrg - 1;  // next round (always a valid entry)
+                const uint32_t* lpn = mylist + 16 * rn;
+                // this lane's entry: pair scalars, branch-free; a padding entry gets zero weights
+                const bool has = active && 16 * r + c < cnt;
+                float d[3];
+                d[0] = delta_axis(pi[0], rj.x, 0, P.g);
+                d[1] = delta_axis(pi[1], rj.y, 1, P.g);
+                d[2] = 0.0f;
+                float r2 = d[0] * d[0];
+                r2 += d[1] * d[1];
+                if constexpr (D == 3) {
+                    d[2] = delta_axis(pi[2], rj.z, 2, P.g);
+                    r2 += d[2] * d[2];
+                }
+                const float smooth = has ? poly6(r2, P.g) : 0.0f;
+                const float vol = has ? rj.w : 0.0f;
+                const bool gok = has && en != s && r2 > 0.0f;  // spiky_gradient_kernel kernels.rs:79-96
+                const float rr = sqrtf(r2);
+                const float tt = P.g.eps - rr;
+                float vg[3] = {0.0f, 0.0f, 0.0f}, dgv[3] = {0.0f, 0.0f, 0.0f};
+                if (want_dg) {
+                    const float mag = 1.0f * P.g.k5 * 3.0f * (tt * tt) / rr;
+#pragma unroll
+                    for (int a = 0; a < D; ++a) dgv[a] = gok ? mag * d[a] : 0.0f;
+                }
+                if (want_sg) {
+                    const float mag = rj.w * P.g.k5 * 3.0f * (tt * tt) / rr;
+#pragma unroll
+                    for (int a = 0; a < D; ++a) vg[a] = gok ? mag * d[a] : 0.0f;
+                }
+                const float w = smooth * vol;  // blur_state weight (density-grad-off branch)
+                float* my = stage + c * SREC;
+                if constexpr (SREC == 4) {
+                    *reinterpret_cast<float4*>(my) = make_float4(w, vg[0], vg[1], vg[2]);
+                } else {
+                    *reinterpret_cast<float4*>(my) = make_float4(branch_a ? smooth : w, vol, vg[0], vg[1]);
+                    *reinterpret_cast<float4*>(my + 4) = make_float4(vg[2], 0.0f, 0.0f, 0.0f);
+                }
+                float* xe = ext + c;
+                {
+                    uint32_t k = 0;  // moment terms delta[ra] * grad[ca], upper triangle
+#pragma unroll
+                    for (int ra = 0; ra < D; ++ra)
+#pragma unroll
+                        for (int ca = ra; ca < D; ++ca) xe[Sh::XSTR * k++] = d[ra] * vg[ca];
+                    if constexpr (NX > NMOM) {
+#pragma unroll
+                        for (int a = 0; a < D; ++a) xe[Sh::XSTR * (NMOM + a)] = dgv[a];
+                    }
+                }
+                en = lpn[c];
+                rj = svol[en];  // the next round's entry
+                wave_sync();
+                // the round's entries in list order
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint4 nx = reinterpret_cast<const uint4*>(lpn)[q];
+                    const uint32_t nslot[4] = {nx.x, nx.y, nx.z, nx.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int e = 4 * q + i;
+                        const float* re = stage + e * SREC;
+                        const float4 r0 = *reinterpret_cast<const float4*>(re);
+                        const float x = sv[e];
+                        if constexpr (SREC == 4) {
+                            blur += x * r0.x;  // blur_state forward.rs:174-180
+                            if (want_sg) {
+                                const float diff = x - si;
+                                gr[0] += diff * r0.y;
+                                gr[1] += diff * r0.z;
+                                if constexpr (D == 3) gr[2] += diff * r0.w;
+                            }
+                        } else {
+                            if (branch_a) blur += x * r0.x * r0.y;  // second_pass_particle forward.rs:263-270
+                            else blur += x * r0.x;
+                            if (want_sg) {
+                                const float diff = x - si;
+                                gr[0] += diff * r0.z;
+                                gr[1] += diff * r0.w;
+                                if constexpr (D == 3) gr[2] += diff * re[4];
+                            }
+                        }
+                        sv[e] = load_sv(nslot[i]);
+                    }
+                }
+                {
+                    const float4* xp = reinterpret_cast<const float4*>(ext + xcomp * Sh::XSTR);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 x = xp[q];
+                        xacc += x.x;
+                        xacc += x.y;
+                        xacc += x.z;
+                        xacc += x.w;
+                    }
+                }
+                wave_sync();
+            }
+        };
+
+        // ---- Phase A: the accepted candidates of each chunk (<= 64 consecutive slots of a cell run,
+        // in visit order), appended to the lists; rounds are consumed whenever a chunk would not fit.
+        // tested chunks: coordinate groups of the wave's targets, then each group's neighbour cells
+        uint64_t pending = 0, grp = 0, cells = 0;
+        int l0 = 0, l1 = 0, l2 = 0;
+        uint32_t lb = 0, nb_beg = 0, nb_end = 0, cbase = 0, cend = 0;
+        bool nb_filter = false, nb_found = false, cfilter = false;
+        int64_t n0 = 0, n1 = 0, n2 = 0;
+        auto next_cell = [&]() -> bool {
+            while (cells) {
+                const int nk = __ffsll((unsigned long long)cells) - 1;  // ascending = visit order
+                cells &= cells - 1;
+                n0 = (int64_t)l0 + nk % 3 - 1;
+                n1 = (int64_t)l1 + (nk / 3) % 3 - 1;
+                n2 = D == 3 ? (int64_t)l2 + nk / 9 - 1 : 0;
+                cbase = (uint32_t)readlane_i((int)nb_beg, nk);
+                cend = (uint32_t)readlane_i((int)nb_end, nk);
+                cfilter = readlane_i((int)nb_filter, nk) != 0;
+                if (cbase < cend) return true;
+            }
+            return false;
+        };
+        auto next_group = [&]() -> bool {
+            while (pending) {
+                const int leader = __ffsll((unsigned long long)pending) - 1;
+                l0 = readlane_i(ci[0], leader);
+                l1 = readlane_i(ci[1], leader);
+                l2 = D == 3 ? readlane_i(ci[2], leader) : 0;
+                lb = (uint32_t)readlane_i((int)b, leader);
+                const bool same = active && ci[0] == l0 && ci[1] == l1 && (D == 2 || ci[2] == l2) && b == lb;
+                grp = __ballot(same) & pending;
+                pending &= ~grp;
+                neighbor_runs<D>(P, bo, lb, l0, l1, l2, lane, nb_beg, nb_end, nb_filter, nb_found);
+                cells = __ballot(nb_found);
+                if (next_cell()) return true;
+            }
+            return false;
+        };
+        const bool recorded = !__ballot(nct > MAXC);
+        if (recorded) {
+            // lane c appends chunk k0 + c of its target: the group's chunks in order, each at the
+            // running count plus the entries of the chunks before it; when a target's list would
+            // overflow, the chunks that fit are appended, the lists consumed, and the rest follow
+            for (uint32_t k0 = 0; __ballot(k0 < nct); k0 += 16) {
+                const bool valid = k0 + c < nct;
+                uint4 rc = rb0;
+                if (k0 > 0) rc = valid ? nb_chunks[(uint64_t)(k0 + c) * P.T + s] : make_uint4(0u, 0u, 0u, 0u);
+                uint64_t m = valid ? ((uint64_t)rc.w << 32) | rc.z : 0ull;
+                uint32_t left = (uint32_t)__popcll(m);
+                for (;;) {
+                    const uint32_t incl = row_incl_sum(left);
+                    const uint32_t room = CAP - cnt;
+                    const bool fits = left > 0 && incl <= room;
+                    if (fits) {
+                        uint32_t pos = cnt + incl - left;
+                        while (m) {
+                            const uint32_t bit = (uint32_t)__builtin_ctzll(m);
+                            m &= m - 1;
+                            mylist[pos++] = rc.x + bit;
+                        }
+                        left = 0;
+                    }
+                    cnt += row_last(row_incl_max(incl <= room ? incl : 0u));  // the entries that fit
+                    if (!__ballot(left > 0)) break;
+                    process();
+                    cnt = 0;
+                }
+            }
+            process();
+            cnt = 0;
+        }
+        bool more = false;
+        if (!recorded) {
+            pending = __ballot(active);
+            more = next_group();
+        }
+        bool have = false;
+        uint64_t acc = 0;
+        uint32_t abase = 0;
+        for (;;) {
+            for (;;) {
+                if (!have) {
+                    if (!more) break;
+                    {
+                        const bool in_group = (grp >> lane) & 1ull;
+                        const uint32_t m = cend - cbase < (uint32_t)kNbChunk ? cend - cbase : (uint32_t)kNbChunk;
+                        acc = 0;
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const uint32_t k = c + 16u * u;
+                            const uint32_t kc = k < m ? k : m - 1;
+                            const float4 r = srec[cbase + kc];
+                            bool ok = in_group & (k < m);
+                            if (cfilter) {
+                                if constexpr (D == 2) {
+                                    ok = ok & ((int64_t)__float_as_int(r.z) == n0) & ((int64_t)__float_as_int(r.w) == n1);
+                                } else {
+                                    const int4 cc = scoord[cbase + kc];
+                                    ok = ok & ((int64_t)cc.x == n0) & ((int64_t)cc.y == n1) & ((int64_t)cc.z == n2);
+                                }
+                            }
+                            const float d0 = delta_axis(pi[0], r.x, 0, P.g);
+                            const float d1 = delta_axis(pi[1], r.y, 1, P.g);
+                            float r2 = d0 * d0;
+                            r2 += d1 * d1;
+                            if constexpr (D == 3) {
+                                const float d2 = delta_axis(pi[2], r.z, 2, P.g);
+                                r2 += d2 * d2;
+                            }
+                            const uint64_t bal = __ballot(ok & (r2 < P.g.eps2));
+                            acc |= ((bal >> (lane & 48u)) & 0xffffull) << (16 * u);
+                        }
+                        abase = cbase;
+                        cbase += kNbChunk;
+                        more = cbase < cend || next_cell() || next_group();
+                    }
+                    have = true;
+                }
+                if (__ballot(cnt + (uint32_t)__popcll(acc) > CAP)) break;
+                // append: lane c takes bits c, c + 16, c + 32, c + 48 of the chunk's mask
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t bit = c + 16u * u;
+                    if ((acc >> bit) & 1ull) {
+                        const uint64_t below = (1ull << bit) - 1ull;
+                        mylist[cnt + (uint32_t)__popcll(acc & below)] = abase + bit;
+                    }
+                }
+                cnt += (uint32_t)__popcll(acc);
+                have = false;
+            }
+            if (recorded) break;
+            process();
+            cnt = 0;
+            if (!have && !more) break;
+        }
+
+        // ---- normalisation (normalize.rs:5-118) and the feature row
+        float mom[D * D], dgs[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < D * D; ++k) mom[k] = 0.0f;
+        {
+            uint32_t k = 0;
+#pragma unroll
+            for (int ra = 0; ra < D; ++ra)
+#pragma unroll
+                for (int ca = ra; ca < D; ++ca) mom[ra * D + ca] = group_lane(xacc, lane, k++);
+        }
+        if constexpr (NX > NMOM) {
+#pragma unroll
+            for (int a = 0; a < D; ++a) dgs[a] = group_lane(xacc, lane, NMOM + a);
+        }
+        if (want_sg) {
+            if (want_m) {  // apply_moment_correction normalize.rs:93-118
+                float inv[D * D];
+                safe_inverse<D>(mom, inv);
+                float corrected[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int o = 0; o < D; ++o)
+#pragma unroll
+                    for (int k = 0; k < D; ++k) corrected[o] += gr[k] * inv[k * D + o];
+#pragma unroll
+                for (int o = 0; o < D; ++o) gr[o] = corrected[o];
+            }
+#pragma unroll
+            for (int a = 0; a < D; ++a) gr[a] *= P.state_scale;  // normalize_state_gradient
+            if (P.log_norm_grad) log_normalize<D>(gr);
+        }
+        if (want_dg) {  // normalize_density_gradient normalize.rs:32-58
+#pragma unroll
+            for (int a = 0; a < D; ++a) dgs[a] *= P.dgrad_scale;
+            if (P.log_norm_dgrad) log_normalize<D>(dgs);
+        }
+        // feature assembly forward.rs:100-133 at the padded positions
+        fg[c] = si;
+        fg[16 + c] = blur;
+#pragma unroll
+        for (int a = 0; a < D; ++a) fg[32 + c * D + a] = want_sg ? gr[a] : 0.0f;
+        if (c == 0) {
+            float rest[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) rest[k] = 0.0f;
+            const float pp[3] = {pos4.x, pos4.y, pos4.z};
+            int nrest = 0;
+            if (want_dg) {
+#pragma unroll
+                for (int a = 0; a < D; ++a) rest[a] = dgs[a];
+                nrest = D;
+            }
+            if (P.position_features) {
+#pragma unroll
+                for (int a = 0; a < D; ++a) {
+                    if (nrest == D) rest[D + a] = pp[a];
+                    else rest[a] = pp[a];
+                }
+            }
+            constexpr uint32_t base_rest = 32 + 16 * D;
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                if (base_rest + r < FP) fg[base_rest + r] = rest[r];
+        }
+        wave_sync();
+
+        // ---- update MLP (model.rs:900-940): hidden units c, c + 16, ..., c + 112
+        float acc1[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) acc1[m] = b1[c + 16 * m];
+        for (uint32_t kb = 0; kb < FP / 4; ++kb) {
+            const float4 f4 = *reinterpret_cast<const float4*>(fg + 4 * kb);
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const float4 w4 = *reinterpret_cast<const float4*>(w1q + ((size_t)kb * HP + c + 16 * m) * 4);
+                acc1[m] += w4.x * f4.x;
+                acc1[m] += w4.y * f4.y;
+                acc1[m] += w4.z * f4.z;
+                acc1[m] += w4.w * f4.w;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < 8; ++m) hg[c + 16 * m] = fmaxf(acc1[m], 0.0f);
+        wave_sync();
+        // outputs: state update D + c and motion output c (lanes c < D)
+        float us = b2[D + c], um = b2[c];
+#pragma unroll 4
+        for (uint32_t hb = 0; hb < HP / 4; ++hb) {
+            const float4 h4 = *reinterpret_cast<const float4*>(hg + 4 * hb);
+            const float4 ws4 = *reinterpret_cast<const float4*>(w2q + ((size_t)hb * OPAD + D + c) * 4);
+            const float4 wm4 = *reinterpret_cast<const float4*>(w2q + ((size_t)hb * OPAD + c) * 4);
+            us += ws4.x * h4.x;
+            us += ws4.y * h4.y;
+            us += ws4.z * h4.z;
+            us += ws4.w * h4.w;
+            um += wm4.x * h4.x;
+            um += wm4.y * h4.y;
+            um += wm4.z * h4.z;
+            um += wm4.w * h4.w;
+        }
+        wave_sync();  // the region is refilled by the next item
+
+        // ---- motion scaling, gates, mask, Euler step (model.rs:806-898, step.rs:4-55)
+        float u[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int a = 0; a < D; ++a) u[a] = group_lane(um, lane, a);
+        float norm = 0.0f;
+#pragma unroll
+        for (int a = 0; a < D; ++a) norm += u[a] * u[a];
+        norm = sqrtf(norm);
+        float dx[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int a = 0; a < D; ++a) dx[a] = P.alpha * u[a] * P.motion_eps / (1.0f + norm);
+        float sgate = 1.0f;
+        if (P.gates3d) {
+            const float liveness = group_lane(si, lane, 3);
+            const float sd = group_lane(si, lane, 7);
+            sgate = clampf_((4.0f - liveness) * 2.0f, 0.0f, 1.0f);
+            float mg;
+            if (pos4.w >= 0.5f) {
+                mg = 0.0f;
+            } else {
+                const float dgate = clampf_((fabsf(sd) - 0.01f) / 0.02f, 0.0f, 1.0f);
+                mg = sgate * dgate;
+            }
+#pragma unroll
+            for (int a = 0; a < D; ++a) dx[a] *= mg;
+        }
+        const float mk = io.mask ? io.mask[i] : hash_mask(li, b, P.N, P.update_prob, P.step_index, P.base_seed);
+        if (active && c == 0) {
+            float pn[4] = {pos4.x, pos4.y, pos4.z, pos4.w};
+            constexpr int MEM = D == 3 ? 4 : 2;
+#pragma unroll
+            for (int a = 0; a < MEM; ++a) pn[a] += P.dt * dx[a] * mk;
+            if (P.g.boundary == 0) {
+#pragma unroll
+                for (int a = 0; a < D; ++a) pn[a] = wrap_axis(pn[a], a, P.g);
+            }
+            io.out_pos[i] = make_float4(pn[0], pn[1], pn[2], pn[3]);
+        }
+        float dsc = us;
+        if (P.gates3d) dsc *= sgate;
+        float next = si + P.dt * dsc * mk;
+        if (clamped_channel(D, P.S, c)) next = clampf_(next, -8.0f, 24.0f);
+        if (active && c < P.S) io.out_states[(uint64_t)i * P.S + c] = next;
+    }
+}
+
+template <int D, int FL>
+static hipError_t launch_fused_t(const StepParams& p, Workspace& ws, const StepIO& io, const float* wfused,
+                                 hipStream_t stream, Profiler* prof) {
+    using Sh = FuseShape<D, FL>;
+    const size_t lds = (fused_weight_floats(p.FP, D) + (size_t)kFuseWaves * Sh::WAVE_FLOATS) * 4;
+    if (lds > kFuseLdsBytes) return hipErrorInvalidValue;
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e = hipFuncSetAttribute((const void*)k_update_fused<D, FL>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFuseLdsBytes);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    // one block per CU at most; never more waves than items of four targets
+    const uint64_t max_items = ((uint64_t)p.T + 3) / 4;
+    const uint32_t blocks = (uint32_t)std::max<uint64_t>(
+        1, std::min<uint64_t>((uint64_t)device_cu_count(), (max_items + kFuseWaves - 1) / kFuseWaves));
+    uint32_t* wl = ws.wl_count.as<uint32_t>();
+    return launch_timed(prof, NPA_KERNEL_UPDATE, k_update_fused<D, FL>, dim3(blocks), dim3(64 * kFuseWaves),
+                        (uint32_t)lds, stream, p, ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(),
+                        ws.svol.as<float4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
+                        ws.act_rows.as<uint32_t>(), (const uint32_t*)(wl + 3), ws.nb_chunks.as<uint4>(),
+                        ws.nb_count.as<uint32_t>(), wfused, io);
+}
+
+template <int D>
+static hipError_t launch_fused_d(const StepParams& p, Workspace& ws, const StepIO& io, const float* wfused,
+                                 hipStream_t stream, Profiler* prof) {
+    if (p.state_grad && p.hybrid && !p.density_grad) return launch_fused_t<D, 5>(p, ws, io, wfused, stream, prof);
+    return launch_fused_t<D, -1>(p, ws, io, wfused, stream, prof);
+}
+
+#if NPA_PART_DIM2
+hipError_t launch_update_fused_2d(const StepParams& p, Workspace& ws, const StepIO& io, const float* wfused,
+                                  hipStream_t stream, Profiler* prof) {
+    return launch_fused_d<2>(p, ws, io, wfused, stream, prof);
+}
+#endif
+#if NPA_PART_DIM3
+hipError_t launch_update_fused_3d(const StepParams& p, Workspace& ws, const StepIO& io, const float* wfused,
+                                  hipStream_t stream, Profiler* prof) {
+    return launch_fused_d<3>(p, ws, io, wfused, stream, prof);
+}
+#endif
+
+}  // namespace npa

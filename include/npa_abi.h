@@ -515,7 +515,8 @@ enum {
     NPA_KERNEL_ACTIVE = 9,     /* reserved: the split kernel (8) now selects the update-mask targets */
     NPA_KERNEL_RENDER = 10,    /* the whole projected 3D render pipeline (npa_render_views) */
     NPA_KERNEL_RASTER = 11,    /* the whole oriented Gaussian raster (npa_raster_gaussians_3d) */
-    NPA_KERNEL_COUNT = 12
+    NPA_KERNEL_UPDATE = 12,    /* second neighbour pass + update MLP + masked Euler in one kernel (16-channel rows) */
+    NPA_KERNEL_COUNT = 13
 };
 /* kernel_mask selects kernels by bit (1 << NPA_KERNEL_*; 0 = off, -1 = all). The
  * library then brackets each launch of a selected kernel with HIP events on the
