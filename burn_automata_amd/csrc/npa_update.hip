@@ -206,8 +206,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
     uint32_t* mylist = reinterpret_cast<uint32_t*>(wl) + g * Sh::LSTR;
     float* stage = wl + 4 * Sh::LSTR + g * Sh::SSTR;       // this group's entry records
     float* ext = wl + 4 * Sh::LSTR + 4 * Sh::SSTR + g * Sh::XGSTR;  // this group's sums' terms
-    float* fg = wl + g * (FP + 4);                          // feature row (after the walk)
-    float* hg = wl + 4 * (FP + 4) + g * Sh::HSTR;           // hidden activations
+    float* hg = wl + 4 * (FP + 4) + g * Sh::HSTR;           // hidden activations (after the walk)
 
     const bool want_sg = FL >= 0 ? (FL & 1) != 0 : P.state_grad != 0;
     const bool want_dg = FL >= 0 ? (FL & 2) != 0 : P.density_grad != 0;
@@ -547,15 +546,13 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
             for (int a = 0; a < D; ++a) dgs[a] *= P.dgrad_scale;
             if (P.log_norm_dgrad) log_normalize<D>(dgs);
         }
-        // feature assembly forward.rs:100-133 at the padded positions
-        fg[c] = si;
-        fg[16 + c] = blur;
+        // feature row forward.rs:100-133: lane c of a target holds features c (state), 16 + c (blur)
+        // and 32 + c D + a (gradient); the rest (density gradient, position, then zeros up to FP) is
+        // the same in every lane of the target
+        float rest[8];
 #pragma unroll
-        for (int a = 0; a < D; ++a) fg[32 + c * D + a] = want_sg ? gr[a] : 0.0f;
-        if (c == 0) {
-            float rest[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) rest[k] = 0.0f;
+        for (int k = 0; k < 8; ++k) rest[k] = 0.0f;
+        {
             const float pp[3] = {pos4.x, pos4.y, pos4.z};
             int nrest = 0;
             if (want_dg) {
@@ -570,30 +567,74 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
                     else rest[a] = pp[a];
                 }
             }
-            constexpr uint32_t base_rest = 32 + 16 * D;
-#pragma unroll
-            for (int r = 0; r < 8; ++r)
-                if (base_rest + r < FP) fg[base_rest + r] = rest[r];
         }
-        wave_sync();
+        float gf[3];
+#pragma unroll
+        for (int a = 0; a < 3; ++a) gf[a] = want_sg ? gr[a] : 0.0f;
 
-        // ---- update MLP (model.rs:900-940): hidden units c, c + 16, ..., c + 112
-        float acc1[8];
+        // ---- update MLP (model.rs:900-940), layer 1: lane l computes hidden units l and l + 64 of the
+        // wave's four targets (each weight is read by one lane and used for four targets); feature k
+        // of target t is read from the lane that holds it into a scalar register. Every sum starts
+        // from its bias and adds the features in index order.
+        constexpr uint32_t KB_FIXED = (32 + 16 * D) / 4;  // blocks of four state/blur/gradient features
+        float h0[4], h1[4];
+        {
+            const float bb0 = b1[lane], bb1 = b1[lane + 64];
 #pragma unroll
-        for (int m = 0; m < 8; ++m) acc1[m] = b1[c + 16 * m];
-        for (uint32_t kb = 0; kb < FP / 4; ++kb) {
-            const float4 f4 = *reinterpret_cast<const float4*>(fg + 4 * kb);
-#pragma unroll
-            for (int m = 0; m < 8; ++m) {
-                const float4 w4 = *reinterpret_cast<const float4*>(w1q + ((size_t)kb * HP + c + 16 * m) * 4);
-                acc1[m] += w4.x * f4.x;
-                acc1[m] += w4.y * f4.y;
-                acc1[m] += w4.z * f4.z;
-                acc1[m] += w4.w * f4.w;
+            for (int t = 0; t < 4; ++t) {
+                h0[t] = bb0;
+                h1[t] = bb1;
             }
         }
+        auto mac_block = [&](uint32_t kb, auto feature_of) {
+            const float4 w0 = *reinterpret_cast<const float4*>(w1q + ((size_t)kb * HP + lane) * 4);
+            const float4 w1 = *reinterpret_cast<const float4*>(w1q + ((size_t)kb * HP + lane + 64) * 4);
+            const float wa[4] = {w0.x, w0.y, w0.z, w0.w}, wb[4] = {w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-        for (int m = 0; m < 8; ++m) hg[c + 16 * m] = fmaxf(acc1[m], 0.0f);
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const float f = feature_of(i, t);
+                    h0[t] += wa[i] * f;
+                    h1[t] += wb[i] * f;
+                }
+            }
+        };
+#pragma unroll
+        for (uint32_t kb = 0; kb < KB_FIXED; ++kb) {
+            mac_block(kb, [&](int i, int t) {
+                const uint32_t k = 4 * kb + i;
+                float v;
+                uint32_t src;
+                if (k < 16) {
+                    v = si;
+                    src = k;
+                } else if (k < 32) {
+                    v = blur;
+                    src = k - 16;
+                } else {
+                    v = gf[(k - 32) % D];
+                    src = (k - 32) / D;
+                }
+                return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)(16 * t + src)));
+            });
+        }
+        if (FP / 4 > KB_FIXED)
+            mac_block(KB_FIXED, [&](int i, int t) {
+                return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rest[i]), 16 * t));
+            });
+        if (FP / 4 > KB_FIXED + 1)
+            mac_block(KB_FIXED + 1, [&](int i, int t) {
+                return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rest[4 + i]), 16 * t));
+            });
+        {
+            float* hw = wl + 4 * (FP + 4);  // [target][HSTR]
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                hw[t * Sh::HSTR + lane] = fmaxf(h0[t], 0.0f);
+                hw[t * Sh::HSTR + lane + 64] = fmaxf(h1[t], 0.0f);
+            }
+        }
         wave_sync();
         // outputs: state update D + c and motion output c (lanes c < D)
         float us = b2[D + c], um = b2[c];

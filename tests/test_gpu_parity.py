@@ -188,12 +188,37 @@ def _model_case(name):
         n = 1024
         pos = np.concatenate([syn.uniform_disk(n, 20 + k) for k in range(4)])
         return m, g, pos, syn.normal_states(4 * n, 16, 20), syn.seeded_weights(m, 20), 4, n
+    if name == "no_sgrad_2d":  # density gradient and positions without the state gradient, H < 128
+        m = NpaConfig(eps0=0.05, hidden_dims=96, state_grad=False, density_grad=True,
+                      position_features=True)
+        _, g = syn.config_c1()
+        n = 3000
+        return (m, g, syn.uniform_disk(n, 31, 0.6), syn.normal_states(n, 16, 31),
+                syn.seeded_weights(m, 31), 1, n)
+    if name == "no_sgrad_3d":  # 24 channels: the two-kernel path
+        m = NpaConfig.torus_field_3dgs().replace(state_grad=False)
+        g = HashGridConfig.growing_3dgs()
+        n = 1024
+        return (m, g, syn.uniform_ball(n, 32, 0.5), syn.normal_states(n, m.state_dims, 32),
+                syn.seeded_weights(m, 32), 1, n)
+    if name == "torus16_gates_3d":  # 16 channels, density gradient, positions, 3D gates
+        m = NpaConfig.torus_field_3dgs().replace(state_dims=16, hidden_dims=128)
+        g = HashGridConfig.growing_3dgs()
+        n = 1024
+        pos = syn.uniform_ball(n, 33, 0.5)
+        pos[::5, 3] = 1.0  # anchored particles
+        st = syn.normal_states(n, m.state_dims, 33, std=1.0)
+        st[:, 3] += 3.5
+        return m, g, pos, st, syn.seeded_weights(m, 33), 1, n
     raise KeyError(name)
 
 
 @pytest.mark.parametrize("name", ["c1", "c1_dgrad", "growing_3d", "torus_gates_3d",
-                                  "texture_periodic", "batch4"])
+                                  "texture_periodic", "batch4", "no_sgrad_2d", "no_sgrad_3d",
+                                  "torus16_gates_3d"])
 def test_step_parity(ctx, name):
+    """One step against NpaModel::step_cpu (model.rs:768-858). 16-channel models run the fused
+    second-pass + MLP kernel, wider ones the two-kernel path; both sum in the reference's order."""
     m, g, pos, st, w, b, n = _model_case(name)
     mask = O.update_mask(b, n, 0.5, 0, 42)
     want = O.step(m, w, pos, st, b, n, g, 1.0, mask)
@@ -201,6 +226,9 @@ def test_step_parity(ctx, name):
     assert rel_err(got.density, want.density) <= STEP_TOL
     assert rel_err(got.next_positions, want.next_positions) <= STEP_TOL
     assert rel_err(got.next_states, want.next_states) <= STEP_TOL
+    np.testing.assert_array_equal(to_np(got.density), want.density)
+    np.testing.assert_array_equal(to_np(got.next_positions), want.next_positions)
+    np.testing.assert_array_equal(to_np(got.next_states), want.next_states)
 
 
 def test_mlp_forward_parity(ctx):
