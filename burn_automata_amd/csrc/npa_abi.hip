@@ -526,7 +526,7 @@ npa_status npa_perceive(npa_context* ctx, const float* positions, const float* s
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null array");
     npa::HashgridPlan plan;
     std::string err;
-    if (!npa::make_plan(*cfg, B, N, &plan, &err, npa::targets_per_item(npa::state_stride_for(S))))
+    if (!npa::make_plan(*cfg, B, N, &plan, &err))
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
     HostIO io(ctx);
     const float4* pos = (const float4*)io.in(positions, total * 16);
@@ -579,7 +579,7 @@ npa_status npa_perceive_adjoint(npa_context* ctx, const float* positions, const 
     if (set_device(ctx)) return NPA_ERR_DEVICE;
     npa::HashgridPlan plan;
     std::string err;
-    if (!npa::make_plan(*cfg, B, N, &plan, &err, npa::targets_per_item(npa::state_stride_for(S))))
+    if (!npa::make_plan(*cfg, B, N, &plan, &err))
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
     HostIO io(ctx);
     const float4* pos = (const float4*)io.in(positions, total * 16);
@@ -688,7 +688,7 @@ npa_status npa_step(npa_context* ctx, const float* positions, const float* state
     if (set_device(ctx)) return NPA_ERR_DEVICE;
     npa::HashgridPlan plan;
     std::string err;
-    if (!npa::make_plan(*grid, B, N, &plan, &err, npa::targets_per_item(npa::state_stride_for(model->state_dims))))
+    if (!npa::make_plan(*grid, B, N, &plan, &err))
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
     HostIO io(ctx);
     npa::StepIO sio;
@@ -754,7 +754,7 @@ npa_status npa_step_noalloc(npa_context* ctx, const float* positions, const floa
                     std::string("no-allocation workspace unavailable: ") + hipGetErrorString(ctx->scratch_err));
     npa::HashgridPlan plan;
     std::string err;
-    if (!npa::make_plan(*grid, B, N, &plan, &err, npa::targets_per_item(npa::state_stride_for(S))))
+    if (!npa::make_plan(*grid, B, N, &plan, &err))
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
     npa::StepParams p = make_params(*grid, opts_for_model(*model), B, N, S);
     apply_model(&p, *model, grid->eps);
@@ -1052,7 +1052,7 @@ npa_status npa_state_create(npa_context* ctx, const npa_model_cfg* model, const 
     if (set_device(ctx)) return NPA_ERR_DEVICE;
     npa::HashgridPlan plan;
     std::string err;
-    if (!npa::make_plan(*grid, B, N, &plan, &err, npa::targets_per_item(npa::state_stride_for(model->state_dims))))
+    if (!npa::make_plan(*grid, B, N, &plan, &err))
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: " + err);
     npa_state* s = new npa_state();
     s->ctx = ctx;

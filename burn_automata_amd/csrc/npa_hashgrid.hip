@@ -83,7 +83,9 @@ static void each_buffer(Workspace& w, const HashgridPlan& plan, uint64_t total, 
     f(w.dir_n, (bins ? bins : 1) * 4);
     f(w.bin_list, (bins ? bins : 1) * 4);
     f(w.dir_e, (bins ? bins : 1) * kDirGroups * 16);
-    f(w.nb_chunks, t1 * max_chunks(dim) * 16);
+    f(w.row_of, t1 * 4);
+    f(w.nb_base, t1 * max_chunks(dim) * 4);
+    f(w.nb_mask, t1 * max_chunks(dim) * 8);
     f(w.nb_count, t1 * 4);
 }
 
@@ -122,7 +124,7 @@ uint64_t Workspace::carve(const HashgridPlan& plan, uint64_t total, uint32_t bat
 void Workspace::release() {
     for (DevBuf* b : {&keys, &ranks, &table, &totals, &bin_offsets, &perm, &inv, &flags, &wl_count,
                       &worklist, &srec, &scoord, &sstate, &svol, &counters, &features, &wpad, &tmpidx,
-                      &dir_n, &dir_e, &bin_list, &act_rows, &nb_chunks, &nb_count})
+                      &dir_n, &dir_e, &bin_list, &act_rows, &row_of, &nb_base, &nb_mask, &nb_count})
         b->release();
 }
 
@@ -525,7 +527,7 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
                                                float* __restrict__ sstate, uint32_t* __restrict__ dir_n,
                                                int4* __restrict__ dir_e, uint2* __restrict__ worklist,
                                                uint32_t* __restrict__ wl_count, uint32_t tpi, SplitTargets T,
-                                               uint32_t* __restrict__ act_rows,
+                                               uint32_t* __restrict__ act_rows, uint32_t* __restrict__ row_of,
                                                const uint32_t* __restrict__ bin_list,
                                                const uint32_t* __restrict__ bin_count) {
     constexpr uint32_t K = kDirGroups;
@@ -669,6 +671,7 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
     if (!has_bin) return;
     auto place = [&](bool valid, bool tgt, uint32_t i, uint32_t dst, uint32_t row) {
         if (!valid) return;
+        row_of[dst] = tgt ? row : ~0u;
         if (tgt) act_rows[row] = dst;
         else if (T.mask_mode != 0) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
     };
@@ -790,7 +793,8 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
                                                    float* __restrict__ sstate, uint32_t* __restrict__ dir_n,
                                                    int4* __restrict__ dir_e, uint2* __restrict__ worklist,
                                                    uint32_t* __restrict__ wl_count, uint32_t tpi, SplitTargets T,
-                                                   uint32_t* __restrict__ act_rows, uint32_t* __restrict__ bin_list) {
+                                                   uint32_t* __restrict__ act_rows, uint32_t* __restrict__ row_of,
+                                                   uint32_t* __restrict__ bin_list) {
     constexpr uint32_t K = kDirGroups;
     __shared__ uint32_t lds_i[kThinThreads / 64], lds_r[kThinThreads / 64], lds_f[kThinThreads / 64];
     __shared__ uint32_t s_base[3];
@@ -913,6 +917,7 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
                 seen_t[k] += tgt ? 1u : 0u;
             }
         write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
+        row_of[dst] = tgt ? row : ~0u;
         if (tgt) act_rows[row] = dst;
         else if (T.mask_mode != 0) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
     }
@@ -1003,7 +1008,8 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                             ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.srec.as<float4>(),
                             ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.dir_n.as<uint32_t>(),
                             ws.dir_e.as<int4>(), ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), plan.tpi, tg,
-                            ws.act_rows.as<uint32_t>(), (const uint32_t*)nullptr, (const uint32_t*)nullptr);
+                            ws.act_rows.as<uint32_t>(), ws.row_of.as<uint32_t>(), (const uint32_t*)nullptr,
+                            (const uint32_t*)nullptr);
     }
     // sparse bins: one lane per small bin, then a wave per listed (larger) bin; a listed bin holds
     // more than kThinMax particles, so at most total / (kThinMax + 1) bins are listed
@@ -1013,7 +1019,8 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                        ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(), ws.perm.as<uint32_t>(),
                        ws.inv.as<uint32_t>(), ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(),
                        ws.dir_n.as<uint32_t>(), ws.dir_e.as<int4>(), ws.worklist.as<uint2>(),
-                       ws.wl_count.as<uint32_t>(), plan.tpi, tg, ws.act_rows.as<uint32_t>(), ws.bin_list.as<uint32_t>());
+                       ws.wl_count.as<uint32_t>(), plan.tpi, tg, ws.act_rows.as<uint32_t>(), ws.row_of.as<uint32_t>(),
+                       ws.bin_list.as<uint32_t>());
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const uint64_t listed_max = total / (kThinMax + 1);
     const uint32_t sblocks = (uint32_t)std::max<uint64_t>(1, (listed_max + kSplitWaves - 1) / kSplitWaves);
@@ -1021,7 +1028,7 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                        ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(), ws.perm.as<uint32_t>(),
                        ws.inv.as<uint32_t>(), ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(),
                        ws.dir_n.as<uint32_t>(), ws.dir_e.as<int4>(), ws.worklist.as<uint2>(),
-                       ws.wl_count.as<uint32_t>(), plan.tpi, tg, ws.act_rows.as<uint32_t>(),
+                       ws.wl_count.as<uint32_t>(), plan.tpi, tg, ws.act_rows.as<uint32_t>(), ws.row_of.as<uint32_t>(),
                        (const uint32_t*)ws.bin_list.as<uint32_t>(), (const uint32_t*)(ws.wl_count.as<uint32_t>() + 1));
     return hipGetLastError();
 }

@@ -110,11 +110,14 @@ struct Workspace {
     // are written to the output by the update-mask kernel). act_rows: compact row -> slot.
     // Counts (u32 words of wl_count): [0] density items, [1] listed bins, [3] compact rows.
     DevBuf act_rows;
-    // Accepted neighbours recorded by the density pass, per target and neighbour chunk (<= 64
-    // consecutive slots of a cell run, in visit order): chunk-major uint4 {first slot, length,
-    // accept mask lo, hi} at [chunk * T + slot] for the first max_chunks(dim) chunks, and the
-    // target's chunk count (the second pass tests the candidates itself when it exceeds the cap).
-    DevBuf nb_chunks, nb_count;
+    // row_of: slot -> compact row of an update-mask target, or ~0u (written by the split).
+    // Accepted neighbours recorded by the density pass for the targets, per neighbour chunk (<= 64
+    // consecutive slots of a cell run, in visit order): the chunk's first slot (nb_base) and its
+    // 64-bit accept mask (nb_mask) at [row * max_chunks(dim) + chunk] for the first max_chunks(dim)
+    // chunks, and the chunk count at nb_count[row] (the second pass tests the candidates itself
+    // when it exceeds the cap). A target's records are contiguous, so the second pass reads them
+    // coalesced.
+    DevBuf row_of, nb_base, nb_mask, nb_count;
     hipError_t reserve(const HashgridPlan& plan, uint64_t total, uint32_t batch, uint32_t state_dims,
                        int dim, uint32_t feature_dims = 0);
     // The same buffers (with wpad_bytes for the padded weights) as views into [base, base +
@@ -130,9 +133,10 @@ constexpr uint64_t kCarveFlagBytes = 256;
 // cell run of more than 64 particles spans several chunks).
 __host__ __device__ constexpr uint32_t max_chunks(int dim) { return dim == 3 ? 48u : 24u; }
 
-// tpi: targets per wave work item emitted for the neighbour passes (64 / lanes per target).
+// tpi: targets per wave work item emitted for the neighbour passes (the density pass serves one
+// with four lanes per target).
 bool make_plan(const npa_grid_cfg& cfg, uint32_t batch, uint32_t particle_count, HashgridPlan* plan,
-               std::string* err, uint32_t tpi = 64);
+               std::string* err, uint32_t tpi = 16);
 GridParams make_grid_params(const npa_grid_cfg& cfg);
 float host_powi(float x, int n);
 

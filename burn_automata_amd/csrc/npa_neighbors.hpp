@@ -37,23 +37,30 @@ __device__ __forceinline__ bool cell_range(const StepParams& P, const uint32_t* 
         filter = true;
         return true;
     }
-    // every directory entry of the bin is loaded at once (no load waits on another)
+    // the bin's directory entries are loaded four at a time (each half's loads issued together);
+    // a run ends where the next entry's run starts, the last one at the bin's end
     const int4* e = P.dir_e + bin * kDirGroups;
-    int4 ek[kDirGroups];
-#pragma unroll
-    for (uint32_t k = 0; k < kDirGroups; ++k) ek[k] = k < nd ? e[k] : make_int4(0, 0, 0, 0);
     const uint32_t last = bo[bin + 1];
     bool found = false;
+    int hit_k = -1;
 #pragma unroll
-    for (uint32_t k = 0; k < kDirGroups; ++k) {
-        const bool hit = !found && k < nd && (int64_t)ek[k].x == n0 && (int64_t)ek[k].y == n1 &&
-                         (int64_t)ek[k].z == n2;
-        if (hit) {
-            beg = (uint32_t)ek[k].w;
-            end = k + 1 < nd ? (uint32_t)ek[k + 1 < kDirGroups ? k + 1 : k].w : last;
-            found = true;
+    for (uint32_t h = 0; h < kDirGroups; h += 4) {
+        if (h >= nd) break;
+        int4 ek[4];
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) ek[k] = h + k < nd ? e[h + k] : make_int4(0, 0, 0, 0);
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) {
+            const bool hit = !found && h + k < nd && (int64_t)ek[k].x == n0 && (int64_t)ek[k].y == n1 &&
+                             (int64_t)ek[k].z == n2;
+            if (hit) {
+                beg = (uint32_t)ek[k].w;
+                hit_k = (int)(h + k);
+                found = true;
+            }
         }
     }
+    if (found) end = (uint32_t)hit_k + 1 < nd ? (uint32_t)e[hit_k + 1].w : last;
     return found;
 }
 

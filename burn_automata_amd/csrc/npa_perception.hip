@@ -107,30 +107,36 @@ __device__ __forceinline__ float ordered_group_sum(float acc, float v) {
     return acc;
 }
 
-// density  forward.rs:145-160: rho_i = sum_j W_poly6(r_ij^2).
-// L lanes per target split each chunk of a neighbour bin round-robin (lane q takes candidates
-// k = q, q + L, ...), loading candidate records straight from the sorted copy in batches of four
-// (indices clamped to the chunk) and testing them branch-free. Every lane rebuilds the target's
-// running sum in candidate order from the L per-lane terms of each round. A rejected candidate
-// contributes +0.0, which leaves the sum unchanged (it starts at +0.0, adds only non-negative
-// terms and therefore never holds -0.0).
-// The accepted candidates are recorded for the second pass, which needs exactly the same set in
-// the same order: per target and chunk (in visit order) {first slot, length, 64-bit accept mask}
-// at nb_chunks[chunk * T + slot] for the first max_chunks(D) chunks, and the chunk count.
-template <int D, int L>
-__global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __restrict__ srec,
-                                                const int4* __restrict__ scoord,
-                                                const uint32_t* __restrict__ bo,
-                                                const uint32_t* __restrict__ perm,
-                                                const uint2* __restrict__ wl,
-                                                const uint32_t* __restrict__ wl_count,
-                                                float4* __restrict__ svol, float* __restrict__ density_out,
-                                                uint4* __restrict__ nb_chunks, uint32_t* __restrict__ nb_count) {
+// density  forward.rs:145-160: rho_i = sum_j W_poly6(r_ij^2), four lanes per target. A work item
+// holds up to 16 consecutive slots of one cell run, so its targets share their 3^D neighbour cells
+// and walk the same candidates in the same order (cells dz, dy, dx; slots ascending). Lane q of a
+// target tests candidates q, q + 4, ... of each chunk (<= 64 consecutive slots of a neighbour run)
+// and every lane rebuilds the target's running sum in candidate order from the four lanes' terms
+// with DPP broadcasts folded into the adds; a rejected candidate adds +0.0, which leaves the sum
+// unchanged (it starts at +0.0 and never holds -0.0). Each round's accept bits come from one
+// ballot. The targets of an unsplit bin (more cells than its directory holds) may lie in different
+// cells: the item's coordinate groups then walk in turn.
+// For the update-mask targets the accepted candidates are recorded for the second pass, which needs
+// exactly the same set in the same order: per chunk (in visit order) its first slot and 64-bit
+// accept mask at [row * max_chunks(D) + chunk] for the first max_chunks(D) chunks, and the chunk
+// count at nb_count[row].
+template <int D>
+__global__ __launch_bounds__(256) void k_density_q(StepParams P, const float4* __restrict__ srec,
+                                                   const int4* __restrict__ scoord,
+                                                   const uint32_t* __restrict__ bo,
+                                                   const uint32_t* __restrict__ perm,
+                                                   const uint32_t* __restrict__ row_of,
+                                                   const uint2* __restrict__ wl,
+                                                   const uint32_t* __restrict__ wl_count,
+                                                   float4* __restrict__ svol, float* __restrict__ density_out,
+                                                   uint32_t* __restrict__ nb_base, uint64_t* __restrict__ nb_mask,
+                                                   uint32_t* __restrict__ nb_count) {
     constexpr uint32_t MAXC = max_chunks(D);
-    const uint32_t lane = threadIdx.x;
-    const uint32_t t = lane / L, q = lane % L;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t t = lane >> 2, q = lane & 3;
     const uint32_t items = *wl_count;
-    for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
+    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
+    for (uint32_t it = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); it < items; it += nwaves) {
         const uint2 item = wl[it];
         const bool active = t < item.y;
         const uint32_t s = item.x + (active ? t : 0u);
@@ -138,8 +144,10 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
         float pi[3];
         int ci[3];
         load_rec<D>(srec, scoord, s, pi, ci);
+        const uint32_t row = active ? row_of[s] : ~0u;
+        const bool record = row != ~0u;
         float rho = 0.0f;
-        uint32_t nch = 0;  // chunks visited by this lane's coordinate group
+        uint32_t nch = 0;
         uint64_t pending = __ballot(active);
         while (pending) {
             const int leader = __ffsll((unsigned long long)pending) - 1;
@@ -149,7 +157,7 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
             const uint64_t group = __ballot(same) & pending;
             pending &= ~group;
             const bool in_group = (group >> lane) & 1ull;
-            uint32_t gch = 0;  // chunk index within this group's visit order (wave-uniform)
+            uint32_t gch = 0;  // chunk index within the group's visit order (wave-uniform)
             uint32_t nb_beg, nb_end;
             bool nb_filter, nb_found;
             neighbor_runs<D>(P, bo, b, l0, l1, l2, lane, nb_beg, nb_end, nb_filter, nb_found);
@@ -162,58 +170,91 @@ __global__ __launch_bounds__(64) void k_density(StepParams P, const float4* __re
                 const bool filter = readlane_i((int)nb_filter, nk) != 0;
                 for (uint32_t base = beg; base < end; base += kChunk, ++gch) {
                     const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
-                    uint64_t acc = 0;  // accepted candidates of this lane's residue class
-                    constexpr int BT = kChunk / L < 4 ? kChunk / L : 4;  // loads per batch
-                    for (int i0 = 0; i0 < kChunk / L; i0 += BT) {
-                        if ((uint32_t)(i0 * L) >= m) break;  // wave-uniform
-                        float4 rc[BT];
-                        int4 cc[BT];
-#pragma unroll
-                        for (int u = 0; u < BT; ++u) {
-                            const uint32_t k = q + (uint32_t)((i0 + u) * L);
-                            const uint32_t kc = k < m ? k : m - 1;
-                            rc[u] = srec[base + kc];
-                            if constexpr (D == 3) cc[u] = scoord[base + kc];
-                        }
-#pragma unroll
-                        for (int u = 0; u < BT; ++u) {
-                            const uint32_t k = q + (uint32_t)((i0 + u) * L);
-                            const float4 r = rc[u];
+                    const float4* cand = srec + base;
+                    uint32_t mk[2] = {0u, 0u};  // accept mask, candidates 0-31 and 32-63
+                    // FILT: an unsplit bin's candidates are tested for the cell; PER: periodic deltas
+                    auto walk = [&](auto FILT, auto PER) {
+                        constexpr bool filt = decltype(FILT)::value, per = decltype(PER)::value;
+                        constexpr bool xy = D == 2 && !filt;  // only the position is read
+                        auto load = [&](uint32_t k) {
+                            const uint32_t kc = k < m ? k : m - 1;  // in bounds for any k
+                            if constexpr (xy) {
+                                const float2 v = *reinterpret_cast<const float2*>(cand + kc);
+                                return make_float4(v.x, v.y, 0.0f, 0.0f);
+                            } else {
+                                return cand[kc];
+                            }
+                        };
+                        auto test = [&](uint32_t r, const float4 rc) {  // round r: candidate 4 r + q
+                            const uint32_t k = 4 * r + q;
                             bool ok = in_group & (k < m);
-                            if (filter) {
+                            if constexpr (filt) {
+                                const uint32_t kc = k < m ? k : m - 1;
                                 if constexpr (D == 2) {
-                                    ok = ok & ((int64_t)__float_as_int(r.z) == n0) &
-                                         ((int64_t)__float_as_int(r.w) == n1);
+                                    ok = ok & ((int64_t)__float_as_int(rc.z) == n0) & ((int64_t)__float_as_int(rc.w) == n1);
                                 } else {
-                                    ok = ok & ((int64_t)cc[u].x == n0) & ((int64_t)cc[u].y == n1) &
-                                         ((int64_t)cc[u].z == n2);
+                                    const int4 cc = scoord[base + kc];
+                                    ok = ok & ((int64_t)cc.x == n0) & ((int64_t)cc.y == n1) & ((int64_t)cc.z == n2);
                                 }
                             }
-                            const float d0 = delta_axis(pi[0], r.x, 0, P.g);
-                            const float d1 = delta_axis(pi[1], r.y, 1, P.g);
+                            auto delta = [&](float a, float bj, int ax) {  // neighbor_delta hashgrid.rs:165-181
+                                const float v = bj - a;
+                                if constexpr (!per) return v;
+                                const float up = v - P.g.extent[ax], dn = v + P.g.extent[ax];
+                                return v > P.g.half[ax] ? up : (v < -P.g.half[ax] ? dn : v);
+                            };
+                            const float d0 = delta(pi[0], rc.x, 0);
+                            const float d1 = delta(pi[1], rc.y, 1);
                             float r2 = d0 * d0;
                             r2 += d1 * d1;
                             if constexpr (D == 3) {
-                                const float d2 = delta_axis(pi[2], r.z, 2, P.g);
+                                const float d2 = delta(pi[2], rc.z, 2);
                                 r2 += d2 * d2;
                             }
                             const bool acc_ok = ok & (r2 < P.g.eps2);
-                            const float v = acc_ok ? poly6(r2, P.g) : 0.0f;
-                            acc |= acc_ok ? (1ull << k) : 0ull;  // k < m <= 64 when acc_ok
-                            rho = ordered_group_sum<L>(rho, v);
+                            rho = ordered_group_sum<4>(rho, acc_ok ? poly6(r2, P.g) : 0.0f);
+                            return __builtin_amdgcn_ballot_w64(acc_ok);
+                        };
+                        const uint32_t rounds = (m + 3) / 4;
+                        // four batches of four rounds (candidates 16 j .. 16 j + 15), each batch's
+                        // loads issued together; batch j fills bits 16 j .. of the mask, four per
+                        // round: this target's four lanes of the round's ballot
+#pragma unroll
+                        for (uint32_t j = 0; j < 4; ++j) {
+                            if (4 * j >= rounds) break;
+                            float4 ra[4];
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) ra[u] = load(16 * j + 4 * u + q);
+                            uint32_t bits = 0;
+#pragma unroll
+                            for (uint32_t u = 0; u < 4; ++u) {
+                                if (4 * j + u < rounds) {
+                                    const uint64_t bal = test(4 * j + u, ra[u]);
+                                    bits |= ((uint32_t)(bal >> (lane & ~3u)) & 0xfu) << (4 * u);
+                                }
+                            }
+                            mk[j >> 1] |= bits << (16 * (j & 1));
                         }
+                    };
+                    const bool periodic = P.g.boundary == 0;
+                    if (filter) {
+                        if (periodic) walk(std::true_type{}, std::true_type{});
+                        else walk(std::true_type{}, std::false_type{});
+                    } else {
+                        if (periodic) walk(std::false_type{}, std::true_type{});
+                        else walk(std::false_type{}, std::false_type{});
                     }
-                    acc = group_or<L>(acc);
-                    if (in_group && q == 0 && gch < MAXC)
-                        nb_chunks[(uint64_t)gch * P.T + s] =
-                            make_uint4(base, m, (uint32_t)acc, (uint32_t)(acc >> 32));
+                    if (in_group && q == 0 && record && gch < MAXC) {
+                        nb_base[(uint64_t)row * MAXC + gch] = base;
+                        nb_mask[(uint64_t)row * MAXC + gch] = ((uint64_t)mk[1] << 32) | mk[0];
+                    }
                 }
             }
             if (in_group) nch = gch;
         }
         if (active && q == 0) {
             svol[s] = make_float4(pi[0], pi[1], pi[2], recip_finite(rho));
-            nb_count[s] = nch;
+            if (record) nb_count[row] = nch;
             if (density_out) density_out[b * P.N + perm[s]] = rho;
         }
     }
@@ -228,13 +269,17 @@ __global__ __launch_bounds__(256) void k_density_sparse(StepParams P, const floa
                                                         const int4* __restrict__ scoord,
                                                         const uint32_t* __restrict__ bo,
                                                         const uint32_t* __restrict__ perm,
+                                                        const uint32_t* __restrict__ row_of,
                                                         float4* __restrict__ svol, float* __restrict__ density_out,
-                                                        uint4* __restrict__ nb_chunks, uint32_t* __restrict__ nb_count) {
+                                                        uint32_t* __restrict__ nb_base, uint64_t* __restrict__ nb_mask,
+                                                        uint32_t* __restrict__ nb_count) {
     constexpr uint32_t MAXC = max_chunks(D);
     constexpr int ZLO = D == 3 ? -1 : 0, ZHI = D == 3 ? 1 : 0;
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= P.T) return;
     const uint32_t b = s / P.N;
+    const uint32_t row = row_of[s];
+    const bool record = row != ~0u;
     float pi[3];
     int ci[3];
     load_rec<D>(srec, scoord, s, pi, ci);
@@ -270,12 +315,14 @@ __global__ __launch_bounds__(256) void k_density_sparse(StepParams P, const floa
                             acc |= 1ull << k;
                         }
                     }
-                    if (gch < MAXC)
-                        nb_chunks[(uint64_t)gch * P.T + s] = make_uint4(base, m, (uint32_t)acc, (uint32_t)(acc >> 32));
+                    if (record && gch < MAXC) {
+                        nb_base[(uint64_t)row * MAXC + gch] = base;
+                        nb_mask[(uint64_t)row * MAXC + gch] = acc;
+                    }
                 }
             }
     svol[s] = make_float4(pi[0], pi[1], pi[2], recip_finite(rho));
-    nb_count[s] = gch;
+    if (record) nb_count[row] = gch;
     if (density_out) density_out[b * P.N + perm[s]] = rho;
 }
 
@@ -329,7 +376,8 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
                                                  const uint32_t* __restrict__ perm,
                                                  const uint32_t* __restrict__ act_rows,
                                                  const uint32_t* __restrict__ row_count,
-                                                 const uint4* __restrict__ nb_chunks,
+                                                 const uint32_t* __restrict__ nb_base,
+                                                 const uint64_t* __restrict__ nb_mask,
                                                  const uint32_t* __restrict__ nb_count,
                                                  float* __restrict__ sfeatures, StepIO io) {
     constexpr int L = LanesPerTarget<SM>::L;
@@ -552,7 +600,7 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
 
         // Phase A. The density pass recorded each target's accepted candidates per chunk, in visit
         // order; the lists are built from those masks (RB chunk records loaded per batch).
-        const uint32_t nct = active ? nb_count[s] : 0u;
+        const uint32_t nct = active ? nb_count[row] : 0u;
         const bool recorded = !__ballot(nct > MAXC);
         constexpr int RB = 2;  // chunk records loaded per batch
         for (uint32_t cb = 0; recorded && __ballot(cb < nct); cb += RB) {
@@ -560,7 +608,12 @@ __global__ __launch_bounds__(64) void k_perceive(StepParams P, const float4* __r
 #pragma unroll
             for (int u = 0; u < RB; ++u) {
                 const uint32_t c = cb + (uint32_t)u;
-                rc[u] = c < nct ? nb_chunks[(uint64_t)c * P.T + s] : make_uint4(0u, 0u, 0u, 0u);
+                if (c < nct) {
+                    const uint64_t mk = nb_mask[(uint64_t)row * MAXC + c];
+                    rc[u] = make_uint4(nb_base[(uint64_t)row * MAXC + c], 0u, (uint32_t)mk, (uint32_t)(mk >> 32));
+                } else {
+                    rc[u] = make_uint4(0u, 0u, 0u, 0u);
+                }
             }
 #pragma unroll
             for (int u = 0; u < RB; ++u) {
@@ -1215,24 +1268,6 @@ __global__ __launch_bounds__(256) void k_neighbor_lists(StepParams P, const floa
 
 // ------------------------------------------------------------------ launch
 #if NPA_PART_MAIN
-template <int D, int L>
-static hipError_t launch_density_t(const StepParams& p, Workspace& ws, float* density_out, int blocks,
-                                   hipStream_t stream, Profiler* prof) {
-    return launch_timed(prof, NPA_KERNEL_DENSITY, k_density<D, L>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
-                       ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
-                       ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.svol.as<float4>(), density_out,
-                       ws.nb_chunks.as<uint4>(), ws.nb_count.as<uint32_t>());
-}
-
-template <int D>
-static hipError_t launch_density_d(const StepParams& p, Workspace& ws, float* density_out, int blocks,
-                                   hipStream_t stream, Profiler* prof) {
-    const uint32_t L = lanes_per_target(p.SS);
-    if (L == 1) return launch_density_t<D, 1>(p, ws, density_out, blocks, stream, prof);
-    if (L == 2) return launch_density_t<D, 2>(p, ws, density_out, blocks, stream, prof);
-    return launch_density_t<D, 4>(p, ws, density_out, blocks, stream, prof);
-}
-
 static StepParams with_directory(const StepParams& p, const Workspace& ws) {
     StepParams q = p;
     q.dir_n = ws.dir_n.as<uint32_t>();
@@ -1249,12 +1284,15 @@ hipError_t launch_density(const StepParams& p_in, Workspace& ws, float* density_
         auto k = p.g.dim == 2 ? k_density_sparse<2> : k_density_sparse<3>;
         return launch_timed(prof, NPA_KERNEL_DENSITY, k, dim3((p.T + 255) / 256), dim3(256), 0, stream, p,
                             ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(),
-                            ws.perm.as<uint32_t>(), ws.svol.as<float4>(), density_out, ws.nb_chunks.as<uint4>(),
-                            ws.nb_count.as<uint32_t>());
+                            ws.perm.as<uint32_t>(), ws.row_of.as<uint32_t>(), ws.svol.as<float4>(), density_out,
+                            ws.nb_base.as<uint32_t>(), ws.nb_mask.as<uint64_t>(), ws.nb_count.as<uint32_t>());
     }
-    const int blocks = grid_blocks * 4;  // one wave per block
-    return p.g.dim == 2 ? launch_density_d<2>(p, ws, density_out, blocks, stream, prof)
-                        : launch_density_d<3>(p, ws, density_out, blocks, stream, prof);
+    auto k = p.g.dim == 2 ? k_density_q<2> : k_density_q<3>;  // four waves per block, a wave per item
+    return launch_timed(prof, NPA_KERNEL_DENSITY, k, dim3(grid_blocks), dim3(256), 0, stream, p, ws.srec.as<float4>(),
+                        ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
+                        ws.row_of.as<uint32_t>(), ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(),
+                        ws.svol.as<float4>(), density_out, ws.nb_base.as<uint32_t>(), ws.nb_mask.as<uint64_t>(),
+                        ws.nb_count.as<uint32_t>());
 }
 
 #endif  // NPA_PART_MAIN
@@ -1265,8 +1303,8 @@ static hipError_t launch_perceive_f(const StepParams& p, Workspace& ws, const St
     return launch_timed(prof, NPA_KERNEL_PERCEIVE, k_perceive<D, SM, MODE, FL>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
                        ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.svol.as<float4>(),
                        ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), ws.act_rows.as<uint32_t>(),
-                       ws.wl_count.as<uint32_t>() + 3, ws.nb_chunks.as<uint4>(), ws.nb_count.as<uint32_t>(),
-                       ws.features.as<float>(), io);
+                       ws.wl_count.as<uint32_t>() + 3, ws.nb_base.as<uint32_t>(), ws.nb_mask.as<uint64_t>(),
+                       ws.nb_count.as<uint32_t>(), ws.features.as<float>(), io);
 }
 
 // The rollout step's usual option sets run a specialised kernel; anything else reads the flags.

@@ -179,7 +179,8 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
                                                        const uint32_t* __restrict__ perm,
                                                        const uint32_t* __restrict__ act_rows,
                                                        const uint32_t* __restrict__ row_count,
-                                                       const uint4* __restrict__ nb_chunks,
+                                                       const uint32_t* __restrict__ nb_base,
+                                                       const uint64_t* __restrict__ nb_mask,
                                                        const uint32_t* __restrict__ nb_count,
                                                        const float* __restrict__ wfused, StepIO io) {
     using Sh = FuseShape<D, FL>;
@@ -235,8 +236,13 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
         int ci[3];
         load_rec<D>(srec, scoord, s, pi, ci);
         const float si = sstate[(uint64_t)s * 16 + c];
-        const uint32_t nct = active ? nb_count[s] : 0u;
-        const uint4 rb0 = nb_chunks[(uint64_t)c * P.T + s];  // the first 16 chunk records (16 <= max_chunks)
+        // the target's chunk records (contiguous per compact row); lane c holds chunk c (16 <= max_chunks)
+        const uint32_t rrow = active ? row : item * 4;
+        const uint32_t nct = active ? nb_count[rrow] : 0u;
+        const uint32_t* rbase = nb_base + (uint64_t)rrow * MAXC;
+        const uint64_t* rmask = nb_mask + (uint64_t)rrow * MAXC;
+        const uint32_t base0 = rbase[c];
+        const uint64_t mask0 = rmask[c];
         const uint32_t li = perm[s];
         if (item + kFuseWaves < item_end) s_next = slot_of(item + kFuseWaves);
         const uint32_t b = s / P.N;
@@ -418,9 +424,13 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
             // overflow, the chunks that fit are appended, the lists consumed, and the rest follow
             for (uint32_t k0 = 0; __ballot(k0 < nct); k0 += 16) {
                 const bool valid = k0 + c < nct;
-                uint4 rc = rb0;
-                if (k0 > 0) rc = valid ? nb_chunks[(uint64_t)(k0 + c) * P.T + s] : make_uint4(0u, 0u, 0u, 0u);
-                uint64_t m = valid ? ((uint64_t)rc.w << 32) | rc.z : 0ull;
+                uint32_t cbase0 = base0;
+                uint64_t m = mask0;
+                if (k0 > 0 && valid) {
+                    cbase0 = rbase[k0 + c];
+                    m = rmask[k0 + c];
+                }
+                if (!valid) m = 0ull;
                 uint32_t left = (uint32_t)__popcll(m);
                 for (;;) {
                     const uint32_t incl = row_incl_sum(left);
@@ -431,7 +441,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
                         while (m) {
                             const uint32_t bit = (uint32_t)__builtin_ctzll(m);
                             m &= m - 1;
-                            mylist[pos++] = rc.x + bit;
+                            mylist[pos++] = cbase0 + bit;
                         }
                         left = 0;
                     }
@@ -721,8 +731,8 @@ static hipError_t launch_fused_t(const StepParams& p, Workspace& ws, const StepI
     return launch_timed(prof, NPA_KERNEL_UPDATE, k_update_fused<D, FL>, dim3(blocks), dim3(64 * kFuseWaves),
                         (uint32_t)lds, stream, p, ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(),
                         ws.svol.as<float4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
-                        ws.act_rows.as<uint32_t>(), (const uint32_t*)(wl + 3), ws.nb_chunks.as<uint4>(),
-                        ws.nb_count.as<uint32_t>(), wfused, io);
+                        ws.act_rows.as<uint32_t>(), (const uint32_t*)(wl + 3), ws.nb_base.as<uint32_t>(),
+                        ws.nb_mask.as<uint64_t>(), ws.nb_count.as<uint32_t>(), wfused, io);
 }
 
 template <int D>
