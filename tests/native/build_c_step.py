@@ -1,0 +1,23 @@
+"""Builds tests/native/c_step, the C caller of libnpa_hip.so (gcc, linked against the in-tree
+library with an rpath to it)."""
+from __future__ import annotations
+
+import os
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+OUT = os.path.join(HERE, "c_step")
+
+
+def build(out: str = OUT) -> str:
+    lib_dir = os.path.join(ROOT, "burn_automata_amd")
+    rpath = os.path.relpath(lib_dir, os.path.dirname(os.path.abspath(out)))
+    subprocess.run(["gcc", "-O2", "-std=c11", "-Wall", "-Wextra", "-o", out, os.path.join(HERE, "c_step.c"),
+                    "-L" + lib_dir, "-lnpa_hip", "-Wl,-rpath,$ORIGIN/" + rpath],
+                   check=True, capture_output=True, text=True)
+    return out
+
+
+if __name__ == "__main__":
+    print(build())
