@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <initializer_list>
 #include <mutex>
@@ -39,6 +40,8 @@ struct npa_context {
     void* scratch = nullptr;
     hipError_t scratch_err = hipSuccess;
     npa::Workspace scratch_flags;
+    // the caller's handle plus one per live npa_state: a state keeps its context until it is destroyed
+    std::atomic<int> refs{1};
     ~npa_context() {
         ws.release();
         splat_ws.release();
@@ -360,11 +363,21 @@ npa_status npa_context_create(int device, void* stream, npa_context** out) {
     return NPA_OK;
 }
 
+namespace {
+// Drops one reference; the last one waits for the context's queued work and frees it.
+void context_release(npa_context* ctx) {
+    if (ctx->refs.fetch_sub(1) != 1) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    delete ctx;
+}
+}  // namespace
+
 void npa_context_destroy(npa_context* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    delete ctx;
+    context_release(ctx);
 }
 
 npa_status npa_context_set_stream(npa_context* ctx, void* stream) {
@@ -1100,15 +1113,18 @@ npa_status npa_state_create(npa_context* ctx, const npa_model_cfg* model, const 
         delete s;
         return hip_fail(ctx, e, "state create");
     }
+    ctx->refs.fetch_add(1);
     *out = s;
     return NPA_OK;
 }
 
 void npa_state_destroy(npa_state* s) {
     if (!s) return;
-    (void)hipSetDevice(s->ctx->device);
-    (void)hipStreamSynchronize(s->ctx->stream);
+    npa_context* ctx = s->ctx;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
     delete s;
+    context_release(ctx);
 }
 
 npa_status npa_state_step(npa_state* s, uint32_t steps) {

@@ -314,7 +314,7 @@ hipError_t launch_pad_weights(const StepParams& p, const float* w1, const float*
 hipError_t launch_pad_weights_fused(const StepParams& p, const float* w1, const float* b1, const float* w2,
                                     const float* b2, float* wf, hipStream_t stream);
 // The fused second pass + update MLP + Euler step (npa_update.hip) for 16-wide sorted rows,
-// H <= 128 and the VALU engine; wfused = the fused layout of the padded weights.
+// H <= 128, either MLP engine; wfused = the fused layout of the padded weights.
 bool fused_update_applies(const StepParams& p);
 hipError_t launch_update_fused_2d(const StepParams& p, Workspace& ws, const StepIO& io, const float* wfused,
                                   hipStream_t stream, Profiler* prof);

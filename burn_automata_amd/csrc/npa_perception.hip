@@ -1341,7 +1341,7 @@ size_t valu_weight_floats(const StepParams& p) {
 size_t padded_weight_floats(const StepParams& p) { return valu_weight_floats(p) + fused_weight_floats(p); }
 
 bool fused_update_applies(const StepParams& p) {
-    return p.SS == 16 && p.H <= 128 && p.mlp_engine == NPA_MLP_VALU && (uint64_t)p.T * 64 < (1ull << 32);
+    return p.SS == 16 && p.H <= 128 && (uint64_t)p.T * 64 < (1ull << 32);
 }
 
 hipError_t launch_pad_weights(const StepParams& p, const float* w1, const float* b1, const float* w2,
@@ -1407,7 +1407,7 @@ static hipError_t launch_mlp_d(const StepParams& p, Workspace& ws, const StepIO&
 }
 
 // Second pass, then (mode 0) the update MLP, for one dimension; the rollout step's usual shape
-// (16-wide rows, H <= 128, VALU engine) runs both in the fused kernel.
+// (16-wide rows, H <= 128) runs both in the fused kernel, with either MLP engine.
 template <int D>
 static hipError_t launch_second_pass(const StepParams& p, Workspace& ws, const StepIO& io, int mode, int blocks,
                                      hipStream_t stream, Profiler* prof) {

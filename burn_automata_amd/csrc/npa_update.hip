@@ -15,22 +15,25 @@
 // slots ascending: the reference's for_each_neighbor order) from the density pass's per-chunk
 // accept masks, or, for a target with more chunks than were recorded, by testing the candidates
 // here. The list is consumed in rounds of 16 entries: lane c computes the pair scalars of entry c
-// (poly6, volume, spiky gradient, moment terms) once and stages them in LDS; every lane then adds
-// the round's 16 entries in list order to its own channel, reading the entry's scalars back with
-// one broadcast load and the neighbour's channel from the sorted state rows. The per-target sums
+// (poly6, volume, spiky gradient, moment terms) once; every lane then adds the round's 16 entries in
+// list order to its own channel, reading the entry's scalars from lane e of its 16-lane row through
+// DPP row_newbcast inside each multiply (the generic option set stages them in LDS instead) and the
+// neighbour's channel from the sorted state rows. The per-target sums
 // that are not per channel (moment matrix, density gradient) are summed by lane k for component k
 // from a component-major copy of the round's terms. Padding entries (a short last round) use the
 // target itself with zero weights. Every sum therefore adds the reference's terms in the reference's
 // order, with the same roundings, and +0.0 terms that change nothing (each sum starts at +0.0).
 //
-// After the walk the feature row (state, blur, gradient, density gradient, position) is staged in
-// LDS; lane j of a target computes hidden units j, j + 16, ..., j + 112 (bias first, then features
-// in index order), the hidden activations go back to LDS, and lane c sums output D + c (its state
-// channel's update) and, for c < D, motion output c, hidden units in index order. Lane 0 writes the
+// After the walk, lane l of the wave computes hidden units l and l + 64 of its four targets (bias
+// first, then features in index order) and the hidden activations go to LDS; then lane c of a target
+// sums output D + c (its state channel's update) and, for c < D, motion output c, hidden units in
+// index order. The VALU engine rounds every product and sum as the reference does; the matrix-core
+// engine (v_mfma_f32_4x4x1f32, same mapping, same order) fuses each multiply-add. Lane 0 writes the
 // position, every lane its state channel.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <utility>
 
 #include "npa_internal.hpp"
 #include "npa_neighbors.hpp"
@@ -170,7 +173,44 @@ __device__ __forceinline__ uint32_t row_last(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x150 + 15, 0xf, 0xf, false);
 }
 
-template <int D, int FL>
+// One list entry of a round applied to this lane's channel: the entry's pair scalars live in lane E
+// of the 16-lane row (the target's group), and each product reads them through DPP row_newbcast:E
+// inside the multiply, so no LDS round trip and no extra instruction:
+//   t0 = w[E] * x, t1 = vg0[E] * diff, t2 = vg1[E] * diff (, t3 = vg2[E] * diff).
+// A DPP source must not have been written by the previous two VALU instructions (five after an
+// EXEC write): the s_nop provides those wait states, since the compiler does not see inside asm.
+template <int E, int D>
+__device__ __forceinline__ void bcast_products(float w, float g0, float g1, float g2, float x, float diff, float& t0,
+                                               float& t1, float& t2, float& t3) {
+    if constexpr (D == 2) {
+        asm volatile("s_nop %c8\n\t"
+                     "v_mul_f32_dpp %0, %3, %6 row_newbcast:%c9 row_mask:0xf bank_mask:0xf\n\t"
+                     "v_mul_f32_dpp %1, %4, %7 row_newbcast:%c9 row_mask:0xf bank_mask:0xf\n\t"
+                     "v_mul_f32_dpp %2, %5, %7 row_newbcast:%c9 row_mask:0xf bank_mask:0xf"
+                     : "=&v"(t0), "=&v"(t1), "=&v"(t2)
+                     : "v"(w), "v"(g0), "v"(g1), "v"(x), "v"(diff), "n"(E == 0 ? 4 : 1), "n"(E));
+        t3 = 0.0f;
+        (void)g2;
+    } else {
+        asm volatile("s_nop %c10\n\t"
+                     "v_mul_f32_dpp %0, %4, %8 row_newbcast:%c11 row_mask:0xf bank_mask:0xf\n\t"
+                     "v_mul_f32_dpp %1, %5, %9 row_newbcast:%c11 row_mask:0xf bank_mask:0xf\n\t"
+                     "v_mul_f32_dpp %2, %6, %9 row_newbcast:%c11 row_mask:0xf bank_mask:0xf\n\t"
+                     "v_mul_f32_dpp %3, %7, %9 row_newbcast:%c11 row_mask:0xf bank_mask:0xf"
+                     : "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+                     : "v"(w), "v"(g0), "v"(g1), "v"(g2), "v"(x), "v"(diff), "n"(E == 0 ? 4 : 1), "n"(E));
+    }
+}
+
+template <typename F, int... E>
+__device__ __forceinline__ void for_each_entry(F&& f, std::integer_sequence<int, E...>) {
+    (f(std::integral_constant<int, E>{}), ...);
+}
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// ENG: 0 = VALU, the reference's roundings (bit-exact); 1 = the MLP on the fp32 matrix cores.
+template <int D, int FL, int ENG>
 __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float4* __restrict__ srec,
                                                        const int4* __restrict__ scoord,
                                                        const float* __restrict__ sstate,
@@ -311,9 +351,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
                 }
                 const float w = smooth * vol;  // blur_state weight (density-grad-off branch)
                 float* my = stage + c * SREC;
-                if constexpr (SREC == 4) {
-                    *reinterpret_cast<float4*>(my) = make_float4(w, vg[0], vg[1], vg[2]);
-                } else {
+                if constexpr (SREC == 8) {  // (four floats per entry travel by DPP broadcast instead)
                     *reinterpret_cast<float4*>(my) = make_float4(branch_a ? smooth : w, vol, vg[0], vg[1]);
                     *reinterpret_cast<float4*>(my + 4) = make_float4(vg[2], 0.0f, 0.0f, 0.0f);
                 }
@@ -333,6 +371,31 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
                 rj = svol[en];  // the next round's entry
                 wave_sync();
                 // the round's entries in list order
+                if constexpr (SREC == 4) {
+                    uint32_t nslot[16];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint4 nx = reinterpret_cast<const uint4*>(lpn)[q];
+                        nslot[4 * q] = nx.x;
+                        nslot[4 * q + 1] = nx.y;
+                        nslot[4 * q + 2] = nx.z;
+                        nslot[4 * q + 3] = nx.w;
+                    }
+                    for_each_entry(
+                        [&](auto ic) {
+                            constexpr int e = decltype(ic)::value;
+                            const float x = sv[e];
+                            const float diff = x - si;
+                            float t0, t1, t2, t3;
+                            bcast_products<e, D>(w, vg[0], vg[1], vg[2], x, diff, t0, t1, t2, t3);
+                            blur += t0;  // blur_state forward.rs:174-180 (x * w)
+                            gr[0] += t1;  // compute_state_gradient forward.rs:297-333 (diff * grad)
+                            gr[1] += t2;
+                            if constexpr (D == 3) gr[2] += t3;
+                            sv[e] = load_sv(nslot[e]);
+                        },
+                        std::make_integer_sequence<int, 16>{});
+                } else {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const uint4 nx = reinterpret_cast<const uint4*>(lpn)[q];
@@ -343,15 +406,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
                         const float* re = stage + e * SREC;
                         const float4 r0 = *reinterpret_cast<const float4*>(re);
                         const float x = sv[e];
-                        if constexpr (SREC == 4) {
-                            blur += x * r0.x;  // blur_state forward.rs:174-180
-                            if (want_sg) {
-                                const float diff = x - si;
-                                gr[0] += diff * r0.y;
-                                gr[1] += diff * r0.z;
-                                if constexpr (D == 3) gr[2] += diff * r0.w;
-                            }
-                        } else {
+                        {
                             if (branch_a) blur += x * r0.x * r0.y;  // second_pass_particle forward.rs:263-270
                             else blur += x * r0.x;
                             if (want_sg) {
@@ -363,6 +418,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
                         }
                         sv[e] = load_sv(nslot[i]);
                     }
+                }
                 }
                 {
                     const float4* xp = reinterpret_cast<const float4*>(ext + xcomp * Sh::XSTR);
@@ -587,6 +643,78 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
         // of target t is read from the lane that holds it into a scalar register. Every sum starts
         // from its bias and adds the features in index order.
         constexpr uint32_t KB_FIXED = (32 + 16 * D) / 4;  // blocks of four state/blur/gradient features
+        float* hw = wl + 4 * (FP + 4);  // hidden activations [target][HSTR]
+        float us, um;
+        if constexpr (ENG == 1) {
+            // Matrix-core engine (v_mfma_f32_4x4x1f32, 16 blocks of 4x4 with K = 1: lane l supplies
+            // A[l / 4][l % 4] and B[l / 4][l % 4] and holds D[l / 4][r][l % 4] in accumulator r).
+            // Layer 1: block b = hidden units 4b..4b+3, A = the four targets' feature k (lane l feeds
+            // target l % 4), B = unit l's weight for feature k; lane l ends with unit l of targets
+            // 0..3, the VALU mapping. One product per instruction, features in index order from the
+            // bias, so the sums differ from the reference's only by the fused multiply-add rounding.
+            float* fr = wl + g * (FP + 4);  // this target's feature row
+            fr[c] = si;
+            fr[16 + c] = blur;
+#pragma unroll
+            for (int a = 0; a < D; ++a) fr[32 + c * D + a] = gf[a];
+            if (c == 0) {
+#pragma unroll
+                for (uint32_t k = 0; k < 8; ++k)
+                    if (4 * KB_FIXED + k < FP) fr[4 * KB_FIXED + k] = rest[k];
+            }
+            wave_sync();
+            const float* myf = wl + (lane & 3u) * (FP + 4);
+            const float bb0 = b1[lane], bb1 = b1[lane + 64];
+            v4f a0 = {bb0, bb0, bb0, bb0}, a1 = {bb1, bb1, bb1, bb1};
+            auto mfma_block = [&](uint32_t kb) {
+                const float4 f4 = *reinterpret_cast<const float4*>(myf + 4 * kb);
+                const float4 w0 = *reinterpret_cast<const float4*>(w1q + ((size_t)kb * HP + lane) * 4);
+                const float4 w1 = *reinterpret_cast<const float4*>(w1q + ((size_t)kb * HP + lane + 64) * 4);
+                a0 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.x, w0.x, a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.x, w1.x, a1, 0, 0, 0);
+                a0 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.y, w0.y, a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.y, w1.y, a1, 0, 0, 0);
+                a0 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.z, w0.z, a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.z, w1.z, a1, 0, 0, 0);
+                a0 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.w, w0.w, a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.w, w1.w, a1, 0, 0, 0);
+            };
+#pragma unroll
+            for (uint32_t kb = 0; kb < KB_FIXED; ++kb) mfma_block(kb);
+            if (FP / 4 > KB_FIXED) mfma_block(KB_FIXED);
+            if (FP / 4 > KB_FIXED + 1) mfma_block(KB_FIXED + 1);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                hw[t * Sh::HSTR + lane] = fmaxf(a0[t], 0.0f);
+                hw[t * Sh::HSTR + lane + 64] = fmaxf(a1[t], 0.0f);
+            }
+            wave_sync();
+            // Layer 2: block b = outputs 4b..4b+3 (blocks past OPAD / 4 compute copies of the last
+            // output and are dropped), A = the four targets' hidden unit k, B = output l's weight
+            // for unit k; lane l < OPAD ends with output l of targets 0..3.
+            const uint32_t lo = lane < OPAD ? lane : OPAD - 1;
+            const float* myh = hw + (lane & 3u) * Sh::HSTR;
+            const float bo2 = b2[lo];
+            v4f u2 = {bo2, bo2, bo2, bo2};
+#pragma unroll 8
+            for (uint32_t hb = 0; hb < HP / 4; ++hb) {
+                const float4 h4 = *reinterpret_cast<const float4*>(myh + 4 * hb);
+                const float4 w4 = *reinterpret_cast<const float4*>(w2q + ((size_t)hb * OPAD + lo) * 4);
+                u2 = __builtin_amdgcn_mfma_f32_4x4x1f32(h4.x, w4.x, u2, 0, 0, 0);
+                u2 = __builtin_amdgcn_mfma_f32_4x4x1f32(h4.y, w4.y, u2, 0, 0, 0);
+                u2 = __builtin_amdgcn_mfma_f32_4x4x1f32(h4.z, w4.z, u2, 0, 0, 0);
+                u2 = __builtin_amdgcn_mfma_f32_4x4x1f32(h4.w, w4.w, u2, 0, 0, 0);
+            }
+            // outputs [target][OPAD + 1] over the feature rows (read before the hidden rows were written)
+            float* uo = wl;
+            if (lane < OPAD) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) uo[t * (OPAD + 1) + lane] = u2[t];
+            }
+            wave_sync();
+            us = uo[g * (OPAD + 1) + D + c];
+            um = uo[g * (OPAD + 1) + (c < D ? c : 0u)];
+        } else {
         float h0[4], h1[4];
         {
             const float bb0 = b1[lane], bb1 = b1[lane + 64];
@@ -637,17 +765,15 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
             mac_block(KB_FIXED + 1, [&](int i, int t) {
                 return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rest[4 + i]), 16 * t));
             });
-        {
-            float* hw = wl + 4 * (FP + 4);  // [target][HSTR]
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                hw[t * Sh::HSTR + lane] = fmaxf(h0[t], 0.0f);
-                hw[t * Sh::HSTR + lane + 64] = fmaxf(h1[t], 0.0f);
-            }
+        for (int t = 0; t < 4; ++t) {
+            hw[t * Sh::HSTR + lane] = fmaxf(h0[t], 0.0f);
+            hw[t * Sh::HSTR + lane + 64] = fmaxf(h1[t], 0.0f);
         }
         wave_sync();
         // outputs: state update D + c and motion output c (lanes c < D)
-        float us = b2[D + c], um = b2[c];
+        us = b2[D + c];
+        um = b2[c];
 #pragma unroll 4
         for (uint32_t hb = 0; hb < HP / 4; ++hb) {
             const float4 h4 = *reinterpret_cast<const float4*>(hg + 4 * hb);
@@ -661,6 +787,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
             um += wm4.y * h4.y;
             um += wm4.z * h4.z;
             um += wm4.w * h4.w;
+        }
         }
         wave_sync();  // the region is refilled by the next item
 
@@ -710,7 +837,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
     }
 }
 
-template <int D, int FL>
+template <int D, int FL, int ENG>
 static hipError_t launch_fused_t(const StepParams& p, Workspace& ws, const StepIO& io, const float* wfused,
                                  hipStream_t stream, Profiler* prof) {
     using Sh = FuseShape<D, FL>;
@@ -718,7 +845,7 @@ static hipError_t launch_fused_t(const StepParams& p, Workspace& ws, const StepI
     if (lds > kFuseLdsBytes) return hipErrorInvalidValue;
     static bool attr = false;
     if (!attr) {
-        const hipError_t e = hipFuncSetAttribute((const void*)k_update_fused<D, FL>,
+        const hipError_t e = hipFuncSetAttribute((const void*)k_update_fused<D, FL, ENG>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFuseLdsBytes);
         if (e != hipSuccess) return e;
         attr = true;
@@ -728,7 +855,7 @@ static hipError_t launch_fused_t(const StepParams& p, Workspace& ws, const StepI
     const uint32_t blocks = (uint32_t)std::max<uint64_t>(
         1, std::min<uint64_t>((uint64_t)device_cu_count(), (max_items + kFuseWaves - 1) / kFuseWaves));
     uint32_t* wl = ws.wl_count.as<uint32_t>();
-    return launch_timed(prof, NPA_KERNEL_UPDATE, k_update_fused<D, FL>, dim3(blocks), dim3(64 * kFuseWaves),
+    return launch_timed(prof, NPA_KERNEL_UPDATE, k_update_fused<D, FL, ENG>, dim3(blocks), dim3(64 * kFuseWaves),
                         (uint32_t)lds, stream, p, ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(),
                         ws.svol.as<float4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
                         ws.act_rows.as<uint32_t>(), (const uint32_t*)(wl + 3), ws.nb_base.as<uint32_t>(),
@@ -738,8 +865,12 @@ static hipError_t launch_fused_t(const StepParams& p, Workspace& ws, const StepI
 template <int D>
 static hipError_t launch_fused_d(const StepParams& p, Workspace& ws, const StepIO& io, const float* wfused,
                                  hipStream_t stream, Profiler* prof) {
-    if (p.state_grad && p.hybrid && !p.density_grad) return launch_fused_t<D, 5>(p, ws, io, wfused, stream, prof);
-    return launch_fused_t<D, -1>(p, ws, io, wfused, stream, prof);
+    const bool common = p.state_grad && p.hybrid && !p.density_grad;
+    if (p.mlp_engine == NPA_MLP_MFMA)
+        return common ? launch_fused_t<D, 5, 1>(p, ws, io, wfused, stream, prof)
+                      : launch_fused_t<D, -1, 1>(p, ws, io, wfused, stream, prof);
+    return common ? launch_fused_t<D, 5, 0>(p, ws, io, wfused, stream, prof)
+                  : launch_fused_t<D, -1, 0>(p, ws, io, wfused, stream, prof);
 }
 
 #if NPA_PART_DIM2

@@ -171,6 +171,8 @@ typedef struct npa_state npa_state;
 /* Creates a context bound to HIP device `device`. `stream` is a hipStream_t
  * (may be NULL for the legacy default stream); the context never destroys it. */
 npa_status npa_context_create(int device, void* stream, npa_context** out);
+/* Ends the caller's use of ctx. States created on it keep it (and its stream) alive: the context's
+ * memory is released when the last of them is destroyed, in either order. */
 void npa_context_destroy(npa_context* ctx);
 npa_status npa_context_set_stream(npa_context* ctx, void* stream);
 /* 0: array arguments are device pointers (default). 1: host pointers, synchronous. */

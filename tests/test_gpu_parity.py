@@ -282,6 +282,23 @@ def test_executor_rollout_64_steps(ctx, name):
     np.testing.assert_array_equal(to_np(gs), want_s)
 
 
+def test_state_outlives_its_context():
+    """A state keeps its context alive: the state still steps and reads after the caller destroyed
+    the context, and destroying the state last releases both (no use of freed memory)."""
+    from burn_automata_amd._lib import lib
+    from burn_automata_amd.runtime import Context
+    m, g, pos, st, w, b, n = _model_case("c1")
+    c = Context(0)
+    ex = HipAutomataExecutor(ctx=c)
+    state = ex.create_state(NpaModel(m, w), pos, st, b, n, g, 1.0, 0.5, 42)
+    ex.step_state(state)
+    want_p, want_s, _ = ex.read_state(state)
+    c.close()
+    assert lib().npa_state_step(state.handle, 1) == 0
+    state.close()
+    assert want_p.shape[0] == b * n and np.isfinite(to_np(want_s)).all()
+
+
 def test_executor_single_steps_match_fused_step(ctx):
     m, g, pos, st, w, b, n = _model_case("c1")
     ex = HipAutomataExecutor(ctx=ctx)
