@@ -497,6 +497,8 @@ def main(argv=None) -> int:
                     help="update MLP on the vector ALUs in the reference's order (bit-exact, default) "
                          "or on the fp32 matrix cores (single-step tolerance)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-alt-engine", action="store_true",
+                    help="skip the matrix-core engine's run beside the headline")
     ap.add_argument("--no-profile", action="store_true",
                     help="skip the HIP-event bracketing of the per-step kernels")
     ap.add_argument("--skip-replay", action="store_true",
@@ -649,6 +651,29 @@ def main(argv=None) -> int:
     elapsed_steps = elapsed
     elapsed = elapsed_steps + owed * (decode_ms or 0.0) * 1e-3
 
+    # The same steps on the matrix-core MLP engine, reported beside the headline (which stays on
+    # the bit-exact engine): that engine meets the single-step gate but not the 64-step one.
+    alt = None
+    if args.mlp_engine == "valu" and not args.no_alt_engine:
+        engine_saved = engine
+        engine = _abi.MLP_MFMA
+        aw = new_state()
+        run(aw, min(args.warmup, 4) or 1)
+        aw.close()
+        astate = new_state()
+        torch.cuda.synchronize()
+        ta0 = time.perf_counter()
+        run(astate, args.steps)
+        torch.cuda.synchronize()
+        alt_elapsed = time.perf_counter() - ta0 + owed * (decode_ms or 0.0) * 1e-3
+        astate.close()
+        engine = engine_saved
+        alt = {"mlp_engine": "mfma", "value": B * N * args.steps / alt_elapsed,
+               "ms_per_step": 1000.0 * alt_elapsed / args.steps,
+               "gates": "single step within 1e-5 of the reference (tests/test_gpu_mfma.py); not the "
+                        "64-step 1e-3 gate: the rollout is chaotic and the reference itself, started "
+                        "one ulp away, drifts as far (same test file)"}
+
     # exact work counts of the timed trajectory (untimed replay of the same steps)
     keys = ("candidates", "pairs", "targets", "target_candidates", "target_pairs")
     sums = dict.fromkeys(keys, 0)
@@ -704,6 +729,8 @@ def main(argv=None) -> int:
                    "steps_wall_ms": 1000.0 * elapsed_steps,
                    "note": "value and ms_per_step include the owed decodes at ms_per_decode each"},
     }
+    if alt is not None:
+        line["alt_engine"] = alt
     if kernel_ms:
         line["kernel_mean_launch_ms"] = kernel_ms  # untimed instrumented pass of the same steps
     if kernel_ms and not args.skip_replay:

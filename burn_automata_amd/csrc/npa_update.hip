@@ -28,8 +28,8 @@
 // first, then features in index order) and the hidden activations go to LDS; then lane c of a target
 // sums output D + c (its state channel's update) and, for c < D, motion output c, hidden units in
 // index order. The VALU engine rounds every product and sum as the reference does; the matrix-core
-// engine (v_mfma_f32_4x4x1f32, same mapping, same order) fuses each multiply-add. Lane 0 writes the
-// position, every lane its state channel.
+// engine (v_mfma_f32_4x4x1f32, same mapping) fuses each multiply-add and splits each sum into
+// independent chains. Lane 0 writes the position, every lane its state channel.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -650,8 +650,8 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
             // A[l / 4][l % 4] and B[l / 4][l % 4] and holds D[l / 4][r][l % 4] in accumulator r).
             // Layer 1: block b = hidden units 4b..4b+3, A = the four targets' feature k (lane l feeds
             // target l % 4), B = unit l's weight for feature k; lane l ends with unit l of targets
-            // 0..3, the VALU mapping. One product per instruction, features in index order from the
-            // bias, so the sums differ from the reference's only by the fused multiply-add rounding.
+            // 0..3, the VALU mapping. The products are fused into the sums and the sums are split
+            // into independent chains, so the result differs from the reference's in the last bits.
             float* fr = wl + g * (FP + 4);  // this target's feature row
             fr[c] = si;
             fr[16 + c] = blur;
@@ -664,20 +664,23 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
             }
             wave_sync();
             const float* myf = wl + (lane & 3u) * (FP + 4);
+            // Two independent accumulators per unit (even and odd feature pairs) keep four MFMA chains
+            // in flight; they are added at the end, so this engine's sums are not in index order.
             const float bb0 = b1[lane], bb1 = b1[lane + 64];
             v4f a0 = {bb0, bb0, bb0, bb0}, a1 = {bb1, bb1, bb1, bb1};
+            v4f c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = {0.0f, 0.0f, 0.0f, 0.0f};
             auto mfma_block = [&](uint32_t kb) {
                 const float4 f4 = *reinterpret_cast<const float4*>(myf + 4 * kb);
                 const float4 w0 = *reinterpret_cast<const float4*>(w1q + ((size_t)kb * HP + lane) * 4);
                 const float4 w1 = *reinterpret_cast<const float4*>(w1q + ((size_t)kb * HP + lane + 64) * 4);
                 a0 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.x, w0.x, a0, 0, 0, 0);
                 a1 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.x, w1.x, a1, 0, 0, 0);
-                a0 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.y, w0.y, a0, 0, 0, 0);
-                a1 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.y, w1.y, a1, 0, 0, 0);
+                c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.y, w0.y, c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.y, w1.y, c1, 0, 0, 0);
                 a0 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.z, w0.z, a0, 0, 0, 0);
                 a1 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.z, w1.z, a1, 0, 0, 0);
-                a0 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.w, w0.w, a0, 0, 0, 0);
-                a1 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.w, w1.w, a1, 0, 0, 0);
+                c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.w, w0.w, c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(f4.w, w1.w, c1, 0, 0, 0);
             };
 #pragma unroll
             for (uint32_t kb = 0; kb < KB_FIXED; ++kb) mfma_block(kb);
@@ -685,8 +688,8 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
             if (FP / 4 > KB_FIXED + 1) mfma_block(KB_FIXED + 1);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                hw[t * Sh::HSTR + lane] = fmaxf(a0[t], 0.0f);
-                hw[t * Sh::HSTR + lane + 64] = fmaxf(a1[t], 0.0f);
+                hw[t * Sh::HSTR + lane] = fmaxf(a0[t] + c0[t], 0.0f);
+                hw[t * Sh::HSTR + lane + 64] = fmaxf(a1[t] + c1[t], 0.0f);
             }
             wave_sync();
             // Layer 2: block b = outputs 4b..4b+3 (blocks past OPAD / 4 compute copies of the last
@@ -695,16 +698,18 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
             const uint32_t lo = lane < OPAD ? lane : OPAD - 1;
             const float* myh = hw + (lane & 3u) * Sh::HSTR;
             const float bo2 = b2[lo];
-            v4f u2 = {bo2, bo2, bo2, bo2};
+            v4f u2 = {bo2, bo2, bo2, bo2};  // four chains over the units 4 hb + i, summed at the end
+            v4f u3 = {0.0f, 0.0f, 0.0f, 0.0f}, u4 = u3, u5 = u3;
 #pragma unroll 8
             for (uint32_t hb = 0; hb < HP / 4; ++hb) {
                 const float4 h4 = *reinterpret_cast<const float4*>(myh + 4 * hb);
                 const float4 w4 = *reinterpret_cast<const float4*>(w2q + ((size_t)hb * OPAD + lo) * 4);
                 u2 = __builtin_amdgcn_mfma_f32_4x4x1f32(h4.x, w4.x, u2, 0, 0, 0);
-                u2 = __builtin_amdgcn_mfma_f32_4x4x1f32(h4.y, w4.y, u2, 0, 0, 0);
-                u2 = __builtin_amdgcn_mfma_f32_4x4x1f32(h4.z, w4.z, u2, 0, 0, 0);
-                u2 = __builtin_amdgcn_mfma_f32_4x4x1f32(h4.w, w4.w, u2, 0, 0, 0);
+                u3 = __builtin_amdgcn_mfma_f32_4x4x1f32(h4.y, w4.y, u3, 0, 0, 0);
+                u4 = __builtin_amdgcn_mfma_f32_4x4x1f32(h4.z, w4.z, u4, 0, 0, 0);
+                u5 = __builtin_amdgcn_mfma_f32_4x4x1f32(h4.w, w4.w, u5, 0, 0, 0);
             }
+            u2 = (u2 + u3) + (u4 + u5);
             // outputs [target][OPAD + 1] over the feature rows (read before the hidden rows were written)
             float* uo = wl;
             if (lane < OPAD) {
