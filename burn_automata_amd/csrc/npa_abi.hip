@@ -392,9 +392,17 @@ npa_status npa_context_set_host_io(npa_context* ctx, int host_io) {
     return NPA_OK;
 }
 
+namespace {
+// NPA_MLP_AUTO -> the engine for a system of `particles` particles.
+uint32_t resolve_engine(int engine, uint64_t particles) {
+    if (engine == NPA_MLP_AUTO) return particles >= NPA_MLP_AUTO_MIN_PARTICLES ? NPA_MLP_MFMA : NPA_MLP_VALU;
+    return (uint32_t)engine;
+}
+}  // namespace
+
 npa_status npa_context_set_mlp_engine(npa_context* ctx, int engine) {
     if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
-    if (engine != NPA_MLP_VALU && engine != NPA_MLP_MFMA)
+    if (engine != NPA_MLP_VALU && engine != NPA_MLP_MFMA && engine != NPA_MLP_AUTO)
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: unknown MLP engine " + std::to_string(engine));
     ctx->mlp_engine = engine;
     return NPA_OK;
@@ -724,7 +732,7 @@ npa_status npa_step(npa_context* ctx, const float* positions, const float* state
     apply_model(&p, *model, grid->eps);
     p.dt = dt;
     p.update_prob = 1.0f;
-    p.mlp_engine = (uint32_t)ctx->mlp_engine;
+    p.mlp_engine = resolve_engine(ctx->mlp_engine, total);
     if (total && npa::state_stride_for(S) == S && !aligned16(sio.out_states))
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: output states must be 16-byte aligned");
     NPA_HIP(ctx, ctx->ws.reserve(plan, total, B, S, (int)grid->dim, p.FP), "workspace");
@@ -773,7 +781,7 @@ npa_status npa_step_noalloc(npa_context* ctx, const float* positions, const floa
     apply_model(&p, *model, grid->eps);
     p.dt = dt;
     p.update_prob = 1.0f;
-    p.mlp_engine = (uint32_t)ctx->mlp_engine;
+    p.mlp_engine = resolve_engine(ctx->mlp_engine, total);
     npa::Workspace ws;  // views into this device's scratch array
     const uint64_t need_bytes = ws.carve(plan, total, B, S, (int)grid->dim, p.FP, npa::padded_weight_floats(p) * 4,
                                          ctx->scratch, NPA_STEP_NOALLOC_SCRATCH_BYTES);
@@ -1137,7 +1145,7 @@ npa_status npa_state_step(npa_state* s, uint32_t steps) {
     p.dt = s->dt;
     p.update_prob = s->update_prob;
     p.base_seed = base_seed(s->seed);
-    p.mlp_engine = (uint32_t)s->mlp_engine;
+    p.mlp_engine = resolve_engine(s->mlp_engine, (uint64_t)s->B * s->N);
     npa::StepIO io;
     io.w1 = s->w1.as<float>();
     io.b1 = s->b1.as<float>();
@@ -1165,7 +1173,7 @@ npa_status npa_state_step(npa_state* s, uint32_t steps) {
 
 npa_status npa_state_set_mlp_engine(npa_state* s, int engine) {
     if (!s) return NPA_ERR_INVALID_ARGUMENT;
-    if (engine != NPA_MLP_VALU && engine != NPA_MLP_MFMA)
+    if (engine != NPA_MLP_VALU && engine != NPA_MLP_MFMA && engine != NPA_MLP_AUTO)
         return fail(s->ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: unknown MLP engine " + std::to_string(engine));
     s->mlp_engine = engine;
     return NPA_OK;

@@ -8,7 +8,7 @@
 //   Euler step    step.rs:4-55, written to the ping-pong output in original particle order
 //
 // Mapping. Sixteen lanes serve one target, lane c owning state channel c; a wave serves the four
-// targets of one item (four consecutive compact rows); a block takes a contiguous range of items.
+// targets of one item (four consecutive compact rows); items are dealt round-robin over the grid's waves.
 // The 16 waves of a block share the padded MLP weights in LDS.
 //
 // Per target, the accepted neighbours are appended to an LDS list in visit order (cells dz, dy, dx,
@@ -257,17 +257,19 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
     const uint32_t nitems = (nrows + 3) / 4;
     const uint32_t xcomp = c < NX ? c : 0u;  // the per-target sum this lane keeps
 
-    // Items of four consecutive compact rows: block k takes a contiguous range, its waves
-    // interleaved (neighbouring rows share cells, so the CU's L1 serves their neighbours).
-    const uint32_t per_block = (nitems + gridDim.x - 1) / gridDim.x;
-    const uint32_t item_end = min(nitems, (blockIdx.x + 1) * per_block);
+    // Items of four consecutive compact rows, dealt round-robin over every wave of the grid: the
+    // block's 16 waves take 16 consecutive items at a time (neighbouring rows share cells, so the
+    // CU's L1 serves their neighbours), and a run of heavy items (a dense region of the sorted
+    // order) is spread over many CUs instead of landing on one.
+    const uint32_t item_end = nitems;
+    const uint32_t item_stride = gridDim.x * kFuseWaves;
     auto slot_of = [&](uint32_t it) {
         const uint32_t r = it * 4 + g;
         return act_rows[r < nrows ? r : it * 4];
     };
-    uint32_t item = blockIdx.x * per_block + wave;
+    uint32_t item = blockIdx.x * kFuseWaves + wave;
     uint32_t s_next = item < item_end ? slot_of(item) : 0u;  // the next item's slot, loaded one item ahead
-    for (; item < item_end; item += kFuseWaves) {
+    for (; item < item_end; item += item_stride) {
         const uint32_t row = item * 4 + g;
         const bool active = row < nrows;
         const uint32_t s = s_next;
@@ -284,7 +286,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
         const uint32_t base0 = rbase[c];
         const uint64_t mask0 = rmask[c];
         const uint32_t li = perm[s];
-        if (item + kFuseWaves < item_end) s_next = slot_of(item + kFuseWaves);
+        if (item + item_stride < item_end) s_next = slot_of(item + item_stride);
         const uint32_t b = s / P.N;
         const uint32_t i = b * P.N + li;
         const float4 pos4 = io.pos[i];

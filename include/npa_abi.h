@@ -180,10 +180,13 @@ npa_status npa_context_set_host_io(npa_context* ctx, int host_io);
 /* Update-MLP engine of npa_step and of states (no counterpart in the reference, whose MLP is a
  * serial f32 loop). NPA_MLP_VALU (default): every sum in the reference's order on the vector
  * ALUs, bit-identical to the CPU path. NPA_MLP_MFMA: the two dense layers on the fp32 matrix
- * cores (v_mfma_f32_16x16x4_f32), whose accumulation order differs from the reference's: a single
- * step stays within 1e-6 of it, while a rollout drifts apart like under any reordering of the
- * sums (the dynamics amplify last-bit differences). */
-enum { NPA_MLP_VALU = 0, NPA_MLP_MFMA = 1 };
+ * cores (v_mfma_f32_4x4x1f32 in the fused step kernel, v_mfma_f32_16x16x4_f32 otherwise), with
+ * fused products and split sums: a single step stays within 1e-6 of the reference, while a
+ * rollout drifts apart as far as the reference itself does from a one-ulp perturbation of its
+ * inputs (the dynamics amplify last-bit differences). NPA_MLP_AUTO: MFMA for systems of at least
+ * NPA_MLP_AUTO_MIN_PARTICLES particles (B*N), VALU below, the measured crossover on MI355X. */
+enum { NPA_MLP_VALU = 0, NPA_MLP_MFMA = 1, NPA_MLP_AUTO = 2 };
+#define NPA_MLP_AUTO_MIN_PARTICLES 32768u
 npa_status npa_context_set_mlp_engine(npa_context* ctx, int engine);
 
 /* Blocks until all work queued on the context's stream has finished. */
