@@ -260,14 +260,17 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
     // Items of four consecutive compact rows, dealt round-robin over every wave of the grid: the
     // block's 16 waves take 16 consecutive items at a time (neighbouring rows share cells, so the
     // CU's L1 serves their neighbours), and a run of heavy items (a dense region of the sorted
-    // order) is spread over many CUs instead of landing on one.
+    // order) is spread over many CUs instead of landing on one. Blocks are dispatched to the eight
+    // XCDs in turn, so block b is renumbered (b % 8) * (G / 8) + b / 8: each XCD then walks one
+    // contiguous run of G / 8 * 16 items per pass and its L2 holds their neighbour rows once.
     const uint32_t item_end = nitems;
     const uint32_t item_stride = gridDim.x * kFuseWaves;
+    const uint32_t lblock = gridDim.x % 8 == 0 ? (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8 : blockIdx.x;
     auto slot_of = [&](uint32_t it) {
         const uint32_t r = it * 4 + g;
         return act_rows[r < nrows ? r : it * 4];
     };
-    uint32_t item = blockIdx.x * kFuseWaves + wave;
+    uint32_t item = lblock * kFuseWaves + wave;
     uint32_t s_next = item < item_end ? slot_of(item) : 0u;  // the next item's slot, loaded one item ahead
     for (; item < item_end; item += item_stride) {
         const uint32_t row = item * 4 + g;
