@@ -15,8 +15,9 @@
 //   k_table_scan   per key, exclusive prefix over the system's tiles (column scan).
 //   k_offsets_scan per system, exclusive prefix over keys -> bin_offsets.
 //   k_scatter      dst = bin_offsets[key] + table[tile][key] + rank; writes the
-//                  permutation, its inverse and (for the rollout step) the sorted particle
-//                  records and state rows the neighbour passes read.
+//                  permutation and its inverse. The rollout step's k_scatter_payload also
+//                  writes the sorted particle records and state rows the neighbour passes
+//                  read, and k_split then orders the bins that hold several cells by cell.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -419,9 +420,8 @@ __global__ __launch_bounds__(1024) void k_offsets_scan(const uint32_t* __restric
     if (b == batch - 1 && threadIdx.x == 0) bin_offsets[(uint64_t)batch * C] = b * n + all;
 }
 
-// payload == 0: perm (slot -> particle of the system) and inv, the reference's snapshot.
-// payload == 1: out[slot] = global particle index in the reference order; k_split then orders
-// each bin by cell and writes the snapshot and the sorted payload.
+// The reference's snapshot only: perm (slot -> particle of the system) and inv. (The rollout step
+// scatters its whole sorted payload with k_scatter_payload.)
 __global__ __launch_bounds__(256) void k_scatter(uint32_t n, uint32_t total, uint32_t tile,
                                                  uint32_t tiles_per_sys, uint32_t C,
                                                  const uint32_t* __restrict__ keys,
@@ -429,7 +429,7 @@ __global__ __launch_bounds__(256) void k_scatter(uint32_t n, uint32_t total, uin
                                                  const uint32_t* __restrict__ table,
                                                  const uint32_t* __restrict__ bin_offsets,
                                                  uint32_t* __restrict__ out, uint32_t* __restrict__ inv,
-                                                 int payload, uint32_t* __restrict__ flags) {
+                                                 uint32_t* __restrict__ flags) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     // This build's coordinate-overflow flag (set by k_hash_rank, which has finished) moves into the
     // sticky word the synchronising entry points report, so the next build starts clean.
@@ -448,10 +448,6 @@ __global__ __launch_bounds__(256) void k_scatter(uint32_t n, uint32_t total, uin
     const uint32_t dst_local = (bin_offsets[(uint64_t)b * C + key] - b * n) +
                                table[((uint64_t)b * tiles_per_sys + t) * C + key] + ranks[i];
     const uint32_t dst = b * n + dst_local;
-    if (payload) {
-        out[dst] = i;
-        return;
-    }
     out[dst] = li;
     inv[i] = dst_local;
 }
@@ -506,15 +502,63 @@ __device__ __forceinline__ void write_sorted(uint32_t dst, uint32_t i, uint32_t 
     }
 }
 
+// Payload scatter: every particle writes its sorted record, state row and snapshot entries at its
+// slot of the stable counting sort (the reference's order within each bin), and a particle outside
+// the step's update mask is written to the step's output here (hold_particle). k_split keeps this
+// payload for a bin that holds one cell, or more cells than its directory holds (both stay in the
+// reference order), and rewrites the bins whose cells it reorders. out[slot] = global particle index.
+template <int D>
+__global__ __launch_bounds__(256) void k_scatter_payload(uint32_t n, uint32_t total, uint32_t tile,
+                                                         uint32_t tiles_per_sys, uint32_t C,
+                                                         const uint32_t* __restrict__ keys,
+                                                         const uint32_t* __restrict__ ranks,
+                                                         const uint32_t* __restrict__ table,
+                                                         const uint32_t* __restrict__ bin_offsets,
+                                                         uint32_t* __restrict__ out, uint32_t* __restrict__ perm,
+                                                         uint32_t* __restrict__ inv, const float4* __restrict__ pos,
+                                                         const float* __restrict__ states, uint32_t S, GridParams g,
+                                                         float4* __restrict__ srec, int4* __restrict__ scoord,
+                                                         float* __restrict__ sstate, SplitTargets T,
+                                                         uint32_t* __restrict__ flags) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    // this build's coordinate-overflow flag (set by k_hash_rank) moves into the sticky word
+    if (i == 0) {
+        const uint32_t f = flags[0];
+        if (f) {
+            flags[1] |= f;
+            flags[0] = 0;
+        }
+    }
+    if (i >= total) return;
+    const uint32_t b = i / n;
+    const uint32_t li = i - b * n;
+    const float4 p4 = pos[i];  // independent of the slot: in flight while the slot is computed
+    const uint32_t key = keys[i];
+    const uint32_t t = li / tile;
+    const uint32_t dst = bin_offsets[(uint64_t)b * C + key] + table[((uint64_t)b * tiles_per_sys + t) * C + key] + ranks[i];
+    out[dst] = i;
+    const float p[4] = {p4.x, p4.y, p4.z, p4.w};
+    int64_t c64[3];
+    bool ovf = false;
+    cell_coords(p, g, c64, &ovf);
+    const int c[3] = {(int)c64[0], (int)c64[1], (int)c64[2]};
+    write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
+    if (T.mask_mode != 0) {
+        const float m = T.mask_mode == 1 ? hash_mask(li, b, n, T.update_prob, T.step_index, T.base_seed) : T.mask[i];
+        if (m == 0.0f) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
+    }
+}
+
 // Orders each bin by true cell, one wave per bin. Pass 1 finds the bin's distinct cells in order
-// of first appearance and their counts; pass 2 writes each particle to
-// run start of its cell + its rank among the earlier particles of that cell, which keeps
-// ascending particle index inside every run (the reference's neighbour order). A bin with more
-// than kDirGroups cells keeps the reference order (dir_n = kDirGroups + 1). Also emits the wave
-// work items of the density pass (<= tpi consecutive slots of one run, or of an unsplit bin) and
-// the second pass's targets: the particles of the step's update mask get consecutive compact rows
-// (act_rows[row] = slot, in slot order within the bin); the others are written to the step's
-// output here (hold_particle), as the CPU euler_step leaves them.
+// of first appearance and their counts (from the scatter's sorted records); pass 2 places each
+// particle at run start of its cell + its rank among the earlier particles of that cell, which
+// keeps ascending particle index inside every run (the reference's neighbour order). A bin of one
+// cell is already in that order, and a bin with more than kDirGroups cells keeps the reference
+// order (dir_n = kDirGroups + 1): both keep the scatter's payload; any other bin is rewritten from
+// the step's input arrays. Also emits the wave work items of the density pass (<= tpi consecutive
+// slots of one run, or of an unsplit bin) and the second pass's targets: the particles of the
+// step's update mask get consecutive compact rows (act_rows[row] = slot, in slot order within the
+// bin); the scatter has written the others to the step's output (hold_particle).
 constexpr uint32_t kSplitWaves = 16;  // bins (waves) per k_split block
 
 template <int D>
@@ -565,7 +609,26 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
         const float m = T.mask_mode == 1 ? hash_mask(li, b, n, T.update_prob, T.step_index, T.base_seed) : T.mask[i];
         return m != 0.0f;
     };
-    // the particle of slot c0 + lane, its record and cell coordinates
+    // the particle of slot c0 + lane and its cell from the scatter's sorted record (coalesced; no
+    // slot of the bin is rewritten before the last pass)
+    auto load_sorted = [&](uint32_t c0, bool& valid, uint32_t& i, int c[3]) {
+        const uint32_t slot = c0 + lane;
+        valid = slot < end;
+        const uint32_t sl = valid ? slot : c0;
+        i = order[sl];
+        if constexpr (D == 2) {
+            const float4 r = srec[sl];
+            c[0] = __float_as_int(r.z);
+            c[1] = __float_as_int(r.w);
+            c[2] = 0;
+        } else {
+            const int4 cc = scoord[sl];
+            c[0] = cc.x;
+            c[1] = cc.y;
+            c[2] = cc.z;
+        }
+    };
+    // the same from the step's input arrays (a bin that is reordered overwrites its sorted records)
     auto load = [&](uint32_t c0, bool& valid, uint32_t& i, float4& p4, int c[3]) {
         const uint32_t slot = c0 + lane;
         valid = slot < end;
@@ -589,15 +652,13 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
     // the first chunk (the whole bin for most bins) is loaded once for both passes
     bool valid0 = false;
     uint32_t i0 = 0;
-    float4 p0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     int cf[3] = {0, 0, 0};
-    if (beg < end) load(beg, valid0, i0, p0, cf);
+    if (beg < end) load_sorted(beg, valid0, i0, cf);
     for (uint32_t c0 = beg; c0 < end && !over; c0 += 64) {
         bool valid = valid0;
         uint32_t i = i0;
-        float4 p4 = p0;
         int c[3] = {cf[0], cf[1], cf[2]};
-        if (c0 != beg) load(c0, valid, i, p4, c);
+        if (c0 != beg) load_sorted(c0, valid, i, c);
         int gid = group_of(c);
         uint64_t unknown = __ballot(valid && gid < 0);
         while (unknown) {
@@ -669,28 +730,24 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
         rbase += s_rows[w];
     }
     if (!has_bin) return;
-    auto place = [&](bool valid, bool tgt, uint32_t i, uint32_t dst, uint32_t row) {
+    auto place = [&](bool valid, bool tgt, uint32_t dst, uint32_t row) {  // (held particles: the scatter)
         if (!valid) return;
         row_of[dst] = tgt ? row : ~0u;
         if (tgt) act_rows[row] = dst;
-        else if (T.mask_mode != 0) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
     };
     if (beg == end) {
         if (lane == 0) dir_n[bin] = 0;
         return;
     }
-    if (over) {
+    if (over) {  // the reference order: the scatter's payload stays
         uint32_t seen_t = 0;
         for (uint32_t c0 = beg; c0 < end; c0 += 64) {
-            bool valid = valid0;
-            uint32_t i = i0;
-            float4 p4 = p0;
-            int c[3] = {cf[0], cf[1], cf[2]};
-            if (c0 != beg) load(c0, valid, i, p4, c);
+            const uint32_t slot = c0 + lane;
+            const bool valid = slot < end;
+            const uint32_t i = valid ? order[slot] : 0u;
             const bool tgt = is_target(valid, i);
             const uint64_t mt = __ballot(tgt);
-            if (valid) write_sorted<D>(c0 + lane, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
-            place(valid, tgt, i, c0 + lane, rbase + seen_t + (uint32_t)__popcll(mt & lt));
+            place(valid, tgt, slot, rbase + seen_t + (uint32_t)__popcll(mt & lt));
             seen_t += (uint32_t)__popcll(mt);
         }
         const uint32_t cnt = end - beg;
@@ -712,12 +769,16 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
             r += gt[k];
         }
     }
+    // one cell: the runs are the scatter's order and its payload stays; several cells are reordered
+    // here from the step's input arrays
+    const bool rewrite = ng > 1;
     for (uint32_t c0 = beg; c0 < end; c0 += 64) {
         bool valid = valid0;
         uint32_t i = i0;
-        float4 p4 = p0;
+        float4 p4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         int c[3] = {cf[0], cf[1], cf[2]};
-        if (c0 != beg) load(c0, valid, i, p4, c);
+        if (rewrite) load(c0, valid, i, p4, c);
+        else if (c0 != beg) load_sorted(c0, valid, i, c);
         const int gid = group_of(c);
         const bool tgt = is_target(valid, i);
         uint32_t dst = 0, row = 0;
@@ -732,8 +793,8 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
             seen[k] += (uint32_t)__popcll(m);
             seen_t[k] += (uint32_t)__popcll(mt);
         }
-        if (valid) write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
-        place(valid, tgt, i, dst, row);
+        if (valid && rewrite) write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
+        place(valid, tgt, dst, row);
     }
     uint32_t off = 0;
 #pragma unroll
@@ -810,6 +871,22 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
         const float m = T.mask_mode == 1 ? hash_mask(li, b, n, T.update_prob, T.step_index, T.base_seed) : T.mask[i];
         return m != 0.0f;
     };
+    // slot q's particle and cell from the scatter's sorted record
+    auto load_sorted = [&](uint32_t q, uint32_t& i, int c[3]) {
+        i = order[q];
+        if constexpr (D == 2) {
+            const float4 r = srec[q];
+            c[0] = __float_as_int(r.z);
+            c[1] = __float_as_int(r.w);
+            c[2] = 0;
+        } else {
+            const int4 cc = scoord[q];
+            c[0] = cc.x;
+            c[1] = cc.y;
+            c[2] = cc.z;
+        }
+    };
+    // the same from the step's input arrays (a reordered bin overwrites its sorted records)
     auto load = [&](uint32_t q, uint32_t& i, float4& p4, int c[3]) {
         i = order[q];
         p4 = pos[i];
@@ -840,9 +917,8 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
     if (thin) {  // pass 1: runs in order of first appearance, their particles and targets
         for (uint32_t q = beg; q < end; ++q) {
             uint32_t i;
-            float4 p4;
             int c[3];
-            load(q, i, p4, c);
+            load_sorted(q, i, c);
             int gid = group_of(c);
             if (gid < 0) {
                 gid = (int)ng;
@@ -900,11 +976,13 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
             seen[k] = seen_t[k] = 0;
         }
     }
+    const bool rewrite = ng > 1;  // one cell: the scatter's payload is already in run order
     for (uint32_t q = beg; q < end; ++q) {
         uint32_t i;
-        float4 p4;
+        float4 p4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         int c[3];
-        load(q, i, p4, c);
+        if (rewrite) load(q, i, p4, c);
+        else load_sorted(q, i, c);
         const int gid = group_of(c);
         const bool tgt = is_target(i);
         uint32_t dst = 0, row = 0;
@@ -916,10 +994,9 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
                 seen[k] += 1;
                 seen_t[k] += tgt ? 1u : 0u;
             }
-        write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
+        if (rewrite) write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
         row_of[dst] = tgt ? row : ~0u;
         if (tgt) act_rows[row] = dst;
-        else if (T.mask_mode != 0) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
     }
     uint32_t off = 0;
 #pragma unroll
@@ -992,15 +1069,21 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                      ws.totals.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), plan.cells, n, batch);
     if (e != hipSuccess) return e;
     const uint32_t blocks = (uint32_t)((total + 255) / 256);
-    e = launch_timed(prof, NPA_KERNEL_SCATTER, k_scatter, dim3(blocks), dim3(256), 0, stream, n, (uint32_t)total,
+    const SplitTargets tg = targets ? *targets : SplitTargets{};
+    if (!payload)
+        return launch_timed(prof, NPA_KERNEL_SCATTER, k_scatter, dim3(blocks), dim3(256), 0, stream, n,
+                            (uint32_t)total, plan.tile, plan.tiles_per_sys, plan.cells, ws.keys.as<uint32_t>(),
+                            ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(),
+                            ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), ws.flags.as<uint32_t>());
+    auto scat = g.dim == 2 ? k_scatter_payload<2> : k_scatter_payload<3>;
+    e = launch_timed(prof, NPA_KERNEL_SCATTER, scat, dim3(blocks), dim3(256), 0, stream, n, (uint32_t)total,
                      plan.tile, plan.tiles_per_sys, plan.cells, ws.keys.as<uint32_t>(), ws.ranks.as<uint32_t>(),
-                     ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(),
-                     payload ? ws.tmpidx.as<uint32_t>() : ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(),
-                     payload ? 1 : 0, ws.flags.as<uint32_t>());
-    if (e != hipSuccess || !payload) return e;
+                     ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(),
+                     ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), pos, states, state_dims, g, ws.srec.as<float4>(),
+                     ws.scoord.as<int4>(), ws.sstate.as<float>(), tg, ws.flags.as<uint32_t>());
+    if (e != hipSuccess) return e;
     const uint32_t nbins = batch * plan.cells;
     auto split = g.dim == 2 ? k_split<2> : k_split<3>;
-    const SplitTargets tg = targets ? *targets : SplitTargets{};
     if ((uint64_t)nbins * 4 <= total) {  // dense bins: a wave per bin
         const uint32_t sblocks = (nbins + kSplitWaves - 1) / kSplitWaves;
         return launch_timed(prof, NPA_KERNEL_SPLIT, split, dim3(sblocks), dim3(64 * kSplitWaves), 0, stream, pos,

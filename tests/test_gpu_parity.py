@@ -40,6 +40,16 @@ def _hashgrid_cases():
                    c1_grid),
         "skewed_gmm": (syn.gaussian_mixture(20000, 3), 1, 20000, c1_grid),
         "single_cell": (np.zeros((300, 4), np.float32), 1, 300, c1_grid),
+        # Particle-mode bins shared by several true cells: 2-8 cells per bin (the split reorders
+        # them), more than 8 (the bin keeps the reference order), and sparse bins (one lane per bin)
+        "collide_reorder": (syn.uniform_disk(4000, 51, radius=0.5), 1, 4000,
+                            c1_grid.replace(grid_size=(8, 8, 1))),
+        "collide_keep": (syn.uniform_disk(4000, 52, radius=0.6), 1, 4000,
+                         c1_grid.replace(grid_size=(4, 4, 1))),
+        "collide_sparse": (syn.uniform_disk(300, 53, radius=1.0), 1, 300,
+                           c1_grid.replace(grid_size=(16, 16, 1))),
+        "collide_3d": (syn.uniform_ball(3000, 54, radius=0.6), 1, 3000,
+                       HashGridConfig.growing_3dgs().replace(grid_size=(8, 8, 8))),
     }
     return cases
 
@@ -56,7 +66,8 @@ def test_hashgrid_bit_exact(ctx, name):
 
 
 @pytest.mark.parametrize("name", ["c1_4096", "texture_2d_periodic", "grid_clamped",
-                                  "growing_3dgs", "batch3", "skewed_gmm", "single_cell"])
+                                  "growing_3dgs", "batch3", "skewed_gmm", "single_cell",
+                                  "collide_reorder", "collide_keep", "collide_sparse", "collide_3d"])
 def test_neighbor_lists_bit_exact(ctx, name):
     pos, b, n, cfg = _hashgrid_cases()[name]
     off_w, idx_w = O.neighbor_lists(pos, b, n, cfg)
@@ -210,12 +221,17 @@ def _model_case(name):
         st = syn.normal_states(n, m.state_dims, 33, std=1.0)
         st[:, 3] += 3.5
         return m, g, pos, st, syn.seeded_weights(m, 33), 1, n
+    if name in ("collide_reorder", "collide_keep", "collide_sparse", "collide_3d"):
+        pos, b, n, g = _hashgrid_cases()[name]
+        m = NpaConfig.growing_3dgs() if g.dim == 3 else syn.config_c1()[0]
+        return (m, g, pos, syn.normal_states(n, m.state_dims, 60), syn.seeded_weights(m, 60), b, n)
     raise KeyError(name)
 
 
 @pytest.mark.parametrize("name", ["c1", "c1_dgrad", "growing_3d", "torus_gates_3d",
                                   "texture_periodic", "batch4", "no_sgrad_2d", "no_sgrad_3d",
-                                  "torus16_gates_3d"])
+                                  "torus16_gates_3d", "collide_reorder", "collide_keep",
+                                  "collide_sparse", "collide_3d"])
 def test_step_parity(ctx, name):
     """One step against NpaModel::step_cpu (model.rs:768-858). 16-channel models run the fused
     second-pass + MLP kernel, wider ones the two-kernel path; both sum in the reference's order."""
