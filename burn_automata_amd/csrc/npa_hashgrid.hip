@@ -365,59 +365,77 @@ __device__ __forceinline__ uint32_t block_scan_1024(uint32_t v, uint32_t* lds, u
 }
 
 // One block per system: bin_offsets[b][k] = b * n + exclusive prefix of totals[b][k] over k.
-// Wave w owns a contiguous range of keys and walks it in segments of 64 (lane = key), so every
-// load and store is coalesced: a first walk sums the range, a block scan orders the waves, and a
-// second walk writes the prefixes with a running carry.
+// Thread t owns the PER consecutive keys [t PER, t PER + PER) (C <= 1024 PER): all of its loads are
+// issued at once (16-byte loads when the rows are aligned), one block scan orders the threads, and
+// the prefixes are written with a running carry - one load, one scan and one store whatever C.
+template <int PER>
 __global__ __launch_bounds__(1024) void k_offsets_scan(const uint32_t* __restrict__ totals,
                                                        uint32_t* __restrict__ bin_offsets,
                                                        uint32_t C, uint32_t n, uint32_t batch) {
-    __shared__ uint32_t wsum[16];
+    __shared__ uint32_t lds[16];
     const uint32_t b = blockIdx.x;
-    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint32_t* tot = totals + (uint64_t)b * C;
     uint32_t* out = bin_offsets + (uint64_t)b * C;
-    const uint32_t per = ((C + nw - 1) / nw + 63) / 64 * 64;  // keys per wave, whole segments
-    const uint32_t k0 = w * per < C ? w * per : C;
-    const uint32_t k1 = k0 + per < C ? k0 + per : C;
-    uint32_t acc = 0;
-    for (uint32_t k = k0 + lane; k < k1; k += 4 * 64) {  // four segments' loads in flight
-        uint32_t v[4];
+    const uint32_t k0 = threadIdx.x * PER;
+    uint32_t v[PER];
+    const bool vec = PER % 4 == 0 && ((uint64_t)b * C) % 4 == 0 && k0 + PER <= C;
+    if (vec) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = k + u * 64 < k1 ? tot[k + u * 64] : 0u;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) acc += v[u];
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if (lane == 0) wsum[w] = acc;
-    __syncthreads();
-    uint32_t carry = b * n, all = 0;
-    for (uint32_t v = 0; v < nw; ++v) {
-        if (v < w) carry += wsum[v];
-        all += wsum[v];
-    }
-    for (uint32_t s0 = k0; s0 < k1; s0 += 4 * 64) {
-        uint32_t v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t k = s0 + u * 64 + lane;
-            v[u] = k < k1 ? tot[k] : 0u;
+        for (int j = 0; j < PER; j += 4) {
+            const uint4 q = *reinterpret_cast<const uint4*>(tot + k0 + j);
+            v[j] = q.x;
+            v[j + 1] = q.y;
+            v[j + 2] = q.z;
+            v[j + 3] = q.w;
         }
+    } else {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t k = s0 + u * 64 + lane;
-            uint32_t x = v[u];
+        for (int j = 0; j < PER; ++j) v[j] = k0 + j < C ? tot[k0 + j] : 0u;
+    }
+    uint32_t sum = 0;
 #pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const uint32_t y = __shfl_up(x, off, 64);
-                if (lane >= (uint32_t)off) x += y;
-            }
-            if (k < k1) out[k] = carry + x - v[u];
-            carry += __shfl(x, 63, 64);
+    for (int j = 0; j < PER; ++j) sum += v[j];
+    uint32_t all;
+    uint32_t run = b * n + block_scan_1024(sum, lds, &all);
+    if (vec) {
+#pragma unroll
+        for (int j = 0; j < PER; j += 4) {
+            uint4 q;
+            q.x = run;
+            run += v[j];
+            q.y = run;
+            run += v[j + 1];
+            q.z = run;
+            run += v[j + 2];
+            q.w = run;
+            run += v[j + 3];
+            *reinterpret_cast<uint4*>(out + k0 + j) = q;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            if (k0 + j < C) out[k0 + j] = run;
+            run += v[j];
         }
     }
     // last entry = total count (every system holds n entries when the counts are per system)
     if (b == batch - 1 && threadIdx.x == 0) bin_offsets[(uint64_t)batch * C] = b * n + all;
+}
+
+// k_offsets_scan with the smallest PER that covers C (<= 65536) keys.
+static hipError_t launch_offsets_scan(const uint32_t* totals, uint32_t* bin_offsets, uint32_t C, uint32_t n,
+                                      uint32_t batch, hipStream_t stream, Profiler* prof) {
+    const uint32_t per = (C + 1023) / 1024;
+    auto launch = [&](auto k) {
+        return launch_timed(prof, NPA_KERNEL_OFFSETS_SCAN, k, dim3(batch), dim3(1024), 0, stream, totals,
+                            bin_offsets, C, n, batch);
+    };
+    if (per <= 1) return launch(k_offsets_scan<1>);
+    if (per <= 4) return launch(k_offsets_scan<4>);
+    if (per <= 8) return launch(k_offsets_scan<8>);
+    if (per <= 16) return launch(k_offsets_scan<16>);
+    if (per <= 32) return launch(k_offsets_scan<32>);
+    return launch(k_offsets_scan<64>);
 }
 
 // The reference's snapshot only: perm (slot -> particle of the system) and inv. (The rollout step
@@ -1065,8 +1083,8 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
     e = launch_timed(prof, NPA_KERNEL_TABLE_SCAN, k_table_scan, dim3((plan.cells + 255) / 256, batch), dim3(256), 0,
                      stream, ws.table.as<uint32_t>(), ws.totals.as<uint32_t>(), plan.cells, plan.tiles_per_sys);
     if (e != hipSuccess) return e;
-    e = launch_timed(prof, NPA_KERNEL_OFFSETS_SCAN, k_offsets_scan, dim3(batch), dim3(1024), 0, stream,
-                     ws.totals.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), plan.cells, n, batch);
+    e = launch_offsets_scan(ws.totals.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), plan.cells, n, batch, stream,
+                            prof);
     if (e != hipSuccess) return e;
     const uint32_t blocks = (uint32_t)((total + 255) / 256);
     const SplitTargets tg = targets ? *targets : SplitTargets{};
@@ -1171,8 +1189,7 @@ hipError_t launch_key_sort(const HashgridPlan& p, const uint32_t* keys, const ui
     hipLaunchKernelGGL(k_table_scan, dim3((p.cells + 255) / 256, 1), dim3(256), 0, stream, table, totals,
                        p.cells, p.tiles_per_sys);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_offsets_scan, dim3(1), dim3(1024), 0, stream, totals, offsets, p.cells, cap, 1u);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = launch_offsets_scan(totals, offsets, p.cells, cap, 1u, stream, nullptr)) != hipSuccess) return e;
     if (cap == 0) return hipSuccess;
     hipLaunchKernelGGL(k_scatter_vals, dim3((cap + 255) / 256), dim3(256), 0, stream, keys, vals, d_count,
                        cap, p.tile, p.cells, ranks, table, offsets, out_vals);

@@ -40,6 +40,9 @@ def _hashgrid_cases():
                    c1_grid),
         "skewed_gmm": (syn.gaussian_mixture(20000, 3), 1, 20000, c1_grid),
         "single_cell": (np.zeros((300, 4), np.float32), 1, 300, c1_grid),
+        # a bin count that is not a multiple of four, in several systems
+        "batch_odd_cells": (np.concatenate([syn.uniform_disk(400, 61 + k, radius=1.2) for k in range(3)]), 3, 400,
+                            HashGridConfig(2, Boundary.Clamped, HashGridMode.Grid, (7, 5, 1), 0.3)),
         # Particle-mode bins shared by several true cells: 2-8 cells per bin (the split reorders
         # them), more than 8 (the bin keeps the reference order), and sparse bins (one lane per bin)
         "collide_reorder": (syn.uniform_disk(4000, 51, radius=0.5), 1, 4000,
