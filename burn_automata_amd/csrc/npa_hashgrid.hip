@@ -904,18 +904,6 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
             c[2] = cc.z;
         }
     };
-    // the same from the step's input arrays (a reordered bin overwrites its sorted records)
-    auto load = [&](uint32_t q, uint32_t& i, float4& p4, int c[3]) {
-        i = order[q];
-        p4 = pos[i];
-        const float p[4] = {p4.x, p4.y, p4.z, p4.w};
-        int64_t c64[3];
-        bool ovf = false;
-        cell_coords(p, g, c64, &ovf);  // overflow was flagged by the hash pass
-        c[0] = (int)c64[0];
-        c[1] = (int)c64[1];
-        c[2] = (int)c64[2];
-    };
     int gx[K], gy[K], gz[K];
     uint32_t gc[K], gt[K];
 #pragma unroll
@@ -931,12 +919,22 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
             if (k < ng && c[0] == gx[k] && c[1] == gy[k] && c[2] == gz[k]) gid = (int)k;
         return gid;
     };
+    // the bin's slots (at most kThinMax), loaded together and kept in registers for both passes
+    uint32_t qi[kThinMax];
+    int qc[kThinMax][3];
+    bool qt[kThinMax];
+    if (thin && beg < end) {
+#pragma unroll
+        for (uint32_t j = 0; j < kThinMax; ++j) load_sorted(beg + j < end ? beg + j : beg, qi[j], qc[j]);
+#pragma unroll
+        for (uint32_t j = 0; j < kThinMax; ++j) qt[j] = beg + j < end && is_target(qi[j]);
+    }
     uint32_t nitems = 0, nrows = 0;
     if (thin) {  // pass 1: runs in order of first appearance, their particles and targets
-        for (uint32_t q = beg; q < end; ++q) {
-            uint32_t i;
-            int c[3];
-            load_sorted(q, i, c);
+#pragma unroll
+        for (uint32_t j = 0; j < kThinMax; ++j) {
+            if (beg + j >= end) break;
+            const int* c = qc[j];
             int gid = group_of(c);
             if (gid < 0) {
                 gid = (int)ng;
@@ -949,7 +947,7 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
                     }
                 ++ng;
             }
-            const uint32_t t = is_target(i) ? 1u : 0u;
+            const uint32_t t = qt[j] ? 1u : 0u;
 #pragma unroll
             for (uint32_t k = 0; k < K; ++k)
                 if ((int)k == gid) {
@@ -995,14 +993,13 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
         }
     }
     const bool rewrite = ng > 1;  // one cell: the scatter's payload is already in run order
-    for (uint32_t q = beg; q < end; ++q) {
-        uint32_t i;
-        float4 p4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        int c[3];
-        if (rewrite) load(q, i, p4, c);
-        else load_sorted(q, i, c);
+#pragma unroll
+    for (uint32_t j = 0; j < kThinMax; ++j) {
+        if (beg + j >= end) break;
+        const uint32_t i = qi[j];
+        const int* c = qc[j];
         const int gid = group_of(c);
-        const bool tgt = is_target(i);
+        const bool tgt = qt[j];
         uint32_t dst = 0, row = 0;
 #pragma unroll
         for (uint32_t k = 0; k < K; ++k)
@@ -1012,7 +1009,8 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
                 seen[k] += 1;
                 seen_t[k] += tgt ? 1u : 0u;
             }
-        if (rewrite) write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
+        // a reordered bin is rewritten from the step's input arrays (its cells are in registers)
+        if (rewrite) write_sorted<D>(dst, i, b, n, pos[i], c, states, S, perm, inv, srec, scoord, sstate);
         row_of[dst] = tgt ? row : ~0u;
         if (tgt) act_rows[row] = dst;
     }
