@@ -219,7 +219,7 @@ bool make_plan(const npa_grid_cfg& cfg, uint32_t batch, uint32_t n, HashgridPlan
 // are read from keys_in and the item count from *d_count (a device-resident count
 // bounded by the tiles the grid covers).
 template <int R>
-__global__ __launch_bounds__(256) void k_hash_rank(const float4* __restrict__ pos,
+__global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ pos,
                                                    const uint32_t* __restrict__ keys_in,
                                                    const uint32_t* __restrict__ d_count, uint32_t n,
                                                    uint32_t tiles_per_sys, uint32_t waves,
@@ -1044,7 +1044,10 @@ static hipError_t launch_rank_r(uint32_t blocks, uint32_t waves, uint32_t lds_by
         if (e != hipSuccess) return e;
         attr_bytes = lds_bytes;
     }
-    return launch_timed(prof, NPA_KERNEL_HASH_RANK, k_hash_rank<R>, dim3(blocks), dim3(256), lds_bytes, stream,
+    // the first `waves` waves rank; all of them clear the tile's counters and write its histogram
+    // row, O(cells) work that wide grids (many cells per tile) spread over 16 waves
+    const uint32_t threads = g.cells >= 4096 ? 1024 : 256;
+    return launch_timed(prof, NPA_KERNEL_HASH_RANK, k_hash_rank<R>, dim3(blocks), dim3(threads), lds_bytes, stream,
                         pos, keys_in, d_count, n, tiles_per_sys, waves, g, key_bits, keys, ranks, table, flags,
                         wl_count);
 }
