@@ -393,6 +393,10 @@ npa_status npa_context_set_host_io(npa_context* ctx, int host_io) {
 }
 
 namespace {
+// Width of the feature-major rows a step's workspace holds: none when the fused second pass + MLP
+// kernel runs the step (its feature rows never leave LDS).
+uint32_t feature_rows_for(const npa::StepParams& p) { return npa::fused_update_applies(p) ? 0u : p.FP; }
+
 // NPA_MLP_AUTO -> the engine for a system of `particles` particles.
 uint32_t resolve_engine(int engine, uint64_t particles) {
     if (engine == NPA_MLP_AUTO) return particles >= NPA_MLP_AUTO_MIN_PARTICLES ? NPA_MLP_MFMA : NPA_MLP_VALU;
@@ -735,7 +739,7 @@ npa_status npa_step(npa_context* ctx, const float* positions, const float* state
     p.mlp_engine = resolve_engine(ctx->mlp_engine, total);
     if (total && npa::state_stride_for(S) == S && !aligned16(sio.out_states))
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: output states must be 16-byte aligned");
-    NPA_HIP(ctx, ctx->ws.reserve(plan, total, B, S, (int)grid->dim, p.FP), "workspace");
+    NPA_HIP(ctx, ctx->ws.reserve(plan, total, B, S, (int)grid->dim, feature_rows_for(p)), "workspace");
     NPA_HIP(ctx, ctx->ws.wpad.reserve(npa::padded_weight_floats(p) * 4), "workspace");
     const int blocks = grid_blocks_for(ctx, plan);
     if (total) {
@@ -783,7 +787,8 @@ npa_status npa_step_noalloc(npa_context* ctx, const float* positions, const floa
     p.update_prob = 1.0f;
     p.mlp_engine = resolve_engine(ctx->mlp_engine, total);
     npa::Workspace ws;  // views into this device's scratch array
-    const uint64_t need_bytes = ws.carve(plan, total, B, S, (int)grid->dim, p.FP, npa::padded_weight_floats(p) * 4,
+    const uint64_t need_bytes = ws.carve(plan, total, B, S, (int)grid->dim, feature_rows_for(p),
+                                         npa::padded_weight_floats(p) * 4,
                                          ctx->scratch, NPA_STEP_NOALLOC_SCRATCH_BYTES);
     if (need_bytes > NPA_STEP_NOALLOC_SCRATCH_BYTES)
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT,
@@ -1104,7 +1109,7 @@ npa_status npa_state_create(npa_context* ctx, const npa_model_cfg* model, const 
         apply_model(&q, *model, grid->eps);
         return q;
     }();
-    if (e == hipSuccess) e = s->ws.reserve(plan, total, B, S, (int)grid->dim, sp.FP);
+    if (e == hipSuccess) e = s->ws.reserve(plan, total, B, S, (int)grid->dim, feature_rows_for(sp));
     if (e == hipSuccess) e = s->ws.wpad.reserve(npa::padded_weight_floats(sp) * 4);
     if (e == hipSuccess) e = hipMemcpyAsync(s->pos[0].ptr, positions, total * 16, kind, ctx->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(s->states[0].ptr, states, total * S * 4, kind, ctx->stream);
