@@ -493,7 +493,7 @@ def main(argv=None) -> int:
                     help="render (default 64) and raster (default 1024) workloads only")
     ap.add_argument("--decode-every", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
-    ap.add_argument("--mlp-engine", choices=("valu", "mfma", "auto"), default="valu",
+    ap.add_argument("--mlp-engine", choices=("valu", "mfma"), default="valu",
                     help="update MLP on the vector ALUs in the reference's order (bit-exact, default) "
                          "or on the fp32 matrix cores (single-step tolerance)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -557,7 +557,7 @@ def main(argv=None) -> int:
             ex.splat_2d(state, splat)
 
     from burn_automata_amd import _abi
-    engine = {"valu": _abi.MLP_VALU, "mfma": _abi.MLP_MFMA, "auto": _abi.MLP_AUTO}[args.mlp_engine]
+    engine = {"valu": _abi.MLP_VALU, "mfma": _abi.MLP_MFMA}[args.mlp_engine]
 
     def new_state():
         st_ = ex.create_state(model, pos, st, B, N, w["grid"], w["dt"], w["update_prob"], w["seed"])

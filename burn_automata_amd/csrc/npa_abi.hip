@@ -396,17 +396,11 @@ namespace {
 // Width of the feature-major rows a step's workspace holds: none when the fused second pass + MLP
 // kernel runs the step (its feature rows never leave LDS).
 uint32_t feature_rows_for(const npa::StepParams& p) { return npa::fused_update_applies(p) ? 0u : p.FP; }
-
-// NPA_MLP_AUTO -> the engine for a system of `particles` particles.
-uint32_t resolve_engine(int engine, uint64_t particles) {
-    if (engine == NPA_MLP_AUTO) return particles >= NPA_MLP_AUTO_MIN_PARTICLES ? NPA_MLP_MFMA : NPA_MLP_VALU;
-    return (uint32_t)engine;
-}
 }  // namespace
 
 npa_status npa_context_set_mlp_engine(npa_context* ctx, int engine) {
     if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
-    if (engine != NPA_MLP_VALU && engine != NPA_MLP_MFMA && engine != NPA_MLP_AUTO)
+    if (engine != NPA_MLP_VALU && engine != NPA_MLP_MFMA)
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: unknown MLP engine " + std::to_string(engine));
     ctx->mlp_engine = engine;
     return NPA_OK;
@@ -736,7 +730,7 @@ npa_status npa_step(npa_context* ctx, const float* positions, const float* state
     apply_model(&p, *model, grid->eps);
     p.dt = dt;
     p.update_prob = 1.0f;
-    p.mlp_engine = resolve_engine(ctx->mlp_engine, total);
+    p.mlp_engine = (uint32_t)ctx->mlp_engine;
     if (total && npa::state_stride_for(S) == S && !aligned16(sio.out_states))
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: output states must be 16-byte aligned");
     NPA_HIP(ctx, ctx->ws.reserve(plan, total, B, S, (int)grid->dim, feature_rows_for(p)), "workspace");
@@ -785,7 +779,7 @@ npa_status npa_step_noalloc(npa_context* ctx, const float* positions, const floa
     apply_model(&p, *model, grid->eps);
     p.dt = dt;
     p.update_prob = 1.0f;
-    p.mlp_engine = resolve_engine(ctx->mlp_engine, total);
+    p.mlp_engine = (uint32_t)ctx->mlp_engine;
     npa::Workspace ws;  // views into this device's scratch array
     const uint64_t need_bytes = ws.carve(plan, total, B, S, (int)grid->dim, feature_rows_for(p),
                                          npa::padded_weight_floats(p) * 4,
@@ -1150,7 +1144,7 @@ npa_status npa_state_step(npa_state* s, uint32_t steps) {
     p.dt = s->dt;
     p.update_prob = s->update_prob;
     p.base_seed = base_seed(s->seed);
-    p.mlp_engine = resolve_engine(s->mlp_engine, (uint64_t)s->B * s->N);
+    p.mlp_engine = (uint32_t)s->mlp_engine;
     npa::StepIO io;
     io.w1 = s->w1.as<float>();
     io.b1 = s->b1.as<float>();
@@ -1178,7 +1172,7 @@ npa_status npa_state_step(npa_state* s, uint32_t steps) {
 
 npa_status npa_state_set_mlp_engine(npa_state* s, int engine) {
     if (!s) return NPA_ERR_INVALID_ARGUMENT;
-    if (engine != NPA_MLP_VALU && engine != NPA_MLP_MFMA && engine != NPA_MLP_AUTO)
+    if (engine != NPA_MLP_VALU && engine != NPA_MLP_MFMA)
         return fail(s->ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: unknown MLP engine " + std::to_string(engine));
     s->mlp_engine = engine;
     return NPA_OK;

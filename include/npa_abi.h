@@ -183,10 +183,9 @@ npa_status npa_context_set_host_io(npa_context* ctx, int host_io);
  * cores (v_mfma_f32_4x4x1f32 in the fused step kernel, v_mfma_f32_16x16x4_f32 otherwise), with
  * fused products and split sums: a single step stays within 1e-6 of the reference, while a
  * rollout drifts apart as far as the reference itself does from a one-ulp perturbation of its
- * inputs (the dynamics amplify last-bit differences). NPA_MLP_AUTO: MFMA for systems of at least
- * NPA_MLP_AUTO_MIN_PARTICLES particles (B*N), VALU below, the measured crossover on MI355X. */
-enum { NPA_MLP_VALU = 0, NPA_MLP_MFMA = 1, NPA_MLP_AUTO = 2 };
-#define NPA_MLP_AUTO_MIN_PARTICLES 32768u
+ * inputs (the dynamics amplify last-bit differences). Measured on MI355X, the matrix-core engine's
+ * step kernel is the faster one at every system size from 256 particles up. */
+enum { NPA_MLP_VALU = 0, NPA_MLP_MFMA = 1 };
 npa_status npa_context_set_mlp_engine(npa_context* ctx, int engine);
 
 /* Blocks until all work queued on the context's stream has finished. */

@@ -109,23 +109,3 @@ def test_mfma_rollout_drift_is_the_dynamics_own(ctx, name, systems):
     assert np.isfinite(to_np(gp)).all() and np.isfinite(to_np(gs)).all()
     assert ep <= 10 * rp and es <= 10 * rs
 
-
-def test_auto_engine_picks_by_system_size(ctx):
-    """NPA_MLP_AUTO: the bit-exact VALU engine below NPA_MLP_AUTO_MIN_PARTICLES, the matrix-core
-    engine from there on (each compared bit for bit with the engine it must pick)."""
-    for name, n, want_engine in (("c1", 4096, _abi.MLP_VALU), ("c2", 65536, _abi.MLP_MFMA)):
-        assert (n >= _abi.MLP_AUTO_MIN_PARTICLES) == (want_engine == _abi.MLP_MFMA)
-        w = syn.workload(name, particles=n)
-        m, g = w["model"], w["grid"]
-        ex = HipAutomataExecutor(ctx=ctx)
-        out = {}
-        for eng in (_abi.MLP_AUTO, want_engine):
-            st = ex.create_state(NpaModel(m, w["weights"]), w["positions"], w["states"], 1, n, g, 1.0, 0.5, 42)
-            try:
-                st.set_mlp_engine(eng)
-                ex.step_state_many(st, 2)
-                out[eng] = ex.read_state(st)
-            finally:
-                st.close()
-        for a, b in zip(out[_abi.MLP_AUTO], out[want_engine]):
-            np.testing.assert_array_equal(to_np(a), to_np(b))
