@@ -231,9 +231,12 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
     const uint32_t FP = P.FP;
     const uint32_t wfloats = (uint32_t)fused_weight_floats(FP, D);
 
+    // the block's next item position (see below), after the waves' regions
+    uint32_t* s_take = reinterpret_cast<uint32_t*>(lds + wfloats + (size_t)kFuseWaves * Sh::WAVE_FLOATS);
     // the block's copy of the padded weights
     for (uint32_t v = threadIdx.x; v < wfloats / 4; v += blockDim.x)
         reinterpret_cast<float4*>(lds)[v] = reinterpret_cast<const float4*>(wfused)[v];
+    if (threadIdx.x == 0) *s_take = kFuseWaves;
     __syncthreads();
     const float* w1q = lds;
     const float* b1 = w1q + (size_t)FP * HP;
@@ -263,16 +266,25 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
     // order) is spread over many CUs instead of landing on one. Blocks are dispatched to the eight
     // XCDs in turn, so block b is renumbered (b % 8) * (G / 8) + b / 8: each XCD then walks one
     // contiguous run of G / 8 * 16 items per pass and its L2 holds their neighbour rows once.
-    const uint32_t item_end = nitems;
+    // Within a block the items are taken in order from an LDS counter (position j = item
+    // lblock * 16 + j % 16 + (j / 16) * G * 16), the first one per wave dealt statically: a wave
+    // that the SIMD's oldest-first issue keeps waiting takes fewer items, so the block's waves end
+    // together instead of the youngest ones running a tail alone.
     const uint32_t item_stride = gridDim.x * kFuseWaves;
     const uint32_t lblock = gridDim.x % 8 == 0 ? (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8 : blockIdx.x;
+    auto item_of = [&](uint32_t j) { return lblock * kFuseWaves + j % kFuseWaves + (j / kFuseWaves) * item_stride; };
+    auto take = [&]() {
+        uint32_t j = 0;
+        if (lane == 0) j = atomicAdd(s_take, 1u);
+        return (uint32_t)__builtin_amdgcn_readfirstlane((int)j);
+    };
     auto slot_of = [&](uint32_t it) {
         const uint32_t r = it * 4 + g;
         return act_rows[r < nrows ? r : it * 4];
     };
-    uint32_t item = lblock * kFuseWaves + wave;
-    uint32_t s_next = item < item_end ? slot_of(item) : 0u;  // the next item's slot, loaded one item ahead
-    for (; item < item_end; item += item_stride) {
+    uint32_t item = item_of(wave);
+    uint32_t s_next = item < nitems ? slot_of(item) : 0u;  // the item's compact-row slot
+    while (item < nitems) {
         const uint32_t row = item * 4 + g;
         const bool active = row < nrows;
         const uint32_t s = s_next;
@@ -289,7 +301,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
         const uint32_t base0 = rbase[c];
         const uint64_t mask0 = rmask[c];
         const uint32_t li = perm[s];
-        if (item + item_stride < item_end) s_next = slot_of(item + item_stride);
+
         const uint32_t b = s / P.N;
         const uint32_t i = b * P.N + li;
         const float4 pos4 = io.pos[i];
@@ -650,14 +662,8 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
         constexpr uint32_t KB_FIXED = (32 + 16 * D) / 4;  // blocks of four state/blur/gradient features
         float* hw = wl + 4 * (FP + 4);  // hidden activations [target][HSTR]
         float us, um;
-        if constexpr (ENG == 1) {
-            // Matrix-core engine (v_mfma_f32_4x4x1f32, 16 blocks of 4x4 with K = 1: lane l supplies
-            // A[l / 4][l % 4] and B[l / 4][l % 4] and holds D[l / 4][r][l % 4] in accumulator r).
-            // Layer 1: block b = hidden units 4b..4b+3, A = the four targets' feature k (lane l feeds
-            // target l % 4), B = unit l's weight for feature k; lane l ends with unit l of targets
-            // 0..3, the VALU mapping. The products are fused into the sums and the sums are split
-            // into independent chains, so the result differs from the reference's in the last bits.
-            float* fr = wl + g * (FP + 4);  // this target's feature row
+        {  // the four targets' feature rows [4][FP + 4]: lane l reads target l % 4's features
+            float* fr = wl + g * (FP + 4);
             fr[c] = si;
             fr[16 + c] = blur;
 #pragma unroll
@@ -668,6 +674,15 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
                     if (4 * KB_FIXED + k < FP) fr[4 * KB_FIXED + k] = rest[k];
             }
             wave_sync();
+        }
+        const float* myf = wl + (lane & 3u) * (FP + 4);
+        if constexpr (ENG == 1) {
+            // Matrix-core engine (v_mfma_f32_4x4x1f32, 16 blocks of 4x4 with K = 1: lane l supplies
+            // A[l / 4][l % 4] and B[l / 4][l % 4] and holds D[l / 4][r][l % 4] in accumulator r).
+            // Layer 1: block b = hidden units 4b..4b+3, A = the four targets' feature k (lane l feeds
+            // target l % 4), B = unit l's weight for feature k; lane l ends with unit l of targets
+            // 0..3, the VALU mapping. The products are fused into the sums and the sums are split
+            // into independent chains, so the result differs from the reference's in the last bits.
             const float* myf = wl + (lane & 3u) * (FP + 4);
             // Two independent accumulators per unit (even and odd feature pairs) keep four MFMA chains
             // in flight; they are added at the end, so this engine's sums are not in index order.
@@ -725,6 +740,11 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
             us = uo[g * (OPAD + 1) + D + c];
             um = uo[g * (OPAD + 1) + (c < D ? c : 0u)];
         } else {
+        // Layer 1, bit-exact: the products on the matrix cores, the sums on the vector ALUs. With a
+        // -0.0 accumulator, v_mfma_f32_4x4x1f32 returns each product a * b rounded once - exactly
+        // what v_mul_f32 returns, signed zeros and denormals included - laid out as the sums need
+        // it (lane l: unit l of targets 0..3, as above); every sum then starts from its bias and
+        // adds the products in feature order with separate roundings, as the reference does.
         float h0[4], h1[4];
         {
             const float bb0 = b1[lane], bb1 = b1[lane + 64];
@@ -734,47 +754,28 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
                 h1[t] = bb1;
             }
         }
-        auto mac_block = [&](uint32_t kb, auto feature_of) {
+        const v4f nzero = {-0.0f, -0.0f, -0.0f, -0.0f};
+        auto prod_block = [&](uint32_t kb) {
+            const float4 f4 = *reinterpret_cast<const float4*>(myf + 4 * kb);
             const float4 w0 = *reinterpret_cast<const float4*>(w1q + ((size_t)kb * HP + lane) * 4);
             const float4 w1 = *reinterpret_cast<const float4*>(w1q + ((size_t)kb * HP + lane + 64) * 4);
+            const float fa[4] = {f4.x, f4.y, f4.z, f4.w};
             const float wa[4] = {w0.x, w0.y, w0.z, w0.w}, wb[4] = {w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                const v4f p0 = __builtin_amdgcn_mfma_f32_4x4x1f32(fa[i], wa[i], nzero, 0, 0, 0);
+                const v4f p1 = __builtin_amdgcn_mfma_f32_4x4x1f32(fa[i], wb[i], nzero, 0, 0, 0);
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    const float f = feature_of(i, t);
-                    h0[t] += wa[i] * f;
-                    h1[t] += wb[i] * f;
+                    h0[t] += p0[t];
+                    h1[t] += p1[t];
                 }
             }
         };
 #pragma unroll
-        for (uint32_t kb = 0; kb < KB_FIXED; ++kb) {
-            mac_block(kb, [&](int i, int t) {
-                const uint32_t k = 4 * kb + i;
-                float v;
-                uint32_t src;
-                if (k < 16) {
-                    v = si;
-                    src = k;
-                } else if (k < 32) {
-                    v = blur;
-                    src = k - 16;
-                } else {
-                    v = gf[(k - 32) % D];
-                    src = (k - 32) / D;
-                }
-                return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)(16 * t + src)));
-            });
-        }
-        if (FP / 4 > KB_FIXED)
-            mac_block(KB_FIXED, [&](int i, int t) {
-                return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rest[i]), 16 * t));
-            });
-        if (FP / 4 > KB_FIXED + 1)
-            mac_block(KB_FIXED + 1, [&](int i, int t) {
-                return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rest[4 + i]), 16 * t));
-            });
+        for (uint32_t kb = 0; kb < KB_FIXED; ++kb) prod_block(kb);
+        if (FP / 4 > KB_FIXED) prod_block(KB_FIXED);
+        if (FP / 4 > KB_FIXED + 1) prod_block(KB_FIXED + 1);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             hw[t * Sh::HSTR + lane] = fmaxf(h0[t], 0.0f);
@@ -844,6 +845,10 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
         float next = si + P.dt * dsc * mk;
         if (clamped_channel(D, P.S, c)) next = clampf_(next, -8.0f, 24.0f);
         if (active && c < P.S) io.out_states[(uint64_t)i * P.S + c] = next;
+        // the next position is taken when this item is done, so a wave that is kept waiting
+        // takes fewer of the block's items
+        item = item_of(take());
+        if (item < nitems) s_next = slot_of(item);
     }
 }
 
@@ -851,7 +856,7 @@ template <int D, int FL, int ENG>
 static hipError_t launch_fused_t(const StepParams& p, Workspace& ws, const StepIO& io, const float* wfused,
                                  hipStream_t stream, Profiler* prof) {
     using Sh = FuseShape<D, FL>;
-    const size_t lds = (fused_weight_floats(p.FP, D) + (size_t)kFuseWaves * Sh::WAVE_FLOATS) * 4;
+    const size_t lds = (fused_weight_floats(p.FP, D) + (size_t)kFuseWaves * Sh::WAVE_FLOATS + 4) * 4;  // + counter
     if (lds > kFuseLdsBytes) return hipErrorInvalidValue;
     static bool attr = false;
     if (!attr) {
