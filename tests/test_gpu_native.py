@@ -46,3 +46,16 @@ def test_c_caller_step_and_rollout(tmp_path):
     wp, ws = O.rollout(m, wt, w["positions"], w["states"], 1, n, w["grid"], steps, 1.0, 0.5, 42, 0)
     np.testing.assert_array_equal(load("roll_positions", (n, 4)), wp)
     np.testing.assert_array_equal(load("roll_states", (n, S)), ws)
+
+
+def test_mfma_product_equals_vector_multiply():
+    """The fused update kernel's bit-exact engine takes layer-1 products from v_mfma_f32_4x4x1f32
+    with a -0.0 accumulator: each must be v_mul_f32's rounded product bit for bit (ordinary values,
+    zeros of both signs, denormal inputs and products; tests/native/mfma_product.cpp)."""
+    exe = os.path.join(HERE, "native", "mfma_product")
+    if not os.path.exists(exe):
+        from tests.native import build_c_step
+        build_c_step.build_mfma_product()
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0 and "mismatches 0 of" in r.stdout, r.stdout + r.stderr
