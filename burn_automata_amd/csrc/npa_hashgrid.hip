@@ -73,8 +73,10 @@ static void each_buffer(Workspace& w, const HashgridPlan& plan, uint64_t total, 
     f(w.worklist, (plan.worklist_cap + 1) * 8);
     // second-pass items: at most one partial item per (64-slot window, cell run) pair
     f(w.act_rows, t1 * 4);
-    f(w.srec, t1 * 16);
-    f(w.scoord, dim == 3 ? t1 * 16 : 16);
+    // sorted records: 64 slots of padding past the last particle, so a pass may load a whole
+    // 64-slot chunk from any run start without clamping the index
+    f(w.srec, (t1 + 64) * 16);
+    f(w.scoord, dim == 3 ? (t1 + 64) * 16 : 16);
     f(w.sstate, t1 * (uint64_t)state_stride_for(state_dims ? state_dims : 1) * 4);
     f(w.svol, t1 * 16);
     f(w.counters, 64);

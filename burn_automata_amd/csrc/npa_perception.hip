@@ -176,24 +176,24 @@ __global__ __launch_bounds__(256) void k_density_q(StepParams P, const float4* _
                     auto walk = [&](auto FILT, auto PER) {
                         constexpr bool filt = decltype(FILT)::value, per = decltype(PER)::value;
                         constexpr bool xy = D == 2 && !filt;  // only the position is read
+                        // k < 64: slots past the run are other runs' records or the records'
+                        // 64-slot padding, loaded and never accepted (k >= m fails `ok`)
                         auto load = [&](uint32_t k) {
-                            const uint32_t kc = k < m ? k : m - 1;  // in bounds for any k
                             if constexpr (xy) {
-                                const float2 v = *reinterpret_cast<const float2*>(cand + kc);
+                                const float2 v = *reinterpret_cast<const float2*>(cand + k);
                                 return make_float4(v.x, v.y, 0.0f, 0.0f);
                             } else {
-                                return cand[kc];
+                                return cand[k];
                             }
                         };
                         auto test = [&](uint32_t r, const float4 rc) {  // round r: candidate 4 r + q
                             const uint32_t k = 4 * r + q;
                             bool ok = in_group & (k < m);
                             if constexpr (filt) {
-                                const uint32_t kc = k < m ? k : m - 1;
                                 if constexpr (D == 2) {
                                     ok = ok & ((int64_t)__float_as_int(rc.z) == n0) & ((int64_t)__float_as_int(rc.w) == n1);
                                 } else {
-                                    const int4 cc = scoord[base + kc];
+                                    const int4 cc = scoord[base + k];
                                     ok = ok & ((int64_t)cc.x == n0) & ((int64_t)cc.y == n1) & ((int64_t)cc.z == n2);
                                 }
                             }
@@ -211,9 +211,12 @@ __global__ __launch_bounds__(256) void k_density_q(StepParams P, const float4* _
                                 const float d2 = delta(pi[2], rc.z, 2);
                                 r2 += d2 * d2;
                             }
-                            const bool acc_ok = ok & (r2 < P.g.eps2);
+                            const bool near = r2 < P.g.eps2;
+                            const bool acc_ok = ok & near;
+                            // the accept bits straight from the two compare masks
+                            const uint64_t bal = __builtin_amdgcn_ballot_w64(near) & __builtin_amdgcn_ballot_w64(ok);
                             rho = ordered_group_sum<4>(rho, acc_ok ? poly6(r2, P.g) : 0.0f);
-                            return __builtin_amdgcn_ballot_w64(acc_ok);
+                            return bal;
                         };
                         const uint32_t rounds = (m + 3) / 4;
                         // four batches of four rounds (candidates 16 j .. 16 j + 15), each batch's
