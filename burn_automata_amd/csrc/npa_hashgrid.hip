@@ -83,6 +83,7 @@ static void each_buffer(Workspace& w, const HashgridPlan& plan, uint64_t total, 
     f(w.features, t1 * (uint64_t)(feature_dims ? feature_dims : 1) * 4);
     f(w.wpad, wpad_bytes ? wpad_bytes : 4);
     f(w.tmpidx, t1 * 4);
+    f(w.scan_status, (uint64_t)batch * ((plan.cells + 255) / 256) * 8 + 8);
     f(w.dir_n, (bins ? bins : 1) * 4);
     f(w.bin_list, (bins ? bins : 1) * 4);
     f(w.dir_e, (bins ? bins : 1) * kDirGroups * 16);
@@ -127,7 +128,7 @@ uint64_t Workspace::carve(const HashgridPlan& plan, uint64_t total, uint32_t bat
 void Workspace::release() {
     for (DevBuf* b : {&keys, &ranks, &table, &totals, &bin_offsets, &perm, &inv, &flags, &wl_count,
                       &worklist, &srec, &scoord, &sstate, &svol, &counters, &features, &wpad, &tmpidx,
-                      &dir_n, &dir_e, &bin_list, &act_rows, &row_of, &nb_base, &nb_mask, &nb_count})
+                      &dir_n, &dir_e, &bin_list, &act_rows, &row_of, &nb_base, &nb_mask, &nb_count, &scan_status})
         b->release();
 }
 
@@ -230,7 +231,9 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
                                                    uint32_t* __restrict__ ranks,
                                                    uint32_t* __restrict__ table,
                                                    uint32_t* __restrict__ flags,
-                                                   uint32_t* __restrict__ wl_count) {
+                                                   uint32_t* __restrict__ wl_count,
+                                                   unsigned long long* __restrict__ scan_status,
+                                                   uint32_t nstatus) {
     extern __shared__ uint16_t cnt[];
     const uint32_t C = g.cells;
     const uint32_t tile = blockIdx.x;
@@ -244,6 +247,8 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
     const uint32_t nwords = waves * C;
     for (uint32_t k = threadIdx.x; k < nwords; k += blockDim.x) cnt[k] = 0;
     if (wl_count && tile == 0 && threadIdx.x < 4) wl_count[threadIdx.x] = 0;  // work-list counters
+    for (uint32_t k = tile * blockDim.x + threadIdx.x; k < nstatus; k += gridDim.x * blockDim.x)
+        scan_status[k] = 0ull;  // the one-pass offsets scan's published totals (see k_table_offsets_scan)
     __syncthreads();
 
     // The first `waves` waves rank (one LDS counter row each); every wave of the block clears the
@@ -336,6 +341,83 @@ __global__ __launch_bounds__(256) void k_table_scan(uint32_t* __restrict__ table
         run += v;
     }
     totals[(uint64_t)b * C + k] = run;
+}
+
+// The column scan and the offsets scan in one pass, for the hashgrid build. Thread k of block x of
+// system b (key k = 256 x + thread): table[t][k] -> exclusive per-tile bases, as k_table_scan, and
+// the key's total. The block publishes the sum of its keys' totals (bit 63 marks it published;
+// k_hash_rank zeroed every status word of this build), adds the totals published by the system's
+// earlier blocks - dispatched before it, so each of them publishes and the wait ends - and writes
+// bin_offsets[b][k] = b * n + its keys' exclusive prefix. The last block of the last system also
+// writes the closing entry bin_offsets[batch * C].
+__global__ __launch_bounds__(256) void k_table_offsets_scan(uint32_t* __restrict__ table,
+                                                            uint32_t* __restrict__ bin_offsets,
+                                                            unsigned long long* __restrict__ status, uint32_t C,
+                                                            uint32_t tiles_per_sys, uint32_t n, uint32_t batch) {
+    __shared__ uint32_t wsum[4];
+    __shared__ uint32_t s_prefix;
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t b = blockIdx.y;
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    uint32_t run = 0;
+    if (k < C) {
+        uint32_t* col = table + (uint64_t)b * tiles_per_sys * C + k;
+        uint32_t t = 0;
+        for (; t + 8 <= tiles_per_sys; t += 8) {  // 8 independent loads per batch
+            uint32_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = col[(uint64_t)(t + u) * C];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                col[(uint64_t)(t + u) * C] = run;
+                run += v[u];
+            }
+        }
+        for (; t < tiles_per_sys; ++t) {
+            const uint32_t v = col[(uint64_t)t * C];
+            col[(uint64_t)t * C] = run;
+            run += v;
+        }
+    }
+    // the keys' exclusive prefix within the block
+    uint32_t x = run;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(x, off, 64);
+        if (lane >= (uint32_t)off) x += y;
+    }
+    if (lane == 63) wsum[w] = x;
+    __syncthreads();
+    uint32_t wpre = 0, btotal = 0;
+#pragma unroll
+    for (uint32_t v = 0; v < 4; ++v) {
+        if (v < w) wpre += wsum[v];
+        btotal += wsum[v];
+    }
+    const uint64_t row = (uint64_t)b * gridDim.x;
+    if (threadIdx.x == 0)
+        __hip_atomic_store(status + row + blockIdx.x, (1ull << 63) | btotal, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    if (w == 0) {  // the system's earlier blocks' totals, 64 at a time
+        uint32_t acc = 0;
+        for (uint32_t base = 0; base < blockIdx.x; base += 64) {
+            const uint32_t j = base + lane;
+            if (j < blockIdx.x) {
+                unsigned long long v;
+                do {
+                    v = __hip_atomic_load(status + row + j, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+                } while (!(v >> 63));
+                acc += (uint32_t)v;
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+        if (lane == 0) s_prefix = acc;
+    }
+    __syncthreads();
+    const uint32_t prefix = s_prefix;
+    if (k < C) bin_offsets[(uint64_t)b * C + k] = b * n + prefix + wpre + x - run;
+    if (b == batch - 1 && blockIdx.x == gridDim.x - 1 && threadIdx.x == 0)
+        bin_offsets[(uint64_t)batch * C] = b * n + prefix + btotal;
 }
 
 // Exclusive scan of one value per thread over a 1024-thread block.
@@ -1038,7 +1120,8 @@ static hipError_t launch_rank_r(uint32_t blocks, uint32_t waves, uint32_t lds_by
                                 uint32_t tiles_per_sys, uint32_t key_bits, const GridParams& g,
                                 const float4* pos, const uint32_t* keys_in, const uint32_t* d_count,
                                 uint32_t n, uint32_t* keys, uint32_t* ranks, uint32_t* table,
-                                uint32_t* flags, uint32_t* wl_count, hipStream_t stream, Profiler* prof) {
+                                uint32_t* flags, uint32_t* wl_count, unsigned long long* scan_status,
+                                uint32_t nstatus, hipStream_t stream, Profiler* prof) {
     static uint32_t attr_bytes = 32768;
     if (lds_bytes > attr_bytes) {
         hipError_t e = hipFuncSetAttribute((const void*)k_hash_rank<R>,
@@ -1051,17 +1134,18 @@ static hipError_t launch_rank_r(uint32_t blocks, uint32_t waves, uint32_t lds_by
     const uint32_t threads = g.cells >= 4096 ? 1024 : 256;
     return launch_timed(prof, NPA_KERNEL_HASH_RANK, k_hash_rank<R>, dim3(blocks), dim3(threads), lds_bytes, stream,
                         pos, keys_in, d_count, n, tiles_per_sys, waves, g, key_bits, keys, ranks, table, flags,
-                        wl_count);
+                        wl_count, scan_status, nstatus);
 }
 
 static hipError_t launch_rank(uint32_t rounds, uint32_t blocks, uint32_t waves, uint32_t lds_bytes,
                               uint32_t tiles_per_sys, uint32_t key_bits, const GridParams& g,
                               const float4* pos, const uint32_t* keys_in, const uint32_t* d_count,
                               uint32_t n, uint32_t* keys, uint32_t* ranks, uint32_t* table,
-                              uint32_t* flags, uint32_t* wl_count, hipStream_t stream, Profiler* prof) {
+                              uint32_t* flags, uint32_t* wl_count, unsigned long long* scan_status,
+                              uint32_t nstatus, hipStream_t stream, Profiler* prof) {
 #define NPA_RANK(RR)                                                                             \
     return launch_rank_r<RR>(blocks, waves, lds_bytes, tiles_per_sys, key_bits, g, pos, keys_in, \
-                             d_count, n, keys, ranks, table, flags, wl_count, stream, prof)
+                             d_count, n, keys, ranks, table, flags, wl_count, scan_status, nstatus, stream, prof)
     switch (rounds) {
         case 1: NPA_RANK(1);
         case 2: NPA_RANK(2);
@@ -1078,16 +1162,16 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                            Workspace& ws, bool payload, hipStream_t stream, Profiler* prof,
                            const SplitTargets* targets) {
     const uint64_t total = (uint64_t)batch * n;
+    const uint32_t kblocks = (plan.cells + 255) / 256;  // 256-key blocks of the one-pass scan
     hipError_t e = launch_rank(plan.rounds, batch * plan.tiles_per_sys, plan.waves, plan.lds_bytes,
                                plan.tiles_per_sys, plan.key_bits, g, pos, nullptr, nullptr, n, ws.keys.as<uint32_t>(),
                                ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(), ws.flags.as<uint32_t>(),
-                               ws.wl_count.as<uint32_t>(), stream, prof);
+                               ws.wl_count.as<uint32_t>(), ws.scan_status.as<unsigned long long>(), batch * kblocks,
+                               stream, prof);
     if (e != hipSuccess) return e;
-    e = launch_timed(prof, NPA_KERNEL_TABLE_SCAN, k_table_scan, dim3((plan.cells + 255) / 256, batch), dim3(256), 0,
-                     stream, ws.table.as<uint32_t>(), ws.totals.as<uint32_t>(), plan.cells, plan.tiles_per_sys);
-    if (e != hipSuccess) return e;
-    e = launch_offsets_scan(ws.totals.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), plan.cells, n, batch, stream,
-                            prof);
+    e = launch_timed(prof, NPA_KERNEL_TABLE_SCAN, k_table_offsets_scan, dim3(kblocks, batch), dim3(256), 0, stream,
+                     ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), ws.scan_status.as<unsigned long long>(),
+                     plan.cells, plan.tiles_per_sys, n, batch);
     if (e != hipSuccess) return e;
     const uint32_t blocks = (uint32_t)((total + 255) / 256);
     const SplitTargets tg = targets ? *targets : SplitTargets{};
@@ -1187,7 +1271,7 @@ hipError_t launch_key_sort(const HashgridPlan& p, const uint32_t* keys, const ui
     g.cells = p.cells;
     hipError_t e = launch_rank(p.rounds, p.tiles_per_sys, p.waves, p.lds_bytes, p.tiles_per_sys,
                                p.key_bits, g, nullptr, keys, d_count, cap, nullptr, ranks, table,
-                               flags, nullptr, stream, nullptr);
+                               flags, nullptr, nullptr, 0u, stream, nullptr);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_table_scan, dim3((p.cells + 255) / 256, 1), dim3(256), 0, stream, table, totals,
                        p.cells, p.tiles_per_sys);

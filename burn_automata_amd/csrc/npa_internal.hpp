@@ -104,6 +104,9 @@ struct Workspace {
     // the second pass gathers a neighbour's position and volume with one load
     DevBuf svol;
     DevBuf tmpidx, dir_n, dir_e;
+    // one-pass offsets scan: per (system, 256-key block) the block's published key total
+    // (bit 63 = published; zeroed by k_hash_rank at the start of every build)
+    DevBuf scan_status;
     // sparse grids: the bins too large for the one-lane split (count in wl_count[1])
     DevBuf bin_list;
     // Targets of the second pass and the update: particles whose update mask is not 0 (the others
