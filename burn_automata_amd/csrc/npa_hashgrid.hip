@@ -4,7 +4,7 @@
 // bin_offsets = exclusive prefix of per-bin counts, and inside each bin the particles
 // keep ascending original index (the reference's serial stable scatter).
 //
-// Four kernels per build:
+// Kernels per build:
 //   k_hash_rank    one block = one tile of `waves*R*64` consecutive particles of one
 //                  system. Each wave walks its contiguous slice in rounds of 64: the cell
 //                  key of each lane, its peers (lanes with the same key) from
@@ -12,8 +12,10 @@
 //                  a per-wave LDS counter per key (u16) carried across rounds. After a
 //                  barrier, ranks are offset by the earlier waves' counters and the tile's
 //                  per-key histogram row is written to table[tile][key].
-//   k_table_scan   per key, exclusive prefix over the system's tiles (column scan).
-//   k_offsets_scan per system, exclusive prefix over keys -> bin_offsets.
+//   k_table_offsets_scan  per key, exclusive prefix over the system's tiles (column scan);
+//                  per block of 256 keys, the prefix of the earlier blocks' key totals from
+//                  their published sums (one pass) -> bin_offsets. The generic key sorts
+//                  run the two scans as k_table_scan and k_offsets_scan.
 //   k_scatter      dst = bin_offsets[key] + table[tile][key] + rank; writes the
 //                  permutation and its inverse. The rollout step's k_scatter_payload also
 //                  writes the sorted particle records and state rows the neighbour passes

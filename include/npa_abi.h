@@ -508,8 +508,8 @@ npa_status npa_sha256(const uint8_t* data, size_t len, uint8_t* digest /* 32 byt
 /* Kernel ids for npa_profile_read. */
 enum {
     NPA_KERNEL_HASH_RANK = 0,
-    NPA_KERNEL_TABLE_SCAN = 1,
-    NPA_KERNEL_OFFSETS_SCAN = 2,
+    NPA_KERNEL_TABLE_SCAN = 1,     /* hashgrid build: tile-column scan fused with the offsets scan */
+    NPA_KERNEL_OFFSETS_SCAN = 2,   /* the separate offsets scan of the generic key sorts */
     NPA_KERNEL_SCATTER = 3,
     NPA_KERNEL_DENSITY = 4,
     NPA_KERNEL_PERCEIVE = 5,   /* second neighbour pass + normalisation + feature rows */
