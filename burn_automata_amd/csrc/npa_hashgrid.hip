@@ -71,7 +71,7 @@ static void each_buffer(Workspace& w, const HashgridPlan& plan, uint64_t total, 
     f(w.bin_offsets, (bins + 1) * 4);
     f(w.perm, t1 * 4);
     f(w.inv, t1 * 4);
-    f(w.wl_count, 64);
+    f(w.wl_count, 256);
     f(w.worklist, (plan.worklist_cap + 1) * 8);
     // second-pass items: at most one partial item per (64-slot window, cell run) pair
     f(w.act_rows, t1 * 4);
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
     }
     const uint32_t nwords = waves * C;
     for (uint32_t k = threadIdx.x; k < nwords; k += blockDim.x) cnt[k] = 0;
-    if (wl_count && tile == 0 && threadIdx.x < 4) wl_count[threadIdx.x] = 0;  // work-list counters
+    if (wl_count && tile == 0 && threadIdx.x < 64) wl_count[threadIdx.x] = 0;  // work-list counters
     for (uint32_t k = tile * blockDim.x + threadIdx.x; k < nstatus; k += gridDim.x * blockDim.x)
         scan_status[k] = 0ull;  // the one-pass offsets scan's published totals (see k_table_offsets_scan)
     __syncthreads();
@@ -664,6 +664,7 @@ __global__ __launch_bounds__(256) void k_scatter_payload(uint32_t n, uint32_t to
 // step's update mask get consecutive compact rows (act_rows[row] = slot, in slot order within the
 // bin); the scatter has written the others to the step's output (hold_particle).
 constexpr uint32_t kSplitWaves = 16;  // bins (waves) per k_split block
+constexpr uint32_t kSplitHeld = 3;    // chunks of 64 slots a k_split wave loads at once and keeps
 
 template <int D>
 __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, const float* __restrict__ states,
@@ -753,16 +754,40 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
             if (k < ng && c[0] == gx[k] && c[1] == gy[k] && c[2] == gz[k]) gid = (int)k;
         return gid;
     };
-    // the first chunk (the whole bin for most bins) is loaded once for both passes
-    bool valid0 = false;
-    uint32_t i0 = 0;
-    int cf[3] = {0, 0, 0};
-    if (beg < end) load_sorted(beg, valid0, i0, cf);
-    for (uint32_t c0 = beg; c0 < end && !over; c0 += 64) {
-        bool valid = valid0;
-        uint32_t i = i0;
-        int c[3] = {cf[0], cf[1], cf[2]};
-        if (c0 != beg) load_sorted(c0, valid, i, c);
+    // the first kSplitHeld chunks (the whole bin for most bins) are loaded together, before any is
+    // used, and kept for both passes; a rewritten bin takes its positions and cells from them
+    constexpr uint32_t NH = kSplitHeld;
+    bool hv[NH], ht[NH];
+    uint32_t hi[NH];
+    int hc[NH][3];
+    float4 hr[NH];
+#pragma unroll
+    for (uint32_t k = 0; k < NH; ++k) {
+        hv[k] = ht[k] = false;
+        hi[k] = 0;
+        hc[k][0] = hc[k][1] = hc[k][2] = 0;
+        hr[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const uint32_t c0 = beg + 64 * k;
+        if (c0 < end) {
+            const uint32_t slot = c0 + lane;
+            hv[k] = slot < end;
+            const uint32_t sl = hv[k] ? slot : c0;
+            hr[k] = srec[sl];
+            if constexpr (D == 2) {
+                hi[k] = order[sl];
+                hc[k][0] = __float_as_int(hr[k].z);
+                hc[k][1] = __float_as_int(hr[k].w);
+            } else {
+                const int4 cc = scoord[sl];
+                hc[k][0] = cc.x;
+                hc[k][1] = cc.y;
+                hc[k][2] = cc.z;
+                hi[k] = (uint32_t)cc.w;
+            }
+        }
+    }
+    // first pass over one chunk: new cells join the directory in order of first appearance
+    auto count_chunk = [&](bool valid, uint32_t i, const int c[3]) -> bool {
         int gid = group_of(c);
         uint64_t unknown = __ballot(valid && gid < 0);
         while (unknown) {
@@ -791,6 +816,17 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
             gc[k] += (uint32_t)__popcll(__ballot(valid && gid == (int)k));
             gt[k] += (uint32_t)__popcll(__ballot(tgt && gid == (int)k));
         }
+        return tgt;
+    };
+#pragma unroll
+    for (uint32_t k = 0; k < NH; ++k)
+        if (beg + 64 * k < end && !over) ht[k] = count_chunk(hv[k], hi[k], hc[k]);
+    for (uint32_t c0 = beg + 64 * NH; c0 < end && !over; c0 += 64) {
+        bool valid;
+        uint32_t i;
+        int c[3];
+        load_sorted(c0, valid, i, c);
+        count_chunk(valid, i, c);
     }
     uint32_t nitems = 0, nrows = 0;
     uint32_t start[K];
@@ -823,8 +859,11 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
             tot += s_items[w];
             rows += s_rows[w];
         }
-        s_base = tot ? atomicAdd(wl_count, tot) : 0u;
-        s_rbase = rows ? atomicAdd(wl_count + 3, rows) : 0u;
+        // items (low word) and rows (high word) reserved by one atomic
+        const unsigned long long add = (unsigned long long)tot | ((unsigned long long)rows << 32);
+        const unsigned long long old = add ? atomicAdd(reinterpret_cast<unsigned long long*>(wl_count), add) : 0ull;
+        s_base = (uint32_t)old;
+        s_rbase = (uint32_t)(old >> 32);
     }
     __syncthreads();
     uint32_t wbase = s_base;  // first work item of this bin
@@ -874,17 +913,11 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
         }
     }
     // one cell: the runs are the scatter's order and its payload stays; several cells are reordered
-    // here from the step's input arrays
+    // here (the held chunks from their sorted records, read in the first pass before any slot is
+    // rewritten; later chunks from the step's input arrays)
     const bool rewrite = ng > 1;
-    for (uint32_t c0 = beg; c0 < end; c0 += 64) {
-        bool valid = valid0;
-        uint32_t i = i0;
-        float4 p4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        int c[3] = {cf[0], cf[1], cf[2]};
-        if (rewrite) load(c0, valid, i, p4, c);
-        else if (c0 != beg) load_sorted(c0, valid, i, c);
+    auto place_chunk = [&](bool valid, uint32_t i, const int c[3], const float4& p4, bool tgt) {
         const int gid = group_of(c);
-        const bool tgt = is_target(valid, i);
         uint32_t dst = 0, row = 0;
 #pragma unroll
         for (uint32_t k = 0; k < K; ++k) {
@@ -899,6 +932,18 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
         }
         if (valid && rewrite) write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
         place(valid, tgt, dst, row);
+    };
+#pragma unroll
+    for (uint32_t k = 0; k < NH; ++k)
+        if (beg + 64 * k < end) place_chunk(hv[k], hi[k], hc[k], hr[k], ht[k]);
+    for (uint32_t c0 = beg + 64 * NH; c0 < end; c0 += 64) {
+        bool valid;
+        uint32_t i;
+        float4 p4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        int c[3];
+        if (rewrite) load(c0, valid, i, p4, c);
+        else load_sorted(c0, valid, i, c);
+        place_chunk(valid, i, c, p4, is_target(valid, i));
     }
     uint32_t off = 0;
 #pragma unroll
@@ -923,7 +968,7 @@ __global__ __launch_bounds__(1024) void k_split(const float4* __restrict__ pos, 
 // bin would spend a whole wave's instructions on an empty or one-particle bin.
 constexpr uint32_t kThinMax = kDirGroups;
 
-constexpr uint32_t kThinThreads = 256;  // bins per k_split_thin block (one reservation each)
+constexpr uint32_t kThinThreads = 512;  // bins per k_split_thin block (one reservation each)
 
 // Exclusive prefix of v over a kThinThreads block and the block's total.
 __device__ __forceinline__ uint32_t block_prefix_thin(uint32_t v, uint32_t* ldsw, uint32_t* total) {
@@ -1053,9 +1098,11 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
     const uint32_t pr_ = block_prefix_thin(nrows, lds_r, &tr);
     const uint32_t pf_ = block_prefix_thin(fat ? 1u : 0u, lds_f, &tf);
     if (threadIdx.x == 0) {
-        s_base[0] = ti ? atomicAdd(wl_count, ti) : 0u;
-        s_base[1] = tr ? atomicAdd(wl_count + 3, tr) : 0u;
-        s_base[2] = tf ? atomicAdd(wl_count + 1, tf) : 0u;
+        const unsigned long long add = (unsigned long long)ti | ((unsigned long long)tr << 32);
+        const unsigned long long old = add ? atomicAdd(reinterpret_cast<unsigned long long*>(wl_count), add) : 0ull;
+        s_base[0] = (uint32_t)old;
+        s_base[1] = (uint32_t)(old >> 32);
+        s_base[2] = tf ? atomicAdd(wl_count + kListedWord, tf) : 0u;
     }
     __syncthreads();
     if (fat) bin_list[s_base[2] + pf_] = bin;
@@ -1219,7 +1266,7 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                        ws.inv.as<uint32_t>(), ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(),
                        ws.dir_n.as<uint32_t>(), ws.dir_e.as<int4>(), ws.worklist.as<uint2>(),
                        ws.wl_count.as<uint32_t>(), plan.tpi, tg, ws.act_rows.as<uint32_t>(), ws.row_of.as<uint32_t>(),
-                       (const uint32_t*)ws.bin_list.as<uint32_t>(), (const uint32_t*)(ws.wl_count.as<uint32_t>() + 1));
+                       (const uint32_t*)ws.bin_list.as<uint32_t>(), (const uint32_t*)(ws.wl_count.as<uint32_t>() + kListedWord));
     return hipGetLastError();
 }
 

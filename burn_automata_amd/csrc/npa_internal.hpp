@@ -94,6 +94,7 @@ struct HashgridPlan {
 // directory entry {cx, cy, cz, first slot} per run; dir_n[bin] = number of runs, or
 // kDirGroups + 1 when the bin holds more cells and keeps the reference order.
 constexpr uint32_t kDirGroups = 8;
+constexpr uint32_t kListedWord = 32;  // wl_count word of the thin split's listed-bin count
 
 struct Workspace {
     // flags: u32 [0] the current build's coordinate overflow (set by k_hash_rank, moved by
@@ -107,11 +108,13 @@ struct Workspace {
     // one-pass offsets scan: per (system, 256-key block) the block's published key total
     // (bit 63 = published; zeroed by k_hash_rank at the start of every build)
     DevBuf scan_status;
-    // sparse grids: the bins too large for the one-lane split (count in wl_count[1])
+    // sparse grids: the bins too large for the one-lane split (count in wl_count[kListedWord])
     DevBuf bin_list;
     // Targets of the second pass and the update: particles whose update mask is not 0 (the others
     // are written to the output by the update-mask kernel). act_rows: compact row -> slot.
-    // Counts (u32 words of wl_count): [0] density items, [1] listed bins, [3] compact rows.
+    // Counts (u32 words of wl_count, 256 bytes): [0] density items, [1] compact rows (one 64-bit
+    // word, so one atomic reserves both), [kListedWord] listed bins (another cache line, so its
+    // atomics do not queue behind the reservations).
     DevBuf act_rows;
     // row_of: slot -> compact row of an update-mask target, or ~0u (written by the split).
     // Accepted neighbours recorded by the density pass for the targets, per neighbour chunk (<= 64
@@ -144,7 +147,7 @@ GridParams make_grid_params(const npa_grid_cfg& cfg);
 float host_powi(float x, int n);
 
 // The particles a step's second pass and update MLP process: those whose update mask is not 0.
-// The split kernel gives them consecutive compact rows (act_rows, count in wl_count[3]) and writes
+// The split kernel gives them consecutive compact rows (act_rows, count in wl_count[1]) and writes
 // every other particle to the step's output with the Euler step's wrap / clamp only
 // (hold_particle). mask_mode: 0 every particle (no copies), 1 the device hash mask, 2 a mask array.
 struct SplitTargets {

@@ -148,7 +148,8 @@ __global__ __launch_bounds__(256) void k_density_q(StepParams P, const float4* _
         const bool record = row != ~0u;
         float rho = 0.0f;
         uint32_t nch = 0;
-        uint64_t pending = __ballot(active);
+        const uint64_t act_all = __ballot(active);
+        uint64_t pending = act_all;
         while (pending) {
             const int leader = __ffsll((unsigned long long)pending) - 1;
             const int l0 = readlane_i(ci[0], leader), l1 = readlane_i(ci[1], leader);
@@ -157,6 +158,7 @@ __global__ __launch_bounds__(256) void k_density_q(StepParams P, const float4* _
             const uint64_t group = __ballot(same) & pending;
             pending &= ~group;
             const bool in_group = (group >> lane) & 1ull;
+            const bool all_in = group == act_all && P.g.k6 <= 3.4028235e38f;  // the rounds' fast form
             uint32_t gch = 0;  // chunk index within the group's visit order (wave-uniform)
             uint32_t nb_beg, nb_end;
             bool nb_filter, nb_found;
@@ -172,12 +174,16 @@ __global__ __launch_bounds__(256) void k_density_q(StepParams P, const float4* _
                     const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
                     const float4* cand = srec + base;
                     uint32_t mk[2] = {0u, 0u};  // accept mask, candidates 0-31 and 32-63
-                    // FILT: an unsplit bin's candidates are tested for the cell; PER: periodic deltas
-                    auto walk = [&](auto FILT, auto PER) {
+                    // FILT: an unsplit bin's candidates are tested for the cell; PER: periodic deltas;
+                    // FAST: the group is every active target of the item (one cell: any item of a
+                    // split bin) and the poly6 constant is finite - no lane masks in the rounds
+                    auto walk = [&](auto FILT, auto PER, auto FAST) {
                         constexpr bool filt = decltype(FILT)::value, per = decltype(PER)::value;
+                        constexpr bool fast = decltype(FAST)::value;
                         constexpr bool xy = D == 2 && !filt;  // only the position is read
                         // k < 64: slots past the run are other runs' records or the records'
-                        // 64-slot padding, loaded and never accepted (k >= m fails `ok`)
+                        // 64-slot padding, loaded and never accepted (k >= m fails `ok`; the fast
+                        // form moves their x to +inf, which no target is near)
                         auto load = [&](uint32_t k) {
                             if constexpr (xy) {
                                 const float2 v = *reinterpret_cast<const float2*>(cand + k);
@@ -187,16 +193,6 @@ __global__ __launch_bounds__(256) void k_density_q(StepParams P, const float4* _
                             }
                         };
                         auto test = [&](uint32_t r, const float4 rc) {  // round r: candidate 4 r + q
-                            const uint32_t k = 4 * r + q;
-                            bool ok = in_group & (k < m);
-                            if constexpr (filt) {
-                                if constexpr (D == 2) {
-                                    ok = ok & ((int64_t)__float_as_int(rc.z) == n0) & ((int64_t)__float_as_int(rc.w) == n1);
-                                } else {
-                                    const int4 cc = scoord[base + k];
-                                    ok = ok & ((int64_t)cc.x == n0) & ((int64_t)cc.y == n1) & ((int64_t)cc.z == n2);
-                                }
-                            }
                             auto delta = [&](float a, float bj, int ax) {  // neighbor_delta hashgrid.rs:165-181
                                 const float v = bj - a;
                                 if constexpr (!per) return v;
@@ -212,6 +208,24 @@ __global__ __launch_bounds__(256) void k_density_q(StepParams P, const float4* _
                                 r2 += d2 * d2;
                             }
                             const bool near = r2 < P.g.eps2;
+                            if constexpr (fast) {
+                                // a rejected candidate's term is +0.0 from x = max(eps^2 - r^2, +0.0)
+                                // (r^2 >= eps^2, +inf or NaN); an accepted one has x > 0 and
+                                // poly6's operations, so the sum is the masked form's
+                                const float x = fmaxf(P.g.eps2 - r2, 0.0f);
+                                rho = ordered_group_sum<4>(rho, P.g.k6 * x * x * x);
+                                return (uint64_t)__builtin_amdgcn_ballot_w64(near);
+                            }
+                            const uint32_t k = 4 * r + q;
+                            bool ok = in_group & (k < m);
+                            if constexpr (filt) {
+                                if constexpr (D == 2) {
+                                    ok = ok & ((int64_t)__float_as_int(rc.z) == n0) & ((int64_t)__float_as_int(rc.w) == n1);
+                                } else {
+                                    const int4 cc = scoord[base + k];
+                                    ok = ok & ((int64_t)cc.x == n0) & ((int64_t)cc.y == n1) & ((int64_t)cc.z == n2);
+                                }
+                            }
                             const bool acc_ok = ok & near;
                             // the accept bits straight from the two compare masks
                             const uint64_t bal = __builtin_amdgcn_ballot_w64(near) & __builtin_amdgcn_ballot_w64(ok);
@@ -228,6 +242,13 @@ __global__ __launch_bounds__(256) void k_density_q(StepParams P, const float4* _
                             float4 ra[4];
 #pragma unroll
                             for (int u = 0; u < 4; ++u) ra[u] = load(16 * j + 4 * u + q);
+                            if constexpr (fast) {
+                                if (16 * j + 16 > m) {  // the batch that reaches past the run
+#pragma unroll
+                                    for (int u = 0; u < 4; ++u)
+                                        if (16 * j + 4 * u + q >= m) ra[u].x = __builtin_inff();
+                                }
+                            }
                             uint32_t bits = 0;
 #pragma unroll
                             for (uint32_t u = 0; u < 4; ++u) {
@@ -240,12 +261,17 @@ __global__ __launch_bounds__(256) void k_density_q(StepParams P, const float4* _
                         }
                     };
                     const bool periodic = P.g.boundary == 0;
+                    using T_ = std::true_type;
+                    using F_ = std::false_type;
                     if (filter) {
-                        if (periodic) walk(std::true_type{}, std::true_type{});
-                        else walk(std::true_type{}, std::false_type{});
+                        if (periodic) walk(T_{}, T_{}, F_{});
+                        else walk(T_{}, F_{}, F_{});
+                    } else if (all_in) {
+                        if (periodic) walk(F_{}, T_{}, T_{});
+                        else walk(F_{}, F_{}, T_{});
                     } else {
-                        if (periodic) walk(std::false_type{}, std::true_type{});
-                        else walk(std::false_type{}, std::false_type{});
+                        if (periodic) walk(F_{}, T_{}, F_{});
+                        else walk(F_{}, F_{}, F_{});
                     }
                     if (in_group && q == 0 && record && gch < MAXC) {
                         nb_base[(uint64_t)row * MAXC + gch] = base;
@@ -1306,7 +1332,7 @@ static hipError_t launch_perceive_f(const StepParams& p, Workspace& ws, const St
     return launch_timed(prof, NPA_KERNEL_PERCEIVE, k_perceive<D, SM, MODE, FL>, dim3(blocks), dim3(64), 0, stream, p, ws.srec.as<float4>(),
                        ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.svol.as<float4>(),
                        ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(), ws.act_rows.as<uint32_t>(),
-                       ws.wl_count.as<uint32_t>() + 3, ws.nb_base.as<uint32_t>(), ws.nb_mask.as<uint64_t>(),
+                       ws.wl_count.as<uint32_t>() + 1, ws.nb_base.as<uint32_t>(), ws.nb_mask.as<uint64_t>(),
                        ws.nb_count.as<uint32_t>(), ws.features.as<float>(), io);
 }
 
@@ -1378,7 +1404,7 @@ static hipError_t launch_mlp_e(const StepParams& p, Workspace& ws, const StepIO&
     const uint32_t blocks = (p.T + 63) / 64;
     return launch_timed(prof, NPA_KERNEL_MLP, k_mlp_euler<D, SM, FM, ENG>, dim3(blocks), dim3(256), (uint32_t)lds,
                         stream, p, ws.features.as<float>(), ws.sstate.as<float>(), ws.perm.as<uint32_t>(),
-                        ws.act_rows.as<uint32_t>(), ws.wl_count.as<uint32_t>() + 3, ws.wpad.as<float>(), io);
+                        ws.act_rows.as<uint32_t>(), ws.wl_count.as<uint32_t>() + 1, ws.wpad.as<float>(), io);
 }
 
 template <int D, int SM, int FM>

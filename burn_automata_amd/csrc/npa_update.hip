@@ -873,7 +873,7 @@ static hipError_t launch_fused_t(const StepParams& p, Workspace& ws, const StepI
     return launch_timed(prof, NPA_KERNEL_UPDATE, k_update_fused<D, FL, ENG>, dim3(blocks), dim3(64 * kFuseWaves),
                         (uint32_t)lds, stream, p, ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(),
                         ws.svol.as<float4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
-                        ws.act_rows.as<uint32_t>(), (const uint32_t*)(wl + 3), ws.nb_base.as<uint32_t>(),
+                        ws.act_rows.as<uint32_t>(), (const uint32_t*)(wl + 1), ws.nb_base.as<uint32_t>(),
                         ws.nb_mask.as<uint64_t>(), ws.nb_count.as<uint32_t>(), wfused, io);
 }
 
