@@ -71,7 +71,7 @@ static void each_buffer(Workspace& w, const HashgridPlan& plan, uint64_t total, 
     f(w.bin_offsets, (bins + 1) * 4);
     f(w.perm, t1 * 4);
     f(w.inv, t1 * 4);
-    f(w.wl_count, 256);
+    f(w.wl_count, 4 * kWlWords);
     f(w.worklist, (plan.worklist_cap + 1) * 8);
     // second-pass items: at most one partial item per (64-slot window, cell run) pair
     f(w.act_rows, t1 * 4);
@@ -248,7 +248,8 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
     }
     const uint32_t nwords = waves * C;
     for (uint32_t k = threadIdx.x; k < nwords; k += blockDim.x) cnt[k] = 0;
-    if (wl_count && tile == 0 && threadIdx.x < 64) wl_count[threadIdx.x] = 0;  // work-list counters
+    if (wl_count && tile == 0)  // work-list counters and item queues
+        for (uint32_t k = threadIdx.x; k < kWlWords; k += blockDim.x) wl_count[k] = 0;
     for (uint32_t k = tile * blockDim.x + threadIdx.x; k < nstatus; k += gridDim.x * blockDim.x)
         scan_status[k] = 0ull;  // the one-pass offsets scan's published totals (see k_table_offsets_scan)
     __syncthreads();

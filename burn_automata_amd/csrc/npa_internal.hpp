@@ -95,6 +95,9 @@ struct HashgridPlan {
 // kDirGroups + 1 when the bin holds more cells and keeps the reference order.
 constexpr uint32_t kDirGroups = 8;
 constexpr uint32_t kListedWord = 32;  // wl_count word of the thin split's listed-bin count
+constexpr uint32_t kQueueWord = 64;    // wl_count word of the fused update's first item queue
+constexpr uint32_t kQueueStride = 32;  // words between queues (one 128-byte line each; eight queues)
+constexpr uint32_t kWlWords = 512;     // wl_count words, all zeroed by the hashgrid build
 
 struct Workspace {
     // flags: u32 [0] the current build's coordinate overflow (set by k_hash_rank, moved by
@@ -112,9 +115,10 @@ struct Workspace {
     DevBuf bin_list;
     // Targets of the second pass and the update: particles whose update mask is not 0 (the others
     // are written to the output by the update-mask kernel). act_rows: compact row -> slot.
-    // Counts (u32 words of wl_count, 256 bytes): [0] density items, [1] compact rows (one 64-bit
+    // Counts (u32 words of wl_count, kWlWords): [0] density items, [1] compact rows (one 64-bit
     // word, so one atomic reserves both), [kListedWord] listed bins (another cache line, so its
-    // atomics do not queue behind the reservations).
+    // atomics do not queue behind the reservations), [kQueueWord + x * kQueueStride] the fused
+    // update's item queue of XCD x.
     DevBuf act_rows;
     // row_of: slot -> compact row of an update-mask target, or ~0u (written by the split).
     // Accepted neighbours recorded by the density pass for the targets, per neighbour chunk (<= 64

@@ -218,7 +218,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
                                                        const uint32_t* __restrict__ bo,
                                                        const uint32_t* __restrict__ perm,
                                                        const uint32_t* __restrict__ act_rows,
-                                                       const uint32_t* __restrict__ row_count,
+                                                       uint32_t* __restrict__ wlc,
                                                        const uint32_t* __restrict__ nb_base,
                                                        const uint64_t* __restrict__ nb_mask,
                                                        const uint32_t* __restrict__ nb_count,
@@ -231,12 +231,9 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
     const uint32_t FP = P.FP;
     const uint32_t wfloats = (uint32_t)fused_weight_floats(FP, D);
 
-    // the block's next item position (see below), after the waves' regions
-    uint32_t* s_take = reinterpret_cast<uint32_t*>(lds + wfloats + (size_t)kFuseWaves * Sh::WAVE_FLOATS);
     // the block's copy of the padded weights
     for (uint32_t v = threadIdx.x; v < wfloats / 4; v += blockDim.x)
         reinterpret_cast<float4*>(lds)[v] = reinterpret_cast<const float4*>(wfused)[v];
-    if (threadIdx.x == 0) *s_take = kFuseWaves;
     __syncthreads();
     const float* w1q = lds;
     const float* b1 = w1q + (size_t)FP * HP;
@@ -256,33 +253,34 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
     const bool want_dg = FL >= 0 ? (FL & 2) != 0 : P.density_grad != 0;
     const bool want_m = FL >= 0 ? (FL & 5) == 5 : (want_sg && P.hybrid);
     const bool branch_a = want_sg && want_dg;
-    const uint32_t nrows = *row_count;
+    const uint32_t nrows = wlc[1];  // compact rows (update-mask targets)
     const uint32_t nitems = (nrows + 3) / 4;
     const uint32_t xcomp = c < NX ? c : 0u;  // the per-target sum this lane keeps
 
-    // Items of four consecutive compact rows, dealt round-robin over every wave of the grid: the
-    // block's 16 waves take 16 consecutive items at a time (neighbouring rows share cells, so the
-    // CU's L1 serves their neighbours), and a run of heavy items (a dense region of the sorted
-    // order) is spread over many CUs instead of landing on one. Blocks are dispatched to the eight
-    // XCDs in turn, so block b is renumbered (b % 8) * (G / 8) + b / 8: each XCD then walks one
-    // contiguous run of G / 8 * 16 items per pass and its L2 holds their neighbour rows once.
-    // Within a block the items are taken in order from an LDS counter (position j = item
-    // lblock * 16 + j % 16 + (j / 16) * G * 16), the first one per wave dealt statically: a wave
-    // that the SIMD's oldest-first issue keeps waiting takes fewer items, so the block's waves end
-    // together instead of the youngest ones running a tail alone.
-    const uint32_t item_stride = gridDim.x * kFuseWaves;
-    const uint32_t lblock = gridDim.x % 8 == 0 ? (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8 : blockIdx.x;
-    auto item_of = [&](uint32_t j) { return lblock * kFuseWaves + j % kFuseWaves + (j / kFuseWaves) * item_stride; };
+    // Items of four consecutive compact rows, in rounds of G * 16 consecutive items (neighbouring
+    // rows share cells, so a CU's L1 and an XCD's L2 serve their neighbours once; a run of heavy
+    // items, a dense region of the sorted order, is spread over many CUs). Blocks are dispatched to
+    // the eight XCDs in turn: the blocks b with b % 8 == x share queue x, which hands out the x-th
+    // eighth of every round (p-th position: round p / R, item round * G * 16 + x * R + p % R with
+    // R = G / 8 * 16). Each wave's first position is dealt statically (block b's waves take
+    // b / 8 * 16 + wave); later ones come from the queue's counter (zeroed with the work-list
+    // counters by the hashgrid build) when an item is done, so the XCD's waves share its items to
+    // the end, and a wave that the SIMD's oldest-first issue keeps waiting takes fewer of them.
+    const uint32_t nq = gridDim.x % 8 == 0 ? 8u : 1u;
+    const uint32_t xq = blockIdx.x % nq;
+    const uint32_t per_round = gridDim.x / nq * kFuseWaves;
+    auto item_at = [&](uint32_t p) { return (p / per_round) * (gridDim.x * kFuseWaves) + xq * per_round + p % per_round; };
+    uint32_t* queue = wlc + kQueueWord + xq * kQueueStride;
     auto take = [&]() {
-        uint32_t j = 0;
-        if (lane == 0) j = atomicAdd(s_take, 1u);
-        return (uint32_t)__builtin_amdgcn_readfirstlane((int)j);
+        uint32_t p = 0;
+        if (lane == 0) p = atomicAdd(queue, 1u);
+        return per_round + (uint32_t)__builtin_amdgcn_readfirstlane((int)p);
     };
     auto slot_of = [&](uint32_t it) {
         const uint32_t r = it * 4 + g;
         return act_rows[r < nrows ? r : it * 4];
     };
-    uint32_t item = item_of(wave);
+    uint32_t item = item_at(blockIdx.x / nq * kFuseWaves + wave);
     uint32_t s_next = item < nitems ? slot_of(item) : 0u;  // the item's compact-row slot
     while (item < nitems) {
         const uint32_t row = item * 4 + g;
@@ -845,9 +843,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
         float next = si + P.dt * dsc * mk;
         if (clamped_channel(D, P.S, c)) next = clampf_(next, -8.0f, 24.0f);
         if (active && c < P.S) io.out_states[(uint64_t)i * P.S + c] = next;
-        // the next position is taken when this item is done, so a wave that is kept waiting
-        // takes fewer of the block's items
-        item = item_of(take());
+        item = item_at(take());
         if (item < nitems) s_next = slot_of(item);
     }
 }
@@ -856,7 +852,7 @@ template <int D, int FL, int ENG>
 static hipError_t launch_fused_t(const StepParams& p, Workspace& ws, const StepIO& io, const float* wfused,
                                  hipStream_t stream, Profiler* prof) {
     using Sh = FuseShape<D, FL>;
-    const size_t lds = (fused_weight_floats(p.FP, D) + (size_t)kFuseWaves * Sh::WAVE_FLOATS + 4) * 4;  // + counter
+    const size_t lds = (fused_weight_floats(p.FP, D) + (size_t)kFuseWaves * Sh::WAVE_FLOATS) * 4;
     if (lds > kFuseLdsBytes) return hipErrorInvalidValue;
     static bool attr = false;
     if (!attr) {
@@ -873,7 +869,7 @@ static hipError_t launch_fused_t(const StepParams& p, Workspace& ws, const StepI
     return launch_timed(prof, NPA_KERNEL_UPDATE, k_update_fused<D, FL, ENG>, dim3(blocks), dim3(64 * kFuseWaves),
                         (uint32_t)lds, stream, p, ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(),
                         ws.svol.as<float4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
-                        ws.act_rows.as<uint32_t>(), (const uint32_t*)(wl + 1), ws.nb_base.as<uint32_t>(),
+                        ws.act_rows.as<uint32_t>(), wl, ws.nb_base.as<uint32_t>(),
                         ws.nb_mask.as<uint64_t>(), ws.nb_count.as<uint32_t>(), wfused, io);
 }
 
