@@ -29,18 +29,27 @@ __device__ __forceinline__ bool cell_range(const StepParams& P, const uint32_t* 
         end = bo[bin + 1];
         return beg < end;
     }
+    // the bin's directory size, its first entry and its end: all that a bin of one cell (most
+    // bins) needs
+    const int4* e = P.dir_e + bin * kDirGroups;
     const uint32_t nd = P.dir_n[bin];
+    const int4 e0 = e[0];
+    const uint32_t last = bo[bin + 1];
     if (nd == 0) return false;
     if (nd > kDirGroups) {
         beg = bo[bin];
-        end = bo[bin + 1];
+        end = last;
         filter = true;
         return true;
     }
-    // the bin's directory entries are loaded four at a time (each half's loads issued together);
-    // a run ends where the next entry's run starts, the last one at the bin's end
-    const int4* e = P.dir_e + bin * kDirGroups;
-    const uint32_t last = bo[bin + 1];
+    if (nd == 1) {
+        if ((int64_t)e0.x != n0 || (int64_t)e0.y != n1 || (int64_t)e0.z != n2) return false;
+        beg = (uint32_t)e0.w;
+        end = last;
+        return true;
+    }
+    // several cells: the directory entries are loaded four at a time (each half's loads issued
+    // together); a run ends where the next entry's run starts, the last one at the bin's end
     bool found = false;
     int hit_k = -1;
 #pragma unroll
