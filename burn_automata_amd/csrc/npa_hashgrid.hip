@@ -424,6 +424,50 @@ __global__ __launch_bounds__(256) void k_table_offsets_scan(uint32_t* __restrict
 }
 
 // Exclusive scan of one value per thread over a 1024-thread block.
+__device__ __forceinline__ uint32_t block_scan_1024(uint32_t v, uint32_t* lds, uint32_t* total);
+
+// The same two scans for many small systems (batched rollouts): one 1024-thread block per system,
+// thread t owning keys [t PER, t PER + PER) (C <= 1024 PER) over TL tiles (tiles_per_sys <= TL). All
+// of a thread's table entries are loaded at once; each key's column becomes its exclusive per-tile
+// bases, and one block scan of the threads' totals gives bin_offsets[b][k] = b * n + the key's
+// exclusive prefix. No block waits for another (the one-pass kernel's look-back polls the other
+// blocks' published totals, which costs more than it saves when thousands of blocks poll at once).
+template <int PER, int TL>
+__global__ __launch_bounds__(1024) void k_table_offsets_sys(uint32_t* __restrict__ table,
+                                                          uint32_t* __restrict__ bin_offsets, uint32_t C,
+                                                          uint32_t tiles_per_sys, uint32_t n, uint32_t batch) {
+    __shared__ uint32_t lds[16];
+    const uint32_t b = blockIdx.x;
+    const uint32_t k0 = threadIdx.x * PER;
+    uint32_t* tab = table + (uint64_t)b * tiles_per_sys * C;
+    uint32_t v[PER][TL];
+#pragma unroll
+    for (int q = 0; q < PER; ++q)
+#pragma unroll
+        for (int t = 0; t < TL; ++t)
+            v[q][t] = k0 + q < C && (uint32_t)t < tiles_per_sys ? tab[(uint64_t)t * C + k0 + q] : 0u;
+    uint32_t tot[PER], sum = 0;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        uint32_t run = 0;
+#pragma unroll
+        for (int t = 0; t < TL; ++t) {
+            if (k0 + q < C && (uint32_t)t < tiles_per_sys) tab[(uint64_t)t * C + k0 + q] = run;
+            run += v[q][t];
+        }
+        tot[q] = run;
+        sum += run;
+    }
+    uint32_t all;
+    uint32_t pre = block_scan_1024(sum, lds, &all);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        if (k0 + q < C) bin_offsets[(uint64_t)b * C + k0 + q] = b * n + pre;
+        pre += tot[q];
+    }
+    if (b == batch - 1 && threadIdx.x == 0) bin_offsets[(uint64_t)batch * C] = b * n + all;
+}
+
 __device__ __forceinline__ uint32_t block_scan_1024(uint32_t v, uint32_t* lds, uint32_t* total) {
     const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const uint32_t nw = blockDim.x >> 6;
@@ -1219,9 +1263,15 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                                ws.wl_count.as<uint32_t>(), ws.scan_status.as<unsigned long long>(), batch * kblocks,
                                stream, prof);
     if (e != hipSuccess) return e;
-    e = launch_timed(prof, NPA_KERNEL_TABLE_SCAN, k_table_offsets_scan, dim3(kblocks, batch), dim3(256), 0, stream,
-                     ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), ws.scan_status.as<unsigned long long>(),
-                     plan.cells, plan.tiles_per_sys, n, batch);
+    if (batch >= 8 && plan.cells <= 4096 && plan.tiles_per_sys <= 4) {  // many small systems: a block each
+        auto k = plan.cells <= 1024 ? k_table_offsets_sys<1, 4> : k_table_offsets_sys<4, 4>;
+        e = launch_timed(prof, NPA_KERNEL_TABLE_SCAN, k, dim3(batch), dim3(1024), 0, stream, ws.table.as<uint32_t>(),
+                         ws.bin_offsets.as<uint32_t>(), plan.cells, plan.tiles_per_sys, n, batch);
+    } else {
+        e = launch_timed(prof, NPA_KERNEL_TABLE_SCAN, k_table_offsets_scan, dim3(kblocks, batch), dim3(256), 0, stream,
+                         ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(),
+                         ws.scan_status.as<unsigned long long>(), plan.cells, plan.tiles_per_sys, n, batch);
+    }
     if (e != hipSuccess) return e;
     const uint32_t blocks = (uint32_t)((total + 255) / 256);
     const SplitTargets tg = targets ? *targets : SplitTargets{};
