@@ -162,6 +162,7 @@ npa::StepParams make_params(const npa_grid_cfg& cfg, const npa_perception_opts& 
                             uint32_t S) {
     npa::StepParams p{};
     p.g = npa::make_grid_params(cfg);
+    p.g.spatial = cfg.mode == NPA_MODE_PARTICLE ? 1 : 0;  // the step's own sort: coordinate bins
     p.N = N;
     p.B = B;
     p.S = S;
@@ -1485,6 +1486,7 @@ npa_status npa_state_pair_counts(npa_state* s, uint64_t* candidates, uint64_t* p
     if (set_device(ctx)) return NPA_ERR_DEVICE;
     const uint32_t S = s->model.state_dims;
     npa::StepParams p = make_params(s->grid, opts_for_model(s->model), s->B, s->N, S);
+    p.g.spatial = 0;  // the reference's bins: candidates count every particle of a neighbour cell's bin
     p.update_prob = s->update_prob;
     p.base_seed = base_seed(s->seed);
     p.step_index = (uint32_t)s->step_index;

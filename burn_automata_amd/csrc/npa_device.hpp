@@ -28,6 +28,13 @@ struct GridParams {
     float half[3];   // extent * 0.5
     float k6;        // poly6 normalisation
     float k5;        // spiky-gradient normalisation
+    // Particle mode: 0 - bins by the reference's mixing hash (particle_cell_hash, hashgrid.rs:147-153),
+    // as npa_build_hashgrid exposes them; 1 - bins by the cell coordinates modulo the grid size, for
+    // the step's own sort. Every neighbour visit looks a cell up by its coordinates and keeps only
+    // that cell's particles, so which cells share a bin changes no result; with coordinate bins a
+    // cloud narrower than the grid puts one cell in each bin, and consecutive bins are neighbouring
+    // cells.
+    int spatial;
 };
 
 // Rust `f as isize` of a floored f32: saturating, NaN -> 0.
@@ -56,6 +63,14 @@ __device__ __forceinline__ uint32_t mix_coord(int64_t value, uint32_t salt) {
 
 // particle_cell_hash  hashgrid.rs:147-153
 __device__ __forceinline__ uint32_t particle_hash(int64_t c0, int64_t c1, int64_t c2, const GridParams& g) {
+    if (g.spatial) {  // coordinate bins (see GridParams::spatial)
+        auto wrap = [](int64_t c, uint32_t m) -> uint32_t {  // Euclidean remainder; a mask for 2^k
+            return (m & (m - 1)) == 0 ? (uint32_t)c & (m - 1) : (uint32_t)rem_euclid_i64(c, m);
+        };
+        uint32_t h = wrap(c0, g.size[0]) + g.size[0] * wrap(c1, g.size[1]);
+        if (g.dim == 3) h += g.size[0] * g.size[1] * wrap(c2, g.size[2]);
+        return h;
+    }
     uint32_t h = mix_coord(c0, 0x9e3779b9u) ^ mix_coord(c1, 0x85ebca6bu);
     if (g.dim == 3) h ^= mix_coord(c2, 0xc2b2ae35u);
     return h % g.cells;
