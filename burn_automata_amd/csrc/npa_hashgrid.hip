@@ -191,7 +191,10 @@ bool make_plan(const npa_grid_cfg& cfg, uint32_t batch, uint32_t n, HashgridPlan
     HashgridPlan p;
     p.cells = (uint32_t)cells;
     p.key_bits = cells <= 1 ? 0 : 32 - __builtin_clz((uint32_t)cells - 1);
-    p.waves = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(4, 32768 / cells));
+    // ranking waves per tile: one LDS counter row (2 bytes per cell) each, up to 128 KiB of rows;
+    // a 1024-thread block (4,096 or more cells) ranks with up to all 16 of its waves, one round each
+    // where the tile budget allows, instead of four waves walking four rounds in turn
+    p.waves = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(cells >= 4096 ? 16 : 4, 65536 / cells));
     p.lds_bytes = p.waves * p.cells * 2;
     // table entries allowed: 4 per particle, or 64 rows of cells when the cells outnumber the
     // particles (sparse grids: more, smaller tiles keep the O(cells) work per tile parallel)
@@ -247,7 +250,8 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
         n = dc < n ? dc : n;
     }
     const uint32_t nwords = waves * C;
-    for (uint32_t k = threadIdx.x; k < nwords; k += blockDim.x) cnt[k] = 0;
+    for (uint32_t k = threadIdx.x; k < nwords / 8; k += blockDim.x) reinterpret_cast<uint4*>(cnt)[k] = make_uint4(0, 0, 0, 0);
+    for (uint32_t k = nwords / 8 * 8 + threadIdx.x; k < nwords; k += blockDim.x) cnt[k] = 0;
     if (wl_count && tile == 0)  // work-list counters and item queues
         for (uint32_t k = threadIdx.x; k < kWlWords; k += blockDim.x) wl_count[k] = 0;
     for (uint32_t k = tile * blockDim.x + threadIdx.x; k < nstatus; k += gridDim.x * blockDim.x)
@@ -266,22 +270,30 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
     for (int r = 0; r < R; ++r) key_r[r] = rank_r[r] = 0;
     bool ovf = false;
     if (ranker) {
+    // every round's key first (all of the wave's loads in flight together), then the rounds' ranks
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t li = wave_start + r * 64 + lane;
+        const uint64_t at = sys_start + (li < n ? li : 0u);  // (a tile has a particle whenever n > 0)
+        if (n == 0) {
+            key_r[r] = 0;
+        } else if (keys_in) {
+            key_r[r] = keys_in[at];
+        } else {
+            const float4 p4 = pos[at];
+            float p[4] = {p4.x, p4.y, p4.z, p4.w};
+            int64_t c[3];
+            bool o = false;
+            cell_coords(p, g, c, &o);
+            key_r[r] = cell_of_coords(c, g);
+            ovf = ovf || (o && li < n);
+        }
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t li = wave_start + r * 64 + lane;
         const bool active = li < n;
-        uint32_t key = 0;
-        if (active) {
-            if (keys_in) {
-                key = keys_in[sys_start + li];
-            } else {
-                float4 p4 = pos[sys_start + li];
-                float p[4] = {p4.x, p4.y, p4.z, p4.w};
-                int64_t c[3];
-                cell_coords(p, g, c, &ovf);
-                key = cell_of_coords(c, g);
-            }
-        }
+        const uint32_t key = active ? key_r[r] : 0u;
         uint64_t peers = __ballot(active);
         for (uint32_t bit = 0; bit < key_bits; ++bit) {
             const uint32_t v = (key >> bit) & 1u;

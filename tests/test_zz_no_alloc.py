@@ -62,8 +62,9 @@ def test_noalloc_step_equals_npa_step_on_calls_in_a_row(ctx):
 
 def test_noalloc_refuses_oversized_systems_and_host_io(ctx):
     L = lib()
-    # 64 systems of 1,024 particles on per-system 64x64 grids need about 88 MiB of workspace
-    w = syn.workload("c5", particles=1024)
+    # C5's 64 systems of 4,096 particles on per-system 64x64 grids need more than 100 MiB of
+    # workspace (about 450 bytes per particle), well over the 64 MiB array
+    w = syn.workload("c5")
     m, g, b, n = w["model"], w["grid"], w["batch"], w["n"]
     wc = NpaWeights.from_arrays(w["weights"]).to_c()
     pos = device_f32(w["positions"]).reshape(-1, 4)
