@@ -246,14 +246,28 @@ __device__ __forceinline__ bool splat_tiles(const SplatParams& P, int64_t bx, in
     return true;
 }
 
+// Value of lane J of each group of four consecutive lanes (DPP quad_perm; every lane reads a valid
+// lane, so bound_ctrl never applies and the compiler folds the move into the consuming add).
+template <int J>
+__device__ __forceinline__ float quad_bcast(float v) {
+    constexpr int c = J | (J << 2) | (J << 4) | (J << 6);
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), c, 0xf, 0xf, true));
+}
+
+// Four lanes per particle: every lane derives the particle's pixel-space centre; lane q computes the
+// window weights of offsets q, q + 4, ... (row-major over (oy, ox), the reference's order), and
+// every lane adds each round's four weights in offset order, so the sum is the serial sum of the
+// reference (an out-of-image offset adds +0.0, which leaves the non-negative sum unchanged).
 __global__ __launch_bounds__(256) void k_splat_prep(SplatParams P, const float4* __restrict__ pos,
                                                     const float* __restrict__ colors,
                                                     const float* __restrict__ states, uint32_t count,
                                                     SplatParticle* __restrict__ out,
                                                     uint32_t* __restrict__ ntiles) {
-    const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x;
-    if (n >= count) return;
-    const float4 p = pos[n];
+    const uint32_t gt = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t q = gt & 3u;
+    const uint32_t n = gt >> 2;
+    const bool valid = n < count;
+    const float4 p = pos[valid ? n : 0u];
     const float fsz = (float)P.size;
     const float px = (p.x - P.lo) / (P.hi - P.lo) * (fsz - 1.0f);
     float py = (p.y - P.lo) / (P.hi - P.lo) * (fsz - 1.0f);
@@ -261,17 +275,35 @@ __global__ __launch_bounds__(256) void k_splat_prep(SplatParams P, const float4*
     const int64_t bx = f32_to_isize(floorf(px)), by = f32_to_isize(floorf(py));
     const float fx = px - (float)bx, fy = py - (float)by;
     int tx0, tx1, ty0, ty1;
-    const bool any = splat_tiles(P, bx, by, &tx0, &tx1, &ty0, &ty1);
+    const bool any = valid && splat_tiles(P, bx, by, &tx0, &tx1, &ty0, &ty1);
     float weight_sum = 0.0f;
-    if (any) {
-        for (int oy = -P.radius; oy <= P.radius; ++oy)
-            for (int ox = -P.radius; ox <= P.radius; ++ox) {
-                const int64_t x = bx + ox, y = by + oy;
-                if (x < 0 || y < 0 || x >= P.size || y >= P.size) continue;
+    if (__ballot(any)) {
+        const int side = 2 * P.radius + 1;
+        const uint32_t terms = (uint32_t)side * (uint32_t)side;
+        int oy = -P.radius, ox = -P.radius + (int)q;  // offset q of the row-major window
+        while (ox > P.radius) {
+            ox -= side;
+            ++oy;
+        }
+        for (uint32_t k0 = 0; k0 < terms; k0 += 4) {
+            float wk = 0.0f;
+            const int64_t x = bx + ox, y = by + oy;
+            if (any && k0 + q < terms && x >= 0 && y >= 0 && x < P.size && y < P.size) {
                 const float dx = (float)ox - fx, dy = (float)oy - fy;
-                weight_sum += expf(-(dx * dx + dy * dy) / P.two_sig2);
+                wk = expf(-(dx * dx + dy * dy) / P.two_sig2);
             }
+            weight_sum += quad_bcast<0>(wk);
+            weight_sum += quad_bcast<1>(wk);
+            weight_sum += quad_bcast<2>(wk);
+            weight_sum += quad_bcast<3>(wk);
+            ox += 4;  // the offset four places on
+            while (ox > P.radius) {
+                ox -= side;
+                ++oy;
+            }
+        }
     }
+    if (!valid || q != 0) return;
     SplatParticle sp;
     sp.fx = fx;
     sp.fy = fy;
@@ -529,8 +561,8 @@ hipError_t launch_splat_2d(const float4* pos, const float* colors, const float* 
     uint32_t* ntiles = ws.item_start.as<uint32_t>() + (count ? count : 1);
     uint32_t* start = ws.item_start.as<uint32_t>();
     if (count) {
-        hipLaunchKernelGGL(k_splat_prep, dim3((count + 255) / 256), dim3(256), 0, stream, P, pos, colors, states,
-                           count, ws.params.as<SplatParticle>(), ntiles);
+        hipLaunchKernelGGL(k_splat_prep, dim3((uint32_t)(((uint64_t)count * 4 + 255) / 256)), dim3(256), 0, stream, P,
+                           pos, colors, states, count, ws.params.as<SplatParticle>(), ntiles);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     {  // start = exclusive prefix of ntiles, total item count into ws.count
