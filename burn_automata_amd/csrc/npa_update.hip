@@ -64,16 +64,21 @@ struct FuseShape {
     static constexpr int NX = COMMON ? NMOM : NMOM + D;   // per-target sums over entries
     static constexpr int CAP = D == 2 ? (COMMON ? 256 : 160) : (COMMON ? 128 : 64);  // list entries
     static constexpr int OPAD = (D + 16 + 3) / 4 * 4;      // padded update outputs
-    // Per wave, one block per target group g: lists [CAP] u32, entry records [16][SREC], the sums'
-    // terms [NX][XSTR]. Every per-group block (and each term row) is padded by 4 floats so that the
-    // four groups' broadcast reads of the same offset fall in different LDS banks. After the walk
-    // the same region holds the feature rows [4][FP + 4] and hidden activations [4][132].
+    // Per wave, one block per target group g, one after the other: its list [CAP] u32, its entry
+    // records [16][SREC] and its sums' terms [NX][XSTR] (so one address per lane reaches all three
+    // through immediate offsets). Each part and each term row is padded by 4 floats, and the
+    // blocks' stride keeps the four groups' broadcast reads of one offset in different LDS banks.
+    // After the walk the same region holds the feature rows [4][FP + 4] and hidden activations
+    // [4][132].
     static constexpr int LSTR = CAP + 4;
     static constexpr int SSTR = 16 * SREC + 4;
     static constexpr int XSTR = 20;
     static constexpr int XGSTR = NX * XSTR + 4;
     static constexpr int HSTR = 128 + 4;
-    static constexpr int WAVE_FLOATS = 4 * LSTR + 4 * SSTR + 4 * XGSTR;
+    // a group's block: its three parts, plus 4 floats when their sum is a multiple of 16 floats
+    // (then two groups' same offsets would share banks)
+    static constexpr int GSTR = LSTR + SSTR + XGSTR + ((LSTR + SSTR + XGSTR) % 16 == 0 ? 4 : 0);
+    static constexpr int WAVE_FLOATS = 4 * GSTR;
     static_assert(4 * (88 + 4 + HSTR) <= WAVE_FLOATS, "feature and hidden rows fit the wave's region");
 };
 
@@ -248,9 +253,11 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t g = lane >> 4, c = lane & 15;
     float* wl = lds + wfloats + (size_t)wave * Sh::WAVE_FLOATS;
-    uint32_t* mylist = reinterpret_cast<uint32_t*>(wl) + g * Sh::LSTR;
-    float* stage = wl + 4 * Sh::LSTR + g * Sh::SSTR;       // this group's entry records
-    float* ext = wl + 4 * Sh::LSTR + 4 * Sh::SSTR + g * Sh::XGSTR;  // this group's sums' terms
+    // this group's block: its list, its entry records, its sums' terms (one base per lane)
+    float* gblk = wl + g * Sh::GSTR;
+    uint32_t* mylist = reinterpret_cast<uint32_t*>(gblk);
+    float* stage = gblk + Sh::LSTR;
+    float* ext = gblk + Sh::LSTR + Sh::SSTR;
     float* hg = wl + 4 * (FP + 4) + g * Sh::HSTR;           // hidden activations (after the walk)
 
     const bool want_sg = FL >= 0 ? (FL & 1) != 0 : P.state_grad != 0;
