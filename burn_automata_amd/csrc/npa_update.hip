@@ -154,8 +154,32 @@ __device__ __forceinline__ void wave_sync() {
 }
 
 // Value of `v` in lane (lane & ~15) + k: the same target's lane k.
+// (DPP row_newbcast:k: no address register and no LDS round trip; k is a constant at every call
+// once the loops are unrolled, and the switch folds to one move)
+template <int K>
+__device__ __forceinline__ float row_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + K, 0xf, 0xf, false));
+}
 __device__ __forceinline__ float group_lane(float v, uint32_t lane, uint32_t k) {
-    return __shfl(v, (int)((lane & 48u) | k));
+    (void)lane;
+    switch (k) {
+        case 0: return row_bcast<0>(v);
+        case 1: return row_bcast<1>(v);
+        case 2: return row_bcast<2>(v);
+        case 3: return row_bcast<3>(v);
+        case 4: return row_bcast<4>(v);
+        case 5: return row_bcast<5>(v);
+        case 6: return row_bcast<6>(v);
+        case 7: return row_bcast<7>(v);
+        case 8: return row_bcast<8>(v);
+        case 9: return row_bcast<9>(v);
+        case 10: return row_bcast<10>(v);
+        case 11: return row_bcast<11>(v);
+        case 12: return row_bcast<12>(v);
+        case 13: return row_bcast<13>(v);
+        case 14: return row_bcast<14>(v);
+        default: return row_bcast<15>(v);
+    }
 }
 
 // Row-wise (16-lane) scans: row_shr:n reads lane i - n of the same row, 0 for the first n lanes.
