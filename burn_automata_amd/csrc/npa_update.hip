@@ -864,7 +864,9 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
 #pragma unroll
             for (int a = 0; a < D; ++a) dx[a] *= mg;
         }
-        const float mk = io.mask ? io.mask[i] : hash_mask(li, b, P.N, P.update_prob, P.step_index, P.base_seed);
+        // every row is a target of the step's update mask: a mask array's value, or the hash mask's
+        // 1.0 (the particles it zeroes get no row; the hashgrid build wrote them out unchanged)
+        const float mk = io.mask ? io.mask[i] : 1.0f;
         if (active && c == 0) {
             float pn[4] = {pos4.x, pos4.y, pos4.z, pos4.w};
             constexpr int MEM = D == 3 ? 4 : 2;
@@ -880,7 +882,11 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
         if (P.gates3d) dsc *= sgate;
         float next = si + P.dt * dsc * mk;
         if (clamped_channel(D, P.S, c)) next = clampf_(next, -8.0f, 24.0f);
-        if (active && c < P.S) io.out_states[(uint64_t)i * P.S + c] = next;
+        // (c passes through an empty asm so that out_states + c is formed here, per item, rather
+        // than hoisted into a 64-bit register pair held across the whole loop)
+        uint32_t cs = c;
+        asm volatile("" : "+v"(cs));
+        if (active && c < P.S) io.out_states[(uint64_t)i * P.S + cs] = next;
         item = item_at(take());
         if (item < nitems) s_next = slot_of(item);
     }
