@@ -148,22 +148,8 @@ __global__ __launch_bounds__(256) void k_density_q(StepParams P, const float4* _
     const uint32_t t = lane >> 2, q = lane & 3;
     float4* stg = staged[kStage ? threadIdx.x >> 6 : 0];  // this wave's chunk, record k at [k]
     const uint32_t items = *wl_count;
-    // Blocks reach the eight XCDs in turn (block b on XCD b mod 8): with a grid of whole rounds of
-    // eight, the blocks of XCD x walk the x-th eighth of the items (a band of neighbouring bins),
-    // so each XCD's L2 holds the records of its own band and its halo rather than all of them.
-    const uint32_t wpb = blockDim.x >> 6;
-    uint32_t it, it_end, it_step;
-    if (gridDim.x % 8 == 0) {
-        const uint32_t x = blockIdx.x % 8, per = (items + 7) / 8;
-        it = x * per + blockIdx.x / 8 * wpb + (threadIdx.x >> 6);
-        it_end = min(items, x * per + per);
-        it_step = gridDim.x / 8 * wpb;
-    } else {
-        it = blockIdx.x * wpb + (threadIdx.x >> 6);
-        it_end = items;
-        it_step = gridDim.x * wpb;
-    }
-    for (; it < it_end; it += it_step) {
+    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
+    for (uint32_t it = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); it < items; it += nwaves) {
         const uint2 item = wl[it];
         const bool active = t < item.y;
         const uint32_t s = item.x + (active ? t : 0u);
