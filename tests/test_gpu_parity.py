@@ -202,6 +202,13 @@ def _model_case(name):
         n = 1024
         pos = np.concatenate([syn.uniform_disk(n, 20 + k) for k in range(4)])
         return m, g, pos, syn.normal_states(4 * n, 16, 20), syn.seeded_weights(m, 20), 4, n
+    if name == "texture_periodic_common":  # the rollout's usual options on a periodic grid: the
+        # fused kernel's periodic variant (wrapped deltas and positions compiled in)
+        m = NpaConfig.texture_2d().replace(density_grad=False)
+        g = HashGridConfig.texture_2d()
+        n = 1500
+        return (m, g, syn.uniform_disk(n, 14, 1.0), syn.normal_states(n, 16, 14),
+                syn.seeded_weights(m, 14), 1, n)
     if name == "no_sgrad_2d":  # density gradient and positions without the state gradient, H < 128
         m = NpaConfig(eps0=0.05, hidden_dims=96, state_grad=False, density_grad=True,
                       position_features=True)
@@ -232,7 +239,8 @@ def _model_case(name):
 
 
 @pytest.mark.parametrize("name", ["c1", "c1_dgrad", "growing_3d", "torus_gates_3d",
-                                  "texture_periodic", "batch4", "no_sgrad_2d", "no_sgrad_3d",
+                                  "texture_periodic", "texture_periodic_common", "batch4",
+                                  "no_sgrad_2d", "no_sgrad_3d",
                                   "torus16_gates_3d", "collide_reorder", "collide_keep",
                                   "collide_sparse", "collide_3d"])
 def test_step_parity(ctx, name):
@@ -346,7 +354,7 @@ def test_update_probability_zero_keeps_state(ctx):
     np.testing.assert_array_equal(to_np(gs), st)
 
 
-@pytest.mark.parametrize("name", ["texture_periodic", "torus_gates_3d"])
+@pytest.mark.parametrize("name", ["texture_periodic", "texture_periodic_common", "torus_gates_3d"])
 def test_masked_particles_follow_the_cpu_euler_step(ctx, name):
     """Particles with update mask 0 skip the second pass and the MLP on the device; the CPU
     euler_step (step.rs:4-55) still wraps their positions on a periodic grid and clamps their 3D
@@ -356,7 +364,7 @@ def test_masked_particles_follow_the_cpu_euler_step(ctx, name):
         st = st.copy()
         st[::3, 3] = 30.0
         st[1::5, 8] = -20.0
-    if name == "texture_periodic":  # particles beyond the periodic extent and at its edges
+    if name.startswith("texture_periodic"):  # particles beyond the periodic extent and at its edges
         pos = pos.copy()
         half = 0.5 * g.grid_size[0] * g.eps
         pos[::11, 0] = np.float32(half * 1.37)
