@@ -340,7 +340,9 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
 
         const uint32_t b = s / P.N;
         const uint32_t i = b * P.N + li;
-        const float4 pos4 = io.pos[i];
+        // (in 3D the position is loaded after the walk: held across it, it would spill)
+        float4 pos4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if constexpr (D == 2) pos4 = io.pos[i];
         float blur = 0.0f, gr[3] = {0.0f, 0.0f, 0.0f}, xacc = 0.0f;
         uint32_t cnt = 0;  // entries in this target's list
 
@@ -671,6 +673,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
         float rest[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) rest[k] = 0.0f;
+        if constexpr (D == 3) pos4 = io.pos[i];
         {
             const float pp[3] = {pos4.x, pos4.y, pos4.z};
             int nrest = 0;
