@@ -765,23 +765,36 @@ def main(argv=None) -> int:
                                 "gbs": by / (ms * 1e-3) / 1e9, "flops_per_launch": fl,
                                 "bytes_per_launch": by}
         k = per_kernel[dominant]
-        on_mfma = args.mlp_engine == "mfma" and dominant == "mlp"
+        # the matrix-core engine runs both MLP layers on MFMA, in the separate MLP kernel and in the
+        # fused update kernel alike; the bit-exact engine takes only layer 1's products from MFMA
+        # (one rounding each, as v_mul_f32) and adds everything on the VALU in the reference's order
+        on_mfma = args.mlp_engine == "mfma" and dominant in ("mlp", "update")
+        if on_mfma:
+            engine_note = ("fp32 matrix cores for both MLP layers (v_mfma_f32_4x4x1f32), neighbour walk "
+                           "and sums on the VALU; peak = the published MI355X fp32 peak")
+        elif dominant == "update":
+            engine_note = ("layer-1 products on the fp32 matrix cores (v_mfma_f32_4x4x1f32 with a -0.0 "
+                           "accumulator: each product rounded once, as v_mul_f32), every sum and the "
+                           "neighbour walk on the VALU, unfused, in the reference's order (bit-exact "
+                           "path); peak = the published MI355X fp32 peak")
+        else:
+            engine_note = ("fp32 VALU, unfused mul/add in the reference's order (bit-exact path); "
+                           "peak = the published MI355X fp32 vector peak")
         line["roofline"] = {
             "bound": "mfma" if on_mfma else "valu", "achieved": k["tflops"], "peak": PEAK_FP32_TFLOPS,
             "unit": "TFLOP/s", "frac": k["tflops"] / PEAK_FP32_TFLOPS,
             "attainable_peak": VALU_CEILING_TOPS,
             "frac_attainable": k["tflops"] / VALU_CEILING_TOPS,
-            "attainable_note": ("unfused, unpacked fp32 VALU issue (256 CUs x 64 lanes x 2.4 GHz): "
-                                "the ceiling of a path that rounds every product and sum as the "
-                                "reference does"),
+            "attainable_note": ("frac_attainable is against unfused, unpacked fp32 VALU issue (256 CUs "
+                                "x 64 lanes x 2.4 GHz = 39.3 T op/s): the ceiling of a path that rounds "
+                                "every sum as the reference does on the vector ALUs, which is where "
+                                "this kernel's sums run whichever engine supplies the products"),
             # the committed counter summary covers the C2 workload only
             "traffic": recorded_traffic(dominant) if args.workload == "c2" and args.particles is None else None,
             "traffic_source": ("profiles/c2_hbm_traffic.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
                                "copy-kernel scaled)" if args.workload == "c2" and args.particles is None
                                else "not measured for this workload"), "kernel": dominant,
-            "engine": ("fp32 matrix cores (update MLP)" if on_mfma else
-                       "fp32 VALU, unfused mul/add in the reference's order (bit-exact path); "
-                       "peak = the published MI355X fp32 vector peak"),
+            "engine": engine_note,
             "mean_launch_ms": k["mean_launch_ms"], "flops_per_launch": k["flops_per_launch"],
             "timing": (f"HIP events around the launches of this kernel on every "
                        f"{min(SAMPLE_EVERY, max(1, args.steps))}th step of the timed region ({live_n} "

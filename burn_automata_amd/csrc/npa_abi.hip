@@ -40,6 +40,9 @@ struct npa_context {
     void* scratch = nullptr;
     hipError_t scratch_err = hipSuccess;
     npa::Workspace scratch_flags;
+    // set by this context's first npa_step_noalloc call: only then does npa_context_synchronize read
+    // the scratch array's flag words (which every context on the GPU shares)
+    std::atomic<bool> used_noalloc{false};
     // the caller's handle plus one per live npa_state: a state keeps its context until it is destroyed
     std::atomic<int> refs{1};
     ~npa_context() {
@@ -412,6 +415,9 @@ npa_status npa_context_synchronize(npa_context* ctx) {
     NPA_HIP(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     npa_status st = check_flags(ctx, ctx->ws);
     if (st) return st;
+    // the no-allocation step's overflow word is per GPU, not per context: a context that never called
+    // npa_step_noalloc neither reads nor clears it
+    if (!ctx->used_noalloc.load(std::memory_order_relaxed)) return NPA_OK;
     return check_flags(ctx, ctx->scratch_flags);
 }
 
@@ -798,6 +804,7 @@ npa_status npa_step_noalloc(npa_context* ctx, const float* positions, const floa
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: output states must be 16-byte aligned");
     if (set_device(ctx)) return NPA_ERR_DEVICE;
     if (!total) return NPA_OK;
+    ctx->used_noalloc.store(true, std::memory_order_relaxed);
     npa::StepIO sio;
     sio.pos = (const float4*)positions;
     sio.states = states;
@@ -1441,7 +1448,9 @@ npa_status npa_state_raster_gaussians_3d(npa_state* s, const npa_gaussian_decode
     if (st) return st;
     if (!image) return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: null image");
     npa_raster_camera cam = *camera;
-    // the export carries SH coefficients (degree-3 layout, DC only); the decode carries colours
+    // the export carries SH coefficients (degree-3 layout, DC only); the decode carries colours in
+    // the first of its K coefficient triples per Gaussian (K = (sh_degree + 1)^2 in oriented mode),
+    // so the raster reads them at that stride
     cam.sh_degree = cfg ? 0u : 3u;
     cam.color_mode = cfg ? NPA_RASTER_COLOR_RGB : NPA_RASTER_COLOR_SH;
     const uint32_t K = cfg ? (cfg->mode == NPA_DECODE_SH0_ORIENTED ? (cfg->sh_degree + 1) * (cfg->sh_degree + 1) : 1u)
@@ -1473,7 +1482,7 @@ npa_status npa_state_raster_gaussians_3d(npa_state* s, const npa_gaussian_decode
                                                  ctx->stream),
                 "gaussian export");
     NPA_HIP(ctx, npa::launch_raster_gaussians((const float4*)dpv, dsh, (const float4*)drot, (const float4*)dso,
-                                              (uint32_t)total, cam, img, ctx->splat_ws, ctx->stream, &ctx->prof),
+                                              (uint32_t)total, cam, img, ctx->splat_ws, ctx->stream, &ctx->prof, K),
             "raster");
     NPA_HIP(ctx, io.finish(), "host io");
     return NPA_OK;

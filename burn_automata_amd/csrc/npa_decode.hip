@@ -1065,6 +1065,7 @@ struct RasterParams {
     float fx, fy, cx, cy, limx, limy, near_plane, far_plane;
     float campos[3];
     uint32_t width, height, tiles_x, tiles_y, count, K, sh_degree, color_mode;
+    uint32_t stride;  // coefficient triples per Gaussian in the input (>= K)
 };
 
 struct alignas(16) RasterSplat {  // 48 bytes
@@ -1160,7 +1161,7 @@ __global__ __launch_bounds__(256) void k_raster_prep(RasterParams P, const float
     o.rx = x0 | (x1 << 16);
     o.ry = y0 | (y1 << 16);
     o.pad = 0;
-    const float* coef = sh + (uint64_t)i * P.K * 3;
+    const float* coef = sh + (uint64_t)i * P.stride * 3;
     if (P.color_mode == NPA_RASTER_COLOR_RGB) {
         o.r = coef[0];
         o.g = coef[1];
@@ -1329,9 +1330,10 @@ __global__ __launch_bounds__(256) void k_raster_tiles(RasterParams P, const Rast
 
 hipError_t launch_raster_gaussians(const float4* pv, const float* sh, const float4* rot, const float4* so,
                                    uint32_t count, const npa_raster_camera& cam, float* image, SplatWorkspace& ws,
-                                   hipStream_t stream, Profiler* prof) {
+                                   hipStream_t stream, Profiler* prof, uint32_t coef_stride) {
+    const uint32_t K = (cam.sh_degree + 1) * (cam.sh_degree + 1);
     if (cam.width == 0 || cam.height == 0 || cam.width > kRasterMaxAxis || cam.height > kRasterMaxAxis ||
-        cam.sh_degree > 3 || count >= (1u << 31))
+        cam.sh_degree > 3 || count >= (1u << 31) || (coef_stride != 0 && coef_stride < K))
         return hipErrorInvalidValue;
     RasterParams P{};
     for (int k = 0; k < 12; ++k) P.view[k] = cam.view[k];
@@ -1350,7 +1352,8 @@ hipError_t launch_raster_gaussians(const float4* pv, const float* sh, const floa
     P.tiles_x = (cam.width + 15) / 16;
     P.tiles_y = (cam.height + 15) / 16;
     P.count = count;
-    P.K = (cam.sh_degree + 1) * (cam.sh_degree + 1);
+    P.K = K;
+    P.stride = coef_stride ? coef_stride : K;
     P.sh_degree = cam.sh_degree;
     P.color_mode = cam.color_mode;
     const uint32_t ntile_total = P.tiles_x * P.tiles_y;

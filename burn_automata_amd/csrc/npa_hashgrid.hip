@@ -374,11 +374,14 @@ __global__ __launch_bounds__(256) void k_table_scan(uint32_t* __restrict__ table
     totals[(uint64_t)b * C + k] = column_scan(table + (uint64_t)b * tiles_per_sys * C + k, C, tiles_per_sys);
 }
 
-// The column scan and the offsets scan in one pass, for the hashgrid build. Thread k of block x of
-// system b (key k = 256 x + thread): table[t][k] -> exclusive per-tile bases, as k_table_scan, and
-// the key's total. The block publishes the sum of its keys' totals (bit 63 marks it published;
-// k_hash_rank zeroed every status word of this build), adds the totals published by the system's
-// earlier blocks - dispatched before it, so each of them publishes and the wait ends - and writes
+// The column scan and the offsets scan in one pass, for the hashgrid build. A block's position
+// comes from a ticket (status[gridDim.x * gridDim.y], an atomic counter), not from its block index:
+// ticket q is block x = q mod gridDim.x of system b = q / gridDim.x. Thread k of that block (key
+// k = 256 x + thread): table[t][k] -> exclusive per-tile bases, as k_table_scan, and the key's
+// total. The block publishes the sum of its keys' totals (bit 63 marks it published; k_hash_rank
+// zeroed every status word of this build and the ticket counter), adds the totals published by the
+// system's earlier blocks - which took smaller tickets, so they are already running whatever order
+// the hardware dispatches blocks in, each of them publishes and the wait ends - and writes
 // bin_offsets[b][k] = b * n + its keys' exclusive prefix. The last block of the last system also
 // writes the closing entry bin_offsets[batch * C].
 __global__ __launch_bounds__(256) void k_table_offsets_scan(uint32_t* __restrict__ table,
@@ -386,9 +389,14 @@ __global__ __launch_bounds__(256) void k_table_offsets_scan(uint32_t* __restrict
                                                             unsigned long long* __restrict__ status, uint32_t C,
                                                             uint32_t tiles_per_sys, uint32_t n, uint32_t batch) {
     __shared__ uint32_t wsum[4];
-    __shared__ uint32_t s_prefix;
-    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
-    const uint32_t b = blockIdx.y;
+    __shared__ uint32_t s_prefix, s_ticket;
+    if (threadIdx.x == 0)
+        s_ticket = (uint32_t)atomicAdd(status + (uint64_t)gridDim.x * gridDim.y, 1ull);
+    __syncthreads();
+    const uint32_t ticket = s_ticket;
+    const uint32_t bx = ticket % gridDim.x;
+    const uint32_t k = bx * 256 + threadIdx.x;
+    const uint32_t b = ticket / gridDim.x;
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     uint32_t run = 0;
     if (k < C) {
@@ -411,12 +419,12 @@ __global__ __launch_bounds__(256) void k_table_offsets_scan(uint32_t* __restrict
     }
     const uint64_t row = (uint64_t)b * gridDim.x;
     if (threadIdx.x == 0)
-        __hip_atomic_store(status + row + blockIdx.x, (1ull << 63) | btotal, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(status + row + bx, (1ull << 63) | btotal, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     if (w == 0) {  // the system's earlier blocks' totals, 64 at a time
         uint32_t acc = 0;
-        for (uint32_t base = 0; base < blockIdx.x; base += 64) {
+        for (uint32_t base = 0; base < bx; base += 64) {
             const uint32_t j = base + lane;
-            if (j < blockIdx.x) {
+            if (j < bx) {
                 unsigned long long v;
                 do {
                     v = __hip_atomic_load(status + row + j, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
@@ -431,7 +439,7 @@ __global__ __launch_bounds__(256) void k_table_offsets_scan(uint32_t* __restrict
     __syncthreads();
     const uint32_t prefix = s_prefix;
     if (k < C) bin_offsets[(uint64_t)b * C + k] = b * n + prefix + wpre + x - run;
-    if (b == batch - 1 && blockIdx.x == gridDim.x - 1 && threadIdx.x == 0)
+    if (b == batch - 1 && bx == gridDim.x - 1 && threadIdx.x == 0)
         bin_offsets[(uint64_t)batch * C] = b * n + prefix + btotal;
 }
 
@@ -1228,12 +1236,10 @@ static hipError_t launch_rank_r(uint32_t blocks, uint32_t waves, uint32_t lds_by
                                 uint32_t n, uint32_t* keys, uint32_t* ranks, uint32_t* table,
                                 uint32_t* flags, uint32_t* wl_count, unsigned long long* scan_status,
                                 uint32_t nstatus, hipStream_t stream, Profiler* prof) {
-    static uint32_t attr_bytes = 32768;
-    if (lds_bytes > attr_bytes) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_hash_rank<R>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+    if (lds_bytes > 32768) {
+        static LdsLimitFlags limit;
+        const hipError_t e = raise_lds_limit((const void*)k_hash_rank<R>, limit);
         if (e != hipSuccess) return e;
-        attr_bytes = lds_bytes;
     }
     // the first `waves` waves rank; all of them clear the tile's counters and write its histogram
     // row, O(cells) work that wide grids (many cells per tile) spread over 16 waves
@@ -1272,7 +1278,8 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
     hipError_t e = launch_rank(plan.rounds, batch * plan.tiles_per_sys, plan.waves, plan.lds_bytes,
                                plan.tiles_per_sys, plan.key_bits, g, pos, nullptr, nullptr, n, ws.keys.as<uint32_t>(),
                                ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(), ws.flags.as<uint32_t>(),
-                               ws.wl_count.as<uint32_t>(), ws.scan_status.as<unsigned long long>(), batch * kblocks,
+                               ws.wl_count.as<uint32_t>(), ws.scan_status.as<unsigned long long>(),
+                               batch * kblocks + 1,  // the status words and the scan's ticket counter
                                stream, prof);
     if (e != hipSuccess) return e;
     if (batch >= 8 && plan.cells <= 4096 && plan.tiles_per_sys <= 4) {  // many small systems: a block each

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include <string>
 #include <vector>
 
@@ -379,11 +381,13 @@ hipError_t launch_render_views(const float4* pos, const float* colors, const flo
 hipError_t sort_index_by_key(const uint32_t* keys, uint32_t* keys_out, uint32_t* order, uint32_t n,
                              uint32_t end_bit, DevBuf& temp, hipStream_t stream);
 // EWA raster of oriented Gaussians (npa_raster_gaussians_3d): image[height][width][4]. Reads the
-// (tile, Gaussian) item total back to the host (one stream synchronisation).
+// (tile, Gaussian) item total back to the host (one stream synchronisation). coef_stride: the
+// coefficient triples stored per Gaussian (0: (sh_degree + 1)^2, the camera's own count); a
+// decode's colours in RGB mode are read from the first triple of each Gaussian's row.
 hipError_t launch_raster_gaussians(const float4* position_visibility, const float* spherical_harmonic,
                                    const float4* rotation, const float4* scale_opacity, uint32_t count,
                                    const npa_raster_camera& cam, float* image, SplatWorkspace& ws,
-                                   hipStream_t stream, Profiler* prof);
+                                   hipStream_t stream, Profiler* prof, uint32_t coef_stride = 0);
 // state_tail_render_attributes (render_loss/attributes.rs:15-87); derivatives may be null.
 hipError_t launch_render_attributes(const float* states, uint32_t count, uint32_t state_dims,
                                     const npa_render_cfg& cfg, float* colors, float* opacities,
@@ -400,5 +404,24 @@ hipError_t launch_perceive_adjoint(const StepParams& p, Workspace& ws, AdjointWo
                                    float* state_adj, float4* pos_adj, hipStream_t stream);
 
 int device_cu_count();
+
+// A kernel's dynamic-LDS limit, raised once per device to the 160 KiB a gfx950 workgroup can hold
+// (each launch still asks for what it uses). Thread-safe: a device's flag is set only after the
+// attribute call succeeded, and threads that race on a first launch all set the same value.
+constexpr int kMaxLdsDevices = 64;
+constexpr uint32_t kMaxLdsBytes = 163840;
+struct LdsLimitFlags {
+    std::atomic<bool> done[kMaxLdsDevices];
+};
+inline hipError_t raise_lds_limit(const void* fn, LdsLimitFlags& flags) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const bool tracked = dev >= 0 && dev < kMaxLdsDevices;
+    if (tracked && flags.done[dev].load(std::memory_order_acquire)) return hipSuccess;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLdsBytes);
+    if (e == hipSuccess && tracked) flags.done[dev].store(true, std::memory_order_release);
+    return e;
+}
 
 }  // namespace npa

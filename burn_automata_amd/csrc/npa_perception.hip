@@ -1424,12 +1424,10 @@ static hipError_t launch_mlp_e(const StepParams& p, Workspace& ws, const StepIO&
     // then the VALU path's w2t copy [H][OP]
     const size_t hid_end = HP == 128 ? std::max<size_t>(HP * 64, 4 * (size_t)FM * 32) : HP * 64;
     const size_t lds = (hid_end + 64 * (OP + 1) + (ENG == 0 ? (size_t)p.H * OP : 0)) * 4;
-    static size_t attr = 65536;
-    if (lds > attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_mlp_euler<D, SM, FM, ENG>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (lds > 65536) {
+        static LdsLimitFlags limit;
+        const hipError_t e = raise_lds_limit((const void*)k_mlp_euler<D, SM, FM, ENG>, limit);
         if (e != hipSuccess) return e;
-        attr = lds;
     }
     const uint32_t blocks = (p.T + 63) / 64;
     return launch_timed(prof, NPA_KERNEL_MLP, k_mlp_euler<D, SM, FM, ENG>, dim3(blocks), dim3(256), (uint32_t)lds,

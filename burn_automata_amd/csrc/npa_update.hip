@@ -901,13 +901,9 @@ static hipError_t launch_fused_t(const StepParams& p, Workspace& ws, const StepI
     using Sh = FuseShape<D, FL>;
     const size_t lds = (fused_weight_floats(p.FP, D) + (size_t)kFuseWaves * Sh::WAVE_FLOATS) * 4;
     if (lds > kFuseLdsBytes) return hipErrorInvalidValue;
-    static bool attr = false;
-    if (!attr) {
-        const hipError_t e = hipFuncSetAttribute((const void*)k_update_fused<D, FL, ENG>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFuseLdsBytes);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    static LdsLimitFlags limit;
+    const hipError_t e = raise_lds_limit((const void*)k_update_fused<D, FL, ENG>, limit);
+    if (e != hipSuccess) return e;
     // one block per CU at most; never more waves than items of four targets
     const uint64_t max_items = ((uint64_t)p.T + 3) / 4;
     const uint32_t blocks = (uint32_t)std::max<uint64_t>(

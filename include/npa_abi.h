@@ -171,8 +171,10 @@ typedef struct npa_state npa_state;
 /* Creates a context bound to HIP device `device`. `stream` is a hipStream_t
  * (may be NULL for the legacy default stream); the context never destroys it. */
 npa_status npa_context_create(int device, void* stream, npa_context** out);
-/* Ends the caller's use of ctx. States created on it keep it (and its stream) alive: the context's
- * memory is released when the last of them is destroyed, in either order. */
+/* Ends the caller's use of ctx. States created on it keep the context's memory alive: it is
+ * released when the last of them is destroyed, in either order. The library never owns the
+ * caller's stream: the caller keeps it valid until the last state of the context is destroyed
+ * (state calls and that final release are queued on it). */
 void npa_context_destroy(npa_context* ctx);
 npa_status npa_context_set_stream(npa_context* ctx, void* stream);
 /* 0: array arguments are device pointers (default). 1: host pointers, synchronous. */
@@ -276,7 +278,8 @@ npa_status npa_step(npa_context* ctx, const float* positions, const float* state
  * work is queued (the C2 system - 65,536 particles, S = 16, F = 64, a 64x64 grid - fits). Every
  * call on one GPU shares that array and the next call overwrites it: calls that overlap on one GPU
  * (on other streams, contexts or threads) race. The kernel profiler does not time it; its
- * coordinate overflows are reported by npa_context_synchronize. */
+ * coordinate overflows are reported by npa_context_synchronize of a context that has called it
+ * (the overflow word is one per GPU, shared by every context there, not one per context). */
 #define NPA_STEP_NOALLOC_SCRATCH_BYTES (64u << 20)
 npa_status npa_step_noalloc(npa_context* ctx, const float* positions, const float* states,
                             uint32_t batch_size, uint32_t particle_count,

@@ -142,6 +142,38 @@ def test_state_raster_after_a_c4_rollout(ctx, mode):
     state.close()
 
 
+@pytest.mark.parametrize("sh_degree,S", [(1, 20), (1, 32)])
+def test_state_raster_oriented_decode_above_degree_zero(ctx, sh_degree, S):
+    """An oriented decode of SH degree d stores (d + 1)^2 coefficient triples per Gaussian, the colour
+    in the first: the state raster must read every Gaussian's colour at that stride (S >= 3 (d + 1)^2
+    + 8; the device path takes up to 32 state channels, so degree 1 is the largest such decode of a
+    state), after a few steps of the two-kernel path."""
+    from burn_automata_amd.config import HashGridConfig, NpaConfig
+
+    m = NpaConfig.growing_3dgs().replace(state_dims=S)
+    g = HashGridConfig.growing_3dgs()
+    n = 1500
+    pos = syn.uniform_ball(n, 71, 0.5)
+    st = syn.normal_states(n, S, 71, std=0.5)
+    ex = HipAutomataExecutor(ctx=ctx)
+    state = ex.create_state(NpaModel(m, syn.seeded_weights(m, 71)), pos, st, 1, n, g, 1.0, 0.5, 42)
+    ex.step_state_many(state, 3)
+    dcfg = GaussianDecodeConfig(mode=GaussianDecodeMode.GaussianSh0Oriented, sh_degree=sh_degree)
+    dec = {k: to_np(v) for k, v in ex.decode_gaussians_3d(state, dcfg).items()}
+    Kc = (sh_degree + 1) ** 2
+    assert dec["spherical_harmonic"].reshape(n, -1).shape[1] == Kc * 3
+    colours = np.ascontiguousarray(dec["spherical_harmonic"].reshape(n, Kc, 3)[:, :1, :])
+    cam = RasterCamera.look_at((0.4, 0.7, 1.8), width=160, height=120)
+    got = ex.raster_gaussians_3d(state, dcfg, cam)
+    want = O.raster_gaussians_3d(dec["position_visibility"], colours, dec["rotation"], dec["scale_opacity"],
+                                 cam.replace(color_mode=RasterColor.Rgb, sh_degree=0))
+    _check(got, want, f"state raster, oriented decode at SH degree {sh_degree}")
+    assert float((want[..., 3] > 0.01).mean()) > 0.05
+    # the coefficients past the first differ from the colour, so a wrong stride would change pixels
+    assert not np.array_equal(dec["spherical_harmonic"].reshape(n, Kc, 3)[:, 1], colours[:, 0])
+    state.close()
+
+
 def test_state_raster_default_camera_keeps_the_decoded_colour(ctx):
     """One opaque particle in front of a default camera (colour mode SH): the state raster draws its
     decoded colour clamp(tail + 0.5), not 0.5 + SH_C0 * colour, both from the decode (RGB) and from
