@@ -538,6 +538,8 @@ def main(argv=None) -> int:
     decode_every = args.decode_every if args.decode_every is not None else w.get("decode_every", 0)
     decode_steps = set() if args.decode_every is not None else set(w.get("decode_steps", ()))
     splat = w.get("splat")
+    camera = w.get("camera")  # C4: the EWA raster of the oriented decode
+    has_decode = splat is not None or camera is not None
     model = NpaModel(w["model"], w["weights"])
     ex = HipAutomataExecutor()
     ctx = ex.ctx
@@ -546,15 +548,13 @@ def main(argv=None) -> int:
     st = torch.from_numpy(w["states"]).cuda()
 
     def due(k):  # decode after step k (1-based count of steps taken)
-        return splat is not None and ((decode_every and k % decode_every == 0) or k in decode_steps)
+        return has_decode and ((decode_every and k % decode_every == 0) or k in decode_steps)
 
     def decode(state):
         if "tiles_x" in w:  # C5: every system in its own window
             ex.splat_2d_tiled(state, splat, w["tiles_x"])
-        elif w.get("decode") is not None:  # C4: Gaussian decode, then a splat of the centres
-            dec = ex.decode_gaussians_3d(state, w["decode"])
-            K.splat_particles_2d(dec["position_visibility"], dec["spherical_harmonic"][:, 0, :],
-                                 splat, ctx=ctx)
+        elif camera is not None:  # C4: oriented Gaussian decode and its EWA raster, one call
+            ex.raster_gaussians_3d(state, w["decode"], camera)
         else:
             ex.splat_2d(state, splat)
 
@@ -654,12 +654,12 @@ def main(argv=None) -> int:
     # final state is timed here and the decodes the timed steps owe beyond the ones they ran are
     # added to the elapsed time at that cost.
     decode_rate = 0.0
-    if splat is not None:
+    if has_decode:
         decode_rate = (1.0 / decode_every) if decode_every else len(decode_steps) / float(w.get("steps", 256))
     decodes_run = sum(1 for k in range(1, args.steps + 1) if due(k))
     decode_ms = None
     owed = max(0.0, args.steps * decode_rate - decodes_run)
-    if splat is not None:
+    if has_decode:
         decode(state)
         torch.cuda.synchronize()
         td0 = time.perf_counter()
@@ -731,6 +731,9 @@ def main(argv=None) -> int:
                          f"p={w['update_prob']}"
                          + (f", {splat.image_size}x{splat.image_size} RGBA splat every "
                             f"{decode_every} steps" if decode_every and splat else "")
+                         + (f", oriented Gaussian decode drawn by the EWA raster at "
+                            f"{camera.width}x{camera.height} every {decode_every} steps"
+                            if decode_every and camera is not None else "")
                          + (f", {w['tiles_x'] * splat.image_size}x{w['tiles_x'] * splat.image_size}"
                             f" tiled splat after steps {sorted(decode_steps)}"
                             if decode_steps and splat else "")),

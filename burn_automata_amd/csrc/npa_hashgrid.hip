@@ -1228,6 +1228,417 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
     dir_n[bin] = ng;
 }
 
+// ------------------------------------------------ one block per system (small systems)
+// The payload build of small systems in two launches instead of four (rank, offsets scan, payload
+// scatter, split). Used when a system has at most kSysMaxCells bins (coordinate bins in Particle
+// mode, cells in Grid mode) and at most kSysMaxRounds * 1024 particles (C1 and C5: 4,096 particles
+// over 4,096 bins; more rounds per wave would spill registers).
+// k_sys_rank, one 1024-thread block per system:
+//   1. wave w ranks its slice [w R 64, (w + 1) R 64) in rounds of 64 with key ballots and a u16 LDS
+//      counter per key (stable, as k_hash_rank); the group's last lane also adds the group's
+//      update-mask targets to a per-key count (two keys' u16 counts per u32 word);
+//   2. per key (thread t: keys 4t .. 4t + 3, read four at a time): each wave's base and the total,
+//      and one block scan of three sums: the key's first slot (bin_offsets), its first work item
+//      (ceil(total / tpi) items of <= tpi slots, as the split emits for a bin of one cell or an
+//      unsplit bin; sys_item[b][key]) and its first compact row; the system's item and row totals go
+//      to sys_tot[b];
+//   3. per particle: its slot within the system (keys[i]) and, for an update-mask target, a compact
+//      row within the system from its bin's counter (ranks[i] = row + 1, 0 for no row; bit 31 marks
+//      the bin's first particle). Consecutive rows per bin, in the order the LDS atomics land: rows
+//      only index the targets, no result depends on their order.
+// k_sys_scatter, one thread per particle: the systems' item and row bases (prefix of sys_tot), then
+// the sorted record, state row and snapshot entries at the particle's slot, the work item starting
+// there, its compact row (act_rows / row_of), the bin's directory entry from its first particle, and
+// the step's output for a particle outside the update mask (hold_particle); block 0 writes the item
+// and row totals and clears the update's item queues.
+// A Particle-mode bin holds one cell unless the system's cell coordinates span the grid on some
+// axis; then every bin of the system is marked unsplit (dir_n = kDirGroups + 1: the neighbour passes
+// walk the whole bin in the reference order and keep the cell's particles), which is exact for any
+// bin. The coordinate-overflow flag goes to the sticky word flags[1] directly.
+constexpr uint32_t kSysThreads = 1024;
+constexpr uint32_t kSysWaves = kSysThreads / 64;
+
+// cell_coords (hashgrid.rs:98-121) in 32-bit arithmetic: the same coordinates whenever they lie
+// within +-2^30 (beyond that *overflow is set, as cell_coords sets it, and the coordinates only
+// have to be some in-range value); a NaN coordinate is 0, as `f as isize` makes it. The key is the
+// bin cell_of_coords gives (coordinate bins in Particle mode, the cell in Grid mode).
+__device__ __forceinline__ void sys_cell(const float* p, const GridParams& g, int c[3], uint32_t* key,
+                                         bool* overflow) {
+    c[0] = c[1] = c[2] = 0;
+    uint32_t h = 0, stride = 1;
+    for (int a = 0; a < g.dim; ++a) {
+        const float f = g.mode == 1 ? floorf(p[a] / g.eps) : floorf((p[a] + g.half[a]) / g.eps);
+        const bool in = f >= -1073741824.0f && f <= 1073741824.0f;
+        if (!in && f == f && g.mode == 1) *overflow = true;  // (Grid mode clamps or wraps below)
+        int v = in ? (int)f : (f != f ? 0 : (f > 0.0f ? 1073741824 : -1073741824));
+        const uint32_t m = g.size[a];
+        if (g.mode == 1) {
+            c[a] = v;
+            const uint32_t w = (m & (m - 1)) == 0 ? (uint32_t)v & (m - 1) : (uint32_t)(((v % (int)m) + (int)m) % (int)m);
+            h += w * stride;
+        } else {
+            if (g.boundary == 0) {  // rem_euclid of the full value (beyond 2^30 in 64-bit arithmetic)
+                v = in ? ((v % (int)m) + (int)m) % (int)m : (int)rem_euclid_i64(f32_to_isize(f), (int64_t)m);
+            } else {
+                v = v < 0 ? 0 : (v > (int)m - 1 ? (int)m - 1 : v);
+            }
+            c[a] = v;
+            h += (uint32_t)v * stride;
+        }
+        stride *= m;
+    }
+    *key = h;
+}
+
+constexpr uint32_t kSysMaxCells = 4096;
+constexpr uint32_t kSysMaxRounds = 4;
+
+__host__ __device__ inline uint32_t sys_row_stride(uint32_t C) { return (C + 3) & ~3u; }  // u16 per counter row
+// counters [waves][cp] u16, starts [cp + 4] u16, rows [cp / 2] u32
+inline uint32_t sys_lds_bytes(uint32_t C) { return 36u * sys_row_stride(C) + 8u; }
+
+template <int D, int R>
+__global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restrict__ pos, uint32_t n, GridParams g,
+                                                          uint32_t key_bits, uint32_t tpi_log2, SplitTargets T,
+                                                          uint32_t* __restrict__ bin_offsets,
+                                                          uint32_t* __restrict__ dir_n, uint32_t* __restrict__ sys_item,
+                                                          unsigned long long* __restrict__ sys_tot,
+                                                          uint32_t* __restrict__ slot_of,
+                                                          uint32_t* __restrict__ row_code, uint32_t batch,
+                                                          uint32_t* __restrict__ flags) {
+    extern __shared__ uint16_t sys_lds[];
+    constexpr uint32_t K = kDirGroups;
+    const uint32_t C = g.cells, cp = sys_row_stride(C);
+    uint16_t* cnt = sys_lds;                                   // ranks per wave, then each wave's base
+    uint16_t* sstart = cnt + kSysWaves * cp;                   // [C + 1] the key's first slot in the system
+    uint32_t* srow = reinterpret_cast<uint32_t*>(sstart + cp + 4);  // two keys' target counts, then row counters
+    __shared__ uint32_t red[3][kSysWaves];
+    __shared__ int red_lo[3][kSysWaves], red_hi[3][kSysWaves];
+    const uint32_t b = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const uint64_t sys = (uint64_t)b * n;
+
+    {
+        uint64_t* c64 = reinterpret_cast<uint64_t*>(sys_lds);
+        for (uint32_t k = tid; k < kSysWaves * cp / 4; k += kSysThreads) c64[k] = 0ull;
+        for (uint32_t k = tid; k < cp / 2; k += kSysThreads) srow[k] = 0u;
+    }
+    __syncthreads();
+
+    // ---- 1. rank
+    const uint64_t lt = lanemask_lt();
+    volatile uint16_t* mine = cnt + w * cp;
+    uint32_t key_r[R], rank_r[R], tgt_bits = 0;
+    int lo[3] = {INT32_MAX, INT32_MAX, INT32_MAX}, hi[3] = {INT32_MIN, INT32_MIN, INT32_MIN};
+    bool ovf = false;
+    float4 p_r[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t li = (w * R + r) * 64 + lane;
+        p_r[r] = li < n ? pos[sys + li] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t li = (w * R + r) * 64 + lane;
+        const bool active = li < n;
+        uint32_t key = 0;
+        bool tgt = false;
+        if (active) {
+            const float p[4] = {p_r[r].x, p_r[r].y, p_r[r].z, p_r[r].w};
+            int c[3];
+            sys_cell(p, g, c, &key, &ovf);
+#pragma unroll
+            for (int a = 0; a < D; ++a) {
+                lo[a] = min(lo[a], c[a]);
+                hi[a] = max(hi[a], c[a]);
+            }
+            tgt = T.mask_mode == 0 ||
+                  (T.mask_mode == 1 ? hash_mask(li, b, n, T.update_prob, T.step_index, T.base_seed) : T.mask[sys + li]) != 0.0f;
+        }
+        uint64_t peers = __ballot(active);
+        for (uint32_t bit = 0; bit < key_bits; ++bit) {
+            const uint32_t v = (key >> bit) & 1u;
+            const uint64_t m = __ballot(v);
+            peers &= v ? m : ~m;
+        }
+        const uint64_t tball = __ballot(active && tgt);
+        uint32_t rank = 0;
+        if (active) {
+            const uint32_t base = mine[key];
+            rank = base + (uint32_t)__popcll(peers & lt);
+            if ((peers >> lane) == 1ull) {  // the group's last lane: the counter and the group's targets
+                mine[key] = (uint16_t)(base + (uint32_t)__popcll(peers));
+                const uint32_t m = (uint32_t)__popcll(peers & tball);
+                if (m) atomicAdd(&srow[key >> 1], m << (16 * (key & 1u)));
+            }
+        }
+        key_r[r] = key;
+        rank_r[r] = rank;
+        if (tgt) tgt_bits |= 1u << r;
+    }
+    // the system's coordinate span (Particle mode: do coordinate bins hold one cell each?)
+#pragma unroll
+    for (int a = 0; a < D; ++a) {
+        int l = lo[a], h = hi[a];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            l = min(l, __shfl_xor(l, off, 64));
+            h = max(h, __shfl_xor(h, off, 64));
+        }
+        if (lane == 0) {
+            red_lo[a][w] = l;
+            red_hi[a][w] = h;
+        }
+    }
+    if (__ballot(ovf) != 0ull && lane == 0) atomicOr(flags + 1, 1u);
+    __syncthreads();
+
+    // ---- 2. per key: wave bases, totals, and the block's three scans
+    const uint32_t k0 = 4 * tid;
+    uint32_t tot[4] = {0u, 0u, 0u, 0u}, msk[4] = {0u, 0u, 0u, 0u}, itm[4] = {0u, 0u, 0u, 0u};
+    if (k0 < cp) {
+        uint64_t v[kSysWaves];
+#pragma unroll
+        for (uint32_t w2 = 0; w2 < kSysWaves; ++w2) v[w2] = *reinterpret_cast<const uint64_t*>(cnt + w2 * cp + k0);
+        uint64_t run = 0;  // four u16 fields: no carries, every total is at most n < 2^16
+#pragma unroll
+        for (uint32_t w2 = 0; w2 < kSysWaves; ++w2) {
+            *reinterpret_cast<uint64_t*>(cnt + w2 * cp + k0) = run;
+            run += v[w2];
+        }
+        const uint64_t m4 = *reinterpret_cast<const uint64_t*>(srow + 2 * tid);  // keys k0 .. k0 + 3
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            tot[q] = (uint32_t)(run >> (16 * q)) & 0xffffu;
+            msk[q] = (uint32_t)(m4 >> (16 * q)) & 0xffffu;
+            itm[q] = (tot[q] + (1u << tpi_log2) - 1) >> tpi_log2;
+        }
+    }
+    const uint32_t sa = tot[0] + tot[1] + tot[2] + tot[3];
+    const uint32_t sb = itm[0] + itm[1] + itm[2] + itm[3];
+    const uint32_t sm = msk[0] + msk[1] + msk[2] + msk[3];
+    uint32_t xa = sa, xb = sb, xm = sm;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t ya = __shfl_up(xa, off, 64), yb = __shfl_up(xb, off, 64), ym = __shfl_up(xm, off, 64);
+        if (lane >= (uint32_t)off) {
+            xa += ya;
+            xb += yb;
+            xm += ym;
+        }
+    }
+    if (lane == 63) {
+        red[0][w] = xa;
+        red[1][w] = xb;
+        red[2][w] = xm;
+    }
+    __syncthreads();
+    // lane v < 16 holds wave v's sums: a 16-lane inclusive scan gives every wave its prefix
+    uint32_t ea = 0, eb = 0, em = 0;
+    if (lane < kSysWaves) {
+        ea = red[0][lane];
+        eb = red[1][lane];
+        em = red[2][lane];
+    }
+#pragma unroll
+    for (int off = 1; off < (int)kSysWaves; off <<= 1) {
+        const uint32_t ya = __shfl_up(ea, off, 64), yb = __shfl_up(eb, off, 64), ym = __shfl_up(em, off, 64);
+        if (lane >= (uint32_t)off) {
+            ea += ya;
+            eb += yb;
+            em += ym;
+        }
+    }
+    const uint32_t pa = w ? (uint32_t)__shfl((int)ea, (int)w - 1, 64) : 0u;  // earlier waves' sums
+    const uint32_t pb = w ? (uint32_t)__shfl((int)eb, (int)w - 1, 64) : 0u;
+    const uint32_t pm = w ? (uint32_t)__shfl((int)em, (int)w - 1, 64) : 0u;
+    const uint32_t tb = (uint32_t)__shfl((int)eb, (int)kSysWaves - 1, 64);
+    const uint32_t tm = (uint32_t)__shfl((int)em, (int)kSysWaves - 1, 64);
+    bool alias = false;
+    if (g.mode == 1) {
+#pragma unroll
+        for (int a = 0; a < D; ++a) {
+            int l = lane < kSysWaves ? red_lo[a][lane] : INT32_MAX;
+            int h = lane < kSysWaves ? red_hi[a][lane] : INT32_MIN;
+#pragma unroll
+            for (int off = 8; off >= 1; off >>= 1) {
+                l = min(l, __shfl_xor(l, off, 64));
+                h = max(h, __shfl_xor(h, off, 64));
+            }
+            l = __shfl(l, 0, 64);
+            h = __shfl(h, 0, 64);
+            if (h >= l && (int64_t)h - (int64_t)l >= (int64_t)g.size[a]) alias = true;
+        }
+    }
+    if (tid == 0) {
+        sys_tot[b] = (unsigned long long)tb | ((unsigned long long)tm << 32);
+        sstart[C] = (uint16_t)n;
+        if (b == batch - 1) bin_offsets[(uint64_t)batch * C] = batch * n;
+    }
+    if (k0 < C) {
+        uint32_t st = pa + xa - sa, it = pb + xb - sb, rw = pm + xm - sm;
+        uint64_t rpack = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t k = k0 + q;
+            if (k < C) {
+                sstart[k] = (uint16_t)st;
+                bin_offsets[(uint64_t)b * C + k] = b * n + st;
+                sys_item[(uint64_t)b * C + k] = it;
+                if (g.mode == 1) dir_n[(uint64_t)b * C + k] = tot[q] ? (alias ? K + 1 : 1u) : 0u;
+                rpack |= (uint64_t)rw << (16 * q);
+            }
+            st += tot[q];
+            it += itm[q];
+            rw += msk[q];
+        }
+        *reinterpret_cast<uint64_t*>(srow + 2 * tid) = rpack;  // the keys' first rows: the row counters
+    }
+    __syncthreads();
+
+    // ---- 3. per particle: slot and compact row within the system
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t li = (w * R + r) * 64 + lane;
+        if (li >= n) continue;
+        const uint32_t key = key_r[r];
+        const uint32_t r_bin = cnt[w * cp + key] + rank_r[r];  // rank among the bin's particles
+        uint32_t code = r_bin == 0 ? 0x80000000u : 0u;
+        if ((tgt_bits >> r) & 1u) {
+            const uint32_t sh = 16 * (key & 1u);
+            const uint32_t old = atomicAdd(&srow[key >> 1], 1u << sh);
+            code |= ((old >> sh) & 0xffffu) + 1u;
+        }
+        slot_of[sys + li] = (uint32_t)sstart[key] + r_bin;
+        row_code[sys + li] = code;
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void k_sys_scatter(const float4* __restrict__ pos, const float* __restrict__ states,
+                                                     uint32_t S, uint32_t n, uint32_t batch, GridParams g,
+                                                     uint32_t tpi_log2, SplitTargets T,
+                                                     const uint32_t* __restrict__ bin_offsets,
+                                                     const uint32_t* __restrict__ sys_item,
+                                                     const unsigned long long* __restrict__ sys_tot,
+                                                     const uint32_t* __restrict__ slot_of,
+                                                     const uint32_t* __restrict__ row_code,
+                                                     uint32_t* __restrict__ perm, uint32_t* __restrict__ inv,
+                                                     float4* __restrict__ srec, int4* __restrict__ scoord,
+                                                     float* __restrict__ sstate, int4* __restrict__ dir_e,
+                                                     uint2* __restrict__ worklist, uint32_t* __restrict__ wl_count,
+                                                     uint32_t* __restrict__ act_rows, uint32_t* __restrict__ row_of) {
+    __shared__ unsigned long long s_base[2], s_part[4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint64_t total = (uint64_t)batch * n;
+    const uint64_t first = (uint64_t)blockIdx.x * blockDim.x;
+    const uint32_t b_lo = (uint32_t)(first / n);  // the block's first system
+    // item and row bases of systems b_lo .. b_hi: prefix sums of the systems' totals (items in the
+    // low word, rows in the high word: no carries, both stay below 2^32); block 0 also sums them all
+    const uint32_t upto = blockIdx.x == 0 ? batch : b_lo;
+    unsigned long long acc = 0;
+    for (uint32_t k = tid; k < upto; k += blockDim.x) acc += sys_tot[k];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) s_part[w] = acc;
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned long long all = s_part[0] + s_part[1] + s_part[2] + s_part[3];
+        if (blockIdx.x == 0) {  // the lists' counts; the update's item queues start at zero
+            wl_count[0] = (uint32_t)all;
+            wl_count[1] = (uint32_t)(all >> 32);
+            s_base[0] = 0ull;
+        } else {
+            s_base[0] = all;
+        }
+    }
+    if (blockIdx.x == 0)
+        for (uint32_t k = 2 + tid; k < kWlWords; k += blockDim.x) wl_count[k] = 0u;
+    __syncthreads();
+    const uint64_t i = first + tid;
+    if (i >= total) return;
+    const uint32_t b = (uint32_t)(i / n);
+    unsigned long long base = s_base[0];
+    for (uint32_t bb = b_lo; bb < b; ++bb) base += sys_tot[bb];  // a block spanning several systems
+    const uint32_t ibase = (uint32_t)base, rbase = (uint32_t)(base >> 32);
+    const float4 p4 = pos[i];
+    const uint32_t local = slot_of[i];
+    const uint32_t code = row_code[i];
+    const float p[4] = {p4.x, p4.y, p4.z, p4.w};
+    int c[3];
+    uint32_t key;
+    bool o = false;
+    sys_cell(p, g, c, &key, &o);  // (an overflow was flagged by the rank kernel)
+    const uint32_t slot = b * n + local;
+    write_sorted<D>(slot, (uint32_t)i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
+    const uint32_t row1 = code & 0x7fffffffu;
+    if (row1) {
+        const uint32_t row = rbase + row1 - 1u;
+        act_rows[row] = slot;
+        row_of[slot] = row;
+    } else {
+        row_of[slot] = ~0u;
+        if (T.mask_mode != 0) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
+    }
+    const uint64_t bin = (uint64_t)b * g.cells + key;
+    const uint32_t beg = bin_offsets[bin];
+    const uint32_t r_bin = slot - beg;
+    const uint32_t tpi = 1u << tpi_log2;
+    if ((r_bin & (tpi - 1)) == 0) {
+        const uint32_t left = bin_offsets[bin + 1] - beg - r_bin;
+        worklist[ibase + sys_item[bin] + (r_bin >> tpi_log2)] = make_uint2(slot, left < tpi ? left : tpi);
+    }
+    if (g.mode == 1 && (code >> 31)) dir_e[bin * kDirGroups] = make_int4(c[0], c[1], c[2], (int)slot);
+}
+
+template <int D, int R>
+static hipError_t launch_sys_r(const GridParams& g, const HashgridPlan& plan, const float4* pos, const float* states,
+                               uint32_t S, uint32_t batch, uint32_t n, Workspace& ws, const SplitTargets& tg,
+                               hipStream_t stream, Profiler* prof) {
+    const uint32_t lds = sys_lds_bytes(plan.cells);
+    if (lds > 32768) {
+        static LdsLimitFlags limit;
+        const hipError_t e = raise_lds_limit((const void*)k_sys_rank<D, R>, limit);
+        if (e != hipSuccess) return e;
+    }
+    // per particle: slot (keys) and row code (ranks); per bin: first item (totals); per system: totals
+    hipError_t e = launch_timed(prof, NPA_KERNEL_HASH_RANK, k_sys_rank<D, R>, dim3(batch), dim3(kSysThreads), lds,
+                                stream, pos, n, g, plan.key_bits, (uint32_t)__builtin_ctz(plan.tpi), tg,
+                                ws.bin_offsets.as<uint32_t>(),
+                                ws.dir_n.as<uint32_t>(), ws.totals.as<uint32_t>(),
+                                ws.scan_status.as<unsigned long long>(), ws.keys.as<uint32_t>(),
+                                ws.ranks.as<uint32_t>(), batch, ws.flags.as<uint32_t>());
+    if (e != hipSuccess) return e;
+    const uint64_t total = (uint64_t)batch * n;
+    return launch_timed(prof, NPA_KERNEL_SCATTER, k_sys_scatter<D>, dim3((uint32_t)((total + 255) / 256)), dim3(256),
+                        0, stream, pos, states, S, n, batch, g, (uint32_t)__builtin_ctz(plan.tpi), tg,
+                        ws.bin_offsets.as<uint32_t>(),
+                        ws.totals.as<uint32_t>(), ws.scan_status.as<unsigned long long>(), ws.keys.as<uint32_t>(),
+                        ws.ranks.as<uint32_t>(), ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(),
+                        ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(), ws.dir_e.as<int4>(),
+                        ws.worklist.as<uint2>(), ws.wl_count.as<uint32_t>(), ws.act_rows.as<uint32_t>(),
+                        ws.row_of.as<uint32_t>());
+}
+
+// The two-launch build applies to a payload build of small systems whose bins are cells or
+// coordinate bins (the reference's mixing-hash bins keep the four-launch build).
+static bool sys_build_applies(const HashgridPlan& plan, const GridParams& g, uint32_t n) {
+    return n > 0 && plan.cells <= kSysMaxCells && n <= kSysMaxRounds * kSysThreads && plan.tpi <= 64 &&
+           (plan.tpi & (plan.tpi - 1)) == 0 && (g.mode != 1 || g.spatial);
+}
+
+static hipError_t launch_sys(const GridParams& g, const HashgridPlan& plan, const float4* pos, const float* states,
+                             uint32_t S, uint32_t batch, uint32_t n, Workspace& ws, const SplitTargets& tg,
+                             hipStream_t stream, Profiler* prof) {
+    const uint32_t rounds = (n + kSysThreads - 1) / kSysThreads;
+#define NPA_SYS(RR) \
+    return g.dim == 2 ? launch_sys_r<2, RR>(g, plan, pos, states, S, batch, n, ws, tg, stream, prof) \
+                      : launch_sys_r<3, RR>(g, plan, pos, states, S, batch, n, ws, tg, stream, prof)
+    if (rounds <= 1) NPA_SYS(1);
+    if (rounds <= 2) NPA_SYS(2);
+    NPA_SYS(4);
+#undef NPA_SYS
+}
+
 // ------------------------------------------------------------------ launch
 template <int R>
 static hipError_t launch_rank_r(uint32_t blocks, uint32_t waves, uint32_t lds_bytes,
@@ -1274,6 +1685,10 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                            Workspace& ws, bool payload, hipStream_t stream, Profiler* prof,
                            const SplitTargets* targets) {
     const uint64_t total = (uint64_t)batch * n;
+    if (payload && sys_build_applies(plan, g, n)) {
+        const SplitTargets tg = targets ? *targets : SplitTargets{};
+        return launch_sys(g, plan, pos, states, state_dims, batch, n, ws, tg, stream, prof);
+    }
     const uint32_t kblocks = (plan.cells + 255) / 256;  // 256-key blocks of the one-pass scan
     hipError_t e = launch_rank(plan.rounds, batch * plan.tiles_per_sys, plan.waves, plan.lds_bytes,
                                plan.tiles_per_sys, plan.key_bits, g, pos, nullptr, nullptr, n, ws.keys.as<uint32_t>(),

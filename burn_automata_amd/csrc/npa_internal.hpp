@@ -406,8 +406,9 @@ hipError_t launch_perceive_adjoint(const StepParams& p, Workspace& ws, AdjointWo
 int device_cu_count();
 
 // A kernel's dynamic-LDS limit, raised once per device to the 160 KiB a gfx950 workgroup can hold
-// (each launch still asks for what it uses). Thread-safe: a device's flag is set only after the
-// attribute call succeeded, and threads that race on a first launch all set the same value.
+// less the kernel's static LDS (each launch still asks for what it uses). Thread-safe: a device's
+// flag is set only after the attribute call succeeded, and threads that race on a first launch all
+// set the same value.
 constexpr int kMaxLdsDevices = 64;
 constexpr uint32_t kMaxLdsBytes = 163840;
 struct LdsLimitFlags {
@@ -419,7 +420,11 @@ inline hipError_t raise_lds_limit(const void* fn, LdsLimitFlags& flags) {
     if (e != hipSuccess) return e;
     const bool tracked = dev >= 0 && dev < kMaxLdsDevices;
     if (tracked && flags.done[dev].load(std::memory_order_acquire)) return hipSuccess;
-    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLdsBytes);
+    hipFuncAttributes attr{};
+    e = hipFuncGetAttributes(&attr, fn);
+    if (e != hipSuccess) return e;
+    const int dyn = (int)kMaxLdsBytes - (int)attr.sharedSizeBytes;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
     if (e == hipSuccess && tracked) flags.done[dev].store(true, std::memory_order_release);
     return e;
 }

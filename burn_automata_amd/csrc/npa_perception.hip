@@ -79,6 +79,17 @@ __device__ __forceinline__ float group_bcast(float v) {
     }
 }
 
+// Value of lane (quad base + j) for a lane index j known only at compile time after unrolling.
+template <int L>
+__device__ __forceinline__ int group_bcast_k(int v, int j) {
+    switch (j) {
+        case 0: return __float_as_int(group_bcast<L, 0>(__int_as_float(v)));
+        case 1: return __float_as_int(group_bcast<L, 1>(__int_as_float(v)));
+        case 2: return __float_as_int(group_bcast<L, 2>(__int_as_float(v)));
+        default: return __float_as_int(group_bcast<L, 3>(__int_as_float(v)));
+    }
+}
+
 // OR of a 64-bit value over each group of L consecutive lanes (L = 1, 2 or 4), via DPP.
 template <int L>
 __device__ __forceinline__ uint64_t group_or(uint64_t m) {
@@ -383,6 +394,179 @@ __global__ __launch_bounds__(256) void k_density_sparse(StepParams P, const floa
     svol[s] = make_float4(pi[0], pi[1], pi[2], recip_finite(rho));
     if (record) nb_count[row] = gch;
     if (density_out) density_out[b * P.N + perm[s]] = rho;
+}
+
+// The density pass for sparse 2D grids, four lanes per target and sixteen consecutive slots per wave:
+// writes exactly what k_density_q writes (the same sum in the same order, the same chunk records),
+// with the lanes of a target sharing its own neighbour runs instead of a wave sharing one cell's.
+//   lookup: lane q of a target looks up its neighbour cells k = q, q + 4, q + 8 (visit order
+//     k = (dy + 1) * 3 + (dx + 1)); the runs' starts, lengths and cell filters are broadcast within
+//     the quad, and every lane holds the visit-order stream of the target's candidates: candidate
+//     j lies in the last run k with P_k <= j (P: exclusive prefix of the run lengths) at slot
+//     j + (start_k - P_k);
+//   rounds: lane q tests candidate 4 r + q of the stream in round r (four rounds' records loaded
+//     together), and every lane rebuilds the running sum in candidate order from the quad's four
+//     terms (a rejected or missing candidate adds +0.0, which leaves the sum unchanged);
+//   records (update-mask targets): the quad's accept nibbles, eight rounds per word, go to an LDS
+//     bit stream of the first kStreamBits candidates (enough for every recorded chunk: max_chunks
+//     of 64 candidates); afterwards the owner lane of run k writes each of the run's 64-slot chunks'
+//     first slot and mask (bits [P_k + 64 c, ...) of the stream) for the first max_chunks chunks,
+//     and nb_count = the target's chunk count, as the chunk loop of k_density_q counts them.
+constexpr uint32_t kStreamWords = 24 * 64 / 32;  // max_chunks(2) chunks of 64 candidates
+
+template <int D>
+__global__ __launch_bounds__(256) void k_density_lanes(StepParams P, const float4* __restrict__ srec,
+                                                       const uint32_t* __restrict__ bo,
+                                                       const uint32_t* __restrict__ perm,
+                                                       const uint32_t* __restrict__ row_of,
+                                                       float4* __restrict__ svol, float* __restrict__ density_out,
+                                                       uint32_t* __restrict__ nb_base, uint64_t* __restrict__ nb_mask,
+                                                       uint32_t* __restrict__ nb_count) {
+    static_assert(D == 2, "the four-lane sparse pass serves 2D grids (nine neighbour cells)");
+    constexpr uint32_t MAXC = max_chunks(D);
+    static_assert(MAXC * 64 == kStreamWords * 32, "the stream holds every recorded chunk");
+    __shared__ uint32_t stream_lds[4][16][kStreamWords + 1];
+    const uint32_t lane = threadIdx.x & 63, t = lane >> 2, q = lane & 3;
+    const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    uint32_t* stream = stream_lds[threadIdx.x >> 6][t];
+    const uint32_t s_raw = wave * 16 + t;
+    if (wave * 16 >= P.T) return;  // (wave-uniform)
+    const bool active = s_raw < P.T;
+    const uint32_t s = active ? s_raw : P.T - 1;
+    const uint32_t b = s / P.N;
+    float pi[3];
+    int ci[3];
+    load_rec<D>(srec, nullptr, s, pi, ci);
+    const uint32_t row = active ? row_of[s] : ~0u;
+    const bool record = row != ~0u;
+    // ---- lookup: lane q, cells q, q + 4, q + 8
+    uint32_t obeg[3], olen[3];
+    bool ofilt[3];
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+        const uint32_t k = q + 4 * u;
+        obeg[u] = 0;
+        olen[u] = 0;
+        ofilt[u] = false;
+        if (k < 9 && active) {
+            uint32_t beg, end;
+            bool filt;
+            if (cell_range(P, bo, b, (int64_t)ci[0] + (int)(k % 3) - 1, (int64_t)ci[1] + (int)(k / 3) - 1, 0, beg,
+                           end, filt)) {
+                obeg[u] = beg;
+                olen[u] = end - beg;
+                ofilt[u] = filt;
+            }
+        }
+    }
+    // every run in every lane of the quad (run k lives in lane k % 4, register k / 4)
+    uint32_t rbeg[9], rlen[9], rfilt = 0;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        rbeg[k] = (uint32_t)group_bcast_k<4>((int)obeg[k / 4], k % 4);
+        rlen[k] = (uint32_t)group_bcast_k<4>((int)olen[k / 4], k % 4);
+        rfilt |= ((uint32_t)group_bcast_k<4>((int)ofilt[k / 4], k % 4) & 1u) << k;
+    }
+    uint32_t pre[9], total = 0;
+    int dlt[9];  // slot - stream position within run k
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        pre[k] = total;
+        dlt[k] = (int)rbeg[k] - (int)total;
+        total += rlen[k];
+    }
+    uint32_t rounds = (total + 3) / 4;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) rounds = max(rounds, (uint32_t)__shfl_xor((int)rounds, off, 64));
+    const bool any_filter = __ballot(rfilt != 0) != 0ull;
+    const float eps2 = P.g.eps2, k6 = P.g.k6;
+    const bool periodic = P.g.boundary == 0;
+    float rho = 0.0f;
+    uint32_t word = 0;  // accept nibbles of eight rounds (candidates 32 w .. 32 w + 31)
+    auto candidate = [&](uint32_t j, uint32_t& slot, int& kk) {  // run of stream position j, and its slot
+        int d = dlt[0];
+        kk = 0;
+#pragma unroll
+        for (int k = 1; k < 9; ++k) {
+            const bool in = j >= pre[k];
+            d = in ? dlt[k] : d;
+            kk = in ? k : kk;
+        }
+        slot = (uint32_t)((int)j + d);
+    };
+    for (uint32_t r0 = 0; r0 < rounds; r0 += 4) {
+        float4 rc[4];
+        bool ok[4];
+        int kr[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t j = 4 * (r0 + u) + q;
+            uint32_t slot;
+            candidate(j, slot, kr[u]);
+            ok[u] = active && j < total;
+            rc[u] = srec[ok[u] ? slot : s];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (r0 + u >= rounds) break;
+            bool acc_ok = ok[u];
+            if (any_filter && ((rfilt >> kr[u]) & 1u)) {  // an unsplit bin: keep this cell's particles
+                const int64_t n0 = (int64_t)ci[0] + kr[u] % 3 - 1, n1 = (int64_t)ci[1] + kr[u] / 3 - 1;
+                acc_ok = acc_ok && (int64_t)__float_as_int(rc[u].z) == n0 && (int64_t)__float_as_int(rc[u].w) == n1;
+            }
+            float d0 = rc[u].x - pi[0], d1 = rc[u].y - pi[1];
+            if (periodic) {
+                d0 = delta_axis(pi[0], rc[u].x, 0, P.g);
+                d1 = delta_axis(pi[1], rc[u].y, 1, P.g);
+            }
+            float r2 = d0 * d0;
+            r2 += d1 * d1;
+            const bool near = acc_ok && r2 < eps2;
+            const float x = eps2 - r2;
+            rho = ordered_group_sum<4>(rho, near ? k6 * x * x * x : 0.0f);  // smoothing_poly6_kernel
+            const uint64_t bal = __builtin_amdgcn_ballot_w64(near);
+            const uint32_t r = r0 + u;
+            word |= ((uint32_t)(bal >> (lane & ~3u)) & 0xfu) << (4 * (r & 7u));
+            if ((r & 7u) == 7u || r + 1 == rounds) {
+                if (q == 0 && r / 8 < kStreamWords) stream[r / 8] = word;
+                word = 0;
+            }
+        }
+    }
+    if (active && q == 0) {
+        svol[s] = make_float4(pi[0], pi[1], pi[2], recip_finite(rho));
+        if (density_out) density_out[b * P.N + perm[s]] = rho;
+    }
+    if (!__ballot(record)) return;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // chunks: run k holds ceil(len / 64), in visit order after the earlier runs' chunks
+    uint32_t gch0[9], nch = 0;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        gch0[k] = nch;
+        nch += (rlen[k] + 63) / 64;
+    }
+    if (!record) return;
+    if (q == 0) nb_count[row] = nch;
+    const uint32_t used = min((total + 31) / 32, kStreamWords);  // stream words written
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+        const uint32_t k = q + 4 * u;
+        if (k >= 9) break;
+        for (uint32_t c = 0; 64 * c < rlen[k] && gch0[k] + c < MAXC; ++c) {
+            const uint32_t a = pre[k] + 64 * c;  // stream bit of the chunk's first candidate
+            const uint32_t L = min(64u, rlen[k] - 64 * c);
+            const uint32_t w0 = a / 32, sh = a % 32;
+            const uint64_t lo = (uint64_t)(w0 < used ? stream[w0] : 0u) | ((uint64_t)(w0 + 1 < used ? stream[w0 + 1] : 0u) << 32);
+            const uint64_t hi = w0 + 2 < used ? stream[w0 + 2] : 0u;
+            uint64_t m = sh ? (lo >> sh) | (hi << (64 - sh)) : lo;
+            if (L < 64) m &= (1ull << L) - 1ull;
+            nb_base[(uint64_t)row * MAXC + gch0[k] + c] = rbeg[k] + 64 * c;
+            nb_mask[(uint64_t)row * MAXC + gch0[k] + c] = m;
+        }
+    }
 }
 
 // Per-wave accepted-neighbour lists of the second pass: the sorted slots of each target's accepted
@@ -1339,12 +1523,12 @@ hipError_t launch_density(const StepParams& p_in, Workspace& ws, float* density_
     const StepParams p = with_directory(p_in, ws);
     // sparse 2D bins: a thread per target (in 3D a target walks 27 cells, and the occupied cells of
     // a sparse grid - a surface, say - hold several particles: the wave pass stays faster there)
-    if (p.g.dim == 2 && (uint64_t)p.B * p.g.cells * 4 > p.T) {
-        auto k = p.g.dim == 2 ? k_density_sparse<2> : k_density_sparse<3>;
-        return launch_timed(prof, NPA_KERNEL_DENSITY, k, dim3((p.T + 255) / 256), dim3(256), 0, stream, p,
-                            ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(),
-                            ws.perm.as<uint32_t>(), ws.row_of.as<uint32_t>(), ws.svol.as<float4>(), density_out,
-                            ws.nb_base.as<uint32_t>(), ws.nb_mask.as<uint64_t>(), ws.nb_count.as<uint32_t>());
+    if (p.g.dim == 2 && (uint64_t)p.B * p.g.cells * 4 > p.T) {  // four lanes per target, 16 per wave
+        const uint32_t waves = (p.T + 15) / 16;
+        return launch_timed(prof, NPA_KERNEL_DENSITY, k_density_lanes<2>, dim3((waves + 3) / 4), dim3(256), 0, stream,
+                            p, ws.srec.as<float4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
+                            ws.row_of.as<uint32_t>(), ws.svol.as<float4>(), density_out, ws.nb_base.as<uint32_t>(),
+                            ws.nb_mask.as<uint64_t>(), ws.nb_count.as<uint32_t>());
     }
     auto k = p.g.dim == 2 ? k_density_q<2> : k_density_q<3>;  // four waves per block, a wave per item
     return launch_timed(prof, NPA_KERNEL_DENSITY, k, dim3(grid_blocks), dim3(256), 0, stream, p, ws.srec.as<float4>(),

@@ -47,7 +47,7 @@
 
 namespace npa {
 
-constexpr int kFuseWaves = 16;          // waves per block (one block per CU)
+constexpr int kFuseWaves = 16;          // waves per block (one block per CU) for systems with many items
 constexpr uint32_t kFuseHidden = 128;   // hidden units held per target (H <= 128, zero padded)
 constexpr uint32_t kFuseLdsBytes = 163840;
 
@@ -304,10 +304,11 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
     // b / 8 * 16 + wave); later ones come from the queue's counter (zeroed with the work-list
     // counters by the hashgrid build) when an item is done, so the XCD's waves share its items to
     // the end, and a wave that the SIMD's oldest-first issue keeps waiting takes fewer of them.
+    const uint32_t nw = blockDim.x >> 6;  // waves per block (kFuseWaves, fewer for small systems)
     const uint32_t nq = gridDim.x % 8 == 0 ? 8u : 1u;
     const uint32_t xq = blockIdx.x % nq;
-    const uint32_t per_round = gridDim.x / nq * kFuseWaves;
-    auto item_at = [&](uint32_t p) { return (p / per_round) * (gridDim.x * kFuseWaves) + xq * per_round + p % per_round; };
+    const uint32_t per_round = gridDim.x / nq * nw;
+    auto item_at = [&](uint32_t p) { return (p / per_round) * (gridDim.x * nw) + xq * per_round + p % per_round; };
     uint32_t* queue = wlc + kQueueWord + xq * kQueueStride;
     auto take = [&]() {
         uint32_t p = 0;
@@ -318,7 +319,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
         const uint32_t r = it * 4 + g;
         return act_rows[r < nrows ? r : it * 4];
     };
-    uint32_t item = item_at(blockIdx.x / nq * kFuseWaves + wave);
+    uint32_t item = item_at(blockIdx.x / nq * nw + wave);
     uint32_t s_next = item < nitems ? slot_of(item) : 0u;  // the item's compact-row slot
     while (item < nitems) {
         const uint32_t row = item * 4 + g;
@@ -899,17 +900,21 @@ template <int D, int FL, int ENG>
 static hipError_t launch_fused_t(const StepParams& p, Workspace& ws, const StepIO& io, const float* wfused,
                                  hipStream_t stream, Profiler* prof) {
     using Sh = FuseShape<D, FL>;
-    const size_t lds = (fused_weight_floats(p.FP, D) + (size_t)kFuseWaves * Sh::WAVE_FLOATS) * 4;
+    // one block per CU at most; never more waves than items of four targets: a system with fewer
+    // items than 16 per CU takes blocks of fewer waves (a power of two), so its items spread over
+    // every CU instead of queueing on a few
+    const uint64_t max_items = ((uint64_t)p.T + 3) / 4;
+    const uint64_t cus = (uint64_t)device_cu_count();
+    uint32_t nw = 1;
+    while (nw < (uint32_t)kFuseWaves && (uint64_t)nw * cus < max_items) nw *= 2;
+    const size_t lds = (fused_weight_floats(p.FP, D) + (size_t)nw * Sh::WAVE_FLOATS) * 4;
     if (lds > kFuseLdsBytes) return hipErrorInvalidValue;
     static LdsLimitFlags limit;
     const hipError_t e = raise_lds_limit((const void*)k_update_fused<D, FL, ENG>, limit);
     if (e != hipSuccess) return e;
-    // one block per CU at most; never more waves than items of four targets
-    const uint64_t max_items = ((uint64_t)p.T + 3) / 4;
-    const uint32_t blocks = (uint32_t)std::max<uint64_t>(
-        1, std::min<uint64_t>((uint64_t)device_cu_count(), (max_items + kFuseWaves - 1) / kFuseWaves));
+    const uint32_t blocks = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(cus, (max_items + nw - 1) / nw));
     uint32_t* wl = ws.wl_count.as<uint32_t>();
-    return launch_timed(prof, NPA_KERNEL_UPDATE, k_update_fused<D, FL, ENG>, dim3(blocks), dim3(64 * kFuseWaves),
+    return launch_timed(prof, NPA_KERNEL_UPDATE, k_update_fused<D, FL, ENG>, dim3(blocks), dim3(64 * nw),
                         (uint32_t)lds, stream, p, ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(),
                         ws.svol.as<float4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
                         ws.act_rows.as<uint32_t>(), wl, ws.nb_base.as<uint32_t>(),

@@ -22,7 +22,7 @@ import math
 import numpy as np
 
 from .config import (Boundary, GaussianDecodeConfig, GaussianDecodeMode, HashGridConfig, HashGridMode,
-                     NpaConfig, Splat2dConfig)
+                     NpaConfig, RasterCamera, Splat2dConfig)
 
 _M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
 
@@ -222,15 +222,15 @@ def workload(name: str, seed: int = 42, particles: int | None = None):
         model = NpaConfig.growing_3dgs().replace(state_dims=16, hidden_dims=128, eps0=0.04,
                                                  density_grad=False, alpha=0.5)
         grid = HashGridConfig(3, Boundary.Clamped, HashGridMode.Particle, (32, 32, 32), 0.04, 64)
-        # decode: oriented Gaussians (gaussian.rs:53-223), drawn as an isotropic 2D splat of their
-        # x/y centres and SH0 colours (the oriented 3D raster has no reference CPU path)
+        # decode: oriented Gaussians (gaussian.rs:53-223) drawn by the EWA raster of oriented
+        # Gaussians at 512x512 (npa_state_raster_gaussians_3d: the viewer's draw of the decode),
+        # from a fixed camera framing the surface (extent about 1.2 x 0.9 x 1.1 around the origin)
         return dict(model=model, grid=grid, batch=1, n=n, positions=closed_surface_3d(n, seed),
                     states=normal_states(n, model.state_dims, seed),
                     weights=seeded_weights(model, seed), steps=256, dt=1.0, update_prob=0.5,
                     seed=seed, decode_every=32,
                     decode=GaussianDecodeConfig(mode=GaussianDecodeMode.GaussianSh0Oriented),
-                    splat=Splat2dConfig(image_size=512, sigma=0.004 * 511 / 2, lo=-1.0, hi=1.0,
-                                        normalize_color=True, y_up=True, pixel_size=2.0 / 512))
+                    camera=RasterCamera.look_at((0.9, 1.2, 2.6), (0.0, 0.0, 0.1), width=512, height=512))
     if name == "c5":
         n = particles or 4096
         b = 64
