@@ -85,7 +85,9 @@ static void each_buffer(Workspace& w, const HashgridPlan& plan, uint64_t total, 
     f(w.features, t1 * (uint64_t)(feature_dims ? feature_dims : 1) * 4);
     f(w.wpad, wpad_bytes ? wpad_bytes : 4);
     f(w.tmpidx, t1 * 4);
-    f(w.scan_status, (uint64_t)batch * ((plan.cells + 255) / 256) * 8 + 8);
+    // two status words per 256-key block (the folded scan's second one) and the blocks' ticket
+    f(w.scan_status, (uint64_t)batch * ((plan.cells + 255) / 256) * 16 + 8);
+    f(w.tile_span, (uint64_t)batch * plan.tiles_per_sys * 32);
     f(w.dir_n, (bins ? bins : 1) * 4);
     f(w.bin_list, (bins ? bins : 1) * 4);
     f(w.dir_e, (bins ? bins : 1) * kDirGroups * 16);
@@ -130,7 +132,8 @@ uint64_t Workspace::carve(const HashgridPlan& plan, uint64_t total, uint32_t bat
 void Workspace::release() {
     for (DevBuf* b : {&keys, &ranks, &table, &totals, &bin_offsets, &perm, &inv, &flags, &wl_count,
                       &worklist, &srec, &scoord, &sstate, &svol, &counters, &features, &wpad, &tmpidx,
-                      &dir_n, &dir_e, &bin_list, &act_rows, &row_of, &nb_base, &nb_mask, &nb_count, &scan_status})
+                      &dir_n, &dir_e, &bin_list, &act_rows, &row_of, &nb_base, &nb_mask, &nb_count, &scan_status,
+                      &tile_span})
         b->release();
 }
 
@@ -238,9 +241,16 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
                                                    uint32_t* __restrict__ flags,
                                                    uint32_t* __restrict__ wl_count,
                                                    unsigned long long* __restrict__ scan_status,
-                                                   uint32_t nstatus) {
+                                                   uint32_t nstatus, SplitTargets T,
+                                                   int* __restrict__ tile_span) {
     extern __shared__ uint16_t cnt[];
+    __shared__ int span_red[6][16];
     const uint32_t C = g.cells;
+    // folded build (tile_span set): the tile's update-mask targets per key are counted too (u16
+    // pairs after the rank counters) and go to the table's high half, and the tile's cell
+    // coordinate span goes to tile_span[tile] (min x, y, z, max x, y, z)
+    const bool fold = tile_span != nullptr;
+    uint32_t* mcnt = reinterpret_cast<uint32_t*>(cnt + ((waves * C + 1) & ~1u));
     const uint32_t tile = blockIdx.x;
     const uint32_t b = tile / tiles_per_sys;
     const uint32_t t = tile - b * tiles_per_sys;
@@ -252,6 +262,8 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
     const uint32_t nwords = waves * C;
     for (uint32_t k = threadIdx.x; k < nwords / 8; k += blockDim.x) reinterpret_cast<uint4*>(cnt)[k] = make_uint4(0, 0, 0, 0);
     for (uint32_t k = nwords / 8 * 8 + threadIdx.x; k < nwords; k += blockDim.x) cnt[k] = 0;
+    if (fold)
+        for (uint32_t k = threadIdx.x; k < (C + 1) / 2; k += blockDim.x) mcnt[k] = 0u;
     if (wl_count && tile == 0)  // work-list counters and item queues
         for (uint32_t k = threadIdx.x; k < kWlWords; k += blockDim.x) wl_count[k] = 0;
     for (uint32_t k = tile * blockDim.x + threadIdx.x; k < nstatus; k += gridDim.x * blockDim.x)
@@ -269,6 +281,8 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
 #pragma unroll
     for (int r = 0; r < R; ++r) key_r[r] = rank_r[r] = 0;
     bool ovf = false;
+    int lo[3] = {INT32_MAX, INT32_MAX, INT32_MAX}, hi[3] = {INT32_MIN, INT32_MIN, INT32_MIN};
+    uint32_t tgt_bits = 0;
     if (ranker) {
     // every round's key first (all of the wave's loads in flight together), then the rounds' ranks
 #pragma unroll
@@ -287,6 +301,18 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
             cell_coords(p, g, c, &o);
             key_r[r] = cell_of_coords(c, g);
             ovf = ovf || (o && li < n);
+            if (fold && li < n) {
+#pragma unroll
+                for (int a = 0; a < 3; ++a) {
+                    const int v = (int)(c[a] < INT32_MIN ? INT32_MIN : (c[a] > INT32_MAX ? INT32_MAX : c[a]));
+                    lo[a] = min(lo[a], v);
+                    hi[a] = max(hi[a], v);
+                }
+                const bool tgt = T.mask_mode == 0 ||
+                                 (T.mask_mode == 1 ? hash_mask(li, b, n, T.update_prob, T.step_index, T.base_seed)
+                                                   : T.mask[at]) != 0.0f;
+                if (tgt) tgt_bits |= 1u << r;
+            }
         }
     }
 #pragma unroll
@@ -300,18 +326,44 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
             const uint64_t m = __ballot(v);
             peers &= v ? m : ~m;
         }
+        const uint64_t tball = fold ? __ballot(active && ((tgt_bits >> r) & 1u)) : 0ull;
         uint32_t rank = 0;
         if (active) {
             const uint32_t below = (uint32_t)__popcll(peers & lt);
             const uint32_t base = mine[key];
             rank = base + below;
-            if ((peers >> lane) == 1ull) mine[key] = (uint16_t)(base + (uint32_t)__popcll(peers));
+            if ((peers >> lane) == 1ull) {
+                mine[key] = (uint16_t)(base + (uint32_t)__popcll(peers));
+                const uint32_t m = (uint32_t)__popcll(peers & tball);
+                if (m) atomicAdd(&mcnt[key >> 1], m << (16 * (key & 1u)));
+            }
         }
         key_r[r] = key;
         rank_r[r] = rank;
     }
     }
+    if (fold) {  // the tile's coordinate span
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            int l = lo[a], h = hi[a];
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                l = min(l, __shfl_xor(l, off, 64));
+                h = max(h, __shfl_xor(h, off, 64));
+            }
+            if (lane == 0) {
+                span_red[a][w] = l;
+                span_red[3 + a][w] = h;
+            }
+        }
+    }
     __syncthreads();
+    if (fold && threadIdx.x < 6) {
+        const bool is_lo = threadIdx.x < 3;
+        int v = is_lo ? INT32_MAX : INT32_MIN;
+        for (uint32_t w2 = 0; w2 < blockDim.x / 64; ++w2) v = is_lo ? min(v, span_red[threadIdx.x][w2]) : max(v, span_red[threadIdx.x][w2]);
+        tile_span[(uint64_t)tile * 8 + threadIdx.x] = v;
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t li = wave_start + r * 64 + lane;
@@ -326,6 +378,8 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
     for (uint32_t k = threadIdx.x; k < C; k += blockDim.x) {
         uint32_t tot = 0;
         for (uint32_t w2 = 0; w2 < waves; ++w2) tot += cnt[w2 * C + k];
+        // folded: the tile's targets of the key in the high half (a tile holds at most 32,768)
+        if (fold) tot |= ((mcnt[k >> 1] >> (16 * (k & 1u))) & 0xffffu) << 16;
         row[k] = tot;
     }
     if (ovf) atomicOr(flags, 1u);
@@ -441,6 +495,185 @@ __global__ __launch_bounds__(256) void k_table_offsets_scan(uint32_t* __restrict
     if (k < C) bin_offsets[(uint64_t)b * C + k] = b * n + prefix + wpre + x - run;
     if (b == batch - 1 && bx == gridDim.x - 1 && threadIdx.x == 0)
         bin_offsets[(uint64_t)batch * C] = b * n + prefix + btotal;
+}
+
+// The column scan of a folded table (count in the low half, the tile's update-mask targets in the
+// high half): per-tile count bases written back as full words; returns the count total and sets
+// *masked to the key's targets.
+__device__ __forceinline__ uint32_t column_scan_fold(uint32_t* __restrict__ col, uint32_t C, uint32_t tiles,
+                                                     uint32_t* masked) {
+    uint32_t run = 0, mrun = 0, t = 0;
+    for (; t + 32 <= tiles; t += 32) {
+        uint32_t v[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) v[u] = col[(uint64_t)(t + u) * C];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) {
+            col[(uint64_t)(t + u) * C] = run;
+            run += v[u] & 0xffffu;
+            mrun += v[u] >> 16;
+        }
+    }
+    for (; t + 8 <= tiles; t += 8) {
+        uint32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = col[(uint64_t)(t + u) * C];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            col[(uint64_t)(t + u) * C] = run;
+            run += v[u] & 0xffffu;
+            mrun += v[u] >> 16;
+        }
+    }
+    for (; t < tiles; ++t) {
+        const uint32_t v = col[(uint64_t)t * C];
+        col[(uint64_t)t * C] = run;
+        run += v & 0xffffu;
+        mrun += v >> 16;
+    }
+    *masked = mrun;
+    return run;
+}
+
+// The folded build's scan (one system): k_table_offsets_scan's column scan and offsets scan, and
+// with them what the split would emit per bin - the first work item of each key (ceil(count / tpi)
+// items of <= tpi slots, the split's items for a bin of one cell or an unsplit bin; item_base) and
+// its first compact row (row_next, the scatter's per-key row counter), the totals (wl_count[0] and
+// [1]) and the directory sizes: one run per occupied bin, or kDirGroups + 1 (unsplit, walked in the
+// reference order with the cell filter) for every bin when the system's cell coordinates span the
+// grid on some axis (then coordinate bins may hold several cells). Blocks take their position
+// from a ticket and publish two status words (count; items | rows << 31) for the look-back, as in
+// k_table_offsets_scan.
+__global__ __launch_bounds__(256) void k_table_offsets_fold(uint32_t* __restrict__ table,
+                                                            uint32_t* __restrict__ bin_offsets,
+                                                            unsigned long long* __restrict__ status, uint32_t C,
+                                                            uint32_t tiles, uint32_t n, uint32_t tpi_log2, GridParams g,
+                                                            const int* __restrict__ tile_span,
+                                                            uint32_t* __restrict__ item_base,
+                                                            uint32_t* __restrict__ row_next,
+                                                            uint32_t* __restrict__ dir_n,
+                                                            uint32_t* __restrict__ wl_count) {
+    __shared__ uint32_t wsum[3][4];
+    __shared__ int span[6][4];
+    __shared__ uint32_t s_pa, s_pb, s_pm, s_ticket;
+    const uint32_t nb = gridDim.x;
+    if (threadIdx.x == 0) s_ticket = (uint32_t)atomicAdd(status + 2ull * nb, 1ull);
+    __syncthreads();
+    const uint32_t bx = s_ticket;
+    const uint32_t k = bx * 256 + threadIdx.x;
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    uint32_t run = 0, msk = 0;
+    if (k < C) run = column_scan_fold(table + k, C, tiles, &msk);
+    const uint32_t itm = (run + (1u << tpi_log2) - 1) >> tpi_log2;
+    // the system's cell coordinate span (Particle mode)
+    int lo[3] = {INT32_MAX, INT32_MAX, INT32_MAX}, hi[3] = {INT32_MIN, INT32_MIN, INT32_MIN};
+    if (g.mode == 1)
+        for (uint32_t t = threadIdx.x; t < tiles; t += 256)
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                lo[a] = min(lo[a], tile_span[(uint64_t)t * 8 + a]);
+                hi[a] = max(hi[a], tile_span[(uint64_t)t * 8 + 3 + a]);
+            }
+    uint32_t xa = run, xb = itm, xm = msk;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t ya = __shfl_up(xa, off, 64), yb = __shfl_up(xb, off, 64), ym = __shfl_up(xm, off, 64);
+        if (lane >= (uint32_t)off) {
+            xa += ya;
+            xb += yb;
+            xm += ym;
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            lo[a] = min(lo[a], __shfl_xor(lo[a], off, 64));
+            hi[a] = max(hi[a], __shfl_xor(hi[a], off, 64));
+        }
+    if (lane == 63) {
+        wsum[0][w] = xa;
+        wsum[1][w] = xb;
+        wsum[2][w] = xm;
+    }
+    if (lane == 0)
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            span[a][w] = lo[a];
+            span[3 + a][w] = hi[a];
+        }
+    __syncthreads();
+    uint32_t pa = 0, pb = 0, pm = 0, ta = 0, tb = 0, tm = 0;
+#pragma unroll
+    for (uint32_t v = 0; v < 4; ++v) {
+        if (v < w) {
+            pa += wsum[0][v];
+            pb += wsum[1][v];
+            pm += wsum[2][v];
+        }
+        ta += wsum[0][v];
+        tb += wsum[1][v];
+        tm += wsum[2][v];
+    }
+    bool alias = false;
+    if (g.mode == 1) {
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            int l = INT32_MAX, h = INT32_MIN;
+#pragma unroll
+            for (uint32_t v = 0; v < 4; ++v) {
+                l = min(l, span[a][v]);
+                h = max(h, span[3 + a][v]);
+            }
+            if (a < g.dim && h >= l && (int64_t)h - (int64_t)l >= (int64_t)g.size[a]) alias = true;
+        }
+    }
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(status + bx, (1ull << 63) | ta, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(status + nb + bx, (1ull << 63) | tb | ((unsigned long long)tm << 31), __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (w == 0) {  // the earlier blocks' totals, 64 at a time (they took smaller tickets: running)
+        uint32_t acc_a = 0, acc_b = 0, acc_m = 0;
+        for (uint32_t base = 0; base < bx; base += 64) {
+            const uint32_t j = base + lane;
+            if (j < bx) {
+                unsigned long long v, u;
+                do {
+                    v = __hip_atomic_load(status + j, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+                } while (!(v >> 63));
+                do {
+                    u = __hip_atomic_load(status + nb + j, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+                } while (!(u >> 63));
+                acc_a += (uint32_t)v;
+                acc_b += (uint32_t)(u & 0x7fffffffull);
+                acc_m += (uint32_t)((u >> 31) & 0x7fffffffull);
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            acc_a += __shfl_xor(acc_a, off, 64);
+            acc_b += __shfl_xor(acc_b, off, 64);
+            acc_m += __shfl_xor(acc_m, off, 64);
+        }
+        if (lane == 0) {
+            s_pa = acc_a;
+            s_pb = acc_b;
+            s_pm = acc_m;
+        }
+    }
+    __syncthreads();
+    if (k < C) {
+        bin_offsets[k] = s_pa + pa + xa - run;
+        item_base[k] = s_pb + pb + xb - itm;
+        row_next[k] = s_pm + pm + xm - msk;
+        if (g.mode == 1) dir_n[k] = run ? (alias ? kDirGroups + 1 : 1u) : 0u;
+    }
+    if (bx == nb - 1 && threadIdx.x == 0) {
+        bin_offsets[C] = s_pa + ta;
+        wl_count[0] = s_pb + tb;
+        wl_count[1] = s_pm + tm;
+    }
 }
 
 // Exclusive scan of one value per thread over a 1024-thread block.
@@ -621,6 +854,18 @@ __global__ __launch_bounds__(256) void k_scatter(uint32_t n, uint32_t total, uin
     inv[i] = dst_local;
 }
 
+// The folded build's per-particle outputs (item_base null: not folding): the split's compact rows,
+// work items and directory entries, written by the payload scatter.
+struct FoldOut {
+    const uint32_t* item_base = nullptr;  // [C] first work item of each key
+    uint32_t* row_next = nullptr;         // [C] next compact row of each key (atomic)
+    uint2* worklist = nullptr;
+    uint32_t* act_rows = nullptr;
+    uint32_t* row_of = nullptr;
+    int4* dir_e = nullptr;
+    uint32_t tpi_log2 = 0;
+};
+
 // Copies nq (1, 2, 4, 6 or 8) float4s with every load issued before the first store.
 template <int NQ>
 __device__ __forceinline__ void copy_row4_n(float4* __restrict__ dst, const float4* __restrict__ src) {
@@ -688,7 +933,7 @@ __global__ __launch_bounds__(256) void k_scatter_payload(uint32_t n, uint32_t to
                                                          const float* __restrict__ states, uint32_t S, GridParams g,
                                                          float4* __restrict__ srec, int4* __restrict__ scoord,
                                                          float* __restrict__ sstate, SplitTargets T,
-                                                         uint32_t* __restrict__ flags) {
+                                                         uint32_t* __restrict__ flags, FoldOut F) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     // this build's coordinate-overflow flag (set by k_hash_rank) moves into the sticky word
     if (i == 0) {
@@ -704,17 +949,36 @@ __global__ __launch_bounds__(256) void k_scatter_payload(uint32_t n, uint32_t to
     const float4 p4 = pos[i];  // independent of the slot: in flight while the slot is computed
     const uint32_t key = keys[i];
     const uint32_t t = li / tile;
-    const uint32_t dst = bin_offsets[(uint64_t)b * C + key] + table[((uint64_t)b * tiles_per_sys + t) * C + key] + ranks[i];
-    out[dst] = i;
+    const uint32_t beg = bin_offsets[(uint64_t)b * C + key];
+    const uint32_t r_bin = table[((uint64_t)b * tiles_per_sys + t) * C + key] + ranks[i];  // rank in the bin
+    const uint32_t dst = beg + r_bin;
+    if (!F.item_base) out[dst] = i;
     const float p[4] = {p4.x, p4.y, p4.z, p4.w};
     int64_t c64[3];
     bool ovf = false;
     cell_coords(p, g, c64, &ovf);
     const int c[3] = {(int)c64[0], (int)c64[1], (int)c64[2]};
     write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
+    bool tgt = true;
     if (T.mask_mode != 0) {
         const float m = T.mask_mode == 1 ? hash_mask(li, b, n, T.update_prob, T.step_index, T.base_seed) : T.mask[i];
-        if (m == 0.0f) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
+        tgt = m != 0.0f;
+        if (!tgt) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
+    }
+    if (F.item_base) {  // folded build (one system): what the split emits for the particle's bin
+        if (tgt) {
+            const uint32_t row = atomicAdd(F.row_next + key, 1u);
+            F.act_rows[row] = dst;
+            F.row_of[dst] = row;
+        } else {
+            F.row_of[dst] = ~0u;
+        }
+        const uint32_t tpi = 1u << F.tpi_log2;
+        if ((r_bin & (tpi - 1)) == 0) {
+            const uint32_t left = bin_offsets[key + 1] - beg - r_bin;
+            F.worklist[F.item_base[key] + (r_bin >> F.tpi_log2)] = make_uint2(dst, left < tpi ? left : tpi);
+        }
+        if (g.mode == 1 && r_bin == 0) F.dir_e[(uint64_t)key * kDirGroups] = make_int4(c[0], c[1], c[2], (int)dst);
     }
 }
 
@@ -1646,7 +1910,8 @@ static hipError_t launch_rank_r(uint32_t blocks, uint32_t waves, uint32_t lds_by
                                 const float4* pos, const uint32_t* keys_in, const uint32_t* d_count,
                                 uint32_t n, uint32_t* keys, uint32_t* ranks, uint32_t* table,
                                 uint32_t* flags, uint32_t* wl_count, unsigned long long* scan_status,
-                                uint32_t nstatus, hipStream_t stream, Profiler* prof) {
+                                uint32_t nstatus, hipStream_t stream, Profiler* prof, const SplitTargets& T,
+                                int* tile_span) {
     if (lds_bytes > 32768) {
         static LdsLimitFlags limit;
         const hipError_t e = raise_lds_limit((const void*)k_hash_rank<R>, limit);
@@ -1657,7 +1922,7 @@ static hipError_t launch_rank_r(uint32_t blocks, uint32_t waves, uint32_t lds_by
     const uint32_t threads = g.cells >= 4096 ? 1024 : 256;
     return launch_timed(prof, NPA_KERNEL_HASH_RANK, k_hash_rank<R>, dim3(blocks), dim3(threads), lds_bytes, stream,
                         pos, keys_in, d_count, n, tiles_per_sys, waves, g, key_bits, keys, ranks, table, flags,
-                        wl_count, scan_status, nstatus);
+                        wl_count, scan_status, nstatus, T, tile_span);
 }
 
 static hipError_t launch_rank(uint32_t rounds, uint32_t blocks, uint32_t waves, uint32_t lds_bytes,
@@ -1665,10 +1930,12 @@ static hipError_t launch_rank(uint32_t rounds, uint32_t blocks, uint32_t waves, 
                               const float4* pos, const uint32_t* keys_in, const uint32_t* d_count,
                               uint32_t n, uint32_t* keys, uint32_t* ranks, uint32_t* table,
                               uint32_t* flags, uint32_t* wl_count, unsigned long long* scan_status,
-                              uint32_t nstatus, hipStream_t stream, Profiler* prof) {
+                              uint32_t nstatus, hipStream_t stream, Profiler* prof,
+                              const SplitTargets& T = SplitTargets{}, int* tile_span = nullptr) {
 #define NPA_RANK(RR)                                                                             \
     return launch_rank_r<RR>(blocks, waves, lds_bytes, tiles_per_sys, key_bits, g, pos, keys_in, \
-                             d_count, n, keys, ranks, table, flags, wl_count, scan_status, nstatus, stream, prof)
+                             d_count, n, keys, ranks, table, flags, wl_count, scan_status, nstatus, stream, prof, \
+                             T, tile_span)
     switch (rounds) {
         case 1: NPA_RANK(1);
         case 2: NPA_RANK(2);
@@ -1690,13 +1957,45 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
         return launch_sys(g, plan, pos, states, state_dims, batch, n, ws, tg, stream, prof);
     }
     const uint32_t kblocks = (plan.cells + 255) / 256;  // 256-key blocks of the one-pass scan
-    hipError_t e = launch_rank(plan.rounds, batch * plan.tiles_per_sys, plan.waves, plan.lds_bytes,
+    const SplitTargets tg = targets ? *targets : SplitTargets{};
+    // Folded build (one system whose bins are cells or coordinate bins): the rank kernel also counts
+    // each tile's update-mask targets per key (in the table's high half) and the scatter emits what
+    // the split would - its launch is saved
+    const uint32_t fold_lds = ((plan.waves * plan.cells + 1) & ~1u) * 2 + (plan.cells + 1) / 2 * 4;
+    const bool fold = payload && batch == 1 && (g.mode != 1 || g.spatial) && (plan.tpi & (plan.tpi - 1)) == 0 &&
+                      fold_lds + 1024 <= kMaxLdsBytes;
+    hipError_t e = launch_rank(plan.rounds, batch * plan.tiles_per_sys, plan.waves, fold ? fold_lds : plan.lds_bytes,
                                plan.tiles_per_sys, plan.key_bits, g, pos, nullptr, nullptr, n, ws.keys.as<uint32_t>(),
                                ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(), ws.flags.as<uint32_t>(),
                                ws.wl_count.as<uint32_t>(), ws.scan_status.as<unsigned long long>(),
-                               batch * kblocks + 1,  // the status words and the scan's ticket counter
-                               stream, prof);
+                               2 * batch * kblocks + 1,  // the status words and the scan's ticket counter
+                               stream, prof, tg, fold ? ws.tile_span.as<int>() : nullptr);
     if (e != hipSuccess) return e;
+    if (fold) {
+        const uint32_t tpi_log2 = (uint32_t)__builtin_ctz(plan.tpi);
+        e = launch_timed(prof, NPA_KERNEL_TABLE_SCAN, k_table_offsets_fold, dim3(kblocks), dim3(256), 0, stream,
+                         ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(),
+                         ws.scan_status.as<unsigned long long>(), plan.cells, plan.tiles_per_sys, n, tpi_log2, g,
+                         (const int*)ws.tile_span.as<int>(), ws.totals.as<uint32_t>(), ws.bin_list.as<uint32_t>(),
+                         ws.dir_n.as<uint32_t>(), ws.wl_count.as<uint32_t>());
+        if (e != hipSuccess) return e;
+        FoldOut F;
+        F.item_base = ws.totals.as<uint32_t>();
+        F.row_next = ws.bin_list.as<uint32_t>();
+        F.worklist = ws.worklist.as<uint2>();
+        F.act_rows = ws.act_rows.as<uint32_t>();
+        F.row_of = ws.row_of.as<uint32_t>();
+        F.dir_e = ws.dir_e.as<int4>();
+        F.tpi_log2 = tpi_log2;
+        auto scat = g.dim == 2 ? k_scatter_payload<2> : k_scatter_payload<3>;
+        const uint32_t blocks = (uint32_t)((total + 255) / 256);
+        return launch_timed(prof, NPA_KERNEL_SCATTER, scat, dim3(blocks), dim3(256), 0, stream, n, (uint32_t)total,
+                            plan.tile, plan.tiles_per_sys, plan.cells, ws.keys.as<uint32_t>(), ws.ranks.as<uint32_t>(),
+                            ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(),
+                            ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), pos, states, state_dims, g,
+                            ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(), tg,
+                            ws.flags.as<uint32_t>(), F);
+    }
     if (batch >= 8 && plan.cells <= 4096 && plan.tiles_per_sys <= 4) {  // many small systems: a block each
         auto k = plan.cells <= 1024 ? k_table_offsets_sys<1, 4> : k_table_offsets_sys<4, 4>;
         e = launch_timed(prof, NPA_KERNEL_TABLE_SCAN, k, dim3(batch), dim3(1024), 0, stream, ws.table.as<uint32_t>(),
@@ -1708,7 +2007,6 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
     }
     if (e != hipSuccess) return e;
     const uint32_t blocks = (uint32_t)((total + 255) / 256);
-    const SplitTargets tg = targets ? *targets : SplitTargets{};
     if (!payload)
         return launch_timed(prof, NPA_KERNEL_SCATTER, k_scatter, dim3(blocks), dim3(256), 0, stream, n,
                             (uint32_t)total, plan.tile, plan.tiles_per_sys, plan.cells, ws.keys.as<uint32_t>(),
@@ -1719,7 +2017,7 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                      plan.tile, plan.tiles_per_sys, plan.cells, ws.keys.as<uint32_t>(), ws.ranks.as<uint32_t>(),
                      ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>(),
                      ws.perm.as<uint32_t>(), ws.inv.as<uint32_t>(), pos, states, state_dims, g, ws.srec.as<float4>(),
-                     ws.scoord.as<int4>(), ws.sstate.as<float>(), tg, ws.flags.as<uint32_t>());
+                     ws.scoord.as<int4>(), ws.sstate.as<float>(), tg, ws.flags.as<uint32_t>(), FoldOut{});
     if (e != hipSuccess) return e;
     const uint32_t nbins = batch * plan.cells;
     auto split = g.dim == 2 ? k_split<2> : k_split<3>;

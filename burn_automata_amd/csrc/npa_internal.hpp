@@ -113,8 +113,11 @@ struct Workspace {
     // one-pass offsets scan: per (system, 256-key block) the block's published key total
     // (bit 63 = published; zeroed by k_hash_rank at the start of every build)
     DevBuf scan_status;
-    // sparse grids: the bins too large for the one-lane split (count in wl_count[kListedWord])
+    // sparse grids: the bins too large for the one-lane split (count in wl_count[kListedWord]); the
+    // folded build's per-key row counters
     DevBuf bin_list;
+    // the folded build: per rank tile, the cell coordinate span (min x, y, z, max x, y, z, 2 spare)
+    DevBuf tile_span;
     // Targets of the second pass and the update: particles whose update mask is not 0 (the others
     // are written to the output by the update-mask kernel). act_rows: compact row -> slot.
     // Counts (u32 words of wl_count, kWlWords): [0] density items, [1] compact rows (one 64-bit
