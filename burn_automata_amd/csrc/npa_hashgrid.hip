@@ -540,8 +540,8 @@ __device__ __forceinline__ uint32_t column_scan_fold(uint32_t* __restrict__ col,
 // items of <= tpi slots, the split's items for a bin of one cell or an unsplit bin; item_base) and
 // its first compact row (row_next, the scatter's per-key row counter), the totals (wl_count[0] and
 // [1]) and the directory sizes: one run per occupied bin, or kDirGroups + 1 (unsplit, walked in the
-// reference order with the cell filter) for every bin when the system's cell coordinates span the
-// grid on some axis (then coordinate bins may hold several cells). Blocks take their position
+// reference order with the cell filter) for a bin that may hold several cells (the system's cell
+// coordinates reach two cells of the bin's residues). Blocks take their position
 // from a ticket and publish two status words (count; items | rows << 31) for the look-back, as in
 // k_table_offsets_scan.
 __global__ __launch_bounds__(256) void k_table_offsets_fold(uint32_t* __restrict__ table,
@@ -615,8 +615,13 @@ __global__ __launch_bounds__(256) void k_table_offsets_fold(uint32_t* __restrict
         tb += wsum[1][v];
         tm += wsum[2][v];
     }
+    // A coordinate bin (residues r_a = c_a mod size_a) can hold two cells only if on some axis two
+    // coordinates of the system's span [lo, hi] share its residue: first = lo + ((r - lo) mod size)
+    // and first + size <= hi. Such bins are marked unsplit (walked with the cell filter, exact for
+    // any bin); every other occupied bin holds one cell.
     bool alias = false;
-    if (g.mode == 1) {
+    if (g.mode == 1 && k < C) {
+        uint32_t rest = k;
 #pragma unroll
         for (int a = 0; a < 3; ++a) {
             int l = INT32_MAX, h = INT32_MIN;
@@ -625,7 +630,15 @@ __global__ __launch_bounds__(256) void k_table_offsets_fold(uint32_t* __restrict
                 l = min(l, span[a][v]);
                 h = max(h, span[3 + a][v]);
             }
-            if (a < g.dim && h >= l && (int64_t)h - (int64_t)l >= (int64_t)g.size[a]) alias = true;
+            if (a < g.dim) {
+                const int64_t m = (int64_t)g.size[a];
+                const int64_t r = (int64_t)(rest % g.size[a]);
+                rest /= g.size[a];
+                if (h >= l && (int64_t)h - (int64_t)l >= m) {
+                    const int64_t first = (int64_t)l + rem_euclid_i64(r - (int64_t)l, m);
+                    if (first + m <= (int64_t)h) alias = true;
+                }
+            }
         }
     }
     if (threadIdx.x == 0) {
@@ -1515,10 +1528,10 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
 // there, its compact row (act_rows / row_of), the bin's directory entry from its first particle, and
 // the step's output for a particle outside the update mask (hold_particle); block 0 writes the item
 // and row totals and clears the update's item queues.
-// A Particle-mode bin holds one cell unless the system's cell coordinates span the grid on some
-// axis; then every bin of the system is marked unsplit (dir_n = kDirGroups + 1: the neighbour passes
-// walk the whole bin in the reference order and keep the cell's particles), which is exact for any
-// bin. The coordinate-overflow flag goes to the sticky word flags[1] directly.
+// A Particle-mode bin holds one cell unless two coordinates of the system's span share its residues
+// on some axis; such bins are marked unsplit (dir_n = kDirGroups + 1: the neighbour passes walk the
+// whole bin in the reference order and keep the cell's particles), which is exact for any bin. The
+// coordinate-overflow flag goes to the sticky word flags[1] directly.
 constexpr uint32_t kSysThreads = 1024;
 constexpr uint32_t kSysWaves = kSysThreads / 64;
 
@@ -1717,7 +1730,9 @@ __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restri
     const uint32_t pm = w ? (uint32_t)__shfl((int)em, (int)w - 1, 64) : 0u;
     const uint32_t tb = (uint32_t)__shfl((int)eb, (int)kSysWaves - 1, 64);
     const uint32_t tm = (uint32_t)__shfl((int)em, (int)kSysWaves - 1, 64);
-    bool alias = false;
+    // the system's coordinate span per axis: a bin may hold two cells only if two coordinates of the
+    // span share its residue on some axis (see k_table_offsets_fold)
+    int span_lo[3] = {0, 0, 0}, span_hi[3] = {0, 0, 0};
     if (g.mode == 1) {
 #pragma unroll
         for (int a = 0; a < D; ++a) {
@@ -1728,11 +1743,23 @@ __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restri
                 l = min(l, __shfl_xor(l, off, 64));
                 h = max(h, __shfl_xor(h, off, 64));
             }
-            l = __shfl(l, 0, 64);
-            h = __shfl(h, 0, 64);
-            if (h >= l && (int64_t)h - (int64_t)l >= (int64_t)g.size[a]) alias = true;
+            span_lo[a] = __shfl(l, 0, 64);
+            span_hi[a] = __shfl(h, 0, 64);
         }
     }
+    auto may_alias = [&](uint32_t k) {
+        bool al = false;
+        uint32_t rest = k;
+#pragma unroll
+        for (int a = 0; a < D; ++a) {
+            const int64_t m = (int64_t)g.size[a];
+            const int64_t r = (int64_t)(rest % g.size[a]);
+            rest /= g.size[a];
+            const int64_t l = span_lo[a], h = span_hi[a];
+            if (h >= l && h - l >= m && l + rem_euclid_i64(r - l, m) + m <= h) al = true;
+        }
+        return al;
+    };
     if (tid == 0) {
         sys_tot[b] = (unsigned long long)tb | ((unsigned long long)tm << 32);
         sstart[C] = (uint16_t)n;
@@ -1748,7 +1775,7 @@ __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restri
                 sstart[k] = (uint16_t)st;
                 bin_offsets[(uint64_t)b * C + k] = b * n + st;
                 sys_item[(uint64_t)b * C + k] = it;
-                if (g.mode == 1) dir_n[(uint64_t)b * C + k] = tot[q] ? (alias ? K + 1 : 1u) : 0u;
+                if (g.mode == 1) dir_n[(uint64_t)b * C + k] = tot[q] ? (may_alias(k) ? K + 1 : 1u) : 0u;
                 rpack |= (uint64_t)rw << (16 * q);
             }
             st += tot[q];

@@ -330,72 +330,6 @@ __global__ __launch_bounds__(256) void k_density_q(StepParams P, const float4* _
     }
 }
 
-// The density pass for sparse 2D grids (fewer than 4 particles per bin on average), one thread per
-// target: the thread walks its 3^D neighbour runs itself (cells dz, dy, dx; slots ascending) and
-// writes exactly what k_density writes - the same sum in the same order, the same chunk records -
-// without spending a wave on a run of one or two targets.
-template <int D>
-__global__ __launch_bounds__(256) void k_density_sparse(StepParams P, const float4* __restrict__ srec,
-                                                        const int4* __restrict__ scoord,
-                                                        const uint32_t* __restrict__ bo,
-                                                        const uint32_t* __restrict__ perm,
-                                                        const uint32_t* __restrict__ row_of,
-                                                        float4* __restrict__ svol, float* __restrict__ density_out,
-                                                        uint32_t* __restrict__ nb_base, uint64_t* __restrict__ nb_mask,
-                                                        uint32_t* __restrict__ nb_count) {
-    constexpr uint32_t MAXC = max_chunks(D);
-    constexpr int ZLO = D == 3 ? -1 : 0, ZHI = D == 3 ? 1 : 0;
-    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= P.T) return;
-    const uint32_t b = s / P.N;
-    const uint32_t row = row_of[s];
-    const bool record = row != ~0u;
-    float pi[3];
-    int ci[3];
-    load_rec<D>(srec, scoord, s, pi, ci);
-    float rho = 0.0f;
-    uint32_t gch = 0;
-    for (int dz = ZLO; dz <= ZHI; ++dz)
-        for (int dy = -1; dy <= 1; ++dy)
-            for (int dx = -1; dx <= 1; ++dx) {
-                const int64_t n0 = (int64_t)ci[0] + dx, n1 = (int64_t)ci[1] + dy, n2 = (int64_t)ci[2] + dz;
-                uint32_t beg, end;
-                bool filter;
-                if (!cell_range(P, bo, b, n0, n1, n2, beg, end, filter)) continue;
-                for (uint32_t base = beg; base < end; base += kChunk, ++gch) {
-                    const uint32_t m = end - base < (uint32_t)kChunk ? end - base : (uint32_t)kChunk;
-                    uint64_t acc = 0;
-                    for (uint32_t k = 0; k < m; ++k) {
-                        float pj[3];
-                        int cj[3];
-                        load_rec<D>(srec, scoord, base + k, pj, cj);
-                        if (filter && ((int64_t)cj[0] != n0 || (int64_t)cj[1] != n1 ||
-                                       (D == 3 && (int64_t)cj[2] != n2)))
-                            continue;
-                        const float d0 = delta_axis(pi[0], pj[0], 0, P.g);
-                        const float d1 = delta_axis(pi[1], pj[1], 1, P.g);
-                        float r2 = d0 * d0;
-                        r2 += d1 * d1;
-                        if constexpr (D == 3) {
-                            const float d2 = delta_axis(pi[2], pj[2], 2, P.g);
-                            r2 += d2 * d2;
-                        }
-                        if (r2 < P.g.eps2) {
-                            rho += poly6(r2, P.g);
-                            acc |= 1ull << k;
-                        }
-                    }
-                    if (record && gch < MAXC) {
-                        nb_base[(uint64_t)row * MAXC + gch] = base;
-                        nb_mask[(uint64_t)row * MAXC + gch] = acc;
-                    }
-                }
-            }
-    svol[s] = make_float4(pi[0], pi[1], pi[2], recip_finite(rho));
-    if (record) nb_count[row] = gch;
-    if (density_out) density_out[b * P.N + perm[s]] = rho;
-}
-
 // The density pass for sparse 2D grids, four lanes per target and sixteen consecutive slots per wave:
 // writes exactly what k_density_q writes (the same sum in the same order, the same chunk records),
 // with the lanes of a target sharing its own neighbour runs instead of a wave sharing one cell's.

@@ -47,7 +47,7 @@
 
 namespace npa {
 
-constexpr int kFuseWaves = 16;          // waves per block (one block per CU) for systems with many items
+constexpr int kFuseWaves = 16;          // waves per block (one block per CU)
 constexpr uint32_t kFuseHidden = 128;   // hidden units held per target (H <= 128, zero padded)
 constexpr uint32_t kFuseLdsBytes = 163840;
 
@@ -243,7 +243,10 @@ __device__ __forceinline__ void for_each_entry(F&& f, std::integer_sequence<int,
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 // ENG: 0 = VALU, the reference's roundings (bit-exact); 1 = the MLP on the fp32 matrix cores.
-template <int D, int FL, int ENG>
+// NW: waves per block (kFuseWaves; small systems with the usual options take blocks of 4 so that
+// their few items spread over every CU; a compile-time count keeps the item arithmetic in the
+// scalar registers the kernel can spare).
+template <int D, int FL, int ENG, int NW>
 __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float4* __restrict__ srec,
                                                        const int4* __restrict__ scoord,
                                                        const float* __restrict__ sstate,
@@ -304,7 +307,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
     // b / 8 * 16 + wave); later ones come from the queue's counter (zeroed with the work-list
     // counters by the hashgrid build) when an item is done, so the XCD's waves share its items to
     // the end, and a wave that the SIMD's oldest-first issue keeps waiting takes fewer of them.
-    const uint32_t nw = blockDim.x >> 6;  // waves per block (kFuseWaves, fewer for small systems)
+    constexpr uint32_t nw = NW;
     const uint32_t nq = gridDim.x % 8 == 0 ? 8u : 1u;
     const uint32_t xq = blockIdx.x % nq;
     const uint32_t per_round = gridDim.x / nq * nw;
@@ -896,25 +899,21 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
     }
 }
 
-template <int D, int FL, int ENG>
+template <int D, int FL, int ENG, int NW>
 static hipError_t launch_fused_t(const StepParams& p, Workspace& ws, const StepIO& io, const float* wfused,
                                  hipStream_t stream, Profiler* prof) {
     using Sh = FuseShape<D, FL>;
-    // one block per CU at most; never more waves than items of four targets: a system with fewer
-    // items than 16 per CU takes blocks of fewer waves (a power of two), so its items spread over
-    // every CU instead of queueing on a few
+    // one block per CU at most; never more waves than items of four targets
     const uint64_t max_items = ((uint64_t)p.T + 3) / 4;
     const uint64_t cus = (uint64_t)device_cu_count();
-    uint32_t nw = 1;
-    while (nw < (uint32_t)kFuseWaves && (uint64_t)nw * cus < max_items) nw *= 2;
-    const size_t lds = (fused_weight_floats(p.FP, D) + (size_t)nw * Sh::WAVE_FLOATS) * 4;
+    const size_t lds = (fused_weight_floats(p.FP, D) + (size_t)NW * Sh::WAVE_FLOATS) * 4;
     if (lds > kFuseLdsBytes) return hipErrorInvalidValue;
     static LdsLimitFlags limit;
-    const hipError_t e = raise_lds_limit((const void*)k_update_fused<D, FL, ENG>, limit);
+    const hipError_t e = raise_lds_limit((const void*)k_update_fused<D, FL, ENG, NW>, limit);
     if (e != hipSuccess) return e;
-    const uint32_t blocks = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(cus, (max_items + nw - 1) / nw));
+    const uint32_t blocks = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(cus, (max_items + NW - 1) / NW));
     uint32_t* wl = ws.wl_count.as<uint32_t>();
-    return launch_timed(prof, NPA_KERNEL_UPDATE, k_update_fused<D, FL, ENG>, dim3(blocks), dim3(64 * nw),
+    return launch_timed(prof, NPA_KERNEL_UPDATE, k_update_fused<D, FL, ENG, NW>, dim3(blocks), dim3(64 * NW),
                         (uint32_t)lds, stream, p, ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.sstate.as<float>(),
                         ws.svol.as<float4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
                         ws.act_rows.as<uint32_t>(), wl, ws.nb_base.as<uint32_t>(),
@@ -927,13 +926,20 @@ static hipError_t launch_fused_d(const StepParams& p, Workspace& ws, const StepI
     // the usual option set (flags 5), clamped or periodic (flag 8), or every option read at run time
     const bool common = p.state_grad && p.hybrid && !p.density_grad;
     const bool per = p.g.boundary == 0;
+    constexpr int W = kFuseWaves;
     if (p.mlp_engine == NPA_MLP_MFMA)
-        return !common ? launch_fused_t<D, -1, 1>(p, ws, io, wfused, stream, prof)
-               : per   ? launch_fused_t<D, 13, 1>(p, ws, io, wfused, stream, prof)
-                       : launch_fused_t<D, 5, 1>(p, ws, io, wfused, stream, prof);
-    return !common ? launch_fused_t<D, -1, 0>(p, ws, io, wfused, stream, prof)
-           : per   ? launch_fused_t<D, 13, 0>(p, ws, io, wfused, stream, prof)
-                   : launch_fused_t<D, 5, 0>(p, ws, io, wfused, stream, prof);
+        return !common ? launch_fused_t<D, -1, 1, W>(p, ws, io, wfused, stream, prof)
+               : per   ? launch_fused_t<D, 13, 1, W>(p, ws, io, wfused, stream, prof)
+                       : launch_fused_t<D, 5, 1, W>(p, ws, io, wfused, stream, prof);
+    // a system with at most four items per CU (C1: 4,096 particles): blocks of four waves, so that
+    // its items spread over every CU instead of queueing on a few
+    const bool small = ((uint64_t)p.T + 3) / 4 <= 4ull * (uint64_t)device_cu_count();
+    if (common && small)
+        return per ? launch_fused_t<D, 13, 0, 4>(p, ws, io, wfused, stream, prof)
+                   : launch_fused_t<D, 5, 0, 4>(p, ws, io, wfused, stream, prof);
+    return !common ? launch_fused_t<D, -1, 0, W>(p, ws, io, wfused, stream, prof)
+           : per   ? launch_fused_t<D, 13, 0, W>(p, ws, io, wfused, stream, prof)
+                   : launch_fused_t<D, 5, 0, W>(p, ws, io, wfused, stream, prof);
 }
 
 #if NPA_PART_DIM2
