@@ -1988,10 +1988,22 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
     // Folded build (one system whose bins are cells or coordinate bins): the rank kernel also counts
     // each tile's update-mask targets per key (in the table's high half) and the scatter emits what
     // the split would - its launch is saved
-    const uint32_t fold_lds = ((plan.waves * plan.cells + 1) & ~1u) * 2 + (plan.cells + 1) / 2 * 4;
+    // (its target counters take C u16 of LDS beside the rank counters: where both do not fit, fewer
+    // waves rank the same tile in more rounds)
+    uint32_t rank_waves = plan.waves, rank_rounds = plan.rounds;
+    auto fold_lds_of = [&](uint32_t wv) { return ((wv * plan.cells + 1) & ~1u) * 2 + (plan.cells + 1) / 2 * 4; };
+    while (fold_lds_of(rank_waves) + 1024 > kMaxLdsBytes && rank_waves > 1 && rank_rounds < 32) {
+        rank_waves /= 2;
+        rank_rounds *= 2;
+    }
+    const uint32_t fold_lds = fold_lds_of(rank_waves);
     const bool fold = payload && batch == 1 && (g.mode != 1 || g.spatial) && (plan.tpi & (plan.tpi - 1)) == 0 &&
                       fold_lds + 1024 <= kMaxLdsBytes;
-    hipError_t e = launch_rank(plan.rounds, batch * plan.tiles_per_sys, plan.waves, fold ? fold_lds : plan.lds_bytes,
+    if (!fold) {
+        rank_waves = plan.waves;
+        rank_rounds = plan.rounds;
+    }
+    hipError_t e = launch_rank(rank_rounds, batch * plan.tiles_per_sys, rank_waves, fold ? fold_lds : plan.lds_bytes,
                                plan.tiles_per_sys, plan.key_bits, g, pos, nullptr, nullptr, n, ws.keys.as<uint32_t>(),
                                ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(), ws.flags.as<uint32_t>(),
                                ws.wl_count.as<uint32_t>(), ws.scan_status.as<unsigned long long>(),

@@ -503,6 +503,170 @@ __global__ __launch_bounds__(256) void k_density_lanes(StepParams P, const float
     }
 }
 
+// The same pass for sparse 3D grids (a surface in a 32^3 grid, say: a few particles per occupied
+// cell), four lanes per target and sixteen consecutive slots per wave. A target's 27 neighbour runs
+// go to a table in LDS (lane q looks up cells q, q + 4, ..., visit order k = (dz + 1) * 9 + (dy + 1)
+// * 3 + (dx + 1)); the quad's first lane forms the runs' stream offsets, slot offsets and chunk
+// numbers; in round r lane q tests stream position 4 r + q, finding its run by advancing through
+// the table (positions only grow). Sums, the accept stream and the chunk records as in the 2D pass.
+constexpr uint32_t kStreamWords3 = 48 * 64 / 32;  // max_chunks(3) chunks of 64 candidates
+
+#if NPA_PART_MAIN
+__global__ __launch_bounds__(256) void k_density_lanes3(StepParams P, const float4* __restrict__ srec,
+                                                        const int4* __restrict__ scoord,
+                                                        const uint32_t* __restrict__ bo,
+                                                        const uint32_t* __restrict__ perm,
+                                                        const uint32_t* __restrict__ row_of,
+                                                        float4* __restrict__ svol, float* __restrict__ density_out,
+                                                        uint32_t* __restrict__ nb_base, uint64_t* __restrict__ nb_mask,
+                                                        uint32_t* __restrict__ nb_count) {
+    constexpr int D = 3;
+    constexpr uint32_t MAXC = max_chunks(D);
+    static_assert(MAXC * 64 == kStreamWords3 * 32, "the stream holds every recorded chunk");
+    struct Runs {
+        uint32_t pre[28];  // stream position of run k's first candidate; pre[27] = the total
+        uint32_t beg[27];  // run k's first slot
+        uint32_t gch[28];  // run k's first chunk number; gch[27] = the chunk count
+        uint32_t filt;     // runs of unsplit bins (cell filter)
+    };
+    __shared__ Runs runs_lds[4][16];
+    __shared__ uint32_t stream_lds[4][16][kStreamWords3 + 1];
+    const uint32_t lane = threadIdx.x & 63, t = lane >> 2, q = lane & 3;
+    const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    Runs& R = runs_lds[threadIdx.x >> 6][t];
+    uint32_t* stream = stream_lds[threadIdx.x >> 6][t];
+    const uint32_t s_raw = wave * 16 + t;
+    if (wave * 16 >= P.T) return;  // (wave-uniform)
+    const bool active = s_raw < P.T;
+    const uint32_t s = active ? s_raw : P.T - 1;
+    const uint32_t b = s / P.N;
+    float pi[3];
+    int ci[3];
+    load_rec<D>(srec, scoord, s, pi, ci);
+    const uint32_t row = active ? row_of[s] : ~0u;
+    const bool record = row != ~0u;
+    // ---- lookup: lane q, cells q, q + 4, ... (lengths to pre[], starts to beg[], filters by bit)
+    uint32_t fbits = 0;
+    for (uint32_t k = q; k < 27; k += 4) {
+        uint32_t beg = 0, end = 0;
+        bool filt = false;
+        if (active && !cell_range(P, bo, b, (int64_t)ci[0] + (int)(k % 3) - 1, (int64_t)ci[1] + (int)((k / 3) % 3) - 1,
+                                  (int64_t)ci[2] + (int)(k / 9) - 1, beg, end, filt)) {
+            beg = end = 0;
+            filt = false;
+        }
+        R.pre[k] = end - beg;
+        R.beg[k] = beg;
+        fbits |= (filt ? 1u : 0u) << k;
+    }
+    fbits |= (uint32_t)group_bcast_k<4>((int)fbits, 1) | (uint32_t)group_bcast_k<4>((int)fbits, 2) |
+             (uint32_t)group_bcast_k<4>((int)fbits, 3) | (uint32_t)group_bcast_k<4>((int)fbits, 0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (q == 0) {  // lengths -> stream offsets and chunk numbers
+        uint32_t run = 0, ch = 0;
+        for (int k = 0; k < 27; ++k) {
+            const uint32_t len = R.pre[k];
+            R.pre[k] = run;
+            R.gch[k] = ch;
+            run += len;
+            ch += (len + 63) / 64;
+        }
+        R.pre[27] = run;
+        R.gch[27] = ch;
+        R.filt = fbits;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t total = R.pre[27];
+    uint32_t rounds = (total + 3) / 4;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) rounds = max(rounds, (uint32_t)__shfl_xor((int)rounds, off, 64));
+    const bool any_filter = __ballot(fbits != 0) != 0ull;
+    const float eps2 = P.g.eps2, k6 = P.g.k6;
+    const bool periodic = P.g.boundary == 0;
+    float rho = 0.0f;
+    uint32_t word = 0;
+    uint32_t kk = 0, knext = R.pre[1];  // the run of this lane's stream position, and where the next starts
+    for (uint32_t r0 = 0; r0 < rounds; r0 += 4) {
+        float4 rc[4];
+        int4 cc[4];
+        bool ok[4];
+        uint32_t kr[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t j = 4 * (r0 + u) + q;
+            ok[u] = active && j < total;
+            if (ok[u])
+                while (j >= knext) {  // advance to the run holding position j (empty runs skipped)
+                    ++kk;
+                    knext = R.pre[kk + 1];
+                }
+            const uint32_t slot = ok[u] ? R.beg[kk] + (j - R.pre[kk]) : s;
+            kr[u] = kk;
+            rc[u] = srec[slot];
+            cc[u] = any_filter ? scoord[slot] : make_int4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (r0 + u >= rounds) break;
+            bool acc_ok = ok[u];
+            if (any_filter && ((fbits >> kr[u]) & 1u)) {  // an unsplit bin: keep this cell's particles
+                const int k = (int)kr[u];
+                acc_ok = acc_ok && (int64_t)cc[u].x == (int64_t)ci[0] + k % 3 - 1 &&
+                         (int64_t)cc[u].y == (int64_t)ci[1] + (k / 3) % 3 - 1 && (int64_t)cc[u].z == (int64_t)ci[2] + k / 9 - 1;
+            }
+            float d0 = rc[u].x - pi[0], d1 = rc[u].y - pi[1], d2 = rc[u].z - pi[2];
+            if (periodic) {
+                d0 = delta_axis(pi[0], rc[u].x, 0, P.g);
+                d1 = delta_axis(pi[1], rc[u].y, 1, P.g);
+                d2 = delta_axis(pi[2], rc[u].z, 2, P.g);
+            }
+            float r2 = d0 * d0;
+            r2 += d1 * d1;
+            r2 += d2 * d2;
+            const bool near = acc_ok && r2 < eps2;
+            const float x = eps2 - r2;
+            rho = ordered_group_sum<4>(rho, near ? k6 * x * x * x : 0.0f);  // smoothing_poly6_kernel
+            const uint64_t bal = __builtin_amdgcn_ballot_w64(near);
+            const uint32_t r = r0 + u;
+            word |= ((uint32_t)(bal >> (lane & ~3u)) & 0xfu) << (4 * (r & 7u));
+            if ((r & 7u) == 7u || r + 1 == rounds) {
+                if (q == 0 && r / 8 < kStreamWords3) stream[r / 8] = word;
+                word = 0;
+            }
+        }
+    }
+    if (active && q == 0) {
+        svol[s] = make_float4(pi[0], pi[1], pi[2], recip_finite(rho));
+        if (density_out) density_out[b * P.N + perm[s]] = rho;
+    }
+    if (!__ballot(record)) return;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (!record) return;
+    if (q == 0) nb_count[row] = R.gch[27];
+    const uint32_t used = min((total + 31) / 32, kStreamWords3);
+    for (uint32_t k = q; k < 27; k += 4) {
+        const uint32_t len = R.pre[k + 1] - R.pre[k], g0 = R.gch[k];
+        for (uint32_t c = 0; 64 * c < len && g0 + c < MAXC; ++c) {
+            const uint32_t a = R.pre[k] + 64 * c;  // stream bit of the chunk's first candidate
+            const uint32_t L = min(64u, len - 64 * c);
+            const uint32_t w0 = a / 32, sh = a % 32;
+            const uint64_t lo = (uint64_t)(w0 < used ? stream[w0] : 0u) | ((uint64_t)(w0 + 1 < used ? stream[w0 + 1] : 0u) << 32);
+            const uint64_t hi = w0 + 2 < used ? stream[w0 + 2] : 0u;
+            uint64_t m = sh ? (lo >> sh) | (hi << (64 - sh)) : lo;
+            if (L < 64) m &= (1ull << L) - 1ull;
+            nb_base[(uint64_t)row * MAXC + g0 + c] = R.beg[k] + 64 * c;
+            nb_mask[(uint64_t)row * MAXC + g0 + c] = m;
+        }
+    }
+}
+#endif  // NPA_PART_MAIN
+
 // Per-wave accepted-neighbour lists of the second pass: the sorted slots of each target's accepted
 // candidates, appended in visit order (cells dz, dy, dx; slots ascending), so walking a list front
 // to back is the reference's neighbour order. kListBytes of LDS per wave for any targets-per-item.
@@ -1463,6 +1627,13 @@ hipError_t launch_density(const StepParams& p_in, Workspace& ws, float* density_
                             p, ws.srec.as<float4>(), ws.bin_offsets.as<uint32_t>(), ws.perm.as<uint32_t>(),
                             ws.row_of.as<uint32_t>(), ws.svol.as<float4>(), density_out, ws.nb_base.as<uint32_t>(),
                             ws.nb_mask.as<uint64_t>(), ws.nb_count.as<uint32_t>());
+    }
+    if (p.g.dim == 3 && (uint64_t)p.B * p.g.cells > p.T) {  // sparse 3D (more cells than particles)
+        const uint32_t waves = (p.T + 15) / 16;
+        return launch_timed(prof, NPA_KERNEL_DENSITY, k_density_lanes3, dim3((waves + 3) / 4), dim3(256), 0, stream,
+                            p, ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(),
+                            ws.perm.as<uint32_t>(), ws.row_of.as<uint32_t>(), ws.svol.as<float4>(), density_out,
+                            ws.nb_base.as<uint32_t>(), ws.nb_mask.as<uint64_t>(), ws.nb_count.as<uint32_t>());
     }
     auto k = p.g.dim == 2 ? k_density_q<2> : k_density_q<3>;  // four waves per block, a wave per item
     return launch_timed(prof, NPA_KERNEL_DENSITY, k, dim3(grid_blocks), dim3(256), 0, stream, p, ws.srec.as<float4>(),

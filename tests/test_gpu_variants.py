@@ -39,11 +39,23 @@ GRIDS = {
     "grid3_clamped": (HashGridConfig(3, C, GRID, (10, 9, 8), 0.1), 3000, 0.6),
     "particle2_periodic": (HashGridConfig(2, P, PART, (16, 16, 1), 0.05), 3000, 0.45),
     "grid2_periodic_small": (HashGridConfig(2, P, GRID, (6, 5, 1), 0.1), 1500, 0.4),
+    # strips longer than the grid along x (radius < 0: half length 2, half width 0.3): coordinate bins
+    # hold two cells there, so the sort marks those bins unsplit and the passes filter by cell; sparse
+    # grids (more cells than particles) take the small-system build and the four-lane density passes
+    "particle2_strip_sparse": (HashGridConfig(2, C, PART, (64, 64, 1), 0.05), 3000, -1.0),
+    "particle3_strip_sparse": (HashGridConfig(3, C, PART, (32, 32, 32), 0.1), 3000, -1.0),
+    "particle2_strip_dense": (HashGridConfig(2, C, PART, (16, 16, 1), 0.05), 6000, -1.0),
 }
 
 
 def _cloud(name, seed=3):
     g, n, radius = GRIDS[name]
+    if radius < 0:  # a strip: x in [-2, 2), the other axes in [-0.3, 0.3)
+        rng = np.random.default_rng(seed)
+        pos = np.zeros((n, 4), np.float32)
+        pos[:, 0] = rng.uniform(-2.0, 2.0, n)
+        pos[:, 1:g.dim] = rng.uniform(-0.3, 0.3, (n, g.dim - 1))
+        return pos, n, g
     pos = syn.uniform_ball(n, seed, radius) if g.dim == 3 else syn.uniform_disk(n, seed, radius)
     return pos, n, g
 
@@ -111,7 +123,8 @@ def test_euler_step_bit_exact(ctx, name):
 
 
 STEP_CASES = [(name, dg) for name in ("grid3_periodic", "particle3_periodic", "grid3_clamped",
-                                      "particle2_periodic", "grid2_periodic_small") for dg in (False, True)]
+                                      "particle2_periodic", "grid2_periodic_small", "particle2_strip_sparse",
+                                      "particle3_strip_sparse", "particle2_strip_dense") for dg in (False, True)]
 
 
 def _step_case(name, density_grad):
