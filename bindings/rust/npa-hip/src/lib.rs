@@ -1,5 +1,8 @@
-//! Safe wrapper over `npa-hip-sys` with the shapes of the reference's operator surface: a host-slice
-//! context for `build_hashgrid` (crates/burn_automata_kernels/src/hashgrid.rs:16-69) and
+//! Safe wrapper over `npa-hip-sys` with the shapes of the reference's operator surface (the
+//! `burn_automata_kernels` exports, crates/burn_automata_kernels/src/lib.rs:40-66): a host-slice
+//! context for `build_hashgrid` (crates/burn_automata_kernels/src/hashgrid.rs:16-69),
+//! `perceive_with_options` (reference/forward.rs:26-143), `euler_step` (reference/step.rs:4-55),
+//! `decode_gaussians_3d` (gaussian.rs:53-100), `splat_particles_2d` (splat.rs:30-93) and
 //! `NpaModel::step_cpu` (crates/burn_automata/src/model.rs:768-858), and a device-resident rollout
 //! state for the GPU executor (`create_state*` / `step_state_many` / `read_state` /
 //! `update_state_model`, crates/burn_automata/src/gpu/executor/). Status codes map onto the
@@ -80,6 +83,29 @@ pub struct HashGridSnapshot {
     pub inverse_permutation: Vec<usize>,
 }
 
+/// `PerceptionOutput` (reference/types.rs:33-41): features [B*N][F], density [B*N], blurred state
+/// [B*N][S], state gradient [B*N][S*d] (empty without the state gradient), density gradient [B*N][d]
+/// (empty without the density gradient).
+#[derive(Clone, Debug)]
+pub struct PerceptionOutput {
+    pub features: Vec<f32>,
+    pub density: Vec<f32>,
+    pub blurred_state: Vec<f32>,
+    pub state_gradient: Vec<f32>,
+    pub density_gradient: Vec<f32>,
+    pub feature_dims: usize,
+}
+
+/// `Gaussian3d` (gaussian.rs:5-11): one decoded Gaussian with (sh_degree + 1)^2 coefficient triples
+/// in oriented mode and one otherwise.
+#[derive(Clone, Debug, PartialEq)]
+pub struct Gaussian3d {
+    pub position_visibility: [f32; 4],
+    pub spherical_harmonic: Vec<[f32; 3]>,
+    pub rotation: [f32; 4],
+    pub scale_opacity: [f32; 4],
+}
+
 /// One step's outputs (`StepOutput`): next positions [B*N][4], next states [B*N][S], density [B*N].
 #[derive(Clone, Debug)]
 pub struct StepOutput {
@@ -150,6 +176,98 @@ impl Context {
         let widen = |v: Vec<u32>| v.into_iter().map(|x| x as usize).collect::<Vec<_>>();
         Ok(HashGridSnapshot { batch_size, particle_count, cell_count: cells, bin_offsets: widen(offsets),
                               permutation: widen(perm), inverse_permutation: widen(inv) })
+    }
+
+    /// `perceive_with_options` (reference/forward.rs:26-143): density, blurred state, moment-corrected
+    /// and normalised gradients and the feature rows of every particle.
+    #[allow(clippy::too_many_arguments)]
+    pub fn perceive_with_options(&self, positions: &[[f32; 4]], states: &[f32], batch_size: usize,
+                                 particle_count: usize, state_dims: usize, cfg: &sys::npa_grid_cfg,
+                                 options: &sys::npa_perception_opts) -> Result<PerceptionOutput> {
+        let total = batch_size * particle_count;
+        let d = cfg.dim as usize;
+        let feature_dims = state_dims * 2 + if options.state_grad != 0 { state_dims * d } else { 0 }
+            + if options.density_grad != 0 { d } else { 0 } + if options.position_features != 0 { d } else { 0 };
+        let mut out = PerceptionOutput {
+            features: vec![0.0; total * feature_dims],
+            density: vec![0.0; total],
+            blurred_state: vec![0.0; total * state_dims],
+            state_gradient: if options.state_grad != 0 { vec![0.0; total * state_dims * d] } else { Vec::new() },
+            density_gradient: if options.density_grad != 0 { vec![0.0; total * d] } else { Vec::new() },
+            feature_dims,
+        };
+        let mut f = 0u32;
+        let sg = if out.state_gradient.is_empty() { ptr::null_mut() } else { out.state_gradient.as_mut_ptr() };
+        let dg = if out.density_gradient.is_empty() { ptr::null_mut() } else { out.density_gradient.as_mut_ptr() };
+        self.check(unsafe {
+            sys::npa_perceive(self.raw, positions.as_ptr() as *const f32, states.as_ptr(), batch_size as u32,
+                              particle_count as u32, state_dims as u32, cfg, options, out.features.as_mut_ptr(),
+                              out.features.len(), out.density.as_mut_ptr(), out.blurred_state.as_mut_ptr(), sg, dg,
+                              &mut f)
+        })?;
+        out.feature_dims = f as usize;
+        Ok(out)
+    }
+
+    /// `euler_step` (reference/step.rs:4-55): positions += dt dx m over the spatial memory axes
+    /// (wrapped on periodic grids), states += dt ds m (3D opacity logits clamped); returns the new
+    /// positions and states.
+    #[allow(clippy::too_many_arguments)]
+    pub fn euler_step(&self, positions: &[[f32; 4]], states: &[f32], dx: &[[f32; 4]], ds: &[f32],
+                      batch_size: usize, particle_count: usize, state_dims: usize, cfg: &sys::npa_grid_cfg,
+                      dt: f32, update_mask: Option<&[f32]>) -> Result<(Vec<[f32; 4]>, Vec<f32>)> {
+        let total = batch_size * particle_count;
+        let mut next_positions = vec![[0.0f32; 4]; total];
+        let mut next_states = vec![0.0f32; total * state_dims];
+        self.check(unsafe {
+            sys::npa_euler_step(self.raw, positions.as_ptr() as *const f32, states.as_ptr(),
+                                dx.as_ptr() as *const f32, ds.as_ptr(), batch_size as u32, particle_count as u32,
+                                state_dims as u32, cfg, dt, update_mask.map_or(ptr::null(), |m| m.as_ptr()),
+                                next_positions.as_mut_ptr() as *mut f32, next_states.as_mut_ptr())
+        })?;
+        Ok((next_positions, next_states))
+    }
+
+    /// `decode_gaussians_3d` (gaussian.rs:53-100). The reference asserts its layout checks; here a
+    /// state width too small for the mode is an `InvalidArgument` error.
+    pub fn decode_gaussians_3d(&self, positions: &[[f32; 4]], states: &[f32], state_dims: usize,
+                               cfg: &sys::npa_gaussian_decode_cfg) -> Result<Vec<Gaussian3d>> {
+        let n = positions.len();
+        let k = if cfg.mode == sys::NPA_DECODE_SH0_ORIENTED {
+            ((cfg.sh_degree + 1) * (cfg.sh_degree + 1)) as usize
+        } else {
+            1
+        };
+        let mut pv = vec![[0.0f32; 4]; n];
+        let mut sh = vec![[0.0f32; 3]; n * k];
+        let mut rot = vec![[0.0f32; 4]; n];
+        let mut so = vec![[0.0f32; 4]; n];
+        self.check(unsafe {
+            sys::npa_decode_gaussians_3d(self.raw, positions.as_ptr() as *const f32, states.as_ptr(), n as u32,
+                                         state_dims as u32, cfg, pv.as_mut_ptr() as *mut f32,
+                                         sh.as_mut_ptr() as *mut f32, rot.as_mut_ptr() as *mut f32,
+                                         so.as_mut_ptr() as *mut f32)
+        })?;
+        Ok((0..n)
+            .map(|i| Gaussian3d { position_visibility: pv[i], spherical_harmonic: sh[i * k..(i + 1) * k].to_vec(),
+                                  rotation: rot[i], scale_opacity: so[i] })
+            .collect())
+    }
+
+    /// `splat_particles_2d` (splat.rs:30-93): the additive RGBA image [size * size][4].
+    pub fn splat_particles_2d(&self, positions: &[[f32; 4]], colors: &[[f32; 3]], cfg: &sys::npa_splat2d_cfg)
+                              -> Result<Vec<[f32; 4]>> {
+        if positions.len() != colors.len() {
+            return Err(Error { kind: NpaError::InvalidArgument,
+                               message: format!("{} positions but {} colors", positions.len(), colors.len()) });
+        }
+        let size = cfg.image_size as usize;
+        let mut image = vec![[0.0f32; 4]; size * size];
+        self.check(unsafe {
+            sys::npa_splat_2d(self.raw, positions.as_ptr() as *const f32, colors.as_ptr() as *const f32,
+                              positions.len() as u32, cfg, image.as_mut_ptr() as *mut f32)
+        })?;
+        Ok(image)
     }
 
     /// `NpaModel::step_cpu` (model.rs:768-858): hashgrid, perception, update MLP, masked Euler step.

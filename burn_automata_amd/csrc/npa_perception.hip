@@ -1619,8 +1619,8 @@ static StepParams with_directory(const StepParams& p, const Workspace& ws) {
 hipError_t launch_density(const StepParams& p_in, Workspace& ws, float* density_out, int grid_blocks,
                           hipStream_t stream, Profiler* prof) {
     const StepParams p = with_directory(p_in, ws);
-    // sparse 2D bins: a thread per target (in 3D a target walks 27 cells, and the occupied cells of
-    // a sparse grid - a surface, say - hold several particles: the wave pass stays faster there)
+    // sparse grids (fewer than 4 particles per cell in 2D, fewer than 1 in 3D): a wave per cell run
+    // would leave most of its lanes idle, so four lanes serve one target and a wave 16 slots
     if (p.g.dim == 2 && (uint64_t)p.B * p.g.cells * 4 > p.T) {  // four lanes per target, 16 per wave
         const uint32_t waves = (p.T + 15) / 16;
         return launch_timed(prof, NPA_KERNEL_DENSITY, k_density_lanes<2>, dim3((waves + 3) / 4), dim3(256), 0, stream,

@@ -309,6 +309,32 @@ def test_executor_rollout_64_steps(ctx, name):
     np.testing.assert_array_equal(to_np(gs), want_s)
 
 
+def test_rollout_trace_with_mean_dx(ctx):
+    """run_rollout_from_particles (rollout/mod.rs:222-297): the final particles are the oracle
+    rollout's bit for bit and each step's mean_dx is the serial f32 mean of the oracle step's
+    motion norms over every particle, masked or not (rollout/mod.rs:277-283), within the
+    single-step tolerance (the trace's MLP pass goes through npa_mlp_forward)."""
+    from burn_automata_amd.config import RolloutConfig
+    from burn_automata_amd.rollout import mean_dx_norm, run_rollout_from_particles
+    m, g, pos, st, w, b, n = _model_case("batch4")
+    cfg = RolloutConfig(batch_size=b, particle_count=n, steps=6, dt=1.0, update_prob=0.5, seed=42)
+    trace = run_rollout_from_particles(NpaModel(m, w), g, cfg, pos, st,
+                                       executor=HipAutomataExecutor(ctx=ctx))
+    p, s, want = pos, st, []
+    for k in range(cfg.steps):
+        out = O.step(m, w, p, s, b, n, g, cfg.dt, O.update_mask(b, n, cfg.update_prob, k, cfg.seed))
+        want.append(mean_dx_norm(out.dx))
+        p, s = out.next_positions, out.next_states
+    np.testing.assert_array_equal(to_np(trace.positions), p)
+    np.testing.assert_array_equal(to_np(trace.states), s)
+    assert len(trace.mean_dx) == cfg.steps and min(want) > 0
+    np.testing.assert_allclose(trace.mean_dx, want, rtol=STEP_TOL, atol=0)
+    fast = run_rollout_from_particles(NpaModel(m, w), g, cfg, pos, st,
+                                      executor=HipAutomataExecutor(ctx=ctx), record_mean_dx=False)
+    assert fast.mean_dx == []
+    np.testing.assert_array_equal(to_np(fast.positions), p)
+
+
 def test_state_outlives_its_context():
     """A state keeps its context alive: the state still steps and reads after the caller destroyed
     the context, and destroying the state last releases both (no use of freed memory)."""

@@ -126,3 +126,16 @@ def test_raster_camera_look_at():
     assert up[1] > 0 and abs(up[0]) < 1e-12  # world up stays in the camera's y-z plane, pointing up
     assert abs(cam.fy - 120.0 / math.tan(math.pi / 8)) < 1e-9 and cam.fx == cam.fy
     assert (cam.cx, cam.cy) == (160.0, 120.0)
+
+
+def test_mean_dx_norm_is_a_serial_f32_mean():
+    """rollout/mod.rs:277-282: |dx| over x, y, z only (the fourth lane is padding), summed left to
+    right in f32, so a large leading norm swallows the unit norms after it, which a pairwise or
+    f64 sum would keep."""
+    from burn_automata_amd.rollout import mean_dx_norm
+    assert mean_dx_norm(np.zeros((0, 4), np.float32)) == 0.0
+    assert mean_dx_norm(np.array([[3, 4, 0, 100], [0, 0, 12, 7]], np.float32)) == 8.5
+    dx = np.zeros((5, 4), np.float32)
+    dx[:, 0] = [2.0 ** 24, 1, 1, 1, 1]
+    assert mean_dx_norm(dx) == float(np.float32(2.0 ** 24) / np.float32(5))
+    assert mean_dx_norm(dx) != float(np.float32((2.0 ** 24 + 4) / 5))

@@ -1,13 +1,16 @@
 """The Rust crates under bindings/rust (cargo is absent here, so they are checked as text): the
 `extern "C"` block of npa-hip-sys declares every function of include/npa_abi.h with the same
 parameter count and return kind, every #[repr(C)] struct has the header's fields in the header's
-order, and every named constant has the header's value."""
+order, and every named constant has the header's value. The safe crate npa-hip wraps each operator
+of the reference's kernel crate (crates/burn_automata_kernels/src/lib.rs:40-66) in a method that
+calls the matching sys function with as many arguments as that function takes."""
 import os
 import re
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "npa_abi.h")
 SYS = os.path.join(ROOT, "bindings", "rust", "npa-hip-sys", "src", "lib.rs")
+SAFE = os.path.join(ROOT, "bindings", "rust", "npa-hip", "src", "lib.rs")
 
 
 def _strip_c(text):
@@ -111,3 +114,53 @@ def test_every_constant_has_the_header_value():
     for name, val in h.items():
         assert name in r, name
         assert r[name] == val, (name, val, r[name])
+
+
+def _safe_methods():
+    """Method name -> body text of each `pub fn` in the safe crate's impl blocks (the first one of a
+    name: `Context::step` comes before `State::step`)."""
+    text = open(SAFE).read()
+    out = {}
+    starts = [(m.group(1), m.start()) for m in re.finditer(r"\n    pub fn (\w+)", text)]
+    for i, (name, at) in enumerate(starts):
+        end = starts[i + 1][1] if i + 1 < len(starts) else len(text)
+        out.setdefault(name, text[at:end])
+    return out
+
+
+def _sys_calls(body):
+    """(sys function, argument count) of every `sys::npa_*(...)` call in a method body."""
+    calls = []
+    for m in re.finditer(r"sys::(npa_\w+)\(", body):
+        depth, i, args, cur = 1, m.end(), [], ""
+        while depth:
+            c = body[i]
+            if c in "([{":
+                depth += 1
+            elif c in ")]}":
+                depth -= 1
+            if depth == 1 and c == ",":
+                args.append(cur)
+                cur = ""
+            elif depth:
+                cur += c
+            i += 1
+        if cur.strip():
+            args.append(cur)
+        calls.append((m.group(1), len(args)))
+    return calls
+
+
+def test_safe_crate_wraps_the_reference_operators():
+    methods = _safe_methods()
+    sys_fns = rust_functions()
+    want = {"build_hashgrid": "npa_build_hashgrid", "perceive_with_options": "npa_perceive",
+            "euler_step": "npa_euler_step", "decode_gaussians_3d": "npa_decode_gaussians_3d",
+            "splat_particles_2d": "npa_splat_2d", "step": "npa_step"}
+    for method, fn in want.items():
+        assert method in methods, method
+        calls = dict(_sys_calls(methods[method]))
+        assert fn in calls, (method, fn, calls)
+        assert calls[fn] == sys_fns[fn][1], (method, fn, calls[fn], sys_fns[fn][1])
+    for st in ("PerceptionOutput", "Gaussian3d", "HashGridSnapshot", "StepOutput"):
+        assert re.search(r"pub struct %s\b" % st, open(SAFE).read()), st
