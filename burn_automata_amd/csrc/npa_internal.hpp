@@ -118,6 +118,11 @@ struct Workspace {
     DevBuf bin_list;
     // the folded build: per rank tile, the cell coordinate span (min x, y, z, max x, y, z, 2 spare)
     DevBuf tile_span;
+    // the binned build (one system): per bin a 64-bit counter (particles | update-mask targets << 32)
+    // and after the C counters eight span words; all zero between builds (zeroed when allocated,
+    // reset by the build's scan). bin_urow: per particle its target index within its bin (~0u for
+    // a particle outside the mask).
+    DevBuf bin_count, bin_urow;
     // Targets of the second pass and the update: particles whose update mask is not 0 (the others
     // are written to the output by the update-mask kernel). act_rows: compact row -> slot.
     // Counts (u32 words of wl_count, kWlWords): [0] density items, [1] compact rows (one 64-bit

@@ -48,9 +48,10 @@ def _case(name, particles, masked):
 
 def test_noalloc_step_equals_npa_step_on_calls_in_a_row(ctx):
     L = lib()
-    # larger, then smaller (the array still holds the first call's workspace), then the C2 system
+    # larger, then smaller (the array still holds the first call's workspace), then the C2 system;
+    # then C4's sparse 3D grid twice (the binned build, whose bin counters the call clears itself)
     for name, particles, masked in (("c1", 4096, True), ("c1", 1024, False), ("c5", 256, True),
-                                    ("c2", None, True)):
+                                    ("c2", None, True), ("c4", None, True), ("c4", 6000, False)):
         w, mask = _case(name, particles, masked)
         print(f"noalloc vs npa_step: {name} batch={w['batch']} n={w['n']} masked={masked}", flush=True)
         want = _run(ctx, L.npa_step, w, mask)
