@@ -1533,19 +1533,20 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
 // scatter, split). Used when a system has at most kSysMaxCells bins (coordinate bins in Particle
 // mode, cells in Grid mode) and at most kSysMaxRounds * 1024 particles (C1 and C5: 4,096 particles
 // over 4,096 bins; more rounds per wave would spill registers).
-// k_sys_rank, one 1024-thread block per system:
-//   1. wave w ranks its slice [w R 64, (w + 1) R 64) in rounds of 64 with key ballots and a u16 LDS
-//      counter per key (stable, as k_hash_rank); the group's last lane also adds the group's
-//      update-mask targets to a per-key count (two keys' u16 counts per u32 word);
-//   2. per key (thread t: keys 4t .. 4t + 3, read four at a time): each wave's base and the total,
-//      and one block scan of three sums: the key's first slot (bin_offsets), its first work item
-//      (ceil(total / tpi) items of <= tpi slots, as the split emits for a bin of one cell or an
-//      unsplit bin; sys_item[b][key]) and its first compact row; the system's item and row totals go
-//      to sys_tot[b];
-//   3. per particle: its slot within the system (keys[i]) and, for an update-mask target, a compact
-//      row within the system from its bin's counter (ranks[i] = row + 1, 0 for no row; bit 31 marks
-//      the bin's first particle). Consecutive rows per bin, in the order the LDS atomics land: rows
-//      only index the targets, no result depends on their order.
+// k_sys_rank, one 1024-thread block per system (wave w owns particles [w R 64, (w + 1) R 64)):
+//   1. per particle its key and one LDS atomic on the key's counter (particles | update-mask
+//      targets << 16), whose old value is the particle's place in its bin and, for a target, its
+//      target index there - in whatever order the atomics land;
+//   2. per key (thread t: keys 4t .. 4t + 3, read four at a time): one block scan of three sums:
+//      the key's first slot (bin_offsets), its first work item (ceil(count / tpi) items of <= tpi
+//      slots, as the split emits for a bin of one cell or an unsplit bin; sys_item[b][key]) and its
+//      first compact row; the system's item and row totals go to sys_tot[b];
+//   3. per particle: members[bin start + place] = particle (LDS);
+//   4. per particle: its rank in the bin = the bin's members with a smaller index (the reference's
+//      order within a bin; a bin of k particles costs each of them k LDS reads), its slot within the
+//      system (keys[i]) and, for a target, its compact row = the bin's first row + its target index
+//      (ranks[i] = row + 1, 0 for no row; bit 31 marks the bin's first particle). Rows only index
+//      the targets, no result depends on their order.
 // k_sys_scatter, one thread per particle: the systems' item and row bases (prefix of sys_tot), then
 // the sorted record, state row and snapshot entries at the particle's slot, the work item starting
 // there, its compact row (act_rows / row_of), the bin's directory entry from its first particle, and
@@ -1593,41 +1594,38 @@ __device__ __forceinline__ void sys_cell(const float* p, const GridParams& g, in
 constexpr uint32_t kSysMaxCells = 4096;
 constexpr uint32_t kSysMaxRounds = 4;
 
-__host__ __device__ inline uint32_t sys_row_stride(uint32_t C) { return (C + 3) & ~3u; }  // u16 per counter row
-// counters [waves][cp] u16, starts [cp + 4] u16, rows [cp / 2] u32
-inline uint32_t sys_lds_bytes(uint32_t C) { return 36u * sys_row_stride(C) + 8u; }
+__host__ __device__ inline uint32_t sys_row_stride(uint32_t C) { return (C + 3) & ~3u; }  // words per key row
+// counters [cp] u32, first slots [cp + 4] u32, first rows [cp] u32, members [kSysMaxRounds * 1024] u16
+inline uint32_t sys_lds_bytes(uint32_t C) { return 12u * sys_row_stride(C) + 16u + 2u * kSysMaxRounds * kSysThreads; }
 
 template <int D, int R>
 __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restrict__ pos, uint32_t n, GridParams g,
-                                                          uint32_t key_bits, uint32_t tpi_log2, SplitTargets T,
+                                                          uint32_t tpi_log2, SplitTargets T,
                                                           uint32_t* __restrict__ bin_offsets,
                                                           uint32_t* __restrict__ dir_n, uint32_t* __restrict__ sys_item,
                                                           unsigned long long* __restrict__ sys_tot,
                                                           uint32_t* __restrict__ slot_of,
                                                           uint32_t* __restrict__ row_code, uint32_t batch,
                                                           uint32_t* __restrict__ flags) {
-    extern __shared__ uint16_t sys_lds[];
+    extern __shared__ uint32_t sys_lds[];
     constexpr uint32_t K = kDirGroups;
     const uint32_t C = g.cells, cp = sys_row_stride(C);
-    uint16_t* cnt = sys_lds;                                   // ranks per wave, then each wave's base
-    uint16_t* sstart = cnt + kSysWaves * cp;                   // [C + 1] the key's first slot in the system
-    uint32_t* srow = reinterpret_cast<uint32_t*>(sstart + cp + 4);  // two keys' target counts, then row counters
+    uint32_t* cnt = sys_lds;                     // per key: particles | update-mask targets << 16
+    uint32_t* sstart = cnt + cp;                 // the key's first slot in the system
+    uint32_t* srow = sstart + cp + 4;            // the key's first compact row in the system
+    uint16_t* members = reinterpret_cast<uint16_t*>(srow + cp);  // the bins' particles, by bin
     __shared__ uint32_t red[3][kSysWaves];
     __shared__ int red_lo[3][kSysWaves], red_hi[3][kSysWaves];
     const uint32_t b = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const uint64_t sys = (uint64_t)b * n;
 
-    {
-        uint64_t* c64 = reinterpret_cast<uint64_t*>(sys_lds);
-        for (uint32_t k = tid; k < kSysWaves * cp / 4; k += kSysThreads) c64[k] = 0ull;
-        for (uint32_t k = tid; k < cp / 2; k += kSysThreads) srow[k] = 0u;
-    }
+    for (uint32_t k = tid; k < cp / 4; k += kSysThreads) reinterpret_cast<uint4*>(cnt)[k] = make_uint4(0, 0, 0, 0);
     __syncthreads();
 
-    // ---- 1. rank
-    const uint64_t lt = lanemask_lt();
-    lds_u16* mine = (lds_u16*)(cnt + w * cp);
-    uint32_t key_r[R], rank_r[R], tgt_bits = 0;
+    // ---- 1. keys, and one LDS atomic per particle on its key's counter: the old value is the
+    // particle's place in its bin and, for a target, its target index there (in whatever order the
+    // atomics land: the ranks below restore the reference's order, and rows only index targets)
+    uint32_t key_r[R], place_r[R], tgt_bits = 0;
     int lo[3] = {INT32_MAX, INT32_MAX, INT32_MAX}, hi[3] = {INT32_MIN, INT32_MIN, INT32_MIN};
     bool ovf = false;
     float4 p_r[R];
@@ -1639,45 +1637,26 @@ __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restri
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t li = (w * R + r) * 64 + lane;
-        const bool active = li < n;
-        uint32_t key = 0;
-        bool tgt = false;
-        if (active) {
+        key_r[r] = 0;
+        place_r[r] = 0;
+        if (li < n) {
             const float p[4] = {p_r[r].x, p_r[r].y, p_r[r].z, p_r[r].w};
             int c[3];
+            uint32_t key;
             sys_cell(p, g, c, &key, &ovf);
 #pragma unroll
             for (int a = 0; a < D; ++a) {
                 lo[a] = min(lo[a], c[a]);
                 hi[a] = max(hi[a], c[a]);
             }
-            tgt = T.mask_mode == 0 ||
-                  (T.mask_mode == 1 ? hash_mask(li, b, n, T.update_prob, T.step_index, T.base_seed) : T.mask[sys + li]) != 0.0f;
+            const bool tgt = T.mask_mode == 0 ||
+                             (T.mask_mode == 1 ? hash_mask(li, b, n, T.update_prob, T.step_index, T.base_seed)
+                                               : T.mask[sys + li]) != 0.0f;
+            const uint32_t old = atomicAdd(cnt + key, 1u | ((uint32_t)tgt << 16));
+            key_r[r] = key;
+            place_r[r] = old;
+            if (tgt) tgt_bits |= 1u << r;
         }
-        key_r[r] = key;
-        if (tgt) tgt_bits |= 1u << r;
-    }
-    // every round's key first (the position loads of all rounds are in flight together), then the ranks
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint32_t li = (w * R + r) * 64 + lane;
-        const bool active = li < n;
-        const uint32_t key = key_r[r];
-        const bool tgt = (tgt_bits >> r) & 1u;
-        uint64_t peers = __ballot(active);
-        peers = match_key_bits(peers, key, key_bits);
-        const uint64_t tball = __ballot(active && tgt);
-        uint32_t rank = 0;
-        if (active) {
-            const uint32_t base = mine[key];
-            rank = base + (uint32_t)__popcll(peers & lt);
-            if ((peers >> lane) == 1ull) {  // the group's last lane: the counter and the group's targets
-                mine[key] = (uint16_t)(base + (uint32_t)__popcll(peers));
-                const uint32_t m = (uint32_t)__popcll(peers & tball);
-                if (m) atomicAdd(&srow[key >> 1], m << (16 * (key & 1u)));
-            }
-        }
-        rank_r[r] = rank;
     }
     // the system's coordinate span (Particle mode: do coordinate bins hold one cell each?)
 #pragma unroll
@@ -1696,24 +1675,19 @@ __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restri
     if (__ballot(ovf) != 0ull && lane == 0) atomicOr(flags + 1, 1u);
     __syncthreads();
 
-    // ---- 2. per key: wave bases, totals, and the block's three scans
+    // ---- 2. per key (thread t: keys 4t .. 4t + 3): one block scan of three sums - the key's first
+    // slot (bin_offsets), its first work item (ceil(count / tpi) items of <= tpi slots, as the split
+    // emits for a bin of one cell or an unsplit bin; sys_item[b][key]) and its first compact row;
+    // the system's item and row totals go to sys_tot[b]
     const uint32_t k0 = 4 * tid;
     uint32_t tot[4] = {0u, 0u, 0u, 0u}, msk[4] = {0u, 0u, 0u, 0u}, itm[4] = {0u, 0u, 0u, 0u};
     if (k0 < cp) {
-        uint64_t v[kSysWaves];
-#pragma unroll
-        for (uint32_t w2 = 0; w2 < kSysWaves; ++w2) v[w2] = *reinterpret_cast<const uint64_t*>(cnt + w2 * cp + k0);
-        uint64_t run = 0;  // four u16 fields: no carries, every total is at most n < 2^16
-#pragma unroll
-        for (uint32_t w2 = 0; w2 < kSysWaves; ++w2) {
-            *reinterpret_cast<uint64_t*>(cnt + w2 * cp + k0) = run;
-            run += v[w2];
-        }
-        const uint64_t m4 = *reinterpret_cast<const uint64_t*>(srow + 2 * tid);  // keys k0 .. k0 + 3
+        const uint4 v = reinterpret_cast<const uint4*>(cnt)[tid];
+        const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            tot[q] = (uint32_t)(run >> (16 * q)) & 0xffffu;
-            msk[q] = (uint32_t)(m4 >> (16 * q)) & 0xffffu;
+            tot[q] = vv[q] & 0xffffu;
+            msk[q] = vv[q] >> 16;
             itm[q] = (tot[q] + (1u << tpi_log2) - 1) >> tpi_log2;
         }
     }
@@ -1758,8 +1732,9 @@ __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restri
     const uint32_t tb = (uint32_t)__shfl((int)eb, (int)kSysWaves - 1, 64);
     const uint32_t tm = (uint32_t)__shfl((int)em, (int)kSysWaves - 1, 64);
     // the system's coordinate span per axis: a bin may hold two cells only if two coordinates of the
-    // span share its residue on some axis (see k_table_offsets_fold)
-    int span_lo[3] = {0, 0, 0}, span_hi[3] = {0, 0, 0};
+    // span share its residue on some axis (see k_bin_scan); no axis wider than the grid, no alias
+    int span_lo_a[3] = {0, 0, 0}, span_hi_a[3] = {0, 0, 0};
+    bool wide = false;
     if (g.mode == 1) {
 #pragma unroll
         for (int a = 0; a < D; ++a) {
@@ -1770,8 +1745,9 @@ __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restri
                 l = min(l, __shfl_xor(l, off, 64));
                 h = max(h, __shfl_xor(h, off, 64));
             }
-            span_lo[a] = __shfl(l, 0, 64);
-            span_hi[a] = __shfl(h, 0, 64);
+            span_lo_a[a] = __shfl(l, 0, 64);
+            span_hi_a[a] = __shfl(h, 0, 64);
+            if (span_hi_a[a] >= span_lo_a[a] && (int64_t)span_hi_a[a] - span_lo_a[a] >= (int64_t)g.size[a]) wide = true;
         }
     }
     auto may_alias = [&](uint32_t k) {
@@ -1782,51 +1758,57 @@ __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restri
             const int64_t m = (int64_t)g.size[a];
             const int64_t r = (int64_t)(rest % g.size[a]);
             rest /= g.size[a];
-            const int64_t l = span_lo[a], h = span_hi[a];
+            const int64_t l = span_lo_a[a], h = span_hi_a[a];
             if (h >= l && h - l >= m && l + rem_euclid_i64(r - l, m) + m <= h) al = true;
         }
         return al;
     };
     if (tid == 0) {
         sys_tot[b] = (unsigned long long)tb | ((unsigned long long)tm << 32);
-        sstart[C] = (uint16_t)n;
         if (b == batch - 1) bin_offsets[(uint64_t)batch * C] = batch * n;
     }
     if (k0 < C) {
         uint32_t st = pa + xa - sa, it = pb + xb - sb, rw = pm + xm - sm;
-        uint64_t rpack = 0;
+        uint32_t sv[4], rv[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint32_t k = k0 + q;
+            sv[q] = st;
+            rv[q] = rw;
             if (k < C) {
-                sstart[k] = (uint16_t)st;
                 bin_offsets[(uint64_t)b * C + k] = b * n + st;
                 sys_item[(uint64_t)b * C + k] = it;
-                if (g.mode == 1) dir_n[(uint64_t)b * C + k] = tot[q] ? (may_alias(k) ? K + 1 : 1u) : 0u;
-                rpack |= (uint64_t)rw << (16 * q);
+                if (g.mode == 1) dir_n[(uint64_t)b * C + k] = tot[q] ? (wide && may_alias(k) ? K + 1 : 1u) : 0u;
             }
             st += tot[q];
             it += itm[q];
             rw += msk[q];
         }
-        *reinterpret_cast<uint64_t*>(srow + 2 * tid) = rpack;  // the keys' first rows: the row counters
+        reinterpret_cast<uint4*>(sstart)[tid] = make_uint4(sv[0], sv[1], sv[2], sv[3]);
+        reinterpret_cast<uint4*>(srow)[tid] = make_uint4(rv[0], rv[1], rv[2], rv[3]);
     }
     __syncthreads();
 
-    // ---- 3. per particle: slot and compact row within the system
+    // ---- 3. each particle at its bin's start + its place, then 4. its rank in the bin = the bin's
+    // members with a smaller index (the reference's order), hence its slot; a target's row is the
+    // bin's first row + its target index; bit 31 marks the bin's first particle
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t li = (w * R + r) * 64 + lane;
+        if (li < n) members[sstart[key_r[r]] + (place_r[r] & 0xffffu)] = (uint16_t)li;
+    }
+    __syncthreads();
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t li = (w * R + r) * 64 + lane;
         if (li >= n) continue;
         const uint32_t key = key_r[r];
-        const uint32_t r_bin = cnt[w * cp + key] + rank_r[r];  // rank among the bin's particles
-        uint32_t code = r_bin == 0 ? 0x80000000u : 0u;
-        if ((tgt_bits >> r) & 1u) {
-            const uint32_t sh = 16 * (key & 1u);
-            const uint32_t old = atomicAdd(&srow[key >> 1], 1u << sh);
-            code |= ((old >> sh) & 0xffffu) + 1u;
-        }
-        slot_of[sys + li] = (uint32_t)sstart[key] + r_bin;
+        const uint32_t beg = sstart[key], end = beg + (cnt[key] & 0xffffu);
+        uint32_t rank = 0;
+        for (uint32_t j = beg; j < end; ++j) rank += (uint32_t)members[j] < li ? 1u : 0u;
+        uint32_t code = rank == 0 ? 0x80000000u : 0u;
+        if ((tgt_bits >> r) & 1u) code |= srow[key] + (place_r[r] >> 16) + 1u;
+        slot_of[sys + li] = beg + rank;
         row_code[sys + li] = code;
     }
 }
@@ -1920,7 +1902,7 @@ static hipError_t launch_sys_r(const GridParams& g, const HashgridPlan& plan, co
     }
     // per particle: slot (keys) and row code (ranks); per bin: first item (totals); per system: totals
     hipError_t e = launch_timed(prof, NPA_KERNEL_HASH_RANK, k_sys_rank<D, R>, dim3(batch), dim3(kSysThreads), lds,
-                                stream, pos, n, g, plan.key_bits, (uint32_t)__builtin_ctz(plan.tpi), tg,
+                                stream, pos, n, g, (uint32_t)__builtin_ctz(plan.tpi), tg,
                                 ws.bin_offsets.as<uint32_t>(),
                                 ws.dir_n.as<uint32_t>(), ws.totals.as<uint32_t>(),
                                 ws.scan_status.as<unsigned long long>(), ws.keys.as<uint32_t>(),

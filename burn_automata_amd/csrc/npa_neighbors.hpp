@@ -73,6 +73,66 @@ __device__ __forceinline__ bool cell_range(const StepParams& P, const uint32_t* 
     return found;
 }
 
+// cell_range for NU cells of one lane at once: every cell's directory loads (its size, first
+// entry and end; a Grid-mode cell's start and end) are issued before the first is used, so the
+// lookups cost one memory round trip instead of NU. A cell not wanted, outside a clamped grid or
+// empty gets beg = end = 0. Bins of several cells (rare) finish through cell_range.
+template <int NU>
+__device__ __forceinline__ void cell_ranges(const StepParams& P, const uint32_t* __restrict__ bo, uint32_t b,
+                                            const int64_t (&n)[NU][3], const bool (&want)[NU], uint32_t (&beg)[NU],
+                                            uint32_t (&end)[NU], bool (&filter)[NU]) {
+    uint64_t bin[NU];
+    bool ok[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+        uint32_t cell = 0;
+        ok[u] = want[u] && cell_index(n[u][0], n[u][1], n[u][2], P.g, &cell);
+        bin[u] = (uint64_t)b * P.g.cells + cell;
+        beg[u] = 0;
+        end[u] = 0;
+        filter[u] = false;
+    }
+    if (P.g.mode != 1) {
+        uint32_t lo[NU], hi[NU];
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            lo[u] = ok[u] ? bo[bin[u]] : 0u;
+            hi[u] = ok[u] ? bo[bin[u] + 1] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            beg[u] = lo[u];
+            end[u] = hi[u];
+        }
+        return;
+    }
+    uint32_t nd[NU], last[NU];
+    int4 e0[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+        nd[u] = ok[u] ? P.dir_n[bin[u]] : 0u;
+        e0[u] = ok[u] ? P.dir_e[bin[u] * kDirGroups] : make_int4(0, 0, 0, 0);
+        last[u] = ok[u] ? bo[bin[u] + 1] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+        if (nd[u] == 1) {
+            if ((int64_t)e0[u].x == n[u][0] && (int64_t)e0[u].y == n[u][1] && (int64_t)e0[u].z == n[u][2]) {
+                beg[u] = (uint32_t)e0[u].w;
+                end[u] = last[u];
+            }
+        } else if (nd[u] != 0) {
+            uint32_t bb = 0, ee = 0;
+            bool ff = false;
+            if (cell_range(P, bo, b, n[u][0], n[u][1], n[u][2], bb, ee, ff)) {
+                beg[u] = bb;
+                end[u] = ee;
+                filter[u] = ff;
+            }
+        }
+    }
+}
+
 // The candidate runs of the 3^D neighbour cells of cell (c0, c1, c2) of system b, looked up in
 // parallel: lane k < 3^D takes neighbour k in the reference's visit order (k = (dz+1)*9 +
 // (dy+1)*3 + (dx+1): dz, then dy, then dx). found: the cell holds particles.

@@ -376,22 +376,21 @@ __global__ __launch_bounds__(256) void k_density_lanes(StepParams P, const float
     // ---- lookup: lane q, cells q, q + 4, q + 8
     uint32_t obeg[3], olen[3];
     bool ofilt[3];
+    {
+        int64_t nc[3][3];
+        bool want[3];
+        uint32_t oend[3];
 #pragma unroll
-    for (int u = 0; u < 3; ++u) {
-        const uint32_t k = q + 4 * u;
-        obeg[u] = 0;
-        olen[u] = 0;
-        ofilt[u] = false;
-        if (k < 9 && active) {
-            uint32_t beg, end;
-            bool filt;
-            if (cell_range(P, bo, b, (int64_t)ci[0] + (int)(k % 3) - 1, (int64_t)ci[1] + (int)(k / 3) - 1, 0, beg,
-                           end, filt)) {
-                obeg[u] = beg;
-                olen[u] = end - beg;
-                ofilt[u] = filt;
-            }
+        for (int u = 0; u < 3; ++u) {
+            const uint32_t k = q + 4 * u;
+            want[u] = k < 9 && active;
+            nc[u][0] = (int64_t)ci[0] + (int)(k % 3) - 1;
+            nc[u][1] = (int64_t)ci[1] + (int)(k / 3) - 1;
+            nc[u][2] = 0;
         }
+        cell_ranges<3>(P, bo, b, nc, want, obeg, oend, ofilt);
+#pragma unroll
+        for (int u = 0; u < 3; ++u) olen[u] = oend[u] - obeg[u];
     }
     // every run in every lane of the quad (run k lives in lane k % 4, register k / 4)
     uint32_t rbeg[9], rlen[9], rfilt = 0;

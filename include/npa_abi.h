@@ -186,7 +186,8 @@ npa_status npa_context_set_host_io(npa_context* ctx, int host_io);
  * fused products and split sums: a single step stays within 1e-6 of the reference, while a
  * rollout drifts apart as far as the reference itself does from a one-ulp perturbation of its
  * inputs (the dynamics amplify last-bit differences). Measured on MI355X, the matrix-core engine's
- * step kernel is the faster one at every system size from 256 particles up. */
+ * step kernel is the faster one from 16,384 particles up; below that the VALU engine's is, as small
+ * systems take four-wave blocks on that engine. */
 enum { NPA_MLP_VALU = 0, NPA_MLP_MFMA = 1 };
 npa_status npa_context_set_mlp_engine(npa_context* ctx, int engine);
 

@@ -88,3 +88,48 @@ def test_noalloc_refuses_oversized_systems_and_host_io(ctx):
     assert code == _abi.NPA_ERR_INVALID_ARGUMENT
     hctx.close()
     ctx.synchronize()
+
+
+@pytest.mark.parametrize("name,particles", [("c1", 4096), ("c4", None)])
+def test_noalloc_step_replays_in_a_hip_graph(ctx, name, particles):
+    """npa_step_noalloc queues kernels only (no allocation, no memset node, no host wait), so a
+    caller can capture it: captured once through torch.cuda.graph on the capture stream, every
+    replay - with eager work and synchronisation in between - equals the eager call bit for bit."""
+    L = lib()
+    w, mask = _case(name, particles, True)
+    m, g, b, n = w["model"], w["grid"], w["batch"], w["n"]
+    total = b * n
+    pos = device_f32(w["positions"]).reshape(-1, 4)
+    st = device_f32(w["states"]).reshape(-1)
+    msk = device_f32(mask)
+    weights = NpaWeights.from_arrays(w["weights"])  # holds the weight tensors the graph reads
+    wc = weights.to_c()
+    gc, mc = g.to_c(), m.to_c()
+    out_p, out_s = torch.empty_like(pos), torch.empty_like(st)
+    dens = torch.empty((total,), dtype=torch.float32, device=pos.device)
+
+    def call():
+        return L.npa_step_noalloc(ctx.handle, ptr(pos), ptr(st), b, n, C.byref(gc), C.byref(mc), C.byref(wc), 1.0,
+                                  ptr(msk), ptr(out_p), ptr(out_s), ptr(dens))
+
+    print(f"graph capture of npa_step_noalloc: {name} n={total}", flush=True)
+    ctx.check(call())  # eager (also sets the kernels' LDS limits, outside the capture)
+    ctx.synchronize()
+    want = [t.cpu().numpy().copy() for t in (out_p, out_s, dens)]
+    graph = torch.cuda.CUDAGraph()
+    home = torch.cuda.current_stream().cuda_stream
+    try:
+        with torch.cuda.graph(graph):
+            ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+            code = call()
+    finally:
+        ctx.set_stream(home)
+    ctx.check(code)
+    for k in range(3):
+        for t in (out_p, out_s, dens):
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for t, ref in zip((out_p, out_s, dens), want):
+            np.testing.assert_array_equal(t.cpu().numpy(), ref, err_msg=f"{name} replay {k}")
