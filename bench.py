@@ -495,9 +495,10 @@ def main(argv=None) -> int:
                     help="render (default 64) and raster (default 1024) workloads only")
     ap.add_argument("--decode-every", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
-    ap.add_argument("--mlp-engine", choices=("valu", "mfma"), default="valu",
-                    help="update MLP on the vector ALUs in the reference's order (bit-exact, default) "
-                         "or on the fp32 matrix cores (single-step tolerance)")
+    ap.add_argument("--mlp-engine", choices=("valu", "mfma", "bf16"), default="valu",
+                    help="update MLP on the vector ALUs in the reference's order (bit-exact, default), "
+                         "on the fp32 matrix cores, or with layer 1 on the bf16 matrix cores (bf16x3 "
+                         "features, bf16 weights; 2D fused kernel) - both single-step tolerance")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-alt-engine", action="store_true",
                     help="skip the matrix-core engine's run beside the headline")
@@ -559,7 +560,7 @@ def main(argv=None) -> int:
             ex.splat_2d(state, splat)
 
     from burn_automata_amd import _abi
-    engine = {"valu": _abi.MLP_VALU, "mfma": _abi.MLP_MFMA}[args.mlp_engine]
+    engine = {"valu": _abi.MLP_VALU, "mfma": _abi.MLP_MFMA, "bf16": _abi.MLP_MFMA_BF16}[args.mlp_engine]
     L = lib()
 
     def new_state():
@@ -774,8 +775,12 @@ def main(argv=None) -> int:
         # the matrix-core engine runs both MLP layers on MFMA, in the separate MLP kernel and in the
         # fused update kernel alike; the bit-exact engine takes only layer 1's products from MFMA
         # (one rounding each, as v_mul_f32) and adds everything on the VALU in the reference's order
-        on_mfma = args.mlp_engine == "mfma" and dominant in ("mlp", "update")
-        if on_mfma:
+        on_mfma = args.mlp_engine in ("mfma", "bf16") and dominant in ("mlp", "update")
+        if on_mfma and args.mlp_engine == "bf16":
+            engine_note = ("layer 1 on the bf16 matrix cores (v_mfma_f32_4x4x4bf16_1k, bf16x3 features, "
+                           "bf16 weights), layer 2 on the fp32 matrix cores, neighbour walk and sums on the "
+                           "VALU; peak = the published MI355X fp32 peak (the MLP's flops are counted as fp32)")
+        elif on_mfma:
             engine_note = ("fp32 matrix cores for both MLP layers (v_mfma_f32_4x4x1f32), neighbour walk "
                            "and sums on the VALU; peak = the published MI355X fp32 peak")
         elif dominant == "update":

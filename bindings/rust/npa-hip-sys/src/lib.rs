@@ -43,6 +43,7 @@ pub const NPA_VIEW_YZ: u32 = 2;
 pub const NPA_VIEW_ISO: u32 = 3;
 pub const NPA_MLP_VALU: c_int = 0;
 pub const NPA_MLP_MFMA: c_int = 1;
+pub const NPA_MLP_MFMA_BF16: c_int = 2;
 pub const NPA_RASTER_COLOR_SH: u32 = 0;
 pub const NPA_RASTER_COLOR_RGB: u32 = 1;
 /// Kernel ids for npa_profile_enable (bit masks) and npa_profile_read.

@@ -31,6 +31,7 @@ NPA_ERR_COORD_OVERFLOW = 32
 # update-MLP engines (npa_context_set_mlp_engine / npa_state_set_mlp_engine)
 MLP_VALU = 0
 MLP_MFMA = 1
+MLP_MFMA_BF16 = 2
 
 # kernel ids for npa_profile_read
 KERNEL_NAMES = ("hash_rank", "table_scan", "offsets_scan", "scatter", "density", "perceive", "splat",

@@ -404,7 +404,7 @@ uint32_t feature_rows_for(const npa::StepParams& p) { return npa::fused_update_a
 
 npa_status npa_context_set_mlp_engine(npa_context* ctx, int engine) {
     if (!ctx) return NPA_ERR_INVALID_ARGUMENT;
-    if (engine != NPA_MLP_VALU && engine != NPA_MLP_MFMA)
+    if (engine != NPA_MLP_VALU && engine != NPA_MLP_MFMA && engine != NPA_MLP_MFMA_BF16)
         return fail(ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: unknown MLP engine " + std::to_string(engine));
     ctx->mlp_engine = engine;
     return NPA_OK;
@@ -1180,7 +1180,7 @@ npa_status npa_state_step(npa_state* s, uint32_t steps) {
 
 npa_status npa_state_set_mlp_engine(npa_state* s, int engine) {
     if (!s) return NPA_ERR_INVALID_ARGUMENT;
-    if (engine != NPA_MLP_VALU && engine != NPA_MLP_MFMA)
+    if (engine != NPA_MLP_VALU && engine != NPA_MLP_MFMA && engine != NPA_MLP_MFMA_BF16)
         return fail(s->ctx, NPA_ERR_INVALID_ARGUMENT, "invalid argument: unknown MLP engine " + std::to_string(engine));
     s->mlp_engine = engine;
     return NPA_OK;

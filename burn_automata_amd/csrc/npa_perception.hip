@@ -1726,7 +1726,7 @@ static hipError_t launch_mlp_e(const StepParams& p, Workspace& ws, const StepIO&
 template <int D, int SM, int FM>
 static hipError_t launch_mlp_t(const StepParams& p, Workspace& ws, const StepIO& io, hipStream_t stream,
                                Profiler* prof) {
-    if (p.mlp_engine == NPA_MLP_MFMA) return launch_mlp_e<D, SM, FM, 1>(p, ws, io, stream, prof);
+    if (p.mlp_engine != NPA_MLP_VALU) return launch_mlp_e<D, SM, FM, 1>(p, ws, io, stream, prof);
     return launch_mlp_e<D, SM, FM, 0>(p, ws, io, stream, prof);
 }
 

@@ -29,7 +29,10 @@
 // sums output D + c (its state channel's update) and, for c < D, motion output c, hidden units in
 // index order. The VALU engine rounds every product and sum as the reference does; the matrix-core
 // engine (v_mfma_f32_4x4x1f32, same mapping) fuses each multiply-add and splits each sum into
-// independent chains. Lane 0 writes the position, every lane its state channel.
+// independent chains; the bf16 matrix-core engine (2D) runs layer 1 on v_mfma_f32_4x4x4bf16_1k with
+// each feature split into three bf16 parts (hi + mid + lo = the feature exactly) and the weights
+// rounded to bf16, so that for bf16-valued weights every product is exact and only the order of the
+// fp32 sums differs. Lane 0 writes the position, every lane its state channel.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -241,8 +244,37 @@ __device__ __forceinline__ void for_each_entry(F&& f, std::integer_sequence<int,
 }
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef short v4s __attribute__((ext_vector_type(4)));
 
-// ENG: 0 = VALU, the reference's roundings (bit-exact); 1 = the MLP on the fp32 matrix cores.
+// f32 -> bf16 bits, round to nearest even (NaN stays a quiet NaN)
+__device__ __forceinline__ uint32_t bf16_rne(float x) {
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float bf16_f32(uint32_t h) { return __uint_as_float(h << 16); }
+__device__ __forceinline__ v4s as_v4s(uint2 v) { return __builtin_bit_cast(v4s, v); }
+
+// Four features as three packed bf16 quads with hi + mid + lo == x exactly for finite x: each part
+// takes the next eight significant bits of what the parts before it left (x - hi and its rest are
+// exact in f32).
+__device__ __forceinline__ void bf16x3_split(const float4& f, uint2& h, uint2& m, uint2& l) {
+    const float x[4] = {f.x, f.y, f.z, f.w};
+    uint32_t hb[4], mb[4], lb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        hb[i] = bf16_rne(x[i]);
+        const float r1 = x[i] - bf16_f32(hb[i]);
+        mb[i] = bf16_rne(r1);
+        lb[i] = bf16_rne(r1 - bf16_f32(mb[i]));
+    }
+    h = make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
+    m = make_uint2(mb[0] | (mb[1] << 16), mb[2] | (mb[3] << 16));
+    l = make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
+}
+
+// ENG: 0 = VALU, the reference's roundings (bit-exact); 1 = the MLP on the fp32 matrix cores;
+// 2 = layer 1 on the bf16 matrix cores (bf16x3 features, bf16 weights; 2D), layer 2 as ENG 1.
 // NW: waves per block (kFuseWaves; small systems with the usual options take blocks of 4 so that
 // their few items spread over every CU; a compile-time count keeps the item arithmetic in the
 // scalar registers the kernel can spare).
@@ -267,9 +299,16 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
     const uint32_t FP = P.FP;
     const uint32_t wfloats = (uint32_t)fused_weight_floats(FP, D);
 
-    // the block's copy of the padded weights
-    for (uint32_t v = threadIdx.x; v < wfloats / 4; v += blockDim.x)
-        reinterpret_cast<float4*>(lds)[v] = reinterpret_cast<const float4*>(wfused)[v];
+    // the block's copy of the padded weights (ENG 2: layer 1's as bf16 quads, w1b[FP/4][128], in the
+    // first half of w1q's region)
+    for (uint32_t v = threadIdx.x; v < wfloats / 4; v += blockDim.x) {
+        const float4 x = reinterpret_cast<const float4*>(wfused)[v];
+        if (ENG == 2 && v < FP * kFuseHidden / 4)
+            reinterpret_cast<uint2*>(lds)[v] =
+                make_uint2(bf16_rne(x.x) | (bf16_rne(x.y) << 16), bf16_rne(x.z) | (bf16_rne(x.w) << 16));
+        else
+            reinterpret_cast<float4*>(lds)[v] = x;
+    }
     __syncthreads();
     const float* w1q = lds;
     const float* b1 = w1q + (size_t)FP * HP;
@@ -719,7 +758,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
             wave_sync();
         }
         const float* myf = wl + (lane & 3u) * (FP + 4);
-        if constexpr (ENG == 1) {
+        if constexpr (ENG >= 1) {
             // Matrix-core engine (v_mfma_f32_4x4x1f32, 16 blocks of 4x4 with K = 1: lane l supplies
             // A[l / 4][l % 4] and B[l / 4][l % 4] and holds D[l / 4][r][l % 4] in accumulator r).
             // Layer 1: block b = hidden units 4b..4b+3, A = the four targets' feature k (lane l feeds
@@ -732,6 +771,36 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
             const float bb0 = b1[lane], bb1 = b1[lane + 64];
             v4f a0 = {bb0, bb0, bb0, bb0}, a1 = {bb1, bb1, bb1, bb1};
             v4f c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = {0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (ENG == 2) {
+                // v_mfma_f32_4x4x4bf16_1k, the same blocks with K = 4: lane l supplies features
+                // 4kb..4kb+3 of target l % 4 (one bf16 part at a time) and unit l's bf16 weights for
+                // them. The parts' rows [3][4 targets][FP / 4 quads] follow the hidden rows.
+                const uint32_t nq = FP / 4;
+                uint2* parts = reinterpret_cast<uint2*>(wl + 4 * (FP + 4) + 4 * Sh::HSTR);
+                for (uint32_t v = lane; v < 4 * nq; v += 64) {
+                    const uint32_t t = v / nq, qd = v - t * nq;
+                    uint2 h, m, l;
+                    bf16x3_split(*reinterpret_cast<const float4*>(wl + t * (FP + 4) + 4 * qd), h, m, l);
+                    parts[t * nq + qd] = h;
+                    parts[(4 + t) * nq + qd] = m;
+                    parts[(8 + t) * nq + qd] = l;
+                }
+                wave_sync();
+                const uint2* ph = parts + (lane & 3u) * nq;
+                const uint2* pm = ph + 4 * nq;
+                const uint2* pl = ph + 8 * nq;
+                const uint2* w1b = reinterpret_cast<const uint2*>(w1q);
+                for (uint32_t kb = 0; kb < nq; ++kb) {
+                    const v4s wa = as_v4s(w1b[kb * HP + lane]), wb = as_v4s(w1b[kb * HP + lane + 64]);
+                    const v4s xh = as_v4s(ph[kb]), xm = as_v4s(pm[kb]), xl = as_v4s(pl[kb]);
+                    a0 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(xh, wa, a0, 0, 0, 0);
+                    a1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(xh, wb, a1, 0, 0, 0);
+                    c0 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(xm, wa, c0, 0, 0, 0);
+                    c1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(xm, wb, c1, 0, 0, 0);
+                    a0 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(xl, wa, a0, 0, 0, 0);
+                    a1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(xl, wb, a1, 0, 0, 0);
+                }
+            } else {
             auto mfma_block = [&](uint32_t kb) {
                 const float4 f4 = *reinterpret_cast<const float4*>(myf + 4 * kb);
                 const float4 w0 = *reinterpret_cast<const float4*>(w1q + ((size_t)kb * HP + lane) * 4);
@@ -749,6 +818,7 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
             for (uint32_t kb = 0; kb < KB_FIXED; ++kb) mfma_block(kb);
             if (FP / 4 > KB_FIXED) mfma_block(KB_FIXED);
             if (FP / 4 > KB_FIXED + 1) mfma_block(KB_FIXED + 1);
+            }
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 hw[t * Sh::HSTR + lane] = fmaxf(a0[t] + c0[t], 0.0f);
@@ -927,7 +997,15 @@ static hipError_t launch_fused_d(const StepParams& p, Workspace& ws, const StepI
     const bool common = p.state_grad && p.hybrid && !p.density_grad;
     const bool per = p.g.boundary == 0;
     constexpr int W = kFuseWaves;
-    if (p.mlp_engine == NPA_MLP_MFMA)
+    if constexpr (D == 2) {  // the bf16 engine (2D; its bf16 feature parts must fit the wave's region)
+        constexpr uint32_t room = (uint32_t)std::min(FuseShape<2, 5>::WAVE_FLOATS, FuseShape<2, 13>::WAVE_FLOATS);
+        if (p.mlp_engine == NPA_MLP_MFMA_BF16 && 10 * p.FP + 4 * (16 + FuseShape<2, 5>::HSTR) <= room &&
+            10 * p.FP + 4 * (16 + FuseShape<2, -1>::HSTR) <= (uint32_t)FuseShape<2, -1>::WAVE_FLOATS)
+            return !common ? launch_fused_t<D, -1, 2, W>(p, ws, io, wfused, stream, prof)
+                   : per   ? launch_fused_t<D, 13, 2, W>(p, ws, io, wfused, stream, prof)
+                           : launch_fused_t<D, 5, 2, W>(p, ws, io, wfused, stream, prof);
+    }
+    if (p.mlp_engine != NPA_MLP_VALU)
         return !common ? launch_fused_t<D, -1, 1, W>(p, ws, io, wfused, stream, prof)
                : per   ? launch_fused_t<D, 13, 1, W>(p, ws, io, wfused, stream, prof)
                        : launch_fused_t<D, 5, 1, W>(p, ws, io, wfused, stream, prof);

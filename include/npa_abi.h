@@ -187,8 +187,12 @@ npa_status npa_context_set_host_io(npa_context* ctx, int host_io);
  * rollout drifts apart as far as the reference itself does from a one-ulp perturbation of its
  * inputs (the dynamics amplify last-bit differences). Measured on MI355X, the matrix-core engine's
  * step kernel is the faster one from 16,384 particles up; below that the VALU engine's is, as small
- * systems take four-wave blocks on that engine. */
-enum { NPA_MLP_VALU = 0, NPA_MLP_MFMA = 1 };
+ * systems take four-wave blocks on that engine. NPA_MLP_MFMA_BF16: in the fused step kernel of 2D
+ * systems, layer 1 on the bf16 matrix cores (v_mfma_f32_4x4x4bf16_1k) with each feature split into
+ * three bf16 parts that sum to it exactly and the weights rounded to bf16: for bf16-valued weights
+ * every product is exact and the step stays within the single-step gate; other weights are rounded
+ * (relative error about 2^-9). Layer 2, 3D systems and the other kernels run as NPA_MLP_MFMA. */
+enum { NPA_MLP_VALU = 0, NPA_MLP_MFMA = 1, NPA_MLP_MFMA_BF16 = 2 };
 npa_status npa_context_set_mlp_engine(npa_context* ctx, int engine);
 
 /* Blocks until all work queued on the context's stream has finished. */

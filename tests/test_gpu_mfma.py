@@ -59,6 +59,44 @@ def test_mfma_step_within_single_step_gate(mctx, name):
     np.testing.assert_array_equal(to_np(got.next_states)[off], want.next_states[off])
 
 
+@pytest.fixture(scope="module")
+def bctx():
+    c = Context(0)
+    c.set_mlp_engine(_abi.MLP_MFMA_BF16)
+    yield c
+    c.close()
+
+
+def _bf16_valued(weights):
+    """Each weight rounded to bf16 (nearest even), as f32: the weights the bf16 engine takes exactly."""
+    out = {}
+    for k, v in weights.items():
+        u = np.ascontiguousarray(v, np.float32).view(np.uint32).astype(np.uint64)
+        r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+        out[k] = r.astype(np.uint32).view(np.float32).reshape(np.shape(v))
+    return out
+
+
+@pytest.mark.parametrize("name", ["c5", "c1", "c2", "growing_3d"])
+def test_bf16_engine_step_within_single_step_gate(bctx, name):
+    """NPA_MLP_MFMA_BF16: layer 1 on v_mfma_f32_4x4x4bf16_1k with bf16x3 features. With bf16-valued
+    weights (C5's are; the others are rounded to bf16 here) every product is exact, so the step
+    stays within the single-step gate; 3D systems run the fp32 matrix-core engine."""
+    m, g, pos, st, w, b, n = _case(name)
+    if name != "c5":
+        w = _bf16_valued(w)
+    mask = O.update_mask(b, n, 0.5, 0, 42)
+    want = O.step(m, w, pos, st, b, n, g, 1.0, mask)
+    got = NpaModel(m, w).step(pos, st, b, n, g, 1.0, update_mask=mask, ctx=bctx)
+    np.testing.assert_array_equal(to_np(got.density), want.density)
+    ep, es = rel_err(got.next_positions, want.next_positions), rel_err(got.next_states, want.next_states)
+    du = rel_err(to_np(got.next_states) - st, want.next_states - st)
+    print(f"{name}: bf16 engine step rel err pos={ep:.2e} state={es:.2e} update={du:.2e}")
+    assert ep <= STEP_TOL and es <= STEP_TOL and du <= STEP_TOL
+    off = mask == 0
+    np.testing.assert_array_equal(to_np(got.next_states)[off], want.next_states[off])
+
+
 def test_mfma_state_engine_and_errors(ctx):
     m, g, pos, st, w, b, n = _case("c1")
     ex = HipAutomataExecutor(ctx=ctx)
