@@ -269,13 +269,16 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
                                                    uint32_t* __restrict__ wl_count,
                                                    unsigned long long* __restrict__ scan_status,
                                                    uint32_t nstatus, SplitTargets T,
-                                                   int* __restrict__ tile_span) {
+                                                   int* __restrict__ tile_span, uint32_t pack) {
     extern __shared__ uint16_t cnt[];
     __shared__ int span_red[6][16];
     const uint32_t C = g.cells;
     // folded build (tile_span set): the tile's update-mask targets per key are counted too (u16
     // pairs after the rank counters) and go to the table's high half, and the tile's cell
-    // coordinate span goes to tile_span[tile] (min x, y, z, max x, y, z)
+    // coordinate span goes to tile_span[tile] (min x, y, z, max x, y, z). With pack (a wave ranks at
+    // most 128 particles, R <= 2) each wave's counter holds its count in the low byte and its
+    // targets in the high byte, so a target also gets its rank among the tile's targets of its key
+    // (ranks[i] = rank | target rank << 16) and no target counters are needed.
     const bool fold = tile_span != nullptr;
     uint32_t* mcnt = reinterpret_cast<uint32_t*>(cnt + ((waves * C + 1) & ~1u));
     const uint32_t tile = blockIdx.x;
@@ -289,7 +292,7 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
     const uint32_t nwords = waves * C;
     for (uint32_t k = threadIdx.x; k < nwords / 8; k += blockDim.x) reinterpret_cast<uint4*>(cnt)[k] = make_uint4(0, 0, 0, 0);
     for (uint32_t k = nwords / 8 * 8 + threadIdx.x; k < nwords; k += blockDim.x) cnt[k] = 0;
-    if (fold)
+    if (fold && !pack)
         for (uint32_t k = threadIdx.x; k < (C + 1) / 2; k += blockDim.x) mcnt[k] = 0u;
     if (wl_count && tile == 0)  // work-list counters and item queues
         for (uint32_t k = threadIdx.x; k < kWlWords; k += blockDim.x) wl_count[k] = 0;
@@ -354,11 +357,18 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
         if (active) {
             const uint32_t below = (uint32_t)__popcll(peers & lt);
             const uint32_t base = mine[key];
-            rank = base + below;
-            if ((peers >> lane) == 1ull) {
-                mine[key] = (uint16_t)(base + (uint32_t)__popcll(peers));
-                const uint32_t m = (uint32_t)__popcll(peers & tball);
-                if (m) atomicAdd(&mcnt[key >> 1], m << (16 * (key & 1u)));
+            if (pack) {
+                rank = (base & 0xffu) + below;
+                rank |= ((base >> 8) + (uint32_t)__popcll(peers & tball & lt)) << 16;
+                if ((peers >> lane) == 1ull)
+                    mine[key] = (uint16_t)(base + (uint32_t)__popcll(peers) + ((uint32_t)__popcll(peers & tball) << 8));
+            } else {
+                rank = base + below;
+                if ((peers >> lane) == 1ull) {
+                    mine[key] = (uint16_t)(base + (uint32_t)__popcll(peers));
+                    const uint32_t m = (uint32_t)__popcll(peers & tball);
+                    if (m) atomicAdd(&mcnt[key >> 1], m << (16 * (key & 1u)));
+                }
             }
         }
         key_r[r] = key;
@@ -392,7 +402,17 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
         const uint32_t li = wave_start + r * 64 + lane;
         if (ranker && li < n) {
             uint32_t prefix = 0;
-            for (uint32_t w2 = 0; w2 < w; ++w2) prefix += cnt[w2 * C + key_r[r]];
+            if (pack) {  // the earlier waves' counts and targets, field by field
+                uint32_t pt = 0;
+                for (uint32_t w2 = 0; w2 < w; ++w2) {
+                    const uint32_t v = cnt[w2 * C + key_r[r]];
+                    prefix += v & 0xffu;
+                    pt += v >> 8;
+                }
+                prefix |= pt << 16;
+            } else {
+                for (uint32_t w2 = 0; w2 < w; ++w2) prefix += cnt[w2 * C + key_r[r]];
+            }
             if (!keys_in) keys[sys_start + li] = key_r[r];
             ranks[sys_start + li] = prefix + rank_r[r];
         }
@@ -400,9 +420,19 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
     uint32_t* row = table + (uint64_t)tile * C;
     for (uint32_t k = threadIdx.x; k < C; k += blockDim.x) {
         uint32_t tot = 0;
-        for (uint32_t w2 = 0; w2 < waves; ++w2) tot += cnt[w2 * C + k];
-        // folded: the tile's targets of the key in the high half (a tile holds at most 32,768)
-        if (fold) tot |= ((mcnt[k >> 1] >> (16 * (k & 1u))) & 0xffffu) << 16;
+        if (pack) {
+            uint32_t tt = 0;
+            for (uint32_t w2 = 0; w2 < waves; ++w2) {
+                const uint32_t v = cnt[w2 * C + k];
+                tot += v & 0xffu;
+                tt += v >> 8;
+            }
+            tot |= tt << 16;
+        } else {
+            for (uint32_t w2 = 0; w2 < waves; ++w2) tot += cnt[w2 * C + k];
+            // folded: the tile's targets of the key in the high half (a tile holds at most 32,768)
+            if (fold) tot |= ((mcnt[k >> 1] >> (16 * (k & 1u))) & 0xffffu) << 16;
+        }
         row[k] = tot;
     }
     if (ovf) atomicOr(flags, 1u);
@@ -524,7 +554,7 @@ __global__ __launch_bounds__(256) void k_table_offsets_scan(uint32_t* __restrict
 // high half): per-tile count bases written back as full words; returns the count total and sets
 // *masked to the key's targets.
 __device__ __forceinline__ uint32_t column_scan_fold(uint32_t* __restrict__ col, uint32_t C, uint32_t tiles,
-                                                     uint32_t* masked) {
+                                                     uint32_t* masked, uint32_t pack) {
     uint32_t run = 0, mrun = 0, t = 0;
     for (; t + 32 <= tiles; t += 32) {
         uint32_t v[32];
@@ -532,7 +562,7 @@ __device__ __forceinline__ uint32_t column_scan_fold(uint32_t* __restrict__ col,
         for (int u = 0; u < 32; ++u) v[u] = col[(uint64_t)(t + u) * C];
 #pragma unroll
         for (int u = 0; u < 32; ++u) {
-            col[(uint64_t)(t + u) * C] = run;
+            col[(uint64_t)(t + u) * C] = pack ? run | (mrun << 16) : run;
             run += v[u] & 0xffffu;
             mrun += v[u] >> 16;
         }
@@ -543,14 +573,14 @@ __device__ __forceinline__ uint32_t column_scan_fold(uint32_t* __restrict__ col,
         for (int u = 0; u < 8; ++u) v[u] = col[(uint64_t)(t + u) * C];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            col[(uint64_t)(t + u) * C] = run;
+            col[(uint64_t)(t + u) * C] = pack ? run | (mrun << 16) : run;
             run += v[u] & 0xffffu;
             mrun += v[u] >> 16;
         }
     }
     for (; t < tiles; ++t) {
         const uint32_t v = col[(uint64_t)t * C];
-        col[(uint64_t)t * C] = run;
+        col[(uint64_t)t * C] = pack ? run | (mrun << 16) : run;
         run += v & 0xffffu;
         mrun += v >> 16;
     }
@@ -575,7 +605,7 @@ __global__ __launch_bounds__(256) void k_table_offsets_fold(uint32_t* __restrict
                                                             uint32_t* __restrict__ item_base,
                                                             uint32_t* __restrict__ row_next,
                                                             uint32_t* __restrict__ dir_n,
-                                                            uint32_t* __restrict__ wl_count) {
+                                                            uint32_t* __restrict__ wl_count, uint32_t pack) {
     __shared__ uint32_t wsum[3][4];
     __shared__ int span[6][4];
     __shared__ uint32_t s_pa, s_pb, s_pm, s_ticket;
@@ -586,7 +616,7 @@ __global__ __launch_bounds__(256) void k_table_offsets_fold(uint32_t* __restrict
     const uint32_t k = bx * 256 + threadIdx.x;
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     uint32_t run = 0, msk = 0;
-    if (k < C) run = column_scan_fold(table + k, C, tiles, &msk);
+    if (k < C) run = column_scan_fold(table + k, C, tiles, &msk, pack);
     const uint32_t itm = (run + (1u << tpi_log2) - 1) >> tpi_log2;
     // the system's cell coordinate span (Particle mode)
     int lo[3] = {INT32_MAX, INT32_MAX, INT32_MAX}, hi[3] = {INT32_MIN, INT32_MIN, INT32_MIN};
@@ -643,24 +673,29 @@ __global__ __launch_bounds__(256) void k_table_offsets_fold(uint32_t* __restrict
     // and first + size <= hi. Such bins are marked unsplit (walked with the cell filter, exact for
     // any bin); every other occupied bin holds one cell.
     bool alias = false;
-    if (g.mode == 1 && k < C) {
+    int sl[3], sh[3];
+    bool wide = false;  // some axis of the span wider than the grid (block-uniform)
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        sl[a] = INT32_MAX;
+        sh[a] = INT32_MIN;
+#pragma unroll
+        for (uint32_t v = 0; v < 4; ++v) {
+            sl[a] = min(sl[a], span[a][v]);
+            sh[a] = max(sh[a], span[3 + a][v]);
+        }
+        if (a < g.dim && sh[a] >= sl[a] && (int64_t)sh[a] - (int64_t)sl[a] >= (int64_t)g.size[a]) wide = true;
+    }
+    if (g.mode == 1 && wide && k < C && run) {
         uint32_t rest = k;
 #pragma unroll
         for (int a = 0; a < 3; ++a) {
-            int l = INT32_MAX, h = INT32_MIN;
-#pragma unroll
-            for (uint32_t v = 0; v < 4; ++v) {
-                l = min(l, span[a][v]);
-                h = max(h, span[3 + a][v]);
-            }
             if (a < g.dim) {
                 const int64_t m = (int64_t)g.size[a];
                 const int64_t r = (int64_t)(rest % g.size[a]);
                 rest /= g.size[a];
-                if (h >= l && (int64_t)h - (int64_t)l >= m) {
-                    const int64_t first = (int64_t)l + rem_euclid_i64(r - (int64_t)l, m);
-                    if (first + m <= (int64_t)h) alias = true;
-                }
+                const int64_t l = sl[a], h = sh[a];
+                if (h >= l && h - l >= m && l + rem_euclid_i64(r - l, m) + m <= h) alias = true;
             }
         }
     }
@@ -900,6 +935,9 @@ struct FoldOut {
     uint32_t* row_of = nullptr;
     int4* dir_e = nullptr;
     uint32_t tpi_log2 = 0;
+    // packed: table entries hold the tile's count | target prefixes << 16 and ranks[i] the rank |
+    // target rank << 16, so a target's compact row needs no atomic
+    uint32_t packed = 0;
 };
 
 // Copies nq (1, 2, 4, 6 or 8) float4s with every load issued before the first store.
@@ -986,7 +1024,8 @@ __global__ __launch_bounds__(256) void k_scatter_payload(uint32_t n, uint32_t to
     const uint32_t key = keys[i];
     const uint32_t t = li / tile;
     const uint32_t beg = bin_offsets[(uint64_t)b * C + key];
-    const uint32_t r_bin = table[((uint64_t)b * tiles_per_sys + t) * C + key] + ranks[i];  // rank in the bin
+    const uint32_t tv = table[((uint64_t)b * tiles_per_sys + t) * C + key], rv = ranks[i];
+    const uint32_t r_bin = F.packed ? (tv & 0xffffu) + (rv & 0xffffu) : tv + rv;  // rank in the bin
     const uint32_t dst = beg + r_bin;
     if (!F.item_base) out[dst] = i;
     const float p[4] = {p4.x, p4.y, p4.z, p4.w};
@@ -1003,7 +1042,7 @@ __global__ __launch_bounds__(256) void k_scatter_payload(uint32_t n, uint32_t to
     }
     if (F.item_base) {  // folded build (one system): what the split emits for the particle's bin
         if (tgt) {
-            const uint32_t row = atomicAdd(F.row_next + key, 1u);
+            const uint32_t row = F.packed ? F.row_next[key] + (tv >> 16) + (rv >> 16) : atomicAdd(F.row_next + key, 1u);
             F.act_rows[row] = dst;
             F.row_of[dst] = row;
         } else {
@@ -2259,7 +2298,7 @@ static hipError_t launch_rank_r(uint32_t blocks, uint32_t waves, uint32_t lds_by
                                 uint32_t n, uint32_t* keys, uint32_t* ranks, uint32_t* table,
                                 uint32_t* flags, uint32_t* wl_count, unsigned long long* scan_status,
                                 uint32_t nstatus, hipStream_t stream, Profiler* prof, const SplitTargets& T,
-                                int* tile_span) {
+                                int* tile_span, uint32_t pack) {
     if (lds_bytes > 32768) {
         static LdsLimitFlags limit;
         const hipError_t e = raise_lds_limit((const void*)k_hash_rank<R>, limit);
@@ -2270,7 +2309,7 @@ static hipError_t launch_rank_r(uint32_t blocks, uint32_t waves, uint32_t lds_by
     const uint32_t threads = g.cells >= 4096 ? 1024 : 256;
     return launch_timed(prof, NPA_KERNEL_HASH_RANK, k_hash_rank<R>, dim3(blocks), dim3(threads), lds_bytes, stream,
                         pos, keys_in, d_count, n, tiles_per_sys, waves, g, key_bits, keys, ranks, table, flags,
-                        wl_count, scan_status, nstatus, T, tile_span);
+                        wl_count, scan_status, nstatus, T, tile_span, pack);
 }
 
 static hipError_t launch_rank(uint32_t rounds, uint32_t blocks, uint32_t waves, uint32_t lds_bytes,
@@ -2279,11 +2318,12 @@ static hipError_t launch_rank(uint32_t rounds, uint32_t blocks, uint32_t waves, 
                               uint32_t n, uint32_t* keys, uint32_t* ranks, uint32_t* table,
                               uint32_t* flags, uint32_t* wl_count, unsigned long long* scan_status,
                               uint32_t nstatus, hipStream_t stream, Profiler* prof,
-                              const SplitTargets& T = SplitTargets{}, int* tile_span = nullptr) {
+                              const SplitTargets& T = SplitTargets{}, int* tile_span = nullptr,
+                              uint32_t pack = 0) {
 #define NPA_RANK(RR)                                                                             \
     return launch_rank_r<RR>(blocks, waves, lds_bytes, tiles_per_sys, key_bits, g, pos, keys_in, \
                              d_count, n, keys, ranks, table, flags, wl_count, scan_status, nstatus, stream, prof, \
-                             T, tile_span)
+                             T, tile_span, pack)
     switch (rounds) {
         case 1: NPA_RANK(1);
         case 2: NPA_RANK(2);
@@ -2315,13 +2355,18 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
     // the split would - its launch is saved
     // (its target counters take C u16 of LDS beside the rank counters: where both do not fit, fewer
     // waves rank the same tile in more rounds)
+    // Packed (a wave ranks at most 128 particles and the system's prefixes fit 16 bits): each wave's
+    // counters carry its targets too, so targets get ranks within their tile's key and the scatter
+    // computes their compact rows without atomics; only the rank counters take LDS.
     uint32_t rank_waves = plan.waves, rank_rounds = plan.rounds;
+    const uint32_t pack_lds = ((rank_waves * plan.cells + 1) & ~1u) * 2;
+    const bool pack = rank_rounds <= 2 && n <= 65536 && pack_lds + 1024 <= kMaxLdsBytes;
     auto fold_lds_of = [&](uint32_t wv) { return ((wv * plan.cells + 1) & ~1u) * 2 + (plan.cells + 1) / 2 * 4; };
-    while (fold_lds_of(rank_waves) + 1024 > kMaxLdsBytes && rank_waves > 1 && rank_rounds < 32) {
+    while (!pack && fold_lds_of(rank_waves) + 1024 > kMaxLdsBytes && rank_waves > 1 && rank_rounds < 32) {
         rank_waves /= 2;
         rank_rounds *= 2;
     }
-    const uint32_t fold_lds = fold_lds_of(rank_waves);
+    const uint32_t fold_lds = pack ? pack_lds : fold_lds_of(rank_waves);
     const bool fold = payload && batch == 1 && (g.mode != 1 || g.spatial) && (plan.tpi & (plan.tpi - 1)) == 0 &&
                       fold_lds + 1024 <= kMaxLdsBytes;
     if (!fold) {
@@ -2333,7 +2378,7 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                                ws.ranks.as<uint32_t>(), ws.table.as<uint32_t>(), ws.flags.as<uint32_t>(),
                                ws.wl_count.as<uint32_t>(), ws.scan_status.as<unsigned long long>(),
                                2 * batch * kblocks + 1,  // the status words and the scan's ticket counter
-                               stream, prof, tg, fold ? ws.tile_span.as<int>() : nullptr);
+                               stream, prof, tg, fold ? ws.tile_span.as<int>() : nullptr, fold && pack ? 1u : 0u);
     if (e != hipSuccess) return e;
     if (fold) {
         const uint32_t tpi_log2 = (uint32_t)__builtin_ctz(plan.tpi);
@@ -2341,7 +2386,7 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
                          ws.table.as<uint32_t>(), ws.bin_offsets.as<uint32_t>(),
                          ws.scan_status.as<unsigned long long>(), plan.cells, plan.tiles_per_sys, n, tpi_log2, g,
                          (const int*)ws.tile_span.as<int>(), ws.totals.as<uint32_t>(), ws.bin_list.as<uint32_t>(),
-                         ws.dir_n.as<uint32_t>(), ws.wl_count.as<uint32_t>());
+                         ws.dir_n.as<uint32_t>(), ws.wl_count.as<uint32_t>(), pack ? 1u : 0u);
         if (e != hipSuccess) return e;
         FoldOut F;
         F.item_base = ws.totals.as<uint32_t>();
@@ -2351,6 +2396,7 @@ hipError_t launch_hashgrid(const HashgridPlan& plan, const GridParams& g, const 
         F.row_of = ws.row_of.as<uint32_t>();
         F.dir_e = ws.dir_e.as<int4>();
         F.tpi_log2 = tpi_log2;
+        F.packed = pack ? 1u : 0u;
         auto scat = g.dim == 2 ? k_scatter_payload<2> : k_scatter_payload<3>;
         const uint32_t blocks = (uint32_t)((total + 255) / 256);
         return launch_timed(prof, NPA_KERNEL_SCATTER, scat, dim3(blocks), dim3(256), 0, stream, n, (uint32_t)total,
