@@ -664,6 +664,209 @@ __global__ __launch_bounds__(256) void k_density_lanes3(StepParams P, const floa
         }
     }
 }
+
+// The sparse pass with a 16-lane row per target (four targets per wave): a sparse grid (a surface in
+// a 32^3 grid, say) gives each target few candidates (about 56 at C4) behind 3^D run look-ups, so
+// the pass is set by its memory round trips, not by issue. Sixteen lanes per target look up the
+// cells in at most two steps (lane q: cells q and q + 16), form the runs' stream offsets and chunk
+// numbers with row scans, and test 16 candidates per round (lane q: stream position 16 r + q, four
+// rounds' records loaded together), the running sum rebuilt in candidate order from the row's 16
+// terms through DPP row_newbcast. Same sum, same order, same records as k_density_q.
+template <int K>
+__device__ __forceinline__ float row_lane(float v) {  // lane K of this lane's 16-lane row
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + K, 0xf, 0xf, false));
+}
+
+// Inclusive prefix sum over the 16 lanes of each row.
+__device__ __forceinline__ uint32_t row_scan16(uint32_t v, uint32_t q) {
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+        const uint32_t u = (uint32_t)__shfl_up((int)v, off, 16);
+        if (q >= (uint32_t)off) v += u;
+    }
+    return v;
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void k_density_rows(StepParams P, const float4* __restrict__ srec,
+                                                       const int4* __restrict__ scoord,
+                                                       const uint32_t* __restrict__ bo,
+                                                       const uint32_t* __restrict__ perm,
+                                                       const uint32_t* __restrict__ row_of,
+                                                       float4* __restrict__ svol, float* __restrict__ density_out,
+                                                       uint32_t* __restrict__ nb_base, uint64_t* __restrict__ nb_mask,
+                                                       uint32_t* __restrict__ nb_count) {
+    constexpr uint32_t MAXC = max_chunks(D);
+    constexpr int NC = D == 3 ? 27 : 9;  // neighbour cells
+    constexpr uint32_t SW = D == 3 ? kStreamWords3 : kStreamWords;
+    static_assert(MAXC * 64 == SW * 32, "the stream holds every recorded chunk");
+    struct Runs {
+        uint32_t pre[NC + 1];  // stream position of run k's first candidate; pre[NC] = the total
+        uint32_t beg[NC];      // run k's first slot
+        uint32_t gch[NC + 1];  // run k's first chunk number; gch[NC] = the chunk count
+    };
+    __shared__ Runs runs_lds[4][4];
+    __shared__ uint32_t stream_lds[4][4][SW + 1];
+    const uint32_t lane = threadIdx.x & 63, t = lane >> 4, q = lane & 15;
+    const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    Runs& R = runs_lds[threadIdx.x >> 6][t];
+    uint32_t* stream = stream_lds[threadIdx.x >> 6][t];
+    const uint32_t s_raw = wave * 4 + t;
+    if (wave * 4 >= P.T) return;  // (wave-uniform)
+    const bool active = s_raw < P.T;
+    const uint32_t s = active ? s_raw : P.T - 1;
+    const uint32_t b = s / P.N;
+    float pi[3];
+    int ci[3];
+    load_rec<D>(srec, scoord, s, pi, ci);
+    const uint32_t row = active ? row_of[s] : ~0u;
+    const bool record = row != ~0u;
+    // ---- look-ups: lane q, cells q and q + 16 (visit order k = (dz + 1) * 9 + (dy + 1) * 3 + (dx + 1))
+    uint32_t beg[2] = {0u, 0u}, len[2] = {0u, 0u}, fbits = 0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const uint32_t k = q + 16 * u;
+        uint32_t bb = 0, ee = 0;
+        bool filt = false;
+        if (k < (uint32_t)NC && active &&
+            cell_range(P, bo, b, (int64_t)ci[0] + (int)(k % 3) - 1, (int64_t)ci[1] + (int)((k / 3) % 3) - 1,
+                       D == 3 ? (int64_t)ci[2] + (int)(k / 9) - 1 : 0, bb, ee, filt)) {
+            beg[u] = bb;
+            len[u] = ee - bb;
+            fbits |= (filt ? 1u : 0u) << k;
+        }
+    }
+    // the row's filter bits, stream offsets and chunk numbers (exclusive prefixes over k)
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) fbits |= (uint32_t)__shfl_xor((int)fbits, off, 16);
+    const uint32_t ch0 = (len[0] + 63) / 64, ch1 = (len[1] + 63) / 64;
+    const uint32_t x0 = row_scan16(len[0], q), x1 = row_scan16(len[1], q);
+    const uint32_t y0 = row_scan16(ch0, q), y1 = row_scan16(ch1, q);
+    const uint32_t tot0 = (uint32_t)__shfl((int)x0, 15, 16), tch0 = (uint32_t)__shfl((int)y0, 15, 16);
+    const uint32_t tot1 = (uint32_t)__shfl((int)x1, 15, 16), tch1 = (uint32_t)__shfl((int)y1, 15, 16);
+    if (q < (uint32_t)NC) {
+        R.pre[q] = x0 - len[0];
+        R.beg[q] = beg[0];
+        R.gch[q] = y0 - ch0;
+    }
+    if (q + 16 < (uint32_t)NC) {
+        R.pre[q + 16] = tot0 + x1 - len[1];
+        R.beg[q + 16] = beg[1];
+        R.gch[q + 16] = tch0 + y1 - ch1;
+    }
+    if (q == 0) {
+        R.pre[NC] = tot0 + tot1;
+        R.gch[NC] = tch0 + tch1;
+    }
+    lds_wave_sync();
+    const uint32_t total = tot0 + tot1;
+    uint32_t rounds = (total + 15) / 16;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) rounds = max(rounds, (uint32_t)__shfl_xor((int)rounds, off, 64));
+    const bool any_filter = __ballot(fbits != 0) != 0ull;
+    const float eps2 = P.g.eps2, k6 = P.g.k6;
+    const bool periodic = P.g.boundary == 0;
+    float rho = 0.0f;
+    uint32_t kk = 0, knext = R.pre[1];  // the run of this lane's stream position, and where the next starts
+    for (uint32_t r0 = 0; r0 < rounds; r0 += 4) {
+        float4 rc[4];
+        int4 cc[4];
+        bool ok[4];
+        uint32_t kr[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t j = 16 * (r0 + u) + q;
+            ok[u] = active && j < total;
+            if (ok[u])
+                while (j >= knext) {  // advance to the run holding position j (empty runs skipped)
+                    ++kk;
+                    knext = R.pre[kk + 1];
+                }
+            const uint32_t slot = ok[u] ? R.beg[kk] + (j - R.pre[kk]) : s;
+            kr[u] = kk;
+            rc[u] = srec[slot];
+            cc[u] = D == 3 && any_filter ? scoord[slot] : make_int4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (r0 + u >= rounds) break;
+            bool acc_ok = ok[u];
+            if (any_filter && ((fbits >> kr[u]) & 1u)) {  // an unsplit bin: keep this cell's particles
+                const int k = (int)kr[u];
+                if constexpr (D == 3)
+                    acc_ok = acc_ok && (int64_t)cc[u].x == (int64_t)ci[0] + k % 3 - 1 &&
+                             (int64_t)cc[u].y == (int64_t)ci[1] + (k / 3) % 3 - 1 &&
+                             (int64_t)cc[u].z == (int64_t)ci[2] + k / 9 - 1;
+                else  // 2D records carry the cell coordinates' bits in z and w
+                    acc_ok = acc_ok && (int64_t)__float_as_int(rc[u].z) == (int64_t)ci[0] + k % 3 - 1 &&
+                             (int64_t)__float_as_int(rc[u].w) == (int64_t)ci[1] + k / 3 - 1;
+            }
+            float d0 = rc[u].x - pi[0], d1 = rc[u].y - pi[1], d2 = D == 3 ? rc[u].z - pi[2] : 0.0f;
+            if (periodic) {
+                d0 = delta_axis(pi[0], rc[u].x, 0, P.g);
+                d1 = delta_axis(pi[1], rc[u].y, 1, P.g);
+                if constexpr (D == 3) d2 = delta_axis(pi[2], rc[u].z, 2, P.g);
+            }
+            float r2 = d0 * d0;
+            r2 += d1 * d1;
+            if constexpr (D == 3) r2 += d2 * d2;
+            const bool near = acc_ok && r2 < eps2;
+            const float x = eps2 - r2;
+            const float term = near ? k6 * x * x * x : 0.0f;  // smoothing_poly6_kernel
+            // the running sum in candidate order: lane 0's term first (a rejected one adds +0.0)
+            rho += row_lane<0>(term);
+            rho += row_lane<1>(term);
+            rho += row_lane<2>(term);
+            rho += row_lane<3>(term);
+            rho += row_lane<4>(term);
+            rho += row_lane<5>(term);
+            rho += row_lane<6>(term);
+            rho += row_lane<7>(term);
+            rho += row_lane<8>(term);
+            rho += row_lane<9>(term);
+            rho += row_lane<10>(term);
+            rho += row_lane<11>(term);
+            rho += row_lane<12>(term);
+            rho += row_lane<13>(term);
+            rho += row_lane<14>(term);
+            rho += row_lane<15>(term);
+            const uint64_t bal = __builtin_amdgcn_ballot_w64(near);
+            const uint32_t r = r0 + u;
+            // the target's 16 accept bits = stream bits 16 r .. 16 r + 15
+            const uint32_t bits = (uint32_t)(bal >> (16 * t)) & 0xffffu;
+            if (q == 0 && r / 2 < SW) {
+                if ((r & 1u) == 0) stream[r / 2] = bits;
+                else stream[r / 2] |= bits << 16;
+            }
+        }
+    }
+    if (active && q == 0) {
+        svol[s] = make_float4(pi[0], pi[1], pi[2], recip_finite(rho));
+        if (density_out) density_out[b * P.N + perm[s]] = rho;
+    }
+    if (!__ballot(record)) return;
+    lds_wave_sync();
+    if (!record) return;
+    if (q == 0) nb_count[row] = R.gch[NC];
+    const uint32_t used = min((total + 31) / 32, SW);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const uint32_t k = q + 16 * u;
+        if (k >= (uint32_t)NC) break;
+        const uint32_t rl = R.pre[k + 1] - R.pre[k], g0 = R.gch[k];
+        for (uint32_t c = 0; 64 * c < rl && g0 + c < MAXC; ++c) {
+            const uint32_t a = R.pre[k] + 64 * c;  // stream bit of the chunk's first candidate
+            const uint32_t L = min(64u, rl - 64 * c);
+            const uint32_t w0 = a / 32, sh = a % 32;
+            const uint64_t lo = (uint64_t)(w0 < used ? stream[w0] : 0u) | ((uint64_t)(w0 + 1 < used ? stream[w0 + 1] : 0u) << 32);
+            const uint64_t hi = w0 + 2 < used ? stream[w0 + 2] : 0u;
+            uint64_t m = sh ? (lo >> sh) | (hi << (64 - sh)) : lo;
+            if (L < 64) m &= (1ull << L) - 1ull;
+            nb_base[(uint64_t)row * MAXC + g0 + c] = R.beg[k] + 64 * c;
+            nb_mask[(uint64_t)row * MAXC + g0 + c] = m;
+        }
+    }
+}
 #endif  // NPA_PART_MAIN
 
 // Per-wave accepted-neighbour lists of the second pass: the sorted slots of each target's accepted
@@ -1619,7 +1822,21 @@ hipError_t launch_density(const StepParams& p_in, Workspace& ws, float* density_
                           hipStream_t stream, Profiler* prof) {
     const StepParams p = with_directory(p_in, ws);
     // sparse grids (fewer than 4 particles per cell in 2D, fewer than 1 in 3D): a wave per cell run
-    // would leave most of its lanes idle, so four lanes serve one target and a wave 16 slots
+    // would leave most of its lanes idle, so each target takes a group of lanes. Systems of at most
+    // 64 targets per CU (C1, C4): a 16-lane row per target, since those
+    // passes are set by their memory round trips (C1 9.3 -> 6.7 us, C4 32.0 -> 16.5 us against four
+    // lanes per target); larger ones (C5: 38.0 against 53.4 us) keep four lanes, the fewer
+    // instructions per candidate
+    const bool rows = (uint64_t)p.T <= 64ull * (uint64_t)device_cu_count();
+    const bool sparse = p.g.dim == 2 ? (uint64_t)p.B * p.g.cells * 4 > p.T : (uint64_t)p.B * p.g.cells > p.T;
+    if (sparse && rows) {
+        const uint32_t waves = (p.T + 3) / 4;
+        auto k = p.g.dim == 2 ? k_density_rows<2> : k_density_rows<3>;
+        return launch_timed(prof, NPA_KERNEL_DENSITY, k, dim3((waves + 3) / 4), dim3(256), 0, stream, p,
+                            ws.srec.as<float4>(), ws.scoord.as<int4>(), ws.bin_offsets.as<uint32_t>(),
+                            ws.perm.as<uint32_t>(), ws.row_of.as<uint32_t>(), ws.svol.as<float4>(), density_out,
+                            ws.nb_base.as<uint32_t>(), ws.nb_mask.as<uint64_t>(), ws.nb_count.as<uint32_t>());
+    }
     if (p.g.dim == 2 && (uint64_t)p.B * p.g.cells * 4 > p.T) {  // four lanes per target, 16 per wave
         const uint32_t waves = (p.T + 15) / 16;
         return launch_timed(prof, NPA_KERNEL_DENSITY, k_density_lanes<2>, dim3((waves + 3) / 4), dim3(256), 0, stream,

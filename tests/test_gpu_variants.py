@@ -45,6 +45,9 @@ GRIDS = {
     "particle2_strip_sparse": (HashGridConfig(2, C, PART, (64, 64, 1), 0.05), 3000, -1.0),
     "particle3_strip_sparse": (HashGridConfig(3, C, PART, (32, 32, 32), 0.1), 3000, -1.0),
     "particle2_strip_dense": (HashGridConfig(2, C, PART, (16, 16, 1), 0.05), 6000, -1.0),
+    # sparse 3D with more than 64 targets per CU: the four-lane sparse density pass (smaller sparse
+    # systems take sixteen lanes per target)
+    "particle3_sparse_large": (HashGridConfig(3, C, PART, (32, 32, 32), 0.1), 20000, 1.2),
 }
 
 
@@ -124,7 +127,8 @@ def test_euler_step_bit_exact(ctx, name):
 
 STEP_CASES = [(name, dg) for name in ("grid3_periodic", "particle3_periodic", "grid3_clamped",
                                       "particle2_periodic", "grid2_periodic_small", "particle2_strip_sparse",
-                                      "particle3_strip_sparse", "particle2_strip_dense") for dg in (False, True)]
+                                      "particle3_strip_sparse", "particle2_strip_dense", "particle3_sparse_large")
+              for dg in (False, True)]
 
 
 def _step_case(name, density_grad):
