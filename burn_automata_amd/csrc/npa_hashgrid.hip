@@ -1967,11 +1967,12 @@ static hipError_t launch_sys_r(const GridParams& g, const HashgridPlan& plan, co
 //                 both in whatever order the atomics land; the cell coordinate span (six atomic
 //                 maxima); block 0 clears the work-list counters, every block its share of the
 //                 offsets scan's status words;
-//   k_bin_scan    per bin: the exclusive prefixes of the counts (bin_offsets), of the work items
-//                 (ceil(count / tpi) items of <= tpi slots, as the split emits for a bin of one
-//                 cell or an unsplit bin) and of the targets (the bin's first compact row), with
-//                 decoupled look-back over ticket-ordered blocks; the directory sizes; it resets the
-//                 counters and the span for the next build;
+//   k_bin_scan    per bin (4,096 per 1024-thread block, four per thread): the exclusive prefixes
+//                 of the counts (bin_offsets), of the work items (ceil(count / tpi) items of <= tpi
+//                 slots, as the split emits for a bin of one cell or an unsplit bin) and of the
+//                 targets (the bin's first compact row), with decoupled look-back over
+//                 ticket-ordered blocks; the directory sizes; it resets the counters and the span
+//                 for the next build;
 //   k_bin_place   per particle: members[bin start + place] = particle;
 //   k_bin_scatter per particle: its rank in the bin = the bin's members with a smaller index (the
 //                 reference's order within a bin), hence its slot; then what k_scatter_payload
@@ -2041,27 +2042,37 @@ __global__ __launch_bounds__(256) void k_bin_count(const float4* __restrict__ po
     }
 }
 
-__global__ __launch_bounds__(256) void k_bin_scan(unsigned long long* __restrict__ count, uint32_t* __restrict__ span,
-                                                  uint32_t C, uint32_t tpi_log2, GridParams g,
-                                                  unsigned long long* __restrict__ status,
-                                                  uint32_t* __restrict__ bin_offsets, uint32_t* __restrict__ item_base,
-                                                  uint32_t* __restrict__ row_base, uint32_t* __restrict__ dir_n,
-                                                  uint32_t* __restrict__ wl_count) {
-    __shared__ uint32_t wsum[3][4];
+__global__ __launch_bounds__(1024) void k_bin_scan(unsigned long long* __restrict__ count, uint32_t* __restrict__ span,
+                                                   uint32_t C, uint32_t tpi_log2, GridParams g,
+                                                   unsigned long long* __restrict__ status,
+                                                   uint32_t* __restrict__ bin_offsets, uint32_t* __restrict__ item_base,
+                                                   uint32_t* __restrict__ row_base, uint32_t* __restrict__ dir_n,
+                                                   uint32_t* __restrict__ wl_count) {
+    // 4,096 keys per block, four per thread (thread t: keys 4t .. 4t + 3 of the block's range)
+    __shared__ uint32_t red[3][16];
     __shared__ int s_span[6];
     __shared__ uint32_t s_pa, s_pb, s_pm, s_ticket;
-    const uint32_t nb = gridDim.x;
-    if (threadIdx.x == 0) s_ticket = (uint32_t)atomicAdd(status + 2ull * nb, 1ull);
-    if (threadIdx.x < 6) s_span[threadIdx.x] = threadIdx.x < 3 ? span_lo(span[threadIdx.x]) : span_hi(span[threadIdx.x]);
+    const uint32_t nb = gridDim.x, tid = threadIdx.x;
+    if (tid == 0) s_ticket = (uint32_t)atomicAdd(status + 2ull * nb, 1ull);
+    if (tid < 6) s_span[tid] = tid < 3 ? span_lo(span[tid]) : span_hi(span[tid]);
     __syncthreads();
     const uint32_t bx = s_ticket;
-    const uint32_t k = bx * 256 + threadIdx.x;
-    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const unsigned long long v = k < C ? count[k] : 0ull;
-    if (v) count[k] = 0ull;  // ready for the next build
-    const uint32_t run = (uint32_t)v, msk = (uint32_t)(v >> 32);
-    const uint32_t itm = (run + (1u << tpi_log2) - 1) >> tpi_log2;
-    uint32_t xa = run, xb = itm, xm = msk;
+    const uint32_t k0 = (bx * 1024 + tid) * 4;
+    const uint32_t lane = tid & 63, w = tid >> 6;
+    uint32_t run[4], msk[4], itm[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t k = k0 + q;
+        const unsigned long long v = k < C ? count[k] : 0ull;
+        if (v) count[k] = 0ull;  // ready for the next build
+        run[q] = (uint32_t)v;
+        msk[q] = (uint32_t)(v >> 32);
+        itm[q] = (run[q] + (1u << tpi_log2) - 1) >> tpi_log2;
+    }
+    const uint32_t sa = run[0] + run[1] + run[2] + run[3];
+    const uint32_t sb = itm[0] + itm[1] + itm[2] + itm[3];
+    const uint32_t sm = msk[0] + msk[1] + msk[2] + msk[3];
+    uint32_t xa = sa, xb = sb, xm = sm;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
         const uint32_t ya = __shfl_up(xa, off, 64), yb = __shfl_up(xb, off, 64), ym = __shfl_up(xm, off, 64);
@@ -2072,23 +2083,32 @@ __global__ __launch_bounds__(256) void k_bin_scan(unsigned long long* __restrict
         }
     }
     if (lane == 63) {
-        wsum[0][w] = xa;
-        wsum[1][w] = xb;
-        wsum[2][w] = xm;
+        red[0][w] = xa;
+        red[1][w] = xb;
+        red[2][w] = xm;
     }
     __syncthreads();
-    uint32_t pa = 0, pb = 0, pm = 0, ta = 0, tb = 0, tm = 0;
-#pragma unroll
-    for (uint32_t u = 0; u < 4; ++u) {
-        if (u < w) {
-            pa += wsum[0][u];
-            pb += wsum[1][u];
-            pm += wsum[2][u];
-        }
-        ta += wsum[0][u];
-        tb += wsum[1][u];
-        tm += wsum[2][u];
+    // lane v < 16 holds wave v's sums: a 16-lane inclusive scan gives every wave its prefix
+    uint32_t ea = 0, eb = 0, em = 0;
+    if (lane < 16) {
+        ea = red[0][lane];
+        eb = red[1][lane];
+        em = red[2][lane];
     }
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+        const uint32_t ya = __shfl_up(ea, off, 64), yb = __shfl_up(eb, off, 64), ym = __shfl_up(em, off, 64);
+        if (lane >= (uint32_t)off) {
+            ea += ya;
+            eb += yb;
+            em += ym;
+        }
+    }
+    const uint32_t pa = w ? (uint32_t)__shfl((int)ea, (int)w - 1, 64) : 0u;  // earlier waves' sums
+    const uint32_t pb = w ? (uint32_t)__shfl((int)eb, (int)w - 1, 64) : 0u;
+    const uint32_t pm = w ? (uint32_t)__shfl((int)em, (int)w - 1, 64) : 0u;
+    const uint32_t ta = (uint32_t)__shfl((int)ea, 15, 64), tb = (uint32_t)__shfl((int)eb, 15, 64);
+    const uint32_t tm = (uint32_t)__shfl((int)em, 15, 64);
     // A coordinate bin (residues r_a = c_a mod size_a) can hold two cells only if on some axis two
     // coordinates of the span [lo, hi] share its residue: first = lo + ((r - lo) mod size) and
     // first + size <= hi. Such bins are marked unsplit (walked in the reference order with the cell
@@ -2097,8 +2117,8 @@ __global__ __launch_bounds__(256) void k_bin_scan(unsigned long long* __restrict
 #pragma unroll
     for (int a = 0; a < 3; ++a)
         if (a < g.dim && s_span[3 + a] >= s_span[a] && (int64_t)s_span[3 + a] - s_span[a] >= (int64_t)g.size[a]) wide = true;
-    bool alias = false;
-    if (g.mode == 1 && wide && k < C && run) {
+    auto alias_of = [&](uint32_t k) {
+        bool al = false;
         uint32_t rest = k;
 #pragma unroll
         for (int a = 0; a < 3; ++a) {
@@ -2107,11 +2127,12 @@ __global__ __launch_bounds__(256) void k_bin_scan(unsigned long long* __restrict
                 const int64_t r = (int64_t)(rest % g.size[a]);
                 rest /= g.size[a];
                 const int64_t l = s_span[a], h = s_span[3 + a];
-                if (h >= l && h - l >= m && l + rem_euclid_i64(r - l, m) + m <= h) alias = true;
+                if (h >= l && h - l >= m && l + rem_euclid_i64(r - l, m) + m <= h) al = true;
             }
         }
-    }
-    if (threadIdx.x == 0) {
+        return al;
+    };
+    if (tid == 0) {
         __hip_atomic_store(status + bx, (1ull << 63) | ta, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(status + nb + bx, (1ull << 63) | tb | ((unsigned long long)tm << 31), __ATOMIC_RELEASE,
                            __HIP_MEMORY_SCOPE_AGENT);
@@ -2121,16 +2142,16 @@ __global__ __launch_bounds__(256) void k_bin_scan(unsigned long long* __restrict
         for (uint32_t base = 0; base < bx; base += 64) {
             const uint32_t j = base + lane;
             if (j < bx) {
-                unsigned long long sa, sb;
+                unsigned long long qa, qb;
                 do {
-                    sa = __hip_atomic_load(status + j, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-                } while (!(sa >> 63));
+                    qa = __hip_atomic_load(status + j, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+                } while (!(qa >> 63));
                 do {
-                    sb = __hip_atomic_load(status + nb + j, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-                } while (!(sb >> 63));
-                acc_a += (uint32_t)sa;
-                acc_b += (uint32_t)(sb & 0x7fffffffull);
-                acc_m += (uint32_t)((sb >> 31) & 0x7fffffffull);
+                    qb = __hip_atomic_load(status + nb + j, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+                } while (!(qb >> 63));
+                acc_a += (uint32_t)qa;
+                acc_b += (uint32_t)(qb & 0x7fffffffull);
+                acc_m += (uint32_t)((qb >> 31) & 0x7fffffffull);
             }
         }
 #pragma unroll
@@ -2146,19 +2167,27 @@ __global__ __launch_bounds__(256) void k_bin_scan(unsigned long long* __restrict
         }
     }
     __syncthreads();
-    if (k < C) {
-        bin_offsets[k] = s_pa + pa + xa - run;
-        item_base[k] = s_pb + pb + xb - itm;
-        row_base[k] = s_pm + pm + xm - msk;
-        if (g.mode == 1) dir_n[k] = run ? (alias ? kDirGroups + 1 : 1u) : 0u;
+    uint32_t st = s_pa + pa + xa - sa, it = s_pb + pb + xb - sb, rw = s_pm + pm + xm - sm;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t k = k0 + q;
+        if (k < C) {
+            bin_offsets[k] = st;
+            item_base[k] = it;
+            row_base[k] = rw;
+            if (g.mode == 1) dir_n[k] = run[q] ? (wide && alias_of(k) ? kDirGroups + 1 : 1u) : 0u;
+        }
+        st += run[q];
+        it += itm[q];
+        rw += msk[q];
     }
     // the last ticket: every other block has read the span and published (its look-back saw them all)
-    if (bx == nb - 1 && threadIdx.x == 0) {
+    if (bx == nb - 1 && tid == 0) {
         bin_offsets[C] = s_pa + ta;
         wl_count[0] = s_pb + tb;
         wl_count[1] = s_pm + tm;
     }
-    if (bx == nb - 1 && threadIdx.x < 6) span[threadIdx.x] = 0u;
+    if (bx == nb - 1 && tid < 6) span[tid] = 0u;
 }
 
 __global__ __launch_bounds__(256) void k_bin_place(uint32_t n, const uint32_t* __restrict__ keys,
@@ -2235,7 +2264,7 @@ __global__ __launch_bounds__(256) void k_clear_u64(unsigned long long* __restric
 static hipError_t launch_bins(const HashgridPlan& plan, const GridParams& g, const float4* pos, const float* states,
                               uint32_t S, uint32_t n, Workspace& ws, const SplitTargets& tg, hipStream_t stream,
                               Profiler* prof) {
-    const uint32_t C = plan.cells, blocks = (n + 255) / 256, kblocks = (C + 255) / 256;
+    const uint32_t C = plan.cells, blocks = (n + 255) / 256, kblocks = (C + 4095) / 4096;
     const uint32_t tpi_log2 = (uint32_t)__builtin_ctz(plan.tpi);
     unsigned long long* count = ws.bin_count.as<unsigned long long>();
     uint32_t* span = reinterpret_cast<uint32_t*>(count + C);
@@ -2251,7 +2280,7 @@ static hipError_t launch_bins(const HashgridPlan& plan, const GridParams& g, con
                      ws.bin_urow.as<uint32_t>(), ws.wl_count.as<uint32_t>(), ws.scan_status.as<unsigned long long>(),
                      2 * kblocks + 1, ws.flags.as<uint32_t>());
     if (e != hipSuccess) return e;
-    e = launch_timed(prof, NPA_KERNEL_TABLE_SCAN, k_bin_scan, dim3(kblocks), dim3(256), 0, stream, count, span, C,
+    e = launch_timed(prof, NPA_KERNEL_TABLE_SCAN, k_bin_scan, dim3(kblocks), dim3(1024), 0, stream, count, span, C,
                      tpi_log2, g, ws.scan_status.as<unsigned long long>(), ws.bin_offsets.as<uint32_t>(),
                      ws.totals.as<uint32_t>(), ws.bin_list.as<uint32_t>(), ws.dir_n.as<uint32_t>(),
                      ws.wl_count.as<uint32_t>());
