@@ -416,11 +416,13 @@ __global__ __launch_bounds__(1024) void k_update_fused(StepParams P, const float
             }
             uint32_t en = mylist[c];
             float4 rj = svol[en];
+            // rounds in which this lane's entry 16 r + c is a list entry: r < lim
+            const uint32_t lim = active && cnt > c ? (cnt - c + 15u) / 16u : 0u;
             for (uint32_t r = 0; r < nr; ++r) {
-                const uint32_t rn = r + 1 < nrg ? r + 1 : nrg - 1;  // next round (always a valid entry)
+                const uint32_t rn = min(r + 1, nrg - 1);  // next round (always a valid entry; nrg >= 1)
                 const uint32_t* lpn = mylist + 16 * rn;
                 // this lane's entry: pair scalars, branch-free; a padding entry gets zero weights
-                const bool has = active && 16 * r + c < cnt;
+                const bool has = r < lim;
                 float d[3];
                 d[0] = delta(pi[0], rj.x, 0);
                 d[1] = delta(pi[1], rj.y, 1);
