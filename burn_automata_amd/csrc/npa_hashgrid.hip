@@ -1808,20 +1808,33 @@ __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restri
     }
     if (k0 < C) {
         uint32_t st = pa + xa - sa, it = pb + xb - sb, rw = pm + xm - sm;
-        uint32_t sv[4], rv[4];
+        uint32_t sv[4], rv[4], ov[4], iv[4], dv[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint32_t k = k0 + q;
             sv[q] = st;
             rv[q] = rw;
-            if (k < C) {
-                bin_offsets[(uint64_t)b * C + k] = b * n + st;
-                sys_item[(uint64_t)b * C + k] = it;
-                if (g.mode == 1) dir_n[(uint64_t)b * C + k] = tot[q] ? (wide && may_alias(k) ? K + 1 : 1u) : 0u;
-            }
+            ov[q] = b * n + st;
+            iv[q] = it;
+            dv[q] = k < C && g.mode == 1 && tot[q] ? (wide && may_alias(k) ? K + 1 : 1u) : 0u;
             st += tot[q];
             it += itm[q];
             rw += msk[q];
+        }
+        const uint64_t at = (uint64_t)b * C + k0;
+        if (k0 + 3 < C && (C & 3u) == 0) {  // one 16-byte store per array (aligned when C % 4 == 0)
+            *reinterpret_cast<uint4*>(bin_offsets + at) = make_uint4(ov[0], ov[1], ov[2], ov[3]);
+            *reinterpret_cast<uint4*>(sys_item + at) = make_uint4(iv[0], iv[1], iv[2], iv[3]);
+            if (g.mode == 1) *reinterpret_cast<uint4*>(dir_n + at) = make_uint4(dv[0], dv[1], dv[2], dv[3]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (k0 + q < C) {
+                    bin_offsets[at + q] = ov[q];
+                    sys_item[at + q] = iv[q];
+                    if (g.mode == 1) dir_n[at + q] = dv[q];
+                }
+            }
         }
         reinterpret_cast<uint4*>(sstart)[tid] = make_uint4(sv[0], sv[1], sv[2], sv[3]);
         reinterpret_cast<uint4*>(srow)[tid] = make_uint4(rv[0], rv[1], rv[2], rv[3]);
@@ -2168,18 +2181,34 @@ __global__ __launch_bounds__(1024) void k_bin_scan(unsigned long long* __restric
     }
     __syncthreads();
     uint32_t st = s_pa + pa + xa - sa, it = s_pb + pb + xb - sb, rw = s_pm + pm + xm - sm;
+    uint32_t ov[4], iv[4], rv[4], dv[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint32_t k = k0 + q;
-        if (k < C) {
-            bin_offsets[k] = st;
-            item_base[k] = it;
-            row_base[k] = rw;
-            if (g.mode == 1) dir_n[k] = run[q] ? (wide && alias_of(k) ? kDirGroups + 1 : 1u) : 0u;
-        }
+        ov[q] = st;
+        iv[q] = it;
+        rv[q] = rw;
+        dv[q] = k < C && g.mode == 1 && run[q] ? (wide && alias_of(k) ? kDirGroups + 1 : 1u) : 0u;
         st += run[q];
         it += itm[q];
         rw += msk[q];
+    }
+    if (k0 + 3 < C) {  // the thread's four keys with one 16-byte store per array
+        *reinterpret_cast<uint4*>(bin_offsets + k0) = make_uint4(ov[0], ov[1], ov[2], ov[3]);
+        *reinterpret_cast<uint4*>(item_base + k0) = make_uint4(iv[0], iv[1], iv[2], iv[3]);
+        *reinterpret_cast<uint4*>(row_base + k0) = make_uint4(rv[0], rv[1], rv[2], rv[3]);
+        if (g.mode == 1) *reinterpret_cast<uint4*>(dir_n + k0) = make_uint4(dv[0], dv[1], dv[2], dv[3]);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t k = k0 + q;
+            if (k < C) {
+                bin_offsets[k] = ov[q];
+                item_base[k] = iv[q];
+                row_base[k] = rv[q];
+                if (g.mode == 1) dir_n[k] = dv[q];
+            }
+        }
     }
     // the last ticket: every other block has read the span and published (its look-back saw them all)
     if (bx == nb - 1 && tid == 0) {
