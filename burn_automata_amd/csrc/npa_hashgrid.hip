@@ -2073,11 +2073,22 @@ __global__ __launch_bounds__(1024) void k_bin_scan(unsigned long long* __restric
     const uint32_t k0 = (bx * 1024 + tid) * 4;
     const uint32_t lane = tid & 63, w = tid >> 6;
     uint32_t run[4], msk[4], itm[4];
+    unsigned long long cv[4];
+    if (k0 + 3 < C) {  // the thread's four counters in two 16-byte loads
+        const ulonglong2 a = reinterpret_cast<const ulonglong2*>(count + k0)[0];
+        const ulonglong2 c2 = reinterpret_cast<const ulonglong2*>(count + k0)[1];
+        cv[0] = a.x;
+        cv[1] = a.y;
+        cv[2] = c2.x;
+        cv[3] = c2.y;
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) cv[q] = k0 + q < C ? count[k0 + q] : 0ull;
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const uint32_t k = k0 + q;
-        const unsigned long long v = k < C ? count[k] : 0ull;
-        if (v) count[k] = 0ull;  // ready for the next build
+        const unsigned long long v = cv[q];
+        if (v) count[k0 + q] = 0ull;  // ready for the next build
         run[q] = (uint32_t)v;
         msk[q] = (uint32_t)(v >> 32);
         itm[q] = (run[q] + (1u << tpi_log2) - 1) >> tpi_log2;
