@@ -418,6 +418,44 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
         }
     }
     uint32_t* row = table + (uint64_t)tile * C;
+    if (pack && (C & 3u) == 0) {
+        // four consecutive keys per thread: one 8-byte LDS read per wave row and one 16-byte store
+        // (C % 4 == 0 keeps every wave row's keys 8-byte aligned)
+        for (uint32_t k4 = 4 * threadIdx.x; k4 < C; k4 += 4 * blockDim.x) {
+            uint32_t c01 = 0, c23 = 0, t01 = 0, t23 = 0;  // counts and targets, two keys per word
+            for (uint32_t w2 = 0; w2 < waves; ++w2) {
+                const uint2 v = *reinterpret_cast<const uint2*>(cnt + w2 * C + k4);
+                // each u16: count in the low byte, targets in the high byte
+                c01 += v.x & 0x00ff00ffu;
+                t01 += (v.x >> 8) & 0x00ff00ffu;
+                c23 += v.y & 0x00ff00ffu;
+                t23 += (v.y >> 8) & 0x00ff00ffu;
+            }
+            *reinterpret_cast<uint4*>(row + k4) =
+                make_uint4((c01 & 0xffffu) | ((t01 & 0xffffu) << 16), (c01 >> 16) | ((t01 >> 16) << 16),
+                           (c23 & 0xffffu) | ((t23 & 0xffffu) << 16), (c23 >> 16) | ((t23 >> 16) << 16));
+        }
+    } else if ((C & 3u) == 0) {
+        // the same shape with whole u16 counts (a wave counts at most 256 particles, so each 16-bit
+        // half of a sum stays below 2^16); folded: the targets from the u16 pairs after the counters
+        for (uint32_t k4 = 4 * threadIdx.x; k4 < C; k4 += 4 * blockDim.x) {
+            uint32_t c01 = 0, c23 = 0;
+            for (uint32_t w2 = 0; w2 < waves; ++w2) {
+                const uint2 v = *reinterpret_cast<const uint2*>(cnt + w2 * C + k4);
+                c01 += v.x;
+                c23 += v.y;
+            }
+            uint4 o = make_uint4(c01 & 0xffffu, c01 >> 16, c23 & 0xffffu, c23 >> 16);
+            if (fold) {
+                const uint2 mm = *reinterpret_cast<const uint2*>(mcnt + (k4 >> 1));
+                o.x |= (mm.x & 0xffffu) << 16;
+                o.y |= (mm.x >> 16) << 16;
+                o.z |= (mm.y & 0xffffu) << 16;
+                o.w |= (mm.y >> 16) << 16;
+            }
+            *reinterpret_cast<uint4*>(row + k4) = o;
+        }
+    } else
     for (uint32_t k = threadIdx.x; k < C; k += blockDim.x) {
         uint32_t tot = 0;
         if (pack) {
