@@ -37,6 +37,52 @@ struct GridParams {
     int spatial;
 };
 
+// Wave-level scans and reductions through DPP: row_shr within each 16-lane row, then row_bcast:15
+// and row_bcast:31 across the rows (a generic shuffle compiles to ds_bpermute, an LDS round trip per
+// step). A lane whose DPP source is outside its row, or whose row the row mask leaves out, adds the
+// identity.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_or_identity(uint32_t identity, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, CTRL, ROWS, 0xf, false);
+}
+// inclusive prefix sum over each 16-lane row
+__device__ __forceinline__ uint32_t row_incl_add(uint32_t v) {
+    v += dpp_or_identity<0x111, 0xf>(0u, v);
+    v += dpp_or_identity<0x112, 0xf>(0u, v);
+    v += dpp_or_identity<0x114, 0xf>(0u, v);
+    v += dpp_or_identity<0x118, 0xf>(0u, v);
+    return v;
+}
+// inclusive prefix sum over the wave's 64 lanes
+__device__ __forceinline__ uint32_t wave_incl_add(uint32_t v) {
+    v = row_incl_add(v);
+    v += dpp_or_identity<0x142, 0xa>(0u, v);  // rows 1, 3 add lane 15, 47
+    v += dpp_or_identity<0x143, 0xc>(0u, v);  // rows 2, 3 add lane 31
+    return v;
+}
+// the wave's minimum / maximum (wave-uniform): quads, half rows, rows, then across the rows into
+// lane 63
+__device__ __forceinline__ int wave_min_i32(int v) {
+    constexpr uint32_t id = 0x7fffffffu;
+    v = min(v, (int)dpp_or_identity<0xb1, 0xf>(id, (uint32_t)v));   // quad_perm [1,0,3,2]
+    v = min(v, (int)dpp_or_identity<0x4e, 0xf>(id, (uint32_t)v));   // quad_perm [2,3,0,1]
+    v = min(v, (int)dpp_or_identity<0x141, 0xf>(id, (uint32_t)v));  // row_half_mirror
+    v = min(v, (int)dpp_or_identity<0x140, 0xf>(id, (uint32_t)v));  // row_mirror
+    v = min(v, (int)dpp_or_identity<0x142, 0xa>(id, (uint32_t)v));  // row_bcast:15
+    v = min(v, (int)dpp_or_identity<0x143, 0xc>(id, (uint32_t)v));  // row_bcast:31
+    return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ int wave_max_i32(int v) {
+    constexpr uint32_t id = 0x80000000u;
+    v = max(v, (int)dpp_or_identity<0xb1, 0xf>(id, (uint32_t)v));
+    v = max(v, (int)dpp_or_identity<0x4e, 0xf>(id, (uint32_t)v));
+    v = max(v, (int)dpp_or_identity<0x141, 0xf>(id, (uint32_t)v));
+    v = max(v, (int)dpp_or_identity<0x140, 0xf>(id, (uint32_t)v));
+    v = max(v, (int)dpp_or_identity<0x142, 0xa>(id, (uint32_t)v));
+    v = max(v, (int)dpp_or_identity<0x143, 0xc>(id, (uint32_t)v));
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 // Rust `f as isize` of a floored f32: saturating, NaN -> 0.
 __device__ __forceinline__ int64_t f32_to_isize(float f) {
     if (f != f) return 0;

@@ -1738,12 +1738,7 @@ __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restri
     // the system's coordinate span (Particle mode: do coordinate bins hold one cell each?)
 #pragma unroll
     for (int a = 0; a < D; ++a) {
-        int l = lo[a], h = hi[a];
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            l = min(l, __shfl_xor(l, off, 64));
-            h = max(h, __shfl_xor(h, off, 64));
-        }
+        const int l = wave_min_i32(lo[a]), h = wave_max_i32(hi[a]);
         if (lane == 0) {
             red_lo[a][w] = l;
             red_hi[a][w] = h;
@@ -1771,16 +1766,7 @@ __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restri
     const uint32_t sa = tot[0] + tot[1] + tot[2] + tot[3];
     const uint32_t sb = itm[0] + itm[1] + itm[2] + itm[3];
     const uint32_t sm = msk[0] + msk[1] + msk[2] + msk[3];
-    uint32_t xa = sa, xb = sb, xm = sm;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t ya = __shfl_up(xa, off, 64), yb = __shfl_up(xb, off, 64), ym = __shfl_up(xm, off, 64);
-        if (lane >= (uint32_t)off) {
-            xa += ya;
-            xb += yb;
-            xm += ym;
-        }
-    }
+    const uint32_t xa = wave_incl_add(sa), xb = wave_incl_add(sb), xm = wave_incl_add(sm);
     if (lane == 63) {
         red[0][w] = xa;
         red[1][w] = xb;
@@ -1794,20 +1780,16 @@ __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restri
         eb = red[1][lane];
         em = red[2][lane];
     }
-#pragma unroll
-    for (int off = 1; off < (int)kSysWaves; off <<= 1) {
-        const uint32_t ya = __shfl_up(ea, off, 64), yb = __shfl_up(eb, off, 64), ym = __shfl_up(em, off, 64);
-        if (lane >= (uint32_t)off) {
-            ea += ya;
-            eb += yb;
-            em += ym;
-        }
-    }
-    const uint32_t pa = w ? (uint32_t)__shfl((int)ea, (int)w - 1, 64) : 0u;  // earlier waves' sums
-    const uint32_t pb = w ? (uint32_t)__shfl((int)eb, (int)w - 1, 64) : 0u;
-    const uint32_t pm = w ? (uint32_t)__shfl((int)em, (int)w - 1, 64) : 0u;
-    const uint32_t tb = (uint32_t)__shfl((int)eb, (int)kSysWaves - 1, 64);
-    const uint32_t tm = (uint32_t)__shfl((int)em, (int)kSysWaves - 1, 64);
+    static_assert(kSysWaves == 16, "the waves' sums are scanned within lanes 0-15 (one DPP row)");
+    ea = row_incl_add(ea);
+    eb = row_incl_add(eb);
+    em = row_incl_add(em);
+    // earlier waves' sums (w is wave-uniform)
+    const uint32_t pa = w ? (uint32_t)__builtin_amdgcn_readlane((int)ea, (int)w - 1) : 0u;
+    const uint32_t pb = w ? (uint32_t)__builtin_amdgcn_readlane((int)eb, (int)w - 1) : 0u;
+    const uint32_t pm = w ? (uint32_t)__builtin_amdgcn_readlane((int)em, (int)w - 1) : 0u;
+    const uint32_t tb = (uint32_t)__builtin_amdgcn_readlane((int)eb, (int)kSysWaves - 1);
+    const uint32_t tm = (uint32_t)__builtin_amdgcn_readlane((int)em, (int)kSysWaves - 1);
     // the system's coordinate span per axis: a bin may hold two cells only if two coordinates of the
     // span share its residue on some axis (see k_bin_scan); no axis wider than the grid, no alias
     int span_lo_a[3] = {0, 0, 0}, span_hi_a[3] = {0, 0, 0};
@@ -1815,15 +1797,8 @@ __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restri
     if (g.mode == 1) {
 #pragma unroll
         for (int a = 0; a < D; ++a) {
-            int l = lane < kSysWaves ? red_lo[a][lane] : INT32_MAX;
-            int h = lane < kSysWaves ? red_hi[a][lane] : INT32_MIN;
-#pragma unroll
-            for (int off = 8; off >= 1; off >>= 1) {
-                l = min(l, __shfl_xor(l, off, 64));
-                h = max(h, __shfl_xor(h, off, 64));
-            }
-            span_lo_a[a] = __shfl(l, 0, 64);
-            span_hi_a[a] = __shfl(h, 0, 64);
+            span_lo_a[a] = wave_min_i32(lane < kSysWaves ? red_lo[a][lane] : INT32_MAX);
+            span_hi_a[a] = wave_max_i32(lane < kSysWaves ? red_hi[a][lane] : INT32_MIN);
             if (span_hi_a[a] >= span_lo_a[a] && (int64_t)span_hi_a[a] - span_lo_a[a] >= (int64_t)g.size[a]) wide = true;
         }
     }
