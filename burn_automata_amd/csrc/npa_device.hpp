@@ -83,6 +83,26 @@ __device__ __forceinline__ int wave_max_i32(int v) {
     return __builtin_amdgcn_readlane(v, 63);
 }
 
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_or_identity<0xb1, 0xf>(0u, v));
+    v = max(v, dpp_or_identity<0x4e, 0xf>(0u, v));
+    v = max(v, dpp_or_identity<0x141, 0xf>(0u, v));
+    v = max(v, dpp_or_identity<0x140, 0xf>(0u, v));
+    v = max(v, dpp_or_identity<0x142, 0xa>(0u, v));
+    v = max(v, dpp_or_identity<0x143, 0xc>(0u, v));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+// the wave's sum (wave-uniform)
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+    v += dpp_or_identity<0xb1, 0xf>(0u, v);
+    v += dpp_or_identity<0x4e, 0xf>(0u, v);
+    v += dpp_or_identity<0x141, 0xf>(0u, v);
+    v += dpp_or_identity<0x140, 0xf>(0u, v);
+    v += dpp_or_identity<0x142, 0xa>(0u, v);
+    v += dpp_or_identity<0x143, 0xc>(0u, v);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // Rust `f as isize` of a floored f32: saturating, NaN -> 0.
 __device__ __forceinline__ int64_t f32_to_isize(float f) {
     if (f != f) return 0;

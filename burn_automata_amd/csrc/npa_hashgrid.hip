@@ -378,12 +378,7 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
     if (fold) {  // the tile's coordinate span
 #pragma unroll
         for (int a = 0; a < 3; ++a) {
-            int l = lo[a], h = hi[a];
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                l = min(l, __shfl_xor(l, off, 64));
-                h = max(h, __shfl_xor(h, off, 64));
-            }
+            const int l = wave_min_i32(lo[a]), h = wave_max_i32(hi[a]);
             if (lane == 0) {
                 span_red[a][w] = l;
                 span_red[3 + a][w] = h;
@@ -548,12 +543,7 @@ __global__ __launch_bounds__(256) void k_table_offsets_scan(uint32_t* __restrict
         run = column_scan(table + (uint64_t)b * tiles_per_sys * C + k, C, tiles_per_sys);
     }
     // the keys' exclusive prefix within the block
-    uint32_t x = run;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t y = __shfl_up(x, off, 64);
-        if (lane >= (uint32_t)off) x += y;
-    }
+    const uint32_t x = wave_incl_add(run);
     if (lane == 63) wsum[w] = x;
     __syncthreads();
     uint32_t wpre = 0, btotal = 0;
@@ -577,8 +567,7 @@ __global__ __launch_bounds__(256) void k_table_offsets_scan(uint32_t* __restrict
                 acc += (uint32_t)v;
             }
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+        acc = wave_sum_u32(acc);
         if (lane == 0) s_prefix = acc;
     }
     __syncthreads();
@@ -665,22 +654,12 @@ __global__ __launch_bounds__(256) void k_table_offsets_fold(uint32_t* __restrict
                 lo[a] = min(lo[a], tile_span[(uint64_t)t * 8 + a]);
                 hi[a] = max(hi[a], tile_span[(uint64_t)t * 8 + 3 + a]);
             }
-    uint32_t xa = run, xb = itm, xm = msk;
+    const uint32_t xa = wave_incl_add(run), xb = wave_incl_add(itm), xm = wave_incl_add(msk);
+    if (g.mode == 1)
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t ya = __shfl_up(xa, off, 64), yb = __shfl_up(xb, off, 64), ym = __shfl_up(xm, off, 64);
-        if (lane >= (uint32_t)off) {
-            xa += ya;
-            xb += yb;
-            xm += ym;
-        }
-    }
-#pragma unroll
-    for (int a = 0; a < 3; ++a)
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            lo[a] = min(lo[a], __shfl_xor(lo[a], off, 64));
-            hi[a] = max(hi[a], __shfl_xor(hi[a], off, 64));
+        for (int a = 0; a < 3; ++a) {
+            lo[a] = wave_min_i32(lo[a]);
+            hi[a] = wave_max_i32(hi[a]);
         }
     if (lane == 63) {
         wsum[0][w] = xa;
@@ -759,12 +738,9 @@ __global__ __launch_bounds__(256) void k_table_offsets_fold(uint32_t* __restrict
                 acc_m += (uint32_t)((u >> 31) & 0x7fffffffull);
             }
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            acc_a += __shfl_xor(acc_a, off, 64);
-            acc_b += __shfl_xor(acc_b, off, 64);
-            acc_m += __shfl_xor(acc_m, off, 64);
-        }
+        acc_a = wave_sum_u32(acc_a);
+        acc_b = wave_sum_u32(acc_b);
+        acc_m = wave_sum_u32(acc_m);
         if (lane == 0) {
             s_pa = acc_a;
             s_pb = acc_b;
@@ -833,21 +809,11 @@ __global__ __launch_bounds__(1024) void k_table_offsets_sys(uint32_t* __restrict
 __device__ __forceinline__ uint32_t block_scan_1024(uint32_t v, uint32_t* lds, uint32_t* total) {
     const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const uint32_t nw = blockDim.x >> 6;
-    uint32_t x = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        uint32_t y = __shfl_up(x, off, 64);
-        if (lane >= (uint32_t)off) x += y;
-    }
+    const uint32_t x = wave_incl_add(v);
     if (lane == 63) lds[wid] = x;
     __syncthreads();
     if (wid == 0) {
-        uint32_t s = lane < nw ? lds[lane] : 0;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            uint32_t y = __shfl_up(s, off, 64);
-            if (lane >= (uint32_t)off) s += y;
-        }
+        const uint32_t s = wave_incl_add(lane < nw ? lds[lane] : 0u);
         if (lane < nw) lds[lane] = s;
     }
     __syncthreads();
@@ -1416,12 +1382,7 @@ constexpr uint32_t kThinThreads = 512;  // bins per k_split_thin block (one rese
 __device__ __forceinline__ uint32_t block_prefix_thin(uint32_t v, uint32_t* ldsw, uint32_t* total) {
     constexpr uint32_t NW = kThinThreads / 64;
     const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    uint32_t x = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t y = __shfl_up(x, off, 64);
-        if (lane >= (uint32_t)off) x += y;
-    }
+    const uint32_t x = wave_incl_add(v);
     if (lane == 63) ldsw[wid] = x;
     __syncthreads();
     uint32_t pre = 0, all = 0;
@@ -1902,8 +1863,7 @@ __global__ __launch_bounds__(256) void k_sys_scatter(const float4* __restrict__ 
     const uint32_t upto = blockIdx.x == 0 ? batch : b_lo;
     unsigned long long acc = 0;
     for (uint32_t k = tid; k < upto; k += blockDim.x) acc += sys_tot[k];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    acc = (unsigned long long)wave_sum_u32((uint32_t)acc) | ((unsigned long long)wave_sum_u32((uint32_t)(acc >> 32)) << 32);
     if (lane == 0) s_part[w] = acc;
     __syncthreads();
     if (tid == 0) {
@@ -2049,12 +2009,10 @@ __global__ __launch_bounds__(256) void k_bin_count(const float4* __restrict__ po
     }
     if (__ballot(ovf) != 0ull && lane == 0) atomicOr(flags + 1, 1u);
 #pragma unroll
-    for (int a = 0; a < D; ++a)
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            lo[a] = max(lo[a], (uint32_t)__shfl_xor((int)lo[a], off, 64));
-            hi[a] = max(hi[a], (uint32_t)__shfl_xor((int)hi[a], off, 64));
-        }
+    for (int a = 0; a < D; ++a) {
+        lo[a] = wave_max_u32(lo[a]);
+        hi[a] = wave_max_u32(hi[a]);
+    }
     if (lane == 0)
 #pragma unroll
         for (int a = 0; a < 3; ++a) {
@@ -2109,16 +2067,7 @@ __global__ __launch_bounds__(1024) void k_bin_scan(unsigned long long* __restric
     const uint32_t sa = run[0] + run[1] + run[2] + run[3];
     const uint32_t sb = itm[0] + itm[1] + itm[2] + itm[3];
     const uint32_t sm = msk[0] + msk[1] + msk[2] + msk[3];
-    uint32_t xa = sa, xb = sb, xm = sm;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t ya = __shfl_up(xa, off, 64), yb = __shfl_up(xb, off, 64), ym = __shfl_up(xm, off, 64);
-        if (lane >= (uint32_t)off) {
-            xa += ya;
-            xb += yb;
-            xm += ym;
-        }
-    }
+    const uint32_t xa = wave_incl_add(sa), xb = wave_incl_add(sb), xm = wave_incl_add(sm);
     if (lane == 63) {
         red[0][w] = xa;
         red[1][w] = xb;
@@ -2132,20 +2081,16 @@ __global__ __launch_bounds__(1024) void k_bin_scan(unsigned long long* __restric
         eb = red[1][lane];
         em = red[2][lane];
     }
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
-        const uint32_t ya = __shfl_up(ea, off, 64), yb = __shfl_up(eb, off, 64), ym = __shfl_up(em, off, 64);
-        if (lane >= (uint32_t)off) {
-            ea += ya;
-            eb += yb;
-            em += ym;
-        }
-    }
-    const uint32_t pa = w ? (uint32_t)__shfl((int)ea, (int)w - 1, 64) : 0u;  // earlier waves' sums
-    const uint32_t pb = w ? (uint32_t)__shfl((int)eb, (int)w - 1, 64) : 0u;
-    const uint32_t pm = w ? (uint32_t)__shfl((int)em, (int)w - 1, 64) : 0u;
-    const uint32_t ta = (uint32_t)__shfl((int)ea, 15, 64), tb = (uint32_t)__shfl((int)eb, 15, 64);
-    const uint32_t tm = (uint32_t)__shfl((int)em, 15, 64);
+    ea = row_incl_add(ea);
+    eb = row_incl_add(eb);
+    em = row_incl_add(em);
+    // earlier waves' sums (w is wave-uniform)
+    const uint32_t pa = w ? (uint32_t)__builtin_amdgcn_readlane((int)ea, (int)w - 1) : 0u;
+    const uint32_t pb = w ? (uint32_t)__builtin_amdgcn_readlane((int)eb, (int)w - 1) : 0u;
+    const uint32_t pm = w ? (uint32_t)__builtin_amdgcn_readlane((int)em, (int)w - 1) : 0u;
+    const uint32_t ta = (uint32_t)__builtin_amdgcn_readlane((int)ea, 15);
+    const uint32_t tb = (uint32_t)__builtin_amdgcn_readlane((int)eb, 15);
+    const uint32_t tm = (uint32_t)__builtin_amdgcn_readlane((int)em, 15);
     // A coordinate bin (residues r_a = c_a mod size_a) can hold two cells only if on some axis two
     // coordinates of the span [lo, hi] share its residue: first = lo + ((r - lo) mod size) and
     // first + size <= hi. Such bins are marked unsplit (walked in the reference order with the cell
@@ -2191,12 +2136,9 @@ __global__ __launch_bounds__(1024) void k_bin_scan(unsigned long long* __restric
                 acc_m += (uint32_t)((qb >> 31) & 0x7fffffffull);
             }
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            acc_a += __shfl_xor(acc_a, off, 64);
-            acc_b += __shfl_xor(acc_b, off, 64);
-            acc_m += __shfl_xor(acc_m, off, 64);
-        }
+        acc_a = wave_sum_u32(acc_a);
+        acc_b = wave_sum_u32(acc_b);
+        acc_m = wave_sum_u32(acc_m);
         if (lane == 0) {
             s_pa = acc_a;
             s_pb = acc_b;
