@@ -1585,8 +1585,10 @@ __global__ __launch_bounds__(kThinThreads) void k_split_thin(const float4* __res
 //      system (keys[i]) and, for a target, its compact row = the bin's first row + its target index
 //      (ranks[i] = row + 1, 0 for no row; bit 31 marks the bin's first particle). Rows only index
 //      the targets, no result depends on their order.
-// k_sys_scatter, one thread per particle: the systems' item and row bases (prefix of sys_tot), then
-// the sorted record, state row and snapshot entries at the particle's slot, the work item starting
+// k_sys_scatter, one thread per particle, one wave per block (the waves spread over every CU): the
+// systems' item and row bases (prefix of sys_tot, summed while the particle's position and state
+// row are in flight), then the sorted record, state row and snapshot entries at the particle's
+// slot, the work item starting
 // there, its compact row (act_rows / row_of), the bin's directory entry from its first particle, and
 // the step's output for a particle outside the update mask (hold_particle); block 0 writes the item
 // and row totals and clears the update's item queues.
@@ -1839,80 +1841,115 @@ __global__ __launch_bounds__(kSysThreads) void k_sys_rank(const float4* __restri
     }
 }
 
-template <int D>
-__global__ __launch_bounds__(256) void k_sys_scatter(const float4* __restrict__ pos, const float* __restrict__ states,
-                                                     uint32_t S, uint32_t n, uint32_t batch, GridParams g,
-                                                     uint32_t tpi_log2, SplitTargets T,
-                                                     const uint32_t* __restrict__ bin_offsets,
-                                                     const uint32_t* __restrict__ sys_item,
-                                                     const unsigned long long* __restrict__ sys_tot,
-                                                     const uint32_t* __restrict__ slot_of,
-                                                     const uint32_t* __restrict__ row_code,
-                                                     uint32_t* __restrict__ perm, uint32_t* __restrict__ inv,
-                                                     float4* __restrict__ srec, int4* __restrict__ scoord,
-                                                     float* __restrict__ sstate, int4* __restrict__ dir_e,
-                                                     uint2* __restrict__ worklist, uint32_t* __restrict__ wl_count,
-                                                     uint32_t* __restrict__ act_rows, uint32_t* __restrict__ row_of) {
-    __shared__ unsigned long long s_base[2], s_part[4];
-    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+template <int D, int NQ>
+__global__ __launch_bounds__(64) void k_sys_scatter(const float4* __restrict__ pos, const float* __restrict__ states,
+                                                    uint32_t S, uint32_t n, uint32_t batch, GridParams g,
+                                                    uint32_t tpi_log2, SplitTargets T,
+                                                    const uint32_t* __restrict__ bin_offsets,
+                                                    const uint32_t* __restrict__ sys_item,
+                                                    const unsigned long long* __restrict__ sys_tot,
+                                                    const uint32_t* __restrict__ slot_of,
+                                                    const uint32_t* __restrict__ row_code,
+                                                    uint32_t* __restrict__ perm, uint32_t* __restrict__ inv,
+                                                    float4* __restrict__ srec, int4* __restrict__ scoord,
+                                                    float* __restrict__ sstate, int4* __restrict__ dir_e,
+                                                    uint2* __restrict__ worklist, uint32_t* __restrict__ wl_count,
+                                                    uint32_t* __restrict__ act_rows, uint32_t* __restrict__ row_of) {
+    const uint32_t lane = threadIdx.x;  // one wave per block
     const uint64_t total = (uint64_t)batch * n;
-    const uint64_t first = (uint64_t)blockIdx.x * blockDim.x;
-    const uint32_t b_lo = (uint32_t)(first / n);  // the block's first system
-    // item and row bases of systems b_lo .. b_hi: prefix sums of the systems' totals (items in the
+    const uint64_t first = (uint64_t)blockIdx.x * 64;  // < total
+    const uint32_t b_lo = (uint32_t)(first / n);       // the block's first system
+    const uint64_t i = first + lane;
+    const bool live = i < total;
+    // the particle's inputs (the state row when NQ > 0: NQ float4s, 16-byte aligned rows) are
+    // independent of the systems' bases: in flight while those are summed
+    const uint64_t ii = live ? i : first;
+    const float4 p4 = pos[ii];
+    const uint32_t local = slot_of[ii];
+    const uint32_t code = row_code[ii];
+    float4 row[NQ > 0 ? NQ : 1];
+    if constexpr (NQ > 0) {
+        const float4* src = reinterpret_cast<const float4*>(states + ii * S);
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) row[q] = src[q];
+    }
+    // item and row bases of the block's systems: prefix sums of the systems' totals (items in the
     // low word, rows in the high word: no carries, both stay below 2^32); block 0 also sums them all
     const uint32_t upto = blockIdx.x == 0 ? batch : b_lo;
     unsigned long long acc = 0;
-    for (uint32_t k = tid; k < upto; k += blockDim.x) acc += sys_tot[k];
-    acc = (unsigned long long)wave_sum_u32((uint32_t)acc) | ((unsigned long long)wave_sum_u32((uint32_t)(acc >> 32)) << 32);
-    if (lane == 0) s_part[w] = acc;
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned long long all = s_part[0] + s_part[1] + s_part[2] + s_part[3];
-        if (blockIdx.x == 0) {  // the lists' counts; the update's item queues start at zero
-            wl_count[0] = (uint32_t)all;
-            wl_count[1] = (uint32_t)(all >> 32);
-            s_base[0] = 0ull;
-        } else {
-            s_base[0] = all;
+    for (uint32_t k = lane; k < upto; k += 64) acc += sys_tot[k];
+    const uint32_t all_items = wave_sum_u32((uint32_t)acc), all_rows = wave_sum_u32((uint32_t)(acc >> 32));
+    if (blockIdx.x == 0) {  // the lists' counts; the update's item queues start at zero
+        if (lane == 0) {
+            wl_count[0] = all_items;
+            wl_count[1] = all_rows;
         }
+        for (uint32_t k = 2 + lane; k < kWlWords; k += 64) wl_count[k] = 0u;
     }
-    if (blockIdx.x == 0)
-        for (uint32_t k = 2 + tid; k < kWlWords; k += blockDim.x) wl_count[k] = 0u;
-    __syncthreads();
-    const uint64_t i = first + tid;
-    if (i >= total) return;
+    if (!live) return;
     const uint32_t b = (uint32_t)(i / n);
-    unsigned long long base = s_base[0];
+    unsigned long long base = blockIdx.x == 0 ? 0ull : ((unsigned long long)all_rows << 32) | all_items;
     for (uint32_t bb = b_lo; bb < b; ++bb) base += sys_tot[bb];  // a block spanning several systems
     const uint32_t ibase = (uint32_t)base, rbase = (uint32_t)(base >> 32);
-    const float4 p4 = pos[i];
-    const uint32_t local = slot_of[i];
-    const uint32_t code = row_code[i];
     const float p[4] = {p4.x, p4.y, p4.z, p4.w};
     int c[3];
     uint32_t key;
     bool o = false;
     sys_cell(p, g, c, &key, &o);  // (an overflow was flagged by the rank kernel)
+    const uint64_t bin = (uint64_t)b * g.cells + key;
+    const uint32_t beg = bin_offsets[bin], nxt = bin_offsets[bin + 1], item0 = sys_item[bin];
+    // used here, so the bin's loads are issued together (read-only loads are otherwise moved down to
+    // their uses, after the stores)
+    asm volatile("" ::"v"(beg), "v"(nxt), "v"(item0));
+    if constexpr (NQ > 0) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) asm volatile("" ::"v"(row[q].x), "v"(row[q].y), "v"(row[q].z), "v"(row[q].w));
+    }
     const uint32_t slot = b * n + local;
-    write_sorted<D>(slot, (uint32_t)i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
+    write_sorted<D>(slot, (uint32_t)i, b, n, p4, c, NQ > 0 ? nullptr : states, S, perm, inv, srec, scoord, sstate);
+    if constexpr (NQ > 0) {
+        float4* o4 = reinterpret_cast<float4*>(sstate + (uint64_t)slot * (4 * NQ));
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) o4[q] = row[q];
+    }
     const uint32_t row1 = code & 0x7fffffffu;
     if (row1) {
-        const uint32_t row = rbase + row1 - 1u;
-        act_rows[row] = slot;
-        row_of[slot] = row;
+        const uint32_t crow = rbase + row1 - 1u;
+        act_rows[crow] = slot;
+        row_of[slot] = crow;
     } else {
         row_of[slot] = ~0u;
-        if (T.mask_mode != 0) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
+        if (T.mask_mode != 0) {
+            bool held = false;
+            if constexpr (NQ > 0) {
+                if (T.pos == pos && T.states == states) {  // the step's input rows, already loaded
+                    hold_loaded<NQ>(i, p4, row, g, T.out_pos, T.out_states);
+                    held = true;
+                }
+            }
+            if (!held) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
+        }
     }
-    const uint64_t bin = (uint64_t)b * g.cells + key;
-    const uint32_t beg = bin_offsets[bin];
     const uint32_t r_bin = slot - beg;
     const uint32_t tpi = 1u << tpi_log2;
     if ((r_bin & (tpi - 1)) == 0) {
-        const uint32_t left = bin_offsets[bin + 1] - beg - r_bin;
-        worklist[ibase + sys_item[bin] + (r_bin >> tpi_log2)] = make_uint2(slot, left < tpi ? left : tpi);
+        const uint32_t left = nxt - beg - r_bin;
+        worklist[ibase + item0 + (r_bin >> tpi_log2)] = make_uint2(slot, left < tpi ? left : tpi);
     }
     if (g.mode == 1 && (code >> 31)) dir_e[bin * kDirGroups] = make_int4(c[0], c[1], c[2], (int)slot);
+}
+
+// The small-system scatter for the state width: rows preloaded when they are whole float4s.
+template <int D>
+static auto sys_scatter_for(const float* states, uint32_t S) -> decltype(&k_sys_scatter<D, 0>) {
+    if (!states || S != state_stride_for(S)) return k_sys_scatter<D, 0>;
+    switch (S / 4) {
+        case 1: return k_sys_scatter<D, 1>;
+        case 2: return k_sys_scatter<D, 2>;
+        case 4: return k_sys_scatter<D, 4>;
+        case 6: return k_sys_scatter<D, 6>;
+        default: return k_sys_scatter<D, 8>;
+    }
 }
 
 template <int D, int R>
@@ -1934,7 +1971,7 @@ static hipError_t launch_sys_r(const GridParams& g, const HashgridPlan& plan, co
                                 ws.ranks.as<uint32_t>(), batch, ws.flags.as<uint32_t>());
     if (e != hipSuccess) return e;
     const uint64_t total = (uint64_t)batch * n;
-    return launch_timed(prof, NPA_KERNEL_SCATTER, k_sys_scatter<D>, dim3((uint32_t)((total + 255) / 256)), dim3(256),
+    return launch_timed(prof, NPA_KERNEL_SCATTER, sys_scatter_for<D>(states, S), dim3((uint32_t)((total + 63) / 64)), dim3(64),
                         0, stream, pos, states, S, n, batch, g, (uint32_t)__builtin_ctz(plan.tpi), tg,
                         ws.bin_offsets.as<uint32_t>(),
                         ws.totals.as<uint32_t>(), ws.scan_status.as<unsigned long long>(), ws.keys.as<uint32_t>(),
@@ -1960,7 +1997,9 @@ static hipError_t launch_sys_r(const GridParams& g, const HashgridPlan& plan, co
 //                 ticket-ordered blocks; the directory sizes; it resets the counters and the span
 //                 for the next build;
 //   k_bin_place   per particle: members[bin start + place] = particle;
-//   k_bin_scatter per particle: its rank in the bin = the bin's members with a smaller index (the
+//   k_bin_scatter per particle (place and scatter run one wave per block, so that the few waves of a
+//                 small system spread over every CU; the position and state row are loaded before
+//                 the slot is known): its rank in the bin = the bin's members with a smaller index (the
 //                 reference's order within a bin), hence its slot; then what k_scatter_payload
 //                 writes there, its compact row (the bin's first row + its target index: rows only
 //                 index the targets, no result depends on their order), the work item that starts
@@ -2185,16 +2224,16 @@ __global__ __launch_bounds__(1024) void k_bin_scan(unsigned long long* __restric
     if (bx == nb - 1 && tid < 6) span[tid] = 0u;
 }
 
-__global__ __launch_bounds__(256) void k_bin_place(uint32_t n, const uint32_t* __restrict__ keys,
+__global__ __launch_bounds__(64) void k_bin_place(uint32_t n, const uint32_t* __restrict__ keys,
                                                    const uint32_t* __restrict__ place,
                                                    const uint32_t* __restrict__ bin_offsets,
                                                    uint32_t* __restrict__ members) {
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.x * 64 + threadIdx.x;
     if (i < n) members[bin_offsets[keys[i]] + place[i]] = i;
 }
 
-template <int D>
-__global__ __launch_bounds__(256) void k_bin_scatter(uint32_t n, const uint32_t* __restrict__ keys,
+template <int D, int NQ>
+__global__ __launch_bounds__(64) void k_bin_scatter(uint32_t n, const uint32_t* __restrict__ keys,
                                                      const uint32_t* __restrict__ urow,
                                                      const uint32_t* __restrict__ bin_offsets,
                                                      const uint32_t* __restrict__ members,
@@ -2207,11 +2246,28 @@ __global__ __launch_bounds__(256) void k_bin_scatter(uint32_t n, const uint32_t*
                                                      SplitTargets T, uint2* __restrict__ worklist,
                                                      uint32_t* __restrict__ act_rows, uint32_t* __restrict__ row_of,
                                                      int4* __restrict__ dir_e) {
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.x * 64 + threadIdx.x;
     if (i >= n) return;
-    const float4 p4 = pos[i];  // independent of the slot: in flight while the rank is counted
+    // the position and state row (NQ > 0: NQ float4s, 16-byte aligned rows) are independent of the
+    // slot: in flight while the rank is counted
+    const float4 p4 = pos[i];
+    float4 row[NQ > 0 ? NQ : 1];
+    if constexpr (NQ > 0) {
+        const float4* src = reinterpret_cast<const float4*>(states + (uint64_t)i * S);
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) row[q] = src[q];
+    }
     const uint32_t key = keys[i], ur = urow[i];
     const uint32_t beg = bin_offsets[key], end = bin_offsets[key + 1];
+    const uint32_t rb = row_base[key], ib = item_base[key];
+    // used here, so these loads are issued together (read-only loads are otherwise moved down to
+    // their uses, after the member walk and the cell coordinates)
+    asm volatile("" ::"v"(rb), "v"(ib));
+    if constexpr (NQ > 0) {
+        asm volatile("" ::"v"(p4.x), "v"(p4.y), "v"(p4.z), "v"(p4.w));
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) asm volatile("" ::"v"(row[q].x), "v"(row[q].y), "v"(row[q].z), "v"(row[q].w));
+    }
     uint32_t r = 0, j = beg;
     for (; j + 4 <= end; j += 4) {
         const uint32_t m0 = members[j], m1 = members[j + 1], m2 = members[j + 2], m3 = members[j + 3];
@@ -2224,22 +2280,47 @@ __global__ __launch_bounds__(256) void k_bin_scatter(uint32_t n, const uint32_t*
     bool ovf = false;
     cell_coords(p, g, c64, &ovf);
     const int c[3] = {(int)c64[0], (int)c64[1], (int)c64[2]};
-    write_sorted<D>(dst, i, 0, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
+    write_sorted<D>(dst, i, 0, n, p4, c, NQ > 0 ? nullptr : states, S, perm, inv, srec, scoord, sstate);
+    if constexpr (NQ > 0) {
+        float4* o4 = reinterpret_cast<float4*>(sstate + (uint64_t)dst * (4 * NQ));
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) o4[q] = row[q];
+    }
     const bool tgt = ur != ~0u;
     if (tgt) {
-        const uint32_t row = row_base[key] + ur;
-        act_rows[row] = dst;
-        row_of[dst] = row;
+        const uint32_t crow = rb + ur;
+        act_rows[crow] = dst;
+        row_of[dst] = crow;
     } else {
         row_of[dst] = ~0u;
-        hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
+        bool held = false;
+        if constexpr (NQ > 0) {
+            if (T.pos == pos && T.states == states) {  // the step's input rows, already loaded
+                hold_loaded<NQ>(i, p4, row, g, T.out_pos, T.out_states);
+                held = true;
+            }
+        }
+        if (!held) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
     }
     const uint32_t tpi = 1u << tpi_log2;
     if ((r & (tpi - 1)) == 0) {
         const uint32_t left = end - dst;
-        worklist[item_base[key] + (r >> tpi_log2)] = make_uint2(dst, left < tpi ? left : tpi);
+        worklist[ib + (r >> tpi_log2)] = make_uint2(dst, left < tpi ? left : tpi);
     }
     if (g.mode == 1 && r == 0) dir_e[(uint64_t)key * kDirGroups] = make_int4(c[0], c[1], c[2], (int)dst);
+}
+
+// The binned scatter for the state width: rows preloaded when they are whole float4s.
+template <int D>
+static auto bin_scatter_for(const float* states, uint32_t S) -> decltype(&k_bin_scatter<D, 0>) {
+    if (!states || S != state_stride_for(S)) return k_bin_scatter<D, 0>;
+    switch (S / 4) {
+        case 1: return k_bin_scatter<D, 1>;
+        case 2: return k_bin_scatter<D, 2>;
+        case 4: return k_bin_scatter<D, 4>;
+        case 6: return k_bin_scatter<D, 6>;
+        default: return k_bin_scatter<D, 8>;
+    }
 }
 
 // The binned build applies to a payload build of one system whose bins are cells or coordinate bins,
@@ -2280,12 +2361,13 @@ static hipError_t launch_bins(const HashgridPlan& plan, const GridParams& g, con
                      ws.totals.as<uint32_t>(), ws.bin_list.as<uint32_t>(), ws.dir_n.as<uint32_t>(),
                      ws.wl_count.as<uint32_t>());
     if (e != hipSuccess) return e;
-    e = launch_timed(prof, NPA_KERNEL_SPLIT, k_bin_place, dim3(blocks), dim3(256), 0, stream, n,
+    const uint32_t wblocks = (n + 63) / 64;  // one wave per block: the waves spread over every CU
+    e = launch_timed(prof, NPA_KERNEL_SPLIT, k_bin_place, dim3(wblocks), dim3(64), 0, stream, n,
                      (const uint32_t*)ws.keys.as<uint32_t>(), (const uint32_t*)ws.ranks.as<uint32_t>(),
                      (const uint32_t*)ws.bin_offsets.as<uint32_t>(), ws.tmpidx.as<uint32_t>());
     if (e != hipSuccess) return e;
-    return launch_timed(prof, NPA_KERNEL_SCATTER, g.dim == 2 ? k_bin_scatter<2> : k_bin_scatter<3>, dim3(blocks),
-                        dim3(256), 0, stream, n, (const uint32_t*)ws.keys.as<uint32_t>(),
+    return launch_timed(prof, NPA_KERNEL_SCATTER, g.dim == 2 ? bin_scatter_for<2>(states, S) : bin_scatter_for<3>(states, S), dim3(wblocks),
+                        dim3(64), 0, stream, n, (const uint32_t*)ws.keys.as<uint32_t>(),
                         (const uint32_t*)ws.bin_urow.as<uint32_t>(), (const uint32_t*)ws.bin_offsets.as<uint32_t>(),
                         (const uint32_t*)ws.tmpidx.as<uint32_t>(), (const uint32_t*)ws.totals.as<uint32_t>(),
                         (const uint32_t*)ws.bin_list.as<uint32_t>(), tpi_log2, pos, states, S, g,

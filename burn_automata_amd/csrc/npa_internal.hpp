@@ -248,6 +248,29 @@ __device__ __forceinline__ void hold_particle(uint64_t i, uint32_t S, const Grid
     }
 }
 
+// hold_particle for a particle whose position and state row (NQ float4s, 16-byte aligned rows) are
+// already in registers.
+template <int NQ>
+__device__ __forceinline__ void hold_loaded(uint64_t i, float4 p, const float4 (&row)[NQ], const GridParams& g,
+                                            float4* __restrict__ out_pos, float* __restrict__ out_states) {
+    if (g.boundary == 0) {
+        p.x = wrap_axis(p.x, 0, g);
+        p.y = wrap_axis(p.y, 1, g);
+        if (g.dim == 3) p.z = wrap_axis(p.z, 2, g);
+    }
+    out_pos[i] = p;
+    float4 v[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) v[q] = row[q];
+    if (g.dim == 3) {
+        v[0].w = clampf_(v[0].w, -8.0f, 24.0f);                               // channel 3
+        if constexpr (NQ > 2) v[2].x = clampf_(v[2].x, -8.0f, 24.0f);          // channel 8 (S > 8)
+    }
+    float4* o4 = reinterpret_cast<float4*>(out_states + i * (4 * NQ));
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) o4[q] = v[q];
+}
+
 // Padded feature row used between the perception and MLP kernels:
 // [state SS][blur SS][grad SS*d][density-grad d?, position d?, zero padded to a multiple of 4].
 __host__ __device__ inline uint32_t padded_features(uint32_t SS, uint32_t d, uint32_t rest) {
