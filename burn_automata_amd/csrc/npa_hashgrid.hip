@@ -1990,7 +1990,7 @@ static hipError_t launch_sys_r(const GridParams& g, const HashgridPlan& plan, co
 //                 both in whatever order the atomics land; the cell coordinate span (six atomic
 //                 maxima); block 0 clears the work-list counters, every block its share of the
 //                 offsets scan's status words;
-//   k_bin_scan    per bin (4,096 per 1024-thread block, four per thread): the exclusive prefixes
+//   k_bin_scan    per bin (2,048 per 512-thread block, four per thread): the exclusive prefixes
 //                 of the counts (bin_offsets), of the work items (ceil(count / tpi) items of <= tpi
 //                 slots, as the split emits for a bin of one cell or an unsplit bin) and of the
 //                 targets (the bin's first compact row), with decoupled look-back over
@@ -2065,14 +2065,16 @@ __global__ __launch_bounds__(256) void k_bin_count(const float4* __restrict__ po
     }
 }
 
-__global__ __launch_bounds__(1024) void k_bin_scan(unsigned long long* __restrict__ count, uint32_t* __restrict__ span,
+template <int W>
+__global__ __launch_bounds__(64 * W) void k_bin_scan(unsigned long long* __restrict__ count, uint32_t* __restrict__ span,
                                                    uint32_t C, uint32_t tpi_log2, GridParams g,
                                                    unsigned long long* __restrict__ status,
                                                    uint32_t* __restrict__ bin_offsets, uint32_t* __restrict__ item_base,
                                                    uint32_t* __restrict__ row_base, uint32_t* __restrict__ dir_n,
                                                    uint32_t* __restrict__ wl_count) {
-    // 4,096 keys per block, four per thread (thread t: keys 4t .. 4t + 3 of the block's range)
-    __shared__ uint32_t red[3][16];
+    // 256 W keys per block (W waves), four per thread (thread t: keys 4t .. 4t + 3 of the block's range)
+    static_assert(W >= 1 && W <= 16, "the waves' sums are scanned within lanes 0 .. W - 1 (one DPP row)");
+    __shared__ uint32_t red[3][W];
     __shared__ int s_span[6];
     __shared__ uint32_t s_pa, s_pb, s_pm, s_ticket;
     const uint32_t nb = gridDim.x, tid = threadIdx.x;
@@ -2080,7 +2082,7 @@ __global__ __launch_bounds__(1024) void k_bin_scan(unsigned long long* __restric
     if (tid < 6) s_span[tid] = tid < 3 ? span_lo(span[tid]) : span_hi(span[tid]);
     __syncthreads();
     const uint32_t bx = s_ticket;
-    const uint32_t k0 = (bx * 1024 + tid) * 4;
+    const uint32_t k0 = (bx * (64 * W) + tid) * 4;
     const uint32_t lane = tid & 63, w = tid >> 6;
     uint32_t run[4], msk[4], itm[4];
     unsigned long long cv[4];
@@ -2113,9 +2115,9 @@ __global__ __launch_bounds__(1024) void k_bin_scan(unsigned long long* __restric
         red[2][w] = xm;
     }
     __syncthreads();
-    // lane v < 16 holds wave v's sums: a 16-lane inclusive scan gives every wave its prefix
+    // lane v < W holds wave v's sums: an inclusive scan over the row gives every wave its prefix
     uint32_t ea = 0, eb = 0, em = 0;
-    if (lane < 16) {
+    if (lane < W) {
         ea = red[0][lane];
         eb = red[1][lane];
         em = red[2][lane];
@@ -2127,9 +2129,9 @@ __global__ __launch_bounds__(1024) void k_bin_scan(unsigned long long* __restric
     const uint32_t pa = w ? (uint32_t)__builtin_amdgcn_readlane((int)ea, (int)w - 1) : 0u;
     const uint32_t pb = w ? (uint32_t)__builtin_amdgcn_readlane((int)eb, (int)w - 1) : 0u;
     const uint32_t pm = w ? (uint32_t)__builtin_amdgcn_readlane((int)em, (int)w - 1) : 0u;
-    const uint32_t ta = (uint32_t)__builtin_amdgcn_readlane((int)ea, 15);
-    const uint32_t tb = (uint32_t)__builtin_amdgcn_readlane((int)eb, 15);
-    const uint32_t tm = (uint32_t)__builtin_amdgcn_readlane((int)em, 15);
+    const uint32_t ta = (uint32_t)__builtin_amdgcn_readlane((int)ea, W - 1);
+    const uint32_t tb = (uint32_t)__builtin_amdgcn_readlane((int)eb, W - 1);
+    const uint32_t tm = (uint32_t)__builtin_amdgcn_readlane((int)em, W - 1);
     // A coordinate bin (residues r_a = c_a mod size_a) can hold two cells only if on some axis two
     // coordinates of the span [lo, hi] share its residue: first = lo + ((r - lo) mod size) and
     // first + size <= hi. Such bins are marked unsplit (walked in the reference order with the cell
@@ -2340,7 +2342,8 @@ __global__ __launch_bounds__(256) void k_clear_u64(unsigned long long* __restric
 static hipError_t launch_bins(const HashgridPlan& plan, const GridParams& g, const float4* pos, const float* states,
                               uint32_t S, uint32_t n, Workspace& ws, const SplitTargets& tg, hipStream_t stream,
                               Profiler* prof) {
-    const uint32_t C = plan.cells, blocks = (n + 255) / 256, kblocks = (C + 4095) / 4096;
+    constexpr int kScanWaves = 8;  // k_bin_scan: 256 keys per wave (C4: 16 blocks; 16 waves were 0.4 us slower)
+    const uint32_t C = plan.cells, blocks = (n + 255) / 256, kblocks = (C + 256 * kScanWaves - 1) / (256 * kScanWaves);
     const uint32_t tpi_log2 = (uint32_t)__builtin_ctz(plan.tpi);
     unsigned long long* count = ws.bin_count.as<unsigned long long>();
     uint32_t* span = reinterpret_cast<uint32_t*>(count + C);
@@ -2356,7 +2359,7 @@ static hipError_t launch_bins(const HashgridPlan& plan, const GridParams& g, con
                      ws.bin_urow.as<uint32_t>(), ws.wl_count.as<uint32_t>(), ws.scan_status.as<unsigned long long>(),
                      2 * kblocks + 1, ws.flags.as<uint32_t>());
     if (e != hipSuccess) return e;
-    e = launch_timed(prof, NPA_KERNEL_TABLE_SCAN, k_bin_scan, dim3(kblocks), dim3(1024), 0, stream, count, span, C,
+    e = launch_timed(prof, NPA_KERNEL_TABLE_SCAN, k_bin_scan<kScanWaves>, dim3(kblocks), dim3(64 * kScanWaves), 0, stream, count, span, C,
                      tpi_log2, g, ws.scan_status.as<unsigned long long>(), ws.bin_offsets.as<uint32_t>(),
                      ws.totals.as<uint32_t>(), ws.bin_list.as<uint32_t>(), ws.dir_n.as<uint32_t>(),
                      ws.wl_count.as<uint32_t>());
