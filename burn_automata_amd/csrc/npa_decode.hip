@@ -207,12 +207,19 @@ hipError_t launch_write_gaussians(const float4* pos, const float* states, uint32
 // ----------------------------------------------------------------- splat
 constexpr int kTile = 16;
 
+// A Gaussian weight exp(-d2 / (2 sigma^2)) (splat.rs:71, image.rs:61) as 2^(-d2 * k2) with
+// k2 = log2(e) / (2 sigma^2) on the hardware exp2; it differs from expf of the IEEE quotient by a
+// few ulps at most.
+constexpr float kLog2e = 1.44269504088896340736f;
+__device__ __forceinline__ float splat_weight(float d2, float k2) { return __builtin_amdgcn_exp2f(-(d2 * k2)); }
+
 struct SplatParams {
     int size;
     int radius;
     int tiles_x, tiles_y;
     float sigma;      // pixel-space sigma after the normalize_color rescale
     float two_sig2;   // 2 * sigma * sigma
+    float k2;         // log2(e) / two_sig2 (splat_weight)
     float norm_scale;
     float lo, hi;
     int normalize, y_up;
@@ -227,7 +234,7 @@ struct SplatParams {
 struct SplatParticle {  // 32 bytes
     float fx, fy;
     int bx, by;
-    float denom;
+    float scale;  // norm_scale / the normaliser (1 without normalize_color)
     float c[3];
 };
 
@@ -290,7 +297,7 @@ __global__ __launch_bounds__(256) void k_splat_prep(SplatParams P, const float4*
             const int64_t x = bx + ox, y = by + oy;
             if (any && k0 + q < terms && x >= 0 && y >= 0 && x < P.size && y < P.size) {
                 const float dx = (float)ox - fx, dy = (float)oy - fy;
-                wk = expf(-(dx * dx + dy * dy) / P.two_sig2);
+                wk = splat_weight(dx * dx + dy * dy, P.k2);
             }
             weight_sum += quad_bcast<0>(wk);
             weight_sum += quad_bcast<1>(wk);
@@ -309,7 +316,7 @@ __global__ __launch_bounds__(256) void k_splat_prep(SplatParams P, const float4*
     sp.fy = fy;
     sp.bx = any ? (int)bx : 0;
     sp.by = any ? (int)by : 0;
-    sp.denom = P.normalize ? fmaxf(weight_sum, 1e-8f) : 1.0f;
+    sp.scale = P.norm_scale / (P.normalize ? fmaxf(weight_sum, 1e-8f) : 1.0f);
     if (colors) {
         sp.c[0] = colors[3 * (uint64_t)n];
         sp.c[1] = colors[3 * (uint64_t)n + 1];
@@ -475,8 +482,7 @@ __global__ __launch_bounds__(256) void k_splat_tiles(SplatParams P, const SplatP
             const int ox = x - p.bx, oy = y - p.by;
             if (ox < -P.radius || ox > P.radius || oy < -P.radius || oy > P.radius) continue;
             const float dx = (float)ox - p.fx, dy = (float)oy - p.fy;
-            float w = expf(-(dx * dx + dy * dy) / P.two_sig2);
-            w = w / p.denom * P.norm_scale;
+            const float w = splat_weight(dx * dx + dy * dy, P.k2) * p.scale;
             acc[0] += p.c[0] * w;
             acc[1] += p.c[1] * w;
             acc[2] += p.c[2] * w;
@@ -512,6 +518,7 @@ hipError_t launch_splat_2d(const float4* pos, const float* colors, const float* 
     P.radius = (int)rf;
     P.sigma = sigma;
     P.two_sig2 = 2.0f * sigma * sigma;
+    P.k2 = kLog2e / P.two_sig2;
     P.norm_scale = 1.0f;
     if (cfg.normalize_color) {
         const float t = fsz * cfg.pixel_size / (cfg.hi - cfg.lo);
@@ -621,10 +628,6 @@ struct alignas(16) RenderParticle {  // 48 bytes
     float pad;
 };
 
-// The splat weight exp(-d2 / (2 sigma^2)) (image.rs:61) as 2^(-d2 * k2) on the hardware exp2;
-// it differs from the reference's expf of the IEEE quotient by a few ulps at most.
-constexpr float kLog2e = 1.44269504088896340736f;
-__device__ __forceinline__ float splat_weight(float d2, float k2) { return __builtin_amdgcn_exp2f(-(d2 * k2)); }
 
 __device__ __forceinline__ bool render_tiles(const RenderParams& P, int64_t bx, int64_t by, int64_t r, int* tx0,
                                              int* tx1, int* ty0, int* ty1) {
