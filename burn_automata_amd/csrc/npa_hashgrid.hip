@@ -1026,24 +1026,25 @@ __global__ __launch_bounds__(256) void k_scatter_payload(uint32_t n, uint32_t to
     const uint32_t li = i - b * n;
     const float4 p4 = pos[i];  // independent of the slot: in flight while the slot is computed
     const uint32_t key = keys[i];
+    // the update mask's hash needs no load: computed while the loads above are in flight (a mask
+    // array's value is loaded with them and tested once the slot is known)
+    const float hm = T.mask_mode == 1 ? hash_mask(li, b, n, T.update_prob, T.step_index, T.base_seed) : 1.0f;
+    const float am = T.mask_mode == 2 ? T.mask[i] : 1.0f;
     const uint32_t t = li / tile;
     const uint32_t beg = bin_offsets[(uint64_t)b * C + key];
     const uint32_t tv = table[((uint64_t)b * tiles_per_sys + t) * C + key], rv = ranks[i];
-    const uint32_t r_bin = F.packed ? (tv & 0xffffu) + (rv & 0xffffu) : tv + rv;  // rank in the bin
-    const uint32_t dst = beg + r_bin;
-    if (!F.item_base) out[dst] = i;
+    // the cell coordinates need only the position: computed while the slot's words are in flight
     const float p[4] = {p4.x, p4.y, p4.z, p4.w};
     int64_t c64[3];
     bool ovf = false;
     cell_coords(p, g, c64, &ovf);
     const int c[3] = {(int)c64[0], (int)c64[1], (int)c64[2]};
+    const uint32_t r_bin = F.packed ? (tv & 0xffffu) + (rv & 0xffffu) : tv + rv;  // rank in the bin
+    const uint32_t dst = beg + r_bin;
+    if (!F.item_base) out[dst] = i;
     write_sorted<D>(dst, i, b, n, p4, c, states, S, perm, inv, srec, scoord, sstate);
-    bool tgt = true;
-    if (T.mask_mode != 0) {
-        const float m = T.mask_mode == 1 ? hash_mask(li, b, n, T.update_prob, T.step_index, T.base_seed) : T.mask[i];
-        tgt = m != 0.0f;
-        if (!tgt) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
-    }
+    const bool tgt = T.mask_mode == 0 || (T.mask_mode == 1 ? hm : am) != 0.0f;
+    if (!tgt) hold_particle(i, S, g, T.pos, T.states, T.out_pos, T.out_states);
     if (F.item_base) {  // folded build (one system): what the split emits for the particle's bin
         if (tgt) {
             const uint32_t row = F.packed ? F.row_next[key] + (tv >> 16) + (rv >> 16) : atomicAdd(F.row_next + key, 1u);
