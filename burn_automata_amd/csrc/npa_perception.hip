@@ -409,8 +409,7 @@ __global__ __launch_bounds__(256) void k_density_lanes(StepParams P, const float
         total += rlen[k];
     }
     uint32_t rounds = (total + 3) / 4;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) rounds = max(rounds, (uint32_t)__shfl_xor((int)rounds, off, 64));
+    rounds = wave_max_u32(rounds);
     const bool any_filter = __ballot(rfilt != 0) != 0ull;
     const float eps2 = P.g.eps2, k6 = P.g.k6;
     const bool periodic = P.g.boundary == 0;
@@ -581,8 +580,7 @@ __global__ __launch_bounds__(256) void k_density_lanes3(StepParams P, const floa
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const uint32_t total = R.pre[27];
     uint32_t rounds = (total + 3) / 4;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) rounds = max(rounds, (uint32_t)__shfl_xor((int)rounds, off, 64));
+    rounds = wave_max_u32(rounds);
     const bool any_filter = __ballot(fbits != 0) != 0ull;
     const float eps2 = P.g.eps2, k6 = P.g.k6;
     const bool periodic = P.g.boundary == 0;
@@ -677,15 +675,16 @@ __device__ __forceinline__ float row_lane(float v) {  // lane K of this lane's 1
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + K, 0xf, 0xf, false));
 }
 
-// Inclusive prefix sum over the 16 lanes of each row.
-__device__ __forceinline__ uint32_t row_scan16(uint32_t v, uint32_t q) {
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
-        const uint32_t u = (uint32_t)__shfl_up((int)v, off, 16);
-        if (q >= (uint32_t)off) v += u;
-    }
+// OR over the 16 lanes of each row (quads, half rows, then the row's halves; DPP, no LDS trip).
+__device__ __forceinline__ uint32_t row_or16(uint32_t v) {
+    v |= dpp_or_identity<0xb1, 0xf>(0u, v);   // quad_perm [1,0,3,2]
+    v |= dpp_or_identity<0x4e, 0xf>(0u, v);   // quad_perm [2,3,0,1]
+    v |= dpp_or_identity<0x141, 0xf>(0u, v);  // row_half_mirror
+    v |= dpp_or_identity<0x140, 0xf>(0u, v);  // row_mirror
     return v;
 }
+// Lane 15 of this lane's row (DPP row_newbcast:15).
+__device__ __forceinline__ uint32_t row_last16(uint32_t v) { return dpp_or_identity<0x15f, 0xf>(0u, v); }
 
 template <int D>
 __global__ __launch_bounds__(256) void k_density_rows(StepParams P, const float4* __restrict__ srec,
@@ -737,13 +736,12 @@ __global__ __launch_bounds__(256) void k_density_rows(StepParams P, const float4
         }
     }
     // the row's filter bits, stream offsets and chunk numbers (exclusive prefixes over k)
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) fbits |= (uint32_t)__shfl_xor((int)fbits, off, 16);
+    fbits = row_or16(fbits);
     const uint32_t ch0 = (len[0] + 63) / 64, ch1 = (len[1] + 63) / 64;
-    const uint32_t x0 = row_scan16(len[0], q), x1 = row_scan16(len[1], q);
-    const uint32_t y0 = row_scan16(ch0, q), y1 = row_scan16(ch1, q);
-    const uint32_t tot0 = (uint32_t)__shfl((int)x0, 15, 16), tch0 = (uint32_t)__shfl((int)y0, 15, 16);
-    const uint32_t tot1 = (uint32_t)__shfl((int)x1, 15, 16), tch1 = (uint32_t)__shfl((int)y1, 15, 16);
+    const uint32_t x0 = row_incl_add(len[0]), x1 = row_incl_add(len[1]);
+    const uint32_t y0 = row_incl_add(ch0), y1 = row_incl_add(ch1);
+    const uint32_t tot0 = row_last16(x0), tch0 = row_last16(y0);
+    const uint32_t tot1 = row_last16(x1), tch1 = row_last16(y1);
     if (q < (uint32_t)NC) {
         R.pre[q] = x0 - len[0];
         R.beg[q] = beg[0];
@@ -761,8 +759,7 @@ __global__ __launch_bounds__(256) void k_density_rows(StepParams P, const float4
     lds_wave_sync();
     const uint32_t total = tot0 + tot1;
     uint32_t rounds = (total + 15) / 16;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) rounds = max(rounds, (uint32_t)__shfl_xor((int)rounds, off, 64));
+    rounds = wave_max_u32(rounds);
     const bool any_filter = __ballot(fbits != 0) != 0ull;
     const float eps2 = P.g.eps2, k6 = P.g.k6;
     const bool periodic = P.g.boundary == 0;
