@@ -118,8 +118,12 @@ constexpr int kCpl = 4;
 
 template <int L>
 __device__ __forceinline__ float group_sum(float v) {
+    // butterfly: partner lane ^ m for m = L/2, ..., 1 (the same pairing in every lane, so each lane
+    // ends with the same sum); m < 4 stays within a quad and travels by DPP quad_perm
 #pragma unroll
-    for (int m = L / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, L);
+    for (int m = L / 2; m >= 4; m >>= 1) v += __shfl_xor(v, m, L);
+    if constexpr (L >= 4) v += __int_as_float((int)dpp_or_identity<0x4e, 0xf>(0u, (uint32_t)__float_as_int(v)));  // lane ^ 2
+    if constexpr (L >= 2) v += __int_as_float((int)dpp_or_identity<0xb1, 0xf>(0u, (uint32_t)__float_as_int(v)));  // lane ^ 1
     return v;
 }
 
