@@ -298,8 +298,8 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
         for (uint32_t k = threadIdx.x; k < kWlWords; k += blockDim.x) wl_count[k] = 0;
     for (uint32_t k = tile * blockDim.x + threadIdx.x; k < nstatus; k += gridDim.x * blockDim.x)
         scan_status[k] = 0ull;  // the one-pass offsets scan's published totals (see k_table_offsets_scan)
-    __syncthreads();
-
+    // every round's key first, while the counters' clear completes: the position loads and the cell
+    // coordinates overlap the clear and the barrier (the keys touch no LDS)
     // The first `waves` waves rank (one LDS counter row each); every wave of the block clears the
     // counters and writes the histogram row, which costs O(C) whatever the tile size.
     const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -345,6 +345,9 @@ __global__ __launch_bounds__(1024) void k_hash_rank(const float4* __restrict__ p
             }
         }
     }
+    }
+    __syncthreads();
+    if (ranker) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t li = wave_start + r * 64 + lane;
